@@ -1,0 +1,227 @@
+/*
+ * sluice.h - C ABI of libsluice_hip.so, the MI355X (gfx950) routed-MoE decode
+ * hot path of Sluice: top-k routing, the streaming gap (slot-cache hit/miss,
+ * expert H2D copies, expert-map refresh), the grouped SwiGLU expert product
+ * over slot buffers and the weighted combine.
+ *
+ * Conventions
+ *   - Every entry point returns int: 0 on success, a positive hipError_t from
+ *     the HIP runtime, or a negative SLUICE_E_* code.  Nothing throws across
+ *     the ABI.  sluice_strerror() turns a code into text.
+ *   - Device pointers are plain device addresses (torch data_ptr()), host
+ *     pointers are host addresses; no torch types appear in any signature.
+ *   - Work is enqueued on the hipStream_t the caller passes (torch's
+ *     current_stream().cuda_stream); calls are asynchronous unless stated.
+ *   - Integer ids are int32, routing weights fp32, activations and unquantized
+ *     weights bf16 (uint16 storage), fp8 weights OCP e4m3fn (uint8 storage).
+ *
+ * Each declaration names the reference interface it replaces
+ * (kfirtoledo/sluice file:line, vLLM 0.23 call sites).
+ */
+#ifndef SLUICE_H_
+#define SLUICE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* sluice_stream_t; /* == hipStream_t */
+
+#define SLUICE_OK 0
+#define SLUICE_E_INVAL (-1)    /* bad argument / shape outside kernel limits */
+#define SLUICE_E_OVERFLOW (-2) /* working set exceeds slots (reference raises) */
+#define SLUICE_E_TIMEOUT (-3)  /* host wait on a device record timed out */
+#define SLUICE_E_NOMEM (-4)    /* host allocation failed */
+#define SLUICE_E_STATE (-5)    /* object used in a state it does not allow */
+
+/* Kernel limits (checked on the host before every launch). */
+#define SLUICE_MAX_EXPERTS 1024  /* global experts E per layer */
+#define SLUICE_MAX_SLOTS 512     /* slots S per layer */
+#define SLUICE_MAX_TOPK 16       /* k */
+#define SLUICE_MAX_PAIRS 4096    /* T*k (token, expert) pairs per call */
+#define SLUICE_BLOCK_M 16        /* tokens per aligned block */
+
+#define SLUICE_ABI_VERSION 1
+
+int sluice_abi_version(void);
+const char* sluice_strerror(int code);
+
+/* ------------------------------------------------------------------------
+ * a1. Top-k routing.  Replaces vLLM's runner.router.select_experts
+ * (called at src/sluice/offloader.py:2583-2585).  One wave64 per token.
+ *   scoring 0 = softmax: select on logits (softmax is monotone), ties go to
+ *               the lower expert id; weight = softmax prob (fp32);
+ *   scoring 1 = sigmoid: s = fp32(1/(1+exp(-x))) evaluated in fp64 and
+ *               rounded once; selection on fp32(s + bias); weight = s.
+ *   n_group > 1 enables group-limited selection: group score is the max
+ *   logit (softmax) or the sum of the two largest biased scores (sigmoid);
+ *   only the topk_group best groups (ties: lower group id) stay eligible.
+ *   renorm divides the k weights by their sum (+1e-20 for sigmoid), then
+ *   every weight is multiplied by scale.
+ * logits [T,E] (dtype 0 = fp32, 1 = bf16), bias [E] fp32 or NULL,
+ * ids_out [T,k] int32, w_out [T,k] fp32, both in descending score order.
+ * ---------------------------------------------------------------------- */
+int sluice_route_topk(const void* logits, int logits_dtype, int T, int E, int k,
+                      int scoring, int renorm, float scale, const float* bias,
+                      int n_group, int topk_group, int32_t* ids_out,
+                      float* w_out, sluice_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * a4. Slot lookup.  Replaces the gap's ids D2H + sorted(set(ids)) + residency
+ * scan (src/sluice/offloader.py:2406-2441).  One workgroup builds an LDS
+ * presence map over the E experts, compacts the selected ids in ascending
+ * order with wave ballots, counts owned-but-unmapped ids (misses against a
+ * standing map) and publishes the record to `rec` (host-mapped pinned memory
+ * or device memory), writing rec->stamp = stamp last with a system-scope
+ * release store.
+ * ---------------------------------------------------------------------- */
+typedef struct sluice_gap_record {
+  volatile int32_t stamp;
+  int32_t n_uniq;
+  int32_t n_miss;
+  int32_t reserved;
+  int32_t uniq[SLUICE_MAX_EXPERTS];
+} sluice_gap_record;
+
+int sluice_slot_lookup(const int32_t* ids, int n, const int32_t* expert_map,
+                       const int32_t* local_of, int E, sluice_gap_record* rec,
+                       int32_t stamp, sluice_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * a7. Standing expert-map refresh.  Replaces _write_map/_write_standing_map
+ * (src/sluice/offloader.py:2083-2123): map = -1 everywhere, then
+ * map[slot_global[s]] = s for every occupied slot s (slot_global[s] < 0 =
+ * empty).  The S-entry table travels as a kernel argument, so no pinned
+ * staging buffer and no host wait on a previous copy are needed.
+ * slot_global is a HOST array; map is device [E] int32.
+ * ---------------------------------------------------------------------- */
+int sluice_map_refresh(int32_t* expert_map, int E, const int32_t* slot_global,
+                       int S, sluice_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * a6. Expert H2D streaming.  Replaces _stream_in (src/sluice/offloader.py:
+ * 2709-2723): n row copies dst[i] <- src[i] of bytes[i] each, issued as
+ * hipMemcpyAsync on `stream` (the caller's dedicated copy stream).
+ * ---------------------------------------------------------------------- */
+int sluice_copy_rows(void* const* dst, const void* const* src,
+                     const size_t* bytes, int n, sluice_stream_t stream);
+
+/* Pinned host store for the experts (replaces `cpu.pin_memory()` in
+ * _install_cache, src/sluice/offloader.py:965-967): hipHostMalloc of exactly
+ * `bytes` (no power-of-two rounding), portable across devices. */
+int sluice_host_alloc(size_t bytes, void** out);
+int sluice_host_free(void* p);
+
+/* ------------------------------------------------------------------------
+ * a9/a10. Grouped SwiGLU expert product over slot buffers + weighted combine.
+ * Replaces torch.ops.vllm.fused_experts(h, w13, w2, tw, ti, activation=
+ * "silu", global_num_experts=E, expert_map=map) (src/sluice/offloader.py:
+ * 2590-2599) and vLLM's moe_sum.
+ *   x [T,H] bf16; w13 [S,2I,H] (gate rows, then up rows); w2 [S,H,I];
+ *   topk_w [T,k] fp32; topk_ids [T,k] int32 global ids; expert_map [E]
+ *   int32 (global -> slot, -1 = not resident: the pair contributes 0) or
+ *   NULL (identity, ids are slots);
+ *   out[t] = bf16( scale * sum_j w[t,j] * W2[s]·(silu(W13g[s]·x_t) * W13u[s]·x_t)
+ *                  + shared[t] )                       (shared may be NULL).
+ * fp8 variant: w13/w2 are e4m3fn with fp32 block scales of block_n x block_k
+ * (128x128): w13_scale [S, ceil(2I/bn), ceil(H/bk)], w2_scale
+ * [S, ceil(H/bn), ceil(I/bk)]; activations stay bf16.
+ * Requires H % 64 == 0, I % 64 == 0, T*k <= SLUICE_MAX_PAIRS.
+ * The workspace (device) must hold sluice_fused_experts_workspace() bytes.
+ * ---------------------------------------------------------------------- */
+size_t sluice_fused_experts_workspace(int T, int H, int I, int k);
+
+int sluice_fused_experts_bf16(const void* x, const void* w13, const void* w2,
+                              const float* topk_w, const int32_t* topk_ids,
+                              const int32_t* expert_map, int T, int H, int I,
+                              int k, int E, int S, float scale,
+                              const void* shared, void* workspace,
+                              size_t workspace_bytes, void* out,
+                              sluice_stream_t stream);
+
+int sluice_fused_experts_fp8(const void* x, const void* w13,
+                             const float* w13_scale, const void* w2,
+                             const float* w2_scale, int block_n, int block_k,
+                             const float* topk_w, const int32_t* topk_ids,
+                             const int32_t* expert_map, int T, int H, int I,
+                             int k, int E, int S, float scale,
+                             const void* shared, void* workspace,
+                             size_t workspace_bytes, void* out,
+                             sluice_stream_t stream);
+
+/* Token permute / align-to-block (vLLM moe_align_block_size): groups the
+ * T*k (token, expert) pairs by slot into blocks of <= SLUICE_BLOCK_M pairs,
+ * slots ascending, pairs ascending within a slot.  plan (device int32):
+ *   plan[0] = n_blocks; then per block 18 ints {slot, count, pair[16]}
+ *   starting at plan[4]; then T*k validity flags at
+ *   plan[4 + 18*T*k].  Exposed for testing; fused_experts runs it itself. */
+size_t sluice_moe_plan_ints(int T, int k);
+int sluice_moe_align(const int32_t* topk_ids, int T, int k,
+                     const int32_t* expert_map, int E, int S, int32_t* plan,
+                     sluice_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * a2-a8. Per-layer slot cache + gap.  Replaces _ExpertLayerCache
+ * (src/sluice/offloader.py:121-169), _install_cache's slot/map layout
+ * (895-1044), the SLRU core _touch/_coldest_protected/_acquire_slot/
+ * _evict_to (2009-2081) and _router_split_gap (2362-2467).  Slot
+ * assignment follows the reference's OrderedDict semantics exactly.
+ * ---------------------------------------------------------------------- */
+typedef struct sluice_layer sluice_layer;
+
+/* local_of [E] host array: global id -> local expert (or -1 = not owned).
+ * expert_map_dev: the device map buffer (may be NULL for host-only use, in
+ * which case sluice_layer_gap_host is the only gap entry allowed). */
+int sluice_layer_create(int E, int local_n, int num_slots, int protected_cap,
+                        const int32_t* local_of, int32_t* expert_map_dev,
+                        sluice_layer** out);
+int sluice_layer_destroy(sluice_layer* layer);
+
+/* Register one per-expert parameter: slot buffer base (device, [S, row])
+ * and pinned host store base ([local_n, row]), row_bytes per expert. */
+int sluice_layer_add_param(sluice_layer* layer, void* slot_base_dev,
+                           const void* host_base, size_t row_bytes);
+
+/* Mark a slot as pre-filled with `local` outside the SLRU segments (full
+ * residency pre-fill and static pins, offloader.py:1000-1010, 1046-1083);
+ * debits protected_cap by one when `debit_protected` is set (pins). */
+int sluice_layer_pin(sluice_layer* layer, int local, int debit_protected,
+                     int* slot_out);
+
+/* The gap, device path: launch the slot lookup on topk_ids (n ids) on
+ * `compute`, wait for its record, run the SLRU bookkeeping, stream misses
+ * on the library's copy stream (fenced by events both ways), refresh the
+ * standing map on `compute`.  Returns SLUICE_E_OVERFLOW when the step's
+ * working set cannot fit (state is then as the reference leaves it). */
+int sluice_layer_gap(sluice_layer* layer, const int32_t* topk_ids, int n,
+                     int fast_hit, sluice_stream_t compute);
+
+/* The gap, host path (no HIP calls): ids is a host array.  Runs the same
+ * bookkeeping and reports the (local, slot) stream-ins in order in
+ * streams[2*i], streams[2*i+1] (capacity 2*max_streams ints) and whether
+ * the standing map would be rewritten (*map_written). */
+int sluice_layer_gap_host(sluice_layer* layer, const int32_t* ids, int n,
+                          int fast_hit, int32_t* streams, int max_streams,
+                          int* n_streams, int* map_written);
+
+/* State snapshot.  Arrays may be NULL.  slot_of [local_n] (-1 = absent),
+ * expert_in_slot [S] (-1 = empty), probation/protected in recency order
+ * (LRU first), free_slots in list order (the last is popped next).
+ * counters[8] = {gaps, misses, fast_hits, map_writes, bytes_lo, bytes_hi,
+ *                map_is_standing, protected_cap}. */
+int sluice_layer_state(const sluice_layer* layer, int32_t* slot_of,
+                       int32_t* expert_in_slot, int32_t* probation,
+                       int* n_probation, int32_t* protected_, int* n_protected,
+                       int32_t* free_slots, int* n_free, int64_t* counters);
+
+/* The standing map the layer would publish (host [E] int32). */
+int sluice_layer_standing_map(const sluice_layer* layer, int32_t* map_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SLUICE_H_ */

@@ -1,0 +1,189 @@
+"""Slot-cache / gap oracle (TEST INFRASTRUCTURE ONLY; see oracle/__init__.py).
+
+A CPU restatement of the reference's per-layer slot cache and the
+router-split gap's bookkeeping, kept in the reference's own data structures
+(OrderedDict segments, a list free stack) so that slot assignment can be
+compared bit for bit with the native implementation:
+
+  install          src/sluice/offloader.py:936-947, 974-989 (num_slots,
+                   protected_cap, free list [S-1..0], local_of / global_of_local,
+                   map all -1), 1000-1010 (full-residency pre-fill)
+  touch            src/sluice/offloader.py:2009-2021
+  coldest (LRU)    src/sluice/offloader.py:2023-2034 (the LFU branch is opt-in
+                   and not on the path)
+  acquire_slot     src/sluice/offloader.py:2036-2074
+  evict_to         src/sluice/offloader.py:2076-2081
+  standing map     src/sluice/offloader.py:2083-2123 (map contents only)
+  gap              src/sluice/offloader.py:2405-2467 (fast-hit, sorted unique,
+                   hit touches, miss acquisition with the claimed set seeded by
+                   the step's hit slots, overflow, standing-map refresh)
+  pins             src/sluice/offloader.py:1046-1083
+"""
+
+from __future__ import annotations
+
+from collections import OrderedDict
+
+
+class GapOverflow(RuntimeError):
+    pass
+
+
+class LayerCache:
+    def __init__(self, global_n: int, local_n: int, slots: int, protect_frac: float = 0.5,
+                 local_of=None):
+        self.global_n = global_n
+        self.local_n = local_n
+        self.num_slots = min(slots, local_n)
+        frac = min(max(float(protect_frac), 0.0), 0.9)
+        self.protected_cap = max(min(int(self.num_slots * frac), self.num_slots - 1), 0)
+        self.local_of = list(range(global_n)) if local_of is None else [int(v) for v in local_of]
+        self.global_of_local = [-1] * local_n
+        for g, loc in enumerate(self.local_of):
+            if 0 <= loc < local_n:
+                self.global_of_local[loc] = g
+        self.slot_of: dict[int, int] = {}
+        self.expert_in_slot: list[int | None] = [None] * self.num_slots
+        self.free_slots = list(range(self.num_slots - 1, -1, -1))
+        self.protected: OrderedDict = OrderedDict()
+        self.probation: OrderedDict = OrderedDict()
+        self.pinned_slots: set = set()
+        self.map = [-1] * global_n
+        self.map_is_standing = False
+        self.gaps = 0
+        self.misses = 0
+        self.fast_hits = 0
+        self.map_writes = 0
+
+    # -- SLRU core -------------------------------------------------------
+    def touch(self, slot: int, friendly: bool = True) -> None:
+        if slot in self.protected:
+            self.protected.move_to_end(slot)
+        elif slot in self.probation:
+            if friendly and self.protected_cap > 0:
+                del self.probation[slot]
+                self.protected[slot] = None
+                while len(self.protected) > self.protected_cap:
+                    victim = next(iter(self.protected))
+                    del self.protected[victim]
+                    self.probation[victim] = None
+            else:
+                self.probation.move_to_end(slot)
+
+    def evict_to(self, slot: int, local: int) -> None:
+        prev = self.expert_in_slot[slot]
+        if prev is not None:
+            self.slot_of.pop(prev, None)
+        self.expert_in_slot[slot] = local
+        self.slot_of[local] = slot
+
+    def acquire_slot(self, local: int, claimed: set, allow_protected: bool = True):
+        chosen = None
+        if self.free_slots:
+            chosen = self.free_slots.pop()
+        else:
+            for cand in self.probation:
+                if cand not in claimed:
+                    chosen = cand
+                    break
+            if chosen is not None:
+                del self.probation[chosen]
+            elif allow_protected:
+                for cand in self.protected:
+                    if cand not in claimed:
+                        chosen = cand
+                        break
+                if chosen is not None:
+                    del self.protected[chosen]
+        if chosen is None:
+            return None
+        self.evict_to(chosen, local)
+        self.probation[chosen] = None
+        return chosen
+
+    def pin(self, local: int, debit_protected: bool = True):
+        if local in self.slot_of or not self.free_slots:
+            return None
+        slot = self.free_slots.pop()
+        self.expert_in_slot[slot] = local
+        self.slot_of[local] = slot
+        self.pinned_slots.add(slot)
+        if debit_protected:
+            self.protected_cap -= 1
+        return slot
+
+    # -- maps ------------------------------------------------------------
+    def standing_map(self) -> list[int]:
+        m = [-1] * self.global_n
+        for slot, local in enumerate(self.expert_in_slot):
+            if local is not None:
+                m[self.global_of_local[local]] = slot
+        return m
+
+    def write_standing_map(self) -> None:
+        self.map = self.standing_map()
+        self.map_is_standing = True
+        self.map_writes += 1
+
+    # -- the gap ---------------------------------------------------------
+    def gap(self, ids, fast_hit: bool = False):
+        """One router-split gap on the flat list of selected global ids.
+
+        Returns the (local, slot) stream-ins in issue order.  Raises
+        GapOverflow where the reference raises RuntimeError."""
+        self.gaps += 1
+        ids_list = [int(v) for v in ids]
+        n_global = len(self.local_of)
+        if fast_hit and self.map_is_standing:
+            all_hit = True
+            for g in ids_list:
+                if 0 <= g < n_global:
+                    loc = self.local_of[g]
+                    if loc >= 0 and loc not in self.slot_of:
+                        all_hit = False
+                        break
+            if all_hit:
+                self.fast_hits += 1
+                return []
+        missing = []
+        hit_slots = set()
+        for g in sorted(set(ids_list)):
+            if not (0 <= g < n_global):
+                continue
+            loc = self.local_of[g]
+            if loc < 0:
+                continue
+            slot = self.slot_of.get(loc)
+            if slot is None:
+                missing.append(loc)
+            else:
+                hit_slots.add(slot)
+                self.touch(slot, True)
+        streams = []
+        changed = False
+        if missing:
+            claimed = set(hit_slots)
+            for loc in missing:
+                slot = self.acquire_slot(loc, claimed, True)
+                if slot is None:
+                    raise GapOverflow(
+                        "Sluice router-split: working set exceeds slots on a decode-sized "
+                        "step; raise SLUICE_SLOTS.")
+                streams.append((loc, slot))
+                claimed.add(slot)
+            self.misses += len(missing)
+            changed = True
+        if changed or not self.map_is_standing:
+            self.write_standing_map()
+        return streams
+
+    def snapshot(self) -> dict:
+        return {
+            "slot_of": [self.slot_of.get(l, -1) for l in range(self.local_n)],
+            "expert_in_slot": [-1 if v is None else v for v in self.expert_in_slot],
+            "probation": list(self.probation.keys()),
+            "protected": list(self.protected.keys()),
+            "free_slots": list(self.free_slots),
+            "map": list(self.map),
+            "map_is_standing": self.map_is_standing,
+        }

@@ -1,0 +1,482 @@
+"""Routing-aware MoE expert streaming offloader, router-split path, on MI355X.
+
+Mirrors the reference's ``ExpertStreamOffloader`` (src/sluice/offloader.py)
+for the router-split decode path: the same lifecycle (``wrap_modules`` ->
+``post_init`` -> ``attach_model``), the same env flags, the same slot-buffer
+and expert-map layout, the same ``vllm::sluice_stream_gap`` op and traced
+``_forward_entry``.  Underneath, the per-layer slot cache and the gap run in
+libsluice_hip.so: a device slot-lookup kernel publishes the step's selected
+experts into pinned host memory, the native SLRU assigns slots exactly as the
+reference's OrderedDict state machine does, missing experts stream with
+hipMemcpyAsync on a dedicated copy stream, and a map kernel rewrites the
+standing expert map the captured expert product reads by pointer.
+
+Execution model per MoE layer per decode step (T <= thr tokens):
+
+    gate + select_experts            [capturable]
+    -> vllm::sluice_stream_gap       [eager gap: lookup, wait, SLRU, H2D, map]
+    -> sluice::fused_experts         [capturable; slots + map by pointer]
+    -> shared experts                [capturable]
+
+Steps above the envelope would need the reference's classic wave path
+(src/sluice/offloader.py:1452-1933), which this build does not include; they
+fail closed with an error instead of computing anything wrong.
+"""
+
+
+import ctypes
+import logging
+import os
+from collections.abc import Generator
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from sluice_amd import _lib, ops
+
+logger = logging.getLogger("sluice")
+
+# Shared/global tensors, not per-expert weights (src/sluice/offloader.py:89-96).
+NON_EXPERT_WEIGHTS = frozenset(
+    {"e_score_correction_bias", "w13_input_scale", "w2_input_scale", "hash_indices_table"}
+)
+
+PROTECT_FRAC_ENV = "SLUICE_PROTECT_FRAC"
+ROUTER_SPLIT_ENV = "SLUICE_ROUTER_SPLIT"
+PIECEWISE_ENV = "SLUICE_PIECEWISE"
+FAST_HIT_ENV = "SLUICE_RS_FAST_HIT"
+NOOP_ENV = "SLUICE_RS_NOOP"
+
+
+@dataclass
+class _ExpertLayerCache:
+    """Per-layer streaming state (src/sluice/offloader.py:121-169).  The SLRU
+    state itself lives in the native layer object; the properties below read
+    it back in the reference's shapes for inspection and tests."""
+
+    local_num_experts: int
+    num_slots: int
+    protected_cap: int
+    device: torch.device
+    param_names: list = field(default_factory=list)
+    gpu_cache: dict = field(default_factory=dict)
+    cpu_store: dict = field(default_factory=dict)
+    host_stores: list = field(default_factory=list)
+    local_of: list = field(default_factory=list)
+    global_of_local: list = field(default_factory=list)
+    expert_map_buf: Optional[torch.Tensor] = None
+    bytes_per_expert: int = 0
+    static_full: bool = False
+    handle: Optional[int] = None
+
+    # -- native state views ------------------------------------------------
+    def _state(self):
+        lib = _lib.load()
+        S, L = self.num_slots, self.local_num_experts
+        slot_of = (ctypes.c_int32 * L)()
+        eis = (ctypes.c_int32 * S)()
+        prob = (ctypes.c_int32 * S)()
+        prot = (ctypes.c_int32 * S)()
+        free = (ctypes.c_int32 * S)()
+        n_prob, n_prot, n_free = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        ctr = (ctypes.c_int64 * 8)()
+        _lib.check(lib.sluice_layer_state(self.handle, slot_of, eis, prob, ctypes.byref(n_prob),
+                                          prot, ctypes.byref(n_prot), free, ctypes.byref(n_free),
+                                          ctr), "sluice_layer_state")
+        return {
+            "slot_of": list(slot_of),
+            "expert_in_slot": list(eis),
+            "probation": list(prob)[: n_prob.value],
+            "protected": list(prot)[: n_prot.value],
+            "free_slots": list(free)[: n_free.value],
+            "counters": list(ctr),
+        }
+
+    @property
+    def slot_of(self) -> dict:
+        return {l: s for l, s in enumerate(self._state()["slot_of"]) if s >= 0}
+
+    @property
+    def expert_in_slot(self) -> list:
+        return [None if v < 0 else v for v in self._state()["expert_in_slot"]]
+
+    @property
+    def probation(self) -> list:
+        return self._state()["probation"]
+
+    @property
+    def protected(self) -> list:
+        return self._state()["protected"]
+
+    @property
+    def free_slots(self) -> list:
+        return self._state()["free_slots"]
+
+    @property
+    def map_is_standing(self) -> bool:
+        return bool(self._state()["counters"][6])
+
+    def stats(self) -> dict:
+        c = self._state()["counters"]
+        return {"gaps": c[0], "misses": c[1], "fast_hits": c[2], "map_writes": c[3],
+                "bytes": c[4] | (c[5] << 32)}
+
+
+class ExpertStreamOffloader:
+    """Stream routed-expert weights host->HBM per decode step, by routing.
+
+    Args:
+        expert_cache_slots: HBM-resident expert slots per MoE layer.
+    """
+
+    def __init__(self, expert_cache_slots: int):
+        assert expert_cache_slots > 0
+        self.expert_cache_slots = expert_cache_slots
+        try:
+            frac = float(os.environ.get(PROTECT_FRAC_ENV, "0.5"))
+        except ValueError:
+            frac = 0.5
+        self.protect_frac = min(max(frac, 0.0), 0.9)
+        self.piecewise = os.environ.get(PIECEWISE_ENV, "0") == "1"
+        self.router_split = os.environ.get(ROUTER_SPLIT_ENV, "0") == "1"
+        self._rs_fast_hit = os.environ.get(FAST_HIT_ENV, "0") == "1"
+        self._rs_noop = os.environ.get(NOOP_ENV, "0") == "1"
+        if self._rs_noop:
+            logger.warning("Sluice: SLUICE_RS_NOOP=1 — the router-split gap is a NO-OP; "
+                           "OUTPUTS ARE INVALID (stale expert map). Perf diagnostic only.")
+        self.pin_memory = torch.cuda.is_available()
+        self._caches: dict[int, _ExpertLayerCache] = {}
+        self._layers: list[nn.Module] = []
+        self._rs_caches: list[_ExpertLayerCache] = []
+        self._rs_gaps = 0
+        self._rs_misses = 0
+        self._rs_fast_hits = 0
+        self._rs_layers = 0
+        self._rs_thr: Optional[int] = None
+        if self.router_split:
+            _register_stream_gap_op(self)
+        logger.info("Sluice ExpertStreamOffloader enabled (%d cache slots per layer, "
+                    "protect_frac=%.2f).", expert_cache_slots, self.protect_frac)
+
+    # -- model construction -------------------------------------------------
+    @staticmethod
+    def _is_moe_layer(module: nn.Module) -> bool:
+        return (hasattr(module, "local_num_experts") and hasattr(module, "global_num_experts")
+                and hasattr(module, "quant_method"))
+
+    @staticmethod
+    def _per_expert_params(module: nn.Module, local_n: int) -> dict:
+        return {
+            name: p for name, p in module.named_parameters(recurse=False)
+            if name not in NON_EXPERT_WEIGHTS and p.dim() >= 1 and p.shape[0] == local_n
+        }
+
+    def wrap_modules(self, modules_generator: Generator) -> list:
+        modules = []
+        for module in modules_generator:
+            for sub in module.modules():
+                if self._is_moe_layer(sub):
+                    self._prepare_layer(sub)
+            modules.append(module)
+        return modules
+
+    def _prepare_layer(self, module: nn.Module) -> None:
+        qm = module.quant_method
+        if qm is None or getattr(qm, "is_monolithic", False):
+            return
+        local_n = int(module.local_num_experts)
+        per_expert = self._per_expert_params(module, local_n)
+        if not per_expert:
+            return
+        for p in per_expert.values():
+            p.data = p.data.to("cpu")
+        if all(id(module) != id(m) for m in self._layers):
+            self._layers.append(module)
+
+    # -- after load -----------------------------------------------------------
+    def post_init(self, config=None) -> None:
+        self._check_config(config)
+        if torch.cuda.is_available():
+            torch.cuda.synchronize()
+        for module in self._layers:
+            self._install_cache(module)
+        if self._caches:
+            host = sum(c.bytes_per_expert * c.local_num_experts for c in self._caches.values()
+                       if not c.static_full)
+            vram = sum(c.bytes_per_expert * c.num_slots for c in self._caches.values())
+            logger.info("Sluice: %d MoE layers ready — host expert store %.1f GiB%s, HBM slot "
+                        "cache %.1f GiB.", len(self._caches), host / 2**30,
+                        " (pinned)" if self.pin_memory else " (pageable)", vram / 2**30)
+
+    def _check_config(self, cfg=None) -> None:
+        """Router-split envelope (src/sluice/offloader.py:807-842): under
+        piecewise capture the whole batch must fit slots//topk tokens."""
+        if cfg is None:
+            try:
+                from vllm.config import get_current_vllm_config
+
+                cfg = get_current_vllm_config()
+            except Exception:
+                cfg = None
+        if cfg is None:
+            return
+        if self.router_split and self.piecewise:
+            topk = 8
+            mc = getattr(cfg, "model_config", None)
+            hf = getattr(mc, "hf_config", None) if mc is not None else None
+            for src in (hf, getattr(hf, "text_config", None)):
+                v = getattr(src, "num_experts_per_tok", None) if src else None
+                if v:
+                    topk = int(v)
+                    break
+            thr = max(1, self.expert_cache_slots // topk)
+            self._rs_thr = thr
+            sched = getattr(cfg, "scheduler_config", None)
+            mbt = getattr(sched, "max_num_batched_tokens", None)
+            if mbt is not None and mbt > thr:
+                raise RuntimeError(
+                    "Sluice router-split under piecewise compiles a single trace whose size "
+                    "branch is resolved at trace time; the whole batch envelope must fit it. "
+                    f"Got max_num_batched_tokens={mbt} > slots//topk={thr}. Set "
+                    f"--max-num-batched-tokens {thr} (prefill runs in {thr}-token chunks) or "
+                    "raise SLUICE_SLOTS.")
+            cc = getattr(cfg, "compilation_config", None)
+            if cc is not None:
+                ops_ = list(getattr(cc, "splitting_ops", None) or [])
+                for op in ("vllm::moe_forward", "vllm::moe_forward_shared",
+                           "vllm::sluice_stream_gap"):
+                    if op not in ops_:
+                        ops_.append(op)
+                cc.splitting_ops = ops_
+
+    @staticmethod
+    def _infer_device(module: nn.Module) -> torch.device:
+        for t in list(module.parameters(recurse=False)) + list(module.buffers(recurse=False)):
+            if t is not None and t.device.type != "cpu":
+                return t.device
+        idx = torch.cuda.current_device() if torch.cuda.is_available() else 0
+        return torch.device("cuda", idx)
+
+    def _install_cache(self, module: nn.Module) -> None:
+        """Slot buffers [S, ...] as the live params, a pinned host store of
+        every local expert, the expert map and the native slot cache
+        (src/sluice/offloader.py:895-1044)."""
+        lib = _lib.load()
+        local_n = int(module.local_num_experts)
+        global_n = int(module.global_num_experts)
+        per_expert = self._per_expert_params(module, local_n)
+        if not per_expert:
+            return
+        device = self._infer_device(module)
+        num_slots = min(self.expert_cache_slots, local_n)
+        protected_cap = max(min(int(num_slots * self.protect_frac), num_slots - 1), 0)
+        cache = _ExpertLayerCache(local_num_experts=local_n, num_slots=num_slots,
+                                  protected_cap=protected_cap, device=device,
+                                  param_names=list(per_expert.keys()))
+        cache.static_full = num_slots >= local_n
+        for name, p in per_expert.items():
+            cpu = p.data if p.data.device.type == "cpu" else p.data.to("cpu")
+            slot = torch.empty((num_slots, *p.shape[1:]), dtype=p.dtype, device=device)
+            if cache.static_full:
+                slot.copy_(cpu)
+            else:
+                store = ops.HostStore(tuple(cpu.shape), cpu.dtype)
+                store.tensor.copy_(cpu)
+                cache.host_stores.append(store)
+                cache.cpu_store[name] = store.tensor
+            cache.gpu_cache[name] = slot
+            p.data = slot
+            cache.bytes_per_expert += cpu[0].nbytes
+        orig_map = getattr(module, "expert_map", None)
+        if orig_map is not None:
+            cache.local_of = [int(v) for v in orig_map.to("cpu").tolist()]
+        else:
+            cache.local_of = list(range(global_n))
+        cache.global_of_local = [-1] * local_n
+        for g, loc in enumerate(cache.local_of):
+            if 0 <= loc < local_n:
+                cache.global_of_local[loc] = g
+        cache.expert_map_buf = torch.full((global_n,), -1, dtype=torch.int32, device=device)
+        if cache.static_full:
+            for g, loc in enumerate(cache.local_of):
+                if loc >= 0:
+                    cache.expert_map_buf[g] = loc
+        module.register_buffer("_expert_map", cache.expert_map_buf, persistent=False)
+
+        h = ctypes.c_void_p()
+        _lib.check(lib.sluice_layer_create(global_n, local_n, num_slots, protected_cap,
+                                           _lib.int32_array(cache.local_of),
+                                           cache.expert_map_buf.data_ptr(), ctypes.byref(h)),
+                   "sluice_layer_create")
+        cache.handle = h.value
+        if not cache.static_full:
+            for name in cache.param_names:
+                slot_t = cache.gpu_cache[name]
+                host_t = cache.cpu_store[name]
+                _lib.check(lib.sluice_layer_add_param(cache.handle, slot_t.data_ptr(),
+                                                      host_t.data_ptr(), host_t[0].nbytes),
+                           "sluice_layer_add_param")
+        self._caches[id(module)] = cache
+        logger.info("Sluice: %d local experts -> %d HBM slots (%d protected), %d params/expert, "
+                    "%.1f MiB/expert.", local_n, num_slots, protected_cap, len(per_expert),
+                    cache.bytes_per_expert / 2**20)
+
+    # -- router split -----------------------------------------------------------
+    def attach_model(self, model: nn.Module) -> None:
+        self.attach_router_split(model)
+
+    def attach_router_split(self, model: nn.Module) -> None:
+        """Patch each eligible layer's ``runner._forward_entry`` with the traced
+        split path (src/sluice/offloader.py:2469-2635)."""
+        if not self.router_split:
+            return
+        patched = 0
+        skips: dict = {}
+        seen = 0
+        for module in model.modules():
+            cache = self._caches.get(id(module))
+            if cache is None:
+                continue
+            seen += 1
+            runner = getattr(module, "runner", None)
+            if runner is None:
+                skips["no-runner"] = skips.get("no-runner", 0) + 1
+                continue
+            if cache.static_full:
+                skips["static-full"] = skips.get("static-full", 0) + 1
+                continue
+            mc = getattr(runner, "moe_config", None)
+            topk = getattr(mc, "experts_per_token", None) if mc else None
+            if topk is None:
+                topk = getattr(module, "top_k", None) or 8
+            idx = len(self._rs_caches)
+            self._rs_caches.append(cache)
+            thr = self._rs_thr
+            if thr is None:
+                thr = max(1, min(16, self.expert_cache_slots // int(topk)))
+            se = getattr(runner, "_shared_experts", None)
+            shared_layer = getattr(se, "_layer", None) if se is not None else None
+            runner._forward_entry = _make_entry(
+                idx, module.w13_weight, module.w2_weight, int(module.global_num_experts),
+                cache.expert_map_buf, shared_layer, runner.router.select_experts,
+                runner._forward_entry, getattr(runner, "gate", None), thr,
+                getattr(module, "w13_weight_scale", None), getattr(module, "w2_weight_scale", None),
+                getattr(module, "block_shape", None))
+            patched += 1
+        self._rs_layers = patched
+        logger.warning("Sluice: ROUTER-SPLIT armed on %d/%d MoE layers. skips=%s", patched, seen,
+                       skips or "{}")
+
+    def _router_split_gap(self, idx: int, topk_ids: torch.Tensor) -> None:
+        """Body of ``vllm::sluice_stream_gap`` (src/sluice/offloader.py:2362-2467)."""
+        cache = self._rs_caches[idx]
+        self._rs_gaps += 1
+        if self._rs_gaps == 1 or self._rs_gaps % 2000 == 0:
+            logger.warning("Sluice DIAG[rs]: router-split layers=%d gap-calls=%d misses=%d "
+                           "fast-hits=%d%s", len(self._rs_caches), self._rs_gaps,
+                           self._rs_misses, self._rs_fast_hits,
+                           " NOOP-GAP(OUTPUTS INVALID)" if self._rs_noop else "")
+        if self._rs_noop:
+            return
+        ids = topk_ids if topk_ids.dtype == torch.int32 else topk_ids.to(torch.int32)
+        ids = ids.contiguous()
+        lib = _lib.load()
+        before = cache.stats() if logger.isEnabledFor(logging.DEBUG) else None
+        rc = lib.sluice_layer_gap(cache.handle, ids.data_ptr(), ids.numel(),
+                                  int(self._rs_fast_hit),
+                                  torch.cuda.current_stream(ids.device).cuda_stream)
+        if rc == _lib.SLUICE_E_OVERFLOW:
+            raise RuntimeError("Sluice router-split: working set exceeds slots on a "
+                               "decode-sized step; raise SLUICE_SLOTS.")
+        _lib.check(rc, "sluice_layer_gap")
+        if before is not None:
+            logger.debug("gap %d: %s", idx, cache.stats())
+
+    def gap_counters(self) -> dict:
+        tot = {"gaps": 0, "misses": 0, "fast_hits": 0, "map_writes": 0, "bytes": 0}
+        for c in self._rs_caches:
+            for k_, v in c.stats().items():
+                tot[k_] += v
+        return tot
+
+    def get_stats(self) -> dict:
+        c = self.gap_counters()
+        return {"rs": {"steps": c["gaps"], "hits": None, "misses": c["misses"],
+                       "bytes": c["bytes"], "waves": c["gaps"], "fast_hits": c["fast_hits"]}}
+
+    def close(self) -> None:
+        lib = _lib.load()
+        for c in self._caches.values():
+            if c.handle:
+                lib.sluice_layer_destroy(c.handle)
+                c.handle = None
+
+
+def _make_entry(idx, w13, w2, gne, emap, shared_layer, sel, orig, gate, thr, w13_scale, w2_scale,
+                block_shape):
+    """Bind one layer's tensors into a fresh traced entry; weights and map are
+    captured BY POINTER, the gap rewrites their contents
+    (src/sluice/offloader.py:2562-2603)."""
+
+    def _forward_entry(hs, rl, sei, iid, lname, unpad):
+        if hs.shape[0] > thr:
+            return orig(hs, rl, sei, iid, lname, unpad)
+        if gate is not None:
+            rl, _ = gate(hs)
+        tw, ti = sel(hidden_states=hs, router_logits=rl, input_ids=iid)
+        h = torch.ops.vllm.sluice_stream_gap(hs, ti, idx)
+        kw = {}
+        if w13_scale is not None:
+            kw = {"w1_scale": w13_scale, "w2_scale": w2_scale,
+                  "block_shape": list(block_shape or [128, 128])}
+        routed = torch.ops.sluice.fused_experts(h, w13, w2, tw, ti, activation="silu",
+                                                global_num_experts=gne, expert_map=emap, **kw)
+        if shared_layer is None:
+            return routed
+        sh = shared_layer(sei if sei is not None else hs)
+        return (sh, routed)
+
+    return _forward_entry
+
+
+# ---------------------------------------------------------------------------
+# vllm::sluice_stream_gap
+# ---------------------------------------------------------------------------
+_ACTIVE_GAP: dict = {"offloader": None}
+
+
+def _sluice_stream_gap_impl(hidden_states: torch.Tensor, topk_ids: torch.Tensor,
+                            layer_idx: int) -> torch.Tensor:
+    off = _ACTIVE_GAP["offloader"]
+    if off is None:
+        raise RuntimeError("vllm::sluice_stream_gap called with no active Sluice offloader")
+    off._router_split_gap(int(layer_idx), topk_ids)
+    return hidden_states.clone()
+
+
+def _register_stream_gap_op(offloader: ExpertStreamOffloader) -> None:
+    """Register ``vllm::sluice_stream_gap(Tensor hidden_states, Tensor topk_ids,
+    int layer_idx) -> Tensor`` once per process (src/sluice/offloader.py:
+    2296-2331); later offloaders rebind the implementation's target."""
+    _ACTIVE_GAP["offloader"] = offloader
+    if _ACTIVE_GAP.get("registered"):
+        return
+    try:
+        from vllm.utils.torch_utils import direct_register_custom_op  # type: ignore
+
+        def _fake(hidden_states, topk_ids, layer_idx):
+            return torch.empty_like(hidden_states)
+
+        direct_register_custom_op(op_name="sluice_stream_gap", op_func=_sluice_stream_gap_impl,
+                                  mutates_args=[], fake_impl=_fake)
+    except ImportError:
+        if not hasattr(torch.ops.vllm, "sluice_stream_gap"):
+            op = torch.library.custom_op("vllm::sluice_stream_gap", mutates_args=())(
+                _sluice_stream_gap_impl)
+
+            @op.register_fake
+            def _(hidden_states, topk_ids, layer_idx):
+                return torch.empty_like(hidden_states)
+    _ACTIVE_GAP["registered"] = True

@@ -1,0 +1,258 @@
+"""Device ops of the decode hot path, over the C ABI of libsluice_hip.so.
+
+  select_experts   top-k routing (replaces vLLM's runner.router.select_experts,
+                   called at src/sluice/offloader.py:2583-2585)
+  fused_experts    grouped SwiGLU product over slot buffers + weighted
+                   combine (replaces torch.ops.vllm.fused_experts as called at
+                   src/sluice/offloader.py:2590-2599)
+  HostStore        exact-size pinned host memory for the expert store
+
+Every call enqueues on torch's current stream and never synchronises.  The
+ops are registered with torch.library as ``sluice::fused_experts`` (and as
+``vllm::fused_experts`` when vLLM is not installed, so code written against
+the vLLM op name runs unchanged); their fake implementations make them
+traceable.
+"""
+
+
+import ctypes
+from typing import Optional
+
+import numpy as np
+import torch
+
+from sluice_amd import _lib
+
+_SCORING = {"softmax": 0, "sigmoid": 1}
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+# ---------------------------------------------------------------------------
+# Routing
+# ---------------------------------------------------------------------------
+def select_experts(router_logits: torch.Tensor, top_k: int, *, scoring: str = "softmax",
+                   renormalize: bool = False, routed_scaling_factor: float = 1.0,
+                   e_score_correction_bias: Optional[torch.Tensor] = None, num_expert_group: int = 1,
+                   topk_group: int = 1, ids_out: Optional[torch.Tensor] = None,
+                   weights_out: Optional[torch.Tensor] = None):
+    """router_logits [T,E] fp32/bf16 on the GPU -> (topk_weights [T,k] fp32,
+    topk_ids [T,k] int32)."""
+    lib = _lib.load()
+    if router_logits.dim() != 2:
+        raise ValueError("router_logits must be [T, E]")
+    if router_logits.dtype not in (torch.float32, torch.bfloat16):
+        router_logits = router_logits.float()
+    logits = router_logits.contiguous()
+    T, E = logits.shape
+    dev = logits.device
+    ids = ids_out if ids_out is not None else torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    w = weights_out if weights_out is not None else torch.empty((T, top_k), dtype=torch.float32,
+                                                                device=dev)
+    bias = e_score_correction_bias
+    if bias is not None:
+        bias = bias.to(device=dev, dtype=torch.float32).contiguous()
+    rc = lib.sluice_route_topk(
+        logits.data_ptr(), 1 if logits.dtype == torch.bfloat16 else 0, T, E, top_k,
+        _SCORING[scoring], int(bool(renormalize)), float(routed_scaling_factor), _ptr(bias),
+        int(num_expert_group), int(topk_group), ids.data_ptr(), w.data_ptr(), _stream(dev))
+    _lib.check(rc, "sluice_route_topk")
+    return w, ids
+
+
+# ---------------------------------------------------------------------------
+# Expert product
+# ---------------------------------------------------------------------------
+class _Workspace:
+    """One grow-only device workspace per device, shared by every layer (the
+    layers run one after another on one stream).  reserve() sizes it ahead of
+    graph capture so captured launches bake a pointer that never moves."""
+
+    def __init__(self):
+        self.buf: dict[int, torch.Tensor] = {}
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        cur = self.buf.get(idx)
+        if cur is None or cur.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    "sluice fused_experts workspace too small during graph capture; call "
+                    "sluice_amd.ops.reserve_workspace(...) before capturing")
+            cur = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            self.buf[idx] = cur
+        return cur
+
+
+_WS = _Workspace()
+
+
+def workspace_bytes(T: int, H: int, I: int, k: int) -> int:
+    return int(_lib.load().sluice_fused_experts_workspace(T, H, I, k))
+
+
+def reserve_workspace(device, max_tokens: int, H: int, I: int, k: int) -> None:
+    _WS.get(torch.device(device), workspace_bytes(max_tokens, H, I, k))
+
+
+def _fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+                        topk_weights: torch.Tensor, topk_ids: torch.Tensor, activation: str,
+                        global_num_experts: int, expert_map: Optional[torch.Tensor],
+                        w1_scale: Optional[torch.Tensor], w2_scale: Optional[torch.Tensor],
+                        block_shape: Optional[list[int]], routed_scaling_factor: float,
+                        shared_output: Optional[torch.Tensor]) -> torch.Tensor:
+    if activation != "silu":
+        raise NotImplementedError(f"activation {activation!r}: only 'silu' is on the path")
+    lib = _lib.load()
+    x = hidden_states
+    if x.dtype != torch.bfloat16:
+        raise TypeError("hidden_states must be bf16")
+    x = x.contiguous()
+    T, H = x.shape
+    S = w1.shape[0]
+    I = w2.shape[2]
+    if w1.shape[1] != 2 * I or w1.shape[2] != H or w2.shape[1] != H:
+        raise ValueError(f"bad expert shapes w13 {tuple(w1.shape)} w2 {tuple(w2.shape)}")
+    k = topk_ids.shape[1]
+    ids = topk_ids if topk_ids.dtype == torch.int32 else topk_ids.to(torch.int32)
+    ids = ids.contiguous()
+    tw = topk_weights if topk_weights.dtype == torch.float32 else topk_weights.float()
+    tw = tw.contiguous()
+    if expert_map is not None:
+        E = expert_map.shape[0]
+        emap = expert_map if expert_map.dtype == torch.int32 else expert_map.to(torch.int32)
+        emap_ptr = emap.data_ptr()
+    else:
+        E = global_num_experts if global_num_experts > 0 else S
+        emap_ptr = None
+    out = torch.empty_like(x)
+    if T == 0:
+        return out
+    nbytes = workspace_bytes(T, H, I, k)
+    ws = _WS.get(x.device, nbytes)
+    sh = None
+    if shared_output is not None:
+        sh = shared_output.contiguous()
+        if sh.dtype != torch.bfloat16 or sh.shape != x.shape:
+            raise ValueError("shared_output must be bf16 [T, H]")
+    stream = _stream(x.device)
+    if w1.dtype == torch.bfloat16:
+        rc = lib.sluice_fused_experts_bf16(
+            x.data_ptr(), w1.data_ptr(), w2.data_ptr(), tw.data_ptr(), ids.data_ptr(), emap_ptr,
+            T, H, I, k, E, S, float(routed_scaling_factor), _ptr(sh), ws.data_ptr(), ws.numel(),
+            out.data_ptr(), stream)
+        _lib.check(rc, "sluice_fused_experts_bf16")
+    elif w1.dtype in (torch.uint8, torch.float8_e4m3fn):
+        if w1_scale is None or w2_scale is None:
+            raise ValueError("fp8 experts need w1_scale and w2_scale")
+        bn, bk = (block_shape or [128, 128])[:2]
+        rc = lib.sluice_fused_experts_fp8(
+            x.data_ptr(), w1.data_ptr(), w1_scale.data_ptr(), w2.data_ptr(), w2_scale.data_ptr(),
+            int(bn), int(bk), tw.data_ptr(), ids.data_ptr(), emap_ptr, T, H, I, k, E, S,
+            float(routed_scaling_factor), _ptr(sh), ws.data_ptr(), ws.numel(), out.data_ptr(),
+            stream)
+        _lib.check(rc, "sluice_fused_experts_fp8")
+    else:
+        raise TypeError(f"unsupported expert dtype {w1.dtype}")
+    return out
+
+
+@torch.library.custom_op("sluice::fused_experts", mutates_args=())
+def fused_experts_op(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+                     topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+                     activation: str = "silu", global_num_experts: int = -1,
+                     expert_map: Optional[torch.Tensor] = None,
+                     w1_scale: Optional[torch.Tensor] = None,
+                     w2_scale: Optional[torch.Tensor] = None,
+                     block_shape: Optional[list[int]] = None,
+                     routed_scaling_factor: float = 1.0,
+                     shared_output: Optional[torch.Tensor] = None) -> torch.Tensor:
+    return _fused_experts_impl(hidden_states, w1, w2, topk_weights, topk_ids, activation,
+                               global_num_experts, expert_map, w1_scale, w2_scale, block_shape,
+                               routed_scaling_factor, shared_output)
+
+
+@fused_experts_op.register_fake
+def _(hidden_states, w1, w2, topk_weights, topk_ids, activation="silu", global_num_experts=-1,
+      expert_map=None, w1_scale=None, w2_scale=None, block_shape=None,
+      routed_scaling_factor=1.0, shared_output=None):
+    return torch.empty_like(hidden_states)
+
+
+def fused_experts(hidden_states, w1, w2, topk_weights, topk_ids, activation="silu",
+                  global_num_experts=-1, expert_map=None, **kw):
+    """Keyword surface of vLLM's fused_experts as the router-split entry uses it."""
+    return torch.ops.sluice.fused_experts(hidden_states, w1, w2, topk_weights, topk_ids,
+                                          activation=activation,
+                                          global_num_experts=global_num_experts,
+                                          expert_map=expert_map, **kw)
+
+
+def _vllm_present() -> bool:
+    try:
+        import vllm  # noqa: F401
+
+        return True
+    except Exception:
+        return False
+
+
+if not _vllm_present() and not hasattr(torch.ops.vllm, "fused_experts"):
+    @torch.library.custom_op("vllm::fused_experts", mutates_args=())
+    def _vllm_fused_experts(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+                            topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+                            activation: str = "silu", global_num_experts: int = -1,
+                            expert_map: Optional[torch.Tensor] = None,
+                            w1_scale: Optional[torch.Tensor] = None,
+                            w2_scale: Optional[torch.Tensor] = None,
+                            block_shape: Optional[list[int]] = None,
+                            routed_scaling_factor: float = 1.0,
+                            shared_output: Optional[torch.Tensor] = None) -> torch.Tensor:
+        return _fused_experts_impl(hidden_states, w1, w2, topk_weights, topk_ids, activation,
+                                   global_num_experts, expert_map, w1_scale, w2_scale,
+                                   block_shape, routed_scaling_factor, shared_output)
+
+    @_vllm_fused_experts.register_fake
+    def _(hidden_states, w1, w2, topk_weights, topk_ids, activation="silu",
+          global_num_experts=-1, expert_map=None, w1_scale=None, w2_scale=None,
+          block_shape=None, routed_scaling_factor=1.0, shared_output=None):
+        return torch.empty_like(hidden_states)
+
+
+# ---------------------------------------------------------------------------
+# Pinned host store
+# ---------------------------------------------------------------------------
+class HostStore:
+    """Exact-size pinned host buffer (hipHostMalloc) viewed as a CPU tensor.
+    Freed when the object is garbage collected; views keep it alive."""
+
+    def __init__(self, shape, dtype: torch.dtype):
+        lib = _lib.load()
+        n = int(np.prod(shape))
+        esz = torch.empty((), dtype=dtype).element_size()
+        self.nbytes = n * esz
+        p = ctypes.c_void_p()
+        _lib.check(lib.sluice_host_alloc(max(self.nbytes, 1), ctypes.byref(p)), "sluice_host_alloc")
+        self._ptr = p.value
+        raw = (ctypes.c_uint8 * max(self.nbytes, 1)).from_address(self._ptr)
+        arr = np.frombuffer(raw, dtype=np.uint8, count=self.nbytes)
+        self.tensor = torch.from_numpy(arr).view(dtype).view(*shape)
+        self.tensor._sluice_host_store = self  # keep the allocation alive with the view
+
+    def data_ptr(self) -> int:
+        return self._ptr
+
+    def __del__(self):
+        p = getattr(self, "_ptr", None)
+        if p and _lib._lib is not None:
+            try:
+                _lib._lib.sluice_host_free(p)
+            except Exception:
+                pass
+            self._ptr = None

@@ -1,0 +1,72 @@
+"""Host-only driver of the native slot cache (sluice_layer_* with no device
+map): runs the same bookkeeping the device gap runs, so the C++ state
+machine can be compared with the oracle and the golden vectors on the CPU."""
+
+import ctypes
+
+from sluice_amd import _lib
+
+
+class NativeCache:
+    def __init__(self, E, local_n, slots, protect_frac=0.5, local_of=None):
+        self.lib = _lib.load()
+        self.E, self.local_n = E, local_n
+        self.S = min(slots, local_n)
+        frac = min(max(float(protect_frac), 0.0), 0.9)
+        cap = max(min(int(self.S * frac), self.S - 1), 0)
+        lof = _lib.int32_array(local_of if local_of is not None else range(E))
+        h = ctypes.c_void_p()
+        _lib.check(self.lib.sluice_layer_create(E, local_n, self.S, cap, lof, None,
+                                                ctypes.byref(h)), "sluice_layer_create")
+        self.h = h.value
+        self._streams = (ctypes.c_int32 * (2 * max(self.S, 1)))()
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.lib.sluice_layer_destroy(self.h)
+            self.h = None
+
+    def pin(self, local, debit=True):
+        s = ctypes.c_int()
+        rc = self.lib.sluice_layer_pin(self.h, local, int(debit), ctypes.byref(s))
+        return None if rc else s.value
+
+    def gap(self, ids, fast_hit=False):
+        """Returns (streams, overflow)."""
+        arr = _lib.int32_array(ids)
+        n = ctypes.c_int()
+        mw = ctypes.c_int()
+        rc = self.lib.sluice_layer_gap_host(self.h, arr, len(ids), int(fast_hit), self._streams,
+                                            self.S, ctypes.byref(n), ctypes.byref(mw))
+        streams = [[self._streams[2 * i], self._streams[2 * i + 1]] for i in range(n.value)]
+        if rc == _lib.SLUICE_E_OVERFLOW:
+            return streams, True
+        _lib.check(rc, "sluice_layer_gap_host")
+        return streams, False
+
+    def state(self):
+        S, L = self.S, self.local_n
+        slot_of = (ctypes.c_int32 * L)()
+        eis = (ctypes.c_int32 * S)()
+        prob = (ctypes.c_int32 * S)()
+        prot = (ctypes.c_int32 * S)()
+        free = (ctypes.c_int32 * S)()
+        n_prob, n_prot, n_free = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        ctr = (ctypes.c_int64 * 8)()
+        m = (ctypes.c_int32 * self.E)()
+        _lib.check(self.lib.sluice_layer_state(self.h, slot_of, eis, prob, ctypes.byref(n_prob),
+                                               prot, ctypes.byref(n_prot), free,
+                                               ctypes.byref(n_free), ctr), "state")
+        _lib.check(self.lib.sluice_layer_standing_map(self.h, m), "standing_map")
+        return {
+            "slot_of": list(slot_of),
+            "expert_in_slot": list(eis),
+            "probation": list(prob)[: n_prob.value],
+            "protected": list(prot)[: n_prot.value],
+            "free_slots": list(free)[: n_free.value],
+            "standing_map": list(m),
+            "map_is_standing": bool(ctr[6]),
+            "protected_cap": int(ctr[7]),
+            "counters": {"gaps": ctr[0], "misses": ctr[1], "fast_hits": ctr[2],
+                         "map_writes": ctr[3]},
+        }

@@ -1,0 +1,57 @@
+"""The C-ABI library loads and exports every symbol include/sluice.h declares
+(no GPU work is started here)."""
+
+import ctypes
+import os
+import re
+
+from sluice_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    src = open(os.path.join(ROOT, "include", "sluice.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(sluice_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "sluice_route_topk" in names and "sluice_layer_gap" in names
+    assert len(names) >= 20
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = _declared()
+    for n in names:
+        assert hasattr(lib, n), f"{n} not exported by {_lib.LIB_PATH}"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_abi_version_and_errors(lib):
+    assert lib.sluice_abi_version() == 1
+    assert b"exceeds slots" in lib.sluice_strerror(_lib.SLUICE_E_OVERFLOW)
+    assert lib.sluice_strerror(0) == b"ok"
+
+
+def test_invalid_arguments_rejected_without_touching_the_gpu(lib):
+    # shape checks run before any HIP call
+    assert lib.sluice_route_topk(None, 0, 1, 0, 1, 0, 0, 1.0, None, 1, 1, None, None,
+                                 None) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_route_topk(None, 0, 1, 64, 17, 0, 0, 1.0, None, 1, 1, None, None,
+                                 None) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_moe_align(None, 1, 8, None, 64, 0, None, None) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_fused_experts_bf16(None, None, None, None, None, None, 1, 2048, 100, 8, 64,
+                                         8, 1.0, None, None, 0, None, None) == _lib.SLUICE_E_INVAL
+    h = ctypes.c_void_p()
+    assert lib.sluice_layer_create(64, 64, 0, 0, None, None, ctypes.byref(h)) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_layer_create(2048, 64, 8, 4, None, None,
+                                   ctypes.byref(h)) == _lib.SLUICE_E_INVAL
+
+
+def test_workspace_size_is_monotone(lib):
+    a = lib.sluice_fused_experts_workspace(1, 2048, 1408, 6)
+    b = lib.sluice_fused_experts_workspace(8, 2048, 1408, 6)
+    assert 0 < a < b
+    assert lib.sluice_moe_plan_ints(8, 6) == 4 + 18 * 48 + 48

@@ -1,0 +1,142 @@
+"""a3-a8 on the GPU: the device gap (slot-lookup kernel -> host record ->
+native SLRU -> hipMemcpyAsync of missing rows -> map kernel) replays the
+reference's golden traces bit for bit: stream-in order, slot assignment,
+segment order and the device expert map after every step, and every
+occupied slot's bytes equal the pinned host row of the expert it holds."""
+
+import types
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+class _Layer(nn.Module):
+    def __init__(self, E, local_n, H=64, I=32, expert_map=None):
+        super().__init__()
+        self.global_num_experts = E
+        self.local_num_experts = local_n
+        self.quant_method = types.SimpleNamespace()
+        g = torch.Generator().manual_seed(E * 1000 + local_n)
+        self.w13_weight = nn.Parameter(
+            torch.randn((local_n, 2 * I, H), generator=g).to(torch.bfloat16), requires_grad=False)
+        self.w2_weight = nn.Parameter(
+            torch.randn((local_n, H, I), generator=g).to(torch.bfloat16), requires_grad=False)
+        if expert_map is not None:
+            self.register_buffer("_orig_map", expert_map)
+
+    @property
+    def expert_map(self):
+        return getattr(self, "_expert_map", None) if hasattr(self, "_expert_map") else getattr(
+            self, "_orig_map", None)
+
+
+def _offloader(monkeypatch, slots, frac, fast_hit):
+    monkeypatch.setenv("SLUICE_ROUTER_SPLIT", "1")
+    monkeypatch.setenv("SLUICE_PROTECT_FRAC", str(frac))
+    monkeypatch.setenv("SLUICE_RS_FAST_HIT", "1" if fast_hit else "0")
+    from sluice_amd.offloader import ExpertStreamOffloader
+
+    return ExpertStreamOffloader(expert_cache_slots=slots)
+
+
+def _check_slots(cache, layer):
+    torch.cuda.synchronize()
+    for name in cache.param_names:
+        slot_t = cache.gpu_cache[name].cpu()
+        host_t = cache.cpu_store[name]
+        for s, loc in enumerate(cache.expert_in_slot):
+            if loc is not None:
+                assert torch.equal(slot_t[s].view(torch.int16), host_t[loc].view(torch.int16)), (
+                    name, s, loc)
+
+
+def _cases(golden):
+    return [i for i, c in enumerate(golden["cases"]) if not c["pins"]]
+
+
+def _case_ids():
+    from conftest import slru_vectors
+
+    g = slru_vectors()
+    return [f"{g['cases'][i]['name']}-fh{int(g['cases'][i]['fast_hit'])}" for i in _cases(g)]
+
+
+@pytest.mark.parametrize("idx", range(18), ids=_case_ids())
+def test_device_gap_replays_reference(monkeypatch, slru_golden, idx):
+    case = slru_golden["cases"][_cases(slru_golden)[idx]]
+    print(f"gap case {case['name']} fast_hit={case['fast_hit']}", flush=True)
+    E, local_n, k = case["E"], case["local_n"], case["k"]
+    emap = None
+    if case["local_of"] is not None:
+        emap = torch.tensor(case["local_of"], dtype=torch.int32)
+    layer = _Layer(E, local_n, expert_map=emap)
+    off = _offloader(monkeypatch, case["slots"], case["protect_frac"], case["fast_hit"])
+    off.wrap_modules(iter([layer]))
+    with torch.cuda.device(DEV):
+        off.post_init()
+    cache = off._caches[id(layer)]
+    off._rs_caches.append(cache)
+    assert cache.free_slots == case["init"]["free_slots"]
+    hs = torch.zeros((1, 64), dtype=torch.bfloat16, device=DEV)
+    for n, step in enumerate(case["steps"]):
+        ids = torch.tensor(step["ids"], dtype=torch.int32, device=DEV).view(-1, k)
+        overflow = False
+        try:
+            out = torch.ops.vllm.sluice_stream_gap(hs, ids, len(off._rs_caches) - 1)
+            assert out.data_ptr() != hs.data_ptr()
+        except RuntimeError as e:
+            assert "exceeds slots" in str(e)
+            overflow = True
+        assert overflow == step["overflow"], n
+        st = cache._state()
+        want = step["state"]
+        assert st["slot_of"] == want["slot_of"], n
+        assert st["expert_in_slot"] == want["expert_in_slot"], n
+        assert st["probation"] == want["probation"], n
+        assert st["protected"] == want["protected"], n
+        assert st["free_slots"] == want["free_slots"], n
+        if not overflow:
+            torch.cuda.synchronize()
+            assert cache.expert_map_buf.cpu().tolist() == want["map"], n
+        if n % 25 == 0 or n == len(case["steps"]) - 1:
+            _check_slots(cache, layer)
+    s = cache.stats()
+    assert s["gaps"] == case["counters"]["gaps"]
+    assert s["misses"] == case["counters"]["misses"]
+    assert s["fast_hits"] == case["counters"]["fast_hits"]
+    off.close()
+
+
+def test_slot_lookup_record(lib):
+    """The lookup kernel's record: sorted unique in-range ids and the count of
+    owned-but-unmapped ones, published with the requested stamp."""
+    import ctypes
+
+    from sluice_amd import _lib
+
+    E = 128
+    rng = np.random.default_rng(3)
+    ids = rng.integers(-5, E + 5, size=96).astype(np.int32)
+    emap = np.full(E, -1, np.int32)
+    emap[rng.choice(E, 40, replace=False)] = np.arange(40)
+    local_of = np.arange(E, dtype=np.int32)
+    local_of[::7] = -1
+    rec = torch.zeros(4 + 1024, dtype=torch.int32, device=DEV)
+    d = {n: torch.from_numpy(a).to(DEV) for n, a in
+         (("ids", ids), ("map", emap), ("lof", local_of))}
+    rc = lib.sluice_slot_lookup(d["ids"].data_ptr(), 96, d["map"].data_ptr(),
+                                d["lof"].data_ptr(), E, ctypes.c_void_p(rec.data_ptr()), 77,
+                                torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "lookup")
+    torch.cuda.synchronize()
+    r = rec.cpu().numpy()
+    uniq = sorted({int(g) for g in ids if 0 <= g < E})
+    assert r[0] == 77 and r[1] == len(uniq)
+    assert r[4:4 + r[1]].tolist() == uniq
+    assert r[2] == sum(1 for g in uniq if local_of[g] >= 0 and emap[g] < 0)

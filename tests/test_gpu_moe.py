@@ -1,0 +1,198 @@
+"""a9/a10 expert product + combine vs the oracle.  Align plan bit-exact;
+outputs within rel-L2 1e-2 (bf16 weights) and 3e-2 (fp8 e4m3fn weights,
+128x128 block scales), the tolerances the path is specified to."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as om
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+BF16_TOL = 1e-2
+FP8_TOL = 3e-2
+
+
+def _routing(T, E, k, rng):
+    return np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+
+
+def _emap(E, S, rng, resident_frac=1.0):
+    """global -> slot map with S resident experts (some selected ids may miss)."""
+    emap = np.full(E, -1, np.int32)
+    res = rng.choice(E, size=S, replace=False)
+    for s, g in enumerate(res):
+        if rng.random() < resident_frac:
+            emap[g] = s
+    return emap
+
+
+def _bf16(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("T,k,E,S,seed", [(1, 6, 64, 48, 0), (8, 6, 64, 48, 1), (12, 8, 128, 96, 2),
+                                          (40, 4, 16, 8, 3), (300, 8, 64, 64, 4), (0, 8, 64, 8, 5)])
+def test_align_plan_bit_exact(T, k, E, S, seed):
+    from sluice_amd import _lib
+
+    lib = _lib.load()
+    rng = np.random.default_rng(seed)
+    ids = _routing(T, E, k, rng) if T else np.zeros((0, k), np.int32)
+    emap = _emap(E, S, rng, resident_frac=0.8)
+    ids[0:1, 0:1] = E + 3 if T else 0  # an out-of-range id is simply invalid
+    n = _lib.load().sluice_moe_plan_ints(max(T, 1), k)
+    plan = torch.full((n,), -7, dtype=torch.int32, device=DEV)
+    ids_d = torch.from_numpy(ids).to(DEV)
+    emap_d = torch.from_numpy(emap).to(DEV)
+    rc = lib.sluice_moe_align(ids_d.data_ptr(), T, k, emap_d.data_ptr(), E, S, plan.data_ptr(),
+                              torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "align")
+    torch.cuda.synchronize()
+    p = plan.cpu().numpy()
+    print(f"align T={T} k={k} E={E} S={S}", flush=True)
+    blocks, valid = om.align_blocks(ids, emap, S, 16)
+    assert p[0] == len(blocks)
+    if T == 0:
+        return
+    P = T * k
+    for b, (slot, pairs) in enumerate(blocks):
+        rec = p[4 + 18 * b: 4 + 18 * (b + 1)]
+        assert rec[0] == slot and rec[1] == len(pairs)
+        assert rec[2:2 + len(pairs)].tolist() == pairs
+    assert p[4 + 18 * P: 4 + 19 * P].tolist() == valid
+
+
+def _moe_case(T, H, I, E, S, k, seed, resident_frac=0.85, use_map=True, scale=1.0, shared=False):
+    from sluice_amd import ops
+
+    rng = np.random.default_rng(seed)
+    x = _bf16(rng.standard_normal((T, H)))
+    w13 = _bf16(rng.standard_normal((S, 2 * I, H)) * 0.02)
+    w2 = _bf16(rng.standard_normal((S, H, I)) * 0.02)
+    ids = _routing(T, E if use_map else S, k, rng)
+    tw = rng.random((T, k)).astype(np.float32)
+    emap = _emap(E, S, rng, resident_frac) if use_map else None
+    sh = _bf16(rng.standard_normal((T, H))) if shared else None
+    out = ops.fused_experts(
+        x.to(DEV), w13.to(DEV), w2.to(DEV), torch.from_numpy(tw).to(DEV),
+        torch.from_numpy(ids).to(DEV), activation="silu",
+        global_num_experts=E, expert_map=None if emap is None else torch.from_numpy(emap).to(DEV),
+        routed_scaling_factor=scale, shared_output=None if sh is None else sh.to(DEV))
+    torch.cuda.synchronize()
+    ref = om.fused_experts(x.float().numpy(), w13.float().numpy(), w2.float().numpy(), tw, ids,
+                           expert_map=emap, scale=scale,
+                           shared=None if sh is None else sh.float().numpy())
+    return out.float().cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("T,H,I,E,S,k", [
+    (1, 2048, 1408, 64, 8, 6),      # V2-Lite expert shape, c=1
+    (8, 2048, 1408, 64, 12, 6),     # V2-Lite c=8
+    (1, 2048, 768, 128, 8, 8),      # Qwen3 c=1
+    (8, 2048, 768, 128, 16, 8),     # Qwen3 c=8
+    (12, 2048, 768, 128, 16, 8),    # Qwen3 c=12
+    (33, 256, 96, 16, 16, 4),       # > 16 pairs per slot: several blocks per expert
+])
+def test_fused_experts_bf16(T, H, I, E, S, k):
+    print(f"fused bf16 T={T} H={H} I={I} E={E} S={S} k={k}", flush=True)
+    got, ref = _moe_case(T, H, I, E, S, k, seed=T * 7 + I)
+    err = om.rel_l2(got, ref)
+    print(f"  rel_l2={err:.2e}", flush=True)
+    assert err <= BF16_TOL
+
+
+def test_fused_experts_bf16_identity_map_scale_shared():
+    got, ref = _moe_case(8, 512, 128, 8, 8, 2, seed=9, use_map=False, scale=2.5, shared=True)
+    assert om.rel_l2(got, ref) <= BF16_TOL
+
+
+def test_fused_experts_all_unmapped_is_zero():
+    got, ref = _moe_case(4, 256, 64, 32, 4, 2, seed=11, resident_frac=0.0)
+    assert np.all(got == 0) and np.all(ref == 0)
+
+
+def test_fused_experts_empty():
+    from sluice_amd import ops
+
+    x = torch.zeros((0, 256), dtype=torch.bfloat16, device=DEV)
+    w13 = torch.zeros((2, 128, 256), dtype=torch.bfloat16, device=DEV)
+    w2 = torch.zeros((2, 256, 64), dtype=torch.bfloat16, device=DEV)
+    out = ops.fused_experts(x, w13, w2, torch.zeros((0, 2), device=DEV),
+                            torch.zeros((0, 2), dtype=torch.int32, device=DEV))
+    assert out.shape == (0, 256)
+
+
+def _fp8_case(T, H, I, E, S, k, seed):
+    from sluice_amd import ops
+
+    rng = np.random.default_rng(seed)
+    x = _bf16(rng.standard_normal((T, H)))
+    q13 = torch.from_numpy(rng.standard_normal((S, 2 * I, H)).astype(np.float32) * 0.5).to(
+        torch.float8_e4m3fn).view(torch.uint8)
+    q2 = torch.from_numpy(rng.standard_normal((S, H, I)).astype(np.float32) * 0.5).to(
+        torch.float8_e4m3fn).view(torch.uint8)
+    s13 = (rng.random((S, 2 * I // 128, H // 128)) * 0.02 + 0.01).astype(np.float32)
+    s2 = (rng.random((S, H // 128, I // 128)) * 0.02 + 0.01).astype(np.float32)
+    ids = _routing(T, E, k, rng)
+    tw = rng.random((T, k)).astype(np.float32)
+    emap = _emap(E, S, rng, 0.9)
+    out = ops.fused_experts(
+        x.to(DEV), q13.to(DEV), q2.to(DEV), torch.from_numpy(tw).to(DEV),
+        torch.from_numpy(ids).to(DEV), global_num_experts=E,
+        expert_map=torch.from_numpy(emap).to(DEV), w1_scale=torch.from_numpy(s13).to(DEV),
+        w2_scale=torch.from_numpy(s2).to(DEV), block_shape=[128, 128])
+    torch.cuda.synchronize()
+    w13f = om.dequant_block(q13.numpy(), s13)
+    w2f = om.dequant_block(q2.numpy(), s2)
+    ref = om.fused_experts(x.float().numpy(), w13f, w2f, tw, ids, expert_map=emap)
+    return out.float().cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("T,H,I,E,S,k", [
+    (8, 7168, 2048, 256, 6, 8),     # DeepSeek-V3 expert shape
+    (1, 7168, 2048, 256, 4, 8),
+    (12, 512, 256, 16, 8, 4),
+])
+def test_fused_experts_fp8(T, H, I, E, S, k):
+    print(f"fused fp8 T={T} H={H} I={I} E={E} S={S} k={k}", flush=True)
+    got, ref = _fp8_case(T, H, I, E, S, k, seed=T + I)
+    err = om.rel_l2(got, ref)
+    print(f"  rel_l2={err:.2e}", flush=True)
+    assert err <= FP8_TOL
+
+
+def test_fp8_decode_all_bytes_exact():
+    """Every e4m3fn byte value decodes exactly: one expert whose gate row r
+    holds byte r at column 0 (NaN encodings zeroed), up rows hold 1.0, the
+    down projection is the identity, x = e_0 and all scales are 1, so
+    out[r] = silu(decode(r)) up to the bf16 rounding of the result."""
+    from sluice_amd import ops
+
+    H = I = 256
+    vals = np.arange(256, dtype=np.uint8)
+    vals[vals == 0x7F] = 0
+    vals[vals == 0xFF] = 0
+    q13 = np.zeros((1, 2 * I, H), np.uint8)
+    q13[0, :I, 0] = vals
+    q13[0, I:, 0] = 0x38  # 1.0
+    q2 = np.zeros((1, H, I), np.uint8)
+    q2[0, np.arange(H), np.arange(I)] = 0x38
+    s13 = np.ones((1, 2 * I // 128, H // 128), np.float32)
+    s2 = np.ones((1, H // 128, I // 128), np.float32)
+    x = torch.zeros((1, H), dtype=torch.bfloat16)
+    x[0, 0] = 1.0
+    out = ops.fused_experts(x.to(DEV), torch.from_numpy(q13).to(DEV), torch.from_numpy(q2).to(DEV),
+                            torch.ones((1, 1), device=DEV),
+                            torch.zeros((1, 1), dtype=torch.int32, device=DEV),
+                            w1_scale=torch.from_numpy(s13).to(DEV),
+                            w2_scale=torch.from_numpy(s2).to(DEV), block_shape=[128, 128])
+    torch.cuda.synchronize()
+    g = om.fp8_e4m3fn_to_f32(vals).astype(np.float64)
+    want = g / (1 + np.exp(-g))
+    got = out.float().cpu().numpy()[0]
+    np.testing.assert_allclose(got, want, rtol=8e-3, atol=1e-30)
