@@ -54,6 +54,9 @@ SIGNATURES = {
     ),
     "sluice_moe_plan_ints": (c_size_t, [c_int, c_int]),
     "sluice_moe_align": (c_int, [_P, c_int, c_int, _P, c_int, c_int, _P, _P]),
+    "sluice_moe_gemm1_bf16": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, _P, _P]),
+    "sluice_moe_gemm2_bf16": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, _P]),
+    "sluice_moe_combine": (c_int, [_P, _P, c_int, c_int, c_int, c_float, _P, _P, _P]),
     "sluice_layer_create": (c_int, [c_int, c_int, c_int, c_int, _P, _P, POINTER(c_void_p)]),
     "sluice_layer_destroy": (c_int, [_P]),
     "sluice_layer_add_param": (c_int, [_P, _P, _P, c_size_t]),

@@ -128,21 +128,44 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   }
 }
 
+// Tunables (compile-time): waves per workgroup splitting K, register
+// prefetch depth in 32-wide K chunks, and hidden rows per GEMM2 item.
+#ifndef SLUICE_G1_KS
+#define SLUICE_G1_KS 4
+#endif
+#ifndef SLUICE_G1_D
+#define SLUICE_G1_D 8
+#endif
+#ifndef SLUICE_G2_KS
+#define SLUICE_G2_KS 4
+#endif
+#ifndef SLUICE_G2_D
+#define SLUICE_G2_D 8
+#endif
+#ifndef SLUICE_G2_TILES
+#define SLUICE_G2_TILES 2
+#endif
+constexpr int kG1KS = SLUICE_G1_KS, kG1D = SLUICE_G1_D;
+constexpr int kG2KS = SLUICE_G2_KS, kG2D = SLUICE_G2_D, kG2T = SLUICE_G2_TILES;
+
 // ---------------------------------------------------------------------------
 // GEMM1: act[pair, i] = bf16(silu(gate) * up) for one 16-row intermediate
-// tile of one block.  bf16 weights.
+// tile of one block.  bf16 weights.  Each wave owns a contiguous K range and
+// keeps kG1D chunks (3 x 16 B per lane each) in flight: the loads for chunk
+// c + kG1D are issued as soon as chunk c has been consumed.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64 * kKS) void moe_gemm1_bf16_kernel(
+__global__ __launch_bounds__(64 * kG1KS) void moe_gemm1_bf16_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w13,
     const int32_t* __restrict__ plan, int H, int I, int k, uint16_t* __restrict__ act) {
-  __shared__ f32x4_t red[kKS][2][64];
+  __shared__ f32x4_t red[kG1KS][2][64];
   const int n_blocks = plan[0];
   const int n_tiles = I / 16;
   const int total = n_blocks * n_tiles;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kg = lane >> 4;
   const int nchunk = H / 32;
-  const int c0 = wave * nchunk / kKS, c1 = (wave + 1) * nchunk / kKS;
+  const int c0 = wave * nchunk / kG1KS, c1 = (wave + 1) * nchunk / kG1KS;
+  const int n = c1 - c0;
   const int32_t* blocks = plan + kPlanHeader;
 
   for (int item = blockIdx.x; item < total; item += gridDim.x) {
@@ -150,17 +173,36 @@ __global__ __launch_bounds__(64 * kKS) void moe_gemm1_bf16_kernel(
     const int32_t* blk = blocks + (size_t)b * kBlockInts;
     const int slot = blk[0], cnt = blk[1];
     const int pair = col < cnt ? blk[2 + col] : -1;
-    const uint16_t* wg = w13 + ((size_t)slot * 2 * I + (size_t)tile * 16 + col) * H + kg * 8;
+    const uint16_t* wg =
+        w13 + ((size_t)slot * 2 * I + (size_t)tile * 16 + col) * H + kg * 8 + c0 * 32;
     const uint16_t* wu = wg + (size_t)I * H;
-    const uint16_t* xr = x + (size_t)(pair >= 0 ? pair / k : 0) * H + kg * 8;
+    const uint16_t* xr = x + (size_t)(pair >= 0 ? pair / k : 0) * H + kg * 8 + c0 * 32;
+    const bool hx = pair >= 0;
     f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int c = c0; c < c1; ++c) {
-      const u32x4_t a0 = ldg16_stream(wg + c * 32);
-      const u32x4_t a1 = ldg16_stream(wu + c * 32);
-      const u32x4_t bx = pair >= 0 ? ldg16(xr + c * 32) : u32x4_t{0u, 0u, 0u, 0u};
-      ag = mfma16x16x32_bf16(a0, bx, ag);
-      au = mfma16x16x32_bf16(a1, bx, au);
+    u32x4_t rg[kG1D], ru[kG1D], rx[kG1D];
+#pragma unroll
+    for (int d = 0; d < kG1D; ++d) {
+      rx[d] = u32x4_t{0u, 0u, 0u, 0u};
+      if (d < n) {
+        rg[d] = ldg16_stream(wg + d * 32);
+        ru[d] = ldg16_stream(wu + d * 32);
+        if (hx) rx[d] = ldg16(xr + d * 32);
+      }
+    }
+    for (int base = 0; base < n; base += kG1D) {
+#pragma unroll
+      for (int d = 0; d < kG1D; ++d) {
+        if (base + d < n) {
+          ag = mfma16x16x32_bf16(rg[d], rx[d], ag);
+          au = mfma16x16x32_bf16(ru[d], rx[d], au);
+          const int nx = base + kG1D + d;
+          if (nx < n) {
+            rg[d] = ldg16_stream(wg + nx * 32);
+            ru[d] = ldg16_stream(wu + nx * 32);
+            if (hx) rx[d] = ldg16(xr + nx * 32);
+          }
+        }
+      }
     }
     red[wave][0][lane] = ag;
     red[wave][1][lane] = au;
@@ -168,7 +210,7 @@ __global__ __launch_bounds__(64 * kKS) void moe_gemm1_bf16_kernel(
     if (wave == 0 && pair >= 0) {
       f32x4_t g = red[0][0][lane], u = red[0][1][lane];
 #pragma unroll
-      for (int w = 1; w < kKS; ++w) {
+      for (int w = 1; w < kG1KS; ++w) {
         g += red[w][0][lane];
         u += red[w][1][lane];
       }
@@ -187,21 +229,23 @@ __global__ __launch_bounds__(64 * kKS) void moe_gemm1_bf16_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// GEMM2: partial[pair, h] = w[pair] * (W2[s] · act[pair])[h] for one
-// 16-row hidden tile of one block.  bf16 weights.
+// GEMM2: partial[pair, h] = w[pair] * (W2[s] · act[pair])[h] for kG2T
+// consecutive 16-row hidden tiles of one block (the act fragment is loaded
+// once per K chunk and feeds kG2T MFMAs).  bf16 weights.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64 * kKS) void moe_gemm2_bf16_kernel(
+__global__ __launch_bounds__(64 * kG2KS) void moe_gemm2_bf16_kernel(
     const uint16_t* __restrict__ act, const uint16_t* __restrict__ w2,
     const int32_t* __restrict__ plan, const float* __restrict__ topk_w, int H, int I,
     float* __restrict__ partial) {
-  __shared__ f32x4_t red[kKS][64];
+  __shared__ f32x4_t red[kG2KS][kG2T][64];
   const int n_blocks = plan[0];
-  const int n_tiles = H / 16;
+  const int n_tiles = H / (16 * kG2T);
   const int total = n_blocks * n_tiles;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kg = lane >> 4;
   const int nchunk = I / 32;
-  const int c0 = wave * nchunk / kKS, c1 = (wave + 1) * nchunk / kKS;
+  const int c0 = wave * nchunk / kG2KS, c1 = (wave + 1) * nchunk / kG2KS;
+  const int n = c1 - c0;
   const int32_t* blocks = plan + kPlanHeader;
 
   for (int item = blockIdx.x; item < total; item += gridDim.x) {
@@ -209,24 +253,53 @@ __global__ __launch_bounds__(64 * kKS) void moe_gemm2_bf16_kernel(
     const int32_t* blk = blocks + (size_t)b * kBlockInts;
     const int slot = blk[0], cnt = blk[1];
     const int pair = col < cnt ? blk[2 + col] : -1;
-    const uint16_t* wr = w2 + ((size_t)slot * H + (size_t)tile * 16 + col) * I + kg * 8;
-    const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I + kg * 8;
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int c = c0; c < c1; ++c) {
-      const u32x4_t a = ldg16_stream(wr + c * 32);
-      const u32x4_t bx = pair >= 0 ? ldg16(ar + c * 32) : u32x4_t{0u, 0u, 0u, 0u};
-      acc = mfma16x16x32_bf16(a, bx, acc);
+    const bool hx = pair >= 0;
+    const uint16_t* wr =
+        w2 + ((size_t)slot * H + (size_t)tile * 16 * kG2T + col) * I + kg * 8 + c0 * 32;
+    const uint16_t* ar = act + (size_t)(hx ? pair : 0) * I + kg * 8 + c0 * 32;
+    f32x4_t acc[kG2T];
+#pragma unroll
+    for (int t = 0; t < kG2T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    u32x4_t ra[kG2D][kG2T], rb[kG2D];
+#pragma unroll
+    for (int d = 0; d < kG2D; ++d) {
+      rb[d] = u32x4_t{0u, 0u, 0u, 0u};
+      if (d < n) {
+#pragma unroll
+        for (int t = 0; t < kG2T; ++t) ra[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + d * 32);
+        if (hx) rb[d] = ldg16(ar + d * 32);
+      }
     }
-    red[wave][lane] = acc;
+    for (int base = 0; base < n; base += kG2D) {
+#pragma unroll
+      for (int d = 0; d < kG2D; ++d) {
+        if (base + d < n) {
+#pragma unroll
+          for (int t = 0; t < kG2T; ++t) acc[t] = mfma16x16x32_bf16(ra[d][t], rb[d], acc[t]);
+          const int nx = base + kG2D + d;
+          if (nx < n) {
+#pragma unroll
+            for (int t = 0; t < kG2T; ++t)
+              ra[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + nx * 32);
+            if (hx) rb[d] = ldg16(ar + nx * 32);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kG2T; ++t) red[wave][t][lane] = acc[t];
     __syncthreads();
     if (wave == 0 && pair >= 0) {
-      f32x4_t s = red[0][lane];
-#pragma unroll
-      for (int w = 1; w < kKS; ++w) s += red[w][lane];
       const float wv = topk_w[pair];
-      f32x4_t o = {wv * s[0], wv * s[1], wv * s[2], wv * s[3]};
-      *reinterpret_cast<f32x4_t*>(partial + (size_t)pair * H + tile * 16 + kg * 4) = o;
+#pragma unroll
+      for (int t = 0; t < kG2T; ++t) {
+        f32x4_t s = red[0][t][lane];
+#pragma unroll
+        for (int w = 1; w < kG2KS; ++w) s += red[w][t][lane];
+        f32x4_t o = {wv * s[0], wv * s[1], wv * s[2], wv * s[3]};
+        *reinterpret_cast<f32x4_t*>(partial + (size_t)pair * H + (tile * kG2T + t) * 16 +
+                                    kg * 4) = o;
+      }
     }
     __syncthreads();
   }
@@ -459,7 +532,7 @@ int check_common(int T, int H, int I, int k, int E, int S, const void* x, const 
       S > SLUICE_MAX_SLOTS)
     return SLUICE_E_INVAL;
   if ((long)T * k > SLUICE_MAX_PAIRS) return SLUICE_E_INVAL;
-  if (H % 32 != 0 || I % 32 != 0) return SLUICE_E_INVAL;
+  if (H % 32 != 0 || H % (16 * kG2T) != 0 || I % 32 != 0) return SLUICE_E_INVAL;
   if (T == 0) return SLUICE_OK;
   if (!x || !w13 || !w2 || !tw || !ti || !ws || !out) return SLUICE_E_INVAL;
   if (ws_bytes < workspace_bytes(T, H, I, k, nullptr, nullptr)) return SLUICE_E_INVAL;
@@ -513,13 +586,50 @@ extern "C" int sluice_fused_experts_bf16(const void* x, const void* w13, const v
   hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, st, topk_ids, P,
                      expert_map, E, S, w.plan);
   SLUICE_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(moe_gemm1_bf16_kernel, dim3(grid_for(P, I / 16)), dim3(64 * kKS), 0, st,
+  hipLaunchKernelGGL(moe_gemm1_bf16_kernel, dim3(grid_for(P, I / 16)), dim3(64 * kG1KS), 0, st,
                      (const uint16_t*)x, (const uint16_t*)w13, w.plan, H, I, k, w.act);
   SLUICE_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(moe_gemm2_bf16_kernel, dim3(grid_for(P, H / 16)), dim3(64 * kKS), 0, st,
-                     w.act, (const uint16_t*)w2, w.plan, topk_w, H, I, w.partial);
+  hipLaunchKernelGGL(moe_gemm2_bf16_kernel, dim3(grid_for(P, H / (16 * kG2T))),
+                     dim3(64 * kG2KS), 0, st, w.act, (const uint16_t*)w2, w.plan, topk_w, H, I,
+                     w.partial);
   SLUICE_HIP_CHECK(hipGetLastError());
   return launch_combine(w, T, k, H, scale, shared, out, st);
+}
+
+extern "C" int sluice_moe_gemm1_bf16(const void* x, const void* w13, const int32_t* plan, int T,
+                                     int H, int I, int k, void* act, sluice_stream_t stream) {
+  if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % 32 || I % 32 || (long)T * k > SLUICE_MAX_PAIRS ||
+      !x || !w13 || !plan || !act)
+    return SLUICE_E_INVAL;
+  hipLaunchKernelGGL(moe_gemm1_bf16_kernel, dim3(grid_for(T * k, I / 16)), dim3(64 * kG1KS), 0,
+                     (hipStream_t)stream, (const uint16_t*)x, (const uint16_t*)w13, plan, H, I, k,
+                     (uint16_t*)act);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sluice_moe_gemm2_bf16(const void* act, const void* w2, const int32_t* plan,
+                                     const float* topk_w, int T, int H, int I, int k,
+                                     float* partial, sluice_stream_t stream) {
+  if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % (16 * kG2T) || I % 32 ||
+      (long)T * k > SLUICE_MAX_PAIRS || !act || !w2 || !plan || !topk_w || !partial)
+    return SLUICE_E_INVAL;
+  hipLaunchKernelGGL(moe_gemm2_bf16_kernel, dim3(grid_for(T * k, H / (16 * kG2T))),
+                     dim3(64 * kG2KS), 0, (hipStream_t)stream, (const uint16_t*)act,
+                     (const uint16_t*)w2, plan, topk_w, H, I, partial);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sluice_moe_combine(const float* partial, const int32_t* plan, int T, int k, int H,
+                                  float scale, const void* shared, void* out,
+                                  sluice_stream_t stream) {
+  if (T <= 0 || k <= 0 || H <= 0 || H % 4 || (long)T * k > SLUICE_MAX_PAIRS || !partial || !plan ||
+      !out)
+    return SLUICE_E_INVAL;
+  Workspace w;
+  w.plan = const_cast<int32_t*>(plan);
+  w.partial = const_cast<float*>(partial);
+  w.act = nullptr;
+  return launch_combine(w, T, k, H, scale, shared, out, (hipStream_t)stream);
 }
 
 extern "C" int sluice_fused_experts_fp8(const void* x, const void* w13, const float* w13_scale,

@@ -188,3 +188,473 @@ def build_offloaded(layers, slots: int, device=None, fast_hit: bool = True,
         off.post_init(config)
     off.attach_model(nn.ModuleList(layers))
     return off
+
+
+# ---------------------------------------------------------------------------
+# Synthetic decoder: model shapes, attention, graph pieces around the gap.
+# ---------------------------------------------------------------------------
+SPECS = {
+    # DeepSeek-V2-Lite: 27 layers (layer 0 dense), MLA attention, 64 routed
+    # experts top-6 (softmax greedy, no renorm) + 2 shared experts.
+    "v2lite": dict(vocab=102400, H=2048, layers=27, first_dense=1, dense_I=10944, E=64, k=6,
+                   I=1408, shared_I=2816, scoring="softmax", renorm=False, routed_scale=1.0,
+                   n_group=1, topk_group=1, e_bias=False, attn="mla", heads=16, kv_lora=512,
+                   qk_nope=128, qk_rope=64, v_head=128, rope_theta=10000.0, fp8=False),
+    # Qwen3-30B-A3B: 48 MoE layers, GQA 32/4 heads of 128 with q/k norm,
+    # 128 experts top-8 (softmax + renorm), no shared expert.
+    "qwen3": dict(vocab=151936, H=2048, layers=48, first_dense=0, dense_I=0, E=128, k=8, I=768,
+                  shared_I=0, scoring="softmax", renorm=True, routed_scale=1.0, n_group=1,
+                  topk_group=1, e_bias=False, attn="gqa", heads=32, kv_heads=4, head_dim=128,
+                  rope_theta=1e6, fp8=False),
+    # DeepSeek-V3 MoE stack (no attention): 8 layers, 256 experts top-8,
+    # sigmoid + bias group-limited (8 groups, top-4), scale 2.5, 1 shared
+    # expert, fp8 e4m3fn weights with 128x128 block scales.
+    "v3": dict(vocab=0, H=7168, layers=8, first_dense=0, dense_I=0, E=256, k=8, I=2048,
+               shared_I=2048, scoring="sigmoid", renorm=True, routed_scale=2.5, n_group=8,
+               topk_group=4, e_bias=True, attn=None, fp8=True),
+}
+
+
+def _rmsnorm(x, w, eps=1e-6):
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (xf * w.float()).to(x.dtype)
+
+
+def _rope(x, cos, sin):
+    """rotate-half RoPE; x [..., d], cos/sin broadcastable [..., d/2]."""
+    d = x.shape[-1] // 2
+    x1, x2 = x[..., :d].float(), x[..., d:].float()
+    return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).to(x.dtype)
+
+
+def _randn(shape, gen, std, dev, dtype=torch.bfloat16):
+    return (torch.randn(shape, generator=gen, device=dev) * std).to(dtype)
+
+
+class _MLA(nn.Module):
+    """Multi-head latent attention, decode form with the up-projections
+    absorbed: scores over the compressed KV latent and the rope key."""
+
+    def __init__(self, sp, batch, max_len, dev, gen):
+        super().__init__()
+        H, nh, lora = sp["H"], sp["heads"], sp["kv_lora"]
+        nope, rope, vh = sp["qk_nope"], sp["qk_rope"], sp["v_head"]
+        self.nh, self.lora, self.nope, self.rope, self.vh = nh, lora, nope, rope, vh
+        self.wq = _randn((nh * (nope + rope), H), gen, 0.02, dev)
+        self.wkva = _randn((lora + rope, H), gen, 0.02, dev)
+        self.kv_norm = torch.ones(lora, device=dev, dtype=torch.bfloat16)
+        self.w_uk = _randn((nh, nope, lora), gen, 0.02, dev)
+        self.w_uv = _randn((nh, lora, vh), gen, 0.02, dev)
+        self.wo = _randn((H, nh * vh), gen, 0.02, dev)
+        self.ckv = torch.zeros((batch, max_len, lora), device=dev, dtype=torch.bfloat16)
+        self.ckvT = torch.zeros((batch, lora, max_len), device=dev, dtype=torch.bfloat16)
+        self.kpeT = torch.zeros((batch, rope, max_len), device=dev, dtype=torch.bfloat16)
+        self.scale = (nope + rope) ** -0.5
+
+    def fill_prompt(self, n, gen):
+        b, _, lora = self.ckv.shape
+        lat = _randn((b, n, lora), gen, 1.0, self.ckv.device)
+        self.ckv[:, :n] = lat
+        self.ckvT[:, :, :n] = lat.transpose(1, 2)
+        self.kpeT[:, :, :n] = _randn((b, self.rope, n), gen, 1.0, self.ckv.device)
+
+    def forward(self, x, pos, bidx, cos, sin, mask):
+        c = x.shape[0]
+        q = F.linear(x, self.wq).view(c, self.nh, self.nope + self.rope)
+        q_nope, q_pe = q[..., : self.nope], q[..., self.nope:]
+        q_pe = _rope(q_pe, cos[:, None, :], sin[:, None, :])
+        kva = F.linear(x, self.wkva)
+        ckv = _rmsnorm(kva[:, : self.lora], self.kv_norm)
+        kpe = _rope(kva[:, self.lora:], cos, sin)
+        self.ckv[bidx, pos] = ckv
+        self.ckvT[bidx, :, pos] = ckv
+        self.kpeT[bidx, :, pos] = kpe
+        q_lat = torch.matmul(q_nope.transpose(0, 1).contiguous(), self.w_uk)  # [nh, c, lora]
+        q_lat = q_lat.transpose(0, 1).contiguous()
+        s = torch.matmul(q_lat, self.ckvT[:c]) + torch.matmul(q_pe.contiguous(), self.kpeT[:c])
+        p = torch.softmax(s.float() * self.scale + mask[:, None, :], dim=-1).to(x.dtype)
+        o_lat = torch.matmul(p, self.ckv[:c])  # [c, nh, lora]
+        o = torch.matmul(o_lat.transpose(0, 1).contiguous(), self.w_uv)  # [nh, c, vh]
+        return F.linear(o.transpose(0, 1).reshape(c, self.nh * self.vh), self.wo)
+
+
+class _GQA(nn.Module):
+    """Grouped-query attention with per-head q/k RMSNorm (Qwen3)."""
+
+    def __init__(self, sp, batch, max_len, dev, gen):
+        super().__init__()
+        H, nh, kvh, hd = sp["H"], sp["heads"], sp["kv_heads"], sp["head_dim"]
+        self.nh, self.kvh, self.hd = nh, kvh, hd
+        self.wqkv = _randn(((nh + 2 * kvh) * hd, H), gen, 0.02, dev)
+        self.q_norm = torch.ones(hd, device=dev, dtype=torch.bfloat16)
+        self.k_norm = torch.ones(hd, device=dev, dtype=torch.bfloat16)
+        self.wo = _randn((H, nh * hd), gen, 0.02, dev)
+        self.kT = torch.zeros((batch, kvh, hd, max_len), device=dev, dtype=torch.bfloat16)
+        self.v = torch.zeros((batch, kvh, max_len, hd), device=dev, dtype=torch.bfloat16)
+        self.scale = hd ** -0.5
+
+    def fill_prompt(self, n, gen):
+        b = self.v.shape[0]
+        self.kT[:, :, :, :n] = _randn((b, self.kvh, self.hd, n), gen, 1.0, self.v.device)
+        self.v[:, :, :n] = _randn((b, self.kvh, n, self.hd), gen, 1.0, self.v.device)
+
+    def forward(self, x, pos, bidx, cos, sin, mask):
+        c = x.shape[0]
+        qkv = F.linear(x, self.wqkv)
+        q = qkv[:, : self.nh * self.hd].view(c, self.nh, self.hd)
+        k = qkv[:, self.nh * self.hd: (self.nh + self.kvh) * self.hd].view(c, self.kvh, self.hd)
+        v = qkv[:, (self.nh + self.kvh) * self.hd:].view(c, self.kvh, self.hd)
+        q = _rope(_rmsnorm(q, self.q_norm), cos[:, None, :], sin[:, None, :])
+        k = _rope(_rmsnorm(k, self.k_norm), cos[:, None, :], sin[:, None, :])
+        self.kT[bidx, :, :, pos] = k
+        self.v[bidx, :, pos] = v
+        qg = q.view(c, self.kvh, self.nh // self.kvh, self.hd)
+        s = torch.matmul(qg, self.kT[:c])  # [c, kvh, g, L]
+        p = torch.softmax(s.float() * self.scale + mask[:, None, None, :], dim=-1).to(x.dtype)
+        o = torch.matmul(p, self.v[:c])  # [c, kvh, g, hd]
+        return F.linear(o.reshape(c, self.nh * self.hd), self.wo)
+
+
+class _DenseMLP(nn.Module):
+    def __init__(self, H, I, dev, gen):
+        super().__init__()
+        self.gate_up = _randn((2 * I, H), gen, 0.02, dev)
+        self.down = _randn((H, I), gen, 0.02, dev)
+        self.I = I
+
+    def forward(self, x):
+        gu = F.linear(x, self.gate_up)
+        return F.linear(F.silu(gu[:, : self.I]) * gu[:, self.I:], self.down)
+
+
+def _expert_store(sp, gen_seed, dev, fp8):
+    """One pinned host store of every expert of a layer ([E, ...] per param),
+    filled from device-generated random values (N(0, 0.02) for bf16; for fp8,
+    e4m3fn codes of N(0, 0.5) with block scales in [0.01, 0.03))."""
+    E, H, I = sp["E"], sp["H"], sp["I"]
+    g = torch.Generator(device=dev).manual_seed(gen_seed)
+    out = {}
+    shapes = {"w13_weight": (E, 2 * I, H), "w2_weight": (E, H, I)}
+    for name, shp in shapes.items():
+        dt = torch.uint8 if fp8 else torch.bfloat16
+        st = ops.HostStore(shp, dt)
+        for e in range(E):
+            if fp8:
+                v = (torch.randn(shp[1:], generator=g, device=dev) * 0.5).to(
+                    torch.float8_e4m3fn).view(torch.uint8)
+            else:
+                v = (torch.randn(shp[1:], generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            st.tensor[e].copy_(v)
+        out[name] = st
+    if fp8:
+        for name, shp in (("w13_weight_scale", (E, 2 * I // 128, H // 128)),
+                          ("w2_weight_scale", (E, H // 128, I // 128))):
+            st = ops.HostStore(shp, torch.float32)
+            st.tensor.copy_(torch.rand(shp, generator=g, device=dev) * 0.02 + 0.01)
+            out[name] = st
+    return out
+
+
+class _StoreMoELayer(nn.Module):
+    """FusedMoE-shaped layer whose per-expert params ARE pinned host stores
+    (possibly shared between layers), adopted by the offloader without a copy."""
+
+    def __init__(self, sp, store, seed, dev, routing_bias, name):
+        super().__init__()
+        E, H = sp["E"], sp["H"]
+        g = torch.Generator(device=dev).manual_seed(5000 + seed)
+        self.H, self.I, self.E, self.top_k = H, sp["I"], E, sp["k"]
+        self.layer_name = name
+        self.global_num_experts = E
+        self.local_num_experts = E
+        self.quant_method = _QuantMethod()
+        for pname, st in store.items():
+            setattr(self, pname, nn.Parameter(st.tensor, requires_grad=False))
+        self.block_shape = [128, 128] if sp["fp8"] else None
+        self.gate = nn.Module()
+        self.gate.weight = nn.Parameter(_randn((E, H), g, 0.02, dev), requires_grad=False)
+        self.e_score_correction_bias = (
+            nn.Parameter(torch.randn(E, generator=g, device=dev) * 0.01, requires_grad=False)
+            if sp["e_bias"] else None)
+        self.shared = (_DenseMLP(H, sp["shared_I"], dev, g) if sp["shared_I"] else None)
+        self.routing_bias = routing_bias
+        self.sp = sp
+
+        # vLLM runner surface, so attach_router_split arms this layer
+        layer = self
+
+        def gate(hs):
+            return layer.logits(hs), None
+
+        def select_experts(hidden_states, router_logits, input_ids=None):
+            return layer.select(router_logits)
+
+        def stock_entry(hs, rl, sei, iid, lname, unpad):
+            raise RuntimeError(f"{lname}: {hs.shape[0]} tokens exceed the router-split envelope")
+
+        self.runner = types.SimpleNamespace(
+            gate=gate, router=types.SimpleNamespace(select_experts=select_experts),
+            _shared_experts=(types.SimpleNamespace(_layer=self.shared) if self.shared else None),
+            moe_config=types.SimpleNamespace(experts_per_token=self.top_k, pcp_size=1),
+            _forward_entry=stock_entry)
+
+    @property
+    def expert_map(self):
+        return self._buffers.get("_expert_map")
+
+    def forward(self, hs: torch.Tensor) -> torch.Tensor:
+        r = self.runner._forward_entry(hs, None, None, None, self.layer_name, False)
+        if isinstance(r, tuple):
+            sh, routed = r
+            return routed + sh
+        return r
+
+    def logits(self, hn):
+        lg = F.linear(hn, self.gate.weight).float()
+        if self.routing_bias is not None:
+            lg = lg + self.routing_bias(hn.shape[0])
+        return lg
+
+    def select(self, lg):
+        sp = self.sp
+        return ops.select_experts(lg, sp["k"], scoring=sp["scoring"], renormalize=sp["renorm"],
+                                  routed_scaling_factor=sp["routed_scale"],
+                                  e_score_correction_bias=self.e_score_correction_bias,
+                                  num_expert_group=sp["n_group"], topk_group=sp["topk_group"])
+
+    def experts(self, hn, tw, ti):
+        kw = {}
+        if self.sp["fp8"]:
+            kw = dict(w1_scale=self.w13_weight_scale, w2_scale=self.w2_weight_scale,
+                      block_shape=[128, 128])
+        return ops.fused_experts(hn, self.w13_weight, self.w2_weight, tw, ti,
+                                 global_num_experts=self.E, expert_map=self._expert_map, **kw)
+
+
+class SyntheticDecoder:
+    """Random-init decoder of a SPECS shape, decoded in hipGraph pieces.
+
+    Piece p holds everything between MoE layer p-1's gap and MoE layer p's
+    gap: MoE layer p-1's expert product + shared experts + residual, every
+    dense/attention block up to MoE layer p, and MoE layer p's norm, gate and
+    top-k routing.  The last piece ends with the final norm, the LM head and
+    the greedy next-token write.  Between pieces the eager gap runs.
+    Prompts are synthetic: the first ``prompt_len`` KV positions hold random
+    latents/keys/values; decoding starts at position ``prompt_len``."""
+
+    def __init__(self, spec: str, max_batch: int, slots: int, prompt_len: int = 128,
+                 gen_len: int = 256, seed: int = 0, device=None, shared_host_pool: bool = True,
+                 zipf_s: float = 1.1, rho: float = 0.7, sigma: float = 1.0,
+                 uniform_routing: bool = False, fast_hit: bool = True, layers: int = None):
+        self.sp = sp = dict(SPECS[spec])
+        if layers is not None:
+            sp["layers"] = layers
+        self.name = spec
+        dev = self.dev = device or torch.device("cuda", torch.cuda.current_device())
+        self.max_batch, self.max_len = max_batch, prompt_len + gen_len + 8
+        self.prompt_len = prompt_len
+        g = torch.Generator(device=dev).manual_seed(seed)
+        H = sp["H"]
+        steps_tbl = gen_len + 64
+        self.has_attn = sp["attn"] is not None
+        self.embed = _randn((sp["vocab"], H), g, 0.02, dev) if self.has_attn else None
+        self.lm_head = _randn((sp["vocab"], H), g, 0.02, dev) if self.has_attn else None
+        self.final_norm = torch.ones(H, device=dev, dtype=torch.bfloat16)
+        self.blocks = []
+        self.moe_layers = []
+        self.bias_tables = []
+        store = None
+        for li in range(sp["layers"]):
+            blk = types.SimpleNamespace(attn=None, mlp=None, moe=None,
+                                        n1=torch.ones(H, device=dev, dtype=torch.bfloat16),
+                                        n2=torch.ones(H, device=dev, dtype=torch.bfloat16))
+            if sp["attn"] == "mla":
+                blk.attn = _MLA(sp, max_batch, self.max_len, dev, g)
+            elif sp["attn"] == "gqa":
+                blk.attn = _GQA(sp, max_batch, self.max_len, dev, g)
+            if blk.attn is not None:
+                blk.attn.fill_prompt(prompt_len, g)
+            if li < sp["first_dense"]:
+                blk.mlp = _DenseMLP(H, sp["dense_I"], dev, g)
+            else:
+                if store is None or not shared_host_pool:
+                    store = _expert_store(sp, 7000 + li, dev, sp["fp8"])
+                rb = None
+                if uniform_routing:
+                    rb = RoutingBias(sp["E"], max_batch, steps_tbl, 0.0, 0.0, 0.0, 8000 + li, dev)
+                    rb.table.normal_(generator=g)
+                    rb.table.mul_(10.0)
+                else:
+                    rb = RoutingBias(sp["E"], max_batch, steps_tbl, zipf_s, rho, sigma, 8000 + li,
+                                     dev)
+                self.bias_tables.append(rb)
+                blk.moe = _StoreMoELayer(sp, store, li, dev, rb, f"layers.{li}.mlp")
+                self.moe_layers.append(blk.moe)
+            self.blocks.append(blk)
+        self.off = build_offloaded([m for m in self.moe_layers], slots, dev, fast_hit=fast_hit)
+        self.caches = [self.off._caches[id(m)] for m in self.moe_layers]
+        assert [id(c) for c in self.off._rs_caches] == [id(c) for c in self.caches]
+        for m in self.moe_layers:
+            ops.reserve_workspace(dev, max_batch, H, sp["I"], sp["k"])
+        rope_d = (sp["qk_rope"] if sp["attn"] == "mla" else sp.get("head_dim", 128))
+        inv = 1.0 / (sp.get("rope_theta", 1e4) ** (torch.arange(0, rope_d, 2, device=dev).float()
+                                                     / rope_d))
+        ang = torch.arange(self.max_len, device=dev).float()[:, None] * inv[None, :]
+        self.cos_tbl, self.sin_tbl = ang.cos(), ang.sin()
+        # per-batch-size static state
+        self.state = {}
+        self.graphs = {}
+        self.pool = None
+
+    # -- state -----------------------------------------------------------------
+    def _state(self, c):
+        st = self.state.get(c)
+        if st is None:
+            dev = self.dev
+            g = torch.Generator(device=dev).manual_seed(99 + c)
+            st = types.SimpleNamespace()
+            st.c = c
+            st.pos = torch.full((c,), self.prompt_len, dtype=torch.long, device=dev)
+            st.bidx = torch.arange(c, device=dev)
+            st.tokens = (torch.randint(0, max(self.sp["vocab"], 1), (c,), generator=g, device=dev)
+                         if self.has_attn else None)
+            st.x = _randn((c, self.sp["H"]), g, 1.0, dev)  # MoE-stack input
+            st.out_tokens = []
+            self.state[c] = st
+        return st
+
+    def reset(self, c):
+        st = self._state(c)
+        st.pos.fill_(self.prompt_len)
+        for rb in self.bias_tables:
+            rb.step.zero_()
+
+    # -- pieces ----------------------------------------------------------------
+    def _attn_block(self, blk, x, st):
+        c = x.shape[0]
+        cos = self.cos_tbl.index_select(0, st.pos)
+        sin = self.sin_tbl.index_select(0, st.pos)
+        ar = torch.arange(self.max_len, device=self.dev)
+        mask = torch.where(ar[None, :] <= st.pos[:, None], 0.0, float("-inf"))
+        return x + blk.attn(_rmsnorm(x, blk.n1), st.pos, st.bidx[:c], cos, sin, mask)
+
+    def _run_until_moe(self, start, x, st):
+        """Blocks from index `start` up to (not including) the next MoE
+        block's experts; returns (x, h, hn, moe_block_index or None)."""
+        i = start
+        while i < len(self.blocks):
+            blk = self.blocks[i]
+            if blk.attn is not None:
+                x = self._attn_block(blk, x, st)
+            if blk.moe is None:
+                x = x + blk.mlp(_rmsnorm(x, blk.n2))
+                i += 1
+                continue
+            hn = _rmsnorm(x, blk.n2)
+            return x, hn, i
+        return x, None, None
+
+    def pieces(self, c):
+        """List of (piece_fn, gap_layer_index or None); piece_fn(io) mutates io."""
+        st = self._state(c)
+        out = []
+        moe_pos = [i for i, b in enumerate(self.blocks) if b.moe is not None]
+
+        def first(io):
+            if self.has_attn:
+                x = self.embed.index_select(0, st.tokens)
+            else:
+                x = st.x.clone()
+            x, hn, i = self._run_until_moe(0, x, st)
+            blk = self.blocks[i]
+            lg = blk.moe.logits(hn)
+            tw, ti = blk.moe.select(lg)
+            io.update(x=x, hn=hn, tw=tw, ti=ti, i=i)
+
+        out.append((first, 0))
+        for n, i in enumerate(moe_pos):
+            last = n == len(moe_pos) - 1
+
+            def mid(io, i=i, last=last):
+                blk = self.blocks[i]
+                routed = blk.moe.experts(io["hn"], io["tw"], io["ti"])
+                if blk.moe.shared is not None:
+                    routed = routed + blk.moe.shared(io["hn"])
+                x = io["x"] + routed
+                if not last:
+                    x, hn, j = self._run_until_moe(i + 1, x, st)
+                    nb = self.blocks[j]
+                    lg = nb.moe.logits(hn)
+                    tw, ti = nb.moe.select(lg)
+                    io.update(x=x, hn=hn, tw=tw, ti=ti, i=j)
+                else:
+                    x, _, _ = self._run_until_moe(i + 1, x, st)
+                    if self.has_attn:
+                        logits = F.linear(_rmsnorm(x, self.final_norm), self.lm_head)
+                        st.tokens.copy_(torch.argmax(logits.float(), dim=-1))
+                        st.pos.add_(1)
+                    else:
+                        st.x.copy_(_rmsnorm(x, self.final_norm))
+                    for rb in self.bias_tables:
+                        rb.step.add_(1)
+                    io.update(x=x)
+
+            out.append((mid, n + 1 if not last else None))
+        return out
+
+    # -- execution ---------------------------------------------------------------
+    def gap(self, n, ti):
+        self.off._router_split_gap(n, ti)
+
+    def step_eager(self, c):
+        """One eager step; the gap goes through the registered
+        ``vllm::sluice_stream_gap`` op and its output feeds the experts."""
+        from sluice_amd.offloader import activate
+
+        activate(self.off)
+        io = {}
+        ps = self.pieces(c)
+        for fn, gap_idx in ps:
+            fn(io)
+            if gap_idx is not None:
+                io["hn"] = torch.ops.vllm.sluice_stream_gap(io["hn"], io["ti"], gap_idx)
+        return io
+
+    def capture(self, c, warmup: int = 2):
+        """Capture every piece for batch size c (after eager warmup steps)."""
+        st = self._state(c)
+        for _ in range(warmup):
+            self.step_eager(c)
+        torch.cuda.synchronize()
+        ps = self.pieces(c)
+        graphs = []
+        io = {}
+        if self.pool is None:
+            self.pool = torch.cuda.graph_pool_handle()
+        s = torch.cuda.Stream(device=self.dev)
+        s.wait_stream(torch.cuda.current_stream())
+        for fn, gap_idx in ps:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=self.pool, stream=s):
+                fn(io)
+            graphs.append((g, gap_idx, dict(io)))
+            if gap_idx is not None:
+                # the captured pieces run only on replay; the recorded routing
+                # tensors are what the gap will read after each replay
+                pass
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        self.graphs[c] = graphs
+        self.reset(c)
+        return graphs
+
+    def step_graphs(self, c):
+        graphs = self.graphs[c]
+        for g, gap_idx, io in graphs:
+            g.replay()
+            if gap_idx is not None:
+                self.gap(gap_idx, io["ti"])
+
+    def gap_counters(self):
+        return self.off.gap_counters()

@@ -282,10 +282,16 @@ class ExpertStreamOffloader:
             if cache.static_full:
                 slot.copy_(cpu)
             else:
-                store = ops.HostStore(tuple(cpu.shape), cpu.dtype)
-                store.tensor.copy_(cpu)
+                store = ops.host_store_of(cpu)
+                if store is not None:
+                    # already pinned (e.g. one host pool shared by several
+                    # layers): adopt it as the host store, no copy
+                    cache.cpu_store[name] = cpu
+                else:
+                    store = ops.HostStore(tuple(cpu.shape), cpu.dtype)
+                    store.tensor.copy_(cpu)
+                    cache.cpu_store[name] = store.tensor
                 cache.host_stores.append(store)
-                cache.cpu_store[name] = store.tensor
             cache.gpu_cache[name] = slot
             p.data = slot
             cache.bytes_per_expert += cpu[0].nbytes
@@ -454,6 +460,12 @@ def _sluice_stream_gap_impl(hidden_states: torch.Tensor, topk_ids: torch.Tensor,
         raise RuntimeError("vllm::sluice_stream_gap called with no active Sluice offloader")
     off._router_split_gap(int(layer_idx), topk_ids)
     return hidden_states.clone()
+
+
+def activate(offloader: ExpertStreamOffloader) -> None:
+    """Make ``offloader`` the one ``vllm::sluice_stream_gap`` dispatches to
+    (the op is process-global; the newest offloader is active by default)."""
+    _ACTIVE_GAP["offloader"] = offloader
 
 
 def _register_stream_gap_op(offloader: ExpertStreamOffloader) -> None:

@@ -228,9 +228,25 @@ if not _vllm_present() and not hasattr(torch.ops.vllm, "fused_experts"):
 # ---------------------------------------------------------------------------
 # Pinned host store
 # ---------------------------------------------------------------------------
+_HOST_STORES: dict = {}  # base address -> HostStore (live allocations)
+
+
+def host_store_of(t: torch.Tensor):
+    """The HostStore whose allocation holds all of tensor ``t`` (a CPU
+    tensor), or None."""
+    if t.device.type != "cpu":
+        return None
+    lo = t.data_ptr()
+    hi = lo + t.numel() * t.element_size()
+    for base, st in _HOST_STORES.items():
+        if base <= lo and hi <= base + st.nbytes:
+            return st
+    return None
+
+
 class HostStore:
     """Exact-size pinned host buffer (hipHostMalloc) viewed as a CPU tensor.
-    Freed when the object is garbage collected; views keep it alive."""
+    Owners keep the HostStore object alive; the memory is freed with it."""
 
     def __init__(self, shape, dtype: torch.dtype):
         lib = _lib.load()
@@ -243,14 +259,16 @@ class HostStore:
         raw = (ctypes.c_uint8 * max(self.nbytes, 1)).from_address(self._ptr)
         arr = np.frombuffer(raw, dtype=np.uint8, count=self.nbytes)
         self.tensor = torch.from_numpy(arr).view(dtype).view(*shape)
-        self.tensor._sluice_host_store = self  # keep the allocation alive with the view
+        _HOST_STORES[self._ptr] = self
 
     def data_ptr(self) -> int:
         return self._ptr
 
     def __del__(self):
         p = getattr(self, "_ptr", None)
-        if p and _lib._lib is not None:
+        if p and _HOST_STORES is not None:
+            _HOST_STORES.pop(p, None)
+        if p and _lib is not None and _lib._lib is not None:
             try:
                 _lib._lib.sluice_host_free(p)
             except Exception:
