@@ -7,23 +7,25 @@
 //   MoE); sigmoid + score-correction bias, group-limited by the sum of each
 //   group's two best biased scores, weights from the unbiased sigmoid,
 //   renormalised and scaled (DeepSeek-V3).
-// Selection is an exact k-round wave argmax (no sort): every round each lane
-// offers its best not-yet-taken candidate and a 6-step xor-shuffle reduction
-// picks the wave winner, ties going to the lower expert id.  Softmax is
-// monotone, so selection runs on the logits themselves; sigmoid scores are
-// evaluated in fp64 and rounded to fp32 once so that selection on
-// fp32(s + bias) is reproducible bit for bit on the host.
+//
+// Selection is by exact rank, with no sort and no k serial rounds: every
+// candidate's key is published in LDS, then each lane counts, over one pass
+// of broadcast LDS reads, how many eligible keys beat each of its own
+// (greater key, or equal key and lower expert id).  A candidate with rank
+// r < k is the r-th choice, so outputs come out best-first with ties going to
+// the lower id.  Softmax is monotone, so selection runs on the logits
+// themselves; sigmoid scores are evaluated in fp64 and rounded to fp32 once,
+// so that selection on fp32(s + bias) is reproducible bit for bit on the host.
+//
+// The kernel is instantiated per scoring mode and per experts-per-lane (NV =
+// 1, 2, 4, 16) so each launch runs compact straight-line code: a decode step
+// launches it once per MoE layer, where cold instruction fetch, not
+// arithmetic, is what a bloated variant pays for.
 #include <math.h>
 
 #include "common.h"
 
 namespace {
-
-constexpr int kMaxPerLane = SLUICE_MAX_EXPERTS / SLUICE_WAVE;  // 16
-
-__device__ __forceinline__ bool better(float v1, int i1, float v2, int i2) {
-  return v1 > v2 || (v1 == v2 && i1 < i2);
-}
 
 __device__ __forceinline__ float load_logit(const void* p, int dtype, size_t i) {
   if (dtype == 1) return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
@@ -42,44 +44,42 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+template <int NV, int SCORING>
 __global__ __launch_bounds__(SLUICE_WAVE) void route_topk_kernel(
-    const void* __restrict__ logits, int dtype, int E, int k, int scoring,
-    int renorm, float scale, const float* __restrict__ bias, int n_group,
-    int topk_group, int32_t* __restrict__ ids_out, float* __restrict__ w_out) {
-  __shared__ float s_raw[SLUICE_MAX_EXPERTS];  // logit (softmax) or sigmoid s
-  __shared__ float s_key[SLUICE_MAX_EXPERTS];  // selection key
+    const void* __restrict__ logits, int dtype, int E, int k, int renorm, float scale,
+    const float* __restrict__ bias, int n_group, int topk_group, int32_t* __restrict__ ids_out,
+    float* __restrict__ w_out) {
+  __shared__ float s_key[SLUICE_MAX_EXPERTS];  // selection key; -inf-tagged if ineligible
+  __shared__ uint8_t s_ok[SLUICE_MAX_EXPERTS];
   __shared__ float s_gscore[SLUICE_WAVE];
   __shared__ int s_gok[SLUICE_WAVE];
   __shared__ int s_sel[SLUICE_MAX_TOPK];
+  __shared__ float s_w[SLUICE_MAX_TOPK];
 
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
   const size_t row = (size_t)t * E;
-  const int nv = (E + SLUICE_WAVE - 1) / SLUICE_WAVE;
 
-  float key[kMaxPerLane];
-  bool eligible[kMaxPerLane];
+  float key[NV], raw[NV];
+  bool ok[NV];
   float lmax = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) {
+  for (int j = 0; j < NV; ++j) {
     const int e = lane + j * SLUICE_WAVE;
+    ok[j] = e < E;
     key[j] = -INFINITY;
-    eligible[j] = false;
-    if (j < nv && e < E) {
+    raw[j] = 0.0f;
+    if (ok[j]) {
       const float l = load_logit(logits, dtype, row + e);
-      float raw, kv;
-      if (scoring == 0) {
-        raw = l;
-        kv = l;
+      if (SCORING == 0) {
+        raw[j] = l;
+        key[j] = l;
+        lmax = fmaxf(lmax, l);
       } else {
-        raw = (float)(1.0 / (1.0 + exp(-(double)l)));
-        kv = raw + (bias != nullptr ? bias[e] : 0.0f);
+        raw[j] = (float)(1.0 / (1.0 + exp(-(double)l)));
+        key[j] = raw[j] + (bias != nullptr ? bias[e] : 0.0f);
       }
-      s_raw[e] = raw;
-      s_key[e] = kv;
-      key[j] = kv;
-      eligible[j] = true;
-      lmax = fmaxf(lmax, l);
+      s_key[e] = key[j];
     }
   }
 
@@ -88,24 +88,18 @@ __global__ __launch_bounds__(SLUICE_WAVE) void route_topk_kernel(
     const int gsize = E / n_group;
     if (lane < n_group) {
       const int g0 = lane * gsize;
-      float score;
-      if (scoring == 0) {
-        score = -INFINITY;
-        for (int e = g0; e < g0 + gsize; ++e) score = fmaxf(score, s_key[e]);
-      } else {
-        float b1 = -INFINITY, b2 = -INFINITY;
-        for (int e = g0; e < g0 + gsize; ++e) {
-          const float v = s_key[e];
-          if (v > b1) {
-            b2 = b1;
-            b1 = v;
-          } else if (v > b2) {
-            b2 = v;
-          }
+      float b1 = -INFINITY, b2 = -INFINITY;
+      for (int e = g0; e < g0 + gsize; ++e) {
+        const float v = s_key[e];
+        if (v > b1) {
+          b2 = b1;
+          b1 = v;
+        } else if (v > b2) {
+          b2 = v;
         }
-        score = gsize >= 2 ? b1 + b2 : b1;
       }
-      s_gscore[lane] = score;
+      // softmax: group max; sigmoid: sum of the two best biased scores
+      s_gscore[lane] = (SCORING == 0 || gsize < 2) ? b1 : b1 + b2;
     }
     __syncthreads();
     if (lane < n_group) {
@@ -119,92 +113,79 @@ __global__ __launch_bounds__(SLUICE_WAVE) void route_topk_kernel(
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
+    for (int j = 0; j < NV; ++j) {
       const int e = lane + j * SLUICE_WAVE;
-      if (eligible[j]) eligible[j] = s_gok[e / gsize] != 0;
+      if (ok[j]) ok[j] = s_gok[e / gsize] != 0;
     }
   }
-
-  // k rounds of exact wave argmax.
-  for (int r = 0; r < k; ++r) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
-      const int e = lane + j * SLUICE_WAVE;
-      if (eligible[j] && better(key[j], e, bv, bi)) {
-        bv = key[j];
-        bi = e;
-      }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, SLUICE_WAVE);
-      const int oi = __shfl_xor(bi, off, SLUICE_WAVE);
-      if (better(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    // bi is uniform across the wave; its owner retires it.
-    if (bi != 0x7fffffff && (bi & (SLUICE_WAVE - 1)) == lane) {
-#pragma unroll
-      for (int j = 0; j < kMaxPerLane; ++j)
-        if (lane + j * SLUICE_WAVE == bi) eligible[j] = false;
-    }
-    if (lane == 0) s_sel[r] = bi;
+  for (int j = 0; j < NV; ++j) {
+    const int e = lane + j * SLUICE_WAVE;
+    if (e < E) s_ok[e] = ok[j] ? 1 : 0;
   }
   __syncthreads();
 
-  // Weights.
-  float denom_all = 1.0f;
-  if (scoring == 0) {
-    const float m = wave_max(lmax);
-    float part = 0.0f;
+  // Exact rank of each eligible candidate among the eligible keys.
+  int rank[NV];
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
+  for (int j = 0; j < NV; ++j) rank[j] = 0;
+#pragma unroll 8
+  for (int e2 = 0; e2 < E; ++e2) {
+    const float v2 = s_key[e2];
+    const bool ok2 = s_ok[e2] != 0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
       const int e = lane + j * SLUICE_WAVE;
-      if (j < nv && e < E) part += expf(s_raw[e] - m);
-    }
-    denom_all = wave_sum(part);
-    if (lane == 0) {
-      float w[SLUICE_MAX_TOPK];
-      float wsum = 0.0f;
-      for (int r = 0; r < k; ++r) {
-        const int e = s_sel[r];
-        w[r] = (e < E) ? expf(s_raw[e] - m) / denom_all : 0.0f;
-        wsum += w[r];
-      }
-      for (int r = 0; r < k; ++r) {
-        float v = renorm ? w[r] / wsum : w[r];
-        ids_out[(size_t)t * k + r] = s_sel[r] < E ? s_sel[r] : -1;
-        w_out[(size_t)t * k + r] = v * scale;
-      }
-    }
-  } else {
-    if (lane == 0) {
-      float w[SLUICE_MAX_TOPK];
-      float wsum = 0.0f;
-      for (int r = 0; r < k; ++r) {
-        const int e = s_sel[r];
-        w[r] = (e < E) ? s_raw[e] : 0.0f;
-        wsum += w[r];
-      }
-      for (int r = 0; r < k; ++r) {
-        float v = renorm ? w[r] / (wsum + 1e-20f) : w[r];
-        ids_out[(size_t)t * k + r] = s_sel[r] < E ? s_sel[r] : -1;
-        w_out[(size_t)t * k + r] = v * scale;
-      }
+      rank[j] += (ok2 && (v2 > key[j] || (v2 == key[j] && e2 < e))) ? 1 : 0;
     }
   }
+
+  // Un-normalised weights of the winners, in rank order.
+  float m = 0.0f, z = 1.0f;
+  if (SCORING == 0) {
+    m = wave_max(lmax);
+    float part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+      if (lane + j * SLUICE_WAVE < E) part += expf(raw[j] - m);
+    z = wave_sum(part);
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    if (ok[j] && rank[j] < k) {
+      s_sel[rank[j]] = lane + j * SLUICE_WAVE;
+      s_w[rank[j]] = SCORING == 0 ? expf(raw[j] - m) / z : raw[j];
+    }
+  }
+  __syncthreads();
+  if (lane < k) {
+    float w = s_w[lane];
+    if (renorm) {
+      float sum = 0.0f;
+      for (int r = 0; r < k; ++r) sum += s_w[r];
+      w = SCORING == 0 ? w / sum : w / (sum + 1e-20f);
+    }
+    ids_out[(size_t)t * k + lane] = s_sel[lane];
+    w_out[(size_t)t * k + lane] = w * scale;
+  }
+}
+
+template <int NV>
+void launch(int scoring, dim3 grid, hipStream_t st, const void* logits, int dtype, int E, int k,
+            int renorm, float scale, const float* bias, int ng, int tg, int32_t* ids, float* w) {
+  if (scoring == 0)
+    hipLaunchKernelGGL((route_topk_kernel<NV, 0>), grid, dim3(SLUICE_WAVE), 0, st, logits, dtype,
+                       E, k, renorm, scale, bias, ng, tg, ids, w);
+  else
+    hipLaunchKernelGGL((route_topk_kernel<NV, 1>), grid, dim3(SLUICE_WAVE), 0, st, logits, dtype,
+                       E, k, renorm, scale, bias, ng, tg, ids, w);
 }
 
 }  // namespace
 
-extern "C" int sluice_route_topk(const void* logits, int logits_dtype, int T,
-                                 int E, int k, int scoring, int renorm,
-                                 float scale, const float* bias, int n_group,
-                                 int topk_group, int32_t* ids_out, float* w_out,
+extern "C" int sluice_route_topk(const void* logits, int logits_dtype, int T, int E, int k,
+                                 int scoring, int renorm, float scale, const float* bias,
+                                 int n_group, int topk_group, int32_t* ids_out, float* w_out,
                                  sluice_stream_t stream) {
   if (T < 0 || E <= 0 || E > SLUICE_MAX_EXPERTS || k <= 0 || k > SLUICE_MAX_TOPK || k > E)
     return SLUICE_E_INVAL;
@@ -218,8 +199,20 @@ extern "C" int sluice_route_topk(const void* logits, int logits_dtype, int T,
   }
   if (T == 0) return SLUICE_OK;
   if (logits == nullptr || ids_out == nullptr || w_out == nullptr) return SLUICE_E_INVAL;
-  hipLaunchKernelGGL(route_topk_kernel, dim3(T), dim3(SLUICE_WAVE), 0,
-                     (hipStream_t)stream, logits, logits_dtype, E, k, scoring,
-                     renorm, scale, bias, n_group, topk_group, ids_out, w_out);
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid(T);
+  const int nv = (E + SLUICE_WAVE - 1) / SLUICE_WAVE;
+  if (nv <= 1)
+    launch<1>(scoring, grid, st, logits, logits_dtype, E, k, renorm, scale, bias, n_group,
+              topk_group, ids_out, w_out);
+  else if (nv <= 2)
+    launch<2>(scoring, grid, st, logits, logits_dtype, E, k, renorm, scale, bias, n_group,
+              topk_group, ids_out, w_out);
+  else if (nv <= 4)
+    launch<4>(scoring, grid, st, logits, logits_dtype, E, k, renorm, scale, bias, n_group,
+              topk_group, ids_out, w_out);
+  else
+    launch<16>(scoring, grid, st, logits, logits_dtype, E, k, renorm, scale, bias, n_group,
+               topk_group, ids_out, w_out);
   return (int)hipGetLastError();
 }
