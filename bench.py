@@ -6,16 +6,18 @@
 A step is one decode step of the whole synthetic decoder at batch c: every
 layer's attention/dense blocks and, per MoE layer, routing -> streaming gap
 -> grouped SwiGLU expert product -> combine, then the LM head and greedy
-next token.  Everything outside the gaps replays as hipGraph pieces.  The
-timed region is K steps bracketed by device synchronisation; the line's
-``value`` is tokens/s at the largest batch size (c * K / seconds).
+next token.  The gap op is a device launch served by the native gap server,
+so a whole step (gaps included) replays as one hipGraph.  The timed region
+is K steps bracketed by device synchronisation; the line's ``value`` is
+tokens/s at the largest batch size (c * K / seconds).
 
 Also measured in the same run:
   roofline      the dominant kernel (moe_gemm1: gate/up weights stream) timed
-                with HIP events on its own stream over the last step's real
-                routing of every layer, rotating layers so the 256 MB
-                last-level cache cannot serve repeats; algorithmic bytes =
-                U*2*I*H*2 (unique experts' w13) + T*H*2 + P*I*2.
+                with HIP events on its own stream over the recorded routing
+                of every layer for 4 decode steps, layers rotating so the
+                256 MB last-level cache cannot serve repeats; algorithmic
+                bytes = U*2*I*H*2 (unique experts' w13) + T*H*2 + P*I*2.
+                gemm2 and the combine are timed the same way ("kernels").
   h2d           peak pinned host->device GB/s (64 MiB copies) and the rate of
                 expert-row stream-ins issued like the gap issues them.
   cpu_baseline  the oracle (numpy/Python CPU restatement of the same path)
@@ -65,13 +67,15 @@ def time_decode(dec, c, steps, warmup):
     dec.reset(c)
     for _ in range(warmup):
         dec.step_graphs(c)
-    torch.cuda.synchronize()
+    dec.sync()
     before = dec.gap_counters()
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         dec.step_graphs(c)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    dec.sync()
     after = dec.gap_counters()
     delta = {k: after[k] - before[k] for k in after}
     n_moe = len(dec.moe_layers)
@@ -85,9 +89,46 @@ def time_decode(dec, c, steps, warmup):
     }
 
 
-def kernel_roofline(dec, c, reps=6):
-    """Time moe_gemm1 with HIP events over the last step's routing of every
-    MoE layer (rotating layers), on a dedicated stream."""
+def record_routing(dec, c, steps):
+    """Decode `steps` more steps and keep every MoE layer's routing of each
+    (the tensors the captured step rewrites are cloned after every replay)."""
+    import torch
+
+    out = []
+    for _ in range(steps):
+        dec.step_graphs(c)
+        torch.cuda.synchronize()
+        for n, io in enumerate(dec.layer_io[c]):
+            out.append((n, io["hn"].clone(), io["ti"].clone(), io["tw"].clone()))
+    dec.sync()
+    return out
+
+
+def _event_loop(stream, fn, items, reps):
+    import torch
+
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        for it in items:  # warm
+            fn(it)
+        e0.record(stream)
+        for _ in range(reps):
+            for it in items:
+                fn(it)
+        e1.record(stream)
+    stream.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * len(items))
+
+
+def kernel_roofline(dec, c, recorded, reps=3):
+    """Time the path's kernels with HIP events on their own stream over the
+    recorded routing of every layer and step (layers rotate, so the 256 MB
+    last-level cache cannot serve repeats).  Algorithmic bytes per launch:
+      gemm1   U*2I*H*2 (unique experts' w13) + T*H*2 (x) + P*I*2 (act out)
+      gemm2   U*H*I*2 (w2) + P*I*2 (act in) + P*H*4 (partials out)
+      combine P*H*4 + T*H*2 (out) [+ T*H*2 shared]
+    where U = unique resident experts of the step, P = valid pairs."""
     import torch
 
     from sluice_amd import _lib
@@ -95,61 +136,71 @@ def kernel_roofline(dec, c, reps=6):
     lib = _lib.load()
     sp = dec.sp
     H, I, k = sp["H"], sp["I"], sp["k"]
-    graphs = dec.graphs[c]
-    # piece p (p >= 1) consumes the routing captured in piece p-1
-    routings = [graphs[p][2] for p in range(len(graphs) - 1)]
     stream = torch.cuda.Stream(device=dec.dev)
     nplan = lib.sluice_moe_plan_ints(c, k)
-    plans, acts, bytes_, flops = [], [], [], []
+    items = []
     with torch.cuda.stream(stream):
-        for n, io in enumerate(routings):
+        for n, hn, ti, tw in recorded:
             m = dec.moe_layers[n]
             plan = torch.empty(nplan, dtype=torch.int32, device=dec.dev)
-            _lib.check(lib.sluice_moe_align(io["ti"].data_ptr(), c, k,
-                                            m._expert_map.data_ptr(), sp["E"],
-                                            m.w13_weight.shape[0], plan.data_ptr(),
+            _lib.check(lib.sluice_moe_align(ti.data_ptr(), c, k, m._expert_map.data_ptr(),
+                                            sp["E"], m.w13_weight.shape[0], plan.data_ptr(),
                                             stream.cuda_stream), "align")
-            plans.append(plan)
-            acts.append(torch.empty((c * k, I), dtype=torch.bfloat16, device=dec.dev))
+            act = torch.empty((c * k, I), dtype=torch.bfloat16, device=dec.dev)
+            part = torch.empty((c * k, H), dtype=torch.float32, device=dec.dev)
+            out = torch.empty((c, H), dtype=torch.bfloat16, device=dec.dev)
+            items.append(dict(n=n, m=m, hn=hn, ti=ti, tw=tw, plan=plan, act=act, part=part,
+                              out=out))
     stream.synchronize()
-    for plan in plans:
-        p = plan.cpu().numpy()
+    b1, b2, b3, fl = [], [], [], []
+    for it in items:
+        p = it["plan"].cpu().numpy()
         nb = int(p[0])
         blocks = p[4: 4 + 18 * nb].reshape(nb, 18) if nb else np.zeros((0, 18), np.int64)
         U = len(set(blocks[:, 0].tolist()))
         pairs = int(blocks[:, 1].sum()) if nb else 0
-        bytes_.append(U * 2 * I * H * 2 + c * H * 2 + pairs * I * 2)
-        flops.append(2 * pairs * 2 * I * H)
+        b1.append(U * 2 * I * H * 2 + c * H * 2 + pairs * I * 2)
+        b2.append(U * H * I * 2 + pairs * I * 2 + pairs * H * 4)
+        b3.append(c * k * H * 4 + c * H * 2)
+        fl.append(2 * pairs * 2 * I * H)
     if sp["fp8"]:
         return None
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        for _ in range(2):
-            for n, io in enumerate(routings):
-                m = dec.moe_layers[n]
-                lib.sluice_moe_gemm1_bf16(io["hn"].data_ptr(), m.w13_weight.data_ptr(),
-                                          plans[n].data_ptr(), c, H, I, k, acts[n].data_ptr(),
-                                          stream.cuda_stream)
-        e0.record(stream)
-        for _ in range(reps):
-            for n, io in enumerate(routings):
-                m = dec.moe_layers[n]
-                lib.sluice_moe_gemm1_bf16(io["hn"].data_ptr(), m.w13_weight.data_ptr(),
-                                          plans[n].data_ptr(), c, H, I, k, acts[n].data_ptr(),
-                                          stream.cuda_stream)
-        e1.record(stream)
-    stream.synchronize()
-    launches = reps * len(routings)
-    us = e0.elapsed_time(e1) * 1e3 / launches
-    avg_bytes = float(np.mean(bytes_))
-    achieved = avg_bytes / (us * 1e-6) / 1e9
-    mfma = float(np.mean(flops)) / (us * 1e-6) / 1e12
-    return {
-        "kernel": "moe_gemm1_bf16_kernel", "c": c, "launches": launches,
-        "avg_us": us, "avg_algorithmic_bytes": avg_bytes, "achieved_GBs": achieved,
-        "mfma_util_pct": 100.0 * mfma / MFMA_BF16_PEAK_TFLOPS,
-    }
+    st = stream.cuda_stream
+
+    def g1(it):
+        lib.sluice_moe_gemm1_bf16(it["hn"].data_ptr(), it["m"].w13_weight.data_ptr(),
+                                  it["plan"].data_ptr(), c, H, I, k, it["act"].data_ptr(), st)
+
+    def g2(it):
+        lib.sluice_moe_gemm2_bf16(it["act"].data_ptr(), it["m"].w2_weight.data_ptr(),
+                                  it["plan"].data_ptr(), it["tw"].data_ptr(), c, H, I, k,
+                                  it["part"].data_ptr(), st)
+
+    def cb(it):
+        lib.sluice_moe_combine(it["part"].data_ptr(), it["plan"].data_ptr(), c, k, H, 1.0, None,
+                               it["out"].data_ptr(), st)
+
+    us1 = _event_loop(stream, g1, items, reps)
+    us2 = _event_loop(stream, g2, items, reps)
+    us3 = _event_loop(stream, cb, items, reps)
+    # a plain device copy of known size: the HBM reference for counter scaling
+    nb = 256 << 20
+    src = torch.empty(nb, dtype=torch.uint8, device=dec.dev)
+    dst = torch.empty_like(src)
+    usc = _event_loop(stream, lambda _: dst.copy_(src), [0], 4)
+
+    def res(name, us, bts):
+        avg = float(np.mean(bts))
+        return {"kernel": name, "avg_us": us, "algorithmic_bytes": avg,
+                "achieved_GBs": avg / (us * 1e-6) / 1e9}
+
+    r1 = res("moe_gemm1_bf16_kernel", us1, b1)
+    r1["mfma_util_pct"] = 100.0 * float(np.mean(fl)) / (us1 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS
+    r2 = res("moe_gemm2_bf16_kernel", us2, b2)
+    r2["mfma_util_pct"] = 100.0 * float(np.mean(fl)) / (us2 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS
+    return {"c": c, "launches": reps * len(items), "gemm1": r1, "gemm2": r2,
+            "combine": res("moe_combine_kernel", us3, b3),
+            "copy_256MiB_GBs": 2 * nb / (usc * 1e-6) / 1e9}
 
 
 def h2d_rates(dec):
@@ -292,7 +343,7 @@ def main():
         results.append(r)
     main_c = max(batches)
     main = [r for r in results if r["c"] == main_c][0]
-    roof = kernel_roofline(dec, main_c)
+    roof = kernel_roofline(dec, main_c, record_routing(dec, main_c, 4))
     h2d = h2d_rates(dec)
     log(f"roofline {roof}")
     log(f"h2d {h2d}")
@@ -328,17 +379,20 @@ def main():
         "cpu_baseline": None,
     }
     if roof:
+        g1 = roof["gemm1"]
         line["roofline"] = {
-            "bound": "hbm", "achieved": roof["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": roof["achieved_GBs"] / HBM_PEAK_GBS, "traffic": None,
-            "kernel": roof["kernel"], "avg_us": roof["avg_us"],
-            "algorithmic_bytes_per_launch": roof["avg_algorithmic_bytes"],
-            "mfma_util_pct": roof["mfma_util_pct"],
+            "bound": "hbm", "achieved": g1["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": g1["achieved_GBs"] / HBM_PEAK_GBS, "traffic": None,
+            "kernel": g1["kernel"], "avg_us": g1["avg_us"],
+            "algorithmic_bytes_per_launch": g1["algorithmic_bytes"],
+            "mfma_util_pct": g1["mfma_util_pct"],
         }
+        line["kernels"] = {kk: roof[kk] for kk in ("gemm2", "combine")}
+        line["kernels"]["copy_256MiB_GBs"] = roof["copy_256MiB_GBs"]
     if cpu:
         line["cpu_baseline"] = {k_: cpu[k_] for k_ in ("value", "unit", "cores", "kind", "sample")}
     print(json.dumps(line), flush=True)
-    dec.off.close()
+    dec.close()
 
 
 if __name__ == "__main__":

@@ -36,6 +36,7 @@ typedef struct ihipStream_t* sluice_stream_t; /* == hipStream_t */
 #define SLUICE_E_TIMEOUT (-3)  /* host wait on a device record timed out */
 #define SLUICE_E_NOMEM (-4)    /* host allocation failed */
 #define SLUICE_E_STATE (-5)    /* object used in a state it does not allow */
+#define SLUICE_E_ABORTED (-6)  /* a device gap wait ended by the abort flag */
 
 /* Kernel limits (checked on the host before every launch). */
 #define SLUICE_MAX_EXPERTS 1024  /* global experts E per layer */
@@ -208,13 +209,60 @@ int sluice_layer_add_param(sluice_layer* layer, void* slot_base_dev,
 int sluice_layer_pin(sluice_layer* layer, int local, int debit_protected,
                      int* slot_out);
 
-/* The gap, device path: launch the slot lookup on topk_ids (n ids) on
- * `compute`, wait for its record, run the SLRU bookkeeping, stream misses
- * on the library's copy stream (fenced by events both ways), refresh the
- * standing map on `compute`.  Returns SLUICE_E_OVERFLOW when the step's
- * working set cannot fit (state is then as the reference leaves it). */
+/* The gap, split where the host is needed (replaces _router_split_gap,
+ * src/sluice/offloader.py:2362-2467, and the ids D2H sync at 2406).
+ *
+ * Device half, sluice_layer_gap_launch: one workgroup on `stream`, no host
+ * call, capturable in a hipGraph.  It builds the step's sorted unique
+ * selected ids and the count of owned ids the device map does not hold,
+ * posts them to the layer's mailbox (host-mapped pinned memory, stamped with
+ * a system-scope release store), copies hs_bytes (multiple of 16, 16-byte
+ * aligned; 0 = none) from hs_src to hs_dst -- the gap op's fresh copy of
+ * hidden_states -- and then waits for the host ONLY if residency must change
+ * (a miss, or no standing map yet); it then installs the standing map the
+ * host sent.  A step without misses never waits: slots and map stay valid
+ * whatever the SLRU bookkeeping does with it.  Device waits are bounded by
+ * SLUICE_GAP_TIMEOUT_S (default 20 s) and by the abort flag.
+ *
+ * Host half, sluice_layer_gap_serve: waits (bounded) for the layer's next
+ * record, runs the reference's bookkeeping exactly (fast-hit, hit touches in
+ * ascending id order, claimed set, victims), streams misses as
+ * hipMemcpyAsync on the library's per-device copy stream, waits for them,
+ * and answers the device with the standing slot table.  `compute` (may be
+ * NULL) is polled for errors while waiting.  SLUICE_E_OVERFLOW when the
+ * working set does not fit (rows acquired before it still stream, the map is
+ * left as it was, as in the reference).
+ *
+ * sluice_layer_gap = launch (no copy) + serve: the reference's eager op. */
+int sluice_layer_gap_launch(sluice_layer* layer, const int32_t* topk_ids, int n,
+                            const void* hs_src, void* hs_dst, size_t hs_bytes,
+                            sluice_stream_t stream);
+int sluice_layer_gap_serve(sluice_layer* layer, int fast_hit,
+                           sluice_stream_t compute);
 int sluice_layer_gap(sluice_layer* layer, const int32_t* topk_ids, int n,
                      int fast_hit, sluice_stream_t compute);
+
+/* Gap server: a native thread that serves every listed layer's records as
+ * the device posts them, so the gap op needs no host code on the stream and
+ * a whole decode step (gaps included) can replay as one hipGraph.  While a
+ * layer is served, sluice_layer_gap/_serve/_gap_host on it return
+ * SLUICE_E_STATE.  On the first error the server raises the abort flag
+ * (waiting gap kernels exit, maps unchanged) and keeps it as its sticky
+ * error.  drain: after the caller has synchronised the streams that launched
+ * gaps, waits until every posted record is served; returns the sticky error.
+ * No counterpart in the reference (its gap is always eager). */
+typedef struct sluice_gap_server sluice_gap_server;
+int sluice_gap_server_create(sluice_layer* const* layers, int n_layers,
+                             int fast_hit, sluice_gap_server** out);
+int sluice_gap_server_drain(sluice_gap_server* server, double timeout_s);
+int sluice_gap_server_error(const sluice_gap_server* server);
+int sluice_gap_server_destroy(sluice_gap_server* server);
+
+/* Raise (set=1) or clear (set=0) the process-wide abort flag; after an abort
+ * and a stream synchronisation, sluice_layer_gap_resync lines a layer's host
+ * stamps up with the device's. */
+int sluice_gap_abort(int set);
+int sluice_layer_gap_resync(sluice_layer* layer);
 
 /* The gap, host path (no HIP calls): ids is a host array.  Runs the same
  * bookkeeping and reports the (local, slot) stream-ins in order in

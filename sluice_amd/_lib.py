@@ -20,6 +20,7 @@ SLUICE_E_OVERFLOW = -2
 SLUICE_E_TIMEOUT = -3
 SLUICE_E_NOMEM = -4
 SLUICE_E_STATE = -5
+SLUICE_E_ABORTED = -6
 
 MAX_EXPERTS = 1024
 MAX_SLOTS = 512
@@ -62,6 +63,14 @@ SIGNATURES = {
     "sluice_layer_add_param": (c_int, [_P, _P, _P, c_size_t]),
     "sluice_layer_pin": (c_int, [_P, c_int, c_int, POINTER(c_int)]),
     "sluice_layer_gap": (c_int, [_P, _P, c_int, c_int, _P]),
+    "sluice_layer_gap_launch": (c_int, [_P, _P, c_int, _P, _P, c_size_t, _P]),
+    "sluice_layer_gap_serve": (c_int, [_P, c_int, _P]),
+    "sluice_gap_server_create": (c_int, [_P, c_int, c_int, POINTER(c_void_p)]),
+    "sluice_gap_server_drain": (c_int, [_P, ctypes.c_double]),
+    "sluice_gap_server_error": (c_int, [_P]),
+    "sluice_gap_server_destroy": (c_int, [_P]),
+    "sluice_gap_abort": (c_int, [c_int]),
+    "sluice_layer_gap_resync": (c_int, [_P]),
     "sluice_layer_gap_host": (
         c_int, [_P, _P, c_int, c_int, _P, c_int, POINTER(c_int), POINTER(c_int)]
     ),

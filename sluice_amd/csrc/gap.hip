@@ -1,22 +1,51 @@
 // a3-a8: the streaming gap on MI355X.
 //
-//   slot_lookup_kernel   ids -> sorted unique selected ids + miss count,
-//                        published straight into host-mapped pinned memory
-//                        (replaces topk_ids.to("cpu") + sorted(set(ids)),
-//                        src/sluice/offloader.py:2406, 2427).
-//   map_refresh_kernel   standing expert map from an S-entry table passed as
-//                        a kernel argument (replaces _write_map's pinned
-//                        staging + map_ev wait, offloader.py:2083-2123).
-//   sluice_layer_*       the per-layer slot cache (slru::Cache) plus the gap
-//                        driver: wait for the record, SLRU bookkeeping,
-//                        hipMemcpyAsync of missing expert rows on a dedicated
-//                        copy stream fenced by events both ways
-//                        (offloader.py:2443-2464, 1979-1991, 2709-2723).
+// The reference's gap (src/sluice/offloader.py:2362-2467) is an eager host
+// region between captured graph pieces: topk_ids.to("cpu") synchronises the
+// stream (2406), the host runs the SLRU bookkeeping, streams misses on a copy
+// stream (2443-2464, 2709-2723) and rewrites the standing expert map
+// (2083-2123).  Here the gap is split at the one point where the host is
+// really needed:
+//
+//   gap_kernel (device, capturable, one workgroup)
+//     - builds the step's sorted unique selected ids in LDS (ballot
+//       compaction) and counts the owned ids the standing map does not hold;
+//     - posts them to the layer's mailbox in host-mapped pinned memory
+//       (system-scope release store of a per-layer stamp);
+//     - writes the gap op's fresh copy of hidden_states;
+//     - waits for the host ONLY when residency has to change (a miss, or no
+//       standing map yet), then installs the map the host sent.  A step
+//       without misses leaves slots and map untouched whatever the SLRU
+//       does, so the device runs on without a host round trip.
+//
+//   serve (host): consumes each posted record in stamp order and runs the
+//     reference's bookkeeping exactly (slru::Cache::gap: fast-hit, touches,
+//     claimed set, victims, overflow).  For a waiting device it issues the
+//     misses' row copies as hipMemcpyAsync on a dedicated copy stream, waits
+//     for them, then answers with the standing slot table.  It runs inline
+//     (sluice_layer_gap: launch + serve, the reference's eager op) or on a
+//     native server thread (sluice_gap_server_*), which makes the gap op
+//     capturable, so a whole decode step replays as one hipGraph.
+//
+// Ordering: a gap kernel runs only after all earlier work on its stream has
+// completed, so when the host sees its record no kernel of that stream can
+// still read a slot about to be overwritten (what the reference fences with
+// an event from the compute stream, 2443-2447); the device waits for the
+// host's answer, which is sent after the copies completed (2464).
+//
+// Every device wait is bounded (SLUICE_GAP_TIMEOUT_S, default 20 s, measured
+// on the constant-rate wall clock) and also ends when the host raises the
+// process-wide abort flag; the kernel then leaves the map unchanged and
+// reports the outcome in the mailbox.
 #include <immintrin.h>
 #include <stdlib.h>
+#include <string.h>
 #include <time.h>
 
+#include <atomic>
 #include <mutex>
+#include <new>
+#include <thread>
 #include <vector>
 
 #include "common.h"
@@ -25,14 +54,17 @@
 namespace {
 
 constexpr int kLookupThreads = 256;
+constexpr int kWaves = kLookupThreads / SLUICE_WAVE;
 
+// ---------------------------------------------------------------------------
+// Stand-alone lookup (sluice_slot_lookup): sorted unique ids + miss count.
+// ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kLookupThreads) void slot_lookup_kernel(
     const int32_t* __restrict__ ids, int n, const int32_t* __restrict__ map,
-    const int32_t* __restrict__ local_of, int E, sluice_gap_record* rec,
-    int32_t stamp) {
+    const int32_t* __restrict__ local_of, int E, sluice_gap_record* rec, int32_t stamp) {
   __shared__ int present[SLUICE_MAX_EXPERTS];
-  __shared__ int wcount[kLookupThreads / SLUICE_WAVE];
-  __shared__ int wmiss[kLookupThreads / SLUICE_WAVE];
+  __shared__ int wcount[kWaves];
+  __shared__ int wmiss[kWaves];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -60,7 +92,7 @@ __global__ __launch_bounds__(kLookupThreads) void slot_lookup_kernel(
     int off = base;
     for (int w = 0; w < wave; ++w) off += wcount[w];
     if (f) rec->uniq[off + mask_rank(fb)] = e;
-    for (int w = 0; w < kLookupThreads / SLUICE_WAVE; ++w) {
+    for (int w = 0; w < kWaves; ++w) {
       base += wcount[w];
       miss += wmiss[w];
     }
@@ -95,25 +127,173 @@ __global__ __launch_bounds__(256) void map_refresh_kernel(int32_t* __restrict__ 
   for (int e = threadIdx.x; e < E; e += 256) map[e] = m[e];
 }
 
-// Per-device resources shared by every layer: one copy stream (default
-// priority) and the two fencing events.
+// ---------------------------------------------------------------------------
+// Mailbox of one layer (host pinned, coherent, mapped into the device).
+// ---------------------------------------------------------------------------
+struct GapMailbox {
+  // written by the device
+  int32_t req_stamp;   // stamp of the last posted record (written last)
+  int32_t n_uniq;      // sorted unique selected ids in uniq[]
+  int32_t n_miss;      // owned ids the device map does not hold
+  int32_t waits;       // 1: the device waits for a response to this record
+  int32_t dev_status;  // first failed device wait (sticky; 0 = none)
+  int32_t dev_pad[11];
+  int32_t uniq[SLUICE_MAX_EXPERTS];
+  // written by the host
+  int32_t ack_stamp;   // last record the host has copied out
+  int32_t resp_stamp;  // stamp the response below answers (written last)
+  int32_t resp_code;   // 0: install slot_global as the map; else leave it
+  int32_t standing;    // the device map is the standing map
+  int32_t n_slots;
+  int32_t host_pad[11];
+  int32_t slot_global[SLUICE_MAX_SLOTS];  // slot -> global id, -1 = empty
+};
+
+__device__ __forceinline__ int32_t ld_sys(const int32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Spin until *p == want.  0, or SLUICE_E_ABORTED / SLUICE_E_TIMEOUT.
+__device__ int wait_eq(const int32_t* p, int32_t want, const int32_t* abort_flag,
+                       long long timeout_ticks) {
+  const long long t0 = wall_clock64();
+  for (;;) {
+    if (ld_sys(p) == want) return 0;
+    if (ld_sys(abort_flag) != 0) return SLUICE_E_ABORTED;
+    if (wall_clock64() - t0 > timeout_ticks) return SLUICE_E_TIMEOUT;
+    __builtin_amdgcn_s_sleep(4);
+  }
+}
+
+__global__ __launch_bounds__(kLookupThreads) void gap_kernel(
+    const int32_t* __restrict__ ids, int n, int32_t* __restrict__ map,
+    const int32_t* __restrict__ local_of, int E, GapMailbox* mb, int32_t* stamp_ctr,
+    const int32_t* abort_flag, long long timeout_ticks, const u32x4_t* __restrict__ copy_src,
+    u32x4_t* __restrict__ copy_dst, int copy_vecs) {
+  __shared__ int present[SLUICE_MAX_EXPERTS];
+  __shared__ int wcount[kWaves];
+  __shared__ int wmiss[kWaves];
+  __shared__ int s_stamp, s_status, s_waits;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+
+  if (tid == 0) {
+    // The host must have copied out this layer's previous record before it
+    // is overwritten (it normally has, long ago).
+    const int32_t prev = *stamp_ctr;
+    int32_t s = prev + 1;
+    if (s <= 0) s = 1;
+    s_stamp = s;
+    s_status = wait_eq(&mb->ack_stamp, prev, abort_flag, timeout_ticks);
+  }
+  for (int e = tid; e < E; e += kLookupThreads) present[e] = 0;
+  __syncthreads();
+  const bool can_post = s_status == 0;
+  int base = 0, miss = 0;
+  if (can_post) {
+    for (int i = tid; i < n; i += kLookupThreads) {
+      const int g = ids[i];
+      if ((unsigned)g < (unsigned)E) present[g] = 1;
+    }
+    __syncthreads();
+    for (int c = 0; c < E; c += kLookupThreads) {
+      const int e = c + tid;
+      const bool f = e < E && present[e] != 0;
+      const bool m = f && local_of[e] >= 0 && map[e] < 0;
+      const uint64_t fb = __ballot(f);
+      const uint64_t mbits = __ballot(m);
+      if (lane == 0) {
+        wcount[wave] = __popcll(fb);
+        wmiss[wave] = __popcll(mbits);
+      }
+      __syncthreads();
+      int off = base;
+      for (int w = 0; w < wave; ++w) off += wcount[w];
+      if (f) mb->uniq[off + mask_rank(fb)] = e;
+      for (int w = 0; w < kWaves; ++w) {
+        base += wcount[w];
+        miss += wmiss[w];
+      }
+      __syncthreads();
+    }
+    __threadfence_system();
+  }
+  __syncthreads();
+  if (tid == 0) {
+    s_waits = 0;
+    if (can_post) {
+      const int32_t s = s_stamp;
+      const int waits = (miss > 0 || ld_sys(&mb->standing) == 0) ? 1 : 0;
+      mb->n_uniq = base;
+      mb->n_miss = miss;
+      mb->waits = waits;
+      *stamp_ctr = s;
+      __threadfence_system();
+      __hip_atomic_store(&mb->req_stamp, s, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+      s_waits = waits;
+    } else {
+      __hip_atomic_store(&mb->dev_status, s_status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  }
+  __syncthreads();
+  // The op's fresh copy of hidden_states does not depend on the host: it is
+  // written while the host works on the record.
+  for (int i = tid; i < copy_vecs; i += kLookupThreads) copy_dst[i] = copy_src[i];
+  if (!s_waits) return;
+  if (tid == 0) {
+    const int st = wait_eq(&mb->resp_stamp, s_stamp, abort_flag, timeout_ticks);
+    s_status = st != 0 ? st : ld_sys(&mb->resp_code);
+    if (st != 0)
+      __hip_atomic_store(&mb->dev_status, st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  __syncthreads();
+  if (s_status != 0) return;
+  // Install the standing map the host sent (already acquired above).
+  const int nS = ld_sys(&mb->n_slots);
+  for (int e = tid; e < E; e += kLookupThreads) present[e] = -1;
+  __syncthreads();
+  for (int s = tid; s < nS; s += kLookupThreads) {
+    const int g = ld_sys(&mb->slot_global[s]);
+    if ((unsigned)g < (unsigned)E) present[g] = s;
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kLookupThreads) map[e] = present[e];
+}
+
+// ---------------------------------------------------------------------------
+// Per-device resources: one copy stream (default priority, non-blocking) and
+// the wall-clock rate; one process-wide abort flag in pinned memory.
+// ---------------------------------------------------------------------------
 struct DeviceRes {
   hipStream_t copy = nullptr;
-  hipEvent_t ev_compute = nullptr;
-  hipEvent_t ev_copy = nullptr;
+  long long clock_khz = 0;
 };
 constexpr int kMaxDevices = 64;
 DeviceRes g_dev[kMaxDevices];
 std::mutex g_dev_mu;
+int32_t* g_abort_host = nullptr;
+int32_t* g_abort_dev = nullptr;
 
 int device_res(int dev, DeviceRes** out) {
   if (dev < 0 || dev >= kMaxDevices) return SLUICE_E_INVAL;
   std::lock_guard<std::mutex> lk(g_dev_mu);
   DeviceRes& r = g_dev[dev];
   if (r.copy == nullptr) {
+    int khz = 0;
+    SLUICE_HIP_CHECK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
     SLUICE_HIP_CHECK(hipStreamCreateWithFlags(&r.copy, hipStreamNonBlocking));
-    SLUICE_HIP_CHECK(hipEventCreateWithFlags(&r.ev_compute, hipEventDisableTiming));
-    SLUICE_HIP_CHECK(hipEventCreateWithFlags(&r.ev_copy, hipEventDisableTiming));
+    r.clock_khz = khz > 0 ? khz : 100000;
+  }
+  if (g_abort_host == nullptr) {
+    void* p = nullptr;
+    SLUICE_HIP_CHECK(hipHostMalloc(&p, 256, hipHostMallocCoherent | hipHostMallocMapped |
+                                                hipHostMallocPortable));
+    static_cast<int32_t*>(p)[0] = 0;
+    void* dp = nullptr;
+    SLUICE_HIP_CHECK(hipHostGetDevicePointer(&dp, p, 0));
+    g_abort_host = static_cast<int32_t*>(p);
+    g_abort_dev = static_cast<int32_t*>(dp);
   }
   *out = &r;
   return SLUICE_OK;
@@ -128,11 +308,13 @@ double now_s() {
 double gap_timeout_s() {
   static double v = [] {
     const char* s = getenv("SLUICE_GAP_TIMEOUT_S");
-    double t = s ? atof(s) : 60.0;
-    return t > 0 ? t : 60.0;
+    double t = s ? atof(s) : 20.0;
+    return t > 0 ? t : 20.0;
   }();
   return v;
 }
+
+int32_t next_stamp(int32_t s) { return s + 1 > 0 ? s + 1 : 1; }
 
 }  // namespace
 
@@ -142,19 +324,186 @@ struct ParamRows {
   size_t row_bytes;
 };
 
+struct sluice_gap_server;
+
 struct sluice_layer {
   slru::Cache c;
+  std::mutex mu;  // guards c, params, bytes against the server thread
   int32_t* map_dev = nullptr;
   std::vector<ParamRows> params;
   int device = -1;
-  sluice_gap_record* rec = nullptr;  // host pointer (pinned, coherent, mapped)
-  sluice_gap_record* rec_dev = nullptr;
-  int32_t* local_of_dev = nullptr;
-  int32_t stamp = 0;
+  GapMailbox* mb = nullptr;      // host pointer
+  GapMailbox* mb_dev = nullptr;  // device view of the same memory
+  int32_t* dev_block = nullptr;  // [E] local_of, then the stamp counter
+  int32_t host_stamp = 0;        // last record copied out
+  std::atomic<int32_t> done_stamp{0};  // last record fully served
   int64_t bytes = 0;
+  sluice_gap_server* server = nullptr;
   std::vector<int> streams;
-  std::vector<int32_t> table;
+  std::vector<int32_t> uniq;
+  // standalone lookup record for the eager path of sluice_slot_lookup users
 };
+
+namespace {
+
+int layer_device_init(sluice_layer* L) {
+  if (L->mb != nullptr) return SLUICE_OK;
+  SLUICE_HIP_CHECK(hipGetDevice(&L->device));
+  DeviceRes* R = nullptr;
+  int rc = device_res(L->device, &R);
+  if (rc) return rc;
+  void* p = nullptr;
+  SLUICE_HIP_CHECK(hipHostMalloc(&p, sizeof(GapMailbox), hipHostMallocCoherent |
+                                                             hipHostMallocMapped));
+  memset(p, 0, sizeof(GapMailbox));
+  L->mb = static_cast<GapMailbox*>(p);
+  void* dp = nullptr;
+  SLUICE_HIP_CHECK(hipHostGetDevicePointer(&dp, p, 0));
+  L->mb_dev = static_cast<GapMailbox*>(dp);
+  const int E = L->c.E;
+  SLUICE_HIP_CHECK(hipMalloc((void**)&L->dev_block, sizeof(int32_t) * (E + 1)));
+  std::vector<int32_t> blk(L->c.local_of.begin(), L->c.local_of.end());
+  blk.push_back(0);  // stamp counter
+  SLUICE_HIP_CHECK(hipMemcpy(L->dev_block, blk.data(), sizeof(int32_t) * (E + 1),
+                             hipMemcpyHostToDevice));
+  return SLUICE_OK;
+}
+
+constexpr int kNothing = 1;  // serve_one: no record posted yet (non-blocking)
+
+void respond(sluice_layer* L, int32_t stamp, int code) {
+  GapMailbox* mb = L->mb;
+  if (code == SLUICE_OK) {
+    L->c.slot_globals(mb->slot_global);
+    mb->n_slots = L->c.S;
+    mb->standing = 1;
+  }
+  mb->resp_code = code;
+  __atomic_store_n(&mb->resp_stamp, stamp, __ATOMIC_RELEASE);
+}
+
+// Serve one posted record of layer L.  block: wait (bounded) for it;
+// `compute` (may be null) is polled for errors while waiting.
+int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
+  GapMailbox* mb = L->mb;
+  const int dev_status = __atomic_load_n(&mb->dev_status, __ATOMIC_ACQUIRE);
+  if (dev_status != 0) return dev_status;  // a device wait failed earlier
+  const int32_t want = next_stamp(L->host_stamp);
+  if (__atomic_load_n(&mb->req_stamp, __ATOMIC_ACQUIRE) != want) {
+    if (!block) return kNothing;
+    const double t0 = now_s();
+    unsigned spins = 0;
+    while (__atomic_load_n(&mb->req_stamp, __ATOMIC_ACQUIRE) != want) {
+      _mm_pause();
+      if ((++spins & 4095u) == 0) {
+        if (compute != nullptr) {
+          hipError_t q = hipStreamQuery(compute);
+          if (q != hipSuccess && q != hipErrorNotReady) return (int)q;
+        }
+        if (now_s() - t0 > gap_timeout_s()) return SLUICE_E_TIMEOUT;
+      }
+    }
+  }
+  // Copy the record out, then let the device reuse the mailbox.
+  const int n_uniq = mb->n_uniq;
+  const int n_miss = mb->n_miss;
+  const bool waits = mb->waits != 0;
+  if (n_uniq < 0 || n_uniq > L->c.E) return SLUICE_E_STATE;
+  L->uniq.assign(mb->uniq, mb->uniq + n_uniq);
+  L->host_stamp = want;
+  __atomic_store_n(&mb->ack_stamp, want, __ATOMIC_RELEASE);
+
+  std::lock_guard<std::mutex> lk(L->mu);
+  L->streams.clear();
+  bool map_write = false;
+  const int grc = L->c.gap(L->uniq.data(), n_uniq, fast_hit, L->streams, map_write);
+  const int n_streams = (int)L->streams.size() / 2;
+  int rc = SLUICE_OK;
+  if (!waits) {
+    // The device ran on with its map: the host must agree nothing changed.
+    if (grc != 0 || n_streams != 0 || map_write || n_miss != 0) rc = SLUICE_E_STATE;
+  } else if (grc == 0 && n_streams != n_miss) {
+    rc = SLUICE_E_STATE;
+  } else if (n_streams > 0) {
+    // On overflow the rows acquired before it still stream, as in the
+    // reference (its copies were issued before the raise); the device map
+    // is left as it was.
+    DeviceRes* R = nullptr;
+    rc = device_res(L->device, &R);
+    for (int i = 0; rc == SLUICE_OK && i < n_streams; ++i) {
+      const int local = L->streams[2 * i], slot = L->streams[2 * i + 1];
+      for (const ParamRows& p : L->params) {
+        hipError_t e = hipMemcpyAsync(p.slot_base + (size_t)slot * p.row_bytes,
+                                      p.host_base + (size_t)local * p.row_bytes, p.row_bytes,
+                                      hipMemcpyHostToDevice, R->copy);
+        if (e != hipSuccess) {
+          rc = (int)e;
+          break;
+        }
+        L->bytes += (int64_t)p.row_bytes;
+      }
+    }
+    if (rc == SLUICE_OK) {
+      hipError_t e = hipStreamSynchronize(R->copy);
+      if (e != hipSuccess) rc = (int)e;
+    }
+  }
+  if (waits && rc == SLUICE_OK && grc != 0) rc = grc;
+  if (waits) respond(L, want, rc);
+  L->done_stamp.store(want, std::memory_order_release);
+  return rc;
+}
+
+long long timeout_ticks(const sluice_layer* L) {
+  const long long khz = g_dev[L->device].clock_khz;
+  return (long long)(gap_timeout_s() * 1000.0 * (double)khz);
+}
+
+int launch_gap(sluice_layer* L, const int32_t* ids, int n, const void* hs_src, void* hs_dst,
+               size_t hs_bytes, hipStream_t st) {
+  if ((hs_bytes & 15) != 0 || ((uintptr_t)hs_src & 15) != 0 || ((uintptr_t)hs_dst & 15) != 0)
+    return SLUICE_E_INVAL;
+  if (hs_bytes > 0 && (hs_src == nullptr || hs_dst == nullptr)) return SLUICE_E_INVAL;
+  hipLaunchKernelGGL(gap_kernel, dim3(1), dim3(kLookupThreads), 0, st, ids, n, L->map_dev,
+                     L->dev_block, L->c.E, L->mb_dev, L->dev_block + L->c.E, g_abort_dev,
+                     timeout_ticks(L), (const u32x4_t*)hs_src, (u32x4_t*)hs_dst,
+                     (int)(hs_bytes / 16));
+  return (int)hipGetLastError();
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Server thread: serves every registered layer's mailbox as records arrive.
+// ---------------------------------------------------------------------------
+struct sluice_gap_server {
+  std::vector<sluice_layer*> layers;
+  bool fast_hit = false;
+  int device = 0;
+  std::thread th;
+  std::atomic<bool> stop{false};
+  std::atomic<int> error{0};
+  std::atomic<int64_t> served{0};
+};
+
+static void server_loop(sluice_gap_server* S) {
+  (void)hipSetDevice(S->device);
+  while (!S->stop.load(std::memory_order_acquire)) {
+    bool any = false;
+    for (sluice_layer* L : S->layers) {
+      const int rc = serve_one(L, S->fast_hit, false, nullptr);
+      if (rc == kNothing) continue;
+      any = true;
+      S->served.fetch_add(1, std::memory_order_relaxed);
+      if (rc != SLUICE_OK) {
+        int zero = 0;
+        S->error.compare_exchange_strong(zero, rc);
+        __atomic_store_n(g_abort_host, 1, __ATOMIC_RELEASE);
+      }
+    }
+    if (!any) _mm_pause();
+  }
+}
 
 extern "C" int sluice_layer_create(int E, int local_n, int num_slots, int protected_cap,
                                    const int32_t* local_of, int32_t* expert_map_dev,
@@ -166,20 +515,28 @@ extern "C" int sluice_layer_create(int E, int local_n, int num_slots, int protec
   if (L == nullptr) return SLUICE_E_NOMEM;
   L->c.init(E, local_n, num_slots, protected_cap, local_of);
   L->map_dev = expert_map_dev;
-  L->table.assign(num_slots, -1);
+  if (expert_map_dev != nullptr) {
+    // Device resources are made here, never under graph capture.
+    const int rc = layer_device_init(L);
+    if (rc != SLUICE_OK) {
+      delete L;
+      return rc;
+    }
+  }
   *out = L;
   return SLUICE_OK;
 }
 
 extern "C" int sluice_layer_destroy(sluice_layer* L) {
   if (L == nullptr) return SLUICE_OK;
+  if (L->server != nullptr) return SLUICE_E_STATE;
   int rc = SLUICE_OK;
-  if (L->rec != nullptr) {
-    hipError_t e = hipHostFree(L->rec);
+  if (L->mb != nullptr) {
+    hipError_t e = hipHostFree(L->mb);
     if (e != hipSuccess) rc = (int)e;
   }
-  if (L->local_of_dev != nullptr) {
-    hipError_t e = hipFree(L->local_of_dev);
+  if (L->dev_block != nullptr) {
+    hipError_t e = hipFree(L->dev_block);
     if (e != hipSuccess) rc = (int)e;
   }
   delete L;
@@ -190,107 +547,136 @@ extern "C" int sluice_layer_add_param(sluice_layer* L, void* slot_base_dev, cons
                                       size_t row_bytes) {
   if (L == nullptr || slot_base_dev == nullptr || host_base == nullptr || row_bytes == 0)
     return SLUICE_E_INVAL;
+  std::lock_guard<std::mutex> lk(L->mu);
   L->params.push_back({(char*)slot_base_dev, (const char*)host_base, row_bytes});
   return SLUICE_OK;
 }
 
 extern "C" int sluice_layer_pin(sluice_layer* L, int local, int debit_protected, int* slot_out) {
   if (L == nullptr) return SLUICE_E_INVAL;
+  std::lock_guard<std::mutex> lk(L->mu);
   const int s = L->c.pin(local, debit_protected != 0);
   if (slot_out) *slot_out = s;
   return s < 0 ? SLUICE_E_STATE : SLUICE_OK;
 }
 
-static int layer_device_init(sluice_layer* L) {
-  if (L->rec != nullptr) return SLUICE_OK;
-  SLUICE_HIP_CHECK(hipGetDevice(&L->device));
-  void* p = nullptr;
-  SLUICE_HIP_CHECK(hipHostMalloc(&p, sizeof(sluice_gap_record),
-                                 hipHostMallocCoherent | hipHostMallocMapped));
-  L->rec = (sluice_gap_record*)p;
-  L->rec->stamp = 0;
-  void* dp = nullptr;
-  SLUICE_HIP_CHECK(hipHostGetDevicePointer(&dp, p, 0));
-  L->rec_dev = (sluice_gap_record*)dp;
-  SLUICE_HIP_CHECK(hipMalloc((void**)&L->local_of_dev, sizeof(int32_t) * L->c.E));
-  std::vector<int32_t> lof(L->c.local_of.begin(), L->c.local_of.end());
-  SLUICE_HIP_CHECK(hipMemcpy(L->local_of_dev, lof.data(), sizeof(int32_t) * L->c.E,
-                             hipMemcpyHostToDevice));
-  return SLUICE_OK;
+extern "C" int sluice_layer_gap_launch(sluice_layer* L, const int32_t* topk_ids, int n,
+                                       const void* hs_src, void* hs_dst, size_t hs_bytes,
+                                       sluice_stream_t stream) {
+  if (L == nullptr || n < 0 || n > SLUICE_MAX_PAIRS || (n > 0 && topk_ids == nullptr))
+    return SLUICE_E_INVAL;
+  if (L->mb == nullptr || L->map_dev == nullptr) return SLUICE_E_STATE;
+  return launch_gap(L, topk_ids, n, hs_src, hs_dst, hs_bytes, (hipStream_t)stream);
+}
+
+extern "C" int sluice_layer_gap_serve(sluice_layer* L, int fast_hit, sluice_stream_t compute) {
+  if (L == nullptr) return SLUICE_E_INVAL;
+  if (L->mb == nullptr || L->server != nullptr) return SLUICE_E_STATE;
+  return serve_one(L, fast_hit != 0, true, (hipStream_t)compute);
 }
 
 extern "C" int sluice_layer_gap(sluice_layer* L, const int32_t* topk_ids, int n, int fast_hit,
                                 sluice_stream_t compute) {
-  if (L == nullptr || n < 0 || (n > 0 && topk_ids == nullptr)) return SLUICE_E_INVAL;
-  if (L->map_dev == nullptr) return SLUICE_E_STATE;
-  int rc = layer_device_init(L);
-  if (rc) return rc;
-  hipStream_t cs = (hipStream_t)compute;
+  if (L == nullptr || n < 0 || n > SLUICE_MAX_PAIRS || (n > 0 && topk_ids == nullptr))
+    return SLUICE_E_INVAL;
+  if (L->mb == nullptr || L->map_dev == nullptr || L->server != nullptr) return SLUICE_E_STATE;
+  int rc = launch_gap(L, topk_ids, n, nullptr, nullptr, 0, (hipStream_t)compute);
+  if (rc != SLUICE_OK) return rc;
+  return serve_one(L, fast_hit != 0, true, (hipStream_t)compute);
+}
 
-  // 1. publish the step's selection into the host record.
-  int32_t stamp = L->stamp + 1;
-  if (stamp <= 0) stamp = 1;
-  L->stamp = stamp;
-  hipLaunchKernelGGL(slot_lookup_kernel, dim3(1), dim3(kLookupThreads), 0, cs, topk_ids, n,
-                     L->map_dev, L->local_of_dev, L->c.E, L->rec_dev, stamp);
-  SLUICE_HIP_CHECK(hipGetLastError());
+extern "C" int sluice_gap_server_create(sluice_layer* const* layers, int n_layers, int fast_hit,
+                                        sluice_gap_server** out) {
+  if (out == nullptr || n_layers <= 0 || layers == nullptr) return SLUICE_E_INVAL;
+  *out = nullptr;
+  sluice_gap_server* S = new (std::nothrow) sluice_gap_server();
+  if (S == nullptr) return SLUICE_E_NOMEM;
+  for (int i = 0; i < n_layers; ++i) {
+    sluice_layer* L = layers[i];
+    if (L == nullptr || L->mb == nullptr || L->server != nullptr) {
+      delete S;
+      return L == nullptr ? SLUICE_E_INVAL : SLUICE_E_STATE;
+    }
+    for (sluice_layer* M : S->layers)
+      if (M == L) {
+        delete S;
+        return SLUICE_E_INVAL;
+      }
+    S->layers.push_back(L);
+  }
+  S->fast_hit = fast_hit != 0;
+  S->device = S->layers[0]->device;
+  for (sluice_layer* L : S->layers) L->server = S;
+  try {
+    S->th = std::thread(server_loop, S);
+  } catch (...) {
+    for (sluice_layer* L : S->layers) L->server = nullptr;
+    delete S;
+    return SLUICE_E_NOMEM;
+  }
+  *out = S;
+  return SLUICE_OK;
+}
 
-  // 2. wait for it (bounded; the exactness anchor of the gap).
-  volatile int32_t* sp = &L->rec->stamp;
-  if (*sp != stamp) {
-    const double t0 = now_s();
-    unsigned spins = 0;
-    while (__atomic_load_n((const int32_t*)sp, __ATOMIC_ACQUIRE) != stamp) {
+// Wait until every record posted so far has been served; returns the sticky
+// error of the server, if any.  Call after the streams that launched gaps
+// have been synchronised.
+extern "C" int sluice_gap_server_drain(sluice_gap_server* S, double timeout_s) {
+  if (S == nullptr) return SLUICE_E_INVAL;
+  const double t0 = now_s();
+  for (sluice_layer* L : S->layers) {
+    for (;;) {
+      const int dev_status = __atomic_load_n(&L->mb->dev_status, __ATOMIC_ACQUIRE);
+      if (dev_status != 0) {
+        int zero = 0;
+        S->error.compare_exchange_strong(zero, dev_status);
+        break;
+      }
+      const int32_t posted = __atomic_load_n(&L->mb->req_stamp, __ATOMIC_ACQUIRE);
+      if (L->done_stamp.load(std::memory_order_acquire) == posted) break;
+      if (S->error.load() != 0) break;
+      if (now_s() - t0 > timeout_s) return SLUICE_E_TIMEOUT;
       _mm_pause();
-      if ((++spins & 4095u) == 0) {
-        hipError_t q = hipStreamQuery(cs);
-        if (q != hipSuccess && q != hipErrorNotReady) return (int)q;
-        if (now_s() - t0 > gap_timeout_s()) return SLUICE_E_TIMEOUT;
-      }
     }
   }
-  __atomic_thread_fence(__ATOMIC_ACQUIRE);
-  const int n_uniq = L->rec->n_uniq;
-  if (n_uniq < 0 || n_uniq > L->c.E) return SLUICE_E_STATE;
+  return S->error.load();
+}
 
-  // 3. bookkeeping.
-  L->streams.clear();
-  bool map_write = false;
-  const int grc = L->c.gap(L->rec->uniq, n_uniq, fast_hit != 0, L->streams, map_write);
+extern "C" int sluice_gap_server_error(const sluice_gap_server* S) {
+  return S == nullptr ? SLUICE_E_INVAL : S->error.load();
+}
 
-  // 4. stream misses: copy stream waits for compute (the previous step's
-  //    GEMM may still read a victim slot), then compute waits for the copies.
-  const int n_streams = (int)L->streams.size() / 2;
-  if (n_streams > 0) {
-    DeviceRes* R = nullptr;
-    rc = device_res(L->device, &R);
-    if (rc) return rc;
-    SLUICE_HIP_CHECK(hipEventRecord(R->ev_compute, cs));
-    SLUICE_HIP_CHECK(hipStreamWaitEvent(R->copy, R->ev_compute, 0));
-    for (int i = 0; i < n_streams; ++i) {
-      const int local = L->streams[2 * i], slot = L->streams[2 * i + 1];
-      for (const ParamRows& p : L->params) {
-        SLUICE_HIP_CHECK(hipMemcpyAsync(p.slot_base + (size_t)slot * p.row_bytes,
-                                        p.host_base + (size_t)local * p.row_bytes, p.row_bytes,
-                                        hipMemcpyHostToDevice, R->copy));
-        L->bytes += (int64_t)p.row_bytes;
-      }
-    }
-    if (grc != 0) return grc;  // overflow: the reference raises before the compute wait
-    SLUICE_HIP_CHECK(hipEventRecord(R->ev_copy, R->copy));
-    SLUICE_HIP_CHECK(hipStreamWaitEvent(cs, R->ev_copy, 0));
-  } else if (grc != 0) {
-    return grc;
-  }
+extern "C" int sluice_gap_server_destroy(sluice_gap_server* S) {
+  if (S == nullptr) return SLUICE_OK;
+  S->stop.store(true, std::memory_order_release);
+  if (S->th.joinable()) S->th.join();
+  for (sluice_layer* L : S->layers) L->server = nullptr;
+  const int err = S->error.load();
+  delete S;
+  return err;
+}
 
-  // 5. standing map.
-  if (map_write) {
-    SlotTable tab;
-    tab.n = L->c.S;
-    L->c.slot_globals(tab.g);
-    hipLaunchKernelGGL(map_refresh_kernel, dim3(1), dim3(256), 0, cs, L->map_dev, L->c.E, tab);
-    SLUICE_HIP_CHECK(hipGetLastError());
-  }
+// After an abort: once every stream that ran gap kernels is synchronised,
+// clear the abort flag and line the host's stamps up with the device's, so
+// the layers can be used again (their slot state is whatever the served
+// records left; the aborted steps' outputs are invalid).
+extern "C" int sluice_gap_abort(int set) {
+  if (g_abort_host == nullptr) return SLUICE_OK;
+  __atomic_store_n(g_abort_host, set ? 1 : 0, __ATOMIC_RELEASE);
+  return SLUICE_OK;
+}
+
+extern "C" int sluice_layer_gap_resync(sluice_layer* L) {
+  if (L == nullptr || L->mb == nullptr || L->server != nullptr) return SLUICE_E_INVAL;
+  int32_t dev_stamp = 0;
+  SLUICE_HIP_CHECK(hipMemcpy(&dev_stamp, L->dev_block + L->c.E, sizeof(int32_t),
+                             hipMemcpyDeviceToHost));
+  std::lock_guard<std::mutex> lk(L->mu);
+  L->host_stamp = dev_stamp;
+  L->done_stamp.store(dev_stamp);
+  __atomic_store_n(&L->mb->ack_stamp, dev_stamp, __ATOMIC_RELEASE);
+  __atomic_store_n(&L->mb->req_stamp, dev_stamp, __ATOMIC_RELEASE);
+  __atomic_store_n(&L->mb->dev_status, 0, __ATOMIC_RELEASE);
   return SLUICE_OK;
 }
 
@@ -298,6 +684,8 @@ extern "C" int sluice_layer_gap_host(sluice_layer* L, const int32_t* ids, int n,
                                      int32_t* streams, int max_streams, int* n_streams,
                                      int* map_written) {
   if (L == nullptr || n < 0 || (n > 0 && ids == nullptr)) return SLUICE_E_INVAL;
+  if (L->server != nullptr) return SLUICE_E_STATE;
+  std::lock_guard<std::mutex> lk(L->mu);
   // sorted(set(ids)) restricted to [0, E)
   std::vector<uint8_t> present(L->c.E, 0);
   for (int i = 0; i < n; ++i)
@@ -319,11 +707,13 @@ extern "C" int sluice_layer_gap_host(sluice_layer* L, const int32_t* ids, int n,
   return rc;
 }
 
-extern "C" int sluice_layer_state(const sluice_layer* L, int32_t* slot_of, int32_t* expert_in_slot,
+extern "C" int sluice_layer_state(const sluice_layer* Lc, int32_t* slot_of, int32_t* expert_in_slot,
                                   int32_t* probation, int* n_probation, int32_t* protected_,
                                   int* n_protected, int32_t* free_slots, int* n_free,
                                   int64_t* counters) {
-  if (L == nullptr) return SLUICE_E_INVAL;
+  if (Lc == nullptr) return SLUICE_E_INVAL;
+  sluice_layer* L = const_cast<sluice_layer*>(Lc);
+  std::lock_guard<std::mutex> lk(L->mu);
   const slru::Cache& c = L->c;
   if (slot_of)
     for (int l = 0; l < c.local_n; ++l) slot_of[l] = c.slot_of[l];
@@ -353,8 +743,10 @@ extern "C" int sluice_layer_state(const sluice_layer* L, int32_t* slot_of, int32
   return SLUICE_OK;
 }
 
-extern "C" int sluice_layer_standing_map(const sluice_layer* L, int32_t* map_out) {
-  if (L == nullptr || map_out == nullptr) return SLUICE_E_INVAL;
+extern "C" int sluice_layer_standing_map(const sluice_layer* Lc, int32_t* map_out) {
+  if (Lc == nullptr || map_out == nullptr) return SLUICE_E_INVAL;
+  sluice_layer* L = const_cast<sluice_layer*>(Lc);
+  std::lock_guard<std::mutex> lk(L->mu);
   L->c.standing_map(map_out);
   return SLUICE_OK;
 }
@@ -413,9 +805,10 @@ extern "C" const char* sluice_strerror(int code) {
     case SLUICE_E_INVAL: return "invalid argument or shape outside kernel limits";
     case SLUICE_E_OVERFLOW:
       return "Sluice router-split: working set exceeds slots on a decode-sized step; raise SLUICE_SLOTS.";
-    case SLUICE_E_TIMEOUT: return "timed out waiting for the device slot-lookup record";
+    case SLUICE_E_TIMEOUT: return "timed out waiting for the device gap record";
     case SLUICE_E_NOMEM: return "host allocation failed";
     case SLUICE_E_STATE: return "object used in a state it does not allow";
+    case SLUICE_E_ABORTED: return "gap aborted after an earlier error";
     default:
       if (code > 0) return hipGetErrorString((hipError_t)code);
       return "unknown sluice error";

@@ -433,13 +433,16 @@ class _StoreMoELayer(nn.Module):
 
 
 class SyntheticDecoder:
-    """Random-init decoder of a SPECS shape, decoded in hipGraph pieces.
+    """Random-init decoder of a SPECS shape, decoded with hipGraphs.
 
     Piece p holds everything between MoE layer p-1's gap and MoE layer p's
     gap: MoE layer p-1's expert product + shared experts + residual, every
     dense/attention block up to MoE layer p, and MoE layer p's norm, gate and
     top-k routing.  The last piece ends with the final norm, the LM head and
-    the greedy next-token write.  Between pieces the eager gap runs.
+    the greedy next-token write.  With the gap server (default) the gap op
+    is a device launch and the whole step -- pieces and gaps -- is captured
+    as one graph; with ``gap_server=False`` each piece is a graph and the
+    reference's eager gap runs between them.
     Prompts are synthetic: the first ``prompt_len`` KV positions hold random
     latents/keys/values; decoding starts at position ``prompt_len``.
 
@@ -456,7 +459,7 @@ class SyntheticDecoder:
                  gen_len: int = 256, seed: int = 0, device=None, shared_host_pool: bool = True,
                  zipf_s: float = 1.1, rho: float = 0.7, sigma: float = 0.5,
                  gate_std: float = 0.004, uniform_routing: bool = False, fast_hit: bool = True,
-                 layers: int = None):
+                 layers: int = None, gap_server: bool = True):
         self.sp = sp = dict(SPECS[spec])
         if layers is not None:
             sp["layers"] = layers
@@ -504,6 +507,8 @@ class SyntheticDecoder:
                 self.moe_layers.append(blk.moe)
             self.blocks.append(blk)
         self.off = build_offloaded([m for m in self.moe_layers], slots, dev, fast_hit=fast_hit)
+        if gap_server:
+            self.off.start_gap_server()
         self.caches = [self.off._caches[id(m)] for m in self.moe_layers]
         assert [id(c) for c in self.off._rs_caches] == [id(c) for c in self.caches]
         for m in self.moe_layers:
@@ -516,6 +521,7 @@ class SyntheticDecoder:
         # per-batch-size static state
         self.state = {}
         self.graphs = {}
+        self.layer_io = {}
         self.pool = None
 
     # -- state -----------------------------------------------------------------
@@ -618,54 +624,88 @@ class SyntheticDecoder:
     def gap(self, n, ti):
         self.off._router_split_gap(n, ti)
 
+    def _step_fn(self, c):
+        """The whole step: every piece, with the ``vllm::sluice_stream_gap``
+        op between a MoE layer's routing and its expert product (the op's
+        output feeds the experts, as in the router-split entry).  Records
+        each MoE layer's routing/activation tensors in ``self.layer_io[c]``."""
+        ps = self.pieces(c)
+        rec = []
+
+        def run(io):
+            rec.clear()
+            for fn, gap_idx in ps:
+                fn(io)
+                if gap_idx is not None:
+                    io["hn"] = torch.ops.vllm.sluice_stream_gap(io["hn"], io["ti"], gap_idx)
+                    rec.append({"hn": io["hn"], "ti": io["ti"], "tw": io["tw"]})
+            self.layer_io[c] = list(rec)
+
+        return run
+
     def step_eager(self, c):
-        """One eager step; the gap goes through the registered
-        ``vllm::sluice_stream_gap`` op and its output feeds the experts."""
+        """One eager step through the registered ops."""
         from sluice_amd.offloader import activate
 
         activate(self.off)
         io = {}
-        ps = self.pieces(c)
-        for fn, gap_idx in ps:
-            fn(io)
-            if gap_idx is not None:
-                io["hn"] = torch.ops.vllm.sluice_stream_gap(io["hn"], io["ti"], gap_idx)
+        self._step_fn(c)(io)
         return io
 
     def capture(self, c, warmup: int = 2):
-        """Capture every piece for batch size c (after eager warmup steps)."""
+        """Capture batch size c after eager warm-up steps.  With the gap
+        server the whole step (gap launches included) is ONE graph; with
+        inline gaps every piece between two gaps is a graph and the gaps run
+        eagerly in between."""
+        from sluice_amd.offloader import activate
+
+        activate(self.off)
         st = self._state(c)
         for _ in range(warmup):
             self.step_eager(c)
-        torch.cuda.synchronize()
-        ps = self.pieces(c)
-        graphs = []
-        io = {}
+        self.sync()
         if self.pool is None:
             self.pool = torch.cuda.graph_pool_handle()
         s = torch.cuda.Stream(device=self.dev)
         s.wait_stream(torch.cuda.current_stream())
-        for fn, gap_idx in ps:
+        graphs = []
+        if self.off._server is not None:
+            io = {}
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, pool=self.pool, stream=s):
-                fn(io)
-            graphs.append((g, gap_idx, dict(io)))
-            if gap_idx is not None:
-                # the captured pieces run only on replay; the recorded routing
-                # tensors are what the gap will read after each replay
-                pass
+                self._step_fn(c)(io)
+            graphs.append((g, None, io))
+        else:
+            ps = self.pieces(c)
+            io = {}
+            rec = []
+            for fn, gap_idx in ps:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, pool=self.pool, stream=s):
+                    fn(io)
+                graphs.append((g, gap_idx, dict(io)))
+                if gap_idx is not None:
+                    rec.append({"hn": io["hn"], "ti": io["ti"], "tw": io["tw"]})
+            self.layer_io[c] = rec
         torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
+        self.sync()
         self.graphs[c] = graphs
         self.reset(c)
+        del st
         return graphs
 
     def step_graphs(self, c):
-        graphs = self.graphs[c]
-        for g, gap_idx, io in graphs:
+        for g, gap_idx, io in self.graphs[c]:
             g.replay()
             if gap_idx is not None:
                 self.gap(gap_idx, io["ti"])
 
+    def sync(self):
+        """Device synchronise + every gap record served (raises gap errors)."""
+        self.off.drain()
+
     def gap_counters(self):
         return self.off.gap_counters()
+
+    def close(self):
+        self.off.close()

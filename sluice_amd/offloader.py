@@ -155,6 +155,7 @@ class ExpertStreamOffloader:
         self._rs_fast_hits = 0
         self._rs_layers = 0
         self._rs_thr: Optional[int] = None
+        self._server: Optional[int] = None
         if self.router_split:
             _register_stream_gap_op(self)
         logger.info("Sluice ExpertStreamOffloader enabled (%d cache slots per layer, "
@@ -375,30 +376,80 @@ class ExpertStreamOffloader:
         logger.warning("Sluice: ROUTER-SPLIT armed on %d/%d MoE layers. skips=%s", patched, seen,
                        skips or "{}")
 
-    def _router_split_gap(self, idx: int, topk_ids: torch.Tensor) -> None:
-        """Body of ``vllm::sluice_stream_gap`` (src/sluice/offloader.py:2362-2467)."""
+    def _router_split_gap(self, idx: int, topk_ids: torch.Tensor,
+                          hidden_states: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
+        """Body of ``vllm::sluice_stream_gap`` (src/sluice/offloader.py:2362-2467).
+
+        Launches the layer's gap kernel on the current stream and, unless a
+        gap server serves this offloader, serves its record inline (the
+        reference's eager gap).  When ``hidden_states`` is given, returns the
+        op's fresh copy of it, written by the gap kernel itself."""
         cache = self._rs_caches[idx]
-        self._rs_gaps += 1
-        if self._rs_gaps == 1 or self._rs_gaps % 2000 == 0:
-            logger.warning("Sluice DIAG[rs]: router-split layers=%d gap-calls=%d misses=%d "
-                           "fast-hits=%d%s", len(self._rs_caches), self._rs_gaps,
-                           self._rs_misses, self._rs_fast_hits,
-                           " NOOP-GAP(OUTPUTS INVALID)" if self._rs_noop else "")
+        if self._server is None:
+            self._rs_gaps += 1
+            if self._rs_gaps == 1 or self._rs_gaps % 2000 == 0:
+                c = self.gap_counters()
+                logger.warning("Sluice DIAG[rs]: router-split layers=%d gap-calls=%d misses=%d "
+                               "fast-hits=%d%s", len(self._rs_caches), self._rs_gaps,
+                               c["misses"], c["fast_hits"],
+                               " NOOP-GAP(OUTPUTS INVALID)" if self._rs_noop else "")
         if self._rs_noop:
-            return
+            return None if hidden_states is None else hidden_states.clone()
         ids = topk_ids if topk_ids.dtype == torch.int32 else topk_ids.to(torch.int32)
         ids = ids.contiguous()
         lib = _lib.load()
-        before = cache.stats() if logger.isEnabledFor(logging.DEBUG) else None
-        rc = lib.sluice_layer_gap(cache.handle, ids.data_ptr(), ids.numel(),
-                                  int(self._rs_fast_hit),
-                                  torch.cuda.current_stream(ids.device).cuda_stream)
-        if rc == _lib.SLUICE_E_OVERFLOW:
-            raise RuntimeError("Sluice router-split: working set exceeds slots on a "
-                               "decode-sized step; raise SLUICE_SLOTS.")
-        _lib.check(rc, "sluice_layer_gap")
-        if before is not None:
-            logger.debug("gap %d: %s", idx, cache.stats())
+        stream = torch.cuda.current_stream(ids.device).cuda_stream
+        out = None
+        src = dst = None
+        nbytes = 0
+        if hidden_states is not None:
+            out = torch.empty_like(hidden_states)
+            nb = hidden_states.numel() * hidden_states.element_size()
+            if (hidden_states.is_contiguous() and nb % 16 == 0
+                    and hidden_states.data_ptr() % 16 == 0 and out.data_ptr() % 16 == 0):
+                src, dst, nbytes = hidden_states.data_ptr(), out.data_ptr(), nb
+            else:
+                out.copy_(hidden_states)
+        rc = lib.sluice_layer_gap_launch(cache.handle, ids.data_ptr(), ids.numel(), src, dst,
+                                         nbytes, stream)
+        _lib.check(rc, "sluice_layer_gap_launch")
+        if self._server is None:
+            rc = lib.sluice_layer_gap_serve(cache.handle, int(self._rs_fast_hit), stream)
+            _raise_gap(rc, "sluice_layer_gap_serve")
+        return out
+
+    # -- gap server ---------------------------------------------------------------
+    def start_gap_server(self) -> None:
+        """Serve every router-split layer's gap records on a native thread:
+        the gap op becomes a pure device launch (capturable), so a whole
+        decode step, gaps included, can replay as one hipGraph.  Slot
+        assignment and maps are the same as with inline gaps."""
+        if self._server is not None or not self._rs_caches:
+            return
+        lib = _lib.load()
+        handles = (ctypes.c_void_p * len(self._rs_caches))(*[c.handle for c in self._rs_caches])
+        srv = ctypes.c_void_p()
+        _lib.check(lib.sluice_gap_server_create(handles, len(self._rs_caches),
+                                                int(self._rs_fast_hit), ctypes.byref(srv)),
+                   "sluice_gap_server_create")
+        self._server = srv.value
+
+    def drain(self, timeout_s: float = 60.0) -> None:
+        """Synchronise the device and wait until every gap record it posted
+        has been served; raises what the gap raised (e.g. the overflow
+        RuntimeError)."""
+        torch.cuda.synchronize()
+        if self._server is None:
+            return
+        rc = _lib.load().sluice_gap_server_drain(self._server, float(timeout_s))
+        _raise_gap(rc, "sluice_gap_server_drain")
+
+    def stop_gap_server(self) -> None:
+        if self._server is None:
+            return
+        self.drain()
+        srv, self._server = self._server, None
+        _raise_gap(_lib.load().sluice_gap_server_destroy(srv), "sluice_gap_server_destroy")
 
     def gap_counters(self) -> dict:
         tot = {"gaps": 0, "misses": 0, "fast_hits": 0, "map_writes": 0, "bytes": 0}
@@ -414,10 +465,22 @@ class ExpertStreamOffloader:
 
     def close(self) -> None:
         lib = _lib.load()
+        if self._server is not None:
+            srv, self._server = self._server, None
+            torch.cuda.synchronize()
+            lib.sluice_gap_server_drain(srv, 60.0)
+            lib.sluice_gap_server_destroy(srv)
         for c in self._caches.values():
             if c.handle:
                 lib.sluice_layer_destroy(c.handle)
                 c.handle = None
+
+
+def _raise_gap(rc: int, what: str) -> None:
+    if rc == _lib.SLUICE_E_OVERFLOW:
+        raise RuntimeError("Sluice router-split: working set exceeds slots on a "
+                           "decode-sized step; raise SLUICE_SLOTS.")
+    _lib.check(rc, what)
 
 
 def _make_entry(idx, w13, w2, gne, emap, shared_layer, sel, orig, gate, thr, w13_scale, w2_scale,
@@ -458,8 +521,7 @@ def _sluice_stream_gap_impl(hidden_states: torch.Tensor, topk_ids: torch.Tensor,
     off = _ACTIVE_GAP["offloader"]
     if off is None:
         raise RuntimeError("vllm::sluice_stream_gap called with no active Sluice offloader")
-    off._router_split_gap(int(layer_idx), topk_ids)
-    return hidden_states.clone()
+    return off._router_split_gap(int(layer_idx), topk_ids, hidden_states)
 
 
 def activate(offloader: ExpertStreamOffloader) -> None:

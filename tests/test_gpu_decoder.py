@@ -12,11 +12,11 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-def _run(spec, layers, c, steps, graphs, slots):
+def _run(spec, layers, c, steps, graphs, slots, gap_server):
     from sluice_amd.decoder import SyntheticDecoder
 
     dec = SyntheticDecoder(spec, max_batch=c, slots=slots, gen_len=steps + 16, layers=layers,
-                           device=DEV, seed=3)
+                           device=DEV, seed=3, gap_server=gap_server)
     toks = []
     if graphs:
         dec.capture(c)
@@ -30,24 +30,36 @@ def _run(spec, layers, c, steps, graphs, slots):
         for _ in range(steps):
             dec.step_eager(c)
             toks.append(dec.state[c].tokens.clone())
-    torch.cuda.synchronize()
+    dec.sync()
     out = torch.stack(toks).cpu().numpy()
     state = [cache._state() for cache in dec.caches]
     maps = [cache.expert_map_buf.cpu().tolist() for cache in dec.caches]
-    dec.off.close()
+    dec.close()
     return out, state, maps
 
 
 @pytest.mark.parametrize("spec,layers,c,slots", [("v2lite", 3, 4, 48), ("qwen3", 2, 8, 64)])
-def test_graph_pieces_match_eager_ops(spec, layers, c, slots):
+def test_one_graph_step_with_gap_server_matches_eager_inline_gaps(spec, layers, c, slots):
+    """Reference structure (eager gaps served inline between ops) against the
+    MI355X structure (gap server, whole step one hipGraph): identical tokens,
+    slot assignment, segment order, counters and maps."""
     print(f"decoder {spec} layers={layers} c={c}", flush=True)
-    a, sa, ma = _run(spec, layers, c, 12, graphs=False, slots=slots)
-    b, sb, mb = _run(spec, layers, c, 12, graphs=True, slots=slots)
+    a, sa, ma = _run(spec, layers, c, 12, graphs=False, slots=slots, gap_server=False)
+    b, sb, mb = _run(spec, layers, c, 12, graphs=True, slots=slots, gap_server=True)
     assert np.array_equal(a, b)
     for x, y in zip(sa, sb):
         assert x["expert_in_slot"] == y["expert_in_slot"]
         assert x["probation"] == y["probation"] and x["protected"] == y["protected"]
         assert x["counters"][:4] == y["counters"][:4]
+    assert ma == mb
+    assert sum(x["counters"][1] for x in sa) > 0  # the miss path was exercised
+
+
+def test_piece_graphs_with_inline_gaps_match_eager():
+    a, sa, ma = _run("v2lite", 2, 2, 8, graphs=False, slots=48, gap_server=False)
+    b, sb, mb = _run("v2lite", 2, 2, 8, graphs=True, slots=48, gap_server=False)
+    assert np.array_equal(a, b)
+    assert [x["expert_in_slot"] for x in sa] == [y["expert_in_slot"] for y in sb]
     assert ma == mb
 
 
@@ -57,7 +69,8 @@ def test_moe_layer_against_oracle():
     from oracle import moe as om
     from sluice_amd.decoder import SyntheticDecoder
 
-    dec = SyntheticDecoder("v2lite", max_batch=8, slots=48, gen_len=16, layers=2, device=DEV)
+    dec = SyntheticDecoder("v2lite", max_batch=8, slots=48, gen_len=16, layers=2, device=DEV,
+                           gap_server=False)
     m = dec.moe_layers[0]
     cache = dec.caches[0]
     rng = np.random.default_rng(0)
@@ -75,4 +88,4 @@ def test_moe_layer_against_oracle():
         err = om.rel_l2(out.float().cpu().numpy(), ref)
         print(f"  step {step} rel_l2={err:.2e}", flush=True)
         assert err <= 1e-2
-    dec.off.close()
+    dec.close()
