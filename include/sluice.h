@@ -153,6 +153,20 @@ int sluice_fused_experts_fp8(const void* x, const void* w13,
                              size_t workspace_bytes, void* out,
                              sluice_stream_t stream);
 
+/* Health of a workspace used by the fused kernel: SLUICE_OK when its work
+ * counters are back at zero (no call in flight or interrupted); *error_out =
+ * 1 if a dependency wait inside the kernel ever ran out of time (2 s; the
+ * results of that call are invalid).  Synchronous; for tests and debugging.
+ * The workspace must be zero-filled before its first use; every call leaves
+ * it so.  Calls sharing a workspace must not overlap. */
+int sluice_fused_experts_status(const void* workspace, int* error_out);
+
+/* Select the launch shape of sluice_fused_experts_*: 1 = one persistent
+ * kernel per call when T*k <= 256 (cross-workgroup hand-offs), 0 = four
+ * staged kernels (the default; SLUICE_MOE_FUSED=1 sets 1 at load).  Returns
+ * the previous setting.  Process-wide; no counterpart in the reference. */
+int sluice_moe_set_fused(int enable);
+
 /* Token permute / align-to-block (vLLM moe_align_block_size): groups the
  * T*k (token, expert) pairs by slot into blocks of <= SLUICE_BLOCK_M pairs,
  * slots ascending, pairs ascending within a slot.  plan (device int32):

@@ -1,0 +1,90 @@
+/*
+ * sluice_decoder.h - kernels of the synthetic decoders that carry the
+ * routed-MoE decode path in the benchmarks (DeepSeek-V2-Lite-shaped MLA
+ * attention, Qwen3-MoE-shaped GQA attention with q/k norm, RMSNorm with a
+ * fused residual add, SwiGLU activation, router logits).  They are not part
+ * of the reference's interface: the reference runs these layers inside
+ * vLLM; here they replace chains of small torch ops so a decode step spends
+ * its time in the MoE path rather than in kernel launches.
+ *
+ * Same conventions as sluice.h: int status (0 ok, positive hipError_t,
+ * negative SLUICE_E_*), plain device pointers, asynchronous on `stream`.
+ * Activations and weights are bf16 (uint16 storage); positions and step
+ * counters are int64 device scalars/arrays (torch long).  Every kernel
+ * checks a position against the cache length and skips rows outside it.
+ */
+#ifndef SLUICE_DECODER_H_
+#define SLUICE_DECODER_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "sluice.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* x [rows, H] becomes bf16(x + delta) in place when delta != NULL; then
+ * out [rows, H] = bf16(x * rsqrt(mean(x^2) + eps) * w), fp32 arithmetic.
+ * H % 8 == 0. */
+int sluice_dec_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int rows, int H,
+                           float eps, sluice_stream_t stream);
+
+/* Skinny GEMM: y [T, N] = bf16(x [T, K] . w [N, K]^T), fp32 accumulation,
+ * T <= 16, N % 16 == 0, K % 32 == 0 (MFMA bf16, weights streamed once). */
+int sluice_dec_linear(const void* x, const void* w, int T, int N, int K, void* y,
+                      sluice_stream_t stream);
+
+/* out [rows, I] = bf16(silu(gu[:, :I]) * gu[:, I:]), gu [rows, 2I].  I % 4 == 0. */
+int sluice_dec_silu_mul(const void* gu, void* out, int rows, int I, sluice_stream_t stream);
+
+/* Router logits: out [rows, E] fp32 = hn [rows, H] . wg [E, H]^T, plus
+ * bias_table[(step % n_steps) * bias_rows + t][e] when bias_table != NULL
+ * (step read from device memory).  rows <= 16, H % 512 == 0. */
+int sluice_dec_gate_logits(const void* hn, const void* wg, const float* bias_table,
+                           const int64_t* step, int n_steps, int bias_rows, int rows, int H, int E,
+                           float* out, sluice_stream_t stream);
+
+/* MLA decode (DeepSeek-V2 latent attention with absorbed up-projections).
+ * prep: q rows of q_stride elements holding nh heads of (nope then rope),
+ *   kva rows of kva_stride elements holding lora then rope values
+ *   -> q_lat [c, nh, lora] fp32 = q_nope . w_uk[h] (w_uk [nh, nope, lora]),
+ *      q_pe [c, nh, rope] fp32 = rope(q_pe),
+ *      ckv_cache [c, L, lora] row pos[t] = bf16(rmsnorm(kva[:lora]) * kv_norm),
+ *      kpe_cache [c, L, rope] row pos[t] = bf16(rope(kva[lora:])).
+ *   rope is rotate-half with cos/sin [*, rope/2] fp32 rows at pos[t].
+ * attend: scores over cache rows 0..pos[t] = (q_lat . ckv + q_pe . kpe) * scale,
+ *   softmax, o_lat = p . ckv, out [c, nh*vh] = bf16(o_lat . w_uv[h])
+ *   (w_uv [nh, lora, vh]).  lora == 512, rope == 64, nope % 2 == 0,
+ *   vh <= 256, L <= 4096. */
+int sluice_dec_mla_prep(const void* q, int q_stride, const void* kva, int kva_stride,
+                        const void* kv_norm, const void* w_uk, const float* cos_t,
+                        const float* sin_t, const int64_t* pos, int c, int nh, int nope, int rope,
+                        int lora, int L, float eps, float* q_lat, float* q_pe, void* ckv_cache,
+                        void* kpe_cache, sluice_stream_t stream);
+int sluice_dec_mla_attend(const float* q_lat, const float* q_pe, const void* ckv_cache,
+                          const void* kpe_cache, const void* w_uv, const int64_t* pos, int c,
+                          int nh, int rope, int lora, int vh, int L, float scale, void* out,
+                          sluice_stream_t stream);
+
+/* GQA decode with per-head q/k RMSNorm (Qwen3-MoE).
+ * prep: qkv [c, (nh + 2*kvh)*hd] -> q [c, nh, hd] fp32 = rope(rmsnorm(q_h) * q_norm),
+ *   k_cache [c, kvh, L, hd] row pos[t] = bf16(rope(rmsnorm(k_g) * k_norm)),
+ *   v_cache [c, kvh, L, hd] row pos[t] = v_g.
+ * attend: per query head h (kv head h / (nh/kvh)): softmax over rows
+ *   0..pos[t] of (q . k) * scale, out [c, nh*hd] = bf16(p . v).
+ *   hd == 128, L <= 4096. */
+int sluice_dec_gqa_prep(const void* qkv, const void* q_norm, const void* k_norm,
+                        const float* cos_t, const float* sin_t, const int64_t* pos, int c, int nh,
+                        int kvh, int hd, int L, float eps, float* q, void* k_cache, void* v_cache,
+                        sluice_stream_t stream);
+int sluice_dec_gqa_attend(const float* q, const void* k_cache, const void* v_cache,
+                          const int64_t* pos, int c, int nh, int kvh, int hd, int L, float scale,
+                          void* out, sluice_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SLUICE_DECODER_H_ */

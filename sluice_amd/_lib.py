@@ -1,4 +1,5 @@
-"""ctypes binding of libsluice_hip.so (the C ABI declared in include/sluice.h).
+"""ctypes binding of libsluice_hip.so (the C ABI declared in include/sluice.h and
+include/sluice_decoder.h).
 
 The shared library is built in-tree (``sluice_amd/libsluice_hip.so``) by
 ``sluice_amd.build``.  There is no fallback: when the library is missing the
@@ -53,6 +54,8 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,
          c_float, _P, _P, c_size_t, _P, _P],
     ),
+    "sluice_fused_experts_status": (c_int, [_P, POINTER(c_int)]),
+    "sluice_moe_set_fused": (c_int, [c_int]),
     "sluice_moe_plan_ints": (c_size_t, [c_int, c_int]),
     "sluice_moe_align": (c_int, [_P, c_int, c_int, _P, c_int, c_int, _P, _P]),
     "sluice_moe_gemm1_bf16": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, _P, _P]),
@@ -79,6 +82,29 @@ SIGNATURES = {
         [_P, _P, _P, _P, POINTER(c_int), _P, POINTER(c_int), _P, POINTER(c_int), _P],
     ),
     "sluice_layer_standing_map": (c_int, [_P, _P]),
+    # include/sluice_decoder.h
+    "sluice_dec_add_rmsnorm": (c_int, [_P, _P, _P, _P, c_int, c_int, c_float, _P]),
+    "sluice_dec_silu_mul": (c_int, [_P, _P, c_int, c_int, _P]),
+    "sluice_dec_linear": (c_int, [_P, _P, c_int, c_int, c_int, _P, _P]),
+    "sluice_dec_gate_logits": (
+        c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, _P]
+    ),
+    "sluice_dec_mla_prep": (
+        c_int,
+        [_P, c_int, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,
+         c_float, _P, _P, _P, _P, _P],
+    ),
+    "sluice_dec_mla_attend": (
+        c_int,
+        [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P],
+    ),
+    "sluice_dec_gqa_prep": (
+        c_int,
+        [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P, _P, _P],
+    ),
+    "sluice_dec_gqa_attend": (
+        c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P]
+    ),
 }
 
 _lib = None

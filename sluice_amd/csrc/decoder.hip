@@ -1,0 +1,711 @@
+// Kernels of the synthetic decoders around the routed-MoE path (not part of
+// the reference's interface; see include/sluice_decoder.h).  Each replaces a
+// chain of small torch ops with one launch: a decode step of a 27-48 layer
+// model otherwise spends most of its time launching 2-5 us kernels.
+#include <math.h>
+
+#include "common.h"
+#include "sluice_decoder.h"
+
+namespace {
+
+constexpr int kT = 256;  // threads per workgroup (4 waves)
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, SLUICE_WAVE);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, SLUICE_WAVE));
+  return v;
+}
+
+// Block-wide sum / max over kT threads (all threads get the result).
+__device__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int i = 0; i < kT / 64; ++i) s += red[i];
+  return s;
+}
+
+__device__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float s = -INFINITY;
+  for (int i = 0; i < kT / 64; ++i) s = fmaxf(s, red[i]);
+  return s;
+}
+
+__device__ __forceinline__ float bf(uint16_t b) { return bf16_bits_to_f32(b); }
+
+__device__ __forceinline__ void unpack8(u32x4_t v, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(v[i] << 16);
+    f[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+}
+
+// ---------------------------------------------------------------------------
+// Residual add + RMSNorm.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kT) void add_rmsnorm_kernel(uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ delta,
+                                                         const uint16_t* __restrict__ w,
+                                                         uint16_t* __restrict__ out, int H,
+                                                         float eps) {
+  __shared__ float red[kT / 64];
+  const int r = blockIdx.x;
+  uint16_t* xr = x + (size_t)r * H;
+  const uint16_t* dr = delta != nullptr ? delta + (size_t)r * H : nullptr;
+  float ss = 0.f;
+  for (int i = threadIdx.x * 8; i < H; i += kT * 8) {
+    float v[8];
+    unpack8(*reinterpret_cast<const u32x4_t*>(xr + i), v);
+    if (dr != nullptr) {
+      float d[8];
+      unpack8(*reinterpret_cast<const u32x4_t*>(dr + i), d);
+      u32x4_t o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = pack2(v[2 * j] + d[2 * j], v[2 * j + 1] + d[2 * j + 1]);
+      *reinterpret_cast<u32x4_t*>(xr + i) = o;
+      unpack8(o, v);  // the rounded sum, as the residual stream holds it
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
+  }
+  const float rstd = rsqrtf(block_sum(ss, red) / (float)H + eps);
+  for (int i = threadIdx.x * 8; i < H; i += kT * 8) {
+    float v[8], g[8];
+    unpack8(*reinterpret_cast<const u32x4_t*>(xr + i), v);
+    unpack8(*reinterpret_cast<const u32x4_t*>(w + i), g);
+    u32x4_t o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = pack2(v[2 * j] * rstd * g[2 * j], v[2 * j + 1] * rstd * g[2 * j + 1]);
+    *reinterpret_cast<u32x4_t*>(out + (size_t)r * H + i) = o;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU activation.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kT) void silu_mul_kernel(const uint16_t* __restrict__ gu,
+                                                      uint16_t* __restrict__ out, int I) {
+  const int r = blockIdx.y;
+  const int i = (blockIdx.x * kT + threadIdx.x) * 4;
+  if (i >= I) return;
+  const uint16_t* g = gu + (size_t)r * 2 * I + i;
+  const uint16_t* u = g + I;
+  const u32x2_t gv = *reinterpret_cast<const u32x2_t*>(g);
+  const u32x2_t uv = *reinterpret_cast<const u32x2_t*>(u);
+  float o[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float g0 = __uint_as_float(gv[j] << 16), g1 = __uint_as_float(gv[j] & 0xffff0000u);
+    const float u0 = __uint_as_float(uv[j] << 16), u1 = __uint_as_float(uv[j] & 0xffff0000u);
+    o[2 * j] = g0 / (1.0f + expf(-g0)) * u0;
+    o[2 * j + 1] = g1 / (1.0f + expf(-g1)) * u1;
+  }
+  *reinterpret_cast<u32x2_t*>(out + (size_t)r * I + i) = u32x2_t{pack2(o[0], o[1]), pack2(o[2], o[3])};
+}
+
+// ---------------------------------------------------------------------------
+// Router logits: one workgroup per expert, the 4 waves split H.
+// ---------------------------------------------------------------------------
+constexpr int kMaxRows = 16;
+
+__global__ __launch_bounds__(kT) void gate_logits_kernel(
+    const uint16_t* __restrict__ hn, const uint16_t* __restrict__ wg,
+    const float* __restrict__ bias_table, const int64_t* __restrict__ step, int n_steps,
+    int bias_rows, int rows, int H, int E, float* __restrict__ out) {
+  __shared__ float red[kT / 64][kMaxRows];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int e = blockIdx.x;
+  float acc[kMaxRows];
+#pragma unroll
+  for (int t = 0; t < kMaxRows; ++t) acc[t] = 0.f;
+  const uint16_t* wr = wg + (size_t)e * H;
+  const int h0 = wave * (H / 4), h1 = h0 + H / 4;
+  for (int i = h0 + lane * 8; i < h1; i += 64 * 8) {
+    float wv[8];
+    unpack8(*reinterpret_cast<const u32x4_t*>(wr + i), wv);
+#pragma unroll
+    for (int t = 0; t < kMaxRows; ++t) {
+      if (t < rows) {
+        float xv[8];
+        unpack8(*reinterpret_cast<const u32x4_t*>(hn + (size_t)t * H + i), xv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[t] += wv[j] * xv[j];
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kMaxRows; ++t) {
+    if (t < rows) {
+      const float v = wave_sum(acc[t]);
+      if (lane == 0) red[wave][t] = v;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < rows) {
+    const int t = threadIdx.x;
+    float v = red[0][t] + red[1][t] + red[2][t] + red[3][t];
+    if (bias_table != nullptr) {
+      long long st = *step;
+      st = ((st % n_steps) + n_steps) % n_steps;
+      v += bias_table[((size_t)st * bias_rows + t) * E + e];
+    }
+    out[(size_t)t * E + e] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MLA (DeepSeek-V2 latent attention, decode, absorbed up-projections).
+// ---------------------------------------------------------------------------
+constexpr int kLora = 512;
+constexpr int kRope = 64;
+constexpr int kMaxL = 4096;
+
+// grid (c, nh + 1): y < nh -> query head y; y == nh -> the token's kv row.
+__global__ __launch_bounds__(kT) void mla_prep_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kva,
+    const uint16_t* __restrict__ kv_norm, const uint16_t* __restrict__ w_uk,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    const int64_t* __restrict__ pos, int nh, int nope, int q_stride, int kva_stride, int L,
+    float eps, float* __restrict__ q_lat, float* __restrict__ q_pe,
+    uint16_t* __restrict__ ckv_cache, uint16_t* __restrict__ kpe_cache) {
+  __shared__ float qn[256];
+  __shared__ float red[kT / 64];
+  __shared__ float ql_part[kT / 64][kLora];
+  const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const long long p = pos[t];
+  if (p < 0 || p >= L) return;
+  const float* cr = cos_t + p * (kRope / 2);
+  const float* sr = sin_t + p * (kRope / 2);
+  if (h < nh) {
+    const uint16_t* qh = q + (size_t)t * q_stride + (size_t)h * (nope + kRope);
+    for (int d = tid; d < nope; d += kT) qn[d] = bf(qh[d]);
+    if (tid < kRope / 2) {
+      const float x1 = bf(qh[nope + tid]), x2 = bf(qh[nope + tid + kRope / 2]);
+      float* o = q_pe + ((size_t)t * nh + h) * kRope;
+      o[tid] = x1 * cr[tid] - x2 * sr[tid];
+      o[tid + kRope / 2] = x2 * cr[tid] + x1 * sr[tid];
+    }
+    __syncthreads();
+    // q_lat[j] = sum_d q_nope[d] w_uk[h][d][j]: wave w takes rows d = w, w+4,
+    // ..., a lane owns columns 8*lane..+8 (16-byte loads, 4 rows in flight);
+    // the waves' sums meet in LDS.
+    const int wave = tid >> 6, lane = tid & 63;
+    const uint16_t* wk = w_uk + (size_t)h * nope * kLora + lane * 8;
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    for (int d0 = wave; d0 < nope; d0 += 16) {
+      u32x4_t wv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int d = d0 + 4 * u;
+        wv[u] = *reinterpret_cast<const u32x4_t*>(wk + (size_t)(d < nope ? d : 0) * kLora);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int d = d0 + 4 * u;
+        const float qd = d < nope ? qn[d] : 0.f;
+        float c[8];
+        unpack8(wv[u], c);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += qd * c[j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ql_part[wave][lane * 8 + j] = acc[j];
+    __syncthreads();
+    float* o = q_lat + ((size_t)t * nh + h) * kLora;
+    for (int j = tid; j < kLora; j += kT)
+      o[j] = ql_part[0][j] + ql_part[1][j] + ql_part[2][j] + ql_part[3][j];
+    return;
+  }
+  // kv row: rmsnorm(kva[:lora]) * kv_norm, rope(kva[lora:])
+  const uint16_t* kr = kva + (size_t)t * kva_stride;
+  const uint32_t v2 = reinterpret_cast<const uint32_t*>(kr)[tid];
+  const float x0 = __uint_as_float(v2 << 16), x1 = __uint_as_float(v2 & 0xffff0000u);
+  const float rstd = rsqrtf(block_sum(x0 * x0 + x1 * x1, red) / (float)kLora + eps);
+  const uint32_t g2 = reinterpret_cast<const uint32_t*>(kv_norm)[tid];
+  uint32_t* crow = reinterpret_cast<uint32_t*>(ckv_cache + ((size_t)t * L + p) * kLora);
+  crow[tid] = pack2(x0 * rstd * __uint_as_float(g2 << 16),
+                    x1 * rstd * __uint_as_float(g2 & 0xffff0000u));
+  if (tid < kRope / 2) {
+    const float a = bf(kr[kLora + tid]), b = bf(kr[kLora + tid + kRope / 2]);
+    uint16_t* krow = kpe_cache + ((size_t)t * L + p) * kRope;
+    krow[tid] = f32_to_bf16_bits(a * cr[tid] - b * sr[tid]);
+    krow[tid + kRope / 2] = f32_to_bf16_bits(b * cr[tid] + a * sr[tid]);
+  }
+}
+
+// grid (c, nh), kA threads.  Scores: each wave takes rows l = wave,
+// wave + W, ... four at a time (four independent 1 KB loads and reductions
+// in flight); the latent sum: each wave accumulates its rows (a lane owns 8
+// latent columns, 16-byte loads, four rows in flight) and the waves are
+// summed in LDS; the value projection: a thread owns 2 value columns and a
+// slice of the latent rows, eight rows of w_uv in flight.
+constexpr int kA = 1024;
+constexpr int kAW = kA / 64;
+
+__global__ __launch_bounds__(kA) void mla_attend_kernel(
+    const float* __restrict__ q_lat, const float* __restrict__ q_pe,
+    const uint16_t* __restrict__ ckv_cache, const uint16_t* __restrict__ kpe_cache,
+    const uint16_t* __restrict__ w_uv, const int64_t* __restrict__ pos, int nh, int vh, int L,
+    float scale, uint16_t* __restrict__ out) {
+  __shared__ float s[kMaxL];
+  __shared__ float part[kAW][kLora];
+  __shared__ float ol[kLora];
+  __shared__ float red[kAW];
+  const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const long long p = pos[t];
+  if (p < 0 || p >= L) return;
+  const int n = (int)p + 1;
+  const uint16_t* cb = ckv_cache + (size_t)t * L * kLora;
+  const uint16_t* kb = kpe_cache + (size_t)t * L * kRope;
+  float ql[8];
+  {
+    const float* qrow = q_lat + ((size_t)t * nh + h) * kLora + lane * 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ql[j] = qrow[j];
+  }
+  const float qp = q_pe[((size_t)t * nh + h) * kRope + lane];
+  constexpr int U = 4;
+  float lmax = -INFINITY;
+  for (int l0 = wave; l0 < n; l0 += U * kAW) {
+    float dsum[U];
+    u32x4_t cv[U];
+    uint16_t kv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int l = l0 + u * kAW;
+      const int lc = l < n ? l : 0;
+      cv[u] = *reinterpret_cast<const u32x4_t*>(cb + (size_t)lc * kLora + lane * 8);
+      kv[u] = kb[(size_t)lc * kRope + lane];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float c[8];
+      unpack8(cv[u], c);
+      float d = qp * bf(kv[u]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) d += ql[j] * c[j];
+      dsum[u] = d;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+      for (int u = 0; u < U; ++u) dsum[u] += __shfl_xor(dsum[u], off, SLUICE_WAVE);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int l = l0 + u * kAW;
+      if (l < n) {
+        const float d = dsum[u] * scale;
+        if (lane == 0) s[l] = d;
+        lmax = fmaxf(lmax, d);
+      }
+    }
+  }
+  // block max
+  lmax = wave_max(lmax);
+  if (lane == 0) red[wave] = lmax;
+  __syncthreads();
+  float m = -INFINITY;
+  for (int i = 0; i < kAW; ++i) m = fmaxf(m, red[i]);
+  __syncthreads();
+  float psum = 0.f;
+  for (int l = tid; l < n; l += kA) {
+    const float e = expf(s[l] - m);
+    s[l] = e;
+    psum += e;
+  }
+  psum = wave_sum(psum);
+  if (lane == 0) red[wave] = psum;
+  __syncthreads();
+  float tot = 0.f;
+  for (int i = 0; i < kAW; ++i) tot += red[i];
+  const float inv = 1.0f / tot;
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  for (int l0 = wave; l0 < n; l0 += U * kAW) {
+    u32x4_t cv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int l = l0 + u * kAW;
+      cv[u] = *reinterpret_cast<const u32x4_t*>(cb + (size_t)(l < n ? l : 0) * kLora + lane * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int l = l0 + u * kAW;
+      const float pl = l < n ? s[l] : 0.f;
+      float c[8];
+      unpack8(cv[u], c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += pl * c[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) part[wave][lane * 8 + j] = acc[j];
+  __syncthreads();
+  for (int j = tid; j < kLora; j += kA) {
+    float v = 0.f;
+    for (int w = 0; w < kAW; ++w) v += part[w][j];
+    ol[j] = v * inv;
+  }
+  __syncthreads();
+  // out[v] = o_lat . w_uv[h][:, v]: thread = (column pair, slice of kAW rows' worth)
+  const uint16_t* wv = w_uv + (size_t)h * kLora * vh;
+  float* pq = &part[0][0];  // reused: [kAW][128] partial sums
+  constexpr int kRows = kLora / kAW;
+  for (int v0 = 0; v0 < vh; v0 += 128) {
+    const int vp = v0 + 2 * lane;
+    float a0 = 0.f, a1 = 0.f;
+    if (vp < vh) {
+      const uint16_t* col = wv + vp;
+      const int j0 = wave * kRows;
+      for (int j = j0; j < j0 + kRows; j += 8) {
+        uint32_t w8[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) w8[u] = *reinterpret_cast<const uint32_t*>(col + (size_t)(j + u) * vh);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          a0 += ol[j + u] * __uint_as_float(w8[u] << 16);
+          a1 += ol[j + u] * __uint_as_float(w8[u] & 0xffff0000u);
+        }
+      }
+    }
+    pq[wave * 128 + 2 * lane] = a0;
+    pq[wave * 128 + 2 * lane + 1] = a1;
+    __syncthreads();
+    if (tid < 128 && v0 + tid < vh) {
+      float v = 0.f;
+      for (int w = 0; w < kAW; ++w) v += pq[w * 128 + tid];
+      out[((size_t)t * nh + h) * vh + v0 + tid] = f32_to_bf16_bits(v);
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GQA with per-head q/k RMSNorm (Qwen3-MoE), head_dim 128.
+// ---------------------------------------------------------------------------
+constexpr int kHd = 128;
+
+// grid (c, nh + kvh), 64 threads: y < nh -> query head, else kv head y - nh.
+__global__ __launch_bounds__(64) void gqa_prep_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_norm,
+    const uint16_t* __restrict__ k_norm, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const int64_t* __restrict__ pos, int nh, int kvh, int L,
+    float eps, float* __restrict__ q, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache) {
+  const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  const long long p = pos[t];
+  if (p < 0 || p >= L) return;
+  const int width = (nh + 2 * kvh) * kHd;
+  const bool is_q = h < nh;
+  const int col = is_q ? h * kHd : (nh + (h - nh)) * kHd;
+  const uint16_t* xr = qkv + (size_t)t * width + col;
+  // lane holds the rotate-half pair (lane, lane + 64)
+  const float x1 = bf(xr[lane]), x2 = bf(xr[lane + 64]);
+  const float rstd = rsqrtf(wave_sum(x1 * x1 + x2 * x2) / (float)kHd + eps);
+  const uint16_t* nw = is_q ? q_norm : k_norm;
+  const float n1 = x1 * rstd * bf(nw[lane]), n2 = x2 * rstd * bf(nw[lane + 64]);
+  const float c = cos_t[p * 64 + lane], sn = sin_t[p * 64 + lane];
+  const float r1 = n1 * c - n2 * sn, r2 = n2 * c + n1 * sn;
+  if (is_q) {
+    float* o = q + ((size_t)t * nh + h) * kHd;
+    o[lane] = r1;
+    o[lane + 64] = r2;
+    return;
+  }
+  const int g = h - nh;
+  const size_t row = (((size_t)t * kvh + g) * L + p) * kHd;
+  k_cache[row + lane] = f32_to_bf16_bits(r1);
+  k_cache[row + lane + 64] = f32_to_bf16_bits(r2);
+  const uint16_t* vr = qkv + (size_t)t * width + (nh + kvh + g) * kHd;
+  v_cache[row + lane] = vr[lane];
+  v_cache[row + lane + 64] = vr[lane + 64];
+}
+
+// grid (c, nh).
+__global__ __launch_bounds__(kT) void gqa_attend_kernel(
+    const float* __restrict__ q, const uint16_t* __restrict__ k_cache,
+    const uint16_t* __restrict__ v_cache, const int64_t* __restrict__ pos, int nh, int kvh, int L,
+    float scale, uint16_t* __restrict__ out) {
+  __shared__ float sq[kHd];
+  __shared__ float s[kMaxL];
+  __shared__ float half2[kT];
+  __shared__ float red[kT / 64];
+  const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const long long p = pos[t];
+  if (p < 0 || p >= L) return;
+  const int n = (int)p + 1;
+  const int g = h / (nh / kvh);
+  if (tid < kHd) sq[tid] = q[((size_t)t * nh + h) * kHd + tid];
+  __syncthreads();
+  const uint16_t* kb = k_cache + ((size_t)t * kvh + g) * L * kHd;
+  const uint16_t* vb = v_cache + ((size_t)t * kvh + g) * L * kHd;
+  // scores: 16 lanes per row (8 elements each), 16 rows per pass
+  const int sub = tid & 15, rw = tid >> 4;
+  float qv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) qv[j] = sq[sub * 8 + j];
+  float lmax = -INFINITY;
+  for (int l0 = 0; l0 < n; l0 += kT / 16) {
+    const int l = l0 + rw;
+    float d = 0.f;
+    if (l < n) {
+      float kv[8];
+      unpack8(*reinterpret_cast<const u32x4_t*>(kb + (size_t)l * kHd + sub * 8), kv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) d += qv[j] * kv[j];
+    }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) d += __shfl_xor(d, off, SLUICE_WAVE);
+    d *= scale;
+    if (l < n) {
+      if (sub == 0) s[l] = d;
+      lmax = fmaxf(lmax, d);
+    }
+  }
+  const float m = block_max(lmax, red);
+  float part = 0.f;
+  for (int l = tid; l < n; l += kT) {
+    const float e = expf(s[l] - m);
+    s[l] = e;
+    part += e;
+  }
+  const float inv = 1.0f / block_sum(part, red);
+  __syncthreads();
+  // out[d] = sum_l p[l] v[l][d]: wave w takes rows l = w, w + 4, ..., a lane
+  // owns 2 columns (4-byte loads), four rows in flight; waves summed in LDS.
+  constexpr int U = 4;
+  float a0 = 0.f, a1 = 0.f;
+  const int wave = tid >> 6, lane = tid & 63;
+  for (int l0 = wave; l0 < n; l0 += U * (kT / 64)) {
+    uint32_t vv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int l = l0 + u * (kT / 64);
+      vv[u] = *reinterpret_cast<const uint32_t*>(vb + (size_t)(l < n ? l : 0) * kHd + 2 * lane);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int l = l0 + u * (kT / 64);
+      const float pl = l < n ? s[l] : 0.f;
+      a0 += pl * __uint_as_float(vv[u] << 16);
+      a1 += pl * __uint_as_float(vv[u] & 0xffff0000u);
+    }
+  }
+  half2[tid] = a0;  // reused as [4 waves][64 lanes] x 2
+  __syncthreads();
+  float* sum1 = s;  // scores are no longer needed: reuse for the odd columns
+  __syncthreads();
+  sum1[tid] = a1;
+  __syncthreads();
+  if (tid < 64) {
+    const float e0 = half2[tid] + half2[64 + tid] + half2[128 + tid] + half2[192 + tid];
+    const float e1 = sum1[tid] + sum1[64 + tid] + sum1[128 + tid] + sum1[192 + tid];
+    *reinterpret_cast<uint32_t*>(out + ((size_t)t * nh + h) * kHd + 2 * tid) =
+        pack2(e0 * inv, e1 * inv);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Skinny GEMM for decode: y [T, N] = x [T, K] . W [N, K]^T, T <= 16.  A weight
+// stream like the expert product: a workgroup takes 16 rows of W (MFMA M)
+// against all T tokens (MFMA N); 4 waves split K and reduce in LDS; each lane
+// keeps 8 chunks of 16 bytes in flight.
+// ---------------------------------------------------------------------------
+constexpr int kLinD = 8;
+
+__global__ __launch_bounds__(kT) void linear_kernel(const uint16_t* __restrict__ x,
+                                                    const uint16_t* __restrict__ w, int T, int N,
+                                                    int K, uint16_t* __restrict__ y) {
+  __shared__ f32x4_t red[kT / 64][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, kg = lane >> 4;
+  const int nchunk = K / 32;
+  const int c0 = wave * nchunk / (kT / 64), c1 = (wave + 1) * nchunk / (kT / 64);
+  const int n = c1 - c0;
+  const bool hx = col < T;
+  for (int tile = blockIdx.x; tile < N / 16; tile += gridDim.x) {
+    const uint16_t* wr = w + ((size_t)tile * 16 + col) * K + kg * 8 + c0 * 32;
+    const uint16_t* xr = x + (size_t)(hx ? col : 0) * K + kg * 8 + c0 * 32;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    u32x4_t rw[kLinD], rx[kLinD];
+#pragma unroll
+    for (int d = 0; d < kLinD; ++d) {
+      rx[d] = u32x4_t{0u, 0u, 0u, 0u};
+      if (d < n) {
+        rw[d] = ldg16_stream(wr + d * 32);
+        if (hx) rx[d] = ldg16(xr + d * 32);
+      }
+    }
+    for (int base = 0; base < n; base += kLinD) {
+#pragma unroll
+      for (int d = 0; d < kLinD; ++d) {
+        if (base + d < n) {
+          acc = mfma16x16x32_bf16(rw[d], rx[d], acc);
+          const int nx = base + kLinD + d;
+          if (nx < n) {
+            rw[d] = ldg16_stream(wr + nx * 32);
+            if (hx) rx[d] = ldg16(xr + nx * 32);
+          }
+        }
+      }
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && hx) {
+      f32x4_t s = red[0][lane];
+#pragma unroll
+      for (int v = 1; v < kT / 64; ++v) s += red[v][lane];
+      *reinterpret_cast<u32x2_t*>(y + (size_t)col * N + tile * 16 + kg * 4) =
+          u32x2_t{pack2(s[0], s[1]), pack2(s[2], s[3])};
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace
+
+extern "C" int sluice_dec_linear(const void* x, const void* w, int T, int N, int K, void* y,
+                                 sluice_stream_t stream) {
+  if (T < 0 || T > 16 || N <= 0 || N % 16 != 0 || K <= 0 || K % 32 != 0 || x == nullptr ||
+      w == nullptr || y == nullptr)
+    return SLUICE_E_INVAL;
+  if (((uintptr_t)x | (uintptr_t)w) & 15 || (uintptr_t)y & 7) return SLUICE_E_INVAL;
+  if (T == 0) return SLUICE_OK;
+  const int tiles = N / 16;
+  const int grid = tiles < 4096 ? tiles : 4096;
+  hipLaunchKernelGGL(linear_kernel, dim3(grid), dim3(kT), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, (const uint16_t*)w, T, N, K, (uint16_t*)y);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sluice_dec_add_rmsnorm(void* x, const void* delta, const void* w, void* out,
+                                      int rows, int H, float eps, sluice_stream_t stream) {
+  if (rows < 0 || H <= 0 || H % 8 != 0 || x == nullptr || w == nullptr || out == nullptr)
+    return SLUICE_E_INVAL;
+  if (((uintptr_t)x | (uintptr_t)delta | (uintptr_t)w | (uintptr_t)out) & 15) return SLUICE_E_INVAL;
+  if (rows == 0) return SLUICE_OK;
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(kT), 0, (hipStream_t)stream,
+                     (uint16_t*)x, (const uint16_t*)delta, (const uint16_t*)w, (uint16_t*)out, H,
+                     eps);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sluice_dec_silu_mul(const void* gu, void* out, int rows, int I,
+                                   sluice_stream_t stream) {
+  if (rows < 0 || I <= 0 || I % 4 != 0 || gu == nullptr || out == nullptr) return SLUICE_E_INVAL;
+  if (((uintptr_t)gu | (uintptr_t)out) & 7) return SLUICE_E_INVAL;
+  if (rows == 0) return SLUICE_OK;
+  dim3 grid((I / 4 + kT - 1) / kT, rows);
+  hipLaunchKernelGGL(silu_mul_kernel, grid, dim3(kT), 0, (hipStream_t)stream,
+                     (const uint16_t*)gu, (uint16_t*)out, I);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sluice_dec_gate_logits(const void* hn, const void* wg, const float* bias_table,
+                                      const int64_t* step, int n_steps, int bias_rows, int rows,
+                                      int H, int E, float* out, sluice_stream_t stream) {
+  if (rows < 0 || rows > kMaxRows || H <= 0 || H % 32 != 0 || E <= 0 || hn == nullptr ||
+      wg == nullptr || out == nullptr)
+    return SLUICE_E_INVAL;
+  if (bias_table != nullptr && (step == nullptr || n_steps <= 0 || bias_rows < rows))
+    return SLUICE_E_INVAL;
+  if (((uintptr_t)hn | (uintptr_t)wg) & 15) return SLUICE_E_INVAL;
+  if (rows == 0) return SLUICE_OK;
+  hipLaunchKernelGGL(gate_logits_kernel, dim3(E), dim3(kT), 0, (hipStream_t)stream,
+                     (const uint16_t*)hn, (const uint16_t*)wg, bias_table, step, n_steps,
+                     bias_rows, rows, H, E, out);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sluice_dec_mla_prep(const void* q, int q_stride, const void* kva, int kva_stride,
+                                   const void* kv_norm, const void* w_uk, const float* cos_t,
+                                   const float* sin_t, const int64_t* pos, int c, int nh, int nope,
+                                   int rope, int lora, int L, float eps, float* q_lat, float* q_pe,
+                                   void* ckv_cache, void* kpe_cache, sluice_stream_t stream) {
+  if (c < 0 || nh <= 0 || nope <= 0 || nope > 256 || nope % 2 != 0 || rope != kRope ||
+      lora != kLora || L <= 0 || L > kMaxL || q_stride < nh * (nope + rope) ||
+      kva_stride < lora + rope || kva_stride % 2 != 0)
+    return SLUICE_E_INVAL;
+  if (((uintptr_t)kva | (uintptr_t)kv_norm | (uintptr_t)w_uk | (uintptr_t)ckv_cache) & 3)
+    return SLUICE_E_INVAL;
+  if (!q || !kva || !kv_norm || !w_uk || !cos_t || !sin_t || !pos || !q_lat || !q_pe ||
+      !ckv_cache || !kpe_cache)
+    return SLUICE_E_INVAL;
+  if (c == 0) return SLUICE_OK;
+  hipLaunchKernelGGL(mla_prep_kernel, dim3(c, nh + 1), dim3(kT), 0, (hipStream_t)stream,
+                     (const uint16_t*)q, (const uint16_t*)kva, (const uint16_t*)kv_norm,
+                     (const uint16_t*)w_uk, cos_t, sin_t, pos, nh, nope, q_stride, kva_stride, L,
+                     eps, q_lat, q_pe, (uint16_t*)ckv_cache, (uint16_t*)kpe_cache);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sluice_dec_mla_attend(const float* q_lat, const float* q_pe, const void* ckv_cache,
+                                     const void* kpe_cache, const void* w_uv, const int64_t* pos,
+                                     int c, int nh, int rope, int lora, int vh, int L, float scale,
+                                     void* out, sluice_stream_t stream) {
+  if (c < 0 || nh <= 0 || rope != kRope || lora != kLora || vh <= 0 || vh > 256 || L <= 0 ||
+      L > kMaxL)
+    return SLUICE_E_INVAL;
+  if (!q_lat || !q_pe || !ckv_cache || !kpe_cache || !w_uv || !pos || !out) return SLUICE_E_INVAL;
+  if ((uintptr_t)ckv_cache & 15) return SLUICE_E_INVAL;
+  if (c == 0) return SLUICE_OK;
+  hipLaunchKernelGGL(mla_attend_kernel, dim3(c, nh), dim3(kA), 0, (hipStream_t)stream, q_lat,
+                     q_pe, (const uint16_t*)ckv_cache, (const uint16_t*)kpe_cache,
+                     (const uint16_t*)w_uv, pos, nh, vh, L, scale, (uint16_t*)out);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sluice_dec_gqa_prep(const void* qkv, const void* q_norm, const void* k_norm,
+                                   const float* cos_t, const float* sin_t, const int64_t* pos,
+                                   int c, int nh, int kvh, int hd, int L, float eps, float* q,
+                                   void* k_cache, void* v_cache, sluice_stream_t stream) {
+  if (c < 0 || nh <= 0 || kvh <= 0 || nh % kvh != 0 || hd != kHd || L <= 0 || L > kMaxL)
+    return SLUICE_E_INVAL;
+  if (!qkv || !q_norm || !k_norm || !cos_t || !sin_t || !pos || !q || !k_cache || !v_cache)
+    return SLUICE_E_INVAL;
+  if (c == 0) return SLUICE_OK;
+  hipLaunchKernelGGL(gqa_prep_kernel, dim3(c, nh + kvh), dim3(64), 0, (hipStream_t)stream,
+                     (const uint16_t*)qkv, (const uint16_t*)q_norm, (const uint16_t*)k_norm, cos_t,
+                     sin_t, pos, nh, kvh, L, eps, q, (uint16_t*)k_cache, (uint16_t*)v_cache);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sluice_dec_gqa_attend(const float* q, const void* k_cache, const void* v_cache,
+                                     const int64_t* pos, int c, int nh, int kvh, int hd, int L,
+                                     float scale, void* out, sluice_stream_t stream) {
+  if (c < 0 || nh <= 0 || kvh <= 0 || nh % kvh != 0 || hd != kHd || L <= 0 || L > kMaxL)
+    return SLUICE_E_INVAL;
+  if (!q || !k_cache || !v_cache || !pos || !out) return SLUICE_E_INVAL;
+  if ((uintptr_t)k_cache & 15) return SLUICE_E_INVAL;
+  if (c == 0) return SLUICE_OK;
+  hipLaunchKernelGGL(gqa_attend_kernel, dim3(c, nh), dim3(kT), 0, (hipStream_t)stream, q,
+                     (const uint16_t*)k_cache, (const uint16_t*)v_cache, pos, nh, kvh, L, scale,
+                     (uint16_t*)out);
+  return (int)hipGetLastError();
+}

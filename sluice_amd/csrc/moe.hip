@@ -10,13 +10,24 @@
 // At decode (T <= 16 tokens, k <= 8) every expert sees 1..16 tokens, so the
 // product is a weight stream: each (expert, 16-row tile) is read once from
 // HBM and multiplied against the expert's token block on MFMA
-// v_mfma_f32_16x16x32_bf16 — weight rows on the MFMA M side (one 16-byte
+// v_mfma_f32_16x16x32_bf16 -- weight rows on the MFMA M side (one 16-byte
 // load per lane per 32-wide K chunk), tokens on the N side.  A workgroup is
-// KS waves that split K and reduce through LDS; the grid strides over
-// (block, tile) items whose count is known only on the device.
+// 4 waves that split K and reduce through LDS.
 //
-// Kernels per call:  align (1 WG)  ->  gemm1 (+silu*up)  ->  gemm2 (*w)
-//                    ->  combine (sum over k, *scale, +shared, -> bf16).
+// Two launch shapes share the same per-item bodies:
+//   fused (opt-in, T*k <= 256): ONE persistent kernel per call, its grid
+//     sized so every workgroup is resident.  Every workgroup builds the align
+//     plan in LDS, then strides over the work items -- all gemm1 items
+//     (block, 16 intermediate rows) before all gemm2 items (block, 32 hidden
+//     rows).  A gemm2 item waits for its block's gemm1 tiles on a per-block
+//     counter (gemm1 items never wait).  The last gemm2 item to finish a
+//     32-column hidden slice combines that slice for every token (j
+//     ascending, so the result does not depend on which workgroup finishes
+//     last).  Counters go back to zero as their last user finishes, so the
+//     workspace needs no clearing between calls.
+//   staged: align (1 WG) -> gemm1 (+silu*up) -> gemm2 (*w) -> combine, four
+//     grid-stride kernels over a plan in global memory (any T*k, and the
+//     per-stage entry points).
 #include <math.h>
 
 #include "common.h"
@@ -27,7 +38,24 @@ constexpr int kBM = SLUICE_BLOCK_M;      // tokens per block (MFMA N)
 constexpr int kBlockInts = 2 + kBM;      // {slot, count, pair[16]}
 constexpr int kPlanHeader = 4;
 constexpr int kKS = 4;                   // waves per workgroup (K split)
-constexpr int kAlignThreads = 256;
+constexpr int kThreads = 64 * kKS;
+constexpr int kG2T = 2;                  // 16-row hidden tiles per gemm2 item
+constexpr int kFusedMaxPairs = 256;      // T*k limit of the fused kernel
+constexpr int kFusedMaxHidden = 16384;   // H limit of the fused kernel
+constexpr int kFp8Blk = 128;
+
+#ifndef SLUICE_G1_D
+#define SLUICE_G1_D 8
+#endif
+#ifndef SLUICE_G2_D
+#define SLUICE_G2_D 8
+#endif
+#ifndef SLUICE_F8_D
+#define SLUICE_F8_D 4
+#endif
+constexpr int kG1D = SLUICE_G1_D;  // bf16 gemm1: 32-wide K chunks in flight per lane
+constexpr int kG2D = SLUICE_G2_D;  // bf16 gemm2
+constexpr int kF8D = SLUICE_F8_D;  // fp8: 64-wide K chunks in flight per lane
 
 __host__ __device__ inline size_t plan_ints(int P) {
   return (size_t)kPlanHeader + (size_t)kBlockInts * P + (size_t)P;
@@ -43,39 +71,39 @@ __device__ __forceinline__ int pair_slot(const int32_t* ids, const int32_t* map,
 
 // ---------------------------------------------------------------------------
 // Align: group the P = T*k pairs by slot into blocks of <= 16, slots
-// ascending and pairs ascending inside a slot (deterministic).
+// ascending and pairs ascending inside a slot (deterministic).  Called by
+// all kThreads threads; `blocks` / `valid` may be global or LDS memory;
+// the scratch arrays are LDS.  Returns the block count to every thread.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
-    const int32_t* __restrict__ ids, int P, const int32_t* __restrict__ map, int E, int S,
-    int32_t* __restrict__ plan) {
-  __shared__ int cnt[SLUICE_MAX_SLOTS];
-  __shared__ int boff[SLUICE_MAX_SLOTS];
-  __shared__ int run[SLUICE_MAX_SLOTS];
-  __shared__ int chunk_slot[kAlignThreads];
-  __shared__ int wsum[kAlignThreads / SLUICE_WAVE];
-  __shared__ int total_blocks;
+struct AlignScratch {
+  int cnt[SLUICE_MAX_SLOTS];
+  int boff[SLUICE_MAX_SLOTS];
+  int run[SLUICE_MAX_SLOTS];
+  int chunk_slot[kThreads];
+  int wsum[kKS];
+  int total;
+};
+
+__device__ int build_plan(const int32_t* __restrict__ ids, int P, const int32_t* __restrict__ map,
+                          int E, int S, AlignScratch& sc, int32_t* blocks, int32_t* valid) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  int32_t* blocks = plan + kPlanHeader;
-  int32_t* valid = plan + kPlanHeader + (size_t)kBlockInts * P;
-
-  for (int s = tid; s < S; s += kAlignThreads) {
-    cnt[s] = 0;
-    run[s] = 0;
+  for (int s = tid; s < S; s += kThreads) {
+    sc.cnt[s] = 0;
+    sc.run[s] = 0;
   }
   __syncthreads();
-  for (int p = tid; p < P; p += kAlignThreads) {
+  for (int p = tid; p < P; p += kThreads) {
     const int s = pair_slot(ids, map, p, E, S);
-    if (s >= 0) atomicAdd(&cnt[s], 1);
+    if (s >= 0) atomicAdd(&sc.cnt[s], 1);
   }
   __syncthreads();
-
   // Exclusive scan of blocks-per-slot; thread t owns slots [t*per, t*per+per).
-  const int per = (S + kAlignThreads - 1) / kAlignThreads;
+  const int per = (S + kThreads - 1) / kThreads;
   int mine = 0;
   for (int i = 0; i < per; ++i) {
     const int s = tid * per + i;
-    if (s < S) mine += (cnt[s] + kBM - 1) / kBM;
+    if (s < S) mine += (sc.cnt[s] + kBM - 1) / kBM;
   }
   int incl = mine;
 #pragma unroll
@@ -83,233 +111,213 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     const int v = __shfl_up(incl, off, SLUICE_WAVE);
     if (lane >= off) incl += v;
   }
-  if (lane == 63) wsum[wave] = incl;
+  if (lane == 63) sc.wsum[wave] = incl;
   __syncthreads();
   int wbase = 0;
-  for (int w = 0; w < wave; ++w) wbase += wsum[w];
+  for (int w = 0; w < wave; ++w) wbase += sc.wsum[w];
   int acc = wbase + incl - mine;
   for (int i = 0; i < per; ++i) {
     const int s = tid * per + i;
     if (s < S) {
-      boff[s] = acc;
-      acc += (cnt[s] + kBM - 1) / kBM;
+      sc.boff[s] = acc;
+      acc += (sc.cnt[s] + kBM - 1) / kBM;
     }
   }
-  if (tid == kAlignThreads - 1) total_blocks = wbase + incl;
+  if (tid == kThreads - 1) sc.total = wbase + incl;
   __syncthreads();
-
-  // Ranks in pair order, one chunk of 256 pairs at a time.
-  for (int c = 0; c < P; c += kAlignThreads) {
+  // Ranks in pair order, one chunk of kThreads pairs at a time.
+  for (int c = 0; c < P; c += kThreads) {
     const int p = c + tid;
     const int s = p < P ? pair_slot(ids, map, p, E, S) : -1;
-    chunk_slot[tid] = s;
+    sc.chunk_slot[tid] = s;
     __syncthreads();
     if (s >= 0) {
-      int r = run[s];
-      for (int q = 0; q < tid; ++q) r += (chunk_slot[q] == s) ? 1 : 0;
-      const int b = boff[s] + r / kBM;
+      int r = sc.run[s];
+      for (int q = 0; q < tid; ++q) r += (sc.chunk_slot[q] == s) ? 1 : 0;
+      const int b = sc.boff[s] + r / kBM;
       const int pos = r % kBM;
       int32_t* blk = blocks + (size_t)b * kBlockInts;
       blk[2 + pos] = p;
       if (pos == 0) {
         blk[0] = s;
-        const int left = cnt[s] - (r / kBM) * kBM;
+        const int left = sc.cnt[s] - (r / kBM) * kBM;
         blk[1] = left < kBM ? left : kBM;
       }
     }
     if (p < P) valid[p] = s >= 0 ? 1 : 0;
     __syncthreads();
-    if (s >= 0) atomicAdd(&run[s], 1);
+    if (s >= 0) atomicAdd(&sc.run[s], 1);
     __syncthreads();
   }
-  if (tid == 0) {
-    plan[0] = total_blocks;
+  return sc.total;
+}
+
+__global__ __launch_bounds__(kThreads) void moe_align_kernel(
+    const int32_t* __restrict__ ids, int P, const int32_t* __restrict__ map, int E, int S,
+    int32_t* __restrict__ plan) {
+  __shared__ AlignScratch sc;
+  const int nb = build_plan(ids, P, map, E, S, sc, plan + kPlanHeader,
+                            plan + kPlanHeader + (size_t)kBlockInts * P);
+  if (threadIdx.x == 0) {
+    plan[0] = nb;
     plan[1] = P;
   }
 }
 
-// Tunables (compile-time): waves per workgroup splitting K, register
-// prefetch depth in 32-wide K chunks, and hidden rows per GEMM2 item.
-#ifndef SLUICE_G1_KS
-#define SLUICE_G1_KS 4
-#endif
-#ifndef SLUICE_G1_D
-#define SLUICE_G1_D 8
-#endif
-#ifndef SLUICE_G2_KS
-#define SLUICE_G2_KS 4
-#endif
-#ifndef SLUICE_G2_D
-#define SLUICE_G2_D 8
-#endif
-#ifndef SLUICE_G2_TILES
-#define SLUICE_G2_TILES 2
-#endif
-constexpr int kG1KS = SLUICE_G1_KS, kG1D = SLUICE_G1_D;
-constexpr int kG2KS = SLUICE_G2_KS, kG2D = SLUICE_G2_D, kG2T = SLUICE_G2_TILES;
+typedef f32x4_t RedBuf[kKS][2][64];
 
-// ---------------------------------------------------------------------------
-// GEMM1: act[pair, i] = bf16(silu(gate) * up) for one 16-row intermediate
-// tile of one block.  bf16 weights.  Each wave owns a contiguous K range and
-// keeps kG1D chunks (3 x 16 B per lane each) in flight: the loads for chunk
-// c + kG1D are issued as soon as chunk c has been consumed.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64 * kG1KS) void moe_gemm1_bf16_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w13,
-    const int32_t* __restrict__ plan, int H, int I, int k, uint16_t* __restrict__ act) {
-  __shared__ f32x4_t red[kG1KS][2][64];
-  const int n_blocks = plan[0];
-  const int n_tiles = I / 16;
-  const int total = n_blocks * n_tiles;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int col = lane & 15, kg = lane >> 4;
-  const int nchunk = H / 32;
-  const int c0 = wave * nchunk / kG1KS, c1 = (wave + 1) * nchunk / kG1KS;
-  const int n = c1 - c0;
-  const int32_t* blocks = plan + kPlanHeader;
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+}
 
-  for (int item = blockIdx.x; item < total; item += gridDim.x) {
-    const int b = item / n_tiles, tile = item - b * n_tiles;
-    const int32_t* blk = blocks + (size_t)b * kBlockInts;
-    const int slot = blk[0], cnt = blk[1];
-    const int pair = col < cnt ? blk[2 + col] : -1;
-    const uint16_t* wg =
-        w13 + ((size_t)slot * 2 * I + (size_t)tile * 16 + col) * H + kg * 8 + c0 * 32;
-    const uint16_t* wu = wg + (size_t)I * H;
-    const uint16_t* xr = x + (size_t)(pair >= 0 ? pair / k : 0) * H + kg * 8 + c0 * 32;
-    const bool hx = pair >= 0;
-    f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-    u32x4_t rg[kG1D], ru[kG1D], rx[kG1D];
+// Wave 0 reduces the 4 K-split partial accumulators and writes
+// act[pair, tile*16 + kg*4 .. +4] = bf16(silu(g) * u).
+__device__ __forceinline__ void g1_epilogue(RedBuf& red, int pair, int tile, int I,
+                                            uint16_t* __restrict__ act) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kg = lane >> 4;
+  __syncthreads();
+  if (wave == 0 && pair >= 0) {
+    f32x4_t g = red[0][0][lane], u = red[0][1][lane];
 #pragma unroll
-    for (int d = 0; d < kG1D; ++d) {
-      rx[d] = u32x4_t{0u, 0u, 0u, 0u};
-      if (d < n) {
-        rg[d] = ldg16_stream(wg + d * 32);
-        ru[d] = ldg16_stream(wu + d * 32);
-        if (hx) rx[d] = ldg16(xr + d * 32);
-      }
+    for (int w = 1; w < kKS; ++w) {
+      g += red[w][0][lane];
+      u += red[w][1][lane];
     }
-    for (int base = 0; base < n; base += kG1D) {
+    float o[4];
 #pragma unroll
-      for (int d = 0; d < kG1D; ++d) {
-        if (base + d < n) {
-          ag = mfma16x16x32_bf16(rg[d], rx[d], ag);
-          au = mfma16x16x32_bf16(ru[d], rx[d], au);
-          const int nx = base + kG1D + d;
-          if (nx < n) {
-            rg[d] = ldg16_stream(wg + nx * 32);
-            ru[d] = ldg16_stream(wu + nx * 32);
-            if (hx) rx[d] = ldg16(xr + nx * 32);
-          }
-        }
-      }
-    }
-    red[wave][0][lane] = ag;
-    red[wave][1][lane] = au;
-    __syncthreads();
-    if (wave == 0 && pair >= 0) {
-      f32x4_t g = red[0][0][lane], u = red[0][1][lane];
-#pragma unroll
-      for (int w = 1; w < kG1KS; ++w) {
-        g += red[w][0][lane];
-        u += red[w][1][lane];
-      }
-      uint16_t o[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float gv = g[r];
-        o[r] = f32_to_bf16_bits(gv / (1.0f + expf(-gv)) * u[r]);
-      }
-      u32x2_t packed = {(uint32_t)o[0] | ((uint32_t)o[1] << 16),
-                        (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
-      *reinterpret_cast<u32x2_t*>(act + (size_t)pair * I + tile * 16 + kg * 4) = packed;
-    }
-    __syncthreads();
+    for (int r = 0; r < 4; ++r) o[r] = g[r] / (1.0f + expf(-g[r])) * u[r];
+    *reinterpret_cast<u32x2_t*>(act + (size_t)pair * I + tile * 16 + kg * 4) =
+        u32x2_t{pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
   }
+  __syncthreads();
+}
+
+// Wave 0 reduces and writes partial[pair, tile2*32 + t*16 + kg*4 .. +4] = w * sum.
+__device__ __forceinline__ void g2_epilogue(RedBuf& red, int pair, int tile2, int H, float wv,
+                                            float* __restrict__ partial) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kg = lane >> 4;
+  __syncthreads();
+  if (wave == 0 && pair >= 0) {
+#pragma unroll
+    for (int t = 0; t < kG2T; ++t) {
+      f32x4_t s = red[0][t][lane];
+#pragma unroll
+      for (int w = 1; w < kKS; ++w) s += red[w][t][lane];
+      *reinterpret_cast<f32x4_t*>(partial + (size_t)pair * H + (tile2 * kG2T + t) * 16 +
+                                  kg * 4) = f32x4_t{wv * s[0], wv * s[1], wv * s[2], wv * s[3]};
+    }
+  }
+  __syncthreads();
 }
 
 // ---------------------------------------------------------------------------
-// GEMM2: partial[pair, h] = w[pair] * (W2[s] · act[pair])[h] for kG2T
-// consecutive 16-row hidden tiles of one block (the act fragment is loaded
-// once per K chunk and feeds kG2T MFMAs).  bf16 weights.
+// gemm1 item, bf16 weights: gate and up rows tile*16..+16 of `slot` against
+// the block's tokens.  `pair` = this lane's pair (column lane & 15), -1 if
+// none.  Each wave owns a contiguous K range and keeps kG1D chunks (3 x 16 B
+// per lane each) in flight: chunk c + kG1D is loaded as soon as chunk c has
+// been consumed.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64 * kG2KS) void moe_gemm2_bf16_kernel(
-    const uint16_t* __restrict__ act, const uint16_t* __restrict__ w2,
-    const int32_t* __restrict__ plan, const float* __restrict__ topk_w, int H, int I,
-    float* __restrict__ partial) {
-  __shared__ f32x4_t red[kG2KS][kG2T][64];
-  const int n_blocks = plan[0];
-  const int n_tiles = H / (16 * kG2T);
-  const int total = n_blocks * n_tiles;
+__device__ __forceinline__ void g1_item_bf16(const uint16_t* __restrict__ x,
+                                             const uint16_t* __restrict__ w13, int slot, int pair,
+                                             int tile, int H, int I, int k,
+                                             uint16_t* __restrict__ act, RedBuf& red) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kg = lane >> 4;
-  const int nchunk = I / 32;
-  const int c0 = wave * nchunk / kG2KS, c1 = (wave + 1) * nchunk / kG2KS;
+  const int nchunk = H / 32;
+  const int c0 = wave * nchunk / kKS, c1 = (wave + 1) * nchunk / kKS;
   const int n = c1 - c0;
-  const int32_t* blocks = plan + kPlanHeader;
-
-  for (int item = blockIdx.x; item < total; item += gridDim.x) {
-    const int b = item / n_tiles, tile = item - b * n_tiles;
-    const int32_t* blk = blocks + (size_t)b * kBlockInts;
-    const int slot = blk[0], cnt = blk[1];
-    const int pair = col < cnt ? blk[2 + col] : -1;
-    const bool hx = pair >= 0;
-    const uint16_t* wr =
-        w2 + ((size_t)slot * H + (size_t)tile * 16 * kG2T + col) * I + kg * 8 + c0 * 32;
-    const uint16_t* ar = act + (size_t)(hx ? pair : 0) * I + kg * 8 + c0 * 32;
-    f32x4_t acc[kG2T];
+  const uint16_t* wg =
+      w13 + ((size_t)slot * 2 * I + (size_t)tile * 16 + col) * H + kg * 8 + c0 * 32;
+  const uint16_t* wu = wg + (size_t)I * H;
+  const bool hx = pair >= 0;
+  const uint16_t* xr = x + (size_t)(hx ? pair / k : 0) * H + kg * 8 + c0 * 32;
+  f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+  u32x4_t rg[kG1D], ru[kG1D], rx[kG1D];
 #pragma unroll
-    for (int t = 0; t < kG2T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    u32x4_t ra[kG2D][kG2T], rb[kG2D];
-#pragma unroll
-    for (int d = 0; d < kG2D; ++d) {
-      rb[d] = u32x4_t{0u, 0u, 0u, 0u};
-      if (d < n) {
-#pragma unroll
-        for (int t = 0; t < kG2T; ++t) ra[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + d * 32);
-        if (hx) rb[d] = ldg16(ar + d * 32);
-      }
+  for (int d = 0; d < kG1D; ++d) {
+    rx[d] = u32x4_t{0u, 0u, 0u, 0u};
+    if (d < n) {
+      rg[d] = ldg16_stream(wg + d * 32);
+      ru[d] = ldg16_stream(wu + d * 32);
+      if (hx) rx[d] = ldg16(xr + d * 32);
     }
-    for (int base = 0; base < n; base += kG2D) {
+  }
+  for (int base = 0; base < n; base += kG1D) {
 #pragma unroll
-      for (int d = 0; d < kG2D; ++d) {
-        if (base + d < n) {
-#pragma unroll
-          for (int t = 0; t < kG2T; ++t) acc[t] = mfma16x16x32_bf16(ra[d][t], rb[d], acc[t]);
-          const int nx = base + kG2D + d;
-          if (nx < n) {
-#pragma unroll
-            for (int t = 0; t < kG2T; ++t)
-              ra[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + nx * 32);
-            if (hx) rb[d] = ldg16(ar + nx * 32);
-          }
+    for (int d = 0; d < kG1D; ++d) {
+      if (base + d < n) {
+        ag = mfma16x16x32_bf16(rg[d], rx[d], ag);
+        au = mfma16x16x32_bf16(ru[d], rx[d], au);
+        const int nx = base + kG1D + d;
+        if (nx < n) {
+          rg[d] = ldg16_stream(wg + nx * 32);
+          ru[d] = ldg16_stream(wu + nx * 32);
+          if (hx) rx[d] = ldg16(xr + nx * 32);
         }
       }
     }
+  }
+  red[wave][0][lane] = ag;
+  red[wave][1][lane] = au;
+  g1_epilogue(red, pair, tile, I, act);
+}
+
+// gemm2 item, bf16 weights: hidden rows tile2*32..+32 of `slot` against
+// the block's act rows (the act fragment is loaded once per K chunk and
+// feeds both 16-row tiles).
+__device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act,
+                                             const uint16_t* __restrict__ w2, int slot, int pair,
+                                             int tile2, int H, int I,
+                                             const float* __restrict__ topk_w,
+                                             float* __restrict__ partial, RedBuf& red) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, kg = lane >> 4;
+  const int nchunk = I / 32;
+  const int c0 = wave * nchunk / kKS, c1 = (wave + 1) * nchunk / kKS;
+  const int n = c1 - c0;
+  const bool hx = pair >= 0;
+  const uint16_t* wr =
+      w2 + ((size_t)slot * H + (size_t)tile2 * 16 * kG2T + col) * I + kg * 8 + c0 * 32;
+  const uint16_t* ar = act + (size_t)(hx ? pair : 0) * I + kg * 8 + c0 * 32;
+  f32x4_t acc[kG2T];
 #pragma unroll
-    for (int t = 0; t < kG2T; ++t) red[wave][t][lane] = acc[t];
-    __syncthreads();
-    if (wave == 0 && pair >= 0) {
-      const float wv = topk_w[pair];
+  for (int t = 0; t < kG2T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  u32x4_t ra[kG2D][kG2T], rb[kG2D];
 #pragma unroll
-      for (int t = 0; t < kG2T; ++t) {
-        f32x4_t s = red[0][t][lane];
+  for (int d = 0; d < kG2D; ++d) {
+    rb[d] = u32x4_t{0u, 0u, 0u, 0u};
+    if (d < n) {
 #pragma unroll
-        for (int w = 1; w < kG2KS; ++w) s += red[w][t][lane];
-        f32x4_t o = {wv * s[0], wv * s[1], wv * s[2], wv * s[3]};
-        *reinterpret_cast<f32x4_t*>(partial + (size_t)pair * H + (tile * kG2T + t) * 16 +
-                                    kg * 4) = o;
+      for (int t = 0; t < kG2T; ++t) ra[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + d * 32);
+      if (hx) rb[d] = ldg16(ar + d * 32);
+    }
+  }
+  for (int base = 0; base < n; base += kG2D) {
+#pragma unroll
+    for (int d = 0; d < kG2D; ++d) {
+      if (base + d < n) {
+#pragma unroll
+        for (int t = 0; t < kG2T; ++t) acc[t] = mfma16x16x32_bf16(ra[d][t], rb[d], acc[t]);
+        const int nx = base + kG2D + d;
+        if (nx < n) {
+#pragma unroll
+          for (int t = 0; t < kG2T; ++t) ra[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + nx * 32);
+          if (hx) rb[d] = ldg16(ar + nx * 32);
+        }
       }
     }
-    __syncthreads();
   }
+#pragma unroll
+  for (int t = 0; t < kG2T; ++t) red[wave][t][lane] = acc[t];
+  g2_epilogue(red, pair, tile2, H, hx ? topk_w[pair] : 0.f, partial);
 }
 
 // ---------------------------------------------------------------------------
 // fp8 e4m3fn weights with 128x128 fp32 block scales, bf16 activations.
-// Each lane loads 16 fp8 (one 64-wide K chunk per lane group), widens them
-// exactly to bf16 and issues two MFMAs; the fp32 sum of a 128-wide K block
-// is multiplied by that block's scale before it joins the accumulator.
+// Each lane loads 16 fp8 bytes of a 64-wide K chunk, widens them exactly to
+// bf16 and issues two MFMAs (the x fragment is loaded with the same K
+// order); the fp32 sum over a 128-wide K block is multiplied by that block's
+// scale before it joins the accumulator.  kF8D chunks are in flight.
 // ---------------------------------------------------------------------------
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 
@@ -334,163 +342,348 @@ __device__ __forceinline__ void fp8x16_to_bf16(u32x4_t q, u32x4_t& lo, u32x4_t& 
   hi = u32x4_t{c[0], c[1], d[0], d[1]};
 }
 
-constexpr int kFp8Blk = 128;
-
-__global__ __launch_bounds__(64 * kKS) void moe_gemm1_fp8_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w13,
-    const float* __restrict__ w13_scale, const int32_t* __restrict__ plan, int H, int I, int k,
-    uint16_t* __restrict__ act) {
-  __shared__ f32x4_t red[kKS][2][64];
-  const int n_blocks = plan[0];
-  const int n_tiles = I / 16;
-  const int total = n_blocks * n_tiles;
+// gemm1 item, fp8 weights.  Wave w owns 64-wide K chunks [c0, c1), an even
+// split of 128-wide scale blocks.
+__device__ __forceinline__ void g1_item_fp8(const uint16_t* __restrict__ x,
+                                            const uint8_t* __restrict__ w13,
+                                            const float* __restrict__ w13_scale, int slot,
+                                            int pair, int tile, int H, int I, int k,
+                                            uint16_t* __restrict__ act, RedBuf& red) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kg = lane >> 4;
-  const int nkb = H / kFp8Blk;                 // K scale blocks
-  const int nrb = (2 * I) / kFp8Blk;           // row scale blocks per expert
-  const int kb0 = wave * nkb / kKS, kb1 = (wave + 1) * nkb / kKS;
-  const int32_t* blocks = plan + kPlanHeader;
-
-  for (int item = blockIdx.x; item < total; item += gridDim.x) {
-    const int b = item / n_tiles, tile = item - b * n_tiles;
-    const int32_t* blk = blocks + (size_t)b * kBlockInts;
-    const int slot = blk[0], cnt = blk[1];
-    const int pair = col < cnt ? blk[2 + col] : -1;
-    const int rg = tile * 16, ru = I + tile * 16;
-    const uint8_t* wg = w13 + ((size_t)slot * 2 * I + rg + col) * H + kg * 16;
-    const uint8_t* wu = w13 + ((size_t)slot * 2 * I + ru + col) * H + kg * 16;
-    const float* sg = w13_scale + ((size_t)slot * nrb + rg / kFp8Blk) * nkb;
-    const float* su = w13_scale + ((size_t)slot * nrb + ru / kFp8Blk) * nkb;
-    const uint16_t* xr = x + (size_t)(pair >= 0 ? pair / k : 0) * H + kg * 16;
-    f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-    for (int kb = kb0; kb < kb1; ++kb) {
-      f32x4_t tg = {0.f, 0.f, 0.f, 0.f}, tu = {0.f, 0.f, 0.f, 0.f};
+  const int nkb = H / kFp8Blk, nrb = (2 * I) / kFp8Blk;
+  const int c0 = 2 * (wave * nkb / kKS), c1 = 2 * ((wave + 1) * nkb / kKS);
+  const int n = c1 - c0;
+  const int rg = tile * 16, ru = I + tile * 16;
+  const uint8_t* wg = w13 + ((size_t)slot * 2 * I + rg + col) * H + kg * 16 + c0 * 64;
+  const uint8_t* wu = w13 + ((size_t)slot * 2 * I + ru + col) * H + kg * 16 + c0 * 64;
+  const float* sg = w13_scale + ((size_t)slot * nrb + rg / kFp8Blk) * nkb;
+  const float* su = w13_scale + ((size_t)slot * nrb + ru / kFp8Blk) * nkb;
+  const bool hx = pair >= 0;
+  const uint16_t* xr = x + (size_t)(hx ? pair / k : 0) * H + kg * 16 + c0 * 64;
+  f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t tg = ag, tu = ag;
+  u32x4_t qg[kF8D], qu[kF8D], b0[kF8D], b1[kF8D];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int k0 = kb * kFp8Blk + h * 64;
-        const u32x4_t qg = ldg16_stream(wg + k0);
-        const u32x4_t qu = ldg16_stream(wu + k0);
-        u32x4_t b0 = {0u, 0u, 0u, 0u}, b1 = {0u, 0u, 0u, 0u};
-        if (pair >= 0) {
-          b0 = ldg16(xr + k0);
-          b1 = ldg16(xr + k0 + 8);
-        }
+  for (int d = 0; d < kF8D; ++d) {
+    b0[d] = b1[d] = u32x4_t{0u, 0u, 0u, 0u};
+    if (d < n) {
+      qg[d] = ldg16_stream(wg + d * 64);
+      qu[d] = ldg16_stream(wu + d * 64);
+      if (hx) {
+        b0[d] = ldg16(xr + d * 64);
+        b1[d] = ldg16(xr + d * 64 + 8);
+      }
+    }
+  }
+  for (int base = 0; base < n; base += kF8D) {
+#pragma unroll
+    for (int d = 0; d < kF8D; ++d) {
+      const int c = base + d;
+      if (c < n) {
         u32x4_t g0, g1, u0, u1;
-        fp8x16_to_bf16(qg, g0, g1);
-        fp8x16_to_bf16(qu, u0, u1);
-        tg = mfma16x16x32_bf16(g0, b0, tg);
-        tg = mfma16x16x32_bf16(g1, b1, tg);
-        tu = mfma16x16x32_bf16(u0, b0, tu);
-        tu = mfma16x16x32_bf16(u1, b1, tu);
+        fp8x16_to_bf16(qg[d], g0, g1);
+        fp8x16_to_bf16(qu[d], u0, u1);
+        tg = mfma16x16x32_bf16(g0, b0[d], tg);
+        tg = mfma16x16x32_bf16(g1, b1[d], tg);
+        tu = mfma16x16x32_bf16(u0, b0[d], tu);
+        tu = mfma16x16x32_bf16(u1, b1[d], tu);
+        const int nx = c + kF8D;
+        if (nx < n) {
+          qg[d] = ldg16_stream(wg + nx * 64);
+          qu[d] = ldg16_stream(wu + nx * 64);
+          if (hx) {
+            b0[d] = ldg16(xr + nx * 64);
+            b1[d] = ldg16(xr + nx * 64 + 8);
+          }
+        }
+        if (c & 1) {  // end of a 128-wide scale block
+          const int kb = (c0 + c) >> 1;
+          ag += sg[kb] * tg;
+          au += su[kb] * tu;
+          tg = tu = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
       }
-      const float scg = sg[kb], scu = su[kb];
-      ag += scg * tg;
-      au += scu * tu;
     }
-    red[wave][0][lane] = ag;
-    red[wave][1][lane] = au;
-    __syncthreads();
-    if (wave == 0 && pair >= 0) {
-      f32x4_t g = red[0][0][lane], u = red[0][1][lane];
-#pragma unroll
-      for (int w = 1; w < kKS; ++w) {
-        g += red[w][0][lane];
-        u += red[w][1][lane];
-      }
-      uint16_t o[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float gv = g[r];
-        o[r] = f32_to_bf16_bits(gv / (1.0f + expf(-gv)) * u[r]);
-      }
-      u32x2_t packed = {(uint32_t)o[0] | ((uint32_t)o[1] << 16),
-                        (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
-      *reinterpret_cast<u32x2_t*>(act + (size_t)pair * I + tile * 16 + kg * 4) = packed;
-    }
-    __syncthreads();
   }
+  red[wave][0][lane] = ag;
+  red[wave][1][lane] = au;
+  g1_epilogue(red, pair, tile, I, act);
 }
 
-__global__ __launch_bounds__(64 * kKS) void moe_gemm2_fp8_kernel(
-    const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
-    const float* __restrict__ w2_scale, const int32_t* __restrict__ plan,
-    const float* __restrict__ topk_w, int H, int I, float* __restrict__ partial) {
-  __shared__ f32x4_t red[kKS][64];
-  const int n_blocks = plan[0];
-  const int n_tiles = H / 16;
-  const int total = n_blocks * n_tiles;
+__device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act,
+                                            const uint8_t* __restrict__ w2,
+                                            const float* __restrict__ w2_scale, int slot,
+                                            int pair, int tile2, int H, int I,
+                                            const float* __restrict__ topk_w,
+                                            float* __restrict__ partial, RedBuf& red) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kg = lane >> 4;
-  const int nkb = I / kFp8Blk;
-  const int nrb = H / kFp8Blk;
-  const int kb0 = wave * nkb / kKS, kb1 = (wave + 1) * nkb / kKS;
-  const int32_t* blocks = plan + kPlanHeader;
-
-  for (int item = blockIdx.x; item < total; item += gridDim.x) {
-    const int b = item / n_tiles, tile = item - b * n_tiles;
-    const int32_t* blk = blocks + (size_t)b * kBlockInts;
-    const int slot = blk[0], cnt = blk[1];
-    const int pair = col < cnt ? blk[2 + col] : -1;
-    const uint8_t* wr = w2 + ((size_t)slot * H + (size_t)tile * 16 + col) * I + kg * 16;
-    const float* sr = w2_scale + ((size_t)slot * nrb + (tile * 16) / kFp8Blk) * nkb;
-    const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I + kg * 16;
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    for (int kb = kb0; kb < kb1; ++kb) {
-      f32x4_t t = {0.f, 0.f, 0.f, 0.f};
+  const int nkb = I / kFp8Blk, nrb = H / kFp8Blk;
+  const int c0 = 2 * (wave * nkb / kKS), c1 = 2 * ((wave + 1) * nkb / kKS);
+  const int n = c1 - c0;
+  const int r0 = tile2 * 16 * kG2T;
+  const uint8_t* wr = w2 + ((size_t)slot * H + r0 + col) * I + kg * 16 + c0 * 64;
+  const float* sr = w2_scale + ((size_t)slot * nrb + r0 / kFp8Blk) * nkb;
+  const bool hx = pair >= 0;
+  const uint16_t* ar = act + (size_t)(hx ? pair : 0) * I + kg * 16 + c0 * 64;
+  f32x4_t acc[kG2T], tmp[kG2T];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int k0 = kb * kFp8Blk + h * 64;
-        const u32x4_t q = ldg16_stream(wr + k0);
-        u32x4_t b0 = {0u, 0u, 0u, 0u}, b1 = {0u, 0u, 0u, 0u};
-        if (pair >= 0) {
-          b0 = ldg16(ar + k0);
-          b1 = ldg16(ar + k0 + 8);
-        }
-        u32x4_t a0, a1;
-        fp8x16_to_bf16(q, a0, a1);
-        t = mfma16x16x32_bf16(a0, b0, t);
-        t = mfma16x16x32_bf16(a1, b1, t);
+  for (int t = 0; t < kG2T; ++t) acc[t] = tmp[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  u32x4_t q[kF8D][kG2T], b0[kF8D], b1[kF8D];
+#pragma unroll
+  for (int d = 0; d < kF8D; ++d) {
+    b0[d] = b1[d] = u32x4_t{0u, 0u, 0u, 0u};
+    if (d < n) {
+#pragma unroll
+      for (int t = 0; t < kG2T; ++t) q[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + d * 64);
+      if (hx) {
+        b0[d] = ldg16(ar + d * 64);
+        b1[d] = ldg16(ar + d * 64 + 8);
       }
-      acc += sr[kb] * t;
     }
-    red[wave][lane] = acc;
-    __syncthreads();
-    if (wave == 0 && pair >= 0) {
-      f32x4_t s = red[0][lane];
-#pragma unroll
-      for (int w = 1; w < kKS; ++w) s += red[w][lane];
-      const float wv = topk_w[pair];
-      f32x4_t o = {wv * s[0], wv * s[1], wv * s[2], wv * s[3]};
-      *reinterpret_cast<f32x4_t*>(partial + (size_t)pair * H + tile * 16 + kg * 4) = o;
-    }
-    __syncthreads();
   }
+  for (int base = 0; base < n; base += kF8D) {
+#pragma unroll
+    for (int d = 0; d < kF8D; ++d) {
+      const int c = base + d;
+      if (c < n) {
+#pragma unroll
+        for (int t = 0; t < kG2T; ++t) {
+          u32x4_t a0, a1;
+          fp8x16_to_bf16(q[d][t], a0, a1);
+          tmp[t] = mfma16x16x32_bf16(a0, b0[d], tmp[t]);
+          tmp[t] = mfma16x16x32_bf16(a1, b1[d], tmp[t]);
+        }
+        const int nx = c + kF8D;
+        if (nx < n) {
+#pragma unroll
+          for (int t = 0; t < kG2T; ++t) q[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + nx * 64);
+          if (hx) {
+            b0[d] = ldg16(ar + nx * 64);
+            b1[d] = ldg16(ar + nx * 64 + 8);
+          }
+        }
+        if (c & 1) {
+          const float s = sr[(c0 + c) >> 1];
+#pragma unroll
+          for (int t = 0; t < kG2T; ++t) {
+            acc[t] += s * tmp[t];
+            tmp[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kG2T; ++t) red[wave][t][lane] = acc[t];
+  g2_epilogue(red, pair, tile2, H, hx ? topk_w[pair] : 0.f, partial);
 }
 
 // ---------------------------------------------------------------------------
-// Combine: out[t, h] = bf16(scale * sum_j valid ? partial[t*k+j, h] : 0
-//                           + shared[t, h]); j ascending.
+// Staged kernels: grid-stride loops over a plan in global memory.
 // ---------------------------------------------------------------------------
+struct Bf16W {
+  const uint8_t* w13;
+  const uint8_t* w2;
+  const float* s13;
+  const float* s2;
+};
+
+template <bool FP8>
+__device__ __forceinline__ void run_g1(const uint16_t* x, const Bf16W& W, int slot, int pair,
+                                       int tile, int H, int I, int k, uint16_t* act,
+                                       RedBuf& red) {
+  if (FP8)
+    g1_item_fp8(x, W.w13, W.s13, slot, pair, tile, H, I, k, act, red);
+  else
+    g1_item_bf16(x, (const uint16_t*)W.w13, slot, pair, tile, H, I, k, act, red);
+}
+
+template <bool FP8>
+__device__ __forceinline__ void run_g2(const uint16_t* act, const Bf16W& W, int slot, int pair,
+                                       int tile2, int H, int I, const float* tw, float* partial,
+                                       RedBuf& red) {
+  if (FP8)
+    g2_item_fp8(act, W.w2, W.s2, slot, pair, tile2, H, I, tw, partial, red);
+  else
+    g2_item_bf16(act, (const uint16_t*)W.w2, slot, pair, tile2, H, I, tw, partial, red);
+}
+
+template <bool FP8>
+__global__ __launch_bounds__(kThreads) void moe_gemm1_kernel(const uint16_t* __restrict__ x,
+                                                             Bf16W W,
+                                                             const int32_t* __restrict__ plan,
+                                                             int H, int I, int k,
+                                                             uint16_t* __restrict__ act) {
+  __shared__ RedBuf red;
+  const int n_tiles = I / 16;
+  const int total = plan[0] * n_tiles;
+  const int col = threadIdx.x & 15;
+  for (int item = blockIdx.x; item < total; item += gridDim.x) {
+    const int b = item / n_tiles, tile = item - b * n_tiles;
+    const int32_t* blk = plan + kPlanHeader + (size_t)b * kBlockInts;
+    const int pair = col < blk[1] ? blk[2 + col] : -1;
+    run_g1<FP8>(x, W, blk[0], pair, tile, H, I, k, act, red);
+  }
+}
+
+template <bool FP8>
+__global__ __launch_bounds__(kThreads) void moe_gemm2_kernel(const uint16_t* __restrict__ act,
+                                                             Bf16W W,
+                                                             const int32_t* __restrict__ plan,
+                                                             const float* __restrict__ topk_w,
+                                                             int H, int I,
+                                                             float* __restrict__ partial) {
+  __shared__ RedBuf red;
+  const int n_tiles = H / (16 * kG2T);
+  const int total = plan[0] * n_tiles;
+  const int col = threadIdx.x & 15;
+  for (int item = blockIdx.x; item < total; item += gridDim.x) {
+    const int b = item / n_tiles, tile2 = item - b * n_tiles;
+    const int32_t* blk = plan + kPlanHeader + (size_t)b * kBlockInts;
+    const int pair = col < blk[1] ? blk[2 + col] : -1;
+    run_g2<FP8>(act, W, blk[0], pair, tile2, H, I, topk_w, partial, red);
+  }
+}
+
+// out[t, h] = bf16(scale * sum_j valid ? partial[t*k+j, h] : 0 + shared[t, h]),
+// j ascending, for 4 consecutive columns at h.
+__device__ __forceinline__ void combine4(const float* __restrict__ partial,
+                                         const int32_t* __restrict__ valid, int t, int k, int H,
+                                         int h, float scale, const uint16_t* __restrict__ shared,
+                                         uint16_t* __restrict__ out) {
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < k; ++j) {
+    const int p = t * k + j;
+    if (valid[p]) acc += *reinterpret_cast<const f32x4_t*>(partial + (size_t)p * H + h);
+  }
+  float o[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    o[r] = scale * acc[r];
+    if (shared != nullptr) o[r] += bf16_bits_to_f32(shared[(size_t)t * H + h + r]);
+  }
+  *reinterpret_cast<u32x2_t*>(out + (size_t)t * H + h) =
+      u32x2_t{pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
+}
+
 __global__ __launch_bounds__(256) void moe_combine_kernel(
     const float* __restrict__ partial, const int32_t* __restrict__ valid, int k, int H,
     float scale, const uint16_t* __restrict__ shared, uint16_t* __restrict__ out) {
   const int t = blockIdx.y;
   const int h = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (h >= H) return;
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < k; ++j) {
-    const int p = t * k + j;
-    if (valid[p]) acc += *reinterpret_cast<const f32x4_t*>(partial + (size_t)p * H + h);
+  combine4(partial, valid, t, k, H, h, scale, shared, out);
+}
+
+// ---------------------------------------------------------------------------
+// Fused persistent kernel (T*k <= kFusedMaxPairs).
+// ---------------------------------------------------------------------------
+// Work counters of the fused kernel (in the workspace; zero at rest):
+//   ctl[0]                      sticky error: a dependency wait ran out of time
+//   blk_done[kFusedMaxPairs]    gemm1 tiles finished, per block
+//   blk_used[kFusedMaxPairs]    gemm2 items finished, per block
+//   tile_done[H / 32]           gemm2 items finished, per 32-column slice
+// Each counter is returned to zero by the last item that uses it (the last
+// gemm2 item of a block, the combining item of a slice), with device-scope
+// atomics only, so no global "all done" count is needed and no address is
+// hit by every workgroup.
+constexpr int kCtlInts = 32;
+
+__device__ __forceinline__ void fence_release_agent() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+}
+__device__ __forceinline__ void fence_acquire_agent() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// Grid-stride over the items (gemm1 items first), with every workgroup of
+// the grid resident at once (the host sizes the grid from the kernel's
+// occupancy): a gemm2 item only waits for gemm1 items, which never wait.
+template <bool FP8>
+__global__ __launch_bounds__(kThreads) void moe_fused_kernel(
+    const uint16_t* __restrict__ x, Bf16W W, const float* __restrict__ topk_w,
+    const int32_t* __restrict__ ids, const int32_t* __restrict__ map, int P, int H, int I, int k,
+    int E, int S, float scale, const uint16_t* __restrict__ shared, uint16_t* __restrict__ out,
+    int32_t* __restrict__ ctl, uint16_t* __restrict__ act, float* __restrict__ partial,
+    long long timeout_ticks) {
+  __shared__ AlignScratch sc;
+  __shared__ int32_t s_blocks[kFusedMaxPairs * kBlockInts];
+  __shared__ int32_t s_valid[kFusedMaxPairs];
+  __shared__ RedBuf red;
+  __shared__ int s_last_blk, s_last_tile;
+  int32_t* blk_done = ctl + kCtlInts;
+  int32_t* blk_used = blk_done + kFusedMaxPairs;
+  int32_t* tile_done = blk_used + kFusedMaxPairs;
+  const int tid = threadIdx.x;
+  const int col = tid & 15;
+  const int T = P / k;
+
+  const int nb = build_plan(ids, P, map, E, S, sc, s_blocks, s_valid);
+  const int n1t = I / 16, n2t = H / (16 * kG2T);
+  const int N1 = nb * n1t, N = N1 + nb * n2t;
+
+  if (nb == 0) {
+    // nothing resident: out = scale * 0 + shared
+    for (int i = blockIdx.x * kThreads + tid; i < T * (H / 4); i += gridDim.x * kThreads) {
+      const int t = i / (H / 4), h = (i - t * (H / 4)) * 4;
+      combine4(partial, s_valid, t, k, H, h, scale, shared, out);
+    }
+    return;
   }
-  uint16_t o[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    float v = scale * acc[r];
-    if (shared != nullptr) v += bf16_bits_to_f32(shared[(size_t)t * H + h + r]);
-    o[r] = f32_to_bf16_bits(v);
+  for (int item = blockIdx.x; item < N; item += gridDim.x) {
+    if (item < N1) {
+      const int b = item / n1t, tile = item - b * n1t;
+      const int32_t* blk = s_blocks + b * kBlockInts;
+      const int pair = col < blk[1] ? blk[2 + col] : -1;
+      run_g1<FP8>(x, W, blk[0], pair, tile, H, I, k, act, red);
+      fence_release_agent();
+      __syncthreads();
+      if (tid == 0) atomicAdd(&blk_done[b], 1);
+      continue;
+    }
+    const int j = item - N1;
+    const int b = j / n2t, tile2 = j - b * n2t;
+    if (tid == 0) {
+      const long long t0 = wall_clock64();
+      while (__hip_atomic_load(&blk_done[b], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < n1t) {
+        if (wall_clock64() - t0 > timeout_ticks) {
+          atomicExch(&ctl[0], 1);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(8);
+      }
+    }
+    __syncthreads();
+    fence_acquire_agent();
+    const int32_t* blk = s_blocks + b * kBlockInts;
+    const int pair = col < blk[1] ? blk[2 + col] : -1;
+    run_g2<FP8>(act, W, blk[0], pair, tile2, H, I, topk_w, partial, red);
+    fence_release_agent();
+    __syncthreads();
+    if (tid == 0) {
+      s_last_tile = atomicAdd(&tile_done[tile2], 1) == nb - 1;
+      s_last_blk = atomicAdd(&blk_used[b], 1) == n2t - 1;
+      if (s_last_blk) {
+        // every gemm2 item of this block has passed its wait
+        atomicExch(&blk_done[b], 0);
+        atomicExch(&blk_used[b], 0);
+      }
+    }
+    __syncthreads();
+    if (s_last_tile) {
+      // every block's partials for this 32-column slice are written
+      fence_acquire_agent();
+      const int h0 = tile2 * 16 * kG2T;
+      for (int i = tid; i < T * (16 * kG2T / 4); i += kThreads) {
+        const int t = i / (16 * kG2T / 4), h = h0 + (i - t * (16 * kG2T / 4)) * 4;
+        combine4(partial, s_valid, t, k, H, h, scale, shared, out);
+      }
+      if (tid == 0) atomicExch(&tile_done[tile2], 0);
+    }
+    __syncthreads();
   }
-  u32x2_t packed = {(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
-  *reinterpret_cast<u32x2_t*>(out + (size_t)t * H + h) = packed;
 }
 
 // ---------------------------------------------------------------------------
@@ -499,31 +692,67 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 struct Workspace {
+  int32_t* ctl;
   int32_t* plan;
   uint16_t* act;
   float* partial;
 };
 
+// [ctl + counters | plan | act [P, I] bf16 | partial [P, H] fp32].  The
+// counter region has a fixed size, so calls of any shape that share the
+// workspace never write over each other's counters.
 size_t workspace_bytes(int T, int H, int I, int k, Workspace* ws, void* base) {
   const int P = T * k;
-  size_t off = 0;
+  const size_t ctl_b =
+      align_up((kCtlInts + 2 * kFusedMaxPairs + (size_t)kFusedMaxHidden / (16 * kG2T)) * 4, 256);
   const size_t plan_b = align_up(plan_ints(P) * sizeof(int32_t), 256);
   const size_t act_b = align_up((size_t)P * I * sizeof(uint16_t), 256);
   const size_t part_b = align_up((size_t)P * H * sizeof(float), 256);
   if (ws != nullptr) {
     char* b = (char*)base;
-    ws->plan = (int32_t*)(b + off);
-    ws->act = (uint16_t*)(b + off + plan_b);
-    ws->partial = (float*)(b + off + plan_b + act_b);
+    ws->ctl = (int32_t*)b;
+    ws->plan = (int32_t*)(b + ctl_b);
+    ws->act = (uint16_t*)(b + ctl_b + plan_b);
+    ws->partial = (float*)(b + ctl_b + plan_b + act_b);
   }
-  return plan_b + act_b + part_b;
+  return ctl_b + plan_b + act_b + part_b;
 }
 
+#ifndef SLUICE_GRID_CAP
+#define SLUICE_GRID_CAP 8192
+#endif
 int grid_for(int P, int n_tiles) {
   const long items = (long)P * n_tiles;  // upper bound on (block, tile) items
-  const long cap = 8192;
+  const long cap = SLUICE_GRID_CAP;
   return (int)(items < cap ? (items > 0 ? items : 1) : cap);
 }
+
+struct DevInfo {
+  int cus = 0;
+  long long clock_khz = 0;
+  int fused_per_cu[2] = {0, 0};  // resident fused workgroups per CU (bf16, fp8)
+};
+DevInfo g_info[64];
+
+int dev_info(DevInfo** out) {
+  int dev = 0;
+  SLUICE_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return SLUICE_E_INVAL;
+  DevInfo& d = g_info[dev];
+  if (d.cus == 0) {
+    int cus = 0, khz = 0;
+    SLUICE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    SLUICE_HIP_CHECK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+    d.clock_khz = khz > 0 ? khz : 100000;
+    d.cus = cus > 0 ? cus : 256;
+  }
+  *out = &d;
+  return SLUICE_OK;
+}
+
+#ifndef SLUICE_FUSED_WG_PER_CU
+#define SLUICE_FUSED_WG_PER_CU 4
+#endif
 
 int check_common(int T, int H, int I, int k, int E, int S, const void* x, const void* w13,
                  const void* w2, const float* tw, const int32_t* ti, void* ws, size_t ws_bytes,
@@ -532,13 +761,74 @@ int check_common(int T, int H, int I, int k, int E, int S, const void* x, const 
       S > SLUICE_MAX_SLOTS)
     return SLUICE_E_INVAL;
   if ((long)T * k > SLUICE_MAX_PAIRS) return SLUICE_E_INVAL;
-  if (H % 32 != 0 || H % (16 * kG2T) != 0 || I % 32 != 0) return SLUICE_E_INVAL;
+  if (H % (16 * kG2T) != 0 || I % 32 != 0) return SLUICE_E_INVAL;
   if (T == 0) return SLUICE_OK;
   if (!x || !w13 || !w2 || !tw || !ti || !ws || !out) return SLUICE_E_INVAL;
   if (ws_bytes < workspace_bytes(T, H, I, k, nullptr, nullptr)) return SLUICE_E_INVAL;
   if (((uintptr_t)x | (uintptr_t)w13 | (uintptr_t)w2 | (uintptr_t)ws | (uintptr_t)out) & 15)
     return SLUICE_E_INVAL;
   return SLUICE_OK;
+}
+
+int launch_combine(const float* partial, const int32_t* valid, int T, int k, int H, float scale,
+                   const void* shared, void* out, hipStream_t st) {
+  dim3 grid((H / 4 + 255) / 256, T);
+  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, st, partial, valid, k, H, scale,
+                     (const uint16_t*)shared, (uint16_t*)out);
+  return (int)hipGetLastError();
+}
+
+int& fused_flag() {
+  static int v = [] {
+    const char* s = getenv("SLUICE_MOE_FUSED");
+    return (s != nullptr && s[0] == '1') ? 1 : 0;
+  }();
+  return v;
+}
+int fused_enabled() { return __atomic_load_n(&fused_flag(), __ATOMIC_RELAXED); }
+
+template <bool FP8>
+int run_experts(const void* x, const Bf16W& W, const float* tw, const int32_t* ti,
+                const int32_t* map, int T, int H, int I, int k, int E, int S, float scale,
+                const void* shared, void* workspace, void* out, hipStream_t st) {
+  Workspace w;
+  workspace_bytes(T, H, I, k, &w, workspace);
+  const int P = T * k;
+  // The fused kernel is opt-in (SLUICE_MOE_FUSED=1): its cross-workgroup
+  // hand-offs need agent-scope cache maintenance that costs more than the
+  // three kernel boundaries it removes.
+  if (P <= kFusedMaxPairs && H <= kFusedMaxHidden && fused_enabled() != 0) {
+    DevInfo* di = nullptr;
+    int rc = dev_info(&di);
+    if (rc) return rc;
+    const long upper = (long)P * (I / 16 + H / (16 * kG2T));  // items with nb <= P
+    int& per_cu = di->fused_per_cu[FP8 ? 1 : 0];
+    if (per_cu == 0) {
+      int n = 0;
+      SLUICE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &n, reinterpret_cast<const void*>(&moe_fused_kernel<FP8>), kThreads, 0));
+      per_cu = n > 0 ? n : 1;
+    }
+    // every workgroup resident at once (a gemm2 item waits for gemm1 items)
+    long grid = (long)di->cus * (per_cu < SLUICE_FUSED_WG_PER_CU ? per_cu : SLUICE_FUSED_WG_PER_CU);
+    if (grid > upper) grid = upper;
+    if (grid < 1) grid = 1;
+    const long long ticks = (long long)(2.0 * 1000.0 * (double)di->clock_khz);
+    hipLaunchKernelGGL((moe_fused_kernel<FP8>), dim3((unsigned)grid), dim3(kThreads), 0, st,
+                       (const uint16_t*)x, W, tw, ti, map, P, H, I, k, E, S, scale,
+                       (const uint16_t*)shared, (uint16_t*)out, w.ctl, w.act, w.partial, ticks);
+    return (int)hipGetLastError();
+  }
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kThreads), 0, st, ti, P, map, E, S, w.plan);
+  SLUICE_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL((moe_gemm1_kernel<FP8>), dim3(grid_for(P, I / 16)), dim3(kThreads), 0, st,
+                     (const uint16_t*)x, W, w.plan, H, I, k, w.act);
+  SLUICE_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL((moe_gemm2_kernel<FP8>), dim3(grid_for(P, H / (16 * kG2T))), dim3(kThreads),
+                     0, st, w.act, W, w.plan, tw, H, I, w.partial);
+  SLUICE_HIP_CHECK(hipGetLastError());
+  return launch_combine(w.partial, w.plan + kPlanHeader + (size_t)kBlockInts * P, T, k, H, scale,
+                        shared, out, st);
 }
 
 }  // namespace
@@ -550,23 +840,25 @@ extern "C" size_t sluice_fused_experts_workspace(int T, int H, int I, int k) {
   return workspace_bytes(T, H, I, k, nullptr, nullptr);
 }
 
+extern "C" int sluice_moe_set_fused(int enable) {
+  return __atomic_exchange_n(&fused_flag(), enable ? 1 : 0, __ATOMIC_RELAXED);
+}
+
+extern "C" int sluice_fused_experts_status(const void* workspace, int* error_out) {
+  if (workspace == nullptr || error_out == nullptr) return SLUICE_E_INVAL;
+  int32_t ctl[kCtlInts];
+  SLUICE_HIP_CHECK(hipMemcpy(ctl, workspace, sizeof(ctl), hipMemcpyDeviceToHost));
+  *error_out = ctl[0];
+  return SLUICE_OK;
+}
+
 extern "C" int sluice_moe_align(const int32_t* topk_ids, int T, int k, const int32_t* expert_map,
                                 int E, int S, int32_t* plan, sluice_stream_t stream) {
   if (T < 0 || k <= 0 || E <= 0 || S <= 0 || S > SLUICE_MAX_SLOTS ||
       (long)T * k > SLUICE_MAX_PAIRS || plan == nullptr)
     return SLUICE_E_INVAL;
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, (hipStream_t)stream,
-                     topk_ids, T * k, expert_map, E, S, plan);
-  return (int)hipGetLastError();
-}
-
-static int launch_combine(const Workspace& w, int T, int k, int H, float scale, const void* shared,
-                          void* out, hipStream_t st) {
-  const int P = T * k;
-  const int32_t* valid = w.plan + kPlanHeader + (size_t)kBlockInts * P;
-  dim3 grid((H / 4 + 255) / 256, T);
-  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, st, w.partial, valid, k, H, scale,
-                     (const uint16_t*)shared, (uint16_t*)out);
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, topk_ids,
+                     T * k, expert_map, E, S, plan);
   return (int)hipGetLastError();
 }
 
@@ -579,57 +871,9 @@ extern "C" int sluice_fused_experts_bf16(const void* x, const void* w13, const v
   int rc = check_common(T, H, I, k, E, S, x, w13, w2, topk_w, topk_ids, workspace,
                         workspace_bytes_, out);
   if (rc != SLUICE_OK || T == 0) return rc;
-  hipStream_t st = (hipStream_t)stream;
-  Workspace w;
-  workspace_bytes(T, H, I, k, &w, workspace);
-  const int P = T * k;
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, st, topk_ids, P,
-                     expert_map, E, S, w.plan);
-  SLUICE_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(moe_gemm1_bf16_kernel, dim3(grid_for(P, I / 16)), dim3(64 * kG1KS), 0, st,
-                     (const uint16_t*)x, (const uint16_t*)w13, w.plan, H, I, k, w.act);
-  SLUICE_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(moe_gemm2_bf16_kernel, dim3(grid_for(P, H / (16 * kG2T))),
-                     dim3(64 * kG2KS), 0, st, w.act, (const uint16_t*)w2, w.plan, topk_w, H, I,
-                     w.partial);
-  SLUICE_HIP_CHECK(hipGetLastError());
-  return launch_combine(w, T, k, H, scale, shared, out, st);
-}
-
-extern "C" int sluice_moe_gemm1_bf16(const void* x, const void* w13, const int32_t* plan, int T,
-                                     int H, int I, int k, void* act, sluice_stream_t stream) {
-  if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % 32 || I % 32 || (long)T * k > SLUICE_MAX_PAIRS ||
-      !x || !w13 || !plan || !act)
-    return SLUICE_E_INVAL;
-  hipLaunchKernelGGL(moe_gemm1_bf16_kernel, dim3(grid_for(T * k, I / 16)), dim3(64 * kG1KS), 0,
-                     (hipStream_t)stream, (const uint16_t*)x, (const uint16_t*)w13, plan, H, I, k,
-                     (uint16_t*)act);
-  return (int)hipGetLastError();
-}
-
-extern "C" int sluice_moe_gemm2_bf16(const void* act, const void* w2, const int32_t* plan,
-                                     const float* topk_w, int T, int H, int I, int k,
-                                     float* partial, sluice_stream_t stream) {
-  if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % (16 * kG2T) || I % 32 ||
-      (long)T * k > SLUICE_MAX_PAIRS || !act || !w2 || !plan || !topk_w || !partial)
-    return SLUICE_E_INVAL;
-  hipLaunchKernelGGL(moe_gemm2_bf16_kernel, dim3(grid_for(T * k, H / (16 * kG2T))),
-                     dim3(64 * kG2KS), 0, (hipStream_t)stream, (const uint16_t*)act,
-                     (const uint16_t*)w2, plan, topk_w, H, I, partial);
-  return (int)hipGetLastError();
-}
-
-extern "C" int sluice_moe_combine(const float* partial, const int32_t* plan, int T, int k, int H,
-                                  float scale, const void* shared, void* out,
-                                  sluice_stream_t stream) {
-  if (T <= 0 || k <= 0 || H <= 0 || H % 4 || (long)T * k > SLUICE_MAX_PAIRS || !partial || !plan ||
-      !out)
-    return SLUICE_E_INVAL;
-  Workspace w;
-  w.plan = const_cast<int32_t*>(plan);
-  w.partial = const_cast<float*>(partial);
-  w.act = nullptr;
-  return launch_combine(w, T, k, H, scale, shared, out, (hipStream_t)stream);
+  Bf16W W{(const uint8_t*)w13, (const uint8_t*)w2, nullptr, nullptr};
+  return run_experts<false>(x, W, topk_w, topk_ids, expert_map, T, H, I, k, E, S, scale, shared,
+                            workspace, out, (hipStream_t)stream);
 }
 
 extern "C" int sluice_fused_experts_fp8(const void* x, const void* w13, const float* w13_scale,
@@ -646,18 +890,41 @@ extern "C" int sluice_fused_experts_fp8(const void* x, const void* w13, const fl
                         workspace_bytes_, out);
   if (rc != SLUICE_OK || T == 0) return rc;
   if (w13_scale == nullptr || w2_scale == nullptr) return SLUICE_E_INVAL;
-  hipStream_t st = (hipStream_t)stream;
-  Workspace w;
-  workspace_bytes(T, H, I, k, &w, workspace);
-  const int P = T * k;
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, st, topk_ids, P,
-                     expert_map, E, S, w.plan);
-  SLUICE_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(moe_gemm1_fp8_kernel, dim3(grid_for(P, I / 16)), dim3(64 * kKS), 0, st,
-                     (const uint16_t*)x, (const uint8_t*)w13, w13_scale, w.plan, H, I, k, w.act);
-  SLUICE_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(moe_gemm2_fp8_kernel, dim3(grid_for(P, H / 16)), dim3(64 * kKS), 0, st,
-                     w.act, (const uint8_t*)w2, w2_scale, w.plan, topk_w, H, I, w.partial);
-  SLUICE_HIP_CHECK(hipGetLastError());
-  return launch_combine(w, T, k, H, scale, shared, out, st);
+  Bf16W W{(const uint8_t*)w13, (const uint8_t*)w2, w13_scale, w2_scale};
+  return run_experts<true>(x, W, topk_w, topk_ids, expert_map, T, H, I, k, E, S, scale, shared,
+                           workspace, out, (hipStream_t)stream);
+}
+
+extern "C" int sluice_moe_gemm1_bf16(const void* x, const void* w13, const int32_t* plan, int T,
+                                     int H, int I, int k, void* act, sluice_stream_t stream) {
+  if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % 32 || I % 32 || (long)T * k > SLUICE_MAX_PAIRS ||
+      !x || !w13 || !plan || !act)
+    return SLUICE_E_INVAL;
+  Bf16W W{(const uint8_t*)w13, nullptr, nullptr, nullptr};
+  hipLaunchKernelGGL(moe_gemm1_kernel<false>, dim3(grid_for(T * k, I / 16)), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const uint16_t*)x, W, plan, H, I, k, (uint16_t*)act);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sluice_moe_gemm2_bf16(const void* act, const void* w2, const int32_t* plan,
+                                     const float* topk_w, int T, int H, int I, int k,
+                                     float* partial, sluice_stream_t stream) {
+  if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % (16 * kG2T) || I % 32 ||
+      (long)T * k > SLUICE_MAX_PAIRS || !act || !w2 || !plan || !topk_w || !partial)
+    return SLUICE_E_INVAL;
+  Bf16W W{nullptr, (const uint8_t*)w2, nullptr, nullptr};
+  hipLaunchKernelGGL(moe_gemm2_kernel<false>, dim3(grid_for(T * k, H / (16 * kG2T))),
+                     dim3(kThreads), 0, (hipStream_t)stream, (const uint16_t*)act, W, plan, topk_w,
+                     H, I, partial);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sluice_moe_combine(const float* partial, const int32_t* plan, int T, int k, int H,
+                                  float scale, const void* shared, void* out,
+                                  sluice_stream_t stream) {
+  if (T <= 0 || k <= 0 || H <= 0 || H % 4 || (long)T * k > SLUICE_MAX_PAIRS || !partial || !plan ||
+      !out)
+    return SLUICE_E_INVAL;
+  return launch_combine(partial, plan + kPlanHeader + (size_t)kBlockInts * T * k, T, k, H, scale,
+                        shared, out, (hipStream_t)stream);
 }

@@ -63,7 +63,7 @@ class RoutingBias:
     through a device index."""
 
     def __init__(self, E: int, rows: int, steps: int, zipf_s: float, rho: float, sigma: float,
-                 seed: int, device):
+                 seed: int, device, step: Optional[torch.Tensor] = None):
         rng = np.random.default_rng(seed)
         p = 1.0 / np.arange(1, E + 1) ** zipf_s
         p = p / p.sum()
@@ -75,7 +75,7 @@ class RoutingBias:
                 np.float32)
             z[t] = cur
         self.table = torch.from_numpy(zipf[None, None, :] + sigma * z).to(device)  # [steps,rows,E]
-        self.step = torch.zeros((), dtype=torch.long, device=device)
+        self.step = step if step is not None else torch.zeros((), dtype=torch.long, device=device)
 
     def __call__(self, T: int) -> torch.Tensor:
         return self.table.index_select(0, self.step.view(1))[0, :T]
@@ -215,17 +215,51 @@ SPECS = {
 }
 
 
-def _rmsnorm(x, w, eps=1e-6):
-    xf = x.float()
-    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    return (xf * w.float()).to(x.dtype)
+_EPS = 1e-6
 
 
-def _rope(x, cos, sin):
-    """rotate-half RoPE; x [..., d], cos/sin broadcastable [..., d/2]."""
-    d = x.shape[-1] // 2
-    x1, x2 = x[..., :d].float(), x[..., d:].float()
-    return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).to(x.dtype)
+def _k():
+    from sluice_amd import _lib
+
+    return _lib.load(), _lib.check
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def add_rmsnorm(x, delta, w, out=None, eps=_EPS):
+    """x += delta (bf16, in place; skipped when delta is None), then
+    out = rmsnorm(x) * w.  One kernel."""
+    lib, check = _k()
+    if out is None:
+        out = torch.empty_like(x)
+    check(lib.sluice_dec_add_rmsnorm(x.data_ptr(), None if delta is None else delta.data_ptr(),
+                                     w.data_ptr(), out.data_ptr(), x.shape[0], x.shape[1],
+                                     float(eps), _stream(x)), "sluice_dec_add_rmsnorm")
+    return out
+
+
+def linear(x, w):
+    """y = x . w^T for decode batches (T <= 16): one streaming MFMA kernel."""
+    lib, check = _k()
+    T, K = x.shape
+    N = w.shape[0]
+    if T > 16:
+        raise ValueError(f"decode linear supports at most 16 rows, got {T}")
+    y = torch.empty((T, N), dtype=x.dtype, device=x.device)
+    check(lib.sluice_dec_linear(x.data_ptr(), w.data_ptr(), T, N, K, y.data_ptr(), _stream(x)),
+          "sluice_dec_linear")
+    return y
+
+
+def silu_mul(gu):
+    lib, check = _k()
+    rows, two_i = gu.shape
+    out = torch.empty((rows, two_i // 2), dtype=gu.dtype, device=gu.device)
+    check(lib.sluice_dec_silu_mul(gu.data_ptr(), out.data_ptr(), rows, two_i // 2, _stream(gu)),
+          "sluice_dec_silu_mul")
+    return out
 
 
 def _randn(shape, gen, std, dev, dtype=torch.bfloat16):
@@ -233,54 +267,58 @@ def _randn(shape, gen, std, dev, dtype=torch.bfloat16):
 
 
 class _MLA(nn.Module):
-    """Multi-head latent attention, decode form with the up-projections
-    absorbed: scores over the compressed KV latent and the rope key."""
+    """Multi-head latent attention (DeepSeek-V2), decode form with the
+    up-projections absorbed: one GEMM for [q ; kv latent + rope key], a prep
+    kernel (q absorption into the latent space, RoPE, latent RMSNorm, cache
+    write), an attention kernel over the latent cache (scores, softmax,
+    weighted latent sum, value up-projection) and the output GEMM."""
 
     def __init__(self, sp, batch, max_len, dev, gen):
         super().__init__()
         H, nh, lora = sp["H"], sp["heads"], sp["kv_lora"]
         nope, rope, vh = sp["qk_nope"], sp["qk_rope"], sp["v_head"]
         self.nh, self.lora, self.nope, self.rope, self.vh = nh, lora, nope, rope, vh
-        self.wq = _randn((nh * (nope + rope), H), gen, 0.02, dev)
-        self.wkva = _randn((lora + rope, H), gen, 0.02, dev)
+        self.nq = nh * (nope + rope)
+        self.w_qkva = _randn((self.nq + lora + rope, H), gen, 0.02, dev)
         self.kv_norm = torch.ones(lora, device=dev, dtype=torch.bfloat16)
         self.w_uk = _randn((nh, nope, lora), gen, 0.02, dev)
         self.w_uv = _randn((nh, lora, vh), gen, 0.02, dev)
         self.wo = _randn((H, nh * vh), gen, 0.02, dev)
         self.ckv = torch.zeros((batch, max_len, lora), device=dev, dtype=torch.bfloat16)
-        self.ckvT = torch.zeros((batch, lora, max_len), device=dev, dtype=torch.bfloat16)
-        self.kpeT = torch.zeros((batch, rope, max_len), device=dev, dtype=torch.bfloat16)
+        self.kpe = torch.zeros((batch, max_len, rope), device=dev, dtype=torch.bfloat16)
         self.scale = (nope + rope) ** -0.5
+        self.L = max_len
 
     def fill_prompt(self, n, gen):
         b, _, lora = self.ckv.shape
-        lat = _randn((b, n, lora), gen, 1.0, self.ckv.device)
-        self.ckv[:, :n] = lat
-        self.ckvT[:, :, :n] = lat.transpose(1, 2)
-        self.kpeT[:, :, :n] = _randn((b, self.rope, n), gen, 1.0, self.ckv.device)
+        self.ckv[:, :n] = _randn((b, n, lora), gen, 1.0, self.ckv.device)
+        self.kpe[:, :n] = _randn((b, n, self.rope), gen, 1.0, self.ckv.device)
 
-    def forward(self, x, pos, bidx, cos, sin, mask):
-        c = x.shape[0]
-        q = F.linear(x, self.wq).view(c, self.nh, self.nope + self.rope)
-        q_nope, q_pe = q[..., : self.nope], q[..., self.nope:]
-        q_pe = _rope(q_pe, cos[:, None, :], sin[:, None, :])
-        kva = F.linear(x, self.wkva)
-        ckv = _rmsnorm(kva[:, : self.lora], self.kv_norm)
-        kpe = _rope(kva[:, self.lora:], cos, sin)
-        self.ckv[bidx, pos] = ckv
-        self.ckvT[bidx, :, pos] = ckv
-        self.kpeT[bidx, :, pos] = kpe
-        q_lat = torch.matmul(q_nope.transpose(0, 1).contiguous(), self.w_uk)  # [nh, c, lora]
-        q_lat = q_lat.transpose(0, 1).contiguous()
-        s = torch.matmul(q_lat, self.ckvT[:c]) + torch.matmul(q_pe.contiguous(), self.kpeT[:c])
-        p = torch.softmax(s.float() * self.scale + mask[:, None, :], dim=-1).to(x.dtype)
-        o_lat = torch.matmul(p, self.ckv[:c])  # [c, nh, lora]
-        o = torch.matmul(o_lat.transpose(0, 1).contiguous(), self.w_uv)  # [nh, c, vh]
-        return F.linear(o.transpose(0, 1).reshape(c, self.nh * self.vh), self.wo)
+    def forward(self, hn, pos, cos_t, sin_t):
+        lib, check = _k()
+        c = hn.shape[0]
+        qkva = linear(hn, self.w_qkva)
+        st = _stream(hn)
+        q_lat = torch.empty((c, self.nh, self.lora), dtype=torch.float32, device=hn.device)
+        q_pe = torch.empty((c, self.nh, self.rope), dtype=torch.float32, device=hn.device)
+        row = qkva.shape[1]
+        check(lib.sluice_dec_mla_prep(
+            qkva.data_ptr(), row, qkva.data_ptr() + self.nq * 2, row, self.kv_norm.data_ptr(),
+            self.w_uk.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(), pos.data_ptr(), c, self.nh,
+            self.nope, self.rope, self.lora, self.L, _EPS, q_lat.data_ptr(), q_pe.data_ptr(),
+            self.ckv.data_ptr(), self.kpe.data_ptr(), st), "sluice_dec_mla_prep")
+        o = torch.empty((c, self.nh * self.vh), dtype=hn.dtype, device=hn.device)
+        check(lib.sluice_dec_mla_attend(
+            q_lat.data_ptr(), q_pe.data_ptr(), self.ckv.data_ptr(), self.kpe.data_ptr(),
+            self.w_uv.data_ptr(), pos.data_ptr(), c, self.nh, self.rope, self.lora, self.vh,
+            self.L, float(self.scale), o.data_ptr(), st), "sluice_dec_mla_attend")
+        return linear(o, self.wo)
 
 
 class _GQA(nn.Module):
-    """Grouped-query attention with per-head q/k RMSNorm (Qwen3)."""
+    """Grouped-query attention with per-head q/k RMSNorm (Qwen3): one QKV
+    GEMM, a prep kernel (norms, RoPE, cache write), an attention kernel and
+    the output GEMM."""
 
     def __init__(self, sp, batch, max_len, dev, gen):
         super().__init__()
@@ -290,33 +328,37 @@ class _GQA(nn.Module):
         self.q_norm = torch.ones(hd, device=dev, dtype=torch.bfloat16)
         self.k_norm = torch.ones(hd, device=dev, dtype=torch.bfloat16)
         self.wo = _randn((H, nh * hd), gen, 0.02, dev)
-        self.kT = torch.zeros((batch, kvh, hd, max_len), device=dev, dtype=torch.bfloat16)
+        self.k = torch.zeros((batch, kvh, max_len, hd), device=dev, dtype=torch.bfloat16)
         self.v = torch.zeros((batch, kvh, max_len, hd), device=dev, dtype=torch.bfloat16)
         self.scale = hd ** -0.5
+        self.L = max_len
 
     def fill_prompt(self, n, gen):
         b = self.v.shape[0]
-        self.kT[:, :, :, :n] = _randn((b, self.kvh, self.hd, n), gen, 1.0, self.v.device)
+        self.k[:, :, :n] = _randn((b, self.kvh, n, self.hd), gen, 1.0, self.v.device)
         self.v[:, :, :n] = _randn((b, self.kvh, n, self.hd), gen, 1.0, self.v.device)
 
-    def forward(self, x, pos, bidx, cos, sin, mask):
-        c = x.shape[0]
-        qkv = F.linear(x, self.wqkv)
-        q = qkv[:, : self.nh * self.hd].view(c, self.nh, self.hd)
-        k = qkv[:, self.nh * self.hd: (self.nh + self.kvh) * self.hd].view(c, self.kvh, self.hd)
-        v = qkv[:, (self.nh + self.kvh) * self.hd:].view(c, self.kvh, self.hd)
-        q = _rope(_rmsnorm(q, self.q_norm), cos[:, None, :], sin[:, None, :])
-        k = _rope(_rmsnorm(k, self.k_norm), cos[:, None, :], sin[:, None, :])
-        self.kT[bidx, :, :, pos] = k
-        self.v[bidx, :, pos] = v
-        qg = q.view(c, self.kvh, self.nh // self.kvh, self.hd)
-        s = torch.matmul(qg, self.kT[:c])  # [c, kvh, g, L]
-        p = torch.softmax(s.float() * self.scale + mask[:, None, None, :], dim=-1).to(x.dtype)
-        o = torch.matmul(p, self.v[:c])  # [c, kvh, g, hd]
-        return F.linear(o.reshape(c, self.nh * self.hd), self.wo)
+    def forward(self, hn, pos, cos_t, sin_t):
+        lib, check = _k()
+        c = hn.shape[0]
+        qkv = linear(hn, self.wqkv)
+        st = _stream(hn)
+        q = torch.empty((c, self.nh, self.hd), dtype=torch.float32, device=hn.device)
+        check(lib.sluice_dec_gqa_prep(
+            qkv.data_ptr(), self.q_norm.data_ptr(), self.k_norm.data_ptr(), cos_t.data_ptr(),
+            sin_t.data_ptr(), pos.data_ptr(), c, self.nh, self.kvh, self.hd, self.L, _EPS,
+            q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), st), "sluice_dec_gqa_prep")
+        o = torch.empty((c, self.nh * self.hd), dtype=hn.dtype, device=hn.device)
+        check(lib.sluice_dec_gqa_attend(
+            q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), pos.data_ptr(), c, self.nh,
+            self.kvh, self.hd, self.L, float(self.scale), o.data_ptr(), st),
+            "sluice_dec_gqa_attend")
+        return linear(o, self.wo)
 
 
 class _DenseMLP(nn.Module):
+    """SwiGLU MLP: gate/up GEMM, one activation kernel, down GEMM."""
+
     def __init__(self, H, I, dev, gen):
         super().__init__()
         self.gate_up = _randn((2 * I, H), gen, 0.02, dev)
@@ -324,8 +366,7 @@ class _DenseMLP(nn.Module):
         self.I = I
 
     def forward(self, x):
-        gu = F.linear(x, self.gate_up)
-        return F.linear(F.silu(gu[:, : self.I]) * gu[:, self.I:], self.down)
+        return linear(silu_mul(linear(x, self.gate_up)), self.down)
 
 
 def _expert_store(sp, gen_seed, dev, fp8):
@@ -411,10 +452,17 @@ class _StoreMoELayer(nn.Module):
         return r
 
     def logits(self, hn):
-        lg = F.linear(hn, self.gate.weight).float()
-        if self.routing_bias is not None:
-            lg = lg + self.routing_bias(hn.shape[0])
-        return lg
+        """Router logits (fp32) = gate GEMV + this step's synthetic bias, one kernel."""
+        lib, check = _k()
+        T = hn.shape[0]
+        out = torch.empty((T, self.E), dtype=torch.float32, device=hn.device)
+        rb = self.routing_bias
+        check(lib.sluice_dec_gate_logits(
+            hn.data_ptr(), self.gate.weight.data_ptr(),
+            None if rb is None else rb.table.data_ptr(), None if rb is None else rb.step.data_ptr(),
+            0 if rb is None else rb.table.shape[0], 0 if rb is None else rb.table.shape[1], T,
+            self.H, self.E, out.data_ptr(), _stream(hn)), "sluice_dec_gate_logits")
+        return out
 
     def select(self, lg):
         sp = self.sp
@@ -423,13 +471,14 @@ class _StoreMoELayer(nn.Module):
                                   e_score_correction_bias=self.e_score_correction_bias,
                                   num_expert_group=sp["n_group"], topk_group=sp["topk_group"])
 
-    def experts(self, hn, tw, ti):
+    def experts(self, hn, tw, ti, shared_output=None):
         kw = {}
         if self.sp["fp8"]:
             kw = dict(w1_scale=self.w13_weight_scale, w2_scale=self.w2_weight_scale,
                       block_shape=[128, 128])
         return ops.fused_experts(hn, self.w13_weight, self.w2_weight, tw, ti,
-                                 global_num_experts=self.E, expert_map=self._expert_map, **kw)
+                                 global_num_experts=self.E, expert_map=self._expert_map,
+                                 shared_output=shared_output, **kw)
 
 
 class SyntheticDecoder:
@@ -477,6 +526,7 @@ class SyntheticDecoder:
         self.blocks = []
         self.moe_layers = []
         self.bias_tables = []
+        self.step = torch.zeros((), dtype=torch.long, device=dev)  # routing-bias row, all layers
         store = None
         for li in range(sp["layers"]):
             blk = types.SimpleNamespace(attn=None, mlp=None, moe=None,
@@ -495,12 +545,13 @@ class SyntheticDecoder:
                     store = _expert_store(sp, 7000 + li, dev, sp["fp8"])
                 rb = None
                 if uniform_routing:
-                    rb = RoutingBias(sp["E"], max_batch, steps_tbl, 0.0, 0.0, 0.0, 8000 + li, dev)
+                    rb = RoutingBias(sp["E"], max_batch, steps_tbl, 0.0, 0.0, 0.0, 8000 + li, dev,
+                                     step=self.step)
                     rb.table.normal_(generator=g)
                     rb.table.mul_(10.0)
                 else:
                     rb = RoutingBias(sp["E"], max_batch, steps_tbl, zipf_s, rho, sigma, 8000 + li,
-                                     dev)
+                                     dev, step=self.step)
                 self.bias_tables.append(rb)
                 blk.moe = _StoreMoELayer(sp, store, li, dev, rb, f"layers.{li}.mlp",
                                          gate_std=gate_std)
@@ -544,78 +595,66 @@ class SyntheticDecoder:
     def reset(self, c):
         st = self._state(c)
         st.pos.fill_(self.prompt_len)
-        for rb in self.bias_tables:
-            rb.step.zero_()
+        self.step.zero_()
 
     # -- pieces ----------------------------------------------------------------
-    def _attn_block(self, blk, x, st):
-        c = x.shape[0]
-        cos = self.cos_tbl.index_select(0, st.pos)
-        sin = self.sin_tbl.index_select(0, st.pos)
-        ar = torch.arange(self.max_len, device=self.dev)
-        mask = torch.where(ar[None, :] <= st.pos[:, None], 0.0, float("-inf"))
-        return x + blk.attn(_rmsnorm(x, blk.n1), st.pos, st.bidx[:c], cos, sin, mask)
+    def _block_front(self, i, io, st):
+        """Block i up to its MLP input: the residual add of the pending
+        delta fused into the attention norm, attention, then the MLP norm
+        (which adds the attention output).  Leaves io["hn"] = MLP input."""
+        blk = self.blocks[i]
+        x = io["x"]
+        if blk.attn is not None:
+            hn = add_rmsnorm(x, io["delta"], blk.n1)
+            io["delta"] = blk.attn(hn, st.pos, self.cos_tbl, self.sin_tbl)
+        io["hn"] = add_rmsnorm(x, io["delta"], blk.n2)
+        io["delta"] = None
 
-    def _run_until_moe(self, start, x, st):
-        """Blocks from index `start` up to (not including) the next MoE
-        block's experts; returns (x, h, hn, moe_block_index or None)."""
-        i = start
+    def _to_next_gap(self, i, io, st):
+        """From block i on: run dense blocks; at the next MoE block compute
+        its norm, router logits and top-k, and return its index (None if
+        the model ends first, after the final norm, LM head and next token)."""
         while i < len(self.blocks):
             blk = self.blocks[i]
-            if blk.attn is not None:
-                x = self._attn_block(blk, x, st)
+            self._block_front(i, io, st)
             if blk.moe is None:
-                x = x + blk.mlp(_rmsnorm(x, blk.n2))
+                io["delta"] = blk.mlp(io["hn"])
                 i += 1
                 continue
-            hn = _rmsnorm(x, blk.n2)
-            return x, hn, i
-        return x, None, None
+            tw, ti = blk.moe.select(blk.moe.logits(io["hn"]))
+            io.update(tw=tw, ti=ti, i=i)
+            return i
+        hf = add_rmsnorm(io["x"], io["delta"], self.final_norm)
+        if self.has_attn:
+            st.tokens.copy_(torch.argmax(linear(hf, self.lm_head), dim=-1))
+            st.pos.add_(1)
+        else:
+            st.x.copy_(hf)
+        self.step.add_(1)
+        return None
 
     def pieces(self, c):
-        """List of (piece_fn, gap_layer_index or None); piece_fn(io) mutates io."""
+        """List of (piece_fn, gap_layer_index or None); piece_fn(io) mutates
+        io.  Piece 0 embeds and runs up to the first MoE routing; piece p runs
+        MoE layer p-1's experts (shared expert folded into the combine) and
+        on to MoE layer p's routing; the last piece ends the step."""
         st = self._state(c)
-        out = []
         moe_pos = [i for i, b in enumerate(self.blocks) if b.moe is not None]
 
         def first(io):
-            if self.has_attn:
-                x = self.embed.index_select(0, st.tokens)
-            else:
-                x = st.x.clone()
-            x, hn, i = self._run_until_moe(0, x, st)
-            blk = self.blocks[i]
-            lg = blk.moe.logits(hn)
-            tw, ti = blk.moe.select(lg)
-            io.update(x=x, hn=hn, tw=tw, ti=ti, i=i)
+            x = self.embed.index_select(0, st.tokens) if self.has_attn else st.x.clone()
+            io.update(x=x, delta=None)
+            self._to_next_gap(0, io, st)
 
-        out.append((first, 0))
+        out = [(first, 0)]
         for n, i in enumerate(moe_pos):
             last = n == len(moe_pos) - 1
 
-            def mid(io, i=i, last=last):
-                blk = self.blocks[i]
-                routed = blk.moe.experts(io["hn"], io["tw"], io["ti"])
-                if blk.moe.shared is not None:
-                    routed = routed + blk.moe.shared(io["hn"])
-                x = io["x"] + routed
-                if not last:
-                    x, hn, j = self._run_until_moe(i + 1, x, st)
-                    nb = self.blocks[j]
-                    lg = nb.moe.logits(hn)
-                    tw, ti = nb.moe.select(lg)
-                    io.update(x=x, hn=hn, tw=tw, ti=ti, i=j)
-                else:
-                    x, _, _ = self._run_until_moe(i + 1, x, st)
-                    if self.has_attn:
-                        logits = F.linear(_rmsnorm(x, self.final_norm), self.lm_head)
-                        st.tokens.copy_(torch.argmax(logits.float(), dim=-1))
-                        st.pos.add_(1)
-                    else:
-                        st.x.copy_(_rmsnorm(x, self.final_norm))
-                    for rb in self.bias_tables:
-                        rb.step.add_(1)
-                    io.update(x=x)
+            def mid(io, i=i):
+                moe = self.blocks[i].moe
+                sh = moe.shared(io["hn"]) if moe.shared is not None else None
+                io["delta"] = moe.experts(io["hn"], io["tw"], io["ti"], shared_output=sh)
+                self._to_next_gap(i + 1, io, st)
 
             out.append((mid, n + 1 if not last else None))
         return out

@@ -1,0 +1,207 @@
+"""Kernels of the synthetic decoders (include/sluice_decoder.h) against plain
+float32 torch references of the same math, computed on the CPU from the same
+bf16 inputs: residual add + RMSNorm, SwiGLU activation, router logits, MLA
+and GQA decode attention (prep + attend)."""
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+TOL = 1e-2
+
+
+def _lib():
+    from sluice_amd import _lib
+
+    return _lib.load(), _lib.check
+
+
+def _st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _rel(a, b):
+    a = a.double().cpu()
+    b = b.double().cpu()
+    return float((a - b).norm() / max(b.norm(), 1e-30))
+
+
+def _rope(x, cos, sin):
+    d = x.shape[-1] // 2
+    x1, x2 = x[..., :d], x[..., d:]
+    return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1)
+
+
+def _rms(x, w, eps=1e-6):
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
+
+
+@pytest.mark.parametrize("rows,H,with_delta", [(8, 2048, True), (1, 7168, False), (12, 2048, True)])
+def test_add_rmsnorm(rows, H, with_delta):
+    from sluice_amd.decoder import add_rmsnorm
+
+    g = torch.Generator().manual_seed(rows + H)
+    x = torch.randn((rows, H), generator=g).bfloat16()
+    d = torch.randn((rows, H), generator=g).bfloat16() if with_delta else None
+    w = (1 + 0.1 * torch.randn(H, generator=g)).bfloat16()
+    xd = x.to(DEV)
+    out = add_rmsnorm(xd, None if d is None else d.to(DEV), w.to(DEV))
+    torch.cuda.synchronize()
+    xs = (x.float() + d.float()).bfloat16() if with_delta else x
+    assert torch.equal(xd.cpu(), xs)  # the residual stream is the bf16 sum, in place
+    ref = _rms(xs.float(), w.float())
+    assert _rel(out, ref) <= TOL
+
+
+def test_silu_mul():
+    from sluice_amd.decoder import silu_mul
+
+    g = torch.Generator().manual_seed(3)
+    gu = torch.randn((8, 2 * 2816), generator=g).bfloat16()
+    out = silu_mul(gu.to(DEV))
+    torch.cuda.synchronize()
+    gf, uf = gu.float()[:, :2816], gu.float()[:, 2816:]
+    assert _rel(out, gf * torch.sigmoid(gf) * uf) <= TOL
+
+
+@pytest.mark.parametrize("rows,H,E,bias", [(8, 2048, 64, True), (1, 2048, 128, False),
+                                           (12, 7168, 256, True)])
+def test_gate_logits(rows, H, E, bias):
+    lib, check = _lib()
+    g = torch.Generator().manual_seed(E + rows)
+    hn = torch.randn((rows, H), generator=g).bfloat16()
+    wg = (0.02 * torch.randn((E, H), generator=g)).bfloat16()
+    steps, brow = 5, 16
+    table = torch.randn((steps, brow, E), generator=g)
+    step = torch.tensor(7, dtype=torch.long)  # wraps to row 7 % 5 = 2
+    out = torch.empty((rows, E), dtype=torch.float32, device=DEV)
+    d = {k: v.to(DEV) for k, v in dict(hn=hn, wg=wg, table=table, step=step).items()}
+    check(lib.sluice_dec_gate_logits(d["hn"].data_ptr(), d["wg"].data_ptr(),
+                                     d["table"].data_ptr() if bias else None,
+                                     d["step"].data_ptr() if bias else None, steps if bias else 0,
+                                     brow if bias else 0, rows, H, E, out.data_ptr(), _st()),
+          "gate_logits")
+    torch.cuda.synchronize()
+    ref = hn.float() @ wg.float().T
+    if bias:
+        ref = ref + table[2, :rows]
+    assert torch.allclose(out.cpu(), ref, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("T,N,K", [(8, 3648, 2048), (1, 2048, 10944), (12, 5632, 2048),
+                                   (16, 160, 96)])
+def test_linear(T, N, K):
+    from sluice_amd.decoder import linear
+
+    g = torch.Generator().manual_seed(T * N + K)
+    x = torch.randn((T, K), generator=g).bfloat16()
+    w = (0.02 * torch.randn((N, K), generator=g)).bfloat16()
+    y = linear(x.to(DEV), w.to(DEV))
+    torch.cuda.synchronize()
+    assert _rel(y, x.float() @ w.float().T) <= TOL
+
+
+def _tables(L, d, theta):
+    inv = 1.0 / (theta ** (torch.arange(0, d, 2).float() / d))
+    ang = torch.arange(L).float()[:, None] * inv[None, :]
+    return ang.cos().contiguous(), ang.sin().contiguous()
+
+
+def test_mla_prep_and_attend():
+    lib, check = _lib()
+    c, nh, nope, rope, lora, vh, L = 4, 16, 128, 64, 512, 128, 64
+    g = torch.Generator().manual_seed(11)
+    nq = nh * (nope + rope)
+    qkva = torch.randn((c, nq + lora + rope), generator=g).bfloat16()
+    kv_norm = (1 + 0.1 * torch.randn(lora, generator=g)).bfloat16()
+    w_uk = (0.05 * torch.randn((nh, nope, lora), generator=g)).bfloat16()
+    w_uv = (0.05 * torch.randn((nh, lora, vh), generator=g)).bfloat16()
+    ckv = torch.randn((c, L, lora), generator=g).bfloat16()
+    kpe = torch.randn((c, L, rope), generator=g).bfloat16()
+    pos = torch.tensor([5, 0, 63, 31], dtype=torch.long)
+    cos_t, sin_t = _tables(L, rope, 1e4)
+    scale = (nope + rope) ** -0.5
+    d = {k: v.to(DEV) for k, v in dict(qkva=qkva, kv_norm=kv_norm, w_uk=w_uk, w_uv=w_uv,
+                                       ckv=ckv.clone(), kpe=kpe.clone(), pos=pos, cos=cos_t,
+                                       sin=sin_t).items()}
+    q_lat = torch.empty((c, nh, lora), dtype=torch.float32, device=DEV)
+    q_pe = torch.empty((c, nh, rope), dtype=torch.float32, device=DEV)
+    out = torch.empty((c, nh * vh), dtype=torch.bfloat16, device=DEV)
+    row = qkva.shape[1]
+    check(lib.sluice_dec_mla_prep(
+        d["qkva"].data_ptr(), row, d["qkva"].data_ptr() + nq * 2, row, d["kv_norm"].data_ptr(),
+        d["w_uk"].data_ptr(), d["cos"].data_ptr(), d["sin"].data_ptr(), d["pos"].data_ptr(), c, nh,
+        nope, rope, lora, L, 1e-6, q_lat.data_ptr(), q_pe.data_ptr(), d["ckv"].data_ptr(),
+        d["kpe"].data_ptr(), _st()), "mla_prep")
+    check(lib.sluice_dec_mla_attend(
+        q_lat.data_ptr(), q_pe.data_ptr(), d["ckv"].data_ptr(), d["kpe"].data_ptr(),
+        d["w_uv"].data_ptr(), d["pos"].data_ptr(), c, nh, rope, lora, vh, L, scale,
+        out.data_ptr(), _st()), "mla_attend")
+    torch.cuda.synchronize()
+    ck, kp = ckv.clone(), kpe.clone()
+    for t in range(c):
+        p = int(pos[t])
+        q = qkva[t, :nq].float().view(nh, nope + rope)
+        qn, qp = q[:, :nope], _rope(q[:, nope:], cos_t[p], sin_t[p])
+        ql = torch.bmm(qn[:, None, :], w_uk.float())[:, 0]
+        assert _rel(q_lat[t], ql) <= 1e-5 and _rel(q_pe[t], qp) <= 1e-5
+        kv = qkva[t, nq:].float()
+        ck[t, p] = _rms(kv[:lora], kv_norm.float()).bfloat16()
+        kp[t, p] = _rope(kv[lora:], cos_t[p], sin_t[p]).bfloat16()
+        assert _rel(d["ckv"][t, p], ck[t, p].float()) <= TOL
+        assert _rel(d["kpe"][t, p], kp[t, p].float()) <= TOL
+        cf, kf = d["ckv"][t, : p + 1].float().cpu(), d["kpe"][t, : p + 1].float().cpu()
+        s = (ql @ cf.T + qp @ kf.T) * scale
+        pr = torch.softmax(s, dim=-1)
+        o = torch.bmm((pr @ cf)[:, None, :], w_uv.float())[:, 0]
+        assert _rel(out[t].view(nh, vh), o) <= TOL, t
+    # rows other than pos[t] are untouched
+    mask = torch.ones((c, L), dtype=torch.bool)
+    mask[torch.arange(c), pos] = False
+    assert torch.equal(d["ckv"].cpu()[mask], ckv[mask])
+
+
+def test_gqa_prep_and_attend():
+    lib, check = _lib()
+    c, nh, kvh, hd, L = 3, 32, 4, 128, 48
+    g = torch.Generator().manual_seed(12)
+    qkv = torch.randn((c, (nh + 2 * kvh) * hd), generator=g).bfloat16()
+    q_norm = (1 + 0.1 * torch.randn(hd, generator=g)).bfloat16()
+    k_norm = (1 + 0.1 * torch.randn(hd, generator=g)).bfloat16()
+    k = torch.randn((c, kvh, L, hd), generator=g).bfloat16()
+    v = torch.randn((c, kvh, L, hd), generator=g).bfloat16()
+    pos = torch.tensor([7, 47, 0], dtype=torch.long)
+    cos_t, sin_t = _tables(L, hd, 1e6)
+    scale = hd ** -0.5
+    d = {kk: vv.to(DEV) for kk, vv in dict(qkv=qkv, qn=q_norm, kn=k_norm, k=k.clone(), v=v.clone(),
+                                           pos=pos, cos=cos_t, sin=sin_t).items()}
+    q = torch.empty((c, nh, hd), dtype=torch.float32, device=DEV)
+    out = torch.empty((c, nh * hd), dtype=torch.bfloat16, device=DEV)
+    check(lib.sluice_dec_gqa_prep(
+        d["qkv"].data_ptr(), d["qn"].data_ptr(), d["kn"].data_ptr(), d["cos"].data_ptr(),
+        d["sin"].data_ptr(), d["pos"].data_ptr(), c, nh, kvh, hd, L, 1e-6, q.data_ptr(),
+        d["k"].data_ptr(), d["v"].data_ptr(), _st()), "gqa_prep")
+    check(lib.sluice_dec_gqa_attend(
+        q.data_ptr(), d["k"].data_ptr(), d["v"].data_ptr(), d["pos"].data_ptr(), c, nh, kvh, hd, L,
+        scale, out.data_ptr(), _st()), "gqa_attend")
+    torch.cuda.synchronize()
+    for t in range(c):
+        p = int(pos[t])
+        x = qkv[t].float()
+        qh = x[: nh * hd].view(nh, hd)
+        kh = x[nh * hd: (nh + kvh) * hd].view(kvh, hd)
+        vh_ = x[(nh + kvh) * hd:].view(kvh, hd)
+        qr = _rope(_rms(qh, q_norm.float()), cos_t[p], sin_t[p])
+        kr = _rope(_rms(kh, k_norm.float()), cos_t[p], sin_t[p])
+        assert _rel(q[t], qr) <= 1e-5
+        assert _rel(d["k"][t, :, p], kr) <= TOL
+        assert torch.equal(d["v"][t, :, p].cpu(), vh_.bfloat16())
+        kc, vc = d["k"][t, :, : p + 1].float().cpu(), d["v"][t, :, : p + 1].float().cpu()
+        grp = nh // kvh
+        for h in range(nh):
+            s = (qr[h] @ kc[h // grp].T) * scale
+            o = torch.softmax(s, dim=-1) @ vc[h // grp]
+            assert _rel(out[t, h * hd:(h + 1) * hd], o) <= TOL, (t, h)
