@@ -159,22 +159,36 @@ def kernel_roofline(dec, c, recorded, reps=3):
         blocks = p[4: 4 + 18 * nb].reshape(nb, 18) if nb else np.zeros((0, 18), np.int64)
         U = len(set(blocks[:, 0].tolist()))
         pairs = int(blocks[:, 1].sum()) if nb else 0
-        b1.append(U * 2 * I * H * 2 + c * H * 2 + pairs * I * 2)
-        b2.append(U * H * I * 2 + pairs * I * 2 + pairs * H * 4)
+        if sp["fp8"]:  # e4m3fn bytes + fp32 128x128 block scales
+            b1.append(U * (2 * I * H + (2 * I // 128) * (H // 128) * 4) + c * H * 2
+                      + pairs * I * 2)
+            b2.append(U * (H * I + (H // 128) * (I // 128) * 4) + pairs * I * 2 + pairs * H * 4)
+        else:
+            b1.append(U * 2 * I * H * 2 + c * H * 2 + pairs * I * 2)
+            b2.append(U * H * I * 2 + pairs * I * 2 + pairs * H * 4)
         b3.append(c * k * H * 4 + c * H * 2)
         fl.append(2 * pairs * 2 * I * H)
-    if sp["fp8"]:
-        return None
     st = stream.cuda_stream
 
-    def g1(it):
-        lib.sluice_moe_gemm1_bf16(it["hn"].data_ptr(), it["m"].w13_weight.data_ptr(),
-                                  it["plan"].data_ptr(), c, H, I, k, it["act"].data_ptr(), st)
+    if sp["fp8"]:
+        def g1(it):
+            lib.sluice_moe_gemm1_fp8(it["hn"].data_ptr(), it["m"].w13_weight.data_ptr(),
+                                     it["m"].w13_weight_scale.data_ptr(), it["plan"].data_ptr(),
+                                     c, H, I, k, it["act"].data_ptr(), st)
 
-    def g2(it):
-        lib.sluice_moe_gemm2_bf16(it["act"].data_ptr(), it["m"].w2_weight.data_ptr(),
-                                  it["plan"].data_ptr(), it["tw"].data_ptr(), c, H, I, k,
-                                  it["part"].data_ptr(), st)
+        def g2(it):
+            lib.sluice_moe_gemm2_fp8(it["act"].data_ptr(), it["m"].w2_weight.data_ptr(),
+                                     it["m"].w2_weight_scale.data_ptr(), it["plan"].data_ptr(),
+                                     it["tw"].data_ptr(), c, H, I, k, it["part"].data_ptr(), st)
+    else:
+        def g1(it):
+            lib.sluice_moe_gemm1_bf16(it["hn"].data_ptr(), it["m"].w13_weight.data_ptr(),
+                                      it["plan"].data_ptr(), c, H, I, k, it["act"].data_ptr(), st)
+
+        def g2(it):
+            lib.sluice_moe_gemm2_bf16(it["act"].data_ptr(), it["m"].w2_weight.data_ptr(),
+                                      it["plan"].data_ptr(), it["tw"].data_ptr(), c, H, I, k,
+                                      it["part"].data_ptr(), st)
 
     def cb(it):
         lib.sluice_moe_combine(it["part"].data_ptr(), it["plan"].data_ptr(), c, k, H, 1.0, None,
@@ -194,9 +208,10 @@ def kernel_roofline(dec, c, recorded, reps=3):
         return {"kernel": name, "avg_us": us, "algorithmic_bytes": avg,
                 "achieved_GBs": avg / (us * 1e-6) / 1e9}
 
-    r1 = res("moe_gemm1_bf16_kernel", us1, b1)
+    kind = "fp8" if sp["fp8"] else "bf16"
+    r1 = res(f"moe_gemm1_kernel<{kind}>", us1, b1)
     r1["mfma_util_pct"] = 100.0 * float(np.mean(fl)) / (us1 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS
-    r2 = res("moe_gemm2_bf16_kernel", us2, b2)
+    r2 = res(f"moe_gemm2_kernel<{kind}>", us2, b2)
     r2["mfma_util_pct"] = 100.0 * float(np.mean(fl)) / (us2 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS
     return {"c": c, "launches": reps * len(items), "gemm1": r1, "gemm2": r2,
             "combine": res("moe_combine_kernel", us3, b3),

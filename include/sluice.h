@@ -178,7 +178,8 @@ int sluice_moe_align(const int32_t* topk_ids, int T, int k,
                      const int32_t* expert_map, int E, int S, int32_t* plan,
                      sluice_stream_t stream);
 
-/* The three compute stages of sluice_fused_experts_bf16, launchable one by
+/* The three compute stages of sluice_fused_experts_bf16 (and the fp8 gemms
+ * of sluice_fused_experts_fp8, with the same block-scale layout), launchable one by
  * one over a plan from sluice_moe_align (for per-kernel timing and tests):
  *   gemm1:   act[pair, I] (bf16) = silu(W13g[s]·x_t) * W13u[s]·x_t
  *   gemm2:   partial[pair, H] (fp32) = w[pair] * W2[s]·act[pair]
@@ -191,6 +192,12 @@ int sluice_moe_gemm2_bf16(const void* act, const void* w2,
                           const int32_t* plan, const float* topk_w, int T,
                           int H, int I, int k, float* partial,
                           sluice_stream_t stream);
+int sluice_moe_gemm1_fp8(const void* x, const void* w13, const float* w13_scale,
+                         const int32_t* plan, int T, int H, int I, int k, void* act,
+                         sluice_stream_t stream);
+int sluice_moe_gemm2_fp8(const void* act, const void* w2, const float* w2_scale,
+                         const int32_t* plan, const float* topk_w, int T, int H, int I,
+                         int k, float* partial, sluice_stream_t stream);
 int sluice_moe_combine(const float* partial, const int32_t* plan, int T, int k,
                        int H, float scale, const void* shared, void* out,
                        sluice_stream_t stream);

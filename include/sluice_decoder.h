@@ -36,6 +36,17 @@ int sluice_dec_add_rmsnorm(void* x, const void* delta, const void* w, void* out,
 int sluice_dec_linear(const void* x, const void* w, int T, int N, int K, void* y,
                       sluice_stream_t stream);
 
+/* The same with the SwiGLU activation fused into the input: y = act . w^T
+ * with act = silu(gu[:, :K]) * gu[:, K:] (gu [T, 2K], rounded to bf16 as
+ * the activation kernel rounds it). */
+int sluice_dec_linear_swiglu(const void* gu, const void* w, int T, int N, int K, void* y,
+                             sluice_stream_t stream);
+
+/* Greedy next token: out[t] (int64) = the first index of the largest value
+ * of x [T, N] bf16 (NaN never wins; an all-NaN row gives 0).  One launch
+ * with no memset, so it is safe inside a replayed hipGraph. */
+int sluice_dec_argmax(const void* x, int T, int N, int64_t* out, sluice_stream_t stream);
+
 /* out [rows, I] = bf16(silu(gu[:, :I]) * gu[:, I:]), gu [rows, 2I].  I % 4 == 0. */
 int sluice_dec_silu_mul(const void* gu, void* out, int rows, int I, sluice_stream_t stream);
 

@@ -60,6 +60,10 @@ SIGNATURES = {
     "sluice_moe_align": (c_int, [_P, c_int, c_int, _P, c_int, c_int, _P, _P]),
     "sluice_moe_gemm1_bf16": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, _P, _P]),
     "sluice_moe_gemm2_bf16": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, _P]),
+    "sluice_moe_gemm1_fp8": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, _P]),
+    "sluice_moe_gemm2_fp8": (
+        c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, _P]
+    ),
     "sluice_moe_combine": (c_int, [_P, _P, c_int, c_int, c_int, c_float, _P, _P, _P]),
     "sluice_layer_create": (c_int, [c_int, c_int, c_int, c_int, _P, _P, POINTER(c_void_p)]),
     "sluice_layer_destroy": (c_int, [_P]),
@@ -85,7 +89,9 @@ SIGNATURES = {
     # include/sluice_decoder.h
     "sluice_dec_add_rmsnorm": (c_int, [_P, _P, _P, _P, c_int, c_int, c_float, _P]),
     "sluice_dec_silu_mul": (c_int, [_P, _P, c_int, c_int, _P]),
+    "sluice_dec_argmax": (c_int, [_P, c_int, c_int, _P, _P]),
     "sluice_dec_linear": (c_int, [_P, _P, c_int, c_int, c_int, _P, _P]),
+    "sluice_dec_linear_swiglu": (c_int, [_P, _P, c_int, c_int, c_int, _P, _P]),
     "sluice_dec_gate_logits": (
         c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, _P]
     ),

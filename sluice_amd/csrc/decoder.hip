@@ -534,43 +534,65 @@ __global__ __launch_bounds__(kT) void gqa_attend_kernel(
 // ---------------------------------------------------------------------------
 // Skinny GEMM for decode: y [T, N] = x [T, K] . W [N, K]^T, T <= 16.  A weight
 // stream like the expert product: a workgroup takes 16 rows of W (MFMA M)
-// against all T tokens (MFMA N); 4 waves split K and reduce in LDS; each lane
-// keeps 8 chunks of 16 bytes in flight.
+// against all T tokens (MFMA N); its KS waves split K and reduce in LDS; each
+// lane keeps 8 chunks of 16 bytes in flight.  KS grows as N shrinks, so a
+// small matrix still puts enough waves in flight to cover HBM latency.
+// SWIGLU: x is the activation silu(g) * u of a [T, 2K] gate|up input,
+// computed as the fragments are loaded.
 // ---------------------------------------------------------------------------
 constexpr int kLinD = 8;
 
-__global__ __launch_bounds__(kT) void linear_kernel(const uint16_t* __restrict__ x,
-                                                    const uint16_t* __restrict__ w, int T, int N,
-                                                    int K, uint16_t* __restrict__ y) {
-  __shared__ f32x4_t red[kT / 64][64];
+template <int KS, bool SWIGLU>
+__global__ __launch_bounds__(64 * KS) void linear_kernel(const uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ w, int T,
+                                                         int N, int K, uint16_t* __restrict__ y) {
+  __shared__ f32x4_t red[KS][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kg = lane >> 4;
   const int nchunk = K / 32;
-  const int c0 = wave * nchunk / (kT / 64), c1 = (wave + 1) * nchunk / (kT / 64);
+  const int c0 = wave * nchunk / KS, c1 = (wave + 1) * nchunk / KS;
   const int n = c1 - c0;
   const bool hx = col < T;
+  const int xstride = SWIGLU ? 2 * K : K;
   for (int tile = blockIdx.x; tile < N / 16; tile += gridDim.x) {
     const uint16_t* wr = w + ((size_t)tile * 16 + col) * K + kg * 8 + c0 * 32;
-    const uint16_t* xr = x + (size_t)(hx ? col : 0) * K + kg * 8 + c0 * 32;
+    const uint16_t* xr = x + (size_t)(hx ? col : 0) * xstride + kg * 8 + c0 * 32;
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    u32x4_t rw[kLinD], rx[kLinD];
+    u32x4_t rw[kLinD], rx[kLinD], ru[SWIGLU ? kLinD : 1];
 #pragma unroll
     for (int d = 0; d < kLinD; ++d) {
       rx[d] = u32x4_t{0u, 0u, 0u, 0u};
+      if (SWIGLU) ru[d] = rx[d];
       if (d < n) {
         rw[d] = ldg16_stream(wr + d * 32);
-        if (hx) rx[d] = ldg16(xr + d * 32);
+        if (hx) {
+          rx[d] = ldg16(xr + d * 32);
+          if (SWIGLU) ru[d] = ldg16(xr + K + d * 32);
+        }
       }
     }
     for (int base = 0; base < n; base += kLinD) {
 #pragma unroll
       for (int d = 0; d < kLinD; ++d) {
         if (base + d < n) {
-          acc = mfma16x16x32_bf16(rw[d], rx[d], acc);
+          u32x4_t xv = rx[d];
+          if (SWIGLU) {
+            float g[8], u[8];
+            unpack8(rx[d], g);
+            unpack8(ru[d], u);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              xv[j] = pack2(g[2 * j] / (1.0f + expf(-g[2 * j])) * u[2 * j],
+                            g[2 * j + 1] / (1.0f + expf(-g[2 * j + 1])) * u[2 * j + 1]);
+          }
+          acc = mfma16x16x32_bf16(rw[d], xv, acc);
           const int nx = base + kLinD + d;
           if (nx < n) {
             rw[d] = ldg16_stream(wr + nx * 32);
-            if (hx) rx[d] = ldg16(xr + nx * 32);
+            if (hx) {
+              rx[d] = ldg16(xr + nx * 32);
+              if (SWIGLU) ru[d] = ldg16(xr + K + nx * 32);
+            }
           }
         }
       }
@@ -580,7 +602,7 @@ __global__ __launch_bounds__(kT) void linear_kernel(const uint16_t* __restrict__
     if (wave == 0 && hx) {
       f32x4_t s = red[0][lane];
 #pragma unroll
-      for (int v = 1; v < kT / 64; ++v) s += red[v][lane];
+      for (int v = 1; v < KS; ++v) s += red[v][lane];
       *reinterpret_cast<u32x2_t*>(y + (size_t)col * N + tile * 16 + kg * 4) =
           u32x2_t{pack2(s[0], s[1]), pack2(s[2], s[3])};
     }
@@ -588,7 +610,83 @@ __global__ __launch_bounds__(kT) void linear_kernel(const uint16_t* __restrict__
   }
 }
 
+template <bool SWIGLU>
+int launch_linear(const void* x, const void* w, int T, int N, int K, void* y, hipStream_t st) {
+  const int tiles = N / 16;
+  const int grid = tiles < 4096 ? tiles : 4096;
+  const int nchunk = K / 32;
+  // (the fused-activation variant needs more registers: at most 8 waves)
+  if (tiles >= 1024 || nchunk < 32)
+    hipLaunchKernelGGL((linear_kernel<4, SWIGLU>), dim3(grid), dim3(256), 0, st,
+                       (const uint16_t*)x, (const uint16_t*)w, T, N, K, (uint16_t*)y);
+  else if (tiles >= 256 || nchunk < 64)
+    hipLaunchKernelGGL((linear_kernel<8, SWIGLU>), dim3(grid), dim3(512), 0, st,
+                       (const uint16_t*)x, (const uint16_t*)w, T, N, K, (uint16_t*)y);
+  else if (SWIGLU)
+    hipLaunchKernelGGL((linear_kernel<8, SWIGLU>), dim3(grid), dim3(512), 0, st,
+                       (const uint16_t*)x, (const uint16_t*)w, T, N, K, (uint16_t*)y);
+  else
+    hipLaunchKernelGGL((linear_kernel<16, SWIGLU>), dim3(grid), dim3(1024), 0, st,
+                       (const uint16_t*)x, (const uint16_t*)w, T, N, K, (uint16_t*)y);
+  return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Greedy next token: out[t] = argmax_n x[t, n] (first index on ties), one
+// workgroup per row.  A graph-safe replacement for a library reduction that
+// would record a memset of its cross-block semaphores.
+// ---------------------------------------------------------------------------
+constexpr int kArg = 1024;
+
+__global__ __launch_bounds__(kArg) void argmax_kernel(const uint16_t* __restrict__ x, int N,
+                                                      int64_t* __restrict__ out) {
+  __shared__ float bv[kArg / 64];
+  __shared__ int bi[kArg / 64];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint16_t* row = x + (size_t)t * N;
+  float best = -INFINITY;
+  int besti = N;  // sentinel above every index
+  for (int i = tid; i < N; i += kArg) {
+    const float v = bf(row[i]);
+    if (v > best || (besti == N && v == best)) {
+      best = v;
+      besti = i;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(best, off, SLUICE_WAVE);
+    const int oi = __shfl_xor(besti, off, SLUICE_WAVE);
+    if (ov > best || (ov == best && oi < besti)) {
+      best = ov;
+      besti = oi;
+    }
+  }
+  if (lane == 0) {
+    bv[wave] = best;
+    bi[wave] = besti;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kArg / 64; ++w)
+      if (bv[w] > best || (bv[w] == best && bi[w] < besti)) {
+        best = bv[w];
+        besti = bi[w];
+      }
+    out[t] = besti < N ? besti : 0;
+  }
+}
+
 }  // namespace
+
+extern "C" int sluice_dec_argmax(const void* x, int T, int N, int64_t* out,
+                                 sluice_stream_t stream) {
+  if (T < 0 || N <= 0 || x == nullptr || out == nullptr) return SLUICE_E_INVAL;
+  if (T == 0) return SLUICE_OK;
+  hipLaunchKernelGGL(argmax_kernel, dim3(T), dim3(kArg), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, N, out);
+  return (int)hipGetLastError();
+}
 
 extern "C" int sluice_dec_linear(const void* x, const void* w, int T, int N, int K, void* y,
                                  sluice_stream_t stream) {
@@ -597,11 +695,17 @@ extern "C" int sluice_dec_linear(const void* x, const void* w, int T, int N, int
     return SLUICE_E_INVAL;
   if (((uintptr_t)x | (uintptr_t)w) & 15 || (uintptr_t)y & 7) return SLUICE_E_INVAL;
   if (T == 0) return SLUICE_OK;
-  const int tiles = N / 16;
-  const int grid = tiles < 4096 ? tiles : 4096;
-  hipLaunchKernelGGL(linear_kernel, dim3(grid), dim3(kT), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, (const uint16_t*)w, T, N, K, (uint16_t*)y);
-  return (int)hipGetLastError();
+  return launch_linear<false>(x, w, T, N, K, y, (hipStream_t)stream);
+}
+
+extern "C" int sluice_dec_linear_swiglu(const void* gu, const void* w, int T, int N, int K,
+                                        void* y, sluice_stream_t stream) {
+  if (T < 0 || T > 16 || N <= 0 || N % 16 != 0 || K <= 0 || K % 32 != 0 || gu == nullptr ||
+      w == nullptr || y == nullptr)
+    return SLUICE_E_INVAL;
+  if (((uintptr_t)gu | (uintptr_t)w) & 15 || (uintptr_t)y & 7) return SLUICE_E_INVAL;
+  if (T == 0) return SLUICE_OK;
+  return launch_linear<true>(gu, w, T, N, K, y, (hipStream_t)stream);
 }
 
 extern "C" int sluice_dec_add_rmsnorm(void* x, const void* delta, const void* w, void* out,

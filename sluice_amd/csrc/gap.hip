@@ -165,15 +165,18 @@ __device__ int wait_eq(const int32_t* p, int32_t want, const int32_t* abort_flag
   }
 }
 
+// dev_state: [0] last stamp issued, [1] 1 once the host has installed a
+// standing map (device-side copy of mb->standing, which never goes back to
+// 0, so later gaps skip that PCIe read).
 __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     const int32_t* __restrict__ ids, int n, int32_t* __restrict__ map,
-    const int32_t* __restrict__ local_of, int E, GapMailbox* mb, int32_t* stamp_ctr,
+    const int32_t* __restrict__ local_of, int E, GapMailbox* mb, int32_t* dev_state,
     const int32_t* abort_flag, long long timeout_ticks, const u32x4_t* __restrict__ copy_src,
     u32x4_t* __restrict__ copy_dst, int copy_vecs) {
   __shared__ int present[SLUICE_MAX_EXPERTS];
   __shared__ int wcount[kWaves];
   __shared__ int wmiss[kWaves];
-  __shared__ int s_stamp, s_status, s_waits;
+  __shared__ int s_stamp, s_status, s_waits, s_standing;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -181,10 +184,11 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
   if (tid == 0) {
     // The host must have copied out this layer's previous record before it
     // is overwritten (it normally has, long ago).
-    const int32_t prev = *stamp_ctr;
+    const int32_t prev = dev_state[0];
     int32_t s = prev + 1;
     if (s <= 0) s = 1;
     s_stamp = s;
+    s_standing = dev_state[1];
     s_status = wait_eq(&mb->ack_stamp, prev, abort_flag, timeout_ticks);
   }
   for (int e = tid; e < E; e += kLookupThreads) present[e] = 0;
@@ -217,19 +221,27 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
       }
       __syncthreads();
     }
-    __threadfence_system();
   }
+  // The op's fresh copy of hidden_states does not depend on the host; its
+  // stores overlap the PCIe writes of the record.
+  for (int i = tid; i < copy_vecs; i += kLookupThreads) copy_dst[i] = copy_src[i];
+  if (can_post) __threadfence_system();  // this thread's record entries are visible
   __syncthreads();
   if (tid == 0) {
     s_waits = 0;
     if (can_post) {
       const int32_t s = s_stamp;
-      const int waits = (miss > 0 || ld_sys(&mb->standing) == 0) ? 1 : 0;
+      if (!s_standing && ld_sys(&mb->standing) != 0) {
+        s_standing = 1;
+        dev_state[1] = 1;
+      }
+      const int waits = (miss > 0 || !s_standing) ? 1 : 0;
       mb->n_uniq = base;
       mb->n_miss = miss;
       mb->waits = waits;
-      *stamp_ctr = s;
-      __threadfence_system();
+      dev_state[0] = s;
+      // release: the header above and (via the fences before the barrier)
+      // every thread's entries are visible before the stamp
       __hip_atomic_store(&mb->req_stamp, s, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
       s_waits = waits;
     } else {
@@ -237,9 +249,6 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     }
   }
   __syncthreads();
-  // The op's fresh copy of hidden_states does not depend on the host: it is
-  // written while the host works on the record.
-  for (int i = tid; i < copy_vecs; i += kLookupThreads) copy_dst[i] = copy_src[i];
   if (!s_waits) return;
   if (tid == 0) {
     const int st = wait_eq(&mb->resp_stamp, s_stamp, abort_flag, timeout_ticks);
@@ -334,7 +343,7 @@ struct sluice_layer {
   int device = -1;
   GapMailbox* mb = nullptr;      // host pointer
   GapMailbox* mb_dev = nullptr;  // device view of the same memory
-  int32_t* dev_block = nullptr;  // [E] local_of, then the stamp counter
+  int32_t* dev_block = nullptr;  // [E] local_of, then last stamp, standing seen
   int32_t host_stamp = 0;        // last record copied out
   std::atomic<int32_t> done_stamp{0};  // last record fully served
   int64_t bytes = 0;
@@ -361,10 +370,11 @@ int layer_device_init(sluice_layer* L) {
   SLUICE_HIP_CHECK(hipHostGetDevicePointer(&dp, p, 0));
   L->mb_dev = static_cast<GapMailbox*>(dp);
   const int E = L->c.E;
-  SLUICE_HIP_CHECK(hipMalloc((void**)&L->dev_block, sizeof(int32_t) * (E + 1)));
+  SLUICE_HIP_CHECK(hipMalloc((void**)&L->dev_block, sizeof(int32_t) * (E + 2)));
   std::vector<int32_t> blk(L->c.local_of.begin(), L->c.local_of.end());
-  blk.push_back(0);  // stamp counter
-  SLUICE_HIP_CHECK(hipMemcpy(L->dev_block, blk.data(), sizeof(int32_t) * (E + 1),
+  blk.push_back(0);  // last stamp issued
+  blk.push_back(0);  // standing map seen
+  SLUICE_HIP_CHECK(hipMemcpy(L->dev_block, blk.data(), sizeof(int32_t) * (E + 2),
                              hipMemcpyHostToDevice));
   return SLUICE_OK;
 }

@@ -919,6 +919,31 @@ extern "C" int sluice_moe_gemm2_bf16(const void* act, const void* w2, const int3
   return (int)hipGetLastError();
 }
 
+extern "C" int sluice_moe_gemm1_fp8(const void* x, const void* w13, const float* w13_scale,
+                                    const int32_t* plan, int T, int H, int I, int k, void* act,
+                                    sluice_stream_t stream) {
+  if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % kFp8Blk || I % kFp8Blk ||
+      (long)T * k > SLUICE_MAX_PAIRS || !x || !w13 || !w13_scale || !plan || !act)
+    return SLUICE_E_INVAL;
+  Bf16W W{(const uint8_t*)w13, nullptr, w13_scale, nullptr};
+  hipLaunchKernelGGL(moe_gemm1_kernel<true>, dim3(grid_for(T * k, I / 16)), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const uint16_t*)x, W, plan, H, I, k, (uint16_t*)act);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sluice_moe_gemm2_fp8(const void* act, const void* w2, const float* w2_scale,
+                                    const int32_t* plan, const float* topk_w, int T, int H, int I,
+                                    int k, float* partial, sluice_stream_t stream) {
+  if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % kFp8Blk || I % kFp8Blk ||
+      (long)T * k > SLUICE_MAX_PAIRS || !act || !w2 || !w2_scale || !plan || !topk_w || !partial)
+    return SLUICE_E_INVAL;
+  Bf16W W{nullptr, (const uint8_t*)w2, nullptr, w2_scale};
+  hipLaunchKernelGGL(moe_gemm2_kernel<true>, dim3(grid_for(T * k, H / (16 * kG2T))),
+                     dim3(kThreads), 0, (hipStream_t)stream, (const uint16_t*)act, W, plan, topk_w,
+                     H, I, partial);
+  return (int)hipGetLastError();
+}
+
 extern "C" int sluice_moe_combine(const float* partial, const int32_t* plan, int T, int k, int H,
                                   float scale, const void* shared, void* out,
                                   sluice_stream_t stream) {

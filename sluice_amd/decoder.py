@@ -253,6 +253,28 @@ def linear(x, w):
     return y
 
 
+def linear_swiglu(gu, w):
+    """y = (silu(gu[:, :K]) * gu[:, K:]) . w^T in one kernel (T <= 16)."""
+    lib, check = _k()
+    T, K2 = gu.shape
+    N = w.shape[0]
+    if T > 16:
+        raise ValueError(f"decode linear supports at most 16 rows, got {T}")
+    y = torch.empty((T, N), dtype=gu.dtype, device=gu.device)
+    check(lib.sluice_dec_linear_swiglu(gu.data_ptr(), w.data_ptr(), T, N, K2 // 2, y.data_ptr(),
+                                       _stream(gu)), "sluice_dec_linear_swiglu")
+    return y
+
+
+def argmax_rows(x, out):
+    """out[t] = argmax x[t] (int64, first index on ties) without library
+    reductions, which record memsets that replayed graphs do not honour."""
+    lib, check = _k()
+    check(lib.sluice_dec_argmax(x.data_ptr(), x.shape[0], x.shape[1], out.data_ptr(), _stream(x)),
+          "sluice_dec_argmax")
+    return out
+
+
 def silu_mul(gu):
     lib, check = _k()
     rows, two_i = gu.shape
@@ -357,7 +379,8 @@ class _GQA(nn.Module):
 
 
 class _DenseMLP(nn.Module):
-    """SwiGLU MLP: gate/up GEMM, one activation kernel, down GEMM."""
+    """SwiGLU MLP: gate/up GEMM, then the down GEMM with the activation fused
+    into its input loads."""
 
     def __init__(self, H, I, dev, gen):
         super().__init__()
@@ -366,7 +389,7 @@ class _DenseMLP(nn.Module):
         self.I = I
 
     def forward(self, x):
-        return linear(silu_mul(linear(x, self.gate_up)), self.down)
+        return linear_swiglu(linear(x, self.gate_up), self.down)
 
 
 def _expert_store(sp, gen_seed, dev, fp8):
@@ -626,7 +649,7 @@ class SyntheticDecoder:
             return i
         hf = add_rmsnorm(io["x"], io["delta"], self.final_norm)
         if self.has_attn:
-            st.tokens.copy_(torch.argmax(linear(hf, self.lm_head), dim=-1))
+            argmax_rows(linear(hf, self.lm_head), st.tokens)
             st.pos.add_(1)
         else:
             st.x.copy_(hf)

@@ -104,6 +104,56 @@ def test_linear(T, N, K):
     assert _rel(y, x.float() @ w.float().T) <= TOL
 
 
+@pytest.mark.parametrize("T,N,K", [(8, 2048, 2816), (1, 2048, 10944), (12, 7168, 2048)])
+def test_linear_swiglu(T, N, K):
+    from sluice_amd.decoder import linear_swiglu
+
+    g = torch.Generator().manual_seed(T + N + K)
+    gu = torch.randn((T, 2 * K), generator=g).bfloat16()
+    w = (0.02 * torch.randn((N, K), generator=g)).bfloat16()
+    y = linear_swiglu(gu.to(DEV), w.to(DEV))
+    torch.cuda.synchronize()
+    gf, uf = gu.float()[:, :K], gu.float()[:, K:]
+    assert _rel(y, (gf * torch.sigmoid(gf) * uf) @ w.float().T) <= TOL
+
+
+@pytest.mark.parametrize("T,N", [(1, 151936), (8, 102400), (3, 1000)])
+def test_argmax(T, N):
+    from sluice_amd.decoder import argmax_rows
+
+    g = torch.Generator().manual_seed(N + T)
+    x = torch.randn((T, N), generator=g).bfloat16()
+    x[0, N // 3] = 50.0  # a clear winner
+    x[-1, 7] = x[-1, N - 1] = 60.0  # a tie: the first index wins
+    out = argmax_rows(x.to(DEV), torch.zeros(T, dtype=torch.long, device=DEV))
+    torch.cuda.synchronize()
+    ref = torch.argmax(x.float(), dim=-1)
+    assert torch.equal(out.cpu(), ref)
+    assert int(out[-1]) == 7
+
+
+def test_argmax_replays_in_a_graph():
+    """Captured once, replayed several times with new inputs in between: each
+    replay's result equals the eager one."""
+    from sluice_amd.decoder import argmax_rows
+
+    x = torch.zeros((1, 151936), dtype=torch.bfloat16, device=DEV)
+    out = torch.zeros(1, dtype=torch.long, device=DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        argmax_rows(x, out)
+    torch.cuda.current_stream().wait_stream(s)
+    for i, pos in enumerate([5, 151935, 77777, 0, 123456]):
+        x.zero_()
+        x[0, pos] = 1.0 + i
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(out[0]) == pos
+
+
 def _tables(L, d, theta):
     inv = 1.0 / (theta ** (torch.arange(0, d, 2).float() / d))
     ang = torch.arange(L).float()[:, None] * inv[None, :]
