@@ -166,12 +166,32 @@ __global__ __launch_bounds__(kThreads) void moe_align_kernel(
 
 typedef f32x4_t RedBuf[kKS][2][64];
 
+// Device-coherent (sc1) 16-byte load / stores: the fused kernel hands act
+// rows and fp32 partials between workgroups on different XCDs through these
+// instead of writing back / invalidating whole L2 caches.
+__device__ __forceinline__ u32x4_t ld16_coh(const void* p) {
+  const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+  const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return u32x4_t{(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
+}
+__device__ __forceinline__ void st8_coh(void* p, uint32_t lo, uint32_t hi) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), (uint64_t)lo | ((uint64_t)hi << 32),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool COH>
+__device__ __forceinline__ u32x4_t ld_act(const void* p) {
+  if (COH) return ld16_coh(p);
+  return ldg16(p);
+}
+
 __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
   return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
 }
 
 // Wave 0 reduces the 4 K-split partial accumulators and writes
 // act[pair, tile*16 + kg*4 .. +4] = bf16(silu(g) * u).
+template <bool COH>
 __device__ __forceinline__ void g1_epilogue(RedBuf& red, int pair, int tile, int I,
                                             uint16_t* __restrict__ act) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kg = lane >> 4;
@@ -186,13 +206,19 @@ __device__ __forceinline__ void g1_epilogue(RedBuf& red, int pair, int tile, int
     float o[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) o[r] = g[r] / (1.0f + expf(-g[r])) * u[r];
-    *reinterpret_cast<u32x2_t*>(act + (size_t)pair * I + tile * 16 + kg * 4) =
-        u32x2_t{pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
+    uint16_t* dst = act + (size_t)pair * I + tile * 16 + kg * 4;
+    if (COH) {
+      st8_coh(dst, pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3]));
+      __builtin_amdgcn_s_waitcnt(0);  // written through before the tile is counted
+    } else {
+      *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
+    }
   }
   __syncthreads();
 }
 
 // Wave 0 reduces and writes partial[pair, tile2*32 + t*16 + kg*4 .. +4] = w * sum.
+template <bool COH>
 __device__ __forceinline__ void g2_epilogue(RedBuf& red, int pair, int tile2, int H, float wv,
                                             float* __restrict__ partial) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kg = lane >> 4;
@@ -203,9 +229,15 @@ __device__ __forceinline__ void g2_epilogue(RedBuf& red, int pair, int tile2, in
       f32x4_t s = red[0][t][lane];
 #pragma unroll
       for (int w = 1; w < kKS; ++w) s += red[w][t][lane];
-      *reinterpret_cast<f32x4_t*>(partial + (size_t)pair * H + (tile2 * kG2T + t) * 16 +
-                                  kg * 4) = f32x4_t{wv * s[0], wv * s[1], wv * s[2], wv * s[3]};
+      float* dst = partial + (size_t)pair * H + (tile2 * kG2T + t) * 16 + kg * 4;
+      if (COH) {
+        st8_coh(dst, __float_as_uint(wv * s[0]), __float_as_uint(wv * s[1]));
+        st8_coh(dst + 2, __float_as_uint(wv * s[2]), __float_as_uint(wv * s[3]));
+      } else {
+        *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{wv * s[0], wv * s[1], wv * s[2], wv * s[3]};
+      }
     }
+    if (COH) __builtin_amdgcn_s_waitcnt(0);
   }
   __syncthreads();
 }
@@ -217,6 +249,7 @@ __device__ __forceinline__ void g2_epilogue(RedBuf& red, int pair, int tile2, in
 // per lane each) in flight: chunk c + kG1D is loaded as soon as chunk c has
 // been consumed.
 // ---------------------------------------------------------------------------
+template <bool COH>
 __device__ __forceinline__ void g1_item_bf16(const uint16_t* __restrict__ x,
                                              const uint16_t* __restrict__ w13, int slot, int pair,
                                              int tile, int H, int I, int k,
@@ -259,12 +292,13 @@ __device__ __forceinline__ void g1_item_bf16(const uint16_t* __restrict__ x,
   }
   red[wave][0][lane] = ag;
   red[wave][1][lane] = au;
-  g1_epilogue(red, pair, tile, I, act);
+  g1_epilogue<COH>(red, pair, tile, I, act);
 }
 
 // gemm2 item, bf16 weights: hidden rows tile2*32..+32 of `slot` against
 // the block's act rows (the act fragment is loaded once per K chunk and
 // feeds both 16-row tiles).
+template <bool COH>
 __device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act,
                                              const uint16_t* __restrict__ w2, int slot, int pair,
                                              int tile2, int H, int I,
@@ -289,7 +323,7 @@ __device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act,
     if (d < n) {
 #pragma unroll
       for (int t = 0; t < kG2T; ++t) ra[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + d * 32);
-      if (hx) rb[d] = ldg16(ar + d * 32);
+      if (hx) rb[d] = ld_act<COH>(ar + d * 32);
     }
   }
   for (int base = 0; base < n; base += kG2D) {
@@ -302,14 +336,14 @@ __device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act,
         if (nx < n) {
 #pragma unroll
           for (int t = 0; t < kG2T; ++t) ra[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + nx * 32);
-          if (hx) rb[d] = ldg16(ar + nx * 32);
+          if (hx) rb[d] = ld_act<COH>(ar + nx * 32);
         }
       }
     }
   }
 #pragma unroll
   for (int t = 0; t < kG2T; ++t) red[wave][t][lane] = acc[t];
-  g2_epilogue(red, pair, tile2, H, hx ? topk_w[pair] : 0.f, partial);
+  g2_epilogue<COH>(red, pair, tile2, H, hx ? topk_w[pair] : 0.f, partial);
 }
 
 // ---------------------------------------------------------------------------
@@ -344,6 +378,7 @@ __device__ __forceinline__ void fp8x16_to_bf16(u32x4_t q, u32x4_t& lo, u32x4_t& 
 
 // gemm1 item, fp8 weights.  Wave w owns 64-wide K chunks [c0, c1), an even
 // split of 128-wide scale blocks.
+template <bool COH>
 __device__ __forceinline__ void g1_item_fp8(const uint16_t* __restrict__ x,
                                             const uint8_t* __restrict__ w13,
                                             const float* __restrict__ w13_scale, int slot,
@@ -408,9 +443,10 @@ __device__ __forceinline__ void g1_item_fp8(const uint16_t* __restrict__ x,
   }
   red[wave][0][lane] = ag;
   red[wave][1][lane] = au;
-  g1_epilogue(red, pair, tile, I, act);
+  g1_epilogue<COH>(red, pair, tile, I, act);
 }
 
+template <bool COH>
 __device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act,
                                             const uint8_t* __restrict__ w2,
                                             const float* __restrict__ w2_scale, int slot,
@@ -438,8 +474,8 @@ __device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act,
 #pragma unroll
       for (int t = 0; t < kG2T; ++t) q[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + d * 64);
       if (hx) {
-        b0[d] = ldg16(ar + d * 64);
-        b1[d] = ldg16(ar + d * 64 + 8);
+        b0[d] = ld_act<COH>(ar + d * 64);
+        b1[d] = ld_act<COH>(ar + d * 64 + 8);
       }
     }
   }
@@ -460,8 +496,8 @@ __device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act,
 #pragma unroll
           for (int t = 0; t < kG2T; ++t) q[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + nx * 64);
           if (hx) {
-            b0[d] = ldg16(ar + nx * 64);
-            b1[d] = ldg16(ar + nx * 64 + 8);
+            b0[d] = ld_act<COH>(ar + nx * 64);
+            b1[d] = ld_act<COH>(ar + nx * 64 + 8);
           }
         }
         if (c & 1) {
@@ -477,7 +513,7 @@ __device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act,
   }
 #pragma unroll
   for (int t = 0; t < kG2T; ++t) red[wave][t][lane] = acc[t];
-  g2_epilogue(red, pair, tile2, H, hx ? topk_w[pair] : 0.f, partial);
+  g2_epilogue<COH>(red, pair, tile2, H, hx ? topk_w[pair] : 0.f, partial);
 }
 
 // ---------------------------------------------------------------------------
@@ -490,24 +526,24 @@ struct Bf16W {
   const float* s2;
 };
 
-template <bool FP8>
+template <bool FP8, bool COH = false>
 __device__ __forceinline__ void run_g1(const uint16_t* x, const Bf16W& W, int slot, int pair,
                                        int tile, int H, int I, int k, uint16_t* act,
                                        RedBuf& red) {
   if (FP8)
-    g1_item_fp8(x, W.w13, W.s13, slot, pair, tile, H, I, k, act, red);
+    g1_item_fp8<COH>(x, W.w13, W.s13, slot, pair, tile, H, I, k, act, red);
   else
-    g1_item_bf16(x, (const uint16_t*)W.w13, slot, pair, tile, H, I, k, act, red);
+    g1_item_bf16<COH>(x, (const uint16_t*)W.w13, slot, pair, tile, H, I, k, act, red);
 }
 
-template <bool FP8>
+template <bool FP8, bool COH = false>
 __device__ __forceinline__ void run_g2(const uint16_t* act, const Bf16W& W, int slot, int pair,
                                        int tile2, int H, int I, const float* tw, float* partial,
                                        RedBuf& red) {
   if (FP8)
-    g2_item_fp8(act, W.w2, W.s2, slot, pair, tile2, H, I, tw, partial, red);
+    g2_item_fp8<COH>(act, W.w2, W.s2, slot, pair, tile2, H, I, tw, partial, red);
   else
-    g2_item_bf16(act, (const uint16_t*)W.w2, slot, pair, tile2, H, I, tw, partial, red);
+    g2_item_bf16<COH>(act, (const uint16_t*)W.w2, slot, pair, tile2, H, I, tw, partial, red);
 }
 
 template <bool FP8>
@@ -549,6 +585,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_kernel(const uint16_t* __r
 
 // out[t, h] = bf16(scale * sum_j valid ? partial[t*k+j, h] : 0 + shared[t, h]),
 // j ascending, for 4 consecutive columns at h.
+template <bool COH = false>
 __device__ __forceinline__ void combine4(const float* __restrict__ partial,
                                          const int32_t* __restrict__ valid, int t, int k, int H,
                                          int h, float scale, const uint16_t* __restrict__ shared,
@@ -556,7 +593,11 @@ __device__ __forceinline__ void combine4(const float* __restrict__ partial,
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < k; ++j) {
     const int p = t * k + j;
-    if (valid[p]) acc += *reinterpret_cast<const f32x4_t*>(partial + (size_t)p * H + h);
+    if (valid[p]) {
+      const float* src = partial + (size_t)p * H + h;
+      acc += COH ? __builtin_bit_cast(f32x4_t, ld16_coh(src))
+                 : *reinterpret_cast<const f32x4_t*>(src);
+    }
   }
   float o[4];
 #pragma unroll
@@ -590,13 +631,6 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
 // atomics only, so no global "all done" count is needed and no address is
 // hit by every workgroup.
 constexpr int kCtlInts = 32;
-
-__device__ __forceinline__ void fence_release_agent() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-}
-__device__ __forceinline__ void fence_acquire_agent() {
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-}
 
 // Grid-stride over the items (gemm1 items first), with every workgroup of
 // the grid resident at once (the host sizes the grid from the kernel's
@@ -637,9 +671,9 @@ __global__ __launch_bounds__(kThreads) void moe_fused_kernel(
       const int b = item / n1t, tile = item - b * n1t;
       const int32_t* blk = s_blocks + b * kBlockInts;
       const int pair = col < blk[1] ? blk[2 + col] : -1;
-      run_g1<FP8>(x, W, blk[0], pair, tile, H, I, k, act, red);
-      fence_release_agent();
-      __syncthreads();
+      run_g1<FP8, true>(x, W, blk[0], pair, tile, H, I, k, act, red);
+      // the act rows went out with device-coherent stores, completed before
+      // the epilogue's barrier
       if (tid == 0) atomicAdd(&blk_done[b], 1);
       continue;
     }
@@ -647,7 +681,7 @@ __global__ __launch_bounds__(kThreads) void moe_fused_kernel(
     const int b = j / n2t, tile2 = j - b * n2t;
     if (tid == 0) {
       const long long t0 = wall_clock64();
-      while (__hip_atomic_load(&blk_done[b], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < n1t) {
+      while (__hip_atomic_load(&blk_done[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < n1t) {
         if (wall_clock64() - t0 > timeout_ticks) {
           atomicExch(&ctl[0], 1);
           break;
@@ -656,12 +690,10 @@ __global__ __launch_bounds__(kThreads) void moe_fused_kernel(
       }
     }
     __syncthreads();
-    fence_acquire_agent();
+    // act is read with device-coherent loads after the counter was seen
     const int32_t* blk = s_blocks + b * kBlockInts;
     const int pair = col < blk[1] ? blk[2 + col] : -1;
-    run_g2<FP8>(act, W, blk[0], pair, tile2, H, I, topk_w, partial, red);
-    fence_release_agent();
-    __syncthreads();
+    run_g2<FP8, true>(act, W, blk[0], pair, tile2, H, I, topk_w, partial, red);
     if (tid == 0) {
       s_last_tile = atomicAdd(&tile_done[tile2], 1) == nb - 1;
       s_last_blk = atomicAdd(&blk_used[b], 1) == n2t - 1;
@@ -674,11 +706,10 @@ __global__ __launch_bounds__(kThreads) void moe_fused_kernel(
     __syncthreads();
     if (s_last_tile) {
       // every block's partials for this 32-column slice are written
-      fence_acquire_agent();
       const int h0 = tile2 * 16 * kG2T;
       for (int i = tid; i < T * (16 * kG2T / 4); i += kThreads) {
         const int t = i / (16 * kG2T / 4), h = h0 + (i - t * (16 * kG2T / 4)) * 4;
-        combine4(partial, s_valid, t, k, H, h, scale, shared, out);
+        combine4<true>(partial, s_valid, t, k, H, h, scale, shared, out);
       }
       if (tid == 0) atomicExch(&tile_done[tile2], 0);
     }
