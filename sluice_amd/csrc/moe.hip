@@ -45,17 +45,17 @@ constexpr int kFusedMaxHidden = 16384;   // H limit of the fused kernel
 constexpr int kFp8Blk = 128;
 
 #ifndef SLUICE_G1_D
-#define SLUICE_G1_D 8
+#define SLUICE_G1_D 4
 #endif
 #ifndef SLUICE_G2_D
-#define SLUICE_G2_D 8
+#define SLUICE_G2_D 4
 #endif
 #ifndef SLUICE_F8_D
-#define SLUICE_F8_D 4
+#define SLUICE_F8_D 2
 #endif
-constexpr int kG1D = SLUICE_G1_D;  // bf16 gemm1: 32-wide K chunks in flight per lane
+constexpr int kG1D = SLUICE_G1_D;  // bf16 gemm1: 64-wide K chunks in flight per wave
 constexpr int kG2D = SLUICE_G2_D;  // bf16 gemm2
-constexpr int kF8D = SLUICE_F8_D;  // fp8: 64-wide K chunks in flight per lane
+constexpr int kF8D = SLUICE_F8_D;  // fp8: 128-wide K chunks in flight per wave
 
 __host__ __device__ inline size_t plan_ints(int P) {
   return (size_t)kPlanHeader + (size_t)kBlockInts * P + (size_t)P;
@@ -243,115 +243,113 @@ __device__ __forceinline__ void g2_epilogue(RedBuf& red, int pair, int tile2, in
 }
 
 // ---------------------------------------------------------------------------
-// gemm1 item, bf16 weights: gate and up rows tile*16..+16 of `slot` against
-// the block's tokens.  `pair` = this lane's pair (column lane & 15), -1 if
-// none.  Each wave owns a contiguous K range and keeps kG1D chunks (3 x 16 B
-// per lane each) in flight: chunk c + kG1D is loaded as soon as chunk c has
-// been consumed.
+// Weight streaming.  A work item multiplies two 16-row weight tiles (the
+// gate and up rows of an intermediate tile for gemm1; 32 consecutive hidden
+// rows for gemm2) by the block's token columns.  Weights are read as whole
+// 128-byte row segments: one 16-byte load per lane covers 8 rows x 128 B
+// (row lane >> 3, segment lane & 7), which keeps HBM streaming near its
+// rate, where loads of 16 rows x 64 B each ran ~15% slower.  Each wave
+// stages its segments through 4 KB of LDS, XOR-swizzled (segment s of row r
+// at s ^ (r & 7)) so that the row-major writes and the MFMA-order reads are
+// both free of bank conflicts, and reads them back in the A layout of
+// v_mfma_f32_16x16x32_bf16 (row lane & 15, K group lane >> 4).  The K
+// groups of a segment go to (MFMA m, K group kb) in a fixed order that the
+// token operand is loaded in too, so every dot product is unchanged.
+//
+// Each wave owns a contiguous range of K chunks and keeps D chunks in
+// flight.  The steady loop issues its loads unconditionally, so the
+// compiler waits for exactly the chunk it consumes (a conditional reload
+// made it drain every load in flight each round).
 // ---------------------------------------------------------------------------
+typedef u32x4_t StageBuf[kKS][256];  // per wave: 2 tiles x 16 rows x 8 segments
+
+struct ItemLds {
+  RedBuf red;
+  StageBuf stage;
+};
+
 template <bool COH>
-__device__ __forceinline__ void g1_item_bf16(const uint16_t* __restrict__ x,
-                                             const uint16_t* __restrict__ w13, int slot, int pair,
-                                             int tile, int H, int I, int k,
-                                             uint16_t* __restrict__ act, RedBuf& red) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int col = lane & 15, kg = lane >> 4;
-  const int nchunk = H / 32;
-  const int c0 = wave * nchunk / kKS, c1 = (wave + 1) * nchunk / kKS;
-  const int n = c1 - c0;
-  const uint16_t* wg =
-      w13 + ((size_t)slot * 2 * I + (size_t)tile * 16 + col) * H + kg * 8 + c0 * 32;
-  const uint16_t* wu = wg + (size_t)I * H;
-  const bool hx = pair >= 0;
-  const uint16_t* xr = x + (size_t)(hx ? pair / k : 0) * H + kg * 8 + c0 * 32;
-  f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-  u32x4_t rg[kG1D], ru[kG1D], rx[kG1D];
-#pragma unroll
-  for (int d = 0; d < kG1D; ++d) {
-    rx[d] = u32x4_t{0u, 0u, 0u, 0u};
-    if (d < n) {
-      rg[d] = ldg16_stream(wg + d * 32);
-      ru[d] = ldg16_stream(wu + d * 32);
-      if (hx) rx[d] = ldg16(xr + d * 32);
-    }
-  }
-  for (int base = 0; base < n; base += kG1D) {
-#pragma unroll
-    for (int d = 0; d < kG1D; ++d) {
-      if (base + d < n) {
-        ag = mfma16x16x32_bf16(rg[d], rx[d], ag);
-        au = mfma16x16x32_bf16(ru[d], rx[d], au);
-        const int nx = base + kG1D + d;
-        if (nx < n) {
-          rg[d] = ldg16_stream(wg + nx * 32);
-          ru[d] = ldg16_stream(wu + nx * 32);
-          if (hx) rx[d] = ldg16(xr + nx * 32);
-        }
-      }
-    }
-  }
-  red[wave][0][lane] = ag;
-  red[wave][1][lane] = au;
-  g1_epilogue<COH>(red, pair, tile, I, act);
+__device__ __forceinline__ u32x4_t ld_tok(const uint16_t* p) {
+  return COH ? ld16_coh(p) : ldg16(p);
 }
 
-// gemm2 item, bf16 weights: hidden rows tile2*32..+32 of `slot` against
-// the block's act rows (the act fragment is loaded once per K chunk and
-// feeds both 16-row tiles).
-template <bool COH>
-__device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act,
-                                             const uint16_t* __restrict__ w2, int slot, int pair,
-                                             int tile2, int H, int I,
-                                             const float* __restrict__ topk_w,
-                                             float* __restrict__ partial, RedBuf& red) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int col = lane & 15, kg = lane >> 4;
-  const int nchunk = I / 32;
-  const int c0 = wave * nchunk / kKS, c1 = (wave + 1) * nchunk / kKS;
-  const int n = c1 - c0;
-  const bool hx = pair >= 0;
-  const uint16_t* wr =
-      w2 + ((size_t)slot * H + (size_t)tile2 * 16 * kG2T + col) * I + kg * 8 + c0 * 32;
-  const uint16_t* ar = act + (size_t)(hx ? pair : 0) * I + kg * 8 + c0 * 32;
-  f32x4_t acc[kG2T];
+// acc0 / acc1 += tile 0 / tile 1 [16 rows, K chunks c0 .. c0+n) . tokens^T.
+// bf16 weights, 64-element chunks; segment group 2*kb + m feeds MFMA m.
+// a0, a1: row 0 of each tile (row stride ld elements); b: this lane's
+// token row (column lane & 15), K offset 0.
+template <bool COH, int D>
+__device__ __forceinline__ void stream_bf16(const uint16_t* __restrict__ a0,
+                                            const uint16_t* __restrict__ a1, size_t ld,
+                                            const uint16_t* __restrict__ b, int c0, int n,
+                                            u32x4_t* st, f32x4_t& acc0, f32x4_t& acc1) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane >> 3, s = lane & 7;
+  const int R = lane & 15, kb = lane >> 4;
+  const uint16_t* p0 = a0 + (size_t)r * ld + (size_t)c0 * 64 + s * 8;
+  const uint16_t* p1 = a1 + (size_t)r * ld + (size_t)c0 * 64 + s * 8;
+  const size_t ld8 = 8 * ld;
+  const uint16_t* pb = b + (size_t)c0 * 64 + kb * 16;
+  const int wl = r * 8 + (s ^ r), wh = wl + 64;
+  const int rd0 = R * 8 + ((2 * kb) ^ (R & 7)), rd1 = R * 8 + ((2 * kb + 1) ^ (R & 7));
+  u32x4_t q0l[D], q0h[D], q1l[D], q1h[D], x0[D], x1[D];
+  auto issue = [&](int d, int c) {
+    const size_t o = (size_t)c * 64;
+    q0l[d] = ldg16_stream(p0 + o);
+    q0h[d] = ldg16_stream(p0 + ld8 + o);
+    q1l[d] = ldg16_stream(p1 + o);
+    q1h[d] = ldg16_stream(p1 + ld8 + o);
+    x0[d] = ld_tok<COH>(pb + o);
+    x1[d] = ld_tok<COH>(pb + o + 8);
+  };
+  auto consume = [&](int d) {
+    st[wl] = q0l[d];
+    st[wh] = q0h[d];
+    st[128 + wl] = q1l[d];
+    st[128 + wh] = q1h[d];
+    __builtin_amdgcn_wave_barrier();
+    const u32x4_t g0 = st[rd0], g1 = st[rd1], u0 = st[128 + rd0], u1 = st[128 + rd1];
+    __builtin_amdgcn_wave_barrier();
+    acc0 = mfma16x16x32_bf16(g0, x0[d], acc0);
+    acc0 = mfma16x16x32_bf16(g1, x1[d], acc0);
+    acc1 = mfma16x16x32_bf16(u0, x0[d], acc1);
+    acc1 = mfma16x16x32_bf16(u1, x1[d], acc1);
+  };
+  if (n <= 0) return;
+  // The prologue issues every group (a wave with n < D re-reads its last
+  // chunk) so that the load count at the loop head does not depend on n.
 #pragma unroll
-  for (int t = 0; t < kG2T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  u32x4_t ra[kG2D][kG2T], rb[kG2D];
+  for (int d = 0; d < D; ++d) {
+    issue(d, d < n ? d : n - 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  int base = 0;
+  for (; base + 2 * D <= n; base += D) {
 #pragma unroll
-  for (int d = 0; d < kG2D; ++d) {
-    rb[d] = u32x4_t{0u, 0u, 0u, 0u};
-    if (d < n) {
-#pragma unroll
-      for (int t = 0; t < kG2T; ++t) ra[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + d * 32);
-      if (hx) rb[d] = ld_act<COH>(ar + d * 32);
+    for (int d = 0; d < D; ++d) {
+      consume(d);
+      issue(d, base + D + d);
+      __builtin_amdgcn_sched_barrier(0);  // keep the load groups in issue order
     }
   }
-  for (int base = 0; base < n; base += kG2D) {
 #pragma unroll
-    for (int d = 0; d < kG2D; ++d) {
-      if (base + d < n) {
-#pragma unroll
-        for (int t = 0; t < kG2T; ++t) acc[t] = mfma16x16x32_bf16(ra[d][t], rb[d], acc[t]);
-        const int nx = base + kG2D + d;
-        if (nx < n) {
-#pragma unroll
-          for (int t = 0; t < kG2T; ++t) ra[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + nx * 32);
-          if (hx) rb[d] = ld_act<COH>(ar + nx * 32);
-        }
-      }
+  for (int d = 0; d < D; ++d) {
+    if (base + d < n) {
+      consume(d);
+      if (base + D + d < n) issue(d, base + D + d);
     }
   }
 #pragma unroll
-  for (int t = 0; t < kG2T; ++t) red[wave][t][lane] = acc[t];
-  g2_epilogue<COH>(red, pair, tile2, H, hx ? topk_w[pair] : 0.f, partial);
+  for (int d = 0; d < D; ++d)
+    if (base + D + d < n) consume(d);
 }
 
 // ---------------------------------------------------------------------------
-// fp8 e4m3fn weights with 128x128 fp32 block scales, bf16 activations.
-// Each lane loads 16 fp8 bytes of a 64-wide K chunk, widens them exactly to
-// bf16 and issues two MFMAs (the x fragment is loaded with the same K
-// order); the fp32 sum over a 128-wide K block is multiplied by that block's
-// scale before it joins the accumulator.  kF8D chunks are in flight.
+// fp8 e4m3fn weights with 128x128 fp32 block scales, bf16 activations.  A
+// chunk is 128 K elements (one scale block, one 128-byte segment per row).
+// Lane (row R, K group kb) reads the 32 fp8 bytes kb*32 .. +32 of its row
+// from LDS, widens them exactly to bf16 and issues four MFMAs against the
+// token elements loaded in the same order; the fp32 sum over the chunk is
+// multiplied by its scale before it joins the accumulator.
 // ---------------------------------------------------------------------------
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 
@@ -376,74 +374,150 @@ __device__ __forceinline__ void fp8x16_to_bf16(u32x4_t q, u32x4_t& lo, u32x4_t& 
   hi = u32x4_t{c[0], c[1], d[0], d[1]};
 }
 
-// gemm1 item, fp8 weights.  Wave w owns 64-wide K chunks [c0, c1), an even
-// split of 128-wide scale blocks.
+// As stream_bf16 for fp8 weights; s0 / s1: the tiles' scales, one per chunk
+// (absolute chunk index).
+template <bool COH, int D>
+__device__ __forceinline__ void stream_fp8(const uint8_t* __restrict__ a0,
+                                           const uint8_t* __restrict__ a1, size_t ld,
+                                           const float* __restrict__ s0,
+                                           const float* __restrict__ s1,
+                                           const uint16_t* __restrict__ b, int c0, int n,
+                                           u32x4_t* st, f32x4_t& acc0, f32x4_t& acc1) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane >> 3, s = lane & 7;
+  const int R = lane & 15, kb = lane >> 4;
+  const uint8_t* p0 = a0 + (size_t)r * ld + (size_t)c0 * 128 + s * 16;
+  const uint8_t* p1 = a1 + (size_t)r * ld + (size_t)c0 * 128 + s * 16;
+  const size_t ld8 = 8 * ld;
+  const uint16_t* pb = b + (size_t)c0 * 128 + kb * 32;
+  const int wl = r * 8 + (s ^ r), wh = wl + 64;
+  const int rd0 = R * 8 + ((2 * kb) ^ (R & 7)), rd1 = R * 8 + ((2 * kb + 1) ^ (R & 7));
+  u32x4_t q0l[D], q0h[D], q1l[D], q1h[D], xb[D][4];
+  auto issue = [&](int d, int c) {
+    const size_t o = (size_t)c * 128;
+    q0l[d] = ldg16_stream(p0 + o);
+    q0h[d] = ldg16_stream(p0 + ld8 + o);
+    q1l[d] = ldg16_stream(p1 + o);
+    q1h[d] = ldg16_stream(p1 + ld8 + o);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) xb[d][m] = ld_tok<COH>(pb + o + m * 8);
+  };
+  auto consume = [&](int d, int c) {
+    st[wl] = q0l[d];
+    st[wh] = q0h[d];
+    st[128 + wl] = q1l[d];
+    st[128 + wh] = q1h[d];
+    __builtin_amdgcn_wave_barrier();
+    const u32x4_t g0 = st[rd0], g1 = st[rd1], u0 = st[128 + rd0], u1 = st[128 + rd1];
+    __builtin_amdgcn_wave_barrier();
+    u32x4_t w0, w1, w2, w3;
+    f32x4_t t0 = {0.f, 0.f, 0.f, 0.f}, t1 = t0;
+    fp8x16_to_bf16(g0, w0, w1);
+    fp8x16_to_bf16(g1, w2, w3);
+    t0 = mfma16x16x32_bf16(w0, xb[d][0], t0);
+    t0 = mfma16x16x32_bf16(w1, xb[d][1], t0);
+    t0 = mfma16x16x32_bf16(w2, xb[d][2], t0);
+    t0 = mfma16x16x32_bf16(w3, xb[d][3], t0);
+    fp8x16_to_bf16(u0, w0, w1);
+    fp8x16_to_bf16(u1, w2, w3);
+    t1 = mfma16x16x32_bf16(w0, xb[d][0], t1);
+    t1 = mfma16x16x32_bf16(w1, xb[d][1], t1);
+    t1 = mfma16x16x32_bf16(w2, xb[d][2], t1);
+    t1 = mfma16x16x32_bf16(w3, xb[d][3], t1);
+    acc0 += s0[c0 + c] * t0;
+    acc1 += s1[c0 + c] * t1;
+  };
+  if (n <= 0) return;
+  // The prologue issues every group (a wave with n < D re-reads its last
+  // chunk) so that the load count at the loop head does not depend on n.
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    issue(d, d < n ? d : n - 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  int base = 0;
+  for (; base + 2 * D <= n; base += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      consume(d, base + d);
+      issue(d, base + D + d);
+      __builtin_amdgcn_sched_barrier(0);  // keep the load groups in issue order
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    if (base + d < n) {
+      consume(d, base + d);
+      if (base + D + d < n) issue(d, base + D + d);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (base + D + d < n) consume(d, base + D + d);
+}
+
+// ---------------------------------------------------------------------------
+// Work items.  `pair` = this lane's pair (column lane & 15), -1 if none; a
+// lane without a pair streams token row 0 (or act row 0) so every load is
+// issued unconditionally, and its column is never written.
+// gemm1: gate and up rows tile*16 .. +16 of `slot` -> act (silu(g) * u).
+// gemm2: hidden rows tile2*32 .. +32 of `slot` against act -> w * partial.
+// ---------------------------------------------------------------------------
+template <bool COH>
+__device__ __forceinline__ void g1_item_bf16(const uint16_t* __restrict__ x,
+                                             const uint16_t* __restrict__ w13, int slot, int pair,
+                                             int tile, int H, int I, int k,
+                                             uint16_t* __restrict__ act, ItemLds& l) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nc = H / 64;
+  const int c0 = wave * nc / kKS, c1 = (wave + 1) * nc / kKS;
+  const uint16_t* a0 = w13 + ((size_t)slot * 2 * I + (size_t)tile * 16) * H;
+  const uint16_t* xr = x + (size_t)(pair >= 0 ? pair / k : 0) * H;
+  f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
+  stream_bf16<false, kG1D>(a0, a0 + (size_t)I * H, H, xr, c0, c1 - c0, l.stage[wave], ag, au);
+  l.red[wave][0][lane] = ag;
+  l.red[wave][1][lane] = au;
+  g1_epilogue<COH>(l.red, pair, tile, I, act);
+}
+
+template <bool COH>
+__device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act,
+                                             const uint16_t* __restrict__ w2, int slot, int pair,
+                                             int tile2, int H, int I,
+                                             const float* __restrict__ topk_w,
+                                             float* __restrict__ partial, ItemLds& l) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nc = I / 64;
+  const int c0 = wave * nc / kKS, c1 = (wave + 1) * nc / kKS;
+  const uint16_t* a0 = w2 + ((size_t)slot * H + (size_t)tile2 * 16 * kG2T) * I;
+  const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
+  f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = a;
+  stream_bf16<COH, kG2D>(a0, a0 + (size_t)16 * I, I, ar, c0, c1 - c0, l.stage[wave], a, b);
+  l.red[wave][0][lane] = a;
+  l.red[wave][1][lane] = b;
+  g2_epilogue<COH>(l.red, pair, tile2, H, pair >= 0 ? topk_w[pair] : 0.f, partial);
+}
+
 template <bool COH>
 __device__ __forceinline__ void g1_item_fp8(const uint16_t* __restrict__ x,
                                             const uint8_t* __restrict__ w13,
                                             const float* __restrict__ w13_scale, int slot,
                                             int pair, int tile, int H, int I, int k,
-                                            uint16_t* __restrict__ act, RedBuf& red) {
+                                            uint16_t* __restrict__ act, ItemLds& l) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int col = lane & 15, kg = lane >> 4;
   const int nkb = H / kFp8Blk, nrb = (2 * I) / kFp8Blk;
-  const int c0 = 2 * (wave * nkb / kKS), c1 = 2 * ((wave + 1) * nkb / kKS);
-  const int n = c1 - c0;
+  const int c0 = wave * nkb / kKS, c1 = (wave + 1) * nkb / kKS;
   const int rg = tile * 16, ru = I + tile * 16;
-  const uint8_t* wg = w13 + ((size_t)slot * 2 * I + rg + col) * H + kg * 16 + c0 * 64;
-  const uint8_t* wu = w13 + ((size_t)slot * 2 * I + ru + col) * H + kg * 16 + c0 * 64;
+  const uint8_t* ag_p = w13 + ((size_t)slot * 2 * I + rg) * H;
+  const uint8_t* au_p = w13 + ((size_t)slot * 2 * I + ru) * H;
   const float* sg = w13_scale + ((size_t)slot * nrb + rg / kFp8Blk) * nkb;
   const float* su = w13_scale + ((size_t)slot * nrb + ru / kFp8Blk) * nkb;
-  const bool hx = pair >= 0;
-  const uint16_t* xr = x + (size_t)(hx ? pair / k : 0) * H + kg * 16 + c0 * 64;
-  f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-  f32x4_t tg = ag, tu = ag;
-  u32x4_t qg[kF8D], qu[kF8D], b0[kF8D], b1[kF8D];
-#pragma unroll
-  for (int d = 0; d < kF8D; ++d) {
-    b0[d] = b1[d] = u32x4_t{0u, 0u, 0u, 0u};
-    if (d < n) {
-      qg[d] = ldg16_stream(wg + d * 64);
-      qu[d] = ldg16_stream(wu + d * 64);
-      if (hx) {
-        b0[d] = ldg16(xr + d * 64);
-        b1[d] = ldg16(xr + d * 64 + 8);
-      }
-    }
-  }
-  for (int base = 0; base < n; base += kF8D) {
-#pragma unroll
-    for (int d = 0; d < kF8D; ++d) {
-      const int c = base + d;
-      if (c < n) {
-        u32x4_t g0, g1, u0, u1;
-        fp8x16_to_bf16(qg[d], g0, g1);
-        fp8x16_to_bf16(qu[d], u0, u1);
-        tg = mfma16x16x32_bf16(g0, b0[d], tg);
-        tg = mfma16x16x32_bf16(g1, b1[d], tg);
-        tu = mfma16x16x32_bf16(u0, b0[d], tu);
-        tu = mfma16x16x32_bf16(u1, b1[d], tu);
-        const int nx = c + kF8D;
-        if (nx < n) {
-          qg[d] = ldg16_stream(wg + nx * 64);
-          qu[d] = ldg16_stream(wu + nx * 64);
-          if (hx) {
-            b0[d] = ldg16(xr + nx * 64);
-            b1[d] = ldg16(xr + nx * 64 + 8);
-          }
-        }
-        if (c & 1) {  // end of a 128-wide scale block
-          const int kb = (c0 + c) >> 1;
-          ag += sg[kb] * tg;
-          au += su[kb] * tu;
-          tg = tu = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        }
-      }
-    }
-  }
-  red[wave][0][lane] = ag;
-  red[wave][1][lane] = au;
-  g1_epilogue<COH>(red, pair, tile, I, act);
+  const uint16_t* xr = x + (size_t)(pair >= 0 ? pair / k : 0) * H;
+  f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
+  stream_fp8<false, kF8D>(ag_p, au_p, H, sg, su, xr, c0, c1 - c0, l.stage[wave], ag, au);
+  l.red[wave][0][lane] = ag;
+  l.red[wave][1][lane] = au;
+  g1_epilogue<COH>(l.red, pair, tile, I, act);
 }
 
 template <bool COH>
@@ -452,68 +526,19 @@ __device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act,
                                             const float* __restrict__ w2_scale, int slot,
                                             int pair, int tile2, int H, int I,
                                             const float* __restrict__ topk_w,
-                                            float* __restrict__ partial, RedBuf& red) {
+                                            float* __restrict__ partial, ItemLds& l) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int col = lane & 15, kg = lane >> 4;
   const int nkb = I / kFp8Blk, nrb = H / kFp8Blk;
-  const int c0 = 2 * (wave * nkb / kKS), c1 = 2 * ((wave + 1) * nkb / kKS);
-  const int n = c1 - c0;
+  const int c0 = wave * nkb / kKS, c1 = (wave + 1) * nkb / kKS;
   const int r0 = tile2 * 16 * kG2T;
-  const uint8_t* wr = w2 + ((size_t)slot * H + r0 + col) * I + kg * 16 + c0 * 64;
+  const uint8_t* a0 = w2 + ((size_t)slot * H + r0) * I;
   const float* sr = w2_scale + ((size_t)slot * nrb + r0 / kFp8Blk) * nkb;
-  const bool hx = pair >= 0;
-  const uint16_t* ar = act + (size_t)(hx ? pair : 0) * I + kg * 16 + c0 * 64;
-  f32x4_t acc[kG2T], tmp[kG2T];
-#pragma unroll
-  for (int t = 0; t < kG2T; ++t) acc[t] = tmp[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  u32x4_t q[kF8D][kG2T], b0[kF8D], b1[kF8D];
-#pragma unroll
-  for (int d = 0; d < kF8D; ++d) {
-    b0[d] = b1[d] = u32x4_t{0u, 0u, 0u, 0u};
-    if (d < n) {
-#pragma unroll
-      for (int t = 0; t < kG2T; ++t) q[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + d * 64);
-      if (hx) {
-        b0[d] = ld_act<COH>(ar + d * 64);
-        b1[d] = ld_act<COH>(ar + d * 64 + 8);
-      }
-    }
-  }
-  for (int base = 0; base < n; base += kF8D) {
-#pragma unroll
-    for (int d = 0; d < kF8D; ++d) {
-      const int c = base + d;
-      if (c < n) {
-#pragma unroll
-        for (int t = 0; t < kG2T; ++t) {
-          u32x4_t a0, a1;
-          fp8x16_to_bf16(q[d][t], a0, a1);
-          tmp[t] = mfma16x16x32_bf16(a0, b0[d], tmp[t]);
-          tmp[t] = mfma16x16x32_bf16(a1, b1[d], tmp[t]);
-        }
-        const int nx = c + kF8D;
-        if (nx < n) {
-#pragma unroll
-          for (int t = 0; t < kG2T; ++t) q[d][t] = ldg16_stream(wr + (size_t)t * 16 * I + nx * 64);
-          if (hx) {
-            b0[d] = ld_act<COH>(ar + nx * 64);
-            b1[d] = ld_act<COH>(ar + nx * 64 + 8);
-          }
-        }
-        if (c & 1) {
-          const float s = sr[(c0 + c) >> 1];
-#pragma unroll
-          for (int t = 0; t < kG2T; ++t) {
-            acc[t] += s * tmp[t];
-            tmp[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-          }
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < kG2T; ++t) red[wave][t][lane] = acc[t];
-  g2_epilogue<COH>(red, pair, tile2, H, hx ? topk_w[pair] : 0.f, partial);
+  const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
+  f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = a;
+  stream_fp8<COH, kF8D>(a0, a0 + (size_t)16 * I, I, sr, sr, ar, c0, c1 - c0, l.stage[wave], a, b);
+  l.red[wave][0][lane] = a;
+  l.red[wave][1][lane] = b;
+  g2_epilogue<COH>(l.red, pair, tile2, H, pair >= 0 ? topk_w[pair] : 0.f, partial);
 }
 
 // ---------------------------------------------------------------------------
@@ -529,21 +554,21 @@ struct Bf16W {
 template <bool FP8, bool COH = false>
 __device__ __forceinline__ void run_g1(const uint16_t* x, const Bf16W& W, int slot, int pair,
                                        int tile, int H, int I, int k, uint16_t* act,
-                                       RedBuf& red) {
+                                       ItemLds& l) {
   if (FP8)
-    g1_item_fp8<COH>(x, W.w13, W.s13, slot, pair, tile, H, I, k, act, red);
+    g1_item_fp8<COH>(x, W.w13, W.s13, slot, pair, tile, H, I, k, act, l);
   else
-    g1_item_bf16<COH>(x, (const uint16_t*)W.w13, slot, pair, tile, H, I, k, act, red);
+    g1_item_bf16<COH>(x, (const uint16_t*)W.w13, slot, pair, tile, H, I, k, act, l);
 }
 
 template <bool FP8, bool COH = false>
 __device__ __forceinline__ void run_g2(const uint16_t* act, const Bf16W& W, int slot, int pair,
                                        int tile2, int H, int I, const float* tw, float* partial,
-                                       RedBuf& red) {
+                                       ItemLds& l) {
   if (FP8)
-    g2_item_fp8<COH>(act, W.w2, W.s2, slot, pair, tile2, H, I, tw, partial, red);
+    g2_item_fp8<COH>(act, W.w2, W.s2, slot, pair, tile2, H, I, tw, partial, l);
   else
-    g2_item_bf16<COH>(act, (const uint16_t*)W.w2, slot, pair, tile2, H, I, tw, partial, red);
+    g2_item_bf16<COH>(act, (const uint16_t*)W.w2, slot, pair, tile2, H, I, tw, partial, l);
 }
 
 template <bool FP8>
@@ -552,7 +577,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm1_kernel(const uint16_t* __r
                                                              const int32_t* __restrict__ plan,
                                                              int H, int I, int k,
                                                              uint16_t* __restrict__ act) {
-  __shared__ RedBuf red;
+  __shared__ ItemLds lds;
   const int n_tiles = I / 16;
   const int total = plan[0] * n_tiles;
   const int col = threadIdx.x & 15;
@@ -560,7 +585,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm1_kernel(const uint16_t* __r
     const int b = item / n_tiles, tile = item - b * n_tiles;
     const int32_t* blk = plan + kPlanHeader + (size_t)b * kBlockInts;
     const int pair = col < blk[1] ? blk[2 + col] : -1;
-    run_g1<FP8>(x, W, blk[0], pair, tile, H, I, k, act, red);
+    run_g1<FP8>(x, W, blk[0], pair, tile, H, I, k, act, lds);
   }
 }
 
@@ -571,7 +596,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_kernel(const uint16_t* __r
                                                              const float* __restrict__ topk_w,
                                                              int H, int I,
                                                              float* __restrict__ partial) {
-  __shared__ RedBuf red;
+  __shared__ ItemLds lds;
   const int n_tiles = H / (16 * kG2T);
   const int total = plan[0] * n_tiles;
   const int col = threadIdx.x & 15;
@@ -579,7 +604,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_kernel(const uint16_t* __r
     const int b = item / n_tiles, tile2 = item - b * n_tiles;
     const int32_t* blk = plan + kPlanHeader + (size_t)b * kBlockInts;
     const int pair = col < blk[1] ? blk[2 + col] : -1;
-    run_g2<FP8>(act, W, blk[0], pair, tile2, H, I, topk_w, partial, red);
+    run_g2<FP8>(act, W, blk[0], pair, tile2, H, I, topk_w, partial, lds);
   }
 }
 
@@ -645,7 +670,7 @@ __global__ __launch_bounds__(kThreads) void moe_fused_kernel(
   __shared__ AlignScratch sc;
   __shared__ int32_t s_blocks[kFusedMaxPairs * kBlockInts];
   __shared__ int32_t s_valid[kFusedMaxPairs];
-  __shared__ RedBuf red;
+  __shared__ ItemLds lds;
   __shared__ int s_last_blk, s_last_tile;
   int32_t* blk_done = ctl + kCtlInts;
   int32_t* blk_used = blk_done + kFusedMaxPairs;
@@ -671,7 +696,7 @@ __global__ __launch_bounds__(kThreads) void moe_fused_kernel(
       const int b = item / n1t, tile = item - b * n1t;
       const int32_t* blk = s_blocks + b * kBlockInts;
       const int pair = col < blk[1] ? blk[2 + col] : -1;
-      run_g1<FP8, true>(x, W, blk[0], pair, tile, H, I, k, act, red);
+      run_g1<FP8, true>(x, W, blk[0], pair, tile, H, I, k, act, lds);
       // the act rows went out with device-coherent stores, completed before
       // the epilogue's barrier
       if (tid == 0) atomicAdd(&blk_done[b], 1);
@@ -693,7 +718,7 @@ __global__ __launch_bounds__(kThreads) void moe_fused_kernel(
     // act is read with device-coherent loads after the counter was seen
     const int32_t* blk = s_blocks + b * kBlockInts;
     const int pair = col < blk[1] ? blk[2 + col] : -1;
-    run_g2<FP8, true>(act, W, blk[0], pair, tile2, H, I, topk_w, partial, red);
+    run_g2<FP8, true>(act, W, blk[0], pair, tile2, H, I, topk_w, partial, lds);
     if (tid == 0) {
       s_last_tile = atomicAdd(&tile_done[tile2], 1) == nb - 1;
       s_last_blk = atomicAdd(&blk_used[b], 1) == n2t - 1;
@@ -792,7 +817,7 @@ int check_common(int T, int H, int I, int k, int E, int S, const void* x, const 
       S > SLUICE_MAX_SLOTS)
     return SLUICE_E_INVAL;
   if ((long)T * k > SLUICE_MAX_PAIRS) return SLUICE_E_INVAL;
-  if (H % (16 * kG2T) != 0 || I % 32 != 0) return SLUICE_E_INVAL;
+  if (H % 64 != 0 || I % 64 != 0) return SLUICE_E_INVAL;
   if (T == 0) return SLUICE_OK;
   if (!x || !w13 || !w2 || !tw || !ti || !ws || !out) return SLUICE_E_INVAL;
   if (ws_bytes < workspace_bytes(T, H, I, k, nullptr, nullptr)) return SLUICE_E_INVAL;
@@ -928,7 +953,7 @@ extern "C" int sluice_fused_experts_fp8(const void* x, const void* w13, const fl
 
 extern "C" int sluice_moe_gemm1_bf16(const void* x, const void* w13, const int32_t* plan, int T,
                                      int H, int I, int k, void* act, sluice_stream_t stream) {
-  if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % 32 || I % 32 || (long)T * k > SLUICE_MAX_PAIRS ||
+  if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % 64 || I % 64 || (long)T * k > SLUICE_MAX_PAIRS ||
       !x || !w13 || !plan || !act)
     return SLUICE_E_INVAL;
   Bf16W W{(const uint8_t*)w13, nullptr, nullptr, nullptr};
@@ -940,7 +965,7 @@ extern "C" int sluice_moe_gemm1_bf16(const void* x, const void* w13, const int32
 extern "C" int sluice_moe_gemm2_bf16(const void* act, const void* w2, const int32_t* plan,
                                      const float* topk_w, int T, int H, int I, int k,
                                      float* partial, sluice_stream_t stream) {
-  if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % (16 * kG2T) || I % 32 ||
+  if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % 64 || I % 64 ||
       (long)T * k > SLUICE_MAX_PAIRS || !act || !w2 || !plan || !topk_w || !partial)
     return SLUICE_E_INVAL;
   Bf16W W{nullptr, (const uint8_t*)w2, nullptr, nullptr};

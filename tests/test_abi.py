@@ -48,6 +48,14 @@ def test_invalid_arguments_rejected_without_touching_the_gpu(lib):
     assert lib.sluice_moe_align(None, 1, 8, None, 64, 0, None, None) == _lib.SLUICE_E_INVAL
     assert lib.sluice_fused_experts_bf16(None, None, None, None, None, None, 1, 2048, 100, 8, 64,
                                          8, 1.0, None, None, 0, None, None) == _lib.SLUICE_E_INVAL
+    # weight rows stream in 64-element (128-byte) segments: H, I % 64 == 0
+    for H, I in ((2048, 96), (2080, 128)):
+        assert lib.sluice_fused_experts_bf16(None, None, None, None, None, None, 1, H, I, 8, 64,
+                                             8, 1.0, None, None, 0, None, None) == _lib.SLUICE_E_INVAL
+        assert lib.sluice_moe_gemm1_bf16(None, None, None, 1, H, I, 8, None,
+                                         None) == _lib.SLUICE_E_INVAL
+        assert lib.sluice_moe_gemm2_bf16(None, None, None, None, 1, H, I, 8, None,
+                                         None) == _lib.SLUICE_E_INVAL
     h = ctypes.c_void_p()
     assert lib.sluice_layer_create(64, 64, 0, 0, None, None, ctypes.byref(h)) == _lib.SLUICE_E_INVAL
     assert lib.sluice_layer_create(2048, 64, 8, 4, None, None,

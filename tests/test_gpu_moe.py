@@ -96,7 +96,8 @@ def _moe_case(T, H, I, E, S, k, seed, resident_frac=0.85, use_map=True, scale=1.
     (1, 2048, 768, 128, 8, 8),      # Qwen3 c=1
     (8, 2048, 768, 128, 16, 8),     # Qwen3 c=8
     (12, 2048, 768, 128, 16, 8),    # Qwen3 c=12
-    (33, 256, 96, 16, 16, 4),       # > 16 pairs per slot: several blocks per expert
+    (33, 256, 192, 16, 16, 4),      # > 16 pairs per slot: several blocks per expert
+    (5, 64, 128, 8, 8, 2),          # K shorter than the waves: some waves stream nothing
 ])
 def test_fused_experts_bf16(T, H, I, E, S, k):
     print(f"fused bf16 T={T} H={H} I={I} E={E} S={S} k={k}", flush=True)
