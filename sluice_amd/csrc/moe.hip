@@ -44,14 +44,16 @@ constexpr int kFusedMaxPairs = 256;      // T*k limit of the fused kernel
 constexpr int kFusedMaxHidden = 16384;   // H limit of the fused kernel
 constexpr int kFp8Blk = 128;
 
+// Chunks in flight per wave.  Deeper pipelines measured no faster for
+// gemm1 and slower for gemm2 and fp8 (fewer resident waves per CU).
 #ifndef SLUICE_G1_D
-#define SLUICE_G1_D 4
+#define SLUICE_G1_D 2
 #endif
 #ifndef SLUICE_G2_D
-#define SLUICE_G2_D 4
+#define SLUICE_G2_D 2
 #endif
 #ifndef SLUICE_F8_D
-#define SLUICE_F8_D 2
+#define SLUICE_F8_D 1
 #endif
 constexpr int kG1D = SLUICE_G1_D;  // bf16 gemm1: 64-wide K chunks in flight per wave
 constexpr int kG2D = SLUICE_G2_D;  // bf16 gemm2
