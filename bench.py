@@ -54,6 +54,12 @@ def parse():
     ap.add_argument("--layers", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
+    ap.add_argument("--save-routing", default=None,
+                    help="also write the routing the roofline is timed over (.npz)")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="time only the kernels, over the routing of --load-routing, and print "
+                         "that (no decode: the workload of the counter runs)")
+    ap.add_argument("--load-routing", default=None)
     return ap.parse_args()
 
 
@@ -90,8 +96,9 @@ def time_decode(dec, c, steps, warmup):
 
 
 def record_routing(dec, c, steps):
-    """Decode `steps` more steps and keep every MoE layer's routing of each
-    (the tensors the captured step rewrites are cloned after every replay)."""
+    """Decode `steps` more steps and keep every MoE layer's routing of each,
+    with the expert map the step's gap left (the tensors the captured step
+    rewrites are cloned after every replay)."""
     import torch
 
     out = []
@@ -99,9 +106,30 @@ def record_routing(dec, c, steps):
         dec.step_graphs(c)
         torch.cuda.synchronize()
         for n, io in enumerate(dec.layer_io[c]):
-            out.append((n, io["hn"].clone(), io["ti"].clone(), io["tw"].clone()))
+            out.append({"n": n, "hn": io["hn"].clone(), "ti": io["ti"].clone(),
+                        "tw": io["tw"].clone(), "map": dec.moe_layers[n]._expert_map.clone()})
     dec.sync()
     return out
+
+
+def save_routing(path, recorded):
+    import torch
+
+    np.savez(path, n=np.array([r["n"] for r in recorded], np.int32),
+             hn=torch.stack([r["hn"] for r in recorded]).view(torch.int16).cpu().numpy(),
+             ti=torch.stack([r["ti"] for r in recorded]).cpu().numpy(),
+             tw=torch.stack([r["tw"] for r in recorded]).cpu().numpy(),
+             map=torch.stack([r["map"] for r in recorded]).cpu().numpy())
+
+
+def load_routing(path, dev):
+    import torch
+
+    z = np.load(path)
+    hn = torch.from_numpy(z["hn"]).to(dev).view(torch.bfloat16)
+    return [{"n": int(z["n"][i]), "hn": hn[i], "ti": torch.from_numpy(z["ti"][i]).to(dev),
+             "tw": torch.from_numpy(z["tw"][i]).to(dev),
+             "map": torch.from_numpy(z["map"][i]).to(dev)} for i in range(len(z["n"]))]
 
 
 def _event_loop(stream, fn, items, reps):
@@ -140,10 +168,11 @@ def kernel_roofline(dec, c, recorded, reps=3):
     nplan = lib.sluice_moe_plan_ints(c, k)
     items = []
     with torch.cuda.stream(stream):
-        for n, hn, ti, tw in recorded:
+        for r in recorded:
+            n, hn, ti, tw = r["n"], r["hn"], r["ti"], r["tw"]
             m = dec.moe_layers[n]
             plan = torch.empty(nplan, dtype=torch.int32, device=dec.dev)
-            _lib.check(lib.sluice_moe_align(ti.data_ptr(), c, k, m._expert_map.data_ptr(),
+            _lib.check(lib.sluice_moe_align(ti.data_ptr(), c, k, r["map"].data_ptr(),
                                             sp["E"], m.w13_weight.shape[0], plan.data_ptr(),
                                             stream.cuda_stream), "align")
             act = torch.empty((c * k, I), dtype=torch.bfloat16, device=dec.dev)
@@ -216,6 +245,22 @@ def kernel_roofline(dec, c, recorded, reps=3):
     return {"c": c, "launches": reps * len(items), "gemm1": r1, "gemm2": r2,
             "combine": res("moe_combine_kernel", us3, b3),
             "copy_256MiB_GBs": 2 * nb / (usc * 1e-6) / 1e9}
+
+
+def measured_traffic(cfg, c, slots, uniform):
+    """HBM bytes per moe_gemm1 launch for this workload, from the committed
+    summary of the two counter runs (FETCH_SIZE, WRITE_SIZE), each scaled by
+    what the counter reads for a 256 MiB device copy; None if not measured."""
+    path = os.path.join(ROOT, "profiles", "gemm1_traffic.json")
+    if uniform or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        table = json.load(f)
+    rec = table.get(f"{cfg}/c{c}/slots{slots}")
+    if rec is None:
+        return None
+    return {"bytes_per_launch": rec["hbm_bytes_per_launch"],
+            "source": f"profiles/gemm1_traffic.json[{cfg}/c{c}/slots{slots}]"}
 
 
 def h2d_rates(dec):
@@ -348,6 +393,17 @@ def main():
                            uniform_routing=a.uniform, layers=a.layers, device=dev)
     log(f"built {cfg} decoder in {time.perf_counter() - t_build:.1f}s "
         f"({len(dec.moe_layers)} MoE layers, slots={slots}, batches={batches})")
+    if a.roofline_only:
+        # no decode step runs here: a counter-collecting profiler serialises
+        # dispatches, which the gap's device/host hand-off cannot run under
+        if not a.load_routing:
+            sys.exit("--roofline-only needs --load-routing (written by --save-routing)")
+        recorded = load_routing(a.load_routing, dev)
+        c = int(recorded[0]["ti"].shape[0])
+        roof = kernel_roofline(dec, c, recorded)
+        print(json.dumps({"config": cfg, "c": c, "roofline": roof}), flush=True)
+        dec.close()
+        return
     results = []
     for c in batches:
         dec.capture(c)
@@ -358,7 +414,10 @@ def main():
         results.append(r)
     main_c = max(batches)
     main = [r for r in results if r["c"] == main_c][0]
-    roof = kernel_roofline(dec, main_c, record_routing(dec, main_c, 4))
+    recorded = record_routing(dec, main_c, 4)
+    if a.save_routing:
+        save_routing(a.save_routing, recorded)
+    roof = kernel_roofline(dec, main_c, recorded)
     h2d = h2d_rates(dec)
     log(f"roofline {roof}")
     log(f"h2d {h2d}")
@@ -395,9 +454,12 @@ def main():
     }
     if roof:
         g1 = roof["gemm1"]
+        traffic = measured_traffic(cfg, main_c, slots, a.uniform)
         line["roofline"] = {
             "bound": "hbm", "achieved": g1["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": g1["achieved_GBs"] / HBM_PEAK_GBS, "traffic": None,
+            "frac": g1["achieved_GBs"] / HBM_PEAK_GBS,
+            "traffic": traffic["bytes_per_launch"] if traffic else None,
+            "traffic_source": traffic["source"] if traffic else None,
             "kernel": g1["kernel"], "avg_us": g1["avg_us"],
             "algorithmic_bytes_per_launch": g1["algorithmic_bytes"],
             "mfma_util_pct": g1["mfma_util_pct"],

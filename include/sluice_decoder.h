@@ -32,15 +32,20 @@ int sluice_dec_add_rmsnorm(void* x, const void* delta, const void* w, void* out,
                            float eps, sluice_stream_t stream);
 
 /* Skinny GEMM: y [T, N] = bf16(x [T, K] . w [N, K]^T), fp32 accumulation,
- * T <= 16, N % 16 == 0, K % 32 == 0 (MFMA bf16, weights streamed once). */
+ * T <= 16, N % 16 == 0, K % 64 == 0 (weights streamed once on MFMA bf16).
+ * workspace (16-byte aligned, sluice_dec_linear_workspace() bytes,
+ * zero-filled before its first use; every call leaves it so) lets a small
+ * matrix split K over more workgroups; NULL runs without the split.  Calls
+ * sharing a workspace must not overlap. */
+size_t sluice_dec_linear_workspace(void);
 int sluice_dec_linear(const void* x, const void* w, int T, int N, int K, void* y,
-                      sluice_stream_t stream);
+                      void* workspace, sluice_stream_t stream);
 
 /* The same with the SwiGLU activation fused into the input: y = act . w^T
  * with act = silu(gu[:, :K]) * gu[:, K:] (gu [T, 2K], rounded to bf16 as
  * the activation kernel rounds it). */
 int sluice_dec_linear_swiglu(const void* gu, const void* w, int T, int N, int K, void* y,
-                             sluice_stream_t stream);
+                             void* workspace, sluice_stream_t stream);
 
 /* Greedy next token: out[t] (int64) = the first index of the largest value
  * of x [T, N] bf16 (NaN never wins; an all-NaN row gives 0).  One launch

@@ -90,8 +90,9 @@ SIGNATURES = {
     "sluice_dec_add_rmsnorm": (c_int, [_P, _P, _P, _P, c_int, c_int, c_float, _P]),
     "sluice_dec_silu_mul": (c_int, [_P, _P, c_int, c_int, _P]),
     "sluice_dec_argmax": (c_int, [_P, c_int, c_int, _P, _P]),
-    "sluice_dec_linear": (c_int, [_P, _P, c_int, c_int, c_int, _P, _P]),
-    "sluice_dec_linear_swiglu": (c_int, [_P, _P, c_int, c_int, c_int, _P, _P]),
+    "sluice_dec_linear_workspace": (c_size_t, []),
+    "sluice_dec_linear": (c_int, [_P, _P, c_int, c_int, c_int, _P, _P, _P]),
+    "sluice_dec_linear_swiglu": (c_int, [_P, _P, c_int, c_int, c_int, _P, _P, _P]),
     "sluice_dec_gate_logits": (
         c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, _P]
     ),

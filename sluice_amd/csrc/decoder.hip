@@ -6,6 +6,7 @@
 
 #include "common.h"
 #include "sluice_decoder.h"
+#include "stream.h"
 
 namespace {
 
@@ -532,102 +533,138 @@ __global__ __launch_bounds__(kT) void gqa_attend_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Skinny GEMM for decode: y [T, N] = x [T, K] . W [N, K]^T, T <= 16.  A weight
-// stream like the expert product: a workgroup takes 16 rows of W (MFMA M)
-// against all T tokens (MFMA N); its KS waves split K and reduce in LDS; each
-// lane keeps 8 chunks of 16 bytes in flight.  KS grows as N shrinks, so a
-// small matrix still puts enough waves in flight to cover HBM latency.
-// SWIGLU: x is the activation silu(g) * u of a [T, 2K] gate|up input,
-// computed as the fragments are loaded.
+// Skinny GEMM for decode: y [T, N] = x [T, K] . W [N, K]^T, T <= 16, the
+// weights streamed by stream_bf16.  A work item is a 32-row tile of W and a
+// part of K; the host splits K into `ks` parts so that the items spread over
+// the CUs (one CU streams only ~27 GB/s, so a small matrix in few items
+// leaves most of HBM idle).  The item's 4 waves split its chunks and reduce
+// in LDS.  With ks > 1 an item writes its fp32 partial tile to the
+// workspace with device-coherent stores and counts itself on the tile's
+// counter; the tile's last item sums the parts in part order (the result
+// does not depend on which item finishes last), writes y and re-arms the
+// counter.  SWIGLU: x is the activation silu(g) * u of a [T, 2K] gate|up
+// input, computed as the fragments are loaded.
 // ---------------------------------------------------------------------------
-constexpr int kLinD = 8;
+constexpr int kLinWaves = 4;
+constexpr int kLinD = 2;
+constexpr int kLinMaxCus = 1024;        // workspace bound: ks * tiles <= 2 * CUs
+constexpr size_t kLinPartBytes = (size_t)2 * kLinMaxCus * 32 * 16 * sizeof(float);
 
-template <int KS, bool SWIGLU>
-__global__ __launch_bounds__(64 * KS) void linear_kernel(const uint16_t* __restrict__ x,
-                                                         const uint16_t* __restrict__ w, int T,
-                                                         int N, int K, uint16_t* __restrict__ y) {
-  __shared__ f32x4_t red[KS][64];
+struct LinLds {
+  f32x4_t red[kLinWaves][2][64];
+  u32x4_t stage[kLinWaves][kStageVecs];
+  int last;
+};
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int T, int N, int K, int ks,
+    uint16_t* __restrict__ y, float* __restrict__ parts, int* __restrict__ counters) {
+  __shared__ LinLds l;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kg = lane >> 4;
-  const int nchunk = K / 32;
-  const int c0 = wave * nchunk / KS, c1 = (wave + 1) * nchunk / KS;
-  const int n = c1 - c0;
-  const bool hx = col < T;
-  const int xstride = SWIGLU ? 2 * K : K;
-  for (int tile = blockIdx.x; tile < N / 16; tile += gridDim.x) {
-    const uint16_t* wr = w + ((size_t)tile * 16 + col) * K + kg * 8 + c0 * 32;
-    const uint16_t* xr = x + (size_t)(hx ? col : 0) * xstride + kg * 8 + c0 * 32;
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    u32x4_t rw[kLinD], rx[kLinD], ru[SWIGLU ? kLinD : 1];
+  const int tile = blockIdx.x / ks, part = blockIdx.x - tile * ks;
+  const int nc = K / 64;
+  const int p0 = part * nc / ks, p1 = (part + 1) * nc / ks;
+  const int c0 = p0 + wave * (p1 - p0) / kLinWaves, c1 = p0 + (wave + 1) * (p1 - p0) / kLinWaves;
+  const int r0 = tile * 32;
+  const bool two = r0 + 16 < N;  // N % 16 == 0: the last tile may hold 16 rows
+  const uint16_t* a0 = w + (size_t)r0 * K;
+  const uint16_t* a1 = two ? a0 + (size_t)16 * K : a0;
+  const uint16_t* xr = x + (size_t)(col < T ? col : T - 1) * (SWIGLU ? 2 * K : K);
+  f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+  stream_bf16<SWIGLU ? kTokSwiglu : kTokPlain, kLinD>(a0, a1, K, xr, K, c0, c1 - c0,
+                                                      l.stage[wave], acc0, acc1);
+  l.red[wave][0][lane] = acc0;
+  l.red[wave][1][lane] = acc1;
+  __syncthreads();
+  const int nt = two ? 2 : 1;
+  // lane (col, kg) of wave 0 owns rows r0 + t*16 + kg*4 .. +4 of token col
+  if (wave == 0 && col < T) {
 #pragma unroll
-    for (int d = 0; d < kLinD; ++d) {
-      rx[d] = u32x4_t{0u, 0u, 0u, 0u};
-      if (SWIGLU) ru[d] = rx[d];
-      if (d < n) {
-        rw[d] = ldg16_stream(wr + d * 32);
-        if (hx) {
-          rx[d] = ldg16(xr + d * 32);
-          if (SWIGLU) ru[d] = ldg16(xr + K + d * 32);
-        }
+    for (int t = 0; t < 2; ++t) {
+      if (t >= nt) break;
+      f32x4_t v = l.red[0][t][lane];
+#pragma unroll
+      for (int u = 1; u < kLinWaves; ++u) v += l.red[u][t][lane];
+      const int row = r0 + t * 16 + kg * 4;
+      if (ks == 1) {
+        *reinterpret_cast<u32x2_t*>(y + (size_t)col * N + row) =
+            u32x2_t{pack2(v[0], v[1]), pack2(v[2], v[3])};
+      } else {
+        float* dst = parts + ((size_t)part * T + col) * N + row;
+        st8_coh(dst, __float_as_uint(v[0]), __float_as_uint(v[1]));
+        st8_coh(dst + 2, __float_as_uint(v[2]), __float_as_uint(v[3]));
       }
     }
-    for (int base = 0; base < n; base += kLinD) {
+    if (ks > 1) __builtin_amdgcn_s_waitcnt(0);  // written through before the item is counted
+  }
+  if (ks == 1) return;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    l.last = atomicAdd(&counters[tile], 1) == ks - 1;
+    if (l.last) atomicExch(&counters[tile], 0);
+  }
+  __syncthreads();
+  if (!l.last || wave != 0 || col >= T) return;
 #pragma unroll
-      for (int d = 0; d < kLinD; ++d) {
-        if (base + d < n) {
-          u32x4_t xv = rx[d];
-          if (SWIGLU) {
-            float g[8], u[8];
-            unpack8(rx[d], g);
-            unpack8(ru[d], u);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              xv[j] = pack2(g[2 * j] / (1.0f + expf(-g[2 * j])) * u[2 * j],
-                            g[2 * j + 1] / (1.0f + expf(-g[2 * j + 1])) * u[2 * j + 1]);
-          }
-          acc = mfma16x16x32_bf16(rw[d], xv, acc);
-          const int nx = base + kLinD + d;
-          if (nx < n) {
-            rw[d] = ldg16_stream(wr + nx * 32);
-            if (hx) {
-              rx[d] = ldg16(xr + nx * 32);
-              if (SWIGLU) ru[d] = ldg16(xr + K + nx * 32);
-            }
-          }
-        }
-      }
-    }
-    red[wave][lane] = acc;
-    __syncthreads();
-    if (wave == 0 && hx) {
-      f32x4_t s = red[0][lane];
-#pragma unroll
-      for (int v = 1; v < KS; ++v) s += red[v][lane];
-      *reinterpret_cast<u32x2_t*>(y + (size_t)col * N + tile * 16 + kg * 4) =
-          u32x2_t{pack2(s[0], s[1]), pack2(s[2], s[3])};
-    }
-    __syncthreads();
+  for (int t = 0; t < 2; ++t) {
+    if (t >= nt) break;
+    const int row = r0 + t * 16 + kg * 4;
+    f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < ks; ++p)
+      v += __builtin_bit_cast(f32x4_t, ld16_coh(parts + ((size_t)p * T + col) * N + row));
+    *reinterpret_cast<u32x2_t*>(y + (size_t)col * N + row) =
+        u32x2_t{pack2(v[0], v[1]), pack2(v[2], v[3])};
   }
 }
 
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus[dev] = n < kLinMaxCus ? n : kLinMaxCus;
+  }
+  return cus[dev];
+}
+
+// Parts of K per tile: the split whose busiest CU finishes first, with an
+// item costing its bytes at ~27 GB/s per CU plus ~1.5 us, and the split's
+// hand-off another ~1.5 us.  ks * tiles <= 2 * CUs keeps the partials
+// within the workspace bound.
+int linear_parts(int N, int K, int cus) {
+  const int tiles = (N + 31) / 32, nc = K / 64;
+  int best = 1;
+  double best_us = 1e30;
+  for (int ks = 1; ks <= 16 && ks <= nc; ++ks) {
+    if (ks > 1 && (long)tiles * ks > 2L * cus) break;
+    const long items = (long)tiles * ks;
+    const long rounds = (items + cus - 1) / cus;
+    const double item_bytes = 32.0 * 2.0 * 64.0 * ((nc + ks - 1) / ks);
+    const double us = rounds * (item_bytes / 27.0e3 + 1.5) + (ks > 1 ? 1.5 : 0.0);
+    if (us < best_us * 0.97) {
+      best_us = us;
+      best = ks;
+    }
+  }
+  return best;
+}
+
 template <bool SWIGLU>
-int launch_linear(const void* x, const void* w, int T, int N, int K, void* y, hipStream_t st) {
-  const int tiles = N / 16;
-  const int grid = tiles < 4096 ? tiles : 4096;
-  const int nchunk = K / 32;
-  // (the fused-activation variant needs more registers: at most 8 waves)
-  if (tiles >= 1024 || nchunk < 32)
-    hipLaunchKernelGGL((linear_kernel<4, SWIGLU>), dim3(grid), dim3(256), 0, st,
-                       (const uint16_t*)x, (const uint16_t*)w, T, N, K, (uint16_t*)y);
-  else if (tiles >= 256 || nchunk < 64)
-    hipLaunchKernelGGL((linear_kernel<8, SWIGLU>), dim3(grid), dim3(512), 0, st,
-                       (const uint16_t*)x, (const uint16_t*)w, T, N, K, (uint16_t*)y);
-  else if (SWIGLU)
-    hipLaunchKernelGGL((linear_kernel<8, SWIGLU>), dim3(grid), dim3(512), 0, st,
-                       (const uint16_t*)x, (const uint16_t*)w, T, N, K, (uint16_t*)y);
-  else
-    hipLaunchKernelGGL((linear_kernel<16, SWIGLU>), dim3(grid), dim3(1024), 0, st,
-                       (const uint16_t*)x, (const uint16_t*)w, T, N, K, (uint16_t*)y);
+int launch_linear(const void* x, const void* w, int T, int N, int K, void* y, void* ws,
+                  hipStream_t st) {
+  const int tiles = (N + 31) / 32;
+  const int ks = ws != nullptr ? linear_parts(N, K, device_cus()) : 1;
+  float* parts = (float*)ws;
+  int* counters = ws != nullptr ? (int*)((char*)ws + kLinPartBytes) : nullptr;
+  hipLaunchKernelGGL((linear_kernel<SWIGLU>), dim3(tiles * ks), dim3(64 * kLinWaves), 0, st,
+                     (const uint16_t*)x, (const uint16_t*)w, T, N, K, ks, (uint16_t*)y, parts,
+                     counters);
   return (int)hipGetLastError();
 }
 
@@ -688,24 +725,30 @@ extern "C" int sluice_dec_argmax(const void* x, int T, int N, int64_t* out,
   return (int)hipGetLastError();
 }
 
+extern "C" size_t sluice_dec_linear_workspace(void) {
+  return kLinPartBytes + (size_t)kLinMaxCus * sizeof(int);
+}
+
 extern "C" int sluice_dec_linear(const void* x, const void* w, int T, int N, int K, void* y,
-                                 sluice_stream_t stream) {
-  if (T < 0 || T > 16 || N <= 0 || N % 16 != 0 || K <= 0 || K % 32 != 0 || x == nullptr ||
+                                 void* workspace, sluice_stream_t stream) {
+  if (T < 0 || T > 16 || N <= 0 || N % 16 != 0 || K <= 0 || K % 64 != 0 || x == nullptr ||
       w == nullptr || y == nullptr)
     return SLUICE_E_INVAL;
-  if (((uintptr_t)x | (uintptr_t)w) & 15 || (uintptr_t)y & 7) return SLUICE_E_INVAL;
+  if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)workspace) & 15 || (uintptr_t)y & 7)
+    return SLUICE_E_INVAL;
   if (T == 0) return SLUICE_OK;
-  return launch_linear<false>(x, w, T, N, K, y, (hipStream_t)stream);
+  return launch_linear<false>(x, w, T, N, K, y, workspace, (hipStream_t)stream);
 }
 
 extern "C" int sluice_dec_linear_swiglu(const void* gu, const void* w, int T, int N, int K,
-                                        void* y, sluice_stream_t stream) {
-  if (T < 0 || T > 16 || N <= 0 || N % 16 != 0 || K <= 0 || K % 32 != 0 || gu == nullptr ||
+                                        void* y, void* workspace, sluice_stream_t stream) {
+  if (T < 0 || T > 16 || N <= 0 || N % 16 != 0 || K <= 0 || K % 64 != 0 || gu == nullptr ||
       w == nullptr || y == nullptr)
     return SLUICE_E_INVAL;
-  if (((uintptr_t)gu | (uintptr_t)w) & 15 || (uintptr_t)y & 7) return SLUICE_E_INVAL;
+  if (((uintptr_t)gu | (uintptr_t)w | (uintptr_t)workspace) & 15 || (uintptr_t)y & 7)
+    return SLUICE_E_INVAL;
   if (T == 0) return SLUICE_OK;
-  return launch_linear<true>(gu, w, T, N, K, y, (hipStream_t)stream);
+  return launch_linear<true>(gu, w, T, N, K, y, workspace, (hipStream_t)stream);
 }
 
 extern "C" int sluice_dec_add_rmsnorm(void* x, const void* delta, const void* w, void* out,

@@ -31,6 +31,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "stream.h"
 
 namespace {
 
@@ -168,25 +169,6 @@ __global__ __launch_bounds__(kThreads) void moe_align_kernel(
 
 typedef f32x4_t RedBuf[kKS][2][64];
 
-// Device-coherent (sc1) 16-byte load / stores: the fused kernel hands act
-// rows and fp32 partials between workgroups on different XCDs through these
-// instead of writing back / invalidating whole L2 caches.
-__device__ __forceinline__ u32x4_t ld16_coh(const void* p) {
-  const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
-  const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return u32x4_t{(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
-}
-__device__ __forceinline__ void st8_coh(void* p, uint32_t lo, uint32_t hi) {
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), (uint64_t)lo | ((uint64_t)hi << 32),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <bool COH>
-__device__ __forceinline__ u32x4_t ld_act(const void* p) {
-  if (COH) return ld16_coh(p);
-  return ldg16(p);
-}
-
 __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
   return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
 }
@@ -245,25 +227,11 @@ __device__ __forceinline__ void g2_epilogue(RedBuf& red, int pair, int tile2, in
 }
 
 // ---------------------------------------------------------------------------
-// Weight streaming.  A work item multiplies two 16-row weight tiles (the
-// gate and up rows of an intermediate tile for gemm1; 32 consecutive hidden
-// rows for gemm2) by the block's token columns.  Weights are read as whole
-// 128-byte row segments: one 16-byte load per lane covers 8 rows x 128 B
-// (row lane >> 3, segment lane & 7), which keeps HBM streaming near its
-// rate, where loads of 16 rows x 64 B each ran ~15% slower.  Each wave
-// stages its segments through 4 KB of LDS, XOR-swizzled (segment s of row r
-// at s ^ (r & 7)) so that the row-major writes and the MFMA-order reads are
-// both free of bank conflicts, and reads them back in the A layout of
-// v_mfma_f32_16x16x32_bf16 (row lane & 15, K group lane >> 4).  The K
-// groups of a segment go to (MFMA m, K group kb) in a fixed order that the
-// token operand is loaded in too, so every dot product is unchanged.
-//
-// Each wave owns a contiguous range of K chunks and keeps D chunks in
-// flight.  The steady loop issues its loads unconditionally, so the
-// compiler waits for exactly the chunk it consumes (a conditional reload
-// made it drain every load in flight each round).
+// Work items stream their weights with stream_bf16 / stream_fp8: two 16-row
+// tiles (the gate and up rows of an intermediate tile for gemm1; 32
+// consecutive hidden rows for gemm2) against the block's token columns.
 // ---------------------------------------------------------------------------
-typedef u32x4_t StageBuf[kKS][256];  // per wave: 2 tiles x 16 rows x 8 segments
+typedef u32x4_t StageBuf[kKS][kStageVecs];
 
 struct ItemLds {
   RedBuf red;
@@ -273,76 +241,6 @@ struct ItemLds {
 template <bool COH>
 __device__ __forceinline__ u32x4_t ld_tok(const uint16_t* p) {
   return COH ? ld16_coh(p) : ldg16(p);
-}
-
-// acc0 / acc1 += tile 0 / tile 1 [16 rows, K chunks c0 .. c0+n) . tokens^T.
-// bf16 weights, 64-element chunks; segment group 2*kb + m feeds MFMA m.
-// a0, a1: row 0 of each tile (row stride ld elements); b: this lane's
-// token row (column lane & 15), K offset 0.
-template <bool COH, int D>
-__device__ __forceinline__ void stream_bf16(const uint16_t* __restrict__ a0,
-                                            const uint16_t* __restrict__ a1, size_t ld,
-                                            const uint16_t* __restrict__ b, int c0, int n,
-                                            u32x4_t* st, f32x4_t& acc0, f32x4_t& acc1) {
-  const int lane = threadIdx.x & 63;
-  const int r = lane >> 3, s = lane & 7;
-  const int R = lane & 15, kb = lane >> 4;
-  const uint16_t* p0 = a0 + (size_t)r * ld + (size_t)c0 * 64 + s * 8;
-  const uint16_t* p1 = a1 + (size_t)r * ld + (size_t)c0 * 64 + s * 8;
-  const size_t ld8 = 8 * ld;
-  const uint16_t* pb = b + (size_t)c0 * 64 + kb * 16;
-  const int wl = r * 8 + (s ^ r), wh = wl + 64;
-  const int rd0 = R * 8 + ((2 * kb) ^ (R & 7)), rd1 = R * 8 + ((2 * kb + 1) ^ (R & 7));
-  u32x4_t q0l[D], q0h[D], q1l[D], q1h[D], x0[D], x1[D];
-  auto issue = [&](int d, int c) {
-    const size_t o = (size_t)c * 64;
-    q0l[d] = ldg16_stream(p0 + o);
-    q0h[d] = ldg16_stream(p0 + ld8 + o);
-    q1l[d] = ldg16_stream(p1 + o);
-    q1h[d] = ldg16_stream(p1 + ld8 + o);
-    x0[d] = ld_tok<COH>(pb + o);
-    x1[d] = ld_tok<COH>(pb + o + 8);
-  };
-  auto consume = [&](int d) {
-    st[wl] = q0l[d];
-    st[wh] = q0h[d];
-    st[128 + wl] = q1l[d];
-    st[128 + wh] = q1h[d];
-    __builtin_amdgcn_wave_barrier();
-    const u32x4_t g0 = st[rd0], g1 = st[rd1], u0 = st[128 + rd0], u1 = st[128 + rd1];
-    __builtin_amdgcn_wave_barrier();
-    acc0 = mfma16x16x32_bf16(g0, x0[d], acc0);
-    acc0 = mfma16x16x32_bf16(g1, x1[d], acc0);
-    acc1 = mfma16x16x32_bf16(u0, x0[d], acc1);
-    acc1 = mfma16x16x32_bf16(u1, x1[d], acc1);
-  };
-  if (n <= 0) return;
-  // The prologue issues every group (a wave with n < D re-reads its last
-  // chunk) so that the load count at the loop head does not depend on n.
-#pragma unroll
-  for (int d = 0; d < D; ++d) {
-    issue(d, d < n ? d : n - 1);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  int base = 0;
-  for (; base + 2 * D <= n; base += D) {
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      consume(d);
-      issue(d, base + D + d);
-      __builtin_amdgcn_sched_barrier(0);  // keep the load groups in issue order
-    }
-  }
-#pragma unroll
-  for (int d = 0; d < D; ++d) {
-    if (base + d < n) {
-      consume(d);
-      if (base + D + d < n) issue(d, base + D + d);
-    }
-  }
-#pragma unroll
-  for (int d = 0; d < D; ++d)
-    if (base + D + d < n) consume(d);
 }
 
 // ---------------------------------------------------------------------------
@@ -476,7 +374,8 @@ __device__ __forceinline__ void g1_item_bf16(const uint16_t* __restrict__ x,
   const uint16_t* a0 = w13 + ((size_t)slot * 2 * I + (size_t)tile * 16) * H;
   const uint16_t* xr = x + (size_t)(pair >= 0 ? pair / k : 0) * H;
   f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
-  stream_bf16<false, kG1D>(a0, a0 + (size_t)I * H, H, xr, c0, c1 - c0, l.stage[wave], ag, au);
+  stream_bf16<kTokPlain, kG1D>(a0, a0 + (size_t)I * H, H, xr, 0, c0, c1 - c0, l.stage[wave], ag,
+                               au);
   l.red[wave][0][lane] = ag;
   l.red[wave][1][lane] = au;
   g1_epilogue<COH>(l.red, pair, tile, I, act);
@@ -494,7 +393,8 @@ __device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act,
   const uint16_t* a0 = w2 + ((size_t)slot * H + (size_t)tile2 * 16 * kG2T) * I;
   const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
   f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = a;
-  stream_bf16<COH, kG2D>(a0, a0 + (size_t)16 * I, I, ar, c0, c1 - c0, l.stage[wave], a, b);
+  stream_bf16<COH ? kTokCoh : kTokPlain, kG2D>(a0, a0 + (size_t)16 * I, I, ar, 0, c0, c1 - c0,
+                                              l.stage[wave], a, b);
   l.red[wave][0][lane] = a;
   l.red[wave][1][lane] = b;
   g2_epilogue<COH>(l.red, pair, tile2, H, pair >= 0 ? topk_w[pair] : 0.f, partial);

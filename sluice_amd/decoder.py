@@ -240,6 +240,17 @@ def add_rmsnorm(x, delta, w, out=None, eps=_EPS):
     return out
 
 
+# One zero-filled workspace per device for the skinny GEMMs' split-K hand-off
+# (its size does not depend on the shape; the calls of a step run one after
+# another on one stream).
+_LIN_WS = ops._Workspace()
+
+
+def _linear_ws(dev):
+    lib, _ = _k()
+    return _LIN_WS.get(dev, int(lib.sluice_dec_linear_workspace()))
+
+
 def linear(x, w):
     """y = x . w^T for decode batches (T <= 16): one streaming MFMA kernel."""
     lib, check = _k()
@@ -248,7 +259,8 @@ def linear(x, w):
     if T > 16:
         raise ValueError(f"decode linear supports at most 16 rows, got {T}")
     y = torch.empty((T, N), dtype=x.dtype, device=x.device)
-    check(lib.sluice_dec_linear(x.data_ptr(), w.data_ptr(), T, N, K, y.data_ptr(), _stream(x)),
+    check(lib.sluice_dec_linear(x.data_ptr(), w.data_ptr(), T, N, K, y.data_ptr(),
+                                _linear_ws(x.device).data_ptr(), _stream(x)),
           "sluice_dec_linear")
     return y
 
@@ -262,7 +274,8 @@ def linear_swiglu(gu, w):
         raise ValueError(f"decode linear supports at most 16 rows, got {T}")
     y = torch.empty((T, N), dtype=gu.dtype, device=gu.device)
     check(lib.sluice_dec_linear_swiglu(gu.data_ptr(), w.data_ptr(), T, N, K2 // 2, y.data_ptr(),
-                                       _stream(gu)), "sluice_dec_linear_swiglu")
+                                       _linear_ws(gu.device).data_ptr(), _stream(gu)),
+          "sluice_dec_linear_swiglu")
     return y
 
 
@@ -587,6 +600,7 @@ class SyntheticDecoder:
         assert [id(c) for c in self.off._rs_caches] == [id(c) for c in self.caches]
         for m in self.moe_layers:
             ops.reserve_workspace(dev, max_batch, H, sp["I"], sp["k"])
+        _linear_ws(dev)  # before any capture: graphs bake its address
         rope_d = (sp["qk_rope"] if sp["attn"] == "mla" else sp.get("head_dim", 128))
         inv = 1.0 / (sp.get("rope_theta", 1e4) ** (torch.arange(0, rope_d, 2, device=dev).float()
                                                      / rope_d))
