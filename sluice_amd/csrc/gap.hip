@@ -55,6 +55,7 @@ namespace {
 
 constexpr int kLookupThreads = 256;
 constexpr int kWaves = kLookupThreads / SLUICE_WAVE;
+constexpr int kCopyU = 8;  // hidden-state vectors per thread in flight in the gap kernel
 
 // ---------------------------------------------------------------------------
 // Stand-alone lookup (sluice_slot_lookup): sorted unique ids + miss count.
@@ -149,17 +150,34 @@ struct GapMailbox {
   int32_t slot_global[SLUICE_MAX_SLOTS];  // slot -> global id, -1 = empty
 };
 
+// The mailbox is coherent host memory, which the device reaches uncached
+// over the bus.  A system-scope store is written through; once a thread's
+// stores have completed (s_waitcnt) the host can see them, without the L2
+// write-back a system-scope release fence costs (several microseconds with
+// the step's dirty lines in L2).  Posted writes over the bus stay in order,
+// so entries completed before the stamp is stored are seen before it.
+__device__ __forceinline__ void st_host(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ int32_t ld_host(const int32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 __device__ __forceinline__ int32_t ld_sys(const int32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// Spin until *p == want.  0, or SLUICE_E_ABORTED / SLUICE_E_TIMEOUT.
+// Spin until *p == want (acquire on success when ACQ: the caller then reads
+// what the host wrote before *p).  0, or SLUICE_E_ABORTED / SLUICE_E_TIMEOUT.
+template <bool ACQ>
 __device__ int wait_eq(const int32_t* p, int32_t want, const int32_t* abort_flag,
                        long long timeout_ticks) {
   const long long t0 = wall_clock64();
   for (;;) {
-    if (ld_sys(p) == want) return 0;
-    if (ld_sys(abort_flag) != 0) return SLUICE_E_ABORTED;
+    if (ld_host(p) == want) {
+      if (ACQ) (void)ld_sys(p);
+      return 0;
+    }
+    if (ld_host(abort_flag) != 0) return SLUICE_E_ABORTED;
     if (wall_clock64() - t0 > timeout_ticks) return SLUICE_E_TIMEOUT;
     __builtin_amdgcn_s_sleep(4);
   }
@@ -181,6 +199,19 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
   const int wave = tid >> 6;
   const int lane = tid & 63;
 
+  // The op's fresh copy of hidden_states does not depend on the host: its
+  // first kCopyU vectors per thread are loaded now and stored after the
+  // record is written, so the loads overlap the mailbox round trips.
+  // (every load is issued, clamped into the buffer, so none waits on another)
+  u32x4_t cv[kCopyU];
+  if (copy_vecs > 0) {
+#pragma unroll
+    for (int u = 0; u < kCopyU; ++u) {
+      const int i = u * kLookupThreads + tid;
+      cv[u] = copy_src[i < copy_vecs ? i : copy_vecs - 1];
+    }
+  }
+
   if (tid == 0) {
     // The host must have copied out this layer's previous record before it
     // is overwritten (it normally has, long ago).
@@ -189,7 +220,7 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     if (s <= 0) s = 1;
     s_stamp = s;
     s_standing = dev_state[1];
-    s_status = wait_eq(&mb->ack_stamp, prev, abort_flag, timeout_ticks);
+    s_status = wait_eq<false>(&mb->ack_stamp, prev, abort_flag, timeout_ticks);
   }
   for (int e = tid; e < E; e += kLookupThreads) present[e] = 0;
   __syncthreads();
@@ -214,7 +245,7 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
       __syncthreads();
       int off = base;
       for (int w = 0; w < wave; ++w) off += wcount[w];
-      if (f) mb->uniq[off + mask_rank(fb)] = e;
+      if (f) st_host(&mb->uniq[off + mask_rank(fb)], e);
       for (int w = 0; w < kWaves; ++w) {
         base += wcount[w];
         miss += wmiss[w];
@@ -222,39 +253,53 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
       __syncthreads();
     }
   }
-  // The op's fresh copy of hidden_states does not depend on the host; its
-  // stores overlap the PCIe writes of the record.
-  for (int i = tid; i < copy_vecs; i += kLookupThreads) copy_dst[i] = copy_src[i];
-  if (can_post) __threadfence_system();  // this thread's record entries are visible
+#pragma unroll
+  for (int u = 0; u < kCopyU; ++u) {
+    const int i = u * kLookupThreads + tid;
+    if (i < copy_vecs) copy_dst[i] = cv[u];
+  }
+  for (int i0 = kCopyU * kLookupThreads; i0 < copy_vecs; i0 += kCopyU * kLookupThreads) {
+#pragma unroll
+    for (int u = 0; u < kCopyU; ++u) {
+      const int i = i0 + u * kLookupThreads + tid;
+      cv[u] = copy_src[i < copy_vecs ? i : copy_vecs - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < kCopyU; ++u) {
+      const int i = i0 + u * kLookupThreads + tid;
+      if (i < copy_vecs) copy_dst[i] = cv[u];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's record entries have reached the host
   __syncthreads();
   if (tid == 0) {
     s_waits = 0;
     if (can_post) {
       const int32_t s = s_stamp;
-      if (!s_standing && ld_sys(&mb->standing) != 0) {
+      if (!s_standing && ld_host(&mb->standing) != 0) {
         s_standing = 1;
         dev_state[1] = 1;
       }
       const int waits = (miss > 0 || !s_standing) ? 1 : 0;
-      mb->n_uniq = base;
-      mb->n_miss = miss;
-      mb->waits = waits;
+      st_host(&mb->n_uniq, base);
+      st_host(&mb->n_miss, miss);
+      st_host(&mb->waits, waits);
       dev_state[0] = s;
-      // release: the header above and (via the fences before the barrier)
-      // every thread's entries are visible before the stamp
-      __hip_atomic_store(&mb->req_stamp, s, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+      // every thread's entries (completed before the barrier) and the
+      // header reach the host before the stamp
+      __builtin_amdgcn_s_waitcnt(0);
+      st_host(&mb->req_stamp, s);
       s_waits = waits;
     } else {
-      __hip_atomic_store(&mb->dev_status, s_status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      st_host(&mb->dev_status, s_status);
     }
   }
   __syncthreads();
   if (!s_waits) return;
   if (tid == 0) {
-    const int st = wait_eq(&mb->resp_stamp, s_stamp, abort_flag, timeout_ticks);
+    const int st = wait_eq<true>(&mb->resp_stamp, s_stamp, abort_flag, timeout_ticks);
     s_status = st != 0 ? st : ld_sys(&mb->resp_code);
-    if (st != 0)
-      __hip_atomic_store(&mb->dev_status, st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (st != 0) st_host(&mb->dev_status, st);
   }
   __syncthreads();
   if (s_status != 0) return;
