@@ -41,11 +41,12 @@ size_t sluice_dec_linear_workspace(void);
 int sluice_dec_linear(const void* x, const void* w, int T, int N, int K, void* y,
                       void* workspace, sluice_stream_t stream);
 
-/* The same with the SwiGLU activation fused into the input: y = act . w^T
- * with act = silu(gu[:, :K]) * gu[:, K:] (gu [T, 2K], rounded to bf16 as
- * the activation kernel rounds it). */
-int sluice_dec_linear_swiglu(const void* gu, const void* w, int T, int N, int K, void* y,
-                             void* workspace, sluice_stream_t stream);
+/* Gate/up projection with the SwiGLU activation applied to its fp32 sums:
+ * w [N, K] holds N/2 gate rows then N/2 up rows; y [T, N/2] =
+ * bf16(silu(x . w_gate^T) * (x . w_up^T)).  N % 32 == 0; workspace as for
+ * sluice_dec_linear. */
+int sluice_dec_linear_glu(const void* x, const void* w, int T, int N, int K, void* y,
+                          void* workspace, sluice_stream_t stream);
 
 /* Greedy next token: out[t] (int64) = the first index of the largest value
  * of x [T, N] bf16 (NaN never wins; an all-NaN row gives 0).  One launch

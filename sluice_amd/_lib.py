@@ -92,7 +92,7 @@ SIGNATURES = {
     "sluice_dec_argmax": (c_int, [_P, c_int, c_int, _P, _P]),
     "sluice_dec_linear_workspace": (c_size_t, []),
     "sluice_dec_linear": (c_int, [_P, _P, c_int, c_int, c_int, _P, _P, _P]),
-    "sluice_dec_linear_swiglu": (c_int, [_P, _P, c_int, c_int, c_int, _P, _P, _P]),
+    "sluice_dec_linear_glu": (c_int, [_P, _P, c_int, c_int, c_int, _P, _P, _P]),
     "sluice_dec_gate_logits": (
         c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, _P]
     ),

@@ -533,21 +533,24 @@ __global__ __launch_bounds__(kT) void gqa_attend_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Skinny GEMM for decode: y [T, N] = x [T, K] . W [N, K]^T, T <= 16, the
-// weights streamed by stream_bf16.  A work item is a 32-row tile of W and a
-// part of K; the host splits K into `ks` parts so that the items spread over
-// the CUs (one CU streams only ~27 GB/s, so a small matrix in few items
-// leaves most of HBM idle).  The item's 4 waves split its chunks and reduce
-// in LDS.  With ks > 1 an item writes its fp32 partial tile to the
-// workspace with device-coherent stores and counts itself on the tile's
-// counter; the tile's last item sums the parts in part order (the result
-// does not depend on which item finishes last), writes y and re-arms the
-// counter.  SWIGLU: x is the activation silu(g) * u of a [T, 2K] gate|up
-// input, computed as the fragments are loaded.
+// Skinny GEMMs for decode, T <= 16 tokens, weights streamed by stream_bf16:
+//   plain: y [T, N] = x [T, K] . W [N, K]^T;
+//   GLU:   y [T, Ni] = silu(g) * u with g|u = x . W^T and W [2*Ni, K] holding
+//          the gate rows then the up rows (the activation is applied to the
+//          fp32 sums, so the [T, 2*Ni] product never exists).
+// A work item is a pair of 16-row tiles (32 consecutive rows; for GLU the
+// gate and up rows of the same 16 channels) and a part of K; the host
+// splits K into `ks` parts so that the items spread over the CUs (one CU
+// streams only ~27 GB/s, so a small matrix in few items leaves most of HBM
+// idle).  The item's 4 waves split its chunks and reduce in LDS.  With
+// ks > 1 an item writes its fp32 partial tiles to the workspace with
+// device-coherent stores and counts itself on the item's counter; the
+// item's last part sums the parts in part order (the result does not
+// depend on which part finishes last), finishes y and re-arms the counter.
 // ---------------------------------------------------------------------------
 constexpr int kLinWaves = 4;
 constexpr int kLinD = 2;
-constexpr int kLinMaxCus = 1024;        // workspace bound: ks * tiles <= 2 * CUs
+constexpr int kLinMaxCus = 1024;        // workspace bound: ks * items <= 2 * CUs
 constexpr size_t kLinPartBytes = (size_t)2 * kLinMaxCus * 32 * 16 * sizeof(float);
 
 struct LinLds {
@@ -556,67 +559,88 @@ struct LinLds {
   int last;
 };
 
-template <bool SWIGLU>
+// Finish 4 rows of token col: plain -> two bf16 row groups (t = 0, 1);
+// GLU -> one bf16 group of silu(g) * u.
+template <bool GLU>
+__device__ __forceinline__ void lin_store(uint16_t* __restrict__ y, int ny, int col, int r0,
+                                          int kg, bool two, f32x4_t v0, f32x4_t v1) {
+  if (GLU) {
+    float o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = v0[r] / (1.0f + expf(-v0[r])) * v1[r];
+    *reinterpret_cast<u32x2_t*>(y + (size_t)col * ny + r0 + kg * 4) =
+        u32x2_t{pack2(o[0], o[1]), pack2(o[2], o[3])};
+  } else {
+    *reinterpret_cast<u32x2_t*>(y + (size_t)col * ny + r0 + kg * 4) =
+        u32x2_t{pack2(v0[0], v0[1]), pack2(v0[2], v0[3])};
+    if (two)
+      *reinterpret_cast<u32x2_t*>(y + (size_t)col * ny + r0 + 16 + kg * 4) =
+          u32x2_t{pack2(v1[0], v1[1]), pack2(v1[2], v1[3])};
+  }
+}
+
+// GLU: item i covers channels 16*i .. +16 (ny = Ni = N / 2); plain: rows
+// 32*i .. +32 (ny = N).
+template <bool GLU>
 __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int T, int N, int K, int ks,
     uint16_t* __restrict__ y, float* __restrict__ parts, int* __restrict__ counters) {
   __shared__ LinLds l;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kg = lane >> 4;
-  const int tile = blockIdx.x / ks, part = blockIdx.x - tile * ks;
+  const int item = blockIdx.x / ks, part = blockIdx.x - item * ks;
   const int nc = K / 64;
   const int p0 = part * nc / ks, p1 = (part + 1) * nc / ks;
   const int c0 = p0 + wave * (p1 - p0) / kLinWaves, c1 = p0 + (wave + 1) * (p1 - p0) / kLinWaves;
-  const int r0 = tile * 32;
-  const bool two = r0 + 16 < N;  // N % 16 == 0: the last tile may hold 16 rows
+  const int ny = GLU ? N / 2 : N;
+  const int r0 = GLU ? item * 16 : item * 32;
+  const bool two = GLU || r0 + 16 < N;  // plain, N % 32 == 16: the last item holds 16 rows
   const uint16_t* a0 = w + (size_t)r0 * K;
-  const uint16_t* a1 = two ? a0 + (size_t)16 * K : a0;
-  const uint16_t* xr = x + (size_t)(col < T ? col : T - 1) * (SWIGLU ? 2 * K : K);
+  const uint16_t* a1 = GLU ? w + (size_t)(ny + r0) * K : (two ? a0 + (size_t)16 * K : a0);
+  const uint16_t* xr = x + (size_t)(col < T ? col : T - 1) * K;
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
-  stream_bf16<SWIGLU ? kTokSwiglu : kTokPlain, kLinD>(a0, a1, K, xr, K, c0, c1 - c0,
-                                                      l.stage[wave], acc0, acc1);
+  stream_bf16<kTokPlain, kLinD>(a0, a1, K, xr, c0, c1 - c0, l.stage[wave], acc0, acc1);
   l.red[wave][0][lane] = acc0;
   l.red[wave][1][lane] = acc1;
   __syncthreads();
-  const int nt = two ? 2 : 1;
-  // lane (col, kg) of wave 0 owns rows r0 + t*16 + kg*4 .. +4 of token col
+  // lane (col, kg) of wave 0 owns rows kg*4 .. +4 of both tiles for token col
   if (wave == 0 && col < T) {
+    f32x4_t v0 = l.red[0][0][lane], v1 = l.red[0][1][lane];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      if (t >= nt) break;
-      f32x4_t v = l.red[0][t][lane];
-#pragma unroll
-      for (int u = 1; u < kLinWaves; ++u) v += l.red[u][t][lane];
-      const int row = r0 + t * 16 + kg * 4;
-      if (ks == 1) {
-        *reinterpret_cast<u32x2_t*>(y + (size_t)col * N + row) =
-            u32x2_t{pack2(v[0], v[1]), pack2(v[2], v[3])};
-      } else {
-        float* dst = parts + ((size_t)part * T + col) * N + row;
-        st8_coh(dst, __float_as_uint(v[0]), __float_as_uint(v[1]));
-        st8_coh(dst + 2, __float_as_uint(v[2]), __float_as_uint(v[3]));
-      }
+    for (int u = 1; u < kLinWaves; ++u) {
+      v0 += l.red[u][0][lane];
+      v1 += l.red[u][1][lane];
     }
-    if (ks > 1) __builtin_amdgcn_s_waitcnt(0);  // written through before the item is counted
+    if (ks == 1) {
+      lin_store<GLU>(y, ny, col, r0, kg, two, v0, v1);
+    } else {
+      // parts [ks][T][2 tiles][items * 16], tile-major so both tiles of an item sit together
+      float* dst = parts + (((size_t)part * T + col) * 2) * (size_t)(gridDim.x / ks) * 16 +
+                   (size_t)item * 16 + kg * 4;
+      const size_t tstride = (size_t)(gridDim.x / ks) * 16;
+      st8_coh(dst, __float_as_uint(v0[0]), __float_as_uint(v0[1]));
+      st8_coh(dst + 2, __float_as_uint(v0[2]), __float_as_uint(v0[3]));
+      st8_coh(dst + tstride, __float_as_uint(v1[0]), __float_as_uint(v1[1]));
+      st8_coh(dst + tstride + 2, __float_as_uint(v1[2]), __float_as_uint(v1[3]));
+    }
+    if (ks > 1) __builtin_amdgcn_s_waitcnt(0);  // written through before the part is counted
   }
   if (ks == 1) return;
   __syncthreads();
   if (threadIdx.x == 0) {
-    l.last = atomicAdd(&counters[tile], 1) == ks - 1;
-    if (l.last) atomicExch(&counters[tile], 0);
+    l.last = atomicAdd(&counters[item], 1) == ks - 1;
+    if (l.last) atomicExch(&counters[item], 0);
   }
   __syncthreads();
   if (!l.last || wave != 0 || col >= T) return;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    if (t >= nt) break;
-    const int row = r0 + t * 16 + kg * 4;
-    f32x4_t v = {0.f, 0.f, 0.f, 0.f};
-    for (int p = 0; p < ks; ++p)
-      v += __builtin_bit_cast(f32x4_t, ld16_coh(parts + ((size_t)p * T + col) * N + row));
-    *reinterpret_cast<u32x2_t*>(y + (size_t)col * N + row) =
-        u32x2_t{pack2(v[0], v[1]), pack2(v[2], v[3])};
+  const size_t tstride = (size_t)(gridDim.x / ks) * 16;
+  f32x4_t v0 = {0.f, 0.f, 0.f, 0.f}, v1 = v0;
+  for (int p = 0; p < ks; ++p) {
+    const float* src = parts + (((size_t)p * T + col) * 2) * tstride + (size_t)item * 16 + kg * 4;
+    v0 += __builtin_bit_cast(f32x4_t, ld16_coh(src));
+    v1 += __builtin_bit_cast(f32x4_t, ld16_coh(src + tstride));
   }
+  lin_store<GLU>(y, ny, col, r0, kg, two, v0, v1);
 }
 
 int device_cus() {
@@ -633,18 +657,18 @@ int device_cus() {
   return cus[dev];
 }
 
-// Parts of K per tile: the split whose busiest CU finishes first, with an
+// Parts of K per item: the split whose busiest CU finishes first, with an
 // item costing its bytes at ~27 GB/s per CU plus ~1.5 us, and the split's
-// hand-off another ~1.5 us.  ks * tiles <= 2 * CUs keeps the partials
+// hand-off another ~1.5 us.  ks * items <= 2 * CUs keeps the partials
 // within the workspace bound.
-int linear_parts(int N, int K, int cus) {
-  const int tiles = (N + 31) / 32, nc = K / 64;
+int linear_parts(int items, int K, int cus) {
+  const int nc = K / 64;
   int best = 1;
   double best_us = 1e30;
   for (int ks = 1; ks <= 16 && ks <= nc; ++ks) {
-    if (ks > 1 && (long)tiles * ks > 2L * cus) break;
-    const long items = (long)tiles * ks;
-    const long rounds = (items + cus - 1) / cus;
+    if (ks > 1 && (long)items * ks > 2L * cus) break;
+    const long n = (long)items * ks;
+    const long rounds = (n + cus - 1) / cus;
     const double item_bytes = 32.0 * 2.0 * 64.0 * ((nc + ks - 1) / ks);
     const double us = rounds * (item_bytes / 27.0e3 + 1.5) + (ks > 1 ? 1.5 : 0.0);
     if (us < best_us * 0.97) {
@@ -655,14 +679,14 @@ int linear_parts(int N, int K, int cus) {
   return best;
 }
 
-template <bool SWIGLU>
+template <bool GLU>
 int launch_linear(const void* x, const void* w, int T, int N, int K, void* y, void* ws,
                   hipStream_t st) {
-  const int tiles = (N + 31) / 32;
-  const int ks = ws != nullptr ? linear_parts(N, K, device_cus()) : 1;
+  const int items = GLU ? N / 32 : (N + 31) / 32;
+  const int ks = ws != nullptr ? linear_parts(items, K, device_cus()) : 1;
   float* parts = (float*)ws;
   int* counters = ws != nullptr ? (int*)((char*)ws + kLinPartBytes) : nullptr;
-  hipLaunchKernelGGL((linear_kernel<SWIGLU>), dim3(tiles * ks), dim3(64 * kLinWaves), 0, st,
+  hipLaunchKernelGGL((linear_kernel<GLU>), dim3(items * ks), dim3(64 * kLinWaves), 0, st,
                      (const uint16_t*)x, (const uint16_t*)w, T, N, K, ks, (uint16_t*)y, parts,
                      counters);
   return (int)hipGetLastError();
@@ -740,15 +764,15 @@ extern "C" int sluice_dec_linear(const void* x, const void* w, int T, int N, int
   return launch_linear<false>(x, w, T, N, K, y, workspace, (hipStream_t)stream);
 }
 
-extern "C" int sluice_dec_linear_swiglu(const void* gu, const void* w, int T, int N, int K,
-                                        void* y, void* workspace, sluice_stream_t stream) {
-  if (T < 0 || T > 16 || N <= 0 || N % 16 != 0 || K <= 0 || K % 64 != 0 || gu == nullptr ||
+extern "C" int sluice_dec_linear_glu(const void* x, const void* w, int T, int N, int K, void* y,
+                                     void* workspace, sluice_stream_t stream) {
+  if (T < 0 || T > 16 || N <= 0 || N % 32 != 0 || K <= 0 || K % 64 != 0 || x == nullptr ||
       w == nullptr || y == nullptr)
     return SLUICE_E_INVAL;
-  if (((uintptr_t)gu | (uintptr_t)w | (uintptr_t)workspace) & 15 || (uintptr_t)y & 7)
+  if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)workspace) & 15 || (uintptr_t)y & 7)
     return SLUICE_E_INVAL;
   if (T == 0) return SLUICE_OK;
-  return launch_linear<true>(gu, w, T, N, K, y, workspace, (hipStream_t)stream);
+  return launch_linear<true>(x, w, T, N, K, y, workspace, (hipStream_t)stream);
 }
 
 extern "C" int sluice_dec_add_rmsnorm(void* x, const void* delta, const void* w, void* out,

@@ -374,7 +374,7 @@ __device__ __forceinline__ void g1_item_bf16(const uint16_t* __restrict__ x,
   const uint16_t* a0 = w13 + ((size_t)slot * 2 * I + (size_t)tile * 16) * H;
   const uint16_t* xr = x + (size_t)(pair >= 0 ? pair / k : 0) * H;
   f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
-  stream_bf16<kTokPlain, kG1D>(a0, a0 + (size_t)I * H, H, xr, 0, c0, c1 - c0, l.stage[wave], ag,
+  stream_bf16<kTokPlain, kG1D>(a0, a0 + (size_t)I * H, H, xr, c0, c1 - c0, l.stage[wave], ag,
                                au);
   l.red[wave][0][lane] = ag;
   l.red[wave][1][lane] = au;
@@ -393,7 +393,7 @@ __device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act,
   const uint16_t* a0 = w2 + ((size_t)slot * H + (size_t)tile2 * 16 * kG2T) * I;
   const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
   f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = a;
-  stream_bf16<COH ? kTokCoh : kTokPlain, kG2D>(a0, a0 + (size_t)16 * I, I, ar, 0, c0, c1 - c0,
+  stream_bf16<COH ? kTokCoh : kTokPlain, kG2D>(a0, a0 + (size_t)16 * I, I, ar, c0, c1 - c0,
                                               l.stage[wave], a, b);
   l.red[wave][0][lane] = a;
   l.red[wave][1][lane] = b;

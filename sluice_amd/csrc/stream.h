@@ -44,22 +44,8 @@ constexpr int kStageVecs = 256;
 // How the token operand is read.
 enum TokMode {
   kTokPlain = 0,  // bf16 rows, ordinary loads
-  kTokCoh = 1,    // bf16 rows written by other workgroups of the same launch
-  kTokSwiglu = 2  // silu(gate) * up of a gate|up row pair (up at +`up` elements),
-                  // rounded to bf16 as the activation kernel rounds it
+  kTokCoh = 1     // bf16 rows written by other workgroups of the same launch
 };
-
-__device__ __forceinline__ u32x4_t swiglu8(u32x4_t g, u32x4_t u) {
-  u32x4_t o;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float g0 = __uint_as_float(g[i] << 16), g1 = __uint_as_float(g[i] & 0xffff0000u);
-    const float u0 = __uint_as_float(u[i] << 16), u1 = __uint_as_float(u[i] & 0xffff0000u);
-    o[i] = (uint32_t)f32_to_bf16_bits(g0 / (1.0f + expf(-g0)) * u0) |
-           ((uint32_t)f32_to_bf16_bits(g1 / (1.0f + expf(-g1)) * u1) << 16);
-  }
-  return o;
-}
 
 // acc0 / acc1 += tile 0 / tile 1 [16 rows, K chunks c0 .. c0+n) . tokens^T.
 // a0, a1: row 0 of each tile (row stride ld elements); b: this lane's token
@@ -68,8 +54,8 @@ __device__ __forceinline__ u32x4_t swiglu8(u32x4_t g, u32x4_t u) {
 template <int TM, int D>
 __device__ __forceinline__ void stream_bf16(const uint16_t* __restrict__ a0,
                                             const uint16_t* __restrict__ a1, size_t ld,
-                                            const uint16_t* __restrict__ b, size_t up, int c0,
-                                            int n, u32x4_t* st, f32x4_t& acc0, f32x4_t& acc1) {
+                                            const uint16_t* __restrict__ b, int c0, int n,
+                                            u32x4_t* st, f32x4_t& acc0, f32x4_t& acc1) {
   if (n <= 0) return;
   const int lane = threadIdx.x & 63;
   const int r = lane >> 3, s = lane & 7;
@@ -80,8 +66,7 @@ __device__ __forceinline__ void stream_bf16(const uint16_t* __restrict__ a0,
   const uint16_t* pb = b + (size_t)c0 * 64 + kb * 16;
   const int wl = r * 8 + (s ^ r), wh = wl + 64;
   const int rd0 = R * 8 + ((2 * kb) ^ (R & 7)), rd1 = R * 8 + ((2 * kb + 1) ^ (R & 7));
-  constexpr int NB = TM == kTokSwiglu ? 4 : 2;
-  u32x4_t q0l[D], q0h[D], q1l[D], q1h[D], xb[D][NB];
+  u32x4_t q0l[D], q0h[D], q1l[D], q1h[D], xb[D][2];
   auto ldb = [&](const uint16_t* p) { return TM == kTokCoh ? ld16_coh(p) : ldg16(p); };
   auto issue = [&](int d, int c) {
     const size_t o = (size_t)c * 64;
@@ -91,10 +76,6 @@ __device__ __forceinline__ void stream_bf16(const uint16_t* __restrict__ a0,
     q1h[d] = ldg16_stream(p1 + ld8 + o);
     xb[d][0] = ldb(pb + o);
     xb[d][1] = ldb(pb + o + 8);
-    if constexpr (TM == kTokSwiglu) {
-      xb[d][2] = ldb(pb + up + o);
-      xb[d][3] = ldb(pb + up + o + 8);
-    }
   };
   auto consume = [&](int d) {
     st[wl] = q0l[d];
@@ -104,11 +85,7 @@ __device__ __forceinline__ void stream_bf16(const uint16_t* __restrict__ a0,
     __builtin_amdgcn_wave_barrier();
     const u32x4_t g0 = st[rd0], g1 = st[rd1], u0 = st[128 + rd0], u1 = st[128 + rd1];
     __builtin_amdgcn_wave_barrier();
-    u32x4_t x0 = xb[d][0], x1 = xb[d][1];
-    if constexpr (TM == kTokSwiglu) {
-      x0 = swiglu8(xb[d][0], xb[d][2]);
-      x1 = swiglu8(xb[d][1], xb[d][3]);
-    }
+    const u32x4_t x0 = xb[d][0], x1 = xb[d][1];
     acc0 = mfma16x16x32_bf16(g0, x0, acc0);
     acc0 = mfma16x16x32_bf16(g1, x1, acc0);
     acc1 = mfma16x16x32_bf16(u0, x0, acc1);

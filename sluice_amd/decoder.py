@@ -265,17 +265,18 @@ def linear(x, w):
     return y
 
 
-def linear_swiglu(gu, w):
-    """y = (silu(gu[:, :K]) * gu[:, K:]) . w^T in one kernel (T <= 16)."""
+def linear_glu(x, w):
+    """silu(x . w[:N/2]^T) * (x . w[N/2:]^T) for decode batches (T <= 16):
+    the gate/up projection with the activation in its epilogue."""
     lib, check = _k()
-    T, K2 = gu.shape
+    T, K = x.shape
     N = w.shape[0]
     if T > 16:
         raise ValueError(f"decode linear supports at most 16 rows, got {T}")
-    y = torch.empty((T, N), dtype=gu.dtype, device=gu.device)
-    check(lib.sluice_dec_linear_swiglu(gu.data_ptr(), w.data_ptr(), T, N, K2 // 2, y.data_ptr(),
-                                       _linear_ws(gu.device).data_ptr(), _stream(gu)),
-          "sluice_dec_linear_swiglu")
+    y = torch.empty((T, N // 2), dtype=x.dtype, device=x.device)
+    check(lib.sluice_dec_linear_glu(x.data_ptr(), w.data_ptr(), T, N, K, y.data_ptr(),
+                                    _linear_ws(x.device).data_ptr(), _stream(x)),
+          "sluice_dec_linear_glu")
     return y
 
 
@@ -392,8 +393,8 @@ class _GQA(nn.Module):
 
 
 class _DenseMLP(nn.Module):
-    """SwiGLU MLP: gate/up GEMM, then the down GEMM with the activation fused
-    into its input loads."""
+    """SwiGLU MLP: the gate/up GEMM with the activation in its epilogue, then
+    the down GEMM."""
 
     def __init__(self, H, I, dev, gen):
         super().__init__()
@@ -402,7 +403,7 @@ class _DenseMLP(nn.Module):
         self.I = I
 
     def forward(self, x):
-        return linear_swiglu(linear(x, self.gate_up), self.down)
+        return linear(linear_glu(x, self.gate_up), self.down)
 
 
 def _expert_store(sp, gen_seed, dev, fp8):

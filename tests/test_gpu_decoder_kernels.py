@@ -104,17 +104,21 @@ def test_linear(T, N, K):
     assert _rel(y, x.float() @ w.float().T) <= TOL
 
 
-@pytest.mark.parametrize("T,N,K", [(8, 2048, 2816), (1, 2048, 10944), (12, 7168, 2048)])
-def test_linear_swiglu(T, N, K):
-    from sluice_amd.decoder import linear_swiglu
+@pytest.mark.parametrize("T,I,K", [(8, 2816, 2048), (1, 10944, 2048), (12, 2048, 7168), (3, 16, 128)])
+def test_linear_glu(T, I, K):
+    """Gate/up projection with SwiGLU applied to the fp32 sums (rows 0..I-1
+    gate, I..2I-1 up) against fp32 torch."""
+    from sluice_amd.decoder import linear_glu
 
-    g = torch.Generator().manual_seed(T + N + K)
-    gu = torch.randn((T, 2 * K), generator=g).bfloat16()
-    w = (0.02 * torch.randn((N, K), generator=g)).bfloat16()
-    y = linear_swiglu(gu.to(DEV), w.to(DEV))
+    g = torch.Generator().manual_seed(T + I + K)
+    x = torch.randn((T, K), generator=g).bfloat16()
+    w = (0.02 * torch.randn((2 * I, K), generator=g)).bfloat16()
+    y = linear_glu(x.to(DEV), w.to(DEV))
     torch.cuda.synchronize()
-    gf, uf = gu.float()[:, :K], gu.float()[:, K:]
-    assert _rel(y, (gf * torch.sigmoid(gf) * uf) @ w.float().T) <= TOL
+    gu = x.float() @ w.float().T
+    gf, uf = gu[:, :I], gu[:, I:]
+    assert y.shape == (T, I)
+    assert _rel(y, gf * torch.sigmoid(gf) * uf) <= TOL
 
 
 def test_linear_split_k_deterministic_and_counters_back_at_zero():
