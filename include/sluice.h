@@ -236,8 +236,9 @@ int sluice_layer_pin(sluice_layer* layer, int local, int debit_protected,
  * Device half, sluice_layer_gap_launch: one workgroup on `stream`, no host
  * call, capturable in a hipGraph.  It builds the step's sorted unique
  * selected ids and the count of owned ids the device map does not hold,
- * posts them to the layer's mailbox (host-mapped pinned memory, stamped with
- * a system-scope release store), copies hs_bytes (multiple of 16, 16-byte
+ * posts them to the layer's mailbox (host-mapped pinned memory; the stamp is
+ * stored after the record's stores have completed), copies hs_bytes
+ * (multiple of 16, 16-byte
  * aligned; 0 = none) from hs_src to hs_dst -- the gap op's fresh copy of
  * hidden_states -- and then waits for the host ONLY if residency must change
  * (a miss, or no standing map yet); it then installs the standing map the
