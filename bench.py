@@ -226,6 +226,20 @@ def kernel_roofline(dec, c, recorded, reps=3):
     us1 = _event_loop(stream, g1, items, reps)
     us2 = _event_loop(stream, g2, items, reps)
     us3 = _event_loop(stream, cb, items, reps)
+    # routing: the decode's router call on fp32 logits of the step's shape
+    # (the logits' values only change which ids win, not the work)
+    from sluice_amd import ops
+
+    m0 = dec.moe_layers[0]
+    gen = torch.Generator(device=dec.dev).manual_seed(3)
+    with torch.cuda.stream(stream):
+        lgs = [torch.randn((c, sp["E"]), generator=gen, device=dec.dev) for _ in range(16)]
+        ids_o = torch.empty((c, k), dtype=torch.int32, device=dec.dev)
+
+    def rt(lg):
+        m0.select_out(lg, ids_o)
+
+    usr = _event_loop(stream, rt, lgs, 8)
     # a plain device copy of known size: the HBM reference for counter scaling
     nb = 256 << 20
     src = torch.empty(nb, dtype=torch.uint8, device=dec.dev)
@@ -242,8 +256,10 @@ def kernel_roofline(dec, c, recorded, reps=3):
     r1["mfma_util_pct"] = 100.0 * float(np.mean(fl)) / (us1 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS
     r2 = res(f"moe_gemm2_kernel<{kind}>", us2, b2)
     r2["mfma_util_pct"] = 100.0 * float(np.mean(fl)) / (us2 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS
+    rb = c * sp["E"] * 4 + (sp["E"] * 4 if sp["e_bias"] else 0) + c * k * 8
     return {"c": c, "launches": reps * len(items), "gemm1": r1, "gemm2": r2,
             "combine": res("moe_combine_kernel", us3, b3),
+            "route": res("route_topk_kernel", usr, [rb]),
             "copy_256MiB_GBs": 2 * nb / (usc * 1e-6) / 1e9}
 
 
@@ -464,7 +480,7 @@ def main():
             "algorithmic_bytes_per_launch": g1["algorithmic_bytes"],
             "mfma_util_pct": g1["mfma_util_pct"],
         }
-        line["kernels"] = {kk: roof[kk] for kk in ("gemm2", "combine")}
+        line["kernels"] = {kk: roof[kk] for kk in ("gemm2", "combine", "route")}
         line["kernels"]["copy_256MiB_GBs"] = roof["copy_256MiB_GBs"]
     if cpu:
         line["cpu_baseline"] = {k_: cpu[k_] for k_ in ("value", "unit", "cores", "kind", "sample")}

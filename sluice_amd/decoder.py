@@ -508,6 +508,15 @@ class _StoreMoELayer(nn.Module):
                                   e_score_correction_bias=self.e_score_correction_bias,
                                   num_expert_group=sp["n_group"], topk_group=sp["topk_group"])
 
+    def select_out(self, lg, ids_out):
+        """select() writing the ids into ids_out (for timing the router alone)."""
+        sp = self.sp
+        return ops.select_experts(lg, sp["k"], scoring=sp["scoring"], renormalize=sp["renorm"],
+                                  routed_scaling_factor=sp["routed_scale"],
+                                  e_score_correction_bias=self.e_score_correction_bias,
+                                  num_expert_group=sp["n_group"], topk_group=sp["topk_group"],
+                                  ids_out=ids_out)
+
     def experts(self, hn, tw, ti, shared_output=None):
         kw = {}
         if self.sp["fp8"]:
