@@ -149,6 +149,32 @@ def _event_loop(stream, fn, items, reps):
     return e0.elapsed_time(e1) * 1e3 / (reps * len(items))
 
 
+def _graph_loop(stream, fn, items, reps):
+    """Like _event_loop for kernels shorter than a host launch: one pass over
+    the items is captured as a hipGraph and replayed, as the decode step runs
+    them (dispatch gaps inside the graph included, host launch cost not)."""
+    import torch
+
+    with torch.cuda.stream(stream):
+        for it in items:  # warm, outside the capture
+            fn(it)
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for it in items:
+            fn(it)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        g.replay()
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+    stream.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * len(items))
+
+
 def kernel_roofline(dec, c, recorded, reps=3):
     """Time the path's kernels with HIP events on their own stream over the
     recorded routing of every layer and step (layers rotate, so the 256 MB
@@ -225,21 +251,25 @@ def kernel_roofline(dec, c, recorded, reps=3):
 
     us1 = _event_loop(stream, g1, items, reps)
     us2 = _event_loop(stream, g2, items, reps)
-    us3 = _event_loop(stream, cb, items, reps)
-    # routing: the decode's router call on fp32 logits of the step's shape
+    us3 = _graph_loop(stream, cb, items, reps)
+    # routing: the decode's router kernel on fp32 logits of the step's shape
     # (the logits' values only change which ids win, not the work)
-    from sluice_amd import ops
+    from sluice_amd.ops import _SCORING
 
-    m0 = dec.moe_layers[0]
+    bias = dec.moe_layers[0].e_score_correction_bias
     gen = torch.Generator(device=dec.dev).manual_seed(3)
     with torch.cuda.stream(stream):
         lgs = [torch.randn((c, sp["E"]), generator=gen, device=dec.dev) for _ in range(16)]
         ids_o = torch.empty((c, k), dtype=torch.int32, device=dec.dev)
+        w_o = torch.empty((c, k), dtype=torch.float32, device=dec.dev)
 
     def rt(lg):
-        m0.select_out(lg, ids_o)
+        lib.sluice_route_topk(lg.data_ptr(), 0, c, sp["E"], k, _SCORING[sp["scoring"]],
+                              int(sp["renorm"]), float(sp["routed_scale"]),
+                              bias.data_ptr() if bias is not None else None, sp["n_group"],
+                              sp["topk_group"], ids_o.data_ptr(), w_o.data_ptr(), st)
 
-    usr = _event_loop(stream, rt, lgs, 8)
+    usr = _graph_loop(stream, rt, lgs, 8)
     # a plain device copy of known size: the HBM reference for counter scaling
     nb = 256 << 20
     src = torch.empty(nb, dtype=torch.uint8, device=dec.dev)

@@ -8,14 +8,15 @@
 //   group's two best biased scores, weights from the unbiased sigmoid,
 //   renormalised and scaled (DeepSeek-V3).
 //
-// Selection is by exact rank, with no sort and no k serial rounds: every
-// candidate's key is published in LDS, then each lane counts, over one pass
-// of broadcast LDS reads, how many eligible keys beat each of its own
-// (greater key, or equal key and lower expert id).  A candidate with rank
-// r < k is the r-th choice, so outputs come out best-first with ties going to
-// the lower id.  Softmax is monotone, so selection runs on the logits
-// themselves; sigmoid scores are evaluated in fp64 and rounded to fp32 once,
-// so that selection on fp32(s + bias) is reproducible bit for bit on the host.
+// Selection: k rounds of a wave-wide argmax over (key, expert id) in the
+// order "greater key, or equal key and lower id", each round reducing with
+// xor-shuffles and retiring the winner in its owning lane.  Round r picks the
+// candidate that exactly r eligible candidates beat, so outputs come out
+// best-first with ties going to the lower id, with no sort and no pass over
+// all E keys per lane (an exact-rank pass of that kind cost ~45 us at
+// E = 256).  Softmax is monotone, so selection runs on the logits themselves;
+// sigmoid scores are evaluated in fp64 and rounded to fp32 once, so that
+// selection on fp32(s + bias) is reproducible bit for bit on the host.
 //
 // The kernel is instantiated per scoring mode and per experts-per-lane (NV =
 // 1, 2, 4, 16) so each launch runs compact straight-line code: a decode step
@@ -49,8 +50,7 @@ __global__ __launch_bounds__(SLUICE_WAVE) void route_topk_kernel(
     const void* __restrict__ logits, int dtype, int E, int k, int renorm, float scale,
     const float* __restrict__ bias, int n_group, int topk_group, int32_t* __restrict__ ids_out,
     float* __restrict__ w_out) {
-  __shared__ float s_key[SLUICE_MAX_EXPERTS];  // selection key; -inf-tagged if ineligible
-  __shared__ uint8_t s_ok[SLUICE_MAX_EXPERTS];
+  __shared__ float s_key[SLUICE_MAX_EXPERTS];  // selection keys (group scores read them)
   __shared__ float s_gscore[SLUICE_WAVE];
   __shared__ int s_gok[SLUICE_WAVE];
   __shared__ int s_sel[SLUICE_MAX_TOPK];
@@ -84,22 +84,41 @@ __global__ __launch_bounds__(SLUICE_WAVE) void route_topk_kernel(
   }
 
   if (n_group > 1) {
-    __syncthreads();
     const int gsize = E / n_group;
-    if (lane < n_group) {
-      const int g0 = lane * gsize;
-      float b1 = -INFINITY, b2 = -INFINITY;
-      for (int e = g0; e < g0 + gsize; ++e) {
-        const float v = s_key[e];
-        if (v > b1) {
-          b2 = b1;
-          b1 = v;
-        } else if (v > b2) {
-          b2 = v;
+    if (gsize <= SLUICE_WAVE && (gsize & (gsize - 1)) == 0) {
+      // A group is gsize consecutive lanes of one register: reduce its two
+      // best keys with xor-shuffles inside the group.
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        float b1 = key[j], b2 = -INFINITY;
+        for (int off = 1; off < gsize; off <<= 1) {
+          const float o1 = __shfl_xor(b1, off, SLUICE_WAVE);
+          const float o2 = __shfl_xor(b2, off, SLUICE_WAVE);
+          const float hi = fmaxf(b1, o1), lo = fminf(b1, o1);
+          b2 = fmaxf(lo, fmaxf(b2, o2));
+          b1 = hi;
         }
+        const int e = lane + j * SLUICE_WAVE;
+        // softmax: group max; sigmoid: sum of the two best biased scores
+        if (e < E && (e & (gsize - 1)) == 0)
+          s_gscore[e / gsize] = (SCORING == 0 || gsize < 2) ? b1 : b1 + b2;
       }
-      // softmax: group max; sigmoid: sum of the two best biased scores
-      s_gscore[lane] = (SCORING == 0 || gsize < 2) ? b1 : b1 + b2;
+    } else {
+      __syncthreads();
+      if (lane < n_group) {
+        const int g0 = lane * gsize;
+        float b1 = -INFINITY, b2 = -INFINITY;
+        for (int e = g0; e < g0 + gsize; ++e) {
+          const float v = s_key[e];
+          if (v > b1) {
+            b2 = b1;
+            b1 = v;
+          } else if (v > b2) {
+            b2 = v;
+          }
+        }
+        s_gscore[lane] = (SCORING == 0 || gsize < 2) ? b1 : b1 + b2;
+      }
     }
     __syncthreads();
     if (lane < n_group) {
@@ -118,29 +137,45 @@ __global__ __launch_bounds__(SLUICE_WAVE) void route_topk_kernel(
       if (ok[j]) ok[j] = s_gok[e / gsize] != 0;
     }
   }
+  // k rounds of a wave argmax; the winner's owner records it and retires it.
+  bool live[NV];
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int e = lane + j * SLUICE_WAVE;
-    if (e < E) s_ok[e] = ok[j] ? 1 : 0;
-  }
-  __syncthreads();
-
-  // Exact rank of each eligible candidate among the eligible keys.
-  int rank[NV];
-#pragma unroll
-  for (int j = 0; j < NV; ++j) rank[j] = 0;
-#pragma unroll 8
-  for (int e2 = 0; e2 < E; ++e2) {
-    const float v2 = s_key[e2];
-    const bool ok2 = s_ok[e2] != 0;
+  for (int j = 0; j < NV; ++j) live[j] = ok[j];
+  for (int r = 0; r < k; ++r) {
+    float bk = -INFINITY;
+    int bi = 0x7fffffff;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int e = lane + j * SLUICE_WAVE;
-      rank[j] += (ok2 && (v2 > key[j] || (v2 == key[j] && e2 < e))) ? 1 : 0;
+      if (live[j] && (key[j] > bk || (key[j] == bk && e < bi))) {
+        bk = key[j];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ok2 = __shfl_xor(bk, off, SLUICE_WAVE);
+      const int oi = __shfl_xor(bi, off, SLUICE_WAVE);
+      if (ok2 > bk || (ok2 == bk && oi < bi)) {
+        bk = ok2;
+        bi = oi;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      if (bi == lane + j * SLUICE_WAVE) {
+        live[j] = false;
+        s_sel[r] = bi;
+        s_w[r] = raw[j];  // softmax: the logit, weighted below
+      }
+    }
+    if (bi == 0x7fffffff && lane == 0) {  // only NaN keys left: no expert, no weight
+      s_sel[r] = -1;
+      s_w[r] = SCORING == 0 ? -INFINITY : 0.0f;
     }
   }
 
-  // Un-normalised weights of the winners, in rank order.
+  // Weights of the winners, in selection order.
   float m = 0.0f, z = 1.0f;
   if (SCORING == 0) {
     m = wave_max(lmax);
@@ -150,13 +185,8 @@ __global__ __launch_bounds__(SLUICE_WAVE) void route_topk_kernel(
       if (lane + j * SLUICE_WAVE < E) part += expf(raw[j] - m);
     z = wave_sum(part);
   }
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    if (ok[j] && rank[j] < k) {
-      s_sel[rank[j]] = lane + j * SLUICE_WAVE;
-      s_w[rank[j]] = SCORING == 0 ? expf(raw[j] - m) / z : raw[j];
-    }
-  }
+  __syncthreads();
+  if (SCORING == 0 && lane < k) s_w[lane] = expf(s_w[lane] - m) / z;
   __syncthreads();
   if (lane < k) {
     float w = s_w[lane];
