@@ -18,6 +18,13 @@ compared bit for bit with the native implementation:
                    hit touches, miss acquisition with the claimed set seeded by
                    the step's hit slots, overflow, standing-map refresh)
   pins             src/sluice/offloader.py:1046-1083
+  classic step     src/sluice/offloader.py:1452-1765 (run_moe with the
+                   defaults: no lazy/hook-lite/prefill-block/LFU modes) and
+                   1846-1933 (_run_waves): decode/scan classification from the
+                   step's decode counts, class-aware touches and acquisition,
+                   wave 0 = hits + the fills that fit, the rest rotated through
+                   the probation slots in two ping-pong groups, one sparse map
+                   per wave
 """
 
 from __future__ import annotations
@@ -176,6 +183,94 @@ class LayerCache:
         if changed or not self.map_is_standing:
             self.write_standing_map()
         return streams
+
+    # -- the classic (wave) step ---------------------------------------------
+    def classic(self, ids, T: int, nd=None, ndec=None, real_step: bool = True,
+                spec_tokens: int = 0):
+        """One classic step on the flat row-major [T, k] list of selected
+        global ids; nd / ndec: the step's decode-token / decode-request counts
+        (None when the engine publishes none), real_step False for dummy runs.
+
+        Returns the waves in execution order, each a dict with "pairs"
+        ([(global, slot)] written as that wave's map, every other entry -1)
+        and "streams" ([(local, slot)] copied before that wave runs)."""
+        ids_list = [int(v) for v in ids]
+        k = len(ids_list) // T if T else 0
+        selected = sorted(set(ids_list))
+        decode_span = ndec * (1 + spec_tokens) if ndec is not None else None
+        pure_decode_region = (real_step and nd is not None and decode_span is not None
+                              and nd == decode_span)
+        if pure_decode_region and 0 < nd <= T:
+            decode_ids = set(selected) if nd == T else set(ids_list[:nd * k])
+        else:
+            decode_ids = None
+        n_global = len(self.local_of)
+        pairs = []
+        for g in selected:
+            if 0 <= g < n_global:
+                loc = self.local_of[g]
+                if loc >= 0:
+                    pairs.append((g, loc, decode_ids is not None and g in decode_ids))
+        ws = len(pairs)
+        mla_forced_scan = real_step and nd is not None and not pure_decode_region
+        if decode_ids is None and not mla_forced_scan:
+            decode_cap = self.protected_cap + len(self.pinned_slots)
+            if real_step and ws <= max(decode_cap, 1):
+                pairs = [(g, loc, True) for g, loc, _ in pairs]
+        if ws == 0:
+            self.map = [-1] * self.global_n
+            self.map_is_standing = False
+            return [{"pairs": [], "streams": []}]
+        hits, missing = [], []
+        for g, loc, dcls in pairs:
+            slot = self.slot_of.get(loc)
+            if slot is None:
+                missing.append((g, loc, dcls))
+            else:
+                self.touch(slot, dcls)
+                hits.append((g, slot))
+        missing.sort(key=lambda t: not t[2])
+        claimed = {slot for _, slot in hits}
+        wave0 = list(hits)
+        streams0 = []
+        taken = len(missing)
+        for i, (g, loc, dcls) in enumerate(missing):
+            slot = self.acquire_slot(loc, claimed, allow_protected=dcls)
+            if slot is None:
+                taken = i
+                break
+            streams0.append((loc, slot))
+            wave0.append((g, slot))
+            claimed.add(slot)
+        self.misses += len(missing)
+        leftover = [(g, loc) for g, loc, _ in missing[taken:]]
+        waves = [{"pairs": wave0, "streams": streams0}]
+        if leftover:
+            rot = list(self.probation.keys())
+            if not rot:
+                rot = [s for s in range(self.num_slots)
+                       if s not in self.pinned_slots][-max(1, self.num_slots // 4):]
+            half = (len(rot) + 1) // 2
+            group_a, group_b = rot[:half], rot[half:]
+            groups = (group_a, group_b if group_b else group_a)
+            i = 0
+            gi = 0
+            while i < len(leftover):
+                group = groups[gi % 2]
+                chunk = []
+                for (g, loc), slot in zip(leftover[i:i + len(group)], group):
+                    self.evict_to(slot, loc)
+                    chunk.append((g, loc, slot))
+                waves.append({"pairs": [(g, slot) for g, _, slot in chunk],
+                              "streams": [(loc, slot) for _, loc, slot in chunk]})
+                i += len(chunk)
+                gi += 1
+        last = [-1] * self.global_n
+        for g, slot in waves[-1]["pairs"]:
+            last[g] = slot
+        self.map = last
+        self.map_is_standing = False
+        return waves
 
     def snapshot(self) -> dict:
         return {

@@ -47,6 +47,22 @@ def slru_golden():
     return slru_vectors()
 
 
+_CLASSIC = None
+
+
+def classic_vectors():
+    global _CLASSIC
+    if _CLASSIC is None:
+        with gzip.open(os.path.join(GOLDEN, "classic_vectors.json.gz"), "rt") as f:
+            _CLASSIC = json.load(f)
+    return _CLASSIC
+
+
+@pytest.fixture(scope="session")
+def classic_golden():
+    return classic_vectors()
+
+
 @pytest.fixture(scope="session")
 def lib():
     from sluice_amd import _lib
