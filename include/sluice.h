@@ -294,6 +294,51 @@ int sluice_layer_gap_host(sluice_layer* layer, const int32_t* ids, int n,
                           int fast_hit, int32_t* streams, int max_streams,
                           int* n_streams, int* map_written);
 
+/* Classic (wave) step: replaces run_moe (src/sluice/offloader.py:1452-1765)
+ * and _run_waves (1846-1933), the path of steps the gap does not take (more
+ * tokens than the router-split envelope, prefill chunks).
+ *
+ * sluice_layer_classic_plan: copies topk_ids [n] (int32, device, row-major
+ * [T, n/T]) to the host on `stream` and synchronises it (the reference's one
+ * host sync per layer, 1552); with a gap server attached, waits until the
+ * layer's posted gap records are served; then runs the reference's
+ * bookkeeping exactly: decode classification from nd / ndec (< 0 = not
+ * published) / real_step / spec_tokens, class-aware touches and fills,
+ * decode-class misses first, leftover misses rotated through the probation
+ * slots in two ping-pong groups.  *n_waves >= 1.  Refuses a capturing
+ * stream (SLUICE_E_STATE).  The map stops being the standing map; the
+ * layer's next gap reinstalls it.
+ *
+ * Then, for w = 0 .. n_waves-1, the caller enqueues the expert product on
+ * `stream` between sluice_layer_classic_wave(w) -- writes wave w's map
+ * (its (global, slot) pairs, -1 elsewhere), and makes `stream` wait for the
+ * wave's row copies, which run on the library's copy stream (wave 0's after
+ * the work already on `stream`) -- and sluice_layer_classic_wave_done(w),
+ * which records the wave's end and issues wave w+1's copies behind the
+ * kernel that last read those slots.  The caller sums the wave outputs.
+ * Waves must run in order; a plan left unfinished has its remaining copies
+ * issued by the next plan. */
+int sluice_layer_classic_plan(sluice_layer* layer, const int32_t* topk_ids,
+                              int n, int T, int nd, int ndec, int real_step,
+                              int spec_tokens, sluice_stream_t stream,
+                              int* n_waves);
+int sluice_layer_classic_wave(sluice_layer* layer, int wave,
+                              sluice_stream_t stream);
+int sluice_layer_classic_wave_done(sluice_layer* layer, int wave,
+                                   sluice_stream_t stream);
+
+/* The classic step's bookkeeping on host ids (no HIP calls). */
+int sluice_layer_classic_host(sluice_layer* layer, const int32_t* ids, int n,
+                              int T, int nd, int ndec, int real_step,
+                              int spec_tokens, int* n_waves);
+
+/* The last classic plan: out = [n_waves, pipelined, then per wave: n_pairs,
+ * n_pairs x (global, slot), n_streams, n_streams x (local, slot)]; *len is
+ * its length (out may be NULL to size it).  counters[2] (may be NULL) =
+ * {classic steps, classic waves}. */
+int sluice_layer_classic_plan_read(const sluice_layer* layer, int32_t* out,
+                                   int cap, int* len, int64_t* counters);
+
 /* State snapshot.  Arrays may be NULL.  slot_of [local_n] (-1 = absent),
  * expert_in_slot [S] (-1 = empty), probation/protected in recency order
  * (LRU first), free_slots in list order (the last is popped next).

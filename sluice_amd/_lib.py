@@ -86,6 +86,15 @@ SIGNATURES = {
         [_P, _P, _P, _P, POINTER(c_int), _P, POINTER(c_int), _P, POINTER(c_int), _P],
     ),
     "sluice_layer_standing_map": (c_int, [_P, _P]),
+    "sluice_layer_classic_plan": (
+        c_int, [_P, _P, c_int, c_int, c_int, c_int, c_int, c_int, _P, POINTER(c_int)]
+    ),
+    "sluice_layer_classic_wave": (c_int, [_P, c_int, _P]),
+    "sluice_layer_classic_wave_done": (c_int, [_P, c_int, _P]),
+    "sluice_layer_classic_host": (
+        c_int, [_P, _P, c_int, c_int, c_int, c_int, c_int, c_int, POINTER(c_int)]
+    ),
+    "sluice_layer_classic_plan_read": (c_int, [_P, _P, c_int, POINTER(c_int), _P]),
     # include/sluice_decoder.h
     "sluice_dec_add_rmsnorm": (c_int, [_P, _P, _P, _P, c_int, c_int, c_float, _P]),
     "sluice_dec_silu_mul": (c_int, [_P, _P, c_int, c_int, _P]),

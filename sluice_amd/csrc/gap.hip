@@ -115,9 +115,14 @@ struct SlotTable {
   int32_t g[SLUICE_MAX_SLOTS];
 };
 
+// map[g] = s for every slot s holding global id g, -1 elsewhere.  A classic
+// wave also clears the device's "standing map seen" flag (standing_flag),
+// so the layer's next gap waits for the host to reinstall the standing map.
 __global__ __launch_bounds__(256) void map_refresh_kernel(int32_t* __restrict__ map, int E,
-                                                          SlotTable tab) {
+                                                          SlotTable tab,
+                                                          int32_t* __restrict__ standing_flag) {
   __shared__ int m[SLUICE_MAX_EXPERTS];
+  if (standing_flag != nullptr && threadIdx.x == 0) *standing_flag = 0;
   for (int e = threadIdx.x; e < E; e += 256) m[e] = -1;
   __syncthreads();
   for (int s = threadIdx.x; s < tab.n; s += 256) {
@@ -395,7 +400,16 @@ struct sluice_layer {
   sluice_gap_server* server = nullptr;
   std::vector<int> streams;
   std::vector<int32_t> uniq;
-  // standalone lookup record for the eager path of sluice_slot_lookup users
+  // classic (wave) step: the plan, how far it has run, and its events
+  slru::Plan plan;
+  int plan_next = 0;          // next wave to run
+  bool plan_in_wave = false;  // between classic_wave and classic_wave_done
+  int plan_copied = 0;        // waves whose row copies have been issued
+  std::vector<hipEvent_t> wave_ev, copy_ev;
+  hipEvent_t pre_ev = nullptr;
+  int32_t* ids_host = nullptr;  // pinned staging of the step's ids
+  size_t ids_cap = 0;
+  int64_t classic_steps = 0, classic_waves = 0;
 };
 
 namespace {
@@ -471,13 +485,16 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
   std::lock_guard<std::mutex> lk(L->mu);
   L->streams.clear();
   bool map_write = false;
+  // The device counts misses against the map it holds; only a standing map
+  // holds every resident expert (a classic wave's map holds that wave's).
+  const bool was_standing = L->c.map_is_standing;
   const int grc = L->c.gap(L->uniq.data(), n_uniq, fast_hit, L->streams, map_write);
   const int n_streams = (int)L->streams.size() / 2;
   int rc = SLUICE_OK;
   if (!waits) {
     // The device ran on with its map: the host must agree nothing changed.
     if (grc != 0 || n_streams != 0 || map_write || n_miss != 0) rc = SLUICE_E_STATE;
-  } else if (grc == 0 && n_streams != n_miss) {
+  } else if (grc == 0 && was_standing && n_streams != n_miss) {
     rc = SLUICE_E_STATE;
   } else if (n_streams > 0) {
     // On overflow the rows acquired before it still stream, as in the
@@ -594,6 +611,13 @@ extern "C" int sluice_layer_destroy(sluice_layer* L) {
     hipError_t e = hipFree(L->dev_block);
     if (e != hipSuccess) rc = (int)e;
   }
+  if (L->ids_host != nullptr) {
+    hipError_t e = hipHostFree(L->ids_host);
+    if (e != hipSuccess) rc = (int)e;
+  }
+  for (std::vector<hipEvent_t>* v : {&L->wave_ev, &L->copy_ev})
+    for (hipEvent_t ev : *v) (void)hipEventDestroy(ev);
+  if (L->pre_ev != nullptr) (void)hipEventDestroy(L->pre_ev);
   delete L;
   return rc;
 }
@@ -762,6 +786,254 @@ extern "C" int sluice_layer_gap_host(sluice_layer* L, const int32_t* ids, int n,
   return rc;
 }
 
+// ---------------------------------------------------------------------------
+// Classic (wave) step: run_moe + _run_waves (src/sluice/offloader.py:
+// 1452-1765, 1846-1933) for steps the gap does not take (more tokens than
+// the router-split envelope, prefill chunks).  plan: one host sync for the
+// ids, then the bookkeeping; the caller then runs the expert product once
+// per wave between classic_wave and classic_wave_done, which order the
+// wave's map write and row copies around it.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int kClassicMaxIds = 1 << 24;
+
+int ensure_events(sluice_layer* L, size_t n) {
+  for (std::vector<hipEvent_t>* v : {&L->wave_ev, &L->copy_ev}) {
+    while (v->size() < n) {
+      hipEvent_t ev = nullptr;
+      SLUICE_HIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+      v->push_back(ev);
+    }
+  }
+  if (L->pre_ev == nullptr)
+    SLUICE_HIP_CHECK(hipEventCreateWithFlags(&L->pre_ev, hipEventDisableTiming));
+  return SLUICE_OK;
+}
+
+// Row copies of wave w on the copy stream (after whatever it waits on).
+int issue_wave_copies(sluice_layer* L, int w, hipStream_t copy) {
+  std::lock_guard<std::mutex> lk(L->mu);
+  const slru::Wave& W = L->plan.waves[w];
+  for (int i = 0; i < W.ns; ++i) {
+    const int local = L->plan.streams[2 * (W.s0 + i)];
+    const int slot = L->plan.streams[2 * (W.s0 + i) + 1];
+    for (const ParamRows& p : L->params) {
+      SLUICE_HIP_CHECK(hipMemcpyAsync(p.slot_base + (size_t)slot * p.row_bytes,
+                                      p.host_base + (size_t)local * p.row_bytes, p.row_bytes,
+                                      hipMemcpyHostToDevice, copy));
+      L->bytes += (int64_t)p.row_bytes;
+    }
+  }
+  return SLUICE_OK;
+}
+
+// A plan whose waves did not all run (the caller failed between waves)
+// still owes the copies its bookkeeping assumed: issue them behind `st`.
+int classic_flush(sluice_layer* L, hipStream_t st) {
+  const int nW = (int)L->plan.waves.size();
+  if (L->plan_copied < nW) {
+    DeviceRes* R = nullptr;
+    int rc = device_res(L->device, &R);
+    if (rc) return rc;
+    rc = ensure_events(L, (size_t)nW);
+    if (rc) return rc;
+    SLUICE_HIP_CHECK(hipEventRecord(L->pre_ev, st));
+    SLUICE_HIP_CHECK(hipStreamWaitEvent(R->copy, L->pre_ev, 0));
+    for (int w = L->plan_copied; w < nW; ++w) {
+      rc = issue_wave_copies(L, w, R->copy);
+      if (rc) return rc;
+    }
+    SLUICE_HIP_CHECK(hipEventRecord(L->pre_ev, R->copy));
+    SLUICE_HIP_CHECK(hipStreamWaitEvent(st, L->pre_ev, 0));
+  }
+  L->plan.clear();
+  L->plan_next = L->plan_copied = 0;
+  L->plan_in_wave = false;
+  return SLUICE_OK;
+}
+
+// With a gap server attached: wait until every record this layer posted has
+// been served, so the bookkeeping below does not race the server thread.
+int wait_served(sluice_layer* L) {
+  const double t0 = now_s();
+  for (;;) {
+    const int dev_status = __atomic_load_n(&L->mb->dev_status, __ATOMIC_ACQUIRE);
+    if (dev_status != 0) return dev_status;
+    if (L->server != nullptr) {
+      const int err = sluice_gap_server_error(L->server);
+      if (err != 0) return err;
+    }
+    const int32_t posted = __atomic_load_n(&L->mb->req_stamp, __ATOMIC_ACQUIRE);
+    if (L->done_stamp.load(std::memory_order_acquire) == posted) return SLUICE_OK;
+    if (now_s() - t0 > gap_timeout_s()) return SLUICE_E_TIMEOUT;
+    _mm_pause();
+  }
+}
+
+void serialize_plan(const slru::Plan& P, std::vector<int32_t>& out) {
+  out.clear();
+  out.push_back((int32_t)P.waves.size());
+  out.push_back(P.pipelined ? 1 : 0);
+  for (const slru::Wave& W : P.waves) {
+    out.push_back(W.np);
+    out.insert(out.end(), P.pairs.begin() + 2 * W.p0, P.pairs.begin() + 2 * (W.p0 + W.np));
+    out.push_back(W.ns);
+    out.insert(out.end(), P.streams.begin() + 2 * W.s0, P.streams.begin() + 2 * (W.s0 + W.ns));
+  }
+}
+
+bool classic_args_ok(int n, int T, const int32_t* ids, int spec_tokens) {
+  if (n < 0 || T < 0 || n > kClassicMaxIds || spec_tokens < 0) return false;
+  if (n > 0 && ids == nullptr) return false;
+  if (T == 0) return n == 0;
+  return n % T == 0;
+}
+
+}  // namespace
+
+extern "C" int sluice_layer_classic_plan(sluice_layer* L, const int32_t* topk_ids, int n, int T,
+                                         int nd, int ndec, int real_step, int spec_tokens,
+                                         sluice_stream_t stream, int* n_waves) {
+  if (L == nullptr || n_waves == nullptr || !classic_args_ok(n, T, topk_ids, spec_tokens))
+    return SLUICE_E_INVAL;
+  if (L->mb == nullptr || L->map_dev == nullptr) return SLUICE_E_STATE;
+  hipStream_t st = (hipStream_t)stream;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  SLUICE_HIP_CHECK(hipStreamIsCapturing(st, &cs));
+  if (cs != hipStreamCaptureStatusNone) return SLUICE_E_STATE;  // needs a host sync
+  int rc = classic_flush(L, st);
+  if (rc) return rc;
+  if ((size_t)n > L->ids_cap) {
+    if (L->ids_host != nullptr) SLUICE_HIP_CHECK(hipHostFree(L->ids_host));
+    L->ids_host = nullptr;
+    L->ids_cap = 0;
+    size_t cap = 4096;
+    while (cap < (size_t)n) cap *= 2;
+    void* p = nullptr;
+    SLUICE_HIP_CHECK(hipHostMalloc(&p, cap * sizeof(int32_t), hipHostMallocPortable));
+    L->ids_host = static_cast<int32_t*>(p);
+    L->ids_cap = cap;
+  }
+  // the one host sync of the step (src/sluice/offloader.py:1552)
+  if (n > 0)
+    SLUICE_HIP_CHECK(hipMemcpyAsync(L->ids_host, topk_ids, sizeof(int32_t) * (size_t)n,
+                                    hipMemcpyDeviceToHost, st));
+  SLUICE_HIP_CHECK(hipStreamSynchronize(st));
+  if (L->server != nullptr) {
+    rc = wait_served(L);
+    if (rc) return rc;
+  }
+  {
+    std::lock_guard<std::mutex> lk(L->mu);
+    rc = L->c.classic(L->ids_host, n, T, nd, ndec, real_step != 0, spec_tokens, L->plan);
+    if (rc) {
+      L->plan.clear();
+      return SLUICE_E_STATE;
+    }
+    ++L->classic_steps;
+    L->classic_waves += (int64_t)L->plan.waves.size();
+  }
+  // the map stops being the standing map with the first wave's write
+  __atomic_store_n(&L->mb->standing, 0, __ATOMIC_RELEASE);
+  *n_waves = (int)L->plan.waves.size();
+  return SLUICE_OK;
+}
+
+extern "C" int sluice_layer_classic_wave(sluice_layer* L, int wave, sluice_stream_t stream) {
+  if (L == nullptr || wave < 0) return SLUICE_E_INVAL;
+  const int nW = (int)L->plan.waves.size();
+  if (wave >= nW || wave != L->plan_next || L->plan_in_wave) return SLUICE_E_STATE;
+  hipStream_t st = (hipStream_t)stream;
+  DeviceRes* R = nullptr;
+  int rc = device_res(L->device, &R);
+  if (rc) return rc;
+  rc = ensure_events(L, (size_t)nW);
+  if (rc) return rc;
+  const slru::Wave& W = L->plan.waves[wave];
+  if (wave == 0) {
+    if (W.ns > 0) {
+      // fills may overwrite a slot that earlier work on `st` reads
+      SLUICE_HIP_CHECK(hipEventRecord(L->pre_ev, st));
+      SLUICE_HIP_CHECK(hipStreamWaitEvent(R->copy, L->pre_ev, 0));
+      rc = issue_wave_copies(L, 0, R->copy);
+      if (rc) return rc;
+      SLUICE_HIP_CHECK(hipEventRecord(L->copy_ev[0], R->copy));
+    }
+    L->plan_copied = 1;
+  }
+  SlotTable tab;
+  tab.n = L->c.S;
+  for (int s = 0; s < L->c.S; ++s) tab.g[s] = -1;
+  for (int i = 0; i < W.np; ++i) tab.g[L->plan.pairs[2 * (W.p0 + i) + 1]] = L->plan.pairs[2 * (W.p0 + i)];
+  hipLaunchKernelGGL(map_refresh_kernel, dim3(1), dim3(256), 0, st, L->map_dev, L->c.E, tab,
+                     L->dev_block + L->c.E + 1);
+  SLUICE_HIP_CHECK(hipGetLastError());
+  if (W.ns > 0) SLUICE_HIP_CHECK(hipStreamWaitEvent(st, L->copy_ev[wave], 0));
+  L->plan_in_wave = true;
+  return SLUICE_OK;
+}
+
+extern "C" int sluice_layer_classic_wave_done(sluice_layer* L, int wave, sluice_stream_t stream) {
+  if (L == nullptr || wave < 0) return SLUICE_E_INVAL;
+  const int nW = (int)L->plan.waves.size();
+  if (wave >= nW || wave != L->plan_next || !L->plan_in_wave) return SLUICE_E_STATE;
+  hipStream_t st = (hipStream_t)stream;
+  SLUICE_HIP_CHECK(hipEventRecord(L->wave_ev[wave], st));
+  L->plan_in_wave = false;
+  L->plan_next = wave + 1;
+  if (wave + 1 < nW) {
+    // Wave w+1's rows go into slots the kernel of wave w-1 (ping-pong: the
+    // other group was read by wave w) or of wave w (one group) read last;
+    // wave 0 maps every slot it uses, so it is the floor (1893-1913).
+    DeviceRes* R = nullptr;
+    int rc = device_res(L->device, &R);
+    if (rc) return rc;
+    const int dep = L->plan.pipelined ? (wave > 0 ? wave - 1 : 0) : wave;
+    SLUICE_HIP_CHECK(hipStreamWaitEvent(R->copy, L->wave_ev[dep], 0));
+    rc = issue_wave_copies(L, wave + 1, R->copy);
+    if (rc) return rc;
+    SLUICE_HIP_CHECK(hipEventRecord(L->copy_ev[wave + 1], R->copy));
+    L->plan_copied = wave + 2;
+  }
+  return SLUICE_OK;
+}
+
+extern "C" int sluice_layer_classic_host(sluice_layer* L, const int32_t* ids, int n, int T, int nd,
+                                         int ndec, int real_step, int spec_tokens, int* n_waves) {
+  if (L == nullptr || !classic_args_ok(n, T, ids, spec_tokens)) return SLUICE_E_INVAL;
+  if (L->server != nullptr) return SLUICE_E_STATE;
+  std::lock_guard<std::mutex> lk(L->mu);
+  const int rc = L->c.classic(ids, n, T, nd, ndec, real_step != 0, spec_tokens, L->plan);
+  L->plan_next = L->plan_copied = (int)L->plan.waves.size();  // nothing to copy on the host
+  L->plan_in_wave = false;
+  if (rc) return SLUICE_E_STATE;
+  ++L->classic_steps;
+  L->classic_waves += (int64_t)L->plan.waves.size();
+  for (const ParamRows& p : L->params)
+    L->bytes += (int64_t)(L->plan.streams.size() / 2) * (int64_t)p.row_bytes;
+  if (n_waves) *n_waves = (int)L->plan.waves.size();
+  return SLUICE_OK;
+}
+
+extern "C" int sluice_layer_classic_plan_read(const sluice_layer* Lc, int32_t* out, int cap,
+                                              int* len, int64_t* counters) {
+  if (Lc == nullptr) return SLUICE_E_INVAL;
+  sluice_layer* L = const_cast<sluice_layer*>(Lc);
+  std::lock_guard<std::mutex> lk(L->mu);
+  std::vector<int32_t> v;
+  serialize_plan(L->plan, v);
+  if (len) *len = (int)v.size();
+  if (counters) {
+    counters[0] = L->classic_steps;
+    counters[1] = L->classic_waves;
+  }
+  if (out == nullptr) return SLUICE_OK;
+  if ((int)v.size() > cap) return SLUICE_E_INVAL;
+  for (size_t i = 0; i < v.size(); ++i) out[i] = v[i];
+  return SLUICE_OK;
+}
+
 extern "C" int sluice_layer_state(const sluice_layer* Lc, int32_t* slot_of, int32_t* expert_in_slot,
                                   int32_t* probation, int* n_probation, int32_t* protected_,
                                   int* n_protected, int32_t* free_slots, int* n_free,
@@ -825,7 +1097,7 @@ extern "C" int sluice_map_refresh(int32_t* expert_map, int E, const int32_t* slo
   tab.n = S;
   for (int s = 0; s < S; ++s) tab.g[s] = slot_global[s];
   hipLaunchKernelGGL(map_refresh_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, expert_map, E,
-                     tab);
+                     tab, (int32_t*)nullptr);
   return (int)hipGetLastError();
 }
 

@@ -7,6 +7,7 @@
 //   _coldest_protected (LRU)      src/sluice/offloader.py:2023-2034
 //   _acquire_slot / _evict_to     src/sluice/offloader.py:2036-2081
 //   _router_split_gap bookkeeping src/sluice/offloader.py:2405-2467
+//   run_moe / _run_waves planning src/sluice/offloader.py:1552-1765, 1846-1890
 // The reference keeps its two segments in OrderedDicts keyed by slot
 // (insertion order = recency, first = LRU).  Here each segment is an
 // intrusive doubly-linked list over slot indices with O(1) unlink and
@@ -17,6 +18,7 @@
 
 #include <stdint.h>
 
+#include <algorithm>
 #include <vector>
 
 namespace slru {
@@ -25,6 +27,40 @@ enum Seg : uint8_t { kNone = 0, kProbation = 1, kProtected = 2, kPinned = 3 };
 
 struct List {
   int head = -1, tail = -1, size = 0;
+};
+
+// One wave of a classic step: pairs [p0, p0 + np) of Plan::pairs are the
+// (global, slot) entries of the map the wave runs with (every other entry
+// -1); streams [s0, s0 + ns) of Plan::streams are the (local, slot) rows
+// copied in before it runs.
+struct Wave {
+  int p0, np, s0, ns;
+};
+
+struct Plan {
+  std::vector<Wave> waves;
+  std::vector<int32_t> pairs;    // (global, slot) flattened
+  std::vector<int32_t> streams;  // (local, slot) flattened
+  bool pipelined = false;        // waves >= 1 alternate between two slot groups
+  void clear() {
+    waves.clear();
+    pairs.clear();
+    streams.clear();
+    pipelined = false;
+  }
+  void open_wave() {
+    waves.push_back({(int)pairs.size() / 2, 0, (int)streams.size() / 2, 0});
+  }
+  void add_pair(int g, int slot) {
+    pairs.push_back(g);
+    pairs.push_back(slot);
+    ++waves.back().np;
+  }
+  void add_stream(int local, int slot) {
+    streams.push_back(local);
+    streams.push_back(slot);
+    ++waves.back().ns;
+  }
 };
 
 struct Cache {
@@ -40,9 +76,16 @@ struct Cache {
   bool map_is_standing = false;
   int64_t gaps = 0, misses = 0, fast_hits = 0, map_writes = 0;
 
-  // scratch reused across gaps
+  // scratch reused across gaps and classic steps
+  struct Pair {
+    int g, local;
+    bool dcls;
+  };
   std::vector<uint8_t> claimed;
   std::vector<int> missing;
+  std::vector<uint8_t> present, decode;
+  std::vector<Pair> cl_pairs, cl_missing;
+  std::vector<int> rot;
 
   void init(int E_, int local_n_, int S_, int cap, const int32_t* lof) {
     E = E_;
@@ -216,6 +259,112 @@ struct Cache {
       map_write = true;
       ++map_writes;
       map_is_standing = true;
+    }
+    return 0;
+  }
+
+  // Classic step (run_moe, src/sluice/offloader.py:1552-1765, and the
+  // planning half of _run_waves, 1855-1890) on the flat row-major [T, k]
+  // ids.  nd / ndec: the step's decode-token / decode-request counts, < 0
+  // when the engine publishes none; real_step false for dummy runs.  Fills
+  // `plan` with the waves in execution order.  Returns 0, or -1 when the
+  // leftover misses have no slot to rotate through (every slot pinned;
+  // the reference would loop forever).
+  int classic(const int32_t* ids, int n, int T, int nd, int ndec, bool real_step,
+              int spec_tokens, Plan& plan) {
+    plan.clear();
+    const int k = T > 0 ? n / T : 0;
+    present.assign(E, 0);
+    for (int i = 0; i < n; ++i)
+      if ((unsigned)ids[i] < (unsigned)E) present[ids[i]] = 1;
+    // Decode-hot rows [0, nd) only when they are all one-token decodes:
+    // nd == ndec * (1 + spec_tokens) (1568-1576).
+    const bool has_nd = nd >= 0, has_ndec = ndec >= 0;
+    const long long span = has_ndec ? (long long)ndec * (1 + spec_tokens) : -1;
+    const bool pure_region = real_step && has_nd && has_ndec && (long long)nd == span;
+    const bool have_dec = pure_region && nd > 0 && nd <= T;
+    decode.assign(E, 0);
+    if (have_dec) {
+      if (nd == T) {
+        decode = present;
+      } else {
+        const int m = nd * k < n ? nd * k : n;
+        for (int i = 0; i < m; ++i)
+          if ((unsigned)ids[i] < (unsigned)E) decode[ids[i]] = 1;
+      }
+    }
+    cl_pairs.clear();  // (global, local, decode class) in ascending global id
+    for (int g = 0; g < E; ++g)
+      if (present[g] && local_of[g] >= 0) cl_pairs.push_back({g, local_of[g], decode[g] != 0});
+    const int ws = (int)cl_pairs.size();
+    // No per-token signal: real steps whose working set fits the decode
+    // capacity (pinned + protected) count as decode-class (1620-1637).
+    const bool forced_scan = real_step && has_nd && !pure_region;
+    if (!have_dec && !forced_scan) {
+      int n_pinned = 0;
+      for (int s = 0; s < S; ++s) n_pinned += seg[s] == kPinned;
+      const int cap = protected_cap + n_pinned;
+      if (real_step && ws <= (cap > 1 ? cap : 1))
+        for (Pair& p : cl_pairs) p.dcls = true;
+    }
+    map_is_standing = false;
+    plan.open_wave();
+    if (ws == 0) return 0;
+    cl_missing.clear();
+    for (int s = 0; s < S; ++s) claimed[s] = 0;
+    for (const Pair& p : cl_pairs) {
+      const int slot = slot_of[p.local];
+      if (slot < 0) {
+        cl_missing.push_back(p);
+      } else {
+        touch(slot, p.dcls);
+        plan.add_pair(p.g, slot);
+        claimed[slot] = 1;
+      }
+    }
+    // decode-class misses take slots first (stable)
+    std::stable_partition(cl_missing.begin(), cl_missing.end(),
+                          [](const Pair& p) { return p.dcls; });
+    size_t taken = cl_missing.size();
+    for (size_t i = 0; i < cl_missing.size(); ++i) {
+      const Pair& p = cl_missing[i];
+      const int slot = acquire(p.local, p.dcls);
+      if (slot < 0) {
+        taken = i;
+        break;
+      }
+      plan.add_stream(p.local, slot);
+      plan.add_pair(p.g, slot);
+      claimed[slot] = 1;
+    }
+    misses += (int64_t)cl_missing.size();
+    if (taken == cl_missing.size()) return 0;
+    // Leftover misses rotate through the probation slots split in two
+    // groups (ping-pong); with no probation slot, through the last S/4
+    // unpinned slots.  Protected slots are never rotated (1855-1890).
+    rot.clear();
+    for (int s = lists[kProbation].head; s >= 0; s = next[s]) rot.push_back(s);
+    if (rot.empty()) {
+      for (int s = 0; s < S; ++s)
+        if (seg[s] != kPinned) rot.push_back(s);
+      const size_t keep = S / 4 > 1 ? (size_t)(S / 4) : 1;
+      if (rot.size() > keep) rot.erase(rot.begin(), rot.end() - keep);
+    }
+    if (rot.empty()) return -1;
+    const size_t half = (rot.size() + 1) / 2;
+    plan.pipelined = rot.size() > half;
+    size_t i = taken;
+    for (int gi = 0; i < cl_missing.size(); ++gi) {
+      const bool b = (gi & 1) && plan.pipelined;
+      const size_t g0 = b ? half : 0, g1 = b ? rot.size() : half;
+      plan.open_wave();
+      for (size_t j = g0; j < g1 && i < cl_missing.size(); ++j, ++i) {
+        const Pair& p = cl_missing[i];
+        const int slot = rot[j];
+        evict_to(slot, p.local);
+        plan.add_pair(p.g, slot);
+        plan.add_stream(p.local, slot);
+      }
     }
     return 0;
   }

@@ -31,9 +31,37 @@ from sluice_amd import ops
 
 
 class _QuantMethod:
-    """Unquantized-method stand-in (not monolithic, applies expert_map)."""
+    """Unquantized-method stand-in (not monolithic, applies expert_map): its
+    ``apply`` is the fused-MoE kernel call of vLLM's stock path, which the
+    offloader wraps with the classic hook."""
 
     is_monolithic = False
+
+    def apply(self, layer, x, topk_weights, topk_ids, **kw):
+        scale = getattr(layer, "w13_weight_scale", None)
+        extra = {}
+        if scale is not None:
+            extra = dict(w1_scale=scale, w2_scale=layer.w2_weight_scale,
+                         block_shape=list(getattr(layer, "block_shape", None) or [128, 128]))
+        return ops.fused_experts(x, layer.w13_weight, layer.w2_weight, topk_weights, topk_ids,
+                                 global_num_experts=layer.global_num_experts,
+                                 expert_map=layer.expert_map, **extra)
+
+
+def _stock_entry(layer, gate, select_experts):
+    """vLLM's stock MoE entry as a runner's ``_forward_entry``: gate, top-k,
+    ``quant_method.apply`` (the classic hook once offloaded), then shared."""
+
+    def stock_entry(hs, rl, sei, iid, lname, unpad):
+        if gate is not None:
+            rl, _ = gate(hs)
+        tw, ti = select_experts(hidden_states=hs, router_logits=rl, input_ids=iid)
+        routed = layer.quant_method.apply(layer=layer, x=hs, topk_weights=tw, topk_ids=ti)
+        if layer.shared is None:
+            return routed
+        return (layer.shared(sei if sei is not None else hs), routed)
+
+    return stock_entry
 
 
 class _SharedMLP(nn.Module):
@@ -134,17 +162,12 @@ class SyntheticMoELayer(nn.Module):
             layer.last_logits, layer.last_ids, layer.last_weights = router_logits, ids, w
             return w, ids
 
-        def stock_entry(hs, rl, sei, iid, lname, unpad):
-            raise RuntimeError(
-                f"{lname}: {hs.shape[0]} tokens exceed the router-split envelope; larger steps "
-                "need the classic wave path, which this build does not include")
-
         self.runner = types.SimpleNamespace(
             gate=gate,
             router=types.SimpleNamespace(select_experts=select_experts),
             _shared_experts=(types.SimpleNamespace(_layer=self.shared) if self.shared else None),
             moe_config=types.SimpleNamespace(experts_per_token=k, pcp_size=1),
-            _forward_entry=stock_entry,
+            _forward_entry=_stock_entry(self, gate, select_experts),
         )
 
     @property
@@ -468,14 +491,11 @@ class _StoreMoELayer(nn.Module):
         def select_experts(hidden_states, router_logits, input_ids=None):
             return layer.select(router_logits)
 
-        def stock_entry(hs, rl, sei, iid, lname, unpad):
-            raise RuntimeError(f"{lname}: {hs.shape[0]} tokens exceed the router-split envelope")
-
         self.runner = types.SimpleNamespace(
             gate=gate, router=types.SimpleNamespace(select_experts=select_experts),
             _shared_experts=(types.SimpleNamespace(_layer=self.shared) if self.shared else None),
             moe_config=types.SimpleNamespace(experts_per_token=self.top_k, pcp_size=1),
-            _forward_entry=stock_entry)
+            _forward_entry=_stock_entry(self, gate, select_experts))
 
     @property
     def expert_map(self):
@@ -607,6 +627,8 @@ class SyntheticDecoder:
         if gap_server:
             self.off.start_gap_server()
         self.caches = [self.off._caches[id(m)] for m in self.moe_layers]
+        # batches above the router-split envelope take the classic path
+        self.thr = self.off._rs_thr or max(1, min(16, slots // sp["k"]))
         assert [id(c) for c in self.off._rs_caches] == [id(c) for c in self.caches]
         for m in self.moe_layers:
             ops.reserve_workspace(dev, max_batch, H, sp["I"], sp["k"])
@@ -680,12 +702,20 @@ class SyntheticDecoder:
         self.step.add_(1)
         return None
 
+    def classic(self, c) -> bool:
+        """Batch size c runs the classic (wave) path: more tokens than the
+        router-split envelope (slots // top_k)."""
+        return c > self.thr
+
     def pieces(self, c):
         """List of (piece_fn, gap_layer_index or None); piece_fn(io) mutates
         io.  Piece 0 embeds and runs up to the first MoE routing; piece p runs
         MoE layer p-1's experts (shared expert folded into the combine) and
-        on to MoE layer p's routing; the last piece ends the step."""
+        on to MoE layer p's routing; the last piece ends the step.  On the
+        classic path MoE layer p-1's routed output is computed between the
+        pieces (io["routed"]) and piece p adds the shared expert to it."""
         st = self._state(c)
+        classic = self.classic(c)
         moe_pos = [i for i, b in enumerate(self.blocks) if b.moe is not None]
 
         def first(io):
@@ -700,7 +730,10 @@ class SyntheticDecoder:
             def mid(io, i=i):
                 moe = self.blocks[i].moe
                 sh = moe.shared(io["hn"]) if moe.shared is not None else None
-                io["delta"] = moe.experts(io["hn"], io["tw"], io["ti"], shared_output=sh)
+                if classic:
+                    io["delta"] = io["routed"] if sh is None else io["routed"] + sh
+                else:
+                    io["delta"] = moe.experts(io["hn"], io["tw"], io["ti"], shared_output=sh)
                 self._to_next_gap(i + 1, io, st)
 
             out.append((mid, n + 1 if not last else None))
@@ -710,21 +743,42 @@ class SyntheticDecoder:
     def gap(self, n, ti):
         self.off._router_split_gap(n, ti)
 
+    def classic_moe(self, n, io, out=None):
+        """MoE layer n's routed output on the classic path: the layer's
+        ``quant_method.apply``, which the offloader's hook runs once per wave
+        (eager: it syncs the host for the ids).  Written into ``out`` when
+        given (the static buffer captured pieces read)."""
+        moe = self.moe_layers[n]
+        routed = moe.quant_method.apply(layer=moe, x=io["hn"], topk_weights=io["tw"],
+                                        topk_ids=io["ti"])
+        if out is None:
+            io["routed"] = routed
+        else:
+            out.copy_(routed)
+
     def _step_fn(self, c):
         """The whole step: every piece, with the ``vllm::sluice_stream_gap``
         op between a MoE layer's routing and its expert product (the op's
-        output feeds the experts, as in the router-split entry).  Records
-        each MoE layer's routing/activation tensors in ``self.layer_io[c]``."""
+        output feeds the experts, as in the router-split entry) -- or, above
+        the envelope, the classic hook.  Records each MoE layer's
+        routing/activation tensors in ``self.layer_io[c]``."""
         ps = self.pieces(c)
         rec = []
+        classic = self.classic(c)
 
         def run(io):
             rec.clear()
+            if classic:
+                self.off.set_step_signal(c, c, True)  # every row a one-token decode
             for fn, gap_idx in ps:
                 fn(io)
-                if gap_idx is not None:
+                if gap_idx is None:
+                    continue
+                if classic:
+                    self.classic_moe(gap_idx, io)
+                else:
                     io["hn"] = torch.ops.vllm.sluice_stream_gap(io["hn"], io["ti"], gap_idx)
-                    rec.append({"hn": io["hn"], "ti": io["ti"], "tw": io["tw"]})
+                rec.append({"hn": io["hn"], "ti": io["ti"], "tw": io["tw"]})
             self.layer_io[c] = list(rec)
 
         return run
@@ -755,7 +809,12 @@ class SyntheticDecoder:
         s = torch.cuda.Stream(device=self.dev)
         s.wait_stream(torch.cuda.current_stream())
         graphs = []
-        if self.off._server is not None:
+        classic = self.classic(c)
+        if classic:
+            self.routed_buf = getattr(self, "routed_buf", {})
+            self.routed_buf[c] = torch.zeros((c, self.sp["H"]), dtype=torch.bfloat16,
+                                             device=self.dev)
+        if self.off._server is not None and not classic:
             io = {}
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, pool=self.pool, stream=s):
@@ -763,7 +822,7 @@ class SyntheticDecoder:
             graphs.append((g, None, io))
         else:
             ps = self.pieces(c)
-            io = {}
+            io = {"routed": self.routed_buf[c]} if classic else {}
             rec = []
             for fn, gap_idx in ps:
                 g = torch.cuda.CUDAGraph()
@@ -781,6 +840,14 @@ class SyntheticDecoder:
         return graphs
 
     def step_graphs(self, c):
+        if self.classic(c):
+            self.off.set_step_signal(c, c, True)
+            out = self.routed_buf[c]
+            for g, gap_idx, io in self.graphs[c]:
+                g.replay()
+                if gap_idx is not None:
+                    self.classic_moe(gap_idx, io, out=out)
+            return
         for g, gap_idx, io in self.graphs[c]:
             g.replay()
             if gap_idx is not None:

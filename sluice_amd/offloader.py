@@ -18,9 +18,15 @@ Execution model per MoE layer per decode step (T <= thr tokens):
     -> sluice::fused_experts         [capturable; slots + map by pointer]
     -> shared experts                [capturable]
 
-Steps above the envelope would need the reference's classic wave path
-(src/sluice/offloader.py:1452-1933), which this build does not include; they
-fail closed with an error instead of computing anything wrong.
+Steps above the envelope (more tokens than slots // top_k: prefill chunks,
+large decode batches) take the classic path instead, as in the reference
+(src/sluice/offloader.py:1452-1933): the layer's ``quant_method.apply`` is
+wrapped so that ``run_moe`` syncs the ids once, the native slot cache plans
+the step -- one wave when the working set fits, else wave 0 (hits + fills)
+and the leftover misses rotated through the probation slots in ping-pong
+groups -- and the expert product runs once per wave against that wave's
+map, its row copies overlapping the previous wave's product on the copy
+stream; wave outputs are summed in fp32.
 """
 
 
@@ -156,6 +162,9 @@ class ExpertStreamOffloader:
         self._rs_layers = 0
         self._rs_thr: Optional[int] = None
         self._server: Optional[int] = None
+        self._spec_tokens = 0
+        self._signal: Optional[tuple] = None
+        self._warned_waves = False
         if self.router_split:
             _register_stream_gap_op(self)
         logger.info("Sluice ExpertStreamOffloader enabled (%d cache slots per layer, "
@@ -203,6 +212,7 @@ class ExpertStreamOffloader:
             torch.cuda.synchronize()
         for module in self._layers:
             self._install_cache(module)
+            self._wrap_apply(module)
         if self._caches:
             host = sum(c.bytes_per_expert * c.local_num_experts for c in self._caches.values()
                        if not c.static_full)
@@ -223,6 +233,14 @@ class ExpertStreamOffloader:
                 cfg = None
         if cfg is None:
             return
+        # A speculative-decode request verifies 1 + k tokens: its decode
+        # region spans ndec * (1 + k) rows (src/sluice/offloader.py:843-851).
+        sc = getattr(cfg, "speculative_config", None)
+        k_spec = getattr(sc, "num_speculative_tokens", 0) if sc is not None else 0
+        try:
+            self._spec_tokens = max(int(k_spec or 0), 0)
+        except (TypeError, ValueError):
+            self._spec_tokens = 0
         if self.router_split and self.piecewise:
             topk = 8
             mc = getattr(cfg, "model_config", None)
@@ -329,6 +347,112 @@ class ExpertStreamOffloader:
         logger.info("Sluice: %d local experts -> %d HBM slots (%d protected), %d params/expert, "
                     "%.1f MiB/expert.", local_n, num_slots, protected_cap, len(per_expert),
                     cache.bytes_per_expert / 2**20)
+
+    # -- classic (wave) path -------------------------------------------------
+    def _wrap_apply(self, module: nn.Module) -> None:
+        """Wrap the layer's ``quant_method.apply`` so steps that reach it
+        (the ones the router-split entry hands to the stock path) run the
+        classic hook (src/sluice/offloader.py:1085-1119)."""
+        qm = module.quant_method
+        if qm is None or getattr(qm, "_sluice_wrapped", False) or not hasattr(qm, "apply"):
+            return
+        original_apply = qm.apply
+        offloader = self
+
+        def apply(*args, **kwargs):
+            layer = kwargs.get("layer", args[0] if args else None)
+            topk_ids = kwargs.get("topk_ids")
+            if layer is None or topk_ids is None:
+                return original_apply(*args, **kwargs)
+            return offloader.run_moe(original_apply, args, kwargs, layer, topk_ids)
+
+        if self.piecewise:
+            # the hook syncs the host: keep it out of any traced region
+            apply = torch._dynamo.disable(apply)
+        qm.apply = apply
+        qm._sluice_wrapped = True
+
+    def set_step_signal(self, nd: Optional[int], ndec: Optional[int],
+                        real_step: bool = True) -> None:
+        """Publish the step's decode split for engines without vLLM's forward
+        context: rows [0, nd) are decode tokens of ndec requests (None: not
+        published); real_step False marks a dummy run."""
+        self._signal = (nd, ndec, bool(real_step))
+
+    def clear_step_signal(self) -> None:
+        self._signal = None
+
+    def _split_signal(self) -> tuple:
+        """``(num_decode_tokens, num_decodes, is_real_step)``
+        (src/sluice/offloader.py:1766-1800): the signal set with
+        set_step_signal, else vLLM's forward context; ``(None, None, False)``
+        (a dummy run) when neither exists."""
+        if self._signal is not None:
+            return self._signal
+        try:
+            from vllm.forward_context import get_forward_context  # type: ignore
+
+            ctx = get_forward_context()
+        except Exception:
+            return None, None, False
+        md = getattr(ctx, "attn_metadata", None)
+        if isinstance(md, dict):
+            md = next(iter(md.values()), None)
+        if md is None:
+            return None, None, False
+        nd = getattr(md, "num_decode_tokens", None)
+        if nd is None:
+            return None, None, True
+        ndec = getattr(md, "num_decodes", None)
+        try:
+            return int(nd), (int(ndec) if ndec is not None else None), True
+        except (TypeError, ValueError):
+            return None, None, True
+
+    def run_moe(self, original_apply, args, kwargs, module, topk_ids):
+        """Classic streaming hook in place of ``quant_method.apply``
+        (src/sluice/offloader.py:1452-1765, 1846-1933).
+
+        One host sync for the ids, the native bookkeeping (decode
+        classification, class-aware fills, ping-pong rotation of leftover
+        misses), then the wrapped kernel once per wave: each wave's map
+        write and row copies are ordered around it by the native layer, and
+        the outputs of a multi-wave step are summed in fp32 (exact in math:
+        an expert outside a wave's map contributes zero to it)."""
+        cache = self._caches.get(id(module))
+        if cache is None or cache.static_full:
+            return original_apply(*args, **kwargs)
+        if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("Sluice: streaming hook reached under CUDA graph capture; "
+                               "run with enforce_eager.")
+        nd, ndec, real_step = self._split_signal()
+        ids = topk_ids if topk_ids.dtype == torch.int32 else topk_ids.to(torch.int32)
+        ids = ids.contiguous()
+        T = int(ids.shape[0]) if ids.dim() else 0
+        lib = _lib.load()
+        stream = torch.cuda.current_stream(ids.device).cuda_stream
+        nw = ctypes.c_int()
+        _raise_gap(lib.sluice_layer_classic_plan(
+            cache.handle, ids.data_ptr(), ids.numel(), T, -1 if nd is None else int(nd),
+            -1 if ndec is None else int(ndec), int(bool(real_step)), int(self._spec_tokens),
+            stream, ctypes.byref(nw)), "sluice_layer_classic_plan")
+        n_waves = nw.value
+        if n_waves > 1 and real_step and not self._warned_waves:
+            self._warned_waves = True
+            logger.warning("Sluice: a step selected more local experts than usable slots; "
+                           "executing in %d waves (exact in math, not bit-identical to a "
+                           "single launch). Raise SLUICE_SLOTS to avoid waves.", n_waves)
+        total = out = None
+        for w in range(n_waves):
+            _lib.check(lib.sluice_layer_classic_wave(cache.handle, w, stream),
+                       "sluice_layer_classic_wave")
+            out = original_apply(*args, **kwargs)
+            _lib.check(lib.sluice_layer_classic_wave_done(cache.handle, w, stream),
+                       "sluice_layer_classic_wave_done")
+            if n_waves == 1:
+                return out
+            total = out.to(torch.float32) if total is None else total.add_(out)
+        return total.to(out.dtype)
 
     # -- router split -----------------------------------------------------------
     def attach_model(self, model: nn.Module) -> None:
@@ -458,10 +582,26 @@ class ExpertStreamOffloader:
                 tot[k_] += v
         return tot
 
+    def classic_counters(self) -> dict:
+        """Classic steps and waves run over every streaming layer."""
+        lib = _lib.load()
+        tot = {"steps": 0, "waves": 0}
+        ctr = (ctypes.c_int64 * 2)()
+        n = ctypes.c_int()
+        for c in self._caches.values():
+            if c.handle and not c.static_full:
+                _lib.check(lib.sluice_layer_classic_plan_read(c.handle, None, 0, ctypes.byref(n),
+                                                              ctr), "classic_plan_read")
+                tot["steps"] += ctr[0]
+                tot["waves"] += ctr[1]
+        return tot
+
     def get_stats(self) -> dict:
         c = self.gap_counters()
+        cl = self.classic_counters()
         return {"rs": {"steps": c["gaps"], "hits": None, "misses": c["misses"],
-                       "bytes": c["bytes"], "waves": c["gaps"], "fast_hits": c["fast_hits"]}}
+                       "bytes": c["bytes"], "waves": c["gaps"], "fast_hits": c["fast_hits"]},
+                "classic": {"steps": cl["steps"], "waves": cl["waves"]}}
 
     def close(self) -> None:
         lib = _lib.load()

@@ -44,6 +44,18 @@ class NativeCache:
         _lib.check(rc, "sluice_layer_gap_host")
         return streams, False
 
+    def classic(self, ids, T, nd=None, ndec=None, real_step=True, spec_tokens=0):
+        """One classic step on host ids; returns the waves as the oracle does
+        ([{"pairs": [(g, slot)], "streams": [(local, slot)]}])."""
+        arr = _lib.int32_array(ids)
+        nw = ctypes.c_int()
+        _lib.check(self.lib.sluice_layer_classic_host(
+            self.h, arr, len(ids), T, -1 if nd is None else nd, -1 if ndec is None else ndec,
+            int(real_step), spec_tokens, ctypes.byref(nw)), "sluice_layer_classic_host")
+        waves, _ = read_plan(self.lib, self.h)
+        assert len(waves) == nw.value
+        return waves
+
     def state(self):
         S, L = self.S, self.local_n
         slot_of = (ctypes.c_int32 * L)()
@@ -70,3 +82,26 @@ class NativeCache:
             "counters": {"gaps": ctr[0], "misses": ctr[1], "fast_hits": ctr[2],
                          "map_writes": ctr[3]},
         }
+
+
+def read_plan(lib, handle):
+    """The layer's last classic plan: (waves, pipelined)."""
+    n = ctypes.c_int()
+    _lib.check(lib.sluice_layer_classic_plan_read(handle, None, 0, ctypes.byref(n), None),
+               "sluice_layer_classic_plan_read")
+    buf = (ctypes.c_int32 * max(n.value, 1))()
+    _lib.check(lib.sluice_layer_classic_plan_read(handle, buf, n.value, ctypes.byref(n), None),
+               "sluice_layer_classic_plan_read")
+    v = list(buf)[: n.value]
+    nw, pipelined, i = v[0], bool(v[1]), 2
+    waves = []
+    for _ in range(nw):
+        npairs = v[i]
+        pairs = [(v[i + 1 + 2 * j], v[i + 2 + 2 * j]) for j in range(npairs)]
+        i += 1 + 2 * npairs
+        ns = v[i]
+        streams = [(v[i + 1 + 2 * j], v[i + 2 + 2 * j]) for j in range(ns)]
+        i += 1 + 2 * ns
+        waves.append({"pairs": pairs, "streams": streams})
+    assert i == len(v)
+    return waves, pipelined

@@ -2,11 +2,13 @@
 for bit: against the golden vectors and against the oracle on long random
 traces (host path of libsluice_hip.so; no GPU work)."""
 
+import ctypes
 import random
 
 import pytest
 
 from native_cache import NativeCache
+from sluice_amd import _lib
 from oracle.slru import GapOverflow, LayerCache
 
 
@@ -89,3 +91,102 @@ def test_full_residency_prefill_pins_every_slot():
     st = c.state()
     assert st["probation"] == [] and st["protected"] == []
     assert st["standing_map"] == list(range(16))
+
+
+# ---------------------------------------------------------------------------
+# Classic (wave) steps
+# ---------------------------------------------------------------------------
+def _classic_vectors():
+    from tests.conftest import classic_vectors
+
+    return classic_vectors()
+
+
+@pytest.mark.parametrize("idx", range(len(_classic_vectors()["cases"])))
+def test_native_classic_matches_reference_vectors(classic_golden, idx):
+    case = classic_golden["cases"][idx]
+    c = _native_for(case)
+    for key in ("slot_of", "expert_in_slot", "probation", "protected", "free_slots",
+                "protected_cap"):
+        assert c.state()[key] == case["init"][key], key
+    for n, step in enumerate(case["steps"]):
+        last_map = None
+        if step["kind"] == "gap":
+            _, overflow = c.gap(step["ids"], fast_hit=True)
+            assert overflow == step["overflow"], n
+        else:
+            waves = c.classic(step["ids"], step["T"], step["nd"], step["ndec"],
+                              step["real_step"])
+            assert len(waves) == len(step["waves"]), (case["name"], n)
+            for w, want in zip(waves, step["waves"]):
+                assert sorted([list(p) for p in w["pairs"]]) == want["pairs"], (case["name"], n)
+                assert [list(x) for x in w["streams"]] == want["streams"], (case["name"], n)
+            last_map = [-1] * case["E"]
+            for g, s in waves[-1]["pairs"]:
+                last_map[g] = s
+        st = c.state()
+        want = step["state"]
+        for key in ("slot_of", "expert_in_slot", "probation", "protected", "free_slots",
+                    "map_is_standing", "protected_cap"):
+            assert st[key] == want[key], (case["name"], n, key)
+        if step.get("overflow"):
+            break  # the reference raised: its map is left stale, and the trace ends
+        if want["map_is_standing"]:
+            assert st["standing_map"] == want["map"], (case["name"], n)
+        elif last_map is not None:
+            assert last_map == want["map"], (case["name"], n)
+
+
+@pytest.mark.parametrize("E,S,k,frac,seed", [(64, 48, 6, 0.5, 7), (128, 64, 8, 0.5, 8),
+                                              (128, 32, 8, 0.9, 9), (256, 64, 8, 0.3, 10)])
+def test_native_classic_matches_oracle_long_random(E, S, k, frac, seed):
+    rnd = random.Random(seed)
+    o = LayerCache(E, E, S, frac)
+    n = NativeCache(E, E, S, frac)
+    hot = rnd.sample(range(E), min(E, 3 * S // 2))
+    thr = max(1, S // k)
+    for step in range(600):
+        T = rnd.choice([rnd.randint(1, thr), rnd.randint(thr + 1, 4 * thr + 8)])
+        pool = hot if rnd.random() < 0.7 else list(range(E))
+        ids = [g for _ in range(T) for g in rnd.sample(pool, k)]
+        if T <= thr and rnd.random() < 0.6:
+            try:
+                o.gap(ids, fast_hit=True)
+                oo = False
+            except GapOverflow:
+                oo = True
+            _, no = n.gap(ids, fast_hit=True)
+            assert oo == no
+            if oo:
+                break
+        else:
+            sig = rnd.choice([(T, T, True), (0, 0, True), (T // 2, T // 2, True),
+                              (T // 2 + 1, T // 2, True), (None, None, True),
+                              (None, None, False)])
+            ow = o.classic(ids, T, *sig)
+            nw = n.classic(ids, T, *sig)
+            assert [sorted(w["pairs"]) for w in ow] == [sorted(w["pairs"]) for w in nw], step
+            assert [w["streams"] for w in ow] == [w["streams"] for w in nw], step
+        st = n.state()
+        snap = o.snapshot()
+        for key in ("slot_of", "expert_in_slot", "probation", "protected", "free_slots"):
+            assert st[key] == snap[key], (step, key)
+        assert st["map_is_standing"] == snap["map_is_standing"]
+        assert st["counters"]["misses"] == o.misses
+
+
+def test_native_classic_argument_checks():
+    c = NativeCache(16, 16, 4, 0.5)
+    lib, h = c.lib, c.h
+    nw = ctypes.c_int()
+    arr = _lib.int32_array([1, 2, 3])
+    assert lib.sluice_layer_classic_host(h, arr, 3, 2, -1, -1, 1, 0, ctypes.byref(nw)) \
+        == _lib.SLUICE_E_INVAL  # 3 ids are not [2, k]
+    assert lib.sluice_layer_classic_host(h, arr, 3, 0, -1, -1, 1, 0, ctypes.byref(nw)) \
+        == _lib.SLUICE_E_INVAL
+    assert lib.sluice_layer_classic_host(h, None, 0, 0, -1, -1, 1, 0, ctypes.byref(nw)) \
+        == _lib.SLUICE_OK and nw.value == 1
+    # the device entry points need a device map
+    assert lib.sluice_layer_classic_plan(h, arr, 3, 3, -1, -1, 1, 0, None, ctypes.byref(nw)) \
+        == _lib.SLUICE_E_STATE
+    assert lib.sluice_layer_classic_wave(h, 5, None) == _lib.SLUICE_E_STATE
