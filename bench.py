@@ -7,7 +7,11 @@ A step is one decode step of the whole synthetic decoder at batch c: every
 layer's attention/dense blocks and, per MoE layer, routing -> streaming gap
 -> grouped SwiGLU expert product -> combine, then the LM head and greedy
 next token.  The gap op is a device launch served by the native gap server,
-so a whole step (gaps included) replays as one hipGraph.  The timed region
+so a whole step (gaps included) replays as one hipGraph.  Batches above the
+router-split envelope (c > slots // top_k) take the classic wave path: the
+pieces between MoE layers replay as hipGraphs and each MoE layer runs the
+eager classic hook (one host sync for the ids, then the expert product once
+per wave).  The timed region
 is K steps bracketed by device synchronisation; the line's ``value`` is
 tokens/s at the largest batch size (c * K / seconds).
 
@@ -75,6 +79,7 @@ def time_decode(dec, c, steps, warmup):
         dec.step_graphs(c)
     dec.sync()
     before = dec.gap_counters()
+    cl0 = dec.off.classic_counters()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -84,9 +89,14 @@ def time_decode(dec, c, steps, warmup):
     dec.sync()
     after = dec.gap_counters()
     delta = {k: after[k] - before[k] for k in after}
+    cl1 = dec.off.classic_counters()
     n_moe = len(dec.moe_layers)
     return {
-        "c": c, "ms_per_step": dt / steps * 1e3, "tok_per_s": c * steps / dt,
+        "c": c, "path": "classic" if dec.classic(c) else "gap",
+        "ms_per_step": dt / steps * 1e3, "tok_per_s": c * steps / dt,
+        "classic_steps": cl1["steps"] - cl0["steps"],
+        "waves_per_classic_step": (cl1["waves"] - cl0["waves"]) / max(cl1["steps"] - cl0["steps"],
+                                                                      1),
         "gap_calls": delta["gaps"], "misses": delta["misses"],
         "fast_hits": delta["fast_hits"], "map_writes": delta["map_writes"],
         "h2d_bytes_per_step": delta["bytes"] / steps,
@@ -430,7 +440,6 @@ def main():
     thr = max(1, slots // k)
     batches = [int(v) for v in a.batches.split(",")] if a.batches else (
         [1, 8] if cfg == "v2lite" else [1, 8, 12] if cfg == "qwen3" else [8])
-    batches = [c for c in batches if c <= thr] or [thr]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     t_build = time.perf_counter()
@@ -454,9 +463,10 @@ def main():
     for c in batches:
         dec.capture(c)
         r = time_decode(dec, c, a.steps, a.warmup)
-        log(f"c={c}: {r['ms_per_step']:.3f} ms/step {r['tok_per_s']:.1f} tok/s "
+        log(f"c={c} ({r['path']}): {r['ms_per_step']:.3f} ms/step {r['tok_per_s']:.1f} tok/s "
             f"misses/layer-step={r['misses_per_layer_step']:.3f} "
-            f"fast-hit={r['fast_hit_share']:.2%}")
+            f"fast-hit={r['fast_hit_share']:.2%} waves/classic-step="
+            f"{r['waves_per_classic_step']:.2f}")
         results.append(r)
     main_c = max(batches)
     main = [r for r in results if r["c"] == main_c][0]
@@ -488,7 +498,8 @@ def main():
         if not a.uniform else "synthetic (random-init weights, uniform i.i.d. routing)",
         "config": {
             "workload": f"{cfg}-shaped decode, {len(dec.moe_layers)} MoE layers, "
-                        f"slots={slots}/{sp['E']}, MAX_BT={thr}, c={main_c}",
+                        f"slots={slots}/{sp['E']}, MAX_BT={thr}, c={main_c}"
+                        + (" (classic wave path)" if dec.classic(main_c) else ""),
             "model_shape": cfg, "slots": slots, "experts": sp["E"], "top_k": k,
             "max_bt": thr, "batch": main_c, "prompt_len": dec.prompt_len,
             "baseline_ref": "reference router-split on 1xH100 (c=8)" if pub else None,

@@ -300,7 +300,7 @@ int sluice_layer_gap_host(sluice_layer* layer, const int32_t* ids, int n,
  *
  * sluice_layer_classic_plan: copies topk_ids [n] (int32, device, row-major
  * [T, n/T]) to the host on `stream` and synchronises it (the reference's one
- * host sync per layer, 1552); with a gap server attached, waits until the
+ * host sync per layer, 1540); with a gap server attached, waits until the
  * layer's posted gap records are served; then runs the reference's
  * bookkeeping exactly: decode classification from nd / ndec (< 0 = not
  * published) / real_step / spec_tokens, class-aware touches and fills,

@@ -915,7 +915,7 @@ extern "C" int sluice_layer_classic_plan(sluice_layer* L, const int32_t* topk_id
     L->ids_host = static_cast<int32_t*>(p);
     L->ids_cap = cap;
   }
-  // the one host sync of the step (src/sluice/offloader.py:1552)
+  // the one host sync of the step (src/sluice/offloader.py:1540)
   if (n > 0)
     SLUICE_HIP_CHECK(hipMemcpyAsync(L->ids_host, topk_ids, sizeof(int32_t) * (size_t)n,
                                     hipMemcpyDeviceToHost, st));

@@ -7,7 +7,7 @@
 //   _coldest_protected (LRU)      src/sluice/offloader.py:2023-2034
 //   _acquire_slot / _evict_to     src/sluice/offloader.py:2036-2081
 //   _router_split_gap bookkeeping src/sluice/offloader.py:2405-2467
-//   run_moe / _run_waves planning src/sluice/offloader.py:1552-1765, 1846-1890
+//   run_moe / _run_waves planning src/sluice/offloader.py:1540-1765, 1846-1890
 // The reference keeps its two segments in OrderedDicts keyed by slot
 // (insertion order = recency, first = LRU).  Here each segment is an
 // intrusive doubly-linked list over slot indices with O(1) unlink and
@@ -263,7 +263,7 @@ struct Cache {
     return 0;
   }
 
-  // Classic step (run_moe, src/sluice/offloader.py:1552-1765, and the
+  // Classic step (run_moe, src/sluice/offloader.py:1540-1765, and the
   // planning half of _run_waves, 1855-1890) on the flat row-major [T, k]
   // ids.  nd / ndec: the step's decode-token / decode-request counts, < 0
   // when the engine publishes none; real_step false for dummy runs.  Fills
