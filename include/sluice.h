@@ -339,6 +339,22 @@ int sluice_layer_classic_host(sluice_layer* layer, const int32_t* ids, int n,
 int sluice_layer_classic_plan_read(const sluice_layer* layer, int32_t* out,
                                    int cap, int* len, int64_t* counters);
 
+/* Opt-in policies of the slot cache, both off by default.
+ *   lfu (SLUICE_LFU, src/sluice/offloader.py:1993-2007, 2023-2034,
+ *     2057-2068): real classic steps count each selected local expert; the
+ *     counts are halved every 256 such steps; while any count is nonzero the
+ *     protected segment demotes, and gives up victims, least frequent first
+ *     (LRU among equals).
+ *   count_experts (SLUICE_EXPERT_COUNTS, 1026-1034, 1664-1671): real classic
+ *     steps count each selected global expert as decode-class or scan-class.
+ * sluice_layer_policy_state: freq [local_n], counts_decode / counts_scan [E]
+ * (each may be NULL); stats[3] = {pure-decode ("small") classic steps, scan
+ * classic steps, steps since the last LFU halving}. */
+int sluice_layer_set_policy(sluice_layer* layer, int lfu, int count_experts);
+int sluice_layer_policy_state(const sluice_layer* layer, int64_t* freq,
+                              int64_t* counts_decode, int64_t* counts_scan,
+                              int64_t* stats);
+
 /* State snapshot.  Arrays may be NULL.  slot_of [local_n] (-1 = absent),
  * expert_in_slot [S] (-1 = empty), probation/protected in recency order
  * (LRU first), free_slots in list order (the last is popped next).

@@ -9,9 +9,14 @@ compared bit for bit with the native implementation:
                    protected_cap, free list [S-1..0], local_of / global_of_local,
                    map all -1), 1000-1010 (full-residency pre-fill)
   touch            src/sluice/offloader.py:2009-2021
-  coldest (LRU)    src/sluice/offloader.py:2023-2034 (the LFU branch is opt-in
-                   and not on the path)
-  acquire_slot     src/sluice/offloader.py:2036-2074
+  coldest          src/sluice/offloader.py:2023-2034 (LRU; with SLUICE_LFU the
+                   least frequently used, LRU among equals)
+  acquire_slot     src/sluice/offloader.py:2036-2074 (with SLUICE_LFU the
+                   protected segment is walked coldest-first)
+  LFU frequency    src/sluice/offloader.py:1993-2007 (per-local counts bumped
+                   by real classic steps, halved every 256 of them)
+  expert counts    src/sluice/offloader.py:1026-1034, 1664-1671 (per-global
+                   decode / scan selection counts of real classic steps)
   evict_to         src/sluice/offloader.py:2076-2081
   standing map     src/sluice/offloader.py:2083-2123 (map contents only)
   gap              src/sluice/offloader.py:2405-2467 (fast-hit, sorted unique,
@@ -19,7 +24,7 @@ compared bit for bit with the native implementation:
                    the step's hit slots, overflow, standing-map refresh)
   pins             src/sluice/offloader.py:1046-1083
   classic step     src/sluice/offloader.py:1452-1765 (run_moe with the
-                   defaults: no lazy/hook-lite/prefill-block/LFU modes) and
+                   defaults: no lazy/hook-lite/prefill-block modes) and
                    1846-1933 (_run_waves): decode/scan classification from the
                    step's decode counts, class-aware touches and acquisition,
                    wave 0 = hits + the fills that fit, the rest rotated through
@@ -36,9 +41,12 @@ class GapOverflow(RuntimeError):
     pass
 
 
+LFU_AGE_STEPS = 256
+
+
 class LayerCache:
     def __init__(self, global_n: int, local_n: int, slots: int, protect_frac: float = 0.5,
-                 local_of=None):
+                 local_of=None, lfu: bool = False, counts: bool = False):
         self.global_n = global_n
         self.local_n = local_n
         self.num_slots = min(slots, local_n)
@@ -61,6 +69,12 @@ class LayerCache:
         self.misses = 0
         self.fast_hits = 0
         self.map_writes = 0
+        self.lfu = lfu
+        self.freq: dict = {}
+        self.lfu_steps = 0
+        self.counts = ([0] * global_n, [0] * global_n) if counts else None
+        self.steps_small = 0
+        self.steps_scan = 0
 
     # -- SLRU core -------------------------------------------------------
     def touch(self, slot: int, friendly: bool = True) -> None:
@@ -71,11 +85,32 @@ class LayerCache:
                 del self.probation[slot]
                 self.protected[slot] = None
                 while len(self.protected) > self.protected_cap:
-                    victim = next(iter(self.protected))
+                    victim = self.coldest_protected()
                     del self.protected[victim]
                     self.probation[victim] = None
             else:
                 self.probation.move_to_end(slot)
+
+    def _heat(self, slot: int) -> int:
+        return self.freq.get(self.expert_in_slot[slot], 0)
+
+    def coldest_protected(self) -> int:
+        if self.lfu and self.freq:
+            return min(self.protected, key=self._heat)  # min keeps the first (LRU) of equals
+        return next(iter(self.protected))
+
+    def bump_freq(self, locals_) -> None:
+        for loc in locals_:
+            self.freq[loc] = self.freq.get(loc, 0) + 1
+        self.lfu_steps += 1
+        if self.lfu_steps >= LFU_AGE_STEPS:
+            self.lfu_steps = 0
+            for loc in list(self.freq):
+                v = self.freq[loc] >> 1
+                if v:
+                    self.freq[loc] = v
+                else:
+                    del self.freq[loc]
 
     def evict_to(self, slot: int, local: int) -> None:
         prev = self.expert_in_slot[slot]
@@ -96,7 +131,10 @@ class LayerCache:
             if chosen is not None:
                 del self.probation[chosen]
             elif allow_protected:
-                for cand in self.protected:
+                order = list(self.protected)
+                if self.lfu and self.freq:
+                    order = sorted(order, key=self._heat)  # stable: LRU among equals
+                for cand in order:
                     if cand not in claimed:
                         chosen = cand
                         break
@@ -213,14 +251,27 @@ class LayerCache:
                     pairs.append((g, loc, decode_ids is not None and g in decode_ids))
         ws = len(pairs)
         mla_forced_scan = real_step and nd is not None and not pure_decode_region
+        heuristic_friendly = None
         if decode_ids is None and not mla_forced_scan:
             decode_cap = self.protected_cap + len(self.pinned_slots)
-            if real_step and ws <= max(decode_cap, 1):
+            heuristic_friendly = real_step and ws <= max(decode_cap, 1)
+            if heuristic_friendly:
                 pairs = [(g, loc, True) for g, loc, _ in pairs]
         if ws == 0:
             self.map = [-1] * self.global_n
             self.map_is_standing = False
             return [{"pairs": [], "streams": []}]
+        if real_step:
+            pure_decode = (nd == T) if decode_ids is not None else heuristic_friendly
+            if pure_decode:
+                self.steps_small += 1
+            else:
+                self.steps_scan += 1
+            if self.lfu:
+                self.bump_freq(loc for _, loc, _ in pairs)
+            if self.counts is not None:
+                for g, _, dcls in pairs:
+                    self.counts[0 if dcls else 1][g] += 1
         hits, missing = [], []
         for g, loc, dcls in pairs:
             slot = self.slot_of.get(loc)

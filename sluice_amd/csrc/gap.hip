@@ -1034,6 +1034,35 @@ extern "C" int sluice_layer_classic_plan_read(const sluice_layer* Lc, int32_t* o
   return SLUICE_OK;
 }
 
+extern "C" int sluice_layer_set_policy(sluice_layer* L, int lfu, int count_experts) {
+  if (L == nullptr) return SLUICE_E_INVAL;
+  std::lock_guard<std::mutex> lk(L->mu);
+  L->c.lfu = lfu != 0;
+  L->c.count = count_experts != 0;
+  return SLUICE_OK;
+}
+
+extern "C" int sluice_layer_policy_state(const sluice_layer* Lc, int64_t* freq,
+                                         int64_t* counts_decode, int64_t* counts_scan,
+                                         int64_t* stats) {
+  if (Lc == nullptr) return SLUICE_E_INVAL;
+  sluice_layer* L = const_cast<sluice_layer*>(Lc);
+  std::lock_guard<std::mutex> lk(L->mu);
+  const slru::Cache& c = L->c;
+  if (freq)
+    for (int l = 0; l < c.local_n; ++l) freq[l] = c.freq[l];
+  if (counts_decode)
+    for (int g = 0; g < c.E; ++g) counts_decode[g] = c.cnt_decode[g];
+  if (counts_scan)
+    for (int g = 0; g < c.E; ++g) counts_scan[g] = c.cnt_scan[g];
+  if (stats) {
+    stats[0] = c.steps_small;
+    stats[1] = c.steps_scan;
+    stats[2] = c.lfu_steps;
+  }
+  return SLUICE_OK;
+}
+
 extern "C" int sluice_layer_state(const sluice_layer* Lc, int32_t* slot_of, int32_t* expert_in_slot,
                                   int32_t* probation, int* n_probation, int32_t* protected_,
                                   int* n_protected, int32_t* free_slots, int* n_free,

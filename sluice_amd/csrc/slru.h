@@ -8,6 +8,8 @@
 //   _acquire_slot / _evict_to     src/sluice/offloader.py:2036-2081
 //   _router_split_gap bookkeeping src/sluice/offloader.py:2405-2467
 //   run_moe / _run_waves planning src/sluice/offloader.py:1540-1765, 1846-1890
+//   opt-in LFU (SLUICE_LFU)       src/sluice/offloader.py:1993-2007, 2023-2034, 2057-2068
+//   opt-in expert counts          src/sluice/offloader.py:1026-1034, 1664-1671
 // The reference keeps its two segments in OrderedDicts keyed by slot
 // (insertion order = recency, first = LRU).  Here each segment is an
 // intrusive doubly-linked list over slot indices with O(1) unlink and
@@ -75,6 +77,17 @@ struct Cache {
   List lists[3];                     // indexed by kProbation / kProtected
   bool map_is_standing = false;
   int64_t gaps = 0, misses = 0, fast_hits = 0, map_writes = 0;
+  // Opt-in policies.  LFU: per-local selection frequency of real classic
+  // steps, halved every kLfuAgeSteps of them; while any is nonzero, protected
+  // victims are taken least frequent first (LRU among equals).  Counts: per-
+  // global decode-class / scan-class selections of real classic steps.
+  static constexpr int kLfuAgeSteps = 256;
+  bool lfu = false, count = false;
+  std::vector<int64_t> freq;       // [local_n]
+  int freq_nonzero = 0;            // entries of freq above zero
+  int lfu_steps = 0;
+  std::vector<int64_t> cnt_decode, cnt_scan;  // [E]
+  int64_t steps_small = 0, steps_scan = 0;
 
   // scratch reused across gaps and classic steps
   struct Pair {
@@ -85,7 +98,7 @@ struct Cache {
   std::vector<int> missing;
   std::vector<uint8_t> present, decode;
   std::vector<Pair> cl_pairs, cl_missing;
-  std::vector<int> rot;
+  std::vector<int> rot, order;
 
   void init(int E_, int local_n_, int S_, int cap, const int32_t* lof) {
     E = E_;
@@ -109,6 +122,40 @@ struct Cache {
     lists[1] = List();
     lists[2] = List();
     claimed.assign(S, 0);
+    freq.assign(local_n, 0);
+    freq_nonzero = 0;
+    lfu_steps = 0;
+    cnt_decode.assign(E, 0);
+    cnt_scan.assign(E, 0);
+  }
+
+  bool lfu_active() const { return lfu && freq_nonzero > 0; }
+  int64_t heat(int slot) const {
+    const int l = expert_in_slot[slot];
+    return l >= 0 ? freq[l] : 0;
+  }
+
+  // _coldest_protected: LRU, or under LFU the least frequent (first of equals)
+  int coldest_protected() const {
+    int best = lists[kProtected].head;
+    if (!lfu_active()) return best;
+    for (int c = best; c >= 0; c = next[c])
+      if (heat(c) < heat(best)) best = c;
+    return best;
+  }
+
+  // _bump_freq
+  void bump_freq(int local) {
+    if (freq[local]++ == 0) ++freq_nonzero;
+  }
+  void age_freq() {
+    if (++lfu_steps < kLfuAgeSteps) return;
+    lfu_steps = 0;
+    freq_nonzero = 0;
+    for (int64_t& f : freq) {
+      f >>= 1;
+      freq_nonzero += f > 0;
+    }
   }
 
   void push_back(Seg sg, int s) {
@@ -148,7 +195,7 @@ struct Cache {
         unlink(slot);
         push_back(kProtected, slot);
         while (lists[kProtected].size > protected_cap) {
-          const int demoted = lists[kProtected].head;  // _coldest_protected (LRU)
+          const int demoted = coldest_protected();
           unlink(demoted);
           push_back(kProbation, demoted);
         }
@@ -180,11 +227,26 @@ struct Cache {
         }
       }
       if (slot < 0 && allow_protected) {
-        for (int c = lists[kProtected].head; c >= 0; c = next[c]) {
-          if (!claimed[c]) {
-            slot = c;
-            unlink(c);
-            break;
+        if (lfu_active()) {
+          // protected walked coldest first, LRU among equals
+          order.clear();
+          for (int c = lists[kProtected].head; c >= 0; c = next[c]) order.push_back(c);
+          std::stable_sort(order.begin(), order.end(),
+                           [this](int a, int b) { return heat(a) < heat(b); });
+          for (int c : order) {
+            if (!claimed[c]) {
+              slot = c;
+              unlink(c);
+              break;
+            }
+          }
+        } else {
+          for (int c = lists[kProtected].head; c >= 0; c = next[c]) {
+            if (!claimed[c]) {
+              slot = c;
+              unlink(c);
+              break;
+            }
           }
         }
       }
@@ -300,16 +362,28 @@ struct Cache {
     // No per-token signal: real steps whose working set fits the decode
     // capacity (pinned + protected) count as decode-class (1620-1637).
     const bool forced_scan = real_step && has_nd && !pure_region;
+    bool friendly = false;  // the working-set heuristic classified the step decode
     if (!have_dec && !forced_scan) {
       int n_pinned = 0;
       for (int s = 0; s < S; ++s) n_pinned += seg[s] == kPinned;
       const int cap = protected_cap + n_pinned;
-      if (real_step && ws <= (cap > 1 ? cap : 1))
+      friendly = real_step && ws <= (cap > 1 ? cap : 1);
+      if (friendly)
         for (Pair& p : cl_pairs) p.dcls = true;
     }
     map_is_standing = false;
     plan.open_wave();
     if (ws == 0) return 0;
+    if (real_step) {
+      const bool pure_decode = have_dec ? nd == T : friendly;
+      ++(pure_decode ? steps_small : steps_scan);
+      if (lfu) {
+        for (const Pair& p : cl_pairs) bump_freq(p.local);
+        age_freq();
+      }
+      if (count)
+        for (const Pair& p : cl_pairs) ++(p.dcls ? cnt_decode : cnt_scan)[p.g];
+    }
     cl_missing.clear();
     for (int s = 0; s < S; ++s) claimed[s] = 0;
     for (const Pair& p : cl_pairs) {

@@ -561,6 +561,10 @@ class SyntheticDecoder:
     Prompts are synthetic: the first ``prompt_len`` KV positions hold random
     latents/keys/values; decoding starts at position ``prompt_len``.
 
+    ``expert_checkpoint`` (a safetensors file or directory, Hugging Face
+    expert naming) loads every MoE layer's routed experts from a checkpoint
+    instead of random values; the other weights stay random.
+
     Routing: router logits = gate GEMM (weights N(0, gate_std)) + log-Zipf
     (zipf_s) popularity over a seeded permutation + sigma * z_t, z_t an AR(1)
     process (rho) per sequence and layer.  The defaults (gate_std 0.004,
@@ -574,7 +578,7 @@ class SyntheticDecoder:
                  gen_len: int = 256, seed: int = 0, device=None, shared_host_pool: bool = True,
                  zipf_s: float = 1.1, rho: float = 0.7, sigma: float = 0.5,
                  gate_std: float = 0.004, uniform_routing: bool = False, fast_hit: bool = True,
-                 layers: int = None, gap_server: bool = True):
+                 layers: int = None, gap_server: bool = True, expert_checkpoint=None):
         self.sp = sp = dict(SPECS[spec])
         if layers is not None:
             sp["layers"] = layers
@@ -607,7 +611,17 @@ class SyntheticDecoder:
             if li < sp["first_dense"]:
                 blk.mlp = _DenseMLP(H, sp["dense_I"], dev, g)
             else:
-                if store is None or not shared_host_pool:
+                if expert_checkpoint is not None:
+                    # the layer's real expert rows (Hugging Face safetensors
+                    # naming), straight into pinned stores in the slot layout
+                    from sluice_amd import loader
+
+                    store = loader.expert_stores_from_checkpoint(expert_checkpoint, li)
+                    shp = tuple(store["w13_weight"].tensor.shape)
+                    if shp != (sp["E"], 2 * sp["I"], sp["H"]):
+                        raise ValueError(f"checkpoint layer {li}: experts {shp} do not match the "
+                                         f"{spec} shape")
+                elif store is None or not shared_host_pool:
                     store = _expert_store(sp, 7000 + li, dev, sp["fp8"])
                 rb = None
                 if uniform_routing:

@@ -30,9 +30,12 @@ stream; wave outputs are summed in fp32.
 """
 
 
+import atexit
 import ctypes
+import json
 import logging
 import os
+import time
 from collections.abc import Generator
 from dataclasses import dataclass, field
 from typing import Optional
@@ -54,6 +57,13 @@ ROUTER_SPLIT_ENV = "SLUICE_ROUTER_SPLIT"
 PIECEWISE_ENV = "SLUICE_PIECEWISE"
 FAST_HIT_ENV = "SLUICE_RS_FAST_HIT"
 NOOP_ENV = "SLUICE_RS_NOOP"
+# Opt-in policies (src/sluice/offloader.py:97-118): LFU-ordered protected
+# victims; per-expert selection counts dumped as JSONL snapshots; a static
+# pin file {"layers": {"<MoE-layer ordinal>": [global ids]}}.
+LFU_ENV = "SLUICE_LFU"
+COUNTS_DIR_ENV = "SLUICE_EXPERT_COUNTS"
+COUNTS_EVERY_ENV = "SLUICE_EXPERT_COUNTS_EVERY"
+PIN_FILE_ENV = "SLUICE_PIN_FILE"
 
 
 @dataclass
@@ -76,6 +86,10 @@ class _ExpertLayerCache:
     bytes_per_expert: int = 0
     static_full: bool = False
     handle: Optional[int] = None
+    pinned_slots: set = field(default_factory=set)
+    ordinal: int = -1
+    layer_name: str = ""
+    policy_steps: int = 0  # real classic steps with selected experts, last seen
 
     # -- native state views ------------------------------------------------
     def _state(self):
@@ -129,6 +143,25 @@ class _ExpertLayerCache:
         return {"gaps": c[0], "misses": c[1], "fast_hits": c[2], "map_writes": c[3],
                 "bytes": c[4] | (c[5] << 32)}
 
+    def policy_state(self) -> dict:
+        """LFU frequencies (local -> count, nonzero only), per-global
+        decode/scan selection counts and the classic step classes."""
+        lib = _lib.load()
+        n, E = self.local_num_experts, len(self.local_of)
+        freq = (ctypes.c_int64 * n)()
+        dec = (ctypes.c_int64 * E)()
+        scan = (ctypes.c_int64 * E)()
+        st = (ctypes.c_int64 * 3)()
+        _lib.check(lib.sluice_layer_policy_state(self.handle, freq, dec, scan, st),
+                   "sluice_layer_policy_state")
+        return {"freq": {l: int(f) for l, f in enumerate(freq) if f},
+                "counts_decode": list(dec), "counts_scan": list(scan),
+                "steps_small": int(st[0]), "steps_scan": int(st[1]), "lfu_steps": int(st[2])}
+
+    @property
+    def freq(self) -> dict:
+        return self.policy_state()["freq"]
+
 
 class ExpertStreamOffloader:
     """Stream routed-expert weights host->HBM per decode step, by routing.
@@ -155,6 +188,7 @@ class ExpertStreamOffloader:
         self.pin_memory = torch.cuda.is_available()
         self._caches: dict[int, _ExpertLayerCache] = {}
         self._layers: list[nn.Module] = []
+        self._prepared_stores: dict[int, list] = {}  # pinned stores made before load
         self._rs_caches: list[_ExpertLayerCache] = []
         self._rs_gaps = 0
         self._rs_misses = 0
@@ -165,6 +199,31 @@ class ExpertStreamOffloader:
         self._spec_tokens = 0
         self._signal: Optional[tuple] = None
         self._warned_waves = False
+        self.lfu = os.environ.get(LFU_ENV, "0") == "1"
+        # expert-count profiling (src/sluice/offloader.py:441-465, 1393-1448)
+        self._counts_dir = os.environ.get(COUNTS_DIR_ENV) or None
+        self._counts_every = 5000
+        self._counts_calls = 0
+        self._counts_snap = 0
+        self._counts_file = None
+        if self._counts_dir:
+            try:
+                self._counts_every = max(int(os.environ.get(COUNTS_EVERY_ENV, "5000")), 1)
+            except ValueError:
+                self._counts_every = 5000
+            atexit.register(self._dump_expert_counts, True)
+        # static pins (src/sluice/offloader.py:466-481): parsed here, applied
+        # per layer at install; a malformed file fails loudly
+        self._pin_layers: Optional[dict] = None
+        self._pin_stats = [0, 0]  # experts pinned, layers with pins
+        pin_path = os.environ.get(PIN_FILE_ENV)
+        if pin_path:
+            with open(pin_path) as f:
+                raw = json.load(f)
+            layers = raw.get("layers", raw)
+            self._pin_layers = {int(k_): [int(g) for g in v] for k_, v in layers.items()}
+            logger.info("Sluice: static pin file %s (%d layers listed).", pin_path,
+                        len(self._pin_layers))
         if self.router_split:
             _register_stream_gap_op(self)
         logger.info("Sluice ExpertStreamOffloader enabled (%d cache slots per layer, "
@@ -193,15 +252,28 @@ class ExpertStreamOffloader:
         return modules
 
     def _prepare_layer(self, module: nn.Module) -> None:
+        """Move a layer's (still empty) per-expert params to host memory so
+        the checkpoint loads there (src/sluice/offloader.py:554-571).  With a
+        GPU present they become views of exact-size pinned host stores, so
+        the loader writes straight into the memory the expert rows stream
+        from, and _install_cache adopts it without a second host copy."""
         qm = module.quant_method
         if qm is None or getattr(qm, "is_monolithic", False):
+            return
+        if getattr(module, "rocm_aiter_fmoe_enabled", False):
             return
         local_n = int(module.local_num_experts)
         per_expert = self._per_expert_params(module, local_n)
         if not per_expert:
             return
         for p in per_expert.values():
-            p.data = p.data.to("cpu")
+            cpu = p.data if p.data.device.type == "cpu" else p.data.to("cpu")
+            if self.pin_memory and ops.host_store_of(cpu) is None:
+                store = ops.HostStore(tuple(cpu.shape), cpu.dtype)
+                store.tensor.copy_(cpu)
+                self._prepared_stores.setdefault(id(module), []).append(store)
+                cpu = store.tensor
+            p.data = cpu
         if all(id(module) != id(m) for m in self._layers):
             self._layers.append(module)
 
@@ -314,6 +386,9 @@ class ExpertStreamOffloader:
             cache.gpu_cache[name] = slot
             p.data = slot
             cache.bytes_per_expert += cpu[0].nbytes
+        # adopted stores now live in cache.host_stores; a static-full layer's
+        # rows are all in HBM, so its prepared stores are released here
+        self._prepared_stores.pop(id(module), None)
         orig_map = getattr(module, "expert_map", None)
         if orig_map is not None:
             cache.local_of = [int(v) for v in orig_map.to("cpu").tolist()]
@@ -336,6 +411,8 @@ class ExpertStreamOffloader:
                                            cache.expert_map_buf.data_ptr(), ctypes.byref(h)),
                    "sluice_layer_create")
         cache.handle = h.value
+        cache.ordinal = len(self._caches)
+        cache.layer_name = getattr(module, "layer_name", "") or ""
         if not cache.static_full:
             for name in cache.param_names:
                 slot_t = cache.gpu_cache[name]
@@ -343,10 +420,97 @@ class ExpertStreamOffloader:
                 _lib.check(lib.sluice_layer_add_param(cache.handle, slot_t.data_ptr(),
                                                       host_t.data_ptr(), host_t[0].nbytes),
                            "sluice_layer_add_param")
+            if self.lfu or self._counts_dir:
+                _lib.check(lib.sluice_layer_set_policy(cache.handle, int(self.lfu),
+                                                       int(bool(self._counts_dir))),
+                           "sluice_layer_set_policy")
+            if self._pin_layers is not None:
+                self._apply_pins(cache, cache.ordinal)
         self._caches[id(module)] = cache
         logger.info("Sluice: %d local experts -> %d HBM slots (%d protected), %d params/expert, "
                     "%.1f MiB/expert.", local_n, num_slots, protected_cap, len(per_expert),
                     cache.bytes_per_expert / 2**20)
+
+    def _apply_pins(self, cache: _ExpertLayerCache, ordinal: int) -> None:
+        """Fill this layer's pinned slots from the pin file, one row copy per
+        expert at init (src/sluice/offloader.py:1046-1083): pins live outside
+        both segments and the free list, so nothing evicts them, and each one
+        is debited from protected_cap so probation keeps its size."""
+        wanted = self._pin_layers.get(ordinal, []) if self._pin_layers else []
+        if not wanted:
+            return
+        lib = _lib.load()
+        budget = cache.protected_cap
+        n = 0
+        resident = set(cache.slot_of)
+        for g in wanted:
+            if n >= budget:
+                logger.warning("Sluice: layer %d pin list (%d ids) exceeds the protected budget "
+                               "(%d); pinning the first %d only.", ordinal, len(wanted), budget,
+                               n)
+                break
+            if not (0 <= g < len(cache.local_of)):
+                continue
+            local = cache.local_of[g]
+            if local < 0 or local in resident:
+                continue
+            slot = ctypes.c_int()
+            if lib.sluice_layer_pin(cache.handle, local, 1, ctypes.byref(slot)) != _lib.SLUICE_OK:
+                continue  # no free slot left
+            for name, gpu in cache.gpu_cache.items():
+                gpu[slot.value].copy_(cache.cpu_store[name][local])
+            resident.add(local)
+            cache.pinned_slots.add(slot.value)
+            n += 1
+        if n:
+            cache.protected_cap -= n
+            self._pin_stats[0] += n
+            self._pin_stats[1] += 1
+
+    # -- expert-count profiling ---------------------------------------------------
+    def _counts_tick(self) -> None:
+        self._counts_calls += 1
+        if self._counts_calls % self._counts_every == 0:
+            self._dump_expert_counts(False)
+
+    def _dump_expert_counts(self, final: bool) -> None:
+        """Append one cumulative JSONL snapshot per streaming layer (nonzero
+        counts only, keyed by global expert id) to
+        <SLUICE_EXPERT_COUNTS>/expert_counts_rank<r>.jsonl, in the
+        reference's record format (src/sluice/offloader.py:1399-1448).  Never
+        raises: profiling must not take serving down."""
+        if not self._counts_dir:
+            return
+        layers = [c for c in self._caches.values() if not c.static_full and c.handle]
+        if not layers:
+            return
+        try:
+            if self._counts_file is None:
+                try:
+                    import torch.distributed as dist
+
+                    rank = dist.get_rank() if dist.is_initialized() else 0
+                except Exception:
+                    rank = int(os.environ.get("RANK", "0") or "0")
+                os.makedirs(self._counts_dir, exist_ok=True)
+                self._counts_file = open(
+                    os.path.join(self._counts_dir, f"expert_counts_rank{rank}.jsonl"), "a")
+            self._counts_snap += 1
+            pols = [c.policy_state() for c in layers]
+            small = sum(p["steps_small"] for p in pols)
+            scan = sum(p["steps_scan"] for p in pols)
+            for c, p in zip(layers, pols):
+                self._counts_file.write(json.dumps({
+                    "snap": self._counts_snap, "final": final, "ts": time.time(),
+                    "hook_calls": self._counts_calls, "steps_small": small, "steps_scan": scan,
+                    "layer": c.ordinal, "layer_name": c.layer_name,
+                    "n_global": len(p["counts_decode"]),
+                    "decode": {str(g): v for g, v in enumerate(p["counts_decode"]) if v},
+                    "scan": {str(g): v for g, v in enumerate(p["counts_scan"]) if v},
+                }) + "\n")
+            self._counts_file.flush()
+        except Exception:
+            logger.exception("Sluice: expert-count dump failed (non-fatal)")
 
     # -- classic (wave) path -------------------------------------------------
     def _wrap_apply(self, module: nn.Module) -> None:
@@ -437,6 +601,14 @@ class ExpertStreamOffloader:
             -1 if ndec is None else int(ndec), int(bool(real_step)), int(self._spec_tokens),
             stream, ctypes.byref(nw)), "sluice_layer_classic_plan")
         n_waves = nw.value
+        if self._counts_dir and real_step:
+            # the reference ticks its profiling clock once per real hook call
+            # that selected experts (the steps the layer classified)
+            pol = cache.policy_state()
+            seen = pol["steps_small"] + pol["steps_scan"]
+            if seen != cache.policy_steps:
+                cache.policy_steps = seen
+                self._counts_tick()
         if n_waves > 1 and real_step and not self._warned_waves:
             self._warned_waves = True
             logger.warning("Sluice: a step selected more local experts than usable slots; "

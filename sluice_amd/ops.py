@@ -24,6 +24,7 @@ import torch
 from sluice_amd import _lib
 
 _SCORING = {"softmax": 0, "sigmoid": 1}
+_MAX_PAIRS = 4096  # SLUICE_MAX_PAIRS: (token, expert) pairs per fused_experts launch
 
 
 def _stream(device: torch.device) -> int:
@@ -134,6 +135,17 @@ def _fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch
         emap_ptr = None
     out = torch.empty_like(x)
     if T == 0:
+        return out
+    chunk = _MAX_PAIRS // k
+    if T > chunk:
+        # more (token, expert) pairs than one launch takes (a prefill chunk on
+        # the classic path): tokens are independent, so run slices of them
+        for t0 in range(0, T, chunk):
+            t1 = min(T, t0 + chunk)
+            out[t0:t1] = _fused_experts_impl(
+                x[t0:t1], w1, w2, tw[t0:t1], ids[t0:t1], activation, global_num_experts,
+                expert_map, w1_scale, w2_scale, block_shape, routed_scaling_factor,
+                None if shared_output is None else shared_output[t0:t1])
         return out
     nbytes = workspace_bytes(T, H, I, k)
     ws = _WS.get(x.device, nbytes)

@@ -9,6 +9,12 @@ ran with (read by the stand-in kernel at call time), the stream-ins issued
 before each wave, and the full cache state after the step.  The output JSON
 holds data only; the reference never leaves this container.
 
+Three more traces run with the opt-in policies the classic hook carries:
+SLUICE_LFU (frequency-ordered victims) and SLUICE_EXPERT_COUNTS (selection
+counts and their JSONL snapshots); for those the LFU frequencies, step
+classes and counts after every classic step, and the JSONL records the
+reference itself wrote (timestamps dropped), are kept too.
+
 Stand-ins, beyond the three vLLM names make_slru_vectors.py supplies:
   - the kernel (`original_apply`) records the layer's expert map and returns
     a scalar zero tensor;
@@ -25,7 +31,9 @@ import gzip
 import json
 import logging
 import os
+import shutil
 import sys
+import tempfile
 
 import torch
 
@@ -81,10 +89,45 @@ CASES = [
     ("dummy_runs", 32, 32, 8, 0.5, 2, [2, 5], 100, "uniform", 142, None, None, "dummy"),
 ]
 
+# Opt-in policies: SLUICE_LFU (frequency-ordered demotion and protected
+# victims, aged every 256 real classic steps) and SLUICE_EXPERT_COUNTS
+# (per-expert selection counts, JSONL snapshots every `every` hook calls).
+POLICY_CASES = [
+    # name, E, local_n, slots, frac, k, T choices, steps, trace, seed, ep, pins, signal, policy
+    ("lfu_cycle", 24, 24, 8, 0.5, 2, [1, 2, 6, 9], 700, "zipf", 151, None, None, "cycle",
+     {"lfu": True, "counts_every": 37}),
+    ("lfu_decode_pins", 32, 32, 10, 0.6, 3, [1, 4, 8], 450, "zipf", 152, None, [2, 9], "decode",
+     {"lfu": True}),
+    ("counts_ep", 32, 16, 6, 0.5, 4, [1, 6], 160, "uniform", 153, "even", None, "cycle",
+     {"counts_every": 23}),
+]
+
+
+def _policy_state(off, cache, mod):
+    out = {"freq": sorted([int(l), int(c)] for l, c in cache.freq.items()),
+           "lfu_steps": int(cache.lfu_steps),
+           "steps_small": int(off._stats["small"].steps),
+           "steps_scan": int(off._stats["scan"].steps)}
+    cnt = off._counts.get(id(mod))
+    if cnt is not None:
+        out["counts_decode"] = [int(v) for v in cnt[0]]
+        out["counts_scan"] = [int(v) for v in cnt[1]]
+    return out
+
 
 def run_case(ESO, name, E, local_n, slots, frac, k, T_choices, steps, kind, seed, ep, pins,
-             signal):
+             signal, policy=None):
+    policy = policy or {}
     os.environ["SLUICE_PROTECT_FRAC"] = str(frac)
+    counts_dir = None
+    for key in ("SLUICE_LFU", "SLUICE_EXPERT_COUNTS", "SLUICE_EXPERT_COUNTS_EVERY"):
+        os.environ.pop(key, None)
+    if policy.get("lfu"):
+        os.environ["SLUICE_LFU"] = "1"
+    if policy.get("counts_every"):
+        counts_dir = tempfile.mkdtemp(prefix="sluice_counts_")
+        os.environ["SLUICE_EXPERT_COUNTS"] = counts_dir
+        os.environ["SLUICE_EXPERT_COUNTS_EVERY"] = str(policy["counts_every"])
     off = ESO(expert_cache_slots=slots)
     emap = None
     local_of = None
@@ -151,11 +194,32 @@ def run_case(ESO, name, E, local_n, slots, frac, k, T_choices, steps, kind, seed
         recs.append({"kind": "classic", "ids": ids, "T": T, "nd": nd, "ndec": ndec,
                      "real_step": real, "waves": rec_waves,
                      "state": base._snapshot(cache)})
-    return {
+        if policy:
+            recs[-1]["policy"] = _policy_state(off, cache, mod)
+    out = {
         "name": name, "E": E, "local_n": local_n, "slots": slots, "protect_frac": frac,
         "k": k, "local_of": local_of, "pins": pins, "thr": thr, "signal": signal,
         "init": init, "steps": recs,
     }
+    if policy:
+        out["policy"] = policy
+    if counts_dir is not None:
+        # the reference's own periodic snapshots so far (the atexit one is
+        # not taken): the JSONL record format, "ts" dropped
+        if off._counts_file is not None:
+            off._counts_file.close()
+            off._counts_file = None
+        off._counts_dir = None  # its atexit hook then writes nothing
+        lines = []
+        for fn in sorted(os.listdir(counts_dir)):
+            with open(os.path.join(counts_dir, fn)) as f:
+                for line in f:
+                    rec = json.loads(line)
+                    rec.pop("ts", None)
+                    lines.append({"file": fn, "record": rec})
+        out["counts_jsonl"] = lines
+        shutil.rmtree(counts_dir, ignore_errors=True)
+    return out
 
 
 def main():
@@ -167,6 +231,7 @@ def main():
     torch.cuda.Event = lambda *a, **k: _NoopEvent()
     logging.getLogger("sluice").setLevel(logging.ERROR)
     cases = [run_case(ExpertStreamOffloader, *case) for case in CASES]
+    cases += [run_case(ExpertStreamOffloader, *case) for case in POLICY_CASES]
     with gzip.open(OUT, "wt") as f:
         json.dump({"source": "src/sluice/offloader.py _install_cache + _router_split_gap + "
                              "run_moe/_run_waves", "cases": cases}, f, separators=(",", ":"))

@@ -8,7 +8,8 @@ from sluice_amd import _lib
 
 
 class NativeCache:
-    def __init__(self, E, local_n, slots, protect_frac=0.5, local_of=None):
+    def __init__(self, E, local_n, slots, protect_frac=0.5, local_of=None, lfu=False,
+                 counts=False):
         self.lib = _lib.load()
         self.E, self.local_n = E, local_n
         self.S = min(slots, local_n)
@@ -20,6 +21,19 @@ class NativeCache:
                                                 ctypes.byref(h)), "sluice_layer_create")
         self.h = h.value
         self._streams = (ctypes.c_int32 * (2 * max(self.S, 1)))()
+        if lfu or counts:
+            _lib.check(self.lib.sluice_layer_set_policy(self.h, int(lfu), int(counts)),
+                       "sluice_layer_set_policy")
+
+    def policy(self):
+        freq = (ctypes.c_int64 * self.local_n)()
+        dec = (ctypes.c_int64 * self.E)()
+        scan = (ctypes.c_int64 * self.E)()
+        st = (ctypes.c_int64 * 3)()
+        _lib.check(self.lib.sluice_layer_policy_state(self.h, freq, dec, scan, st), "policy")
+        return {"freq": [[l, f] for l, f in enumerate(freq) if f],
+                "counts_decode": list(dec), "counts_scan": list(scan),
+                "steps_small": st[0], "steps_scan": st[1], "lfu_steps": st[2]}
 
     def __del__(self):
         if getattr(self, "h", None):

@@ -83,12 +83,13 @@ def _check_slots(cache):
 def _classic_cases():
     from conftest import classic_vectors
 
-    g = classic_vectors()
-    return [c for c in g["cases"] if not c["pins"]]
+    return classic_vectors()["cases"]
 
 
 @pytest.mark.parametrize("case", _classic_cases(), ids=lambda c: c["name"])
-def test_device_classic_replays_reference(monkeypatch, case):
+def test_device_classic_replays_reference(monkeypatch, tmp_path, case):
+    import json
+
     print(f"classic case {case['name']}", flush=True)
     E, local_n, k = case["E"], case["local_n"], case["k"]
     emap = None
@@ -96,7 +97,15 @@ def test_device_classic_replays_reference(monkeypatch, case):
         emap = torch.tensor(case["local_of"], dtype=torch.int32)
     layer = _Layer(E, local_n, expert_map=emap)
     qm = layer.quant_method
+    pol = case.get("policy", {})
+    if pol.get("lfu"):
+        monkeypatch.setenv("SLUICE_LFU", "1")
+    if pol.get("counts_every"):
+        monkeypatch.setenv("SLUICE_EXPERT_COUNTS", str(tmp_path))
+        monkeypatch.setenv("SLUICE_EXPERT_COUNTS_EVERY", str(pol["counts_every"]))
     off = _offloader(monkeypatch, case["slots"], case["protect_frac"])
+    if case["pins"]:
+        off._pin_layers = {0: list(case["pins"])}  # what SLUICE_PIN_FILE would hold
     off.wrap_modules(iter([layer]))
     with torch.cuda.device(DEV):
         off.post_init()
@@ -143,10 +152,28 @@ def test_device_classic_replays_reference(monkeypatch, case):
         assert cache.map_is_standing == want["map_is_standing"], n
         torch.cuda.synchronize()
         assert cache.expert_map_buf.cpu().tolist() == want["map"], n
+        if "policy" in step:
+            got, wp = cache.policy_state(), step["policy"]
+            assert sorted([l, f] for l, f in got["freq"].items()) == wp["freq"], n
+            assert (got["steps_small"], got["steps_scan"], got["lfu_steps"]) == (
+                wp["steps_small"], wp["steps_scan"], wp["lfu_steps"]), n
+            if "counts_decode" in wp:
+                assert got["counts_decode"] == wp["counts_decode"], n
+                assert got["counts_scan"] == wp["counts_scan"], n
         if n % 20 == 0 or n == len(case["steps"]) - 1:
             _check_slots(cache)
     _check_slots(cache)
     assert off.classic_counters() == {"steps": n_classic, "waves": n_waves}
+    if case.get("counts_jsonl"):
+        # the snapshots the offloader wrote == the ones the reference wrote
+        recs = []
+        for fn in sorted(p.name for p in tmp_path.iterdir()):
+            for line in open(tmp_path / fn):
+                r = json.loads(line)
+                r.pop("ts")
+                recs.append({"file": fn, "record": r})
+        assert recs == case["counts_jsonl"]
+    off._counts_dir = None
     off.close()
 
 
@@ -241,3 +268,78 @@ def test_decoder_above_envelope_graphs_match_eager(spec, layers, slots, schedule
         assert x["counters"][:4] == y["counters"][:4]
     assert ma == mb
     assert ca == cb and ca["steps"] > 0
+
+
+def test_prefill_sized_classic_step_matches_dense_oracle():
+    """A prefill-sized step (700 tokens x top-8 = 5600 pairs, more than one
+    expert-product launch takes) on the classic path: prefill signal, every
+    expert selected, several waves, against the oracle."""
+    from oracle import moe as om
+    from sluice_amd.decoder import SyntheticMoELayer, build_offloaded
+
+    E, k, H, I, T = 32, 8, 128, 64, 700
+    layer = SyntheticMoELayer(H, I, E, k, scoring="softmax", renorm=True, seed=9, device=DEV)
+    off = build_offloaded([layer], 12, DEV)
+    off.set_step_signal(0, 0, True)
+    rng = np.random.default_rng(2)
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(
+        torch.bfloat16).to(DEV)
+    out = layer(x)
+    torch.cuda.synchronize()
+    assert off.classic_counters()["waves"] > 1
+    ref = om.fused_experts(x.float().cpu().numpy(), layer.host_w13.float().numpy(),
+                           layer.host_w2.float().numpy(), layer.last_weights.cpu().numpy(),
+                           layer.last_ids.cpu().numpy())
+    err = om.rel_l2(out.float().cpu().numpy(), ref)
+    print(f"  T={T} waves={off.classic_counters()['waves']} rel_l2={err:.2e}", flush=True)
+    assert err <= 1e-2
+    _check_slots(off._caches[id(layer)])
+    off.close()
+
+
+def test_checkpoint_loaded_layer_matches_oracle(tmp_path):
+    """Expert rows from a safetensors checkpoint -> pinned stores (loader)
+    -> adopted by the offloader -> slots -> the expert product: a layer's
+    outputs on the gap path (T <= thr) and the classic path (T > thr)
+    against the oracle over the checkpoint's own tensors."""
+    from safetensors.torch import save_file
+
+    from oracle import moe as om
+    from sluice_amd import loader
+    from sluice_amd.decoder import _StoreMoELayer, build_offloaded
+
+    E, k, H, I = 16, 4, 256, 128
+    sp = dict(E=E, H=H, I=I, k=k, fp8=False, e_bias=False, shared_I=0, scoring="softmax",
+              renorm=True, routed_scale=1.0, n_group=1, topk_group=1)
+    g = torch.Generator().manual_seed(11)
+    t = {}
+    for e in range(E):
+        for proj, shp in (("gate_proj", (I, H)), ("up_proj", (I, H)), ("down_proj", (H, I))):
+            t[f"model.layers.3.mlp.experts.{e}.{proj}.weight"] = (
+                torch.randn(shp, generator=g) * 0.05).to(torch.bfloat16)
+    save_file(t, str(tmp_path / "model.safetensors"))
+    store = loader.expert_stores_from_checkpoint(str(tmp_path), 3)
+    host13 = torch.stack([torch.cat([t[f"model.layers.3.mlp.experts.{e}.gate_proj.weight"],
+                                     t[f"model.layers.3.mlp.experts.{e}.up_proj.weight"]])
+                          for e in range(E)]).float().numpy()
+    host2 = torch.stack([t[f"model.layers.3.mlp.experts.{e}.down_proj.weight"]
+                         for e in range(E)]).float().numpy()
+    layer = _StoreMoELayer(sp, store, 0, DEV, None, "layers.3.mlp", gate_std=0.05)
+    off = build_offloaded([layer], 8, DEV)  # thr = 2
+    cache = off._caches[id(layer)]
+    assert cache.cpu_store["w13_weight"].data_ptr() == store["w13_weight"].tensor.data_ptr()
+    rng = np.random.default_rng(4)
+    for T in (1, 2, 6, 2):
+        off.set_step_signal(T, T, True)
+        x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(
+            torch.bfloat16).to(DEV)
+        out = layer(x)
+        torch.cuda.synchronize()
+        tw, ti = layer.select(layer.logits(x))
+        ref = om.fused_experts(x.float().cpu().numpy(), host13, host2, tw.cpu().numpy(),
+                               ti.cpu().numpy())
+        err = om.rel_l2(out.float().cpu().numpy(), ref)
+        print(f"  T={T} rel_l2={err:.2e}", flush=True)
+        assert err <= 1e-2
+    _check_slots(cache)
+    off.close()

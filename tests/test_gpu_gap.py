@@ -57,7 +57,7 @@ def _check_slots(cache, layer):
 
 
 def _cases(golden):
-    return [i for i, c in enumerate(golden["cases"]) if not c["pins"]]
+    return list(range(len(golden["cases"])))
 
 
 def _case_ids():
@@ -67,7 +67,7 @@ def _case_ids():
     return [f"{g['cases'][i]['name']}-fh{int(g['cases'][i]['fast_hit'])}" for i in _cases(g)]
 
 
-@pytest.mark.parametrize("idx", range(18), ids=_case_ids())
+@pytest.mark.parametrize("idx", range(20), ids=_case_ids())
 def test_device_gap_replays_reference(monkeypatch, slru_golden, idx):
     case = slru_golden["cases"][_cases(slru_golden)[idx]]
     print(f"gap case {case['name']} fast_hit={case['fast_hit']}", flush=True)
@@ -77,12 +77,17 @@ def test_device_gap_replays_reference(monkeypatch, slru_golden, idx):
         emap = torch.tensor(case["local_of"], dtype=torch.int32)
     layer = _Layer(E, local_n, expert_map=emap)
     off = _offloader(monkeypatch, case["slots"], case["protect_frac"], case["fast_hit"])
+    if case["pins"]:
+        off._pin_layers = {0: list(case["pins"])}  # what SLUICE_PIN_FILE would hold
     off.wrap_modules(iter([layer]))
     with torch.cuda.device(DEV):
         off.post_init()
     cache = off._caches[id(layer)]
     off._rs_caches.append(cache)
     assert cache.free_slots == case["init"]["free_slots"]
+    assert cache.expert_in_slot == [None if v < 0 else v
+                                    for v in case["init"]["expert_in_slot"]]
+    _check_slots(cache, layer)  # pinned rows were copied in at install
     hs = torch.zeros((1, 64), dtype=torch.bfloat16, device=DEV)
     for n, step in enumerate(case["steps"]):
         ids = torch.tensor(step["ids"], dtype=torch.int32, device=DEV).view(-1, k)

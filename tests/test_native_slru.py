@@ -13,8 +13,10 @@ from oracle.slru import GapOverflow, LayerCache
 
 
 def _native_for(case):
+    pol = case.get("policy", {})
     c = NativeCache(case["E"], case["local_n"], case["slots"], case["protect_frac"],
-                    local_of=case["local_of"])
+                    local_of=case["local_of"], lfu=bool(pol.get("lfu")),
+                    counts=bool(pol.get("counts_every")))
     lof = case["local_of"] or list(range(case["E"]))
     cap = c.state()["protected_cap"]
     for g in case["pins"] or []:
@@ -129,6 +131,13 @@ def test_native_classic_matches_reference_vectors(classic_golden, idx):
         for key in ("slot_of", "expert_in_slot", "probation", "protected", "free_slots",
                     "map_is_standing", "protected_cap"):
             assert st[key] == want[key], (case["name"], n, key)
+        if "policy" in step:
+            pol, want_pol = c.policy(), step["policy"]
+            for key in ("freq", "lfu_steps", "steps_small", "steps_scan"):
+                assert pol[key] == want_pol[key], (case["name"], n, key)
+            if "counts_decode" in want_pol:
+                assert pol["counts_decode"] == want_pol["counts_decode"], (case["name"], n)
+                assert pol["counts_scan"] == want_pol["counts_scan"], (case["name"], n)
         if step.get("overflow"):
             break  # the reference raised: its map is left stale, and the trace ends
         if want["map_is_standing"]:
@@ -137,12 +146,13 @@ def test_native_classic_matches_reference_vectors(classic_golden, idx):
             assert last_map == want["map"], (case["name"], n)
 
 
-@pytest.mark.parametrize("E,S,k,frac,seed", [(64, 48, 6, 0.5, 7), (128, 64, 8, 0.5, 8),
-                                              (128, 32, 8, 0.9, 9), (256, 64, 8, 0.3, 10)])
-def test_native_classic_matches_oracle_long_random(E, S, k, frac, seed):
+@pytest.mark.parametrize("E,S,k,frac,seed,lfu", [
+    (64, 48, 6, 0.5, 7, False), (128, 64, 8, 0.5, 8, False), (128, 32, 8, 0.9, 9, False),
+    (256, 64, 8, 0.3, 10, False), (64, 16, 6, 0.5, 11, True), (128, 64, 8, 0.7, 12, True)])
+def test_native_classic_matches_oracle_long_random(E, S, k, frac, seed, lfu):
     rnd = random.Random(seed)
-    o = LayerCache(E, E, S, frac)
-    n = NativeCache(E, E, S, frac)
+    o = LayerCache(E, E, S, frac, lfu=lfu, counts=True)
+    n = NativeCache(E, E, S, frac, lfu=lfu, counts=True)
     hot = rnd.sample(range(E), min(E, 3 * S // 2))
     thr = max(1, S // k)
     for step in range(600):
@@ -173,6 +183,11 @@ def test_native_classic_matches_oracle_long_random(E, S, k, frac, seed):
             assert st[key] == snap[key], (step, key)
         assert st["map_is_standing"] == snap["map_is_standing"]
         assert st["counters"]["misses"] == o.misses
+        pol = n.policy()
+        assert pol["freq"] == sorted([l, f] for l, f in o.freq.items())
+        assert (pol["counts_decode"], pol["counts_scan"]) == o.counts
+        assert (pol["steps_small"], pol["steps_scan"], pol["lfu_steps"]) == (
+            o.steps_small, o.steps_scan, o.lfu_steps)
 
 
 def test_native_classic_argument_checks():

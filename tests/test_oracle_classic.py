@@ -10,8 +10,10 @@ from tests.conftest import classic_vectors
 
 
 def _oracle_for(case):
+    pol = case.get("policy", {})
     c = LayerCache(case["E"], case["local_n"], case["slots"], case["protect_frac"],
-                   local_of=case["local_of"])
+                   local_of=case["local_of"], lfu=bool(pol.get("lfu")),
+                   counts=bool(pol.get("counts_every")))
     for g in case["pins"] or []:
         loc = c.local_of[g]
         if loc >= 0 and c.protected_cap > 0:
@@ -34,6 +36,11 @@ def test_golden_cases_exercise_waves_and_every_signal(classic_golden):
                 else None) for s in steps}
     assert len(signals) >= 4
     assert any(s["kind"] == "gap" for c in cases for s in c["steps"])
+    # the opt-in policies: LFU aged at least once, counts with JSONL snapshots
+    lfu = [c for c in cases if c.get("policy", {}).get("lfu")]
+    assert lfu and all(any(s["policy"]["lfu_steps"] == 0 for s in c["steps"][50:]
+                           if s["kind"] == "classic") for c in lfu)
+    assert any(len(c.get("counts_jsonl", [])) >= 3 for c in cases)
 
 
 @pytest.mark.parametrize("idx", range(len(classic_vectors()["cases"])))
@@ -62,6 +69,13 @@ def test_oracle_classic_matches_reference_vectors(classic_golden, idx):
         got = _state(c)
         for key, want in step["state"].items():
             assert got[key] == want, (case["name"], n, key)
+        if "policy" in step:
+            pol = step["policy"]
+            assert sorted([l, f] for l, f in c.freq.items()) == pol["freq"], (case["name"], n)
+            assert c.lfu_steps == pol["lfu_steps"], n
+            assert (c.steps_small, c.steps_scan) == (pol["steps_small"], pol["steps_scan"]), n
+            if "counts_decode" in pol:
+                assert c.counts == (pol["counts_decode"], pol["counts_scan"]), (case["name"], n)
 
 
 def test_classic_hand_worked_waves():
