@@ -55,6 +55,7 @@ NON_EXPERT_WEIGHTS = frozenset(
 PROTECT_FRAC_ENV = "SLUICE_PROTECT_FRAC"
 ROUTER_SPLIT_ENV = "SLUICE_ROUTER_SPLIT"
 PIECEWISE_ENV = "SLUICE_PIECEWISE"
+GRAPH_ENV = "SLUICE_GRAPH"
 FAST_HIT_ENV = "SLUICE_RS_FAST_HIT"
 NOOP_ENV = "SLUICE_RS_NOOP"
 # Opt-in policies (src/sluice/offloader.py:97-118): LFU-ordered protected
@@ -180,6 +181,7 @@ class ExpertStreamOffloader:
         self.protect_frac = min(max(frac, 0.0), 0.9)
         self.piecewise = os.environ.get(PIECEWISE_ENV, "0") == "1"
         self.router_split = os.environ.get(ROUTER_SPLIT_ENV, "0") == "1"
+        self.graph_mode = os.environ.get(GRAPH_ENV, "0") == "1"
         self._rs_fast_hit = os.environ.get(FAST_HIT_ENV, "0") == "1"
         self._rs_noop = os.environ.get(NOOP_ENV, "0") == "1"
         if self._rs_noop:
@@ -285,6 +287,16 @@ class ExpertStreamOffloader:
         for module in self._layers:
             self._install_cache(module)
             self._wrap_apply(module)
+        # SLUICE_GRAPH relaxed the eager guard on the promise that every
+        # layer is static-full (a constant map is safe to capture)
+        if self.graph_mode:
+            streaming = [k_ for k_, c in self._caches.items() if not c.static_full]
+            if streaming:
+                raise RuntimeError(
+                    "Sluice: SLUICE_GRAPH=1 requires every layer to be static_full (slots >= "
+                    f"local experts), but {len(streaming)} layer(s) are streaming. A captured "
+                    "graph would freeze a changing expert map. Raise SLUICE_SLOTS to full "
+                    "residency or unset SLUICE_GRAPH.")
         if self._caches:
             host = sum(c.bytes_per_expert * c.local_num_experts for c in self._caches.values()
                        if not c.static_full)
@@ -294,28 +306,71 @@ class ExpertStreamOffloader:
                         " (pinned)" if self.pin_memory else " (pageable)", vram / 2**30)
 
     def _check_config(self, cfg=None) -> None:
-        """Router-split envelope (src/sluice/offloader.py:807-842): under
-        piecewise capture the whole batch must fit slots//topk tokens."""
+        """The engine-configuration guards (src/sluice/offloader.py:663-851).
+
+        With vLLM installed the config must be readable (fail closed); without
+        vLLM (the standalone harness) there is nothing to check unless a
+        config object is passed in.  Refuses DP > 1 and EPLB (this build
+        serves one rank's experts and owns the expert map), and any CUDA-graph
+        mode that would capture the streaming hook: eager is required unless
+        SLUICE_PIECEWISE (the hook runs in a graph break; FULL capture is
+        still refused) or SLUICE_GRAPH (every layer static-full, checked in
+        post_init).  Under piecewise it makes the MoE ops and the gap op
+        graph split points and enforces the router-split envelope: the whole
+        batch must fit slots // top_k tokens.  Records the speculative depth
+        the decode classifier needs."""
         if cfg is None:
             try:
-                from vllm.config import get_current_vllm_config
-
+                from vllm.config import get_current_vllm_config  # type: ignore
+            except ImportError:
+                return  # no engine: the standalone harness drives the offloader
+            try:
                 cfg = get_current_vllm_config()
-            except Exception:
-                cfg = None
-        if cfg is None:
-            return
-        # A speculative-decode request verifies 1 + k tokens: its decode
-        # region spans ndec * (1 + k) rows (src/sluice/offloader.py:843-851).
-        sc = getattr(cfg, "speculative_config", None)
-        k_spec = getattr(sc, "num_speculative_tokens", 0) if sc is not None else 0
-        try:
-            self._spec_tokens = max(int(k_spec or 0), 0)
-        except (TypeError, ValueError):
-            self._spec_tokens = 0
+            except Exception as e:
+                raise RuntimeError("Sluice: could not read the vLLM config to verify it is safe "
+                                   "(DP/EPLB/eager); refusing to run. This usually means an "
+                                   "unexpected vLLM version.") from e
+            if cfg is None:
+                raise RuntimeError("Sluice: vLLM config is None; cannot verify a safe "
+                                   "configuration (DP/EPLB/eager). Refusing to run.")
+        pc = getattr(cfg, "parallel_config", None)
+        if pc is not None:
+            if (getattr(pc, "data_parallel_size", 1) or 1) > 1:
+                raise RuntimeError("Sluice (MI355X build): data parallelism > 1 is not supported "
+                                   "(one rank's expert shard per process; no post-dispatch "
+                                   "seam).")
+            if getattr(pc, "enable_eplb", False):
+                raise RuntimeError("Sluice: EPLB is unsupported (it re-registers the expert map "
+                                   "buffer over Sluice's slot map).")
+        relax_eager = self.graph_mode or self.piecewise
+        mc = getattr(cfg, "model_config", None)
+        if mc is not None and not getattr(mc, "enforce_eager", False) and not relax_eager:
+            raise RuntimeError(
+                "Sluice: requires eager execution — run with --enforce-eager. Without it, "
+                "CUDA-graph capture freezes a stale expert map (silently wrong output) and stock "
+                "torch.compile skips the post_init that installs Sluice's expert cache. (Set "
+                "SLUICE_GRAPH=1 only with slots >= experts / static_full.)")
+        cc = getattr(cfg, "compilation_config", None)
+        cg = getattr(cc, "cudagraph_mode", None) if cc is not None else None
+        cg_name = getattr(cg, "name", str(cg)) if cg is not None else "NONE"
+        if self.piecewise and "FULL" in cg_name:
+            raise RuntimeError(
+                "Sluice: SLUICE_PIECEWISE requires PIECEWISE cudagraph (the hook runs eager in a "
+                f"graph break); got {cg_name}. FULL would try to capture the hook's D2H sync.")
+        if cg is not None and cg_name != "NONE" and not relax_eager:
+            raise RuntimeError(
+                "Sluice: CUDA graphs would capture a frozen expert map and replay it with stale "
+                "routing (silently wrong outputs). Run with enforce_eager (--enforce-eager).")
+        if self.piecewise and cc is not None:
+            # the MoE layer (whose apply runs the hook) and the gap op are
+            # eager gaps between the captured pieces
+            ops_ = list(getattr(cc, "splitting_ops", None) or [])
+            wanted = ["vllm::moe_forward", "vllm::moe_forward_shared"]
+            if self.router_split:
+                wanted.append("vllm::sluice_stream_gap")
+            cc.splitting_ops = ops_ + [op for op in wanted if op not in ops_]
         if self.router_split and self.piecewise:
             topk = 8
-            mc = getattr(cfg, "model_config", None)
             hf = getattr(mc, "hf_config", None) if mc is not None else None
             for src in (hf, getattr(hf, "text_config", None)):
                 v = getattr(src, "num_experts_per_tok", None) if src else None
@@ -333,14 +388,14 @@ class ExpertStreamOffloader:
                     f"Got max_num_batched_tokens={mbt} > slots//topk={thr}. Set "
                     f"--max-num-batched-tokens {thr} (prefill runs in {thr}-token chunks) or "
                     "raise SLUICE_SLOTS.")
-            cc = getattr(cfg, "compilation_config", None)
-            if cc is not None:
-                ops_ = list(getattr(cc, "splitting_ops", None) or [])
-                for op in ("vllm::moe_forward", "vllm::moe_forward_shared",
-                           "vllm::sluice_stream_gap"):
-                    if op not in ops_:
-                        ops_.append(op)
-                cc.splitting_ops = ops_
+        # A speculative-decode request verifies 1 + k tokens: its decode
+        # region spans ndec * (1 + k) rows (src/sluice/offloader.py:843-851).
+        sc = getattr(cfg, "speculative_config", None)
+        k_spec = getattr(sc, "num_speculative_tokens", 0) if sc is not None else 0
+        try:
+            self._spec_tokens = max(int(k_spec or 0), 0)
+        except (TypeError, ValueError):
+            self._spec_tokens = 0
 
     @staticmethod
     def _infer_device(module: nn.Module) -> torch.device:
