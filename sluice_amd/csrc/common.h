@@ -57,3 +57,42 @@ __device__ __forceinline__ u32x4_t ldg16(const void* p) {
 __device__ __forceinline__ u32x4_t ldg16_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
 }
+
+// Wave-wide reductions on DPP: row_shr:1,2,4,8 leave each 16-lane row's
+// result in its lane 15, row_bcast:15 and row_bcast:31 carry it into lane
+// 63, which every lane then reads as a scalar.  Lanes a DPP step cannot
+// source from take the identity.  (An xor-shuffle butterfly compiles to
+// ds_bpermute round trips through LDS, several times slower per step.)
+// Every lane gets the result.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t identity, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v, uint32_t identity, Op op) {
+  v = op(v, dpp_mov<0x111, 0xf>(identity, v));
+  v = op(v, dpp_mov<0x112, 0xf>(identity, v));
+  v = op(v, dpp_mov<0x114, 0xf>(identity, v));
+  v = op(v, dpp_mov<0x118, 0xf>(identity, v));
+  v = op(v, dpp_mov<0x142, 0xa>(identity, v));
+  v = op(v, dpp_mov<0x143, 0xc>(identity, v));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  return wave_reduce_u32(v, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+  return __uint_as_float(wave_reduce_u32(__float_as_uint(v), 0xff800000u, [](uint32_t a,
+                                                                              uint32_t b) {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }));
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  return __uint_as_float(wave_reduce_u32(__float_as_uint(v), 0u, [](uint32_t a, uint32_t b) {
+    return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+  }));
+}

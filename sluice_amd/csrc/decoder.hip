@@ -4,7 +4,10 @@
 // model otherwise spends most of its time launching 2-5 us kernels.
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.h"
+#include "route.h"
 #include "sluice_decoder.h"
 #include "stream.h"
 
@@ -12,17 +15,9 @@ namespace {
 
 constexpr int kT = 256;  // threads per workgroup (4 waves)
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, SLUICE_WAVE);
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return wave_sum_f32(v); }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, SLUICE_WAVE));
-  return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return wave_max_f32(v); }
 
 // Block-wide sum / max over kT threads (all threads get the result).
 __device__ float block_sum(float v, float* red) {
@@ -130,33 +125,66 @@ __global__ __launch_bounds__(kT) void silu_mul_kernel(const uint16_t* __restrict
 // ---------------------------------------------------------------------------
 constexpr int kMaxRows = 16;
 
+// Lane partial sums of one expert's logits for every token row over the H
+// quarter q: lane covers 8 elements per 512-wide step.  MAXR >= rows rows are
+// loaded unconditionally (rows past the last repeat it), so each step's
+// loads are all in flight together; the gate kernels below both use it, so
+// their logits are the same bits whatever MAXR they run with.
+template <int MAXR>
+__device__ __forceinline__ void gate_partial(const uint16_t* __restrict__ hn,
+                                             const uint16_t* __restrict__ wr, int rows, int H,
+                                             int q, float (&acc)[MAXR]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int t = 0; t < MAXR; ++t) acc[t] = 0.f;
+  const int h0 = q * (H / 4), h1 = h0 + H / 4;
+  for (int i = h0 + lane * 8; i < h1; i += 64 * 8) {
+    const u32x4_t wq = *reinterpret_cast<const u32x4_t*>(wr + i);
+    u32x4_t xq[MAXR];
+#pragma unroll
+    for (int t = 0; t < MAXR; ++t) {
+      const int tt = t < rows ? t : rows - 1;
+      xq[t] = *reinterpret_cast<const u32x4_t*>(hn + (size_t)tt * H + i);
+    }
+    float wv[8];
+    unpack8(wq, wv);
+#pragma unroll
+    for (int t = 0; t < MAXR; ++t) {
+      float xv[8];
+      unpack8(xq[t], xv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[t] += wv[j] * xv[j];
+    }
+  }
+}
+
+// The logit from the four quarter sums (quarters in order) plus the
+// step's synthetic routing bias.
+__device__ __forceinline__ float gate_finish(float q0, float q1, float q2, float q3,
+                                             const float* __restrict__ bias_table,
+                                             const int64_t* __restrict__ step, int n_steps,
+                                             int bias_rows, int t, int e, int E) {
+  float v = q0 + q1 + q2 + q3;
+  if (bias_table != nullptr) {
+    long long st = *step;
+    st = ((st % n_steps) + n_steps) % n_steps;
+    v += bias_table[((size_t)st * bias_rows + t) * E + e];
+  }
+  return v;
+}
+
+template <int MAXR>
 __global__ __launch_bounds__(kT) void gate_logits_kernel(
     const uint16_t* __restrict__ hn, const uint16_t* __restrict__ wg,
     const float* __restrict__ bias_table, const int64_t* __restrict__ step, int n_steps,
     int bias_rows, int rows, int H, int E, float* __restrict__ out) {
-  __shared__ float red[kT / 64][kMaxRows];
+  __shared__ float red[kT / 64][MAXR];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int e = blockIdx.x;
-  float acc[kMaxRows];
+  float acc[MAXR];
+  gate_partial<MAXR>(hn, wg + (size_t)e * H, rows, H, wave, acc);
 #pragma unroll
-  for (int t = 0; t < kMaxRows; ++t) acc[t] = 0.f;
-  const uint16_t* wr = wg + (size_t)e * H;
-  const int h0 = wave * (H / 4), h1 = h0 + H / 4;
-  for (int i = h0 + lane * 8; i < h1; i += 64 * 8) {
-    float wv[8];
-    unpack8(*reinterpret_cast<const u32x4_t*>(wr + i), wv);
-#pragma unroll
-    for (int t = 0; t < kMaxRows; ++t) {
-      if (t < rows) {
-        float xv[8];
-        unpack8(*reinterpret_cast<const u32x4_t*>(hn + (size_t)t * H + i), xv);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[t] += wv[j] * xv[j];
-      }
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < kMaxRows; ++t) {
+  for (int t = 0; t < MAXR; ++t) {
     if (t < rows) {
       const float v = wave_sum(acc[t]);
       if (lane == 0) red[wave][t] = v;
@@ -165,14 +193,111 @@ __global__ __launch_bounds__(kT) void gate_logits_kernel(
   __syncthreads();
   if (threadIdx.x < rows) {
     const int t = threadIdx.x;
-    float v = red[0][t] + red[1][t] + red[2][t] + red[3][t];
-    if (bias_table != nullptr) {
-      long long st = *step;
-      st = ((st % n_steps) + n_steps) % n_steps;
-      v += bias_table[((size_t)st * bias_rows + t) * E + e];
-    }
-    out[(size_t)t * E + e] = v;
+    out[(size_t)t * E + e] = gate_finish(red[0][t], red[1][t], red[2][t], red[3][t], bias_table,
+                                         step, n_steps, bias_rows, t, e, E);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Router logits + top-k routing in one launch.  A workgroup of 16 waves
+// computes 4 experts' logits (waves 4j..4j+3 take expert j's H quarters, as
+// gate_logits_kernel's waves do) and writes them through to memory with
+// device-coherent stores; the last workgroup to finish (a device-scope
+// counter, returned to zero by that workgroup) reads every logit back with
+// device-coherent loads and routes the tokens, one wave each, with
+// route_token -- the same ids and weight bits route_topk_kernel gives for
+// the same logits.  Workgroups never wait for each other.
+// ---------------------------------------------------------------------------
+constexpr int kGR = 1024;                // threads per workgroup (16 waves)
+constexpr int kGRExperts = kGR / 256;    // experts per workgroup
+
+__device__ __forceinline__ void st_coh_f32(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coh_f32(const float* p) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+template <int NV, int SCORING, int MAXR>
+__global__ __launch_bounds__(kGR) void gate_route_kernel(
+    const uint16_t* __restrict__ hn, const uint16_t* __restrict__ wg,
+    const float* __restrict__ bias_table, const int64_t* __restrict__ step, int n_steps,
+    int bias_rows, int rows, int H, int E, int k, int renorm, float scale,
+    const float* __restrict__ score_bias, int n_group, int topk_group, float* __restrict__ logits,
+    int32_t* __restrict__ ids, float* __restrict__ w, int32_t* __restrict__ counter) {
+  __shared__ float red[kGR / 64][MAXR];
+  __shared__ RouteLds<NV * SLUICE_WAVE> rl[kGR / 64];
+  __shared__ int s_last;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int e = blockIdx.x * kGRExperts + (wave >> 2);
+  if (e < E) {
+    float acc[MAXR];
+    gate_partial<MAXR>(hn, wg + (size_t)e * H, rows, H, wave & 3, acc);
+#pragma unroll
+    for (int t = 0; t < MAXR; ++t) {
+      if (t < rows) {
+        const float v = wave_sum(acc[t]);
+        if (lane == 0) red[wave][t] = v;
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < kGRExperts * MAXR) {  // (expert j, row t)
+    const int j = threadIdx.x / MAXR, t = threadIdx.x % MAXR;
+    const int ej = blockIdx.x * kGRExperts + j;
+    if (t < rows && ej < E)
+      st_coh_f32(logits + (size_t)t * E + ej,
+                 gate_finish(red[4 * j][t], red[4 * j + 1][t], red[4 * j + 2][t],
+                             red[4 * j + 3][t], bias_table, step, n_steps, bias_rows, t, ej, E));
+    __builtin_amdgcn_s_waitcnt(0);  // written through before the workgroup is counted
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = atomicAdd(counter, 1) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (!s_last) return;
+  // every workgroup's logits are in memory; no other workgroup of this
+  // launch touches the counter again
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int t = wave; t < rows; t += kGR / 64) {
+    const float* row = logits + (size_t)t * E;
+    route_token<NV, SCORING>([&](int x) { return ld_coh_f32(row + x); }, E, k, renorm, scale,
+                             score_bias, n_group, topk_group, rl[wave], ids + (size_t)t * k,
+                             w + (size_t)t * k);
+  }
+}
+
+// Row buckets of the gate kernels: rows <= MAXR loaded per step.
+template <typename F>
+void with_row_bucket(int rows, F f) {
+  if (rows <= 1)
+    f(std::integral_constant<int, 1>{});
+  else if (rows <= 4)
+    f(std::integral_constant<int, 4>{});
+  else if (rows <= 8)
+    f(std::integral_constant<int, 8>{});
+  else
+    f(std::integral_constant<int, 16>{});
+}
+
+template <int NV>
+void launch_gate_route(int scoring, dim3 grid, hipStream_t st, const uint16_t* hn,
+                       const uint16_t* wg, const float* bt, const int64_t* step, int n_steps,
+                       int bias_rows, int rows, int H, int E, int k, int renorm, float scale,
+                       const float* sb, int ng, int tg, float* logits, int32_t* ids, float* w,
+                       int32_t* counter) {
+  with_row_bucket(rows, [&](auto mr) {
+    constexpr int R = decltype(mr)::value;
+    if (scoring == 0)
+      hipLaunchKernelGGL((gate_route_kernel<NV, 0, R>), grid, dim3(kGR), 0, st, hn, wg, bt, step,
+                         n_steps, bias_rows, rows, H, E, k, renorm, scale, sb, ng, tg, logits,
+                         ids, w, counter);
+    else
+      hipLaunchKernelGGL((gate_route_kernel<NV, 1, R>), grid, dim3(kGR), 0, st, hn, wg, bt, step,
+                         n_steps, bias_rows, rows, H, E, k, renorm, scale, sb, ng, tg, logits,
+                         ids, w, counter);
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -808,9 +933,53 @@ extern "C" int sluice_dec_gate_logits(const void* hn, const void* wg, const floa
     return SLUICE_E_INVAL;
   if (((uintptr_t)hn | (uintptr_t)wg) & 15) return SLUICE_E_INVAL;
   if (rows == 0) return SLUICE_OK;
-  hipLaunchKernelGGL(gate_logits_kernel, dim3(E), dim3(kT), 0, (hipStream_t)stream,
-                     (const uint16_t*)hn, (const uint16_t*)wg, bias_table, step, n_steps,
-                     bias_rows, rows, H, E, out);
+  with_row_bucket(rows, [&](auto mr) {
+    constexpr int R = decltype(mr)::value;
+    hipLaunchKernelGGL((gate_logits_kernel<R>), dim3(E), dim3(kT), 0, (hipStream_t)stream,
+                       (const uint16_t*)hn, (const uint16_t*)wg, bias_table, step, n_steps,
+                       bias_rows, rows, H, E, out);
+  });
+  return (int)hipGetLastError();
+}
+
+extern "C" int sluice_dec_gate_route(const void* hn, const void* wg, const float* bias_table,
+                                     const int64_t* step, int n_steps, int bias_rows, int rows,
+                                     int H, int E, int k, int scoring, int renorm, float scale,
+                                     const float* score_bias, int n_group, int topk_group,
+                                     float* logits, int32_t* ids, float* w, int32_t* counter,
+                                     sluice_stream_t stream) {
+  if (rows < 0 || rows > kMaxRows || H <= 0 || H % 32 != 0 || E <= 0 ||
+      E > 4 * SLUICE_WAVE || k <= 0 || k > SLUICE_MAX_TOPK || k > E || hn == nullptr ||
+      wg == nullptr || logits == nullptr || ids == nullptr || w == nullptr || counter == nullptr)
+    return SLUICE_E_INVAL;
+  if (scoring != 0 && scoring != 1) return SLUICE_E_INVAL;
+  if (bias_table != nullptr && (step == nullptr || n_steps <= 0 || bias_rows < rows))
+    return SLUICE_E_INVAL;
+  if (n_group < 1) n_group = 1;
+  if (n_group > 1) {
+    if (n_group > SLUICE_WAVE || E % n_group != 0) return SLUICE_E_INVAL;
+    if (topk_group < 1 || topk_group > n_group) return SLUICE_E_INVAL;
+    if (topk_group * (E / n_group) < k) return SLUICE_E_INVAL;
+  }
+  if (((uintptr_t)hn | (uintptr_t)wg) & 15) return SLUICE_E_INVAL;
+  if (rows == 0) return SLUICE_OK;
+  const dim3 grid((E + kGRExperts - 1) / kGRExperts);
+  hipStream_t st = (hipStream_t)stream;
+  const int nv = (E + SLUICE_WAVE - 1) / SLUICE_WAVE;
+  auto* h = (const uint16_t*)hn;
+  auto* g = (const uint16_t*)wg;
+  if (nv <= 1)
+    launch_gate_route<1>(scoring, grid, st, h, g, bias_table, step, n_steps, bias_rows, rows, H,
+                         E, k, renorm, scale, score_bias, n_group, topk_group, logits, ids, w,
+                         counter);
+  else if (nv <= 2)
+    launch_gate_route<2>(scoring, grid, st, h, g, bias_table, step, n_steps, bias_rows, rows, H,
+                         E, k, renorm, scale, score_bias, n_group, topk_group, logits, ids, w,
+                         counter);
+  else
+    launch_gate_route<4>(scoring, grid, st, h, g, bias_table, step, n_steps, bias_rows, rows, H,
+                         E, k, renorm, scale, score_bias, n_group, topk_group, logits, ids, w,
+                         counter);
   return (int)hipGetLastError();
 }
 
