@@ -63,20 +63,6 @@ int sluice_dec_gate_logits(const void* hn, const void* wg, const float* bias_tab
                            const int64_t* step, int n_steps, int bias_rows, int rows, int H, int E,
                            float* out, sluice_stream_t stream);
 
-/* Router logits and top-k routing in one launch: logits as
- * sluice_dec_gate_logits (the same bits), then ids/w as sluice_route_topk
- * computes them from those logits (same arguments, same bits).  This is the
- * gate GEMV of the router-split entry (src/sluice/offloader.py:2582)
- * followed by select_experts (2583-2585) without a kernel boundary: the
- * last workgroup to finish its logits routes every row.  E <= 256,
- * rows <= 16; counter is one device int32, zero before the first call
- * (every call leaves it zero).  Calls sharing a counter must not overlap. */
-int sluice_dec_gate_route(const void* hn, const void* wg, const float* bias_table,
-                          const int64_t* step, int n_steps, int bias_rows, int rows, int H, int E,
-                          int k, int scoring, int renorm, float scale, const float* score_bias,
-                          int n_group, int topk_group, float* logits, int32_t* ids, float* w,
-                          int32_t* counter, sluice_stream_t stream);
-
 /* MLA decode (DeepSeek-V2 latent attention with absorbed up-projections).
  * prep: q rows of q_stride elements holding nh heads of (nope then rope),
  *   kva rows of kva_stride elements holding lora then rope values

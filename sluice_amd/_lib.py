@@ -107,11 +107,6 @@ SIGNATURES = {
     "sluice_dec_gate_logits": (
         c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, _P]
     ),
-    "sluice_dec_gate_route": (
-        c_int,
-        [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P,
-         c_int, c_int, _P, _P, _P, _P, _P],
-    ),
     "sluice_dec_mla_prep": (
         c_int,
         [_P, c_int, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,

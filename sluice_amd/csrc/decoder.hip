@@ -7,7 +7,6 @@
 #include <type_traits>
 
 #include "common.h"
-#include "route.h"
 #include "sluice_decoder.h"
 #include "stream.h"
 
@@ -97,6 +96,67 @@ __global__ __launch_bounds__(kT) void add_rmsnorm_kernel(uint16_t* __restrict__ 
   }
 }
 
+// The same for H <= NI * 2048: every load (x, delta, w) goes out at once
+// and the rows stay in registers, so the kernel waits on memory once.
+template <int NI>
+__global__ __launch_bounds__(kT) void add_rmsnorm_reg_kernel(uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ delta,
+                                                             const uint16_t* __restrict__ w,
+                                                             uint16_t* __restrict__ out, int H,
+                                                             float eps) {
+  __shared__ float red[kT / 64];
+  const int r = blockIdx.x;
+  uint16_t* xr = x + (size_t)r * H;
+  const uint16_t* dr = delta != nullptr ? delta + (size_t)r * H : nullptr;
+  u32x4_t xv[NI], dv[NI], wv[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int i = threadIdx.x * 8 + j * kT * 8;
+    if (i < H) {
+      xv[j] = *reinterpret_cast<const u32x4_t*>(xr + i);
+      wv[j] = *reinterpret_cast<const u32x4_t*>(w + i);
+      if (dr != nullptr) dv[j] = *reinterpret_cast<const u32x4_t*>(dr + i);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int i = threadIdx.x * 8 + j * kT * 8;
+    if (i < H) {
+      if (dr != nullptr) {
+        float v[8], d[8];
+        unpack8(xv[j], v);
+        unpack8(dv[j], d);
+        u32x4_t o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          o[q] = pack2(v[2 * q] + d[2 * q], v[2 * q + 1] + d[2 * q + 1]);
+        *reinterpret_cast<u32x4_t*>(xr + i) = o;
+        xv[j] = o;  // the rounded sum, as the residual stream holds it
+      }
+      float v[8];
+      unpack8(xv[j], v);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) ss += v[q] * v[q];
+    }
+  }
+  const float rstd = rsqrtf(block_sum(ss, red) / (float)H + eps);
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int i = threadIdx.x * 8 + j * kT * 8;
+    if (i < H) {
+      float v[8], g[8];
+      unpack8(xv[j], v);
+      unpack8(wv[j], g);
+      u32x4_t o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = pack2(v[2 * q] * rstd * g[2 * q], v[2 * q + 1] * rstd * g[2 * q + 1]);
+      *reinterpret_cast<u32x4_t*>(out + (size_t)r * H + i) = o;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // SwiGLU activation.
 // ---------------------------------------------------------------------------
@@ -128,8 +188,8 @@ constexpr int kMaxRows = 16;
 // Lane partial sums of one expert's logits for every token row over the H
 // quarter q: lane covers 8 elements per 512-wide step.  MAXR >= rows rows are
 // loaded unconditionally (rows past the last repeat it), so each step's
-// loads are all in flight together; the gate kernels below both use it, so
-// their logits are the same bits whatever MAXR they run with.
+// loads are all in flight together (loads under per-row conditions were
+// each waited for before the next was issued).
 template <int MAXR>
 __device__ __forceinline__ void gate_partial(const uint16_t* __restrict__ hn,
                                              const uint16_t* __restrict__ wr, int rows, int H,
@@ -198,77 +258,8 @@ __global__ __launch_bounds__(kT) void gate_logits_kernel(
   }
 }
 
-// ---------------------------------------------------------------------------
-// Router logits + top-k routing in one launch.  A workgroup of 16 waves
-// computes 4 experts' logits (waves 4j..4j+3 take expert j's H quarters, as
-// gate_logits_kernel's waves do) and writes them through to memory with
-// device-coherent stores; the last workgroup to finish (a device-scope
-// counter, returned to zero by that workgroup) reads every logit back with
-// device-coherent loads and routes the tokens, one wave each, with
-// route_token -- the same ids and weight bits route_topk_kernel gives for
-// the same logits.  Workgroups never wait for each other.
-// ---------------------------------------------------------------------------
-constexpr int kGR = 1024;                // threads per workgroup (16 waves)
-constexpr int kGRExperts = kGR / 256;    // experts per workgroup
 
-__device__ __forceinline__ void st_coh_f32(float* p, float v) {
-  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_coh_f32(const float* p) {
-  return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p),
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-}
-
-template <int NV, int SCORING, int MAXR>
-__global__ __launch_bounds__(kGR) void gate_route_kernel(
-    const uint16_t* __restrict__ hn, const uint16_t* __restrict__ wg,
-    const float* __restrict__ bias_table, const int64_t* __restrict__ step, int n_steps,
-    int bias_rows, int rows, int H, int E, int k, int renorm, float scale,
-    const float* __restrict__ score_bias, int n_group, int topk_group, float* __restrict__ logits,
-    int32_t* __restrict__ ids, float* __restrict__ w, int32_t* __restrict__ counter) {
-  __shared__ float red[kGR / 64][MAXR];
-  __shared__ RouteLds<NV * SLUICE_WAVE> rl[kGR / 64];
-  __shared__ int s_last;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int e = blockIdx.x * kGRExperts + (wave >> 2);
-  if (e < E) {
-    float acc[MAXR];
-    gate_partial<MAXR>(hn, wg + (size_t)e * H, rows, H, wave & 3, acc);
-#pragma unroll
-    for (int t = 0; t < MAXR; ++t) {
-      if (t < rows) {
-        const float v = wave_sum(acc[t]);
-        if (lane == 0) red[wave][t] = v;
-      }
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x < kGRExperts * MAXR) {  // (expert j, row t)
-    const int j = threadIdx.x / MAXR, t = threadIdx.x % MAXR;
-    const int ej = blockIdx.x * kGRExperts + j;
-    if (t < rows && ej < E)
-      st_coh_f32(logits + (size_t)t * E + ej,
-                 gate_finish(red[4 * j][t], red[4 * j + 1][t], red[4 * j + 2][t],
-                             red[4 * j + 3][t], bias_table, step, n_steps, bias_rows, t, ej, E));
-    __builtin_amdgcn_s_waitcnt(0);  // written through before the workgroup is counted
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = atomicAdd(counter, 1) == (int)gridDim.x - 1;
-  __syncthreads();
-  if (!s_last) return;
-  // every workgroup's logits are in memory; no other workgroup of this
-  // launch touches the counter again
-  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (int t = wave; t < rows; t += kGR / 64) {
-    const float* row = logits + (size_t)t * E;
-    route_token<NV, SCORING>([&](int x) { return ld_coh_f32(row + x); }, E, k, renorm, scale,
-                             score_bias, n_group, topk_group, rl[wave], ids + (size_t)t * k,
-                             w + (size_t)t * k);
-  }
-}
-
-// Row buckets of the gate kernels: rows <= MAXR loaded per step.
+// Row buckets of the gate kernel: rows <= MAXR loaded per step.
 template <typename F>
 void with_row_bucket(int rows, F f) {
   if (rows <= 1)
@@ -279,25 +270,6 @@ void with_row_bucket(int rows, F f) {
     f(std::integral_constant<int, 8>{});
   else
     f(std::integral_constant<int, 16>{});
-}
-
-template <int NV>
-void launch_gate_route(int scoring, dim3 grid, hipStream_t st, const uint16_t* hn,
-                       const uint16_t* wg, const float* bt, const int64_t* step, int n_steps,
-                       int bias_rows, int rows, int H, int E, int k, int renorm, float scale,
-                       const float* sb, int ng, int tg, float* logits, int32_t* ids, float* w,
-                       int32_t* counter) {
-  with_row_bucket(rows, [&](auto mr) {
-    constexpr int R = decltype(mr)::value;
-    if (scoring == 0)
-      hipLaunchKernelGGL((gate_route_kernel<NV, 0, R>), grid, dim3(kGR), 0, st, hn, wg, bt, step,
-                         n_steps, bias_rows, rows, H, E, k, renorm, scale, sb, ng, tg, logits,
-                         ids, w, counter);
-    else
-      hipLaunchKernelGGL((gate_route_kernel<NV, 1, R>), grid, dim3(kGR), 0, st, hn, wg, bt, step,
-                         n_steps, bias_rows, rows, H, E, k, renorm, scale, sb, ng, tg, logits,
-                         ids, w, counter);
-  });
 }
 
 // ---------------------------------------------------------------------------
@@ -906,9 +878,23 @@ extern "C" int sluice_dec_add_rmsnorm(void* x, const void* delta, const void* w,
     return SLUICE_E_INVAL;
   if (((uintptr_t)x | (uintptr_t)delta | (uintptr_t)w | (uintptr_t)out) & 15) return SLUICE_E_INVAL;
   if (rows == 0) return SLUICE_OK;
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(kT), 0, (hipStream_t)stream,
-                     (uint16_t*)x, (const uint16_t*)delta, (const uint16_t*)w, (uint16_t*)out, H,
-                     eps);
+  const int ni = (H + kT * 8 - 1) / (kT * 8);
+  auto* xp = (uint16_t*)x;
+  auto* dp = (const uint16_t*)delta;
+  auto* wp = (const uint16_t*)w;
+  auto* op = (uint16_t*)out;
+  hipStream_t st = (hipStream_t)stream;
+  if (ni <= 1)
+    hipLaunchKernelGGL(add_rmsnorm_reg_kernel<1>, dim3(rows), dim3(kT), 0, st, xp, dp, wp, op, H,
+                       eps);
+  else if (ni <= 2)
+    hipLaunchKernelGGL(add_rmsnorm_reg_kernel<2>, dim3(rows), dim3(kT), 0, st, xp, dp, wp, op, H,
+                       eps);
+  else if (ni <= 4)
+    hipLaunchKernelGGL(add_rmsnorm_reg_kernel<4>, dim3(rows), dim3(kT), 0, st, xp, dp, wp, op, H,
+                       eps);
+  else
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(kT), 0, st, xp, dp, wp, op, H, eps);
   return (int)hipGetLastError();
 }
 
@@ -939,47 +925,6 @@ extern "C" int sluice_dec_gate_logits(const void* hn, const void* wg, const floa
                        (const uint16_t*)hn, (const uint16_t*)wg, bias_table, step, n_steps,
                        bias_rows, rows, H, E, out);
   });
-  return (int)hipGetLastError();
-}
-
-extern "C" int sluice_dec_gate_route(const void* hn, const void* wg, const float* bias_table,
-                                     const int64_t* step, int n_steps, int bias_rows, int rows,
-                                     int H, int E, int k, int scoring, int renorm, float scale,
-                                     const float* score_bias, int n_group, int topk_group,
-                                     float* logits, int32_t* ids, float* w, int32_t* counter,
-                                     sluice_stream_t stream) {
-  if (rows < 0 || rows > kMaxRows || H <= 0 || H % 32 != 0 || E <= 0 ||
-      E > 4 * SLUICE_WAVE || k <= 0 || k > SLUICE_MAX_TOPK || k > E || hn == nullptr ||
-      wg == nullptr || logits == nullptr || ids == nullptr || w == nullptr || counter == nullptr)
-    return SLUICE_E_INVAL;
-  if (scoring != 0 && scoring != 1) return SLUICE_E_INVAL;
-  if (bias_table != nullptr && (step == nullptr || n_steps <= 0 || bias_rows < rows))
-    return SLUICE_E_INVAL;
-  if (n_group < 1) n_group = 1;
-  if (n_group > 1) {
-    if (n_group > SLUICE_WAVE || E % n_group != 0) return SLUICE_E_INVAL;
-    if (topk_group < 1 || topk_group > n_group) return SLUICE_E_INVAL;
-    if (topk_group * (E / n_group) < k) return SLUICE_E_INVAL;
-  }
-  if (((uintptr_t)hn | (uintptr_t)wg) & 15) return SLUICE_E_INVAL;
-  if (rows == 0) return SLUICE_OK;
-  const dim3 grid((E + kGRExperts - 1) / kGRExperts);
-  hipStream_t st = (hipStream_t)stream;
-  const int nv = (E + SLUICE_WAVE - 1) / SLUICE_WAVE;
-  auto* h = (const uint16_t*)hn;
-  auto* g = (const uint16_t*)wg;
-  if (nv <= 1)
-    launch_gate_route<1>(scoring, grid, st, h, g, bias_table, step, n_steps, bias_rows, rows, H,
-                         E, k, renorm, scale, score_bias, n_group, topk_group, logits, ids, w,
-                         counter);
-  else if (nv <= 2)
-    launch_gate_route<2>(scoring, grid, st, h, g, bias_table, step, n_steps, bias_rows, rows, H,
-                         E, k, renorm, scale, score_bias, n_group, topk_group, logits, ids, w,
-                         counter);
-  else
-    launch_gate_route<4>(scoring, grid, st, h, g, bias_table, step, n_steps, bias_rows, rows, H,
-                         E, k, renorm, scale, score_bias, n_group, topk_group, logits, ids, w,
-                         counter);
   return (int)hipGetLastError();
 }
 

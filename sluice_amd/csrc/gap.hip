@@ -10,8 +10,9 @@
 //   gap_kernel (device, capturable, one workgroup)
 //     - builds the step's sorted unique selected ids in LDS (ballot
 //       compaction) and counts the owned ids the standing map does not hold;
-//     - posts them to the layer's mailbox in host-mapped pinned memory
-//       (system-scope release store of a per-layer stamp);
+//     - posts them to the layer's mailbox in host-mapped pinned memory as
+//       8-byte words that each carry the record's stamp, so the words need
+//       no ordering and the kernel never waits for its bus writes to land;
 //     - writes the gap op's fresh copy of hidden_states;
 //     - waits for the host ONLY when residency has to change (a miss, or no
 //       standing map yet), then installs the map the host sent.  A step
@@ -137,14 +138,13 @@ __global__ __launch_bounds__(256) void map_refresh_kernel(int32_t* __restrict__ 
 // Mailbox of one layer (host pinned, coherent, mapped into the device).
 // ---------------------------------------------------------------------------
 struct GapMailbox {
-  // written by the device
-  int32_t req_stamp;   // stamp of the last posted record (written last)
-  int32_t n_uniq;      // sorted unique selected ids in uniq[]
-  int32_t n_miss;      // owned ids the device map does not hold
-  int32_t waits;       // 1: the device waits for a response to this record
+  // written by the device: the record.  Every word carries the record's
+  // stamp in its low half, so the host takes a word once its stamp matches
+  // and the device needs no ordering (and no wait) between the words.
+  uint64_t hdr;        // stamp | n_uniq << 32 | n_miss << 43 | waits << 54
   int32_t dev_status;  // first failed device wait (sticky; 0 = none)
-  int32_t dev_pad[11];
-  int32_t uniq[SLUICE_MAX_EXPERTS];
+  int32_t dev_pad[13];
+  uint64_t ent[SLUICE_MAX_EXPERTS];  // stamp | id << 32: sorted unique selected ids
   // written by the host
   int32_t ack_stamp;   // last record the host has copied out
   int32_t resp_stamp;  // stamp the response below answers (written last)
@@ -155,13 +155,25 @@ struct GapMailbox {
   int32_t slot_global[SLUICE_MAX_SLOTS];  // slot -> global id, -1 = empty
 };
 
+constexpr int kRecCountBits = 11;  // n_uniq, n_miss <= SLUICE_MAX_EXPERTS
+static_assert(SLUICE_MAX_EXPERTS < (1 << kRecCountBits), "record count field");
+
+__host__ __device__ inline uint64_t rec_word(int32_t stamp, uint32_t hi) {
+  return (uint64_t)(uint32_t)stamp | ((uint64_t)hi << 32);
+}
+__host__ __device__ inline uint32_t rec_hdr_hi(int n_uniq, int n_miss, int waits) {
+  return (uint32_t)n_uniq | ((uint32_t)n_miss << kRecCountBits) |
+         ((uint32_t)waits << (2 * kRecCountBits));
+}
+inline int32_t rec_stamp(uint64_t w) { return (int32_t)(uint32_t)w; }
+
 // The mailbox is coherent host memory, which the device reaches uncached
-// over the bus.  A system-scope store is written through; once a thread's
-// stores have completed (s_waitcnt) the host can see them, without the L2
-// write-back a system-scope release fence costs (several microseconds with
-// the step's dirty lines in L2).  Posted writes over the bus stay in order,
-// so entries completed before the stamp is stored are seen before it.
+// over the bus.  A system-scope store is written through; an aligned 8-byte
+// store is one bus write, so a record word is seen whole or not at all.
 __device__ __forceinline__ void st_host(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void st_host64(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ int32_t ld_host(const int32_t* p) {
@@ -190,13 +202,16 @@ __device__ int wait_eq(const int32_t* p, int32_t want, const int32_t* abort_flag
 
 // dev_state: [0] last stamp issued, [1] 1 once the host has installed a
 // standing map (device-side copy of mb->standing, which never goes back to
-// 0, so later gaps skip that PCIe read).
+// 0, so later gaps skip that bus read).
+constexpr int kGapMaxPerThread = SLUICE_MAX_EXPERTS / kLookupThreads;
+
 __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     const int32_t* __restrict__ ids, int n, int32_t* __restrict__ map,
     const int32_t* __restrict__ local_of, int E, GapMailbox* mb, int32_t* dev_state,
     const int32_t* abort_flag, long long timeout_ticks, const u32x4_t* __restrict__ copy_src,
     u32x4_t* __restrict__ copy_dst, int copy_vecs) {
   __shared__ int present[SLUICE_MAX_EXPERTS];
+  __shared__ int s_uniq[SLUICE_MAX_EXPERTS];
   __shared__ int wcount[kWaves];
   __shared__ int wmiss[kWaves];
   __shared__ int s_stamp, s_status, s_waits, s_standing;
@@ -204,10 +219,10 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
   const int wave = tid >> 6;
   const int lane = tid & 63;
 
-  // The op's fresh copy of hidden_states does not depend on the host: its
-  // first kCopyU vectors per thread are loaded now and stored after the
-  // record is written, so the loads overlap the mailbox round trips.
-  // (every load is issued, clamped into the buffer, so none waits on another)
+  // Loads that do not depend on each other go out together: the op's fresh
+  // copy of hidden_states (its first kCopyU vectors per thread, stored after
+  // the record is written), and the map / ownership of this thread's
+  // experts.  (every copy load is issued, clamped into the buffer)
   u32x4_t cv[kCopyU];
   if (copy_vecs > 0) {
 #pragma unroll
@@ -216,47 +231,77 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
       cv[u] = copy_src[i < copy_vecs ? i : copy_vecs - 1];
     }
   }
-
+  bool unmapped[kGapMaxPerThread];
+#pragma unroll
+  for (int c = 0; c < kGapMaxPerThread; ++c) {
+    const int e = c * kLookupThreads + tid;
+    unmapped[c] = e < E && local_of[e] >= 0 && map[e] < 0;
+  }
+  int32_t prev = 0, ack = 0;
   if (tid == 0) {
-    // The host must have copied out this layer's previous record before it
-    // is overwritten (it normally has, long ago).
-    const int32_t prev = dev_state[0];
-    int32_t s = prev + 1;
-    if (s <= 0) s = 1;
-    s_stamp = s;
+    prev = dev_state[0];
     s_standing = dev_state[1];
-    s_status = wait_eq<false>(&mb->ack_stamp, prev, abort_flag, timeout_ticks);
   }
   for (int e = tid; e < E; e += kLookupThreads) present[e] = 0;
   __syncthreads();
-  const bool can_post = s_status == 0;
+  // The host must have copied out this layer's previous record before it is
+  // overwritten (it normally has, long ago): the bus read of its ack goes
+  // out now and is checked after the ids are compacted.
+  if (tid == 0) ack = ld_host(&mb->ack_stamp);
+  for (int i = tid; i < n; i += kLookupThreads) {
+    const int g = ids[i];
+    if ((unsigned)g < (unsigned)E) present[g] = 1;
+  }
+  __syncthreads();
+  // Sorted unique selected ids into LDS (ballot compaction); misses = owned
+  // selected ids the device map does not hold.
   int base = 0, miss = 0;
-  if (can_post) {
-    for (int i = tid; i < n; i += kLookupThreads) {
-      const int g = ids[i];
-      if ((unsigned)g < (unsigned)E) present[g] = 1;
+#pragma unroll
+  for (int c = 0; c < kGapMaxPerThread; ++c) {
+    if (c * kLookupThreads >= E) break;
+    const int e = c * kLookupThreads + tid;
+    const bool f = e < E && present[e] != 0;
+    const bool m = f && unmapped[c];
+    const uint64_t fb = __ballot(f);
+    const uint64_t mbits = __ballot(m);
+    if (lane == 0) {
+      wcount[wave] = __popcll(fb);
+      wmiss[wave] = __popcll(mbits);
     }
     __syncthreads();
-    for (int c = 0; c < E; c += kLookupThreads) {
-      const int e = c + tid;
-      const bool f = e < E && present[e] != 0;
-      const bool m = f && local_of[e] >= 0 && map[e] < 0;
-      const uint64_t fb = __ballot(f);
-      const uint64_t mbits = __ballot(m);
-      if (lane == 0) {
-        wcount[wave] = __popcll(fb);
-        wmiss[wave] = __popcll(mbits);
-      }
-      __syncthreads();
-      int off = base;
-      for (int w = 0; w < wave; ++w) off += wcount[w];
-      if (f) st_host(&mb->uniq[off + mask_rank(fb)], e);
-      for (int w = 0; w < kWaves; ++w) {
-        base += wcount[w];
-        miss += wmiss[w];
-      }
-      __syncthreads();
+    int off = base;
+    for (int w = 0; w < wave; ++w) off += wcount[w];
+    if (f) s_uniq[off + mask_rank(fb)] = e;
+    for (int w = 0; w < kWaves; ++w) {
+      base += wcount[w];
+      miss += wmiss[w];
     }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    int32_t s = prev + 1;
+    if (s <= 0) s = 1;
+    s_stamp = s;
+    s_status = ack == prev ? 0 : wait_eq<false>(&mb->ack_stamp, prev, abort_flag, timeout_ticks);
+    s_waits = 0;
+    if (s_status == 0) {
+      if (!s_standing && ld_host(&mb->standing) != 0) {
+        s_standing = 1;
+        dev_state[1] = 1;
+      }
+      s_waits = (miss > 0 || !s_standing) ? 1 : 0;
+      dev_state[0] = s;
+    } else {
+      st_host(&mb->dev_status, s_status);
+    }
+  }
+  __syncthreads();
+  if (s_status == 0) {
+    // the record: entries and header in any order (each word is stamped)
+    const int32_t s = s_stamp;
+    for (int i = tid; i < base; i += kLookupThreads)
+      st_host64(&mb->ent[i], rec_word(s, (uint32_t)s_uniq[i]));
+    if (tid == 0) st_host64(&mb->hdr, rec_word(s, rec_hdr_hi(base, miss, s_waits)));
   }
 #pragma unroll
   for (int u = 0; u < kCopyU; ++u) {
@@ -275,31 +320,6 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
       if (i < copy_vecs) copy_dst[i] = cv[u];
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's record entries have reached the host
-  __syncthreads();
-  if (tid == 0) {
-    s_waits = 0;
-    if (can_post) {
-      const int32_t s = s_stamp;
-      if (!s_standing && ld_host(&mb->standing) != 0) {
-        s_standing = 1;
-        dev_state[1] = 1;
-      }
-      const int waits = (miss > 0 || !s_standing) ? 1 : 0;
-      st_host(&mb->n_uniq, base);
-      st_host(&mb->n_miss, miss);
-      st_host(&mb->waits, waits);
-      dev_state[0] = s;
-      // every thread's entries (completed before the barrier) and the
-      // header reach the host before the stamp
-      __builtin_amdgcn_s_waitcnt(0);
-      st_host(&mb->req_stamp, s);
-      s_waits = waits;
-    } else {
-      st_host(&mb->dev_status, s_status);
-    }
-  }
-  __syncthreads();
   if (!s_waits) return;
   if (tid == 0) {
     const int st = wait_eq<true>(&mb->resp_stamp, s_stamp, abort_flag, timeout_ticks);
@@ -458,11 +478,13 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
   const int dev_status = __atomic_load_n(&mb->dev_status, __ATOMIC_ACQUIRE);
   if (dev_status != 0) return dev_status;  // a device wait failed earlier
   const int32_t want = next_stamp(L->host_stamp);
-  if (__atomic_load_n(&mb->req_stamp, __ATOMIC_ACQUIRE) != want) {
+  uint64_t hdr = __atomic_load_n(&mb->hdr, __ATOMIC_ACQUIRE);
+  double t0 = 0.0;
+  if (rec_stamp(hdr) != want) {
     if (!block) return kNothing;
-    const double t0 = now_s();
+    t0 = now_s();
     unsigned spins = 0;
-    while (__atomic_load_n(&mb->req_stamp, __ATOMIC_ACQUIRE) != want) {
+    while (rec_stamp(hdr = __atomic_load_n(&mb->hdr, __ATOMIC_ACQUIRE)) != want) {
       _mm_pause();
       if ((++spins & 4095u) == 0) {
         if (compute != nullptr) {
@@ -473,12 +495,26 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
       }
     }
   }
-  // Copy the record out, then let the device reuse the mailbox.
-  const int n_uniq = mb->n_uniq;
-  const int n_miss = mb->n_miss;
-  const bool waits = mb->waits != 0;
-  if (n_uniq < 0 || n_uniq > L->c.E) return SLUICE_E_STATE;
-  L->uniq.assign(mb->uniq, mb->uniq + n_uniq);
+  // Copy the record out (each entry once its stamp shows: the device writes
+  // the words in no particular order), then let the device reuse the mailbox.
+  const uint32_t hi = (uint32_t)(hdr >> 32);
+  const uint32_t cmask = (1u << kRecCountBits) - 1;
+  const int n_uniq = (int)(hi & cmask);
+  const int n_miss = (int)((hi >> kRecCountBits) & cmask);
+  const bool waits = ((hi >> (2 * kRecCountBits)) & 1u) != 0;
+  if (n_uniq > L->c.E) return SLUICE_E_STATE;
+  L->uniq.resize(n_uniq);
+  for (int i = 0; i < n_uniq; ++i) {
+    uint64_t w = __atomic_load_n(&mb->ent[i], __ATOMIC_ACQUIRE);
+    if (rec_stamp(w) != want) {
+      if (t0 == 0.0) t0 = now_s();
+      while (rec_stamp(w = __atomic_load_n(&mb->ent[i], __ATOMIC_ACQUIRE)) != want) {
+        _mm_pause();
+        if (now_s() - t0 > gap_timeout_s()) return SLUICE_E_TIMEOUT;
+      }
+    }
+    L->uniq[i] = (int32_t)(w >> 32);
+  }
   L->host_stamp = want;
   __atomic_store_n(&mb->ack_stamp, want, __ATOMIC_RELEASE);
 
@@ -711,7 +747,7 @@ extern "C" int sluice_gap_server_drain(sluice_gap_server* S, double timeout_s) {
         S->error.compare_exchange_strong(zero, dev_status);
         break;
       }
-      const int32_t posted = __atomic_load_n(&L->mb->req_stamp, __ATOMIC_ACQUIRE);
+      const int32_t posted = rec_stamp(__atomic_load_n(&L->mb->hdr, __ATOMIC_ACQUIRE));
       if (L->done_stamp.load(std::memory_order_acquire) == posted) break;
       if (S->error.load() != 0) break;
       if (now_s() - t0 > timeout_s) return SLUICE_E_TIMEOUT;
@@ -754,7 +790,7 @@ extern "C" int sluice_layer_gap_resync(sluice_layer* L) {
   L->host_stamp = dev_stamp;
   L->done_stamp.store(dev_stamp);
   __atomic_store_n(&L->mb->ack_stamp, dev_stamp, __ATOMIC_RELEASE);
-  __atomic_store_n(&L->mb->req_stamp, dev_stamp, __ATOMIC_RELEASE);
+  __atomic_store_n(&L->mb->hdr, rec_word(dev_stamp, 0u), __ATOMIC_RELEASE);
   __atomic_store_n(&L->mb->dev_status, 0, __ATOMIC_RELEASE);
   return SLUICE_OK;
 }
@@ -864,7 +900,7 @@ int wait_served(sluice_layer* L) {
       const int err = sluice_gap_server_error(L->server);
       if (err != 0) return err;
     }
-    const int32_t posted = __atomic_load_n(&L->mb->req_stamp, __ATOMIC_ACQUIRE);
+    const int32_t posted = rec_stamp(__atomic_load_n(&L->mb->hdr, __ATOMIC_ACQUIRE));
     if (L->done_stamp.load(std::memory_order_acquire) == posted) return SLUICE_OK;
     if (now_s() - t0 > gap_timeout_s()) return SLUICE_E_TIMEOUT;
     _mm_pause();

@@ -511,26 +511,36 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_kernel(const uint16_t* __r
 }
 
 // out[t, h] = bf16(scale * sum_j valid ? partial[t*k+j, h] : 0 + shared[t, h]),
-// j ascending, for 4 consecutive columns at h.
+// j ascending, for 4 consecutive columns at h.  Every pair's load is issued
+// up front (rows of invalid pairs are read and not added), so the thread
+// waits on memory once.
 template <bool COH = false>
 __device__ __forceinline__ void combine4(const float* __restrict__ partial,
                                          const int32_t* __restrict__ valid, int t, int k, int H,
                                          int h, float scale, const uint16_t* __restrict__ shared,
                                          uint16_t* __restrict__ out) {
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < k; ++j) {
-    const int p = t * k + j;
-    if (valid[p]) {
-      const float* src = partial + (size_t)p * H + h;
-      acc += COH ? __builtin_bit_cast(f32x4_t, ld16_coh(src))
-                 : *reinterpret_cast<const f32x4_t*>(src);
-    }
+  f32x4_t v[SLUICE_MAX_TOPK];
+  bool ok[SLUICE_MAX_TOPK];
+  u32x2_t sh = {0u, 0u};
+  if (shared != nullptr) sh = *reinterpret_cast<const u32x2_t*>(shared + (size_t)t * H + h);
+#pragma unroll
+  for (int j = 0; j < SLUICE_MAX_TOPK; ++j) {
+    const int p = t * k + (j < k ? j : k - 1);
+    ok[j] = j < k && valid[p] != 0;
+    const float* src = partial + (size_t)p * H + h;
+    v[j] = COH ? __builtin_bit_cast(f32x4_t, ld16_coh(src))
+               : *reinterpret_cast<const f32x4_t*>(src);
   }
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < SLUICE_MAX_TOPK; ++j)
+    if (ok[j]) acc += v[j];
   float o[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     o[r] = scale * acc[r];
-    if (shared != nullptr) o[r] += bf16_bits_to_f32(shared[(size_t)t * H + h + r]);
+    if (shared != nullptr)
+      o[r] += __uint_as_float(r & 1 ? (sh[r >> 1] & 0xffff0000u) : (sh[r >> 1] << 16));
   }
   *reinterpret_cast<u32x2_t*>(out + (size_t)t * H + h) =
       u32x2_t{pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
@@ -713,8 +723,8 @@ int dev_info(DevInfo** out) {
 #endif
 
 int check_common(int T, int H, int I, int k, int E, int S, const void* x, const void* w13,
-                 const void* w2, const float* tw, const int32_t* ti, void* ws, size_t ws_bytes,
-                 void* out) {
+                 const void* w2, const float* tw, const int32_t* ti, const void* shared, void* ws,
+                 size_t ws_bytes, void* out) {
   if (T < 0 || H <= 0 || I <= 0 || k <= 0 || k > SLUICE_MAX_TOPK || E <= 0 || S <= 0 ||
       S > SLUICE_MAX_SLOTS)
     return SLUICE_E_INVAL;
@@ -725,6 +735,7 @@ int check_common(int T, int H, int I, int k, int E, int S, const void* x, const 
   if (ws_bytes < workspace_bytes(T, H, I, k, nullptr, nullptr)) return SLUICE_E_INVAL;
   if (((uintptr_t)x | (uintptr_t)w13 | (uintptr_t)w2 | (uintptr_t)ws | (uintptr_t)out) & 15)
     return SLUICE_E_INVAL;
+  if ((uintptr_t)shared & 7) return SLUICE_E_INVAL;
   return SLUICE_OK;
 }
 
@@ -826,7 +837,7 @@ extern "C" int sluice_fused_experts_bf16(const void* x, const void* w13, const v
                                          int E, int S, float scale, const void* shared,
                                          void* workspace, size_t workspace_bytes_, void* out,
                                          sluice_stream_t stream) {
-  int rc = check_common(T, H, I, k, E, S, x, w13, w2, topk_w, topk_ids, workspace,
+  int rc = check_common(T, H, I, k, E, S, x, w13, w2, topk_w, topk_ids, shared, workspace,
                         workspace_bytes_, out);
   if (rc != SLUICE_OK || T == 0) return rc;
   Bf16W W{(const uint8_t*)w13, (const uint8_t*)w2, nullptr, nullptr};
@@ -844,7 +855,7 @@ extern "C" int sluice_fused_experts_fp8(const void* x, const void* w13, const fl
                                         sluice_stream_t stream) {
   if (block_n != kFp8Blk || block_k != kFp8Blk) return SLUICE_E_INVAL;
   if (H % kFp8Blk != 0 || I % kFp8Blk != 0) return SLUICE_E_INVAL;
-  int rc = check_common(T, H, I, k, E, S, x, w13, w2, topk_w, topk_ids, workspace,
+  int rc = check_common(T, H, I, k, E, S, x, w13, w2, topk_w, topk_ids, shared, workspace,
                         workspace_bytes_, out);
   if (rc != SLUICE_OK || T == 0) return rc;
   if (w13_scale == nullptr || w2_scale == nullptr) return SLUICE_E_INVAL;
@@ -906,7 +917,7 @@ extern "C" int sluice_moe_combine(const float* partial, const int32_t* plan, int
                                   float scale, const void* shared, void* out,
                                   sluice_stream_t stream) {
   if (T <= 0 || k <= 0 || H <= 0 || H % 4 || (long)T * k > SLUICE_MAX_PAIRS || !partial || !plan ||
-      !out)
+      !out || (((uintptr_t)shared | (uintptr_t)out | (uintptr_t)partial) & 7))
     return SLUICE_E_INVAL;
   return launch_combine(partial, plan + kPlanHeader + (size_t)kBlockInts * T * k, T, k, H, scale,
                         shared, out, (hipStream_t)stream);

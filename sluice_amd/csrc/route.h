@@ -1,9 +1,7 @@
 // Top-k routing of one token by one wave64 (gfx950).
 //
-// Shared by route_topk_kernel (one wave per token over logits in memory) and
-// the decoder's fused gate + routing kernel (the last workgroup of the gate
-// GEMV routes every token, one wave each), so both produce the same ids and
-// the same weight bits from the same logits.
+// route_topk_kernel runs it with one wave per token; any kernel that routes
+// with it gets the same ids and weight bits from the same logits.
 //
 // The closed forms are those of vLLM's select_experts as the router-split
 // entry calls it (src/sluice/offloader.py:2583-2585):

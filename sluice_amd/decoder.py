@@ -481,8 +481,6 @@ class _StoreMoELayer(nn.Module):
         self.shared = (_DenseMLP(H, sp["shared_I"], dev, g) if sp["shared_I"] else None)
         self.routing_bias = routing_bias
         self.sp = sp
-        # the fused gate + routing kernel's arrival counter (zero at rest)
-        self._route_counter = torch.zeros(1, dtype=torch.int32, device=dev)
 
         # vLLM runner surface, so attach_router_split arms this layer
         layer = self
@@ -529,34 +527,6 @@ class _StoreMoELayer(nn.Module):
                                   routed_scaling_factor=sp["routed_scale"],
                                   e_score_correction_bias=self.e_score_correction_bias,
                                   num_expert_group=sp["n_group"], topk_group=sp["topk_group"])
-
-    def route(self, hn):
-        """logits() then select() in one launch (the same logits, ids and
-        weights); layers with more than 256 experts or batches above 16 rows
-        run the two kernels."""
-        sp = self.sp
-        T = hn.shape[0]
-        if self.E > 256 or T > 16:
-            return self.select(self.logits(hn))
-        lib, check = _k()
-        dev = hn.device
-        lg = torch.empty((T, self.E), dtype=torch.float32, device=dev)
-        ti = torch.empty((T, self.top_k), dtype=torch.int32, device=dev)
-        tw = torch.empty((T, self.top_k), dtype=torch.float32, device=dev)
-        rb = self.routing_bias
-        sb = self.e_score_correction_bias
-        if sb is not None:
-            sb = sb.detach().float().contiguous()
-        check(lib.sluice_dec_gate_route(
-            hn.data_ptr(), self.gate.weight.data_ptr(),
-            None if rb is None else rb.table.data_ptr(), None if rb is None else rb.step.data_ptr(),
-            0 if rb is None else rb.table.shape[0], 0 if rb is None else rb.table.shape[1], T,
-            self.H, self.E, self.top_k, ops._SCORING[sp["scoring"]], int(bool(sp["renorm"])),
-            float(sp["routed_scale"]), None if sb is None else sb.data_ptr(), int(sp["n_group"]),
-            int(sp["topk_group"]), lg.data_ptr(), ti.data_ptr(), tw.data_ptr(),
-            self._route_counter.data_ptr(), _stream(hn)), "sluice_dec_gate_route")
-        self.last_route_logits = lg
-        return tw, ti
 
     def select_out(self, lg, ids_out):
         """select() writing the ids into ids_out (for timing the router alone)."""
@@ -734,7 +704,7 @@ class SyntheticDecoder:
                 io["delta"] = blk.mlp(io["hn"])
                 i += 1
                 continue
-            tw, ti = blk.moe.route(io["hn"])
+            tw, ti = blk.moe.select(blk.moe.logits(io["hn"]))
             io.update(tw=tw, ti=ti, i=i)
             return i
         hf = add_rmsnorm(io["x"], io["delta"], self.final_norm)

@@ -91,111 +91,6 @@ def test_gate_logits(rows, H, E, bias):
     assert torch.allclose(out.cpu(), ref, rtol=1e-4, atol=1e-4)
 
 
-# (rows, H, E, k, scoring, renorm, scale, n_group, topk_group, score bias, bias table)
-_GATE_ROUTE = [
-    (8, 2048, 64, 6, "softmax", False, 1.0, 1, 1, False, True),    # DeepSeek-V2-Lite
-    (1, 2048, 64, 6, "softmax", False, 1.0, 1, 1, False, False),
-    (8, 2048, 128, 8, "softmax", True, 1.0, 1, 1, False, True),    # Qwen3-30B-A3B
-    (12, 2048, 128, 8, "softmax", True, 1.0, 1, 1, False, True),
-    (16, 2048, 96, 4, "softmax", True, 1.0, 1, 1, False, False),   # ragged E, all 16 rows
-    (8, 7168, 256, 8, "sigmoid", True, 2.5, 8, 4, True, False),    # DeepSeek-V3
-    (3, 7168, 256, 8, "sigmoid", True, 2.5, 8, 4, True, True),
-]
-
-
-@pytest.mark.parametrize("rows,H,E,k,scoring,renorm,scale,ng,tg,sbias,btab", _GATE_ROUTE)
-def test_gate_route_matches_gate_then_route(rows, H, E, k, scoring, renorm, scale, ng, tg, sbias,
-                                            btab):
-    """The fused gate + routing kernel gives the bits of sluice_dec_gate_logits
-    followed by sluice_route_topk (logits, ids in order, weights), the ids the
-    oracle selects from those logits, the same result on repeated calls and
-    in graph replays, and leaves its arrival counter at zero."""
-    from oracle import routing as orr
-    from sluice_amd import ops
-
-    lib, check = _lib()
-    g = torch.Generator().manual_seed(E * 31 + rows)
-    hn = torch.randn((rows, H), generator=g).bfloat16().to(DEV)
-    wg = (0.02 * torch.randn((E, H), generator=g)).bfloat16().to(DEV)
-    steps, brow = 5, 16
-    table = torch.randn((steps, brow, E), generator=g).to(DEV)
-    step = torch.tensor(7, dtype=torch.long, device=DEV)
-    sb = (0.01 * torch.randn(E, generator=g)).to(DEV) if sbias else None
-    sc = ops._SCORING[scoring]
-    tab = (table.data_ptr(), step.data_ptr(), steps, brow) if btab else (None, None, 0, 0)
-    # unfused: logits, then routing
-    lg_ref = torch.empty((rows, E), dtype=torch.float32, device=DEV)
-    check(lib.sluice_dec_gate_logits(hn.data_ptr(), wg.data_ptr(), *tab, rows, H, E,
-                                     lg_ref.data_ptr(), _st()), "gate_logits")
-    ids_ref = torch.empty((rows, k), dtype=torch.int32, device=DEV)
-    w_ref = torch.empty((rows, k), dtype=torch.float32, device=DEV)
-    check(lib.sluice_route_topk(lg_ref.data_ptr(), 0, rows, E, k, sc, int(renorm), scale,
-                                None if sb is None else sb.data_ptr(), ng, tg, ids_ref.data_ptr(),
-                                w_ref.data_ptr(), _st()), "route_topk")
-    counter = torch.zeros(1, dtype=torch.int32, device=DEV)
-    lg = torch.full((rows, E), float("nan"), dtype=torch.float32, device=DEV)
-    ids = torch.full((rows, k), -7, dtype=torch.int32, device=DEV)
-    w = torch.full((rows, k), float("nan"), dtype=torch.float32, device=DEV)
-
-    def fused():
-        check(lib.sluice_dec_gate_route(hn.data_ptr(), wg.data_ptr(), *tab, rows, H, E, k, sc,
-                                        int(renorm), scale, None if sb is None else sb.data_ptr(),
-                                        ng, tg, lg.data_ptr(), ids.data_ptr(), w.data_ptr(),
-                                        counter.data_ptr(), _st()), "gate_route")
-
-    for rep in range(3):
-        lg.fill_(float("nan"))
-        ids.fill_(-7)
-        fused()
-        torch.cuda.synchronize()
-        assert torch.equal(lg, lg_ref), f"call {rep}: logits differ from gate_logits"
-        assert torch.equal(ids, ids_ref), f"call {rep}: ids differ from route_topk"
-        assert torch.equal(w.view(torch.int32), w_ref.view(torch.int32)), f"call {rep}: weights"
-        assert int(counter.item()) == 0
-    lgn = lg_ref.cpu().numpy()
-    if scoring == "softmax":
-        oid, ow = orr.softmax_topk(lgn, k, renorm=renorm)
-    else:
-        oid, ow = orr.sigmoid_topk(lgn, sb.cpu().numpy(), k, ng, tg, renorm=renorm, scale=scale)
-    assert np.array_equal(ids.cpu().numpy(), oid)
-    assert np.allclose(w.cpu().numpy(), ow, rtol=1e-5, atol=1e-6)
-    # graph replays, with eager work and synchronisation between them
-    gr = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(gr, stream=s):
-            fused()
-    torch.cuda.current_stream().wait_stream(s)
-    for rep in range(3):
-        ids.fill_(-7)
-        lg.fill_(float("nan"))
-        torch.cuda.synchronize()
-        gr.replay()
-        torch.cuda.synchronize()
-        assert torch.equal(lg, lg_ref) and torch.equal(ids, ids_ref), f"replay {rep}"
-        assert torch.equal(w.view(torch.int32), w_ref.view(torch.int32)), f"replay {rep}"
-        assert int(counter.item()) == 0
-
-
-def test_gate_route_rejects_what_it_cannot_route():
-    lib, _ = _lib()
-    hn = torch.zeros((2, 2048), dtype=torch.bfloat16, device=DEV)
-    wg = torch.zeros((512, 2048), dtype=torch.bfloat16, device=DEV)
-    out = torch.empty((2, 512), dtype=torch.float32, device=DEV)
-    ids = torch.empty((2, 8), dtype=torch.int32, device=DEV)
-    c = torch.zeros(1, dtype=torch.int32, device=DEV)
-    args = [hn.data_ptr(), wg.data_ptr(), None, None, 0, 0]
-    tail = [out.data_ptr(), ids.data_ptr(), out.data_ptr(), c.data_ptr(), _st()]
-    # E above 256
-    assert lib.sluice_dec_gate_route(*args, 2, 2048, 512, 8, 0, 0, 1.0, None, 1, 1, *tail) == -1
-    # more than 16 rows
-    assert lib.sluice_dec_gate_route(*args, 17, 2048, 64, 8, 0, 0, 1.0, None, 1, 1, *tail) == -1
-    # no counter
-    tail[3] = None
-    assert lib.sluice_dec_gate_route(*args, 2, 2048, 64, 8, 0, 0, 1.0, None, 1, 1, *tail) == -1
-
-
 @pytest.mark.parametrize("T,N,K", [(8, 3648, 2048), (1, 2048, 10944), (12, 5632, 2048),
                                    (16, 160, 128), (5, 176, 192), (8, 576, 2048)])
 def test_linear(T, N, K):

@@ -154,6 +154,76 @@ def _deterministic_case(ctypes, _lib, ops):
     assert om.rel_l2(outs[0].float().cpu().numpy(), ref) <= BF16_TOL
 
 
+def _staged(lib, x, w13, w2, tw, ids, emap, T, H, I, E, S, k, scale, sh, st, fp8=None):
+    """align -> gemm1 -> gemm2 -> combine, one stage entry point at a time."""
+    P = T * k
+    plan = torch.empty(lib.sluice_moe_plan_ints(T, k), dtype=torch.int32, device=DEV)
+    act = torch.empty((P, I), dtype=torch.bfloat16, device=DEV)
+    part = torch.empty((P, H), dtype=torch.float32, device=DEV)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=DEV)
+    assert lib.sluice_moe_align(ids.data_ptr(), T, k, emap.data_ptr(), E, S, plan.data_ptr(),
+                                st) == 0
+    if fp8 is None:
+        assert lib.sluice_moe_gemm1_bf16(x.data_ptr(), w13.data_ptr(), plan.data_ptr(), T, H, I,
+                                         k, act.data_ptr(), st) == 0
+        assert lib.sluice_moe_gemm2_bf16(act.data_ptr(), w2.data_ptr(), plan.data_ptr(),
+                                         tw.data_ptr(), T, H, I, k, part.data_ptr(), st) == 0
+    else:
+        s13, s2 = fp8
+        assert lib.sluice_moe_gemm1_fp8(x.data_ptr(), w13.data_ptr(), s13.data_ptr(),
+                                        plan.data_ptr(), T, H, I, k, act.data_ptr(), st) == 0
+        assert lib.sluice_moe_gemm2_fp8(act.data_ptr(), w2.data_ptr(), s2.data_ptr(),
+                                        plan.data_ptr(), tw.data_ptr(), T, H, I, k,
+                                        part.data_ptr(), st) == 0
+    assert lib.sluice_moe_combine(part.data_ptr(), plan.data_ptr(), T, k, H, scale,
+                                  None if sh is None else sh.data_ptr(), out.data_ptr(), st) == 0
+    return out
+
+
+@pytest.mark.parametrize("T,H,I,E,S,k,frac,shared,fp8", [
+    (8, 2048, 1408, 64, 48, 6, 0.85, True, False),   # V2-Lite shape, shared expert added
+    (12, 2048, 768, 128, 96, 8, 0.85, False, False),  # Qwen3 shape
+    (33, 256, 192, 16, 16, 4, 0.85, False, False),   # several blocks per slot
+    (4, 256, 64, 32, 4, 2, 0.0, True, False),        # nothing resident: out = shared
+    (8, 7168, 2048, 256, 12, 8, 0.85, True, True),   # V3 shape, fp8 + block scales
+])
+def test_fused_experts_matches_its_stages(T, H, I, E, S, k, frac, shared, fp8):
+    """fused_experts gives the bits of its stages run one entry point at a
+    time (align, gemm1, gemm2, combine), on every call."""
+    from sluice_amd import _lib, ops
+
+    lib = _lib.load()
+    rng = np.random.default_rng(T * 13 + I)
+    x = _bf16(rng.standard_normal((T, H))).to(DEV)
+    kw, scales = {}, None
+    if fp8:
+        def codes(shape):  # e4m3fn codes without the two NaN encodings
+            q = rng.integers(0, 256, size=shape, dtype=np.uint8)
+            q[(q & 0x7F) == 0x7F] = 0x38
+            return torch.from_numpy(q).to(DEV)
+
+        w13, w2 = codes((S, 2 * I, H)), codes((S, H, I))
+        scales = (torch.rand((S, 2 * I // 128, H // 128), device=DEV) * 0.02 + 0.01,
+                  torch.rand((S, H // 128, I // 128), device=DEV) * 0.02 + 0.01)
+        kw = dict(w1_scale=scales[0], w2_scale=scales[1], block_shape=[128, 128])
+    else:
+        w13 = _bf16(rng.standard_normal((S, 2 * I, H)) * 0.02).to(DEV)
+        w2 = _bf16(rng.standard_normal((S, H, I)) * 0.02).to(DEV)
+    ids = torch.from_numpy(_routing(T, E, k, rng)).to(DEV)
+    emap = torch.from_numpy(_emap(E, S, rng, frac)).to(DEV)
+    tw = torch.rand((T, k), device=DEV)
+    sh = _bf16(rng.standard_normal((T, H))).to(DEV) if shared else None
+    st = torch.cuda.current_stream().cuda_stream
+    ref = _staged(lib, x, w13, w2, tw, ids, emap, T, H, I, E, S, k, 1.5, sh, st, fp8=scales)
+    for rep in range(3):
+        got = ops.fused_experts(x, w13, w2, tw, ids, global_num_experts=E, expert_map=emap,
+                                routed_scaling_factor=1.5, shared_output=sh, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"call {rep}"
+    if frac == 0.0:
+        assert torch.equal(ref, sh)
+
+
 def test_fused_experts_bf16_identity_map_scale_shared():
     got, ref = _moe_case(8, 512, 128, 8, 8, 2, seed=9, use_map=False, scale=2.5, shared=True)
     assert om.rel_l2(got, ref) <= BF16_TOL
