@@ -387,7 +387,7 @@ __global__ __launch_bounds__(kA) void mla_attend_kernel(
     for (int j = 0; j < 8; ++j) ql[j] = qrow[j];
   }
   const float qp = q_pe[((size_t)t * nh + h) * kRope + lane];
-  constexpr int U = 4;
+  constexpr int U = 8;  // cache rows in flight per wave
   float lmax = -INFINITY;
   for (int l0 = wave; l0 < n; l0 += U * kAW) {
     float dsum[U];
@@ -410,9 +410,7 @@ __global__ __launch_bounds__(kA) void mla_attend_kernel(
       dsum[u] = d;
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-#pragma unroll
-      for (int u = 0; u < U; ++u) dsum[u] += __shfl_xor(dsum[u], off, SLUICE_WAVE);
+    for (int u = 0; u < U; ++u) dsum[u] = wave_sum(dsum[u]);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int l = l0 + u * kAW;
@@ -545,7 +543,23 @@ __global__ __launch_bounds__(64) void gqa_prep_kernel(
   v_cache[row + lane + 64] = vr[lane + 64];
 }
 
-// grid (c, nh).
+// Sum of v over each 16-lane row of the wave, left in the row's lane 15
+// (DPP row shifts; other lanes hold partial sums).
+__device__ __forceinline__ float row16_sum_to_lane15(float v) {
+  uint32_t u = __float_as_uint(v);
+  u = __float_as_uint(__uint_as_float(u) + __uint_as_float(dpp_mov<0x111, 0xf>(0u, u)));
+  u = __float_as_uint(__uint_as_float(u) + __uint_as_float(dpp_mov<0x112, 0xf>(0u, u)));
+  u = __float_as_uint(__uint_as_float(u) + __uint_as_float(dpp_mov<0x114, 0xf>(0u, u)));
+  u = __float_as_uint(__uint_as_float(u) + __uint_as_float(dpp_mov<0x118, 0xf>(0u, u)));
+  return __uint_as_float(u);
+}
+
+// grid (c, nh).  Scores: 16 lanes per cache row (8 elements each), 16 rows
+// per pass and kSP passes' loads in flight; values: each wave takes rows
+// w, w + 4, ... with kVP rows' loads in flight, a lane owning 2 columns.
+constexpr int kSP = 8;
+constexpr int kVP = 16;
+
 __global__ __launch_bounds__(kT) void gqa_attend_kernel(
     const float* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, const int64_t* __restrict__ pos, int nh, int kvh, int L,
@@ -563,27 +577,31 @@ __global__ __launch_bounds__(kT) void gqa_attend_kernel(
   __syncthreads();
   const uint16_t* kb = k_cache + ((size_t)t * kvh + g) * L * kHd;
   const uint16_t* vb = v_cache + ((size_t)t * kvh + g) * L * kHd;
-  // scores: 16 lanes per row (8 elements each), 16 rows per pass
   const int sub = tid & 15, rw = tid >> 4;
   float qv[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) qv[j] = sq[sub * 8 + j];
   float lmax = -INFINITY;
-  for (int l0 = 0; l0 < n; l0 += kT / 16) {
-    const int l = l0 + rw;
-    float d = 0.f;
-    if (l < n) {
-      float kv[8];
-      unpack8(*reinterpret_cast<const u32x4_t*>(kb + (size_t)l * kHd + sub * 8), kv);
+  for (int l0 = 0; l0 < n; l0 += kSP * (kT / 16)) {
+    u32x4_t kr[kSP];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) d += qv[j] * kv[j];
+    for (int u = 0; u < kSP; ++u) {
+      const int l = l0 + u * (kT / 16) + rw;
+      kr[u] = *reinterpret_cast<const u32x4_t*>(kb + (size_t)(l < n ? l : 0) * kHd + sub * 8);
     }
 #pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) d += __shfl_xor(d, off, SLUICE_WAVE);
-    d *= scale;
-    if (l < n) {
-      if (sub == 0) s[l] = d;
-      lmax = fmaxf(lmax, d);
+    for (int u = 0; u < kSP; ++u) {
+      const int l = l0 + u * (kT / 16) + rw;
+      float kv[8];
+      unpack8(kr[u], kv);
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) d += qv[j] * kv[j];
+      d = row16_sum_to_lane15(d) * scale;
+      if (sub == 15 && l < n) {
+        s[l] = d;
+        lmax = fmaxf(lmax, d);
+      }
     }
   }
   const float m = block_max(lmax, red);
@@ -595,20 +613,18 @@ __global__ __launch_bounds__(kT) void gqa_attend_kernel(
   }
   const float inv = 1.0f / block_sum(part, red);
   __syncthreads();
-  // out[d] = sum_l p[l] v[l][d]: wave w takes rows l = w, w + 4, ..., a lane
-  // owns 2 columns (4-byte loads), four rows in flight; waves summed in LDS.
-  constexpr int U = 4;
+  // out[d] = sum_l p[l] v[l][d]; waves summed in LDS.
   float a0 = 0.f, a1 = 0.f;
   const int wave = tid >> 6, lane = tid & 63;
-  for (int l0 = wave; l0 < n; l0 += U * (kT / 64)) {
-    uint32_t vv[U];
+  for (int l0 = wave; l0 < n; l0 += kVP * (kT / 64)) {
+    uint32_t vv[kVP];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < kVP; ++u) {
       const int l = l0 + u * (kT / 64);
       vv[u] = *reinterpret_cast<const uint32_t*>(vb + (size_t)(l < n ? l : 0) * kHd + 2 * lane);
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < kVP; ++u) {
       const int l = l0 + u * (kT / 64);
       const float pl = l < n ? s[l] : 0.f;
       a0 += pl * __uint_as_float(vv[u] << 16);
@@ -754,33 +770,25 @@ int device_cus() {
   return cus[dev];
 }
 
-// Parts of K per item: the split whose busiest CU finishes first, with an
-// item costing its bytes at ~27 GB/s per CU plus ~1.5 us, and the split's
-// hand-off another ~1.5 us.  ks * items <= 2 * CUs keeps the partials
-// within the workspace bound.
-int linear_parts(int items, int K, int cus) {
+// Parts of K per item, from per-kernel costs measured in replayed graphs on
+// MI355X (decode shapes, T = 1 and 8, N 2048-21888, K 2048-10944): the
+// hand-off of a split costs more than streaming a 2048-long row slice on
+// one CU when T > 4 (its partial tiles are larger), so short K stays whole
+// there; longer K splits in 3 (up to 4096) or 4.  ks * items <= 2 * CUs
+// keeps the partials within the workspace bound.
+int linear_parts(int items, int K, int T, int cus) {
   const int nc = K / 64;
-  int best = 1;
-  double best_us = 1e30;
-  for (int ks = 1; ks <= 16 && ks <= nc; ++ks) {
-    if (ks > 1 && (long)items * ks > 2L * cus) break;
-    const long n = (long)items * ks;
-    const long rounds = (n + cus - 1) / cus;
-    const double item_bytes = 32.0 * 2.0 * 64.0 * ((nc + ks - 1) / ks);
-    const double us = rounds * (item_bytes / 27.0e3 + 1.5) + (ks > 1 ? 1.5 : 0.0);
-    if (us < best_us * 0.97) {
-      best_us = us;
-      best = ks;
-    }
-  }
-  return best;
+  int ks = T > 4 ? (nc <= 32 ? 1 : nc <= 64 ? 3 : 4) : (nc <= 16 ? 1 : nc <= 64 ? 3 : 4);
+  if (ks > nc) ks = nc;
+  while (ks > 1 && (long)items * ks > 2L * cus) --ks;
+  return ks;
 }
 
 template <bool GLU>
 int launch_linear(const void* x, const void* w, int T, int N, int K, void* y, void* ws,
                   hipStream_t st) {
   const int items = GLU ? N / 32 : (N + 31) / 32;
-  const int ks = ws != nullptr ? linear_parts(items, K, device_cus()) : 1;
+  const int ks = ws != nullptr ? linear_parts(items, K, T, device_cus()) : 1;
   float* parts = (float*)ws;
   int* counters = ws != nullptr ? (int*)((char*)ws + kLinPartBytes) : nullptr;
   hipLaunchKernelGGL((linear_kernel<GLU>), dim3(items * ks), dim3(64 * kLinWaves), 0, st,
