@@ -126,20 +126,30 @@ int sluice_host_free(void* p);
  *   int32 (global -> slot, -1 = not resident: the pair contributes 0) or
  *   NULL (identity, ids are slots);
  *   out[t] = bf16( scale * sum_j w[t,j] * W2[s]·(silu(W13g[s]·x_t) * W13u[s]·x_t)
- *                  + shared[t] )                       (shared may be NULL).
+ *                  + SharedMLP(x_t) + shared[t] )
+ *   shared (may be NULL): a precomputed shared-expert output [T,H] bf16.
+ *   SharedMLP: the layer's shared experts run inside the same grouped
+ *     product (the traced tail's shared_experts(x), offloader.py:341-342,
+ *     2602, added unscaled): shared_w13 [2*shared_I, H] (gate rows, then up
+ *     rows), shared_w2 [H, shared_I]; shared_I a multiple of I (at most
+ *     4*I), or 0 with NULL weights for none.  It is computed as shared_I/I
+ *     groups of I channels, each one more expert block over every token.
  * fp8 variant: w13/w2 are e4m3fn with fp32 block scales of block_n x block_k
  * (128x128): w13_scale [S, ceil(2I/bn), ceil(H/bk)], w2_scale
- * [S, ceil(H/bn), ceil(I/bk)]; activations stay bf16.
- * Requires H % 64 == 0, I % 64 == 0, T*k <= SLUICE_MAX_PAIRS.
+ * [S, ceil(H/bn), ceil(I/bk)]; activations stay bf16.  Shared weights are
+ * e4m3fn too, with shared_w13_scale [2*shared_I/128, H/128] and
+ * shared_w2_scale [H/128, shared_I/128].
+ * Requires H % 64 == 0, I % 64 == 0, T*(k + shared_I/I) <= SLUICE_MAX_PAIRS.
  * The workspace (device) must hold sluice_fused_experts_workspace() bytes.
  * ---------------------------------------------------------------------- */
-size_t sluice_fused_experts_workspace(int T, int H, int I, int k);
+size_t sluice_fused_experts_workspace(int T, int H, int I, int k, int shared_I);
 
 int sluice_fused_experts_bf16(const void* x, const void* w13, const void* w2,
                               const float* topk_w, const int32_t* topk_ids,
                               const int32_t* expert_map, int T, int H, int I,
                               int k, int E, int S, float scale,
-                              const void* shared, void* workspace,
+                              const void* shared_w13, const void* shared_w2,
+                              int shared_I, const void* shared, void* workspace,
                               size_t workspace_bytes, void* out,
                               sluice_stream_t stream);
 
@@ -149,7 +159,9 @@ int sluice_fused_experts_fp8(const void* x, const void* w13,
                              const float* topk_w, const int32_t* topk_ids,
                              const int32_t* expert_map, int T, int H, int I,
                              int k, int E, int S, float scale,
-                             const void* shared, void* workspace,
+                             const void* shared_w13, const float* shared_w13_scale,
+                             const void* shared_w2, const float* shared_w2_scale,
+                             int shared_I, const void* shared, void* workspace,
                              size_t workspace_bytes, void* out,
                              sluice_stream_t stream);
 

@@ -61,7 +61,8 @@ def dequant_block(q: np.ndarray, scale: np.ndarray, block: int = 128) -> np.ndar
 
 
 def silu(v: np.ndarray) -> np.ndarray:
-    return v / (1.0 + np.exp(-v))
+    with np.errstate(over="ignore"):  # exp(-v) = inf for v << 0 gives the limit -0
+        return v / (1.0 + np.exp(-v))
 
 
 def fused_experts(x, w13, w2, topk_w, topk_ids, expert_map=None, scale: float = 1.0,
@@ -101,6 +102,20 @@ def fused_experts(x, w13, w2, topk_w, topk_ids, expert_map=None, scale: float = 
     if shared is not None:
         out += np.asarray(shared, dtype=np.float64)
     return out
+
+
+def shared_mlp(x, gate_up, down) -> np.ndarray:
+    """The shared experts as one SwiGLU MLP (the traced tail's
+    shared_experts(x), src/sluice/offloader.py:341-342, 2602; closed form of
+    TF:deepseek_v2/modeling_deepseek_v2.py DeepseekV2MLP):
+    down @ (silu(gate @ x_t) * (up @ x_t)), gate_up [2*Is, H] holding the
+    gate rows then the up rows, down [H, Is] -> [T, H] float64."""
+    x = np.asarray(x, dtype=np.float64)
+    gu = np.asarray(gate_up, dtype=np.float64)
+    d = np.asarray(down, dtype=np.float64)
+    Is = d.shape[1]
+    h = x @ gu.T
+    return (silu(h[:, :Is]) * h[:, Is:]) @ d.T
 
 
 def rel_l2(got, ref) -> float:

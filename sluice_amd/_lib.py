@@ -43,16 +43,16 @@ SIGNATURES = {
     "sluice_copy_rows": (c_int, [_P, _P, _P, c_int, _P]),
     "sluice_host_alloc": (c_int, [c_size_t, POINTER(c_void_p)]),
     "sluice_host_free": (c_int, [_P]),
-    "sluice_fused_experts_workspace": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "sluice_fused_experts_workspace": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "sluice_fused_experts_bf16": (
         c_int,
-        [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P,
-         c_size_t, _P, _P],
+        [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P, c_int,
+         _P, _P, c_size_t, _P, _P],
     ),
     "sluice_fused_experts_fp8": (
         c_int,
         [_P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,
-         c_float, _P, _P, c_size_t, _P, _P],
+         c_float, _P, _P, _P, _P, c_int, _P, _P, c_size_t, _P, _P],
     ),
     "sluice_fused_experts_status": (c_int, [_P, POINTER(c_int)]),
     "sluice_moe_set_fused": (c_int, [c_int]),

@@ -88,7 +88,8 @@ struct AlignScratch {
 };
 
 __device__ int build_plan(const int32_t* __restrict__ ids, int P, const int32_t* __restrict__ map,
-                          int E, int S, AlignScratch& sc, int32_t* blocks, int32_t* valid) {
+                          int E, int S, int T, int n_sh, AlignScratch& sc, int32_t* blocks,
+                          int32_t* valid) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   for (int s = tid; s < S; s += kThreads) {
@@ -152,18 +153,37 @@ __device__ int build_plan(const int32_t* __restrict__ ids, int P, const int32_t*
     if (s >= 0) atomicAdd(&sc.run[s], 1);
     __syncthreads();
   }
-  return sc.total;
+  // The shared experts' virtual experts (slots S + v) after the routed
+  // blocks: every token, pairs P + v*T + t, blocks of <= 16 tokens.
+  const int nbt = (T + kBM - 1) / kBM;
+  const int nsb = n_sh * nbt;
+  for (int i = tid; i < nsb * kBM; i += kThreads) {
+    const int sb = i / kBM, pos = i - sb * kBM;
+    const int v = sb / nbt, c = sb - v * nbt;
+    const int t = c * kBM + pos;
+    int32_t* blk = blocks + (size_t)(sc.total + sb) * kBlockInts;
+    if (pos == 0) {
+      blk[0] = S + v;
+      const int left = T - c * kBM;
+      blk[1] = left < kBM ? left : kBM;
+    }
+    if (t < T) blk[2 + pos] = P + v * T + t;
+  }
+  for (int q = tid; q < n_sh * T; q += kThreads) valid[P + q] = 1;
+  return sc.total + nsb;
 }
 
+// plan: [nb, P2, 0, 0 | P2 block records | P2 validity flags], P2 = P + n_sh*T.
 __global__ __launch_bounds__(kThreads) void moe_align_kernel(
-    const int32_t* __restrict__ ids, int P, const int32_t* __restrict__ map, int E, int S,
-    int32_t* __restrict__ plan) {
+    const int32_t* __restrict__ ids, int T, int k, const int32_t* __restrict__ map, int E, int S,
+    int n_sh, int32_t* __restrict__ plan) {
   __shared__ AlignScratch sc;
-  const int nb = build_plan(ids, P, map, E, S, sc, plan + kPlanHeader,
-                            plan + kPlanHeader + (size_t)kBlockInts * P);
+  const int P = T * k, P2 = P + n_sh * T;
+  const int nb = build_plan(ids, P, map, E, S, T, n_sh, sc, plan + kPlanHeader,
+                            plan + kPlanHeader + (size_t)kBlockInts * P2);
   if (threadIdx.x == 0) {
     plan[0] = nb;
-    plan[1] = P;
+    plan[1] = P2;
   }
 }
 
@@ -357,169 +377,265 @@ __device__ __forceinline__ void stream_fp8(const uint8_t* __restrict__ a0,
 }
 
 // ---------------------------------------------------------------------------
+// Expert weights of a call.  Slots 0..S-1 are the routed slot buffers; slots
+// S..S+n_sh-1 are the shared experts' virtual experts: the shared MLP of
+// intermediate I_s = n_sh * I split into n_sh column groups of width I
+// (silu(g) * u is per channel and the down projection sums over channels, so
+// the MLP is exactly the sum of its groups).  Virtual expert v takes gate rows
+// v*I.. and up rows I_s + v*I.. of sh_w13 [2*I_s, H] and columns v*I.. of
+// sh_w2 [H, I_s]; fp8 scales cover 128x128 blocks of both, like the slots'.
+// ---------------------------------------------------------------------------
+struct ExpertW {
+  const uint8_t* w13;
+  const uint8_t* w2;
+  const float* s13;
+  const float* s2;
+  const uint8_t* sh_w13;
+  const uint8_t* sh_w2;
+  const float* sh_s13;
+  const float* sh_s2;
+  int S;      // routed slots
+  int I_s;    // shared intermediate (n_sh * I), 0 = none
+};
+
+// Call shape: T tokens, k routed pairs each (P = T*k routed pairs); shared
+// pairs follow as P + v*T + t.
+struct CallShape {
+  int T, k, H, I;
+};
+
+__device__ __forceinline__ int pair_token(const CallShape& c, int pair) {
+  const int P = c.T * c.k;
+  return pair < P ? pair / c.k : (pair - P) % c.T;
+}
+
+// Where gemm1's gate and up tiles (16 rows at `tile`) of `slot` live.
+struct G1Src {
+  const uint8_t* gate;
+  const uint8_t* up;
+  const float* sg;  // fp8 scale rows of the tiles (chunk c at [c])
+  const float* su;
+};
+
+template <int ESZ>
+__device__ __forceinline__ G1Src g1_src(const ExpertW& W, const CallShape& c, int slot, int tile) {
+  const int H = c.H, I = c.I;
+  const int nkb = H / kFp8Blk;
+  G1Src r;
+  if (slot < W.S) {
+    const size_t rg = (size_t)slot * 2 * I + (size_t)tile * 16, ru = rg + I;
+    r.gate = W.w13 + rg * H * ESZ;
+    r.up = W.w13 + ru * H * ESZ;
+    const size_t nrb = (size_t)(2 * I) / kFp8Blk;
+    r.sg = W.s13 + ((size_t)slot * nrb + (size_t)tile * 16 / kFp8Blk) * nkb;
+    r.su = W.s13 + ((size_t)slot * nrb + (size_t)(I + tile * 16) / kFp8Blk) * nkb;
+  } else {
+    const size_t v = (size_t)(slot - W.S);
+    const size_t rg = v * I + (size_t)tile * 16, ru = (size_t)W.I_s + rg;
+    r.gate = W.sh_w13 + rg * H * ESZ;
+    r.up = W.sh_w13 + ru * H * ESZ;
+    r.sg = W.sh_s13 + rg / kFp8Blk * nkb;
+    r.su = W.sh_s13 + ru / kFp8Blk * nkb;
+  }
+  return r;
+}
+
+// Where gemm2's 32 hidden rows at tile2 of `slot` live: row r0's first K
+// element, the row stride, fp8 scales of the 128-row block (chunk c at [c]).
+struct G2Src {
+  const uint8_t* a0;
+  size_t ld;
+  const float* sr;
+};
+
+template <int ESZ>
+__device__ __forceinline__ G2Src g2_src(const ExpertW& W, const CallShape& c, int slot,
+                                        int tile2) {
+  const int H = c.H, I = c.I;
+  const size_t r0 = (size_t)tile2 * 16 * kG2T;
+  G2Src r;
+  if (slot < W.S) {
+    r.a0 = W.w2 + ((size_t)slot * H + r0) * I * ESZ;
+    r.ld = (size_t)I;
+    r.sr = W.s2 + ((size_t)slot * (H / kFp8Blk) + r0 / kFp8Blk) * (I / kFp8Blk);
+  } else {
+    const size_t v = (size_t)(slot - W.S);
+    r.a0 = W.sh_w2 + (r0 * W.I_s + v * I) * ESZ;
+    r.ld = (size_t)W.I_s;
+    r.sr = W.sh_s2 + r0 / kFp8Blk * (W.I_s / kFp8Blk) + v * I / kFp8Blk;
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------------------
 // Work items.  `pair` = this lane's pair (column lane & 15), -1 if none; a
 // lane without a pair streams token row 0 (or act row 0) so every load is
 // issued unconditionally, and its column is never written.
 // gemm1: gate and up rows tile*16 .. +16 of `slot` -> act (silu(g) * u).
-// gemm2: hidden rows tile2*32 .. +32 of `slot` against act -> w * partial.
+// gemm2: hidden rows tile2*32 .. +32 of `slot` against act -> w * partial,
+// w = the routing weight of a routed pair, 1 for a shared pair.
 // ---------------------------------------------------------------------------
 template <bool COH>
-__device__ __forceinline__ void g1_item_bf16(const uint16_t* __restrict__ x,
-                                             const uint16_t* __restrict__ w13, int slot, int pair,
-                                             int tile, int H, int I, int k,
+__device__ __forceinline__ void g1_item_bf16(const uint16_t* __restrict__ x, const ExpertW& W,
+                                             const CallShape& cs, int slot, int pair, int tile,
                                              uint16_t* __restrict__ act, ItemLds& l) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int H = cs.H;
   const int nc = H / 64;
   const int c0 = wave * nc / kKS, c1 = (wave + 1) * nc / kKS;
-  const uint16_t* a0 = w13 + ((size_t)slot * 2 * I + (size_t)tile * 16) * H;
-  const uint16_t* xr = x + (size_t)(pair >= 0 ? pair / k : 0) * H;
+  const G1Src src = g1_src<2>(W, cs, slot, tile);
+  const uint16_t* xr = x + (size_t)(pair >= 0 ? pair_token(cs, pair) : 0) * H;
   f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
-  stream_bf16<kTokPlain, kG1D>(a0, a0 + (size_t)I * H, H, xr, c0, c1 - c0, l.stage[wave], ag,
-                               au);
+  stream_bf16<kTokPlain, kG1D>((const uint16_t*)src.gate, (const uint16_t*)src.up, H, xr, c0,
+                               c1 - c0, l.stage[wave], ag, au);
   l.red[wave][0][lane] = ag;
   l.red[wave][1][lane] = au;
-  g1_epilogue<COH>(l.red, pair, tile, I, act);
+  g1_epilogue<COH>(l.red, pair, tile, cs.I, act);
 }
 
-template <bool COH>
-__device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act,
-                                             const uint16_t* __restrict__ w2, int slot, int pair,
-                                             int tile2, int H, int I,
+__device__ __forceinline__ float pair_weight(const CallShape& cs, const float* __restrict__ tw,
+                                             int pair) {
+  return pair < 0 ? 0.f : pair < cs.T * cs.k ? tw[pair] : 1.0f;
+}
+
+template <bool COH, bool COH_OUT = COH>
+__device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act, const ExpertW& W,
+                                             const CallShape& cs, int slot, int pair, int tile2,
                                              const float* __restrict__ topk_w,
                                              float* __restrict__ partial, ItemLds& l) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int I = cs.I;
   const int nc = I / 64;
   const int c0 = wave * nc / kKS, c1 = (wave + 1) * nc / kKS;
-  const uint16_t* a0 = w2 + ((size_t)slot * H + (size_t)tile2 * 16 * kG2T) * I;
+  const G2Src src = g2_src<2>(W, cs, slot, tile2);
+  const uint16_t* a0 = (const uint16_t*)src.a0;
   const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
   f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = a;
-  stream_bf16<COH ? kTokCoh : kTokPlain, kG2D>(a0, a0 + (size_t)16 * I, I, ar, c0, c1 - c0,
+  stream_bf16<COH ? kTokCoh : kTokPlain, kG2D>(a0, a0 + 16 * src.ld, src.ld, ar, c0, c1 - c0,
                                               l.stage[wave], a, b);
   l.red[wave][0][lane] = a;
   l.red[wave][1][lane] = b;
-  g2_epilogue<COH>(l.red, pair, tile2, H, pair >= 0 ? topk_w[pair] : 0.f, partial);
+  g2_epilogue<COH_OUT>(l.red, pair, tile2, cs.H, pair_weight(cs, topk_w, pair), partial);
 }
 
 template <bool COH>
-__device__ __forceinline__ void g1_item_fp8(const uint16_t* __restrict__ x,
-                                            const uint8_t* __restrict__ w13,
-                                            const float* __restrict__ w13_scale, int slot,
-                                            int pair, int tile, int H, int I, int k,
+__device__ __forceinline__ void g1_item_fp8(const uint16_t* __restrict__ x, const ExpertW& W,
+                                            const CallShape& cs, int slot, int pair, int tile,
                                             uint16_t* __restrict__ act, ItemLds& l) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int nkb = H / kFp8Blk, nrb = (2 * I) / kFp8Blk;
+  const int H = cs.H;
+  const int nkb = H / kFp8Blk;
   const int c0 = wave * nkb / kKS, c1 = (wave + 1) * nkb / kKS;
-  const int rg = tile * 16, ru = I + tile * 16;
-  const uint8_t* ag_p = w13 + ((size_t)slot * 2 * I + rg) * H;
-  const uint8_t* au_p = w13 + ((size_t)slot * 2 * I + ru) * H;
-  const float* sg = w13_scale + ((size_t)slot * nrb + rg / kFp8Blk) * nkb;
-  const float* su = w13_scale + ((size_t)slot * nrb + ru / kFp8Blk) * nkb;
-  const uint16_t* xr = x + (size_t)(pair >= 0 ? pair / k : 0) * H;
+  const G1Src src = g1_src<1>(W, cs, slot, tile);
+  const uint16_t* xr = x + (size_t)(pair >= 0 ? pair_token(cs, pair) : 0) * H;
   f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
-  stream_fp8<false, kF8D>(ag_p, au_p, H, sg, su, xr, c0, c1 - c0, l.stage[wave], ag, au);
+  stream_fp8<false, kF8D>(src.gate, src.up, H, src.sg, src.su, xr, c0, c1 - c0, l.stage[wave],
+                          ag, au);
   l.red[wave][0][lane] = ag;
   l.red[wave][1][lane] = au;
-  g1_epilogue<COH>(l.red, pair, tile, I, act);
+  g1_epilogue<COH>(l.red, pair, tile, cs.I, act);
 }
 
-template <bool COH>
-__device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act,
-                                            const uint8_t* __restrict__ w2,
-                                            const float* __restrict__ w2_scale, int slot,
-                                            int pair, int tile2, int H, int I,
+template <bool COH, bool COH_OUT = COH>
+__device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act, const ExpertW& W,
+                                            const CallShape& cs, int slot, int pair, int tile2,
                                             const float* __restrict__ topk_w,
                                             float* __restrict__ partial, ItemLds& l) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int nkb = I / kFp8Blk, nrb = H / kFp8Blk;
+  const int I = cs.I;
+  const int nkb = I / kFp8Blk;
   const int c0 = wave * nkb / kKS, c1 = (wave + 1) * nkb / kKS;
-  const int r0 = tile2 * 16 * kG2T;
-  const uint8_t* a0 = w2 + ((size_t)slot * H + r0) * I;
-  const float* sr = w2_scale + ((size_t)slot * nrb + r0 / kFp8Blk) * nkb;
+  const G2Src src = g2_src<1>(W, cs, slot, tile2);
   const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
   f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = a;
-  stream_fp8<COH, kF8D>(a0, a0 + (size_t)16 * I, I, sr, sr, ar, c0, c1 - c0, l.stage[wave], a, b);
+  stream_fp8<COH, kF8D>(src.a0, src.a0 + 16 * src.ld, src.ld, src.sr, src.sr, ar, c0, c1 - c0,
+                        l.stage[wave], a, b);
   l.red[wave][0][lane] = a;
   l.red[wave][1][lane] = b;
-  g2_epilogue<COH>(l.red, pair, tile2, H, pair >= 0 ? topk_w[pair] : 0.f, partial);
+  g2_epilogue<COH_OUT>(l.red, pair, tile2, cs.H, pair_weight(cs, topk_w, pair), partial);
 }
 
 // ---------------------------------------------------------------------------
 // Staged kernels: grid-stride loops over a plan in global memory.
 // ---------------------------------------------------------------------------
-struct Bf16W {
-  const uint8_t* w13;
-  const uint8_t* w2;
-  const float* s13;
-  const float* s2;
-};
-
 template <bool FP8, bool COH = false>
-__device__ __forceinline__ void run_g1(const uint16_t* x, const Bf16W& W, int slot, int pair,
-                                       int tile, int H, int I, int k, uint16_t* act,
-                                       ItemLds& l) {
+__device__ __forceinline__ void run_g1(const uint16_t* x, const ExpertW& W, const CallShape& cs,
+                                       int slot, int pair, int tile, uint16_t* act, ItemLds& l) {
   if (FP8)
-    g1_item_fp8<COH>(x, W.w13, W.s13, slot, pair, tile, H, I, k, act, l);
+    g1_item_fp8<COH>(x, W, cs, slot, pair, tile, act, l);
   else
-    g1_item_bf16<COH>(x, (const uint16_t*)W.w13, slot, pair, tile, H, I, k, act, l);
+    g1_item_bf16<COH>(x, W, cs, slot, pair, tile, act, l);
 }
 
-template <bool FP8, bool COH = false>
-__device__ __forceinline__ void run_g2(const uint16_t* act, const Bf16W& W, int slot, int pair,
-                                       int tile2, int H, int I, const float* tw, float* partial,
-                                       ItemLds& l) {
+// COH: act is read with device-coherent loads (rows written by other
+// workgroups of the same launch); COH_OUT: partials are written through.
+template <bool FP8, bool COH = false, bool COH_OUT = COH>
+__device__ __forceinline__ void run_g2(const uint16_t* act, const ExpertW& W, const CallShape& cs,
+                                       int slot, int pair, int tile2, const float* tw,
+                                       float* partial, ItemLds& l) {
   if (FP8)
-    g2_item_fp8<COH>(act, W.w2, W.s2, slot, pair, tile2, H, I, tw, partial, l);
+    g2_item_fp8<COH, COH_OUT>(act, W, cs, slot, pair, tile2, tw, partial, l);
   else
-    g2_item_bf16<COH>(act, (const uint16_t*)W.w2, slot, pair, tile2, H, I, tw, partial, l);
+    g2_item_bf16<COH, COH_OUT>(act, W, cs, slot, pair, tile2, tw, partial, l);
 }
 
 template <bool FP8>
 __global__ __launch_bounds__(kThreads) void moe_gemm1_kernel(const uint16_t* __restrict__ x,
-                                                             Bf16W W,
+                                                             ExpertW W,
                                                              const int32_t* __restrict__ plan,
-                                                             int H, int I, int k,
+                                                             CallShape cs,
                                                              uint16_t* __restrict__ act) {
   __shared__ ItemLds lds;
-  const int n_tiles = I / 16;
+  const int n_tiles = cs.I / 16;
   const int total = plan[0] * n_tiles;
   const int col = threadIdx.x & 15;
   for (int item = blockIdx.x; item < total; item += gridDim.x) {
     const int b = item / n_tiles, tile = item - b * n_tiles;
     const int32_t* blk = plan + kPlanHeader + (size_t)b * kBlockInts;
     const int pair = col < blk[1] ? blk[2 + col] : -1;
-    run_g1<FP8>(x, W, blk[0], pair, tile, H, I, k, act, lds);
+    run_g1<FP8>(x, W, cs, blk[0], pair, tile, act, lds);
   }
 }
 
 template <bool FP8>
 __global__ __launch_bounds__(kThreads) void moe_gemm2_kernel(const uint16_t* __restrict__ act,
-                                                             Bf16W W,
+                                                             ExpertW W,
                                                              const int32_t* __restrict__ plan,
                                                              const float* __restrict__ topk_w,
-                                                             int H, int I,
+                                                             CallShape cs,
                                                              float* __restrict__ partial) {
   __shared__ ItemLds lds;
-  const int n_tiles = H / (16 * kG2T);
+  const int n_tiles = cs.H / (16 * kG2T);
   const int total = plan[0] * n_tiles;
   const int col = threadIdx.x & 15;
   for (int item = blockIdx.x; item < total; item += gridDim.x) {
     const int b = item / n_tiles, tile2 = item - b * n_tiles;
     const int32_t* blk = plan + kPlanHeader + (size_t)b * kBlockInts;
     const int pair = col < blk[1] ? blk[2 + col] : -1;
-    run_g2<FP8>(act, W, blk[0], pair, tile2, H, I, topk_w, partial, lds);
+    run_g2<FP8>(act, W, cs, blk[0], pair, tile2, topk_w, partial, lds);
   }
 }
 
-// out[t, h] = bf16(scale * sum_j valid ? partial[t*k+j, h] : 0 + shared[t, h]),
-// j ascending, for 4 consecutive columns at h.  Every pair's load is issued
-// up front (rows of invalid pairs are read and not added), so the thread
-// waits on memory once.
+// out[t, h] = bf16(scale * sum_j valid ? partial[t*k+j, h] : 0
+//                  + sum_v partial[T*k + v*T + t, h] + shared[t, h]),
+// j and v ascending, for 4 consecutive columns at h: the routed pairs
+// scaled, the shared experts' virtual experts (n_sh <= kMaxShared) and a
+// precomputed shared output added unscaled.  Every load is issued up front
+// (rows of invalid pairs are read and not added), so the thread waits on
+// memory once.
+constexpr int kMaxShared = 4;
+
 template <bool COH = false>
 __device__ __forceinline__ void combine4(const float* __restrict__ partial,
-                                         const int32_t* __restrict__ valid, int t, int k, int H,
-                                         int h, float scale, const uint16_t* __restrict__ shared,
+                                         const int32_t* __restrict__ valid, int t, int T, int k,
+                                         int n_sh, int H, int h, float scale,
+                                         const uint16_t* __restrict__ shared,
                                          uint16_t* __restrict__ out) {
-  f32x4_t v[SLUICE_MAX_TOPK];
+  auto ld = [&](int p) {
+    const float* src = partial + (size_t)p * H + h;
+    return COH ? __builtin_bit_cast(f32x4_t, ld16_coh(src)) : *reinterpret_cast<const f32x4_t*>(src);
+  };
+  f32x4_t v[SLUICE_MAX_TOPK], vs[kMaxShared];
   bool ok[SLUICE_MAX_TOPK];
   u32x2_t sh = {0u, 0u};
   if (shared != nullptr) sh = *reinterpret_cast<const u32x2_t*>(shared + (size_t)t * H + h);
@@ -527,18 +643,22 @@ __device__ __forceinline__ void combine4(const float* __restrict__ partial,
   for (int j = 0; j < SLUICE_MAX_TOPK; ++j) {
     const int p = t * k + (j < k ? j : k - 1);
     ok[j] = j < k && valid[p] != 0;
-    const float* src = partial + (size_t)p * H + h;
-    v[j] = COH ? __builtin_bit_cast(f32x4_t, ld16_coh(src))
-               : *reinterpret_cast<const f32x4_t*>(src);
+    v[j] = ld(p);
   }
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  const int P = T * k;
+#pragma unroll
+  for (int u = 0; u < kMaxShared; ++u) vs[u] = ld(u < n_sh ? P + u * T + t : t * k);
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, acs = acc;
 #pragma unroll
   for (int j = 0; j < SLUICE_MAX_TOPK; ++j)
     if (ok[j]) acc += v[j];
+#pragma unroll
+  for (int u = 0; u < kMaxShared; ++u)
+    if (u < n_sh) acs += vs[u];
   float o[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    o[r] = scale * acc[r];
+    o[r] = scale * acc[r] + acs[r];
     if (shared != nullptr)
       o[r] += __uint_as_float(r & 1 ? (sh[r >> 1] & 0xffff0000u) : (sh[r >> 1] << 16));
   }
@@ -547,12 +667,12 @@ __device__ __forceinline__ void combine4(const float* __restrict__ partial,
 }
 
 __global__ __launch_bounds__(256) void moe_combine_kernel(
-    const float* __restrict__ partial, const int32_t* __restrict__ valid, int k, int H,
-    float scale, const uint16_t* __restrict__ shared, uint16_t* __restrict__ out) {
+    const float* __restrict__ partial, const int32_t* __restrict__ valid, int T, int k, int n_sh,
+    int H, float scale, const uint16_t* __restrict__ shared, uint16_t* __restrict__ out) {
   const int t = blockIdx.y;
   const int h = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (h >= H) return;
-  combine4(partial, valid, t, k, H, h, scale, shared, out);
+  combine4(partial, valid, t, T, k, n_sh, H, h, scale, shared, out);
 }
 
 // ---------------------------------------------------------------------------
@@ -574,7 +694,7 @@ constexpr int kCtlInts = 32;
 // occupancy): a gemm2 item only waits for gemm1 items, which never wait.
 template <bool FP8>
 __global__ __launch_bounds__(kThreads) void moe_fused_kernel(
-    const uint16_t* __restrict__ x, Bf16W W, const float* __restrict__ topk_w,
+    const uint16_t* __restrict__ x, ExpertW W, const float* __restrict__ topk_w,
     const int32_t* __restrict__ ids, const int32_t* __restrict__ map, int P, int H, int I, int k,
     int E, int S, float scale, const uint16_t* __restrict__ shared, uint16_t* __restrict__ out,
     int32_t* __restrict__ ctl, uint16_t* __restrict__ act, float* __restrict__ partial,
@@ -590,8 +710,9 @@ __global__ __launch_bounds__(kThreads) void moe_fused_kernel(
   const int tid = threadIdx.x;
   const int col = tid & 15;
   const int T = P / k;
+  const CallShape cs{T, k, H, I};
 
-  const int nb = build_plan(ids, P, map, E, S, sc, s_blocks, s_valid);
+  const int nb = build_plan(ids, P, map, E, S, T, 0, sc, s_blocks, s_valid);
   const int n1t = I / 16, n2t = H / (16 * kG2T);
   const int N1 = nb * n1t, N = N1 + nb * n2t;
 
@@ -599,7 +720,7 @@ __global__ __launch_bounds__(kThreads) void moe_fused_kernel(
     // nothing resident: out = scale * 0 + shared
     for (int i = blockIdx.x * kThreads + tid; i < T * (H / 4); i += gridDim.x * kThreads) {
       const int t = i / (H / 4), h = (i - t * (H / 4)) * 4;
-      combine4(partial, s_valid, t, k, H, h, scale, shared, out);
+      combine4(partial, s_valid, t, T, k, 0, H, h, scale, shared, out);
     }
     return;
   }
@@ -608,7 +729,7 @@ __global__ __launch_bounds__(kThreads) void moe_fused_kernel(
       const int b = item / n1t, tile = item - b * n1t;
       const int32_t* blk = s_blocks + b * kBlockInts;
       const int pair = col < blk[1] ? blk[2 + col] : -1;
-      run_g1<FP8, true>(x, W, blk[0], pair, tile, H, I, k, act, lds);
+      run_g1<FP8, true>(x, W, cs, blk[0], pair, tile, act, lds);
       // the act rows went out with device-coherent stores, completed before
       // the epilogue's barrier
       if (tid == 0) atomicAdd(&blk_done[b], 1);
@@ -630,7 +751,7 @@ __global__ __launch_bounds__(kThreads) void moe_fused_kernel(
     // act is read with device-coherent loads after the counter was seen
     const int32_t* blk = s_blocks + b * kBlockInts;
     const int pair = col < blk[1] ? blk[2 + col] : -1;
-    run_g2<FP8, true>(act, W, blk[0], pair, tile2, H, I, topk_w, partial, lds);
+    run_g2<FP8, true>(act, W, cs, blk[0], pair, tile2, topk_w, partial, lds);
     if (tid == 0) {
       s_last_tile = atomicAdd(&tile_done[tile2], 1) == nb - 1;
       s_last_blk = atomicAdd(&blk_used[b], 1) == n2t - 1;
@@ -646,7 +767,7 @@ __global__ __launch_bounds__(kThreads) void moe_fused_kernel(
       const int h0 = tile2 * 16 * kG2T;
       for (int i = tid; i < T * (16 * kG2T / 4); i += kThreads) {
         const int t = i / (16 * kG2T / 4), h = h0 + (i - t * (16 * kG2T / 4)) * 4;
-        combine4<true>(partial, s_valid, t, k, H, h, scale, shared, out);
+        combine4<true>(partial, s_valid, t, T, k, 0, H, h, scale, shared, out);
       }
       if (tid == 0) atomicExch(&tile_done[tile2], 0);
     }
@@ -666,11 +787,12 @@ struct Workspace {
   float* partial;
 };
 
-// [ctl + counters | plan | act [P, I] bf16 | partial [P, H] fp32].  The
-// counter region has a fixed size, so calls of any shape that share the
-// workspace never write over each other's counters.
-size_t workspace_bytes(int T, int H, int I, int k, Workspace* ws, void* base) {
-  const int P = T * k;
+// [ctl + counters | plan | act [P2, I] bf16 | partial [P2, H] fp32], P2 =
+// T*k routed + n_sh*T shared pairs.  The counter region has a fixed size, so
+// calls of any shape that share the workspace never write over each other's
+// counters.
+size_t workspace_bytes(int T, int H, int I, int k, int n_sh, Workspace* ws, void* base) {
+  const int P = T * k + n_sh * T;
   const size_t ctl_b =
       align_up((kCtlInts + 2 * kFusedMaxPairs + (size_t)kFusedMaxHidden / (16 * kG2T)) * 4, 256);
   const size_t plan_b = align_up(plan_ints(P) * sizeof(int32_t), 256);
@@ -722,28 +844,30 @@ int dev_info(DevInfo** out) {
 #define SLUICE_FUSED_WG_PER_CU 4
 #endif
 
-int check_common(int T, int H, int I, int k, int E, int S, const void* x, const void* w13,
-                 const void* w2, const float* tw, const int32_t* ti, const void* shared, void* ws,
-                 size_t ws_bytes, void* out) {
+int check_common(int T, int H, int I, int k, int E, int S, int n_sh, const void* x,
+                 const void* w13, const void* w2, const float* tw, const int32_t* ti,
+                 const void* shared, void* ws, size_t ws_bytes, void* out) {
   if (T < 0 || H <= 0 || I <= 0 || k <= 0 || k > SLUICE_MAX_TOPK || E <= 0 || S <= 0 ||
       S > SLUICE_MAX_SLOTS)
     return SLUICE_E_INVAL;
   if ((long)T * k > SLUICE_MAX_PAIRS) return SLUICE_E_INVAL;
+  if (n_sh < 0 || n_sh > kMaxShared || (long)T * (k + n_sh) > SLUICE_MAX_PAIRS)
+    return SLUICE_E_INVAL;
   if (H % 64 != 0 || I % 64 != 0) return SLUICE_E_INVAL;
   if (T == 0) return SLUICE_OK;
   if (!x || !w13 || !w2 || !tw || !ti || !ws || !out) return SLUICE_E_INVAL;
-  if (ws_bytes < workspace_bytes(T, H, I, k, nullptr, nullptr)) return SLUICE_E_INVAL;
+  if (ws_bytes < workspace_bytes(T, H, I, k, n_sh, nullptr, nullptr)) return SLUICE_E_INVAL;
   if (((uintptr_t)x | (uintptr_t)w13 | (uintptr_t)w2 | (uintptr_t)ws | (uintptr_t)out) & 15)
     return SLUICE_E_INVAL;
   if ((uintptr_t)shared & 7) return SLUICE_E_INVAL;
   return SLUICE_OK;
 }
 
-int launch_combine(const float* partial, const int32_t* valid, int T, int k, int H, float scale,
-                   const void* shared, void* out, hipStream_t st) {
+int launch_combine(const float* partial, const int32_t* valid, int T, int k, int n_sh, int H,
+                   float scale, const void* shared, void* out, hipStream_t st) {
   dim3 grid((H / 4 + 255) / 256, T);
-  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, st, partial, valid, k, H, scale,
-                     (const uint16_t*)shared, (uint16_t*)out);
+  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, st, partial, valid, T, k, n_sh, H,
+                     scale, (const uint16_t*)shared, (uint16_t*)out);
   return (int)hipGetLastError();
 }
 
@@ -757,16 +881,16 @@ int& fused_flag() {
 int fused_enabled() { return __atomic_load_n(&fused_flag(), __ATOMIC_RELAXED); }
 
 template <bool FP8>
-int run_experts(const void* x, const Bf16W& W, const float* tw, const int32_t* ti,
-                const int32_t* map, int T, int H, int I, int k, int E, int S, float scale,
-                const void* shared, void* workspace, void* out, hipStream_t st) {
+int run_experts(const void* x, const ExpertW& W, const float* tw, const int32_t* ti,
+                const int32_t* map, int T, int H, int I, int k, int E, int S, int n_sh,
+                float scale, const void* shared, void* workspace, void* out, hipStream_t st) {
   Workspace w;
-  workspace_bytes(T, H, I, k, &w, workspace);
-  const int P = T * k;
+  workspace_bytes(T, H, I, k, n_sh, &w, workspace);
+  const int P = T * k, P2 = P + n_sh * T;
   // The fused kernel is opt-in (SLUICE_MOE_FUSED=1): its cross-workgroup
   // hand-offs need agent-scope cache maintenance that costs more than the
   // three kernel boundaries it removes.
-  if (P <= kFusedMaxPairs && H <= kFusedMaxHidden && fused_enabled() != 0) {
+  if (n_sh == 0 && P <= kFusedMaxPairs && H <= kFusedMaxHidden && fused_enabled() != 0) {
     DevInfo* di = nullptr;
     int rc = dev_info(&di);
     if (rc) return rc;
@@ -788,25 +912,45 @@ int run_experts(const void* x, const Bf16W& W, const float* tw, const int32_t* t
                        (const uint16_t*)shared, (uint16_t*)out, w.ctl, w.act, w.partial, ticks);
     return (int)hipGetLastError();
   }
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kThreads), 0, st, ti, P, map, E, S, w.plan);
+  const CallShape cs{T, k, H, I};
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kThreads), 0, st, ti, T, k, map, E, S, n_sh,
+                     w.plan);
   SLUICE_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL((moe_gemm1_kernel<FP8>), dim3(grid_for(P, I / 16)), dim3(kThreads), 0, st,
-                     (const uint16_t*)x, W, w.plan, H, I, k, w.act);
+  hipLaunchKernelGGL((moe_gemm1_kernel<FP8>), dim3(grid_for(P2, I / 16)), dim3(kThreads), 0, st,
+                     (const uint16_t*)x, W, w.plan, cs, w.act);
   SLUICE_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL((moe_gemm2_kernel<FP8>), dim3(grid_for(P, H / (16 * kG2T))), dim3(kThreads),
-                     0, st, w.act, W, w.plan, tw, H, I, w.partial);
+  hipLaunchKernelGGL((moe_gemm2_kernel<FP8>), dim3(grid_for(P2, H / (16 * kG2T))),
+                     dim3(kThreads), 0, st, w.act, W, w.plan, tw, cs, w.partial);
   SLUICE_HIP_CHECK(hipGetLastError());
-  return launch_combine(w.partial, w.plan + kPlanHeader + (size_t)kBlockInts * P, T, k, H, scale,
-                        shared, out, st);
+  return launch_combine(w.partial, w.plan + kPlanHeader + (size_t)kBlockInts * P2, T, k, n_sh, H,
+                        scale, shared, out, st);
+}
+
+// Shared-expert weights: none (shared_I == 0), or n_sh = shared_I / I
+// virtual experts (shared_I a multiple of I, n_sh <= kMaxShared).
+int shared_groups(int shared_I, int I, const void* sw13, const void* sw2, int* n_sh) {
+  *n_sh = 0;
+  if (shared_I == 0) return SLUICE_OK;
+  if (shared_I < 0 || I <= 0 || shared_I % I != 0 || shared_I / I > kMaxShared || !sw13 || !sw2 ||
+      (((uintptr_t)sw13 | (uintptr_t)sw2) & 15))
+    return SLUICE_E_INVAL;
+  *n_sh = shared_I / I;
+  return SLUICE_OK;
+}
+
+// Weights of the per-stage entry points: every block's slot is routed.
+ExpertW routed_only(const uint8_t* w13, const uint8_t* w2, const float* s13, const float* s2) {
+  return ExpertW{w13, w2, s13, s2, nullptr, nullptr, nullptr, nullptr, 0x7fffffff, 0};
 }
 
 }  // namespace
 
 extern "C" size_t sluice_moe_plan_ints(int T, int k) { return plan_ints(T * k); }
 
-extern "C" size_t sluice_fused_experts_workspace(int T, int H, int I, int k) {
+extern "C" size_t sluice_fused_experts_workspace(int T, int H, int I, int k, int shared_I) {
   if (T <= 0 || k <= 0) return 256;
-  return workspace_bytes(T, H, I, k, nullptr, nullptr);
+  const int n_sh = (I > 0 && shared_I > 0) ? (shared_I + I - 1) / I : 0;
+  return workspace_bytes(T, H, I, k, n_sh, nullptr, nullptr);
 }
 
 extern "C" int sluice_moe_set_fused(int enable) {
@@ -827,22 +971,28 @@ extern "C" int sluice_moe_align(const int32_t* topk_ids, int T, int k, const int
       (long)T * k > SLUICE_MAX_PAIRS || plan == nullptr)
     return SLUICE_E_INVAL;
   hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, topk_ids,
-                     T * k, expert_map, E, S, plan);
+                     T, k, expert_map, E, S, 0, plan);
   return (int)hipGetLastError();
 }
 
 extern "C" int sluice_fused_experts_bf16(const void* x, const void* w13, const void* w2,
                                          const float* topk_w, const int32_t* topk_ids,
                                          const int32_t* expert_map, int T, int H, int I, int k,
-                                         int E, int S, float scale, const void* shared,
+                                         int E, int S, float scale, const void* shared_w13,
+                                         const void* shared_w2, int shared_I, const void* shared,
                                          void* workspace, size_t workspace_bytes_, void* out,
                                          sluice_stream_t stream) {
-  int rc = check_common(T, H, I, k, E, S, x, w13, w2, topk_w, topk_ids, shared, workspace,
-                        workspace_bytes_, out);
+  int n_sh = 0;
+  int rc = shared_groups(shared_I, I, shared_w13, shared_w2, &n_sh);
+  if (rc != SLUICE_OK) return rc;
+  rc = check_common(T, H, I, k, E, S, n_sh, x, w13, w2, topk_w, topk_ids, shared, workspace,
+                    workspace_bytes_, out);
   if (rc != SLUICE_OK || T == 0) return rc;
-  Bf16W W{(const uint8_t*)w13, (const uint8_t*)w2, nullptr, nullptr};
-  return run_experts<false>(x, W, topk_w, topk_ids, expert_map, T, H, I, k, E, S, scale, shared,
-                            workspace, out, (hipStream_t)stream);
+  const ExpertW W{(const uint8_t*)w13, (const uint8_t*)w2, nullptr, nullptr,
+                  (const uint8_t*)shared_w13, (const uint8_t*)shared_w2, nullptr, nullptr, S,
+                  shared_I};
+  return run_experts<false>(x, W, topk_w, topk_ids, expert_map, T, H, I, k, E, S, n_sh, scale,
+                            shared, workspace, out, (hipStream_t)stream);
 }
 
 extern "C" int sluice_fused_experts_fp8(const void* x, const void* w13, const float* w13_scale,
@@ -850,18 +1000,27 @@ extern "C" int sluice_fused_experts_fp8(const void* x, const void* w13, const fl
                                         int block_k, const float* topk_w,
                                         const int32_t* topk_ids, const int32_t* expert_map, int T,
                                         int H, int I, int k, int E, int S, float scale,
-                                        const void* shared, void* workspace,
+                                        const void* shared_w13, const float* shared_w13_scale,
+                                        const void* shared_w2, const float* shared_w2_scale,
+                                        int shared_I, const void* shared, void* workspace,
                                         size_t workspace_bytes_, void* out,
                                         sluice_stream_t stream) {
   if (block_n != kFp8Blk || block_k != kFp8Blk) return SLUICE_E_INVAL;
   if (H % kFp8Blk != 0 || I % kFp8Blk != 0) return SLUICE_E_INVAL;
-  int rc = check_common(T, H, I, k, E, S, x, w13, w2, topk_w, topk_ids, shared, workspace,
-                        workspace_bytes_, out);
+  int n_sh = 0;
+  int rc = shared_groups(shared_I, I, shared_w13, shared_w2, &n_sh);
+  if (rc != SLUICE_OK) return rc;
+  if (n_sh > 0 && (shared_w13_scale == nullptr || shared_w2_scale == nullptr))
+    return SLUICE_E_INVAL;
+  rc = check_common(T, H, I, k, E, S, n_sh, x, w13, w2, topk_w, topk_ids, shared, workspace,
+                    workspace_bytes_, out);
   if (rc != SLUICE_OK || T == 0) return rc;
   if (w13_scale == nullptr || w2_scale == nullptr) return SLUICE_E_INVAL;
-  Bf16W W{(const uint8_t*)w13, (const uint8_t*)w2, w13_scale, w2_scale};
-  return run_experts<true>(x, W, topk_w, topk_ids, expert_map, T, H, I, k, E, S, scale, shared,
-                           workspace, out, (hipStream_t)stream);
+  const ExpertW W{(const uint8_t*)w13, (const uint8_t*)w2, w13_scale, w2_scale,
+                  (const uint8_t*)shared_w13, (const uint8_t*)shared_w2, shared_w13_scale,
+                  shared_w2_scale, S, shared_I};
+  return run_experts<true>(x, W, topk_w, topk_ids, expert_map, T, H, I, k, E, S, n_sh, scale,
+                           shared, workspace, out, (hipStream_t)stream);
 }
 
 extern "C" int sluice_moe_gemm1_bf16(const void* x, const void* w13, const int32_t* plan, int T,
@@ -869,9 +1028,10 @@ extern "C" int sluice_moe_gemm1_bf16(const void* x, const void* w13, const int32
   if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % 64 || I % 64 || (long)T * k > SLUICE_MAX_PAIRS ||
       !x || !w13 || !plan || !act)
     return SLUICE_E_INVAL;
-  Bf16W W{(const uint8_t*)w13, nullptr, nullptr, nullptr};
+  const ExpertW W = routed_only((const uint8_t*)w13, nullptr, nullptr, nullptr);
   hipLaunchKernelGGL(moe_gemm1_kernel<false>, dim3(grid_for(T * k, I / 16)), dim3(kThreads), 0,
-                     (hipStream_t)stream, (const uint16_t*)x, W, plan, H, I, k, (uint16_t*)act);
+                     (hipStream_t)stream, (const uint16_t*)x, W, plan, CallShape{T, k, H, I},
+                     (uint16_t*)act);
   return (int)hipGetLastError();
 }
 
@@ -881,10 +1041,10 @@ extern "C" int sluice_moe_gemm2_bf16(const void* act, const void* w2, const int3
   if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % 64 || I % 64 ||
       (long)T * k > SLUICE_MAX_PAIRS || !act || !w2 || !plan || !topk_w || !partial)
     return SLUICE_E_INVAL;
-  Bf16W W{nullptr, (const uint8_t*)w2, nullptr, nullptr};
+  const ExpertW W = routed_only(nullptr, (const uint8_t*)w2, nullptr, nullptr);
   hipLaunchKernelGGL(moe_gemm2_kernel<false>, dim3(grid_for(T * k, H / (16 * kG2T))),
                      dim3(kThreads), 0, (hipStream_t)stream, (const uint16_t*)act, W, plan, topk_w,
-                     H, I, partial);
+                     CallShape{T, k, H, I}, partial);
   return (int)hipGetLastError();
 }
 
@@ -894,9 +1054,10 @@ extern "C" int sluice_moe_gemm1_fp8(const void* x, const void* w13, const float*
   if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % kFp8Blk || I % kFp8Blk ||
       (long)T * k > SLUICE_MAX_PAIRS || !x || !w13 || !w13_scale || !plan || !act)
     return SLUICE_E_INVAL;
-  Bf16W W{(const uint8_t*)w13, nullptr, w13_scale, nullptr};
+  const ExpertW W = routed_only((const uint8_t*)w13, nullptr, w13_scale, nullptr);
   hipLaunchKernelGGL(moe_gemm1_kernel<true>, dim3(grid_for(T * k, I / 16)), dim3(kThreads), 0,
-                     (hipStream_t)stream, (const uint16_t*)x, W, plan, H, I, k, (uint16_t*)act);
+                     (hipStream_t)stream, (const uint16_t*)x, W, plan, CallShape{T, k, H, I},
+                     (uint16_t*)act);
   return (int)hipGetLastError();
 }
 
@@ -906,10 +1067,10 @@ extern "C" int sluice_moe_gemm2_fp8(const void* act, const void* w2, const float
   if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || H % kFp8Blk || I % kFp8Blk ||
       (long)T * k > SLUICE_MAX_PAIRS || !act || !w2 || !w2_scale || !plan || !topk_w || !partial)
     return SLUICE_E_INVAL;
-  Bf16W W{nullptr, (const uint8_t*)w2, nullptr, w2_scale};
+  const ExpertW W = routed_only(nullptr, (const uint8_t*)w2, nullptr, w2_scale);
   hipLaunchKernelGGL(moe_gemm2_kernel<true>, dim3(grid_for(T * k, H / (16 * kG2T))),
                      dim3(kThreads), 0, (hipStream_t)stream, (const uint16_t*)act, W, plan, topk_w,
-                     H, I, partial);
+                     CallShape{T, k, H, I}, partial);
   return (int)hipGetLastError();
 }
 
@@ -919,6 +1080,6 @@ extern "C" int sluice_moe_combine(const float* partial, const int32_t* plan, int
   if (T <= 0 || k <= 0 || H <= 0 || H % 4 || (long)T * k > SLUICE_MAX_PAIRS || !partial || !plan ||
       !out || (((uintptr_t)shared | (uintptr_t)out | (uintptr_t)partial) & 7))
     return SLUICE_E_INVAL;
-  return launch_combine(partial, plan + kPlanHeader + (size_t)kBlockInts * T * k, T, k, H, scale,
+  return launch_combine(partial, plan + kPlanHeader + (size_t)kBlockInts * T * k, T, k, 0, H, scale,
                         shared, out, (hipStream_t)stream);
 }

@@ -429,6 +429,33 @@ class _DenseMLP(nn.Module):
         return linear(linear_glu(x, self.gate_up), self.down)
 
 
+class _Fp8SharedMLP(nn.Module):
+    """A SwiGLU shared expert in e4m3fn codes with 128x128 fp32 block scales
+    (gate rows then up rows in gate_up [2*I, H], down [H, I]), like the
+    routed experts of an fp8 layer.  Alone it runs as a one-expert product;
+    inside the routed product it rides along as fused_experts' shared
+    weights."""
+
+    def __init__(self, H, I, dev, gen):
+        super().__init__()
+        self.gate_up = (torch.randn((2 * I, H), generator=gen, device=dev) * 0.5).to(
+            torch.float8_e4m3fn).view(torch.uint8)
+        self.down = (torch.randn((H, I), generator=gen, device=dev) * 0.5).to(
+            torch.float8_e4m3fn).view(torch.uint8)
+        self.gate_up_scale = torch.rand((2 * I // 128, H // 128), generator=gen,
+                                        device=dev) * 0.02 + 0.01
+        self.down_scale = torch.rand((H // 128, I // 128), generator=gen, device=dev) * 0.02 + 0.01
+        self.I = I
+
+    def forward(self, x):
+        T = x.shape[0]
+        ids = torch.zeros((T, 1), dtype=torch.int32, device=x.device)
+        w = torch.ones((T, 1), dtype=torch.float32, device=x.device)
+        return ops.fused_experts(x, self.gate_up[None], self.down[None], w, ids,
+                                 global_num_experts=1, w1_scale=self.gate_up_scale[None],
+                                 w2_scale=self.down_scale[None], block_shape=[128, 128])
+
+
 def _expert_store(sp, gen_seed, dev, fp8):
     """One pinned host store of every expert of a layer ([E, ...] per param),
     filled from device-generated random values (N(0, 0.02) for bf16; for fp8,
@@ -478,7 +505,10 @@ class _StoreMoELayer(nn.Module):
         self.e_score_correction_bias = (
             nn.Parameter(torch.randn(E, generator=g, device=dev) * 0.01, requires_grad=False)
             if sp["e_bias"] else None)
-        self.shared = (_DenseMLP(H, sp["shared_I"], dev, g) if sp["shared_I"] else None)
+        self.shared = None
+        if sp["shared_I"]:
+            self.shared = (_Fp8SharedMLP(H, sp["shared_I"], dev, g) if sp["fp8"]
+                           else _DenseMLP(H, sp["shared_I"], dev, g))
         self.routing_bias = routing_bias
         self.sp = sp
 
@@ -537,11 +567,24 @@ class _StoreMoELayer(nn.Module):
                                   num_expert_group=sp["n_group"], topk_group=sp["topk_group"],
                                   ids_out=ids_out)
 
-    def experts(self, hn, tw, ti, shared_output=None):
+    def shared_foldable(self) -> bool:
+        """The shared experts can run inside the routed product: their
+        intermediate is a multiple (<= 4) of the routed experts'."""
+        sh = self.shared
+        return sh is not None and sh.I % self.I == 0 and sh.I // self.I <= 4
+
+    def experts(self, hn, tw, ti, shared_output=None, fold_shared=False):
+        """Routed experts (+ shared_output), or with fold_shared the routed
+        and the shared experts in one grouped product."""
         kw = {}
         if self.sp["fp8"]:
             kw = dict(w1_scale=self.w13_weight_scale, w2_scale=self.w2_weight_scale,
                       block_shape=[128, 128])
+        if fold_shared:
+            sh = self.shared
+            kw.update(shared_w1=sh.gate_up, shared_w2=sh.down)
+            if self.sp["fp8"]:
+                kw.update(shared_w1_scale=sh.gate_up_scale, shared_w2_scale=sh.down_scale)
         return ops.fused_experts(hn, self.w13_weight, self.w2_weight, tw, ti,
                                  global_num_experts=self.E, expert_map=self._expert_map,
                                  shared_output=shared_output, **kw)
@@ -645,7 +688,7 @@ class SyntheticDecoder:
         self.thr = self.off._rs_thr or max(1, min(16, slots // sp["k"]))
         assert [id(c) for c in self.off._rs_caches] == [id(c) for c in self.caches]
         for m in self.moe_layers:
-            ops.reserve_workspace(dev, max_batch, H, sp["I"], sp["k"])
+            ops.reserve_workspace(dev, max_batch, H, sp["I"], sp["k"], sp["shared_I"])
         _linear_ws(dev)  # before any capture: graphs bake its address
         rope_d = (sp["qk_rope"] if sp["attn"] == "mla" else sp.get("head_dim", 128))
         inv = 1.0 / (sp.get("rope_theta", 1e4) ** (torch.arange(0, rope_d, 2, device=dev).float()
@@ -743,11 +786,15 @@ class SyntheticDecoder:
 
             def mid(io, i=i):
                 moe = self.blocks[i].moe
-                sh = moe.shared(io["hn"]) if moe.shared is not None else None
-                if classic:
-                    io["delta"] = io["routed"] if sh is None else io["routed"] + sh
+                if not classic and moe.shared_foldable():
+                    # routed and shared experts in one grouped product
+                    io["delta"] = moe.experts(io["hn"], io["tw"], io["ti"], fold_shared=True)
                 else:
-                    io["delta"] = moe.experts(io["hn"], io["tw"], io["ti"], shared_output=sh)
+                    sh = moe.shared(io["hn"]) if moe.shared is not None else None
+                    if classic:
+                        io["delta"] = io["routed"] if sh is None else io["routed"] + sh
+                    else:
+                        io["delta"] = moe.experts(io["hn"], io["tw"], io["ti"], shared_output=sh)
                 self._to_next_gap(i + 1, io, st)
 
             out.append((mid, n + 1 if not last else None))

@@ -95,12 +95,13 @@ class _Workspace:
 _WS = _Workspace()
 
 
-def workspace_bytes(T: int, H: int, I: int, k: int) -> int:
-    return int(_lib.load().sluice_fused_experts_workspace(T, H, I, k))
+def workspace_bytes(T: int, H: int, I: int, k: int, shared_I: int = 0) -> int:
+    return int(_lib.load().sluice_fused_experts_workspace(T, H, I, k, shared_I))
 
 
-def reserve_workspace(device, max_tokens: int, H: int, I: int, k: int) -> None:
-    _WS.get(torch.device(device), workspace_bytes(max_tokens, H, I, k))
+def reserve_workspace(device, max_tokens: int, H: int, I: int, k: int,
+                      shared_I: int = 0) -> None:
+    _WS.get(torch.device(device), workspace_bytes(max_tokens, H, I, k, shared_I))
 
 
 def _fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
@@ -108,7 +109,14 @@ def _fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch
                         global_num_experts: int, expert_map: Optional[torch.Tensor],
                         w1_scale: Optional[torch.Tensor], w2_scale: Optional[torch.Tensor],
                         block_shape: Optional[list[int]], routed_scaling_factor: float,
-                        shared_output: Optional[torch.Tensor]) -> torch.Tensor:
+                        shared_output: Optional[torch.Tensor],
+                        shared_w1: Optional[torch.Tensor] = None,
+                        shared_w2: Optional[torch.Tensor] = None,
+                        shared_w1_scale: Optional[torch.Tensor] = None,
+                        shared_w2_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """shared_w1 [2*Is, H] / shared_w2 [H, Is] (Is a multiple of I): the
+    layer's shared experts, computed inside the grouped product and added
+    unscaled (fp8 with their own block scales when the experts are fp8)."""
     if activation != "silu":
         raise NotImplementedError(f"activation {activation!r}: only 'silu' is on the path")
     lib = _lib.load()
@@ -133,10 +141,20 @@ def _fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch
     else:
         E = global_num_experts if global_num_experts > 0 else S
         emap_ptr = None
+    Is = 0
+    if shared_w1 is not None or shared_w2 is not None:
+        if shared_w1 is None or shared_w2 is None:
+            raise ValueError("shared experts need shared_w1 and shared_w2")
+        Is = shared_w2.shape[1]
+        if (shared_w1.shape != (2 * Is, H) or shared_w2.shape != (H, Is) or Is % I != 0
+                or shared_w1.dtype != w1.dtype or shared_w2.dtype != w2.dtype):
+            raise ValueError(f"bad shared expert shapes w13 {tuple(shared_w1.shape)} "
+                             f"w2 {tuple(shared_w2.shape)} for I={I}, H={H}")
+        shared_w1, shared_w2 = shared_w1.contiguous(), shared_w2.contiguous()
     out = torch.empty_like(x)
     if T == 0:
         return out
-    chunk = _MAX_PAIRS // k
+    chunk = _MAX_PAIRS // (k + Is // I)
     if T > chunk:
         # more (token, expert) pairs than one launch takes (a prefill chunk on
         # the classic path): tokens are independent, so run slices of them
@@ -145,9 +163,10 @@ def _fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch
             out[t0:t1] = _fused_experts_impl(
                 x[t0:t1], w1, w2, tw[t0:t1], ids[t0:t1], activation, global_num_experts,
                 expert_map, w1_scale, w2_scale, block_shape, routed_scaling_factor,
-                None if shared_output is None else shared_output[t0:t1])
+                None if shared_output is None else shared_output[t0:t1], shared_w1, shared_w2,
+                shared_w1_scale, shared_w2_scale)
         return out
-    nbytes = workspace_bytes(T, H, I, k)
+    nbytes = workspace_bytes(T, H, I, k, Is)
     ws = _WS.get(x.device, nbytes)
     sh = None
     if shared_output is not None:
@@ -158,18 +177,21 @@ def _fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch
     if w1.dtype == torch.bfloat16:
         rc = lib.sluice_fused_experts_bf16(
             x.data_ptr(), w1.data_ptr(), w2.data_ptr(), tw.data_ptr(), ids.data_ptr(), emap_ptr,
-            T, H, I, k, E, S, float(routed_scaling_factor), _ptr(sh), ws.data_ptr(), ws.numel(),
-            out.data_ptr(), stream)
+            T, H, I, k, E, S, float(routed_scaling_factor), _ptr(shared_w1), _ptr(shared_w2), Is,
+            _ptr(sh), ws.data_ptr(), ws.numel(), out.data_ptr(), stream)
         _lib.check(rc, "sluice_fused_experts_bf16")
     elif w1.dtype in (torch.uint8, torch.float8_e4m3fn):
         if w1_scale is None or w2_scale is None:
             raise ValueError("fp8 experts need w1_scale and w2_scale")
         bn, bk = (block_shape or [128, 128])[:2]
+        if Is and (shared_w1_scale is None or shared_w2_scale is None):
+            raise ValueError("fp8 shared experts need shared_w1_scale and shared_w2_scale")
         rc = lib.sluice_fused_experts_fp8(
             x.data_ptr(), w1.data_ptr(), w1_scale.data_ptr(), w2.data_ptr(), w2_scale.data_ptr(),
             int(bn), int(bk), tw.data_ptr(), ids.data_ptr(), emap_ptr, T, H, I, k, E, S,
-            float(routed_scaling_factor), _ptr(sh), ws.data_ptr(), ws.numel(), out.data_ptr(),
-            stream)
+            float(routed_scaling_factor), _ptr(shared_w1), _ptr(shared_w1_scale),
+            _ptr(shared_w2), _ptr(shared_w2_scale), Is, _ptr(sh), ws.data_ptr(), ws.numel(),
+            out.data_ptr(), stream)
         _lib.check(rc, "sluice_fused_experts_fp8")
     else:
         raise TypeError(f"unsupported expert dtype {w1.dtype}")
@@ -185,16 +207,22 @@ def fused_experts_op(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
                      w2_scale: Optional[torch.Tensor] = None,
                      block_shape: Optional[list[int]] = None,
                      routed_scaling_factor: float = 1.0,
-                     shared_output: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     shared_output: Optional[torch.Tensor] = None,
+                     shared_w1: Optional[torch.Tensor] = None,
+                     shared_w2: Optional[torch.Tensor] = None,
+                     shared_w1_scale: Optional[torch.Tensor] = None,
+                     shared_w2_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
     return _fused_experts_impl(hidden_states, w1, w2, topk_weights, topk_ids, activation,
                                global_num_experts, expert_map, w1_scale, w2_scale, block_shape,
-                               routed_scaling_factor, shared_output)
+                               routed_scaling_factor, shared_output, shared_w1, shared_w2,
+                               shared_w1_scale, shared_w2_scale)
 
 
 @fused_experts_op.register_fake
 def _(hidden_states, w1, w2, topk_weights, topk_ids, activation="silu", global_num_experts=-1,
       expert_map=None, w1_scale=None, w2_scale=None, block_shape=None,
-      routed_scaling_factor=1.0, shared_output=None):
+      routed_scaling_factor=1.0, shared_output=None, shared_w1=None, shared_w2=None,
+      shared_w1_scale=None, shared_w2_scale=None):
     return torch.empty_like(hidden_states)
 
 
@@ -226,15 +254,21 @@ if not _vllm_present() and not hasattr(torch.ops.vllm, "fused_experts"):
                             w2_scale: Optional[torch.Tensor] = None,
                             block_shape: Optional[list[int]] = None,
                             routed_scaling_factor: float = 1.0,
-                            shared_output: Optional[torch.Tensor] = None) -> torch.Tensor:
+                            shared_output: Optional[torch.Tensor] = None,
+                            shared_w1: Optional[torch.Tensor] = None,
+                            shared_w2: Optional[torch.Tensor] = None,
+                            shared_w1_scale: Optional[torch.Tensor] = None,
+                            shared_w2_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
         return _fused_experts_impl(hidden_states, w1, w2, topk_weights, topk_ids, activation,
                                    global_num_experts, expert_map, w1_scale, w2_scale,
-                                   block_shape, routed_scaling_factor, shared_output)
+                                   block_shape, routed_scaling_factor, shared_output, shared_w1,
+                                   shared_w2, shared_w1_scale, shared_w2_scale)
 
     @_vllm_fused_experts.register_fake
     def _(hidden_states, w1, w2, topk_weights, topk_ids, activation="silu",
           global_num_experts=-1, expert_map=None, w1_scale=None, w2_scale=None,
-          block_shape=None, routed_scaling_factor=1.0, shared_output=None):
+          block_shape=None, routed_scaling_factor=1.0, shared_output=None, shared_w1=None,
+          shared_w2=None, shared_w1_scale=None, shared_w2_scale=None):
         return torch.empty_like(hidden_states)
 
 

@@ -47,11 +47,13 @@ def test_invalid_arguments_rejected_without_touching_the_gpu(lib):
                                  None) == _lib.SLUICE_E_INVAL
     assert lib.sluice_moe_align(None, 1, 8, None, 64, 0, None, None) == _lib.SLUICE_E_INVAL
     assert lib.sluice_fused_experts_bf16(None, None, None, None, None, None, 1, 2048, 100, 8, 64,
-                                         8, 1.0, None, None, 0, None, None) == _lib.SLUICE_E_INVAL
+                                         8, 1.0, None, None, 0, None, None, 0, None,
+                                         None) == _lib.SLUICE_E_INVAL
     # weight rows stream in 64-element (128-byte) segments: H, I % 64 == 0
     for H, I in ((2048, 96), (2080, 128)):
         assert lib.sluice_fused_experts_bf16(None, None, None, None, None, None, 1, H, I, 8, 64,
-                                             8, 1.0, None, None, 0, None, None) == _lib.SLUICE_E_INVAL
+                                             8, 1.0, None, None, 0, None, None, 0, None,
+                                             None) == _lib.SLUICE_E_INVAL
         assert lib.sluice_moe_gemm1_bf16(None, None, None, 1, H, I, 8, None,
                                          None) == _lib.SLUICE_E_INVAL
         assert lib.sluice_moe_gemm2_bf16(None, None, None, None, 1, H, I, 8, None,
@@ -62,8 +64,21 @@ def test_invalid_arguments_rejected_without_touching_the_gpu(lib):
                                    ctypes.byref(h)) == _lib.SLUICE_E_INVAL
 
 
+def test_shared_experts_argument_checks(lib):
+    """Shared-expert weights whose intermediate is not a multiple of I (or
+    above 4*I, or missing) are refused before any device work."""
+    args = [ctypes.c_void_p(16)] * 6
+    for shared_I, w in ((96, 16), (5 * 64, 16), (128, 0)):
+        sw = ctypes.c_void_p(w) if w else None
+        rc = lib.sluice_fused_experts_bf16(*args, 2, 256, 64, 2, 8, 4, 1.0, sw, sw, shared_I,
+                                           None, ctypes.c_void_p(16), 1 << 30,
+                                           ctypes.c_void_p(16), None)
+        assert rc == _lib.SLUICE_E_INVAL
+
+
 def test_workspace_size_is_monotone(lib):
-    a = lib.sluice_fused_experts_workspace(1, 2048, 1408, 6)
-    b = lib.sluice_fused_experts_workspace(8, 2048, 1408, 6)
-    assert 0 < a < b
+    a = lib.sluice_fused_experts_workspace(1, 2048, 1408, 6, 0)
+    b = lib.sluice_fused_experts_workspace(8, 2048, 1408, 6, 0)
+    c = lib.sluice_fused_experts_workspace(8, 2048, 1408, 6, 2816)
+    assert 0 < a < b < c
     assert lib.sluice_moe_plan_ints(8, 6) == 4 + 18 * 48 + 48

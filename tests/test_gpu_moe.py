@@ -224,6 +224,82 @@ def test_fused_experts_matches_its_stages(T, H, I, E, S, k, frac, shared, fp8):
         assert torch.equal(ref, sh)
 
 
+@pytest.mark.parametrize("T,H,I,Is,E,S,k,frac,fp8", [
+    (8, 2048, 1408, 2816, 64, 48, 6, 0.85, False),   # V2-Lite: 2 shared experts
+    (1, 2048, 1408, 2816, 64, 48, 6, 0.85, False),
+    (20, 256, 64, 192, 16, 8, 4, 0.85, False),       # > 16 tokens: two shared blocks each
+    (4, 256, 64, 128, 32, 4, 2, 0.0, False),         # nothing routed resident: shared only
+    (8, 7168, 2048, 2048, 256, 12, 8, 0.85, True),   # DeepSeek-V3: 1 fp8 shared expert
+])
+def test_fused_experts_with_shared_experts(T, H, I, Is, E, S, k, frac, fp8):
+    """Shared experts inside the grouped product (shared_w1/shared_w2, Is/I
+    groups of I channels, added unscaled) against the oracle's routed sum
+    times the routed scale plus the SwiGLU shared MLP; repeated calls give the
+    same bits."""
+    from sluice_amd import ops
+
+    rng = np.random.default_rng(T * 31 + Is)
+    x = _bf16(rng.standard_normal((T, H)))
+    ids = _routing(T, E, k, rng)
+    tw = rng.random((T, k)).astype(np.float32)
+    emap = _emap(E, S, rng, frac)
+    if fp8:
+        def codes(shape):
+            q = rng.integers(0, 256, size=shape, dtype=np.uint8)
+            q[(q & 0x7F) == 0x7F] = 0x38
+            return q
+
+        def scales(shape):
+            return (rng.random(shape) * 0.02 + 0.01).astype(np.float32)
+
+        q13, q2 = codes((S, 2 * I, H)), codes((S, H, I))
+        s13, s2 = scales((S, 2 * I // 128, H // 128)), scales((S, H // 128, I // 128))
+        qgu, qd = codes((2 * Is, H)), codes((H, Is))
+        sgu, sd = scales((2 * Is // 128, H // 128)), scales((H // 128, Is // 128))
+        w13, w2 = om.dequant_block(q13, s13), om.dequant_block(q2, s2)
+        gu, d = om.dequant_block(qgu, sgu), om.dequant_block(qd, sd)
+        args = [torch.from_numpy(a).to(DEV) for a in (q13, q2, qgu, qd)]
+        kw = dict(w1_scale=torch.from_numpy(s13).to(DEV), w2_scale=torch.from_numpy(s2).to(DEV),
+                  block_shape=[128, 128], shared_w1=args[2], shared_w2=args[3],
+                  shared_w1_scale=torch.from_numpy(sgu).to(DEV),
+                  shared_w2_scale=torch.from_numpy(sd).to(DEV))
+        tol = FP8_TOL
+    else:
+        w13 = _bf16(rng.standard_normal((S, 2 * I, H)) * 0.02)
+        w2 = _bf16(rng.standard_normal((S, H, I)) * 0.02)
+        gu = _bf16(rng.standard_normal((2 * Is, H)) * 0.02)
+        d = _bf16(rng.standard_normal((H, Is)) * 0.02)
+        args = [w13.to(DEV), w2.to(DEV)]
+        kw = dict(shared_w1=gu.to(DEV), shared_w2=d.to(DEV))
+        w13, w2, gu, d = (a.float().numpy() for a in (w13, w2, gu, d))
+        tol = BF16_TOL
+    outs = [ops.fused_experts(x.to(DEV), args[0], args[1], torch.from_numpy(tw).to(DEV),
+                              torch.from_numpy(ids).to(DEV), global_num_experts=E,
+                              expert_map=torch.from_numpy(emap).to(DEV),
+                              routed_scaling_factor=2.5, **kw) for _ in range(2)]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    xf = x.float().numpy()
+    ref = om.fused_experts(xf, w13, w2, tw, ids, expert_map=emap, scale=2.5,
+                           shared=om.shared_mlp(xf, gu, d))
+    err = om.rel_l2(outs[0].float().cpu().numpy(), ref)
+    print(f"shared fold T={T} I={I} Is={Is} fp8={fp8}: rel_l2={err:.2e}", flush=True)
+    assert err <= tol
+
+
+def test_fused_experts_rejects_shared_not_a_multiple_of_I():
+    from sluice_amd import ops
+
+    x = torch.zeros((2, 256), dtype=torch.bfloat16, device=DEV)
+    w13 = torch.zeros((4, 128, 256), dtype=torch.bfloat16, device=DEV)
+    w2 = torch.zeros((4, 256, 64), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        ops.fused_experts(x, w13, w2, torch.ones((2, 2), device=DEV),
+                          torch.zeros((2, 2), dtype=torch.int32, device=DEV),
+                          shared_w1=torch.zeros((192, 256), dtype=torch.bfloat16, device=DEV),
+                          shared_w2=torch.zeros((256, 96), dtype=torch.bfloat16, device=DEV))
+
+
 def test_fused_experts_bf16_identity_map_scale_shared():
     got, ref = _moe_case(8, 512, 128, 8, 8, 2, seed=9, use_map=False, scale=2.5, shared=True)
     assert om.rel_l2(got, ref) <= BF16_TOL

@@ -48,6 +48,40 @@ def test_matches_transformers_experts(family):
     assert moe.rel_l2(got, ref.numpy()) < 1e-12
 
 
+def test_shared_mlp_matches_transformers_mlp():
+    """The shared-expert oracle against DeepseekV2MLP (gate_proj, up_proj,
+    down_proj, silu) in float64, and against the expert oracle with the MLP
+    as one expert of weight 1; splitting its channels into groups sums to it."""
+    from transformers.models.deepseek_v2.configuration_deepseek_v2 import DeepseekV2Config
+    from transformers.models.deepseek_v2.modeling_deepseek_v2 import DeepseekV2MLP
+
+    rng = np.random.default_rng(7)
+    T, H, Is = 5, 64, 96
+    cfg = DeepseekV2Config(hidden_size=H, intermediate_size=Is, num_attention_heads=1,
+                           num_key_value_heads=1)
+    mlp = DeepseekV2MLP(cfg, intermediate_size=Is).double()
+    gu = _rand((2 * Is, H), rng, 0.1)
+    d = _rand((H, Is), rng, 0.1)
+    with torch.no_grad():
+        mlp.gate_proj.weight.copy_(torch.from_numpy(gu[:Is]))
+        mlp.up_proj.weight.copy_(torch.from_numpy(gu[Is:]))
+        mlp.down_proj.weight.copy_(torch.from_numpy(d))
+    x = _rand((T, H), rng)
+    with torch.no_grad():
+        ref = mlp(torch.from_numpy(x).double()).numpy()
+    got = moe.shared_mlp(x, gu, d)
+    assert moe.rel_l2(got, ref) < 1e-12
+    one = moe.fused_experts(x, gu[None], d[None], np.ones((T, 1)), np.zeros((T, 1), np.int64))
+    assert moe.rel_l2(one, ref) < 1e-12
+    # three groups of 32 channels, each one expert of intermediate 32
+    I = 32
+    w13 = np.stack([np.concatenate([gu[v * I:(v + 1) * I], gu[Is + v * I:Is + (v + 1) * I]])
+                    for v in range(3)])
+    w2 = np.stack([d[:, v * I:(v + 1) * I] for v in range(3)])
+    grouped = moe.fused_experts(x, w13, w2, np.ones((T, 3)), np.tile(np.arange(3), (T, 1)))
+    assert moe.rel_l2(grouped, ref) < 1e-12
+
+
 def test_expert_map_slots_and_unmapped_contribute_zero():
     rng = np.random.default_rng(1)
     T, H, I, E, S, k = 4, 32, 16, 10, 4, 2
