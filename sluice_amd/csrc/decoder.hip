@@ -962,8 +962,8 @@ extern "C" int sluice_dec_mla_attend(const float* q_lat, const float* q_pe, cons
                                      const void* kpe_cache, const void* w_uv, const int64_t* pos,
                                      int c, int nh, int rope, int lora, int vh, int L, float scale,
                                      void* out, sluice_stream_t stream) {
-  if (c < 0 || nh <= 0 || rope != kRope || lora != kLora || vh <= 0 || vh > 256 || L <= 0 ||
-      L > kMaxL)
+  if (c < 0 || nh <= 0 || rope != kRope || lora != kLora || vh <= 0 || vh > 256 || vh % 2 ||
+      L <= 0 || L > kMaxL)
     return SLUICE_E_INVAL;
   if (!q_lat || !q_pe || !ckv_cache || !kpe_cache || !w_uv || !pos || !out) return SLUICE_E_INVAL;
   if ((uintptr_t)ckv_cache & 15) return SLUICE_E_INVAL;

@@ -196,10 +196,13 @@ def _tables(L, d, theta):
     return ang.cos().contiguous(), ang.sin().contiguous()
 
 
-def test_mla_prep_and_attend():
+@pytest.mark.parametrize("L,positions,vh", [(64, [5, 0, 63, 31], 128),
+                                            (512, [300, 1, 511, 130], 128),
+                                            (256, [200, 17, 255, 64], 192)])
+def test_mla_prep_and_attend(L, positions, vh):
     lib, check = _lib()
-    c, nh, nope, rope, lora, vh, L = 4, 16, 128, 64, 512, 128, 64
-    g = torch.Generator().manual_seed(11)
+    c, nh, nope, rope, lora = 4, 16, 128, 64, 512
+    g = torch.Generator().manual_seed(11 + L)
     nq = nh * (nope + rope)
     qkva = torch.randn((c, nq + lora + rope), generator=g).bfloat16()
     kv_norm = (1 + 0.1 * torch.randn(lora, generator=g)).bfloat16()
@@ -207,7 +210,7 @@ def test_mla_prep_and_attend():
     w_uv = (0.05 * torch.randn((nh, lora, vh), generator=g)).bfloat16()
     ckv = torch.randn((c, L, lora), generator=g).bfloat16()
     kpe = torch.randn((c, L, rope), generator=g).bfloat16()
-    pos = torch.tensor([5, 0, 63, 31], dtype=torch.long)
+    pos = torch.tensor(positions, dtype=torch.long)
     cos_t, sin_t = _tables(L, rope, 1e4)
     scale = (nope + rope) ** -0.5
     d = {k: v.to(DEV) for k, v in dict(qkva=qkva, kv_norm=kv_norm, w_uk=w_uk, w_uv=w_uv,
@@ -250,16 +253,17 @@ def test_mla_prep_and_attend():
     assert torch.equal(d["ckv"].cpu()[mask], ckv[mask])
 
 
-def test_gqa_prep_and_attend():
+@pytest.mark.parametrize("L,positions", [(48, [7, 47, 0]), (600, [300, 599, 129])])
+def test_gqa_prep_and_attend(L, positions):
     lib, check = _lib()
-    c, nh, kvh, hd, L = 3, 32, 4, 128, 48
-    g = torch.Generator().manual_seed(12)
+    c, nh, kvh, hd = 3, 32, 4, 128
+    g = torch.Generator().manual_seed(12 + L)
     qkv = torch.randn((c, (nh + 2 * kvh) * hd), generator=g).bfloat16()
     q_norm = (1 + 0.1 * torch.randn(hd, generator=g)).bfloat16()
     k_norm = (1 + 0.1 * torch.randn(hd, generator=g)).bfloat16()
     k = torch.randn((c, kvh, L, hd), generator=g).bfloat16()
     v = torch.randn((c, kvh, L, hd), generator=g).bfloat16()
-    pos = torch.tensor([7, 47, 0], dtype=torch.long)
+    pos = torch.tensor(positions, dtype=torch.long)
     cos_t, sin_t = _tables(L, hd, 1e6)
     scale = hd ** -0.5
     d = {kk: vv.to(DEV) for kk, vv in dict(qkv=qkv, qn=q_norm, kn=k_norm, k=k.clone(), v=v.clone(),
