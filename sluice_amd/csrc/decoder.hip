@@ -772,13 +772,13 @@ int device_cus() {
 
 // Parts of K per item, from per-kernel costs measured in replayed graphs on
 // MI355X (decode shapes, T = 1 and 8, N 2048-21888, K 2048-10944): the
-// hand-off of a split costs more than streaming a 2048-long row slice on
-// one CU when T > 4 (its partial tiles are larger), so short K stays whole
-// there; longer K splits in 3 (up to 4096) or 4.  ks * items <= 2 * CUs
-// keeps the partials within the workspace bound.
+// hand-off of a split costs about as much as streaming a 3072-long row slice
+// on one CU, so K up to 3072 stays whole; longer K splits in 3 (up to 4096)
+// or 4.  ks * items <= 2 * CUs keeps the partials within the workspace bound.
 int linear_parts(int items, int K, int T, int cus) {
+  (void)T;
   const int nc = K / 64;
-  int ks = T > 4 ? (nc <= 32 ? 1 : nc <= 64 ? 3 : 4) : (nc <= 16 ? 1 : nc <= 64 ? 3 : 4);
+  int ks = nc <= 48 ? 1 : nc <= 64 ? 3 : 4;
   if (ks > nc) ks = nc;
   while (ks > 1 && (long)items * ks > 2L * cus) --ks;
   return ks;
