@@ -812,11 +812,40 @@ __global__ __launch_bounds__(kArg) void argmax_kernel(const uint16_t* __restrict
   const uint16_t* row = x + (size_t)t * N;
   float best = -INFINITY;
   int besti = N;  // sentinel above every index
-  for (int i = tid; i < N; i += kArg) {
-    const float v = bf(row[i]);
-    if (v > best || (besti == N && v == best)) {
-      best = v;
-      besti = i;
+  if ((N & 7) == 0 && ((uintptr_t)row & 15) == 0) {
+    // 8 values per 16-byte load, 4 loads in flight per thread; a thread's
+    // indices only grow, so a strict '>' keeps the first of equal values
+    const int nv = N / 8;
+    const u32x4_t* rv = reinterpret_cast<const u32x4_t*>(row);
+    for (int v0 = tid; v0 < nv; v0 += 4 * kArg) {
+      u32x4_t q[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int v = v0 + u * kArg;
+        q[u] = rv[v < nv ? v : v0];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int v = v0 + u * kArg;
+        if (v < nv) {
+          float f[8];
+          unpack8(q[u], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (f[e] > best || (besti == N && f[e] == best)) {
+              best = f[e];
+              besti = v * 8 + e;
+            }
+        }
+      }
+    }
+  } else {
+    for (int i = tid; i < N; i += kArg) {
+      const float v = bf(row[i]);
+      if (v > best || (besti == N && v == best)) {
+        best = v;
+        besti = i;
+      }
     }
   }
 #pragma unroll

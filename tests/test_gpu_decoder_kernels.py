@@ -153,17 +153,18 @@ def test_linear_split_k_deterministic_and_counters_back_at_zero():
     assert int(counters.abs().sum()) == 0
 
 
-@pytest.mark.parametrize("T,N", [(1, 151936), (8, 102400), (3, 1000)])
+@pytest.mark.parametrize("T,N", [(1, 151936), (8, 102400), (3, 1000), (2, 1001)])
 def test_argmax(T, N):
     from sluice_amd.decoder import argmax_rows
 
     g = torch.Generator().manual_seed(N + T)
     x = torch.randn((T, N), generator=g).bfloat16()
     x[0, N // 3] = 50.0  # a clear winner
+    x[0, 3] = float("nan")  # NaN never wins
     x[-1, 7] = x[-1, N - 1] = 60.0  # a tie: the first index wins
     out = argmax_rows(x.to(DEV), torch.zeros(T, dtype=torch.long, device=DEV))
     torch.cuda.synchronize()
-    ref = torch.argmax(x.float(), dim=-1)
+    ref = torch.argmax(torch.nan_to_num(x.float(), nan=-float("inf")), dim=-1)
     assert torch.equal(out.cpu(), ref)
     assert int(out[-1]) == 7
 
