@@ -271,7 +271,6 @@ __device__ __forceinline__ u32x4_t ld_tok(const uint16_t* p) {
 // token elements loaded in the same order; the fp32 sum over the chunk is
 // multiplied by its scale before it joins the accumulator.
 // ---------------------------------------------------------------------------
-typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 
 __device__ __forceinline__ uint32_t pack_bf16_hi(float a, float b) {
   // fp8 values are exact in bf16: keep the top 16 bits of each fp32.
