@@ -137,14 +137,27 @@ __global__ __launch_bounds__(256) void map_refresh_kernel(int32_t* __restrict__ 
 // ---------------------------------------------------------------------------
 // Mailbox of one layer (host pinned, coherent, mapped into the device).
 // ---------------------------------------------------------------------------
-struct GapMailbox {
-  // written by the device: the record.  Every word carries the record's
-  // stamp in its low half, so the host takes a word once its stamp matches
-  // and the device needs no ordering (and no wait) between the words.
-  uint64_t hdr;        // stamp | n_uniq << 32 | n_miss << 43 | waits << 54
-  int32_t dev_status;  // first failed device wait (sticky; 0 = none)
-  int32_t dev_pad[13];
+// A record.  Every word carries the record's stamp in its low half, so the
+// host takes a word once its stamp matches and the device needs no ordering
+// (and no wait) between the words.
+struct GapRecord {
+  uint64_t hdr;  // stamp | n_uniq << 32 | n_miss << 43 | waits << 54
+  uint64_t pad[7];
   uint64_t ent[SLUICE_MAX_EXPERTS];  // stamp | id << 32: sorted unique selected ids
+};
+
+// Records of a layer rotate through kRing slots (record s in slot s % kRing),
+// so the device need not know whether the host has copied out the previous
+// record: only the one kRing records back, which it checks against the last
+// ack it read and re-reads over the bus only when that is too old (once every
+// kRing - 1 gaps at most, when the host keeps up).
+constexpr int kRing = 4;
+
+struct GapMailbox {
+  // written by the device
+  GapRecord rec[kRing];
+  int32_t dev_status;  // first failed device wait (sticky; 0 = none)
+  int32_t dev_pad[15];
   // written by the host
   int32_t ack_stamp;   // last record the host has copied out
   int32_t resp_stamp;  // stamp the response below answers (written last)
@@ -183,6 +196,30 @@ __device__ __forceinline__ int32_t ld_sys(const int32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// Stamps run 1, 2, ..., INT32_MAX, 1, ... (0 is "none yet", the stamp before
+// 1).  Steps from stamp b forward to stamp a.
+__host__ __device__ inline int32_t stamp_dist(int32_t a, int32_t b) {
+  int64_t d = (int64_t)a - (int64_t)b;
+  if (d < 0) d += INT32_MAX;
+  return (int32_t)d;
+}
+
+// Spin until the host's ack *p is at most kRing stamps behind stamp s, so
+// that record s's slot is free; the last value read goes to *seen.  0, or
+// SLUICE_E_ABORTED / SLUICE_E_TIMEOUT.
+__device__ int wait_slot(const int32_t* p, int32_t s, const int32_t* abort_flag,
+                         long long timeout_ticks, int32_t* seen) {
+  const long long t0 = wall_clock64();
+  for (;;) {
+    const int32_t v = ld_host(p);
+    *seen = v;
+    if (stamp_dist(s, v) <= kRing) return 0;
+    if (ld_host(abort_flag) != 0) return SLUICE_E_ABORTED;
+    if (wall_clock64() - t0 > timeout_ticks) return SLUICE_E_TIMEOUT;
+    __builtin_amdgcn_s_sleep(4);
+  }
+}
+
 // Spin until *p == want (acquire on success when ACQ: the caller then reads
 // what the host wrote before *p).  0, or SLUICE_E_ABORTED / SLUICE_E_TIMEOUT.
 template <bool ACQ>
@@ -202,7 +239,7 @@ __device__ int wait_eq(const int32_t* p, int32_t want, const int32_t* abort_flag
 
 // dev_state: [0] last stamp issued, [1] 1 once the host has installed a
 // standing map (device-side copy of mb->standing, which never goes back to
-// 0, so later gaps skip that bus read).
+// 0, so later gaps skip that bus read), [2] the last host ack read.
 constexpr int kGapMaxPerThread = SLUICE_MAX_EXPERTS / kLookupThreads;
 
 __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
@@ -237,17 +274,23 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     const int e = c * kLookupThreads + tid;
     unmapped[c] = e < E && local_of[e] >= 0 && map[e] < 0;
   }
-  int32_t prev = 0, ack = 0;
+  int32_t s = 0, seen = 0;
+  bool fresh = false;
   if (tid == 0) {
-    prev = dev_state[0];
+    s = dev_state[0] + 1;
+    if (s <= 0) s = 1;
     s_standing = dev_state[1];
+    seen = dev_state[2];
   }
   for (int e = tid; e < E; e += kLookupThreads) present[e] = 0;
   __syncthreads();
-  // The host must have copied out this layer's previous record before it is
-  // overwritten (it normally has, long ago): the bus read of its ack goes
-  // out now and is checked after the ids are compacted.
-  if (tid == 0) ack = ld_host(&mb->ack_stamp);
+  // Record s reuses the slot of record s - kRing, which the host must have
+  // copied out (it normally has, long ago).  When the last ack read does not
+  // show it, a fresh read goes out now and is checked after the compaction.
+  if (tid == 0 && stamp_dist(s, seen) > kRing) {
+    seen = ld_host(&mb->ack_stamp);
+    fresh = true;
+  }
   for (int i = tid; i < n; i += kLookupThreads) {
     const int g = ids[i];
     if ((unsigned)g < (unsigned)E) present[g] = 1;
@@ -279,10 +322,11 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     __syncthreads();
   }
   if (tid == 0) {
-    int32_t s = prev + 1;
-    if (s <= 0) s = 1;
     s_stamp = s;
-    s_status = ack == prev ? 0 : wait_eq<false>(&mb->ack_stamp, prev, abort_flag, timeout_ticks);
+    s_status = 0;
+    if (stamp_dist(s, seen) > kRing)
+      s_status = wait_slot(&mb->ack_stamp, s, abort_flag, timeout_ticks, &seen);
+    if (fresh) dev_state[2] = seen;
     s_waits = 0;
     if (s_status == 0) {
       if (!s_standing && ld_host(&mb->standing) != 0) {
@@ -299,9 +343,10 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
   if (s_status == 0) {
     // the record: entries and header in any order (each word is stamped)
     const int32_t s = s_stamp;
+    GapRecord* r = &mb->rec[s % kRing];
     for (int i = tid; i < base; i += kLookupThreads)
-      st_host64(&mb->ent[i], rec_word(s, (uint32_t)s_uniq[i]));
-    if (tid == 0) st_host64(&mb->hdr, rec_word(s, rec_hdr_hi(base, miss, s_waits)));
+      st_host64(&r->ent[i], rec_word(s, (uint32_t)s_uniq[i]));
+    if (tid == 0) st_host64(&r->hdr, rec_word(s, rec_hdr_hi(base, miss, s_waits)));
   }
 #pragma unroll
   for (int u = 0; u < kCopyU; ++u) {
@@ -413,7 +458,7 @@ struct sluice_layer {
   int device = -1;
   GapMailbox* mb = nullptr;      // host pointer
   GapMailbox* mb_dev = nullptr;  // device view of the same memory
-  int32_t* dev_block = nullptr;  // [E] local_of, then last stamp, standing seen
+  int32_t* dev_block = nullptr;  // [E] local_of, then last stamp, standing seen, last ack read
   int32_t host_stamp = 0;        // last record copied out
   std::atomic<int32_t> done_stamp{0};  // last record fully served
   int64_t bytes = 0;
@@ -449,11 +494,12 @@ int layer_device_init(sluice_layer* L) {
   SLUICE_HIP_CHECK(hipHostGetDevicePointer(&dp, p, 0));
   L->mb_dev = static_cast<GapMailbox*>(dp);
   const int E = L->c.E;
-  SLUICE_HIP_CHECK(hipMalloc((void**)&L->dev_block, sizeof(int32_t) * (E + 2)));
+  SLUICE_HIP_CHECK(hipMalloc((void**)&L->dev_block, sizeof(int32_t) * (E + 3)));
   std::vector<int32_t> blk(L->c.local_of.begin(), L->c.local_of.end());
   blk.push_back(0);  // last stamp issued
   blk.push_back(0);  // standing map seen
-  SLUICE_HIP_CHECK(hipMemcpy(L->dev_block, blk.data(), sizeof(int32_t) * (E + 2),
+  blk.push_back(0);  // last ack read
+  SLUICE_HIP_CHECK(hipMemcpy(L->dev_block, blk.data(), sizeof(int32_t) * (E + 3),
                              hipMemcpyHostToDevice));
   return SLUICE_OK;
 }
@@ -471,6 +517,13 @@ void respond(sluice_layer* L, int32_t stamp, int code) {
   __atomic_store_n(&mb->resp_stamp, stamp, __ATOMIC_RELEASE);
 }
 
+// A record after the last one served has been posted (records are posted
+// in stamp order, so looking at the next stamp's slot is enough).
+bool record_pending(sluice_layer* L) {
+  const int32_t next = next_stamp(L->done_stamp.load(std::memory_order_acquire));
+  return rec_stamp(__atomic_load_n(&L->mb->rec[next % kRing].hdr, __ATOMIC_ACQUIRE)) == next;
+}
+
 // Serve one posted record of layer L.  block: wait (bounded) for it;
 // `compute` (may be null) is polled for errors while waiting.
 int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
@@ -478,13 +531,14 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
   const int dev_status = __atomic_load_n(&mb->dev_status, __ATOMIC_ACQUIRE);
   if (dev_status != 0) return dev_status;  // a device wait failed earlier
   const int32_t want = next_stamp(L->host_stamp);
-  uint64_t hdr = __atomic_load_n(&mb->hdr, __ATOMIC_ACQUIRE);
+  GapRecord* rec = &mb->rec[want % kRing];
+  uint64_t hdr = __atomic_load_n(&rec->hdr, __ATOMIC_ACQUIRE);
   double t0 = 0.0;
   if (rec_stamp(hdr) != want) {
     if (!block) return kNothing;
     t0 = now_s();
     unsigned spins = 0;
-    while (rec_stamp(hdr = __atomic_load_n(&mb->hdr, __ATOMIC_ACQUIRE)) != want) {
+    while (rec_stamp(hdr = __atomic_load_n(&rec->hdr, __ATOMIC_ACQUIRE)) != want) {
       _mm_pause();
       if ((++spins & 4095u) == 0) {
         if (compute != nullptr) {
@@ -505,10 +559,10 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
   if (n_uniq > L->c.E) return SLUICE_E_STATE;
   L->uniq.resize(n_uniq);
   for (int i = 0; i < n_uniq; ++i) {
-    uint64_t w = __atomic_load_n(&mb->ent[i], __ATOMIC_ACQUIRE);
+    uint64_t w = __atomic_load_n(&rec->ent[i], __ATOMIC_ACQUIRE);
     if (rec_stamp(w) != want) {
       if (t0 == 0.0) t0 = now_s();
-      while (rec_stamp(w = __atomic_load_n(&mb->ent[i], __ATOMIC_ACQUIRE)) != want) {
+      while (rec_stamp(w = __atomic_load_n(&rec->ent[i], __ATOMIC_ACQUIRE)) != want) {
         _mm_pause();
         if (now_s() - t0 > gap_timeout_s()) return SLUICE_E_TIMEOUT;
       }
@@ -747,8 +801,7 @@ extern "C" int sluice_gap_server_drain(sluice_gap_server* S, double timeout_s) {
         S->error.compare_exchange_strong(zero, dev_status);
         break;
       }
-      const int32_t posted = rec_stamp(__atomic_load_n(&L->mb->hdr, __ATOMIC_ACQUIRE));
-      if (L->done_stamp.load(std::memory_order_acquire) == posted) break;
+      if (!record_pending(L)) break;
       if (S->error.load() != 0) break;
       if (now_s() - t0 > timeout_s) return SLUICE_E_TIMEOUT;
       _mm_pause();
@@ -790,7 +843,7 @@ extern "C" int sluice_layer_gap_resync(sluice_layer* L) {
   L->host_stamp = dev_stamp;
   L->done_stamp.store(dev_stamp);
   __atomic_store_n(&L->mb->ack_stamp, dev_stamp, __ATOMIC_RELEASE);
-  __atomic_store_n(&L->mb->hdr, rec_word(dev_stamp, 0u), __ATOMIC_RELEASE);
+  for (int i = 0; i < kRing; ++i) __atomic_store_n(&L->mb->rec[i].hdr, (uint64_t)0, __ATOMIC_RELEASE);
   __atomic_store_n(&L->mb->dev_status, 0, __ATOMIC_RELEASE);
   return SLUICE_OK;
 }
@@ -900,8 +953,7 @@ int wait_served(sluice_layer* L) {
       const int err = sluice_gap_server_error(L->server);
       if (err != 0) return err;
     }
-    const int32_t posted = rec_stamp(__atomic_load_n(&L->mb->hdr, __ATOMIC_ACQUIRE));
-    if (L->done_stamp.load(std::memory_order_acquire) == posted) return SLUICE_OK;
+    if (!record_pending(L)) return SLUICE_OK;
     if (now_s() - t0 > gap_timeout_s()) return SLUICE_E_TIMEOUT;
     _mm_pause();
   }
