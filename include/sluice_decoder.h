@@ -85,20 +85,17 @@ int sluice_dec_mla_attend(const float* q_lat, const float* q_pe, const void* ckv
                           int nh, int rope, int lora, int vh, int L, float scale, void* out,
                           sluice_stream_t stream);
 
-/* GQA decode with per-head q/k RMSNorm (Qwen3-MoE).
- * prep: qkv [c, (nh + 2*kvh)*hd] -> q [c, nh, hd] fp32 = rope(rmsnorm(q_h) * q_norm),
+/* GQA decode with per-head q/k RMSNorm (Qwen3-MoE), one launch:
+ *   from qkv [c, (nh + 2*kvh)*hd]: q_h = rope(rmsnorm(q_h) * q_norm) (bf16),
  *   k_cache [c, kvh, L, hd] row pos[t] = bf16(rope(rmsnorm(k_g) * k_norm)),
- *   v_cache [c, kvh, L, hd] row pos[t] = v_g.
- * attend: per query head h (kv head h / (nh/kvh)): softmax over rows
- *   0..pos[t] of (q . k) * scale, out [c, nh*hd] = bf16(p . v).
- *   hd == 128, L <= 4096. */
-int sluice_dec_gqa_prep(const void* qkv, const void* q_norm, const void* k_norm,
-                        const float* cos_t, const float* sin_t, const int64_t* pos, int c, int nh,
-                        int kvh, int hd, int L, float eps, float* q, void* k_cache, void* v_cache,
-                        sluice_stream_t stream);
-int sluice_dec_gqa_attend(const float* q, const void* k_cache, const void* v_cache,
-                          const int64_t* pos, int c, int nh, int kvh, int hd, int L, float scale,
-                          void* out, sluice_stream_t stream);
+ *   v_cache [c, kvh, L, hd] row pos[t] = v_g; then per query head h (kv head
+ *   h / (nh/kvh)): softmax over rows 0..pos[t] of (q . k) * scale,
+ *   out [c, nh*hd] = bf16(p . v).  hd == 128, L <= 4096; qkv, q_norm,
+ *   k_norm, cos_t, sin_t and the caches 16-byte aligned, out 4-byte aligned. */
+int sluice_dec_gqa_decode(const void* qkv, const void* q_norm, const void* k_norm,
+                          const float* cos_t, const float* sin_t, const int64_t* pos, int c,
+                          int nh, int kvh, int hd, int L, float eps, float scale, void* k_cache,
+                          void* v_cache, void* out, sluice_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -116,12 +116,10 @@ SIGNATURES = {
         c_int,
         [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P],
     ),
-    "sluice_dec_gqa_prep": (
+    "sluice_dec_gqa_decode": (
         c_int,
-        [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P, _P, _P],
-    ),
-    "sluice_dec_gqa_attend": (
-        c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P]
+        [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_float, c_float, _P, _P,
+         _P, _P],
     ),
 }
 

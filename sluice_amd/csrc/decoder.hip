@@ -503,145 +503,232 @@ __global__ __launch_bounds__(kA) void mla_attend_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// GQA with per-head q/k RMSNorm (Qwen3-MoE), head_dim 128.
+// GQA with per-head q/k RMSNorm (Qwen3-MoE), head_dim 128, in one launch:
+// the head's q/k RMSNorm and RoPE, the new cache row, and attention over
+// rows 0..pos[t].
+//
+// grid (c, nh), WAVES waves.  A wave is four 16-lane groups; lane `sub` of a
+// group owns head columns 8*sub .. 8*sub + 7 of q, k and v (lanes sub and
+// sub + 8 hold the rotate-half partners).  Group i takes cache rows i,
+// i + NG, ... of each chunk of NG*RG rows (a wave's load reads 4
+// consecutive rows), keeping a running max / sum / value accumulator of its
+// own (online softmax); the groups' states are merged in LDS at the end.
+// q . k runs on v_dot2_f32_bf16 with q rounded to bf16 (the cache's
+// precision), fp32 sums; the softmax runs in base 2 (v_exp_f32) on scores
+// scaled by log2(e).  The new row (position pos[t]) is computed in registers from qkv and
+// enters group 0's state first; the first query head of each kv head writes
+// it to the caches.  Every other cache row is only read, so no workgroup
+// reads a row another one writes.
 // ---------------------------------------------------------------------------
+
 constexpr int kHd = 128;
 
-// grid (c, nh + kvh), 64 threads: y < nh -> query head, else kv head y - nh.
-__global__ __launch_bounds__(64) void gqa_prep_kernel(
-    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_norm,
-    const uint16_t* __restrict__ k_norm, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t, const int64_t* __restrict__ pos, int nh, int kvh, int L,
-    float eps, float* __restrict__ q, uint16_t* __restrict__ k_cache,
-    uint16_t* __restrict__ v_cache) {
-  const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-  const long long p = pos[t];
-  if (p < 0 || p >= L) return;
-  const int width = (nh + 2 * kvh) * kHd;
-  const bool is_q = h < nh;
-  const int col = is_q ? h * kHd : (nh + (h - nh)) * kHd;
-  const uint16_t* xr = qkv + (size_t)t * width + col;
-  // lane holds the rotate-half pair (lane, lane + 64)
-  const float x1 = bf(xr[lane]), x2 = bf(xr[lane + 64]);
-  const float rstd = rsqrtf(wave_sum(x1 * x1 + x2 * x2) / (float)kHd + eps);
-  const uint16_t* nw = is_q ? q_norm : k_norm;
-  const float n1 = x1 * rstd * bf(nw[lane]), n2 = x2 * rstd * bf(nw[lane + 64]);
-  const float c = cos_t[p * 64 + lane], sn = sin_t[p * 64 + lane];
-  const float r1 = n1 * c - n2 * sn, r2 = n2 * c + n1 * sn;
-  if (is_q) {
-    float* o = q + ((size_t)t * nh + h) * kHd;
-    o[lane] = r1;
-    o[lane + 64] = r2;
-    return;
-  }
-  const int g = h - nh;
-  const size_t row = (((size_t)t * kvh + g) * L + p) * kHd;
-  k_cache[row + lane] = f32_to_bf16_bits(r1);
-  k_cache[row + lane + 64] = f32_to_bf16_bits(r2);
-  const uint16_t* vr = qkv + (size_t)t * width + (nh + kvh + g) * kHd;
-  v_cache[row + lane] = vr[lane];
-  v_cache[row + lane + 64] = vr[lane + 64];
-}
-
-// Sum of v over each 16-lane row of the wave, left in the row's lane 15
-// (DPP row shifts; other lanes hold partial sums).
-__device__ __forceinline__ float row16_sum_to_lane15(float v) {
+// Sum over each 16-lane row of the wave, left in every lane of the row
+// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror).
+__device__ __forceinline__ float row16_allsum(float v) {
   uint32_t u = __float_as_uint(v);
-  u = __float_as_uint(__uint_as_float(u) + __uint_as_float(dpp_mov<0x111, 0xf>(0u, u)));
-  u = __float_as_uint(__uint_as_float(u) + __uint_as_float(dpp_mov<0x112, 0xf>(0u, u)));
-  u = __float_as_uint(__uint_as_float(u) + __uint_as_float(dpp_mov<0x114, 0xf>(0u, u)));
-  u = __float_as_uint(__uint_as_float(u) + __uint_as_float(dpp_mov<0x118, 0xf>(0u, u)));
+  u = __float_as_uint(__uint_as_float(u) + __uint_as_float(dpp_mov<0xb1, 0xf>(0u, u)));
+  u = __float_as_uint(__uint_as_float(u) + __uint_as_float(dpp_mov<0x4e, 0xf>(0u, u)));
+  u = __float_as_uint(__uint_as_float(u) + __uint_as_float(dpp_mov<0x141, 0xf>(0u, u)));
+  u = __float_as_uint(__uint_as_float(u) + __uint_as_float(dpp_mov<0x140, 0xf>(0u, u)));
   return __uint_as_float(u);
 }
 
-// grid (c, nh).  Scores: 16 lanes per cache row (8 elements each), 16 rows
-// per pass and kSP passes' loads in flight; values: each wave takes rows
-// w, w + 4, ... with kVP rows' loads in flight, a lane owning 2 columns.
-constexpr int kSP = 8;
-constexpr int kVP = 16;
+// The value of lane sub ^ 8 of the same 16-lane row (row_ror:8).
+__device__ __forceinline__ float row16_partner(float v) {
+  return __uint_as_float(dpp_mov<0x128, 0xf>(0u, __float_as_uint(v)));
+}
 
-__global__ __launch_bounds__(kT) void gqa_attend_kernel(
-    const float* __restrict__ q, const uint16_t* __restrict__ k_cache,
-    const uint16_t* __restrict__ v_cache, const int64_t* __restrict__ pos, int nh, int kvh, int L,
-    float scale, uint16_t* __restrict__ out) {
-  __shared__ float sq[kHd];
-  __shared__ float s[kMaxL];
-  __shared__ float half2[kT];
-  __shared__ float red[kT / 64];
+// rope(rmsnorm(x) * w) of one head for this lane's 8 columns.
+__device__ __forceinline__ void head_norm_rope(u32x4_t x, u32x4_t w, const float* cs,
+                                               const float* sn, float eps, bool first_half,
+                                               float* r) {
+  float f[8], wf[8], n[8];
+  unpack8(x, f);
+  unpack8(w, wf);
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+  const float rstd = rsqrtf(row16_allsum(ss) / (float)kHd + eps);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) n[j] = f[j] * rstd * wf[j];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float o = row16_partner(n[j]);
+    r[j] = first_half ? n[j] * cs[j] - o * sn[j] : n[j] * cs[j] + o * sn[j];
+  }
+}
+
+// Cache rows c0 + gi + NG*r (r < RG) of this lane's columns; rows at or past
+// nc load row 0 (in bounds) and are masked by gqa_chunk.
+template <int RG, int NG>
+__device__ __forceinline__ void gqa_load_chunk(const uint16_t* __restrict__ k_cache,
+                                               const uint16_t* __restrict__ v_cache, size_t cbase,
+                                               int c0, int gi, int nc, u32x4_t* kr, u32x4_t* vr) {
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const int l = c0 + gi + NG * r;
+    const size_t off = (size_t)(l < nc ? l : 0) * kHd;
+    kr[r] = ldg16(k_cache + cbase + off);
+    vr[r] = ldg16(v_cache + cbase + off);
+  }
+}
+
+// q . k over this lane's 8 columns (bf16 pairs, fp32 accumulation).
+__device__ __forceinline__ float dot8_bf16(u32x4_t a, u32x4_t b) {
+  float d = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    // (the elements go through scalars: hipcc 7.2 bit-casts a vector element
+    // expression as if it were element 0)
+    const uint32_t aj = a[j], bj = b[j];
+    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, aj),
+                                        __builtin_bit_cast(bf16x2_t, bj), d, false);
+  }
+  return d;
+}
+
+// One chunk into a group's online-softmax state: running max m and sum
+// lsum of 2^score (scores carry the log2(e) factor), value accumulator acc
+// of this lane's 8 columns.
+template <int RG, int NG>
+__device__ __forceinline__ void gqa_chunk(const u32x4_t* kr, const u32x4_t* vr, int c0, int gi,
+                                          int nc, u32x4_t qb, float sl2, float& m, float& lsum,
+                                          float* acc) {
+  float s[RG];
+  float mc = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const float d = row16_allsum(dot8_bf16(qb, kr[r])) * sl2;
+    s[r] = c0 + gi + NG * r < nc ? d : -INFINITY;
+    mc = fmaxf(mc, s[r]);
+  }
+  const float mn = fmaxf(m, mc);
+  if (mn == -INFINITY) return;
+  const float f = __builtin_amdgcn_exp2f(m - mn);
+  lsum *= f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] *= f;
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const float pw = __builtin_amdgcn_exp2f(s[r] - mn);
+    float vf[8];
+    unpack8(vr[r], vf);
+    lsum += pw;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] += pw * vf[j];
+  }
+  m = mn;
+}
+
+// 8 waves, 2 rows per group per chunk (256 rows per chunk): measured in
+// replayed graphs against 4 waves x 4 or 8 rows and 8 waves x 4 rows at
+// positions 0..1000.
+constexpr int kGqaWaves = 8;
+constexpr int kGqaRows = 2;
+
+template <int WAVES, int RG>
+__global__ __launch_bounds__(WAVES * 64) void gqa_decode_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_norm,
+    const uint16_t* __restrict__ k_norm, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const int64_t* __restrict__ pos, int nh, int kvh, int L,
+    float eps, float scale, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+    uint16_t* __restrict__ out) {
+  constexpr int NG = WAVES * 4;
+  constexpr int CH = NG * RG;
+  __shared__ float gacc[NG][kHd];
+  __shared__ float gm[NG], gl[NG];
   const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int grp = nh / kvh, g = h / grp;
+  const int sub = tid & 15, gi = tid >> 4;
+  const int col = sub * 8;
+  const uint16_t* xr = qkv + (size_t)t * (nh + 2 * kvh) * kHd;
+  const size_t cbase = ((size_t)t * kvh + g) * L * kHd + col;
+
+  // Everything that does not depend on the position goes out with its
+  // load: the head's q, the new k and v, the norm weights and the first
+  // chunk of cache rows (rows past the position are loaded, in bounds, and
+  // masked below).
+  const u32x4_t xq = ldg16(xr + h * kHd + col);
+  const u32x4_t xk = ldg16(xr + (nh + g) * kHd + col);
+  const u32x4_t xv = ldg16(xr + (nh + kvh + g) * kHd + col);
+  const u32x4_t wq = ldg16(q_norm + col), wk = ldg16(k_norm + col);
+  u32x4_t kr[RG], vr[RG];
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const int l = gi + NG * r;
+    const size_t off = (size_t)(l < L ? l : L - 1) * kHd;
+    kr[r] = ldg16(k_cache + cbase + off);
+    vr[r] = ldg16(v_cache + cbase + off);
+  }
   const long long p = pos[t];
   if (p < 0 || p >= L) return;
-  const int n = (int)p + 1;
-  const int g = h / (nh / kvh);
-  if (tid < kHd) sq[tid] = q[((size_t)t * nh + h) * kHd + tid];
-  __syncthreads();
-  const uint16_t* kb = k_cache + ((size_t)t * kvh + g) * L * kHd;
-  const uint16_t* vb = v_cache + ((size_t)t * kvh + g) * L * kHd;
-  const int sub = tid & 15, rw = tid >> 4;
-  float qv[8];
+  const int nc = (int)p;  // cache rows before the new one
+  const int ci = (int)p * 64 + (sub & 7) * 8;
+  float cs[8], sn[8];
+  *reinterpret_cast<f32x4_t*>(cs) = *reinterpret_cast<const f32x4_t*>(cos_t + ci);
+  *reinterpret_cast<f32x4_t*>(cs + 4) = *reinterpret_cast<const f32x4_t*>(cos_t + ci + 4);
+  *reinterpret_cast<f32x4_t*>(sn) = *reinterpret_cast<const f32x4_t*>(sin_t + ci);
+  *reinterpret_cast<f32x4_t*>(sn + 4) = *reinterpret_cast<const f32x4_t*>(sin_t + ci + 4);
+
+  const bool first_half = sub < 8;
+  float qf[8], kf[8];
+  head_norm_rope(xq, wq, cs, sn, eps, first_half, qf);
+  head_norm_rope(xk, wk, cs, sn, eps, first_half, kf);
+  // q and the new k row in bf16 (the k row as the cache holds it)
+  u32x4_t qb, kb;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) qv[j] = sq[sub * 8 + j];
-  float lmax = -INFINITY;
-  for (int l0 = 0; l0 < n; l0 += kSP * (kT / 16)) {
-    u32x4_t kr[kSP];
-#pragma unroll
-    for (int u = 0; u < kSP; ++u) {
-      const int l = l0 + u * (kT / 16) + rw;
-      kr[u] = *reinterpret_cast<const u32x4_t*>(kb + (size_t)(l < n ? l : 0) * kHd + sub * 8);
-    }
-#pragma unroll
-    for (int u = 0; u < kSP; ++u) {
-      const int l = l0 + u * (kT / 16) + rw;
-      float kv[8];
-      unpack8(kr[u], kv);
-      float d = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) d += qv[j] * kv[j];
-      d = row16_sum_to_lane15(d) * scale;
-      if (sub == 15 && l < n) {
-        s[l] = d;
-        lmax = fmaxf(lmax, d);
-      }
-    }
+  for (int j = 0; j < 4; ++j) {
+    qb[j] = pack2(qf[2 * j], qf[2 * j + 1]);
+    kb[j] = pack2(kf[2 * j], kf[2 * j + 1]);
   }
-  const float m = block_max(lmax, red);
-  float part = 0.f;
-  for (int l = tid; l < n; l += kT) {
-    const float e = expf(s[l] - m);
-    s[l] = e;
-    part += e;
+  if (h % grp == 0 && gi == 0) {
+    *reinterpret_cast<u32x4_t*>(k_cache + cbase + (size_t)p * kHd) = kb;
+    *reinterpret_cast<u32x4_t*>(v_cache + cbase + (size_t)p * kHd) = xv;
   }
-  const float inv = 1.0f / block_sum(part, red);
-  __syncthreads();
-  // out[d] = sum_l p[l] v[l][d]; waves summed in LDS.
-  float a0 = 0.f, a1 = 0.f;
-  const int wave = tid >> 6, lane = tid & 63;
-  for (int l0 = wave; l0 < n; l0 += kVP * (kT / 64)) {
-    uint32_t vv[kVP];
+  const float sl2 = scale * 1.4426950408889634f;  // scores in log2 units
+  float m = -INFINITY, lsum = 0.f, acc[8];
 #pragma unroll
-    for (int u = 0; u < kVP; ++u) {
-      const int l = l0 + u * (kT / 64);
-      vv[u] = *reinterpret_cast<const uint32_t*>(vb + (size_t)(l < n ? l : 0) * kHd + 2 * lane);
-    }
-#pragma unroll
-    for (int u = 0; u < kVP; ++u) {
-      const int l = l0 + u * (kT / 64);
-      const float pl = l < n ? s[l] : 0.f;
-      a0 += pl * __uint_as_float(vv[u] << 16);
-      a1 += pl * __uint_as_float(vv[u] & 0xffff0000u);
-    }
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  if (gi == 0) {
+    m = row16_allsum(dot8_bf16(qb, kb)) * sl2;
+    lsum = 1.f;
+    unpack8(xv, acc);
   }
-  half2[tid] = a0;  // reused as [4 waves][64 lanes] x 2
+
+  // Chunks alternate between two register buffers: the next chunk's loads
+  // are in flight while this one is scored and accumulated.
+  u32x4_t kr2[RG], vr2[RG];
+  for (int c0 = 0; c0 < nc; c0 += 2 * CH) {
+    if (c0 + CH < nc) gqa_load_chunk<RG, NG>(k_cache, v_cache, cbase, c0 + CH, gi, nc, kr2, vr2);
+    gqa_chunk<RG, NG>(kr, vr, c0, gi, nc, qb, sl2, m, lsum, acc);
+    if (c0 + CH >= nc) break;
+    if (c0 + 2 * CH < nc) gqa_load_chunk<RG, NG>(k_cache, v_cache, cbase, c0 + 2 * CH, gi, nc, kr, vr);
+    gqa_chunk<RG, NG>(kr2, vr2, c0 + CH, gi, nc, qb, sl2, m, lsum, acc);
+  }
+
+  if (sub == 0) {
+    gm[gi] = m;
+    gl[gi] = lsum;
+  }
+  *reinterpret_cast<f32x4_t*>(&gacc[gi][col]) = *reinterpret_cast<const f32x4_t*>(acc);
+  *reinterpret_cast<f32x4_t*>(&gacc[gi][col + 4]) = *reinterpret_cast<const f32x4_t*>(acc + 4);
   __syncthreads();
-  float* sum1 = s;  // scores are no longer needed: reuse for the odd columns
-  __syncthreads();
-  sum1[tid] = a1;
-  __syncthreads();
-  if (tid < 64) {
-    const float e0 = half2[tid] + half2[64 + tid] + half2[128 + tid] + half2[192 + tid];
-    const float e1 = sum1[tid] + sum1[64 + tid] + sum1[128 + tid] + sum1[192 + tid];
+  if (tid < kHd / 2) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NG; ++i) M = fmaxf(M, gm[i]);
+    float den = 0.f, a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const float f = __builtin_amdgcn_exp2f(gm[i] - M);  // empty groups: 2^-inf = 0
+      den += f * gl[i];
+      a0 += f * gacc[i][2 * tid];
+      a1 += f * gacc[i][2 * tid + 1];
+    }
+    const float inv = 1.0f / den;
     *reinterpret_cast<uint32_t*>(out + ((size_t)t * nh + h) * kHd + 2 * tid) =
-        pack2(e0 * inv, e1 * inv);
+        pack2(a0 * inv, a1 * inv);
   }
 }
 
@@ -1003,31 +1090,24 @@ extern "C" int sluice_dec_mla_attend(const float* q_lat, const float* q_pe, cons
   return (int)hipGetLastError();
 }
 
-extern "C" int sluice_dec_gqa_prep(const void* qkv, const void* q_norm, const void* k_norm,
-                                   const float* cos_t, const float* sin_t, const int64_t* pos,
-                                   int c, int nh, int kvh, int hd, int L, float eps, float* q,
-                                   void* k_cache, void* v_cache, sluice_stream_t stream) {
+extern "C" int sluice_dec_gqa_decode(const void* qkv, const void* q_norm, const void* k_norm,
+                                     const float* cos_t, const float* sin_t, const int64_t* pos,
+                                     int c, int nh, int kvh, int hd, int L, float eps, float scale,
+                                     void* k_cache, void* v_cache, void* out,
+                                     sluice_stream_t stream) {
   if (c < 0 || nh <= 0 || kvh <= 0 || nh % kvh != 0 || hd != kHd || L <= 0 || L > kMaxL)
     return SLUICE_E_INVAL;
-  if (!qkv || !q_norm || !k_norm || !cos_t || !sin_t || !pos || !q || !k_cache || !v_cache)
+  if (!qkv || !q_norm || !k_norm || !cos_t || !sin_t || !pos || !k_cache || !v_cache || !out)
+    return SLUICE_E_INVAL;
+  if ((((uintptr_t)qkv | (uintptr_t)q_norm | (uintptr_t)k_norm | (uintptr_t)cos_t |
+        (uintptr_t)sin_t | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15) != 0 ||
+      ((uintptr_t)out & 3) != 0)
     return SLUICE_E_INVAL;
   if (c == 0) return SLUICE_OK;
-  hipLaunchKernelGGL(gqa_prep_kernel, dim3(c, nh + kvh), dim3(64), 0, (hipStream_t)stream,
-                     (const uint16_t*)qkv, (const uint16_t*)q_norm, (const uint16_t*)k_norm, cos_t,
-                     sin_t, pos, nh, kvh, L, eps, q, (uint16_t*)k_cache, (uint16_t*)v_cache);
+  hipLaunchKernelGGL((gqa_decode_kernel<kGqaWaves, kGqaRows>), dim3(c, nh),
+                     dim3(kGqaWaves * 64), 0, (hipStream_t)stream, (const uint16_t*)qkv,
+                     (const uint16_t*)q_norm, (const uint16_t*)k_norm, cos_t, sin_t, pos, nh, kvh,
+                     L, eps, scale, (uint16_t*)k_cache, (uint16_t*)v_cache, (uint16_t*)out);
   return (int)hipGetLastError();
 }
 
-extern "C" int sluice_dec_gqa_attend(const float* q, const void* k_cache, const void* v_cache,
-                                     const int64_t* pos, int c, int nh, int kvh, int hd, int L,
-                                     float scale, void* out, sluice_stream_t stream) {
-  if (c < 0 || nh <= 0 || kvh <= 0 || nh % kvh != 0 || hd != kHd || L <= 0 || L > kMaxL)
-    return SLUICE_E_INVAL;
-  if (!q || !k_cache || !v_cache || !pos || !out) return SLUICE_E_INVAL;
-  if ((uintptr_t)k_cache & 15) return SLUICE_E_INVAL;
-  if (c == 0) return SLUICE_OK;
-  hipLaunchKernelGGL(gqa_attend_kernel, dim3(c, nh), dim3(kT), 0, (hipStream_t)stream, q,
-                     (const uint16_t*)k_cache, (const uint16_t*)v_cache, pos, nh, kvh, L, scale,
-                     (uint16_t*)out);
-  return (int)hipGetLastError();
-}

@@ -376,8 +376,8 @@ class _MLA(nn.Module):
 
 class _GQA(nn.Module):
     """Grouped-query attention with per-head q/k RMSNorm (Qwen3): one QKV
-    GEMM, a prep kernel (norms, RoPE, cache write), an attention kernel and
-    the output GEMM."""
+    GEMM, one attention kernel (norms, RoPE, cache write, attention) and the
+    output GEMM."""
 
     def __init__(self, sp, batch, max_len, dev, gen):
         super().__init__()
@@ -401,17 +401,12 @@ class _GQA(nn.Module):
         lib, check = _k()
         c = hn.shape[0]
         qkv = linear(hn, self.wqkv)
-        st = _stream(hn)
-        q = torch.empty((c, self.nh, self.hd), dtype=torch.float32, device=hn.device)
-        check(lib.sluice_dec_gqa_prep(
+        o = torch.empty((c, self.nh * self.hd), dtype=hn.dtype, device=hn.device)
+        check(lib.sluice_dec_gqa_decode(
             qkv.data_ptr(), self.q_norm.data_ptr(), self.k_norm.data_ptr(), cos_t.data_ptr(),
             sin_t.data_ptr(), pos.data_ptr(), c, self.nh, self.kvh, self.hd, self.L, _EPS,
-            q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), st), "sluice_dec_gqa_prep")
-        o = torch.empty((c, self.nh * self.hd), dtype=hn.dtype, device=hn.device)
-        check(lib.sluice_dec_gqa_attend(
-            q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), pos.data_ptr(), c, self.nh,
-            self.kvh, self.hd, self.L, float(self.scale), o.data_ptr(), st),
-            "sluice_dec_gqa_attend")
+            float(self.scale), self.k.data_ptr(), self.v.data_ptr(), o.data_ptr(), _stream(hn)),
+            "sluice_dec_gqa_decode")
         return linear(o, self.wo)
 
 

@@ -1,7 +1,7 @@
 """Kernels of the synthetic decoders (include/sluice_decoder.h) against plain
 float32 torch references of the same math, computed on the CPU from the same
 bf16 inputs: residual add + RMSNorm, SwiGLU activation, router logits, MLA
-and GQA decode attention (prep + attend)."""
+and GQA decode attention."""
 
 import numpy as np
 import pytest
@@ -254,8 +254,9 @@ def test_mla_prep_and_attend(L, positions, vh):
     assert torch.equal(d["ckv"].cpu()[mask], ckv[mask])
 
 
-@pytest.mark.parametrize("L,positions", [(48, [7, 47, 0]), (600, [300, 599, 129])])
-def test_gqa_prep_and_attend(L, positions):
+@pytest.mark.parametrize("L,positions", [(48, [7, 47, 0]), (600, [300, 599, 129]),
+                                         (4096, [4095, 2500, 1])])
+def test_gqa_decode(L, positions):
     lib, check = _lib()
     c, nh, kvh, hd = 3, 32, 4, 128
     g = torch.Generator().manual_seed(12 + L)
@@ -269,15 +270,11 @@ def test_gqa_prep_and_attend(L, positions):
     scale = hd ** -0.5
     d = {kk: vv.to(DEV) for kk, vv in dict(qkv=qkv, qn=q_norm, kn=k_norm, k=k.clone(), v=v.clone(),
                                            pos=pos, cos=cos_t, sin=sin_t).items()}
-    q = torch.empty((c, nh, hd), dtype=torch.float32, device=DEV)
     out = torch.empty((c, nh * hd), dtype=torch.bfloat16, device=DEV)
-    check(lib.sluice_dec_gqa_prep(
+    check(lib.sluice_dec_gqa_decode(
         d["qkv"].data_ptr(), d["qn"].data_ptr(), d["kn"].data_ptr(), d["cos"].data_ptr(),
-        d["sin"].data_ptr(), d["pos"].data_ptr(), c, nh, kvh, hd, L, 1e-6, q.data_ptr(),
-        d["k"].data_ptr(), d["v"].data_ptr(), _st()), "gqa_prep")
-    check(lib.sluice_dec_gqa_attend(
-        q.data_ptr(), d["k"].data_ptr(), d["v"].data_ptr(), d["pos"].data_ptr(), c, nh, kvh, hd, L,
-        scale, out.data_ptr(), _st()), "gqa_attend")
+        d["sin"].data_ptr(), d["pos"].data_ptr(), c, nh, kvh, hd, L, 1e-6, scale,
+        d["k"].data_ptr(), d["v"].data_ptr(), out.data_ptr(), _st()), "gqa_decode")
     torch.cuda.synchronize()
     for t in range(c):
         p = int(pos[t])
@@ -287,7 +284,6 @@ def test_gqa_prep_and_attend(L, positions):
         vh_ = x[(nh + kvh) * hd:].view(kvh, hd)
         qr = _rope(_rms(qh, q_norm.float()), cos_t[p], sin_t[p])
         kr = _rope(_rms(kh, k_norm.float()), cos_t[p], sin_t[p])
-        assert _rel(q[t], qr) <= 1e-5
         assert _rel(d["k"][t, :, p], kr) <= TOL
         assert torch.equal(d["v"][t, :, p].cpu(), vh_.bfloat16())
         kc, vc = d["k"][t, :, : p + 1].float().cpu(), d["v"][t, :, : p + 1].float().cpu()
@@ -296,3 +292,9 @@ def test_gqa_prep_and_attend(L, positions):
             s = (qr[h] @ kc[h // grp].T) * scale
             o = torch.softmax(s, dim=-1) @ vc[h // grp]
             assert _rel(out[t, h * hd:(h + 1) * hd], o) <= TOL, (t, h)
+    # rows other than pos[t] are untouched
+    mask = torch.ones((c, L), dtype=torch.bool)
+    mask[torch.arange(c), pos] = False
+    for name, ref in (("k", k), ("v", v)):
+        got = d[name].cpu().permute(0, 2, 1, 3)
+        assert torch.equal(got[mask], ref.permute(0, 2, 1, 3)[mask]), name
