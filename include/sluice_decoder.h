@@ -63,27 +63,32 @@ int sluice_dec_gate_logits(const void* hn, const void* wg, const float* bias_tab
                            const int64_t* step, int n_steps, int bias_rows, int rows, int H, int E,
                            float* out, sluice_stream_t stream);
 
-/* MLA decode (DeepSeek-V2 latent attention with absorbed up-projections).
- * prep: q rows of q_stride elements holding nh heads of (nope then rope),
- *   kva rows of kva_stride elements holding lora then rope values
- *   -> q_lat [c, nh, lora] fp32 = q_nope . w_uk[h] (w_uk [nh, nope, lora]),
- *      q_pe [c, nh, rope] fp32 = rope(q_pe),
- *      ckv_cache [c, L, lora] row pos[t] = bf16(rmsnorm(kva[:lora]) * kv_norm),
- *      kpe_cache [c, L, rope] row pos[t] = bf16(rope(kva[lora:])).
- *   rope is rotate-half with cos/sin [*, rope/2] fp32 rows at pos[t].
- * attend: scores over cache rows 0..pos[t] = (q_lat . ckv + q_pe . kpe) * scale,
- *   softmax, o_lat = p . ckv, out [c, nh*vh] = bf16(o_lat . w_uv[h])
- *   (w_uv [nh, lora, vh]).  lora == 512, rope == 64, nope % 2 == 0,
- *   vh <= 256, L <= 4096. */
-int sluice_dec_mla_prep(const void* q, int q_stride, const void* kva, int kva_stride,
-                        const void* kv_norm, const void* w_uk, const float* cos_t,
-                        const float* sin_t, const int64_t* pos, int c, int nh, int nope, int rope,
-                        int lora, int L, float eps, float* q_lat, float* q_pe, void* ckv_cache,
-                        void* kpe_cache, sluice_stream_t stream);
-int sluice_dec_mla_attend(const float* q_lat, const float* q_pe, const void* ckv_cache,
-                          const void* kpe_cache, const void* w_uv, const int64_t* pos, int c,
-                          int nh, int rope, int lora, int vh, int L, float scale, void* out,
-                          sluice_stream_t stream);
+/* MLA decode (DeepSeek-V2 latent attention with absorbed up-projections) on
+ * the matrix cores, three launches (q absorption + new cache rows, row splits
+ * of the attention, merge + value up-projection):
+ *   q rows of q_stride elements hold nh heads of (nope then rope) values,
+ *   kva rows of kva_stride elements hold lora then rope values;
+ *   q_lat = q_nope . w_uk[h] (w_ukt [nh, lora, nope] is w_uk transposed),
+ *   q_pe = rope(q_pe); ckv_cache [c, L, lora] row pos[t] =
+ *   bf16(rmsnorm(kva[:lora]) * kv_norm), kpe_cache [c, L, rope] row pos[t] =
+ *   bf16(rope(kva[lora:])); scores over cache rows 0..pos[t] =
+ *   (q_lat . ckv + q_pe . kpe) * scale, softmax, o_lat = p . ckv,
+ *   out [c, nh*vh] = bf16(o_lat . w_uv[h]) (w_uv [nh, lora, vh]).
+ * rope is rotate-half with cos/sin [*, rope/2] fp32 rows at pos[t].  The
+ * latent cache is kept twice: ckv_cache and ckvt_cache [c, L/32, lora, 32],
+ * row r of each 32-row block at slot 8*((r & 15) >> 2) + 4*(r >> 4) + (r & 3)
+ * of each latent column; row pos[t] is written to both.  q_lat and p are
+ * rounded to bf16 for the products.  lora == 512, rope == 64, nh % 16 == 0,
+ * nope % 32 == 0, vh % 8 == 0 and <= 256, c <= 16, L % 32 == 0 and <= 4096.
+ * work: sluice_dec_mla_workspace(c, nh) bytes; q, w_ukt, w_uv, the caches and
+ * work 16-byte aligned, kva and kv_norm 4-byte aligned. */
+size_t sluice_dec_mla_workspace(int c, int nh);
+int sluice_dec_mla_decode(const void* q, int q_stride, const void* kva, int kva_stride,
+                          const void* kv_norm, const void* w_ukt, const void* w_uv,
+                          const float* cos_t, const float* sin_t, const int64_t* pos, int c,
+                          int nh, int nope, int rope, int lora, int vh, int L, float eps,
+                          float scale, void* ckv_cache, void* ckvt_cache, void* kpe_cache,
+                          void* work, void* out, sluice_stream_t stream);
 
 /* GQA decode with per-head q/k RMSNorm (Qwen3-MoE), one launch:
  *   from qkv [c, (nh + 2*kvh)*hd]: q_h = rope(rmsnorm(q_h) * q_norm) (bf16),

@@ -107,14 +107,11 @@ SIGNATURES = {
     "sluice_dec_gate_logits": (
         c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, _P]
     ),
-    "sluice_dec_mla_prep": (
+    "sluice_dec_mla_workspace": (c_size_t, [c_int, c_int]),
+    "sluice_dec_mla_decode": (
         c_int,
-        [_P, c_int, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,
-         c_float, _P, _P, _P, _P, _P],
-    ),
-    "sluice_dec_mla_attend": (
-        c_int,
-        [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P],
+        [_P, c_int, _P, c_int, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,
+         c_int, c_float, c_float, _P, _P, _P, _P, _P, _P],
     ),
     "sluice_dec_gqa_decode": (
         c_int,

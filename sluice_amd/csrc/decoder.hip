@@ -279,226 +279,369 @@ constexpr int kLora = 512;
 constexpr int kRope = 64;
 constexpr int kMaxL = 4096;
 
-// grid (c, nh + 1): y < nh -> query head y; y == nh -> the token's kv row.
-__global__ __launch_bounds__(kT) void mla_prep_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kva,
-    const uint16_t* __restrict__ kv_norm, const uint16_t* __restrict__ w_uk,
+// ---------------------------------------------------------------------------
+// MLA decode on the matrix cores, three launches:
+//   mla_absorb_kernel   q_lat = q_nope . W_uk per head as one MFMA product over
+//                       the batch (W_uk read once per head, not per token),
+//                       q_pe RoPE, and the new latent / rope-key cache rows;
+//   mla_partial_kernel  per (token, split of the rows, 16 heads): scores
+//                       S = [q_lat ; q_pe] . [ckv ; kpe]^T and the latent sum
+//                       O = P . ckv on v_mfma_f32_16x16x32_bf16 (the 16 heads
+//                       are the M dimension), online softmax over 64-row
+//                       steps, the split's (max, sum, O) to a workspace;
+//   mla_merge_kernel    per (token, head): the splits merged, then the value
+//                       up-projection.
+// The P . ckv product contracts over cache rows, so its ckv operand needs 8
+// consecutive rows of one latent column per lane: the cache keeps a second,
+// transposed copy, ckvt [c][L/32][512][32], whose 32-row blocks hold the rows
+// in the K order of that product (mla_kpos), so both products load their
+// operands with plain 16-byte loads.  Scores and P are bf16 MFMA operands
+// (q_lat rounded to bf16), sums fp32, softmax in base 2.
+// ---------------------------------------------------------------------------
+constexpr int kMlaSplit = 32;  // row splits per token
+constexpr int kMlaStep = 32;   // rows per step of a split (one 16-row tile per wave)
+constexpr int kMlaRec = kLora + 4;  // per (token, split, head): m, l, -, -, O[512]
+
+// Slot of row r (0..31) of a 32-row block in the transposed cache: K index
+// 8g + j (j < 4) holds row 4g + j, 8g + 4 + j holds row 16 + 4g + j -- the
+// rows lane group g holds in the score tiles of rows 0..15 and 16..31.
+__host__ __device__ inline int mla_kpos(int r) {
+  const int hi = r >> 4, q = r & 15;
+  return 8 * (q >> 2) + 4 * hi + (q & 3);
+}
+
+// Rows per split for n rows: a multiple of the step.
+__host__ __device__ inline int mla_chunk(int n) {
+  const int per = (n + kMlaSplit - 1) / kMlaSplit;
+  return (per + kMlaStep - 1) / kMlaStep * kMlaStep;
+}
+
+// grid (nh * 8 + c), kT threads.  Block b < nh * 8: head b / 8, latent
+// columns 64 * (b % 8) .. +64 of q_lat for every token (wave w: 16 columns,
+// tokens on M, K = nope); block 8 * h also ropes head h's q_pe.  Block
+// nh * 8 + t: token t's cache rows.
+__global__ __launch_bounds__(kT) void mla_absorb_kernel(
+    const uint16_t* __restrict__ q, int q_stride, const uint16_t* __restrict__ kva,
+    int kva_stride, const uint16_t* __restrict__ kv_norm, const uint16_t* __restrict__ w_ukt,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-    const int64_t* __restrict__ pos, int nh, int nope, int q_stride, int kva_stride, int L,
-    float eps, float* __restrict__ q_lat, float* __restrict__ q_pe,
-    uint16_t* __restrict__ ckv_cache, uint16_t* __restrict__ kpe_cache) {
-  __shared__ float qn[256];
+    const int64_t* __restrict__ pos, int c, int nh, int nope, int L, float eps,
+    uint16_t* __restrict__ q_lat, uint16_t* __restrict__ q_pe, uint16_t* __restrict__ ckv,
+    uint16_t* __restrict__ ckvt, uint16_t* __restrict__ kpe) {
   __shared__ float red[kT / 64];
-  __shared__ float ql_part[kT / 64][kLora];
-  const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-  const long long p = pos[t];
-  if (p < 0 || p >= L) return;
-  const float* cr = cos_t + p * (kRope / 2);
-  const float* sr = sin_t + p * (kRope / 2);
-  if (h < nh) {
-    const uint16_t* qh = q + (size_t)t * q_stride + (size_t)h * (nope + kRope);
-    for (int d = tid; d < nope; d += kT) qn[d] = bf(qh[d]);
-    if (tid < kRope / 2) {
-      const float x1 = bf(qh[nope + tid]), x2 = bf(qh[nope + tid + kRope / 2]);
-      float* o = q_pe + ((size_t)t * nh + h) * kRope;
-      o[tid] = x1 * cr[tid] - x2 * sr[tid];
-      o[tid + kRope / 2] = x2 * cr[tid] + x1 * sr[tid];
-    }
-    __syncthreads();
-    // q_lat[j] = sum_d q_nope[d] w_uk[h][d][j]: wave w takes rows d = w, w+4,
-    // ..., a lane owns columns 8*lane..+8 (16-byte loads, 4 rows in flight);
-    // the waves' sums meet in LDS.
-    const int wave = tid >> 6, lane = tid & 63;
-    const uint16_t* wk = w_uk + (size_t)h * nope * kLora + lane * 8;
-    float acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-    for (int d0 = wave; d0 < nope; d0 += 16) {
-      u32x4_t wv[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int kTiles = kLora / 64;
+  const int b = blockIdx.x;
+  if (b < nh * kTiles) {
+    const int h = b / kTiles, jt = b % kTiles;
+    const int R = lane & 15, g = lane >> 4;
+    const int j = jt * 64 + wave * 16 + R;
+    const int qh = h * (nope + kRope);
+    const uint16_t* arow = q + (size_t)(R < c ? R : 0) * q_stride + qh + 8 * g;
+    const uint16_t* brow = w_ukt + ((size_t)h * kLora + j) * nope + 8 * g;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < nope; k0 += 128) {
+      // four K steps' loads in flight (steps past nope re-load step 0 and
+      // are skipped)
+      u32x4_t av[4], bv[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int d = d0 + 4 * u;
-        wv[u] = *reinterpret_cast<const u32x4_t*>(wk + (size_t)(d < nope ? d : 0) * kLora);
+        const int k = k0 + 32 * u < nope ? k0 + 32 * u : 0;
+        av[u] = ldg16(arow + k);
+        bv[u] = ldg16(brow + k);
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int d = d0 + 4 * u;
-        const float qd = d < nope ? qn[d] : 0.f;
-        float c[8];
-        unpack8(wv[u], c);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] += qd * c[j];
-      }
+      for (int u = 0; u < 4; ++u)
+        if (k0 + 32 * u < nope) acc = mfma16x16x32_bf16(av[u], bv[u], acc);
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ql_part[wave][lane * 8 + j] = acc[j];
-    __syncthreads();
-    float* o = q_lat + ((size_t)t * nh + h) * kLora;
-    for (int j = tid; j < kLora; j += kT)
-      o[j] = ql_part[0][j] + ql_part[1][j] + ql_part[2][j] + ql_part[3][j];
+    for (int r = 0; r < 4; ++r) {
+      const int t = 4 * g + r;  // D row = token, column = j
+      if (t < c) q_lat[((size_t)t * nh + h) * kLora + j] = f32_to_bf16_bits(acc[r]);
+    }
+    if (jt == 0) {
+      for (int i = tid; i < c * (kRope / 2); i += kT) {
+        const int t = i / (kRope / 2), d = i % (kRope / 2);
+        const long long p = pos[t];
+        if (p < 0 || p >= L) continue;
+        const uint16_t* qr = q + (size_t)t * q_stride + qh + nope;
+        const float x1 = bf(qr[d]), x2 = bf(qr[d + kRope / 2]);
+        const float cs = cos_t[p * (kRope / 2) + d], sn = sin_t[p * (kRope / 2) + d];
+        uint16_t* o = q_pe + ((size_t)t * nh + h) * kRope;
+        o[d] = f32_to_bf16_bits(x1 * cs - x2 * sn);
+        o[d + kRope / 2] = f32_to_bf16_bits(x2 * cs + x1 * sn);
+      }
+    }
     return;
   }
-  // kv row: rmsnorm(kva[:lora]) * kv_norm, rope(kva[lora:])
+  // token t's cache rows: rmsnorm(kva[:lora]) * kv_norm, rope(kva[lora:])
+  const int t = b - nh * kTiles;
+  const long long p = pos[t];
+  if (p < 0 || p >= L) return;
   const uint16_t* kr = kva + (size_t)t * kva_stride;
   const uint32_t v2 = reinterpret_cast<const uint32_t*>(kr)[tid];
   const float x0 = __uint_as_float(v2 << 16), x1 = __uint_as_float(v2 & 0xffff0000u);
   const float rstd = rsqrtf(block_sum(x0 * x0 + x1 * x1, red) / (float)kLora + eps);
   const uint32_t g2 = reinterpret_cast<const uint32_t*>(kv_norm)[tid];
-  uint32_t* crow = reinterpret_cast<uint32_t*>(ckv_cache + ((size_t)t * L + p) * kLora);
-  crow[tid] = pack2(x0 * rstd * __uint_as_float(g2 << 16),
-                    x1 * rstd * __uint_as_float(g2 & 0xffff0000u));
+  const uint32_t packed = pack2(x0 * rstd * __uint_as_float(g2 << 16),
+                                x1 * rstd * __uint_as_float(g2 & 0xffff0000u));
+  reinterpret_cast<uint32_t*>(ckv + ((size_t)t * L + p) * kLora)[tid] = packed;
+  uint16_t* tcol = ckvt + (((size_t)t * (L / 32) + (p >> 5)) * kLora + 2 * tid) * 32 +
+                   mla_kpos((int)(p & 31));
+  tcol[0] = (uint16_t)packed;
+  tcol[32] = (uint16_t)(packed >> 16);
   if (tid < kRope / 2) {
-    const float a = bf(kr[kLora + tid]), b = bf(kr[kLora + tid + kRope / 2]);
-    uint16_t* krow = kpe_cache + ((size_t)t * L + p) * kRope;
-    krow[tid] = f32_to_bf16_bits(a * cr[tid] - b * sr[tid]);
-    krow[tid + kRope / 2] = f32_to_bf16_bits(b * cr[tid] + a * sr[tid]);
+    const float cr = cos_t[p * (kRope / 2) + tid], sr = sin_t[p * (kRope / 2) + tid];
+    const float a = bf(kr[kLora + tid]), bb = bf(kr[kLora + tid + kRope / 2]);
+    uint16_t* krow = kpe + ((size_t)t * L + p) * kRope;
+    krow[tid] = f32_to_bf16_bits(a * cr - bb * sr);
+    krow[tid + kRope / 2] = f32_to_bf16_bits(bb * cr + a * sr);
   }
 }
 
-// grid (c, nh), kA threads.  Scores: each wave takes rows l = wave,
-// wave + W, ... four at a time (four independent 1 KB loads and reductions
-// in flight); the latent sum: each wave accumulates its rows (a lane owns 8
-// latent columns, 16-byte loads, four rows in flight) and the waves are
-// summed in LDS; the value projection: a thread owns 2 value columns and a
-// slice of the latent rows, eight rows of w_uv in flight.
-constexpr int kA = 1024;
-constexpr int kAW = kA / 64;
+// grid (c, kMlaSplit, nh / 16), 2 waves.  Split s of token t covers rows
+// [s * chunk, min(n, (s + 1) * chunk)) in steps of 32 rows: wave w scores
+// rows +16w .. +16w+15 for the 16 heads (A = cache rows, B = q from LDS),
+// the scores meet in LDS, both waves derive the same softmax state, and
+// wave w accumulates latent columns 256w .. 256w+255 of O (A = P, B = ckvt).
+constexpr int kMlaWaves = 2;
+constexpr int kMlaQRow = kLora + kRope + 8;  // LDS row of one head's q (padded)
 
-__global__ __launch_bounds__(kA) void mla_attend_kernel(
-    const float* __restrict__ q_lat, const float* __restrict__ q_pe,
-    const uint16_t* __restrict__ ckv_cache, const uint16_t* __restrict__ kpe_cache,
-    const uint16_t* __restrict__ w_uv, const int64_t* __restrict__ pos, int nh, int vh, int L,
-    float scale, uint16_t* __restrict__ out) {
-  __shared__ float s[kMaxL];
-  __shared__ float part[kAW][kLora];
-  __shared__ float ol[kLora];
-  __shared__ float red[kAW];
-  const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+__global__ __launch_bounds__(kMlaWaves * 64) void mla_partial_kernel(
+    const uint16_t* __restrict__ q_lat, const uint16_t* __restrict__ q_pe,
+    const uint16_t* __restrict__ ckv, const uint16_t* __restrict__ ckvt,
+    const uint16_t* __restrict__ kpe, const int64_t* __restrict__ pos, int nh, int L, float sl2,
+    float* __restrict__ part) {
+  __shared__ __align__(16) uint16_t qs[16 * kMlaQRow];
+  __shared__ float sc[kMlaStep][17];  // scores [row][head], log2 units
+  const int t = blockIdx.x, s = blockIdx.y, hg = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int R = lane & 15, g = lane >> 4;
+  // The 16 heads' [q_lat ; q_pe] (72 16-byte pieces per head) go out before
+  // the position is known; the first step's operands follow it, and q then
+  // goes to LDS.
+  constexpr int kPieces = 16 * 72 / (kMlaWaves * 64);
+  static_assert(kPieces * kMlaWaves * 64 == 16 * 72, "q pieces per thread");
+  u32x4_t qv[kPieces];
+#pragma unroll
+  for (int u = 0; u < kPieces; ++u) {
+    const int i = tid + u * kMlaWaves * 64, hh = i / 72, k = i % 72;
+    const size_t row = (size_t)t * nh + hg * 16 + hh;
+    qv[u] = k < 64 ? ldg16(q_lat + row * kLora + 8 * k) : ldg16(q_pe + row * kRope + 8 * (k - 64));
+  }
   const long long p = pos[t];
   if (p < 0 || p >= L) return;
   const int n = (int)p + 1;
-  const uint16_t* cb = ckv_cache + (size_t)t * L * kLora;
-  const uint16_t* kb = kpe_cache + (size_t)t * L * kRope;
-  float ql[8];
-  {
-    const float* qrow = q_lat + ((size_t)t * nh + h) * kLora + lane * 8;
+  const int chunk = mla_chunk(n);
+  const int r0 = s * chunk;
+  if (r0 >= n) return;
+  const int r1 = min(n, r0 + chunk);
+  const uint16_t* cb = ckv + (size_t)t * L * kLora;
+  const uint16_t* kb = kpe + (size_t)t * L * kRope;
+  const uint16_t* tb = ckvt + (size_t)t * L * kLora;
+  // A step's operands: a = the cache rows of this wave's score tile, vt =
+  // the step's ckvt block, column tiles 16w + i.
+  u32x4_t a[kLora / 32 + kRope / 32], vt[16];
+  auto load_step = [&](int b0) {
+    const int row = min(b0 + 16 * w + R, r1 - 1);
+    const uint16_t* ar = cb + (size_t)row * kLora + 8 * g;
+    const uint16_t* pr = kb + (size_t)row * kRope + 8 * g;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ql[j] = qrow[j];
+    for (int kk = 0; kk < kLora / 32; ++kk) a[kk] = ldg16(ar + 32 * kk);
+    a[kLora / 32] = ldg16(pr);
+    a[kLora / 32 + 1] = ldg16(pr + 32);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      vt[i] = ldg16(tb + ((size_t)(b0 >> 5) * kLora + 16 * (16 * w + i) + R) * 32 + 8 * g);
+  };
+  load_step(r0);
+#pragma unroll
+  for (int u = 0; u < kPieces; ++u) {
+    const int i = tid + u * kMlaWaves * 64, hh = i / 72, k = i % 72;
+    *reinterpret_cast<u32x4_t*>(&qs[hh * kMlaQRow + 8 * k]) = qv[u];
   }
-  const float qp = q_pe[((size_t)t * nh + h) * kRope + lane];
-  constexpr int U = 8;  // cache rows in flight per wave
-  float lmax = -INFINITY;
-  for (int l0 = wave; l0 < n; l0 += U * kAW) {
-    float dsum[U];
-    u32x4_t cv[U];
-    uint16_t kv[U];
+  f32x4_t o[16];  // o[i][r] = O[head 4g + r][column 16 * (16w + i) + R]
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int l = l0 + u * kAW;
-      const int lc = l < n ? l : 0;
-      cv[u] = *reinterpret_cast<const u32x4_t*>(cb + (size_t)lc * kLora + lane * 8);
-      kv[u] = kb[(size_t)lc * kRope + lane];
+  for (int i = 0; i < 16; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;  // head R's running max and sum
+  const uint16_t* qrow = &qs[R * kMlaQRow + 8 * g];
+  for (int b0 = r0; b0 < r1; b0 += kMlaStep) {
+    if (b0 + kMlaStep > r1) {
+      // rows past the last one hold whatever the cache held: zero them, so
+      // that a non-finite stale value cannot meet its zero weight
+      uint32_t keep[4];
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const int e = 2 * e2;
+        const int lo = b0 + (e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4));
+        keep[e2] = (lo < r1 ? 0x0000ffffu : 0u) | (lo + 1 < r1 ? 0xffff0000u : 0u);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) vt[i][e2] &= keep[e2];
+    }
+    __syncthreads();  // q is in LDS; the previous step's readers of sc are done
+    // two accumulation chains (even and odd K steps) halve the dependent
+    // product latency
+    f32x4_t sa0 = {0.f, 0.f, 0.f, 0.f}, sa1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < kLora / 32 + kRope / 32; kk += 2) {
+      sa0 = mfma16x16x32_bf16(a[kk], *reinterpret_cast<const u32x4_t*>(qrow + 32 * kk), sa0);
+      sa1 = mfma16x16x32_bf16(a[kk + 1], *reinterpret_cast<const u32x4_t*>(qrow + 32 * kk + 32),
+                              sa1);
+    }
+    const f32x4_t sacc = sa0 + sa1;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int rr = 16 * w + 4 * g + r;  // S^T[row 4g + r][head R] of the wave's tile
+      sc[rr][R] = b0 + rr < r1 ? sacc[r] * sl2 : -INFINITY;
+    }
+    __syncthreads();
+    // head R's step max over the 32 rows (lane group g reads rows 8g..8g+7)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, sc[8 * g + i][R]);
+    mx = rows4_max(mx);
+    const float mn = fmaxf(m, mx);  // finite: row b0 is in every step
+    const float f = __builtin_amdgcn_exp2f(m - mn);
+    // P in the K order of ckvt (A operand: head R, K group g) and its sum
+    u32x4_t pa;
+    float ps = 0.f;
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      float pv[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int e = 2 * e2 + u;
+        pv[u] = __builtin_amdgcn_exp2f(sc[e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4)][R] - mn);
+        ps += pv[u];
+      }
+      pa[e2] = pack2(pv[0], pv[1]);
+    }
+    ps = rows4_sum(ps);
+    l = l * f + ps;
+    m = mn;
+    if (b0 > r0) {
+      // o[i][r] is head 4g + r's: its factor comes from lane 4g + r (on the
+      // first step o is still zero)
+      float fr[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) fr[r] = __shfl(f, 4 * g + r);
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[i][r] *= fr[r];
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float c[8];
-      unpack8(cv[u], c);
-      float d = qp * bf(kv[u]);
+    for (int i = 0; i < 16; ++i) o[i] = mfma16x16x32_bf16(pa, vt[i], o[i]);
+    if (b0 + kMlaStep < r1) load_step(b0 + kMlaStep);
+  }
+  float* rec = part + (((size_t)t * kMlaSplit + s) * nh + hg * 16) * kMlaRec;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) d += ql[j] * c[j];
-      dsum[u] = d;
-    }
+  for (int i = 0; i < 16; ++i)
 #pragma unroll
-    for (int u = 0; u < U; ++u) dsum[u] = wave_sum(dsum[u]);
+    for (int r = 0; r < 4; ++r)
+      rec[(size_t)(4 * g + r) * kMlaRec + 4 + 16 * (16 * w + i) + R] = o[i][r];
+  if (w == 0 && g == 0) {
+    rec[(size_t)R * kMlaRec] = m;
+    rec[(size_t)R * kMlaRec + 1] = l;
+  }
+}
+
+// grid (c, nh, ceil(vh / 64)), kT threads: the splits of (token, head)
+// merged into the normalised latent output, then value columns 64z .. 64z+63
+// of out = o_lat . w_uv[h]: a thread owns 8 columns and 16 latent rows (lane
+// group and wave pick the rows), the 32 row groups meet in LDS.  Everything
+// whose address does not depend on the position goes out first: the w_uv
+// rows, every split's (max, sum) and the first 8 splits' partial sums (splits
+// past the position are never used, so whatever they hold is harmless:
+// they are selected away, not multiplied by 0).
+__global__ __launch_bounds__(kT) void mla_merge_kernel(const float* __restrict__ part,
+                                                       const uint16_t* __restrict__ w_uv,
+                                                       const int64_t* __restrict__ pos, int nh,
+                                                       int vh, int L, uint16_t* __restrict__ out) {
+  __shared__ float ol[kLora];
+  __shared__ float ws[kMlaSplit];
+  __shared__ float pq[32][64];
+  const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int c8 = lane & 7, jg = (lane >> 3) + 8 * wave;  // 32 row groups
+  const int v = 64 * blockIdx.z + 8 * c8;
+  const uint16_t* wv = w_uv + (size_t)h * kLora * vh + (v < vh ? v : 0);
+  u32x4_t wr[kLora / 32];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int l = l0 + u * kAW;
-      if (l < n) {
-        const float d = dsum[u] * scale;
-        if (lane == 0) s[l] = d;
-        lmax = fmaxf(lmax, d);
+  for (int u = 0; u < kLora / 32; ++u) wr[u] = ldg16(wv + (size_t)(jg + 32 * u) * vh);
+  const float* rec = part + ((size_t)t * kMlaSplit * nh + h) * kMlaRec;
+  const size_t sstride = (size_t)nh * kMlaRec;
+  static_assert(2 * kT == kLora, "two latent columns per thread");
+  f32x2_t pv[8];  // splits 0..7, columns 2 * tid, 2 * tid + 1
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    pv[u] = *reinterpret_cast<const f32x2_t*>(rec + u * sstride + 4 + 2 * tid);
+  float ms = -INFINITY, ls = 0.f;
+  if (tid < kMlaSplit) {
+    ms = rec[tid * sstride];
+    ls = rec[tid * sstride + 1];
+  }
+  const long long p = pos[t];
+  if (p < 0 || p >= L) return;
+  const int n = (int)p + 1;
+  const int chunk = mla_chunk(n);
+  const int na = (n + chunk - 1) / chunk;
+  if (tid < 64) {
+    const bool ok = tid < na;
+    const float M = wave_max(ok ? ms : -INFINITY);
+    const float e = ok ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
+    const float den = wave_sum(ok ? e * ls : 0.f);
+    if (tid < kMlaSplit) ws[tid] = e / den;
+  }
+  __syncthreads();
+  {
+    float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (u < na) {
+        v0 += ws[u] * pv[u][0];
+        v1 += ws[u] * pv[u][1];
       }
     }
-  }
-  // block max
-  lmax = wave_max(lmax);
-  if (lane == 0) red[wave] = lmax;
-  __syncthreads();
-  float m = -INFINITY;
-  for (int i = 0; i < kAW; ++i) m = fmaxf(m, red[i]);
-  __syncthreads();
-  float psum = 0.f;
-  for (int l = tid; l < n; l += kA) {
-    const float e = expf(s[l] - m);
-    s[l] = e;
-    psum += e;
-  }
-  psum = wave_sum(psum);
-  if (lane == 0) red[wave] = psum;
-  __syncthreads();
-  float tot = 0.f;
-  for (int i = 0; i < kAW; ++i) tot += red[i];
-  const float inv = 1.0f / tot;
-  float acc[8];
+    for (int s0 = 8; s0 < na; s0 += 8) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-  for (int l0 = wave; l0 < n; l0 += U * kAW) {
-    u32x4_t cv[U];
+      for (int u = 0; u < 8; ++u) {
+        const int sp = s0 + u < na ? s0 + u : 0;
+        pv[u] = *reinterpret_cast<const f32x2_t*>(rec + sp * sstride + 4 + 2 * tid);
+      }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int l = l0 + u * kAW;
-      cv[u] = *reinterpret_cast<const u32x4_t*>(cb + (size_t)(l < n ? l : 0) * kLora + lane * 8);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int l = l0 + u * kAW;
-      const float pl = l < n ? s[l] : 0.f;
-      float c[8];
-      unpack8(cv[u], c);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] += pl * c[j];
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) part[wave][lane * 8 + j] = acc[j];
-  __syncthreads();
-  for (int j = tid; j < kLora; j += kA) {
-    float v = 0.f;
-    for (int w = 0; w < kAW; ++w) v += part[w][j];
-    ol[j] = v * inv;
-  }
-  __syncthreads();
-  // out[v] = o_lat . w_uv[h][:, v]: thread = (column pair, slice of kAW rows' worth)
-  const uint16_t* wv = w_uv + (size_t)h * kLora * vh;
-  float* pq = &part[0][0];  // reused: [kAW][128] partial sums
-  constexpr int kRows = kLora / kAW;
-  for (int v0 = 0; v0 < vh; v0 += 128) {
-    const int vp = v0 + 2 * lane;
-    float a0 = 0.f, a1 = 0.f;
-    if (vp < vh) {
-      const uint16_t* col = wv + vp;
-      const int j0 = wave * kRows;
-      for (int j = j0; j < j0 + kRows; j += 8) {
-        uint32_t w8[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) w8[u] = *reinterpret_cast<const uint32_t*>(col + (size_t)(j + u) * vh);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          a0 += ol[j + u] * __uint_as_float(w8[u] << 16);
-          a1 += ol[j + u] * __uint_as_float(w8[u] & 0xffff0000u);
+      for (int u = 0; u < 8; ++u) {
+        if (s0 + u < na) {
+          v0 += ws[s0 + u] * pv[u][0];
+          v1 += ws[s0 + u] * pv[u][1];
         }
       }
     }
-    pq[wave * 128 + 2 * lane] = a0;
-    pq[wave * 128 + 2 * lane + 1] = a1;
-    __syncthreads();
-    if (tid < 128 && v0 + tid < vh) {
-      float v = 0.f;
-      for (int w = 0; w < kAW; ++w) v += pq[w * 128 + tid];
-      out[((size_t)t * nh + h) * vh + v0 + tid] = f32_to_bf16_bits(v);
-    }
-    __syncthreads();
+    ol[2 * tid] = v0;
+    ol[2 * tid + 1] = v1;
+  }
+  __syncthreads();
+  float acc[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc[k] = 0.f;
+#pragma unroll
+  for (int u = 0; u < kLora / 32; ++u) {
+    const float oj = ol[jg + 32 * u];
+    float wf[8];
+    unpack8(wr[u], wf);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] += oj * wf[k];
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) pq[jg][8 * c8 + k] = acc[k];
+  __syncthreads();
+  if (tid < 64 && 64 * (int)blockIdx.z + tid < vh) {
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) sum += pq[i][tid];
+    out[((size_t)t * nh + h) * vh + 64 * blockIdx.z + tid] = f32_to_bf16_bits(sum);
   }
 }
 
@@ -1052,41 +1195,48 @@ extern "C" int sluice_dec_gate_logits(const void* hn, const void* wg, const floa
   return (int)hipGetLastError();
 }
 
-extern "C" int sluice_dec_mla_prep(const void* q, int q_stride, const void* kva, int kva_stride,
-                                   const void* kv_norm, const void* w_uk, const float* cos_t,
-                                   const float* sin_t, const int64_t* pos, int c, int nh, int nope,
-                                   int rope, int lora, int L, float eps, float* q_lat, float* q_pe,
-                                   void* ckv_cache, void* kpe_cache, sluice_stream_t stream) {
-  if (c < 0 || nh <= 0 || nope <= 0 || nope > 256 || nope % 2 != 0 || rope != kRope ||
-      lora != kLora || L <= 0 || L > kMaxL || q_stride < nh * (nope + rope) ||
-      kva_stride < lora + rope || kva_stride % 2 != 0)
-    return SLUICE_E_INVAL;
-  if (((uintptr_t)kva | (uintptr_t)kv_norm | (uintptr_t)w_uk | (uintptr_t)ckv_cache) & 3)
-    return SLUICE_E_INVAL;
-  if (!q || !kva || !kv_norm || !w_uk || !cos_t || !sin_t || !pos || !q_lat || !q_pe ||
-      !ckv_cache || !kpe_cache)
-    return SLUICE_E_INVAL;
-  if (c == 0) return SLUICE_OK;
-  hipLaunchKernelGGL(mla_prep_kernel, dim3(c, nh + 1), dim3(kT), 0, (hipStream_t)stream,
-                     (const uint16_t*)q, (const uint16_t*)kva, (const uint16_t*)kv_norm,
-                     (const uint16_t*)w_uk, cos_t, sin_t, pos, nh, nope, q_stride, kva_stride, L,
-                     eps, q_lat, q_pe, (uint16_t*)ckv_cache, (uint16_t*)kpe_cache);
-  return (int)hipGetLastError();
+extern "C" size_t sluice_dec_mla_workspace(int c, int nh) {
+  if (c <= 0 || nh <= 0) return 0;
+  const size_t ql = (size_t)c * nh * (kLora + kRope) * sizeof(uint16_t);
+  return (ql + 255) / 256 * 256 + (size_t)c * kMlaSplit * nh * kMlaRec * sizeof(float);
 }
 
-extern "C" int sluice_dec_mla_attend(const float* q_lat, const float* q_pe, const void* ckv_cache,
-                                     const void* kpe_cache, const void* w_uv, const int64_t* pos,
-                                     int c, int nh, int rope, int lora, int vh, int L, float scale,
-                                     void* out, sluice_stream_t stream) {
-  if (c < 0 || nh <= 0 || rope != kRope || lora != kLora || vh <= 0 || vh > 256 || vh % 2 ||
-      L <= 0 || L > kMaxL)
+extern "C" int sluice_dec_mla_decode(const void* q, int q_stride, const void* kva,
+                                     int kva_stride, const void* kv_norm, const void* w_ukt,
+                                     const void* w_uv, const float* cos_t, const float* sin_t,
+                                     const int64_t* pos, int c, int nh, int nope, int rope,
+                                     int lora, int vh, int L, float eps, float scale,
+                                     void* ckv_cache, void* ckvt_cache, void* kpe_cache,
+                                     void* work, void* out, sluice_stream_t stream) {
+  if (c < 0 || c > 16 || nh <= 0 || nh % 16 != 0 || nope <= 0 || nope % 32 != 0 ||
+      rope != kRope || lora != kLora || vh <= 0 || vh > 256 || vh % 8 != 0 || L <= 0 ||
+      L > kMaxL || L % 32 != 0 || q_stride < nh * (nope + rope) || q_stride % 8 != 0 ||
+      kva_stride < lora + rope || kva_stride % 2 != 0)
     return SLUICE_E_INVAL;
-  if (!q_lat || !q_pe || !ckv_cache || !kpe_cache || !w_uv || !pos || !out) return SLUICE_E_INVAL;
-  if ((uintptr_t)ckv_cache & 15) return SLUICE_E_INVAL;
+  if (!q || !kva || !kv_norm || !w_ukt || !w_uv || !cos_t || !sin_t || !pos || !ckv_cache ||
+      !ckvt_cache || !kpe_cache || !work || !out)
+    return SLUICE_E_INVAL;
+  if ((((uintptr_t)q | (uintptr_t)w_ukt | (uintptr_t)w_uv | (uintptr_t)ckv_cache |
+        (uintptr_t)ckvt_cache | (uintptr_t)kpe_cache | (uintptr_t)work) & 15) != 0 ||
+      (((uintptr_t)kva | (uintptr_t)kv_norm) & 3) != 0)
+    return SLUICE_E_INVAL;
   if (c == 0) return SLUICE_OK;
-  hipLaunchKernelGGL(mla_attend_kernel, dim3(c, nh), dim3(kA), 0, (hipStream_t)stream, q_lat,
-                     q_pe, (const uint16_t*)ckv_cache, (const uint16_t*)kpe_cache,
-                     (const uint16_t*)w_uv, pos, nh, vh, L, scale, (uint16_t*)out);
+  hipStream_t st = (hipStream_t)stream;
+  uint16_t* q_lat = (uint16_t*)work;
+  uint16_t* q_pe = q_lat + (size_t)c * nh * kLora;
+  const size_t ql = (size_t)c * nh * (kLora + kRope) * sizeof(uint16_t);
+  float* part = (float*)((char*)work + (ql + 255) / 256 * 256);
+  hipLaunchKernelGGL(mla_absorb_kernel, dim3(nh * (kLora / 64) + c), dim3(kT), 0, st,
+                     (const uint16_t*)q, q_stride, (const uint16_t*)kva, kva_stride,
+                     (const uint16_t*)kv_norm, (const uint16_t*)w_ukt, cos_t, sin_t, pos, c, nh,
+                     nope, L, eps, q_lat, q_pe, (uint16_t*)ckv_cache, (uint16_t*)ckvt_cache,
+                     (uint16_t*)kpe_cache);
+  hipLaunchKernelGGL(mla_partial_kernel, dim3(c, kMlaSplit, nh / 16), dim3(kMlaWaves * 64), 0,
+                     st, q_lat,
+                     q_pe, (const uint16_t*)ckv_cache, (const uint16_t*)ckvt_cache,
+                     (const uint16_t*)kpe_cache, pos, nh, L, scale * 1.4426950408889634f, part);
+  hipLaunchKernelGGL(mla_merge_kernel, dim3(c, nh, (vh + 63) / 64), dim3(kT), 0, st, part,
+                     (const uint16_t*)w_uv, pos, nh, vh, L, (uint16_t*)out);
   return (int)hipGetLastError();
 }
 

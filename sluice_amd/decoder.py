@@ -325,12 +325,21 @@ def _randn(shape, gen, std, dev, dtype=torch.bfloat16):
     return (torch.randn(shape, generator=gen, device=dev) * std).to(dtype)
 
 
+def _mla_kslot(dev):
+    """Slot of row r of a 32-row block in the transposed latent cache (the
+    K order of the kernels' P . ckv product)."""
+    return torch.tensor([8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3) for r in range(32)],
+                        device=dev)
+
+
 class _MLA(nn.Module):
     """Multi-head latent attention (DeepSeek-V2), decode form with the
-    up-projections absorbed: one GEMM for [q ; kv latent + rope key], a prep
-    kernel (q absorption into the latent space, RoPE, latent RMSNorm, cache
-    write), an attention kernel over the latent cache (scores, softmax,
-    weighted latent sum, value up-projection) and the output GEMM."""
+    up-projections absorbed: one GEMM for [q ; kv latent + rope key], then
+    sluice_dec_mla_decode (q absorption into the latent space and the new
+    cache rows; scores, softmax and the weighted latent sum over row splits
+    on the matrix cores; merge and value up-projection) and the output
+    GEMM.  The latent cache is kept row-major and, for the P . ckv product,
+    transposed in 32-row blocks (ckvt)."""
 
     def __init__(self, sp, batch, max_len, dev, gen):
         super().__init__()
@@ -341,36 +350,41 @@ class _MLA(nn.Module):
         self.w_qkva = _randn((self.nq + lora + rope, H), gen, 0.02, dev)
         self.kv_norm = torch.ones(lora, device=dev, dtype=torch.bfloat16)
         self.w_uk = _randn((nh, nope, lora), gen, 0.02, dev)
+        self.w_ukt = self.w_uk.transpose(1, 2).contiguous()
         self.w_uv = _randn((nh, lora, vh), gen, 0.02, dev)
         self.wo = _randn((H, nh * vh), gen, 0.02, dev)
+        if max_len % 32:
+            raise ValueError(f"MLA cache length {max_len} is not a multiple of 32")
         self.ckv = torch.zeros((batch, max_len, lora), device=dev, dtype=torch.bfloat16)
+        self.ckvt = torch.zeros((batch, max_len // 32, lora, 32), device=dev, dtype=torch.bfloat16)
         self.kpe = torch.zeros((batch, max_len, rope), device=dev, dtype=torch.bfloat16)
         self.scale = (nope + rope) ** -0.5
         self.L = max_len
+        self._work = {}
 
     def fill_prompt(self, n, gen):
-        b, _, lora = self.ckv.shape
+        b, L, lora = self.ckv.shape
         self.ckv[:, :n] = _randn((b, n, lora), gen, 1.0, self.ckv.device)
         self.kpe[:, :n] = _randn((b, n, self.rope), gen, 1.0, self.ckv.device)
+        self.ckvt[..., _mla_kslot(self.ckv.device)] = self.ckv.view(b, L // 32, 32, lora).transpose(2, 3)
 
     def forward(self, hn, pos, cos_t, sin_t):
         lib, check = _k()
         c = hn.shape[0]
         qkva = linear(hn, self.w_qkva)
-        st = _stream(hn)
-        q_lat = torch.empty((c, self.nh, self.lora), dtype=torch.float32, device=hn.device)
-        q_pe = torch.empty((c, self.nh, self.rope), dtype=torch.float32, device=hn.device)
+        work = self._work.get(c)
+        if work is None:  # fixed per batch size, so captured graphs keep it
+            work = self._work[c] = torch.empty(
+                int(lib.sluice_dec_mla_workspace(c, self.nh)), dtype=torch.uint8,
+                device=hn.device)
         row = qkva.shape[1]
-        check(lib.sluice_dec_mla_prep(
-            qkva.data_ptr(), row, qkva.data_ptr() + self.nq * 2, row, self.kv_norm.data_ptr(),
-            self.w_uk.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(), pos.data_ptr(), c, self.nh,
-            self.nope, self.rope, self.lora, self.L, _EPS, q_lat.data_ptr(), q_pe.data_ptr(),
-            self.ckv.data_ptr(), self.kpe.data_ptr(), st), "sluice_dec_mla_prep")
         o = torch.empty((c, self.nh * self.vh), dtype=hn.dtype, device=hn.device)
-        check(lib.sluice_dec_mla_attend(
-            q_lat.data_ptr(), q_pe.data_ptr(), self.ckv.data_ptr(), self.kpe.data_ptr(),
-            self.w_uv.data_ptr(), pos.data_ptr(), c, self.nh, self.rope, self.lora, self.vh,
-            self.L, float(self.scale), o.data_ptr(), st), "sluice_dec_mla_attend")
+        check(lib.sluice_dec_mla_decode(
+            qkva.data_ptr(), row, qkva.data_ptr() + self.nq * 2, row, self.kv_norm.data_ptr(),
+            self.w_ukt.data_ptr(), self.w_uv.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(),
+            pos.data_ptr(), c, self.nh, self.nope, self.rope, self.lora, self.vh, self.L, _EPS,
+            float(self.scale), self.ckv.data_ptr(), self.ckvt.data_ptr(), self.kpe.data_ptr(),
+            work.data_ptr(), o.data_ptr(), _stream(hn)), "sluice_dec_mla_decode")
         return linear(o, self.wo)
 
 
@@ -622,7 +636,8 @@ class SyntheticDecoder:
             sp["layers"] = layers
         self.name = spec
         dev = self.dev = device or torch.device("cuda", torch.cuda.current_device())
-        self.max_batch, self.max_len = max_batch, prompt_len + gen_len + 8
+        # (a multiple of 32: the MLA latent cache is also kept in 32-row blocks)
+        self.max_batch, self.max_len = max_batch, (prompt_len + gen_len + 8 + 31) // 32 * 32
         self.prompt_len = prompt_len
         g = torch.Generator(device=dev).manual_seed(seed)
         H = sp["H"]

@@ -1,7 +1,7 @@
 """Kernels of the synthetic decoders (include/sluice_decoder.h) against plain
 float32 torch references of the same math, computed on the CPU from the same
 bf16 inputs: residual add + RMSNorm, SwiGLU activation, router logits, MLA
-and GQA decode attention."""
+and GQA decode attention (with their cache layouts)."""
 
 import numpy as np
 import pytest
@@ -197,10 +197,15 @@ def _tables(L, d, theta):
     return ang.cos().contiguous(), ang.sin().contiguous()
 
 
+def _mla_kpos(r):
+    return 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3)
+
+
 @pytest.mark.parametrize("L,positions,vh", [(64, [5, 0, 63, 31], 128),
                                             (512, [300, 1, 511, 130], 128),
-                                            (256, [200, 17, 255, 64], 192)])
-def test_mla_prep_and_attend(L, positions, vh):
+                                            (256, [200, 17, 255, 64], 192),
+                                            (4096, [4095, 2047, 64, 700], 128)])
+def test_mla_decode(L, positions, vh):
     lib, check = _lib()
     c, nh, nope, rope, lora = 4, 16, 128, 64, 512
     g = torch.Generator().manual_seed(11 + L)
@@ -214,22 +219,23 @@ def test_mla_prep_and_attend(L, positions, vh):
     pos = torch.tensor(positions, dtype=torch.long)
     cos_t, sin_t = _tables(L, rope, 1e4)
     scale = (nope + rope) ** -0.5
-    d = {k: v.to(DEV) for k, v in dict(qkva=qkva, kv_norm=kv_norm, w_uk=w_uk, w_uv=w_uv,
-                                       ckv=ckv.clone(), kpe=kpe.clone(), pos=pos, cos=cos_t,
-                                       sin=sin_t).items()}
-    q_lat = torch.empty((c, nh, lora), dtype=torch.float32, device=DEV)
-    q_pe = torch.empty((c, nh, rope), dtype=torch.float32, device=DEV)
+    # the transposed latent cache: [c, L/32, lora, 32]
+    kslot = torch.tensor([_mla_kpos(r) for r in range(32)])
+    ckvt = torch.empty((c, L // 32, lora, 32), dtype=torch.bfloat16)
+    ckvt[..., kslot] = ckv.view(c, L // 32, 32, lora).transpose(2, 3)
+    d = {k: v.to(DEV) for k, v in dict(qkva=qkva, kv_norm=kv_norm,
+                                       w_ukt=w_uk.transpose(1, 2).contiguous(), w_uv=w_uv,
+                                       ckv=ckv.clone(), ckvt=ckvt, kpe=kpe.clone(), pos=pos,
+                                       cos=cos_t, sin=sin_t).items()}
     out = torch.empty((c, nh * vh), dtype=torch.bfloat16, device=DEV)
+    work = torch.empty(int(lib.sluice_dec_mla_workspace(c, nh)), dtype=torch.uint8, device=DEV)
     row = qkva.shape[1]
-    check(lib.sluice_dec_mla_prep(
+    check(lib.sluice_dec_mla_decode(
         d["qkva"].data_ptr(), row, d["qkva"].data_ptr() + nq * 2, row, d["kv_norm"].data_ptr(),
-        d["w_uk"].data_ptr(), d["cos"].data_ptr(), d["sin"].data_ptr(), d["pos"].data_ptr(), c, nh,
-        nope, rope, lora, L, 1e-6, q_lat.data_ptr(), q_pe.data_ptr(), d["ckv"].data_ptr(),
-        d["kpe"].data_ptr(), _st()), "mla_prep")
-    check(lib.sluice_dec_mla_attend(
-        q_lat.data_ptr(), q_pe.data_ptr(), d["ckv"].data_ptr(), d["kpe"].data_ptr(),
-        d["w_uv"].data_ptr(), d["pos"].data_ptr(), c, nh, rope, lora, vh, L, scale,
-        out.data_ptr(), _st()), "mla_attend")
+        d["w_ukt"].data_ptr(), d["w_uv"].data_ptr(), d["cos"].data_ptr(), d["sin"].data_ptr(),
+        d["pos"].data_ptr(), c, nh, nope, rope, lora, vh, L, 1e-6, scale, d["ckv"].data_ptr(),
+        d["ckvt"].data_ptr(), d["kpe"].data_ptr(), work.data_ptr(), out.data_ptr(), _st()),
+        "mla_decode")
     torch.cuda.synchronize()
     ck, kp = ckv.clone(), kpe.clone()
     for t in range(c):
@@ -237,7 +243,6 @@ def test_mla_prep_and_attend(L, positions, vh):
         q = qkva[t, :nq].float().view(nh, nope + rope)
         qn, qp = q[:, :nope], _rope(q[:, nope:], cos_t[p], sin_t[p])
         ql = torch.bmm(qn[:, None, :], w_uk.float())[:, 0]
-        assert _rel(q_lat[t], ql) <= 1e-5 and _rel(q_pe[t], qp) <= 1e-5
         kv = qkva[t, nq:].float()
         ck[t, p] = _rms(kv[:lora], kv_norm.float()).bfloat16()
         kp[t, p] = _rope(kv[lora:], cos_t[p], sin_t[p]).bfloat16()
@@ -252,6 +257,26 @@ def test_mla_prep_and_attend(L, positions, vh):
     mask = torch.ones((c, L), dtype=torch.bool)
     mask[torch.arange(c), pos] = False
     assert torch.equal(d["ckv"].cpu()[mask], ckv[mask])
+    # the transposed copy holds exactly the row-major cache, new rows included
+    got = d["ckvt"].cpu()[..., kslot].transpose(2, 3).reshape(c, L, lora)
+    assert torch.equal(got, d["ckv"].cpu())
+
+
+def test_mla_decode_rejects_bad_shapes():
+    lib, _ = _lib()
+    x = torch.zeros(1 << 16, dtype=torch.uint8, device=DEV)
+    p = x.data_ptr()
+    args = dict(q=p, q_stride=3648, kva=p, kva_stride=3648, kv_norm=p, w_ukt=p, w_uv=p,
+                cos=p, sin=p, pos=p, c=1, nh=16, nope=128, rope=64, lora=512, vh=128, L=64,
+                eps=1e-6, scale=0.1, ckv=p, ckvt=p, kpe=p, work=p, out=p)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return lib.sluice_dec_mla_decode(*a.values(), _st())
+
+    for bad in (dict(nh=8), dict(vh=100), dict(L=48), dict(c=17), dict(nope=48),
+                dict(lora=256), dict(rope=32), dict(q=p + 8)):
+        assert call(**bad) != 0, bad
 
 
 @pytest.mark.parametrize("L,positions", [(48, [7, 47, 0]), (600, [300, 599, 129]),
