@@ -63,6 +63,18 @@ int sluice_dec_gate_logits(const void* hn, const void* wg, const float* bias_tab
                            const int64_t* step, int n_steps, int bias_rows, int rows, int H, int E,
                            float* out, sluice_stream_t stream);
 
+/* Residual add + RMSNorm + router logits in one launch:
+ *   x_out = bf16(x + delta) (x when delta is NULL), hn_out = bf16(rmsnorm(x_out) * w)
+ *   (bit-identical to sluice_dec_add_rmsnorm), logits as sluice_dec_gate_logits
+ *   computes them from hn_out (bit-identical when H == 2048).  x_out must not
+ *   alias x.  Shapes it takes: sluice_dec_add_rmsnorm_gate_ok(rows, H) != 0
+ *   (H % 8 == 0, H <= 8192, rows <= 16); pointers 16-byte aligned. */
+int sluice_dec_add_rmsnorm_gate_ok(int rows, int H);
+int sluice_dec_add_rmsnorm_gate(const void* x, const void* delta, const void* w, void* x_out,
+                                void* hn_out, const void* wg, const float* bias_table,
+                                const int64_t* step, int n_steps, int bias_rows, int rows, int H,
+                                int E, float eps, float* logits, sluice_stream_t stream);
+
 /* MLA decode (DeepSeek-V2 latent attention with absorbed up-projections) on
  * the matrix cores, three launches (q absorption + new cache rows, row splits
  * of the attention, merge + value up-projection):

@@ -259,6 +259,106 @@ __global__ __launch_bounds__(kT) void gate_logits_kernel(
 }
 
 
+// Residual add + RMSNorm + router logits in one launch, for the MoE layers'
+// second norm.  grid (rows, ceil(E / EPW)): workgroup (t, b) normalises row
+// t (the same per-thread element order and reductions as
+// add_rmsnorm_reg_kernel, so hn is bit-identical to it) and takes experts
+// EPW*b .. EPW*b + EPW-1 of that row (the same element order as
+// gate_logits_kernel when H == 2048).  Workgroup (t, 0) writes the row's new
+// residual to x_out (x is read by every workgroup of the row) and hn.
+// H <= NI * 2048.
+template <int NI, int EPW>
+__global__ __launch_bounds__(kT) void add_rmsnorm_gate_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ delta,
+    const uint16_t* __restrict__ w, uint16_t* __restrict__ x_out, uint16_t* __restrict__ hn_out,
+    const uint16_t* __restrict__ wg, const float* __restrict__ bias_table,
+    const int64_t* __restrict__ step, int n_steps, int bias_rows, int H, int E, float eps,
+    float* __restrict__ logits) {
+  __shared__ float red[kT / 64][EPW + 1];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int t = blockIdx.x, e0 = blockIdx.y * EPW;
+  const uint16_t* xr = x + (size_t)t * H;
+  const uint16_t* dr = delta != nullptr ? delta + (size_t)t * H : nullptr;
+  u32x4_t xv[NI], dv[NI], wv[NI], gv[EPW][NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int i = tid * 8 + j * kT * 8;
+    const int ic = i < H ? i : 0;
+    xv[j] = ldg16(xr + ic);
+    wv[j] = ldg16(w + ic);
+    if (dr != nullptr) dv[j] = ldg16(dr + ic);
+#pragma unroll
+    for (int u = 0; u < EPW; ++u) {
+      const int e = e0 + u < E ? e0 + u : E - 1;
+      gv[u][j] = ldg16(wg + (size_t)e * H + ic);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    if (tid * 8 + j * kT * 8 < H) {
+      if (dr != nullptr) {
+        float v[8], d[8];
+        unpack8(xv[j], v);
+        unpack8(dv[j], d);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xv[j][q] = pack2(v[2 * q] + d[2 * q], v[2 * q + 1] + d[2 * q + 1]);
+      }
+      float v[8];
+      unpack8(xv[j], v);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) ss += v[q] * v[q];
+    }
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave][EPW] = ss;
+  __syncthreads();
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < kT / 64; ++i) sum += red[i][EPW];
+  const float rstd = rsqrtf(sum / (float)H + eps);
+  float acc[EPW];
+#pragma unroll
+  for (int u = 0; u < EPW; ++u) acc[u] = 0.f;
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int i = tid * 8 + j * kT * 8;
+    if (i >= H) continue;
+    float v[8], g[8];
+    unpack8(xv[j], v);
+    unpack8(wv[j], g);
+    u32x4_t o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      o[q] = pack2(v[2 * q] * rstd * g[2 * q], v[2 * q + 1] * rstd * g[2 * q + 1]);
+    if (blockIdx.y == 0) {
+      *reinterpret_cast<u32x4_t*>(x_out + (size_t)t * H + i) = xv[j];
+      *reinterpret_cast<u32x4_t*>(hn_out + (size_t)t * H + i) = o;
+    }
+    float hv[8];
+    unpack8(o, hv);
+#pragma unroll
+    for (int u = 0; u < EPW; ++u) {
+      float gw[8];
+      unpack8(gv[u][j], gw);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[u] += gw[q] * hv[q];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < EPW; ++u) {
+    const float v = wave_sum(acc[u]);
+    if (lane == 0) red[wave][u] = v;
+  }
+  __syncthreads();
+  if (tid < EPW) {
+    const int e = e0 + tid;
+    if (e < E)
+      logits[(size_t)t * E + e] = gate_finish(red[0][tid], red[1][tid], red[2][tid], red[3][tid],
+                                              bias_table, step, n_steps, bias_rows, t, e, E);
+  }
+}
+
 // Row buckets of the gate kernel: rows <= MAXR loaded per step.
 template <typename F>
 void with_row_bucket(int rows, F f) {
@@ -1192,6 +1292,48 @@ extern "C" int sluice_dec_gate_logits(const void* hn, const void* wg, const floa
                        (const uint16_t*)hn, (const uint16_t*)wg, bias_table, step, n_steps,
                        bias_rows, rows, H, E, out);
   });
+  return (int)hipGetLastError();
+}
+
+// Experts per workgroup of the fused norm + router kernel: 4 measured
+// faster than 8 or 16 in replayed graphs (more workgroups, each shorter).
+constexpr int kNormGateEpw = 4;
+
+extern "C" int sluice_dec_add_rmsnorm_gate_ok(int rows, int H) {
+  return rows >= 0 && rows <= kMaxRows && H > 0 && H % 8 == 0 && H <= 4 * kT * 8;
+}
+
+extern "C" int sluice_dec_add_rmsnorm_gate(const void* x, const void* delta, const void* w,
+                                          void* x_out, void* hn_out, const void* wg,
+                                          const float* bias_table, const int64_t* step,
+                                          int n_steps, int bias_rows, int rows, int H, int E,
+                                          float eps, float* logits, sluice_stream_t stream) {
+  if (!sluice_dec_add_rmsnorm_gate_ok(rows, H) || E <= 0 || !x || !w || !x_out || !hn_out || !wg ||
+      !logits)
+    return SLUICE_E_INVAL;
+  if (bias_table != nullptr && (step == nullptr || n_steps <= 0 || bias_rows < rows))
+    return SLUICE_E_INVAL;
+  if (((uintptr_t)x | (uintptr_t)delta | (uintptr_t)w | (uintptr_t)x_out | (uintptr_t)hn_out |
+       (uintptr_t)wg) & 15)
+    return SLUICE_E_INVAL;
+  if (rows == 0) return SLUICE_OK;
+  constexpr int EPW = kNormGateEpw;
+  const dim3 grid(rows, (E + EPW - 1) / EPW);
+  hipStream_t st = (hipStream_t)stream;
+  auto go = [&](auto ni) {
+    constexpr int NI = decltype(ni)::value;
+    hipLaunchKernelGGL((add_rmsnorm_gate_kernel<NI, EPW>), grid, dim3(kT), 0, st,
+                       (const uint16_t*)x, (const uint16_t*)delta, (const uint16_t*)w,
+                       (uint16_t*)x_out, (uint16_t*)hn_out, (const uint16_t*)wg, bias_table, step,
+                       n_steps, bias_rows, H, E, eps, logits);
+  };
+  const int ni = (H + kT * 8 - 1) / (kT * 8);
+  if (ni <= 1)
+    go(std::integral_constant<int, 1>{});
+  else if (ni <= 2)
+    go(std::integral_constant<int, 2>{});
+  else
+    go(std::integral_constant<int, 4>{});
   return (int)hipGetLastError();
 }
 

@@ -560,6 +560,26 @@ class _StoreMoELayer(nn.Module):
             self.H, self.E, out.data_ptr(), _stream(hn)), "sluice_dec_gate_logits")
         return out
 
+    def norm_logits(self, x, delta, w):
+        """(x_out, hn, logits): the residual add, the RMSNorm before this layer
+        and its router logits in one kernel (x_out = x + delta, hn =
+        rmsnorm(x_out) * w, as add_rmsnorm computes them), or None when the
+        batch shape is one the fused kernel does not take."""
+        lib, check = _k()
+        T = x.shape[0]
+        if not lib.sluice_dec_add_rmsnorm_gate_ok(T, self.H):
+            return None
+        x_out, hn = torch.empty_like(x), torch.empty_like(x)
+        out = torch.empty((T, self.E), dtype=torch.float32, device=x.device)
+        rb = self.routing_bias
+        check(lib.sluice_dec_add_rmsnorm_gate(
+            x.data_ptr(), None if delta is None else delta.data_ptr(), w.data_ptr(),
+            x_out.data_ptr(), hn.data_ptr(), self.gate.weight.data_ptr(),
+            None if rb is None else rb.table.data_ptr(), None if rb is None else rb.step.data_ptr(),
+            0 if rb is None else rb.table.shape[0], 0 if rb is None else rb.table.shape[1], T,
+            self.H, self.E, _EPS, out.data_ptr(), _stream(x)), "sluice_dec_add_rmsnorm_gate")
+        return x_out, hn, out
+
     def select(self, lg):
         sp = self.sp
         return ops.select_experts(lg, sp["k"], scoring=sp["scoring"], renormalize=sp["renorm"],
@@ -743,7 +763,12 @@ class SyntheticDecoder:
         if blk.attn is not None:
             hn = add_rmsnorm(x, io["delta"], blk.n1)
             io["delta"] = blk.attn(hn, st.pos, self.cos_tbl, self.sin_tbl)
-        io["hn"] = add_rmsnorm(x, io["delta"], blk.n2)
+        fused = blk.moe.norm_logits(x, io["delta"], blk.n2) if blk.moe is not None else None
+        if fused is not None:
+            # a MoE layer's norm and router logits in one kernel
+            io["x"], io["hn"], io["lg"] = fused
+        else:
+            io["hn"] = add_rmsnorm(x, io["delta"], blk.n2)
         io["delta"] = None
 
     def _to_next_gap(self, i, io, st):
@@ -757,7 +782,8 @@ class SyntheticDecoder:
                 io["delta"] = blk.mlp(io["hn"])
                 i += 1
                 continue
-            tw, ti = blk.moe.select(blk.moe.logits(io["hn"]))
+            lg = io.pop("lg", None)
+            tw, ti = blk.moe.select(lg if lg is not None else blk.moe.logits(io["hn"]))
             io.update(tw=tw, ti=ti, i=i)
             return i
         hf = add_rmsnorm(io["x"], io["delta"], self.final_norm)

@@ -82,3 +82,9 @@ def test_workspace_size_is_monotone(lib):
     c = lib.sluice_fused_experts_workspace(8, 2048, 1408, 6, 2816)
     assert 0 < a < b < c
     assert lib.sluice_moe_plan_ints(8, 6) == 4 + 18 * 48 + 48
+
+
+def test_add_rmsnorm_gate_shapes(lib):
+    ok = lib.sluice_dec_add_rmsnorm_gate_ok
+    assert ok(16, 2048) and ok(16, 7168) and ok(1, 8192) and not ok(1, 8200)
+    assert not ok(17, 2048) and not ok(4, 2044)

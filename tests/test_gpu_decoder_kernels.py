@@ -91,6 +91,55 @@ def test_gate_logits(rows, H, E, bias):
     assert torch.allclose(out.cpu(), ref, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("rows,H,E,delta,bias", [(8, 2048, 128, True, True),
+                                                 (1, 2048, 64, True, False),
+                                                 (12, 2048, 128, False, True),
+                                                 (16, 2048, 60, True, True),
+                                                 (8, 4096, 256, True, True),
+                                                 (12, 7168, 256, True, True),
+                                                 (3, 2560, 7, True, False)])
+def test_add_rmsnorm_gate_matches_the_two_kernels(rows, H, E, delta, bias):
+    """The fused norm + router logits against add_rmsnorm then gate_logits:
+    hn and the residual bit for bit; logits bit for bit at H == 2048 (same
+    element order), to fp32 rounding otherwise."""
+    from sluice_amd.decoder import add_rmsnorm
+
+    lib, check = _lib()
+    assert lib.sluice_dec_add_rmsnorm_gate_ok(rows, H)
+    g = torch.Generator().manual_seed(rows * 7 + H + E)
+    x = torch.randn((rows, H), generator=g).bfloat16()
+    dl = torch.randn((rows, H), generator=g).bfloat16() if delta else None
+    w = (1 + 0.1 * torch.randn(H, generator=g)).bfloat16()
+    wg = (0.02 * torch.randn((E, H), generator=g)).bfloat16()
+    steps, brow = 5, 16
+    table = torch.randn((steps, brow, E), generator=g)
+    step = torch.tensor(7, dtype=torch.long)
+    d = {k: v.to(DEV) for k, v in dict(x=x, w=w, wg=wg, table=table, step=step).items()}
+    dd = dl.to(DEV) if delta else None
+    x_out, hn = torch.empty_like(d["x"]), torch.empty_like(d["x"])
+    lg = torch.empty((rows, E), dtype=torch.float32, device=DEV)
+    bargs = ((d["table"].data_ptr(), d["step"].data_ptr(), steps, brow) if bias
+             else (None, None, 0, 0))
+    check(lib.sluice_dec_add_rmsnorm_gate(
+        d["x"].data_ptr(), dd.data_ptr() if delta else None, d["w"].data_ptr(), x_out.data_ptr(),
+        hn.data_ptr(), d["wg"].data_ptr(), *bargs, rows, H, E, 1e-6, lg.data_ptr(), _st()),
+        "add_rmsnorm_gate")
+    # the two-kernel path on a copy of x
+    x2 = d["x"].clone()
+    hn2 = add_rmsnorm(x2, dd, d["w"])
+    lg2 = torch.empty_like(lg)
+    check(lib.sluice_dec_gate_logits(hn2.data_ptr(), d["wg"].data_ptr(), *bargs, rows, H, E,
+                                     lg2.data_ptr(), _st()), "gate_logits")
+    torch.cuda.synchronize()
+    assert torch.equal(d["x"].cpu(), x)  # x itself is not written
+    assert torch.equal(x_out.cpu(), x2.cpu())
+    assert torch.equal(hn.cpu(), hn2.cpu())
+    if H == 2048:
+        assert torch.equal(lg.cpu(), lg2.cpu())
+    else:
+        assert torch.allclose(lg.cpu(), lg2.cpu(), rtol=1e-5, atol=1e-5)
+
+
 @pytest.mark.parametrize("T,N,K", [(8, 3648, 2048), (1, 2048, 10944), (12, 5632, 2048),
                                    (16, 160, 128), (5, 176, 192), (8, 576, 2048)])
 def test_linear(T, N, K):
