@@ -45,6 +45,13 @@ int sluice_dec_linear(const void* x, const void* w, int T, int N, int K, void* y
  * w [N, K] holds N/2 gate rows then N/2 up rows; y [T, N/2] =
  * bf16(silu(x . w_gate^T) * (x . w_up^T)).  N % 32 == 0; workspace as for
  * sluice_dec_linear. */
+/* The plain projection left as its K parts: parts [ks, T, N] fp32 (row-major,
+ * 16-byte aligned), ks = sluice_dec_linear_split_parts(T, N, K) (>= 1, 0 for
+ * a shape it does not take); bf16(sum of the parts in order) equals what
+ * sluice_dec_linear writes. */
+int sluice_dec_linear_split_parts(int T, int N, int K);
+int sluice_dec_linear_split(const void* x, const void* w, int T, int N, int K, float* parts,
+                            sluice_stream_t stream);
 int sluice_dec_linear_glu(const void* x, const void* w, int T, int N, int K, void* y,
                           void* workspace, sluice_stream_t stream);
 
@@ -66,12 +73,16 @@ int sluice_dec_gate_logits(const void* hn, const void* wg, const float* bias_tab
 /* Residual add + RMSNorm + router logits in one launch:
  *   x_out = bf16(x + delta) (x when delta is NULL), hn_out = bf16(rmsnorm(x_out) * w)
  *   (bit-identical to sluice_dec_add_rmsnorm), logits as sluice_dec_gate_logits
- *   computes them from hn_out (bit-identical when H == 2048).  x_out must not
+ *   computes them from hn_out (bit-identical when H == 2048).  The delta may
+ *   instead come as delta_parts [n_parts, rows, H] fp32 (n_parts <= 4, delta
+ *   NULL): delta = bf16(sum of the parts in order), as sluice_dec_linear_split
+ *   leaves a projection.  x_out must not
  *   alias x.  Shapes it takes: sluice_dec_add_rmsnorm_gate_ok(rows, H) != 0
  *   (H % 8 == 0, H <= 8192, rows <= 16); pointers 16-byte aligned. */
 int sluice_dec_add_rmsnorm_gate_ok(int rows, int H);
-int sluice_dec_add_rmsnorm_gate(const void* x, const void* delta, const void* w, void* x_out,
-                                void* hn_out, const void* wg, const float* bias_table,
+int sluice_dec_add_rmsnorm_gate(const void* x, const void* delta, const float* delta_parts,
+                                int n_parts, const void* w, void* x_out, void* hn_out,
+                                const void* wg, const float* bias_table,
                                 const int64_t* step, int n_steps, int bias_rows, int rows, int H,
                                 int E, float eps, float* logits, sluice_stream_t stream);
 

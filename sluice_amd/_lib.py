@@ -107,8 +107,11 @@ SIGNATURES = {
     "sluice_dec_add_rmsnorm_gate_ok": (c_int, [c_int, c_int]),
     "sluice_dec_add_rmsnorm_gate": (
         c_int,
-        [_P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P],
+        [_P, _P, _P, c_int, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_float, _P,
+         _P],
     ),
+    "sluice_dec_linear_split_parts": (c_int, [c_int, c_int, c_int]),
+    "sluice_dec_linear_split": (c_int, [_P, _P, c_int, c_int, c_int, _P, _P]),
     "sluice_dec_gate_logits": (
         c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, _P]
     ),

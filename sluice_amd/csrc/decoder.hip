@@ -259,6 +259,8 @@ __global__ __launch_bounds__(kT) void gate_logits_kernel(
 }
 
 
+constexpr int kMaxDeltaParts = 4;  // K parts of a projection the fused norm sums
+
 // Residual add + RMSNorm + router logits in one launch, for the MoE layers'
 // second norm.  grid (rows, ceil(E / EPW)): workgroup (t, b) normalises row
 // t (the same per-thread element order and reductions as
@@ -270,6 +272,7 @@ __global__ __launch_bounds__(kT) void gate_logits_kernel(
 template <int NI, int EPW>
 __global__ __launch_bounds__(kT) void add_rmsnorm_gate_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ delta,
+    const float* __restrict__ dparts, int nparts,
     const uint16_t* __restrict__ w, uint16_t* __restrict__ x_out, uint16_t* __restrict__ hn_out,
     const uint16_t* __restrict__ wg, const float* __restrict__ bias_table,
     const int64_t* __restrict__ step, int n_steps, int bias_rows, int H, int E, float eps,
@@ -280,6 +283,7 @@ __global__ __launch_bounds__(kT) void add_rmsnorm_gate_kernel(
   const uint16_t* xr = x + (size_t)t * H;
   const uint16_t* dr = delta != nullptr ? delta + (size_t)t * H : nullptr;
   u32x4_t xv[NI], dv[NI], wv[NI], gv[EPW][NI];
+  f32x4_t pv[kMaxDeltaParts][NI][2];
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
     const int i = tid * 8 + j * kT * 8;
@@ -287,11 +291,36 @@ __global__ __launch_bounds__(kT) void add_rmsnorm_gate_kernel(
     xv[j] = ldg16(xr + ic);
     wv[j] = ldg16(w + ic);
     if (dr != nullptr) dv[j] = ldg16(dr + ic);
+    if (dparts != nullptr) {
+      // a projection's K parts [nparts][rows][H] (fp32): delta = bf16(sum in part order)
+#pragma unroll
+      for (int q = 0; q < kMaxDeltaParts; ++q) {
+        const float* src = dparts + ((size_t)(q < nparts ? q : 0) * gridDim.x + t) * H + ic;
+        pv[q][j][0] = *reinterpret_cast<const f32x4_t*>(src);
+        pv[q][j][1] = *reinterpret_cast<const f32x4_t*>(src + 4);
+      }
+    }
 #pragma unroll
     for (int u = 0; u < EPW; ++u) {
       const int e = e0 + u < E ? e0 + u : E - 1;
       gv[u][j] = ldg16(wg + (size_t)e * H + ic);
     }
+  }
+  if (dparts != nullptr) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+      for (int q = 0; q < kMaxDeltaParts; ++q) {
+        if (q < nparts) {
+          s0 += pv[q][j][0];
+          s1 += pv[q][j][1];
+        }
+      }
+      dv[j] = u32x4_t{pack2(s0[0], s0[1]), pack2(s0[2], s0[3]), pack2(s1[0], s1[1]),
+                      pack2(s1[2], s1[3])};
+    }
+    dr = xr;  // (any non-null pointer: the delta is in dv)
   }
   float ss = 0.f;
 #pragma unroll
@@ -1027,7 +1056,8 @@ __device__ __forceinline__ void lin_store(uint16_t* __restrict__ y, int ny, int 
 template <bool GLU>
 __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int T, int N, int K, int ks,
-    uint16_t* __restrict__ y, float* __restrict__ parts, int* __restrict__ counters) {
+    uint16_t* __restrict__ y, float* __restrict__ parts, int* __restrict__ counters,
+    float* __restrict__ split) {
   __shared__ LinLds l;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, kg = lane >> 4;
@@ -1054,6 +1084,13 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(
       v0 += l.red[u][0][lane];
       v1 += l.red[u][1][lane];
     }
+    if (!GLU && split != nullptr) {
+      // the parts themselves, row-major [ks][T][N], for the next kernel to sum
+      float* dst = split + ((size_t)part * T + col) * N + r0 + kg * 4;
+      *reinterpret_cast<f32x4_t*>(dst) = v0;
+      if (two) *reinterpret_cast<f32x4_t*>(dst + 16) = v1;
+      return;
+    }
     if (ks == 1) {
       lin_store<GLU>(y, ny, col, r0, kg, two, v0, v1);
     } else {
@@ -1068,7 +1105,7 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(
     }
     if (ks > 1) __builtin_amdgcn_s_waitcnt(0);  // written through before the part is counted
   }
-  if (ks == 1) return;
+  if (ks == 1 || split != nullptr) return;
   __syncthreads();
   if (threadIdx.x == 0) {
     l.last = atomicAdd(&counters[item], 1) == ks - 1;
@@ -1123,7 +1160,7 @@ int launch_linear(const void* x, const void* w, int T, int N, int K, void* y, vo
   int* counters = ws != nullptr ? (int*)((char*)ws + kLinPartBytes) : nullptr;
   hipLaunchKernelGGL((linear_kernel<GLU>), dim3(items * ks), dim3(64 * kLinWaves), 0, st,
                      (const uint16_t*)x, (const uint16_t*)w, T, N, K, ks, (uint16_t*)y, parts,
-                     counters);
+                     counters, (float*)nullptr);
   return (int)hipGetLastError();
 }
 
@@ -1228,6 +1265,26 @@ extern "C" int sluice_dec_linear(const void* x, const void* w, int T, int N, int
   return launch_linear<false>(x, w, T, N, K, y, workspace, (hipStream_t)stream);
 }
 
+extern "C" int sluice_dec_linear_split_parts(int T, int N, int K) {
+  if (T <= 0 || T > 16 || N <= 0 || N % 16 != 0 || K <= 0 || K % 64 != 0) return 0;
+  return linear_parts((N + 31) / 32, K, T, device_cus());
+}
+
+extern "C" int sluice_dec_linear_split(const void* x, const void* w, int T, int N, int K,
+                                       float* parts, sluice_stream_t stream) {
+  if (T < 0 || T > 16 || N <= 0 || N % 16 != 0 || K <= 0 || K % 64 != 0 || x == nullptr ||
+      w == nullptr || parts == nullptr)
+    return SLUICE_E_INVAL;
+  if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)parts) & 15) return SLUICE_E_INVAL;
+  if (T == 0) return SLUICE_OK;
+  const int items = (N + 31) / 32;
+  const int ks = linear_parts(items, K, T, device_cus());
+  hipLaunchKernelGGL((linear_kernel<false>), dim3(items * ks), dim3(64 * kLinWaves), 0,
+                     (hipStream_t)stream, (const uint16_t*)x, (const uint16_t*)w, T, N, K, ks,
+                     (uint16_t*)nullptr, (float*)nullptr, (int*)nullptr, parts);
+  return (int)hipGetLastError();
+}
+
 extern "C" int sluice_dec_linear_glu(const void* x, const void* w, int T, int N, int K, void* y,
                                      void* workspace, sluice_stream_t stream) {
   if (T < 0 || T > 16 || N <= 0 || N % 32 != 0 || K <= 0 || K % 64 != 0 || x == nullptr ||
@@ -1303,13 +1360,17 @@ extern "C" int sluice_dec_add_rmsnorm_gate_ok(int rows, int H) {
   return rows >= 0 && rows <= kMaxRows && H > 0 && H % 8 == 0 && H <= 4 * kT * 8;
 }
 
-extern "C" int sluice_dec_add_rmsnorm_gate(const void* x, const void* delta, const void* w,
+extern "C" int sluice_dec_add_rmsnorm_gate(const void* x, const void* delta,
+                                          const float* delta_parts, int n_parts, const void* w,
                                           void* x_out, void* hn_out, const void* wg,
                                           const float* bias_table, const int64_t* step,
                                           int n_steps, int bias_rows, int rows, int H, int E,
                                           float eps, float* logits, sluice_stream_t stream) {
   if (!sluice_dec_add_rmsnorm_gate_ok(rows, H) || E <= 0 || !x || !w || !x_out || !hn_out || !wg ||
       !logits)
+    return SLUICE_E_INVAL;
+  if (delta_parts != nullptr &&
+      (delta != nullptr || n_parts < 1 || n_parts > kMaxDeltaParts || ((uintptr_t)delta_parts & 15)))
     return SLUICE_E_INVAL;
   if (bias_table != nullptr && (step == nullptr || n_steps <= 0 || bias_rows < rows))
     return SLUICE_E_INVAL;
@@ -1323,7 +1384,8 @@ extern "C" int sluice_dec_add_rmsnorm_gate(const void* x, const void* delta, con
   auto go = [&](auto ni) {
     constexpr int NI = decltype(ni)::value;
     hipLaunchKernelGGL((add_rmsnorm_gate_kernel<NI, EPW>), grid, dim3(kT), 0, st,
-                       (const uint16_t*)x, (const uint16_t*)delta, (const uint16_t*)w,
+                       (const uint16_t*)x, (const uint16_t*)delta, delta_parts, n_parts,
+                       (const uint16_t*)w,
                        (uint16_t*)x_out, (uint16_t*)hn_out, (const uint16_t*)wg, bias_table, step,
                        n_steps, bias_rows, H, E, eps, logits);
   };

@@ -411,7 +411,13 @@ class _GQA(nn.Module):
         self.k[:, :, :n] = _randn((b, self.kvh, n, self.hd), gen, 1.0, self.v.device)
         self.v[:, :, :n] = _randn((b, self.kvh, n, self.hd), gen, 1.0, self.v.device)
 
-    def forward(self, hn, pos, cos_t, sin_t):
+    # the output projection can hand its K parts to the next (fused) norm
+    splits_output = True
+
+    def forward(self, hn, pos, cos_t, sin_t, split=False):
+        """Attention output [c, H] bf16, or with split=True the output
+        projection's K parts [ks, c, H] fp32 (their in-order sum, rounded to
+        bf16, is the bf16 output)."""
         lib, check = _k()
         c = hn.shape[0]
         qkv = linear(hn, self.wqkv)
@@ -421,6 +427,14 @@ class _GQA(nn.Module):
             sin_t.data_ptr(), pos.data_ptr(), c, self.nh, self.kvh, self.hd, self.L, _EPS,
             float(self.scale), self.k.data_ptr(), self.v.data_ptr(), o.data_ptr(), _stream(hn)),
             "sluice_dec_gqa_decode")
+        if split:
+            H, K = self.wo.shape
+            parts = torch.empty((lib.sluice_dec_linear_split_parts(c, H, K), c, H),
+                                dtype=torch.float32, device=hn.device)
+            check(lib.sluice_dec_linear_split(o.data_ptr(), self.wo.data_ptr(), c, H, K,
+                                              parts.data_ptr(), _stream(hn)),
+                  "sluice_dec_linear_split")
+            return parts
         return linear(o, self.wo)
 
 
@@ -564,16 +578,20 @@ class _StoreMoELayer(nn.Module):
         """(x_out, hn, logits): the residual add, the RMSNorm before this layer
         and its router logits in one kernel (x_out = x + delta, hn =
         rmsnorm(x_out) * w, as add_rmsnorm computes them), or None when the
-        batch shape is one the fused kernel does not take."""
+        batch shape is one the fused kernel does not take.  delta may be a
+        projection's fp32 K parts [ks, T, H] (their in-order sum rounded to
+        bf16 is the delta)."""
         lib, check = _k()
         T = x.shape[0]
         if not lib.sluice_dec_add_rmsnorm_gate_ok(T, self.H):
             return None
+        parts = delta is not None and delta.dtype == torch.float32
         x_out, hn = torch.empty_like(x), torch.empty_like(x)
         out = torch.empty((T, self.E), dtype=torch.float32, device=x.device)
         rb = self.routing_bias
         check(lib.sluice_dec_add_rmsnorm_gate(
-            x.data_ptr(), None if delta is None else delta.data_ptr(), w.data_ptr(),
+            x.data_ptr(), None if delta is None or parts else delta.data_ptr(),
+            delta.data_ptr() if parts else None, delta.shape[0] if parts else 0, w.data_ptr(),
             x_out.data_ptr(), hn.data_ptr(), self.gate.weight.data_ptr(),
             None if rb is None else rb.table.data_ptr(), None if rb is None else rb.step.data_ptr(),
             0 if rb is None else rb.table.shape[0], 0 if rb is None else rb.table.shape[1], T,
@@ -760,10 +778,16 @@ class SyntheticDecoder:
         (which adds the attention output).  Leaves io["hn"] = MLP input."""
         blk = self.blocks[i]
         x = io["x"]
+        lib, _ = _k()
+        fuse = blk.moe is not None and lib.sluice_dec_add_rmsnorm_gate_ok(x.shape[0], x.shape[1])
         if blk.attn is not None:
             hn = add_rmsnorm(x, io["delta"], blk.n1)
-            io["delta"] = blk.attn(hn, st.pos, self.cos_tbl, self.sin_tbl)
-        fused = blk.moe.norm_logits(x, io["delta"], blk.n2) if blk.moe is not None else None
+            if fuse and getattr(blk.attn, "splits_output", False):
+                # the output projection's K parts go straight into the fused norm
+                io["delta"] = blk.attn(hn, st.pos, self.cos_tbl, self.sin_tbl, split=True)
+            else:
+                io["delta"] = blk.attn(hn, st.pos, self.cos_tbl, self.sin_tbl)
+        fused = blk.moe.norm_logits(x, io["delta"], blk.n2) if fuse else None
         if fused is not None:
             # a MoE layer's norm and router logits in one kernel
             io["x"], io["hn"], io["lg"] = fused

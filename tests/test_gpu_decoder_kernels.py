@@ -121,9 +121,9 @@ def test_add_rmsnorm_gate_matches_the_two_kernels(rows, H, E, delta, bias):
     bargs = ((d["table"].data_ptr(), d["step"].data_ptr(), steps, brow) if bias
              else (None, None, 0, 0))
     check(lib.sluice_dec_add_rmsnorm_gate(
-        d["x"].data_ptr(), dd.data_ptr() if delta else None, d["w"].data_ptr(), x_out.data_ptr(),
-        hn.data_ptr(), d["wg"].data_ptr(), *bargs, rows, H, E, 1e-6, lg.data_ptr(), _st()),
-        "add_rmsnorm_gate")
+        d["x"].data_ptr(), dd.data_ptr() if delta else None, None, 0, d["w"].data_ptr(),
+        x_out.data_ptr(), hn.data_ptr(), d["wg"].data_ptr(), *bargs, rows, H, E, 1e-6,
+        lg.data_ptr(), _st()), "add_rmsnorm_gate")
     # the two-kernel path on a copy of x
     x2 = d["x"].clone()
     hn2 = add_rmsnorm(x2, dd, d["w"])
@@ -138,6 +138,47 @@ def test_add_rmsnorm_gate_matches_the_two_kernels(rows, H, E, delta, bias):
         assert torch.equal(lg.cpu(), lg2.cpu())
     else:
         assert torch.allclose(lg.cpu(), lg2.cpu(), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("T,H,K,E", [(8, 2048, 4096, 128), (1, 2048, 4096, 128),
+                                     (12, 2048, 2048, 64), (16, 2048, 8192, 128),
+                                     (4, 1040, 4096, 8)])
+def test_linear_split_parts_into_the_fused_norm(T, H, K, E):
+    """A projection left as its K parts and summed by the fused norm gives the
+    same residual, hn and logits, bit for bit, as the projection's bf16 output
+    fed to it (and the parts sum to that output)."""
+    from sluice_amd.decoder import linear
+
+    lib, check = _lib()
+    g = torch.Generator().manual_seed(T * 31 + K)
+    o = torch.randn((T, K), generator=g).bfloat16().to(DEV)
+    wo = (0.02 * torch.randn((H, K), generator=g)).bfloat16().to(DEV)
+    x = torch.randn((T, H), generator=g).bfloat16().to(DEV)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).bfloat16().to(DEV)
+    wg = (0.02 * torch.randn((E, H), generator=g)).bfloat16().to(DEV)
+    ks = lib.sluice_dec_linear_split_parts(T, H, K)
+    assert 1 <= ks <= 4
+    parts = torch.empty((ks, T, H), dtype=torch.float32, device=DEV)
+    check(lib.sluice_dec_linear_split(o.data_ptr(), wo.data_ptr(), T, H, K, parts.data_ptr(),
+                                      _st()), "linear_split")
+    y = linear(o, wo)
+    outs = []
+    for src in ("bf16", "parts"):
+        x_out, hn = torch.empty_like(x), torch.empty_like(x)
+        lg = torch.empty((T, E), dtype=torch.float32, device=DEV)
+        check(lib.sluice_dec_add_rmsnorm_gate(
+            x.data_ptr(), y.data_ptr() if src == "bf16" else None,
+            parts.data_ptr() if src == "parts" else None, ks if src == "parts" else 0,
+            w.data_ptr(), x_out.data_ptr(), hn.data_ptr(), wg.data_ptr(), None, None, 0, 0, T, H,
+            E, 1e-6, lg.data_ptr(), _st()), "add_rmsnorm_gate")
+        outs.append((x_out, hn, lg))
+    torch.cuda.synchronize()
+    s = parts[0].clone()
+    for p in range(1, ks):
+        s = s + parts[p]
+    assert torch.equal(s.bfloat16(), y)
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("T,N,K", [(8, 3648, 2048), (1, 2048, 10944), (12, 5632, 2048),
