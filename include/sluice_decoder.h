@@ -119,8 +119,12 @@ int sluice_dec_mla_decode(const void* q, int q_stride, const void* kva, int kva_
  *   v_cache [c, kvh, L, hd] row pos[t] = v_g; then per query head h (kv head
  *   h / (nh/kvh)): softmax over rows 0..pos[t] of (q . k) * scale,
  *   out [c, nh*hd] = bf16(p . v).  hd == 128, L <= 4096; qkv, q_norm,
- *   k_norm, cos_t, sin_t and the caches 16-byte aligned, out 4-byte aligned. */
-int sluice_dec_gqa_decode(const void* qkv, const void* q_norm, const void* k_norm,
+ *   k_norm, cos_t, sin_t and the caches 16-byte aligned, out 4-byte aligned.
+ *   Exactly one of qkv and qkv_parts: the QKV projection's K parts
+ *   [n_parts, c, (nh + 2*kvh)*hd] fp32 (n_parts <= 4, as sluice_dec_linear_split
+ *   leaves them) are summed in order and rounded to bf16 first. */
+int sluice_dec_gqa_decode(const void* qkv, const float* qkv_parts, int n_parts,
+                          const void* q_norm, const void* k_norm,
                           const float* cos_t, const float* sin_t, const int64_t* pos, int c,
                           int nh, int kvh, int hd, int L, float eps, float scale, void* k_cache,
                           void* v_cache, void* out, sluice_stream_t stream);

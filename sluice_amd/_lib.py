@@ -123,8 +123,8 @@ SIGNATURES = {
     ),
     "sluice_dec_gqa_decode": (
         c_int,
-        [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_float, c_float, _P, _P,
-         _P, _P],
+        [_P, _P, c_int, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_float, c_float,
+         _P, _P, _P, _P],
     ),
 }
 

@@ -901,7 +901,8 @@ constexpr int kGqaRows = 2;
 
 template <int WAVES, int RG>
 __global__ __launch_bounds__(WAVES * 64) void gqa_decode_kernel(
-    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_norm,
+    const uint16_t* __restrict__ qkv, const float* __restrict__ qkv_parts, int nparts,
+    const uint16_t* __restrict__ q_norm,
     const uint16_t* __restrict__ k_norm, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, const int64_t* __restrict__ pos, int nh, int kvh, int L,
     float eps, float scale, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
@@ -921,9 +922,41 @@ __global__ __launch_bounds__(WAVES * 64) void gqa_decode_kernel(
   // load: the head's q, the new k and v, the norm weights and the first
   // chunk of cache rows (rows past the position are loaded, in bounds, and
   // masked below).
-  const u32x4_t xq = ldg16(xr + h * kHd + col);
-  const u32x4_t xk = ldg16(xr + (nh + g) * kHd + col);
-  const u32x4_t xv = ldg16(xr + (nh + kvh + g) * kHd + col);
+  u32x4_t xq, xk, xv;
+  if (qkv_parts != nullptr) {
+    // the projection's K parts [nparts][c][width] fp32: bf16(sum in part order)
+    const size_t width = (size_t)(nh + 2 * kvh) * kHd;
+    const int offs[3] = {h * kHd + col, (nh + g) * kHd + col, (nh + kvh + g) * kHd + col};
+    f32x4_t pv[3][kMaxDeltaParts][2];
+#pragma unroll
+    for (int v = 0; v < 3; ++v)
+#pragma unroll
+      for (int q = 0; q < kMaxDeltaParts; ++q) {
+        const float* src = qkv_parts + ((size_t)(q < nparts ? q : 0) * gridDim.x + t) * width + offs[v];
+        pv[v][q][0] = *reinterpret_cast<const f32x4_t*>(src);
+        pv[v][q][1] = *reinterpret_cast<const f32x4_t*>(src + 4);
+      }
+    u32x4_t xs[3];
+#pragma unroll
+    for (int v = 0; v < 3; ++v) {
+      f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+      for (int q = 0; q < kMaxDeltaParts; ++q)
+        if (q < nparts) {
+          s0 += pv[v][q][0];
+          s1 += pv[v][q][1];
+        }
+      xs[v] = u32x4_t{pack2(s0[0], s0[1]), pack2(s0[2], s0[3]), pack2(s1[0], s1[1]),
+                      pack2(s1[2], s1[3])};
+    }
+    xq = xs[0];
+    xk = xs[1];
+    xv = xs[2];
+  } else {
+    xq = ldg16(xr + h * kHd + col);
+    xk = ldg16(xr + (nh + g) * kHd + col);
+    xv = ldg16(xr + (nh + kvh + g) * kHd + col);
+  }
   const u32x4_t wq = ldg16(q_norm + col), wk = ldg16(k_norm + col);
   u32x4_t kr[RG], vr[RG];
 #pragma unroll
@@ -1265,9 +1298,26 @@ extern "C" int sluice_dec_linear(const void* x, const void* w, int T, int N, int
   return launch_linear<false>(x, w, T, N, K, y, workspace, (hipStream_t)stream);
 }
 
+// K parts of a projection whose parts the next kernel sums (no hand-off).
+#ifndef SPLIT_KS
+#define SPLIT_KS 0
+#endif
+// Measured in replayed graphs with distinct weights per launch (T = 1 and 8):
+// 4 parts for K <= 2048 (N = 2048: 3.8 vs 5.6 us whole; N = 5120: 5.9 vs
+// 6.1), 3 for K <= 4096 (N = 2048: 5.3 vs 8.7 us whole, 5.8 with 4), 4 beyond.
+int split_parts(int items, int K, int T) {
+  (void)items;
+  (void)T;
+  const int nc = K / 64;
+  if (SPLIT_KS > 0) return SPLIT_KS <= nc ? SPLIT_KS : 1;
+  int ks = nc <= 32 ? 4 : nc <= 64 ? 3 : 4;
+  while (ks > 1 && nc < 8 * ks) --ks;  // at least 8 chunks per part
+  return ks;
+}
+
 extern "C" int sluice_dec_linear_split_parts(int T, int N, int K) {
   if (T <= 0 || T > 16 || N <= 0 || N % 16 != 0 || K <= 0 || K % 64 != 0) return 0;
-  return linear_parts((N + 31) / 32, K, T, device_cus());
+  return split_parts((N + 31) / 32, K, T);
 }
 
 extern "C" int sluice_dec_linear_split(const void* x, const void* w, int T, int N, int K,
@@ -1278,7 +1328,7 @@ extern "C" int sluice_dec_linear_split(const void* x, const void* w, int T, int 
   if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)parts) & 15) return SLUICE_E_INVAL;
   if (T == 0) return SLUICE_OK;
   const int items = (N + 31) / 32;
-  const int ks = linear_parts(items, K, T, device_cus());
+  const int ks = split_parts(items, K, T);
   hipLaunchKernelGGL((linear_kernel<false>), dim3(items * ks), dim3(64 * kLinWaves), 0,
                      (hipStream_t)stream, (const uint16_t*)x, (const uint16_t*)w, T, N, K, ks,
                      (uint16_t*)nullptr, (float*)nullptr, (int*)nullptr, parts);
@@ -1444,23 +1494,26 @@ extern "C" int sluice_dec_mla_decode(const void* q, int q_stride, const void* kv
   return (int)hipGetLastError();
 }
 
-extern "C" int sluice_dec_gqa_decode(const void* qkv, const void* q_norm, const void* k_norm,
+extern "C" int sluice_dec_gqa_decode(const void* qkv, const float* qkv_parts, int n_parts,
+                                     const void* q_norm, const void* k_norm,
                                      const float* cos_t, const float* sin_t, const int64_t* pos,
                                      int c, int nh, int kvh, int hd, int L, float eps, float scale,
                                      void* k_cache, void* v_cache, void* out,
                                      sluice_stream_t stream) {
   if (c < 0 || nh <= 0 || kvh <= 0 || nh % kvh != 0 || hd != kHd || L <= 0 || L > kMaxL)
     return SLUICE_E_INVAL;
-  if (!qkv || !q_norm || !k_norm || !cos_t || !sin_t || !pos || !k_cache || !v_cache || !out)
+  if ((qkv == nullptr) == (qkv_parts == nullptr)) return SLUICE_E_INVAL;  // exactly one
+  if (qkv_parts != nullptr && (n_parts < 1 || n_parts > kMaxDeltaParts)) return SLUICE_E_INVAL;
+  if (!q_norm || !k_norm || !cos_t || !sin_t || !pos || !k_cache || !v_cache || !out)
     return SLUICE_E_INVAL;
-  if ((((uintptr_t)qkv | (uintptr_t)q_norm | (uintptr_t)k_norm | (uintptr_t)cos_t |
+  if ((((uintptr_t)qkv | (uintptr_t)qkv_parts | (uintptr_t)q_norm | (uintptr_t)k_norm | (uintptr_t)cos_t |
         (uintptr_t)sin_t | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15) != 0 ||
       ((uintptr_t)out & 3) != 0)
     return SLUICE_E_INVAL;
   if (c == 0) return SLUICE_OK;
   hipLaunchKernelGGL((gqa_decode_kernel<kGqaWaves, kGqaRows>), dim3(c, nh),
                      dim3(kGqaWaves * 64), 0, (hipStream_t)stream, (const uint16_t*)qkv,
-                     (const uint16_t*)q_norm, (const uint16_t*)k_norm, cos_t, sin_t, pos, nh, kvh,
+                     qkv_parts, n_parts, (const uint16_t*)q_norm, (const uint16_t*)k_norm, cos_t, sin_t, pos, nh, kvh,
                      L, eps, scale, (uint16_t*)k_cache, (uint16_t*)v_cache, (uint16_t*)out);
   return (int)hipGetLastError();
 }

@@ -288,6 +288,22 @@ def linear(x, w):
     return y
 
 
+def linear_split(x, w):
+    """x . w^T left as its K parts [ks, T, N] fp32 (T <= 16): their in-order
+    sum rounded to bf16 is the projection; the next kernel sums them, so no
+    workgroup waits for another's part."""
+    lib, check = _k()
+    T, K = x.shape
+    N = w.shape[0]
+    ks = lib.sluice_dec_linear_split_parts(T, N, K)
+    if ks < 1:
+        raise ValueError(f"linear_split does not take T={T}, N={N}, K={K}")
+    parts = torch.empty((ks, T, N), dtype=torch.float32, device=x.device)
+    check(lib.sluice_dec_linear_split(x.data_ptr(), w.data_ptr(), T, N, K, parts.data_ptr(),
+                                      _stream(x)), "sluice_dec_linear_split")
+    return parts
+
+
 def linear_glu(x, w):
     """silu(x . w[:N/2]^T) * (x . w[N/2:]^T) for decode batches (T <= 16):
     the gate/up projection with the activation in its epilogue."""
@@ -368,7 +384,12 @@ class _MLA(nn.Module):
         self.kpe[:, :n] = _randn((b, n, self.rope), gen, 1.0, self.ckv.device)
         self.ckvt[..., _mla_kslot(self.ckv.device)] = self.ckv.view(b, L // 32, 32, lora).transpose(2, 3)
 
-    def forward(self, hn, pos, cos_t, sin_t):
+    # the output projection can hand its K parts to the next (fused) norm
+    splits_output = True
+
+    def forward(self, hn, pos, cos_t, sin_t, split=False):
+        """Attention output [c, H] bf16, or with split=True the output
+        projection's K parts [ks, c, H] fp32."""
         lib, check = _k()
         c = hn.shape[0]
         qkva = linear(hn, self.w_qkva)
@@ -385,7 +406,7 @@ class _MLA(nn.Module):
             pos.data_ptr(), c, self.nh, self.nope, self.rope, self.lora, self.vh, self.L, _EPS,
             float(self.scale), self.ckv.data_ptr(), self.ckvt.data_ptr(), self.kpe.data_ptr(),
             work.data_ptr(), o.data_ptr(), _stream(hn)), "sluice_dec_mla_decode")
-        return linear(o, self.wo)
+        return linear_split(o, self.wo) if split else linear(o, self.wo)
 
 
 class _GQA(nn.Module):
@@ -420,22 +441,17 @@ class _GQA(nn.Module):
         bf16, is the bf16 output)."""
         lib, check = _k()
         c = hn.shape[0]
+        # (the QKV projection stays whole: every 16-lane group of the attention
+        # kernel reads the head's q, k and v, and reading K parts instead cost
+        # the kernel more than splitting saved the projection)
         qkv = linear(hn, self.wqkv)
         o = torch.empty((c, self.nh * self.hd), dtype=hn.dtype, device=hn.device)
         check(lib.sluice_dec_gqa_decode(
-            qkv.data_ptr(), self.q_norm.data_ptr(), self.k_norm.data_ptr(), cos_t.data_ptr(),
-            sin_t.data_ptr(), pos.data_ptr(), c, self.nh, self.kvh, self.hd, self.L, _EPS,
-            float(self.scale), self.k.data_ptr(), self.v.data_ptr(), o.data_ptr(), _stream(hn)),
-            "sluice_dec_gqa_decode")
-        if split:
-            H, K = self.wo.shape
-            parts = torch.empty((lib.sluice_dec_linear_split_parts(c, H, K), c, H),
-                                dtype=torch.float32, device=hn.device)
-            check(lib.sluice_dec_linear_split(o.data_ptr(), self.wo.data_ptr(), c, H, K,
-                                              parts.data_ptr(), _stream(hn)),
-                  "sluice_dec_linear_split")
-            return parts
-        return linear(o, self.wo)
+            qkv.data_ptr(), None, 0, self.q_norm.data_ptr(),
+            self.k_norm.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(), pos.data_ptr(), c,
+            self.nh, self.kvh, self.hd, self.L, _EPS, float(self.scale), self.k.data_ptr(),
+            self.v.data_ptr(), o.data_ptr(), _stream(hn)), "sluice_dec_gqa_decode")
+        return linear_split(o, self.wo) if split else linear(o, self.wo)
 
 
 class _DenseMLP(nn.Module):

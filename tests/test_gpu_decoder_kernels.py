@@ -145,8 +145,9 @@ def test_add_rmsnorm_gate_matches_the_two_kernels(rows, H, E, delta, bias):
                                      (4, 1040, 4096, 8)])
 def test_linear_split_parts_into_the_fused_norm(T, H, K, E):
     """A projection left as its K parts and summed by the fused norm gives the
-    same residual, hn and logits, bit for bit, as the projection's bf16 output
-    fed to it (and the parts sum to that output)."""
+    same residual, hn and logits, bit for bit, as bf16(in-order sum of the
+    parts) fed to it as a bf16 delta; that sum is the projection (to fp32
+    rounding of a different K split)."""
     from sluice_amd.decoder import linear
 
     lib, check = _lib()
@@ -161,7 +162,12 @@ def test_linear_split_parts_into_the_fused_norm(T, H, K, E):
     parts = torch.empty((ks, T, H), dtype=torch.float32, device=DEV)
     check(lib.sluice_dec_linear_split(o.data_ptr(), wo.data_ptr(), T, H, K, parts.data_ptr(),
                                       _st()), "linear_split")
-    y = linear(o, wo)
+    torch.cuda.synchronize()
+    s = parts[0].clone()
+    for p in range(1, ks):
+        s = s + parts[p]
+    y = s.bfloat16()
+    assert _rel(y, linear(o, wo).float()) <= 1e-2
     outs = []
     for src in ("bf16", "parts"):
         x_out, hn = torch.empty_like(x), torch.empty_like(x)
@@ -173,10 +179,6 @@ def test_linear_split_parts_into_the_fused_norm(T, H, K, E):
             E, 1e-6, lg.data_ptr(), _st()), "add_rmsnorm_gate")
         outs.append((x_out, hn, lg))
     torch.cuda.synchronize()
-    s = parts[0].clone()
-    for p in range(1, ks):
-        s = s + parts[p]
-    assert torch.equal(s.bfloat16(), y)
     for a, b in zip(outs[0], outs[1]):
         assert torch.equal(a, b)
 
@@ -387,9 +389,19 @@ def test_gqa_decode(L, positions):
                                            pos=pos, cos=cos_t, sin=sin_t).items()}
     out = torch.empty((c, nh * hd), dtype=torch.bfloat16, device=DEV)
     check(lib.sluice_dec_gqa_decode(
-        d["qkv"].data_ptr(), d["qn"].data_ptr(), d["kn"].data_ptr(), d["cos"].data_ptr(),
+        d["qkv"].data_ptr(), None, 0, d["qn"].data_ptr(), d["kn"].data_ptr(), d["cos"].data_ptr(),
         d["sin"].data_ptr(), d["pos"].data_ptr(), c, nh, kvh, hd, L, 1e-6, scale,
         d["k"].data_ptr(), d["v"].data_ptr(), out.data_ptr(), _st()), "gqa_decode")
+    # the same from the projection's K parts (qkv/4 + qkv/4 + qkv/2 sums to qkv exactly):
+    # bit-identical output and cache rows
+    qf = d["qkv"].float()
+    parts = torch.stack([qf / 4, qf / 4, qf / 2]).contiguous()
+    k2, v2 = k.clone().to(DEV), v.clone().to(DEV)
+    out2 = torch.empty_like(out)
+    check(lib.sluice_dec_gqa_decode(
+        None, parts.data_ptr(), 3, d["qn"].data_ptr(), d["kn"].data_ptr(), d["cos"].data_ptr(),
+        d["sin"].data_ptr(), d["pos"].data_ptr(), c, nh, kvh, hd, L, 1e-6, scale, k2.data_ptr(),
+        v2.data_ptr(), out2.data_ptr(), _st()), "gqa_decode parts")
     torch.cuda.synchronize()
     for t in range(c):
         p = int(pos[t])
@@ -407,6 +419,8 @@ def test_gqa_decode(L, positions):
             s = (qr[h] @ kc[h // grp].T) * scale
             o = torch.softmax(s, dim=-1) @ vc[h // grp]
             assert _rel(out[t, h * hd:(h + 1) * hd], o) <= TOL, (t, h)
+    assert torch.equal(out2, out)
+    assert torch.equal(k2, d["k"]) and torch.equal(v2, d["v"])
     # rows other than pos[t] are untouched
     mask = torch.ones((c, L), dtype=torch.bool)
     mask[torch.arange(c), pos] = False
