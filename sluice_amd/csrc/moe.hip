@@ -64,14 +64,6 @@ __host__ __device__ inline size_t plan_ints(int P) {
   return (size_t)kPlanHeader + (size_t)kBlockInts * P + (size_t)P;
 }
 
-__device__ __forceinline__ int pair_slot(const int32_t* ids, const int32_t* map, int p, int E,
-                                         int S) {
-  const int g = ids[p];
-  if ((unsigned)g >= (unsigned)E) return -1;
-  const int s = map != nullptr ? map[g] : g;
-  return ((unsigned)s < (unsigned)S) ? s : -1;
-}
-
 // ---------------------------------------------------------------------------
 // Align: group the P = T*k pairs by slot into blocks of <= 16, slots
 // ascending and pairs ascending inside a slot (deterministic).  Called by
@@ -79,6 +71,7 @@ __device__ __forceinline__ int pair_slot(const int32_t* ids, const int32_t* map,
 // the scratch arrays are LDS.  Returns the block count to every thread.
 // ---------------------------------------------------------------------------
 struct AlignScratch {
+  int slot_of[SLUICE_MAX_EXPERTS];  // the map, staged (or the identity)
   int cnt[SLUICE_MAX_SLOTS];
   int boff[SLUICE_MAX_SLOTS];
   int run[SLUICE_MAX_SLOTS];
@@ -92,13 +85,22 @@ __device__ int build_plan(const int32_t* __restrict__ ids, int P, const int32_t*
                           int32_t* valid) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
+  // The first kThreads ids and the whole map are loaded together and the map
+  // is staged in LDS, so the slot lookups need no second memory round trip.
+  const int id0 = tid < P ? ids[tid] : -1;
+  for (int e = tid; e < E; e += kThreads) sc.slot_of[e] = map != nullptr ? map[e] : e;
   for (int s = tid; s < S; s += kThreads) {
     sc.cnt[s] = 0;
     sc.run[s] = 0;
   }
   __syncthreads();
+  auto slot_of = [&](int g) {
+    if ((unsigned)g >= (unsigned)E) return -1;
+    const int s = sc.slot_of[g];
+    return (unsigned)s < (unsigned)S ? s : -1;
+  };
   for (int p = tid; p < P; p += kThreads) {
-    const int s = pair_slot(ids, map, p, E, S);
+    const int s = slot_of(p == tid ? id0 : ids[p]);
     if (s >= 0) atomicAdd(&sc.cnt[s], 1);
   }
   __syncthreads();
@@ -132,7 +134,7 @@ __device__ int build_plan(const int32_t* __restrict__ ids, int P, const int32_t*
   // Ranks in pair order, one chunk of kThreads pairs at a time.
   for (int c = 0; c < P; c += kThreads) {
     const int p = c + tid;
-    const int s = p < P ? pair_slot(ids, map, p, E, S) : -1;
+    const int s = p < P ? slot_of(c == 0 ? id0 : ids[p]) : -1;
     sc.chunk_slot[tid] = s;
     __syncthreads();
     if (s >= 0) {
