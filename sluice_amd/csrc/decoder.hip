@@ -1299,9 +1299,6 @@ extern "C" int sluice_dec_linear(const void* x, const void* w, int T, int N, int
 }
 
 // K parts of a projection whose parts the next kernel sums (no hand-off).
-#ifndef SPLIT_KS
-#define SPLIT_KS 0
-#endif
 // Measured in replayed graphs with distinct weights per launch (T = 1 and 8):
 // 4 parts for K <= 2048 (N = 2048: 3.8 vs 5.6 us whole; N = 5120: 5.9 vs
 // 6.1), 3 for K <= 4096 (N = 2048: 5.3 vs 8.7 us whole, 5.8 with 4), 4 beyond.
@@ -1309,7 +1306,6 @@ int split_parts(int items, int K, int T) {
   (void)items;
   (void)T;
   const int nc = K / 64;
-  if (SPLIT_KS > 0) return SPLIT_KS <= nc ? SPLIT_KS : 1;
   int ks = nc <= 32 ? 4 : nc <= 64 ? 3 : 4;
   while (ks > 1 && nc < 8 * ks) --ks;  // at least 8 chunks per part
   return ks;
