@@ -88,3 +88,26 @@ def test_add_rmsnorm_gate_shapes(lib):
     ok = lib.sluice_dec_add_rmsnorm_gate_ok
     assert ok(16, 2048) and ok(16, 7168) and ok(1, 8192) and not ok(1, 8200)
     assert not ok(17, 2048) and not ok(4, 2044)
+
+
+def test_linear_split_parts_and_argument_checks(lib):
+    parts = lib.sluice_dec_linear_split_parts
+    assert parts(8, 2048, 2048) == 4 and parts(1, 2048, 2048) == 4
+    assert parts(8, 2048, 4096) == 3 and parts(16, 2048, 8192) == 4
+    assert parts(8, 2048, 256) == 1 and parts(8, 2048, 1024) == 2  # >= 8 K chunks per part
+    assert parts(17, 2048, 2048) == 0 and parts(8, 2040, 2048) == 0 and parts(8, 2048, 100) == 0
+    # rejected before any launch: bad shapes, misalignment, missing output
+    import ctypes
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = ctypes.addressof(buf)
+    p16 = (p + 15) & ~15
+    assert lib.sluice_dec_linear_split(p16, p16, 17, 2048, 2048, p16, None) != 0
+    assert lib.sluice_dec_linear_split(p16, p16, 8, 2040, 2048, p16, None) != 0
+    assert lib.sluice_dec_linear_split(p16 + 4, p16, 8, 2048, 2048, p16, None) != 0
+    assert lib.sluice_dec_linear_split(p16, p16, 8, 2048, 2048, None, None) != 0
+
+
+def test_mla_workspace_grows_with_batch_and_heads(lib):
+    ws = lib.sluice_dec_mla_workspace
+    assert ws(0, 16) == 0 and ws(1, 0) == 0
+    assert 0 < ws(1, 16) < ws(8, 16) < ws(16, 16) < ws(16, 32)
