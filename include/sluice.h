@@ -139,8 +139,11 @@ int sluice_host_free(void* p);
  * [S, ceil(H/bn), ceil(I/bk)]; activations stay bf16.  Shared weights are
  * e4m3fn too, with shared_w13_scale [2*shared_I/128, H/128] and
  * shared_w2_scale [H/128, shared_I/128].
- * Requires H % 64 == 0, I % 64 == 0, T*(k + shared_I/I) <= SLUICE_MAX_PAIRS.
- * The workspace (device) must hold sluice_fused_experts_workspace() bytes.
+ * Requires H % 64 == 0, I % 64 == 0, E <= SLUICE_MAX_EXPERTS,
+ * T*(k + shared_I/I) <= SLUICE_MAX_PAIRS.
+ * The workspace (device) must hold sluice_fused_experts_workspace() bytes;
+ * it needs no initial contents and keeps none between calls (calls that
+ * share one must not overlap).
  * ---------------------------------------------------------------------- */
 size_t sluice_fused_experts_workspace(int T, int H, int I, int k, int shared_I);
 
@@ -164,20 +167,6 @@ int sluice_fused_experts_fp8(const void* x, const void* w13,
                              int shared_I, const void* shared, void* workspace,
                              size_t workspace_bytes, void* out,
                              sluice_stream_t stream);
-
-/* Health of a workspace used by the fused kernel: SLUICE_OK when its work
- * counters are back at zero (no call in flight or interrupted); *error_out =
- * 1 if a dependency wait inside the kernel ever ran out of time (2 s; the
- * results of that call are invalid).  Synchronous; for tests and debugging.
- * The workspace must be zero-filled before its first use; every call leaves
- * it so.  Calls sharing a workspace must not overlap. */
-int sluice_fused_experts_status(const void* workspace, int* error_out);
-
-/* Select the launch shape of sluice_fused_experts_*: 1 = one persistent
- * kernel per call when T*k <= 256 (cross-workgroup hand-offs), 0 = four
- * staged kernels (the default; SLUICE_MOE_FUSED=1 sets 1 at load).  Returns
- * the previous setting.  Process-wide; no counterpart in the reference. */
-int sluice_moe_set_fused(int enable);
 
 /* Token permute / align-to-block (vLLM moe_align_block_size): groups the
  * T*k (token, expert) pairs by slot into blocks of <= SLUICE_BLOCK_M pairs,

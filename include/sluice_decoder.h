@@ -47,8 +47,9 @@ int sluice_dec_linear(const void* x, const void* w, int T, int N, int K, void* y
  * sluice_dec_linear. */
 /* The plain projection left as its K parts: parts [ks, T, N] fp32 (row-major,
  * 16-byte aligned), ks = sluice_dec_linear_split_parts(T, N, K) (>= 1, 0 for
- * a shape it does not take); bf16(sum of the parts in order) equals what
- * sluice_dec_linear writes. */
+ * a shape it does not take).  bf16(sum of the parts in order) is the
+ * projection; it can differ from what sluice_dec_linear writes by the fp32
+ * rounding of a different K split (the two may split K differently). */
 int sluice_dec_linear_split_parts(int T, int N, int K);
 int sluice_dec_linear_split(const void* x, const void* w, int T, int N, int K, float* parts,
                             sluice_stream_t stream);

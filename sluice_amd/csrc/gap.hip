@@ -51,6 +51,7 @@
 
 #include "common.h"
 #include "slru.h"
+#include "stamp.h"
 
 namespace {
 
@@ -146,12 +147,13 @@ struct GapRecord {
   uint64_t ent[SLUICE_MAX_EXPERTS];  // stamp | id << 32: sorted unique selected ids
 };
 
-// Records of a layer rotate through kRing slots (record s in slot s % kRing),
-// so the device need not know whether the host has copied out the previous
-// record: only the one kRing records back, which it checks against the last
-// ack it read and re-reads over the bus only when that is too old (once every
-// kRing - 1 gaps at most, when the host keeps up).
-constexpr int kRing = 4;
+// Records of a layer rotate through kRing slots (record s in slot s % kRing,
+// stamps wrapping at a multiple of kRing: stamp.h), so the device need not
+// know whether the host has copied out the previous record: only the one
+// kRing records back, which it checks against the last ack it read and
+// re-reads over the bus only when that is too old (once every kRing - 1 gaps
+// at most, when the host keeps up).
+using sluice_stamp::kRing;
 
 struct GapMailbox {
   // written by the device
@@ -196,12 +198,9 @@ __device__ __forceinline__ int32_t ld_sys(const int32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// Stamps run 1, 2, ..., INT32_MAX, 1, ... (0 is "none yet", the stamp before
-// 1).  Steps from stamp b forward to stamp a.
+// Records from stamp b forward to stamp a (stamp.h).
 __host__ __device__ inline int32_t stamp_dist(int32_t a, int32_t b) {
-  int64_t d = (int64_t)a - (int64_t)b;
-  if (d < 0) d += INT32_MAX;
-  return (int32_t)d;
+  return sluice_stamp::dist(a, b);
 }
 
 // Spin until the host's ack *p is at most kRing stamps behind stamp s, so
@@ -277,8 +276,7 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
   int32_t s = 0, seen = 0;
   bool fresh = false;
   if (tid == 0) {
-    s = dev_state[0] + 1;
-    if (s <= 0) s = 1;
+    s = sluice_stamp::next(dev_state[0]);
     s_standing = dev_state[1];
     seen = dev_state[2];
   }
@@ -343,7 +341,7 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
   if (s_status == 0) {
     // the record: entries and header in any order (each word is stamped)
     const int32_t s = s_stamp;
-    GapRecord* r = &mb->rec[s % kRing];
+    GapRecord* r = &mb->rec[sluice_stamp::slot(s)];
     for (int i = tid; i < base; i += kLookupThreads)
       st_host64(&r->ent[i], rec_word(s, (uint32_t)s_uniq[i]));
     if (tid == 0) st_host64(&r->hdr, rec_word(s, rec_hdr_hi(base, miss, s_waits)));
@@ -438,7 +436,7 @@ double gap_timeout_s() {
   return v;
 }
 
-int32_t next_stamp(int32_t s) { return s + 1 > 0 ? s + 1 : 1; }
+int32_t next_stamp(int32_t s) { return sluice_stamp::next(s); }
 
 }  // namespace
 
@@ -521,7 +519,8 @@ void respond(sluice_layer* L, int32_t stamp, int code) {
 // in stamp order, so looking at the next stamp's slot is enough).
 bool record_pending(sluice_layer* L) {
   const int32_t next = next_stamp(L->done_stamp.load(std::memory_order_acquire));
-  return rec_stamp(__atomic_load_n(&L->mb->rec[next % kRing].hdr, __ATOMIC_ACQUIRE)) == next;
+  return rec_stamp(__atomic_load_n(&L->mb->rec[sluice_stamp::slot(next)].hdr,
+                                   __ATOMIC_ACQUIRE)) == next;
 }
 
 // Serve one posted record of layer L.  block: wait (bounded) for it;
@@ -531,7 +530,7 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
   const int dev_status = __atomic_load_n(&mb->dev_status, __ATOMIC_ACQUIRE);
   if (dev_status != 0) return dev_status;  // a device wait failed earlier
   const int32_t want = next_stamp(L->host_stamp);
-  GapRecord* rec = &mb->rec[want % kRing];
+  GapRecord* rec = &mb->rec[sluice_stamp::slot(want)];
   uint64_t hdr = __atomic_load_n(&rec->hdr, __ATOMIC_ACQUIRE);
   double t0 = 0.0;
   if (rec_stamp(hdr) != want) {

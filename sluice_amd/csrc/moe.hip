@@ -14,20 +14,10 @@
 // load per lane per 32-wide K chunk), tokens on the N side.  A workgroup is
 // 4 waves that split K and reduce through LDS.
 //
-// Two launch shapes share the same per-item bodies:
-//   fused (opt-in, T*k <= 256): ONE persistent kernel per call, its grid
-//     sized so every workgroup is resident.  Every workgroup builds the align
-//     plan in LDS, then strides over the work items -- all gemm1 items
-//     (block, 16 intermediate rows) before all gemm2 items (block, 32 hidden
-//     rows).  A gemm2 item waits for its block's gemm1 tiles on a per-block
-//     counter (gemm1 items never wait).  The last gemm2 item to finish a
-//     32-column hidden slice combines that slice for every token (j
-//     ascending, so the result does not depend on which workgroup finishes
-//     last).  Counters go back to zero as their last user finishes, so the
-//     workspace needs no clearing between calls.
-//   staged: align (1 WG) -> gemm1 (+silu*up) -> gemm2 (*w) -> combine, four
-//     grid-stride kernels over a plan in global memory (any T*k, and the
-//     per-stage entry points).
+// Launch shape: align (1 WG) -> gemm1 (+silu*up) -> gemm2 (*w) -> combine,
+// four grid-stride kernels over a plan in global memory.  (A single
+// persistent kernel with cross-workgroup hand-offs was measured 1.6-1.8x
+// slower than these four launches and is not kept.)
 #include <math.h>
 
 #include "common.h"
@@ -41,8 +31,6 @@ constexpr int kPlanHeader = 4;
 constexpr int kKS = 4;                   // waves per workgroup (K split)
 constexpr int kThreads = 64 * kKS;
 constexpr int kG2T = 2;                  // 16-row hidden tiles per gemm2 item
-constexpr int kFusedMaxPairs = 256;      // T*k limit of the fused kernel
-constexpr int kFusedMaxHidden = 16384;   // H limit of the fused kernel
 constexpr int kFp8Blk = 128;
 
 // Chunks in flight per wave.  Deeper pipelines measured no faster for
@@ -197,7 +185,6 @@ __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
 
 // Wave 0 reduces the 4 K-split partial accumulators and writes
 // act[pair, tile*16 + kg*4 .. +4] = bf16(silu(g) * u).
-template <bool COH>
 __device__ __forceinline__ void g1_epilogue(RedBuf& red, int pair, int tile, int I,
                                             uint16_t* __restrict__ act) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kg = lane >> 4;
@@ -213,18 +200,12 @@ __device__ __forceinline__ void g1_epilogue(RedBuf& red, int pair, int tile, int
 #pragma unroll
     for (int r = 0; r < 4; ++r) o[r] = g[r] / (1.0f + expf(-g[r])) * u[r];
     uint16_t* dst = act + (size_t)pair * I + tile * 16 + kg * 4;
-    if (COH) {
-      st8_coh(dst, pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3]));
-      __builtin_amdgcn_s_waitcnt(0);  // written through before the tile is counted
-    } else {
-      *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
-    }
+    *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
   }
   __syncthreads();
 }
 
 // Wave 0 reduces and writes partial[pair, tile2*32 + t*16 + kg*4 .. +4] = w * sum.
-template <bool COH>
 __device__ __forceinline__ void g2_epilogue(RedBuf& red, int pair, int tile2, int H, float wv,
                                             float* __restrict__ partial) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kg = lane >> 4;
@@ -236,14 +217,8 @@ __device__ __forceinline__ void g2_epilogue(RedBuf& red, int pair, int tile2, in
 #pragma unroll
       for (int w = 1; w < kKS; ++w) s += red[w][t][lane];
       float* dst = partial + (size_t)pair * H + (tile2 * kG2T + t) * 16 + kg * 4;
-      if (COH) {
-        st8_coh(dst, __float_as_uint(wv * s[0]), __float_as_uint(wv * s[1]));
-        st8_coh(dst + 2, __float_as_uint(wv * s[2]), __float_as_uint(wv * s[3]));
-      } else {
-        *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{wv * s[0], wv * s[1], wv * s[2], wv * s[3]};
-      }
+      *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{wv * s[0], wv * s[1], wv * s[2], wv * s[3]};
     }
-    if (COH) __builtin_amdgcn_s_waitcnt(0);
   }
   __syncthreads();
 }
@@ -259,11 +234,6 @@ struct ItemLds {
   RedBuf red;
   StageBuf stage;
 };
-
-template <bool COH>
-__device__ __forceinline__ u32x4_t ld_tok(const uint16_t* p) {
-  return COH ? ld16_coh(p) : ldg16(p);
-}
 
 // ---------------------------------------------------------------------------
 // fp8 e4m3fn weights with 128x128 fp32 block scales, bf16 activations.  A
@@ -297,7 +267,7 @@ __device__ __forceinline__ void fp8x16_to_bf16(u32x4_t q, u32x4_t& lo, u32x4_t& 
 
 // As stream_bf16 for fp8 weights; s0 / s1: the tiles' scales, one per chunk
 // (absolute chunk index).
-template <bool COH, int D>
+template <int D>
 __device__ __forceinline__ void stream_fp8(const uint8_t* __restrict__ a0,
                                            const uint8_t* __restrict__ a1, size_t ld,
                                            const float* __restrict__ s0,
@@ -321,7 +291,7 @@ __device__ __forceinline__ void stream_fp8(const uint8_t* __restrict__ a0,
     q1l[d] = ldg16_stream(p1 + o);
     q1h[d] = ldg16_stream(p1 + ld8 + o);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) xb[d][m] = ld_tok<COH>(pb + o + m * 8);
+    for (int m = 0; m < 4; ++m) xb[d][m] = ldg16(pb + o + m * 8);
   };
   auto consume = [&](int d, int c) {
     st[wl] = q0l[d];
@@ -476,7 +446,6 @@ __device__ __forceinline__ G2Src g2_src(const ExpertW& W, const CallShape& c, in
 // gemm2: hidden rows tile2*32 .. +32 of `slot` against act -> w * partial,
 // w = the routing weight of a routed pair, 1 for a shared pair.
 // ---------------------------------------------------------------------------
-template <bool COH>
 __device__ __forceinline__ void g1_item_bf16(const uint16_t* __restrict__ x, const ExpertW& W,
                                              const CallShape& cs, int slot, int pair, int tile,
                                              uint16_t* __restrict__ act, ItemLds& l) {
@@ -491,7 +460,7 @@ __device__ __forceinline__ void g1_item_bf16(const uint16_t* __restrict__ x, con
                                c1 - c0, l.stage[wave], ag, au);
   l.red[wave][0][lane] = ag;
   l.red[wave][1][lane] = au;
-  g1_epilogue<COH>(l.red, pair, tile, cs.I, act);
+  g1_epilogue(l.red, pair, tile, cs.I, act);
 }
 
 __device__ __forceinline__ float pair_weight(const CallShape& cs, const float* __restrict__ tw,
@@ -499,7 +468,6 @@ __device__ __forceinline__ float pair_weight(const CallShape& cs, const float* _
   return pair < 0 ? 0.f : pair < cs.T * cs.k ? tw[pair] : 1.0f;
 }
 
-template <bool COH, bool COH_OUT = COH>
 __device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act, const ExpertW& W,
                                              const CallShape& cs, int slot, int pair, int tile2,
                                              const float* __restrict__ topk_w,
@@ -512,14 +480,13 @@ __device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act, c
   const uint16_t* a0 = (const uint16_t*)src.a0;
   const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
   f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = a;
-  stream_bf16<COH ? kTokCoh : kTokPlain, kG2D>(a0, a0 + 16 * src.ld, src.ld, ar, c0, c1 - c0,
-                                              l.stage[wave], a, b);
+  stream_bf16<kTokPlain, kG2D>(a0, a0 + 16 * src.ld, src.ld, ar, c0, c1 - c0, l.stage[wave], a,
+                               b);
   l.red[wave][0][lane] = a;
   l.red[wave][1][lane] = b;
-  g2_epilogue<COH_OUT>(l.red, pair, tile2, cs.H, pair_weight(cs, topk_w, pair), partial);
+  g2_epilogue(l.red, pair, tile2, cs.H, pair_weight(cs, topk_w, pair), partial);
 }
 
-template <bool COH>
 __device__ __forceinline__ void g1_item_fp8(const uint16_t* __restrict__ x, const ExpertW& W,
                                             const CallShape& cs, int slot, int pair, int tile,
                                             uint16_t* __restrict__ act, ItemLds& l) {
@@ -530,14 +497,13 @@ __device__ __forceinline__ void g1_item_fp8(const uint16_t* __restrict__ x, cons
   const G1Src src = g1_src<1>(W, cs, slot, tile);
   const uint16_t* xr = x + (size_t)(pair >= 0 ? pair_token(cs, pair) : 0) * H;
   f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
-  stream_fp8<false, kF8D>(src.gate, src.up, H, src.sg, src.su, xr, c0, c1 - c0, l.stage[wave],
+  stream_fp8<kF8D>(src.gate, src.up, H, src.sg, src.su, xr, c0, c1 - c0, l.stage[wave],
                           ag, au);
   l.red[wave][0][lane] = ag;
   l.red[wave][1][lane] = au;
-  g1_epilogue<COH>(l.red, pair, tile, cs.I, act);
+  g1_epilogue(l.red, pair, tile, cs.I, act);
 }
 
-template <bool COH, bool COH_OUT = COH>
 __device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act, const ExpertW& W,
                                             const CallShape& cs, int slot, int pair, int tile2,
                                             const float* __restrict__ topk_w,
@@ -549,35 +515,33 @@ __device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act, co
   const G2Src src = g2_src<1>(W, cs, slot, tile2);
   const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
   f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = a;
-  stream_fp8<COH, kF8D>(src.a0, src.a0 + 16 * src.ld, src.ld, src.sr, src.sr, ar, c0, c1 - c0,
+  stream_fp8<kF8D>(src.a0, src.a0 + 16 * src.ld, src.ld, src.sr, src.sr, ar, c0, c1 - c0,
                         l.stage[wave], a, b);
   l.red[wave][0][lane] = a;
   l.red[wave][1][lane] = b;
-  g2_epilogue<COH_OUT>(l.red, pair, tile2, cs.H, pair_weight(cs, topk_w, pair), partial);
+  g2_epilogue(l.red, pair, tile2, cs.H, pair_weight(cs, topk_w, pair), partial);
 }
 
 // ---------------------------------------------------------------------------
 // Staged kernels: grid-stride loops over a plan in global memory.
 // ---------------------------------------------------------------------------
-template <bool FP8, bool COH = false>
+template <bool FP8>
 __device__ __forceinline__ void run_g1(const uint16_t* x, const ExpertW& W, const CallShape& cs,
                                        int slot, int pair, int tile, uint16_t* act, ItemLds& l) {
   if (FP8)
-    g1_item_fp8<COH>(x, W, cs, slot, pair, tile, act, l);
+    g1_item_fp8(x, W, cs, slot, pair, tile, act, l);
   else
-    g1_item_bf16<COH>(x, W, cs, slot, pair, tile, act, l);
+    g1_item_bf16(x, W, cs, slot, pair, tile, act, l);
 }
 
-// COH: act is read with device-coherent loads (rows written by other
-// workgroups of the same launch); COH_OUT: partials are written through.
-template <bool FP8, bool COH = false, bool COH_OUT = COH>
+template <bool FP8>
 __device__ __forceinline__ void run_g2(const uint16_t* act, const ExpertW& W, const CallShape& cs,
                                        int slot, int pair, int tile2, const float* tw,
                                        float* partial, ItemLds& l) {
   if (FP8)
-    g2_item_fp8<COH, COH_OUT>(act, W, cs, slot, pair, tile2, tw, partial, l);
+    g2_item_fp8(act, W, cs, slot, pair, tile2, tw, partial, l);
   else
-    g2_item_bf16<COH, COH_OUT>(act, W, cs, slot, pair, tile2, tw, partial, l);
+    g2_item_bf16(act, W, cs, slot, pair, tile2, tw, partial, l);
 }
 
 template <bool FP8>
@@ -626,16 +590,12 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_kernel(const uint16_t* __r
 // memory once.
 constexpr int kMaxShared = 4;
 
-template <bool COH = false>
 __device__ __forceinline__ void combine4(const float* __restrict__ partial,
                                          const int32_t* __restrict__ valid, int t, int T, int k,
                                          int n_sh, int H, int h, float scale,
                                          const uint16_t* __restrict__ shared,
                                          uint16_t* __restrict__ out) {
-  auto ld = [&](int p) {
-    const float* src = partial + (size_t)p * H + h;
-    return COH ? __builtin_bit_cast(f32x4_t, ld16_coh(src)) : *reinterpret_cast<const f32x4_t*>(src);
-  };
+  auto ld = [&](int p) { return *reinterpret_cast<const f32x4_t*>(partial + (size_t)p * H + h); };
   f32x4_t v[SLUICE_MAX_TOPK], vs[kMaxShared];
   bool ok[SLUICE_MAX_TOPK];
   u32x2_t sh = {0u, 0u};
@@ -677,136 +637,33 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Fused persistent kernel (T*k <= kFusedMaxPairs).
-// ---------------------------------------------------------------------------
-// Work counters of the fused kernel (in the workspace; zero at rest):
-//   ctl[0]                      sticky error: a dependency wait ran out of time
-//   blk_done[kFusedMaxPairs]    gemm1 tiles finished, per block
-//   blk_used[kFusedMaxPairs]    gemm2 items finished, per block
-//   tile_done[H / 32]           gemm2 items finished, per 32-column slice
-// Each counter is returned to zero by the last item that uses it (the last
-// gemm2 item of a block, the combining item of a slice), with device-scope
-// atomics only, so no global "all done" count is needed and no address is
-// hit by every workgroup.
-constexpr int kCtlInts = 32;
-
-// Grid-stride over the items (gemm1 items first), with every workgroup of
-// the grid resident at once (the host sizes the grid from the kernel's
-// occupancy): a gemm2 item only waits for gemm1 items, which never wait.
-template <bool FP8>
-__global__ __launch_bounds__(kThreads) void moe_fused_kernel(
-    const uint16_t* __restrict__ x, ExpertW W, const float* __restrict__ topk_w,
-    const int32_t* __restrict__ ids, const int32_t* __restrict__ map, int P, int H, int I, int k,
-    int E, int S, float scale, const uint16_t* __restrict__ shared, uint16_t* __restrict__ out,
-    int32_t* __restrict__ ctl, uint16_t* __restrict__ act, float* __restrict__ partial,
-    long long timeout_ticks) {
-  __shared__ AlignScratch sc;
-  __shared__ int32_t s_blocks[kFusedMaxPairs * kBlockInts];
-  __shared__ int32_t s_valid[kFusedMaxPairs];
-  __shared__ ItemLds lds;
-  __shared__ int s_last_blk, s_last_tile;
-  int32_t* blk_done = ctl + kCtlInts;
-  int32_t* blk_used = blk_done + kFusedMaxPairs;
-  int32_t* tile_done = blk_used + kFusedMaxPairs;
-  const int tid = threadIdx.x;
-  const int col = tid & 15;
-  const int T = P / k;
-  const CallShape cs{T, k, H, I};
-
-  const int nb = build_plan(ids, P, map, E, S, T, 0, sc, s_blocks, s_valid);
-  const int n1t = I / 16, n2t = H / (16 * kG2T);
-  const int N1 = nb * n1t, N = N1 + nb * n2t;
-
-  if (nb == 0) {
-    // nothing resident: out = scale * 0 + shared
-    for (int i = blockIdx.x * kThreads + tid; i < T * (H / 4); i += gridDim.x * kThreads) {
-      const int t = i / (H / 4), h = (i - t * (H / 4)) * 4;
-      combine4(partial, s_valid, t, T, k, 0, H, h, scale, shared, out);
-    }
-    return;
-  }
-  for (int item = blockIdx.x; item < N; item += gridDim.x) {
-    if (item < N1) {
-      const int b = item / n1t, tile = item - b * n1t;
-      const int32_t* blk = s_blocks + b * kBlockInts;
-      const int pair = col < blk[1] ? blk[2 + col] : -1;
-      run_g1<FP8, true>(x, W, cs, blk[0], pair, tile, act, lds);
-      // the act rows went out with device-coherent stores, completed before
-      // the epilogue's barrier
-      if (tid == 0) atomicAdd(&blk_done[b], 1);
-      continue;
-    }
-    const int j = item - N1;
-    const int b = j / n2t, tile2 = j - b * n2t;
-    if (tid == 0) {
-      const long long t0 = wall_clock64();
-      while (__hip_atomic_load(&blk_done[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < n1t) {
-        if (wall_clock64() - t0 > timeout_ticks) {
-          atomicExch(&ctl[0], 1);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(8);
-      }
-    }
-    __syncthreads();
-    // act is read with device-coherent loads after the counter was seen
-    const int32_t* blk = s_blocks + b * kBlockInts;
-    const int pair = col < blk[1] ? blk[2 + col] : -1;
-    run_g2<FP8, true>(act, W, cs, blk[0], pair, tile2, topk_w, partial, lds);
-    if (tid == 0) {
-      s_last_tile = atomicAdd(&tile_done[tile2], 1) == nb - 1;
-      s_last_blk = atomicAdd(&blk_used[b], 1) == n2t - 1;
-      if (s_last_blk) {
-        // every gemm2 item of this block has passed its wait
-        atomicExch(&blk_done[b], 0);
-        atomicExch(&blk_used[b], 0);
-      }
-    }
-    __syncthreads();
-    if (s_last_tile) {
-      // every block's partials for this 32-column slice are written
-      const int h0 = tile2 * 16 * kG2T;
-      for (int i = tid; i < T * (16 * kG2T / 4); i += kThreads) {
-        const int t = i / (16 * kG2T / 4), h = h0 + (i - t * (16 * kG2T / 4)) * 4;
-        combine4<true>(partial, s_valid, t, T, k, 0, H, h, scale, shared, out);
-      }
-      if (tid == 0) atomicExch(&tile_done[tile2], 0);
-    }
-    __syncthreads();
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 struct Workspace {
-  int32_t* ctl;
   int32_t* plan;
   uint16_t* act;
   float* partial;
 };
 
-// [ctl + counters | plan | act [P2, I] bf16 | partial [P2, H] fp32], P2 =
-// T*k routed + n_sh*T shared pairs.  The counter region has a fixed size, so
-// calls of any shape that share the workspace never write over each other's
-// counters.
+// [plan | act [P2, I] bf16 | partial [P2, H] fp32], P2 = T*k routed +
+// n_sh*T shared pairs.  Every call writes what it reads (align writes the
+// whole plan, gemm1 the act rows of the planned pairs, gemm2 their partials;
+// the combine adds only valid pairs), so the workspace needs no clearing and
+// holds nothing between calls.
 size_t workspace_bytes(int T, int H, int I, int k, int n_sh, Workspace* ws, void* base) {
   const int P = T * k + n_sh * T;
-  const size_t ctl_b =
-      align_up((kCtlInts + 2 * kFusedMaxPairs + (size_t)kFusedMaxHidden / (16 * kG2T)) * 4, 256);
   const size_t plan_b = align_up(plan_ints(P) * sizeof(int32_t), 256);
   const size_t act_b = align_up((size_t)P * I * sizeof(uint16_t), 256);
   const size_t part_b = align_up((size_t)P * H * sizeof(float), 256);
   if (ws != nullptr) {
     char* b = (char*)base;
-    ws->ctl = (int32_t*)b;
-    ws->plan = (int32_t*)(b + ctl_b);
-    ws->act = (uint16_t*)(b + ctl_b + plan_b);
-    ws->partial = (float*)(b + ctl_b + plan_b + act_b);
+    ws->plan = (int32_t*)b;
+    ws->act = (uint16_t*)(b + plan_b);
+    ws->partial = (float*)(b + plan_b + act_b);
   }
-  return ctl_b + plan_b + act_b + part_b;
+  return plan_b + act_b + part_b;
 }
 
 #ifndef SLUICE_GRID_CAP
@@ -818,38 +675,12 @@ int grid_for(int P, int n_tiles) {
   return (int)(items < cap ? (items > 0 ? items : 1) : cap);
 }
 
-struct DevInfo {
-  int cus = 0;
-  long long clock_khz = 0;
-  int fused_per_cu[2] = {0, 0};  // resident fused workgroups per CU (bf16, fp8)
-};
-DevInfo g_info[64];
-
-int dev_info(DevInfo** out) {
-  int dev = 0;
-  SLUICE_HIP_CHECK(hipGetDevice(&dev));
-  if (dev < 0 || dev >= 64) return SLUICE_E_INVAL;
-  DevInfo& d = g_info[dev];
-  if (d.cus == 0) {
-    int cus = 0, khz = 0;
-    SLUICE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    SLUICE_HIP_CHECK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
-    d.clock_khz = khz > 0 ? khz : 100000;
-    d.cus = cus > 0 ? cus : 256;
-  }
-  *out = &d;
-  return SLUICE_OK;
-}
-
-#ifndef SLUICE_FUSED_WG_PER_CU
-#define SLUICE_FUSED_WG_PER_CU 4
-#endif
-
+// The align kernel stages the map of all E experts in LDS (AlignScratch).
 int check_common(int T, int H, int I, int k, int E, int S, int n_sh, const void* x,
                  const void* w13, const void* w2, const float* tw, const int32_t* ti,
                  const void* shared, void* ws, size_t ws_bytes, void* out) {
-  if (T < 0 || H <= 0 || I <= 0 || k <= 0 || k > SLUICE_MAX_TOPK || E <= 0 || S <= 0 ||
-      S > SLUICE_MAX_SLOTS)
+  if (T < 0 || H <= 0 || I <= 0 || k <= 0 || k > SLUICE_MAX_TOPK || E <= 0 ||
+      E > SLUICE_MAX_EXPERTS || S <= 0 || S > SLUICE_MAX_SLOTS)
     return SLUICE_E_INVAL;
   if ((long)T * k > SLUICE_MAX_PAIRS) return SLUICE_E_INVAL;
   if (n_sh < 0 || n_sh > kMaxShared || (long)T * (k + n_sh) > SLUICE_MAX_PAIRS)
@@ -872,47 +703,13 @@ int launch_combine(const float* partial, const int32_t* valid, int T, int k, int
   return (int)hipGetLastError();
 }
 
-int& fused_flag() {
-  static int v = [] {
-    const char* s = getenv("SLUICE_MOE_FUSED");
-    return (s != nullptr && s[0] == '1') ? 1 : 0;
-  }();
-  return v;
-}
-int fused_enabled() { return __atomic_load_n(&fused_flag(), __ATOMIC_RELAXED); }
-
 template <bool FP8>
 int run_experts(const void* x, const ExpertW& W, const float* tw, const int32_t* ti,
                 const int32_t* map, int T, int H, int I, int k, int E, int S, int n_sh,
                 float scale, const void* shared, void* workspace, void* out, hipStream_t st) {
   Workspace w;
   workspace_bytes(T, H, I, k, n_sh, &w, workspace);
-  const int P = T * k, P2 = P + n_sh * T;
-  // The fused kernel is opt-in (SLUICE_MOE_FUSED=1): its cross-workgroup
-  // hand-offs need agent-scope cache maintenance that costs more than the
-  // three kernel boundaries it removes.
-  if (n_sh == 0 && P <= kFusedMaxPairs && H <= kFusedMaxHidden && fused_enabled() != 0) {
-    DevInfo* di = nullptr;
-    int rc = dev_info(&di);
-    if (rc) return rc;
-    const long upper = (long)P * (I / 16 + H / (16 * kG2T));  // items with nb <= P
-    int& per_cu = di->fused_per_cu[FP8 ? 1 : 0];
-    if (per_cu == 0) {
-      int n = 0;
-      SLUICE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &n, reinterpret_cast<const void*>(&moe_fused_kernel<FP8>), kThreads, 0));
-      per_cu = n > 0 ? n : 1;
-    }
-    // every workgroup resident at once (a gemm2 item waits for gemm1 items)
-    long grid = (long)di->cus * (per_cu < SLUICE_FUSED_WG_PER_CU ? per_cu : SLUICE_FUSED_WG_PER_CU);
-    if (grid > upper) grid = upper;
-    if (grid < 1) grid = 1;
-    const long long ticks = (long long)(2.0 * 1000.0 * (double)di->clock_khz);
-    hipLaunchKernelGGL((moe_fused_kernel<FP8>), dim3((unsigned)grid), dim3(kThreads), 0, st,
-                       (const uint16_t*)x, W, tw, ti, map, P, H, I, k, E, S, scale,
-                       (const uint16_t*)shared, (uint16_t*)out, w.ctl, w.act, w.partial, ticks);
-    return (int)hipGetLastError();
-  }
+  const int P2 = T * k + n_sh * T;
   const CallShape cs{T, k, H, I};
   hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kThreads), 0, st, ti, T, k, map, E, S, n_sh,
                      w.plan);
@@ -954,21 +751,9 @@ extern "C" size_t sluice_fused_experts_workspace(int T, int H, int I, int k, int
   return workspace_bytes(T, H, I, k, n_sh, nullptr, nullptr);
 }
 
-extern "C" int sluice_moe_set_fused(int enable) {
-  return __atomic_exchange_n(&fused_flag(), enable ? 1 : 0, __ATOMIC_RELAXED);
-}
-
-extern "C" int sluice_fused_experts_status(const void* workspace, int* error_out) {
-  if (workspace == nullptr || error_out == nullptr) return SLUICE_E_INVAL;
-  int32_t ctl[kCtlInts];
-  SLUICE_HIP_CHECK(hipMemcpy(ctl, workspace, sizeof(ctl), hipMemcpyDeviceToHost));
-  *error_out = ctl[0];
-  return SLUICE_OK;
-}
-
 extern "C" int sluice_moe_align(const int32_t* topk_ids, int T, int k, const int32_t* expert_map,
                                 int E, int S, int32_t* plan, sluice_stream_t stream) {
-  if (T < 0 || k <= 0 || E <= 0 || S <= 0 || S > SLUICE_MAX_SLOTS ||
+  if (T < 0 || k <= 0 || E <= 0 || E > SLUICE_MAX_EXPERTS || S <= 0 || S > SLUICE_MAX_SLOTS ||
       (long)T * k > SLUICE_MAX_PAIRS || plan == nullptr)
     return SLUICE_E_INVAL;
   hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, topk_ids,

@@ -86,8 +86,7 @@ class _Workspace:
                 raise RuntimeError(
                     "sluice fused_experts workspace too small during graph capture; call "
                     "sluice_amd.ops.reserve_workspace(...) before capturing")
-            # zero-filled: the fused kernel's work counters start (and end) at 0
-            cur = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            cur = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
             self.buf[idx] = cur
         return cur
 

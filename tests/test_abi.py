@@ -58,6 +58,18 @@ def test_invalid_arguments_rejected_without_touching_the_gpu(lib):
                                          None) == _lib.SLUICE_E_INVAL
         assert lib.sluice_moe_gemm2_bf16(None, None, None, None, 1, H, I, 8, None,
                                          None) == _lib.SLUICE_E_INVAL
+    # more experts than the align kernel stages in LDS: refused before any
+    # launch (pointers are aligned stand-ins; nothing may dereference them)
+    fake = 1 << 20
+    E_big = _lib.MAX_EXPERTS + 1
+    assert lib.sluice_moe_align(fake, 1, 8, fake, E_big, 8, fake, None) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_fused_experts_bf16(fake, fake, fake, fake, fake, fake, 1, 2048, 1408, 8,
+                                         E_big, 8, 1.0, None, None, 0, None, fake, 1 << 30, fake,
+                                         None) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_fused_experts_fp8(fake, fake, fake, fake, fake, 128, 128, fake, fake, fake,
+                                        1, 2048, 1408 // 128 * 128, 8, E_big, 8, 1.0, None, None,
+                                        None, None, 0, None, fake, 1 << 30, fake,
+                                        None) == _lib.SLUICE_E_INVAL
     h = ctypes.c_void_p()
     assert lib.sluice_layer_create(64, 64, 0, 0, None, None, ctypes.byref(h)) == _lib.SLUICE_E_INVAL
     assert lib.sluice_layer_create(2048, 64, 8, 4, None, None,

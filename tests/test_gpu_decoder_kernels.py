@@ -142,7 +142,8 @@ def test_add_rmsnorm_gate_matches_the_two_kernels(rows, H, E, delta, bias):
 
 @pytest.mark.parametrize("T,H,K,E", [(8, 2048, 4096, 128), (1, 2048, 4096, 128),
                                      (12, 2048, 2048, 64), (16, 2048, 8192, 128),
-                                     (4, 1040, 4096, 8)])
+                                     (4, 1040, 4096, 8), (8, 4096, 2048, 128),
+                                     (8, 7168, 2048, 256), (3, 7168, 4096, 256)])
 def test_linear_split_parts_into_the_fused_norm(T, H, K, E):
     """A projection left as its K parts and summed by the fused norm gives the
     same residual, hn and logits, bit for bit, as bf16(in-order sum of the

@@ -107,31 +107,17 @@ def test_fused_experts_bf16(T, H, I, E, S, k):
     assert err <= BF16_TOL
 
 
-def test_fused_experts_bf16_staged_path_for_large_batches():
-    """T*k above the fused kernel's limit runs the staged kernels."""
+def test_fused_experts_bf16_large_batch():
+    """A prefill-sized call (40 tokens, 320 pairs)."""
     got, ref = _moe_case(40, 256, 64, 32, 16, 8, seed=21)
     assert om.rel_l2(got, ref) <= BF16_TOL
 
 
-@pytest.mark.parametrize("fused", [1, 0])
-def test_fused_experts_deterministic_and_counters_back_at_zero(fused):
-    """Both launch shapes (one persistent kernel; four staged kernels):
-    identical calls give identical bits (the combine order does not depend on
-    which workgroup finishes last), the persistent kernel's work counters are
-    back at zero with no timed-out dependency wait, and the result matches
-    the oracle."""
-    import ctypes
+def test_fused_experts_deterministic():
+    """Identical calls give identical bits (every pair's sum is reduced in a
+    fixed order), and the result matches the oracle."""
+    from sluice_amd import ops
 
-    from sluice_amd import _lib, ops
-
-    prev = _lib.load().sluice_moe_set_fused(fused)
-    try:
-        _deterministic_case(ctypes, _lib, ops)
-    finally:
-        _lib.load().sluice_moe_set_fused(prev)
-
-
-def _deterministic_case(ctypes, _lib, ops):
     rng = np.random.default_rng(5)
     T, H, I, E, S, k = 8, 2048, 768, 128, 32, 8
     x = _bf16(rng.standard_normal((T, H))).to(DEV)
@@ -144,10 +130,6 @@ def _deterministic_case(ctypes, _lib, ops):
             for _ in range(3)]
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
-    ws = ops._WS.buf[DEV.index or 0]
-    err = ctypes.c_int(-1)
-    rc = _lib.load().sluice_fused_experts_status(ws.data_ptr(), ctypes.byref(err))
-    assert rc == 0 and err.value == 0
     ref = om.fused_experts(x.float().cpu().numpy(), w13.float().cpu().numpy(),
                            w2.float().cpu().numpy(), tw.cpu().numpy(), ids.cpu().numpy(),
                            expert_map=emap.cpu().numpy())
