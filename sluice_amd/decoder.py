@@ -266,7 +266,7 @@ def add_rmsnorm(x, delta, w, out=None, eps=_EPS):
 # One zero-filled workspace per device for the skinny GEMMs' split-K hand-off
 # (its size does not depend on the shape; the calls of a step run one after
 # another on one stream).
-_LIN_WS = ops._Workspace()
+_LIN_WS = ops._Workspace(zero=True)  # split-K counters start (and end) at zero
 
 
 def _linear_ws(dev):

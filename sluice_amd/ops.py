@@ -73,10 +73,14 @@ def select_experts(router_logits: torch.Tensor, top_k: int, *, scoring: str = "s
 class _Workspace:
     """One grow-only device workspace per device, shared by every layer (the
     layers run one after another on one stream).  reserve() sizes it ahead of
-    graph capture so captured launches bake a pointer that never moves."""
+    graph capture so captured launches bake a pointer that never moves.
+    ``zero``: the buffer is zero-filled when (re)allocated, for kernels that
+    keep counters in it; the expert product's workspace needs no initial
+    contents."""
 
-    def __init__(self):
+    def __init__(self, zero: bool = False):
         self.buf: dict[int, torch.Tensor] = {}
+        self.zero = zero
 
     def get(self, device: torch.device, nbytes: int) -> torch.Tensor:
         idx = device.index if device.index is not None else torch.cuda.current_device()
@@ -86,7 +90,8 @@ class _Workspace:
                 raise RuntimeError(
                     "sluice fused_experts workspace too small during graph capture; call "
                     "sluice_amd.ops.reserve_workspace(...) before capturing")
-            cur = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            alloc = torch.zeros if self.zero else torch.empty
+            cur = alloc(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
             self.buf[idx] = cur
         return cur
 
