@@ -37,6 +37,7 @@ typedef struct ihipStream_t* sluice_stream_t; /* == hipStream_t */
 #define SLUICE_E_NOMEM (-4)    /* host allocation failed */
 #define SLUICE_E_STATE (-5)    /* object used in a state it does not allow */
 #define SLUICE_E_ABORTED (-6)  /* a device gap wait ended by the abort flag */
+#define SLUICE_E_SCRATCH (-7)  /* call too large for the no-alloc entry's scratch */
 
 /* Kernel limits (checked on the host before every launch). */
 #define SLUICE_MAX_EXPERTS 1024  /* global experts E per layer */
@@ -155,6 +156,28 @@ int sluice_fused_experts_bf16(const void* x, const void* w13, const void* w2,
                               int shared_I, const void* shared, void* workspace,
                               size_t workspace_bytes, void* out,
                               sluice_stream_t stream);
+
+/* No-allocation variant of sluice_fused_experts_bf16 (same arguments minus
+ * the workspace, same kernels, bit-identical results).  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * hipGraph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Its scratch is a fixed device array of SLUICE_NOALLOC_SCRATCH_BYTES in the
+ * library, one per GPU, held until the process ends; the call allocates and
+ * frees nothing.  Calls needing more than that
+ * (sluice_fused_experts_workspace(T, H, I, k, shared_I) bytes) return
+ * SLUICE_E_SCRATCH before any device work.  The scratch needs no initial
+ * contents; every call on a GPU shares that GPU's copy, so calls that overlap
+ * on one GPU (different streams or threads) race and must be serialised by
+ * the caller.  The current device must be the one x, the weights and stream
+ * belong to.  The first call on a device looks the scratch's address up. */
+#define SLUICE_NOALLOC_SCRATCH_BYTES (8u << 20)
+int sluice_fused_experts_bf16_noalloc(const void* x, const void* w13, const void* w2,
+                                      const float* topk_w, const int32_t* topk_ids,
+                                      const int32_t* expert_map, int T, int H, int I,
+                                      int k, int E, int S, float scale,
+                                      const void* shared_w13, const void* shared_w2,
+                                      int shared_I, const void* shared, void* out,
+                                      sluice_stream_t stream);
 
 int sluice_fused_experts_fp8(const void* x, const void* w13,
                              const float* w13_scale, const void* w2,

@@ -22,6 +22,8 @@ SLUICE_E_TIMEOUT = -3
 SLUICE_E_NOMEM = -4
 SLUICE_E_STATE = -5
 SLUICE_E_ABORTED = -6
+SLUICE_E_SCRATCH = -7
+NOALLOC_SCRATCH_BYTES = 8 << 20  # SLUICE_NOALLOC_SCRATCH_BYTES
 
 MAX_EXPERTS = 1024
 MAX_SLOTS = 512
@@ -48,6 +50,11 @@ SIGNATURES = {
         c_int,
         [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P, c_int,
          _P, _P, c_size_t, _P, _P],
+    ),
+    "sluice_fused_experts_bf16_noalloc": (
+        c_int,
+        [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P, c_int,
+         _P, _P, _P],
     ),
     "sluice_fused_experts_fp8": (
         c_int,

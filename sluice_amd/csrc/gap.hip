@@ -1252,6 +1252,9 @@ extern "C" const char* sluice_strerror(int code) {
     case SLUICE_E_NOMEM: return "host allocation failed";
     case SLUICE_E_STATE: return "object used in a state it does not allow";
     case SLUICE_E_ABORTED: return "gap aborted after an earlier error";
+    case SLUICE_E_SCRATCH:
+      return "the call needs more scratch than sluice_fused_experts_bf16_noalloc holds "
+             "(SLUICE_NOALLOC_SCRATCH_BYTES); use sluice_fused_experts_bf16 with a workspace";
     default:
       if (code > 0) return hipGetErrorString((hipError_t)code);
       return "unknown sluice error";

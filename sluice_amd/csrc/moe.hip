@@ -20,8 +20,17 @@
 // slower than these four launches and is not kept.)
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 #include "stream.h"
+
+// Scratch of sluice_fused_experts_bf16_noalloc (align plan, activations, fp32
+// partials), for callers that cannot allocate.  Every GPU the library runs on
+// holds its own copy until the process ends; host code reaches it only
+// through the per-device address hipGetSymbolAddress returns (the name
+// itself is not a device address in host code).
+static __device__ __align__(256) uint8_t scratch[SLUICE_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -736,6 +745,27 @@ int shared_groups(int shared_I, int I, const void* sw13, const void* sw2, int* n
   return SLUICE_OK;
 }
 
+// The device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_ptr(void** out) {
+  int dev = 0;
+  SLUICE_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return SLUICE_E_INVAL;
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    SLUICE_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (p == nullptr) return SLUICE_E_STATE;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SLUICE_OK;
+}
+
 // Weights of the per-stage entry points: every block's slot is routed.
 ExpertW routed_only(const uint8_t* w13, const uint8_t* w2, const float* s13, const float* s2) {
   return ExpertW{w13, w2, s13, s2, nullptr, nullptr, nullptr, nullptr, 0x7fffffff, 0};
@@ -779,6 +809,33 @@ extern "C" int sluice_fused_experts_bf16(const void* x, const void* w13, const v
                   shared_I};
   return run_experts<false>(x, W, topk_w, topk_ids, expert_map, T, H, I, k, E, S, n_sh, scale,
                             shared, workspace, out, (hipStream_t)stream);
+}
+
+extern "C" int sluice_fused_experts_bf16_noalloc(
+    const void* x, const void* w13, const void* w2, const float* topk_w,
+    const int32_t* topk_ids, const int32_t* expert_map, int T, int H, int I, int k, int E, int S,
+    float scale, const void* shared_w13, const void* shared_w2, int shared_I, const void* shared,
+    void* out, sluice_stream_t stream) {
+  int n_sh = 0;
+  int rc = shared_groups(shared_I, I, shared_w13, shared_w2, &n_sh);
+  if (rc != SLUICE_OK) return rc;
+  // Every check runs before the scratch is looked up, so a refused call
+  // touches no device state.
+  if (T > 0 && H > 0 && I > 0 && k > 0 && (long)T * (k + n_sh) <= SLUICE_MAX_PAIRS &&
+      workspace_bytes(T, H, I, k, n_sh, nullptr, nullptr) > SLUICE_NOALLOC_SCRATCH_BYTES)
+    return SLUICE_E_SCRATCH;
+  // (the workspace argument is an aligned stand-in for the scratch)
+  rc = check_common(T, H, I, k, E, S, n_sh, x, w13, w2, topk_w, topk_ids, shared,
+                    reinterpret_cast<void*>(uintptr_t{256}), SLUICE_NOALLOC_SCRATCH_BYTES, out);
+  if (rc != SLUICE_OK || T == 0) return rc;
+  void* ws = nullptr;
+  rc = scratch_ptr(&ws);
+  if (rc != SLUICE_OK) return rc;
+  const ExpertW W{(const uint8_t*)w13, (const uint8_t*)w2, nullptr, nullptr,
+                  (const uint8_t*)shared_w13, (const uint8_t*)shared_w2, nullptr, nullptr, S,
+                  shared_I};
+  return run_experts<false>(x, W, topk_w, topk_ids, expert_map, T, H, I, k, E, S, n_sh, scale,
+                            shared, ws, out, (hipStream_t)stream);
 }
 
 extern "C" int sluice_fused_experts_fp8(const void* x, const void* w13, const float* w13_scale,
