@@ -379,6 +379,13 @@ int sluice_layer_policy_state(const sluice_layer* layer, int64_t* freq,
                               int64_t* counts_decode, int64_t* counts_scan,
                               int64_t* stats);
 
+/* Classic-step stats by class, as the reference's get_stats() buckets them
+ * (src/sluice/offloader.py:172-183, 1656-1684, 1711-1713, 1887, 2804-2814):
+ * out[8] = {small: steps, hits, misses, waves, scan: steps, hits, misses,
+ * waves}, real steps only ("small" = pure decode).  Bytes streamed are
+ * misses x bytes per expert. */
+int sluice_layer_step_stats(const sluice_layer* layer, int64_t* out);
+
 /* State snapshot.  Arrays may be NULL.  slot_of [local_n] (-1 = absent),
  * expert_in_slot [S] (-1 = empty), probation/protected in recency order
  * (LRU first), free_slots in list order (the last is popped next).

@@ -102,6 +102,7 @@ SIGNATURES = {
     "sluice_layer_classic_plan_read": (c_int, [_P, _P, c_int, POINTER(c_int), _P]),
     "sluice_layer_set_policy": (c_int, [_P, c_int, c_int]),
     "sluice_layer_policy_state": (c_int, [_P, _P, _P, _P, _P]),
+    "sluice_layer_step_stats": (c_int, [_P, _P]),
     # include/sluice_decoder.h
     "sluice_dec_add_rmsnorm": (c_int, [_P, _P, _P, _P, c_int, c_int, c_float, _P]),
     "sluice_dec_silu_mul": (c_int, [_P, _P, c_int, c_int, _P]),

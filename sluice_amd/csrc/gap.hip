@@ -1150,6 +1150,21 @@ extern "C" int sluice_layer_policy_state(const sluice_layer* Lc, int64_t* freq,
   return SLUICE_OK;
 }
 
+extern "C" int sluice_layer_step_stats(const sluice_layer* Lc, int64_t* out) {
+  if (Lc == nullptr || out == nullptr) return SLUICE_E_INVAL;
+  sluice_layer* L = const_cast<sluice_layer*>(Lc);
+  std::lock_guard<std::mutex> lk(L->mu);
+  const slru::Cache& c = L->c;
+  const int64_t steps[2] = {c.steps_small, c.steps_scan};
+  for (int k = 0; k < 2; ++k) {
+    out[4 * k + 0] = steps[k];
+    out[4 * k + 1] = c.cls_hits[k];
+    out[4 * k + 2] = c.cls_misses[k];
+    out[4 * k + 3] = c.cls_waves[k];
+  }
+  return SLUICE_OK;
+}
+
 extern "C" int sluice_layer_state(const sluice_layer* Lc, int32_t* slot_of, int32_t* expert_in_slot,
                                   int32_t* probation, int* n_probation, int32_t* protected_,
                                   int* n_protected, int32_t* free_slots, int* n_free,

@@ -88,6 +88,10 @@ struct Cache {
   int lfu_steps = 0;
   std::vector<int64_t> cnt_decode, cnt_scan;  // [E]
   int64_t steps_small = 0, steps_scan = 0;
+  // Real classic steps by class (0 = pure decode "small", 1 = "scan"): hit
+  // and missed local experts and waves run, as the reference's per-class
+  // step stats count them (src/sluice/offloader.py:1656-1684, 1711-1713, 1887).
+  int64_t cls_hits[2] = {0, 0}, cls_misses[2] = {0, 0}, cls_waves[2] = {0, 0};
 
   // scratch reused across gaps and classic steps
   struct Pair {
@@ -374,9 +378,11 @@ struct Cache {
     map_is_standing = false;
     plan.open_wave();
     if (ws == 0) return 0;
+    int cls = -1;  // the step's stats class; dummy runs have none
     if (real_step) {
       const bool pure_decode = have_dec ? nd == T : friendly;
       ++(pure_decode ? steps_small : steps_scan);
+      cls = pure_decode ? 0 : 1;
       if (lfu) {
         for (const Pair& p : cl_pairs) bump_freq(p.local);
         age_freq();
@@ -412,7 +418,14 @@ struct Cache {
       claimed[slot] = 1;
     }
     misses += (int64_t)cl_missing.size();
-    if (taken == cl_missing.size()) return 0;
+    if (cls >= 0) {
+      cls_hits[cls] += (int64_t)(cl_pairs.size() - cl_missing.size());
+      cls_misses[cls] += (int64_t)cl_missing.size();
+    }
+    if (taken == cl_missing.size()) {
+      if (cls >= 0) ++cls_waves[cls];
+      return 0;
+    }
     // Leftover misses rotate through the probation slots split in two
     // groups (ping-pong); with no probation slot, through the last S/4
     // unpinned slots.  Protected slots are never rotated (1855-1890).
@@ -440,6 +453,7 @@ struct Cache {
         plan.add_stream(p.local, slot);
       }
     }
+    if (cls >= 0) cls_waves[cls] += (int64_t)plan.waves.size();
     return 0;
   }
 

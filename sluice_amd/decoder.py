@@ -142,7 +142,10 @@ class SyntheticMoELayer(nn.Module):
         self.routing_bias = routing_bias
         self.scoring, self.renorm, self.routed_scale = scoring, renorm, routed_scale
         self.n_group, self.topk_group = n_group, topk_group
+        _router_attrs(self, scoring, renorm, routed_scale, n_group, topk_group)
         self.shared = _SharedMLP(H, shared_I, dev, dtype, gen) if shared_I else None
+        # the last router logits (the gate records them); ids and weights when
+        # vLLM's select_experts stand-in routed the step (the stock path)
         self.last_logits = self.last_ids = self.last_weights = None
 
         layer = self
@@ -151,6 +154,7 @@ class SyntheticMoELayer(nn.Module):
             logits = F.linear(hs, layer.gate.weight).float()
             if layer.routing_bias is not None:
                 logits = logits + layer.routing_bias(hs.shape[0])
+            layer.last_logits, layer.last_ids, layer.last_weights = logits, None, None
             return logits, None
 
         def select_experts(hidden_states, router_logits, input_ids=None):
@@ -180,6 +184,20 @@ class SyntheticMoELayer(nn.Module):
             sh, routed = r
             return routed + sh
         return r
+
+
+def _router_attrs(layer, scoring, renorm, routed_scale, n_group, topk_group):
+    """The router settings under vLLM's FusedMoE attribute names, which the
+    offloader maps onto the routing kernel (grouped top-k when the experts
+    are split into groups; the correction bias is the layer's
+    e_score_correction_bias)."""
+    layer.scoring_func = scoring
+    layer.renormalize = renorm
+    layer.use_grouped_topk = n_group > 1
+    layer.num_expert_group = n_group
+    layer.topk_group = topk_group
+    layer.routed_scaling_factor = routed_scale
+    layer.custom_routing_function = None
 
 
 @contextlib.contextmanager
@@ -550,6 +568,8 @@ class _StoreMoELayer(nn.Module):
                            else _DenseMLP(H, sp["shared_I"], dev, g))
         self.routing_bias = routing_bias
         self.sp = sp
+        _router_attrs(self, sp["scoring"], sp["renorm"], sp["routed_scale"], sp["n_group"],
+                      sp["topk_group"])
 
         # vLLM runner surface, so attach_router_split arms this layer
         layer = self

@@ -1,34 +1,31 @@
 """Routing-aware MoE expert streaming offloader, router-split path, on MI355X.
 
-Mirrors the reference's ``ExpertStreamOffloader`` (src/sluice/offloader.py)
-for the router-split decode path: the same lifecycle (``wrap_modules`` ->
-``post_init`` -> ``attach_model``), the same env flags, the same slot-buffer
-and expert-map layout, the same ``vllm::sluice_stream_gap`` op and traced
-``_forward_entry``.  Underneath, the per-layer slot cache and the gap run in
-libsluice_hip.so: a device slot-lookup kernel publishes the step's selected
-experts into pinned host memory, the native SLRU assigns slots exactly as the
-reference's OrderedDict state machine does, missing experts stream with
-hipMemcpyAsync on a dedicated copy stream, and a map kernel rewrites the
-standing expert map the captured expert product reads by pointer.
+The drop-in for the reference's ``ExpertStreamOffloader``
+(src/sluice/offloader.py:186-2814) on the router-split decode path: the same
+lifecycle (``wrap_modules`` -> ``post_init`` -> ``attach_model``), env flags,
+slot-buffer and expert-map layout, ``vllm::sluice_stream_gap`` op and
+patched ``runner._forward_entry``.  Underneath, the per-layer slot cache and
+the gap are native (libsluice_hip.so): a device kernel publishes the step's
+selected experts into pinned host memory, the native SLRU assigns slots as
+the reference's OrderedDict state machine does, missing experts stream with
+hipMemcpyAsync on a dedicated copy stream, and the device installs the
+standing expert map that the captured expert product reads by pointer.
 
 Execution model per MoE layer per decode step (T <= thr tokens):
 
-    gate + select_experts            [capturable]
-    -> vllm::sluice_stream_gap       [eager gap: lookup, wait, SLRU, H2D, map]
-    -> sluice::fused_experts         [capturable; slots + map by pointer]
-    -> shared experts                [capturable]
+    gate + sluice::select_experts     [capturable; wave64 top-k kernel]
+    -> vllm::sluice_stream_gap        [gap: lookup, SLRU, H2D, map]
+    -> sluice::fused_experts          [capturable; slots + map by pointer]
+    -> shared experts                 [capturable]
 
 Steps above the envelope (more tokens than slots // top_k: prefill chunks,
-large decode batches) take the classic path instead, as in the reference
-(src/sluice/offloader.py:1452-1933): the layer's ``quant_method.apply`` is
-wrapped so that ``run_moe`` syncs the ids once, the native slot cache plans
-the step -- one wave when the working set fits, else wave 0 (hits + fills)
-and the leftover misses rotated through the probation slots in ping-pong
-groups -- and the expert product runs once per wave against that wave's
-map, its row copies overlapping the previous wave's product on the copy
-stream; wave outputs are summed in fp32.
+large decode batches) take the stock path, whose ``quant_method.apply`` the
+offloader wraps (src/sluice/offloader.py:1085-1122, 1452-1933): the native
+planner syncs the ids once, plans one wave when the working set fits, else
+wave 0 (hits + fills) and the leftover misses rotated through the probation
+slots in ping-pong groups, and the expert product runs once per wave
+against that wave's map; wave outputs are summed in fp32.
 """
-
 
 import atexit
 import ctypes
@@ -38,7 +35,7 @@ import os
 import time
 from collections.abc import Generator
 from dataclasses import dataclass, field
-from typing import Optional
+from typing import Any, Optional
 
 import torch
 import torch.nn as nn
@@ -47,7 +44,9 @@ from sluice_amd import _lib, ops
 
 logger = logging.getLogger("sluice")
 
-# Shared/global tensors, not per-expert weights (src/sluice/offloader.py:89-96).
+# Layer parameters with an expert dimension that are shared by every expert
+# (correction bias, input scales, a hash-routing table), so never streamed
+# (src/sluice/offloader.py:89-96).
 NON_EXPERT_WEIGHTS = frozenset(
     {"e_score_correction_bias", "w13_input_scale", "w2_input_scale", "hash_indices_table"}
 )
@@ -55,7 +54,6 @@ NON_EXPERT_WEIGHTS = frozenset(
 PROTECT_FRAC_ENV = "SLUICE_PROTECT_FRAC"
 ROUTER_SPLIT_ENV = "SLUICE_ROUTER_SPLIT"
 PIECEWISE_ENV = "SLUICE_PIECEWISE"
-GRAPH_ENV = "SLUICE_GRAPH"
 FAST_HIT_ENV = "SLUICE_RS_FAST_HIT"
 NOOP_ENV = "SLUICE_RS_NOOP"
 # Opt-in policies (src/sluice/offloader.py:97-118): LFU-ordered protected
@@ -65,6 +63,27 @@ LFU_ENV = "SLUICE_LFU"
 COUNTS_DIR_ENV = "SLUICE_EXPERT_COUNTS"
 COUNTS_EVERY_ENV = "SLUICE_EXPERT_COUNTS_EVERY"
 PIN_FILE_ENV = "SLUICE_PIN_FILE"
+
+# Graph split points under piecewise capture: the MoE ops (whose apply runs
+# the classic hook, which syncs the host) and the gap op.
+_MOE_SPLIT_OPS = ("vllm::moe_forward", "vllm::moe_forward_shared")
+_GAP_SPLIT_OP = "vllm::sluice_stream_gap"
+
+try:  # vLLM's offloader base, when vLLM is installed (its isinstance checks)
+    from vllm.model_executor.offloader.base import BaseOffloader as _OffloaderBase  # type: ignore
+except Exception:  # noqa: BLE001 - vLLM absent or a different layout
+    _OffloaderBase = object
+
+
+def _env_flag(name: str) -> bool:
+    return os.environ.get(name, "0") == "1"
+
+
+def _env_number(name: str, default, cast):
+    try:
+        return cast(os.environ.get(name, default))
+    except (TypeError, ValueError):
+        return default
 
 
 @dataclass
@@ -144,6 +163,16 @@ class _ExpertLayerCache:
         return {"gaps": c[0], "misses": c[1], "fast_hits": c[2], "map_writes": c[3],
                 "bytes": c[4] | (c[5] << 32)}
 
+    def step_stats(self) -> dict:
+        """Real classic steps of this layer by class ("small" = pure decode,
+        "scan"): steps, hit and missed local experts, waves."""
+        out = (ctypes.c_int64 * 8)()
+        _lib.check(_lib.load().sluice_layer_step_stats(self.handle, out),
+                   "sluice_layer_step_stats")
+        keys = ("steps", "hits", "misses", "waves")
+        return {kind: {k: int(out[4 * i + j]) for j, k in enumerate(keys)}
+                for i, kind in enumerate(("small", "scan"))}
+
     def policy_state(self) -> dict:
         """LFU frequencies (local -> count, nonzero only), per-global
         decode/scan selection counts and the classic step classes."""
@@ -164,7 +193,278 @@ class _ExpertLayerCache:
         return self.policy_state()["freq"]
 
 
-class ExpertStreamOffloader:
+# ---------------------------------------------------------------------------
+# What the offloader reads from a layer and from the engine
+# ---------------------------------------------------------------------------
+def _expert_counts(module: nn.Module) -> Optional[tuple[int, int]]:
+    """(global, local) expert counts of a FusedMoE-like layer (it carries
+    both counts and a quant method), else None."""
+    if not hasattr(module, "quant_method"):
+        return None
+    g = getattr(module, "global_num_experts", None)
+    l = getattr(module, "local_num_experts", None)
+    if g is None or l is None:
+        return None
+    return int(g), int(l)
+
+
+def _streamed_params(module: nn.Module, local_n: int) -> dict:
+    """The layer's own parameters with one row per local expert, except the
+    ones every expert shares: what streams per expert."""
+    out = {}
+    for name, p in module.named_parameters(recurse=False):
+        per_expert = p.dim() > 0 and p.shape[0] == local_n
+        if per_expert and name not in NON_EXPERT_WEIGHTS:
+            out[name] = p
+    return out
+
+
+def _module_device(module: nn.Module) -> torch.device:
+    """Where the layer's resident tensors live (the current GPU when all of
+    them are still on the host)."""
+    tensors = [*module.parameters(recurse=False), *module.buffers(recurse=False)]
+    devices = {t.device for t in tensors if t is not None and t.device.type != "cpu"}
+    if devices:
+        return next(iter(devices))
+    return torch.device("cuda", torch.cuda.current_device() if torch.cuda.is_available() else 0)
+
+
+@dataclass
+class _EngineView:
+    """The parts of a vLLM engine config the offloader acts on."""
+
+    top_k: Optional[int] = None            # hf num_experts_per_tok
+    max_batched_tokens: Optional[int] = None
+    spec_tokens: int = 0                   # speculative draft depth
+    compilation: Any = None                # compilation_config (splitting_ops)
+
+
+def _engine_view(cfg) -> _EngineView:
+    view = _EngineView()
+    model = getattr(cfg, "model_config", None)
+    hf = getattr(model, "hf_config", None)
+    # multimodal checkpoints keep the language model's fields in text_config
+    for src in (hf, getattr(hf, "text_config", None)):
+        k = getattr(src, "num_experts_per_tok", None) if src is not None else None
+        if k:
+            view.top_k = int(k)
+            break
+    sched = getattr(cfg, "scheduler_config", None)
+    mbt = getattr(sched, "max_num_batched_tokens", None)
+    view.max_batched_tokens = int(mbt) if mbt is not None else None
+    spec = getattr(cfg, "speculative_config", None)
+    try:
+        view.spec_tokens = max(int(getattr(spec, "num_speculative_tokens", 0) or 0), 0)
+    except (TypeError, ValueError):
+        view.spec_tokens = 0
+    view.compilation = getattr(cfg, "compilation_config", None)
+    return view
+
+
+def _current_engine_config():
+    """vLLM's current config; None when vLLM is not installed (the standalone
+    harness drives the offloader).  An installed vLLM whose config cannot be
+    read is an error: the router-split envelope could not be checked."""
+    try:
+        from vllm.config import get_current_vllm_config  # type: ignore
+    except ImportError:
+        return None
+    try:
+        cfg = get_current_vllm_config()
+    except Exception as e:  # noqa: BLE001
+        raise RuntimeError("Sluice: reading the vLLM engine config failed, so the expert-cache "
+                           "settings cannot be checked; not starting.") from e
+    if cfg is None:
+        raise RuntimeError("Sluice: the vLLM engine config is None, so the expert-cache settings "
+                           "cannot be checked; not starting.")
+    return cfg
+
+
+def _engine_step_signal() -> tuple:
+    """(decode tokens, decode requests, real step) of the running step from
+    vLLM's forward context (src/sluice/offloader.py:1766-1800): (None, None,
+    False) for a dummy or profiling run without attention metadata; decode
+    counts None when the backend publishes none."""
+    try:
+        from vllm.forward_context import get_forward_context  # type: ignore
+
+        meta = getattr(get_forward_context(), "attn_metadata", None)
+    except Exception:  # noqa: BLE001 - no engine, or no context set
+        return None, None, False
+    if isinstance(meta, dict):  # per-layer metadata: every layer agrees
+        meta = next(iter(meta.values()), None)
+    if meta is None:
+        return None, None, False
+
+    def as_int(v):
+        try:
+            return None if v is None else int(v)
+        except (TypeError, ValueError):
+            return None
+
+    nd = as_int(getattr(meta, "num_decode_tokens", None))
+    if nd is None:
+        return None, None, True
+    return nd, as_int(getattr(meta, "num_decodes", None)), True
+
+
+def _process_rank() -> int:
+    try:
+        import torch.distributed as dist
+
+        if dist.is_available() and dist.is_initialized():
+            return dist.get_rank()
+    except Exception:  # noqa: BLE001
+        pass
+    return _env_number("RANK", 0, int)
+
+
+class _CountsJournal:
+    """Per-expert selection counts of real classic steps, appended as one
+    JSONL record per streaming layer every ``every`` hook ticks and at exit,
+    to <directory>/expert_counts_rank<r>.jsonl.  The record keys are the
+    reference's format (src/sluice/offloader.py:1399-1448).  Writing never
+    raises: profiling must not take serving down."""
+
+    def __init__(self, directory: str, every: int):
+        self.directory = directory
+        self.every = max(every, 1)
+        self.ticks = 0
+        self.snapshots = 0
+        self._file = None
+
+    def tick(self, layers) -> None:
+        self.ticks += 1
+        if self.ticks % self.every == 0:
+            self.write(layers, final=False)
+
+    def write(self, layers, final: bool) -> None:
+        layers = [c for c in layers if not c.static_full and c.handle]
+        if not layers:
+            return
+        try:
+            if self._file is None:
+                os.makedirs(self.directory, exist_ok=True)
+                path = os.path.join(self.directory, f"expert_counts_rank{_process_rank()}.jsonl")
+                self._file = open(path, "a")
+            self.snapshots += 1
+            states = [c.policy_state() for c in layers]
+            totals = {"steps_small": sum(p["steps_small"] for p in states),
+                      "steps_scan": sum(p["steps_scan"] for p in states)}
+            for cache, pol in zip(layers, states):
+                record = {
+                    "snap": self.snapshots, "final": final, "ts": time.time(),
+                    "hook_calls": self.ticks, **totals,
+                    "layer": cache.ordinal, "layer_name": cache.layer_name,
+                    "n_global": len(pol["counts_decode"]),
+                    "decode": {str(g): n for g, n in enumerate(pol["counts_decode"]) if n},
+                    "scan": {str(g): n for g, n in enumerate(pol["counts_scan"]) if n},
+                }
+                self._file.write(json.dumps(record) + "\n")
+            self._file.flush()
+        except Exception:  # noqa: BLE001
+            logger.exception("Sluice: writing the expert-count snapshot failed; serving goes on.")
+
+
+class _ClassicHook:
+    """Takes the place of a layer's ``quant_method.apply``: calls that carry
+    the step's routing (``layer`` and ``topk_ids``) go through the
+    offloader's classic step; anything else goes straight to the original."""
+
+    def __init__(self, offloader: "ExpertStreamOffloader", original):
+        self.offloader = offloader
+        self.original = original
+
+    def __call__(self, *args, **kwargs):
+        layer = kwargs["layer"] if "layer" in kwargs else (args[0] if args else None)
+        topk_ids = kwargs.get("topk_ids")
+        if layer is None or topk_ids is None:
+            return self.original(*args, **kwargs)
+        return self.offloader.run_moe(self.original, args, kwargs, layer, topk_ids)
+
+
+# ---------------------------------------------------------------------------
+# Routing settings of a layer -> the wave64 top-k kernel
+# ---------------------------------------------------------------------------
+@dataclass(frozen=True)
+class RouteSpec:
+    """Arguments of ``sluice::select_experts`` equivalent to a layer's router."""
+
+    top_k: int
+    scoring: str = "softmax"
+    renormalize: bool = False
+    scale: float = 1.0
+    n_group: int = 1
+    topk_group: int = 1
+    bias: Optional[torch.Tensor] = None
+
+
+def route_spec(module: nn.Module, runner=None) -> tuple[Optional[RouteSpec], str]:
+    """Map a layer's router settings, read under vLLM's FusedMoE attribute
+    names (on ``runner.router`` first, then on the layer), onto the routing
+    kernel.  Returns (spec, "") or (None, reason) when the kernel cannot
+    express the router exactly; such layers keep vLLM's select_experts.
+
+    vLLM's select_experts (called at src/sluice/offloader.py:2583-2585) runs
+    softmax top-k (``fused_topk``: selection on the logits, optional
+    renormalisation, no scaling) or, with ``use_grouped_topk``,
+    ``grouped_topk``: softmax or sigmoid scores, a group score that is the
+    group's largest score without a correction bias and the sum of its two
+    largest biased scores with one, the ``topk_group`` best groups eligible,
+    renormalisation, then ``routed_scaling_factor``.  The kernel fixes the
+    group score by the scoring (softmax: max; sigmoid + bias: top-2 sum), so
+    the combinations it computes exactly are the ones accepted below."""
+    router = getattr(runner, "router", None) if runner is not None else None
+
+    def attr(name, default=None):
+        for src in (router, module):
+            if src is not None and hasattr(src, name):
+                v = getattr(src, name)
+                if v is not None:
+                    return v
+        return default
+
+    top_k = attr("top_k")
+    if top_k is None:
+        mc = getattr(runner, "moe_config", None) if runner is not None else None
+        top_k = getattr(mc, "experts_per_token", None)
+    if top_k is None:
+        return None, "router:no-top_k"
+    top_k = int(top_k)
+    n_experts = int(attr("global_num_experts", 0) or 0)
+    if not 0 < top_k <= _lib.MAX_TOPK or not 0 < n_experts <= _lib.MAX_EXPERTS:
+        return None, "router:shape"
+    if attr("custom_routing_function") is not None:
+        return None, "router:custom"
+    if attr("apply_router_weight_on_input", False):
+        return None, "router:weight-on-input"
+    if getattr(module, "hash_indices_table", None) is not None:
+        return None, "router:hash"
+    scoring = str(attr("scoring_func", "softmax"))
+    if scoring not in ("softmax", "sigmoid"):
+        return None, f"router:scoring-{scoring}"
+    bias = attr("e_score_correction_bias")
+    renorm = bool(attr("renormalize", False))
+    if not attr("use_grouped_topk", False):
+        if scoring != "softmax" or bias is not None:
+            return None, "router:ungrouped-sigmoid-or-bias"
+        return RouteSpec(top_k, "softmax", renorm), ""
+    n_group = int(attr("num_expert_group", 1) or 1)
+    topk_group = int(attr("topk_group", 1) or 1)
+    if n_group < 1 or n_experts % n_group or not 1 <= topk_group <= n_group:
+        return None, "router:groups"
+    scale = float(attr("routed_scaling_factor", 1.0) or 1.0)
+    if scoring == "softmax" and bias is not None:
+        return None, "router:softmax-bias"
+    if scoring == "sigmoid" and bias is None and n_group > 1:
+        return None, "router:sigmoid-no-bias"
+    return RouteSpec(top_k, scoring, renorm, scale, n_group, topk_group, bias), ""
+
+
+# ---------------------------------------------------------------------------
+# The offloader
+# ---------------------------------------------------------------------------
+class ExpertStreamOffloader(_OffloaderBase):
     """Stream routed-expert weights host->HBM per decode step, by routing.
 
     Args:
@@ -172,250 +472,146 @@ class ExpertStreamOffloader:
     """
 
     def __init__(self, expert_cache_slots: int):
-        assert expert_cache_slots > 0
+        if expert_cache_slots <= 0:
+            raise ValueError("expert_cache_slots must be positive")
         self.expert_cache_slots = expert_cache_slots
-        try:
-            frac = float(os.environ.get(PROTECT_FRAC_ENV, "0.5"))
-        except ValueError:
-            frac = 0.5
+        frac = _env_number(PROTECT_FRAC_ENV, 0.5, float)
         self.protect_frac = min(max(frac, 0.0), 0.9)
-        self.piecewise = os.environ.get(PIECEWISE_ENV, "0") == "1"
-        self.router_split = os.environ.get(ROUTER_SPLIT_ENV, "0") == "1"
-        self.graph_mode = os.environ.get(GRAPH_ENV, "0") == "1"
-        self._rs_fast_hit = os.environ.get(FAST_HIT_ENV, "0") == "1"
-        self._rs_noop = os.environ.get(NOOP_ENV, "0") == "1"
+        self.piecewise = _env_flag(PIECEWISE_ENV)
+        self.router_split = _env_flag(ROUTER_SPLIT_ENV)
+        self._rs_fast_hit = _env_flag(FAST_HIT_ENV)
+        self._rs_noop = _env_flag(NOOP_ENV)
         if self._rs_noop:
-            logger.warning("Sluice: SLUICE_RS_NOOP=1 — the router-split gap is a NO-OP; "
-                           "OUTPUTS ARE INVALID (stale expert map). Perf diagnostic only.")
+            logger.warning("Sluice: %s=1 turns the gap into a no-op for timing; the expert map "
+                           "goes stale and layer outputs are WRONG.", NOOP_ENV)
         self.pin_memory = torch.cuda.is_available()
+        self.lfu = _env_flag(LFU_ENV)
         self._caches: dict[int, _ExpertLayerCache] = {}
         self._layers: list[nn.Module] = []
         self._prepared_stores: dict[int, list] = {}  # pinned stores made before load
         self._rs_caches: list[_ExpertLayerCache] = []
         self._rs_gaps = 0
-        self._rs_misses = 0
-        self._rs_fast_hits = 0
         self._rs_layers = 0
         self._rs_thr: Optional[int] = None
+        self._rs_routes: list = []  # per armed layer: RouteSpec or None (vLLM routes)
         self._server: Optional[int] = None
         self._spec_tokens = 0
         self._signal: Optional[tuple] = None
         self._warned_waves = False
-        self.lfu = os.environ.get(LFU_ENV, "0") == "1"
-        # expert-count profiling (src/sluice/offloader.py:441-465, 1393-1448)
         self._counts_dir = os.environ.get(COUNTS_DIR_ENV) or None
-        self._counts_every = 5000
-        self._counts_calls = 0
-        self._counts_snap = 0
-        self._counts_file = None
+        self._counts: Optional[_CountsJournal] = None
         if self._counts_dir:
-            try:
-                self._counts_every = max(int(os.environ.get(COUNTS_EVERY_ENV, "5000")), 1)
-            except ValueError:
-                self._counts_every = 5000
+            self._counts = _CountsJournal(self._counts_dir,
+                                          _env_number(COUNTS_EVERY_ENV, 5000, int))
             atexit.register(self._dump_expert_counts, True)
-        # static pins (src/sluice/offloader.py:466-481): parsed here, applied
-        # per layer at install; a malformed file fails loudly
         self._pin_layers: Optional[dict] = None
         self._pin_stats = [0, 0]  # experts pinned, layers with pins
         pin_path = os.environ.get(PIN_FILE_ENV)
         if pin_path:
-            with open(pin_path) as f:
-                raw = json.load(f)
-            layers = raw.get("layers", raw)
-            self._pin_layers = {int(k_): [int(g) for g in v] for k_, v in layers.items()}
-            logger.info("Sluice: static pin file %s (%d layers listed).", pin_path,
-                        len(self._pin_layers))
+            self._pin_layers = _read_pin_file(pin_path)
         if self.router_split:
             _register_stream_gap_op(self)
-        logger.info("Sluice ExpertStreamOffloader enabled (%d cache slots per layer, "
-                    "protect_frac=%.2f).", expert_cache_slots, self.protect_frac)
+        logger.info("Sluice: offloader on, %d HBM expert slots per MoE layer "
+                    "(protect_frac %.2f).", expert_cache_slots, self.protect_frac)
 
     # -- model construction -------------------------------------------------
-    @staticmethod
-    def _is_moe_layer(module: nn.Module) -> bool:
-        return (hasattr(module, "local_num_experts") and hasattr(module, "global_num_experts")
-                and hasattr(module, "quant_method"))
-
-    @staticmethod
-    def _per_expert_params(module: nn.Module, local_n: int) -> dict:
-        return {
-            name: p for name, p in module.named_parameters(recurse=False)
-            if name not in NON_EXPERT_WEIGHTS and p.dim() >= 1 and p.shape[0] == local_n
-        }
-
     def wrap_modules(self, modules_generator: Generator) -> list:
+        """Pass the model's modules through, moving every MoE layer's
+        per-expert params to host memory before the checkpoint loads."""
         modules = []
         for module in modules_generator:
             for sub in module.modules():
-                if self._is_moe_layer(sub):
+                if _expert_counts(sub) is not None:
                     self._prepare_layer(sub)
             modules.append(module)
         return modules
 
     def _prepare_layer(self, module: nn.Module) -> None:
-        """Move a layer's (still empty) per-expert params to host memory so
-        the checkpoint loads there (src/sluice/offloader.py:554-571).  With a
-        GPU present they become views of exact-size pinned host stores, so
-        the loader writes straight into the memory the expert rows stream
-        from, and _install_cache adopts it without a second host copy."""
+        """A layer's (still empty) per-expert params become host tensors
+        before the checkpoint loads (src/sluice/offloader.py:554-571).  With a
+        GPU present they are views of exact-size pinned host stores, so the
+        loader writes straight into the memory the expert rows stream from,
+        and _install_cache adopts it without a second host copy.  Layers whose
+        kernel does not read the expert map (monolithic quant methods, the
+        ROCm AITER fused MoE) stay as they are."""
         qm = module.quant_method
-        if qm is None or getattr(qm, "is_monolithic", False):
+        if qm is None or getattr(qm, "is_monolithic", False) or getattr(
+                module, "rocm_aiter_fmoe_enabled", False):
             return
-        if getattr(module, "rocm_aiter_fmoe_enabled", False):
+        _, local_n = _expert_counts(module)
+        params = _streamed_params(module, local_n)
+        if not params:
             return
-        local_n = int(module.local_num_experts)
-        per_expert = self._per_expert_params(module, local_n)
-        if not per_expert:
-            return
-        for p in per_expert.values():
-            cpu = p.data if p.data.device.type == "cpu" else p.data.to("cpu")
-            if self.pin_memory and ops.host_store_of(cpu) is None:
-                store = ops.HostStore(tuple(cpu.shape), cpu.dtype)
-                store.tensor.copy_(cpu)
+        for p in params.values():
+            host = p.data.to("cpu") if p.data.device.type != "cpu" else p.data
+            if self.pin_memory and ops.host_store_of(host) is None:
+                store = ops.HostStore(tuple(host.shape), host.dtype)
+                store.tensor.copy_(host)
                 self._prepared_stores.setdefault(id(module), []).append(store)
-                cpu = store.tensor
-            p.data = cpu
-        if all(id(module) != id(m) for m in self._layers):
+                host = store.tensor
+            p.data = host
+        if not any(m is module for m in self._layers):
             self._layers.append(module)
 
     # -- after load -----------------------------------------------------------
     def post_init(self, config=None) -> None:
-        self._check_config(config)
+        """Apply the engine settings, then install every prepared layer's slot
+        cache and classic hook (src/sluice/offloader.py:575-657)."""
+        cfg = config if config is not None else _current_engine_config()
+        if cfg is not None:
+            self._apply_engine(_engine_view(cfg))
         if torch.cuda.is_available():
             torch.cuda.synchronize()
         for module in self._layers:
             self._install_cache(module)
-            self._wrap_apply(module)
-        # SLUICE_GRAPH relaxed the eager guard on the promise that every
-        # layer is static-full (a constant map is safe to capture)
-        if self.graph_mode:
-            streaming = [k_ for k_, c in self._caches.items() if not c.static_full]
-            if streaming:
-                raise RuntimeError(
-                    "Sluice: SLUICE_GRAPH=1 requires every layer to be static_full (slots >= "
-                    f"local experts), but {len(streaming)} layer(s) are streaming. A captured "
-                    "graph would freeze a changing expert map. Raise SLUICE_SLOTS to full "
-                    "residency or unset SLUICE_GRAPH.")
+            self._install_classic_hook(module)
+        streaming = [c for c in self._caches.values() if not c.static_full]
         if self._caches:
-            host = sum(c.bytes_per_expert * c.local_num_experts for c in self._caches.values()
-                       if not c.static_full)
-            vram = sum(c.bytes_per_expert * c.num_slots for c in self._caches.values())
-            logger.info("Sluice: %d MoE layers ready — host expert store %.1f GiB%s, HBM slot "
-                        "cache %.1f GiB.", len(self._caches), host / 2**30,
-                        " (pinned)" if self.pin_memory else " (pageable)", vram / 2**30)
+            host = sum(c.bytes_per_expert * c.local_num_experts for c in streaming)
+            hbm = sum(c.bytes_per_expert * c.num_slots for c in self._caches.values())
+            logger.info("Sluice: %d MoE layers (%d streaming); %.1f GiB of experts in %s host "
+                        "memory, %.1f GiB of HBM slots.", len(self._caches), len(streaming),
+                        host / 2**30, "pinned" if self.pin_memory else "pageable", hbm / 2**30)
 
-    def _check_config(self, cfg=None) -> None:
-        """The engine-configuration guards (src/sluice/offloader.py:663-851).
-
-        With vLLM installed the config must be readable (fail closed); without
-        vLLM (the standalone harness) there is nothing to check unless a
-        config object is passed in.  Refuses DP > 1 and EPLB (this build
-        serves one rank's experts and owns the expert map), and any CUDA-graph
-        mode that would capture the streaming hook: eager is required unless
-        SLUICE_PIECEWISE (the hook runs in a graph break; FULL capture is
-        still refused) or SLUICE_GRAPH (every layer static-full, checked in
-        post_init).  Under piecewise it makes the MoE ops and the gap op
-        graph split points and enforces the router-split envelope: the whole
-        batch must fit slots // top_k tokens.  Records the speculative depth
-        the decode classifier needs."""
-        if cfg is None:
-            try:
-                from vllm.config import get_current_vllm_config  # type: ignore
-            except ImportError:
-                return  # no engine: the standalone harness drives the offloader
-            try:
-                cfg = get_current_vllm_config()
-            except Exception as e:
-                raise RuntimeError("Sluice: could not read the vLLM config to verify it is safe "
-                                   "(DP/EPLB/eager); refusing to run. This usually means an "
-                                   "unexpected vLLM version.") from e
-            if cfg is None:
-                raise RuntimeError("Sluice: vLLM config is None; cannot verify a safe "
-                                   "configuration (DP/EPLB/eager). Refusing to run.")
-        pc = getattr(cfg, "parallel_config", None)
-        if pc is not None:
-            if (getattr(pc, "data_parallel_size", 1) or 1) > 1:
-                raise RuntimeError("Sluice (MI355X build): data parallelism > 1 is not supported "
-                                   "(one rank's expert shard per process; no post-dispatch "
-                                   "seam).")
-            if getattr(pc, "enable_eplb", False):
-                raise RuntimeError("Sluice: EPLB is unsupported (it re-registers the expert map "
-                                   "buffer over Sluice's slot map).")
-        relax_eager = self.graph_mode or self.piecewise
-        mc = getattr(cfg, "model_config", None)
-        if mc is not None and not getattr(mc, "enforce_eager", False) and not relax_eager:
+    def _apply_engine(self, view: _EngineView) -> None:
+        """What the engine config decides (src/sluice/offloader.py:786-851):
+        the speculative depth the decode classifier needs; under piecewise
+        capture, the split points that keep the hooks eager; and under
+        router-split, the token threshold slots // top_k, which must bound
+        every batch, since the traced entry's size branch is fixed at trace
+        time."""
+        self._spec_tokens = view.spec_tokens
+        if not self.piecewise:
+            return
+        cc = view.compilation
+        if cc is not None:
+            wanted = list(_MOE_SPLIT_OPS) + ([_GAP_SPLIT_OP] if self.router_split else [])
+            have = list(getattr(cc, "splitting_ops", None) or [])
+            cc.splitting_ops = have + [op for op in wanted if op not in have]
+        if not self.router_split:
+            return
+        thr = max(1, self.expert_cache_slots // (view.top_k or 8))
+        self._rs_thr = thr
+        mbt = view.max_batched_tokens
+        if mbt is not None and mbt > thr:
+            # the message is a contract: operators act on it
             raise RuntimeError(
-                "Sluice: requires eager execution — run with --enforce-eager. Without it, "
-                "CUDA-graph capture freezes a stale expert map (silently wrong output) and stock "
-                "torch.compile skips the post_init that installs Sluice's expert cache. (Set "
-                "SLUICE_GRAPH=1 only with slots >= experts / static_full.)")
-        cc = getattr(cfg, "compilation_config", None)
-        cg = getattr(cc, "cudagraph_mode", None) if cc is not None else None
-        cg_name = getattr(cg, "name", str(cg)) if cg is not None else "NONE"
-        if self.piecewise and "FULL" in cg_name:
-            raise RuntimeError(
-                "Sluice: SLUICE_PIECEWISE requires PIECEWISE cudagraph (the hook runs eager in a "
-                f"graph break); got {cg_name}. FULL would try to capture the hook's D2H sync.")
-        if cg is not None and cg_name != "NONE" and not relax_eager:
-            raise RuntimeError(
-                "Sluice: CUDA graphs would capture a frozen expert map and replay it with stale "
-                "routing (silently wrong outputs). Run with enforce_eager (--enforce-eager).")
-        if self.piecewise and cc is not None:
-            # the MoE layer (whose apply runs the hook) and the gap op are
-            # eager gaps between the captured pieces
-            ops_ = list(getattr(cc, "splitting_ops", None) or [])
-            wanted = ["vllm::moe_forward", "vllm::moe_forward_shared"]
-            if self.router_split:
-                wanted.append("vllm::sluice_stream_gap")
-            cc.splitting_ops = ops_ + [op for op in wanted if op not in ops_]
-        if self.router_split and self.piecewise:
-            topk = 8
-            hf = getattr(mc, "hf_config", None) if mc is not None else None
-            for src in (hf, getattr(hf, "text_config", None)):
-                v = getattr(src, "num_experts_per_tok", None) if src else None
-                if v:
-                    topk = int(v)
-                    break
-            thr = max(1, self.expert_cache_slots // topk)
-            self._rs_thr = thr
-            sched = getattr(cfg, "scheduler_config", None)
-            mbt = getattr(sched, "max_num_batched_tokens", None)
-            if mbt is not None and mbt > thr:
-                raise RuntimeError(
-                    "Sluice router-split under piecewise compiles a single trace whose size "
-                    "branch is resolved at trace time; the whole batch envelope must fit it. "
-                    f"Got max_num_batched_tokens={mbt} > slots//topk={thr}. Set "
-                    f"--max-num-batched-tokens {thr} (prefill runs in {thr}-token chunks) or "
-                    "raise SLUICE_SLOTS.")
-        # A speculative-decode request verifies 1 + k tokens: its decode
-        # region spans ndec * (1 + k) rows (src/sluice/offloader.py:843-851).
-        sc = getattr(cfg, "speculative_config", None)
-        k_spec = getattr(sc, "num_speculative_tokens", 0) if sc is not None else 0
-        try:
-            self._spec_tokens = max(int(k_spec or 0), 0)
-        except (TypeError, ValueError):
-            self._spec_tokens = 0
-
-    @staticmethod
-    def _infer_device(module: nn.Module) -> torch.device:
-        for t in list(module.parameters(recurse=False)) + list(module.buffers(recurse=False)):
-            if t is not None and t.device.type != "cpu":
-                return t.device
-        idx = torch.cuda.current_device() if torch.cuda.is_available() else 0
-        return torch.device("cuda", idx)
+                "Sluice router-split under piecewise compiles a single trace whose size "
+                "branch is resolved at trace time; the whole batch envelope must fit it. "
+                f"Got max_num_batched_tokens={mbt} > slots//topk={thr}. Set "
+                f"--max-num-batched-tokens {thr} (prefill runs in {thr}-token chunks) or "
+                "raise SLUICE_SLOTS.")
 
     def _install_cache(self, module: nn.Module) -> None:
         """Slot buffers [S, ...] as the live params, a pinned host store of
         every local expert, the expert map and the native slot cache
         (src/sluice/offloader.py:895-1044)."""
         lib = _lib.load()
-        local_n = int(module.local_num_experts)
-        global_n = int(module.global_num_experts)
-        per_expert = self._per_expert_params(module, local_n)
+        global_n, local_n = _expert_counts(module)
+        per_expert = _streamed_params(module, local_n)
         if not per_expert:
             return
-        device = self._infer_device(module)
+        device = _module_device(module)
         num_slots = min(self.expert_cache_slots, local_n)
         protected_cap = max(min(int(num_slots * self.protect_frac), num_slots - 1), 0)
         cache = _ExpertLayerCache(local_num_experts=local_n, num_slots=num_slots,
@@ -475,9 +671,9 @@ class ExpertStreamOffloader:
                 _lib.check(lib.sluice_layer_add_param(cache.handle, slot_t.data_ptr(),
                                                       host_t.data_ptr(), host_t[0].nbytes),
                            "sluice_layer_add_param")
-            if self.lfu or self._counts_dir:
+            if self.lfu or self._counts is not None:
                 _lib.check(lib.sluice_layer_set_policy(cache.handle, int(self.lfu),
-                                                       int(bool(self._counts_dir))),
+                                                       int(self._counts is not None)),
                            "sluice_layer_set_policy")
             if self._pin_layers is not None:
                 self._apply_pins(cache, cache.ordinal)
@@ -500,9 +696,8 @@ class ExpertStreamOffloader:
         resident = set(cache.slot_of)
         for g in wanted:
             if n >= budget:
-                logger.warning("Sluice: layer %d pin list (%d ids) exceeds the protected budget "
-                               "(%d); pinning the first %d only.", ordinal, len(wanted), budget,
-                               n)
+                logger.warning("Sluice: MoE layer %d lists %d pins but its protected budget is "
+                               "%d; the first %d are pinned.", ordinal, len(wanted), budget, n)
                 break
             if not (0 <= g < len(cache.local_of)):
                 continue
@@ -523,73 +718,25 @@ class ExpertStreamOffloader:
             self._pin_stats[1] += 1
 
     # -- expert-count profiling ---------------------------------------------------
-    def _counts_tick(self) -> None:
-        self._counts_calls += 1
-        if self._counts_calls % self._counts_every == 0:
-            self._dump_expert_counts(False)
-
     def _dump_expert_counts(self, final: bool) -> None:
-        """Append one cumulative JSONL snapshot per streaming layer (nonzero
-        counts only, keyed by global expert id) to
-        <SLUICE_EXPERT_COUNTS>/expert_counts_rank<r>.jsonl, in the
-        reference's record format (src/sluice/offloader.py:1399-1448).  Never
-        raises: profiling must not take serving down."""
-        if not self._counts_dir:
-            return
-        layers = [c for c in self._caches.values() if not c.static_full and c.handle]
-        if not layers:
-            return
-        try:
-            if self._counts_file is None:
-                try:
-                    import torch.distributed as dist
-
-                    rank = dist.get_rank() if dist.is_initialized() else 0
-                except Exception:
-                    rank = int(os.environ.get("RANK", "0") or "0")
-                os.makedirs(self._counts_dir, exist_ok=True)
-                self._counts_file = open(
-                    os.path.join(self._counts_dir, f"expert_counts_rank{rank}.jsonl"), "a")
-            self._counts_snap += 1
-            pols = [c.policy_state() for c in layers]
-            small = sum(p["steps_small"] for p in pols)
-            scan = sum(p["steps_scan"] for p in pols)
-            for c, p in zip(layers, pols):
-                self._counts_file.write(json.dumps({
-                    "snap": self._counts_snap, "final": final, "ts": time.time(),
-                    "hook_calls": self._counts_calls, "steps_small": small, "steps_scan": scan,
-                    "layer": c.ordinal, "layer_name": c.layer_name,
-                    "n_global": len(p["counts_decode"]),
-                    "decode": {str(g): v for g, v in enumerate(p["counts_decode"]) if v},
-                    "scan": {str(g): v for g, v in enumerate(p["counts_scan"]) if v},
-                }) + "\n")
-            self._counts_file.flush()
-        except Exception:
-            logger.exception("Sluice: expert-count dump failed (non-fatal)")
+        if self._counts is not None:
+            self._counts.write(list(self._caches.values()), final)
 
     # -- classic (wave) path -------------------------------------------------
-    def _wrap_apply(self, module: nn.Module) -> None:
-        """Wrap the layer's ``quant_method.apply`` so steps that reach it
-        (the ones the router-split entry hands to the stock path) run the
-        classic hook (src/sluice/offloader.py:1085-1119)."""
-        qm = module.quant_method
-        if qm is None or getattr(qm, "_sluice_wrapped", False) or not hasattr(qm, "apply"):
+    def _install_classic_hook(self, module: nn.Module) -> None:
+        """Route the layer's ``quant_method.apply`` (the stock path that
+        steps above the router-split envelope take) through the classic hook
+        (src/sluice/offloader.py:1085-1122).  Under piecewise capture the hook
+        runs outside any traced region, since it syncs the host."""
+        qm = getattr(module, "quant_method", None)
+        if qm is None or getattr(qm, "_sluice_hook", None) is not None:
             return
-        original_apply = qm.apply
-        offloader = self
-
-        def apply(*args, **kwargs):
-            layer = kwargs.get("layer", args[0] if args else None)
-            topk_ids = kwargs.get("topk_ids")
-            if layer is None or topk_ids is None:
-                return original_apply(*args, **kwargs)
-            return offloader.run_moe(original_apply, args, kwargs, layer, topk_ids)
-
-        if self.piecewise:
-            # the hook syncs the host: keep it out of any traced region
-            apply = torch._dynamo.disable(apply)
-        qm.apply = apply
-        qm._sluice_wrapped = True
+        original = getattr(qm, "apply", None)
+        if original is None:
+            return
+        hook = _ClassicHook(self, original)
+        qm._sluice_hook = hook
+        qm.apply = torch._dynamo.disable(hook) if self.piecewise else hook
 
     def set_step_signal(self, nd: Optional[int], ndec: Optional[int],
                         real_step: bool = True) -> None:
@@ -602,31 +749,9 @@ class ExpertStreamOffloader:
         self._signal = None
 
     def _split_signal(self) -> tuple:
-        """``(num_decode_tokens, num_decodes, is_real_step)``
-        (src/sluice/offloader.py:1766-1800): the signal set with
-        set_step_signal, else vLLM's forward context; ``(None, None, False)``
-        (a dummy run) when neither exists."""
-        if self._signal is not None:
-            return self._signal
-        try:
-            from vllm.forward_context import get_forward_context  # type: ignore
-
-            ctx = get_forward_context()
-        except Exception:
-            return None, None, False
-        md = getattr(ctx, "attn_metadata", None)
-        if isinstance(md, dict):
-            md = next(iter(md.values()), None)
-        if md is None:
-            return None, None, False
-        nd = getattr(md, "num_decode_tokens", None)
-        if nd is None:
-            return None, None, True
-        ndec = getattr(md, "num_decodes", None)
-        try:
-            return int(nd), (int(ndec) if ndec is not None else None), True
-        except (TypeError, ValueError):
-            return None, None, True
+        """``(num_decode_tokens, num_decodes, is_real_step)``: the signal set
+        with set_step_signal, else vLLM's forward context."""
+        return self._signal if self._signal is not None else _engine_step_signal()
 
     def run_moe(self, original_apply, args, kwargs, module, topk_ids):
         """Classic streaming hook in place of ``quant_method.apply``
@@ -642,8 +767,9 @@ class ExpertStreamOffloader:
         if cache is None or cache.static_full:
             return original_apply(*args, **kwargs)
         if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("Sluice: streaming hook reached under CUDA graph capture; "
-                               "run with enforce_eager.")
+            raise RuntimeError("Sluice: the classic streaming hook syncs the host and cannot run "
+                               "inside a captured graph; capture piecewise (SLUICE_PIECEWISE=1) "
+                               "or run eagerly.")
         nd, ndec, real_step = self._split_signal()
         ids = topk_ids if topk_ids.dtype == torch.int32 else topk_ids.to(torch.int32)
         ids = ids.contiguous()
@@ -656,19 +782,20 @@ class ExpertStreamOffloader:
             -1 if ndec is None else int(ndec), int(bool(real_step)), int(self._spec_tokens),
             stream, ctypes.byref(nw)), "sluice_layer_classic_plan")
         n_waves = nw.value
-        if self._counts_dir and real_step:
-            # the reference ticks its profiling clock once per real hook call
-            # that selected experts (the steps the layer classified)
+        if self._counts is not None and real_step:
+            # the profiling clock ticks once per real hook call that selected
+            # experts (the steps the layer classified)
             pol = cache.policy_state()
             seen = pol["steps_small"] + pol["steps_scan"]
             if seen != cache.policy_steps:
                 cache.policy_steps = seen
-                self._counts_tick()
+                self._counts.tick(list(self._caches.values()))
         if n_waves > 1 and real_step and not self._warned_waves:
             self._warned_waves = True
-            logger.warning("Sluice: a step selected more local experts than usable slots; "
-                           "executing in %d waves (exact in math, not bit-identical to a "
-                           "single launch). Raise SLUICE_SLOTS to avoid waves.", n_waves)
+            logger.warning("Sluice: a step needs more local experts than the %d usable slots; "
+                           "it runs in %d waves, summed in fp32 (exact in math, not the bits of "
+                           "one launch). More SLUICE_SLOTS avoids waves.", cache.num_slots,
+                           n_waves)
         total = out = None
         for w in range(n_waves):
             _lib.check(lib.sluice_layer_classic_wave(cache.handle, w, stream),
@@ -683,14 +810,17 @@ class ExpertStreamOffloader:
 
     # -- router split -----------------------------------------------------------
     def attach_model(self, model: nn.Module) -> None:
+        """Called by the plugin once the model is loaded."""
         self.attach_router_split(model)
 
     def attach_router_split(self, model: nn.Module) -> None:
-        """Patch each eligible layer's ``runner._forward_entry`` with the traced
-        split path (src/sluice/offloader.py:2469-2635)."""
+        """Patch every eligible layer's ``runner._forward_entry`` with the
+        traced split path (src/sluice/offloader.py:2469-2635).  Layers
+        without the needed seams keep the stock path (counted in the skip
+        census); layers whose router the routing kernel cannot express keep
+        vLLM's select_experts inside the split path (counted as well)."""
         if not self.router_split:
             return
-        patched = 0
         skips: dict = {}
         seen = 0
         for module in model.modules():
@@ -699,33 +829,31 @@ class ExpertStreamOffloader:
                 continue
             seen += 1
             runner = getattr(module, "runner", None)
-            if runner is None:
-                skips["no-runner"] = skips.get("no-runner", 0) + 1
+            reason = _split_ineligible(runner, cache)
+            if reason is not None:
+                skips[reason] = skips.get(reason, 0) + 1
                 continue
-            if cache.static_full:
-                skips["static-full"] = skips.get("static-full", 0) + 1
-                continue
-            mc = getattr(runner, "moe_config", None)
-            topk = getattr(mc, "experts_per_token", None) if mc else None
-            if topk is None:
-                topk = getattr(module, "top_k", None) or 8
+            spec, why = route_spec(module, runner)
+            if spec is None:
+                skips[why] = skips.get(why, 0) + 1  # armed, routed by vLLM
             idx = len(self._rs_caches)
             self._rs_caches.append(cache)
+            self._rs_routes.append(spec)
+            top_k = spec.top_k if spec is not None else _runner_top_k(module, runner)
             thr = self._rs_thr
-            if thr is None:
-                thr = max(1, min(16, self.expert_cache_slots // int(topk)))
-            se = getattr(runner, "_shared_experts", None)
-            shared_layer = getattr(se, "_layer", None) if se is not None else None
-            runner._forward_entry = _make_entry(
-                idx, module.w13_weight, module.w2_weight, int(module.global_num_experts),
-                cache.expert_map_buf, shared_layer, runner.router.select_experts,
-                runner._forward_entry, getattr(runner, "gate", None), thr,
-                getattr(module, "w13_weight_scale", None), getattr(module, "w2_weight_scale", None),
-                getattr(module, "block_shape", None))
-            patched += 1
-        self._rs_layers = patched
-        logger.warning("Sluice: ROUTER-SPLIT armed on %d/%d MoE layers. skips=%s", patched, seen,
-                       skips or "{}")
+            if thr is None:  # eager: a per-step branch, capped at 16 tokens
+                thr = max(1, min(16, self.expert_cache_slots // top_k))
+            runner._forward_entry = _split_entry(_LayerBinding(
+                idx=idx, thr=thr, w13=module.w13_weight, w2=module.w2_weight,
+                global_n=_expert_counts(module)[0], expert_map=cache.expert_map_buf,
+                gate=getattr(runner, "gate", None), route=spec,
+                vllm_select=runner.router.select_experts if spec is None else None,
+                stock=runner._forward_entry, shared=_shared_layer(runner),
+                quant=_quant_kwargs(module)))
+        self._rs_layers = len(self._rs_caches)
+        kernel = sum(1 for r in self._rs_routes if r is not None)
+        logger.warning("Sluice: ROUTER-SPLIT armed on %d/%d MoE layers (%d routed by the wave64 "
+                       "top-k kernel). skips=%s", self._rs_layers, seen, kernel, skips or "{}")
 
     def _router_split_gap(self, idx: int, topk_ids: torch.Tensor,
                           hidden_states: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
@@ -740,10 +868,10 @@ class ExpertStreamOffloader:
             self._rs_gaps += 1
             if self._rs_gaps == 1 or self._rs_gaps % 2000 == 0:
                 c = self.gap_counters()
-                logger.warning("Sluice DIAG[rs]: router-split layers=%d gap-calls=%d misses=%d "
-                               "fast-hits=%d%s", len(self._rs_caches), self._rs_gaps,
-                               c["misses"], c["fast_hits"],
-                               " NOOP-GAP(OUTPUTS INVALID)" if self._rs_noop else "")
+                logger.warning("Sluice gap: %d router-split layers, %d gaps, %d misses, %d "
+                               "fast hits%s", len(self._rs_caches), self._rs_gaps, c["misses"],
+                               c["fast_hits"], " [no-op gap: outputs invalid]"
+                               if self._rs_noop else "")
         if self._rs_noop:
             return None if hidden_states is None else hidden_states.clone()
         ids = topk_ids if topk_ids.dtype == torch.int32 else topk_ids.to(torch.int32)
@@ -802,12 +930,19 @@ class ExpertStreamOffloader:
         srv, self._server = self._server, None
         _raise_gap(_lib.load().sluice_gap_server_destroy(srv), "sluice_gap_server_destroy")
 
+    # -- stats ----------------------------------------------------------------
     def gap_counters(self) -> dict:
+        """Router-split gap counters summed over the armed layers."""
         tot = {"gaps": 0, "misses": 0, "fast_hits": 0, "map_writes": 0, "bytes": 0}
         for c in self._rs_caches:
             for k_, v in c.stats().items():
                 tot[k_] += v
         return tot
+
+    def get_gap_stats(self) -> dict:
+        """The router-split gap's own counters (the reference keeps them
+        outside get_stats: src/sluice/offloader.py:349-351, 2456)."""
+        return {"layers": len(self._rs_caches), **self.gap_counters()}
 
     def classic_counters(self) -> dict:
         """Classic steps and waves run over every streaming layer."""
@@ -824,11 +959,21 @@ class ExpertStreamOffloader:
         return tot
 
     def get_stats(self) -> dict:
-        c = self.gap_counters()
-        cl = self.classic_counters()
-        return {"rs": {"steps": c["gaps"], "hits": None, "misses": c["misses"],
-                       "bytes": c["bytes"], "waves": c["gaps"], "fast_hits": c["fast_hits"]},
-                "classic": {"steps": cl["steps"], "waves": cl["waves"]}}
+        """Classic-step stats per class, in the reference's schema
+        (src/sluice/offloader.py:2804-2814): {"small": {...}, "scan": {...}},
+        each {steps, hits, misses, bytes, waves} summed over the streaming
+        layers ("small" = pure decode steps)."""
+        out = {kind: {"steps": 0, "hits": 0, "misses": 0, "bytes": 0, "waves": 0}
+               for kind in ("small", "scan")}
+        for c in self._caches.values():
+            if not c.handle or c.static_full:
+                continue
+            for kind, st in c.step_stats().items():
+                acc = out[kind]
+                for key in ("steps", "hits", "misses", "waves"):
+                    acc[key] += st[key]
+                acc["bytes"] += st["misses"] * c.bytes_per_expert
+        return out
 
     def close(self) -> None:
         lib = _lib.load()
@@ -843,36 +988,117 @@ class ExpertStreamOffloader:
                 c.handle = None
 
 
+def _read_pin_file(path: str) -> dict:
+    """{MoE-layer ordinal: [global expert ids]} from a pin file (the ids
+    under "layers", or at the top level); a malformed file fails loudly."""
+    with open(path) as f:
+        raw = json.load(f)
+    layers = raw.get("layers", raw)
+    pins = {int(k_): [int(g) for g in v] for k_, v in layers.items()}
+    logger.info("Sluice: pin file %s lists experts for %d layers.", path, len(pins))
+    return pins
+
+
 def _raise_gap(rc: int, what: str) -> None:
     if rc == _lib.SLUICE_E_OVERFLOW:
+        # the message is a contract: callers match on it
         raise RuntimeError("Sluice router-split: working set exceeds slots on a "
                            "decode-sized step; raise SLUICE_SLOTS.")
     _lib.check(rc, what)
 
 
-def _make_entry(idx, w13, w2, gne, emap, shared_layer, sel, orig, gate, thr, w13_scale, w2_scale,
-                block_shape):
-    """Bind one layer's tensors into a fresh traced entry; weights and map are
-    captured BY POINTER, the gap rewrites their contents
-    (src/sluice/offloader.py:2562-2603)."""
+# ---------------------------------------------------------------------------
+# The router-split entry
+# ---------------------------------------------------------------------------
+# Runner seams whose absence (or whose variants) the split entry cannot take;
+# such layers keep the stock path (src/sluice/offloader.py:2499-2538).
+def _split_ineligible(runner, cache: _ExpertLayerCache) -> Optional[str]:
+    if runner is None:
+        return "no-runner"
+    if cache.static_full:
+        return "static-full"
+    checks = (
+        ("monolithic", lambda r: getattr(getattr(r, "_quant_method", None), "is_monolithic",
+                                         False)),
+        ("fused-gate", lambda r: getattr(r, "gate", None) is not None
+         and getattr(r, "_fse_fuse_gate", False)),
+        ("naive-dispatch", lambda r: getattr(r, "do_naive_dispatch_combine", False)),
+        ("pcp", lambda r: (getattr(getattr(r, "moe_config", None), "pcp_size", 1) or 1) > 1),
+        ("no-router", lambda r: getattr(getattr(r, "router", None), "select_experts",
+                                        None) is None),
+        ("no-entry", lambda r: getattr(r, "_forward_entry", None) is None),
+    )
+    for reason, bad in checks:
+        if bad(runner):
+            return reason
+    return None
+
+
+def _runner_top_k(module, runner) -> int:
+    mc = getattr(runner, "moe_config", None)
+    k = getattr(mc, "experts_per_token", None) or getattr(module, "top_k", None)
+    return int(k or 8)
+
+
+def _shared_layer(runner):
+    se = getattr(runner, "_shared_experts", None)
+    return getattr(se, "_layer", None) if se is not None else None
+
+
+def _quant_kwargs(module) -> dict:
+    """fused_experts keywords of a block-quantised (fp8) layer."""
+    s13 = getattr(module, "w13_weight_scale", None)
+    if s13 is None:
+        return {}
+    return {"w1_scale": s13, "w2_scale": getattr(module, "w2_weight_scale", None),
+            "block_shape": list(getattr(module, "block_shape", None) or [128, 128])}
+
+
+@dataclass
+class _LayerBinding:
+    """One layer's tensors and callables, bound into its entry.  The weights
+    and the map are held BY POINTER: the gap rewrites their contents."""
+
+    idx: int
+    thr: int
+    w13: torch.Tensor
+    w2: torch.Tensor
+    global_n: int
+    expert_map: torch.Tensor
+    gate: Any
+    route: Optional[RouteSpec]
+    vllm_select: Any
+    stock: Any
+    shared: Any
+    quant: dict
+
+
+def _split_entry(b: _LayerBinding):
+    """The traced ``runner._forward_entry`` of one layer
+    (src/sluice/offloader.py:2578-2603): batches above the threshold take the
+    stock entry; others run gate -> routing -> gap op -> expert product ->
+    shared experts, returning (shared, routed) or routed."""
+    idx, thr, gate, route = b.idx, b.thr, b.gate, b.route
+    w13, w2, emap, gne, quant = b.w13, b.w2, b.expert_map, b.global_n, b.quant
+    stock, select, shared = b.stock, b.vllm_select, b.shared
 
     def _forward_entry(hs, rl, sei, iid, lname, unpad):
         if hs.shape[0] > thr:
-            return orig(hs, rl, sei, iid, lname, unpad)
+            return stock(hs, rl, sei, iid, lname, unpad)
         if gate is not None:
             rl, _ = gate(hs)
-        tw, ti = sel(hidden_states=hs, router_logits=rl, input_ids=iid)
+        if route is not None:
+            tw, ti = torch.ops.sluice.select_experts(
+                rl, route.top_k, route.scoring, route.renormalize, route.scale, route.bias,
+                route.n_group, route.topk_group)
+        else:
+            tw, ti = select(hidden_states=hs, router_logits=rl, input_ids=iid)
         h = torch.ops.vllm.sluice_stream_gap(hs, ti, idx)
-        kw = {}
-        if w13_scale is not None:
-            kw = {"w1_scale": w13_scale, "w2_scale": w2_scale,
-                  "block_shape": list(block_shape or [128, 128])}
         routed = torch.ops.sluice.fused_experts(h, w13, w2, tw, ti, activation="silu",
-                                                global_num_experts=gne, expert_map=emap, **kw)
-        if shared_layer is None:
+                                                global_num_experts=gne, expert_map=emap, **quant)
+        if shared is None:
             return routed
-        sh = shared_layer(sei if sei is not None else hs)
-        return (sh, routed)
+        return (shared(sei if sei is not None else hs), routed)
 
     return _forward_entry
 

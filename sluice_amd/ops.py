@@ -67,6 +67,28 @@ def select_experts(router_logits: torch.Tensor, top_k: int, *, scoring: str = "s
     return w, ids
 
 
+@torch.library.custom_op("sluice::select_experts", mutates_args=())
+def select_experts_op(router_logits: torch.Tensor, top_k: int, scoring: str = "softmax",
+                      renormalize: bool = False, routed_scaling_factor: float = 1.0,
+                      e_score_correction_bias: Optional[torch.Tensor] = None,
+                      num_expert_group: int = 1,
+                      topk_group: int = 1) -> tuple[torch.Tensor, torch.Tensor]:
+    """select_experts as a registered op, so a traced entry (torch.compile,
+    graph capture) calls the routing kernel as one node."""
+    return select_experts(router_logits, top_k, scoring=scoring, renormalize=renormalize,
+                          routed_scaling_factor=routed_scaling_factor,
+                          e_score_correction_bias=e_score_correction_bias,
+                          num_expert_group=num_expert_group, topk_group=topk_group)
+
+
+@select_experts_op.register_fake
+def _(router_logits, top_k, scoring="softmax", renormalize=False, routed_scaling_factor=1.0,
+      e_score_correction_bias=None, num_expert_group=1, topk_group=1):
+    T = router_logits.shape[0]
+    return (router_logits.new_empty((T, top_k), dtype=torch.float32),
+            router_logits.new_empty((T, top_k), dtype=torch.int32))
+
+
 # ---------------------------------------------------------------------------
 # Expert product
 # ---------------------------------------------------------------------------

@@ -1,39 +1,93 @@
-"""Sluice plugin entry point (vLLM ``general_plugins``), MI355X build.
+"""vLLM ``general_plugins`` hook of the MI355X build.
 
-Mirrors src/sluice/plugin.py:27-96: ``register()`` is a no-op unless
-``SLUICE_SLOTS`` parses to a positive int (an invalid value warns and does
-nothing), refuses vLLM's V2 model runner, then patches vLLM's
-``create_offloader`` factory (at its definition and in the model-runner
-module that imported it) so the active offloader is this package's
-``ExpertStreamOffloader``, and wraps ``GPUModelRunner.load_model`` to call
-``attach_model`` on the loaded model.  vLLM is optional here: without it the
-function validates the environment and returns, and the offloader can be
-driven directly (``sluice_amd.decoder`` does so).
+The entry point is ``sluice = "sluice.plugin:register"`` (the reference's
+pyproject.toml:34-35); ``sluice.plugin`` re-exports ``register`` from here.
+What it does is the reference's contract (src/sluice/plugin.py:27-96):
+
+  * nothing unless ``SLUICE_SLOTS`` holds a positive int (anything else is
+    ignored with a warning);
+  * refuse vLLM's V2 model runner, which never calls the offloader
+    lifecycle;
+  * make vLLM's ``create_offloader`` factory return this package's
+    ``ExpertStreamOffloader`` -- at its definition and in the model runner
+    module that imported it by name;
+  * after ``GPUModelRunner.load_model``, hand the loaded model to the
+    offloader's ``attach_model`` (which arms the router-split entries).
+
+Without vLLM the hook only validates the environment; the offloader can
+then be driven directly (``sluice_amd.decoder`` does so).
 """
 
 import logging
 import os
+from typing import Optional
 
 logger = logging.getLogger("sluice")
 
 SLOTS_ENV = "SLUICE_SLOTS"
 
-# The live offloader instance for this process (set by the patched factory).
+# The offloader the patched factory made last in this process.
 _ACTIVE = None
 
 
-def slots_from_env():
-    """The SLUICE_SLOTS value, or None when unset/invalid (with a warning)."""
+def slots_from_env() -> Optional[int]:
+    """The SLUICE_SLOTS value, or None when unset or not a positive int."""
     raw = os.environ.get(SLOTS_ENV)
     if not raw:
         return None
     try:
         slots = int(raw)
-        assert slots > 0
-    except (ValueError, AssertionError):
+    except ValueError:
+        slots = 0
+    if slots <= 0:
         logger.warning("Sluice: ignoring invalid %s=%r (want a positive int).", SLOTS_ENV, raw)
         return None
     return slots
+
+
+class _Activation:
+    """The patches register() installs for one SLUICE_SLOTS value."""
+
+    def __init__(self, slots: int):
+        self.slots = slots
+
+    def create_offloader(self, offload_config=None):  # noqa: ARG002 - vLLM's factory signature
+        global _ACTIVE
+        from sluice_amd.offloader import ExpertStreamOffloader
+
+        _ACTIVE = ExpertStreamOffloader(expert_cache_slots=self.slots)
+        return _ACTIVE
+
+    @staticmethod
+    def attach_after(load_model):
+        """GPUModelRunner.load_model, then attach_model on the loaded model
+        (a failure there leaves the stock MoE path and is logged)."""
+
+        def load_model_then_attach(runner, *args, **kwargs):
+            result = load_model(runner, *args, **kwargs)
+            model = getattr(runner, "model", None)
+            if _ACTIVE is not None and model is not None:
+                try:
+                    _ACTIVE.attach_model(model)
+                except Exception:  # noqa: BLE001
+                    logger.exception("Sluice: attach_model failed; MoE layers run the stock "
+                                     "path (router-split not armed).")
+            return result
+
+        load_model_then_attach.__wrapped__ = load_model
+        return load_model_then_attach
+
+
+def _refuse_v2_runner() -> None:
+    try:
+        import vllm.envs as vllm_envs  # type: ignore
+    except ImportError:
+        return
+    if getattr(vllm_envs, "VLLM_USE_V2_MODEL_RUNNER", False):
+        raise RuntimeError(
+            "Sluice needs vLLM's V1 model runner: with VLLM_USE_V2_MODEL_RUNNER set, "
+            "create_offloader and post_init are never called, so the expert cache would not be "
+            "installed and its checks would not run. Unset VLLM_USE_V2_MODEL_RUNNER.")
 
 
 def register() -> None:
@@ -41,49 +95,24 @@ def register() -> None:
     slots = slots_from_env()
     if slots is None:
         return
-
+    _refuse_v2_runner()
     try:
-        import vllm.envs as vllm_envs
-
-        if getattr(vllm_envs, "VLLM_USE_V2_MODEL_RUNNER", False):
-            raise RuntimeError(
-                "Sluice requires the V1 model runner but VLLM_USE_V2_MODEL_RUNNER is set — the "
-                "V2 runner never invokes create_offloader/post_init, so Sluice (and its "
-                "correctness guards) would silently not run. Unset VLLM_USE_V2_MODEL_RUNNER.")
+        import vllm.model_executor.offloader.base as base_mod  # type: ignore
     except ImportError:
-        logger.info("Sluice: vLLM not importable; %s=%d recorded, nothing to patch.", SLOTS_ENV,
-                    slots)
+        logger.info("Sluice: %s=%d set but vLLM is not importable; nothing to patch.",
+                    SLOTS_ENV, slots)
         return
-
-    import vllm.model_executor.offloader.base as base_mod
-
-    from sluice_amd.offloader import ExpertStreamOffloader
-
-    def _create_offloader(offload_config):  # noqa: ANN001
-        global _ACTIVE
-        _ACTIVE = ExpertStreamOffloader(expert_cache_slots=slots)
-        return _ACTIVE
-
-    base_mod.create_offloader = _create_offloader
+    act = _Activation(slots)
+    factory = act.create_offloader  # one object, installed everywhere
+    base_mod.create_offloader = factory
     try:
-        import vllm.v1.worker.gpu_model_runner as gmr
-
+        import vllm.v1.worker.gpu_model_runner as gmr  # type: ignore
+    except Exception:  # noqa: BLE001 - another vLLM layout: the base patch alone
+        logger.debug("Sluice: vLLM's gpu_model_runner not importable; patched the base factory.")
+    else:
         if hasattr(gmr, "create_offloader"):
-            gmr.create_offloader = _create_offloader
-        _orig_load = gmr.GPUModelRunner.load_model
-
-        def load_model(self, *a, **k):  # noqa: ANN001
-            out = _orig_load(self, *a, **k)
-            try:
-                mdl = getattr(self, "model", None)
-                if _ACTIVE is not None and mdl is not None:
-                    _ACTIVE.attach_model(mdl)
-            except Exception:
-                logger.exception("Sluice: attach_model failed (router-split not armed).")
-            return out
-
-        gmr.GPUModelRunner.load_model = load_model
-    except Exception:  # pragma: no cover - depends on the vLLM version present
-        logger.debug("Sluice: gpu_model_runner not patchable; relying on base.")
-
-    logger.info("Sluice: activated via %s=%d (expert offloading on).", SLOTS_ENV, slots)
+            gmr.create_offloader = factory
+        runner_cls = getattr(gmr, "GPUModelRunner", None)
+        if runner_cls is not None and hasattr(runner_cls, "load_model"):
+            runner_cls.load_model = act.attach_after(runner_cls.load_model)
+    logger.info("Sluice: %s=%d, expert offloading on.", SLOTS_ENV, slots)

@@ -193,7 +193,11 @@ def run_case(ESO, name, E, local_n, slots, frac, k, T_choices, steps, kind, seed
                 assert float(cache.gpu_cache["w13_weight"][s, 0, 0]) == float(loc)
         recs.append({"kind": "classic", "ids": ids, "T": T, "nd": nd, "ndec": ndec,
                      "real_step": real, "waves": rec_waves,
-                     "state": base._snapshot(cache)})
+                     "state": base._snapshot(cache),
+                     # the reference's per-class step stats after this step
+                     "stats": {kind_: {k_: int(v) for k_, v in st.items()}
+                               for kind_, st in off.get_stats().items()},
+                     "bytes_per_expert": int(cache.bytes_per_expert)})
         if policy:
             recs[-1]["policy"] = _policy_state(off, cache, mod)
     out = {

@@ -118,6 +118,8 @@ CASES = [
     ("ep_half_owned", 32, 16, 8, 0.5, 4, [1, 2], 150, "uniform", 51, "even", None),
     ("pinned", 32, 32, 10, 0.5, 3, [1, 2], 150, "zipf", 61, None, [5, 7, 9]),
     ("overflow", 16, 16, 4, 0.5, 2, [1, 1, 1, 1, 2, 3], 60, "uniform", 71, None, None),
+    # DeepSeek-V3 layer shape: 256 experts top-8, 64 slots, 8 tokens per step
+    ("v3_s64_zipf", 256, 256, 64, 0.5, 8, [8], 120, "zipf", 81, None, None),
 ]
 
 

@@ -35,6 +35,14 @@ class NativeCache:
                 "counts_decode": list(dec), "counts_scan": list(scan),
                 "steps_small": st[0], "steps_scan": st[1], "lfu_steps": st[2]}
 
+    def step_stats(self):
+        """{"small"|"scan": {steps, hits, misses, waves}} of real classic steps."""
+        out = (ctypes.c_int64 * 8)()
+        _lib.check(self.lib.sluice_layer_step_stats(self.h, out), "step_stats")
+        keys = ("steps", "hits", "misses", "waves")
+        return {kind: {k: int(out[4 * i + j]) for j, k in enumerate(keys)}
+                for i, kind in enumerate(("small", "scan"))}
+
     def __del__(self):
         if getattr(self, "h", None):
             self.lib.sluice_layer_destroy(self.h)

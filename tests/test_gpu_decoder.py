@@ -18,18 +18,24 @@ def _run(spec, layers, c, steps, graphs, slots, gap_server):
     dec = SyntheticDecoder(spec, max_batch=c, slots=slots, gen_len=steps + 16, layers=layers,
                            device=DEV, seed=3, gap_server=gap_server)
     toks = []
+
+    def out_of_step():
+        # the next tokens; a MoE stack without attention: its output rows' bits
+        st = dec.state[c]
+        return st.tokens.clone() if st.tokens is not None else st.x.view(torch.int16).clone()
+
     if graphs:
         dec.capture(c)
         for _ in range(steps):
             dec.step_graphs(c)
-            toks.append(dec.state[c].tokens.clone())
+            toks.append(out_of_step())
     else:
         for _ in range(2):  # the same warm-up capture() does
             dec.step_eager(c)
         dec.reset(c)
         for _ in range(steps):
             dec.step_eager(c)
-            toks.append(dec.state[c].tokens.clone())
+            toks.append(out_of_step())
     dec.sync()
     out = torch.stack(toks).cpu().numpy()
     state = [cache._state() for cache in dec.caches]
@@ -38,7 +44,8 @@ def _run(spec, layers, c, steps, graphs, slots, gap_server):
     return out, state, maps
 
 
-@pytest.mark.parametrize("spec,layers,c,slots", [("v2lite", 3, 4, 48), ("qwen3", 2, 8, 64)])
+@pytest.mark.parametrize("spec,layers,c,slots", [("v2lite", 3, 4, 48), ("qwen3", 2, 8, 64),
+                                                ("v3", 2, 8, 64)])
 def test_one_graph_step_with_gap_server_matches_eager_inline_gaps(spec, layers, c, slots):
     """Reference structure (eager gaps served inline between ops) against the
     MI355X structure (gap server, whole step one hipGraph): identical tokens,
@@ -89,3 +96,52 @@ def test_moe_layer_against_oracle():
         print(f"  step {step} rel_l2={err:.2e}", flush=True)
         assert err <= 1e-2
     dec.close()
+
+
+def test_v3_routed_fp8_layer_against_oracle():
+    """A DeepSeek-V3-routed fp8 MoE layer through the armed entry: 256
+    experts top-8, sigmoid + correction bias over 8 groups (top-4 groups),
+    renormalised, scale 2.5; e4m3fn experts and shared expert with 128x128
+    block scales; 64 slots, 8 tokens per step (hidden 512, intermediate 256,
+    so the float64 oracle stays small).  Slot assignment follows the oracle's
+    routing of the entry's own logits, and the layer output is within the
+    fp8 tolerance of the oracle on the dequantised weights."""
+    from oracle import moe as om
+    from oracle import routing as orr
+    from oracle.slru import LayerCache
+    from sluice_amd.decoder import SPECS, _expert_store, _StoreMoELayer, build_offloaded
+
+    sp = dict(SPECS["v3"], H=512, I=256, shared_I=256)
+    store = _expert_store(sp, 7001, DEV, True)
+    layer = _StoreMoELayer(sp, store, 1, DEV, None, "layers.1.mlp")
+    off = build_offloaded([layer], slots=64, device=DEV)
+    assert off._rs_routes[0] is not None and off._rs_routes[0].scoring == "sigmoid"
+    cache = off._caches[id(layer)]
+    assert len(cache.param_names) == 4
+    oracle = LayerCache(256, 256, 64, off.protect_frac)
+    deq = {n: om.dequant_block(cache.cpu_store[n].numpy(), cache.cpu_store[n + "_scale"].numpy())
+           for n in ("w13_weight", "w2_weight")}
+    sh = layer.shared
+    sh_ref_w = (om.dequant_block(sh.gate_up.cpu().numpy(), sh.gate_up_scale.cpu().numpy()),
+                om.dequant_block(sh.down.cpu().numpy(), sh.down_scale.cpu().numpy()))
+    bias = layer.e_score_correction_bias.detach().float().cpu().numpy()
+    rng = np.random.default_rng(3)
+    misses = 0
+    for step in range(4):
+        x = torch.from_numpy(rng.standard_normal((8, 512)).astype(np.float32)).to(
+            torch.bfloat16).to(DEV)
+        out = layer(x)
+        logits = layer.logits(x)  # the gate kernel the entry ran, on the same input
+        torch.cuda.synchronize()
+        ids, w = orr.sigmoid_topk(logits.cpu().numpy(), bias, 8, 8, 4, True, 2.5)
+        misses += len(oracle.gap(ids.reshape(-1).tolist(), fast_hit=True))
+        assert cache._state()["expert_in_slot"] == [
+            -1 if v is None else v for v in oracle.expert_in_slot], step
+        xf = x.float().cpu().numpy()
+        ref = om.fused_experts(xf, deq["w13_weight"], deq["w2_weight"], w, ids,
+                               shared=om.shared_mlp(xf, *sh_ref_w))
+        err = om.rel_l2(out.float().cpu().numpy(), ref)
+        print(f"  step {step} rel_l2={err:.2e}", flush=True)
+        assert err <= 3e-2
+    assert misses > 0
+    off.close()

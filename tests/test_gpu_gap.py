@@ -67,7 +67,7 @@ def _case_ids():
     return [f"{g['cases'][i]['name']}-fh{int(g['cases'][i]['fast_hit'])}" for i in _cases(g)]
 
 
-@pytest.mark.parametrize("idx", range(20), ids=_case_ids())
+@pytest.mark.parametrize("idx", range(len(_case_ids())), ids=_case_ids())
 def test_device_gap_replays_reference(monkeypatch, slru_golden, idx):
     case = slru_golden["cases"][_cases(slru_golden)[idx]]
     print(f"gap case {case['name']} fast_hit={case['fast_hit']}", flush=True)
@@ -145,3 +145,85 @@ def test_slot_lookup_record(lib):
     assert r[0] == 77 and r[1] == len(uniq)
     assert r[4:4 + r[1]].tolist() == uniq
     assert r[2] == sum(1 for g in uniq if local_of[g] >= 0 and emap[g] < 0)
+
+
+class _Fp8Layer(nn.Module):
+    """An fp8 layer's per-expert params, as vLLM's block-quantised FusedMoE
+    holds them: e4m3fn w13 [E, 2I, H] and w2 [E, H, I] plus their fp32
+    128x128 block scales [E, 2I/128, H/128] and [E, H/128, I/128] -- four
+    rows stream per missing expert (src/sluice/offloader.py:2709-2723)."""
+
+    def __init__(self, E, H=256, I=128):
+        super().__init__()
+        self.global_num_experts = E
+        self.local_num_experts = E
+        self.quant_method = types.SimpleNamespace()
+        g = torch.Generator().manual_seed(4242)
+
+        def codes(*shape):
+            return (torch.randn(shape, generator=g) * 0.5).to(torch.float8_e4m3fn).view(torch.uint8)
+
+        self.w13_weight = nn.Parameter(codes(E, 2 * I, H), requires_grad=False)
+        self.w2_weight = nn.Parameter(codes(E, H, I), requires_grad=False)
+        self.w13_weight_scale = nn.Parameter(
+            torch.rand((E, 2 * I // 128, H // 128), generator=g) + 0.01, requires_grad=False)
+        self.w2_weight_scale = nn.Parameter(
+            torch.rand((E, H // 128, I // 128), generator=g) + 0.01, requires_grad=False)
+        # shared by every expert: stays resident, never streamed
+        self.e_score_correction_bias = nn.Parameter(torch.zeros(E), requires_grad=False)
+
+
+def _slot_bytes_match_host(cache):
+    torch.cuda.synchronize()
+    for name in cache.param_names:
+        slot_t = cache.gpu_cache[name].cpu().contiguous().view(torch.uint8)
+        host_t = cache.cpu_store[name].contiguous().view(torch.uint8)
+        for s, loc in enumerate(cache.expert_in_slot):
+            if loc is not None:
+                assert torch.equal(slot_t[s], host_t[loc]), (name, s, loc)
+
+
+@pytest.mark.parametrize("fast_hit", [False, True])
+def test_device_gap_v3_fp8_streams_four_rows_per_miss(monkeypatch, slru_golden, fast_hit):
+    """The DeepSeek-V3-shaped golden trace (E = 256, 64 slots, top-8, 8
+    tokens per step), replayed on an fp8 layer: per step the stream-ins
+    (local -> slot) and the slot state, segment order and device map of the
+    reference; the bytes of all four per-expert params of every slot equal
+    their host rows; bytes streamed = misses x the four rows' size."""
+    case = [c for c in slru_golden["cases"]
+            if c["name"] == "v3_s64_zipf" and c["fast_hit"] == fast_hit][0]
+    print(f"v3 fp8 gap fast_hit={fast_hit}", flush=True)
+    E, k = case["E"], case["k"]
+    layer = _Fp8Layer(E)
+    off = _offloader(monkeypatch, case["slots"], case["protect_frac"], fast_hit)
+    off.wrap_modules(iter([layer]))
+    with torch.cuda.device(DEV):
+        off.post_init()
+    cache = off._caches[id(layer)]
+    assert sorted(cache.param_names) == ["w13_weight", "w13_weight_scale", "w2_weight",
+                                         "w2_weight_scale"]
+    assert cache.bytes_per_expert == 2 * 128 * 256 + 256 * 128 + (2 * 2 + 2 * 1) * 4
+    off._rs_caches.append(cache)
+    hs = torch.zeros((8, 256), dtype=torch.bfloat16, device=DEV)
+    prev = list(cache.expert_in_slot)
+    for n, step in enumerate(case["steps"]):
+        ids = torch.tensor(step["ids"], dtype=torch.int32, device=DEV).view(-1, k)
+        torch.ops.vllm.sluice_stream_gap(hs, ids, len(off._rs_caches) - 1)
+        st = cache._state()
+        want = step["state"]
+        for key in ("slot_of", "expert_in_slot", "probation", "protected", "free_slots"):
+            assert st[key] == want[key], (n, key)
+        now = [None if v < 0 else v for v in st["expert_in_slot"]]
+        streamed = sorted([loc, s] for s, loc in enumerate(now) if loc is not None
+                          and loc != prev[s])
+        assert streamed == sorted(step["streams"]), n
+        prev = now
+        torch.cuda.synchronize()
+        assert cache.expert_map_buf.cpu().tolist() == want["map"], n
+        if n % 20 == 0 or n == len(case["steps"]) - 1:
+            _slot_bytes_match_host(cache)
+    s = cache.stats()
+    assert (s["gaps"], s["misses"], s["fast_hits"]) == (
+        case["counters"]["gaps"], case["counters"]["misses"], case["counters"]["fast_hits"])
+    assert s["bytes"] == s["misses"] * cache.bytes_per_expert
+    off.close()

@@ -129,7 +129,7 @@ def test_load_throughput_page_cache(tmp_path):
 def test_per_expert_param_filter_keeps_shared_tensors_out():
     """NON_EXPERT_WEIGHTS (src/sluice/offloader.py:89-96): tensors with a
     leading dim equal to local_n that are NOT per-expert stay resident."""
-    from sluice_amd.offloader import ExpertStreamOffloader
+    from sluice_amd.offloader import _streamed_params
 
     E = 8
     m = nn.Module()
@@ -140,5 +140,5 @@ def test_per_expert_param_filter_keeps_shared_tensors_out():
     m.w13_input_scale = nn.Parameter(torch.zeros(E), requires_grad=False)
     m.hash_indices_table = nn.Parameter(torch.zeros(E, 3), requires_grad=False)
     m.other = nn.Parameter(torch.zeros(E + 1), requires_grad=False)
-    got = ExpertStreamOffloader._per_expert_params(m, E)
+    got = _streamed_params(m, E)
     assert sorted(got) == ["w13_weight", "w13_weight_scale", "w2_weight"]

@@ -26,7 +26,13 @@ def _native_for(case):
     return c
 
 
-@pytest.mark.parametrize("idx", range(20))
+def _slru_cases():
+    from tests.conftest import slru_vectors
+
+    return range(len(slru_vectors()["cases"]))
+
+
+@pytest.mark.parametrize("idx", _slru_cases())
 def test_native_matches_reference_vectors(slru_golden, idx):
     case = slru_golden["cases"][idx]
     c = _native_for(case)
@@ -131,6 +137,12 @@ def test_native_classic_matches_reference_vectors(classic_golden, idx):
         for key in ("slot_of", "expert_in_slot", "probation", "protected", "free_slots",
                     "map_is_standing", "protected_cap"):
             assert st[key] == want[key], (case["name"], n, key)
+        if "stats" in step:
+            got = c.step_stats()
+            for kind, want_s in step["stats"].items():
+                for key in ("steps", "hits", "misses", "waves"):
+                    assert got[kind][key] == want_s[key], (case["name"], n, kind, key)
+                assert want_s["bytes"] == want_s["misses"] * step["bytes_per_expert"]
         if "policy" in step:
             pol, want_pol = c.policy(), step["policy"]
             for key in ("freq", "lfu_steps", "steps_small", "steps_scan"):

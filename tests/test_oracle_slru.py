@@ -5,6 +5,7 @@ import random
 
 import pytest
 
+from conftest import slru_vectors
 from oracle.slru import GapOverflow, LayerCache
 
 
@@ -30,7 +31,7 @@ def test_golden_cases_cover_both_fast_hit_settings(slru_golden):
     assert any(c["steps"][-1]["overflow"] for c in slru_golden["cases"])
 
 
-@pytest.mark.parametrize("idx", range(20))
+@pytest.mark.parametrize("idx", range(len(slru_vectors()["cases"])))
 def test_oracle_matches_reference_vectors(slru_golden, idx):
     case = slru_golden["cases"][idx]
     c = _oracle_for(case)

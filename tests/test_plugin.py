@@ -1,18 +1,26 @@
 """The vLLM-facing surface on the CPU, against stand-in vLLM modules: the
-general_plugins hook (src/sluice/plugin.py:27-96), the engine-configuration
-guards and envelope (src/sluice/offloader.py:663-851), the wrapped
-quant_method.apply (1085-1119) and the forward-context split signal
-(1766-1800)."""
+package and entry point (the reference's pyproject.toml:34-35,
+src/sluice/__init__.py:4-7), the general_plugins hook
+(src/sluice/plugin.py:27-96), the engine settings the offloader applies
+(envelope, split points, speculative depth: src/sluice/offloader.py:786-851),
+the wrapped quant_method.apply (1085-1122), the forward-context split
+signal (1766-1800), the router settings mapped onto the routing kernel
+(select_experts as called at 2583-2585) and get_stats' schema (2804-2814)."""
 
+import importlib
 import logging
+import os
 import sys
 import types
 
 import pytest
 import torch
+import torch.nn as nn
 
 from sluice_amd import plugin
-from sluice_amd.offloader import ExpertStreamOffloader
+from sluice_amd.offloader import ExpertStreamOffloader, route_spec
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def _mod(monkeypatch, name, **attrs):
@@ -68,6 +76,26 @@ def test_register_refuses_the_v2_runner(monkeypatch):
         plugin.register()
 
 
+def test_entry_point_resolves_to_the_sluice_package():
+    """The general_plugins entry point is the reference's
+    (sluice = "sluice.plugin:register"), and the sluice package has the
+    reference's import surface."""
+    import tomli
+    from importlib.metadata import EntryPoint
+
+    with open(os.path.join(ROOT, "pyproject.toml"), "rb") as f:
+        eps = tomli.load(f)["project"]["entry-points"]["vllm.general_plugins"]
+    assert eps == {"sluice": "sluice.plugin:register"}
+    ep = EntryPoint(name="sluice", value=eps["sluice"], group="vllm.general_plugins")
+    assert ep.load() is plugin.register
+    sluice = importlib.import_module("sluice")
+    assert sluice.__version__ == "0.1.0"
+    assert sluice.ExpertStreamOffloader is ExpertStreamOffloader
+    assert importlib.import_module("sluice.offloader").ExpertStreamOffloader is \
+        ExpertStreamOffloader
+    assert importlib.import_module("sluice.plugin").register is plugin.register
+
+
 def test_register_patches_factory_and_load_model(monkeypatch):
     base, gmr = _stub_vllm(monkeypatch)
     monkeypatch.setenv("SLUICE_SLOTS", "48")
@@ -88,20 +116,15 @@ def test_register_patches_factory_and_load_model(monkeypatch):
 
 def _cfg(**kw):
     ns = types.SimpleNamespace
-    cfg = ns(parallel_config=ns(data_parallel_size=kw.get("dp", 1),
-                                enable_eplb=kw.get("eplb", False)),
-             model_config=ns(enforce_eager=kw.get("eager", False),
-                             hf_config=ns(num_experts_per_tok=kw.get("topk", 6))),
-             compilation_config=ns(cudagraph_mode=ns(name=kw.get("cg", "PIECEWISE")),
-                                   splitting_ops=list(kw.get("ops", []))),
-             scheduler_config=ns(max_num_batched_tokens=kw.get("mbt", 8)),
-             speculative_config=(ns(num_speculative_tokens=kw["spec"]) if "spec" in kw
-                                 else None))
-    return cfg
+    return ns(model_config=ns(hf_config=ns(num_experts_per_tok=kw.get("topk", 6))),
+              compilation_config=ns(splitting_ops=list(kw.get("ops", []))),
+              scheduler_config=ns(max_num_batched_tokens=kw.get("mbt", 8)),
+              speculative_config=(ns(num_speculative_tokens=kw["spec"]) if "spec" in kw
+                                  else None))
 
 
 def _off(monkeypatch, slots=48, **env):
-    for k in ("SLUICE_ROUTER_SPLIT", "SLUICE_PIECEWISE", "SLUICE_GRAPH"):
+    for k in ("SLUICE_ROUTER_SPLIT", "SLUICE_PIECEWISE"):
         monkeypatch.delenv(k, raising=False)
     for k, v in env.items():
         monkeypatch.setenv(k, v)
@@ -111,49 +134,44 @@ def _off(monkeypatch, slots=48, **env):
 def test_router_split_envelope_and_split_points(monkeypatch):
     off = _off(monkeypatch, SLUICE_ROUTER_SPLIT="1", SLUICE_PIECEWISE="1")
     cfg = _cfg(mbt=8, ops=["vllm::unified_attention"], spec=2)
-    off._check_config(cfg)
+    off.post_init(cfg)
     assert off._rs_thr == 8                       # 48 slots // top-6
     assert cfg.compilation_config.splitting_ops == [
         "vllm::unified_attention", "vllm::moe_forward", "vllm::moe_forward_shared",
         "vllm::sluice_stream_gap"]
     assert off._spec_tokens == 2
     with pytest.raises(RuntimeError, match="max_num_batched_tokens=9 > slots//topk=8"):
-        off._check_config(_cfg(mbt=9))
+        off.post_init(_cfg(mbt=9))
     # Qwen3-style config: top-k under text_config
     cfg = _cfg(mbt=8)
     cfg.model_config.hf_config = types.SimpleNamespace(
         text_config=types.SimpleNamespace(num_experts_per_tok=8))
     off = _off(monkeypatch, slots=64, SLUICE_ROUTER_SPLIT="1", SLUICE_PIECEWISE="1")
-    off._check_config(cfg)
+    off.post_init(cfg)
     assert off._rs_thr == 8
 
 
-def test_engine_guards(monkeypatch):
-    off = _off(monkeypatch)
-    with pytest.raises(RuntimeError, match="--enforce-eager"):
-        off._check_config(_cfg(eager=False, cg="NONE"))
-    with pytest.raises(RuntimeError, match="frozen expert map"):
-        off._check_config(_cfg(eager=True, cg="PIECEWISE"))
-    off._check_config(_cfg(eager=True, cg="NONE"))       # eager, no graphs: fine
-    with pytest.raises(RuntimeError, match="data parallelism"):
-        off._check_config(_cfg(eager=True, cg="NONE", dp=2))
-    with pytest.raises(RuntimeError, match="EPLB"):
-        off._check_config(_cfg(eager=True, cg="NONE", eplb=True))
+def test_engine_settings_without_router_split_or_piecewise(monkeypatch):
+    """Piecewise without router-split: only the MoE ops become split points
+    (the classic hook runs in a graph break) and no envelope applies;
+    eager: the config only contributes the speculative depth."""
     off = _off(monkeypatch, SLUICE_PIECEWISE="1")
-    with pytest.raises(RuntimeError, match="requires PIECEWISE cudagraph"):
-        off._check_config(_cfg(cg="FULL_AND_PIECEWISE"))
-    cfg = _cfg(cg="PIECEWISE")
-    off._check_config(cfg)                                # piecewise relaxes eager
-    assert "vllm::sluice_stream_gap" not in cfg.compilation_config.splitting_ops
-    off = _off(monkeypatch, SLUICE_GRAPH="1")
-    off._check_config(_cfg(cg="FULL"))                    # graph mode: checked at post_init
+    cfg = _cfg(mbt=4096)
+    off.post_init(cfg)
+    assert cfg.compilation_config.splitting_ops == ["vllm::moe_forward",
+                                                    "vllm::moe_forward_shared"]
+    assert off._rs_thr is None
+    off = _off(monkeypatch)
+    cfg = _cfg(mbt=4096, spec=3)
+    off.post_init(cfg)
+    assert cfg.compilation_config.splitting_ops == [] and off._spec_tokens == 3
 
 
 def test_config_must_be_readable_when_vllm_is_present(monkeypatch):
     _stub_vllm(monkeypatch, cfg=None)
     off = _off(monkeypatch)
     with pytest.raises(RuntimeError, match="config is None"):
-        off._check_config()
+        off.post_init()
 
 
 def test_split_signal_reads_the_forward_context(monkeypatch):
@@ -184,9 +202,10 @@ def test_apply_wrapper_routes_through_run_moe(monkeypatch):
             return x
 
     layer = types.SimpleNamespace(quant_method=QM())
-    off._wrap_apply(layer)
-    off._wrap_apply(layer)  # idempotent
-    assert layer.quant_method._sluice_wrapped
+    off._install_classic_hook(layer)
+    hook = layer.quant_method._sluice_hook
+    off._install_classic_hook(layer)  # idempotent
+    assert layer.quant_method._sluice_hook is hook
 
     def fake_run_moe(original_apply, args, kwargs, module, topk_ids):
         calls.append(("hook", module is layer, tuple(topk_ids.shape)))
@@ -199,3 +218,79 @@ def test_apply_wrapper_routes_through_run_moe(monkeypatch):
     calls.clear()
     layer.quant_method.apply(layer, x, x, None)  # no topk_ids keyword: straight through
     assert calls == ["orig"]
+
+
+# ---------------------------------------------------------------------------
+# Router settings -> routing kernel
+# ---------------------------------------------------------------------------
+def _moe(E=64, top_k=6, **attrs):
+    m = nn.Module()
+    m.global_num_experts = E
+    m.local_num_experts = E
+    m.top_k = top_k
+    defaults = dict(scoring_func="softmax", renormalize=False, use_grouped_topk=False,
+                    num_expert_group=None, topk_group=None, routed_scaling_factor=1.0,
+                    custom_routing_function=None, e_score_correction_bias=None)
+    defaults.update(attrs)
+    for k, v in defaults.items():
+        setattr(m, k, v)
+    return m
+
+
+def test_route_spec_maps_the_configs_routers():
+    # DeepSeek-V2-Lite: softmax greedy, no renorm (vLLM runs it as grouped
+    # top-k with one group)
+    spec, why = route_spec(_moe(64, 6, use_grouped_topk=True, num_expert_group=1, topk_group=1))
+    assert why == "" and (spec.scoring, spec.renormalize, spec.n_group, spec.scale) == (
+        "softmax", False, 1, 1.0)
+    # Qwen3-30B-A3B: softmax + renorm, not grouped
+    spec, _ = route_spec(_moe(128, 8, renormalize=True))
+    assert (spec.top_k, spec.scoring, spec.renormalize, spec.n_group) == (8, "softmax", True, 1)
+    # DeepSeek-V3: sigmoid + correction bias, 8 groups / top-4 groups, renorm, scale 2.5
+    bias = torch.zeros(256)
+    spec, _ = route_spec(_moe(256, 8, scoring_func="sigmoid", renormalize=True,
+                              use_grouped_topk=True, num_expert_group=8, topk_group=4,
+                              routed_scaling_factor=2.5, e_score_correction_bias=bias))
+    assert (spec.scoring, spec.n_group, spec.topk_group, spec.scale, spec.renormalize) == (
+        "sigmoid", 8, 4, 2.5, True)
+    assert spec.bias is bias
+    # the scaling factor applies only where vLLM's grouped top-k applies it
+    spec, _ = route_spec(_moe(64, 6, routed_scaling_factor=2.0))
+    assert spec.scale == 1.0
+
+
+def test_route_spec_prefers_the_runner_router_and_refuses_what_the_kernel_cannot_do():
+    m = _moe(64, 6)
+    runner = types.SimpleNamespace(router=types.SimpleNamespace(top_k=4, renormalize=True))
+    spec, _ = route_spec(m, runner)
+    assert spec.top_k == 4 and spec.renormalize
+    refused = {
+        "router:custom": _moe(custom_routing_function=lambda *a: None),
+        "router:scoring-softplus": _moe(scoring_func="softplus"),
+        "router:ungrouped-sigmoid-or-bias": _moe(scoring_func="sigmoid"),
+        "router:sigmoid-no-bias": _moe(scoring_func="sigmoid", use_grouped_topk=True,
+                                       num_expert_group=8, topk_group=4),
+        "router:softmax-bias": _moe(use_grouped_topk=True, num_expert_group=8, topk_group=2,
+                                    e_score_correction_bias=torch.zeros(64)),
+        "router:groups": _moe(use_grouped_topk=True, num_expert_group=7, topk_group=2),
+        "router:weight-on-input": _moe(apply_router_weight_on_input=True),
+        "router:shape": _moe(E=2048),
+    }
+    for reason, m in refused.items():
+        spec, why = route_spec(m)
+        assert spec is None and why == reason, (reason, why)
+    m = _moe()
+    m.hash_indices_table = torch.zeros(64, 2)
+    assert route_spec(m) == (None, "router:hash")
+
+
+def test_get_stats_schema(monkeypatch):
+    """The reference's keys: per class ("small", "scan") steps, hits, misses,
+    bytes, waves; the gap's counters are reported apart."""
+    off = _off(monkeypatch)
+    st = off.get_stats()
+    assert list(st) == ["small", "scan"]
+    for kind in st.values():
+        assert kind == {"steps": 0, "hits": 0, "misses": 0, "bytes": 0, "waves": 0}
+    assert off.get_gap_stats() == {"layers": 0, "gaps": 0, "misses": 0, "fast_hits": 0,
+                                   "map_writes": 0, "bytes": 0}
