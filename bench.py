@@ -1,31 +1,48 @@
 """Decode benchmark of the router-split MoE hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config v2lite]
-                    [--batches 1,8] [--slots S] [--no-cpu-baseline]
+                    [--batches 1,8] [--slots S] [--no-extras] [--no-cpu-baseline]
 
 A step is one decode step of the whole synthetic decoder at batch c: every
 layer's attention/dense blocks and, per MoE layer, routing -> streaming gap
 -> grouped SwiGLU expert product -> combine, then the LM head and greedy
 next token.  The gap op is a device launch served by the native gap server,
 so a whole step (gaps included) replays as one hipGraph.  Batches above the
-router-split envelope (c > slots // top_k) take the classic wave path: the
-pieces between MoE layers replay as hipGraphs and each MoE layer runs the
-eager classic hook (one host sync for the ids, then the expert product once
-per wave).  The timed region
-is K steps bracketed by device synchronisation; the line's ``value`` is
-tokens/s at the largest batch size (c * K / seconds).
+router-split envelope (c > slots // top_k) take the classic wave path.
+
+Per batch size: the step is captured, then the batch's 128-token synthetic
+prompts are processed position by position through the captured step
+(untimed; every prompt token is routed through every MoE layer, so the slot
+caches start warm and the KV caches hold the prompts), then W warm-up decode
+steps, then the K timed steps -- decode positions 128+W .. 128+W+K of a
+256-token decode (longer if W + K needs it).  The timed region is bracketed
+by device synchronisation; ``value`` is tokens/s of the headline workload
+(DeepSeek-V2-Lite shape, 48 slots, c=8).
+
+Routing: logits = gate GEMM + ln Zipf(1.1) popularity + sigma * z_t, z_t a
+unit-variance AR(1) with rho = 0.7 per sequence and layer (sigma 1.2, gate
+weights N(0, 0.004): the selections' top-k share is the one Zipf(1.1)
+popularity gives, and the logits' lag-1 correlation ~0.7).  The knobs and the
+measured top-k share, unique experts and misses per layer-step are in the
+line.  Rows labelled "locality" rerun the batch with sigma 0.5, whose
+fast-hit share lies in the band the reference reports for real models.
 
 Also measured in the same run:
   roofline      the dominant kernel (moe_gemm1: gate/up weights stream) timed
                 with HIP events on its own stream over the recorded routing
-                of every layer for 4 decode steps, layers rotating so the
+                of every layer for 8 decode steps, layers rotating so the
                 256 MB last-level cache cannot serve repeats; algorithmic
                 bytes = U*2*I*H*2 (unique experts' w13) + T*H*2 + P*I*2.
-                gemm2 and the combine are timed the same way ("kernels").
+                gemm2, the combine and the router are timed the same way.
   h2d           peak pinned host->device GB/s (64 MiB copies) and the rate of
                 expert-row stream-ins issued like the gap issues them.
-  cpu_baseline  the oracle (numpy/Python CPU restatement of the same path)
-                on one layer of the same shape, time-bounded sample.
+  extras        the other configurations: Qwen3-30B-A3B shape (48 layers)
+                at 64 slots c=1/8 and 96 slots c=12, the DeepSeek-V3 fp8
+                MoE stack (8 layers, 64 slots) at c=8, and the miss-dominated
+                stress (Qwen3 shape, 32 slots, uniform routing, c=4), each
+                with its gemm1 roofline fraction and H2D rate.
+  cpu_baseline  the path in torch fp32 on the host cores (oracle/cpu_path.py)
+                on one DeepSeek-V2-Lite-shaped layer, per-stage medians.
 """
 
 import argparse
@@ -44,6 +61,10 @@ DEFAULT_SLOTS = {"v2lite": 48, "qwen3": 64, "v3": 64}
 PUBLISHED_C8 = {"v2lite": 1062.6}  # reference, 1xH100 router-split, c=8 (tok/s)
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+DECODE_LEN = 256   # output tokens of the configured decode
+PROMPT_LEN = 128
+ROUTING = {"zipf_s": 1.1, "rho": 0.7, "sigma": 1.2, "gate_std": 0.004}
+LOCALITY_SIGMA = 0.5
 
 
 def parse():
@@ -55,9 +76,16 @@ def parse():
     ap.add_argument("--batches", default=None)
     ap.add_argument("--slots", type=int, default=None)
     ap.add_argument("--uniform", action="store_true", help="i.i.d. uniform routing (stress)")
+    ap.add_argument("--sigma", type=float, default=ROUTING["sigma"])
     ap.add_argument("--layers", type=int, default=None)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="only the headline configuration (no Qwen3 / V3 / stress rows)")
+    ap.add_argument("--no-locality", action="store_true",
+                    help="skip the sigma-0.5 locality rows")
+    ap.add_argument("--host-pool", default="auto", choices=["auto", "shared", "per-layer"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget-s", type=float, default=15.0)
+    ap.add_argument("--cpu-budget-s", type=float, default=20.0)
     ap.add_argument("--save-routing", default=None,
                     help="also write the routing the roofline is timed over (.npz)")
     ap.add_argument("--roofline-only", action="store_true",
@@ -71,15 +99,26 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_decode(dec, c, steps, warmup):
+def run_batch(dec, c, steps, warmup, prefill=True, label=None):
+    """Capture batch c, process its prompts (untimed), W warm-up steps, then
+    time K steps; counters are the timed steps' own."""
     import torch
 
-    dec.reset(c)
+    if c not in dec.graphs:
+        dec.capture(c)
+    t0 = time.perf_counter()
+    if prefill:
+        dec.prefill(c)
+    else:
+        dec.reset(c)
+    dec.sync()
+    prefill_s = time.perf_counter() - t0
     for _ in range(warmup):
         dec.step_graphs(c)
     dec.sync()
     before = dec.gap_counters()
     cl0 = dec.off.classic_counters()
+    pos0 = int(dec.state[c].pos[0]) if dec.has_attn else None
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -91,18 +130,54 @@ def time_decode(dec, c, steps, warmup):
     delta = {k: after[k] - before[k] for k in after}
     cl1 = dec.off.classic_counters()
     n_moe = len(dec.moe_layers)
+    h2d = delta["bytes"] / steps
     return {
-        "c": c, "path": "classic" if dec.classic(c) else "gap",
+        "c": c, "path": "classic" if dec.classic(c) else "gap", "routing": label or "zipf",
         "ms_per_step": dt / steps * 1e3, "tok_per_s": c * steps / dt,
         "classic_steps": cl1["steps"] - cl0["steps"],
         "waves_per_classic_step": (cl1["waves"] - cl0["waves"]) / max(cl1["steps"] - cl0["steps"],
                                                                       1),
         "gap_calls": delta["gaps"], "misses": delta["misses"],
         "fast_hits": delta["fast_hits"], "map_writes": delta["map_writes"],
-        "h2d_bytes_per_step": delta["bytes"] / steps,
+        "h2d_bytes_per_step": h2d, "h2d_GBs_in_step": h2d / (dt / steps) / 1e9,
         "misses_per_layer_step": delta["misses"] / max(steps * n_moe, 1),
         "fast_hit_share": delta["fast_hits"] / max(delta["gaps"], 1),
+        "prefill": {"tokens_per_sequence": dec.prompt_len if prefill else 0,
+                    "seconds": prefill_s},
+        "timed_positions": [pos0, pos0 + steps] if pos0 is not None else None,
     }
+
+
+def routing_stats(dec, recorded):
+    """Properties of the routing the step actually ran (recorded steps): the
+    share of selections that go to each layer's k most selected experts
+    (against what Zipf(zipf_s) popularity gives them), unique experts per
+    layer-step, the gate term's standard deviation and the logits' lag-1
+    correlation that follows from it."""
+    import torch
+
+    sp, knobs = dec.sp, dec.routing_knobs
+    E, k = sp["E"], sp["k"]
+    by_layer = {}
+    for r in recorded:
+        by_layer.setdefault(r["n"], []).append(r["ti"].cpu().numpy())
+    shares, uniq = [], []
+    for lst in by_layer.values():
+        cnt = np.bincount(np.concatenate([a.reshape(-1) for a in lst]), minlength=E)
+        shares.append(np.sort(cnt)[::-1][:k].sum() / max(cnt.sum(), 1))
+        uniq += [len(np.unique(a)) for a in lst]
+    out = {"top_k_share": float(np.mean(shares)), "unique_per_layer_step": float(np.mean(uniq)),
+           "recorded_steps": len(recorded) // max(len(by_layer), 1)}
+    if "zipf_s" in knobs:
+        p = 1.0 / np.arange(1, E + 1) ** knobs["zipf_s"]
+        out["zipf_top_k_share"] = float(p[:k].sum() / p.sum())
+        m = dec.moe_layers[0]
+        hn = torch.stack([r["hn"] for r in recorded if r["n"] == 0]).float()
+        g = float((hn @ m.gate.weight.float().T).std())
+        sig = knobs["sigma"]
+        out["gate_logit_std"] = g
+        out["lag1_logit_corr"] = knobs["rho"] * sig * sig / (sig * sig + g * g)
+    return out
 
 
 def record_routing(dec, c, steps):
@@ -303,10 +378,12 @@ def kernel_roofline(dec, c, recorded, reps=3):
             "copy_256MiB_GBs": 2 * nb / (usc * 1e-6) / 1e9}
 
 
-def measured_traffic(cfg, c, slots, uniform):
+def measured_traffic(cfg, c, slots, uniform, algorithmic_bytes):
     """HBM bytes per moe_gemm1 launch for this workload, from the committed
     summary of the two counter runs (FETCH_SIZE, WRITE_SIZE), each scaled by
-    what the counter reads for a 256 MiB device copy; None if not measured."""
+    what the counter reads for a 256 MiB device copy.  None when no counter
+    run covers this workload: no entry, or one measured over routing whose
+    algorithmic bytes per launch differ by more than 3% from this run's."""
     path = os.path.join(ROOT, "profiles", "gemm1_traffic.json")
     if uniform or not os.path.exists(path):
         return None
@@ -315,7 +392,11 @@ def measured_traffic(cfg, c, slots, uniform):
     rec = table.get(f"{cfg}/c{c}/slots{slots}")
     if rec is None:
         return None
+    if abs(rec["algorithmic_bytes_per_launch"] / algorithmic_bytes - 1.0) > 0.03:
+        return None
     return {"bytes_per_launch": rec["hbm_bytes_per_launch"],
+            "ratio_to_algorithmic": rec["hbm_bytes_per_launch"]
+            / rec["algorithmic_bytes_per_launch"],
             "source": f"profiles/gemm1_traffic.json[{cfg}/c{c}/slots{slots}]"}
 
 
@@ -369,57 +450,127 @@ def h2d_rates(dec):
             "bytes_per_expert": cache.bytes_per_expert}
 
 
-def cpu_baseline(spec_name, budget_s):
-    """The oracle on one MoE layer of the configured shape: routing, gap
-    bookkeeping and the dense per-token expert product, T=8 tokens/step,
-    fp32 weights, until the time budget is spent."""
-    from oracle import moe as om
-    from oracle import routing as orr
-    from oracle.slru import LayerCache
-    from sluice_amd.decoder import SPECS
+def cpu_baseline(budget_s, n_moe_layers):
+    """The reference's per-layer decode path in torch fp32 on the host cores
+    (oracle/cpu_path.py): one DeepSeek-V2-Lite-shaped MoE layer, T=8 tokens
+    per step, 64 timed steps (fewer if the budget runs out) after 4 untimed;
+    per-stage medians; tok/s = 8 / (MoE layers x the median layer step)."""
+    from oracle import cpu_path
 
-    sp = SPECS[spec_name]
-    E, H, I, k = sp["E"], sp["H"], sp["I"], sp["k"]
-    S = DEFAULT_SLOTS[spec_name]
-    T = 8
-    rng = np.random.default_rng(1)
-    w13 = (rng.standard_normal((E, 2 * I, H), dtype=np.float32) * 0.02)
-    w2 = (rng.standard_normal((E, H, I), dtype=np.float32) * 0.02)
-    gate = (rng.standard_normal((E, H), dtype=np.float32) * 0.02)
-    p = 1.0 / np.arange(1, E + 1) ** 1.1
-    zipf = np.log(p / p.sum())[rng.permutation(E)].astype(np.float32)
-    cache = LayerCache(E, E, S, 0.5)
-    slots13 = np.zeros((S, 2 * I, H), np.float32)
-    slots2 = np.zeros((S, H, I), np.float32)
-    steps = 0
-    t0 = time.perf_counter()
-    while True:
-        x = rng.standard_normal((T, H), dtype=np.float32)
-        logits = x @ gate.T + zipf[None, :] + rng.standard_normal((T, E), dtype=np.float32)
-        if sp["scoring"] == "softmax":
-            ids, w = orr.softmax_topk(logits, k, renorm=sp["renorm"])
-        else:
-            ids, w = orr.sigmoid_topk(logits, None, k, sp["n_group"], sp["topk_group"],
-                                      sp["renorm"], sp["routed_scale"])
-        for loc, slot in cache.gap(ids.reshape(-1).tolist(), fast_hit=True):
-            slots13[slot] = w13[loc]
-            slots2[slot] = w2[loc]
-        om.fused_experts(x, slots13, slots2, w, ids, expert_map=cache.map)
-        steps += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    dt = time.perf_counter() - t0
-    per_layer_step = dt / steps
-    n_moe = sp["layers"] - sp["first_dense"]
-    threads = len(os.sched_getaffinity(0))
+    r = cpu_path.run(T=8, steps=64, warmup=4, budget_s=budget_s)
+    step = r["step_median_s"]
     return {
-        "value": T / (per_layer_step * n_moe), "unit": "tok/s", "cores": threads,
-        "kind": "port",
-        "sample": (f"oracle (numpy) on one {spec_name}-shaped MoE layer: T={T} tokens/step, "
-                   f"{steps} steps in {dt:.1f}s, fp32 weights, S={S}; tok/s extrapolated to "
-                   f"{n_moe} MoE layers (attention and LM head not counted)"),
-        "ms_per_layer_step": per_layer_step * 1e3,
+        "value": r["tokens_per_step"] / (n_moe_layers * step), "unit": "tok/s",
+        "cores": r["threads"], "kind": "port",
+        "sample": (f"the path in torch fp32 on one DeepSeek-V2-Lite-shaped MoE layer (64 experts "
+                   f"top-6 + 2 shared, 48 slots, weights N(0,0.02), Zipf(1.1) router bias): "
+                   f"routing, gap bookkeeping, host row copies, expert product, combine; T=8, "
+                   f"{r['steps']} timed steps; tok/s = 8 / ({n_moe_layers} MoE layers x "
+                   f"{step * 1e3:.2f} ms median layer step); attention and LM head not counted"),
+        "stages_median_us": r["stages_us"], "stages_mean_us": r["stages_mean_us"],
+        "layer_step_ms": step * 1e3, "torch_threads": r["threads"],
+        "affinity_cores": r["affinity"], "misses": r["misses"], "steps": r["steps"],
     }
+
+
+def _every(n, fn):
+    """A progress callback passing on every n-th message."""
+    count = [0]
+
+    def cb(msg):
+        count[0] += 1
+        if count[0] % n == 0:
+            fn(msg)
+
+    return cb
+
+
+def build_decoder(cfg, slots, max_batch, a, dev, gen_len, uniform=False, stores=None):
+    from sluice_amd.decoder import SyntheticDecoder
+
+    t = time.perf_counter()
+    dec = SyntheticDecoder(cfg, max_batch=max_batch, slots=slots, prompt_len=PROMPT_LEN,
+                           gen_len=gen_len, uniform_routing=uniform, layers=a.layers, device=dev,
+                           host_pool=a.host_pool, stores=stores, zipf_s=ROUTING["zipf_s"],
+                           rho=ROUTING["rho"], sigma=a.sigma, gate_std=ROUTING["gate_std"],
+                           progress=_every(8, log))
+    build_s = time.perf_counter() - t
+    log(f"built {cfg} decoder in {build_s:.1f}s ({len(dec.moe_layers)} MoE layers, slots={slots}, "
+        f"host stores {dec.host_pool}, {dec.host_store_bytes / 2**30:.1f} GiB per layer)")
+    return dec, build_s
+
+
+def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, locality=(),
+            prefill=True, h2d=False):
+    """One configuration: its batches, the routing it ran, the kernels'
+    roofline at the largest batch, optional locality rows; returns the
+    result and the decoder's host stores (for reuse by the same shape)."""
+    import gc
+
+    import torch
+
+    dec, build_s = build_decoder(cfg, slots, max(batches), a, dev, gen_len, uniform, stores)
+    rows = []
+    for c in batches:
+        r = run_batch(dec, c, a.steps, a.warmup, prefill=prefill and not uniform,
+                      label="uniform" if uniform else "zipf")
+        log(f"{cfg} s{slots} c={c} ({r['path']}, {r['routing']}): {r['ms_per_step']:.3f} ms/step "
+            f"{r['tok_per_s']:.1f} tok/s misses/layer-step={r['misses_per_layer_step']:.3f} "
+            f"fast-hit={r['fast_hit_share']:.2%} H2D {r['h2d_GBs_in_step']:.1f} GB/s")
+        rows.append(r)
+    c_main = max(batches)
+    recorded = record_routing(dec, c_main, 8)
+    if a.save_routing and cfg == a.config:
+        save_routing(a.save_routing, recorded)
+    rstats = routing_stats(dec, recorded)
+    roof = kernel_roofline(dec, c_main, recorded)
+    rates = h2d_rates(dec) if h2d else None
+    for c in locality:
+        for rb in dec.bias_tables:
+            rb.refill(ROUTING["zipf_s"], ROUTING["rho"], LOCALITY_SIGMA, rb.knobs["seed"])
+        r = run_batch(dec, c, a.steps, a.warmup, prefill=prefill, label="locality")
+        r["sigma"] = LOCALITY_SIGMA
+        log(f"{cfg} s{slots} c={c} (locality sigma={LOCALITY_SIGMA}): {r['ms_per_step']:.3f} "
+            f"ms/step {r['tok_per_s']:.1f} tok/s misses/layer-step="
+            f"{r['misses_per_layer_step']:.3f} fast-hit={r['fast_hit_share']:.2%}")
+        rows.append(r)
+    sp = dec.sp
+    g1 = roof["gemm1"]
+    out = {
+        "config": {"model_shape": cfg, "moe_layers": len(dec.moe_layers), "experts": sp["E"],
+                   "top_k": sp["k"], "slots": slots, "max_bt": dec.thr,
+                   "dtype": "f8e4m3/bf16" if sp["fp8"] else "bf16",
+                   "routing": dict(dec.routing_knobs, **rstats),
+                   "host_pool": dec.host_pool, "host_pool_note": dec.host_pool_note,
+                   "host_store_GiB": dec.host_store_bytes * len({id(st) for st in dec.stores})
+                   / 2**30,
+                   "build_s": build_s},
+        "per_batch": rows,
+        "gemm1": {"c": c_main, "avg_us": g1["avg_us"], "achieved_GBs": g1["achieved_GBs"],
+                  "frac": g1["achieved_GBs"] / HBM_PEAK_GBS,
+                  "algorithmic_bytes_per_launch": g1["algorithmic_bytes"],
+                  "mfma_util_pct": g1["mfma_util_pct"]},
+        "kernels": {kk: roof[kk] for kk in ("gemm2", "combine", "route")},
+        "copy_256MiB_GBs": roof["copy_256MiB_GBs"],
+    }
+    if rates:
+        out["h2d"] = rates
+    stores = dec.stores
+    dec.close()
+    del dec, recorded
+    gc.collect()
+    torch.cuda.empty_cache()
+    return out, stores
+
+
+def _release():
+    """Free host stores and device memory no longer referenced."""
+    import gc
+
+    import torch
+
+    gc.collect()
+    torch.cuda.empty_cache()
 
 
 def main():
@@ -431,102 +582,104 @@ def main():
         sys.exit(2)
     import torch
 
-    from sluice_amd.decoder import SPECS, SyntheticDecoder
+    from sluice_amd.decoder import SPECS
 
     cfg = a.config
     sp = SPECS[cfg]
     slots = a.slots or DEFAULT_SLOTS[cfg]
-    k = sp["k"]
-    thr = max(1, slots // k)
     batches = [int(v) for v in a.batches.split(",")] if a.batches else (
         [1, 8] if cfg == "v2lite" else [1, 8, 12] if cfg == "qwen3" else [8])
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    t_build = time.perf_counter()
-    gen_len = a.warmup + a.steps + 8
-    dec = SyntheticDecoder(cfg, max_batch=max(batches), slots=slots, gen_len=gen_len,
-                           uniform_routing=a.uniform, layers=a.layers, device=dev)
-    log(f"built {cfg} decoder in {time.perf_counter() - t_build:.1f}s "
-        f"({len(dec.moe_layers)} MoE layers, slots={slots}, batches={batches})")
+    gen_len = max(DECODE_LEN, a.warmup + a.steps + 8)
     if a.roofline_only:
         # no decode step runs here: a counter-collecting profiler serialises
         # dispatches, which the gap's device/host hand-off cannot run under
         if not a.load_routing:
             sys.exit("--roofline-only needs --load-routing (written by --save-routing)")
+        a.host_pool = "shared"  # the kernels read the slots only; their contents do not matter
+        dec, _ = build_decoder(cfg, slots, max(batches), a, dev, gen_len, a.uniform)
         recorded = load_routing(a.load_routing, dev)
         c = int(recorded[0]["ti"].shape[0])
         roof = kernel_roofline(dec, c, recorded)
         print(json.dumps({"config": cfg, "c": c, "roofline": roof}), flush=True)
         dec.close()
         return
-    results = []
-    for c in batches:
-        dec.capture(c)
-        r = time_decode(dec, c, a.steps, a.warmup)
-        log(f"c={c} ({r['path']}): {r['ms_per_step']:.3f} ms/step {r['tok_per_s']:.1f} tok/s "
-            f"misses/layer-step={r['misses_per_layer_step']:.3f} "
-            f"fast-hit={r['fast_hit_share']:.2%} waves/classic-step="
-            f"{r['waves_per_classic_step']:.2f}")
-        results.append(r)
+    locality = () if (a.no_locality or a.uniform) else tuple(batches)
+    head, stores = measure(cfg, slots, batches, a, dev, gen_len, uniform=a.uniform,
+                           locality=locality, prefill=not a.no_prefill, h2d=True)
+    del stores
+    _release()
+    extras = []
+    if not a.no_extras and cfg == "v2lite" and not (a.uniform or a.slots or a.batches
+                                                    or a.layers):
+        q64, qstores = measure("qwen3", 64, [1, 8], a, dev, gen_len,
+                               locality=() if a.no_locality else (8,))
+        extras.append(q64)
+        q96 = measure("qwen3", 96, [12], a, dev, gen_len, stores=qstores,
+                      locality=() if a.no_locality else (12,))[0]
+        extras.append(q96)
+        stress = measure("qwen3", 32, [4], a, dev, gen_len, uniform=True, stores=qstores)[0]
+        stress["config"]["workload"] = "stress: uniform i.i.d. top-8, no prompt (no locality)"
+        extras.append(stress)
+        del qstores
+        _release()
+        v3 = measure("v3", 64, [8], a, dev, gen_len)[0]
+        extras.append(v3)
+    n_moe = sp["layers"] - sp["first_dense"] if a.layers is None else a.layers - min(
+        a.layers, sp["first_dense"])
+    cpu = None
+    if not a.no_cpu_baseline:
+        cpu = cpu_baseline(a.cpu_budget_s, n_moe)
+        log(f"cpu baseline {cpu['value']:.2f} tok/s, layer step {cpu['layer_step_ms']:.2f} ms, "
+            f"stages {cpu['stages_median_us']}")
     main_c = max(batches)
-    main = [r for r in results if r["c"] == main_c][0]
-    recorded = record_routing(dec, main_c, 4)
-    if a.save_routing:
-        save_routing(a.save_routing, recorded)
-    roof = kernel_roofline(dec, main_c, recorded)
-    h2d = h2d_rates(dec)
-    log(f"roofline {roof}")
-    log(f"h2d {h2d}")
-    cpu = None if a.no_cpu_baseline else cpu_baseline(cfg, a.cpu_budget_s)
-    if cpu:
-        log(f"cpu baseline {cpu}")
+    main_row = [r for r in head["per_batch"] if r["c"] == main_c and r["routing"] != "locality"][0]
     pub = PUBLISHED_C8.get(cfg) if main_c == 8 and not a.uniform and slots == DEFAULT_SLOTS[cfg] \
         else None
+    hc = head["config"]
     line = {
         "metric": "moe_decode_tok_per_s",
-        "value": main["tok_per_s"],
+        "value": main_row["tok_per_s"],
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": main["ms_per_step"],
+        "ms_per_step": main_row["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": (main["tok_per_s"] / pub) if pub else None,
+        "vs_baseline": (main_row["tok_per_s"] / pub) if pub else None,
         "dtype": "f8e4m3/bf16" if sp["fp8"] else "bf16",
-        "data": "synthetic (random-init weights, synthetic prompts, Zipf+AR(1) routing bias)"
-        if not a.uniform else "synthetic (random-init weights, uniform i.i.d. routing)",
-        "config": {
-            "workload": f"{cfg}-shaped decode, {len(dec.moe_layers)} MoE layers, "
-                        f"slots={slots}/{sp['E']}, MAX_BT={thr}, c={main_c}"
-                        + (" (classic wave path)" if dec.classic(main_c) else ""),
-            "model_shape": cfg, "slots": slots, "experts": sp["E"], "top_k": k,
-            "max_bt": thr, "batch": main_c, "prompt_len": dec.prompt_len,
-            "baseline_ref": "reference router-split on 1xH100 (c=8)" if pub else None,
-        },
-        "per_batch": results,
+        "data": ("synthetic (random-init weights, seeded 128-token prompts processed before "
+                 "timing, Zipf(1.1) + AR(1) rho=0.7 routing logits)") if not a.uniform else
+                "synthetic (random-init weights, uniform i.i.d. routing)",
+        "config": dict(hc, workload=(
+            f"{cfg}-shaped decode, {hc['moe_layers']} MoE layers, slots={slots}/{sp['E']}, "
+            f"MAX_BT={hc['max_bt']}, c={main_c}, 128-token prompts then decode positions "
+            f"{main_row['timed_positions']} of a {gen_len}-token decode"
+            + (" (classic wave path)" if main_row["path"] == "classic" else "")),
+            batch=main_c, prompt_len=PROMPT_LEN, decode_len=gen_len,
+            baseline_ref="reference router-split on 1xH100 with real-model routing (c=8)"
+            if pub else None),
+        "per_batch": head["per_batch"],
         "roofline": None,
-        "h2d": h2d,
-        "cpu_baseline": None,
+        "kernels": dict(head["kernels"], copy_256MiB_GBs=head["copy_256MiB_GBs"]),
+        "h2d": head.get("h2d"),
+        "cpu_baseline": cpu,
+        "extras": extras,
     }
-    if roof:
-        g1 = roof["gemm1"]
-        traffic = measured_traffic(cfg, main_c, slots, a.uniform)
-        line["roofline"] = {
-            "bound": "hbm", "achieved": g1["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": g1["achieved_GBs"] / HBM_PEAK_GBS,
-            "traffic": traffic["bytes_per_launch"] if traffic else None,
-            "traffic_source": traffic["source"] if traffic else None,
-            "kernel": g1["kernel"], "avg_us": g1["avg_us"],
-            "algorithmic_bytes_per_launch": g1["algorithmic_bytes"],
-            "mfma_util_pct": g1["mfma_util_pct"],
-        }
-        line["kernels"] = {kk: roof[kk] for kk in ("gemm2", "combine", "route")}
-        line["kernels"]["copy_256MiB_GBs"] = roof["copy_256MiB_GBs"]
-    if cpu:
-        line["cpu_baseline"] = {k_: cpu[k_] for k_ in ("value", "unit", "cores", "kind", "sample")}
+    g1 = head["gemm1"]
+    traffic = measured_traffic(cfg, main_c, slots, a.uniform, g1["algorithmic_bytes_per_launch"])
+    line["roofline"] = {
+        "bound": "hbm", "achieved": g1["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": g1["frac"],
+        "traffic": traffic["bytes_per_launch"] if traffic else None,
+        "traffic_source": traffic["source"] if traffic else None,
+        "kernel": "moe_gemm1_kernel<fp8>" if sp["fp8"] else "moe_gemm1_kernel<bf16>",
+        "avg_us": g1["avg_us"], "algorithmic_bytes_per_launch": g1["algorithmic_bytes_per_launch"],
+        "mfma_util_pct": g1["mfma_util_pct"],
+    }
     print(json.dumps(line), flush=True)
-    dec.close()
 
 
 if __name__ == "__main__":

@@ -1245,7 +1245,14 @@ extern "C" int sluice_copy_rows(void* const* dst, const void* const* src, const 
 extern "C" int sluice_host_alloc(size_t bytes, void** out) {
   if (out == nullptr || bytes == 0) return SLUICE_E_INVAL;
   *out = nullptr;
-  SLUICE_HIP_CHECK(hipHostMalloc(out, bytes, hipHostMallocPortable));
+  const hipError_t e = hipHostMalloc(out, bytes, hipHostMallocPortable);
+  if (e != hipSuccess) {
+    // the failure is reported here; clear it, or the runtime's sticky last
+    // error would be reported again by the caller's next, unrelated call
+    (void)hipGetLastError();
+    *out = nullptr;
+    return (int)e;
+  }
   return SLUICE_OK;
 }
 

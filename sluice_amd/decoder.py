@@ -86,12 +86,22 @@ class _SharedMLP(nn.Module):
 class RoutingBias:
     """Per-layer synthetic router bias: log-Zipf popularity + AR(1) noise.
 
-    The noise for every step is precomputed on the CPU from a seeded
-    generator and uploaded once, so a captured graph reads step ``i``'s row
-    through a device index."""
+    table[t, r, e] = ln p(e) + sigma * z_t[r, e]: p a Zipf(zipf_s)
+    popularity over a seeded permutation of the experts, z_t per row
+    (sequence) an AR(1) process z_t = rho z_{t-1} + sqrt(1 - rho^2) eps_t
+    with unit variance.  Every step's row is precomputed on the CPU from a
+    seeded generator and uploaded once, so a captured graph reads step
+    ``i``'s row through a device index; ``refill`` rewrites the table in
+    place (captured graphs keep reading it)."""
 
     def __init__(self, E: int, rows: int, steps: int, zipf_s: float, rho: float, sigma: float,
                  seed: int, device, step: Optional[torch.Tensor] = None):
+        self.table = torch.empty((steps, rows, E), dtype=torch.float32, device=device)
+        self.step = step if step is not None else torch.zeros((), dtype=torch.long, device=device)
+        self.refill(zipf_s, rho, sigma, seed)
+
+    def refill(self, zipf_s: float, rho: float, sigma: float, seed: int) -> None:
+        steps, rows, E = self.table.shape
         rng = np.random.default_rng(seed)
         p = 1.0 / np.arange(1, E + 1) ** zipf_s
         p = p / p.sum()
@@ -102,8 +112,14 @@ class RoutingBias:
             cur = rho * cur + np.sqrt(1 - rho * rho) * rng.standard_normal((rows, E)).astype(
                 np.float32)
             z[t] = cur
-        self.table = torch.from_numpy(zipf[None, None, :] + sigma * z).to(device)  # [steps,rows,E]
-        self.step = step if step is not None else torch.zeros((), dtype=torch.long, device=device)
+        self.table.copy_(torch.from_numpy(zipf[None, None, :] + sigma * z))
+        self.knobs = {"zipf_s": zipf_s, "rho": rho, "sigma": sigma, "seed": seed}
+
+    def fill_uniform(self, gen: torch.Generator, scale: float = 10.0) -> None:
+        """Large i.i.d. noise in every entry: uniform top-k routing."""
+        self.table.normal_(generator=gen)
+        self.table.mul_(scale)
+        self.knobs = {"uniform": True, "scale": scale}
 
     def __call__(self, T: int) -> torch.Tensor:
         return self.table.index_select(0, self.step.view(1))[0, :T]
@@ -516,7 +532,8 @@ class _Fp8SharedMLP(nn.Module):
 def _expert_store(sp, gen_seed, dev, fp8):
     """One pinned host store of every expert of a layer ([E, ...] per param),
     filled from device-generated random values (N(0, 0.02) for bf16; for fp8,
-    e4m3fn codes of N(0, 0.5) with block scales in [0.01, 0.03))."""
+    e4m3fn codes of N(0, 0.5) with block scales in [0.01, 0.03)), generated
+    and copied down in chunks of experts (about 1 GB each)."""
     E, H, I = sp["E"], sp["H"], sp["I"]
     g = torch.Generator(device=dev).manual_seed(gen_seed)
     out = {}
@@ -524,13 +541,17 @@ def _expert_store(sp, gen_seed, dev, fp8):
     for name, shp in shapes.items():
         dt = torch.uint8 if fp8 else torch.bfloat16
         st = ops.HostStore(shp, dt)
-        for e in range(E):
+        row_bytes = st.nbytes // E
+        n = max(1, (1 << 30) // max(row_bytes, 1))
+        for e0 in range(0, E, n):
+            e1 = min(E, e0 + n)
+            v = torch.randn((e1 - e0, *shp[1:]), generator=g, device=dev)
             if fp8:
-                v = (torch.randn(shp[1:], generator=g, device=dev) * 0.5).to(
-                    torch.float8_e4m3fn).view(torch.uint8)
+                v = v.mul_(0.5).to(torch.float8_e4m3fn).view(torch.uint8)
             else:
-                v = (torch.randn(shp[1:], generator=g, device=dev) * 0.02).to(torch.bfloat16)
-            st.tensor[e].copy_(v)
+                v = v.mul_(0.02).to(torch.bfloat16)
+            st.tensor[e0:e1].copy_(v)
+            del v
         out[name] = st
     if fp8:
         for name, shp in (("w13_weight_scale", (E, 2 * I // 128, H // 128)),
@@ -539,6 +560,47 @@ def _expert_store(sp, gen_seed, dev, fp8):
             st.tensor.copy_(torch.rand(shp, generator=g, device=dev) * 0.02 + 0.01)
             out[name] = st
     return out
+
+
+def expert_store_bytes(sp) -> int:
+    """Host bytes of one layer's expert store."""
+    E, H, I = sp["E"], sp["H"], sp["I"]
+    if sp["fp8"]:
+        return E * (3 * I * H + ((2 * I // 128) * (H // 128) + (H // 128) * (I // 128)) * 4)
+    return E * 3 * I * H * 2
+
+
+def host_memory_available() -> Optional[int]:
+    """MemAvailable of this host (bytes), bounded by the cgroup limit if one
+    is set; None if unknown."""
+    avail = None
+    try:
+        with open("/proc/meminfo") as f:
+            for line in f:
+                if line.startswith("MemAvailable:"):
+                    avail = int(line.split()[1]) * 1024
+    except OSError:
+        return None
+    for path in ("/sys/fs/cgroup/memory.max", "/sys/fs/cgroup/memory/memory.limit_in_bytes"):
+        try:
+            with open(path) as f:
+                raw = f.read().strip()
+            if raw and raw != "max" and int(raw) < (1 << 60):
+                used = 0
+                for upath in ("/sys/fs/cgroup/memory.current",
+                              "/sys/fs/cgroup/memory/memory.usage_in_bytes"):
+                    try:
+                        with open(upath) as uf:
+                            used = int(uf.read().strip())
+                        break
+                    except OSError:
+                        continue
+                lim = int(raw) - used
+                avail = lim if avail is None else min(avail, lim)
+            break
+        except (OSError, ValueError):
+            continue
+    return avail
 
 
 class _StoreMoELayer(nn.Module):
@@ -684,27 +746,38 @@ class SyntheticDecoder:
     is a device launch and the whole step -- pieces and gaps -- is captured
     as one graph; with ``gap_server=False`` each piece is a graph and the
     reference's eager gap runs between them.
-    Prompts are synthetic: the first ``prompt_len`` KV positions hold random
-    latents/keys/values; decoding starts at position ``prompt_len``.
+    Prompts are synthetic: until ``prefill`` runs, the first ``prompt_len``
+    KV positions hold random latents/keys/values; ``prefill(c)`` decodes a
+    seeded random prompt through the model position by position instead
+    (every prompt token routed through every MoE layer).  Decoding starts at
+    position ``prompt_len``; the caches hold prompt_len + gen_len positions.
 
     ``expert_checkpoint`` (a safetensors file or directory, Hugging Face
     expert naming) loads every MoE layer's routed experts from a checkpoint
     instead of random values; the other weights stay random.
 
     Routing: router logits = gate GEMM (weights N(0, gate_std)) + log-Zipf
-    (zipf_s) popularity over a seeded permutation + sigma * z_t, z_t an AR(1)
-    process (rho) per sequence and layer.  The defaults (gate_std 0.004,
-    sigma 0.5) put the gap's fast-hit share in the 84-89% band at V2-Lite
-    slots=48, matching the 86-99% the reference reports for real models
-    (docs/router-split.md:330, README.md:155); ``uniform_routing`` replaces
-    the bias with large i.i.d. noise (uniform top-k, the miss-dominated
-    stress case)."""
+    (zipf_s) popularity over a seeded permutation + sigma * z_t, z_t a
+    unit-variance AR(1) process (rho) per sequence and layer.  The defaults
+    (zipf_s 1.1, rho 0.7, sigma 1.2, gate_std 0.004: a gate term of standard
+    deviation ~0.18 at hidden 2048) give selections whose top-k experts take
+    the share Zipf(1.1) popularity gives them (55-57% at 64 experts top-6
+    and 128 top-8) and logits whose step-to-step correlation is ~0.68;
+    ``RoutingBias.refill`` changes the knobs in place.
+    ``uniform_routing`` replaces the bias with large i.i.d. noise (uniform
+    top-k, the miss-dominated stress case).
+
+    Host stores: ``host_pool`` "shared" (one store of the layer shape, every
+    MoE layer streams from it), "per-layer", or "auto" (per-layer when they
+    fit in half of the host memory available, else shared); ``stores``
+    adopts the per-layer stores of another decoder of the same shape."""
 
     def __init__(self, spec: str, max_batch: int, slots: int, prompt_len: int = 128,
-                 gen_len: int = 256, seed: int = 0, device=None, shared_host_pool: bool = True,
-                 zipf_s: float = 1.1, rho: float = 0.7, sigma: float = 0.5,
+                 gen_len: int = 256, seed: int = 0, device=None, host_pool: str = "shared",
+                 zipf_s: float = 1.1, rho: float = 0.7, sigma: float = 1.2,
                  gate_std: float = 0.004, uniform_routing: bool = False, fast_hit: bool = True,
-                 layers: int = None, gap_server: bool = True, expert_checkpoint=None):
+                 layers: int = None, gap_server: bool = True, expert_checkpoint=None,
+                 stores=None, progress=None):
         self.sp = sp = dict(SPECS[spec])
         if layers is not None:
             sp["layers"] = layers
@@ -713,9 +786,26 @@ class SyntheticDecoder:
         # (a multiple of 32: the MLA latent cache is also kept in 32-row blocks)
         self.max_batch, self.max_len = max_batch, (prompt_len + gen_len + 8 + 31) // 32 * 32
         self.prompt_len = prompt_len
+        self.gen_len = gen_len
         g = torch.Generator(device=dev).manual_seed(seed)
         H = sp["H"]
-        steps_tbl = gen_len + 64
+        steps_tbl = prompt_len + gen_len + 64
+        n_moe = sp["layers"] - sp["first_dense"]
+        self.host_store_bytes = expert_store_bytes(sp)
+        if stores is not None:
+            host_pool = "adopted"
+        elif host_pool == "auto":
+            avail = host_memory_available()
+            fits = avail is not None and n_moe * self.host_store_bytes <= avail // 2
+            host_pool = "per-layer" if fits else "shared"
+        if host_pool not in ("shared", "per-layer", "adopted"):
+            raise ValueError(f"host_pool {host_pool!r}")
+        self.host_pool = host_pool
+        self.host_pool_note = None
+        self.stores = []
+        self.routing_knobs = ({"uniform": True} if uniform_routing else
+                              {"zipf_s": zipf_s, "rho": rho, "sigma": sigma})
+        self.routing_knobs["gate_std"] = gate_std
         self.has_attn = sp["attn"] is not None
         self.embed = _randn((sp["vocab"], H), g, 0.02, dev) if self.has_attn else None
         self.lm_head = _randn((sp["vocab"], H), g, 0.02, dev) if self.has_attn else None
@@ -748,14 +838,29 @@ class SyntheticDecoder:
                     if shp != (sp["E"], 2 * sp["I"], sp["H"]):
                         raise ValueError(f"checkpoint layer {li}: experts {shp} do not match the "
                                          f"{spec} shape")
-                elif store is None or not shared_host_pool:
-                    store = _expert_store(sp, 7000 + li, dev, sp["fp8"])
+                elif stores is not None:
+                    store = stores[len(self.moe_layers)]
+                elif store is None or host_pool == "per-layer":
+                    try:
+                        store = _expert_store(sp, 7000 + li, dev, sp["fp8"])
+                    except RuntimeError as e:
+                        if store is None or host_pool != "per-layer":
+                            raise
+                        # pinned memory ran out: the remaining layers share
+                        # the last store made
+                        self.host_pool = host_pool = "per-layer, then shared"
+                        self.host_pool_note = (f"pinned allocation failed at MoE layer "
+                                               f"{len(self.moe_layers)}: {e}")
+                        if progress is not None:
+                            progress(self.host_pool_note)
+                    if progress is not None:
+                        progress(f"host store of layer {li} ready")
+                self.stores.append(store)
                 rb = None
                 if uniform_routing:
                     rb = RoutingBias(sp["E"], max_batch, steps_tbl, 0.0, 0.0, 0.0, 8000 + li, dev,
                                      step=self.step)
-                    rb.table.normal_(generator=g)
-                    rb.table.mul_(10.0)
+                    rb.fill_uniform(g)
                 else:
                     rb = RoutingBias(sp["E"], max_batch, steps_tbl, zipf_s, rho, sigma, 8000 + li,
                                      dev, step=self.step)
@@ -797,6 +902,8 @@ class SyntheticDecoder:
             st.bidx = torch.arange(c, device=dev)
             st.tokens = (torch.randint(0, max(self.sp["vocab"], 1), (c,), generator=g, device=dev)
                          if self.has_attn else None)
+            st.prompt = (torch.randint(0, max(self.sp["vocab"], 1), (c, self.prompt_len),
+                                       generator=g, device=dev) if self.has_attn else None)
             st.x = _randn((c, self.sp["H"]), g, 1.0, dev)  # MoE-stack input
             st.out_tokens = []
             self.state[c] = st
@@ -806,6 +913,26 @@ class SyntheticDecoder:
         st = self._state(c)
         st.pos.fill_(self.prompt_len)
         self.step.zero_()
+
+    def prefill(self, c, graphs: bool = True) -> None:
+        """Process batch c's synthetic prompts, untimed: position by position
+        through the decode step (the captured one when ``graphs``), each
+        step's input token the prompt's next one, so every prompt token is
+        routed through every MoE layer -- the slot caches warm up on the
+        prompts' routing -- and the KV caches hold the prompts' keys and
+        values.  Ends at position prompt_len with the first generated token
+        as the next input.  (A MoE stack without attention steps its hidden
+        state prompt_len times.)"""
+        st = self._state(c)
+        st.pos.zero_()
+        self.step.zero_()
+        for p in range(self.prompt_len):
+            if st.prompt is not None:
+                st.tokens.copy_(st.prompt[:, p])
+            if graphs:
+                self.step_graphs(c)
+            else:
+                self.step_eager(c)
 
     # -- pieces ----------------------------------------------------------------
     def _block_front(self, i, io, st):

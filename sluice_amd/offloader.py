@@ -976,6 +976,10 @@ class ExpertStreamOffloader(_OffloaderBase):
         return out
 
     def close(self) -> None:
+        """Stop the gap server, destroy the native layers and drop this
+        offloader's references to host stores and layers (the slot buffers
+        live on as the layers' params while the model does); the gap op no
+        longer dispatches here."""
         lib = _lib.load()
         if self._server is not None:
             srv, self._server = self._server, None
@@ -986,6 +990,12 @@ class ExpertStreamOffloader(_OffloaderBase):
             if c.handle:
                 lib.sluice_layer_destroy(c.handle)
                 c.handle = None
+            c.cpu_store.clear()
+            c.host_stores.clear()
+        self._prepared_stores.clear()
+        self._layers.clear()
+        if _ACTIVE_GAP.get("offloader") is self:
+            _ACTIVE_GAP["offloader"] = None
 
 
 def _read_pin_file(path: str) -> dict:

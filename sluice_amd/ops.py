@@ -16,6 +16,7 @@ traceable.
 
 
 import ctypes
+import weakref
 from typing import Optional
 
 import numpy as np
@@ -301,7 +302,9 @@ if not _vllm_present() and not hasattr(torch.ops.vllm, "fused_experts"):
 # ---------------------------------------------------------------------------
 # Pinned host store
 # ---------------------------------------------------------------------------
-_HOST_STORES: dict = {}  # base address -> HostStore (live allocations)
+# base address -> HostStore of every live store (weak: the registry keeps
+# nothing alive).
+_HOST_STORES: "weakref.WeakValueDictionary" = weakref.WeakValueDictionary()
 
 
 def host_store_of(t: torch.Tensor):
@@ -311,15 +314,26 @@ def host_store_of(t: torch.Tensor):
         return None
     lo = t.data_ptr()
     hi = lo + t.numel() * t.element_size()
-    for base, st in _HOST_STORES.items():
+    for base, st in list(_HOST_STORES.items()):
         if base <= lo and hi <= base + st.nbytes:
             return st
     return None
 
 
+def _free_host(ptr: int) -> None:
+    lib = _lib._lib
+    if lib is not None:
+        lib.sluice_host_free(ptr)
+
+
 class HostStore:
     """Exact-size pinned host buffer (hipHostMalloc) viewed as a CPU tensor.
-    Owners keep the HostStore object alive; the memory is freed with it."""
+
+    The memory lives as long as any tensor viewing it: the tensor keeps the
+    buffer object it was made from, and the buffer's finalizer frees the
+    allocation when the last view goes (no reference cycle, so nothing
+    waits for the cycle collector).  Memory still held at interpreter exit is
+    left to the process teardown."""
 
     def __init__(self, shape, dtype: torch.dtype):
         lib = _lib.load()
@@ -330,20 +344,11 @@ class HostStore:
         _lib.check(lib.sluice_host_alloc(max(self.nbytes, 1), ctypes.byref(p)), "sluice_host_alloc")
         self._ptr = p.value
         raw = (ctypes.c_uint8 * max(self.nbytes, 1)).from_address(self._ptr)
+        fin = weakref.finalize(raw, _free_host, self._ptr)
+        fin.atexit = False
         arr = np.frombuffer(raw, dtype=np.uint8, count=self.nbytes)
         self.tensor = torch.from_numpy(arr).view(dtype).view(*shape)
         _HOST_STORES[self._ptr] = self
 
     def data_ptr(self) -> int:
         return self._ptr
-
-    def __del__(self):
-        p = getattr(self, "_ptr", None)
-        if p and _HOST_STORES is not None:
-            _HOST_STORES.pop(p, None)
-        if p and _lib is not None and _lib._lib is not None:
-            try:
-                _lib._lib.sluice_host_free(p)
-            except Exception:
-                pass
-            self._ptr = None
