@@ -378,18 +378,18 @@ def kernel_roofline(dec, c, recorded, reps=3):
             "copy_256MiB_GBs": 2 * nb / (usc * 1e-6) / 1e9}
 
 
-def measured_traffic(cfg, c, slots, uniform, algorithmic_bytes):
-    """HBM bytes per moe_gemm1 launch for this workload, from the committed
+def measured_traffic(cfg, c, slots, uniform, algorithmic_bytes, kernel="moe_gemm1"):
+    """HBM bytes per launch of `kernel` for this workload, from the committed
     summary of the two counter runs (FETCH_SIZE, WRITE_SIZE), each scaled by
     what the counter reads for a 256 MiB device copy.  None when no counter
     run covers this workload: no entry, or one measured over routing whose
     algorithmic bytes per launch differ by more than 3% from this run's."""
-    path = os.path.join(ROOT, "profiles", "gemm1_traffic.json")
+    path = os.path.join(ROOT, "profiles", "moe_kernels_traffic.json")
     if uniform or not os.path.exists(path):
         return None
     with open(path) as f:
         table = json.load(f)
-    rec = table.get(f"{cfg}/c{c}/slots{slots}")
+    rec = table.get(f"{cfg}/c{c}/slots{slots}", {}).get(kernel)
     if rec is None:
         return None
     if abs(rec["algorithmic_bytes_per_launch"] / algorithmic_bytes - 1.0) > 0.03:
@@ -397,7 +397,7 @@ def measured_traffic(cfg, c, slots, uniform, algorithmic_bytes):
     return {"bytes_per_launch": rec["hbm_bytes_per_launch"],
             "ratio_to_algorithmic": rec["hbm_bytes_per_launch"]
             / rec["algorithmic_bytes_per_launch"],
-            "source": f"profiles/gemm1_traffic.json[{cfg}/c{c}/slots{slots}]"}
+            "source": f"profiles/moe_kernels_traffic.json[{cfg}/c{c}/slots{slots}][{kernel}]"}
 
 
 def h2d_rates(dec):
