@@ -44,12 +44,14 @@
 #include <time.h>
 
 #include <atomic>
+#include <cmath>
 #include <mutex>
 #include <new>
 #include <thread>
 #include <vector>
 
 #include "common.h"
+#include "slotwait.h"
 #include "slru.h"
 #include "stamp.h"
 
@@ -166,8 +168,11 @@ struct GapMailbox {
   int32_t resp_code;   // 0: install slot_global as the map; else leave it
   int32_t standing;    // the device map is the standing map
   int32_t n_slots;
-  int32_t host_pad[11];
+  int32_t n_fill;      // slots the answered gap filled (their rows may still stream)
+  int32_t host_pad[10];
   int32_t slot_global[SLUICE_MAX_SLOTS];  // slot -> global id, -1 = empty
+  int32_t fill[SLUICE_MAX_SLOTS];         // the filled slots
+  int32_t slot_ready[SLUICE_MAX_SLOTS];   // stamp of the last gap whose rows into the slot landed
 };
 
 constexpr int kRecCountBits = 11;  // n_uniq, n_miss <= SLUICE_MAX_EXPERTS
@@ -241,11 +246,16 @@ __device__ int wait_eq(const int32_t* p, int32_t want, const int32_t* abort_flag
 // 0, so later gaps skip that bus read), [2] the last host ack read.
 constexpr int kGapMaxPerThread = SLUICE_MAX_EXPERTS / kLookupThreads;
 
+// pending [S]: the stamp of the gap that filled each slot, while its rows may
+// still stream (0 = none); prev: [0] = count, [1..] = the slots the last
+// waiting gap filled, cleared by the next gap (the expert product of that
+// gap's step waited for each of them).
 __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     const int32_t* __restrict__ ids, int n, int32_t* __restrict__ map,
     const int32_t* __restrict__ local_of, int E, GapMailbox* mb, int32_t* dev_state,
-    const int32_t* abort_flag, long long timeout_ticks, const u32x4_t* __restrict__ copy_src,
-    u32x4_t* __restrict__ copy_dst, int copy_vecs) {
+    int32_t* __restrict__ pending, int32_t* __restrict__ prev, int S, const int32_t* abort_flag,
+    long long timeout_ticks, const u32x4_t* __restrict__ copy_src, u32x4_t* __restrict__ copy_dst,
+    int copy_vecs) {
   __shared__ int present[SLUICE_MAX_EXPERTS];
   __shared__ int s_uniq[SLUICE_MAX_EXPERTS];
   __shared__ int wcount[kWaves];
@@ -281,7 +291,12 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     seen = dev_state[2];
   }
   for (int e = tid; e < E; e += kLookupThreads) present[e] = 0;
+  {
+    const int np = prev[0];
+    for (int i = tid; i < np; i += kLookupThreads) pending[prev[1 + i]] = 0;
+  }
   __syncthreads();
+  if (tid == 0) prev[0] = 0;
   // Record s reuses the slot of record s - kRing, which the host must have
   // copied out (it normally has, long ago).  When the last ack read does not
   // show it, a fresh read goes out now and is checked after the compaction.
@@ -381,6 +396,21 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
   }
   __syncthreads();
   for (int e = tid; e < E; e += kLookupThreads) map[e] = present[e];
+  // The slots the host is still filling: the expert product waits for them.
+  // Their poll claims and seen marks (after the fill list) start over.
+  int32_t* claim = prev + 1 + S;
+  const int nf = min(ld_sys(&mb->n_fill), S);
+  for (int i = tid; i < nf; i += kLookupThreads) {
+    const int sl = ld_sys(&mb->fill[i]);
+    const int ok = (unsigned)sl < (unsigned)S;
+    if (ok) {
+      pending[sl] = s_stamp;
+      claim[sl] = 0;
+      claim[S + sl] = 0;
+    }
+    prev[1 + i] = ok ? sl : 0;
+  }
+  if (tid == 0) prev[0] = nf;
 }
 
 // ---------------------------------------------------------------------------
@@ -473,6 +503,7 @@ struct sluice_layer {
   int32_t* ids_host = nullptr;  // pinned staging of the step's ids
   size_t ids_cap = 0;
   int64_t classic_steps = 0, classic_waves = 0;
+  std::vector<hipEvent_t> fill_ev;  // one per expert streamed by a gap
 };
 
 namespace {
@@ -491,28 +522,77 @@ int layer_device_init(sluice_layer* L) {
   void* dp = nullptr;
   SLUICE_HIP_CHECK(hipHostGetDevicePointer(&dp, p, 0));
   L->mb_dev = static_cast<GapMailbox*>(dp);
-  const int E = L->c.E;
-  SLUICE_HIP_CHECK(hipMalloc((void**)&L->dev_block, sizeof(int32_t) * (E + 3)));
+  const int E = L->c.E, S = L->c.S;
+  // [E] local_of | last stamp, standing map seen, last ack read | [S] pending
+  // | prev count, [S] prev fills | [S] claim | [S] seen
+  const size_t n = (size_t)E + 3 + S + 1 + S + S + S;
+  SLUICE_HIP_CHECK(hipMalloc((void**)&L->dev_block, sizeof(int32_t) * n));
   std::vector<int32_t> blk(L->c.local_of.begin(), L->c.local_of.end());
-  blk.push_back(0);  // last stamp issued
-  blk.push_back(0);  // standing map seen
-  blk.push_back(0);  // last ack read
-  SLUICE_HIP_CHECK(hipMemcpy(L->dev_block, blk.data(), sizeof(int32_t) * (E + 3),
+  blk.resize(n, 0);
+  SLUICE_HIP_CHECK(hipMemcpy(L->dev_block, blk.data(), sizeof(int32_t) * n,
                              hipMemcpyHostToDevice));
+  if (L->map_dev != nullptr) {
+    SlotWait w;
+    w.pending = L->dev_block + E + 3;
+    w.ready = L->mb_dev->slot_ready;
+    w.claim = L->dev_block + E + 3 + S + 1 + S;
+    w.seen = w.claim + S;
+    w.abort_flag = g_abort_dev;
+    w.status = &L->mb_dev->dev_status;
+    w.timeout_ticks = (long long)(gap_timeout_s() * 1000.0 * (double)R->clock_khz);
+    slotwait_register(L->map_dev, w);
+  }
   return SLUICE_OK;
 }
 
 constexpr int kNothing = 1;  // serve_one: no record posted yet (non-blocking)
 
-void respond(sluice_layer* L, int32_t stamp, int code) {
+// Answer the device's gap `stamp`: on success the standing slot table and
+// the slots being filled (the product waits for each one's ready mark).
+void respond(sluice_layer* L, int32_t stamp, int code, int n_fill) {
   GapMailbox* mb = L->mb;
   if (code == SLUICE_OK) {
     L->c.slot_globals(mb->slot_global);
     mb->n_slots = L->c.S;
     mb->standing = 1;
+    for (int i = 0; i < n_fill; ++i) mb->fill[i] = L->streams[2 * i + 1];
+    mb->n_fill = n_fill;
+  } else {
+    mb->n_fill = 0;
   }
   mb->resp_code = code;
   __atomic_store_n(&mb->resp_stamp, stamp, __ATOMIC_RELEASE);
+}
+
+// Experts whose rows share one completion event.  Each event recorded
+// between copies idles the copy engine a few microseconds (~6 us measured
+// between 9.4 MB copies), while a group's rows only become usable once the
+// whole group landed, which exposes the last group's expert product (its
+// weights read at HBM rate, ~5 TB/s) after the stream ends.  With T bytes
+// streamed, groups of g bytes cost about (T / g) * 6 us + g / 5 TB/s, least
+// at g = sqrt(3e7 B * T): one expert per event for a few misses, several for
+// a miss-dominated gap.
+int experts_per_event(const sluice_layer* L, int n_streams) {
+  size_t per_expert = 0;
+  for (const ParamRows& p : L->params) per_expert += p.row_bytes;
+  if (per_expert == 0 || n_streams <= 1) return 1;
+  const double total = (double)per_expert * (double)n_streams;
+  const double group = std::sqrt(3.0e7 * total);
+  const int k = (int)(group / (double)per_expert + 0.5);
+  return std::max(1, std::min(k, n_streams));
+}
+
+// Spin until `ev` completed (bounded).  0 or an error code.
+int wait_event(hipEvent_t ev) {
+  const double t0 = now_s();
+  unsigned spins = 0;
+  for (;;) {
+    const hipError_t q = hipEventQuery(ev);
+    if (q == hipSuccess) return SLUICE_OK;
+    if (q != hipErrorNotReady) return (int)q;
+    _mm_pause();
+    if ((++spins & 1023u) == 0 && now_s() - t0 > gap_timeout_s()) return SLUICE_E_TIMEOUT;
+  }
 }
 
 // A record after the last one served has been posted (records are posted
@@ -586,11 +666,25 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
   } else if (grc == 0 && was_standing && n_streams != n_miss) {
     rc = SLUICE_E_STATE;
   } else if (n_streams > 0) {
-    // On overflow the rows acquired before it still stream, as in the
-    // reference (its copies were issued before the raise); the device map
-    // is left as it was.
     DeviceRes* R = nullptr;
     rc = device_res(L->device, &R);
+    // A waiting gap whose bookkeeping succeeded is answered before its rows
+    // land: the device installs the map at once and its expert product
+    // computes the hit experts while the misses stream, waiting per filled
+    // slot for the ready mark set below.  (On overflow the rows acquired
+    // before it still stream, as in the reference, whose copies were issued
+    // before the raise; the device map is left as it was, answered after.)
+    const bool early = waits && grc == 0 && rc == SLUICE_OK;
+    const int per_event = experts_per_event(L, n_streams);
+    const int n_events = (n_streams + per_event - 1) / per_event;
+    while (rc == SLUICE_OK && (int)L->fill_ev.size() < n_events) {
+      hipEvent_t ev = nullptr;
+      const hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+      if (e != hipSuccess) rc = (int)e;
+      else L->fill_ev.push_back(ev);
+    }
+    if (early && rc == SLUICE_OK) respond(L, want, SLUICE_OK, n_streams);
+    int issued = 0;  // events recorded
     for (int i = 0; rc == SLUICE_OK && i < n_streams; ++i) {
       const int local = L->streams[2 * i], slot = L->streams[2 * i + 1];
       for (const ParamRows& p : L->params) {
@@ -603,14 +697,31 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
         }
         L->bytes += (int64_t)p.row_bytes;
       }
+      if (rc == SLUICE_OK && ((i + 1) % per_event == 0 || i + 1 == n_streams)) {
+        const hipError_t e = hipEventRecord(L->fill_ev[issued], R->copy);
+        if (e != hipSuccess) rc = (int)e;
+        else ++issued;
+      }
     }
-    if (rc == SLUICE_OK) {
-      hipError_t e = hipStreamSynchronize(R->copy);
-      if (e != hipSuccess) rc = (int)e;
+    // Each group of experts landed: mark its slots ready for this gap.
+    for (int g = 0; g < issued; ++g) {
+      const int w = wait_event(L->fill_ev[g]);
+      if (w != SLUICE_OK) {
+        if (rc == SLUICE_OK) rc = w;
+        break;
+      }
+      if (!early) continue;
+      const int end = std::min(n_streams, (g + 1) * per_event);
+      for (int i = g * per_event; i < end; ++i)
+        __atomic_store_n(&mb->slot_ready[L->streams[2 * i + 1]], want, __ATOMIC_RELEASE);
+    }
+    if (early) {
+      L->done_stamp.store(want, std::memory_order_release);
+      return rc;
     }
   }
   if (waits && rc == SLUICE_OK && grc != 0) rc = grc;
-  if (waits) respond(L, want, rc);
+  if (waits) respond(L, want, rc, 0);
   L->done_stamp.store(want, std::memory_order_release);
   return rc;
 }
@@ -625,9 +736,11 @@ int launch_gap(sluice_layer* L, const int32_t* ids, int n, const void* hs_src, v
   if ((hs_bytes & 15) != 0 || ((uintptr_t)hs_src & 15) != 0 || ((uintptr_t)hs_dst & 15) != 0)
     return SLUICE_E_INVAL;
   if (hs_bytes > 0 && (hs_src == nullptr || hs_dst == nullptr)) return SLUICE_E_INVAL;
+  const int E = L->c.E, S = L->c.S;
+  int32_t* pending = L->dev_block + E + 3;
   hipLaunchKernelGGL(gap_kernel, dim3(1), dim3(kLookupThreads), 0, st, ids, n, L->map_dev,
-                     L->dev_block, L->c.E, L->mb_dev, L->dev_block + L->c.E, g_abort_dev,
-                     timeout_ticks(L), (const u32x4_t*)hs_src, (u32x4_t*)hs_dst,
+                     L->dev_block, E, L->mb_dev, L->dev_block + E, pending, pending + S, S,
+                     g_abort_dev, timeout_ticks(L), (const u32x4_t*)hs_src, (u32x4_t*)hs_dst,
                      (int)(hs_bytes / 16));
   return (int)hipGetLastError();
 }
@@ -692,6 +805,8 @@ extern "C" int sluice_layer_destroy(sluice_layer* L) {
   if (L == nullptr) return SLUICE_OK;
   if (L->server != nullptr) return SLUICE_E_STATE;
   int rc = SLUICE_OK;
+  if (L->map_dev != nullptr && L->mb != nullptr) slotwait_unregister(L->map_dev);
+  for (hipEvent_t ev : L->fill_ev) (void)hipEventDestroy(ev);
   if (L->mb != nullptr) {
     hipError_t e = hipHostFree(L->mb);
     if (e != hipSuccess) rc = (int)e;
@@ -844,6 +959,11 @@ extern "C" int sluice_layer_gap_resync(sluice_layer* L) {
   __atomic_store_n(&L->mb->ack_stamp, dev_stamp, __ATOMIC_RELEASE);
   for (int i = 0; i < kRing; ++i) __atomic_store_n(&L->mb->rec[i].hdr, (uint64_t)0, __ATOMIC_RELEASE);
   __atomic_store_n(&L->mb->dev_status, 0, __ATOMIC_RELEASE);
+  // no slot is left waiting for rows: the aborted gaps' rows are not coming
+  const size_t n_pend = (size_t)L->c.S + 1 + L->c.S + 2 * (size_t)L->c.S;
+  std::vector<int32_t> zero(n_pend, 0);
+  SLUICE_HIP_CHECK(hipMemcpy(L->dev_block + L->c.E + 3, zero.data(), sizeof(int32_t) * n_pend,
+                             hipMemcpyHostToDevice));
   return SLUICE_OK;
 }
 
@@ -1281,4 +1401,38 @@ extern "C" const char* sluice_strerror(int code) {
       if (code > 0) return hipGetErrorString((hipError_t)code);
       return "unknown sluice error";
   }
+}
+
+// ---------------------------------------------------------------------------
+// Slot-wait registry: a streaming layer's expert map -> its slot-wait view.
+// ---------------------------------------------------------------------------
+namespace {
+std::mutex g_wait_mu;
+std::vector<std::pair<const int32_t*, SlotWait>> g_wait;
+}  // namespace
+
+void slotwait_register(const int32_t* map, const SlotWait& w) {
+  std::lock_guard<std::mutex> lk(g_wait_mu);
+  for (auto& e : g_wait)
+    if (e.first == map) {
+      e.second = w;
+      return;
+    }
+  g_wait.emplace_back(map, w);
+}
+
+void slotwait_unregister(const int32_t* map) {
+  std::lock_guard<std::mutex> lk(g_wait_mu);
+  for (size_t i = 0; i < g_wait.size(); ++i)
+    if (g_wait[i].first == map) {
+      g_wait.erase(g_wait.begin() + (long)i);
+      return;
+    }
+}
+
+SlotWait slotwait_lookup(const int32_t* map) {
+  std::lock_guard<std::mutex> lk(g_wait_mu);
+  for (const auto& e : g_wait)
+    if (e.first == map) return e.second;
+  return SlotWait{};
 }

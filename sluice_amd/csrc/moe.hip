@@ -23,6 +23,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "slotwait.h"
 #include "stream.h"
 
 // Scratch of sluice_fused_experts_bf16_noalloc (align plan, activations, fp32
@@ -36,6 +37,11 @@ namespace {
 
 constexpr int kBM = SLUICE_BLOCK_M;      // tokens per block (MFMA N)
 constexpr int kBlockInts = 2 + kBM;      // {slot, count, pair[16]}
+// A block's slot field carries this bit when the slot's rows may still be
+// streaming in (a pending slot of the layer's last gap): its work items
+// wait for the slot before they read its weights.
+constexpr int kPendingBit = 1 << 30;
+constexpr int kSlotMask = kPendingBit - 1;
 constexpr int kPlanHeader = 4;
 constexpr int kKS = 4;                   // waves per workgroup (K split)
 constexpr int kThreads = 64 * kKS;
@@ -72,14 +78,19 @@ struct AlignScratch {
   int cnt[SLUICE_MAX_SLOTS];
   int boff[SLUICE_MAX_SLOTS];
   int run[SLUICE_MAX_SLOTS];
+  int pend[SLUICE_MAX_SLOTS];       // the slot's rows may still be streaming
   int chunk_slot[kThreads];
-  int wsum[kKS];
+  int wsum[2][kKS];
   int total;
 };
 
+// pending [S] (device, may be null): nonzero for the slots whose rows the
+// layer's last gap is still streaming; their blocks come after every other
+// routed block (so the work on resident experts is dispatched first) and
+// carry kPendingBit.
 __device__ int build_plan(const int32_t* __restrict__ ids, int P, const int32_t* __restrict__ map,
-                          int E, int S, int T, int n_sh, AlignScratch& sc, int32_t* blocks,
-                          int32_t* valid) {
+                          int E, int S, int T, int n_sh, const int32_t* __restrict__ pending,
+                          AlignScratch& sc, int32_t* blocks, int32_t* valid) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   // The first kThreads ids and the whole map are loaded together and the map
@@ -89,6 +100,7 @@ __device__ int build_plan(const int32_t* __restrict__ ids, int P, const int32_t*
   for (int s = tid; s < S; s += kThreads) {
     sc.cnt[s] = 0;
     sc.run[s] = 0;
+    sc.pend[s] = pending != nullptr && pending[s] != 0;
   }
   __syncthreads();
   auto slot_of = [&](int g) {
@@ -101,32 +113,45 @@ __device__ int build_plan(const int32_t* __restrict__ ids, int P, const int32_t*
     if (s >= 0) atomicAdd(&sc.cnt[s], 1);
   }
   __syncthreads();
-  // Exclusive scan of blocks-per-slot; thread t owns slots [t*per, t*per+per).
+  // Exclusive scans of blocks-per-slot, resident slots first, then pending
+  // ones; thread t owns slots [t*per, t*per+per).
   const int per = (S + kThreads - 1) / kThreads;
-  int mine = 0;
+  int mine[2] = {0, 0};
   for (int i = 0; i < per; ++i) {
     const int s = tid * per + i;
-    if (s < S) mine += (sc.cnt[s] + kBM - 1) / kBM;
+    if (s < S) mine[sc.pend[s]] += (sc.cnt[s] + kBM - 1) / kBM;
   }
-  int incl = mine;
+  int incl[2] = {mine[0], mine[1]};
 #pragma unroll
   for (int off = 1; off < SLUICE_WAVE; off <<= 1) {
-    const int v = __shfl_up(incl, off, SLUICE_WAVE);
-    if (lane >= off) incl += v;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int v = __shfl_up(incl[c], off, SLUICE_WAVE);
+      if (lane >= off) incl[c] += v;
+    }
   }
-  if (lane == 63) sc.wsum[wave] = incl;
+  if (lane == 63) {
+    sc.wsum[0][wave] = incl[0];
+    sc.wsum[1][wave] = incl[1];
+  }
   __syncthreads();
-  int wbase = 0;
-  for (int w = 0; w < wave; ++w) wbase += sc.wsum[w];
-  int acc = wbase + incl - mine;
+  int wbase[2] = {0, 0}, tot[2] = {0, 0};
+  for (int w = 0; w < kKS; ++w)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      if (w < wave) wbase[c] += sc.wsum[c][w];
+      tot[c] += sc.wsum[c][w];
+    }
+  int acc[2] = {wbase[0] + incl[0] - mine[0], tot[0] + wbase[1] + incl[1] - mine[1]};
   for (int i = 0; i < per; ++i) {
     const int s = tid * per + i;
     if (s < S) {
-      sc.boff[s] = acc;
-      acc += (sc.cnt[s] + kBM - 1) / kBM;
+      const int c = sc.pend[s];
+      sc.boff[s] = acc[c];
+      acc[c] += (sc.cnt[s] + kBM - 1) / kBM;
     }
   }
-  if (tid == kThreads - 1) sc.total = wbase + incl;
+  if (tid == 0) sc.total = tot[0] + tot[1];
   __syncthreads();
   // Ranks in pair order, one chunk of kThreads pairs at a time.
   for (int c = 0; c < P; c += kThreads) {
@@ -142,7 +167,7 @@ __device__ int build_plan(const int32_t* __restrict__ ids, int P, const int32_t*
       int32_t* blk = blocks + (size_t)b * kBlockInts;
       blk[2 + pos] = p;
       if (pos == 0) {
-        blk[0] = s;
+        blk[0] = s | (sc.pend[s] ? kPendingBit : 0);
         const int left = sc.cnt[s] - (r / kBM) * kBM;
         blk[1] = left < kBM ? left : kBM;
       }
@@ -175,10 +200,10 @@ __device__ int build_plan(const int32_t* __restrict__ ids, int P, const int32_t*
 // plan: [nb, P2, 0, 0 | P2 block records | P2 validity flags], P2 = P + n_sh*T.
 __global__ __launch_bounds__(kThreads) void moe_align_kernel(
     const int32_t* __restrict__ ids, int T, int k, const int32_t* __restrict__ map, int E, int S,
-    int n_sh, int32_t* __restrict__ plan) {
+    int n_sh, const int32_t* __restrict__ pending, int32_t* __restrict__ plan) {
   __shared__ AlignScratch sc;
   const int P = T * k, P2 = P + n_sh * T;
-  const int nb = build_plan(ids, P, map, E, S, T, n_sh, sc, plan + kPlanHeader,
+  const int nb = build_plan(ids, P, map, E, S, T, n_sh, pending, sc, plan + kPlanHeader,
                             plan + kPlanHeader + (size_t)kBlockInts * P2);
   if (threadIdx.x == 0) {
     plan[0] = nb;
@@ -376,7 +401,69 @@ struct ExpertW {
   const float* sh_s2;
   int S;      // routed slots
   int I_s;    // shared intermediate (n_sh * I), 0 = none
+  SlotWait wait;  // slots whose rows may still stream (none for plain calls)
 };
+
+// A work item on a block flagged kPendingBit waits (bounded by the gap's
+// timeout and the abort flag) until the slot's rows of the pending gap have
+// landed.  The first workgroup to claim the slot for that gap polls the
+// host-mapped ready mark (and, now and then, the abort flag), gently, and
+// publishes the stamp -- or kSeenFailed -- in device memory; the others poll
+// that, reading no host memory (device reads of host memory share the link
+// with the rows streaming in).  Each then takes a system-scope acquire, so no
+// cache returns the slot's previous expert; the workgroup's loads follow the
+// barrier.  A failed wait is recorded in the layer's status word (the host
+// reports it) and the item computes on whatever the slot holds.
+constexpr int32_t kSeenFailed = -1;
+
+__device__ __forceinline__ void await_slot(const SlotWait& w, int slot_field) {
+  if ((slot_field & kPendingBit) == 0 || w.pending == nullptr) return;
+  if (threadIdx.x == 0) {
+    const int slot = slot_field & kSlotMask;
+    const int32_t p = w.pending[slot];
+    if (p != 0 &&
+        __hip_atomic_load(&w.seen[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != p) {
+      const bool poller = atomicExch(&w.claim[slot], p) != p;
+      const long long t0 = wall_clock64();
+      int st = 0;
+      if (poller) {
+        for (unsigned it = 1;; ++it) {
+          if (__hip_atomic_load(w.ready + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == p)
+            break;
+          if ((it & 15u) == 0 &&
+              __hip_atomic_load(w.abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != 0) {
+            st = SLUICE_E_ABORTED;
+            break;
+          }
+          if (wall_clock64() - t0 > w.timeout_ticks) {
+            st = SLUICE_E_TIMEOUT;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(127);
+        }
+        if (st != 0) {
+          __hip_atomic_store(w.status, st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+          __hip_atomic_store(&w.seen[slot], kSeenFailed, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          (void)__hip_atomic_load(w.ready + slot, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+          __hip_atomic_store(&w.seen[slot], p, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else {
+        for (;;) {
+          const int32_t v =
+              __hip_atomic_load(&w.seen[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (v == p || v == kSeenFailed) break;
+          // the poller's own bound ends every wait; this one is a backstop
+          if (wall_clock64() - t0 > w.timeout_ticks) break;
+          __builtin_amdgcn_s_sleep(32);
+        }
+      }
+    }
+    if (p != 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+  }
+  __syncthreads();
+}
 
 // Call shape: T tokens, k routed pairs each (P = T*k routed pairs); shared
 // pairs follow as P + v*T + t.
@@ -567,7 +654,9 @@ __global__ __launch_bounds__(kThreads) void moe_gemm1_kernel(const uint16_t* __r
     const int b = item / n_tiles, tile = item - b * n_tiles;
     const int32_t* blk = plan + kPlanHeader + (size_t)b * kBlockInts;
     const int pair = col < blk[1] ? blk[2 + col] : -1;
-    run_g1<FP8>(x, W, cs, blk[0], pair, tile, act, lds);
+    const int slot_field = blk[0];
+    await_slot(W.wait, slot_field);
+    run_g1<FP8>(x, W, cs, slot_field & kSlotMask, pair, tile, act, lds);
   }
 }
 
@@ -586,7 +675,9 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_kernel(const uint16_t* __r
     const int b = item / n_tiles, tile2 = item - b * n_tiles;
     const int32_t* blk = plan + kPlanHeader + (size_t)b * kBlockInts;
     const int pair = col < blk[1] ? blk[2 + col] : -1;
-    run_g2<FP8>(act, W, cs, blk[0], pair, tile2, topk_w, partial, lds);
+    const int slot_field = blk[0];
+    await_slot(W.wait, slot_field);
+    run_g2<FP8>(act, W, cs, slot_field & kSlotMask, pair, tile2, topk_w, partial, lds);
   }
 }
 
@@ -720,14 +811,16 @@ int run_experts(const void* x, const ExpertW& W, const float* tw, const int32_t*
   workspace_bytes(T, H, I, k, n_sh, &w, workspace);
   const int P2 = T * k + n_sh * T;
   const CallShape cs{T, k, H, I};
+  ExpertW Ww = W;
+  if (map != nullptr) Ww.wait = slotwait_lookup(map);
   hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kThreads), 0, st, ti, T, k, map, E, S, n_sh,
-                     w.plan);
+                     Ww.wait.pending, w.plan);
   SLUICE_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL((moe_gemm1_kernel<FP8>), dim3(grid_for(P2, I / 16)), dim3(kThreads), 0, st,
-                     (const uint16_t*)x, W, w.plan, cs, w.act);
+                     (const uint16_t*)x, Ww, w.plan, cs, w.act);
   SLUICE_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL((moe_gemm2_kernel<FP8>), dim3(grid_for(P2, H / (16 * kG2T))),
-                     dim3(kThreads), 0, st, w.act, W, w.plan, tw, cs, w.partial);
+                     dim3(kThreads), 0, st, w.act, Ww, w.plan, tw, cs, w.partial);
   SLUICE_HIP_CHECK(hipGetLastError());
   return launch_combine(w.partial, w.plan + kPlanHeader + (size_t)kBlockInts * P2, T, k, n_sh, H,
                         scale, shared, out, st);
@@ -768,7 +861,7 @@ int scratch_ptr(void** out) {
 
 // Weights of the per-stage entry points: every block's slot is routed.
 ExpertW routed_only(const uint8_t* w13, const uint8_t* w2, const float* s13, const float* s2) {
-  return ExpertW{w13, w2, s13, s2, nullptr, nullptr, nullptr, nullptr, 0x7fffffff, 0};
+  return ExpertW{w13, w2, s13, s2, nullptr, nullptr, nullptr, nullptr, 0x7fffffff, 0, SlotWait{}};
 }
 
 }  // namespace
@@ -787,7 +880,7 @@ extern "C" int sluice_moe_align(const int32_t* topk_ids, int T, int k, const int
       (long)T * k > SLUICE_MAX_PAIRS || plan == nullptr)
     return SLUICE_E_INVAL;
   hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, topk_ids,
-                     T, k, expert_map, E, S, 0, plan);
+                     T, k, expert_map, E, S, 0, nullptr, plan);
   return (int)hipGetLastError();
 }
 
