@@ -145,6 +145,11 @@ int sluice_host_free(void* p);
  * The workspace (device) must hold sluice_fused_experts_workspace() bytes;
  * it needs no initial contents and keeps none between calls (calls that
  * share one must not overlap).
+ * plan (may be NULL): the plan of these topk_ids over this expert_map (the
+ * sluice_moe_align layout), built on `stream` before the call -- by the
+ * layer's gap (sluice_layer_gap_launch with a plan buffer), which leaves the
+ * map this call reads; the call then launches no align kernel of its own.
+ * NULL: the call builds the plan in its workspace.
  * ---------------------------------------------------------------------- */
 size_t sluice_fused_experts_workspace(int T, int H, int I, int k, int shared_I);
 
@@ -154,7 +159,7 @@ int sluice_fused_experts_bf16(const void* x, const void* w13, const void* w2,
                               int k, int E, int S, float scale,
                               const void* shared_w13, const void* shared_w2,
                               int shared_I, const void* shared, void* workspace,
-                              size_t workspace_bytes, void* out,
+                              size_t workspace_bytes, void* out, const int32_t* plan,
                               sluice_stream_t stream);
 
 /* No-allocation variant of sluice_fused_experts_bf16 (same arguments minus
@@ -177,7 +182,7 @@ int sluice_fused_experts_bf16_noalloc(const void* x, const void* w13, const void
                                       int k, int E, int S, float scale,
                                       const void* shared_w13, const void* shared_w2,
                                       int shared_I, const void* shared, void* out,
-                                      sluice_stream_t stream);
+                                      const int32_t* plan, sluice_stream_t stream);
 
 int sluice_fused_experts_fp8(const void* x, const void* w13,
                              const float* w13_scale, const void* w2,
@@ -188,15 +193,18 @@ int sluice_fused_experts_fp8(const void* x, const void* w13,
                              const void* shared_w13, const float* shared_w13_scale,
                              const void* shared_w2, const float* shared_w2_scale,
                              int shared_I, const void* shared, void* workspace,
-                             size_t workspace_bytes, void* out,
+                             size_t workspace_bytes, void* out, const int32_t* plan,
                              sluice_stream_t stream);
 
 /* Token permute / align-to-block (vLLM moe_align_block_size): groups the
  * T*k (token, expert) pairs by slot into blocks of <= SLUICE_BLOCK_M pairs,
  * slots ascending, pairs ascending within a slot.  plan (device int32):
- *   plan[0] = n_blocks; then per block 18 ints {slot, count, pair[16]}
- *   starting at plan[4]; then T*k validity flags at
- *   plan[4 + 18*T*k].  Exposed for testing; fused_experts runs it itself. */
+ *   plan[0] = n_blocks, plan[1] = T*k; then per block 18 ints {slot field,
+ *   count, pair[16]} starting at plan[4]; then T*k validity flags at
+ *   plan[4 + 18*T*k].  Slots whose rows a router-split gap of this map is
+ *   still streaming come last, their slot field or-ed with 1<<30.  The shared
+ *   experts' blocks are not in the plan (the product derives them).  Exposed
+ *   for testing; fused_experts runs it itself unless given a plan. */
 size_t sluice_moe_plan_ints(int T, int k);
 int sluice_moe_align(const int32_t* topk_ids, int T, int k,
                      const int32_t* expert_map, int E, int S, int32_t* plan,
@@ -272,17 +280,25 @@ int sluice_layer_pin(sluice_layer* layer, int local, int debit_protected,
  *
  * Host half, sluice_layer_gap_serve: waits (bounded) for the layer's next
  * record, runs the reference's bookkeeping exactly (fast-hit, hit touches in
- * ascending id order, claimed set, victims), streams misses as
- * hipMemcpyAsync on the library's per-device copy stream, waits for them,
- * and answers the device with the standing slot table.  `compute` (may be
- * NULL) is polled for errors while waiting.  SLUICE_E_OVERFLOW when the
- * working set does not fit (rows acquired before it still stream, the map is
- * left as it was, as in the reference).
+ * ascending id order, claimed set, victims), answers the device with the
+ * standing slot table and the slots being filled, then streams the misses
+ * as hipMemcpyAsync on the library's per-device copy stream and marks each
+ * filled slot ready as its rows land: the expert product computes resident
+ * experts meanwhile and waits per filled slot.  `compute` (may be NULL) is
+ * polled for errors while waiting.  SLUICE_E_OVERFLOW when the working set
+ * does not fit (rows acquired before it still stream and land before the
+ * answer, the map is left as it was, as in the reference).
  *
- * sluice_layer_gap = launch (no copy) + serve: the reference's eager op. */
+ * plan (may be NULL): a device buffer of sluice_moe_plan_ints(1, n) ints;
+ * the kernel then also builds the expert product's plan of these ids over
+ * the map it leaves installed (and its pending slots), for
+ * sluice_fused_experts_* to take instead of launching its align kernel.
+ *
+ * sluice_layer_gap = launch (no copy, no plan) + serve: the reference's
+ * eager op. */
 int sluice_layer_gap_launch(sluice_layer* layer, const int32_t* topk_ids, int n,
                             const void* hs_src, void* hs_dst, size_t hs_bytes,
-                            sluice_stream_t stream);
+                            int32_t* plan, sluice_stream_t stream);
 int sluice_layer_gap_serve(sluice_layer* layer, int fast_hit,
                            sluice_stream_t compute);
 int sluice_layer_gap(sluice_layer* layer, const int32_t* topk_ids, int n,

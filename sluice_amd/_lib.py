@@ -49,17 +49,17 @@ SIGNATURES = {
     "sluice_fused_experts_bf16": (
         c_int,
         [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P, c_int,
-         _P, _P, c_size_t, _P, _P],
+         _P, _P, c_size_t, _P, _P, _P],
     ),
     "sluice_fused_experts_bf16_noalloc": (
         c_int,
         [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _P, _P, c_int,
-         _P, _P, _P],
+         _P, _P, _P, _P],
     ),
     "sluice_fused_experts_fp8": (
         c_int,
         [_P, _P, _P, _P, _P, c_int, c_int, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,
-         c_float, _P, _P, _P, _P, c_int, _P, _P, c_size_t, _P, _P],
+         c_float, _P, _P, _P, _P, c_int, _P, _P, c_size_t, _P, _P, _P],
     ),
     "sluice_moe_plan_ints": (c_size_t, [c_int, c_int]),
     "sluice_moe_align": (c_int, [_P, c_int, c_int, _P, c_int, c_int, _P, _P]),
@@ -75,7 +75,7 @@ SIGNATURES = {
     "sluice_layer_add_param": (c_int, [_P, _P, _P, c_size_t]),
     "sluice_layer_pin": (c_int, [_P, c_int, c_int, POINTER(c_int)]),
     "sluice_layer_gap": (c_int, [_P, _P, c_int, c_int, _P]),
-    "sluice_layer_gap_launch": (c_int, [_P, _P, c_int, _P, _P, c_size_t, _P]),
+    "sluice_layer_gap_launch": (c_int, [_P, _P, c_int, _P, _P, c_size_t, _P, _P]),
     "sluice_layer_gap_serve": (c_int, [_P, c_int, _P]),
     "sluice_gap_server_create": (c_int, [_P, c_int, c_int, POINTER(c_void_p)]),
     "sluice_gap_server_drain": (c_int, [_P, ctypes.c_double]),

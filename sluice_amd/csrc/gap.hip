@@ -51,6 +51,7 @@
 #include <vector>
 
 #include "common.h"
+#include "plan.h"
 #include "slotwait.h"
 #include "slru.h"
 #include "stamp.h"
@@ -255,8 +256,9 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     const int32_t* __restrict__ local_of, int E, GapMailbox* mb, int32_t* dev_state,
     int32_t* __restrict__ pending, int32_t* __restrict__ prev, int S, const int32_t* abort_flag,
     long long timeout_ticks, const u32x4_t* __restrict__ copy_src, u32x4_t* __restrict__ copy_dst,
-    int copy_vecs) {
+    int copy_vecs, int32_t* __restrict__ plan) {
   __shared__ int present[SLUICE_MAX_EXPERTS];
+  __shared__ sluice_plan::Scratch psc;
   __shared__ int s_uniq[SLUICE_MAX_EXPERTS];
   __shared__ int wcount[kWaves];
   __shared__ int wmiss[kWaves];
@@ -378,39 +380,48 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
       if (i < copy_vecs) copy_dst[i] = cv[u];
     }
   }
-  if (!s_waits) return;
-  if (tid == 0) {
-    const int st = wait_eq<true>(&mb->resp_stamp, s_stamp, abort_flag, timeout_ticks);
-    s_status = st != 0 ? st : ld_sys(&mb->resp_code);
-    if (st != 0) st_host(&mb->dev_status, st);
-  }
-  __syncthreads();
-  if (s_status != 0) return;
-  // Install the standing map the host sent (already acquired above).
-  const int nS = ld_sys(&mb->n_slots);
-  for (int e = tid; e < E; e += kLookupThreads) present[e] = -1;
-  __syncthreads();
-  for (int s = tid; s < nS; s += kLookupThreads) {
-    const int g = ld_sys(&mb->slot_global[s]);
-    if ((unsigned)g < (unsigned)E) present[g] = s;
-  }
-  __syncthreads();
-  for (int e = tid; e < E; e += kLookupThreads) map[e] = present[e];
-  // The slots the host is still filling: the expert product waits for them.
-  // Their poll claims and seen marks (after the fill list) start over.
-  int32_t* claim = prev + 1 + S;
-  const int nf = min(ld_sys(&mb->n_fill), S);
-  for (int i = tid; i < nf; i += kLookupThreads) {
-    const int sl = ld_sys(&mb->fill[i]);
-    const int ok = (unsigned)sl < (unsigned)S;
-    if (ok) {
-      pending[sl] = s_stamp;
-      claim[sl] = 0;
-      claim[S + sl] = 0;
+  if (s_waits) {
+    if (tid == 0) {
+      const int st = wait_eq<true>(&mb->resp_stamp, s_stamp, abort_flag, timeout_ticks);
+      s_status = st != 0 ? st : ld_sys(&mb->resp_code);
+      if (st != 0) st_host(&mb->dev_status, st);
     }
-    prev[1 + i] = ok ? sl : 0;
+    __syncthreads();
+    if (s_status == 0) {
+      // Install the standing map the host sent (already acquired above).
+      const int nS = ld_sys(&mb->n_slots);
+      for (int e = tid; e < E; e += kLookupThreads) present[e] = -1;
+      __syncthreads();
+      for (int s = tid; s < nS; s += kLookupThreads) {
+        const int g = ld_sys(&mb->slot_global[s]);
+        if ((unsigned)g < (unsigned)E) present[g] = s;
+      }
+      __syncthreads();
+      for (int e = tid; e < E; e += kLookupThreads) map[e] = present[e];
+      // The slots the host is still filling: the expert product waits for
+      // them.  Their poll claims and seen marks (after the fill list) start
+      // over.
+      int32_t* claim = prev + 1 + S;
+      const int nf = min(ld_sys(&mb->n_fill), S);
+      for (int i = tid; i < nf; i += kLookupThreads) {
+        const int sl = ld_sys(&mb->fill[i]);
+        const int ok = (unsigned)sl < (unsigned)S;
+        if (ok) {
+          pending[sl] = s_stamp;
+          claim[sl] = 0;
+          claim[S + sl] = 0;
+        }
+        prev[1 + i] = ok ? sl : 0;
+      }
+      if (tid == 0) prev[0] = nf;
+    }
   }
-  if (tid == 0) prev[0] = nf;
+  // The expert product's plan of these ids over the map (and pending marks)
+  // this gap leaves behind, so the product needs no align launch of its own.
+  if (plan != nullptr) {
+    __syncthreads();
+    (void)sluice_plan::plan_build(ids, n, map, E, S, pending, psc, plan);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -732,7 +743,7 @@ long long timeout_ticks(const sluice_layer* L) {
 }
 
 int launch_gap(sluice_layer* L, const int32_t* ids, int n, const void* hs_src, void* hs_dst,
-               size_t hs_bytes, hipStream_t st) {
+               size_t hs_bytes, int32_t* plan, hipStream_t st) {
   if ((hs_bytes & 15) != 0 || ((uintptr_t)hs_src & 15) != 0 || ((uintptr_t)hs_dst & 15) != 0)
     return SLUICE_E_INVAL;
   if (hs_bytes > 0 && (hs_src == nullptr || hs_dst == nullptr)) return SLUICE_E_INVAL;
@@ -741,7 +752,7 @@ int launch_gap(sluice_layer* L, const int32_t* ids, int n, const void* hs_src, v
   hipLaunchKernelGGL(gap_kernel, dim3(1), dim3(kLookupThreads), 0, st, ids, n, L->map_dev,
                      L->dev_block, E, L->mb_dev, L->dev_block + E, pending, pending + S, S,
                      g_abort_dev, timeout_ticks(L), (const u32x4_t*)hs_src, (u32x4_t*)hs_dst,
-                     (int)(hs_bytes / 16));
+                     (int)(hs_bytes / 16), plan);
   return (int)hipGetLastError();
 }
 
@@ -845,11 +856,12 @@ extern "C" int sluice_layer_pin(sluice_layer* L, int local, int debit_protected,
 
 extern "C" int sluice_layer_gap_launch(sluice_layer* L, const int32_t* topk_ids, int n,
                                        const void* hs_src, void* hs_dst, size_t hs_bytes,
-                                       sluice_stream_t stream) {
+                                       int32_t* plan, sluice_stream_t stream) {
   if (L == nullptr || n < 0 || n > SLUICE_MAX_PAIRS || (n > 0 && topk_ids == nullptr))
     return SLUICE_E_INVAL;
+  if (((uintptr_t)plan & 3) != 0) return SLUICE_E_INVAL;
   if (L->mb == nullptr || L->map_dev == nullptr) return SLUICE_E_STATE;
-  return launch_gap(L, topk_ids, n, hs_src, hs_dst, hs_bytes, (hipStream_t)stream);
+  return launch_gap(L, topk_ids, n, hs_src, hs_dst, hs_bytes, plan, (hipStream_t)stream);
 }
 
 extern "C" int sluice_layer_gap_serve(sluice_layer* L, int fast_hit, sluice_stream_t compute) {
@@ -863,7 +875,7 @@ extern "C" int sluice_layer_gap(sluice_layer* L, const int32_t* topk_ids, int n,
   if (L == nullptr || n < 0 || n > SLUICE_MAX_PAIRS || (n > 0 && topk_ids == nullptr))
     return SLUICE_E_INVAL;
   if (L->mb == nullptr || L->map_dev == nullptr || L->server != nullptr) return SLUICE_E_STATE;
-  int rc = launch_gap(L, topk_ids, n, nullptr, nullptr, 0, (hipStream_t)compute);
+  int rc = launch_gap(L, topk_ids, n, nullptr, nullptr, 0, nullptr, (hipStream_t)compute);
   if (rc != SLUICE_OK) return rc;
   return serve_one(L, fast_hit != 0, true, (hipStream_t)compute);
 }

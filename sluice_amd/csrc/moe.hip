@@ -23,6 +23,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "plan.h"
 #include "slotwait.h"
 #include "stream.h"
 
@@ -35,16 +36,18 @@ static __device__ __align__(256) uint8_t scratch[SLUICE_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
-constexpr int kBM = SLUICE_BLOCK_M;      // tokens per block (MFMA N)
-constexpr int kBlockInts = 2 + kBM;      // {slot, count, pair[16]}
-// A block's slot field carries this bit when the slot's rows may still be
+using sluice_plan::kBM;          // tokens per block (MFMA N)
+using sluice_plan::kBlockInts;   // {slot field, count, pair[16]}
+// A block's slot field carries kPendingBit when the slot's rows may still be
 // streaming in (a pending slot of the layer's last gap): its work items
 // wait for the slot before they read its weights.
-constexpr int kPendingBit = 1 << 30;
-constexpr int kSlotMask = kPendingBit - 1;
-constexpr int kPlanHeader = 4;
+using sluice_plan::kPendingBit;
+using sluice_plan::kSlotMask;
+using sluice_plan::plan_ints;
+constexpr int kPlanHeader = sluice_plan::kHeader;
 constexpr int kKS = 4;                   // waves per workgroup (K split)
 constexpr int kThreads = 64 * kKS;
+static_assert(kThreads == sluice_plan::kPlanThreads, "the align kernel builds the plan");
 constexpr int kG2T = 2;                  // 16-row hidden tiles per gemm2 item
 constexpr int kFp8Blk = 128;
 
@@ -63,152 +66,13 @@ constexpr int kG1D = SLUICE_G1_D;  // bf16 gemm1: 64-wide K chunks in flight per
 constexpr int kG2D = SLUICE_G2_D;  // bf16 gemm2
 constexpr int kF8D = SLUICE_F8_D;  // fp8: 128-wide K chunks in flight per wave
 
-__host__ __device__ inline size_t plan_ints(int P) {
-  return (size_t)kPlanHeader + (size_t)kBlockInts * P + (size_t)P;
-}
 
-// ---------------------------------------------------------------------------
-// Align: group the P = T*k pairs by slot into blocks of <= 16, slots
-// ascending and pairs ascending inside a slot (deterministic).  Called by
-// all kThreads threads; `blocks` / `valid` may be global or LDS memory;
-// the scratch arrays are LDS.  Returns the block count to every thread.
-// ---------------------------------------------------------------------------
-struct AlignScratch {
-  int slot_of[SLUICE_MAX_EXPERTS];  // the map, staged (or the identity)
-  int cnt[SLUICE_MAX_SLOTS];
-  int boff[SLUICE_MAX_SLOTS];
-  int run[SLUICE_MAX_SLOTS];
-  int pend[SLUICE_MAX_SLOTS];       // the slot's rows may still be streaming
-  int chunk_slot[kThreads];
-  int wsum[2][kKS];
-  int total;
-};
-
-// pending [S] (device, may be null): nonzero for the slots whose rows the
-// layer's last gap is still streaming; their blocks come after every other
-// routed block (so the work on resident experts is dispatched first) and
-// carry kPendingBit.
-__device__ int build_plan(const int32_t* __restrict__ ids, int P, const int32_t* __restrict__ map,
-                          int E, int S, int T, int n_sh, const int32_t* __restrict__ pending,
-                          AlignScratch& sc, int32_t* blocks, int32_t* valid) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  // The first kThreads ids and the whole map are loaded together and the map
-  // is staged in LDS, so the slot lookups need no second memory round trip.
-  const int id0 = tid < P ? ids[tid] : -1;
-  for (int e = tid; e < E; e += kThreads) sc.slot_of[e] = map != nullptr ? map[e] : e;
-  for (int s = tid; s < S; s += kThreads) {
-    sc.cnt[s] = 0;
-    sc.run[s] = 0;
-    sc.pend[s] = pending != nullptr && pending[s] != 0;
-  }
-  __syncthreads();
-  auto slot_of = [&](int g) {
-    if ((unsigned)g >= (unsigned)E) return -1;
-    const int s = sc.slot_of[g];
-    return (unsigned)s < (unsigned)S ? s : -1;
-  };
-  for (int p = tid; p < P; p += kThreads) {
-    const int s = slot_of(p == tid ? id0 : ids[p]);
-    if (s >= 0) atomicAdd(&sc.cnt[s], 1);
-  }
-  __syncthreads();
-  // Exclusive scans of blocks-per-slot, resident slots first, then pending
-  // ones; thread t owns slots [t*per, t*per+per).
-  const int per = (S + kThreads - 1) / kThreads;
-  int mine[2] = {0, 0};
-  for (int i = 0; i < per; ++i) {
-    const int s = tid * per + i;
-    if (s < S) mine[sc.pend[s]] += (sc.cnt[s] + kBM - 1) / kBM;
-  }
-  int incl[2] = {mine[0], mine[1]};
-#pragma unroll
-  for (int off = 1; off < SLUICE_WAVE; off <<= 1) {
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int v = __shfl_up(incl[c], off, SLUICE_WAVE);
-      if (lane >= off) incl[c] += v;
-    }
-  }
-  if (lane == 63) {
-    sc.wsum[0][wave] = incl[0];
-    sc.wsum[1][wave] = incl[1];
-  }
-  __syncthreads();
-  int wbase[2] = {0, 0}, tot[2] = {0, 0};
-  for (int w = 0; w < kKS; ++w)
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      if (w < wave) wbase[c] += sc.wsum[c][w];
-      tot[c] += sc.wsum[c][w];
-    }
-  int acc[2] = {wbase[0] + incl[0] - mine[0], tot[0] + wbase[1] + incl[1] - mine[1]};
-  for (int i = 0; i < per; ++i) {
-    const int s = tid * per + i;
-    if (s < S) {
-      const int c = sc.pend[s];
-      sc.boff[s] = acc[c];
-      acc[c] += (sc.cnt[s] + kBM - 1) / kBM;
-    }
-  }
-  if (tid == 0) sc.total = tot[0] + tot[1];
-  __syncthreads();
-  // Ranks in pair order, one chunk of kThreads pairs at a time.
-  for (int c = 0; c < P; c += kThreads) {
-    const int p = c + tid;
-    const int s = p < P ? slot_of(c == 0 ? id0 : ids[p]) : -1;
-    sc.chunk_slot[tid] = s;
-    __syncthreads();
-    if (s >= 0) {
-      int r = sc.run[s];
-      for (int q = 0; q < tid; ++q) r += (sc.chunk_slot[q] == s) ? 1 : 0;
-      const int b = sc.boff[s] + r / kBM;
-      const int pos = r % kBM;
-      int32_t* blk = blocks + (size_t)b * kBlockInts;
-      blk[2 + pos] = p;
-      if (pos == 0) {
-        blk[0] = s | (sc.pend[s] ? kPendingBit : 0);
-        const int left = sc.cnt[s] - (r / kBM) * kBM;
-        blk[1] = left < kBM ? left : kBM;
-      }
-    }
-    if (p < P) valid[p] = s >= 0 ? 1 : 0;
-    __syncthreads();
-    if (s >= 0) atomicAdd(&sc.run[s], 1);
-    __syncthreads();
-  }
-  // The shared experts' virtual experts (slots S + v) after the routed
-  // blocks: every token, pairs P + v*T + t, blocks of <= 16 tokens.
-  const int nbt = (T + kBM - 1) / kBM;
-  const int nsb = n_sh * nbt;
-  for (int i = tid; i < nsb * kBM; i += kThreads) {
-    const int sb = i / kBM, pos = i - sb * kBM;
-    const int v = sb / nbt, c = sb - v * nbt;
-    const int t = c * kBM + pos;
-    int32_t* blk = blocks + (size_t)(sc.total + sb) * kBlockInts;
-    if (pos == 0) {
-      blk[0] = S + v;
-      const int left = T - c * kBM;
-      blk[1] = left < kBM ? left : kBM;
-    }
-    if (t < T) blk[2 + pos] = P + v * T + t;
-  }
-  for (int q = tid; q < n_sh * T; q += kThreads) valid[P + q] = 1;
-  return sc.total + nsb;
-}
-
-// plan: [nb, P2, 0, 0 | P2 block records | P2 validity flags], P2 = P + n_sh*T.
+// Align: the plan of the P routed pairs (sluice_plan::plan_build).
 __global__ __launch_bounds__(kThreads) void moe_align_kernel(
-    const int32_t* __restrict__ ids, int T, int k, const int32_t* __restrict__ map, int E, int S,
-    int n_sh, const int32_t* __restrict__ pending, int32_t* __restrict__ plan) {
-  __shared__ AlignScratch sc;
-  const int P = T * k, P2 = P + n_sh * T;
-  const int nb = build_plan(ids, P, map, E, S, T, n_sh, pending, sc, plan + kPlanHeader,
-                            plan + kPlanHeader + (size_t)kBlockInts * P2);
-  if (threadIdx.x == 0) {
-    plan[0] = nb;
-    plan[1] = P2;
-  }
+    const int32_t* __restrict__ ids, int P, const int32_t* __restrict__ map, int E, int S,
+    const int32_t* __restrict__ pending, int32_t* __restrict__ plan) {
+  __shared__ sluice_plan::Scratch sc;
+  (void)sluice_plan::plan_build(ids, P, map, E, S, pending, sc, plan);
 }
 
 typedef f32x4_t RedBuf[kKS][2][64];
@@ -239,22 +103,40 @@ __device__ __forceinline__ void g1_epilogue(RedBuf& red, int pair, int tile, int
   __syncthreads();
 }
 
-// Wave 0 reduces and writes partial[pair, tile2*32 + t*16 + kg*4 .. +4] = w * sum.
-__device__ __forceinline__ void g2_epilogue(RedBuf& red, int pair, int tile2, int H, float wv,
-                                            float* __restrict__ partial) {
+// gemm2 work items: R row groups x kKS / R K parts per workgroup.  Wave w
+// takes the 32-row tile group*R + w % R and K part w / R; the K parts of a
+// tile reduce through LDS.  Measured over recorded decode routing (fraction
+// of 8 TB/s for R = 1 / 2 / 4): bf16 V2-Lite (K = 1408, 22 chunks: 5+6+5+6
+// at R = 1) 0.732 / 0.696 / 0.614, bf16 Qwen3 0.687 / 0.658 / 0.654, fp8
+// DeepSeek-V3 0.778 / 0.811 / 0.786.  Smaller items (R = 1) balance the
+// short bf16 launches best, despite uneven K parts; fp8 streams one chunk
+// in flight per wave, so its waves gain from the longer streams of R = 2.
+template <bool FP8>
+struct G2Shape {
+  static constexpr int R = FP8 ? 2 : 1;
+  static constexpr int K = kKS / R;
+  static_assert(R * K == kKS, "gemm2 waves");
+};
+
+// The first K part of each tile sums the tile's K parts and writes
+// partial[pair, tile2*32 + t*16 + kg*4 .. +4] = w * sum.
+template <int R>
+__device__ __forceinline__ void g2_epilogue(RedBuf& red, int pair, int tile2, int n_tiles,
+                                            int H, float wv, float* __restrict__ partial) {
+  constexpr int K = kKS / R;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kg = lane >> 4;
-  __syncthreads();
-  if (wave == 0 && pair >= 0) {
+  if (K > 1) __syncthreads();
+  if (wave < R && pair >= 0 && tile2 < n_tiles) {
 #pragma unroll
     for (int t = 0; t < kG2T; ++t) {
-      f32x4_t s = red[0][t][lane];
+      f32x4_t v = red[wave][t][lane];
 #pragma unroll
-      for (int w = 1; w < kKS; ++w) s += red[w][t][lane];
+      for (int q = 1; q < K; ++q) v += red[wave + q * R][t][lane];
       float* dst = partial + (size_t)pair * H + (tile2 * kG2T + t) * 16 + kg * 4;
-      *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{wv * s[0], wv * s[1], wv * s[2], wv * s[3]};
+      *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{wv * v[0], wv * v[1], wv * v[2], wv * v[3]};
     }
   }
-  __syncthreads();
+  if (K > 1) __syncthreads();
 }
 
 // ---------------------------------------------------------------------------
@@ -565,22 +447,26 @@ __device__ __forceinline__ float pair_weight(const CallShape& cs, const float* _
 }
 
 __device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act, const ExpertW& W,
-                                             const CallShape& cs, int slot, int pair, int tile2,
+                                             const CallShape& cs, int slot, int pair, int group,
                                              const float* __restrict__ topk_w,
                                              float* __restrict__ partial, ItemLds& l) {
+  constexpr int R = G2Shape<false>::R, K = kKS / R;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int I = cs.I;
-  const int nc = I / 64;
-  const int c0 = wave * nc / kKS, c1 = (wave + 1) * nc / kKS;
-  const G2Src src = g2_src<2>(W, cs, slot, tile2);
-  const uint16_t* a0 = (const uint16_t*)src.a0;
-  const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
+  const int I = cs.I, n_tiles = cs.H / (16 * kG2T);
+  const int tile2 = group * R + wave % R, kp = wave / R;
   f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = a;
-  stream_bf16<kTokPlain, kG2D>(a0, a0 + 16 * src.ld, src.ld, ar, c0, c1 - c0, l.stage[wave], a,
-                               b);
+  if (tile2 < n_tiles) {
+    const int nc = I / 64;
+    const int c0 = kp * nc / K, c1 = (kp + 1) * nc / K;
+    const G2Src src = g2_src<2>(W, cs, slot, tile2);
+    const uint16_t* a0 = (const uint16_t*)src.a0;
+    const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
+    stream_bf16<kTokPlain, kG2D>(a0, a0 + 16 * src.ld, src.ld, ar, c0, c1 - c0, l.stage[wave],
+                                 a, b);
+  }
   l.red[wave][0][lane] = a;
   l.red[wave][1][lane] = b;
-  g2_epilogue(l.red, pair, tile2, cs.H, pair_weight(cs, topk_w, pair), partial);
+  g2_epilogue<R>(l.red, pair, tile2, n_tiles, cs.H, pair_weight(cs, topk_w, pair), partial);
 }
 
 __device__ __forceinline__ void g1_item_fp8(const uint16_t* __restrict__ x, const ExpertW& W,
@@ -601,21 +487,25 @@ __device__ __forceinline__ void g1_item_fp8(const uint16_t* __restrict__ x, cons
 }
 
 __device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act, const ExpertW& W,
-                                            const CallShape& cs, int slot, int pair, int tile2,
+                                            const CallShape& cs, int slot, int pair, int group,
                                             const float* __restrict__ topk_w,
                                             float* __restrict__ partial, ItemLds& l) {
+  constexpr int R = G2Shape<true>::R, K = kKS / R;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int I = cs.I;
-  const int nkb = I / kFp8Blk;
-  const int c0 = wave * nkb / kKS, c1 = (wave + 1) * nkb / kKS;
-  const G2Src src = g2_src<1>(W, cs, slot, tile2);
-  const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
+  const int I = cs.I, n_tiles = cs.H / (16 * kG2T);
+  const int tile2 = group * R + wave % R, kp = wave / R;
   f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = a;
-  stream_fp8<kF8D>(src.a0, src.a0 + 16 * src.ld, src.ld, src.sr, src.sr, ar, c0, c1 - c0,
-                        l.stage[wave], a, b);
+  if (tile2 < n_tiles) {
+    const int nkb = I / kFp8Blk;
+    const int c0 = kp * nkb / K, c1 = (kp + 1) * nkb / K;
+    const G2Src src = g2_src<1>(W, cs, slot, tile2);
+    const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
+    stream_fp8<kF8D>(src.a0, src.a0 + 16 * src.ld, src.ld, src.sr, src.sr, ar, c0, c1 - c0,
+                     l.stage[wave], a, b);
+  }
   l.red[wave][0][lane] = a;
   l.red[wave][1][lane] = b;
-  g2_epilogue(l.red, pair, tile2, cs.H, pair_weight(cs, topk_w, pair), partial);
+  g2_epilogue<R>(l.red, pair, tile2, n_tiles, cs.H, pair_weight(cs, topk_w, pair), partial);
 }
 
 // ---------------------------------------------------------------------------
@@ -632,12 +522,51 @@ __device__ __forceinline__ void run_g1(const uint16_t* x, const ExpertW& W, cons
 
 template <bool FP8>
 __device__ __forceinline__ void run_g2(const uint16_t* act, const ExpertW& W, const CallShape& cs,
-                                       int slot, int pair, int tile2, const float* tw,
+                                       int slot, int pair, int group, const float* tw,
                                        float* partial, ItemLds& l) {
   if (FP8)
-    g2_item_fp8(act, W, cs, slot, pair, tile2, tw, partial, l);
+    g2_item_fp8(act, W, cs, slot, pair, group, tw, partial, l);
   else
-    g2_item_bf16(act, W, cs, slot, pair, tile2, tw, partial, l);
+    g2_item_bf16(act, W, cs, slot, pair, group, tw, partial, l);
+}
+
+// The blocks of a call: the plan's routed blocks, then the shared experts'
+// virtual experts (slot S + v, n_sh = I_s / I of them), each over every
+// token in blocks of <= kBM, pairs P + v*T + t (P = T*k).  A plan handed in
+// by the caller is only read within this call's bounds: a block count
+// above P, a pair outside [0, P) or a slot outside [0, S) cannot send a
+// load or store out of the call's buffers.
+__device__ __forceinline__ int routed_blocks(const int32_t* __restrict__ plan,
+                                             const CallShape& cs) {
+  return min(max(plan[0], 0), cs.T * cs.k);
+}
+
+__device__ __forceinline__ int call_blocks(const int32_t* __restrict__ plan, const ExpertW& W,
+                                           const CallShape& cs) {
+  const int n_sh = W.I_s / cs.I;
+  return routed_blocks(plan, cs) + n_sh * ((cs.T + kBM - 1) / kBM);
+}
+
+// Block b's slot field and the pair of token column `col` (-1 if none).
+__device__ __forceinline__ void block_at(const int32_t* __restrict__ plan, const ExpertW& W,
+                                         const CallShape& cs, int b, int col, int& slot_field,
+                                         int& pair) {
+  const int nr = routed_blocks(plan, cs);
+  if (b < nr) {
+    const int32_t* blk = plan + kPlanHeader + (size_t)b * kBlockInts;
+    slot_field = blk[0];
+    const int p = col < blk[1] ? blk[2 + col] : -1;
+    const bool ok = (unsigned)(slot_field & kSlotMask) < (unsigned)W.S &&
+                    (unsigned)p < (unsigned)(cs.T * cs.k);
+    pair = ok ? p : -1;
+    if ((unsigned)(slot_field & kSlotMask) >= (unsigned)W.S) slot_field = 0;
+  } else {
+    const int nbt = (cs.T + kBM - 1) / kBM;
+    const int sb = b - nr, v = sb / nbt, c = sb - v * nbt;
+    const int t = c * kBM + col;
+    slot_field = W.S + v;
+    pair = t < cs.T ? cs.T * cs.k + v * cs.T + t : -1;
+  }
 }
 
 template <bool FP8>
@@ -648,16 +577,21 @@ __global__ __launch_bounds__(kThreads) void moe_gemm1_kernel(const uint16_t* __r
                                                              uint16_t* __restrict__ act) {
   __shared__ ItemLds lds;
   const int n_tiles = cs.I / 16;
-  const int total = plan[0] * n_tiles;
+  const int total = call_blocks(plan, W, cs) * n_tiles;
   const int col = threadIdx.x & 15;
   for (int item = blockIdx.x; item < total; item += gridDim.x) {
     const int b = item / n_tiles, tile = item - b * n_tiles;
-    const int32_t* blk = plan + kPlanHeader + (size_t)b * kBlockInts;
-    const int pair = col < blk[1] ? blk[2 + col] : -1;
-    const int slot_field = blk[0];
+    int slot_field, pair;
+    block_at(plan, W, cs, b, col, slot_field, pair);
     await_slot(W.wait, slot_field);
     run_g1<FP8>(x, W, cs, slot_field & kSlotMask, pair, tile, act, lds);
   }
+}
+
+__host__ __device__ inline int g2_groups(int H, bool fp8) {
+  const int n_tiles = H / (16 * kG2T);
+  const int R = fp8 ? G2Shape<true>::R : G2Shape<false>::R;
+  return (n_tiles + R - 1) / R;
 }
 
 template <bool FP8>
@@ -668,16 +602,15 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_kernel(const uint16_t* __r
                                                              CallShape cs,
                                                              float* __restrict__ partial) {
   __shared__ ItemLds lds;
-  const int n_tiles = cs.H / (16 * kG2T);
-  const int total = plan[0] * n_tiles;
+  const int n_groups = g2_groups(cs.H, FP8);
+  const int total = call_blocks(plan, W, cs) * n_groups;
   const int col = threadIdx.x & 15;
   for (int item = blockIdx.x; item < total; item += gridDim.x) {
-    const int b = item / n_tiles, tile2 = item - b * n_tiles;
-    const int32_t* blk = plan + kPlanHeader + (size_t)b * kBlockInts;
-    const int pair = col < blk[1] ? blk[2 + col] : -1;
-    const int slot_field = blk[0];
+    const int b = item / n_groups, g = item - b * n_groups;
+    int slot_field, pair;
+    block_at(plan, W, cs, b, col, slot_field, pair);
     await_slot(W.wait, slot_field);
-    run_g2<FP8>(act, W, cs, slot_field & kSlotMask, pair, tile2, topk_w, partial, lds);
+    run_g2<FP8>(act, W, cs, slot_field & kSlotMask, pair, g, topk_w, partial, lds);
   }
 }
 
@@ -747,16 +680,16 @@ struct Workspace {
   float* partial;
 };
 
-// [plan | act [P2, I] bf16 | partial [P2, H] fp32], P2 = T*k routed +
-// n_sh*T shared pairs.  Every call writes what it reads (align writes the
-// whole plan, gemm1 the act rows of the planned pairs, gemm2 their partials;
-// the combine adds only valid pairs), so the workspace needs no clearing and
-// holds nothing between calls.
+// [plan of the T*k routed pairs | act [P2, I] bf16 | partial [P2, H] fp32],
+// P2 = T*k routed + n_sh*T shared pairs.  Every call writes what it reads
+// (align writes the whole plan, gemm1 the act rows of the planned pairs,
+// gemm2 their partials; the combine adds only valid pairs), so the workspace
+// needs no clearing and holds nothing between calls.
 size_t workspace_bytes(int T, int H, int I, int k, int n_sh, Workspace* ws, void* base) {
-  const int P = T * k + n_sh * T;
-  const size_t plan_b = align_up(plan_ints(P) * sizeof(int32_t), 256);
-  const size_t act_b = align_up((size_t)P * I * sizeof(uint16_t), 256);
-  const size_t part_b = align_up((size_t)P * H * sizeof(float), 256);
+  const int P2 = T * k + n_sh * T;
+  const size_t plan_b = align_up(plan_ints(T * k) * sizeof(int32_t), 256);
+  const size_t act_b = align_up((size_t)P2 * I * sizeof(uint16_t), 256);
+  const size_t part_b = align_up((size_t)P2 * H * sizeof(float), 256);
   if (ws != nullptr) {
     char* b = (char*)base;
     ws->plan = (int32_t*)b;
@@ -775,7 +708,7 @@ int grid_for(int P, int n_tiles) {
   return (int)(items < cap ? (items > 0 ? items : 1) : cap);
 }
 
-// The align kernel stages the map of all E experts in LDS (AlignScratch).
+// The align kernel stages the map of all E experts in LDS.
 int check_common(int T, int H, int I, int k, int E, int S, int n_sh, const void* x,
                  const void* w13, const void* w2, const float* tw, const int32_t* ti,
                  const void* shared, void* ws, size_t ws_bytes, void* out) {
@@ -803,26 +736,33 @@ int launch_combine(const float* partial, const int32_t* valid, int T, int k, int
   return (int)hipGetLastError();
 }
 
+// plan: a plan of these ids over this map built on the stream before the
+// call (by the layer's gap kernel), or nullptr: the align kernel builds one
+// in the workspace.
 template <bool FP8>
 int run_experts(const void* x, const ExpertW& W, const float* tw, const int32_t* ti,
                 const int32_t* map, int T, int H, int I, int k, int E, int S, int n_sh,
-                float scale, const void* shared, void* workspace, void* out, hipStream_t st) {
+                float scale, const void* shared, void* workspace, const int32_t* plan,
+                void* out, hipStream_t st) {
   Workspace w;
   workspace_bytes(T, H, I, k, n_sh, &w, workspace);
-  const int P2 = T * k + n_sh * T;
+  const int P = T * k, P2 = P + n_sh * T;
   const CallShape cs{T, k, H, I};
   ExpertW Ww = W;
   if (map != nullptr) Ww.wait = slotwait_lookup(map);
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kThreads), 0, st, ti, T, k, map, E, S, n_sh,
-                     Ww.wait.pending, w.plan);
-  SLUICE_HIP_CHECK(hipGetLastError());
+  if (plan == nullptr) {
+    hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kThreads), 0, st, ti, P, map, E, S,
+                       Ww.wait.pending, w.plan);
+    SLUICE_HIP_CHECK(hipGetLastError());
+    plan = w.plan;
+  }
   hipLaunchKernelGGL((moe_gemm1_kernel<FP8>), dim3(grid_for(P2, I / 16)), dim3(kThreads), 0, st,
-                     (const uint16_t*)x, Ww, w.plan, cs, w.act);
+                     (const uint16_t*)x, Ww, plan, cs, w.act);
   SLUICE_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL((moe_gemm2_kernel<FP8>), dim3(grid_for(P2, H / (16 * kG2T))),
-                     dim3(kThreads), 0, st, w.act, Ww, w.plan, tw, cs, w.partial);
+  hipLaunchKernelGGL((moe_gemm2_kernel<FP8>), dim3(grid_for(P2, g2_groups(H, FP8))),
+                     dim3(kThreads), 0, st, w.act, Ww, plan, tw, cs, w.partial);
   SLUICE_HIP_CHECK(hipGetLastError());
-  return launch_combine(w.partial, w.plan + kPlanHeader + (size_t)kBlockInts * P2, T, k, n_sh, H,
+  return launch_combine(w.partial, plan + kPlanHeader + (size_t)kBlockInts * P, T, k, n_sh, H,
                         scale, shared, out, st);
 }
 
@@ -879,8 +819,10 @@ extern "C" int sluice_moe_align(const int32_t* topk_ids, int T, int k, const int
   if (T < 0 || k <= 0 || E <= 0 || E > SLUICE_MAX_EXPERTS || S <= 0 || S > SLUICE_MAX_SLOTS ||
       (long)T * k > SLUICE_MAX_PAIRS || plan == nullptr)
     return SLUICE_E_INVAL;
+  const int32_t* pending =
+      expert_map != nullptr ? slotwait_lookup(expert_map).pending : nullptr;
   hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, topk_ids,
-                     T, k, expert_map, E, S, 0, nullptr, plan);
+                     T * k, expert_map, E, S, pending, plan);
   return (int)hipGetLastError();
 }
 
@@ -890,7 +832,7 @@ extern "C" int sluice_fused_experts_bf16(const void* x, const void* w13, const v
                                          int E, int S, float scale, const void* shared_w13,
                                          const void* shared_w2, int shared_I, const void* shared,
                                          void* workspace, size_t workspace_bytes_, void* out,
-                                         sluice_stream_t stream) {
+                                         const int32_t* plan, sluice_stream_t stream) {
   int n_sh = 0;
   int rc = shared_groups(shared_I, I, shared_w13, shared_w2, &n_sh);
   if (rc != SLUICE_OK) return rc;
@@ -901,14 +843,14 @@ extern "C" int sluice_fused_experts_bf16(const void* x, const void* w13, const v
                   (const uint8_t*)shared_w13, (const uint8_t*)shared_w2, nullptr, nullptr, S,
                   shared_I};
   return run_experts<false>(x, W, topk_w, topk_ids, expert_map, T, H, I, k, E, S, n_sh, scale,
-                            shared, workspace, out, (hipStream_t)stream);
+                            shared, workspace, plan, out, (hipStream_t)stream);
 }
 
 extern "C" int sluice_fused_experts_bf16_noalloc(
     const void* x, const void* w13, const void* w2, const float* topk_w,
     const int32_t* topk_ids, const int32_t* expert_map, int T, int H, int I, int k, int E, int S,
     float scale, const void* shared_w13, const void* shared_w2, int shared_I, const void* shared,
-    void* out, sluice_stream_t stream) {
+    void* out, const int32_t* plan, sluice_stream_t stream) {
   int n_sh = 0;
   int rc = shared_groups(shared_I, I, shared_w13, shared_w2, &n_sh);
   if (rc != SLUICE_OK) return rc;
@@ -928,7 +870,7 @@ extern "C" int sluice_fused_experts_bf16_noalloc(
                   (const uint8_t*)shared_w13, (const uint8_t*)shared_w2, nullptr, nullptr, S,
                   shared_I};
   return run_experts<false>(x, W, topk_w, topk_ids, expert_map, T, H, I, k, E, S, n_sh, scale,
-                            shared, ws, out, (hipStream_t)stream);
+                            shared, ws, plan, out, (hipStream_t)stream);
 }
 
 extern "C" int sluice_fused_experts_fp8(const void* x, const void* w13, const float* w13_scale,
@@ -940,7 +882,7 @@ extern "C" int sluice_fused_experts_fp8(const void* x, const void* w13, const fl
                                         const void* shared_w2, const float* shared_w2_scale,
                                         int shared_I, const void* shared, void* workspace,
                                         size_t workspace_bytes_, void* out,
-                                        sluice_stream_t stream) {
+                                        const int32_t* plan, sluice_stream_t stream) {
   if (block_n != kFp8Blk || block_k != kFp8Blk) return SLUICE_E_INVAL;
   if (H % kFp8Blk != 0 || I % kFp8Blk != 0) return SLUICE_E_INVAL;
   int n_sh = 0;
@@ -956,7 +898,7 @@ extern "C" int sluice_fused_experts_fp8(const void* x, const void* w13, const fl
                   (const uint8_t*)shared_w13, (const uint8_t*)shared_w2, shared_w13_scale,
                   shared_w2_scale, S, shared_I};
   return run_experts<true>(x, W, topk_w, topk_ids, expert_map, T, H, I, k, E, S, n_sh, scale,
-                           shared, workspace, out, (hipStream_t)stream);
+                           shared, workspace, plan, out, (hipStream_t)stream);
 }
 
 extern "C" int sluice_moe_gemm1_bf16(const void* x, const void* w13, const int32_t* plan, int T,
@@ -978,7 +920,7 @@ extern "C" int sluice_moe_gemm2_bf16(const void* act, const void* w2, const int3
       (long)T * k > SLUICE_MAX_PAIRS || !act || !w2 || !plan || !topk_w || !partial)
     return SLUICE_E_INVAL;
   const ExpertW W = routed_only(nullptr, (const uint8_t*)w2, nullptr, nullptr);
-  hipLaunchKernelGGL(moe_gemm2_kernel<false>, dim3(grid_for(T * k, H / (16 * kG2T))),
+  hipLaunchKernelGGL(moe_gemm2_kernel<false>, dim3(grid_for(T * k, g2_groups(H, false))),
                      dim3(kThreads), 0, (hipStream_t)stream, (const uint16_t*)act, W, plan, topk_w,
                      CallShape{T, k, H, I}, partial);
   return (int)hipGetLastError();
@@ -1004,7 +946,7 @@ extern "C" int sluice_moe_gemm2_fp8(const void* act, const void* w2, const float
       (long)T * k > SLUICE_MAX_PAIRS || !act || !w2 || !w2_scale || !plan || !topk_w || !partial)
     return SLUICE_E_INVAL;
   const ExpertW W = routed_only(nullptr, (const uint8_t*)w2, nullptr, w2_scale);
-  hipLaunchKernelGGL(moe_gemm2_kernel<true>, dim3(grid_for(T * k, H / (16 * kG2T))),
+  hipLaunchKernelGGL(moe_gemm2_kernel<true>, dim3(grid_for(T * k, g2_groups(H, true))),
                      dim3(kThreads), 0, (hipStream_t)stream, (const uint16_t*)act, W, plan, topk_w,
                      CallShape{T, k, H, I}, partial);
   return (int)hipGetLastError();

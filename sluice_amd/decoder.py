@@ -718,12 +718,13 @@ class _StoreMoELayer(nn.Module):
         sh = self.shared
         return sh is not None and sh.I % self.I == 0 and sh.I // self.I <= 4
 
-    def experts(self, hn, tw, ti, shared_output=None, fold_shared=False):
+    def experts(self, hn, tw, ti, shared_output=None, fold_shared=False, plan=None):
         """Routed experts (+ shared_output), or with fold_shared the routed
-        and the shared experts in one grouped product."""
-        kw = {}
+        and the shared experts in one grouped product.  plan: the product's
+        plan the layer's gap built for ti (None: the product plans itself)."""
+        kw = {} if plan is None else {"plan": plan}
         if self.sp["fp8"]:
-            kw = dict(w1_scale=self.w13_weight_scale, w2_scale=self.w2_weight_scale,
+            kw.update(w1_scale=self.w13_weight_scale, w2_scale=self.w2_weight_scale,
                       block_shape=[128, 128])
         if fold_shared:
             sh = self.shared
@@ -1007,17 +1008,21 @@ class SyntheticDecoder:
         for n, i in enumerate(moe_pos):
             last = n == len(moe_pos) - 1
 
-            def mid(io, i=i):
+            def mid(io, i=i, n=n):
                 moe = self.blocks[i].moe
+                # the plan this layer's gap op built for its ids
+                plan = None if classic else self.off.gap_plan(n, io["ti"].numel())
                 if not classic and moe.shared_foldable():
                     # routed and shared experts in one grouped product
-                    io["delta"] = moe.experts(io["hn"], io["tw"], io["ti"], fold_shared=True)
+                    io["delta"] = moe.experts(io["hn"], io["tw"], io["ti"], fold_shared=True,
+                                              plan=plan)
                 else:
                     sh = moe.shared(io["hn"]) if moe.shared is not None else None
                     if classic:
                         io["delta"] = io["routed"] if sh is None else io["routed"] + sh
                     else:
-                        io["delta"] = moe.experts(io["hn"], io["tw"], io["ti"], shared_output=sh)
+                        io["delta"] = moe.experts(io["hn"], io["tw"], io["ti"], shared_output=sh,
+                                                  plan=plan)
                 self._to_next_gap(i + 1, io, st)
 
             out.append((mid, n + 1 if not last else None))

@@ -110,6 +110,9 @@ class _ExpertLayerCache:
     ordinal: int = -1
     layer_name: str = ""
     policy_steps: int = 0  # real classic steps with selected experts, last seen
+    # router-split layers: the expert product's plan, filled by each gap
+    # kernel for ids of up to num_slots pairs (int32, device)
+    plan: Optional[torch.Tensor] = None
 
     # -- native state views ------------------------------------------------
     def _state(self):
@@ -839,6 +842,9 @@ class ExpertStreamOffloader(_OffloaderBase):
             idx = len(self._rs_caches)
             self._rs_caches.append(cache)
             self._rs_routes.append(spec)
+            if cache.plan is None and not self._rs_noop:
+                cache.plan = torch.zeros(_lib.load().sluice_moe_plan_ints(1, cache.num_slots),
+                                         dtype=torch.int32, device=cache.device)
             top_k = spec.top_k if spec is not None else _runner_top_k(module, runner)
             thr = self._rs_thr
             if thr is None:  # eager: a per-step branch, capped at 16 tokens
@@ -849,7 +855,7 @@ class ExpertStreamOffloader(_OffloaderBase):
                 gate=getattr(runner, "gate", None), route=spec,
                 vllm_select=runner.router.select_experts if spec is None else None,
                 stock=runner._forward_entry, shared=_shared_layer(runner),
-                quant=_quant_kwargs(module)))
+                quant=_quant_kwargs(module), plan=cache.plan, plan_pairs=cache.num_slots))
         self._rs_layers = len(self._rs_caches)
         kernel = sum(1 for r in self._rs_routes if r is not None)
         logger.warning("Sluice: ROUTER-SPLIT armed on %d/%d MoE layers (%d routed by the wave64 "
@@ -889,13 +895,24 @@ class ExpertStreamOffloader(_OffloaderBase):
                 src, dst, nbytes = hidden_states.data_ptr(), out.data_ptr(), nb
             else:
                 out.copy_(hidden_states)
+        plan = self.gap_plan(idx, ids.numel())
         rc = lib.sluice_layer_gap_launch(cache.handle, ids.data_ptr(), ids.numel(), src, dst,
-                                         nbytes, stream)
+                                         nbytes, None if plan is None else plan.data_ptr(),
+                                         stream)
         _lib.check(rc, "sluice_layer_gap_launch")
         if self._server is None:
             rc = lib.sluice_layer_gap_serve(cache.handle, int(self._rs_fast_hit), stream)
             _raise_gap(rc, "sluice_layer_gap_serve")
         return out
+
+    def gap_plan(self, idx: int, n_pairs: int) -> Optional[torch.Tensor]:
+        """The buffer router-split layer ``idx``'s gap fills with the expert
+        product's plan for ids of ``n_pairs`` pairs (the product then needs
+        no align launch), or None when its gap builds none."""
+        cache = self._rs_caches[idx]
+        if cache.plan is None or n_pairs > cache.num_slots:
+            return None
+        return cache.plan
 
     # -- gap server ---------------------------------------------------------------
     def start_gap_server(self) -> None:
@@ -1081,6 +1098,8 @@ class _LayerBinding:
     stock: Any
     shared: Any
     quant: dict
+    plan: Optional[torch.Tensor] = None  # filled by the layer's gap (ids of <= plan_pairs)
+    plan_pairs: int = 0
 
 
 def _split_entry(b: _LayerBinding):
@@ -1091,6 +1110,7 @@ def _split_entry(b: _LayerBinding):
     idx, thr, gate, route = b.idx, b.thr, b.gate, b.route
     w13, w2, emap, gne, quant = b.w13, b.w2, b.expert_map, b.global_n, b.quant
     stock, select, shared = b.stock, b.vllm_select, b.shared
+    plan, plan_pairs = b.plan, b.plan_pairs
 
     def _forward_entry(hs, rl, sei, iid, lname, unpad):
         if hs.shape[0] > thr:
@@ -1104,8 +1124,12 @@ def _split_entry(b: _LayerBinding):
         else:
             tw, ti = select(hidden_states=hs, router_logits=rl, input_ids=iid)
         h = torch.ops.vllm.sluice_stream_gap(hs, ti, idx)
+        # the gap op built the product's plan of ti over the map it left
+        # (its output h orders the product after it)
+        p = plan if plan is not None and ti.numel() <= plan_pairs else None
         routed = torch.ops.sluice.fused_experts(h, w13, w2, tw, ti, activation="silu",
-                                                global_num_experts=gne, expert_map=emap, **quant)
+                                                global_num_experts=gne, expert_map=emap,
+                                                plan=p, **quant)
         if shared is None:
             return routed
         return (shared(sei if sei is not None else hs), routed)

@@ -140,10 +140,14 @@ def _fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch
                         shared_w1: Optional[torch.Tensor] = None,
                         shared_w2: Optional[torch.Tensor] = None,
                         shared_w1_scale: Optional[torch.Tensor] = None,
-                        shared_w2_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+                        shared_w2_scale: Optional[torch.Tensor] = None,
+                        plan: Optional[torch.Tensor] = None) -> torch.Tensor:
     """shared_w1 [2*Is, H] / shared_w2 [H, Is] (Is a multiple of I): the
     layer's shared experts, computed inside the grouped product and added
-    unscaled (fp8 with their own block scales when the experts are fp8)."""
+    unscaled (fp8 with their own block scales when the experts are fp8).
+    plan: int32 device buffer holding the plan of these ids over this map,
+    built on the stream before the call by the layer's gap; the product then
+    launches no align kernel of its own."""
     if activation != "silu":
         raise NotImplementedError(f"activation {activation!r}: only 'silu' is on the path")
     lib = _lib.load()
@@ -182,6 +186,12 @@ def _fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch
     if T == 0:
         return out
     chunk = _MAX_PAIRS // (k + Is // I)
+    if plan is not None:
+        if (plan.dtype != torch.int32 or plan.device != x.device or not plan.is_contiguous()
+                or plan.numel() < lib.sluice_moe_plan_ints(T, k) or T > chunk):
+            raise ValueError(f"plan must be a contiguous int32 buffer of >= "
+                             f"{lib.sluice_moe_plan_ints(T, k)} ints on {x.device} "
+                             f"(T={T}, k={k}, at most {chunk} tokens)")
     if T > chunk:
         # more (token, expert) pairs than one launch takes (a prefill chunk on
         # the classic path): tokens are independent, so run slices of them
@@ -205,7 +215,7 @@ def _fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch
         rc = lib.sluice_fused_experts_bf16(
             x.data_ptr(), w1.data_ptr(), w2.data_ptr(), tw.data_ptr(), ids.data_ptr(), emap_ptr,
             T, H, I, k, E, S, float(routed_scaling_factor), _ptr(shared_w1), _ptr(shared_w2), Is,
-            _ptr(sh), ws.data_ptr(), ws.numel(), out.data_ptr(), stream)
+            _ptr(sh), ws.data_ptr(), ws.numel(), out.data_ptr(), _ptr(plan), stream)
         _lib.check(rc, "sluice_fused_experts_bf16")
     elif w1.dtype in (torch.uint8, torch.float8_e4m3fn):
         if w1_scale is None or w2_scale is None:
@@ -218,7 +228,7 @@ def _fused_experts_impl(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch
             int(bn), int(bk), tw.data_ptr(), ids.data_ptr(), emap_ptr, T, H, I, k, E, S,
             float(routed_scaling_factor), _ptr(shared_w1), _ptr(shared_w1_scale),
             _ptr(shared_w2), _ptr(shared_w2_scale), Is, _ptr(sh), ws.data_ptr(), ws.numel(),
-            out.data_ptr(), stream)
+            out.data_ptr(), _ptr(plan), stream)
         _lib.check(rc, "sluice_fused_experts_fp8")
     else:
         raise TypeError(f"unsupported expert dtype {w1.dtype}")
@@ -238,18 +248,19 @@ def fused_experts_op(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Te
                      shared_w1: Optional[torch.Tensor] = None,
                      shared_w2: Optional[torch.Tensor] = None,
                      shared_w1_scale: Optional[torch.Tensor] = None,
-                     shared_w2_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     shared_w2_scale: Optional[torch.Tensor] = None,
+                     plan: Optional[torch.Tensor] = None) -> torch.Tensor:
     return _fused_experts_impl(hidden_states, w1, w2, topk_weights, topk_ids, activation,
                                global_num_experts, expert_map, w1_scale, w2_scale, block_shape,
                                routed_scaling_factor, shared_output, shared_w1, shared_w2,
-                               shared_w1_scale, shared_w2_scale)
+                               shared_w1_scale, shared_w2_scale, plan)
 
 
 @fused_experts_op.register_fake
 def _(hidden_states, w1, w2, topk_weights, topk_ids, activation="silu", global_num_experts=-1,
       expert_map=None, w1_scale=None, w2_scale=None, block_shape=None,
       routed_scaling_factor=1.0, shared_output=None, shared_w1=None, shared_w2=None,
-      shared_w1_scale=None, shared_w2_scale=None):
+      shared_w1_scale=None, shared_w2_scale=None, plan=None):
     return torch.empty_like(hidden_states)
 
 

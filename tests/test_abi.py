@@ -47,12 +47,12 @@ def test_invalid_arguments_rejected_without_touching_the_gpu(lib):
                                  None) == _lib.SLUICE_E_INVAL
     assert lib.sluice_moe_align(None, 1, 8, None, 64, 0, None, None) == _lib.SLUICE_E_INVAL
     assert lib.sluice_fused_experts_bf16(None, None, None, None, None, None, 1, 2048, 100, 8, 64,
-                                         8, 1.0, None, None, 0, None, None, 0, None,
+                                         8, 1.0, None, None, 0, None, None, 0, None, None,
                                          None) == _lib.SLUICE_E_INVAL
     # weight rows stream in 64-element (128-byte) segments: H, I % 64 == 0
     for H, I in ((2048, 96), (2080, 128)):
         assert lib.sluice_fused_experts_bf16(None, None, None, None, None, None, 1, H, I, 8, 64,
-                                             8, 1.0, None, None, 0, None, None, 0, None,
+                                             8, 1.0, None, None, 0, None, None, 0, None, None,
                                              None) == _lib.SLUICE_E_INVAL
         assert lib.sluice_moe_gemm1_bf16(None, None, None, 1, H, I, 8, None,
                                          None) == _lib.SLUICE_E_INVAL
@@ -65,11 +65,11 @@ def test_invalid_arguments_rejected_without_touching_the_gpu(lib):
     assert lib.sluice_moe_align(fake, 1, 8, fake, E_big, 8, fake, None) == _lib.SLUICE_E_INVAL
     assert lib.sluice_fused_experts_bf16(fake, fake, fake, fake, fake, fake, 1, 2048, 1408, 8,
                                          E_big, 8, 1.0, None, None, 0, None, fake, 1 << 30, fake,
-                                         None) == _lib.SLUICE_E_INVAL
+                                         None, None) == _lib.SLUICE_E_INVAL
     assert lib.sluice_fused_experts_fp8(fake, fake, fake, fake, fake, 128, 128, fake, fake, fake,
                                         1, 2048, 1408 // 128 * 128, 8, E_big, 8, 1.0, None, None,
                                         None, None, 0, None, fake, 1 << 30, fake,
-                                        None) == _lib.SLUICE_E_INVAL
+                                        None, None) == _lib.SLUICE_E_INVAL
     h = ctypes.c_void_p()
     assert lib.sluice_layer_create(64, 64, 0, 0, None, None, ctypes.byref(h)) == _lib.SLUICE_E_INVAL
     assert lib.sluice_layer_create(2048, 64, 8, 4, None, None,
@@ -84,7 +84,7 @@ def test_shared_experts_argument_checks(lib):
         sw = ctypes.c_void_p(w) if w else None
         rc = lib.sluice_fused_experts_bf16(*args, 2, 256, 64, 2, 8, 4, 1.0, sw, sw, shared_I,
                                            None, ctypes.c_void_p(16), 1 << 30,
-                                           ctypes.c_void_p(16), None)
+                                           ctypes.c_void_p(16), None, None)
         assert rc == _lib.SLUICE_E_INVAL
 
 

@@ -60,6 +60,31 @@ def _cases(golden):
     return list(range(len(golden["cases"])))
 
 
+def _check_plan(cache, ids, k, E):
+    """The expert product's plan the gap kernel built equals the align
+    kernel's plan of the same ids over the map (and pending slots) the gap
+    left: block count, each block's slot field, count and pairs, and the
+    validity flags."""
+    from sluice_amd import _lib
+
+    lib = _lib.load()
+    P = ids.numel()
+    ref = torch.full_like(cache.plan, -7)
+    rc = lib.sluice_moe_align(ids.data_ptr(), P // k, k, cache.expert_map_buf.data_ptr(), E,
+                              cache.num_slots, ref.data_ptr(),
+                              torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "sluice_moe_align")
+    torch.cuda.synchronize()
+    got, want = cache.plan.cpu().numpy(), ref.cpu().numpy()
+    nb = int(want[0])
+    assert int(got[0]) == nb and int(got[1]) == P
+    for b in range(nb):
+        g, w = got[4 + 18 * b: 4 + 18 * (b + 1)], want[4 + 18 * b: 4 + 18 * (b + 1)]
+        assert g[0] == w[0] and g[1] == w[1], b
+        assert g[2:2 + w[1]].tolist() == w[2:2 + w[1]].tolist(), b
+    assert got[4 + 18 * P: 4 + 19 * P].tolist() == want[4 + 18 * P: 4 + 19 * P].tolist()
+
+
 def _case_ids():
     from conftest import slru_vectors
 
@@ -84,6 +109,11 @@ def test_device_gap_replays_reference(monkeypatch, slru_golden, idx):
         off.post_init()
     cache = off._caches[id(layer)]
     off._rs_caches.append(cache)
+    # the buffer attach_router_split gives a router-split layer: each gap
+    # kernel also builds the expert product's plan into it
+    from sluice_amd import _lib
+    cache.plan = torch.zeros(_lib.load().sluice_moe_plan_ints(1, cache.num_slots),
+                             dtype=torch.int32, device=DEV)
     assert cache.free_slots == case["init"]["free_slots"]
     assert cache.expert_in_slot == [None if v < 0 else v
                                     for v in case["init"]["expert_in_slot"]]
@@ -109,6 +139,8 @@ def test_device_gap_replays_reference(monkeypatch, slru_golden, idx):
         if not overflow:
             torch.cuda.synchronize()
             assert cache.expert_map_buf.cpu().tolist() == want["map"], n
+        if ids.numel() <= cache.num_slots:
+            _check_plan(cache, ids, k, E)
         if n % 25 == 0 or n == len(case["steps"]) - 1:
             _check_slots(cache, layer)
     s = cache.stats()
@@ -204,6 +236,9 @@ def test_device_gap_v3_fp8_streams_four_rows_per_miss(monkeypatch, slru_golden, 
                                          "w2_weight_scale"]
     assert cache.bytes_per_expert == 2 * 128 * 256 + 256 * 128 + (2 * 2 + 2 * 1) * 4
     off._rs_caches.append(cache)
+    from sluice_amd import _lib
+    cache.plan = torch.zeros(_lib.load().sluice_moe_plan_ints(1, cache.num_slots),
+                             dtype=torch.int32, device=DEV)
     hs = torch.zeros((8, 256), dtype=torch.bfloat16, device=DEV)
     prev = list(cache.expert_in_slot)
     for n, step in enumerate(case["steps"]):
@@ -220,6 +255,7 @@ def test_device_gap_v3_fp8_streams_four_rows_per_miss(monkeypatch, slru_golden, 
         prev = now
         torch.cuda.synchronize()
         assert cache.expert_map_buf.cpu().tolist() == want["map"], n
+        _check_plan(cache, ids, k, E)
         if n % 20 == 0 or n == len(case["steps"]) - 1:
             _slot_bytes_match_host(cache)
     s = cache.stats()

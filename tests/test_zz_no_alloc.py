@@ -48,12 +48,13 @@ def _run(lib, c, noalloc):
               c["ids"].data_ptr(), c["emap"].data_ptr(), c["T"], c["H"], c["I"], c["k"], c["E"],
               c["S"], 1.0, _ptr(c["sw13"]), _ptr(c["sw2"]), c["shared_I"], None)
     if noalloc:
-        rc = lib.sluice_fused_experts_bf16_noalloc(*common, out.data_ptr(), st)
+        rc = lib.sluice_fused_experts_bf16_noalloc(*common, out.data_ptr(), None, st)
         _lib.check(rc, "sluice_fused_experts_bf16_noalloc")
     else:
         nb = lib.sluice_fused_experts_workspace(c["T"], c["H"], c["I"], c["k"], c["shared_I"])
         ws = torch.empty(nb, dtype=torch.uint8, device=DEV)
-        rc = lib.sluice_fused_experts_bf16(*common, ws.data_ptr(), ws.numel(), out.data_ptr(), st)
+        rc = lib.sluice_fused_experts_bf16(*common, ws.data_ptr(), ws.numel(), out.data_ptr(), None,
+                                           st)
         _lib.check(rc, "sluice_fused_experts_bf16")
     return out
 
@@ -66,7 +67,7 @@ def test_oversize_call_refused_without_device_work(lib):
     T, H, I, k = 512, 7168, 2048, 8
     assert lib.sluice_fused_experts_workspace(T, H, I, k, 0) > _lib.NOALLOC_SCRATCH_BYTES
     rc = lib.sluice_fused_experts_bf16_noalloc(fake, fake, fake, fake, fake, fake, T, H, I, k, 256,
-                                               64, 1.0, None, None, 0, None, fake, None)
+                                               64, 1.0, None, None, 0, None, fake, None, None)
     assert rc == _lib.SLUICE_E_SCRATCH
     assert "scratch" in _lib.strerror(rc)
 
