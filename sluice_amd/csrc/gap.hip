@@ -279,12 +279,19 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
       cv[u] = copy_src[i < copy_vecs ? i : copy_vecs - 1];
     }
   }
+  // (with a plan to build, the map is staged for it as it is read, and no
+  // slot is pending until this gap installs its fills: the previous gap's
+  // pending slots are cleared below, and only a gap's install marks any)
   bool unmapped[kGapMaxPerThread];
 #pragma unroll
   for (int c = 0; c < kGapMaxPerThread; ++c) {
     const int e = c * kLookupThreads + tid;
-    unmapped[c] = e < E && local_of[e] >= 0 && map[e] < 0;
+    const int mv = e < E ? map[e] : -1;
+    unmapped[c] = e < E && local_of[e] >= 0 && mv < 0;
+    if (plan != nullptr && e < E) psc.slot_of[e] = mv;
   }
+  if (plan != nullptr)
+    for (int i = tid; i < S; i += kLookupThreads) psc.pend[i] = 0;
   int32_t s = 0, seen = 0;
   bool fresh = false;
   if (tid == 0) {
@@ -306,8 +313,10 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     seen = ld_host(&mb->ack_stamp);
     fresh = true;
   }
+  int id0 = -1;  // ids[tid], kept for the plan
   for (int i = tid; i < n; i += kLookupThreads) {
     const int g = ids[i];
+    if (i == tid) id0 = g;
     if ((unsigned)g < (unsigned)E) present[g] = 1;
   }
   __syncthreads();
@@ -397,7 +406,10 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
         if ((unsigned)g < (unsigned)E) present[g] = s;
       }
       __syncthreads();
-      for (int e = tid; e < E; e += kLookupThreads) map[e] = present[e];
+      for (int e = tid; e < E; e += kLookupThreads) {
+        map[e] = present[e];
+        if (plan != nullptr) psc.slot_of[e] = present[e];
+      }
       // The slots the host is still filling: the expert product waits for
       // them.  Their poll claims and seen marks (after the fill list) start
       // over.
@@ -410,6 +422,7 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
           pending[sl] = s_stamp;
           claim[sl] = 0;
           claim[S + sl] = 0;
+          if (plan != nullptr) psc.pend[sl] = 1;
         }
         prev[1 + i] = ok ? sl : 0;
       }
@@ -417,11 +430,9 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     }
   }
   // The expert product's plan of these ids over the map (and pending marks)
-  // this gap leaves behind, so the product needs no align launch of its own.
-  if (plan != nullptr) {
-    __syncthreads();
-    (void)sluice_plan::plan_build(ids, n, map, E, S, pending, psc, plan);
-  }
+  // this gap leaves behind, staged above, so the product needs no align
+  // launch of its own.
+  if (plan != nullptr) (void)sluice_plan::plan_build_staged(id0, ids, n, E, S, psc, plan);
 }
 
 // ---------------------------------------------------------------------------

@@ -34,33 +34,60 @@ struct Scratch {
   int boff[SLUICE_MAX_SLOTS];
   int run[SLUICE_MAX_SLOTS];
   int pend[SLUICE_MAX_SLOTS];       // the slot's rows may still be streaming
-  int chunk_slot[kPlanThreads];
   int wsum[2][kPlanWaves];
-  int total;
 };
 
-// Builds the plan of the P pairs `ids` over `map` (global -> slot, -1 = not
-// resident; nullptr = identity) into `plan`.  pending [S] (may be null):
-// nonzero for the slots whose rows the layer's last gap is still streaming;
-// their blocks come after every other block (so the work on resident experts
-// is dispatched first) and carry kPendingBit.  Called by all kPlanThreads
+// Rank of this lane among the lower lanes of its wave that hold the same
+// key (keys < 0 take no part), the number of lanes holding it, and whether
+// this lane is the lowest of them.  Wave-uniform loop, one pass per
+// distinct key.
+__device__ inline int wave_rank(int key, int& count, bool& lowest) {
+  const int lane = threadIdx.x & (SLUICE_WAVE - 1);
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (SLUICE_WAVE - lane));
+  int rank = 0;
+  count = 0;
+  lowest = false;
+  uint64_t todo = __ballot(key >= 0);
+  while (todo != 0) {
+    const int l = __builtin_ctzll(todo);
+    const int k = __shfl(key, l, SLUICE_WAVE);
+    const uint64_t m = __ballot(key == k);
+    if (key == k) {
+      rank = __popcll(m & below);
+      count = __popcll(m);
+      lowest = lane == l;
+    }
+    todo &= ~m;
+  }
+  return rank;
+}
+
+// Stages the map (global -> slot, -1 = not resident; nullptr = identity)
+// and the pending marks (nonzero = the slot's rows may still be streaming;
+// nullptr = none) in the scratch.
+__device__ inline void plan_stage(const int32_t* __restrict__ map, int E, int S,
+                                  const int32_t* __restrict__ pending, Scratch& sc) {
+  for (int e = threadIdx.x; e < E; e += kPlanThreads) sc.slot_of[e] = map != nullptr ? map[e] : e;
+  for (int s = threadIdx.x; s < S; s += kPlanThreads)
+    sc.pend[s] = pending != nullptr && pending[s] != 0;
+}
+
+// Builds the plan of the P pairs `ids` into `plan` over the map and pending
+// marks staged in sc.slot_of / sc.pend (written by this workgroup before
+// the call; the first barrier below publishes them).  id0 = ids[tid] for
+// tid < P (-1 otherwise), as the caller loaded it.  Blocks of pending slots
+// come after every other block (so the work on resident experts is
+// dispatched first) and carry kPendingBit.  Called by all kPlanThreads
 // threads of the workgroup; returns the block count to every thread.
-__device__ inline int plan_build(const int32_t* __restrict__ ids, int P,
-                                 const int32_t* __restrict__ map, int E, int S,
-                                 const int32_t* __restrict__ pending, Scratch& sc,
-                                 int32_t* __restrict__ plan) {
+__device__ inline int plan_build_staged(int id0, const int32_t* __restrict__ ids, int P, int E,
+                                        int S, Scratch& sc, int32_t* __restrict__ plan) {
   const int tid = threadIdx.x;
   const int lane = tid & (SLUICE_WAVE - 1), wave = tid / SLUICE_WAVE;
   int32_t* blocks = plan + kHeader;
   int32_t* valid = blocks + (size_t)kBlockInts * P;
-  // The first kPlanThreads ids and the whole map are loaded together and the
-  // map is staged in LDS, so the slot lookups need no second round trip.
-  const int id0 = tid < P ? ids[tid] : -1;
-  for (int e = tid; e < E; e += kPlanThreads) sc.slot_of[e] = map != nullptr ? map[e] : e;
   for (int s = tid; s < S; s += kPlanThreads) {
     sc.cnt[s] = 0;
     sc.run[s] = 0;
-    sc.pend[s] = pending != nullptr && pending[s] != 0;
   }
   __syncthreads();
   auto slot_of = [&](int g) {
@@ -111,33 +138,37 @@ __device__ inline int plan_build(const int32_t* __restrict__ ids, int P,
       acc[c] += (sc.cnt[s] + kBM - 1) / kBM;
     }
   }
-  if (tid == 0) sc.total = tot[0] + tot[1];
   __syncthreads();
-  // Ranks in pair order, one chunk of kPlanThreads pairs at a time.
+  // Ranks in pair order, one chunk of kPlanThreads pairs at a time: within a
+  // wave by ballot, across the chunk's waves in wave order (each wave adds
+  // its per-slot counts to run[] before the next one reads it).
   for (int c = 0; c < P; c += kPlanThreads) {
     const int p = c + tid;
     const int s = p < P ? slot_of(c == 0 ? id0 : ids[p]) : -1;
-    sc.chunk_slot[tid] = s;
-    __syncthreads();
-    if (s >= 0) {
-      int r = sc.run[s];
-      for (int q = 0; q < tid; ++q) r += (sc.chunk_slot[q] == s) ? 1 : 0;
-      const int b = sc.boff[s] + r / kBM;
-      const int pos = r % kBM;
-      int32_t* blk = blocks + (size_t)b * kBlockInts;
-      blk[2 + pos] = p;
-      if (pos == 0) {
-        blk[0] = s | (sc.pend[s] ? kPendingBit : 0);
-        const int left = sc.cnt[s] - (r / kBM) * kBM;
-        blk[1] = left < kBM ? left : kBM;
+    int n_same;
+    bool lowest;
+    const int wr = wave_rank(s, n_same, lowest);
+    const int waves = min(kPlanWaves, (P - c + SLUICE_WAVE - 1) / SLUICE_WAVE);
+    for (int w = 0; w < waves; ++w) {
+      if (wave == w && s >= 0) {
+        const int r = sc.run[s] + wr;
+        const int b = sc.boff[s] + r / kBM;
+        const int pos = r % kBM;
+        int32_t* blk = blocks + (size_t)b * kBlockInts;
+        blk[2 + pos] = p;
+        if (pos == 0) {
+          blk[0] = s | (sc.pend[s] ? kPendingBit : 0);
+          const int left = sc.cnt[s] - (r / kBM) * kBM;
+          blk[1] = left < kBM ? left : kBM;
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (lowest) sc.run[s] += n_same;
       }
+      __syncthreads();
     }
     if (p < P) valid[p] = s >= 0 ? 1 : 0;
-    __syncthreads();
-    if (s >= 0) atomicAdd(&sc.run[s], 1);
-    __syncthreads();
   }
-  const int nb = sc.total;
+  const int nb = tot[0] + tot[1];
   if (tid == 0) {
     plan[0] = nb;
     plan[1] = P;
@@ -145,6 +176,16 @@ __device__ inline int plan_build(const int32_t* __restrict__ ids, int P,
     plan[3] = 0;
   }
   return nb;
+}
+
+// plan_build_staged over a map and pending marks in global memory.
+__device__ inline int plan_build(const int32_t* __restrict__ ids, int P,
+                                 const int32_t* __restrict__ map, int E, int S,
+                                 const int32_t* __restrict__ pending, Scratch& sc,
+                                 int32_t* __restrict__ plan) {
+  const int id0 = (int)threadIdx.x < P ? ids[threadIdx.x] : -1;
+  plan_stage(map, E, S, pending, sc);
+  return plan_build_staged(id0, ids, P, E, S, sc, plan);
 }
 
 }  // namespace sluice_plan
