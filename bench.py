@@ -366,11 +366,29 @@ def kernel_roofline(dec, c, recorded, reps=3):
         return {"kernel": name, "avg_us": us, "algorithmic_bytes": avg,
                 "achieved_GBs": avg / (us * 1e-6) / 1e9}
 
+    def read_probe(nbytes):
+        """A plain streaming-read kernel over nbytes per launch (regions
+        rotating through 4x that, like the layers above), timed the same way:
+        what a kernel that only reads reaches at this launch size."""
+        nbytes = max(16, int(nbytes) // 16 * 16)
+        buf = torch.empty(4 * nbytes, dtype=torch.uint8, device=dec.dev)
+        sink = torch.zeros(1, dtype=torch.int32, device=dec.dev)
+        regions = [buf.data_ptr() + i * nbytes for i in range(4)]
+        us = _event_loop(stream, lambda p: _lib.check(
+            lib.sluice_read_probe(p, nbytes, sink.data_ptr(), st), "read_probe"), regions,
+            max(2, reps * len(items) // 4))
+        del buf
+        return {"bytes": nbytes, "avg_us": us, "achieved_GBs": nbytes / (us * 1e-6) / 1e9}
+
     kind = "fp8" if sp["fp8"] else "bf16"
     r1 = res(f"moe_gemm1_kernel<{kind}>", us1, b1)
     r1["mfma_util_pct"] = 100.0 * float(np.mean(fl)) / (us1 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS
     r2 = res(f"moe_gemm2_kernel<{kind}>", us2, b2)
     r2["mfma_util_pct"] = 100.0 * float(np.mean(fl)) / (us2 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS
+    for r in (r1, r2):
+        rp = read_probe(r["algorithmic_bytes"])
+        r["read_probe_GBs"] = rp["achieved_GBs"]
+        r["frac_of_read_probe"] = r["achieved_GBs"] / rp["achieved_GBs"]
     rb = c * sp["E"] * 4 + (sp["E"] * 4 if sp["e_bias"] else 0) + c * k * 8
     return {"c": c, "launches": reps * len(items), "gemm1": r1, "gemm2": r2,
             "combine": res("moe_combine_kernel", us3, b3),
@@ -549,7 +567,9 @@ def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, lo
         "gemm1": {"c": c_main, "avg_us": g1["avg_us"], "achieved_GBs": g1["achieved_GBs"],
                   "frac": g1["achieved_GBs"] / HBM_PEAK_GBS,
                   "algorithmic_bytes_per_launch": g1["algorithmic_bytes"],
-                  "mfma_util_pct": g1["mfma_util_pct"]},
+                  "mfma_util_pct": g1["mfma_util_pct"],
+                  "read_probe_GBs": g1["read_probe_GBs"],
+                  "frac_of_read_probe": g1["frac_of_read_probe"]},
         "kernels": {kk: roof[kk] for kk in ("gemm2", "combine", "route")},
         "copy_256MiB_GBs": roof["copy_256MiB_GBs"],
     }
@@ -678,6 +698,9 @@ def main():
         "kernel": "moe_gemm1_kernel<fp8>" if sp["fp8"] else "moe_gemm1_kernel<bf16>",
         "avg_us": g1["avg_us"], "algorithmic_bytes_per_launch": g1["algorithmic_bytes_per_launch"],
         "mfma_util_pct": g1["mfma_util_pct"],
+        # a plain streaming-read kernel timed the same way at the same bytes
+        # per launch: the HBM rate a kernel that only reads reaches there
+        "read_probe_GBs": g1["read_probe_GBs"], "frac_of_read_probe": g1["frac_of_read_probe"],
     }
     print(json.dumps(line), flush=True)
 

@@ -62,6 +62,7 @@ SIGNATURES = {
          c_float, _P, _P, _P, _P, c_int, _P, _P, c_size_t, _P, _P, _P],
     ),
     "sluice_moe_plan_ints": (c_size_t, [c_int, c_int]),
+    "sluice_read_probe": (c_int, [_P, c_size_t, _P, _P]),
     "sluice_moe_align": (c_int, [_P, c_int, c_int, _P, c_int, c_int, _P, _P]),
     "sluice_moe_gemm1_bf16": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, _P, _P]),
     "sluice_moe_gemm2_bf16": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, _P]),

@@ -23,7 +23,7 @@ INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(HERE, "libsluice_hip.so")
 BUILD_DIR = os.path.join(ROOT, "_build")
 
-SOURCES = ["routing.hip", "gap.hip", "moe.hip", "decoder.hip"]
+SOURCES = ["routing.hip", "gap.hip", "moe.hip", "decoder.hip", "probe.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
