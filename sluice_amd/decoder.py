@@ -861,7 +861,9 @@ class SyntheticDecoder:
                 if uniform_routing:
                     rb = RoutingBias(sp["E"], max_batch, steps_tbl, 0.0, 0.0, 0.0, 8000 + li, dev,
                                      step=self.step)
-                    rb.fill_uniform(g)
+                    # sigmoid scores saturate to 1.0 in fp32 past |x| ~ 17, which
+                    # would tie many experts (the lowest ids win): smaller noise
+                    rb.fill_uniform(g, scale=3.0 if sp["scoring"] == "sigmoid" else 10.0)
                 else:
                     rb = RoutingBias(sp["E"], max_batch, steps_tbl, zipf_s, rho, sigma, 8000 + li,
                                      dev, step=self.step)

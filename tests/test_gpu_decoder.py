@@ -12,11 +12,11 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-def _run(spec, layers, c, steps, graphs, slots, gap_server):
+def _run(spec, layers, c, steps, graphs, slots, gap_server, uniform=False):
     from sluice_amd.decoder import SyntheticDecoder
 
     dec = SyntheticDecoder(spec, max_batch=c, slots=slots, gen_len=steps + 16, layers=layers,
-                           device=DEV, seed=3, gap_server=gap_server)
+                           device=DEV, seed=3, gap_server=gap_server, uniform_routing=uniform)
     toks = []
 
     def out_of_step():
@@ -60,6 +60,30 @@ def test_one_graph_step_with_gap_server_matches_eager_inline_gaps(spec, layers, 
         assert x["counters"][:4] == y["counters"][:4]
     assert ma == mb
     assert sum(x["counters"][1] for x in sa) > 0  # the miss path was exercised
+
+
+@pytest.mark.parametrize("spec,layers,c,slots,steps", [("qwen3", 2, 4, 32, 10),
+                                                      ("v3", 2, 8, 64, 5)])
+def test_miss_heavy_graph_decode_matches_eager(spec, layers, c, slots, steps):
+    """Uniform routing over few slots: nearly every selected expert misses,
+    so in the replayed graph each layer's expert product computes its
+    resident experts while the misses' rows stream and waits per filled
+    slot (the gap server answers before the rows land).  Tokens, slot state,
+    counters and maps equal eager decoding, whose inline gaps return only
+    after every row has landed."""
+    print(f"miss-heavy decoder {spec} layers={layers} c={c} slots={slots}", flush=True)
+    a, sa, ma = _run(spec, layers, c, steps, graphs=False, slots=slots, gap_server=False,
+                     uniform=True)
+    b, sb, mb = _run(spec, layers, c, steps, graphs=True, slots=slots, gap_server=True,
+                     uniform=True)
+    assert np.array_equal(a, b)
+    for x, y in zip(sa, sb):
+        assert x["expert_in_slot"] == y["expert_in_slot"]
+        assert x["counters"][:4] == y["counters"][:4]
+    assert ma == mb
+    # most of each step's (token, expert) pairs missed
+    misses = sum(y["counters"][1] for y in sb)
+    assert misses >= steps * layers * c * 2, misses
 
 
 def test_piece_graphs_with_inline_gaps_match_eager():
