@@ -639,6 +639,11 @@ def main():
         q96 = measure("qwen3", 96, [12], a, dev, gen_len, stores=qstores,
                       locality=() if a.no_locality else (12,))[0]
         extras.append(q96)
+        # c=12 at 64 slots is above the router-split envelope (12 * 8 > 64): the
+        # classic wave path serves it (the reference's router-split has no number)
+        q64c = measure("qwen3", 64, [12], a, dev, gen_len, stores=qstores, locality=())[0]
+        q64c["config"]["workload"] = "classic wave path: c=12 above the router-split envelope"
+        extras.append(q64c)
         stress = measure("qwen3", 32, [4], a, dev, gen_len, uniform=True, stores=qstores)[0]
         stress["config"]["workload"] = "stress: uniform i.i.d. top-8, no prompt (no locality)"
         extras.append(stress)

@@ -726,6 +726,7 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
       }
     }
     // Each group of experts landed: mark its slots ready for this gap.
+    int marked = 0;  // streams whose slots are marked
     for (int g = 0; g < issued; ++g) {
       const int w = wait_event(L->fill_ev[g]);
       if (w != SLUICE_OK) {
@@ -734,9 +735,15 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
       }
       if (!early) continue;
       const int end = std::min(n_streams, (g + 1) * per_event);
-      for (int i = g * per_event; i < end; ++i)
-        __atomic_store_n(&mb->slot_ready[L->streams[2 * i + 1]], want, __ATOMIC_RELEASE);
+      for (; marked < end; ++marked)
+        __atomic_store_n(&mb->slot_ready[L->streams[2 * marked + 1]], want, __ATOMIC_RELEASE);
     }
+    // A failed stream-in is reported to the caller (and, under the server,
+    // raises the abort flag): the device must not wait for rows that are
+    // not coming, so the rest of the answered slots are marked too.
+    if (early && rc != SLUICE_OK)
+      for (; marked < n_streams; ++marked)
+        __atomic_store_n(&mb->slot_ready[L->streams[2 * marked + 1]], want, __ATOMIC_RELEASE);
     if (early) {
       L->done_stamp.store(want, std::memory_order_release);
       return rc;
