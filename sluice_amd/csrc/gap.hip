@@ -397,13 +397,27 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     }
     __syncthreads();
     if (s_status == 0) {
-      // Install the standing map the host sent (already acquired above).
-      const int nS = ld_sys(&mb->n_slots);
+      // Install the standing map the host sent.  The answer was acquired
+      // above, so its words are read relaxed, all in one bus round trip:
+      // the slot table and the fill list (both at most S entries) with
+      // their counts.
+      constexpr int kPer = SLUICE_MAX_SLOTS / kLookupThreads;
+      static_assert(SLUICE_MAX_SLOTS % kLookupThreads == 0, "answer words per thread");
+      int sg[kPer], fl[kPer];
+      const int ns_word = ld_host(&mb->n_slots), nf_word = ld_host(&mb->n_fill);
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int i = u * kLookupThreads + tid;
+        sg[u] = i < S ? ld_host(&mb->slot_global[i]) : -1;
+        fl[u] = i < S ? ld_host(&mb->fill[i]) : -1;
+      }
+      const int nS = min(ns_word, S);
       for (int e = tid; e < E; e += kLookupThreads) present[e] = -1;
       __syncthreads();
-      for (int s = tid; s < nS; s += kLookupThreads) {
-        const int g = ld_sys(&mb->slot_global[s]);
-        if ((unsigned)g < (unsigned)E) present[g] = s;
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int sl = u * kLookupThreads + tid;
+        if (sl < nS && (unsigned)sg[u] < (unsigned)E) present[sg[u]] = sl;
       }
       __syncthreads();
       for (int e = tid; e < E; e += kLookupThreads) {
@@ -414,9 +428,12 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
       // them.  Their poll claims and seen marks (after the fill list) start
       // over.
       int32_t* claim = prev + 1 + S;
-      const int nf = min(ld_sys(&mb->n_fill), S);
-      for (int i = tid; i < nf; i += kLookupThreads) {
-        const int sl = ld_sys(&mb->fill[i]);
+      const int nf = min(nf_word, S);
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int i = u * kLookupThreads + tid;
+        if (i >= nf) continue;
+        const int sl = fl[u];
         const int ok = (unsigned)sl < (unsigned)S;
         if (ok) {
           pending[sl] = s_stamp;
