@@ -99,3 +99,56 @@ def test_entry_keeps_vllm_routing_when_the_kernel_cannot_express_it():
                            layer.last_ids.cpu().numpy())
     assert om.rel_l2(out.float().cpu().numpy(), ref) <= 1e-2
     off.close()
+
+
+@pytest.mark.parametrize("kind", sorted(ROUTERS))
+def test_gap_built_plan_gives_the_product_it_plans_itself(kind):
+    """After each gap op (misses streaming while the product runs), the
+    expert product over the plan the gap kernel built equals, bit for bit,
+    the product that plans itself (its align kernel) on the same ids and map,
+    shared experts folded in or not; a plan buffer too small for the call or
+    of the wrong type is refused before anything is launched."""
+    from sluice_amd import ops
+    from sluice_amd.decoder import SyntheticMoELayer, build_offloaded
+
+    E, k, scoring, renorm, scale, n_group, topk_group, e_bias = ROUTERS[kind]
+    H, I, S, T = 256, 128, 32, 4
+    print(f"gap-built plan {kind}", flush=True)
+    layer = SyntheticMoELayer(H, I, E, k, scoring=scoring, renorm=renorm, routed_scale=scale,
+                              n_group=n_group, topk_group=topk_group, e_bias=e_bias, seed=9,
+                              device=DEV, shared_I=2 * I)
+    off = build_offloaded([layer], slots=S, device=DEV)
+    cache = off._caches[id(layer)]
+    rng = np.random.default_rng(17)
+    sh = layer.shared
+
+    def route(x):
+        logits, _ = layer.runner.gate(x)
+        return layer.runner.router.select_experts(hidden_states=x, router_logits=logits)
+
+    for step in range(6):
+        x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(
+            torch.bfloat16).to(DEV)
+        tw, ti = route(x)
+        h = torch.ops.vllm.sluice_stream_gap(x, ti, 0)
+        plan = off.gap_plan(0, ti.numel())
+        assert plan is not None
+        kw = dict(global_num_experts=E, expert_map=cache.expert_map_buf)
+        got = ops.fused_experts(h, layer.w13_weight, layer.w2_weight, tw, ti, plan=plan, **kw)
+        want = ops.fused_experts(h, layer.w13_weight, layer.w2_weight, tw, ti, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), step
+        if sh is not None:
+            kw.update(shared_w1=sh.gate_up, shared_w2=sh.down)
+            got = ops.fused_experts(h, layer.w13_weight, layer.w2_weight, tw, ti, plan=plan, **kw)
+            want = ops.fused_experts(h, layer.w13_weight, layer.w2_weight, tw, ti, **kw)
+            torch.cuda.synchronize()
+            assert torch.equal(got.view(torch.int16), want.view(torch.int16)), step
+    x = torch.zeros((T, H), dtype=torch.bfloat16, device=DEV)
+    tw, ti = route(x)
+    for bad in (torch.zeros(8, dtype=torch.int32, device=DEV),
+                torch.zeros(cache.plan.numel(), dtype=torch.int64, device=DEV)):
+        with pytest.raises(ValueError):
+            ops.fused_experts(x, layer.w13_weight, layer.w2_weight, tw, ti, plan=bad,
+                              global_num_experts=E, expert_map=cache.expert_map_buf)
+    off.close()
