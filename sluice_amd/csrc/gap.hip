@@ -722,7 +722,10 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
       if (e != hipSuccess) rc = (int)e;
       else L->fill_ev.push_back(ev);
     }
-    if (early && rc == SLUICE_OK) respond(L, want, SLUICE_OK, n_streams);
+    // The link is the bottleneck of a missing step: the first expert's rows
+    // are queued before the device is answered (its resident experts then
+    // compute while the rows stream), the other experts' after.
+    bool answered = !early;
     int issued = 0;  // events recorded
     for (int i = 0; rc == SLUICE_OK && i < n_streams; ++i) {
       const int local = L->streams[2 * i], slot = L->streams[2 * i + 1];
@@ -741,7 +744,14 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
         if (e != hipSuccess) rc = (int)e;
         else ++issued;
       }
+      if (!answered && rc == SLUICE_OK) {
+        respond(L, want, SLUICE_OK, n_streams);
+        answered = true;
+      }
     }
+    // (a failure before the answer still answers the device: the map and
+    // the fill list are the bookkeeping's; the slots are marked below)
+    if (!answered) respond(L, want, SLUICE_OK, n_streams);
     // Each group of experts landed: mark its slots ready for this gap.
     int marked = 0;  // streams whose slots are marked
     for (int g = 0; g < issued; ++g) {
