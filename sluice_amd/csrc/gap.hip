@@ -542,7 +542,7 @@ struct sluice_layer {
   int32_t* ids_host = nullptr;  // pinned staging of the step's ids
   size_t ids_cap = 0;
   int64_t classic_steps = 0, classic_waves = 0;
-  std::vector<hipEvent_t> fill_ev;  // one per expert streamed by a gap
+  std::vector<hipEvent_t> fill_ev;  // one per group of experts a gap streams
 };
 
 namespace {

@@ -15,9 +15,10 @@
 // 4 waves that split K and reduce through LDS.
 //
 // Launch shape: align (1 WG) -> gemm1 (+silu*up) -> gemm2 (*w) -> combine,
-// four grid-stride kernels over a plan in global memory.  (A single
-// persistent kernel with cross-workgroup hand-offs was measured 1.6-1.8x
-// slower than these four launches and is not kept.)
+// grid-stride kernels over a plan in global memory; the align launch is
+// skipped when the caller hands in the plan its router-split gap kernel
+// built.  (A single persistent kernel with cross-workgroup hand-offs was
+// measured 1.6-1.8x slower than these launches and is not kept.)
 #include <math.h>
 
 #include <mutex>

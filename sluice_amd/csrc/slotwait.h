@@ -3,7 +3,7 @@
 // When a router-split gap misses, the host answers the gap kernel as soon as
 // the slot bookkeeping is done -- before the rows have landed -- and marks
 // each filled slot ready (the gap's stamp in ready[slot], host-mapped
-// memory) once that expert's copies completed.  The gap kernel records the
+// memory) once the copies of its group of experts completed.  The gap kernel records the
 // filled slots in pending[slot] (device memory, the gap's stamp).  The expert
 // product then computes the hit experts while the misses stream: its work
 // items on a pending slot wait until ready[slot] == pending[slot] and take a
