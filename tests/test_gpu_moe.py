@@ -96,6 +96,10 @@ def _moe_case(T, H, I, E, S, k, seed, resident_frac=0.85, use_map=True, scale=1.
     (1, 2048, 768, 128, 8, 8),      # Qwen3 c=1
     (8, 2048, 768, 128, 16, 8),     # Qwen3 c=8
     (12, 2048, 768, 128, 16, 8),    # Qwen3 c=12
+    (8, 4096, 14336, 8, 2, 2),      # Mixtral-8x7B expert shape (top-2, long K in gemm2)
+    (8, 5120, 1536, 160, 8, 6),     # DeepSeek-V2 (236B) expert shape
+    (8, 2048, 1024, 64, 16, 8),     # OLMoE-1B-7B expert shape
+    (8, 2048, 1408, 60, 16, 4),     # Qwen1.5-MoE-A2.7B expert shape (60 experts)
     (33, 256, 192, 16, 16, 4),      # > 16 pairs per slot: several blocks per expert
     (5, 64, 128, 8, 8, 2),          # K shorter than the waves: some waves stream nothing
 ])

@@ -18,6 +18,9 @@ CASES = [
     (8, 256, 8, "sigmoid", True, 2.5, 8, 4, torch.float32, True),      # V3
     (8, 256, 8, "sigmoid", True, 2.5, 8, 4, torch.bfloat16, True),
     (16, 160, 6, "softmax", False, 16.0, 8, 3, torch.float32, False),  # V2 group-limited
+    (8, 8, 2, "softmax", True, 1.0, 1, 1, torch.bfloat16, False),      # Mixtral top-2
+    (8, 64, 8, "softmax", False, 1.0, 1, 1, torch.bfloat16, False),    # OLMoE
+    (8, 60, 4, "softmax", False, 1.0, 1, 1, torch.bfloat16, False),    # Qwen1.5-MoE
     (64, 1024, 16, "softmax", True, 1.0, 1, 1, torch.float32, False),  # limits
     (5, 100, 7, "sigmoid", False, 1.0, 1, 1, torch.float32, True),     # ragged E
 ]
