@@ -123,3 +123,30 @@ def test_mla_workspace_grows_with_batch_and_heads(lib):
     ws = lib.sluice_dec_mla_workspace
     assert ws(0, 16) == 0 and ws(1, 0) == 0
     assert 0 < ws(1, 16) < ws(8, 16) < ws(16, 16) < ws(16, 32)
+
+
+def test_gap_launch_and_read_probe_argument_checks(lib):
+    """The gap launch refuses a misaligned plan buffer before looking at the
+    layer's device state (a host-only layer has none: SLUICE_E_STATE); the
+    read probe refuses null or unaligned buffers and launches nothing for
+    zero bytes.  No GPU work is started."""
+    h = ctypes.c_void_p()
+    lof = (ctypes.c_int32 * 16)(*range(16))
+    assert lib.sluice_layer_create(16, 16, 8, 4, lof, None, ctypes.byref(h)) == _lib.SLUICE_OK
+    try:
+        ids = ctypes.c_void_p(1 << 20)  # an aligned stand-in nothing dereferences
+        assert lib.sluice_layer_gap_launch(h, ids, 8, None, None, 0, ctypes.c_void_p((1 << 20) + 2),
+                                           None) == _lib.SLUICE_E_INVAL
+        assert lib.sluice_layer_gap_launch(h, ids, 8, None, None, 0, None,
+                                           None) == _lib.SLUICE_E_STATE
+        assert lib.sluice_layer_gap_launch(h, None, 8, None, None, 0, None,
+                                           None) == _lib.SLUICE_E_INVAL
+    finally:
+        assert lib.sluice_layer_destroy(h) == _lib.SLUICE_OK
+    sink = ctypes.c_void_p(1 << 20)
+    assert lib.sluice_read_probe(None, 16, sink, None) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_read_probe(ctypes.c_void_p(1 << 20), 24, sink, None) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_read_probe(ctypes.c_void_p((1 << 20) + 8), 16, sink,
+                                 None) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_read_probe(ctypes.c_void_p(1 << 20), 16, None, None) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_read_probe(ctypes.c_void_p(1 << 20), 0, sink, None) == _lib.SLUICE_OK
