@@ -217,3 +217,94 @@ def expert_stores_from_checkpoint(path, layer: int, pinned: bool = True, threads
 class _PlainStore:
     def __init__(self, t: torch.Tensor):
         self.tensor = t
+
+
+def _bench(argv=None) -> dict:
+    """Loader throughput on a synthetic checkpoint of a model's expert shape:
+    one safetensors file per MoE layer (every expert's gate/up/down rows, and
+    fp8 block scales for an fp8 shape; each expert's rows hold a distinct
+    byte value) written to --dir (default: a fresh directory in /dev/shm, so
+    the files are in memory as a warm page cache would be), then each layer
+    loaded into pinned host stores: the stores' allocation timed apart from
+    the copies, every expert's placement spot-checked."""
+    import argparse
+    import shutil
+    import tempfile
+    import time
+
+    from safetensors.torch import save_file
+
+    from sluice_amd import ops
+    from sluice_amd.decoder import SPECS
+
+    ap = argparse.ArgumentParser(description=_bench.__doc__)
+    ap.add_argument("--bench", action="store_true")
+    ap.add_argument("--shape", choices=sorted(SPECS), default="qwen3")
+    ap.add_argument("--layers", type=int, default=2)
+    ap.add_argument("--threads", type=int, default=8)
+    ap.add_argument("--dir", default=None)
+    a = ap.parse_args(argv)
+    sp = SPECS[a.shape]
+    E, I, H, fp8 = sp["E"], sp["I"], sp["H"], sp["fp8"]
+    cd = lambda n: (n + 127) // 128  # noqa: E731
+    own = a.dir is None
+    d = a.dir or tempfile.mkdtemp(prefix="sluice_ckpt_",
+                                  dir="/dev/shm" if os.path.isdir("/dev/shm") else None)
+    try:
+        t0 = time.perf_counter()
+        for L in range(a.layers):
+            tensors = {}
+            for e in range(E):
+                v = (L * 37 + e) % 120 + 1
+                for proj, (r, c) in (("gate_proj", (I, H)), ("up_proj", (I, H)),
+                                     ("down_proj", (H, I))):
+                    name = EXPERT_KEY.format(layer=L, e=e, proj=proj, kind="weight")
+                    raw = torch.full((r, c * (1 if fp8 else 2)), v, dtype=torch.uint8)
+                    tensors[name] = raw.view(torch.float8_e4m3fn) if fp8 else \
+                        raw.view(torch.bfloat16)
+                    if fp8:
+                        tensors[EXPERT_KEY.format(layer=L, e=e, proj=proj,
+                                                  kind="weight_scale_inv")] = torch.full(
+                            (cd(r), cd(c)), float(v), dtype=torch.float32)
+            save_file(tensors, os.path.join(d, f"layer-{L:03d}.safetensors"))
+            del tensors
+        write_s = time.perf_counter() - t0
+        ck = Checkpoint(d)
+        try:
+            t0 = time.perf_counter()
+            stores = {n: ops.HostStore(shape, dt)
+                      for n, (shape, dt) in store_shapes(E, I, H, fp8).items()}
+            alloc_s = time.perf_counter() - t0
+            views = {n: s.tensor for n, s in stores.items()}
+            per_layer = []
+            for L in range(a.layers):
+                t0 = time.perf_counter()
+                nbytes = load_experts(ck, L, views, threads=a.threads)
+                dt = time.perf_counter() - t0
+                w13 = views["w13_weight"].view(torch.uint8)
+                w2 = views["w2_weight"].view(torch.uint8)
+                for e in (0, E // 2, E - 1):
+                    v = (L * 37 + e) % 120 + 1
+                    if int(w13[e, 0, 0]) != v or int(w13[e, -1, -1]) != v or \
+                            int(w2[e, -1, -1]) != v:
+                        raise RuntimeError(f"layer {L} expert {e}: rows misplaced")
+                per_layer.append({"bytes": nbytes, "s": dt, "GBs": nbytes / dt / 1e9})
+            store_bytes = sum(t.numel() * t.element_size() for t in views.values())
+        finally:
+            ck.close()
+        out = {"shape": a.shape, "experts": E, "layers": a.layers, "threads": a.threads,
+               "fp8": fp8, "store_GB": store_bytes / 1e9, "write_s": write_s,
+               "pinned_alloc_s": alloc_s, "pinned_alloc_GBs": store_bytes / alloc_s / 1e9,
+               "per_layer": per_layer,
+               "load_GBs": sum(x["bytes"] for x in per_layer) / sum(x["s"] for x in per_layer)
+               / 1e9,
+               "source": "/dev/shm" if d.startswith("/dev/shm") else d}
+        del stores, views
+        return out
+    finally:
+        if own:
+            shutil.rmtree(d, ignore_errors=True)
+
+
+if __name__ == "__main__":
+    print(json.dumps(_bench()), flush=True)
