@@ -263,3 +263,65 @@ def test_device_gap_v3_fp8_streams_four_rows_per_miss(monkeypatch, slru_golden, 
         case["counters"]["gaps"], case["counters"]["misses"], case["counters"]["fast_hits"])
     assert s["bytes"] == s["misses"] * cache.bytes_per_expert
     off.close()
+
+
+def test_abort_ends_an_unserved_gap_and_resync_resumes(monkeypatch):
+    """Failure handling forced from the host: with the process-wide abort
+    flag raised, a gap whose ids miss is launched and never served.  Its
+    bounded wait ends at once (the stream completes), the device map and the
+    host's slot state stay as they were, and the layer reports the abort.
+    After the flag is cleared and the layer resynchronised, later gaps
+    assign slots exactly as an oracle that never saw the aborted step."""
+    import time
+
+    from oracle.slru import LayerCache
+    from sluice_amd import _lib
+
+    E, S, k = 64, 16, 4
+    print("gap abort + resync", flush=True)
+    layer = _Layer(E, E)
+    off = _offloader(monkeypatch, S, 0.5, False)
+    off.wrap_modules(iter([layer]))
+    with torch.cuda.device(DEV):
+        off.post_init()
+    cache = off._caches[id(layer)]
+    off._rs_caches.append(cache)
+    lib = _lib.load()
+    oracle = LayerCache(E, E, S, 0.5)
+    hs = torch.zeros((2, 64), dtype=torch.bfloat16, device=DEV)
+    rng = np.random.default_rng(5)
+
+    def served_step():
+        ids_np = rng.choice(E, 2 * k, replace=False).astype(np.int32)
+        torch.ops.vllm.sluice_stream_gap(hs, torch.from_numpy(ids_np).to(DEV).view(-1, k), 0)
+        oracle.gap(ids_np.tolist(), fast_hit=False)
+        torch.cuda.synchronize()
+        assert cache._state()["expert_in_slot"] == [
+            -1 if v is None else v for v in oracle.expert_in_slot]
+        assert cache.expert_map_buf.cpu().tolist() == oracle.map
+
+    for _ in range(3):
+        served_step()
+    map_before = cache.expert_map_buf.cpu().tolist()
+    state_before = cache._state()
+    missing = np.array([g for g in range(E) if map_before[g] < 0][:2 * k], dtype=np.int32)
+    ids = torch.from_numpy(missing).to(DEV).view(-1, k)
+    st = torch.cuda.current_stream(DEV).cuda_stream
+    assert lib.sluice_gap_abort(1) == 0
+    try:
+        t0 = time.time()
+        _lib.check(lib.sluice_layer_gap_launch(cache.handle, ids.data_ptr(), ids.numel(), None,
+                                               None, 0, None, st), "sluice_layer_gap_launch")
+        torch.cuda.synchronize()
+        assert time.time() - t0 < 10.0  # the wait's own bound is 20 s
+        assert lib.sluice_layer_gap_serve(cache.handle, 0, st) == _lib.SLUICE_E_ABORTED
+    finally:
+        lib.sluice_gap_abort(0)
+    assert cache.expert_map_buf.cpu().tolist() == map_before
+    after = cache._state()
+    for key in ("expert_in_slot", "probation", "protected", "free_slots"):
+        assert after[key] == state_before[key], key
+    assert lib.sluice_layer_gap_resync(cache.handle) == 0
+    for _ in range(6):
+        served_step()
+    off.close()
