@@ -947,6 +947,26 @@ class ExpertStreamOffloader(_OffloaderBase):
         srv, self._server = self._server, None
         _raise_gap(_lib.load().sluice_gap_server_destroy(srv), "sluice_gap_server_destroy")
 
+    def reset_gaps(self) -> None:
+        """After a gap raised (overflow, a timed-out or aborted wait) and the
+        caller has handled it: synchronise the device, stop the gap server
+        (dropping the error it kept), clear the abort flag and line every
+        router-split layer's host stamps up with the device's, then restart
+        the server if one was running.  Slot state is what the served records
+        left; the outputs of the failed steps are invalid.  No counterpart in
+        the reference, whose gap errors end the engine."""
+        torch.cuda.synchronize()
+        lib = _lib.load()
+        restart = self._server is not None
+        if restart:
+            srv, self._server = self._server, None
+            lib.sluice_gap_server_destroy(srv)  # returns the error already raised
+        _lib.check(lib.sluice_gap_abort(0), "sluice_gap_abort")
+        for c in self._rs_caches:
+            _lib.check(lib.sluice_layer_gap_resync(c.handle), "sluice_layer_gap_resync")
+        if restart:
+            self.start_gap_server()
+
     # -- stats ----------------------------------------------------------------
     def gap_counters(self) -> dict:
         """Router-split gap counters summed over the armed layers."""

@@ -325,3 +325,54 @@ def test_abort_ends_an_unserved_gap_and_resync_resumes(monkeypatch):
     for _ in range(6):
         served_step()
     off.close()
+
+
+def test_server_overflow_raises_at_drain_and_reset_resumes(monkeypatch):
+    """With the gap server serving the records, a step whose working set
+    exceeds the slots makes drain() raise the reference's overflow error;
+    the device map stays as it was and the host keeps the reference's
+    partial acquisition.  reset_gaps() then brings the layer back: later
+    gaps follow the oracle again."""
+    from oracle.slru import GapOverflow, LayerCache
+
+    E, S, k = 64, 16, 4
+    print("gap server overflow + reset", flush=True)
+    layer = _Layer(E, E)
+    off = _offloader(monkeypatch, S, 0.5, False)
+    off.wrap_modules(iter([layer]))
+    with torch.cuda.device(DEV):
+        off.post_init()
+    cache = off._caches[id(layer)]
+    off._rs_caches.append(cache)
+    off.start_gap_server()
+    oracle = LayerCache(E, E, S, 0.5)
+    rng = np.random.default_rng(9)
+
+    def step(T, expect_overflow=False):
+        ids_np = rng.choice(E, T * k, replace=False).astype(np.int32)
+        hs = torch.zeros((T, 64), dtype=torch.bfloat16, device=DEV)
+        torch.ops.vllm.sluice_stream_gap(hs, torch.from_numpy(ids_np).to(DEV).view(-1, k), 0)
+        if expect_overflow:
+            with pytest.raises(RuntimeError, match="exceeds slots"):
+                off.drain()
+            with pytest.raises(GapOverflow):
+                oracle.gap(ids_np.tolist(), fast_hit=False)
+        else:
+            off.drain()
+            oracle.gap(ids_np.tolist(), fast_hit=False)
+        st = cache._state()
+        assert st["expert_in_slot"] == [-1 if v is None else v for v in oracle.expert_in_slot]
+        assert st["probation"] == list(oracle.probation)
+        assert st["protected"] == list(oracle.protected)
+
+    for _ in range(4):
+        step(2)
+        assert cache.expert_map_buf.cpu().tolist() == oracle.map
+    map_before = cache.expert_map_buf.cpu().tolist()
+    step(5, expect_overflow=True)  # 20 unique experts > 16 slots
+    assert cache.expert_map_buf.cpu().tolist() == map_before
+    off.reset_gaps()
+    for _ in range(5):
+        step(2)
+        assert cache.expert_map_buf.cpu().tolist() == oracle.map
+    off.close()
