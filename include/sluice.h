@@ -324,6 +324,12 @@ int sluice_gap_server_destroy(sluice_gap_server* server);
  * and a stream synchronisation, sluice_layer_gap_resync lines a layer's host
  * stamps up with the device's. */
 int sluice_gap_abort(int set);
+
+/* The bound of the gap's waits (device and host) for launches after the
+ * call, in seconds; 0 restores SLUICE_GAP_TIMEOUT_S (default 20).  No
+ * counterpart in the reference (its gap waits are host syncs without a
+ * bound); it lets callers, and tests, shorten a wait that must end. */
+int sluice_gap_set_timeout(double seconds);
 int sluice_layer_gap_resync(sluice_layer* layer);
 
 /* The gap, host path (no HIP calls): ids is a host array.  Runs the same

@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+from ctypes import POINTER, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsluice_hip.so")
@@ -83,6 +83,7 @@ SIGNATURES = {
     "sluice_gap_server_error": (c_int, [_P]),
     "sluice_gap_server_destroy": (c_int, [_P]),
     "sluice_gap_abort": (c_int, [c_int]),
+    "sluice_gap_set_timeout": (c_int, [c_double]),
     "sluice_layer_gap_resync": (c_int, [_P]),
     "sluice_layer_gap_host": (
         c_int, [_P, _P, c_int, c_int, _P, c_int, POINTER(c_int), POINTER(c_int)]

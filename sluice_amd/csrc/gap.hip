@@ -496,7 +496,13 @@ double now_s() {
   return ts.tv_sec + 1e-9 * ts.tv_nsec;
 }
 
+// The bound of every gap wait (device and host), in seconds: set by
+// sluice_gap_set_timeout, else SLUICE_GAP_TIMEOUT_S, else 20.
+std::atomic<double> g_timeout_set{0.0};
+
 double gap_timeout_s() {
+  const double set = g_timeout_set.load(std::memory_order_relaxed);
+  if (set > 0) return set;
   static double v = [] {
     const char* s = getenv("SLUICE_GAP_TIMEOUT_S");
     double t = s ? atof(s) : 20.0;
@@ -578,8 +584,7 @@ int layer_device_init(sluice_layer* L) {
     w.seen = w.claim + S;
     w.abort_flag = g_abort_dev;
     w.status = &L->mb_dev->dev_status;
-    w.timeout_ticks = (long long)(gap_timeout_s() * 1000.0 * (double)R->clock_khz);
-    slotwait_register(L->map_dev, w);
+    slotwait_register(L->map_dev, w, R->clock_khz);
   }
   return SLUICE_OK;
 }
@@ -999,6 +1004,12 @@ extern "C" int sluice_gap_server_destroy(sluice_gap_server* S) {
 // clear the abort flag and line the host's stamps up with the device's, so
 // the layers can be used again (their slot state is whatever the served
 // records left; the aborted steps' outputs are invalid).
+extern "C" int sluice_gap_set_timeout(double seconds) {
+  if (!(seconds >= 0.0) || seconds > 86400.0) return SLUICE_E_INVAL;
+  g_timeout_set.store(seconds, std::memory_order_relaxed);
+  return SLUICE_OK;
+}
+
 extern "C" int sluice_gap_abort(int set) {
   if (g_abort_host == nullptr) return SLUICE_OK;
   __atomic_store_n(g_abort_host, set ? 1 : 0, __ATOMIC_RELEASE);
@@ -1461,27 +1472,35 @@ extern "C" const char* sluice_strerror(int code) {
 }
 
 // ---------------------------------------------------------------------------
-// Slot-wait registry: a streaming layer's expert map -> its slot-wait view.
+// Slot-wait registry: a streaming layer's expert map -> its slot-wait view
+// (and its device's wall-clock rate, so a lookup carries the wait bound in
+// force at the launch it serves).
 // ---------------------------------------------------------------------------
 namespace {
+struct WaitEntry {
+  const int32_t* map;
+  SlotWait w;
+  long long clock_khz;
+};
 std::mutex g_wait_mu;
-std::vector<std::pair<const int32_t*, SlotWait>> g_wait;
+std::vector<WaitEntry> g_wait;
 }  // namespace
 
-void slotwait_register(const int32_t* map, const SlotWait& w) {
+void slotwait_register(const int32_t* map, const SlotWait& w, long long clock_khz) {
   std::lock_guard<std::mutex> lk(g_wait_mu);
   for (auto& e : g_wait)
-    if (e.first == map) {
-      e.second = w;
+    if (e.map == map) {
+      e.w = w;
+      e.clock_khz = clock_khz;
       return;
     }
-  g_wait.emplace_back(map, w);
+  g_wait.push_back({map, w, clock_khz});
 }
 
 void slotwait_unregister(const int32_t* map) {
   std::lock_guard<std::mutex> lk(g_wait_mu);
   for (size_t i = 0; i < g_wait.size(); ++i)
-    if (g_wait[i].first == map) {
+    if (g_wait[i].map == map) {
       g_wait.erase(g_wait.begin() + (long)i);
       return;
     }
@@ -1490,6 +1509,10 @@ void slotwait_unregister(const int32_t* map) {
 SlotWait slotwait_lookup(const int32_t* map) {
   std::lock_guard<std::mutex> lk(g_wait_mu);
   for (const auto& e : g_wait)
-    if (e.first == map) return e.second;
+    if (e.map == map) {
+      SlotWait w = e.w;
+      w.timeout_ticks = (long long)(gap_timeout_s() * 1000.0 * (double)e.clock_khz);
+      return w;
+    }
   return SlotWait{};
 }

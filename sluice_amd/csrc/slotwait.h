@@ -28,7 +28,8 @@ struct SlotWait {
 };
 
 // Registry from a layer's device expert map to its slot-wait view (kept by
-// the gap layers, read by the expert product).
-void slotwait_register(const int32_t* expert_map, const SlotWait& w);
+// the gap layers, read by the expert product; a lookup fills timeout_ticks
+// from the wait bound in force, at the layer's device clock rate).
+void slotwait_register(const int32_t* expert_map, const SlotWait& w, long long clock_khz);
 void slotwait_unregister(const int32_t* expert_map);
 SlotWait slotwait_lookup(const int32_t* expert_map);

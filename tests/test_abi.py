@@ -150,3 +150,6 @@ def test_gap_launch_and_read_probe_argument_checks(lib):
                                  None) == _lib.SLUICE_E_INVAL
     assert lib.sluice_read_probe(ctypes.c_void_p(1 << 20), 16, None, None) == _lib.SLUICE_E_INVAL
     assert lib.sluice_read_probe(ctypes.c_void_p(1 << 20), 0, sink, None) == _lib.SLUICE_OK
+    assert lib.sluice_gap_set_timeout(-1.0) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_gap_set_timeout(float("nan")) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_gap_set_timeout(0.0) == _lib.SLUICE_OK

@@ -265,20 +265,23 @@ def test_device_gap_v3_fp8_streams_four_rows_per_miss(monkeypatch, slru_golden, 
     off.close()
 
 
-def test_abort_ends_an_unserved_gap_and_resync_resumes(monkeypatch):
-    """Failure handling forced from the host: with the process-wide abort
-    flag raised, a gap whose ids miss is launched and never served.  Its
-    bounded wait ends at once (the stream completes), the device map and the
-    host's slot state stay as they were, and the layer reports the abort.
-    After the flag is cleared and the layer resynchronised, later gaps
-    assign slots exactly as an oracle that never saw the aborted step."""
+@pytest.mark.parametrize("mode", ["abort", "timeout"])
+def test_unserved_gap_wait_ends_and_resync_resumes(monkeypatch, mode):
+    """Failure handling forced from the host: a gap whose ids miss is
+    launched and never served, with the process-wide abort flag raised
+    ("abort") or the wait bound set to 0.3 s ("timeout").  The device wait
+    ends by itself (the stream completes), the device map and the host's slot
+    state stay as they were, and the layer reports SLUICE_E_ABORTED or
+    SLUICE_E_TIMEOUT.  After the flag or bound is restored and the layer
+    resynchronised, later gaps assign slots exactly as an oracle that never
+    saw the failed step."""
     import time
 
     from oracle.slru import LayerCache
     from sluice_amd import _lib
 
     E, S, k = 64, 16, 4
-    print("gap abort + resync", flush=True)
+    print(f"unserved gap: {mode}", flush=True)
     layer = _Layer(E, E)
     off = _offloader(monkeypatch, S, 0.5, False)
     off.wrap_modules(iter([layer]))
@@ -307,16 +310,25 @@ def test_abort_ends_an_unserved_gap_and_resync_resumes(monkeypatch):
     missing = np.array([g for g in range(E) if map_before[g] < 0][:2 * k], dtype=np.int32)
     ids = torch.from_numpy(missing).to(DEV).view(-1, k)
     st = torch.cuda.current_stream(DEV).cuda_stream
-    assert lib.sluice_gap_abort(1) == 0
+    if mode == "abort":
+        assert lib.sluice_gap_abort(1) == 0
+    else:
+        assert lib.sluice_gap_set_timeout(0.3) == 0
     try:
         t0 = time.time()
         _lib.check(lib.sluice_layer_gap_launch(cache.handle, ids.data_ptr(), ids.numel(), None,
                                                None, 0, None, st), "sluice_layer_gap_launch")
         torch.cuda.synchronize()
-        assert time.time() - t0 < 10.0  # the wait's own bound is 20 s
-        assert lib.sluice_layer_gap_serve(cache.handle, 0, st) == _lib.SLUICE_E_ABORTED
+        waited = time.time() - t0
+        print(f"  device wait ended after {waited:.3f} s", flush=True)
+        assert waited < 10.0  # the default bound is 20 s
+        if mode == "timeout":
+            assert waited >= 0.25
+        want = _lib.SLUICE_E_ABORTED if mode == "abort" else _lib.SLUICE_E_TIMEOUT
+        assert lib.sluice_layer_gap_serve(cache.handle, 0, st) == want
     finally:
         lib.sluice_gap_abort(0)
+        lib.sluice_gap_set_timeout(0.0)
     assert cache.expert_map_buf.cpu().tolist() == map_before
     after = cache._state()
     for key in ("expert_in_slot", "probation", "protected", "free_slots"):
