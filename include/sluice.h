@@ -33,7 +33,7 @@ typedef struct ihipStream_t* sluice_stream_t; /* == hipStream_t */
 #define SLUICE_OK 0
 #define SLUICE_E_INVAL (-1)    /* bad argument / shape outside kernel limits */
 #define SLUICE_E_OVERFLOW (-2) /* working set exceeds slots (reference raises) */
-#define SLUICE_E_TIMEOUT (-3)  /* host wait on a device record timed out */
+#define SLUICE_E_TIMEOUT (-3)  /* a bounded gap wait (host or device) timed out */
 #define SLUICE_E_NOMEM (-4)    /* host allocation failed */
 #define SLUICE_E_STATE (-5)    /* object used in a state it does not allow */
 #define SLUICE_E_ABORTED (-6)  /* a device gap wait ended by the abort flag */

@@ -1458,7 +1458,7 @@ extern "C" const char* sluice_strerror(int code) {
     case SLUICE_E_INVAL: return "invalid argument or shape outside kernel limits";
     case SLUICE_E_OVERFLOW:
       return "Sluice router-split: working set exceeds slots on a decode-sized step; raise SLUICE_SLOTS.";
-    case SLUICE_E_TIMEOUT: return "timed out waiting for the device gap record";
+    case SLUICE_E_TIMEOUT: return "a gap wait (host or device) reached its bound";
     case SLUICE_E_NOMEM: return "host allocation failed";
     case SLUICE_E_STATE: return "object used in a state it does not allow";
     case SLUICE_E_ABORTED: return "gap aborted after an earlier error";
