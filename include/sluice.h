@@ -199,10 +199,11 @@ int sluice_fused_experts_fp8(const void* x, const void* w13,
 /* Token permute / align-to-block (vLLM moe_align_block_size): groups the
  * T*k (token, expert) pairs by slot into blocks of <= SLUICE_BLOCK_M pairs,
  * slots ascending, pairs ascending within a slot.  plan (device int32):
- *   plan[0] = n_blocks, plan[1] = T*k; then per block 18 ints {slot field,
- *   count, pair[16]} starting at plan[4]; then T*k validity flags at
- *   plan[4 + 18*T*k].  Slots whose rows a router-split gap of this map is
- *   still streaming come last, their slot field or-ed with 1<<30.  The shared
+ *   plan[0] = n_blocks, plan[1] = T*k, plan[2] = n_resident; then per block
+ *   18 ints {slot field, count, pair[16]} starting at plan[4]; then T*k
+ *   validity flags at plan[4 + 18*T*k].  Slots whose rows a router-split gap
+ *   of this map is still streaming come last, their slot field or-ed with
+ *   1<<30; the n_resident blocks before them are the others.  The shared
  *   experts' blocks are not in the plan (the product derives them).  Exposed
  *   for testing; fused_experts runs it itself unless given a plan. */
 size_t sluice_moe_plan_ints(int T, int k);

@@ -83,7 +83,10 @@ __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
 }
 
 // Wave 0 reduces the 4 K-split partial accumulators and writes
-// act[pair, tile*16 + kg*4 .. +4] = bf16(silu(g) * u).
+// act[pair, tile*16 + kg*4 .. +4] = bf16(silu(g) * u).  COH: the row is read
+// by other workgroups of the same launch, so it is stored device-coherent
+// and written through before the closing barrier.
+template <bool COH>
 __device__ __forceinline__ void g1_epilogue(RedBuf& red, int pair, int tile, int I,
                                             uint16_t* __restrict__ act) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kg = lane >> 4;
@@ -99,7 +102,12 @@ __device__ __forceinline__ void g1_epilogue(RedBuf& red, int pair, int tile, int
 #pragma unroll
     for (int r = 0; r < 4; ++r) o[r] = g[r] / (1.0f + expf(-g[r])) * u[r];
     uint16_t* dst = act + (size_t)pair * I + tile * 16 + kg * 4;
-    *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
+    if (COH) {
+      st8_coh(dst, pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3]));
+      __builtin_amdgcn_s_waitcnt(0);
+    } else {
+      *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
+    }
   }
   __syncthreads();
 }
@@ -184,7 +192,7 @@ __device__ __forceinline__ void fp8x16_to_bf16(u32x4_t q, u32x4_t& lo, u32x4_t& 
 
 // As stream_bf16 for fp8 weights; s0 / s1: the tiles' scales, one per chunk
 // (absolute chunk index).
-template <int D>
+template <int TM, int D>
 __device__ __forceinline__ void stream_fp8(const uint8_t* __restrict__ a0,
                                            const uint8_t* __restrict__ a1, size_t ld,
                                            const float* __restrict__ s0,
@@ -208,7 +216,8 @@ __device__ __forceinline__ void stream_fp8(const uint8_t* __restrict__ a0,
     q1l[d] = ldg16_stream(p1 + o);
     q1h[d] = ldg16_stream(p1 + ld8 + o);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) xb[d][m] = ldg16(pb + o + m * 8);
+    for (int m = 0; m < 4; ++m)
+      xb[d][m] = TM == kTokCoh ? ld16_coh(pb + o + m * 8) : ldg16(pb + o + m * 8);
   };
   auto consume = [&](int d, int c) {
     st[wl] = q0l[d];
@@ -425,6 +434,7 @@ __device__ __forceinline__ G2Src g2_src(const ExpertW& W, const CallShape& c, in
 // gemm2: hidden rows tile2*32 .. +32 of `slot` against act -> w * partial,
 // w = the routing weight of a routed pair, 1 for a shared pair.
 // ---------------------------------------------------------------------------
+template <bool COH>
 __device__ __forceinline__ void g1_item_bf16(const uint16_t* __restrict__ x, const ExpertW& W,
                                              const CallShape& cs, int slot, int pair, int tile,
                                              uint16_t* __restrict__ act, ItemLds& l) {
@@ -439,7 +449,7 @@ __device__ __forceinline__ void g1_item_bf16(const uint16_t* __restrict__ x, con
                                c1 - c0, l.stage[wave], ag, au);
   l.red[wave][0][lane] = ag;
   l.red[wave][1][lane] = au;
-  g1_epilogue(l.red, pair, tile, cs.I, act);
+  g1_epilogue<COH>(l.red, pair, tile, cs.I, act);
 }
 
 __device__ __forceinline__ float pair_weight(const CallShape& cs, const float* __restrict__ tw,
@@ -447,6 +457,7 @@ __device__ __forceinline__ float pair_weight(const CallShape& cs, const float* _
   return pair < 0 ? 0.f : pair < cs.T * cs.k ? tw[pair] : 1.0f;
 }
 
+template <int TM>
 __device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act, const ExpertW& W,
                                              const CallShape& cs, int slot, int pair, int group,
                                              const float* __restrict__ topk_w,
@@ -462,14 +473,14 @@ __device__ __forceinline__ void g2_item_bf16(const uint16_t* __restrict__ act, c
     const G2Src src = g2_src<2>(W, cs, slot, tile2);
     const uint16_t* a0 = (const uint16_t*)src.a0;
     const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
-    stream_bf16<kTokPlain, kG2D>(a0, a0 + 16 * src.ld, src.ld, ar, c0, c1 - c0, l.stage[wave],
-                                 a, b);
+    stream_bf16<TM, kG2D>(a0, a0 + 16 * src.ld, src.ld, ar, c0, c1 - c0, l.stage[wave], a, b);
   }
   l.red[wave][0][lane] = a;
   l.red[wave][1][lane] = b;
   g2_epilogue<R>(l.red, pair, tile2, n_tiles, cs.H, pair_weight(cs, topk_w, pair), partial);
 }
 
+template <bool COH>
 __device__ __forceinline__ void g1_item_fp8(const uint16_t* __restrict__ x, const ExpertW& W,
                                             const CallShape& cs, int slot, int pair, int tile,
                                             uint16_t* __restrict__ act, ItemLds& l) {
@@ -480,13 +491,14 @@ __device__ __forceinline__ void g1_item_fp8(const uint16_t* __restrict__ x, cons
   const G1Src src = g1_src<1>(W, cs, slot, tile);
   const uint16_t* xr = x + (size_t)(pair >= 0 ? pair_token(cs, pair) : 0) * H;
   f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
-  stream_fp8<kF8D>(src.gate, src.up, H, src.sg, src.su, xr, c0, c1 - c0, l.stage[wave],
-                          ag, au);
+  stream_fp8<kTokPlain, kF8D>(src.gate, src.up, H, src.sg, src.su, xr, c0, c1 - c0,
+                              l.stage[wave], ag, au);
   l.red[wave][0][lane] = ag;
   l.red[wave][1][lane] = au;
-  g1_epilogue(l.red, pair, tile, cs.I, act);
+  g1_epilogue<COH>(l.red, pair, tile, cs.I, act);
 }
 
+template <int TM>
 __device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act, const ExpertW& W,
                                             const CallShape& cs, int slot, int pair, int group,
                                             const float* __restrict__ topk_w,
@@ -501,8 +513,8 @@ __device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act, co
     const int c0 = kp * nkb / K, c1 = (kp + 1) * nkb / K;
     const G2Src src = g2_src<1>(W, cs, slot, tile2);
     const uint16_t* ar = act + (size_t)(pair >= 0 ? pair : 0) * I;
-    stream_fp8<kF8D>(src.a0, src.a0 + 16 * src.ld, src.ld, src.sr, src.sr, ar, c0, c1 - c0,
-                     l.stage[wave], a, b);
+    stream_fp8<TM, kF8D>(src.a0, src.a0 + 16 * src.ld, src.ld, src.sr, src.sr, ar, c0, c1 - c0,
+                         l.stage[wave], a, b);
   }
   l.red[wave][0][lane] = a;
   l.red[wave][1][lane] = b;
@@ -512,23 +524,23 @@ __device__ __forceinline__ void g2_item_fp8(const uint16_t* __restrict__ act, co
 // ---------------------------------------------------------------------------
 // Staged kernels: grid-stride loops over a plan in global memory.
 // ---------------------------------------------------------------------------
-template <bool FP8>
+template <bool FP8, bool COH = false>
 __device__ __forceinline__ void run_g1(const uint16_t* x, const ExpertW& W, const CallShape& cs,
                                        int slot, int pair, int tile, uint16_t* act, ItemLds& l) {
   if (FP8)
-    g1_item_fp8(x, W, cs, slot, pair, tile, act, l);
+    g1_item_fp8<COH>(x, W, cs, slot, pair, tile, act, l);
   else
-    g1_item_bf16(x, W, cs, slot, pair, tile, act, l);
+    g1_item_bf16<COH>(x, W, cs, slot, pair, tile, act, l);
 }
 
-template <bool FP8>
+template <bool FP8, int TM = kTokPlain>
 __device__ __forceinline__ void run_g2(const uint16_t* act, const ExpertW& W, const CallShape& cs,
                                        int slot, int pair, int group, const float* tw,
                                        float* partial, ItemLds& l) {
   if (FP8)
-    g2_item_fp8(act, W, cs, slot, pair, group, tw, partial, l);
+    g2_item_fp8<TM>(act, W, cs, slot, pair, group, tw, partial, l);
   else
-    g2_item_bf16(act, W, cs, slot, pair, group, tw, partial, l);
+    g2_item_bf16<TM>(act, W, cs, slot, pair, group, tw, partial, l);
 }
 
 // The blocks of a call: the plan's routed blocks, then the shared experts'
@@ -570,20 +582,39 @@ __device__ __forceinline__ void block_at(const int32_t* __restrict__ plan, const
   }
 }
 
+// The plan's first routed blocks whose slots are not pending (plan[2],
+// clamped to the routed blocks; any value gives the same product, only the
+// order of the work changes).
+__device__ __forceinline__ int resident_blocks(const int32_t* __restrict__ plan,
+                                               const CallShape& cs) {
+  return min(max(plan[2], 0), routed_blocks(plan, cs));
+}
+
+// gemm1 over the call's blocks.  With a hand-off area (the split launch
+// below follows) it covers only the resident routed blocks and the shared
+// ones, and workgroup 0 clears the area: [ticket counter | per pending
+// block: gemm1 items done].
 template <bool FP8>
 __global__ __launch_bounds__(kThreads) void moe_gemm1_kernel(const uint16_t* __restrict__ x,
                                                              ExpertW W,
                                                              const int32_t* __restrict__ plan,
                                                              CallShape cs,
-                                                             uint16_t* __restrict__ act) {
+                                                             uint16_t* __restrict__ act,
+                                                             int32_t* __restrict__ handoff) {
   __shared__ ItemLds lds;
   const int n_tiles = cs.I / 16;
-  const int total = call_blocks(plan, W, cs) * n_tiles;
+  const int nr = routed_blocks(plan, cs);
+  const int n_res = handoff != nullptr ? resident_blocks(plan, cs) : nr;
+  const int n_skip = nr - n_res;  // routed blocks [n_res, nr) are left to the split launch
+  if (handoff != nullptr && blockIdx.x == 0)
+    for (int i = threadIdx.x; i <= cs.T * cs.k; i += kThreads)
+      __hip_atomic_store(handoff + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int total = (call_blocks(plan, W, cs) - n_skip) * n_tiles;
   const int col = threadIdx.x & 15;
   for (int item = blockIdx.x; item < total; item += gridDim.x) {
-    const int b = item / n_tiles, tile = item - b * n_tiles;
+    const int bb = item / n_tiles, tile = item - bb * n_tiles;
     int slot_field, pair;
-    block_at(plan, W, cs, b, col, slot_field, pair);
+    block_at(plan, W, cs, bb < n_res ? bb : bb + n_skip, col, slot_field, pair);
     await_slot(W.wait, slot_field);
     run_g1<FP8>(x, W, cs, slot_field & kSlotMask, pair, tile, act, lds);
   }
@@ -612,6 +643,83 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_kernel(const uint16_t* __r
     block_at(plan, W, cs, b, col, slot_field, pair);
     await_slot(W.wait, slot_field);
     run_g2<FP8>(act, W, cs, slot_field & kSlotMask, pair, g, topk_w, partial, lds);
+  }
+}
+
+// Bounded wait (thread 0) until *count reaches `want`; a bound reached is
+// recorded as a timeout in the status word (when there is one).
+__device__ __forceinline__ void wait_count(const int32_t* count, int want, long long ticks,
+                                           int32_t* status) {
+  const long long t0 = wall_clock64();
+  while (__hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < want) {
+    if (wall_clock64() - t0 > ticks) {
+      if (status != nullptr)
+        __hip_atomic_store(status, SLUICE_E_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(4);
+  }
+}
+
+// The second launch of a product whose plan may hold pending blocks, one work
+// item per workgroup, so that gemm2 of the resident experts runs while the
+// pending slots' rows still stream in (with the single gemm2 launch it waited
+// for gemm1 of the last pending expert).  Items:
+//   [gemm2 of the resident and shared blocks | gemm1 of the pending blocks |
+//    gemm2 of the pending blocks];
+// a pending gemm1 item stores its act tile device-coherent and counts itself
+// in its block's hand-off counter; a pending gemm2 item waits for its slot,
+// then (bounded) for its block's count to reach the gemm1 tile count, and
+// reads act coherently.
+// The pending items take their order from a ticket counter, not from
+// blockIdx: a workgroup holding a gemm2 ticket waits only on gemm1 tickets
+// already taken, i.e. on running workgroups that wait for nothing but the
+// host's ready marks, so the waits end whatever order the hardware
+// dispatches workgroups in.  The grid must cover every item (the host sizes
+// it for the largest plan of the call); workgroups beyond the items exit.
+template <bool FP8>
+__global__ __launch_bounds__(kThreads) void moe_gemm2_split_kernel(
+    const uint16_t* __restrict__ x, uint16_t* __restrict__ act, ExpertW W,
+    const int32_t* __restrict__ plan, const float* __restrict__ topk_w, CallShape cs,
+    float* __restrict__ partial, int32_t* __restrict__ handoff, long long spin_ticks) {
+  __shared__ ItemLds lds;
+  __shared__ int s_ticket;
+  const int n_groups = g2_groups(cs.H, FP8), n_tiles = cs.I / 16;
+  const int nr = routed_blocks(plan, cs), n_res = resident_blocks(plan, cs);
+  const int n_pend = nr - n_res;
+  const int n_first = (call_blocks(plan, W, cs) - n_pend) * n_groups;
+  const int n_g1 = n_pend * n_tiles, n_g2 = n_pend * n_groups;
+  const int col = threadIdx.x & 15;
+  const int item = blockIdx.x;
+  int slot_field, pair;
+  if (item < n_first) {
+    const int bb = item / n_groups, g = item - bb * n_groups;
+    block_at(plan, W, cs, bb < n_res ? bb : bb + n_pend, col, slot_field, pair);
+    await_slot(W.wait, slot_field);
+    run_g2<FP8>(act, W, cs, slot_field & kSlotMask, pair, g, topk_w, partial, lds);
+    return;
+  }
+  if (item >= n_first + n_g1 + n_g2) return;
+  if (threadIdx.x == 0) s_ticket = atomicAdd(handoff, 1);
+  __syncthreads();
+  const int t = s_ticket;
+  int32_t* done = handoff + 1;
+  if (t < n_g1) {
+    const int pb = t / n_tiles, tile = t - pb * n_tiles;
+    block_at(plan, W, cs, n_res + pb, col, slot_field, pair);
+    await_slot(W.wait, slot_field);
+    run_g1<FP8, true>(x, W, cs, slot_field & kSlotMask, pair, tile, act, lds);
+    if (threadIdx.x == 0) atomicAdd(done + pb, 1);
+  } else if (t < n_g1 + n_g2) {
+    // First the slot (a gentle wait, like the gemm1 items'), then the few
+    // microseconds of its gemm1 items (a tight one): a tight wait over the
+    // whole stream-in would poll one word as hard as the copies write.
+    const int pb = (t - n_g1) / n_groups, g = (t - n_g1) - pb * n_groups;
+    block_at(plan, W, cs, n_res + pb, col, slot_field, pair);
+    await_slot(W.wait, slot_field);
+    if (threadIdx.x == 0) wait_count(done + pb, n_tiles, spin_ticks, W.wait.status);
+    __syncthreads();
+    run_g2<FP8, kTokCoh>(act, W, cs, slot_field & kSlotMask, pair, g, topk_w, partial, lds);
   }
 }
 
@@ -677,27 +785,31 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 struct Workspace {
   int32_t* plan;
+  int32_t* handoff;
   uint16_t* act;
   float* partial;
 };
 
-// [plan of the T*k routed pairs | act [P2, I] bf16 | partial [P2, H] fp32],
-// P2 = T*k routed + n_sh*T shared pairs.  Every call writes what it reads
-// (align writes the whole plan, gemm1 the act rows of the planned pairs,
-// gemm2 their partials; the combine adds only valid pairs), so the workspace
-// needs no clearing and holds nothing between calls.
+// [plan of the T*k routed pairs | hand-off counters (1 + T*k) | act [P2, I]
+// bf16 | partial [P2, H] fp32], P2 = T*k routed + n_sh*T shared pairs.  Every
+// call writes what it reads (align writes the whole plan, gemm1 clears the
+// counters the split launch uses and writes the act rows of the planned
+// pairs, gemm2 their partials; the combine adds only valid pairs), so the
+// workspace needs no clearing and holds nothing between calls.
 size_t workspace_bytes(int T, int H, int I, int k, int n_sh, Workspace* ws, void* base) {
   const int P2 = T * k + n_sh * T;
   const size_t plan_b = align_up(plan_ints(T * k) * sizeof(int32_t), 256);
+  const size_t hand_b = align_up((size_t)(1 + T * k) * sizeof(int32_t), 256);
   const size_t act_b = align_up((size_t)P2 * I * sizeof(uint16_t), 256);
   const size_t part_b = align_up((size_t)P2 * H * sizeof(float), 256);
   if (ws != nullptr) {
     char* b = (char*)base;
     ws->plan = (int32_t*)b;
-    ws->act = (uint16_t*)(b + plan_b);
-    ws->partial = (float*)(b + plan_b + act_b);
+    ws->handoff = (int32_t*)(b + plan_b);
+    ws->act = (uint16_t*)(b + plan_b + hand_b);
+    ws->partial = (float*)(b + plan_b + hand_b + act_b);
   }
-  return plan_b + act_b + part_b;
+  return plan_b + hand_b + act_b + part_b;
 }
 
 #ifndef SLUICE_GRID_CAP
@@ -707,6 +819,24 @@ int grid_for(int P, int n_tiles) {
   const long items = (long)P * n_tiles;  // upper bound on (block, tile) items
   const long cap = SLUICE_GRID_CAP;
   return (int)(items < cap ? (items > 0 ? items : 1) : cap);
+}
+
+// Grid of the split launch: one workgroup per item of the largest plan of
+// the call (every routed block pending costs a gemm1 and a gemm2 item per
+// block, P >= routed blocks, P2 >= all blocks), or 0 when that exceeds
+// kSplitGridMax (prefill-sized calls keep the two grid-stride launches).
+constexpr long kSplitGridMax = 1L << 15;
+long split_grid_for(int P, int P2, int I, int n_groups) {
+  const long g = (long)P2 * n_groups + (long)P * (I / 16);
+  return g <= kSplitGridMax ? g : 0;
+}
+
+// Bound of a split-launch wait for a pending block's gemm1 items: they wait
+// for the block's slot (bounded by the slot wait's own bound) and then
+// compute, so twice that bound, or 20 s at the 100 MHz wall clock when the
+// call has none.
+long long split_spin_ticks(const SlotWait& w) {
+  return w.timeout_ticks > 0 ? 2 * w.timeout_ticks : 2000000000LL;
 }
 
 // The align kernel stages the map of all E experts in LDS.
@@ -757,12 +887,26 @@ int run_experts(const void* x, const ExpertW& W, const float* tw, const int32_t*
     SLUICE_HIP_CHECK(hipGetLastError());
     plan = w.plan;
   }
-  hipLaunchKernelGGL((moe_gemm1_kernel<FP8>), dim3(grid_for(P2, I / 16)), dim3(kThreads), 0, st,
-                     (const uint16_t*)x, Ww, plan, cs, w.act);
-  SLUICE_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL((moe_gemm2_kernel<FP8>), dim3(grid_for(P2, g2_groups(H, FP8))),
-                     dim3(kThreads), 0, st, w.act, Ww, plan, tw, cs, w.partial);
-  SLUICE_HIP_CHECK(hipGetLastError());
+  const long split_grid = split_grid_for(P, P2, I, g2_groups(H, FP8));
+  if (Ww.wait.pending != nullptr && split_grid > 0) {
+    // Slots of this map may stream: gemm1 of the resident blocks, then the
+    // split launch (gemm2 of the resident blocks while the pending ones
+    // stream, their gemm1 and gemm2 as their rows land).
+    hipLaunchKernelGGL((moe_gemm1_kernel<FP8>), dim3(grid_for(P2, I / 16)), dim3(kThreads), 0, st,
+                       (const uint16_t*)x, Ww, plan, cs, w.act, w.handoff);
+    SLUICE_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL((moe_gemm2_split_kernel<FP8>), dim3((unsigned)split_grid), dim3(kThreads),
+                       0, st, (const uint16_t*)x, w.act, Ww, plan, tw, cs, w.partial, w.handoff,
+                       split_spin_ticks(Ww.wait));
+    SLUICE_HIP_CHECK(hipGetLastError());
+  } else {
+    hipLaunchKernelGGL((moe_gemm1_kernel<FP8>), dim3(grid_for(P2, I / 16)), dim3(kThreads), 0,
+                       st, (const uint16_t*)x, Ww, plan, cs, w.act, (int32_t*)nullptr);
+    SLUICE_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL((moe_gemm2_kernel<FP8>), dim3(grid_for(P2, g2_groups(H, FP8))),
+                       dim3(kThreads), 0, st, w.act, Ww, plan, tw, cs, w.partial);
+    SLUICE_HIP_CHECK(hipGetLastError());
+  }
   return launch_combine(w.partial, plan + kPlanHeader + (size_t)kBlockInts * P, T, k, n_sh, H,
                         scale, shared, out, st);
 }
@@ -910,7 +1054,7 @@ extern "C" int sluice_moe_gemm1_bf16(const void* x, const void* w13, const int32
   const ExpertW W = routed_only((const uint8_t*)w13, nullptr, nullptr, nullptr);
   hipLaunchKernelGGL(moe_gemm1_kernel<false>, dim3(grid_for(T * k, I / 16)), dim3(kThreads), 0,
                      (hipStream_t)stream, (const uint16_t*)x, W, plan, CallShape{T, k, H, I},
-                     (uint16_t*)act);
+                     (uint16_t*)act, (int32_t*)nullptr);
   return (int)hipGetLastError();
 }
 
@@ -936,7 +1080,7 @@ extern "C" int sluice_moe_gemm1_fp8(const void* x, const void* w13, const float*
   const ExpertW W = routed_only((const uint8_t*)w13, nullptr, w13_scale, nullptr);
   hipLaunchKernelGGL(moe_gemm1_kernel<true>, dim3(grid_for(T * k, I / 16)), dim3(kThreads), 0,
                      (hipStream_t)stream, (const uint16_t*)x, W, plan, CallShape{T, k, H, I},
-                     (uint16_t*)act);
+                     (uint16_t*)act, (int32_t*)nullptr);
   return (int)hipGetLastError();
 }
 

@@ -6,9 +6,11 @@
 // the ids and map it leaves behind (one launch fewer per layer); both run
 // plan_build in one workgroup of kPlanThreads threads.
 //
-// Layout (int32): [n_blocks, P, 0, 0 | P block records {slot field, count,
-// pair[16]} | P validity flags (1 = the pair's expert is resident)].  A slot
-// field carries kPendingBit when the slot's rows may still be streaming in.
+// Layout (int32): [n_blocks, P, n_resident, 0 | P block records {slot
+// field, count, pair[16]} | P validity flags (1 = the pair's expert is
+// resident)]; the first n_resident blocks are those of slots not pending.
+// A slot field carries kPendingBit when the slot's rows may still be
+// streaming in.
 // The shared experts' blocks are not in the plan: the kernels derive them.
 #pragma once
 
@@ -172,7 +174,7 @@ __device__ inline int plan_build_staged(int id0, const int32_t* __restrict__ ids
   if (tid == 0) {
     plan[0] = nb;
     plan[1] = P;
-    plan[2] = 0;
+    plan[2] = tot[0];
     plan[3] = 0;
   }
   return nb;

@@ -138,6 +138,12 @@ def test_gap_built_plan_gives_the_product_it_plans_itself(kind):
         want = ops.fused_experts(h, layer.w13_weight, layer.w2_weight, tw, ti, **kw)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), step
+        # a copy of the map has no slots streaming: the single gemm2 launch
+        # (the rows have landed: the product above waited for them)
+        one = ops.fused_experts(h, layer.w13_weight, layer.w2_weight, tw, ti,
+                                **dict(kw, expert_map=cache.expert_map_buf.clone()))
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), one.view(torch.int16)), step
         if sh is not None:
             kw.update(shared_w1=sh.gate_up, shared_w2=sh.down)
             got = ops.fused_experts(h, layer.w13_weight, layer.w2_weight, tw, ti, plan=plan, **kw)
@@ -151,4 +157,44 @@ def test_gap_built_plan_gives_the_product_it_plans_itself(kind):
         with pytest.raises(ValueError):
             ops.fused_experts(x, layer.w13_weight, layer.w2_weight, tw, ti, plan=bad,
                               global_num_experts=E, expert_map=cache.expert_map_buf)
+    off.close()
+
+
+def test_fp8_split_launch_equals_single_gemm2_launch():
+    """DeepSeek-V3-routed fp8 layer (shared expert folded in): after each
+    gap op, the product over the layer's map -- gemm2 of the resident
+    experts while the missed ones stream, their gemm1 and gemm2 handed over
+    inside one launch -- equals, bit for bit, the product over a copy of the
+    map, which has no streaming slots and runs one gemm2 launch after gemm1."""
+    from sluice_amd.decoder import SPECS, _expert_store, _StoreMoELayer, build_offloaded
+
+    sp = dict(SPECS["v3"], H=512, I=256, shared_I=256)
+    store = _expert_store(sp, 7003, DEV, True)
+    layer = _StoreMoELayer(sp, store, 1, DEV, None, "layers.1.mlp")
+    off = build_offloaded([layer], slots=64, device=DEV)
+    cache = off._caches[id(layer)]
+    rng = np.random.default_rng(23)
+    pending_blocks = 0
+    for step in range(5):
+        print(f"fp8 split step {step}", flush=True)
+        x = torch.from_numpy(rng.standard_normal((8, 512)).astype(np.float32)).to(
+            torch.bfloat16).to(DEV)
+        tw, ti = layer.select(layer.logits(x))
+        h = torch.ops.vllm.sluice_stream_gap(x, ti, 0)
+        plan = off.gap_plan(0, ti.numel())
+        assert plan is not None
+        got = layer.experts(h, tw, ti, fold_shared=True, plan=plan)
+        torch.cuda.synchronize()
+        head = plan[:3].cpu().tolist()
+        pending_blocks += head[0] - head[2]
+        emap = layer._buffers["_expert_map"]
+        layer._buffers["_expert_map"] = emap.clone()
+        try:
+            one = layer.experts(h, tw, ti, fold_shared=True)
+        finally:
+            layer._buffers["_expert_map"] = emap
+        torch.cuda.synchronize()
+        assert not torch.isnan(one.float()).any()
+        assert torch.equal(got.view(torch.int16), one.view(torch.int16)), step
+    assert pending_blocks > 0
     off.close()

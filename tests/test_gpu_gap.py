@@ -78,6 +78,10 @@ def _check_plan(cache, ids, k, E):
     got, want = cache.plan.cpu().numpy(), ref.cpu().numpy()
     nb = int(want[0])
     assert int(got[0]) == nb and int(got[1]) == P
+    # plan[2]: the blocks of slots not pending, which come first
+    pend = [bool(int(want[4 + 18 * b]) & (1 << 30)) for b in range(nb)]
+    assert int(got[2]) == int(want[2]) == pend.count(False)
+    assert not any(pend[:pend.count(False)])
     for b in range(nb):
         g, w = got[4 + 18 * b: 4 + 18 * (b + 1)], want[4 + 18 * b: 4 + 18 * (b + 1)]
         assert g[0] == w[0] and g[1] == w[1], b

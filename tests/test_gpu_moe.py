@@ -57,6 +57,7 @@ def test_align_plan_bit_exact(T, k, E, S, seed):
     print(f"align T={T} k={k} E={E} S={S}", flush=True)
     blocks, valid = om.align_blocks(ids, emap, S, 16)
     assert p[0] == len(blocks)
+    assert p[2] == len(blocks)  # no slot of this map streams: every block is resident
     if T == 0:
         return
     P = T * k
