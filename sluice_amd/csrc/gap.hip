@@ -21,9 +21,11 @@
 //
 //   serve (host): consumes each posted record in stamp order and runs the
 //     reference's bookkeeping exactly (slru::Cache::gap: fast-hit, touches,
-//     claimed set, victims, overflow).  For a waiting device it issues the
-//     misses' row copies as hipMemcpyAsync on a dedicated copy stream, waits
-//     for them, then answers with the standing slot table.  It runs inline
+//     claimed set, victims, overflow).  For a waiting device it answers with
+//     the standing slot table and the slots being filled, issues the misses'
+//     row copies as hipMemcpyAsync on the dedicated copy streams, and marks
+//     each filled slot ready once its rows landed (the expert product waits
+//     per slot).  It runs inline
 //     (sluice_layer_gap: launch + serve, the reference's eager op) or on a
 //     native server thread (sluice_gap_server_*), which makes the gap op
 //     capturable, so a whole decode step replays as one hipGraph.
@@ -31,8 +33,9 @@
 // Ordering: a gap kernel runs only after all earlier work on its stream has
 // completed, so when the host sees its record no kernel of that stream can
 // still read a slot about to be overwritten (what the reference fences with
-// an event from the compute stream, 2443-2447); the device waits for the
-// host's answer, which is sent after the copies completed (2464).
+// an event from the compute stream, 2443-2447); where the reference makes
+// the compute stream wait for the copies (2464), the expert product waits
+// for each filled slot's ready mark.
 //
 // Every device wait is bounded (SLUICE_GAP_TIMEOUT_S, default 20 s, measured
 // on the constant-rate wall clock) and also ends when the host raises the
@@ -43,6 +46,7 @@
 #include <string.h>
 #include <time.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <mutex>
@@ -453,11 +457,23 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Per-device resources: one copy stream (default priority, non-blocking) and
-// the wall-clock rate; one process-wide abort flag in pinned memory.
+// Per-device resources: the copy lanes (default priority, non-blocking
+// streams) and the wall-clock rate; one process-wide abort flag in pinned
+// memory.
+//
+// Expert rows go over kLanes copy streams, each per-expert param on the lane
+// its layer assigned it (the lanes' row bytes balanced).  Every
+// hipMemcpyAsync leaves the copy engine idle for ~9 us between copies on one
+// stream (measured on MI355X, also through HSA's own async copy), and a bf16
+// expert is two copies (w13 and w2 rows), an fp8 expert four: on one stream
+// 326.9 us per 17.3 MB expert (52.9 GB/s), 1306 us for four; with w13 and w2
+// on two streams the engines' gaps overlap the other lane's transfer, 318.4
+// and 1237 us (55.95 GB/s, against 56.3 GB/s for 64 MiB copies).
 // ---------------------------------------------------------------------------
+constexpr int kLanes = 2;
+
 struct DeviceRes {
-  hipStream_t copy = nullptr;
+  hipStream_t copy[kLanes] = {};
   long long clock_khz = 0;
 };
 constexpr int kMaxDevices = 64;
@@ -470,10 +486,11 @@ int device_res(int dev, DeviceRes** out) {
   if (dev < 0 || dev >= kMaxDevices) return SLUICE_E_INVAL;
   std::lock_guard<std::mutex> lk(g_dev_mu);
   DeviceRes& r = g_dev[dev];
-  if (r.copy == nullptr) {
+  if (r.copy[kLanes - 1] == nullptr) {
     int khz = 0;
     SLUICE_HIP_CHECK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
-    SLUICE_HIP_CHECK(hipStreamCreateWithFlags(&r.copy, hipStreamNonBlocking));
+    for (hipStream_t& s : r.copy)
+      if (s == nullptr) SLUICE_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
     r.clock_khz = khz > 0 ? khz : 100000;
   }
   if (g_abort_host == nullptr) {
@@ -519,6 +536,7 @@ struct ParamRows {
   char* slot_base;
   const char* host_base;
   size_t row_bytes;
+  int lane;  // copy lane of this param's rows
 };
 
 struct sluice_gap_server;
@@ -548,7 +566,9 @@ struct sluice_layer {
   int32_t* ids_host = nullptr;  // pinned staging of the step's ids
   size_t ids_cap = 0;
   int64_t classic_steps = 0, classic_waves = 0;
-  std::vector<hipEvent_t> fill_ev;  // one per group of experts a gap streams
+  // per group of experts a gap streams, one per lane: [kLanes * g + lane]
+  std::vector<hipEvent_t> fill_ev;
+  unsigned lane_mask = 0;  // lanes that carry some param's rows
 };
 
 namespace {
@@ -721,7 +741,7 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     const bool early = waits && grc == 0 && rc == SLUICE_OK;
     const int per_event = experts_per_event(L, n_streams);
     const int n_events = (n_streams + per_event - 1) / per_event;
-    while (rc == SLUICE_OK && (int)L->fill_ev.size() < n_events) {
+    while (rc == SLUICE_OK && (int)L->fill_ev.size() < kLanes * n_events) {
       hipEvent_t ev = nullptr;
       const hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
       if (e != hipSuccess) rc = (int)e;
@@ -737,7 +757,7 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
       for (const ParamRows& p : L->params) {
         hipError_t e = hipMemcpyAsync(p.slot_base + (size_t)slot * p.row_bytes,
                                       p.host_base + (size_t)local * p.row_bytes, p.row_bytes,
-                                      hipMemcpyHostToDevice, R->copy);
+                                      hipMemcpyHostToDevice, R->copy[p.lane]);
         if (e != hipSuccess) {
           rc = (int)e;
           break;
@@ -745,9 +765,12 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
         L->bytes += (int64_t)p.row_bytes;
       }
       if (rc == SLUICE_OK && ((i + 1) % per_event == 0 || i + 1 == n_streams)) {
-        const hipError_t e = hipEventRecord(L->fill_ev[issued], R->copy);
-        if (e != hipSuccess) rc = (int)e;
-        else ++issued;
+        for (int l = 0; l < kLanes && rc == SLUICE_OK; ++l) {
+          if ((L->lane_mask >> l & 1u) == 0) continue;
+          const hipError_t e = hipEventRecord(L->fill_ev[kLanes * issued + l], R->copy[l]);
+          if (e != hipSuccess) rc = (int)e;
+        }
+        if (rc == SLUICE_OK) ++issued;
       }
       if (!answered && rc == SLUICE_OK) {
         respond(L, want, SLUICE_OK, n_streams);
@@ -760,7 +783,9 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     // Each group of experts landed: mark its slots ready for this gap.
     int marked = 0;  // streams whose slots are marked
     for (int g = 0; g < issued; ++g) {
-      const int w = wait_event(L->fill_ev[g]);
+      int w = SLUICE_OK;
+      for (int l = 0; l < kLanes && w == SLUICE_OK; ++l)
+        if (L->lane_mask >> l & 1u) w = wait_event(L->fill_ev[kLanes * g + l]);
       if (w != SLUICE_OK) {
         if (rc == SLUICE_OK) rc = w;
         break;
@@ -892,7 +917,24 @@ extern "C" int sluice_layer_add_param(sluice_layer* L, void* slot_base_dev, cons
   if (L == nullptr || slot_base_dev == nullptr || host_base == nullptr || row_bytes == 0)
     return SLUICE_E_INVAL;
   std::lock_guard<std::mutex> lk(L->mu);
-  L->params.push_back({(char*)slot_base_dev, (const char*)host_base, row_bytes});
+  L->params.push_back({(char*)slot_base_dev, (const char*)host_base, row_bytes, 0});
+  // Lanes: largest rows first, each to the lane with the fewest bytes so
+  // far (bf16: w13 | w2; fp8: w13 | w2 + both scale rows).
+  std::vector<int> order(L->params.size());
+  for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+    return L->params[a].row_bytes > L->params[b].row_bytes;
+  });
+  size_t load[kLanes] = {};
+  L->lane_mask = 0;
+  for (int i : order) {
+    int best = 0;
+    for (int l = 1; l < kLanes; ++l)
+      if (load[l] < load[best]) best = l;
+    L->params[i].lane = best;
+    load[best] += L->params[i].row_bytes;
+    L->lane_mask |= 1u << best;
+  }
   return SLUICE_OK;
 }
 
@@ -1076,7 +1118,8 @@ constexpr int kClassicMaxIds = 1 << 24;
 
 int ensure_events(sluice_layer* L, size_t n) {
   for (std::vector<hipEvent_t>* v : {&L->wave_ev, &L->copy_ev}) {
-    while (v->size() < n) {
+    // copy_ev: one per wave and lane, [kLanes * w + lane]
+    while (v->size() < (v == &L->copy_ev ? kLanes * n : n)) {
       hipEvent_t ev = nullptr;
       SLUICE_HIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
       v->push_back(ev);
@@ -1087,8 +1130,29 @@ int ensure_events(sluice_layer* L, size_t n) {
   return SLUICE_OK;
 }
 
-// Row copies of wave w on the copy stream (after whatever it waits on).
-int issue_wave_copies(sluice_layer* L, int w, hipStream_t copy) {
+// Every used copy lane waits for `ev`.
+int lanes_wait(const sluice_layer* L, DeviceRes* R, hipEvent_t ev) {
+  for (int l = 0; l < kLanes; ++l)
+    if (L->lane_mask >> l & 1u) SLUICE_HIP_CHECK(hipStreamWaitEvent(R->copy[l], ev, 0));
+  return SLUICE_OK;
+}
+
+// Record evs[lane] on every used copy lane.
+int lanes_record(const sluice_layer* L, DeviceRes* R, hipEvent_t* evs) {
+  for (int l = 0; l < kLanes; ++l)
+    if (L->lane_mask >> l & 1u) SLUICE_HIP_CHECK(hipEventRecord(evs[l], R->copy[l]));
+  return SLUICE_OK;
+}
+
+// `st` waits for evs[lane] of every used copy lane.
+int wait_lanes(const sluice_layer* L, hipStream_t st, hipEvent_t* evs) {
+  for (int l = 0; l < kLanes; ++l)
+    if (L->lane_mask >> l & 1u) SLUICE_HIP_CHECK(hipStreamWaitEvent(st, evs[l], 0));
+  return SLUICE_OK;
+}
+
+// Row copies of wave w on the copy lanes (after whatever they wait on).
+int issue_wave_copies(sluice_layer* L, int w, DeviceRes* R) {
   std::lock_guard<std::mutex> lk(L->mu);
   const slru::Wave& W = L->plan.waves[w];
   for (int i = 0; i < W.ns; ++i) {
@@ -1097,7 +1161,7 @@ int issue_wave_copies(sluice_layer* L, int w, hipStream_t copy) {
     for (const ParamRows& p : L->params) {
       SLUICE_HIP_CHECK(hipMemcpyAsync(p.slot_base + (size_t)slot * p.row_bytes,
                                       p.host_base + (size_t)local * p.row_bytes, p.row_bytes,
-                                      hipMemcpyHostToDevice, copy));
+                                      hipMemcpyHostToDevice, R->copy[p.lane]));
       L->bytes += (int64_t)p.row_bytes;
     }
   }
@@ -1115,13 +1179,17 @@ int classic_flush(sluice_layer* L, hipStream_t st) {
     rc = ensure_events(L, (size_t)nW);
     if (rc) return rc;
     SLUICE_HIP_CHECK(hipEventRecord(L->pre_ev, st));
-    SLUICE_HIP_CHECK(hipStreamWaitEvent(R->copy, L->pre_ev, 0));
+    rc = lanes_wait(L, R, L->pre_ev);
+    if (rc) return rc;
     for (int w = L->plan_copied; w < nW; ++w) {
-      rc = issue_wave_copies(L, w, R->copy);
+      rc = issue_wave_copies(L, w, R);
       if (rc) return rc;
     }
-    SLUICE_HIP_CHECK(hipEventRecord(L->pre_ev, R->copy));
-    SLUICE_HIP_CHECK(hipStreamWaitEvent(st, L->pre_ev, 0));
+    hipEvent_t* evs = &L->copy_ev[kLanes * (nW - 1)];
+    rc = lanes_record(L, R, evs);
+    if (rc) return rc;
+    rc = wait_lanes(L, st, evs);
+    if (rc) return rc;
   }
   L->plan.clear();
   L->plan_next = L->plan_copied = 0;
@@ -1230,10 +1298,12 @@ extern "C" int sluice_layer_classic_wave(sluice_layer* L, int wave, sluice_strea
     if (W.ns > 0) {
       // fills may overwrite a slot that earlier work on `st` reads
       SLUICE_HIP_CHECK(hipEventRecord(L->pre_ev, st));
-      SLUICE_HIP_CHECK(hipStreamWaitEvent(R->copy, L->pre_ev, 0));
-      rc = issue_wave_copies(L, 0, R->copy);
+      rc = lanes_wait(L, R, L->pre_ev);
       if (rc) return rc;
-      SLUICE_HIP_CHECK(hipEventRecord(L->copy_ev[0], R->copy));
+      rc = issue_wave_copies(L, 0, R);
+      if (rc) return rc;
+      rc = lanes_record(L, R, &L->copy_ev[0]);
+      if (rc) return rc;
     }
     L->plan_copied = 1;
   }
@@ -1244,7 +1314,10 @@ extern "C" int sluice_layer_classic_wave(sluice_layer* L, int wave, sluice_strea
   hipLaunchKernelGGL(map_refresh_kernel, dim3(1), dim3(256), 0, st, L->map_dev, L->c.E, tab,
                      L->dev_block + L->c.E + 1);
   SLUICE_HIP_CHECK(hipGetLastError());
-  if (W.ns > 0) SLUICE_HIP_CHECK(hipStreamWaitEvent(st, L->copy_ev[wave], 0));
+  if (W.ns > 0) {
+    rc = wait_lanes(L, st, &L->copy_ev[kLanes * wave]);
+    if (rc) return rc;
+  }
   L->plan_in_wave = true;
   return SLUICE_OK;
 }
@@ -1265,10 +1338,12 @@ extern "C" int sluice_layer_classic_wave_done(sluice_layer* L, int wave, sluice_
     int rc = device_res(L->device, &R);
     if (rc) return rc;
     const int dep = L->plan.pipelined ? (wave > 0 ? wave - 1 : 0) : wave;
-    SLUICE_HIP_CHECK(hipStreamWaitEvent(R->copy, L->wave_ev[dep], 0));
-    rc = issue_wave_copies(L, wave + 1, R->copy);
+    rc = lanes_wait(L, R, L->wave_ev[dep]);
     if (rc) return rc;
-    SLUICE_HIP_CHECK(hipEventRecord(L->copy_ev[wave + 1], R->copy));
+    rc = issue_wave_copies(L, wave + 1, R);
+    if (rc) return rc;
+    rc = lanes_record(L, R, &L->copy_ev[kLanes * (wave + 1)]);
+    if (rc) return rc;
     L->plan_copied = wave + 2;
   }
   return SLUICE_OK;
