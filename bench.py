@@ -119,12 +119,20 @@ def run_batch(dec, c, steps, warmup, prefill=True, label=None):
     before = dec.gap_counters()
     cl0 = dec.off.classic_counters()
     pos0 = int(dec.state[c].pos[0]) if dec.has_attn else None
+    # per-step times from events between the steps (the value is the
+    # wall-clock total); they show whether a slow window is one stall or
+    # every step
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    stream = torch.cuda.current_stream()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
+    for i in range(steps):
+        marks[i].record(stream)
         dec.step_graphs(c)
+    marks[steps].record(stream)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    per_step = sorted(marks[i].elapsed_time(marks[i + 1]) for i in range(steps))
     dec.sync()
     after = dec.gap_counters()
     delta = {k: after[k] - before[k] for k in after}
@@ -145,6 +153,8 @@ def run_batch(dec, c, steps, warmup, prefill=True, label=None):
         "prefill": {"tokens_per_sequence": dec.prompt_len if prefill else 0,
                     "seconds": prefill_s},
         "timed_positions": [pos0, pos0 + steps] if pos0 is not None else None,
+        "step_ms_min_median_max": [per_step[0], per_step[len(per_step) // 2], per_step[-1]]
+        if per_step else None,
     }
 
 
@@ -419,6 +429,11 @@ def measured_traffic(cfg, c, slots, uniform, algorithmic_bytes, kernel="moe_gemm
 
 
 def h2d_rates(dec):
+    """Pinned host->device rates: one 64 MiB copy (the link's peak), and
+    expert stream-ins issued as the gap issues them -- one copy per
+    per-expert param per missing expert, slot rows <- host rows, each param
+    on its copy lane (two streams; the largest rows first, each to the lane
+    with fewer bytes so far: w13 | w2 for bf16)."""
     import torch
 
     from sluice_amd import _lib, ops
@@ -426,37 +441,53 @@ def h2d_rates(dec):
     lib = _lib.load()
     st = ops.HostStore((64 << 20,), torch.uint8)
     d = torch.empty((64 << 20,), dtype=torch.uint8, device=dec.dev)
-    s = torch.cuda.Stream(device=dec.dev)
+    lanes = [torch.cuda.Stream(device=dec.dev), torch.cuda.Stream(device=dec.dev)]
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
-    def copies(dsts, srcs, sizes, reps):
-        n = len(dsts)
-        D = (ctypes.c_void_p * n)(*dsts)
-        S = (ctypes.c_void_p * n)(*srcs)
-        B = (ctypes.c_size_t * n)(*sizes)
-        _lib.check(lib.sluice_copy_rows(D, S, B, n, s.cuda_stream), "copy")  # warm
-        e0.record(s)
+    def issue(groups):
+        for lane, (D, S, B, n) in zip(lanes, groups):
+            if n:
+                _lib.check(lib.sluice_copy_rows(D, S, B, n, lane.cuda_stream), "copy")
+
+    def copies(dsts, srcs, sizes, lane_of, reps):
+        groups = []
+        for lane in range(len(lanes)):
+            idx = [i for i in range(len(dsts)) if lane_of[i] == lane]
+            n = len(idx)
+            groups.append(((ctypes.c_void_p * n)(*[dsts[i] for i in idx]),
+                           (ctypes.c_void_p * n)(*[srcs[i] for i in idx]),
+                           (ctypes.c_size_t * n)(*[sizes[i] for i in idx]), n))
+        issue(groups)  # warm
+        torch.cuda.synchronize()
+        e0.record(lanes[0])
+        lanes[1].wait_event(e0)
         for _ in range(reps):
-            _lib.check(lib.sluice_copy_rows(D, S, B, n, s.cuda_stream), "copy")
-        e1.record(s)
-        s.synchronize()
+            issue(groups)
+        lanes[0].wait_stream(lanes[1])
+        e1.record(lanes[0])
+        torch.cuda.synchronize()
         return sum(sizes) * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
 
-    peak = copies([d.data_ptr()], [st.data_ptr()], [64 << 20], 8)
-    # expert stream-ins exactly as the gap issues them: one copy per
-    # per-expert param per missing expert, slot rows <- host rows
+    peak = copies([d.data_ptr()], [st.data_ptr()], [64 << 20], [0], 8)
     cache = dec.caches[0]
-    dsts, srcs, sizes = [], [], []
+    row = {name: cache.cpu_store[name][0].nbytes for name in cache.param_names}
+    load, lane_of_param = [0, 0], {}
+    for name in sorted(cache.param_names, key=lambda n: -row[n]):
+        lane = 0 if load[0] <= load[1] else 1
+        lane_of_param[name] = lane
+        load[lane] += row[name]
+    dsts, srcs, sizes, lane_of = [], [], [], []
     for e in range(8):
         slot = e % cache.num_slots
         for name in cache.param_names:
             t_slot, t_host = cache.gpu_cache[name], cache.cpu_store[name]
-            rb = t_host[0].nbytes
+            rb = row[name]
             dsts.append(t_slot.data_ptr() + slot * rb)
             srcs.append(t_host.data_ptr() + e * rb)
             sizes.append(rb)
+            lane_of.append(lane_of_param[name])
     torch.cuda.synchronize()
-    expert = copies(dsts, srcs, sizes, 3)
+    expert = copies(dsts, srcs, sizes, lane_of, 3)
     # put the touched slots back to what the cache says they hold
     for name in cache.param_names:
         for slot, loc in enumerate(cache.expert_in_slot):
@@ -534,7 +565,8 @@ def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, lo
                       label="uniform" if uniform else "zipf")
         log(f"{cfg} s{slots} c={c} ({r['path']}, {r['routing']}): {r['ms_per_step']:.3f} ms/step "
             f"{r['tok_per_s']:.1f} tok/s misses/layer-step={r['misses_per_layer_step']:.3f} "
-            f"fast-hit={r['fast_hit_share']:.2%} H2D {r['h2d_GBs_in_step']:.1f} GB/s")
+            f"fast-hit={r['fast_hit_share']:.2%} H2D {r['h2d_GBs_in_step']:.1f} GB/s "
+            f"steps min/med/max {'/'.join(f'{v:.2f}' for v in r['step_ms_min_median_max'])} ms")
         rows.append(r)
     c_main = max(batches)
     recorded = record_routing(dec, c_main, 8)
