@@ -41,10 +41,6 @@ size_t sluice_dec_linear_workspace(void);
 int sluice_dec_linear(const void* x, const void* w, int T, int N, int K, void* y,
                       void* workspace, sluice_stream_t stream);
 
-/* Gate/up projection with the SwiGLU activation applied to its fp32 sums:
- * w [N, K] holds N/2 gate rows then N/2 up rows; y [T, N/2] =
- * bf16(silu(x . w_gate^T) * (x . w_up^T)).  N % 32 == 0; workspace as for
- * sluice_dec_linear. */
 /* The plain projection left as its K parts: parts [ks, T, N] fp32 (row-major,
  * 16-byte aligned), ks = sluice_dec_linear_split_parts(T, N, K) (>= 1, 0 for
  * a shape it does not take).  bf16(sum of the parts in order) is the
@@ -53,6 +49,11 @@ int sluice_dec_linear(const void* x, const void* w, int T, int N, int K, void* y
 int sluice_dec_linear_split_parts(int T, int N, int K);
 int sluice_dec_linear_split(const void* x, const void* w, int T, int N, int K, float* parts,
                             sluice_stream_t stream);
+
+/* Gate/up projection with the SwiGLU activation applied to its fp32 sums:
+ * w [N, K] holds N/2 gate rows then N/2 up rows; y [T, N/2] =
+ * bf16(silu(x . w_gate^T) * (x . w_up^T)).  N % 32 == 0; workspace as for
+ * sluice_dec_linear. */
 int sluice_dec_linear_glu(const void* x, const void* w, int T, int N, int K, void* y,
                           void* workspace, sluice_stream_t stream);
 
