@@ -584,6 +584,48 @@ __device__ __forceinline__ void block_at(const int32_t* __restrict__ plan, const
   }
 }
 
+// A block record loaded before the plan header is known, so the first item's
+// record and the header come back in one memory round trip (b is clamped
+// into the plan's T*k records: the loads stay inside the plan buffer).
+// Used by gemm1: 1.3-1.9% shorter launches over recorded decode routing
+// (V2-Lite and Qwen3 c=8); gemm2 measured no change with it.
+struct PreBlock {
+  int b, field, count, pair;
+};
+
+__device__ __forceinline__ PreBlock block_pre(const int32_t* __restrict__ plan,
+                                              const CallShape& cs, int b, int col) {
+  const int bc = min(b, max(cs.T * cs.k - 1, 0));
+  const int32_t* blk = plan + kPlanHeader + (size_t)bc * kBlockInts;
+  PreBlock r;
+  r.b = b;
+  r.field = blk[0];
+  r.count = blk[1];
+  r.pair = blk[2 + col];
+  // The empty asm makes the loads (and the header's) issue here, together;
+  // otherwise the compiler sinks them into the item loop, behind the
+  // header's round trip.
+  const int h0 = plan[0], h2 = plan[2];
+  asm volatile("" ::"s"(r.field), "s"(r.count), "v"(r.pair), "s"(h0), "s"(h2));
+  return r;
+}
+
+// block_at, taking block pre.b's record from `pre`.
+__device__ __forceinline__ void block_at_pre(const int32_t* __restrict__ plan, const ExpertW& W,
+                                             const CallShape& cs, int b, int col,
+                                             const PreBlock& pre, int& slot_field, int& pair) {
+  if (b == pre.b && b < routed_blocks(plan, cs)) {
+    slot_field = pre.field;
+    const int p = col < pre.count ? pre.pair : -1;
+    const bool ok = (unsigned)(slot_field & kSlotMask) < (unsigned)W.S &&
+                    (unsigned)p < (unsigned)(cs.T * cs.k);
+    pair = ok ? p : -1;
+    if ((unsigned)(slot_field & kSlotMask) >= (unsigned)W.S) slot_field = 0;
+  } else {
+    block_at(plan, W, cs, b, col, slot_field, pair);
+  }
+}
+
 // The plan's first routed blocks whose slots are not pending (plan[2],
 // clamped to the routed blocks; any value gives the same product, only the
 // order of the work changes).
@@ -605,6 +647,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm1_kernel(const uint16_t* __r
                                                              int32_t* __restrict__ handoff) {
   __shared__ ItemLds lds;
   const int n_tiles = cs.I / 16;
+  const PreBlock pre = block_pre(plan, cs, blockIdx.x / n_tiles, threadIdx.x & 15);
   const int nr = routed_blocks(plan, cs);
   const int n_res = handoff != nullptr ? resident_blocks(plan, cs) : nr;
   const int n_skip = nr - n_res;  // routed blocks [n_res, nr) are left to the split launch
@@ -616,7 +659,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm1_kernel(const uint16_t* __r
   for (int item = blockIdx.x; item < total; item += gridDim.x) {
     const int bb = item / n_tiles, tile = item - bb * n_tiles;
     int slot_field, pair;
-    block_at(plan, W, cs, bb < n_res ? bb : bb + n_skip, col, slot_field, pair);
+    block_at_pre(plan, W, cs, bb < n_res ? bb : bb + n_skip, col, pre, slot_field, pair);
     await_slot(W.wait, slot_field);
     run_g1<FP8>(x, W, cs, slot_field & kSlotMask, pair, tile, act, lds);
   }
