@@ -283,8 +283,10 @@ int sluice_layer_pin(sluice_layer* layer, int local, int debit_protected,
  * record, runs the reference's bookkeeping exactly (fast-hit, hit touches in
  * ascending id order, claimed set, victims), answers the device with the
  * standing slot table and the slots being filled, then streams the misses
- * as hipMemcpyAsync on the library's per-device copy stream and marks each
- * filled slot ready as its rows land: the expert product computes resident
+ * as hipMemcpyAsync on the library's per-device copy lanes (two streams;
+ * each per-expert param on the lane its layer assigned it, row bytes
+ * balanced) and marks each filled slot ready once its rows landed on every
+ * lane: the expert product computes resident
  * experts meanwhile and waits per filled slot.  `compute` (may be NULL) is
  * polled for errors while waiting.  SLUICE_E_OVERFLOW when the working set
  * does not fit (rows acquired before it still stream and land before the
@@ -359,7 +361,7 @@ int sluice_layer_gap_host(sluice_layer* layer, const int32_t* ids, int n,
  * Then, for w = 0 .. n_waves-1, the caller enqueues the expert product on
  * `stream` between sluice_layer_classic_wave(w) -- writes wave w's map
  * (its (global, slot) pairs, -1 elsewhere), and makes `stream` wait for the
- * wave's row copies, which run on the library's copy stream (wave 0's after
+ * wave's row copies, which run on the library's copy lanes (wave 0's after
  * the work already on `stream`) -- and sluice_layer_classic_wave_done(w),
  * which records the wave's end and issues wave w+1's copies behind the
  * kernel that last read those slots.  The caller sums the wave outputs.

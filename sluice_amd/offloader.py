@@ -8,7 +8,7 @@ patched ``runner._forward_entry``.  Underneath, the per-layer slot cache and
 the gap are native (libsluice_hip.so): a device kernel publishes the step's
 selected experts into pinned host memory, the native SLRU assigns slots as
 the reference's OrderedDict state machine does, missing experts stream with
-hipMemcpyAsync on a dedicated copy stream, and the device installs the
+hipMemcpyAsync on two dedicated copy streams, and the device installs the
 standing expert map that the captured expert product reads by pointer.
 
 Execution model per MoE layer per decode step (T <= thr tokens):
