@@ -343,3 +343,63 @@ def test_checkpoint_loaded_layer_matches_oracle(tmp_path):
         assert err <= 1e-2
     _check_slots(cache)
     off.close()
+
+
+def test_fp8_checkpoint_loaded_layer_matches_oracle(tmp_path):
+    """A block-quantised fp8 checkpoint (DeepSeek-V3 naming: e4m3fn
+    ``weight`` plus 128x128 ``weight_scale_inv``) -> pinned stores (loader:
+    four per-expert params) -> the offloader's slots (each miss streams four
+    rows) -> the fp8 expert product, on the gap path (T <= thr) and the
+    classic path (T > thr): slot rows equal the checkpoint's bytes and the
+    layer output is within the fp8 tolerance (3e-2) of the oracle over the
+    checkpoint's dequantised tensors."""
+    from safetensors.torch import save_file
+
+    from oracle import moe as om
+    from sluice_amd import loader
+    from sluice_amd.decoder import _StoreMoELayer, build_offloaded
+
+    E, k, H, I = 16, 4, 256, 128
+    sp = dict(E=E, H=H, I=I, k=k, fp8=True, e_bias=False, shared_I=0, scoring="softmax",
+              renorm=True, routed_scale=1.0, n_group=1, topk_group=1)
+    g = torch.Generator().manual_seed(12)
+    t = {}
+    key = "model.layers.5.mlp.experts.{e}.{proj}.{kind}"
+    for e in range(E):
+        for proj, shp in (("gate_proj", (I, H)), ("up_proj", (I, H)), ("down_proj", (H, I))):
+            t[key.format(e=e, proj=proj, kind="weight")] = (
+                torch.randn(shp, generator=g) * 4).to(torch.float8_e4m3fn)
+            t[key.format(e=e, proj=proj, kind="weight_scale_inv")] = (
+                torch.rand((shp[0] // 128, shp[1] // 128), generator=g) * 0.005 + 0.005)
+    save_file(t, str(tmp_path / "model.safetensors"))
+    store = loader.expert_stores_from_checkpoint(str(tmp_path), 5)
+    assert sorted(store) == ["w13_weight", "w13_weight_scale", "w2_weight", "w2_weight_scale"]
+
+    def deq(proj, e):
+        q = t[key.format(e=e, proj=proj, kind="weight")].view(torch.uint8).numpy()
+        s = t[key.format(e=e, proj=proj, kind="weight_scale_inv")].numpy()
+        return om.dequant_block(q, s)
+
+    host13 = np.stack([np.concatenate([deq("gate_proj", e), deq("up_proj", e)])
+                       for e in range(E)])
+    host2 = np.stack([deq("down_proj", e) for e in range(E)])
+    layer = _StoreMoELayer(sp, store, 0, DEV, None, "layers.5.mlp", gate_std=0.05)
+    off = build_offloaded([layer], 8, DEV)  # thr = 2
+    cache = off._caches[id(layer)]
+    assert len(cache.param_names) == 4
+    rng = np.random.default_rng(6)
+    for T in (1, 2, 6, 2, 1):
+        off.set_step_signal(T, T, True)
+        x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(
+            torch.bfloat16).to(DEV)
+        out = layer(x)
+        torch.cuda.synchronize()
+        tw, ti = layer.select(layer.logits(x))
+        ref = om.fused_experts(x.float().cpu().numpy(), host13, host2, tw.cpu().numpy(),
+                               ti.cpu().numpy())
+        err = om.rel_l2(out.float().cpu().numpy(), ref)
+        print(f"  T={T} rel_l2={err:.2e}", flush=True)
+        assert err <= 3e-2
+        _check_slots(cache)
+    assert off.classic_counters()["steps"] >= 1
+    off.close()
