@@ -65,6 +65,9 @@ DECODE_LEN = 256   # output tokens of the configured decode
 PROMPT_LEN = 128
 ROUTING = {"zipf_s": 1.1, "rho": 0.7, "sigma": 1.2, "gate_std": 0.004}
 LOCALITY_SIGMA = 0.5
+ORCH_GRAPH = "one graph per step, gap served by the native thread, misses pipelined"
+ORCH_REFERENCE = ("reference: eager gap between captured pieces (host waits for each layer's "
+                  "ids), expert product after the copies")
 
 
 def parse():
@@ -83,6 +86,8 @@ def parse():
                     help="only the headline configuration (no Qwen3 / V3 / stress rows)")
     ap.add_argument("--no-locality", action="store_true",
                     help="skip the sigma-0.5 locality rows")
+    ap.add_argument("--no-reference", action="store_true",
+                    help="skip the rows in the reference's orchestration")
     ap.add_argument("--host-pool", default="auto", choices=["auto", "shared", "per-layer"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=20.0)
@@ -141,6 +146,7 @@ def run_batch(dec, c, steps, warmup, prefill=True, label=None):
     h2d = delta["bytes"] / steps
     return {
         "c": c, "path": "classic" if dec.classic(c) else "gap", "routing": label or "zipf",
+        "orchestration": ORCH_GRAPH if dec.off._server is not None else ORCH_REFERENCE,
         "ms_per_step": dt / steps * 1e3, "tok_per_s": c * steps / dt,
         "classic_steps": cl1["steps"] - cl0["steps"],
         "waves_per_classic_step": (cl1["waves"] - cl0["waves"]) / max(cl1["steps"] - cl0["steps"],
@@ -550,10 +556,11 @@ def build_decoder(cfg, slots, max_batch, a, dev, gen_len, uniform=False, stores=
 
 
 def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, locality=(),
-            prefill=True, h2d=False):
+            prefill=True, h2d=False, reference=()):
     """One configuration: its batches, the routing it ran, the kernels'
-    roofline at the largest batch, optional locality rows; returns the
-    result and the decoder's host stores (for reuse by the same shape)."""
+    roofline at the largest batch, optional rows in the reference's
+    orchestration (same routing) and locality rows; returns the result and
+    the decoder's host stores (for reuse by the same shape)."""
     import gc
 
     import torch
@@ -575,6 +582,21 @@ def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, lo
     rstats = routing_stats(dec, recorded)
     roof = kernel_roofline(dec, c_main, recorded)
     rates = h2d_rates(dec) if h2d else None
+    if reference:
+        # The same batches and routing with the reference's orchestration:
+        # each MoE layer's gap runs eagerly between captured pieces, the host
+        # waiting for its ids, and a gap with misses answers only after its
+        # rows landed (the expert product does not overlap the copies).
+        dec.set_gap_mode(server=False, pipelined=False)
+        for c in reference:
+            r = run_batch(dec, c, a.steps, a.warmup, prefill=prefill and not uniform,
+                          label="uniform" if uniform else "zipf")
+            r["orchestration"] = ORCH_REFERENCE
+            log(f"{cfg} s{slots} c={c} (reference orchestration): {r['ms_per_step']:.3f} ms/step "
+                f"{r['tok_per_s']:.1f} tok/s misses/layer-step={r['misses_per_layer_step']:.3f} "
+                f"fast-hit={r['fast_hit_share']:.2%} H2D {r['h2d_GBs_in_step']:.1f} GB/s")
+            rows.append(r)
+        dec.set_gap_mode(server=True, pipelined=True)
     for c in locality:
         for rb in dec.bias_tables:
             rb.refill(ROUTING["zipf_s"], ROUTING["rho"], LOCALITY_SIGMA, rb.knobs["seed"])
@@ -658,8 +680,10 @@ def main():
         dec.close()
         return
     locality = () if (a.no_locality or a.uniform) else tuple(batches)
+    reference = () if (a.no_reference or a.uniform) else tuple(batches)
     head, stores = measure(cfg, slots, batches, a, dev, gen_len, uniform=a.uniform,
-                           locality=locality, prefill=not a.no_prefill, h2d=True)
+                           locality=locality, prefill=not a.no_prefill, h2d=True,
+                           reference=reference)
     del stores
     _release()
     extras = []
@@ -691,7 +715,9 @@ def main():
         log(f"cpu baseline {cpu['value']:.2f} tok/s, layer step {cpu['layer_step_ms']:.2f} ms, "
             f"stages {cpu['stages_median_us']}")
     main_c = max(batches)
-    main_row = [r for r in head["per_batch"] if r["c"] == main_c and r["routing"] != "locality"][0]
+    main_row = [r for r in head["per_batch"] if r["c"] == main_c and r["routing"] != "locality"
+                and r["orchestration"] == ORCH_GRAPH][0]
+    ref_rows = {r["c"]: r for r in head["per_batch"] if r["orchestration"] == ORCH_REFERENCE}
     pub = PUBLISHED_C8.get(cfg) if main_c == 8 and not a.uniform and slots == DEFAULT_SLOTS[cfg] \
         else None
     hc = head["config"]
@@ -719,6 +745,14 @@ def main():
             baseline_ref="reference router-split on 1xH100 with real-model routing (c=8)"
             if pub else None),
         "per_batch": head["per_batch"],
+        # this build's kernels in the reference's orchestration, same box,
+        # workload and routing: what the pipelined one-graph gap adds
+        "vs_reference_orchestration": {
+            c: {"ms_per_step": r["ms_per_step"], "tok_per_s": r["tok_per_s"],
+                "speedup": next(g["tok_per_s"] for g in head["per_batch"]
+                                if g["c"] == c and g["routing"] == r["routing"]
+                                and g["orchestration"] == ORCH_GRAPH) / r["tok_per_s"]}
+            for c, r in ref_rows.items()} or None,
         "roofline": None,
         "kernels": dict(head["kernels"], copy_256MiB_GBs=head["copy_256MiB_GBs"]),
         "h2d": head.get("h2d"),

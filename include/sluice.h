@@ -333,6 +333,15 @@ int sluice_gap_abort(int set);
  * counterpart in the reference (its gap waits are host syncs without a
  * bound); it lets callers, and tests, shorten a wait that must end. */
 int sluice_gap_set_timeout(double seconds);
+
+/* on=1 (default): a gap that streams misses is answered before the rows
+ * land and the expert product waits per filled slot.  on=0: the answer
+ * waits until every row landed, the order of the reference's gap, whose
+ * compute stream waits for the copy event before the expert product
+ * (src/sluice/offloader.py:2464, 1986-1991); slot assignment, maps and
+ * outputs are the same either way.  Applies to records served after the
+ * call. */
+int sluice_gap_set_pipelined(int on);
 int sluice_layer_gap_resync(sluice_layer* layer);
 
 /* The gap, host path (no HIP calls): ids is a host array.  Runs the same

@@ -517,6 +517,11 @@ double now_s() {
 // sluice_gap_set_timeout, else SLUICE_GAP_TIMEOUT_S, else 20.
 std::atomic<double> g_timeout_set{0.0};
 
+// Whether a missing gap is answered before its rows land (the expert
+// product then waits per filled slot) or, as the reference orders it, only
+// after every row landed (sluice_gap_set_pipelined).
+std::atomic<int> g_pipelined{1};
+
 double gap_timeout_s() {
   const double set = g_timeout_set.load(std::memory_order_relaxed);
   if (set > 0) return set;
@@ -738,7 +743,8 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     // slot for the ready mark set below.  (On overflow the rows acquired
     // before it still stream, as in the reference, whose copies were issued
     // before the raise; the device map is left as it was, answered after.)
-    const bool early = waits && grc == 0 && rc == SLUICE_OK;
+    const bool early = waits && grc == 0 && rc == SLUICE_OK &&
+                       g_pipelined.load(std::memory_order_relaxed) != 0;
     const int per_event = experts_per_event(L, n_streams);
     const int n_events = (n_streams + per_event - 1) / per_event;
     while (rc == SLUICE_OK && (int)L->fill_ev.size() < kLanes * n_events) {
@@ -1042,13 +1048,15 @@ extern "C" int sluice_gap_server_destroy(sluice_gap_server* S) {
   return err;
 }
 
-// After an abort: once every stream that ran gap kernels is synchronised,
-// clear the abort flag and line the host's stamps up with the device's, so
-// the layers can be used again (their slot state is whatever the served
-// records left; the aborted steps' outputs are invalid).
 extern "C" int sluice_gap_set_timeout(double seconds) {
   if (!(seconds >= 0.0) || seconds > 86400.0) return SLUICE_E_INVAL;
   g_timeout_set.store(seconds, std::memory_order_relaxed);
+  return SLUICE_OK;
+}
+
+extern "C" int sluice_gap_set_pipelined(int on) {
+  if (on != 0 && on != 1) return SLUICE_E_INVAL;
+  g_pipelined.store(on, std::memory_order_relaxed);
   return SLUICE_OK;
 }
 
@@ -1058,6 +1066,10 @@ extern "C" int sluice_gap_abort(int set) {
   return SLUICE_OK;
 }
 
+// After an abort: once every stream that ran gap kernels is synchronised,
+// clear the abort flag and line the host's stamps up with the device's, so
+// the layers can be used again (their slot state is whatever the served
+// records left; the aborted steps' outputs are invalid).
 extern "C" int sluice_layer_gap_resync(sluice_layer* L) {
   if (L == nullptr || L->mb == nullptr || L->server != nullptr) return SLUICE_E_INVAL;
   int32_t dev_stamp = 0;

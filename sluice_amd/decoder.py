@@ -1148,6 +1148,27 @@ class SyntheticDecoder:
         """Device synchronise + every gap record served (raises gap errors)."""
         self.off.drain()
 
+    def set_gap_mode(self, server: bool, pipelined: bool) -> None:
+        """How the gaps of later steps run.  server: served by the native
+        thread, the whole step one captured graph; else inline, the host
+        waiting for each MoE layer's ids between captured pieces (the
+        reference's eager gap op, src/sluice/offloader.py:2311-2331, 2406).
+        pipelined: a missing gap is answered before its rows land and the
+        expert product waits per filled slot; else only after every row
+        landed (the reference's copy-then-compute order, 2464).  Drops the
+        captured graphs: the next run of a batch size recaptures."""
+        from sluice_amd import _lib
+
+        self.sync()
+        self.graphs = {}
+        self.pool = None  # the dropped graphs' pool is released with them
+        if server:
+            self.off.start_gap_server()
+        else:
+            self.off.stop_gap_server()
+        _lib.check(_lib.load().sluice_gap_set_pipelined(int(pipelined)),
+                   "sluice_gap_set_pipelined")
+
     def gap_counters(self):
         return self.off.gap_counters()
 

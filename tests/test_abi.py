@@ -153,3 +153,7 @@ def test_gap_launch_and_read_probe_argument_checks(lib):
     assert lib.sluice_gap_set_timeout(-1.0) == _lib.SLUICE_E_INVAL
     assert lib.sluice_gap_set_timeout(float("nan")) == _lib.SLUICE_E_INVAL
     assert lib.sluice_gap_set_timeout(0.0) == _lib.SLUICE_OK
+    assert lib.sluice_gap_set_pipelined(2) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_gap_set_pipelined(-1) == _lib.SLUICE_E_INVAL
+    assert lib.sluice_gap_set_pipelined(0) == _lib.SLUICE_OK
+    assert lib.sluice_gap_set_pipelined(1) == _lib.SLUICE_OK

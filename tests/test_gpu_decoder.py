@@ -12,11 +12,21 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-def _run(spec, layers, c, steps, graphs, slots, gap_server, uniform=False):
+def _run(spec, layers, c, steps, graphs, slots, gap_server, uniform=False, pipelined=True):
+    from sluice_amd import _lib
     from sluice_amd.decoder import SyntheticDecoder
 
     dec = SyntheticDecoder(spec, max_batch=c, slots=slots, gen_len=steps + 16, layers=layers,
                            device=DEV, seed=3, gap_server=gap_server, uniform_routing=uniform)
+    try:
+        if not pipelined:
+            dec.set_gap_mode(server=gap_server, pipelined=False)
+        return _decode(dec, c, steps, graphs)
+    finally:
+        _lib.load().sluice_gap_set_pipelined(1)  # process-wide: restore the default
+
+
+def _decode(dec, c, steps, graphs):
     toks = []
 
     def out_of_step():
@@ -84,6 +94,29 @@ def test_miss_heavy_graph_decode_matches_eager(spec, layers, c, slots, steps):
     # most of each step's (token, expert) pairs missed
     misses = sum(y["counters"][1] for y in sb)
     assert misses >= steps * layers * c * 2, misses
+
+
+@pytest.mark.parametrize("spec,layers,c,slots,steps", [("qwen3", 2, 4, 32, 8),
+                                                      ("v3", 2, 8, 64, 4)])
+def test_copies_before_compute_matches_pipelined_gap(spec, layers, c, slots, steps):
+    """The reference's order -- a missing gap answered only after its rows
+    landed (sluice_gap_set_pipelined(0)), so the expert product never
+    overlaps the copies -- in both orchestrations (one graph with the gap
+    server; captured pieces around inline gaps, the host waiting for each
+    layer's ids) decodes the same tokens, with the same slot state, counters
+    and maps, as the pipelined one-graph step, on miss-heavy routing."""
+    print(f"copy order {spec} layers={layers} c={c} slots={slots}", flush=True)
+    a, sa, ma = _run(spec, layers, c, steps, graphs=True, slots=slots, gap_server=True,
+                     uniform=True)
+    for server in (True, False):
+        b, sb, mb = _run(spec, layers, c, steps, graphs=True, slots=slots, gap_server=server,
+                         uniform=True, pipelined=False)
+        assert np.array_equal(a, b), server
+        for x, y in zip(sa, sb):
+            assert x["expert_in_slot"] == y["expert_in_slot"]
+            assert x["counters"][:4] == y["counters"][:4]
+        assert ma == mb
+    assert sum(x["counters"][1] for x in sa) >= steps * layers * c * 2
 
 
 def test_piece_graphs_with_inline_gaps_match_eager():
