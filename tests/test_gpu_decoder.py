@@ -202,3 +202,62 @@ def test_v3_routed_fp8_layer_against_oracle():
         assert err <= 3e-2
     assert misses > 0
     off.close()
+
+
+
+@pytest.mark.parametrize("spec,slots,c,steps", [("v2lite", 48, 8, 24), ("qwen3", 64, 8, 16),
+                                              ("qwen3", 96, 12, 40), ("v3", 64, 8, 8)])
+def test_full_size_decode_slots_follow_the_oracle(spec, slots, c, steps):
+    """The configured models at full depth and shape (DeepSeek-V2-Lite: 26
+    MoE layers of 64 experts at 48 slots; Qwen3-30B-A3B: 48 layers of 128 at
+    64 and 96 slots; the DeepSeek-V3 fp8 stack: 8 layers of 256 at 64),
+    decoded from empty slot caches with the Zipf + AR(1) routing -- two eager
+    steps, then the captured one-graph step with the gap server: after every
+    step every layer's expert map, and at the end its slot assignment, SLRU
+    segment order and counters, equal the oracle's SLRU replaying the ids the
+    layer routed; the last layer's occupied slots hold their experts' host
+    rows byte for byte."""
+    from oracle.slru import LayerCache
+    from sluice_amd.decoder import SyntheticDecoder
+
+    print(f"full-size decode {spec} slots={slots} c={c} steps={steps}", flush=True)
+    dec = SyntheticDecoder(spec, max_batch=c, slots=slots, gen_len=steps + 16, device=DEV,
+                           host_pool="shared")
+    try:
+        E = dec.sp["E"]
+        oracles = [LayerCache(E, E, slots, dec.off.protect_frac) for _ in dec.moe_layers]
+
+        def check_step(label):
+            dec.sync()
+            for n, (io, m) in enumerate(zip(dec.layer_io[c], dec.moe_layers)):
+                ids = io["ti"].cpu().numpy().reshape(-1).tolist()
+                oracles[n].gap(ids, fast_hit=True)
+                assert m._expert_map.cpu().tolist() == oracles[n].map, (label, n)
+
+        for i in range(2):
+            dec.step_eager(c)
+            check_step(f"eager {i}")
+        dec.capture(c, warmup=0)
+        for i in range(steps):
+            dec.step_graphs(c)
+            check_step(f"graph {i}")
+        misses = 0
+        for n, (cache, o) in enumerate(zip(dec.caches, oracles)):
+            st = cache._state()
+            assert st["expert_in_slot"] == [-1 if v is None else v for v in o.expert_in_slot], n
+            assert st["probation"] == list(o.probation) and st["protected"] == list(o.protected), n
+            assert st["counters"][:3] == [o.gaps, o.misses, o.fast_hits], n
+            misses += o.misses
+        # past the cold fill: some layer evicted and streamed into used slots
+        assert any(o.misses > slots for o in oracles), misses
+        cache = dec.caches[-1]
+        occ = [(s, e) for s, e in enumerate(cache.expert_in_slot) if e is not None]
+        sl = torch.tensor([s for s, _ in occ], device=DEV)
+        ex = torch.tensor([e for _, e in occ])
+        for name in cache.param_names:
+            got = cache.gpu_cache[name].index_select(0, sl)
+            want = cache.cpu_store[name].index_select(0, ex).to(DEV)
+            assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), name
+        print(f"  {len(oracles)} layers, {misses} misses, {len(occ)} slots checked", flush=True)
+    finally:
+        dec.close()
