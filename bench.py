@@ -59,6 +59,10 @@ sys.path.insert(0, ROOT)
 
 DEFAULT_SLOTS = {"v2lite": 48, "qwen3": 64, "v3": 64}
 PUBLISHED_C8 = {"v2lite": 1062.6}  # reference, 1xH100 router-split, c=8 (tok/s)
+# the reference's published router-split decode (1xH100, real-model routing,
+# README.md:51, docs/router-split.md:324, 330): tok/s by batch and the share of
+# its gaps that take the fast-hit path
+PUBLISHED = {"v2lite": {"tok_per_s": {1: 147.2, 8: 1062.6}, "fast_hit_share": 0.86}}
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 DECODE_LEN = 256   # output tokens of the configured decode
@@ -753,6 +757,16 @@ def main():
                                 if g["c"] == c and g["routing"] == r["routing"]
                                 and g["orchestration"] == ORCH_GRAPH) / r["tok_per_s"]}
             for c, r in ref_rows.items()} or None,
+        # each batch's tok/s against the reference's published figure, with
+        # both fast-hit shares: where they match the routing is like for like
+        "vs_published": {
+            c: {"reference_tok_per_s": ref_tps, "tok_per_s": r["tok_per_s"],
+                "ratio": r["tok_per_s"] / ref_tps, "fast_hit_share": r["fast_hit_share"],
+                "reference_fast_hit_share": PUBLISHED[cfg]["fast_hit_share"]}
+            for c, ref_tps in PUBLISHED.get(cfg, {}).get("tok_per_s", {}).items()
+            for r in head["per_batch"]
+            if r["c"] == c and r["routing"] == "zipf" and r["orchestration"] == ORCH_GRAPH
+            and slots == DEFAULT_SLOTS[cfg]} or None,
         "roofline": None,
         "kernels": dict(head["kernels"], copy_256MiB_GBs=head["copy_256MiB_GBs"]),
         "h2d": head.get("h2d"),
