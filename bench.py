@@ -59,10 +59,19 @@ sys.path.insert(0, ROOT)
 
 DEFAULT_SLOTS = {"v2lite": 48, "qwen3": 64, "v3": 64}
 PUBLISHED_C8 = {"v2lite": 1062.6}  # reference, 1xH100 router-split, c=8 (tok/s)
-# the reference's published router-split decode (1xH100, real-model routing,
-# README.md:51, docs/router-split.md:324, 330): tok/s by batch and the share of
-# its gaps that take the fast-hit path
-PUBLISHED = {"v2lite": {"tok_per_s": {1: 147.2, 8: 1062.6}, "fast_hit_share": 0.86}}
+# The reference's published router-split decode (1xH100, real-model routing):
+# tok/s by slots and batch, and the share of its gaps that take the fast-hit
+# path (V2-Lite: README.md:51, docs/router-split.md:324, 330; Qwen3-30B-A3B:
+# README.md:66-67, docs/router-split.md:360, 375, 384).
+PUBLISHED = {
+    "v2lite": {"tok_per_s": {48: {1: 147.2, 8: 1062.6}}, "fast_hit_share": 0.86},
+    "qwen3": {"tok_per_s": {64: {1: 121.2, 8: 864.5}, 96: {1: 122.8, 8: 883.7, 12: 1263.8}},
+              "fast_hit_share": 0.99},
+}
+# Routing noise at which a batch's gaps take the fast-hit path as often as the
+# reference's do (86% for V2-Lite; measured 86.2% at c=8 with sigma 0.8); the
+# Zipf rows (sigma 1.2) are the configured workload, these rows the like-for-like one.
+MATCHED_SIGMA = {"v2lite": {8: 0.8}}
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 DECODE_LEN = 256   # output tokens of the configured decode
@@ -560,7 +569,7 @@ def build_decoder(cfg, slots, max_batch, a, dev, gen_len, uniform=False, stores=
 
 
 def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, locality=(),
-            prefill=True, h2d=False, reference=()):
+            prefill=True, h2d=False, reference=(), matched=()):
     """One configuration: its batches, the routing it ran, the kernels'
     roofline at the largest batch, optional rows in the reference's
     orchestration (same routing) and locality rows; returns the result and
@@ -601,6 +610,15 @@ def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, lo
                 f"fast-hit={r['fast_hit_share']:.2%} H2D {r['h2d_GBs_in_step']:.1f} GB/s")
             rows.append(r)
         dec.set_gap_mode(server=True, pipelined=True)
+    for c, sigma in matched:
+        for rb in dec.bias_tables:
+            rb.refill(ROUTING["zipf_s"], ROUTING["rho"], sigma, rb.knobs["seed"])
+        r = run_batch(dec, c, a.steps, a.warmup, prefill=prefill, label="matched")
+        r["sigma"] = sigma
+        log(f"{cfg} s{slots} c={c} (fast-hit matched, sigma={sigma}): {r['ms_per_step']:.3f} "
+            f"ms/step {r['tok_per_s']:.1f} tok/s misses/layer-step="
+            f"{r['misses_per_layer_step']:.3f} fast-hit={r['fast_hit_share']:.2%}")
+        rows.append(r)
     for c in locality:
         for rb in dec.bias_tables:
             rb.refill(ROUTING["zipf_s"], ROUTING["rho"], LOCALITY_SIGMA, rb.knobs["seed"])
@@ -639,6 +657,23 @@ def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, lo
     gc.collect()
     torch.cuda.empty_cache()
     return out, stores
+
+
+def vs_published(rows):
+    """Rows (model shape, slots, row) that have a published reference
+    figure, each with its ratio to it; None when none has."""
+    out = []
+    for cfg, slots, r in rows:
+        pub = PUBLISHED.get(cfg)
+        ref = (pub or {}).get("tok_per_s", {}).get(slots, {}).get(r["c"])
+        if ref is None or r["path"] != "gap" or r["orchestration"] != ORCH_GRAPH:
+            continue
+        out.append({"model_shape": cfg, "slots": slots, "c": r["c"], "routing": r["routing"],
+                    "sigma": r.get("sigma"), "tok_per_s": r["tok_per_s"],
+                    "reference_tok_per_s": ref, "ratio": r["tok_per_s"] / ref,
+                    "fast_hit_share": r["fast_hit_share"],
+                    "reference_fast_hit_share": pub["fast_hit_share"]})
+    return out or None
 
 
 def _release():
@@ -685,9 +720,11 @@ def main():
         return
     locality = () if (a.no_locality or a.uniform) else tuple(batches)
     reference = () if (a.no_reference or a.uniform) else tuple(batches)
+    matched = () if (a.no_locality or a.uniform or slots != DEFAULT_SLOTS[cfg]) else tuple(
+        (c, sg) for c, sg in MATCHED_SIGMA.get(cfg, {}).items() if c in batches)
     head, stores = measure(cfg, slots, batches, a, dev, gen_len, uniform=a.uniform,
                            locality=locality, prefill=not a.no_prefill, h2d=True,
-                           reference=reference)
+                           reference=reference, matched=matched)
     del stores
     _release()
     extras = []
@@ -757,16 +794,13 @@ def main():
                                 if g["c"] == c and g["routing"] == r["routing"]
                                 and g["orchestration"] == ORCH_GRAPH) / r["tok_per_s"]}
             for c, r in ref_rows.items()} or None,
-        # each batch's tok/s against the reference's published figure, with
-        # both fast-hit shares: where they match the routing is like for like
-        "vs_published": {
-            c: {"reference_tok_per_s": ref_tps, "tok_per_s": r["tok_per_s"],
-                "ratio": r["tok_per_s"] / ref_tps, "fast_hit_share": r["fast_hit_share"],
-                "reference_fast_hit_share": PUBLISHED[cfg]["fast_hit_share"]}
-            for c, ref_tps in PUBLISHED.get(cfg, {}).get("tok_per_s", {}).items()
-            for r in head["per_batch"]
-            if r["c"] == c and r["routing"] == "zipf" and r["orchestration"] == ORCH_GRAPH
-            and slots == DEFAULT_SLOTS[cfg]} or None,
+        # every measured row with a published reference figure (same model
+        # shape, slots and batch), with both fast-hit shares: where they
+        # match, the routing is like for like
+        "vs_published": vs_published(
+            [(cfg, slots, r) for r in head["per_batch"]]
+            + [(e["config"]["model_shape"], e["config"]["slots"], r) for e in extras
+               for r in e["per_batch"]]),
         "roofline": None,
         "kernels": dict(head["kernels"], copy_256MiB_GBs=head["copy_256MiB_GBs"]),
         "h2d": head.get("h2d"),
