@@ -25,7 +25,12 @@ weights N(0, 0.004): the selections' top-k share is the one Zipf(1.1)
 popularity gives, and the logits' lag-1 correlation ~0.7).  The knobs and the
 measured top-k share, unique experts and misses per layer-step are in the
 line.  Rows labelled "locality" rerun the batch with sigma 0.5, whose
-fast-hit share lies in the band the reference reports for real models.
+fast-hit share lies in the band the reference reports for real models; the
+"matched" row reruns V2-Lite c=8 with sigma 0.8, where the share of fast-hit
+gaps equals the reference's (86%).  Rows "in the reference's orchestration"
+rerun the headline batches with the gaps eager between captured pieces and
+each missing gap answered after its rows landed.  ``vs_published`` lists
+every row that has a published reference figure, with both fast-hit shares.
 
 Also measured in the same run:
   roofline      the dominant kernel (moe_gemm1: gate/up weights stream) timed
