@@ -261,3 +261,56 @@ def test_full_size_decode_slots_follow_the_oracle(spec, slots, c, steps):
         print(f"  {len(oracles)} layers, {misses} misses, {len(occ)} slots checked", flush=True)
     finally:
         dec.close()
+
+
+def test_full_size_mixed_classic_and_gap_steps_follow_the_oracle():
+    """Qwen3-30B-A3B at full depth (48 MoE layers of 128 experts, 64 slots)
+    decoding a schedule that alternates batches above the router-split
+    envelope (12 tokens x top-8 > 64 slots: the classic hook, waves planned
+    on the host between captured pieces) with batches inside it (8 tokens:
+    the gap), from empty caches: every layer's expert map after every step,
+    and at the end its slot assignment, segment order and counters, equal
+    the oracle replaying the same ids through the same kind of step."""
+    from oracle.slru import LayerCache
+    from sluice_amd.decoder import SyntheticDecoder
+
+    schedule = [12, 8, 12, 12, 8, 8, 12, 8, 12, 12, 12, 8]
+    print(f"full-size mixed decode qwen3 slots=64 schedule={schedule}", flush=True)
+    dec = SyntheticDecoder("qwen3", max_batch=12, slots=64, gen_len=len(schedule) + 16,
+                           device=DEV, host_pool="shared")
+    try:
+        E = dec.sp["E"]
+        oracles = [LayerCache(E, E, 64, dec.off.protect_frac) for _ in dec.moe_layers]
+        classic_steps = 0
+
+        def check_step(c, label):
+            nonlocal classic_steps
+            dec.sync()
+            classic = dec.classic(c)
+            classic_steps += classic
+            for n, (io, m) in enumerate(zip(dec.layer_io[c], dec.moe_layers)):
+                ids = io["ti"].cpu().numpy().reshape(-1).tolist()
+                if classic:
+                    oracles[n].classic(ids, c, c, c, True)
+                else:
+                    oracles[n].gap(ids, fast_hit=True)
+                assert m._expert_map.cpu().tolist() == oracles[n].map, (label, n)
+
+        assert dec.classic(12) and not dec.classic(8)
+        for c in (8, 12):  # one recorded eager step per batch size, then capture
+            dec.step_eager(c)
+            check_step(c, f"eager c={c}")
+            dec.capture(c, warmup=0)
+        for i, c in enumerate(schedule):
+            dec.step_graphs(c)
+            check_step(c, f"step {i} c={c}")
+        for n, (cache, o) in enumerate(zip(dec.caches, oracles)):
+            st = cache._state()
+            assert st["expert_in_slot"] == [-1 if v is None else v for v in o.expert_in_slot], n
+            assert st["probation"] == list(o.probation) and st["protected"] == list(o.protected), n
+            assert st["counters"][:3] == [o.gaps, o.misses, o.fast_hits], n
+        assert classic_steps == 1 + schedule.count(12)
+        print(f"  {classic_steps} classic steps, {sum(o.misses for o in oracles)} misses",
+              flush=True)
+    finally:
+        dec.close()
