@@ -13,9 +13,11 @@ router-split envelope (c > slots // top_k) take the classic wave path.
 Per batch size: the step is captured, then the batch's 128-token synthetic
 prompts are processed position by position through the captured step
 (untimed; every prompt token is routed through every MoE layer, so the slot
-caches start warm and the KV caches hold the prompts), then W warm-up decode
-steps, then the K timed steps -- decode positions 128+W .. 128+W+K of a
-256-token decode (longer if W + K needs it).  The timed region is bracketed
+caches start warm and the KV caches hold the prompts), then untimed decode
+steps up to the middle of a 256-token decode (the last W of them the warm-up),
+then the K timed steps, centred in the decode: positions 128+(256-K)/2 ..
++K (the stress row, without prompts, times from its first steps).  The timed
+region is bracketed
 by device synchronisation; ``value`` is tokens/s of the headline workload
 (DeepSeek-V2-Lite shape, 48 slots, c=8).
 
@@ -123,8 +125,10 @@ def log(*a):
 
 
 def run_batch(dec, c, steps, warmup, prefill=True, label=None):
-    """Capture batch c, process its prompts (untimed), W warm-up steps, then
-    time K steps; counters are the timed steps' own."""
+    """Capture batch c, process its prompts (untimed), decode untimed up to
+    the middle of the configured decode, W warm-up steps, then time K steps
+    (the window centred in the decode); counters are the timed steps' own.
+    Without prompts (the uniform stress) the window starts at once."""
     import torch
 
     if c not in dec.graphs:
@@ -136,7 +140,8 @@ def run_batch(dec, c, steps, warmup, prefill=True, label=None):
         dec.reset(c)
     dec.sync()
     prefill_s = time.perf_counter() - t0
-    for _ in range(warmup):
+    lead = max(0, (DECODE_LEN - steps) // 2 - warmup) if prefill else 0
+    for _ in range(lead + warmup):
         dec.step_graphs(c)
     dec.sync()
     before = dec.gap_counters()
@@ -176,6 +181,7 @@ def run_batch(dec, c, steps, warmup, prefill=True, label=None):
         "fast_hit_share": delta["fast_hits"] / max(delta["gaps"], 1),
         "prefill": {"tokens_per_sequence": dec.prompt_len if prefill else 0,
                     "seconds": prefill_s},
+        "untimed_decode_steps": lead + warmup,
         "timed_positions": [pos0, pos0 + steps] if pos0 is not None else None,
         "step_ms_min_median_max": [per_step[0], per_step[len(per_step) // 2], per_step[-1]]
         if per_step else None,
@@ -492,7 +498,11 @@ def h2d_rates(dec):
         torch.cuda.synchronize()
         return sum(sizes) * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
 
-    peak = copies([d.data_ptr()], [st.data_ptr()], [64 << 20], [0], 8)
+    # medians of several short timings: a single one occasionally catches a
+    # stall of a few milliseconds (seen on the box: 40-45 GB/s once in six
+    # back-to-back measurements, 55 GB/s the rest)
+    peak = float(np.median([copies([d.data_ptr()], [st.data_ptr()], [64 << 20], [0], 8)
+                            for _ in range(3)]))
     cache = dec.caches[0]
     row = {name: cache.cpu_store[name][0].nbytes for name in cache.param_names}
     load, lane_of_param = [0, 0], {}
@@ -511,7 +521,7 @@ def h2d_rates(dec):
             sizes.append(rb)
             lane_of.append(lane_of_param[name])
     torch.cuda.synchronize()
-    expert = copies(dsts, srcs, sizes, lane_of, 3)
+    expert = float(np.median([copies(dsts, srcs, sizes, lane_of, 3) for _ in range(5)]))
     # put the touched slots back to what the cache says they hold
     for name in cache.param_names:
         for slot, loc in enumerate(cache.expert_in_slot):
