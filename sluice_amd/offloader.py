@@ -63,6 +63,9 @@ LFU_ENV = "SLUICE_LFU"
 COUNTS_DIR_ENV = "SLUICE_EXPERT_COUNTS"
 COUNTS_EVERY_ENV = "SLUICE_EXPERT_COUNTS_EVERY"
 PIN_FILE_ENV = "SLUICE_PIN_FILE"
+# Full residency with the streaming hook kept (src/sluice/offloader.py:289-293,
+# 948-1012): every expert pre-filled into its own slot and pinned there.
+NO_STATIC_FULL_ENV = "SLUICE_NO_STATIC_FULL"
 
 # Graph split points under piecewise capture: the MoE ops (whose apply runs
 # the classic hook, which syncs the host) and the gap op.
@@ -489,6 +492,7 @@ class ExpertStreamOffloader(_OffloaderBase):
                            "goes stale and layer outputs are WRONG.", NOOP_ENV)
         self.pin_memory = torch.cuda.is_available()
         self.lfu = _env_flag(LFU_ENV)
+        self.no_static_full = _env_flag(NO_STATIC_FULL_ENV)
         self._caches: dict[int, _ExpertLayerCache] = {}
         self._layers: list[nn.Module] = []
         self._prepared_stores: dict[int, list] = {}  # pinned stores made before load
@@ -620,7 +624,10 @@ class ExpertStreamOffloader(_OffloaderBase):
         cache = _ExpertLayerCache(local_num_experts=local_n, num_slots=num_slots,
                                   protected_cap=protected_cap, device=device,
                                   param_names=list(per_expert.keys()))
-        cache.static_full = num_slots >= local_n
+        cache.static_full = num_slots >= local_n and not self.no_static_full
+        # capacity for every expert but the hook kept on: all of them are
+        # loaded once here and pinned, so nothing ever streams
+        prefill_resident = num_slots >= local_n and not cache.static_full
         for name, p in per_expert.items():
             cpu = p.data if p.data.device.type == "cpu" else p.data.to("cpu")
             slot = torch.empty((num_slots, *p.shape[1:]), dtype=p.dtype, device=device)
@@ -678,6 +685,17 @@ class ExpertStreamOffloader(_OffloaderBase):
                 _lib.check(lib.sluice_layer_set_policy(cache.handle, int(self.lfu),
                                                        int(self._counts is not None)),
                            "sluice_layer_set_policy")
+            if prefill_resident:
+                slot = ctypes.c_int()
+                for local in range(local_n):
+                    _lib.check(lib.sluice_layer_pin(cache.handle, local, 0, ctypes.byref(slot)),
+                               "sluice_layer_pin")
+                    if slot.value != local:
+                        raise RuntimeError(f"Sluice: full-residency pre-fill put expert {local} "
+                                           f"in slot {slot.value}")
+                for name in cache.param_names:
+                    cache.gpu_cache[name][:local_n].copy_(cache.cpu_store[name])
+                cache.pinned_slots.update(range(local_n))
             if self._pin_layers is not None:
                 self._apply_pins(cache, cache.ordinal)
         self._caches[id(module)] = cache

@@ -314,3 +314,45 @@ def test_full_size_mixed_classic_and_gap_steps_follow_the_oracle():
               flush=True)
     finally:
         dec.close()
+
+
+@pytest.mark.parametrize("spec,layers,slots,c,steps", [("v2lite", None, 48, 8, 24),
+                                                     ("qwen3", None, 64, 8, 16),
+                                                     ("v3", 2, 64, 8, 8)])
+def test_offloaded_decode_equals_fully_resident_decode(monkeypatch, spec, layers, slots, c,
+                                                       steps):
+    """Streaming experts must not change the output (the reference's own
+    correctness demo, examples/bitcompare_v2lite.py: greedy ids of an
+    offloaded run diffed against an all-resident one).  The same seeded
+    decoder decodes the same steps twice through the captured one-graph
+    step: with fewer slots than experts (gaps streaming and evicting) and
+    with a slot for every expert, pre-filled and pinned, the hook kept on
+    (SLUICE_NO_STATIC_FULL=1, src/sluice/offloader.py:289-293, 948-1012:
+    nothing streams); the next tokens of every step (the output rows' bits
+    for the MoE stack without attention) are identical."""
+    from sluice_amd.decoder import SyntheticDecoder
+
+    def decode(n_slots):
+        dec = SyntheticDecoder(spec, max_batch=c, slots=n_slots, gen_len=steps + 16,
+                               layers=layers, device=DEV, host_pool="shared")
+        try:
+            dec.capture(c)
+            out = []
+            for _ in range(steps):
+                dec.step_graphs(c)
+                st = dec.state[c]
+                out.append(st.tokens.clone() if st.tokens is not None
+                           else st.x.view(torch.int16).clone())
+            dec.sync()
+            streamed = dec.gap_counters()["misses"]
+            return torch.stack(out).cpu().numpy(), streamed
+        finally:
+            dec.close()
+
+    E = __import__("sluice_amd.decoder", fromlist=["SPECS"]).SPECS[spec]["E"]
+    print(f"bitcompare {spec} slots {slots} vs {E}, c={c}, {steps} steps", flush=True)
+    off, misses = decode(slots)
+    monkeypatch.setenv("SLUICE_NO_STATIC_FULL", "1")
+    full, full_misses = decode(E)
+    assert misses > slots and full_misses == 0, (misses, full_misses)
+    assert np.array_equal(off, full)
