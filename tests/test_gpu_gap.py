@@ -392,3 +392,47 @@ def test_server_overflow_raises_at_drain_and_reset_resumes(monkeypatch):
         step(2)
         assert cache.expert_map_buf.cpu().tolist() == oracle.map
     off.close()
+
+
+@pytest.mark.parametrize("fast_hit", [False, True])
+def test_device_gap_with_no_tokens(monkeypatch, fast_hit):
+    """A step with no tokens (an empty batch reaching the gap op): the op
+    returns an empty fresh tensor; before the first standing map the empty
+    step still installs one (src/sluice/offloader.py:2427-2467 with an empty
+    sorted set: no touch, no fill, the standing map written), after it the
+    step changes nothing -- slots, segments, counters and the device map
+    follow the oracle through empty steps mixed with routed ones."""
+    from oracle.slru import LayerCache
+    from sluice_amd import _lib
+
+    E, local_n, k, S = 16, 16, 2, 6
+    layer = _Layer(E, local_n)
+    off = _offloader(monkeypatch, S, 0.5, fast_hit)
+    off.wrap_modules(iter([layer]))
+    with torch.cuda.device(DEV):
+        off.post_init()
+    cache = off._caches[id(layer)]
+    off._rs_caches.append(cache)
+    cache.plan = torch.zeros(_lib.load().sluice_moe_plan_ints(1, cache.num_slots),
+                             dtype=torch.int32, device=DEV)
+    oracle = LayerCache(E, local_n, S, 0.5)
+    rng = np.random.default_rng(5)
+    schedule = [0, 0, 3, 0, 2, 0, 0, 3, 1, 0]  # T*k <= S: within the envelope
+    for n, T in enumerate(schedule):
+        ids_np = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32) \
+            if T else np.zeros((0, k), np.int32)
+        ids = torch.from_numpy(ids_np).to(DEV)
+        hs = torch.randn((T, 64), device=DEV).to(torch.bfloat16)
+        out = torch.ops.vllm.sluice_stream_gap(hs, ids, 0)
+        assert out.shape == hs.shape and (T == 0 or out.data_ptr() != hs.data_ptr())
+        assert torch.equal(out, hs)
+        oracle.gap(ids_np.reshape(-1).tolist(), fast_hit=fast_hit)
+        torch.cuda.synchronize()
+        st = cache._state()
+        assert st["expert_in_slot"] == [-1 if v is None else v for v in oracle.expert_in_slot], n
+        assert st["probation"] == list(oracle.probation), n
+        assert st["protected"] == list(oracle.protected), n
+        assert st["counters"][:3] == [oracle.gaps, oracle.misses, oracle.fast_hits], n
+        assert cache.expert_map_buf.cpu().tolist() == oracle.map, n
+    _check_slots(cache, layer)
+    off.close()
