@@ -23,6 +23,10 @@ CASES = [
     (8, 60, 4, "softmax", False, 1.0, 1, 1, torch.bfloat16, False),    # Qwen1.5-MoE
     (64, 1024, 16, "softmax", True, 1.0, 1, 1, torch.float32, False),  # limits
     (5, 100, 7, "sigmoid", False, 1.0, 1, 1, torch.float32, True),     # ragged E
+    (512, 64, 6, "softmax", False, 1.0, 1, 1, torch.bfloat16, False),  # a prompt chunk
+    (8, 16, 1, "softmax", True, 1.0, 1, 1, torch.float32, False),      # top-1
+    (4, 8, 8, "softmax", True, 1.0, 1, 1, torch.bfloat16, False),      # k == E
+    (8, 256, 8, "sigmoid", True, 2.5, 8, 8, torch.float32, True),      # every group kept
 ]
 
 
@@ -42,7 +46,7 @@ def _run(T, E, k, scoring, renorm, scale, ng, tg, dtype, use_bias, logits32, bia
     return ids.cpu().numpy(), w.cpu().numpy(), rid, rw
 
 
-@pytest.mark.parametrize("case", CASES, ids=[f"T{c[0]}E{c[1]}k{c[2]}{c[3]}{c[6]}" for c in CASES])
+@pytest.mark.parametrize("case", CASES, ids=[f"T{c[0]}E{c[1]}k{c[2]}{c[3]}g{c[6]}x{c[7]}{str(c[8])[6:]}" for c in CASES])
 @pytest.mark.parametrize("seed", [0, 1])
 def test_routing_bit_exact(case, seed):
     T, E, k, scoring, renorm, scale, ng, tg, dtype, use_bias = case
@@ -76,3 +80,16 @@ def test_routing_empty_batch():
     lg = torch.zeros((0, 64), device="cuda:0")
     w, ids = ops.select_experts(lg, 6)
     assert ids.shape == (0, 6) and w.shape == (0, 6)
+
+
+def test_routing_half_logits_route_as_float32():
+    # fp16 logits are widened to fp32 before the kernel: the same ids and
+    # weights as the fp32 logits of the same values
+    rng = np.random.default_rng(11)
+    T, E, k = 8, 64, 6
+    logits = (rng.standard_normal((T, E)) * 1.5).astype(np.float16).astype(np.float32)
+    bias = np.zeros(E, np.float32)
+    ids, w, rid, rw = _run(T, E, k, "softmax", False, 1.0, 1, 1, torch.float16, False,
+                           logits, bias)
+    assert np.array_equal(ids, rid)
+    np.testing.assert_allclose(w, rw, rtol=1e-5, atol=1e-7)
