@@ -44,10 +44,16 @@ Also measured in the same run:
   h2d           peak pinned host->device GB/s (64 MiB copies) and the rate of
                 expert-row stream-ins issued like the gap issues them.
   extras        the other configurations: Qwen3-30B-A3B shape (48 layers)
-                at 64 slots c=1/8 and 96 slots c=12, the DeepSeek-V3 fp8
-                MoE stack (8 layers, 64 slots) at c=8, and the miss-dominated
-                stress (Qwen3 shape, 32 slots, uniform routing, c=4), each
+                at 64 slots c=1/8 (c=12 on the classic wave path) and 96
+                slots c=1/8/12, the DeepSeek-V3 fp8 MoE stack (8 layers, 64
+                slots) at c=8, and the miss-dominated stress (Qwen3 shape, 32
+                slots, uniform routing, c=4, --stress-steps timed steps), each
                 with its gemm1 roofline fraction and H2D rate.
+
+Output: the full record (every row, kernel and baseline figure) goes to
+--record and to stderr; the last stdout line is a compact headline object
+(compact_line: the contract's fields, roofline, cpu_baseline, H2D rates and
+one short row per measured batch), kept under LINE_LIMIT bytes.
   cpu_baseline  the path in torch fp32 on the host cores (oracle/cpu_path.py)
                 on one DeepSeek-V2-Lite-shaped layer, per-stage medians.
 """
@@ -117,6 +123,12 @@ def parse():
                     help="time only the kernels, over the routing of --load-routing, and print "
                          "that (no decode: the workload of the counter runs)")
     ap.add_argument("--load-routing", default=None)
+    ap.add_argument("--stress-steps", type=int, default=64,
+                    help="timed steps of the miss-dominated stress row (uniform i.i.d. routing "
+                         "is stationary, so the per-step figure does not depend on the count)")
+    ap.add_argument("--record", default="bench_record.json",
+                    help="file for the full record (every row, kernel and baseline figure); "
+                         "the last stdout line is the compact headline object")
     return ap.parse_args()
 
 
@@ -168,7 +180,8 @@ def run_batch(dec, c, steps, warmup, prefill=True, label=None):
     n_moe = len(dec.moe_layers)
     h2d = delta["bytes"] / steps
     return {
-        "c": c, "path": "classic" if dec.classic(c) else "gap", "routing": label or "zipf",
+        "c": c, "steps": steps, "path": "classic" if dec.classic(c) else "gap",
+        "routing": label or "zipf",
         "orchestration": ORCH_GRAPH if dec.off._server is not None else ORCH_REFERENCE,
         "ms_per_step": dt / steps * 1e3, "tok_per_s": c * steps / dt,
         "classic_steps": cl1["steps"] - cl0["steps"],
@@ -584,7 +597,7 @@ def build_decoder(cfg, slots, max_batch, a, dev, gen_len, uniform=False, stores=
 
 
 def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, locality=(),
-            prefill=True, h2d=False, reference=(), matched=()):
+            prefill=True, h2d=False, reference=(), matched=(), steps=None):
     """One configuration: its batches, the routing it ran, the kernels'
     roofline at the largest batch, optional rows in the reference's
     orchestration (same routing) and locality rows; returns the result and
@@ -593,10 +606,11 @@ def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, lo
 
     import torch
 
+    steps = steps or a.steps
     dec, build_s = build_decoder(cfg, slots, max(batches), a, dev, gen_len, uniform, stores)
     rows = []
     for c in batches:
-        r = run_batch(dec, c, a.steps, a.warmup, prefill=prefill and not uniform,
+        r = run_batch(dec, c, steps, a.warmup, prefill=prefill and not uniform,
                       label="uniform" if uniform else "zipf")
         log(f"{cfg} s{slots} c={c} ({r['path']}, {r['routing']}): {r['ms_per_step']:.3f} ms/step "
             f"{r['tok_per_s']:.1f} tok/s misses/layer-step={r['misses_per_layer_step']:.3f} "
@@ -617,7 +631,7 @@ def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, lo
         # rows landed (the expert product does not overlap the copies).
         dec.set_gap_mode(server=False, pipelined=False)
         for c in reference:
-            r = run_batch(dec, c, a.steps, a.warmup, prefill=prefill and not uniform,
+            r = run_batch(dec, c, steps, a.warmup, prefill=prefill and not uniform,
                           label="uniform" if uniform else "zipf")
             r["orchestration"] = ORCH_REFERENCE
             log(f"{cfg} s{slots} c={c} (reference orchestration): {r['ms_per_step']:.3f} ms/step "
@@ -628,7 +642,7 @@ def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, lo
     for c, sigma in matched:
         for rb in dec.bias_tables:
             rb.refill(ROUTING["zipf_s"], ROUTING["rho"], sigma, rb.knobs["seed"])
-        r = run_batch(dec, c, a.steps, a.warmup, prefill=prefill, label="matched")
+        r = run_batch(dec, c, steps, a.warmup, prefill=prefill, label="matched")
         r["sigma"] = sigma
         log(f"{cfg} s{slots} c={c} (fast-hit matched, sigma={sigma}): {r['ms_per_step']:.3f} "
             f"ms/step {r['tok_per_s']:.1f} tok/s misses/layer-step="
@@ -637,7 +651,7 @@ def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, lo
     for c in locality:
         for rb in dec.bias_tables:
             rb.refill(ROUTING["zipf_s"], ROUTING["rho"], LOCALITY_SIGMA, rb.knobs["seed"])
-        r = run_batch(dec, c, a.steps, a.warmup, prefill=prefill, label="locality")
+        r = run_batch(dec, c, steps, a.warmup, prefill=prefill, label="locality")
         r["sigma"] = LOCALITY_SIGMA
         log(f"{cfg} s{slots} c={c} (locality sigma={LOCALITY_SIGMA}): {r['ms_per_step']:.3f} "
             f"ms/step {r['tok_per_s']:.1f} tok/s misses/layer-step="
@@ -748,7 +762,7 @@ def main():
         q64, qstores = measure("qwen3", 64, [1, 8], a, dev, gen_len,
                                locality=() if a.no_locality else (8,))
         extras.append(q64)
-        q96 = measure("qwen3", 96, [12], a, dev, gen_len, stores=qstores,
+        q96 = measure("qwen3", 96, [1, 8, 12], a, dev, gen_len, stores=qstores,
                       locality=() if a.no_locality else (12,))[0]
         extras.append(q96)
         # c=12 at 64 slots is above the router-split envelope (12 * 8 > 64): the
@@ -756,8 +770,11 @@ def main():
         q64c = measure("qwen3", 64, [12], a, dev, gen_len, stores=qstores, locality=())[0]
         q64c["config"]["workload"] = "classic wave path: c=12 above the router-split envelope"
         extras.append(q64c)
-        stress = measure("qwen3", 32, [4], a, dev, gen_len, uniform=True, stores=qstores)[0]
-        stress["config"]["workload"] = "stress: uniform i.i.d. top-8, no prompt (no locality)"
+        stress = measure("qwen3", 32, [4], a, dev, max(gen_len, a.stress_steps + a.warmup + 8),
+                         uniform=True, stores=qstores, steps=a.stress_steps)[0]
+        stress["config"]["workload"] = (
+            f"stress: uniform i.i.d. top-8, no prompt (no locality), {a.stress_steps} timed steps "
+            f"after {a.warmup} warm-up steps (the configured run is 512 steps)")
         extras.append(stress)
         del qstores
         _release()
@@ -770,6 +787,21 @@ def main():
         cpu = cpu_baseline(a.cpu_budget_s, n_moe)
         log(f"cpu baseline {cpu['value']:.2f} tok/s, layer step {cpu['layer_step_ms']:.2f} ms, "
             f"stages {cpu['stages_median_us']}")
+    record = full_record(a, cfg, sp, slots, batches, gen_len, head, extras, cpu)
+    record["record_file"] = os.path.abspath(a.record) if a.record else None
+    text = json.dumps(record)
+    if a.record:
+        with open(a.record, "w") as f:
+            f.write(text + "\n")
+    # the whole record on stderr, then the headline object as the last stdout line
+    log(f"full record: {text}")
+    print(json.dumps(compact_line(record), separators=(",", ":")), flush=True)
+
+
+def full_record(a, cfg, sp, slots, batches, gen_len, head, extras, cpu):
+    """Everything measured in the run: the headline fields, every batch row
+    of every configuration, the kernels' timings, the H2D rates, the CPU
+    baseline and the rows with a published reference figure."""
     main_c = max(batches)
     main_row = [r for r in head["per_batch"] if r["c"] == main_c and r["routing"] != "locality"
                 and r["orchestration"] == ORCH_GRAPH][0]
@@ -836,7 +868,94 @@ def main():
         # per launch: the HBM rate a kernel that only reads reaches there
         "read_probe_GBs": g1["read_probe_GBs"], "frac_of_read_probe": g1["frac_of_read_probe"],
     }
-    print(json.dumps(line), flush=True)
+    line["gemm1"] = head["gemm1"]
+    return line
+
+
+# columns of the compact line's batch rows
+ROW_COLS = ["shape", "slots", "c", "path", "routing", "steps", "ms_per_step", "tok_per_s",
+            "misses_per_layer_step", "fast_hit_share", "h2d_GBs_in_step", "ref_tok_per_s"]
+LINE_LIMIT = 6000  # bytes; the last stdout line must stay whole in a short tail
+
+
+def _r(v, nd):
+    return None if v is None else round(float(v), nd)
+
+
+def compact_line(rec):
+    """The headline object: the contract's fields, the roofline and CPU
+    baseline, the H2D rates and one short row per measured batch of every
+    configuration (columns ROW_COLS; path "gap", "classic" or "gap/ref-orch"
+    for this build's kernels in the reference's orchestration;
+    ref_tok_per_s is the reference's published figure for that shape, slots
+    and batch, or null).  The full record is in rec["record_file"]."""
+    c = rec["config"]
+    rows, g1, g2 = [], {}, {}
+    configs = [(c["model_shape"], c["slots"], rec["per_batch"], rec.get("gemm1"),
+                rec.get("kernels", {}).get("gemm2"))]
+    configs += [(e["config"]["model_shape"], e["config"]["slots"], e["per_batch"], e.get("gemm1"),
+                 e.get("kernels", {}).get("gemm2")) for e in rec.get("extras") or []]
+    for shape, slots, per_batch, k1, k2 in configs:
+        for r in per_batch:
+            path = r["path"] + ("/ref-orch" if r["orchestration"] == ORCH_REFERENCE else "")
+            ref = None
+            if r["path"] == "gap" and r["orchestration"] == ORCH_GRAPH:
+                ref = PUBLISHED.get(shape, {}).get("tok_per_s", {}).get(slots, {}).get(r["c"])
+            routing = r["routing"] + (f"/s{r['sigma']}" if r.get("sigma") is not None else "")
+            rows.append([shape, slots, r["c"], path, routing, r.get("steps", rec["steps"]),
+                         _r(r["ms_per_step"], 3),
+                         _r(r["tok_per_s"], 1), _r(r["misses_per_layer_step"], 3),
+                         _r(r["fast_hit_share"], 3), _r(r["h2d_GBs_in_step"], 1), ref])
+        if k1:
+            key = f"{shape}/s{slots}/c{k1['c']}"
+            g1[key] = _r(k1.get("frac", k1["achieved_GBs"] / HBM_PEAK_GBS), 3)
+            if k2:
+                g2[key] = _r(k2["achieved_GBs"] / HBM_PEAK_GBS, 3)
+    roof = rec["roofline"]
+    cpu = rec.get("cpu_baseline")
+    h2d = rec.get("h2d")
+    head_rows = [r for r in rec["per_batch"] if r["c"] == c["batch"]
+                 and r["orchestration"] == ORCH_GRAPH and r["routing"] not in ("locality",
+                                                                              "matched")]
+    in_step = head_rows[0]["h2d_GBs_in_step"] if head_rows else None
+    line = {
+        "metric": rec["metric"], "value": _r(rec["value"], 2), "unit": rec["unit"],
+        "n_gpus": rec["n_gpus"], "steps": rec["steps"], "warmup": rec["warmup"],
+        "ms_per_step": _r(rec["ms_per_step"], 4), "higher_is_better": rec["higher_is_better"],
+        "scaling": rec["scaling"], "vs_baseline": _r(rec["vs_baseline"], 4),
+        "dtype": rec["dtype"], "data": rec["data"],
+        "config": {"workload": c["workload"], "model_shape": c["model_shape"],
+                   "moe_layers": c["moe_layers"], "experts": c["experts"], "top_k": c["top_k"],
+                   "slots": c["slots"], "max_bt": c["max_bt"], "batch": c["batch"],
+                   "prompt_len": c["prompt_len"], "decode_len": c["decode_len"],
+                   "routing": {k: c["routing"][k] for k in ("zipf_s", "rho", "sigma", "gate_std")
+                               if k in c["routing"]},
+                   "baseline_ref": c.get("baseline_ref")},
+        "roofline": {"bound": roof["bound"], "achieved": _r(roof["achieved"], 1),
+                     "peak": roof["peak"], "unit": roof["unit"], "frac": _r(roof["frac"], 4),
+                     "traffic": roof["traffic"], "kernel": roof["kernel"],
+                     "avg_us": _r(roof["avg_us"], 2),
+                     "algorithmic_bytes_per_launch": _r(roof["algorithmic_bytes_per_launch"], 0),
+                     "read_probe_GBs": _r(roof["read_probe_GBs"], 1),
+                     "frac_of_read_probe": _r(roof["frac_of_read_probe"], 3),
+                     "mfma_util_pct": _r(roof["mfma_util_pct"], 3),
+                     "traffic_source": roof.get("traffic_source")},
+        "cpu_baseline": None if cpu is None else {
+            "value": _r(cpu["value"], 2), "unit": cpu["unit"], "cores": cpu["cores"],
+            "kind": cpu["kind"], "sample": cpu["sample"],
+            "layer_step_ms": _r(cpu["layer_step_ms"], 2),
+            "stages_median_us": {k: _r(v, 1) for k, v in cpu["stages_median_us"].items()}},
+        "h2d": None if h2d is None else {
+            "peak_pinned_GBs": _r(h2d["peak_pinned_GBs"], 1),
+            "expert_stream_GBs": _r(h2d["expert_stream_GBs"], 1),
+            "in_step_GBs": _r(in_step, 1),
+            "in_step_frac_of_peak": _r(in_step / h2d["peak_pinned_GBs"], 3)
+            if in_step is not None else None},
+        "gemm1_frac_of_8TBs": g1, "gemm2_frac_of_8TBs": g2,
+        "row_cols": ROW_COLS, "rows": rows,
+        "record_file": rec.get("record_file"),
+    }
+    return line
 
 
 if __name__ == "__main__":
