@@ -328,10 +328,13 @@ int sluice_gap_server_destroy(sluice_gap_server* server);
  * stamps up with the device's. */
 int sluice_gap_abort(int set);
 
-/* The bound of the gap's waits (device and host) for launches after the
- * call, in seconds; 0 restores SLUICE_GAP_TIMEOUT_S (default 20).  No
- * counterpart in the reference (its gap waits are host syncs without a
- * bound); it lets callers, and tests, shorten a wait that must end. */
+/* The bound of the gap's waits (device and host), in seconds; 0 restores
+ * SLUICE_GAP_TIMEOUT_S (default 20).  The device waits read the bound from
+ * a per-device word when they begin, so it applies to every wait that
+ * begins after the call, in direct launches and in graphs captured before
+ * it alike.  No counterpart in the reference (its gap waits are host syncs
+ * without a bound); it lets callers, and tests, shorten a wait that must
+ * end. */
 int sluice_gap_set_timeout(double seconds);
 
 /* on=1 (default): a gap that streams misses is answered before the rows
@@ -342,7 +345,31 @@ int sluice_gap_set_timeout(double seconds);
  * outputs are the same either way.  Applies to records served after the
  * call. */
 int sluice_gap_set_pipelined(int on);
+
+/* After an abort or a failed gap, once every stream that ran the layer's
+ * gap kernels is synchronised: drains the copy lanes, lines the host's
+ * stamps up with the device's, clears the pending-slot marks and writes the
+ * host's standing map into the device map (which may lag the slot cache:
+ * a device wait that ended after the host served its record, or fills
+ * dropped after a failed copy).  No counterpart in the reference, whose gap
+ * errors end the engine. */
 int sluice_layer_gap_resync(sluice_layer* layer);
+
+/* Recovery from a fill whose rows did not land: the expert in `slot` leaves
+ * the slot cache (its segment, slot_of, expert_in_slot), the slot goes back
+ * on the free list (taken next) and the map stops being the standing map,
+ * so the next gap selecting the expert misses and streams it again.  The
+ * served gap does this itself for every fill of a failed stream-in that was
+ * not seen to land.  SLUICE_E_STATE for an empty or pinned slot.  No
+ * counterpart in the reference (its copy errors end the engine). */
+int sluice_layer_unfill(sluice_layer* layer, int slot);
+
+/* Failure injection for tests of the recovery path, forced from the host:
+ * the (after+1)-th row copy a served gap issues from now on is not issued
+ * and reports hipErrorInvalidValue, once; after < 0 disarms.  Every kernel
+ * still exits normally (the failed gap's slots are marked ready, the
+ * failure is reported).  No counterpart in the reference. */
+int sluice_gap_inject_copy_failure(int after);
 
 /* The gap, host path (no HIP calls): ids is a host array.  Runs the same
  * bookkeeping and reports the (local, slot) stream-ins in order in

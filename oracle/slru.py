@@ -157,6 +157,24 @@ class LayerCache:
             self.protected_cap -= 1
         return slot
 
+    def unfill(self, slot: int) -> bool:
+        """Recovery after a fill whose rows did not land (a failed copy): the
+        slot's expert leaves the cache and the slot goes back on the free list
+        (popped next); the map stops being standing.  No reference
+        counterpart (the reference's copy errors end the engine): these are
+        this build's recovery semantics, stated here so the native cache can
+        be checked against them."""
+        local = self.expert_in_slot[slot]
+        if local is None or slot in self.pinned_slots:
+            return False
+        self.probation.pop(slot, None)
+        self.protected.pop(slot, None)
+        self.slot_of.pop(local, None)
+        self.expert_in_slot[slot] = None
+        self.free_slots.append(slot)
+        self.map_is_standing = False
+        return True
+
     # -- maps ------------------------------------------------------------
     def standing_map(self) -> list[int]:
         m = [-1] * self.global_n

@@ -86,6 +86,8 @@ SIGNATURES = {
     "sluice_gap_set_timeout": (c_int, [c_double]),
     "sluice_gap_set_pipelined": (c_int, [c_int]),
     "sluice_layer_gap_resync": (c_int, [_P]),
+    "sluice_layer_unfill": (c_int, [_P, c_int]),
+    "sluice_gap_inject_copy_failure": (c_int, [c_int]),
     "sluice_layer_gap_host": (
         c_int, [_P, _P, c_int, c_int, _P, c_int, POINTER(c_int), POINTER(c_int)]
     ),

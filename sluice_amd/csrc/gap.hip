@@ -217,8 +217,9 @@ __host__ __device__ inline int32_t stamp_dist(int32_t a, int32_t b) {
 // that record s's slot is free; the last value read goes to *seen.  0, or
 // SLUICE_E_ABORTED / SLUICE_E_TIMEOUT.
 __device__ int wait_slot(const int32_t* p, int32_t s, const int32_t* abort_flag,
-                         long long timeout_ticks, int32_t* seen) {
+                         const long long* bound, int32_t* seen) {
   const long long t0 = wall_clock64();
+  const long long timeout_ticks = *bound;
   for (;;) {
     const int32_t v = ld_host(p);
     *seen = v;
@@ -233,8 +234,9 @@ __device__ int wait_slot(const int32_t* p, int32_t s, const int32_t* abort_flag,
 // what the host wrote before *p).  0, or SLUICE_E_ABORTED / SLUICE_E_TIMEOUT.
 template <bool ACQ>
 __device__ int wait_eq(const int32_t* p, int32_t want, const int32_t* abort_flag,
-                       long long timeout_ticks) {
+                       const long long* bound) {
   const long long t0 = wall_clock64();
+  const long long timeout_ticks = *bound;
   for (;;) {
     if (ld_host(p) == want) {
       if (ACQ) (void)ld_sys(p);
@@ -259,7 +261,7 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     const int32_t* __restrict__ ids, int n, int32_t* __restrict__ map,
     const int32_t* __restrict__ local_of, int E, GapMailbox* mb, int32_t* dev_state,
     int32_t* __restrict__ pending, int32_t* __restrict__ prev, int S, const int32_t* abort_flag,
-    long long timeout_ticks, const u32x4_t* __restrict__ copy_src, u32x4_t* __restrict__ copy_dst,
+    const long long* bound, const u32x4_t* __restrict__ copy_src, u32x4_t* __restrict__ copy_dst,
     int copy_vecs, int32_t* __restrict__ plan) {
   __shared__ int present[SLUICE_MAX_EXPERTS];
   __shared__ sluice_plan::Scratch psc;
@@ -353,7 +355,7 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     s_stamp = s;
     s_status = 0;
     if (stamp_dist(s, seen) > kRing)
-      s_status = wait_slot(&mb->ack_stamp, s, abort_flag, timeout_ticks, &seen);
+      s_status = wait_slot(&mb->ack_stamp, s, abort_flag, bound, &seen);
     if (fresh) dev_state[2] = seen;
     s_waits = 0;
     if (s_status == 0) {
@@ -395,7 +397,7 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
   }
   if (s_waits) {
     if (tid == 0) {
-      const int st = wait_eq<true>(&mb->resp_stamp, s_stamp, abort_flag, timeout_ticks);
+      const int st = wait_eq<true>(&mb->resp_stamp, s_stamp, abort_flag, bound);
       s_status = st != 0 ? st : ld_sys(&mb->resp_code);
       if (st != 0) st_host(&mb->dev_status, st);
     }
@@ -472,9 +474,18 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kLanes = 2;
 
+double gap_timeout_s();
+long long bound_ticks(long long clock_khz) {
+  return (long long)(gap_timeout_s() * 1000.0 * (double)clock_khz);
+}
+
 struct DeviceRes {
   hipStream_t copy[kLanes] = {};
   long long clock_khz = 0;
+  // device word: the bound of every device wait, in wall-clock ticks; the
+  // kernels read it when they start to wait (sluice_gap_set_timeout
+  // rewrites it, so graphs captured earlier follow the new bound)
+  long long* bound_dev = nullptr;
 };
 constexpr int kMaxDevices = 64;
 DeviceRes g_dev[kMaxDevices];
@@ -492,6 +503,13 @@ int device_res(int dev, DeviceRes** out) {
     for (hipStream_t& s : r.copy)
       if (s == nullptr) SLUICE_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
     r.clock_khz = khz > 0 ? khz : 100000;
+  }
+  if (r.bound_dev == nullptr) {
+    long long* b = nullptr;
+    SLUICE_HIP_CHECK(hipMalloc((void**)&b, 256));
+    const long long ticks = bound_ticks(r.clock_khz);
+    SLUICE_HIP_CHECK(hipMemcpy(b, &ticks, sizeof(ticks), hipMemcpyHostToDevice));
+    r.bound_dev = b;
   }
   if (g_abort_host == nullptr) {
     void* p = nullptr;
@@ -516,6 +534,10 @@ double now_s() {
 // The bound of every gap wait (device and host), in seconds: set by
 // sluice_gap_set_timeout, else SLUICE_GAP_TIMEOUT_S, else 20.
 std::atomic<double> g_timeout_set{0.0};
+
+// Failure injection (sluice_gap_inject_copy_failure): row copies a served
+// gap may still issue before one fails; < 0 = disarmed.
+std::atomic<int> g_fail_after{-1};
 
 // Whether a missing gap is answered before its rows land (the expert
 // product then waits per filled slot) or, as the reference orders it, only
@@ -609,7 +631,8 @@ int layer_device_init(sluice_layer* L) {
     w.seen = w.claim + S;
     w.abort_flag = g_abort_dev;
     w.status = &L->mb_dev->dev_status;
-    slotwait_register(L->map_dev, w, R->clock_khz);
+    w.bound = R->bound_dev;
+    slotwait_register(L->map_dev, w);
   }
   return SLUICE_OK;
 }
@@ -761,9 +784,14 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     for (int i = 0; rc == SLUICE_OK && i < n_streams; ++i) {
       const int local = L->streams[2 * i], slot = L->streams[2 * i + 1];
       for (const ParamRows& p : L->params) {
-        hipError_t e = hipMemcpyAsync(p.slot_base + (size_t)slot * p.row_bytes,
-                                      p.host_base + (size_t)local * p.row_bytes, p.row_bytes,
-                                      hipMemcpyHostToDevice, R->copy[p.lane]);
+        int left = g_fail_after.load(std::memory_order_relaxed);
+        while (left >= 0 && !g_fail_after.compare_exchange_weak(left, left - 1)) {
+        }
+        hipError_t e = left == 0 ? hipErrorInvalidValue
+                                 : hipMemcpyAsync(p.slot_base + (size_t)slot * p.row_bytes,
+                                                  p.host_base + (size_t)local * p.row_bytes,
+                                                  p.row_bytes, hipMemcpyHostToDevice,
+                                                  R->copy[p.lane]);
         if (e != hipSuccess) {
           rc = (int)e;
           break;
@@ -788,6 +816,7 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     if (!answered) respond(L, want, SLUICE_OK, n_streams);
     // Each group of experts landed: mark its slots ready for this gap.
     int marked = 0;  // streams whose slots are marked
+    int landed = 0;  // streams whose group's copies completed
     for (int g = 0; g < issued; ++g) {
       int w = SLUICE_OK;
       for (int l = 0; l < kLanes && w == SLUICE_OK; ++l)
@@ -796,17 +825,23 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
         if (rc == SLUICE_OK) rc = w;
         break;
       }
+      landed = std::min(n_streams, (g + 1) * per_event);
       if (!early) continue;
-      const int end = std::min(n_streams, (g + 1) * per_event);
-      for (; marked < end; ++marked)
+      for (; marked < landed; ++marked)
         __atomic_store_n(&mb->slot_ready[L->streams[2 * marked + 1]], want, __ATOMIC_RELEASE);
     }
-    // A failed stream-in is reported to the caller (and, under the server,
-    // raises the abort flag): the device must not wait for rows that are
-    // not coming, so the rest of the answered slots are marked too.
-    if (early && rc != SLUICE_OK)
-      for (; marked < n_streams; ++marked)
-        __atomic_store_n(&mb->slot_ready[L->streams[2 * marked + 1]], want, __ATOMIC_RELEASE);
+    if (rc != SLUICE_OK) {
+      // A failed stream-in is reported to the caller (and, under the server,
+      // raises the abort flag).  The device must not wait for rows that are
+      // not coming, so the rest of the answered slots are marked too; and the
+      // experts whose rows were not seen to land leave the slot cache, so
+      // that no later gap takes them as hits.  The device map still holds
+      // them until sluice_layer_gap_resync writes the host's.
+      if (early)
+        for (; marked < n_streams; ++marked)
+          __atomic_store_n(&mb->slot_ready[L->streams[2 * marked + 1]], want, __ATOMIC_RELEASE);
+      for (int i = landed; i < n_streams; ++i) (void)L->c.unfill(L->streams[2 * i + 1]);
+    }
     if (early) {
       L->done_stamp.store(want, std::memory_order_release);
       return rc;
@@ -818,11 +853,6 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
   return rc;
 }
 
-long long timeout_ticks(const sluice_layer* L) {
-  const long long khz = g_dev[L->device].clock_khz;
-  return (long long)(gap_timeout_s() * 1000.0 * (double)khz);
-}
-
 int launch_gap(sluice_layer* L, const int32_t* ids, int n, const void* hs_src, void* hs_dst,
                size_t hs_bytes, int32_t* plan, hipStream_t st) {
   if ((hs_bytes & 15) != 0 || ((uintptr_t)hs_src & 15) != 0 || ((uintptr_t)hs_dst & 15) != 0)
@@ -832,7 +862,7 @@ int launch_gap(sluice_layer* L, const int32_t* ids, int n, const void* hs_src, v
   int32_t* pending = L->dev_block + E + 3;
   hipLaunchKernelGGL(gap_kernel, dim3(1), dim3(kLookupThreads), 0, st, ids, n, L->map_dev,
                      L->dev_block, E, L->mb_dev, L->dev_block + E, pending, pending + S, S,
-                     g_abort_dev, timeout_ticks(L), (const u32x4_t*)hs_src, (u32x4_t*)hs_dst,
+                     g_abort_dev, g_dev[L->device].bound_dev, (const u32x4_t*)hs_src, (u32x4_t*)hs_dst,
                      (int)(hs_bytes / 16), plan);
   return (int)hipGetLastError();
 }
@@ -1050,8 +1080,39 @@ extern "C" int sluice_gap_server_destroy(sluice_gap_server* S) {
 
 extern "C" int sluice_gap_set_timeout(double seconds) {
   if (!(seconds >= 0.0) || seconds > 86400.0) return SLUICE_E_INVAL;
+  std::lock_guard<std::mutex> lk(g_dev_mu);
   g_timeout_set.store(seconds, std::memory_order_relaxed);
+  // every device's bound word follows (the kernels read it when they wait);
+  // no HIP call before any device was set up
+  bool any = false;
+  for (int d = 0; d < kMaxDevices; ++d) any = any || g_dev[d].bound_dev != nullptr;
+  if (!any) return SLUICE_OK;
+  int cur = -1;
+  SLUICE_HIP_CHECK(hipGetDevice(&cur));
+  int rc = SLUICE_OK;
+  for (int d = 0; d < kMaxDevices && rc == SLUICE_OK; ++d) {
+    if (g_dev[d].bound_dev == nullptr) continue;
+    const long long ticks = bound_ticks(g_dev[d].clock_khz);
+    hipError_t e = hipSetDevice(d);
+    if (e == hipSuccess)
+      e = hipMemcpy(g_dev[d].bound_dev, &ticks, sizeof(ticks), hipMemcpyHostToDevice);
+    if (e != hipSuccess) rc = (int)e;
+  }
+  const hipError_t e = hipSetDevice(cur);
+  if (rc == SLUICE_OK && e != hipSuccess) rc = (int)e;
+  return rc;
+}
+
+extern "C" int sluice_gap_inject_copy_failure(int after) {
+  g_fail_after.store(after < 0 ? -1 : after, std::memory_order_relaxed);
   return SLUICE_OK;
+}
+
+extern "C" int sluice_layer_unfill(sluice_layer* L, int slot) {
+  if (L == nullptr || slot < 0 || slot >= L->c.S) return SLUICE_E_INVAL;
+  if (L->server != nullptr) return SLUICE_E_STATE;
+  std::lock_guard<std::mutex> lk(L->mu);
+  return L->c.unfill(slot) ? SLUICE_OK : SLUICE_E_STATE;
 }
 
 extern "C" int sluice_gap_set_pipelined(int on) {
@@ -1069,13 +1130,32 @@ extern "C" int sluice_gap_abort(int set) {
 // After an abort: once every stream that ran gap kernels is synchronised,
 // clear the abort flag and line the host's stamps up with the device's, so
 // the layers can be used again (their slot state is whatever the served
-// records left; the aborted steps' outputs are invalid).
+// records left; the aborted steps' outputs are invalid).  The device map
+// may lag the host's slot cache (a device wait that ended after the host
+// served the record, or fills dropped after a failed copy): the copy lanes
+// are drained and the host's standing map is written to the device, which
+// then holds the standing map again.
 extern "C" int sluice_layer_gap_resync(sluice_layer* L) {
   if (L == nullptr || L->mb == nullptr || L->server != nullptr) return SLUICE_E_INVAL;
+  DeviceRes* R = nullptr;
+  const int rrc = device_res(L->device, &R);
+  if (rrc != SLUICE_OK) return rrc;
+  for (hipStream_t s : R->copy) SLUICE_HIP_CHECK(hipStreamSynchronize(s));
   int32_t dev_stamp = 0;
   SLUICE_HIP_CHECK(hipMemcpy(&dev_stamp, L->dev_block + L->c.E, sizeof(int32_t),
                              hipMemcpyDeviceToHost));
   std::lock_guard<std::mutex> lk(L->mu);
+  {
+    std::vector<int32_t> m((size_t)L->c.E);
+    L->c.standing_map(m.data());
+    SLUICE_HIP_CHECK(hipMemcpy(L->map_dev, m.data(), sizeof(int32_t) * m.size(),
+                               hipMemcpyHostToDevice));
+    const int32_t one = 1;  // the device's "standing map seen" word
+    SLUICE_HIP_CHECK(hipMemcpy(L->dev_block + L->c.E + 1, &one, sizeof(int32_t),
+                               hipMemcpyHostToDevice));
+    L->c.map_is_standing = true;
+    __atomic_store_n(&L->mb->standing, 1, __ATOMIC_RELEASE);
+  }
   L->host_stamp = dev_stamp;
   L->done_stamp.store(dev_stamp);
   __atomic_store_n(&L->mb->ack_stamp, dev_stamp, __ATOMIC_RELEASE);
@@ -1560,28 +1640,25 @@ extern "C" const char* sluice_strerror(int code) {
 
 // ---------------------------------------------------------------------------
 // Slot-wait registry: a streaming layer's expert map -> its slot-wait view
-// (and its device's wall-clock rate, so a lookup carries the wait bound in
-// force at the launch it serves).
+// (with its device's bound word, which the kernels read when they wait).
 // ---------------------------------------------------------------------------
 namespace {
 struct WaitEntry {
   const int32_t* map;
   SlotWait w;
-  long long clock_khz;
 };
 std::mutex g_wait_mu;
 std::vector<WaitEntry> g_wait;
 }  // namespace
 
-void slotwait_register(const int32_t* map, const SlotWait& w, long long clock_khz) {
+void slotwait_register(const int32_t* map, const SlotWait& w) {
   std::lock_guard<std::mutex> lk(g_wait_mu);
   for (auto& e : g_wait)
     if (e.map == map) {
       e.w = w;
-      e.clock_khz = clock_khz;
       return;
     }
-  g_wait.push_back({map, w, clock_khz});
+  g_wait.push_back({map, w});
 }
 
 void slotwait_unregister(const int32_t* map) {
@@ -1596,10 +1673,6 @@ void slotwait_unregister(const int32_t* map) {
 SlotWait slotwait_lookup(const int32_t* map) {
   std::lock_guard<std::mutex> lk(g_wait_mu);
   for (const auto& e : g_wait)
-    if (e.map == map) {
-      SlotWait w = e.w;
-      w.timeout_ticks = (long long)(gap_timeout_s() * 1000.0 * (double)e.clock_khz);
-      return w;
-    }
+    if (e.map == map) return e.w;
   return SlotWait{};
 }

@@ -319,6 +319,7 @@ __device__ __forceinline__ void await_slot(const SlotWait& w, int slot_field) {
         __hip_atomic_load(&w.seen[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != p) {
       const bool poller = atomicExch(&w.claim[slot], p) != p;
       const long long t0 = wall_clock64();
+      const long long lim = w.bound != nullptr ? *w.bound : kDefaultWaitTicks;
       int st = 0;
       if (poller) {
         for (unsigned it = 1;; ++it) {
@@ -329,7 +330,7 @@ __device__ __forceinline__ void await_slot(const SlotWait& w, int slot_field) {
             st = SLUICE_E_ABORTED;
             break;
           }
-          if (wall_clock64() - t0 > w.timeout_ticks) {
+          if (wall_clock64() - t0 > lim) {
             st = SLUICE_E_TIMEOUT;
             break;
           }
@@ -349,7 +350,7 @@ __device__ __forceinline__ void await_slot(const SlotWait& w, int slot_field) {
               __hip_atomic_load(&w.seen[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           if (v == p || v == kSeenFailed) break;
           // the poller's own bound ends every wait; this one is a backstop
-          if (wall_clock64() - t0 > w.timeout_ticks) break;
+          if (wall_clock64() - t0 > lim) break;
           __builtin_amdgcn_s_sleep(32);
         }
       }
@@ -692,10 +693,13 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_kernel(const uint16_t* __r
 }
 
 // Bounded wait (thread 0) until *count reaches `want`; a bound reached is
-// recorded as a timeout in the status word (when there is one).
-__device__ __forceinline__ void wait_count(const int32_t* count, int want, long long ticks,
+// recorded as a timeout in the status word (when there is one).  The bound
+// is twice the slot wait's: the items counted wait for their slot (bounded
+// by it) and then compute.
+__device__ __forceinline__ void wait_count(const int32_t* count, int want, const long long* bound,
                                            int32_t* status) {
   const long long t0 = wall_clock64();
+  const long long ticks = 2 * (bound != nullptr ? *bound : kDefaultWaitTicks);
   while (__hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < want) {
     if (wall_clock64() - t0 > ticks) {
       if (status != nullptr)
@@ -726,7 +730,7 @@ template <bool FP8>
 __global__ __launch_bounds__(kThreads) void moe_gemm2_split_kernel(
     const uint16_t* __restrict__ x, uint16_t* __restrict__ act, ExpertW W,
     const int32_t* __restrict__ plan, const float* __restrict__ topk_w, CallShape cs,
-    float* __restrict__ partial, int32_t* __restrict__ handoff, long long spin_ticks) {
+    float* __restrict__ partial, int32_t* __restrict__ handoff) {
   __shared__ ItemLds lds;
   __shared__ int s_ticket;
   const int n_groups = g2_groups(cs.H, FP8), n_tiles = cs.I / 16;
@@ -762,7 +766,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_split_kernel(
     const int pb = (t - n_g1) / n_groups, g = (t - n_g1) - pb * n_groups;
     block_at(plan, W, cs, n_res + pb, col, slot_field, pair);
     await_slot(W.wait, slot_field);
-    if (threadIdx.x == 0) wait_count(done + pb, n_tiles, spin_ticks, W.wait.status);
+    if (threadIdx.x == 0) wait_count(done + pb, n_tiles, W.wait.bound, W.wait.status);
     __syncthreads();
     run_g2<FP8, kTokCoh>(act, W, cs, slot_field & kSlotMask, pair, g, topk_w, partial, lds);
   }
@@ -772,31 +776,44 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_split_kernel(
 //                  + sum_v partial[T*k + v*T + t, h] + shared[t, h]),
 // j and v ascending, for 4 consecutive columns at h: the routed pairs
 // scaled, the shared experts' virtual experts (n_sh <= kMaxShared) and a
-// precomputed shared output added unscaled.  Every load is issued up front
-// (rows of invalid pairs are read and not added), so the thread waits on
-// memory once.
+// precomputed shared output added unscaled.  Only rows that are added are
+// loaded.  The shared groups present are known from the arguments; whether
+// a routed pair is valid is a plan word.  SPEC (decode-sized calls, where
+// every pair inside the router-split envelope is valid and the kernel is
+// latency-bound): the valid words and the rows go out together and the
+// thread waits on memory once; a row whose pair turns out invalid is read
+// and not added.  !SPEC (large calls: prefill chunks, classic waves, where
+// many pairs of a wave are invalid and the kernel is bandwidth-bound): the
+// valid words first, then only the valid rows.
 constexpr int kMaxShared = 4;
+// partial bytes of a call above which the combine reads valid words first
+constexpr long kCombineCheckFirstBytes = 2L << 20;
 
+template <bool SPEC>
 __device__ __forceinline__ void combine4(const float* __restrict__ partial,
                                          const int32_t* __restrict__ valid, int t, int T, int k,
                                          int n_sh, int H, int h, float scale,
                                          const uint16_t* __restrict__ shared,
                                          uint16_t* __restrict__ out) {
   auto ld = [&](int p) { return *reinterpret_cast<const f32x4_t*>(partial + (size_t)p * H + h); };
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
   f32x4_t v[SLUICE_MAX_TOPK], vs[kMaxShared];
   bool ok[SLUICE_MAX_TOPK];
   u32x2_t sh = {0u, 0u};
   if (shared != nullptr) sh = *reinterpret_cast<const u32x2_t*>(shared + (size_t)t * H + h);
 #pragma unroll
+  for (int j = 0; j < SLUICE_MAX_TOPK; ++j) ok[j] = j < k && valid[t * k + j] != 0;
+#pragma unroll
   for (int j = 0; j < SLUICE_MAX_TOPK; ++j) {
-    const int p = t * k + (j < k ? j : k - 1);
-    ok[j] = j < k && valid[p] != 0;
-    v[j] = ld(p);
+    if (SPEC)
+      v[j] = j < k ? ld(t * k + j) : zero;
+    else
+      v[j] = ok[j] ? ld(t * k + j) : zero;
   }
   const int P = T * k;
 #pragma unroll
-  for (int u = 0; u < kMaxShared; ++u) vs[u] = ld(u < n_sh ? P + u * T + t : t * k);
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, acs = acc;
+  for (int u = 0; u < kMaxShared; ++u) vs[u] = u < n_sh ? ld(P + u * T + t) : zero;
+  f32x4_t acc = zero, acs = zero;
 #pragma unroll
   for (int j = 0; j < SLUICE_MAX_TOPK; ++j)
     if (ok[j]) acc += v[j];
@@ -814,13 +831,14 @@ __device__ __forceinline__ void combine4(const float* __restrict__ partial,
       u32x2_t{pack2_bf16(o[0], o[1]), pack2_bf16(o[2], o[3])};
 }
 
+template <bool SPEC>
 __global__ __launch_bounds__(256) void moe_combine_kernel(
     const float* __restrict__ partial, const int32_t* __restrict__ valid, int T, int k, int n_sh,
     int H, float scale, const uint16_t* __restrict__ shared, uint16_t* __restrict__ out) {
   const int t = blockIdx.y;
   const int h = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (h >= H) return;
-  combine4(partial, valid, t, T, k, n_sh, H, h, scale, shared, out);
+  combine4<SPEC>(partial, valid, t, T, k, n_sh, H, h, scale, shared, out);
 }
 
 // ---------------------------------------------------------------------------
@@ -876,14 +894,6 @@ long split_grid_for(int P, int P2, int I, int n_groups) {
   return g <= kSplitGridMax ? g : 0;
 }
 
-// Bound of a split-launch wait for a pending block's gemm1 items: they wait
-// for the block's slot (bounded by the slot wait's own bound) and then
-// compute, so twice that bound, or 20 s at the 100 MHz wall clock when the
-// call has none.
-long long split_spin_ticks(const SlotWait& w) {
-  return w.timeout_ticks > 0 ? 2 * w.timeout_ticks : 2000000000LL;
-}
-
 // The align kernel stages the map of all E experts in LDS.
 int check_common(int T, int H, int I, int k, int E, int S, int n_sh, const void* x,
                  const void* w13, const void* w2, const float* tw, const int32_t* ti,
@@ -907,8 +917,12 @@ int check_common(int T, int H, int I, int k, int E, int S, int n_sh, const void*
 int launch_combine(const float* partial, const int32_t* valid, int T, int k, int n_sh, int H,
                    float scale, const void* shared, void* out, hipStream_t st) {
   dim3 grid((H / 4 + 255) / 256, T);
-  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, st, partial, valid, T, k, n_sh, H,
-                     scale, (const uint16_t*)shared, (uint16_t*)out);
+  if ((long)T * k * H * (long)sizeof(float) > kCombineCheckFirstBytes)
+    hipLaunchKernelGGL(moe_combine_kernel<false>, grid, dim3(256), 0, st, partial, valid, T, k,
+                       n_sh, H, scale, (const uint16_t*)shared, (uint16_t*)out);
+  else
+    hipLaunchKernelGGL(moe_combine_kernel<true>, grid, dim3(256), 0, st, partial, valid, T, k,
+                       n_sh, H, scale, (const uint16_t*)shared, (uint16_t*)out);
   return (int)hipGetLastError();
 }
 
@@ -941,8 +955,7 @@ int run_experts(const void* x, const ExpertW& W, const float* tw, const int32_t*
                        (const uint16_t*)x, Ww, plan, cs, w.act, w.handoff);
     SLUICE_HIP_CHECK(hipGetLastError());
     hipLaunchKernelGGL((moe_gemm2_split_kernel<FP8>), dim3((unsigned)split_grid), dim3(kThreads),
-                       0, st, (const uint16_t*)x, w.act, Ww, plan, tw, cs, w.partial, w.handoff,
-                       split_spin_ticks(Ww.wait));
+                       0, st, (const uint16_t*)x, w.act, Ww, plan, tw, cs, w.partial, w.handoff);
     SLUICE_HIP_CHECK(hipGetLastError());
   } else {
     hipLaunchKernelGGL((moe_gemm1_kernel<FP8>), dim3(grid_for(P2, I / 16)), dim3(kThreads), 0,

@@ -24,12 +24,17 @@ struct SlotWait {
   int32_t* seen = nullptr;              // device [S]: the stamp whose ready mark was seen
   const int32_t* abort_flag = nullptr;  // host-mapped process-wide abort flag
   int32_t* status = nullptr;            // host-mapped: first failed wait
-  long long timeout_ticks = 0;          // bound of one wait (wall-clock ticks)
+  // device word: bound of one wait in wall-clock ticks, read by the kernel
+  // when it starts to wait, so a graph captured earlier follows the bound
+  // set since (sluice_gap_set_timeout rewrites the word)
+  const long long* bound = nullptr;
 };
 
+// Bound of a wait when a call has no bound word: 20 s at the 100 MHz clock.
+constexpr long long kDefaultWaitTicks = 2000000000LL;
+
 // Registry from a layer's device expert map to its slot-wait view (kept by
-// the gap layers, read by the expert product; a lookup fills timeout_ticks
-// from the wait bound in force, at the layer's device clock rate).
-void slotwait_register(const int32_t* expert_map, const SlotWait& w, long long clock_khz);
+// the gap layers, read by the expert product).
+void slotwait_register(const int32_t* expert_map, const SlotWait& w);
 void slotwait_unregister(const int32_t* expert_map);
 SlotWait slotwait_lookup(const int32_t* expert_map);

@@ -261,6 +261,25 @@ struct Cache {
     return slot;
   }
 
+  // Recovery after a fill whose rows did not land (a failed copy): the
+  // slot's expert leaves the cache -- its segment, slot_of, expert_in_slot
+  // -- and the slot goes back on the free list (popped next), so the next
+  // gap that selects the expert misses and streams it again.  The map stops
+  // being the standing map.  No counterpart in the reference, whose copy
+  // errors end the engine.  Returns false for a slot holding nothing or a
+  // pinned expert (pins are loaded once, at install).
+  bool unfill(int slot) {
+    if (slot < 0 || slot >= S) return false;
+    const int l = expert_in_slot[slot];
+    if (l < 0 || seg[slot] == kPinned) return false;
+    if (seg[slot] != kNone) unlink(slot);
+    slot_of[l] = -1;
+    expert_in_slot[slot] = -1;
+    free_slots.push_back(slot);
+    map_is_standing = false;
+    return true;
+  }
+
   // Static pin / full-residency pre-fill: take the next free slot outside
   // both segments (src/sluice/offloader.py:1046-1083, 1000-1010).
   int pin(int local, bool debit_protected) {

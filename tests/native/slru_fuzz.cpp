@@ -119,6 +119,19 @@ int main(int argc, char** argv) {
           for (int g : uniq)
             if (lof[g] >= 0 && c.slot_of[lof[g]] < 0)
               return fail("selected expert not resident after gap", cfg, step, g, 0);
+        // now and then the fills' copies fail: the tail of the streams leaves
+        // the cache again (recovery), and a random slot is asked to as well
+        if (!streams.empty() && uni(0, 4) == 0) {
+          const int ns = (int)streams.size() / 2, landed = uni(0, ns - 1);
+          for (int i = landed; i < ns; ++i) {
+            const int slot = streams[2 * i + 1];
+            const bool pinned = c.seg[slot] == slru::kPinned;
+            if (c.unfill(slot) == pinned) return fail("unfill of a fill", cfg, step, slot, 0);
+          }
+          const int s = uni(0, S - 1);
+          const bool had = c.expert_in_slot[s] >= 0 && c.seg[s] != slru::kPinned;
+          if (c.unfill(s) != had) return fail("unfill of a random slot", cfg, step, s, 0);
+        }
       } else {
         const int n = (int)ids.size();
         if (uni(0, 9) == 0) ids[uni(0, n - 1)] = E + uni(0, 5);  // out-of-range ids are ignored

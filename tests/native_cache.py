@@ -53,6 +53,14 @@ class NativeCache:
         rc = self.lib.sluice_layer_pin(self.h, local, int(debit), ctypes.byref(s))
         return None if rc else s.value
 
+    def unfill(self, slot):
+        """True when the slot's expert left the cache."""
+        rc = self.lib.sluice_layer_unfill(self.h, slot)
+        if rc == _lib.SLUICE_E_STATE:
+            return False
+        _lib.check(rc, "sluice_layer_unfill")
+        return True
+
     def gap(self, ids, fast_hit=False):
         """Returns (streams, overflow)."""
         arr = _lib.int32_array(ids)

@@ -205,9 +205,10 @@ def test_v3_routed_fp8_layer_against_oracle():
 
 
 
-@pytest.mark.parametrize("spec,slots,c,steps", [("v2lite", 48, 8, 24), ("qwen3", 64, 8, 16),
-                                              ("qwen3", 96, 12, 40), ("v3", 64, 8, 8)])
-def test_full_size_decode_slots_follow_the_oracle(spec, slots, c, steps):
+@pytest.mark.parametrize("spec,slots,c,steps,uniform", [
+    ("v2lite", 48, 8, 24, False), ("qwen3", 64, 8, 16, False), ("qwen3", 96, 12, 40, False),
+    ("v3", 64, 8, 8, False), ("qwen3", 32, 4, 64, True)])
+def test_full_size_decode_slots_follow_the_oracle(spec, slots, c, steps, uniform):
     """The configured models at full depth and shape (DeepSeek-V2-Lite: 26
     MoE layers of 64 experts at 48 slots; Qwen3-30B-A3B: 48 layers of 128 at
     64 and 96 slots; the DeepSeek-V3 fp8 stack: 8 layers of 256 at 64),
@@ -216,13 +217,18 @@ def test_full_size_decode_slots_follow_the_oracle(spec, slots, c, steps):
     step every layer's expert map, and at the end its slot assignment, SLRU
     segment order and counters, equal the oracle's SLRU replaying the ids the
     layer routed; the last layer's occupied slots hold their experts' host
-    rows byte for byte."""
+    rows byte for byte.  The miss-dominated stress runs the same checks:
+    Qwen3 shape at 48 layers, 32 slots, 4 tokens per step with uniform
+    i.i.d. top-8 routing, where nearly every step of every layer evicts
+    (src/sluice/offloader.py:2036-2081, the victim scan under constant
+    eviction)."""
     from oracle.slru import LayerCache
     from sluice_amd.decoder import SyntheticDecoder
 
-    print(f"full-size decode {spec} slots={slots} c={c} steps={steps}", flush=True)
+    print(f"full-size decode {spec} slots={slots} c={c} steps={steps} uniform={uniform}",
+          flush=True)
     dec = SyntheticDecoder(spec, max_batch=c, slots=slots, gen_len=steps + 16, device=DEV,
-                           host_pool="shared")
+                           host_pool="shared", uniform_routing=uniform)
     try:
         E = dec.sp["E"]
         oracles = [LayerCache(E, E, slots, dec.off.protect_frac) for _ in dec.moe_layers]
@@ -250,6 +256,8 @@ def test_full_size_decode_slots_follow_the_oracle(spec, slots, c, steps):
             misses += o.misses
         # past the cold fill: some layer evicted and streamed into used slots
         assert any(o.misses > slots for o in oracles), misses
+        if uniform:  # every layer evicts on most steps
+            assert all(o.misses > (steps + 2) * slots // 2 for o in oracles), misses
         cache = dec.caches[-1]
         occ = [(s, e) for s, e in enumerate(cache.expert_in_slot) if e is not None]
         sl = torch.tensor([s for s, _ in occ], device=DEV)

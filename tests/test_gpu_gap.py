@@ -388,9 +388,15 @@ def test_server_overflow_raises_at_drain_and_reset_resumes(monkeypatch):
     step(5, expect_overflow=True)  # 20 unique experts > 16 slots
     assert cache.expert_map_buf.cpu().tolist() == map_before
     off.reset_gaps()
+    # the reference's map variable still holds the map before the overflow,
+    # whose slots the partial acquisition has refilled; the resync installs
+    # the host's standing map on the device instead
+    oracle.map = oracle.standing_map()
+    assert cache.expert_map_buf.cpu().tolist() == oracle.map
     for _ in range(5):
         step(2)
         assert cache.expert_map_buf.cpu().tolist() == oracle.map
+    _check_slots(cache, layer)
     off.close()
 
 
@@ -435,4 +441,156 @@ def test_device_gap_with_no_tokens(monkeypatch, fast_hit):
         assert st["counters"][:3] == [oracle.gaps, oracle.misses, oracle.fast_hits], n
         assert cache.expert_map_buf.cpu().tolist() == oracle.map, n
     _check_slots(cache, layer)
+    off.close()
+
+
+def test_failed_stream_in_drops_unlanded_fills_and_resync_installs_host_map(monkeypatch):
+    """Failure handling forced from the host: in a gap whose 8 ids all miss
+    (Qwen3-sized experts, 9.4 MB each, so the fills stream in two groups of
+    5 and 3 experts with a completion event each), the 13th row copy is
+    made to fail (sluice_gap_inject_copy_failure).  The inline gap reports
+    the error; the device waited for nothing (its slots were marked ready);
+    the experts of the first group, seen to land, stay cached and hold their
+    host rows, those of the second leave the host's slot cache (their slots
+    free, taken next).  sluice_layer_gap_resync then writes the host's
+    standing map into the device map, and later gaps -- selecting the
+    dropped experts again -- follow the oracle after the same drops."""
+    from oracle.slru import LayerCache
+    from sluice_amd import _lib
+
+    E, S, k, H, I = 32, 16, 4, 2048, 768
+    print("failed stream-in: 8 misses, copy 13 fails", flush=True)
+    layer = _Layer(E, E, H=H, I=I)
+    off = _offloader(monkeypatch, S, 0.5, False)
+    off.wrap_modules(iter([layer]))
+    with torch.cuda.device(DEV):
+        off.post_init()
+    cache = off._caches[id(layer)]
+    off._rs_caches.append(cache)
+    lib = _lib.load()
+    oracle = LayerCache(E, E, S, 0.5)
+    hs = torch.zeros((2, 64), dtype=torch.bfloat16, device=DEV)
+    rng = np.random.default_rng(21)
+
+    def gap(ids_np):
+        torch.ops.vllm.sluice_stream_gap(hs[: len(ids_np) // k],
+                                         torch.from_numpy(ids_np).to(DEV).view(-1, k), 0)
+        torch.cuda.synchronize()
+
+    def check_state():
+        st = cache._state()
+        assert st["expert_in_slot"] == [-1 if v is None else v for v in oracle.expert_in_slot]
+        assert st["probation"] == list(oracle.probation)
+        assert st["protected"] == list(oracle.protected)
+        assert st["free_slots"] == list(oracle.free_slots)
+
+    for _ in range(2):
+        ids_np = rng.choice(E, 2 * k, replace=False).astype(np.int32)
+        gap(ids_np)
+        oracle.gap(ids_np.tolist())
+        check_state()
+    m = cache.expert_map_buf.cpu().tolist()
+    missing = np.array([g for g in range(E) if m[g] < 0][:2 * k], dtype=np.int32)
+    assert len(missing) == 2 * k
+    assert lib.sluice_gap_inject_copy_failure(12) == 0
+    try:
+        with pytest.raises(RuntimeError):
+            gap(missing)
+    finally:
+        lib.sluice_gap_inject_copy_failure(-1)
+    streams = oracle.gap(missing.tolist())
+    assert len(streams) == 8
+    for _, slot in streams[5:]:  # the second group's fills did not land
+        assert oracle.unfill(slot)
+    check_state()
+    assert lib.sluice_layer_gap_resync(cache.handle) == 0
+    # the device map is now the host's standing map
+    oracle.map, oracle.map_is_standing = oracle.standing_map(), True
+    assert cache.expert_map_buf.cpu().tolist() == oracle.map
+    _check_slots(cache, layer)
+    dropped = [oracle.global_of_local[loc] for loc, _ in streams[5:]]
+    for n in range(5):
+        if n == 0:  # the dropped experts are selected again: they miss and stream
+            others = rng.permutation([g for g in range(E) if g not in dropped])
+            ids_np = np.array(dropped + others[: 2 * k - len(dropped)].tolist(), np.int32)
+        else:
+            ids_np = rng.choice(E, 2 * k, replace=False).astype(np.int32)
+        gap(ids_np)
+        oracle.gap(ids_np.tolist())
+        check_state()
+        assert cache.expert_map_buf.cpu().tolist() == oracle.map, n
+    _check_slots(cache, layer)
+    off.close()
+
+
+def test_wait_bound_set_after_capture_applies_to_replays(monkeypatch):
+    """The bound of the gap's device waits is read when a wait begins, so a
+    hipGraph captured under the default bound (20 s) follows a bound set
+    after the capture: a captured gap whose ids miss, replayed unserved
+    after sluice_gap_set_timeout(0.3), ends its wait after ~0.3 s and
+    reports SLUICE_E_TIMEOUT; after a resync the layer follows the oracle.
+    (A host timer raises the abort flag after 5 s, so the replay ends even
+    if the new bound were not read.)"""
+    import threading
+    import time
+
+    from oracle.slru import LayerCache
+    from sluice_amd import _lib
+
+    E, S, k = 64, 16, 4
+    print("captured gap, bound set after capture", flush=True)
+    layer = _Layer(E, E)
+    off = _offloader(monkeypatch, S, 0.5, False)
+    off.wrap_modules(iter([layer]))
+    with torch.cuda.device(DEV):
+        off.post_init()
+    cache = off._caches[id(layer)]
+    off._rs_caches.append(cache)
+    lib = _lib.load()
+    oracle = LayerCache(E, E, S, 0.5)
+    hs = torch.zeros((2, 64), dtype=torch.bfloat16, device=DEV)
+    rng = np.random.default_rng(8)
+
+    def served_step():
+        ids_np = rng.choice(E, 2 * k, replace=False).astype(np.int32)
+        torch.ops.vllm.sluice_stream_gap(hs, torch.from_numpy(ids_np).to(DEV).view(-1, k), 0)
+        oracle.gap(ids_np.tolist(), fast_hit=False)
+        torch.cuda.synchronize()
+        assert cache.expert_map_buf.cpu().tolist() == oracle.map
+
+    for _ in range(3):
+        served_step()
+    m = cache.expert_map_buf.cpu().tolist()
+    ids = torch.from_numpy(np.array([g for g in range(E) if m[g] < 0][:2 * k],
+                                    dtype=np.int32)).to(DEV).view(-1, k)
+    stream = torch.cuda.Stream(device=DEV)
+    stream.wait_stream(torch.cuda.current_stream(DEV))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        _lib.check(lib.sluice_layer_gap_launch(cache.handle, ids.data_ptr(), ids.numel(), None,
+                                               None, 0, None, stream.cuda_stream),
+                   "sluice_layer_gap_launch")
+    torch.cuda.synchronize()
+    backstop = threading.Timer(5.0, lambda: lib.sluice_gap_abort(1))
+    assert lib.sluice_gap_set_timeout(0.3) == 0
+    try:
+        backstop.start()
+        t0 = time.time()
+        g.replay()
+        torch.cuda.synchronize()
+        waited = time.time() - t0
+        backstop.cancel()
+        print(f"  replayed wait ended after {waited:.3f} s", flush=True)
+        assert 0.25 <= waited < 4.0
+        rc = lib.sluice_layer_gap_serve(cache.handle, 0, torch.cuda.current_stream(DEV).cuda_stream)
+        assert rc == _lib.SLUICE_E_TIMEOUT
+    finally:
+        backstop.cancel()
+        lib.sluice_gap_abort(0)
+        lib.sluice_gap_set_timeout(0.0)
+    del g
+    assert cache.expert_map_buf.cpu().tolist() == oracle.map
+    assert lib.sluice_layer_gap_resync(cache.handle) == 0
+    for _ in range(4):
+        served_step()
     off.close()

@@ -217,3 +217,52 @@ def test_native_classic_argument_checks():
     assert lib.sluice_layer_classic_plan(h, arr, 3, 3, -1, -1, 1, 0, None, ctypes.byref(nw)) \
         == _lib.SLUICE_E_STATE
     assert lib.sluice_layer_classic_wave(h, 5, None) == _lib.SLUICE_E_STATE
+
+
+@pytest.mark.parametrize("E,S,k,frac,seed", [(64, 48, 6, 0.5, 11), (128, 32, 8, 0.5, 12),
+                                             (128, 64, 8, 0.0, 13)])
+def test_unfill_after_failed_fills_matches_oracle(E, S, k, frac, seed):
+    """Recovery from a stream-in whose rows did not land (the served gap drops
+    every fill of a failed stream-in that was not seen to land): the dropped
+    experts leave their segment and their slots go back on the free list
+    (taken next), the map stops being standing, and later gaps -- which
+    miss on the dropped experts and stream them again -- assign slots as the
+    oracle does after the same drops.  A free or pinned slot is refused."""
+    rnd = random.Random(seed)
+    o = LayerCache(E, E, S, frac)
+    n = NativeCache(E, E, S, frac)
+    hot = rnd.sample(range(E), min(E, 3 * S // 2))
+    dropped = 0
+    for step in range(600):
+        T = rnd.randint(1, max(1, S // k))
+        ids = [g for _ in range(T) for g in rnd.sample(hot if rnd.random() < 0.8 else
+                                                       list(range(E)), k)]
+        ws = o.gap(ids, fast_hit=True)
+        ns, _ = n.gap(ids, fast_hit=True)
+        assert [list(x) for x in ws] == ns, step
+        if ns and rnd.random() < 0.3:
+            # the copies failed after the first `landed` fills
+            landed = rnd.randint(0, len(ns) - 1)
+            for _, slot in ns[landed:]:
+                assert o.unfill(slot) and n.unfill(slot)
+                dropped += 1
+            assert not n.state()["map_is_standing"] and not o.map_is_standing
+        st = n.state()
+        snap = o.snapshot()
+        for key in ("slot_of", "probation", "protected", "free_slots"):
+            assert st[key] == snap[key], (step, key)
+        assert st["map_is_standing"] == o.map_is_standing
+        assert st["standing_map"] == o.standing_map()
+    assert dropped > 20
+    free = n.state()["free_slots"]
+    if free:
+        assert not n.unfill(free[0]) and not o.unfill(free[0])
+
+
+def test_unfill_refuses_pinned_slots():
+    o = LayerCache(16, 16, 8, 0.5)
+    n = NativeCache(16, 16, 8, 0.5)
+    s_o, s_n = o.pin(3), n.pin(3)
+    assert s_o == s_n is not None
+    assert not o.unfill(s_o) and not n.unfill(s_n)
+    assert n.state()["expert_in_slot"][s_n] == 3
