@@ -371,6 +371,22 @@ int sluice_layer_unfill(sluice_layer* layer, int slot);
  * failure is reported).  No counterpart in the reference. */
 int sluice_gap_inject_copy_failure(int after);
 
+/* Gap timeline tracing, for the -DSLUICE_TRACE build only (every call
+ * returns SLUICE_E_STATE in the default build).  The gap kernel, the expert
+ * product's split launch and the combine stamp events with the device wall
+ * clock; the host gap service stamps its steps with CLOCK_MONOTONIC.
+ * sluice_trace_read: which 0 = gap kernel ring, 1 = expert product ring
+ * (both 2^20 records of {tag << 56 | value, wall clock}, 16 bytes), 2 = host
+ * ring (2^18 records {uint32 tag, uint32 layer, int32 stamp, int32 value,
+ * double seconds}); *n = records written since the last reset (a ring keeps
+ * its last 2^20 or 2^18); out may be NULL.  sluice_trace_calibrate: n pairs of
+ * (host seconds, device wall-clock ticks mod 2^48) of the same instants up to
+ * the bus latency; returns the pairs taken.  No counterpart in the
+ * reference; diagnostics only. */
+int sluice_trace_calibrate(int n, double* host_s, unsigned long long* dev_ticks);
+int sluice_trace_read(int which, void* out, unsigned* n);
+int sluice_trace_reset(void);
+
 /* The gap, host path (no HIP calls): ids is a host array.  Runs the same
  * bookkeeping and reports the (local, slot) stream-ins in order in
  * streams[2*i], streams[2*i+1] (capacity 2*max_streams ints) and whether

@@ -13,7 +13,10 @@ import os
 from ctypes import POINTER, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libsluice_hip.so")
+# SLUICE_TRACE=1 loads the gap-timeline build (python -m sluice_amd.build
+# --trace; sluice_amd/timeline.py): the same library with trace hooks.
+LIB_PATH = os.path.join(_HERE, "libsluice_hip_trace.so" if os.environ.get("SLUICE_TRACE") == "1"
+                        else "libsluice_hip.so")
 
 SLUICE_OK = 0
 SLUICE_E_INVAL = -1
@@ -87,6 +90,9 @@ SIGNATURES = {
     "sluice_gap_set_pipelined": (c_int, [c_int]),
     "sluice_layer_gap_resync": (c_int, [_P]),
     "sluice_layer_unfill": (c_int, [_P, c_int]),
+    "sluice_trace_calibrate": (c_int, [c_int, _P, _P]),
+    "sluice_trace_read": (c_int, [c_int, _P, POINTER(ctypes.c_uint)]),
+    "sluice_trace_reset": (c_int, []),
     "sluice_gap_inject_copy_failure": (c_int, [c_int]),
     "sluice_layer_gap_host": (
         c_int, [_P, _P, c_int, c_int, _P, c_int, POINTER(c_int), POINTER(c_int)]

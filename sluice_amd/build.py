@@ -1,6 +1,7 @@
 """Build libsluice_hip.so in-tree with hipcc for gfx950.
 
-    python -m sluice_amd.build
+    python -m sluice_amd.build            # sluice_amd/libsluice_hip.so
+    python -m sluice_amd.build --trace    # sluice_amd/libsluice_hip_trace.so
 
 Each HIP source compiles to an object in parallel, then one link step makes
 ``sluice_amd/libsluice_hip.so``.  The library links against the HIP runtime
@@ -21,6 +22,9 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(HERE, "libsluice_hip.so")
+# The gap-timeline build (-DSLUICE_TRACE: csrc/trace.h), loaded instead of the
+# default library when SLUICE_TRACE=1 (sluice_amd/timeline.py sets it).
+OUT_TRACE = os.path.join(HERE, "libsluice_hip_trace.so")
 BUILD_DIR = os.path.join(ROOT, "_build")
 
 SOURCES = ["routing.hip", "gap.hip", "moe.hip", "decoder.hip", "probe.hip"]
@@ -67,15 +71,18 @@ def _run(cmd: list[str]) -> None:
             print(line, file=sys.stderr)
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, trace: bool = False) -> str:
     hipcc = _hipcc()
-    os.makedirs(BUILD_DIR, exist_ok=True)
+    bdir = os.path.join(BUILD_DIR, "trace") if trace else BUILD_DIR
+    out = OUT_TRACE if trace else OUT
+    os.makedirs(bdir, exist_ok=True)
     objs = []
     cmds = []
     for src in SOURCES:
-        obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
+        obj = os.path.join(bdir, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
-        cmds.append([hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([hipcc, *HIPCC_FLAGS, *(["-DSLUICE_TRACE"] if trace else []), "-c",
+                     os.path.join(CSRC, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
         for fut in [ex.submit(_run, c) for c in cmds]:
             fut.result()
@@ -83,14 +90,14 @@ def build(verbose: bool = False) -> str:
     tl = _torch_lib()
     if tl:
         link += [f"-L{tl}", f"-Wl,-rpath,{tl}"]
-    tmp = OUT + ".tmp"
+    tmp = out + ".tmp"
     link += ["-o", tmp]
     _run(link)
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {OUT}")
-    return OUT
+        print(f"built {out}")
+    return out
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, trace="--trace" in sys.argv[1:])

@@ -59,6 +59,7 @@
 #include "slotwait.h"
 #include "slru.h"
 #include "stamp.h"
+#include "trace.h"
 
 namespace {
 
@@ -302,6 +303,7 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
   bool fresh = false;
   if (tid == 0) {
     s = sluice_stamp::next(dev_state[0]);
+    SLUICE_TRACE_GAP(1, map, s);
     s_standing = dev_state[1];
     seen = dev_state[2];
   }
@@ -377,6 +379,7 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     for (int i = tid; i < base; i += kLookupThreads)
       st_host64(&r->ent[i], rec_word(s, (uint32_t)s_uniq[i]));
     if (tid == 0) st_host64(&r->hdr, rec_word(s, rec_hdr_hi(base, miss, s_waits)));
+    if (tid == 0) SLUICE_TRACE_GAP(2, map, s);
   }
 #pragma unroll
   for (int u = 0; u < kCopyU; ++u) {
@@ -399,6 +402,7 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     if (tid == 0) {
       const int st = wait_eq<true>(&mb->resp_stamp, s_stamp, abort_flag, bound);
       s_status = st != 0 ? st : ld_sys(&mb->resp_code);
+      SLUICE_TRACE_GAP(3, map, s_stamp);
       if (st != 0) st_host(&mb->dev_status, st);
     }
     __syncthreads();
@@ -456,6 +460,10 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
   // this gap leaves behind, staged above, so the product needs no align
   // launch of its own.
   if (plan != nullptr) (void)sluice_plan::plan_build_staged(id0, ids, n, E, S, psc, plan);
+#ifdef SLUICE_TRACE
+  __syncthreads();
+  if (tid == 0) SLUICE_TRACE_GAP(4, map, s_stamp);
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -473,6 +481,27 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
 // and 1237 us (55.95 GB/s, against 56.3 GB/s for 64 MiB copies).
 // ---------------------------------------------------------------------------
 constexpr int kLanes = 2;
+
+double now_s();
+
+#ifdef SLUICE_TRACE
+// Host ring of the gap service's steps (see trace.h).
+struct TraceHostRec {
+  uint32_t tag, layer;
+  int32_t stamp, value;
+  double t;
+};
+constexpr unsigned kTraceHostRing = 1u << 18;
+TraceHostRec g_trace_host[kTraceHostRing];
+std::atomic<unsigned> g_trace_host_n{0};
+void trace_host(uint32_t tag, const void* map, int32_t stamp, int32_t value) {
+  const unsigned i = g_trace_host_n.fetch_add(1, std::memory_order_relaxed) & (kTraceHostRing - 1);
+  g_trace_host[i] = {tag, (uint32_t)(((uintptr_t)map >> 8) & 0xffffffffu), stamp, value, now_s()};
+}
+#define SLUICE_HTRACE(tag, L, stamp, value) trace_host((tag), (L)->map_dev, (stamp), (value))
+#else
+#define SLUICE_HTRACE(tag, L, stamp, value) ((void)0)
+#endif
 
 double gap_timeout_s();
 long long bound_ticks(long long clock_khz) {
@@ -742,6 +771,7 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
   }
   L->host_stamp = want;
   __atomic_store_n(&mb->ack_stamp, want, __ATOMIC_RELEASE);
+  SLUICE_HTRACE(21, L, want, n_miss);
 
   std::lock_guard<std::mutex> lk(L->mu);
   L->streams.clear();
@@ -751,6 +781,7 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
   const bool was_standing = L->c.map_is_standing;
   const int grc = L->c.gap(L->uniq.data(), n_uniq, fast_hit, L->streams, map_write);
   const int n_streams = (int)L->streams.size() / 2;
+  SLUICE_HTRACE(22, L, want, n_streams);
   int rc = SLUICE_OK;
   if (!waits) {
     // The device ran on with its map: the host must agree nothing changed.
@@ -797,6 +828,7 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
           break;
         }
         L->bytes += (int64_t)p.row_bytes;
+        if (i == 0) SLUICE_HTRACE(23, L, want, p.lane);
       }
       if (rc == SLUICE_OK && ((i + 1) % per_event == 0 || i + 1 == n_streams)) {
         for (int l = 0; l < kLanes && rc == SLUICE_OK; ++l) {
@@ -809,11 +841,13 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
       if (!answered && rc == SLUICE_OK) {
         respond(L, want, SLUICE_OK, n_streams);
         answered = true;
+        SLUICE_HTRACE(24, L, want, per_event);
       }
     }
     // (a failure before the answer still answers the device: the map and
     // the fill list are the bookkeeping's; the slots are marked below)
     if (!answered) respond(L, want, SLUICE_OK, n_streams);
+    SLUICE_HTRACE(25, L, want, issued);
     // Each group of experts landed: mark its slots ready for this gap.
     int marked = 0;  // streams whose slots are marked
     int landed = 0;  // streams whose group's copies completed
@@ -826,9 +860,11 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
         break;
       }
       landed = std::min(n_streams, (g + 1) * per_event);
+      SLUICE_HTRACE(26, L, want, g);
       if (!early) continue;
       for (; marked < landed; ++marked)
         __atomic_store_n(&mb->slot_ready[L->streams[2 * marked + 1]], want, __ATOMIC_RELEASE);
+      SLUICE_HTRACE(27, L, want, g);
     }
     if (rc != SLUICE_OK) {
       // A failed stream-in is reported to the caller (and, under the server,
@@ -1675,4 +1711,102 @@ SlotWait slotwait_lookup(const int32_t* map) {
   for (const auto& e : g_wait)
     if (e.map == map) return e.w;
   return SlotWait{};
+}
+
+// ---------------------------------------------------------------------------
+// Gap timeline tracing (trace.h): the entry points of a -DSLUICE_TRACE build;
+// SLUICE_E_STATE otherwise.
+// ---------------------------------------------------------------------------
+int trace_moe_read(unsigned long long* out, unsigned* n);  // moe.hip
+int trace_moe_reset();
+
+namespace {
+#ifdef SLUICE_TRACE
+// One thread writes its wall clock into mapped host memory every ~20 us; the
+// host notes when each value appears.  The smallest host - device difference
+// bounds the clocks' offset (to within the bus latency).
+__global__ void trace_calib_kernel(unsigned long long* slot, int n) {
+  for (int i = 0; i < n; ++i) {
+    const unsigned long long t = wall_clock64();
+    __hip_atomic_store(slot, ((unsigned long long)(i + 1) << 48) | (t & ((1ull << 48) - 1)),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const long long t0 = wall_clock64();
+    while (wall_clock64() - t0 < 2000) __builtin_amdgcn_s_sleep(8);
+  }
+}
+#endif
+}  // namespace
+
+extern "C" int sluice_trace_calibrate(int n, double* host_s, unsigned long long* dev_ticks) {
+#ifdef SLUICE_TRACE
+  if (n <= 0 || n > 100000 || host_s == nullptr || dev_ticks == nullptr) return SLUICE_E_INVAL;
+  void* p = nullptr;
+  SLUICE_HIP_CHECK(hipHostMalloc(&p, 256, hipHostMallocCoherent | hipHostMallocMapped));
+  volatile unsigned long long* h = static_cast<volatile unsigned long long*>(p);
+  *h = 0;
+  void* dp = nullptr;
+  hipStream_t st = nullptr;
+  hipError_t e = hipHostGetDevicePointer(&dp, p, 0);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    (void)hipHostFree(p);
+    return (int)e;
+  }
+  hipLaunchKernelGGL(trace_calib_kernel, dim3(1), dim3(1), 0, st, (unsigned long long*)dp, n);
+  int seen = 0;
+  const double t0 = now_s();
+  while (seen < n && now_s() - t0 < 10.0) {
+    const unsigned long long v = *h;
+    const int i = (int)(v >> 48);
+    if (i > seen) {
+      const double t = now_s();
+      for (int j = seen; j < i - 1; ++j) {
+        host_s[j] = -1.0;
+        dev_ticks[j] = 0;
+      }
+      host_s[i - 1] = t;
+      dev_ticks[i - 1] = v & ((1ull << 48) - 1);
+      seen = i;
+    }
+  }
+  e = hipStreamSynchronize(st);
+  (void)hipStreamDestroy(st);
+  (void)hipHostFree(p);
+  return e != hipSuccess ? (int)e : seen;
+#else
+  (void)n;
+  (void)host_s;
+  (void)dev_ticks;
+  return SLUICE_E_STATE;
+#endif
+}
+
+extern "C" int sluice_trace_read(int which, void* out, unsigned* n) {
+#ifdef SLUICE_TRACE
+  if (n == nullptr) return SLUICE_E_INVAL;
+  if (which == 0) return trace_dev_read(static_cast<unsigned long long*>(out), n);
+  if (which == 1) return trace_moe_read(static_cast<unsigned long long*>(out), n);
+  if (which == 2) {
+    *n = g_trace_host_n.load();
+    if (out != nullptr) memcpy(out, g_trace_host, sizeof(g_trace_host));
+    return SLUICE_OK;
+  }
+  return SLUICE_E_INVAL;
+#else
+  (void)which;
+  (void)out;
+  (void)n;
+  return SLUICE_E_STATE;
+#endif
+}
+
+extern "C" int sluice_trace_reset(void) {
+#ifdef SLUICE_TRACE
+  int rc = trace_dev_reset();
+  if (rc == SLUICE_OK) rc = trace_moe_reset();
+  g_trace_host_n.store(0);
+  return rc;
+#else
+  return SLUICE_E_STATE;
+#endif
 }

@@ -25,6 +25,7 @@
 
 #include "common.h"
 #include "plan.h"
+#include "trace.h"
 #include "slotwait.h"
 #include "stream.h"
 
@@ -305,8 +306,10 @@ struct ExpertW {
 // memory (device reads of host memory share the link with the rows
 // streaming in; a poll every ~3.4 us measured 0.3% slower decode steps at
 // V2-Lite c=8).  Each then takes a system-scope acquire, so no
-// cache returns the slot's previous expert; the workgroup's loads follow the
-// barrier.  A failed wait is recorded in the layer's status word (the host
+// cache returns the slot's previous expert -- the poller right after the
+// relaxed load that saw the mark (a second, acquiring read of the mark cost
+// a bus round trip, ~1.1 us of every streamed layer's tail) and before it
+// publishes; the workgroup's loads follow the barrier.  A failed wait is recorded in the layer's status word (the host
 // reports it) and the item computes on whatever the slot holds.
 constexpr int32_t kSeenFailed = -1;
 
@@ -315,6 +318,7 @@ __device__ __forceinline__ void await_slot(const SlotWait& w, int slot_field) {
   if (threadIdx.x == 0) {
     const int slot = slot_field & kSlotMask;
     const int32_t p = w.pending[slot];
+    bool acquired = false;  // this thread's system-scope acquire already taken
     if (p != 0 &&
         __hip_atomic_load(&w.seen[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != p) {
       const bool poller = atomicExch(&w.claim[slot], p) != p;
@@ -336,12 +340,17 @@ __device__ __forceinline__ void await_slot(const SlotWait& w, int slot_field) {
           }
           __builtin_amdgcn_s_sleep(16);
         }
+        SLUICE_DTRACE(10, ((unsigned long long)slot << 24) | ((unsigned long long)p & 0xffffff));
         if (st != 0) {
           __hip_atomic_store(w.status, st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
           __hip_atomic_store(&w.seen[slot], kSeenFailed, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
         } else {
-          (void)__hip_atomic_load(w.ready + slot, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+          // The load that saw the mark, then a system-scope acquire fence
+          // (no second read over the bus), before the release that the
+          // others acquire through seen[].
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+          acquired = true;
           __hip_atomic_store(&w.seen[slot], p, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         }
       } else {
@@ -355,7 +364,7 @@ __device__ __forceinline__ void await_slot(const SlotWait& w, int slot_field) {
         }
       }
     }
-    if (p != 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+    if (p != 0 && !acquired) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
   }
   __syncthreads();
 }
@@ -740,6 +749,7 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_split_kernel(
   const int n_g1 = n_pend * n_tiles, n_g2 = n_pend * n_groups;
   const int col = threadIdx.x & 15;
   const int item = blockIdx.x;
+  if (item == 0 && threadIdx.x == 0) SLUICE_DTRACE(11, gridDim.x);
   int slot_field, pair;
   if (item < n_first) {
     const int bb = item / n_groups, g = item - bb * n_groups;
@@ -757,8 +767,10 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_split_kernel(
     const int pb = t / n_tiles, tile = t - pb * n_tiles;
     block_at(plan, W, cs, n_res + pb, col, slot_field, pair);
     await_slot(W.wait, slot_field);
+    if (threadIdx.x == 0) SLUICE_DTRACE(14, t);
     run_g1<FP8, true>(x, W, cs, slot_field & kSlotMask, pair, tile, act, lds);
     if (threadIdx.x == 0) atomicAdd(done + pb, 1);
+    if (threadIdx.x == 0) SLUICE_DTRACE(15, t);
   } else if (t < n_g1 + n_g2) {
     // First the slot (a gentle wait, like the gemm1 items'), then the few
     // microseconds of its gemm1 items (a tight one): a tight wait over the
@@ -767,8 +779,10 @@ __global__ __launch_bounds__(kThreads) void moe_gemm2_split_kernel(
     block_at(plan, W, cs, n_res + pb, col, slot_field, pair);
     await_slot(W.wait, slot_field);
     if (threadIdx.x == 0) wait_count(done + pb, n_tiles, W.wait.bound, W.wait.status);
+    if (threadIdx.x == 0) SLUICE_DTRACE(17, t);
     __syncthreads();
     run_g2<FP8, kTokCoh>(act, W, cs, slot_field & kSlotMask, pair, g, topk_w, partial, lds);
+    if (threadIdx.x == 0) SLUICE_DTRACE(16, t);
   }
 }
 
@@ -837,6 +851,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
     int H, float scale, const uint16_t* __restrict__ shared, uint16_t* __restrict__ out) {
   const int t = blockIdx.y;
   const int h = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) SLUICE_DTRACE(13, T);
   if (h >= H) return;
   combine4<SPEC>(partial, valid, t, T, k, n_sh, H, h, scale, shared, out);
 }
@@ -1163,4 +1178,22 @@ extern "C" int sluice_moe_combine(const float* partial, const int32_t* plan, int
     return SLUICE_E_INVAL;
   return launch_combine(partial, plan + kPlanHeader + (size_t)kBlockInts * T * k, T, k, 0, H, scale,
                         shared, out, (hipStream_t)stream);
+}
+
+// Gap timeline tracing (trace.h): this translation unit's ring.
+int trace_moe_read(unsigned long long* out, unsigned* n) {
+#ifdef SLUICE_TRACE
+  return trace_dev_read(out, n);
+#else
+  (void)out;
+  (void)n;
+  return SLUICE_E_STATE;
+#endif
+}
+int trace_moe_reset() {
+#ifdef SLUICE_TRACE
+  return trace_dev_reset();
+#else
+  return SLUICE_E_STATE;
+#endif
 }
