@@ -22,9 +22,11 @@ microseconds from the gap kernel's start):
          gemm1 counts reached (first, last) and the last done, combine
          started, next layer's gap started;
 
-and the link-idle time per step between copy windows, split into the
-transitions between consecutive layers with stream-ins and the stretches
-that cover layers without any.
+the duration of each pending item of the expert product (a gemm1 item from
+its slot wait to done, a gemm2 item from its gemm1 count to done), and the
+link-idle time per step between copy windows, split into the transitions
+between consecutive layers with stream-ins and the stretches that cover
+layers without any.
 """
 
 from __future__ import annotations
@@ -139,8 +141,21 @@ def analyse(rings, clock, layer_ids, steps, bytes_per_expert):
     moe = rings["moe"]
     mt = clock(moe[:, 1])
     mtag = (moe[:, 0] >> TAG_SHIFT).astype(int)
+    mval = (moe[:, 0] & np.uint64((1 << 56) - 1)).astype(np.int64)
     order = np.argsort(mt)
-    mt, mtag = mt[order], mtag[order]
+    mt, mtag, mval = mt[order], mtag[order], mval[order]
+    # each pending item's own duration: its two stamps paired by ticket within
+    # one split launch (tag 11 opens a launch)
+    item_g1, item_g2, open_ = [], [], {}
+    for t_, a, v in zip(mt, mtag, mval):
+        if a == 11:
+            open_ = {}
+        elif a in (14, 17):
+            open_[(a, int(v))] = t_
+        elif a == 15 and (14, int(v)) in open_:
+            item_g1.append(t_ - open_.pop((14, int(v))))
+        elif a == 16 and (17, int(v)) in open_:
+            item_g2.append(t_ - open_.pop((17, int(v))))
     gaps = sorted((v[1], k) for k, v in G.items() if 1 in v)
     starts = np.array([g[0] for g in gaps] + [np.inf])
     rows = []
@@ -190,7 +205,9 @@ def analyse(rings, clock, layer_ids, steps, bytes_per_expert):
                "marked", "ready_seen", "g1_started_first", "g1_started_last", "g1_done_first",
                "g1_done", "g2_counted_first", "g2_counted_last", "g2_done", "combine", "next")},
            "without_stream_ins": {k: stat(r[k] for r in hit) for k in ("posted", "gap_end",
-                                                                         "next")}}
+                                                                         "next")},
+           "pending_item": {"gemm1_wait_end_to_done": stat(item_g1),
+                            "gemm2_count_to_done": stat(item_g2)}}
     win = [(r["landed"] - r["first_copy"], r["streams"]) for r in miss]
     out["copy_window"] = {
         "rate_GBs_median": round(float(np.median([n * bytes_per_expert / w / 1e9
