@@ -795,7 +795,7 @@ def main():
             f.write(text + "\n")
     # the whole record on stderr, then the headline object as the last stdout line
     log(f"full record: {text}")
-    print(json.dumps(compact_line(record), separators=(",", ":")), flush=True)
+    print(json.dumps(compact_line(record), separators=(",", ":"), allow_nan=False), flush=True)
 
 
 def full_record(a, cfg, sp, slots, batches, gen_len, head, extras, cpu):
@@ -879,7 +879,11 @@ LINE_LIMIT = 6000  # bytes; the last stdout line must stay whole in a short tail
 
 
 def _r(v, nd):
-    return None if v is None else round(float(v), nd)
+    """v rounded to nd digits; None for a missing or non-finite value (the
+    line stays strict JSON)."""
+    if v is None or not np.isfinite(float(v)):
+        return None
+    return round(float(v), nd)
 
 
 def compact_line(rec):

@@ -828,7 +828,7 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
           break;
         }
         L->bytes += (int64_t)p.row_bytes;
-        if (i == 0) SLUICE_HTRACE(23, L, want, p.lane);
+        if (i == 0 && &p == &L->params[0]) SLUICE_HTRACE(23, L, want, p.lane);
       }
       if (rc == SLUICE_OK && ((i + 1) % per_event == 0 || i + 1 == n_streams)) {
         for (int l = 0; l < kLanes && rc == SLUICE_OK; ++l) {

@@ -44,7 +44,7 @@ def test_compact_line_fits_and_parses():
     import bench
 
     rec = _fixture_record()
-    text = json.dumps(bench.compact_line(rec), separators=(",", ":"))
+    text = json.dumps(bench.compact_line(rec), separators=(",", ":"), allow_nan=False)
     assert len(text.encode()) <= bench.LINE_LIMIT, len(text)
     line = json.loads(text)
     for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
@@ -79,3 +79,18 @@ def test_compact_line_stays_under_the_limit_with_every_row_doubled():
     rec["per_batch"] = rec["per_batch"] * 2
     text = json.dumps(bench.compact_line(rec), separators=(",", ":"))
     assert len(text.encode()) <= bench.LINE_LIMIT, len(text)
+
+
+def test_compact_line_is_strict_json_when_a_figure_is_missing():
+    """A non-finite figure (a row that streamed nothing, a kernel not timed)
+    becomes null, so the line parses with a strict JSON reader."""
+    import json
+
+    import bench
+
+    rec = _fixture_record()
+    rec["per_batch"][0]["h2d_GBs_in_step"] = float("nan")
+    rec["roofline"]["read_probe_GBs"] = float("inf")
+    line = json.loads(json.dumps(bench.compact_line(rec), allow_nan=False))
+    assert line["rows"][0][line["row_cols"].index("h2d_GBs_in_step")] is None
+    assert line["roofline"]["read_probe_GBs"] is None
