@@ -12,6 +12,7 @@ and the library always share one runtime.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -61,14 +62,67 @@ def _torch_lib() -> str | None:
         return None
 
 
-def _run(cmd: list[str]) -> None:
+RESOURCE_REMARKS = "-Rpass-analysis=kernel-resource-usage"
+
+
+def _run(cmd: list[str]) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
-    noise = "is not a recognized feature for this target"
+    noise = ("is not a recognized feature for this target", RESOURCE_REMARKS)
     for line in (r.stdout + r.stderr).splitlines():
-        if line.strip() and noise not in line:
+        if line.strip() and not any(n in line for n in noise) and not line.lstrip().startswith(
+                ("|", "^")) and not re.match(r"^\s*\d+ \|", line):
             print(line, file=sys.stderr)
+    return r.stdout + r.stderr
+
+
+# Room the split launch of the expert product must leave per SIMD.  Its
+# pending workgroups wait for slots while the copies that fill them run, and
+# the runtime copies small host rows (fp8 scale rows) with a kernel of its
+# own: one 512-thread workgroup (two waves per SIMD) allocating 16 VGPRs per
+# lane (the rocprofv3 kernel trace of __amd_rocclr_copyBuffer on MI355X).  If
+# the split launch's waves filled the 512-VGPR file of every SIMD, such a copy
+# could not start while they wait and the waits would run to their bound.
+VGPR_FILE = 512
+COPY_KERNEL_VGPRS_PER_SIMD = 2 * 16
+WAITING_KERNELS = ("moe_gemm2_split_kernel",)
+
+
+def kernel_resources(remarks: str) -> dict[str, dict[str, int]]:
+    """{mangled kernel name: {"VGPRs", "AGPRs", "Occupancy"}} from hipcc's
+    kernel-resource-usage remarks."""
+    out: dict[str, dict[str, int]] = {}
+    cur = None
+    for line in remarks.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            cur = out.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"remark:\s+(VGPRs|AGPRs|Occupancy \[waves/SIMD\]): (\d+)", line)
+        if m and cur is not None:
+            cur[m.group(1).split()[0]] = int(m.group(2))
+    return out
+
+
+def vgpr_alloc(vgprs: int, agprs: int) -> int:
+    """VGPRs a wave holds in gfx950's unified register file: the arch VGPRs
+    rounded up to 4, the AGPRs after them, the total in granules of 8."""
+    return -(-(-(-vgprs // 4) * 4 + agprs) // 8) * 8
+
+
+def check_wait_room(remarks: str) -> list[str]:
+    """Names of waiting kernels whose waves, at their occupancy, leave less
+    than the copy kernel's VGPRs per SIMD free (empty: all fit)."""
+    bad = []
+    for name, r in kernel_resources(remarks).items():
+        if not any(k in name for k in WAITING_KERNELS):
+            continue
+        used = r["Occupancy"] * vgpr_alloc(r["VGPRs"], r["AGPRs"])
+        if VGPR_FILE - used < COPY_KERNEL_VGPRS_PER_SIMD:
+            bad.append(f"{name}: {r['Occupancy']} waves x {vgpr_alloc(r['VGPRs'], r['AGPRs'])} "
+                       f"VGPRs leave {VGPR_FILE - used} of {COPY_KERNEL_VGPRS_PER_SIMD} free")
+    return bad
 
 
 def build(verbose: bool = False, trace: bool = False) -> str:
@@ -81,11 +135,15 @@ def build(verbose: bool = False, trace: bool = False) -> str:
     for src in SOURCES:
         obj = os.path.join(bdir, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
-        cmds.append([hipcc, *HIPCC_FLAGS, *(["-DSLUICE_TRACE"] if trace else []), "-c",
+        cmds.append([hipcc, *HIPCC_FLAGS, *(["-DSLUICE_TRACE"] if trace else []),
+                     *([RESOURCE_REMARKS] if src == "moe.hip" else []), "-c",
                      os.path.join(CSRC, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
-        for fut in [ex.submit(_run, c) for c in cmds]:
-            fut.result()
+        logs = [fut.result() for fut in [ex.submit(_run, c) for c in cmds]]
+    bad = check_wait_room(logs[SOURCES.index("moe.hip")])
+    if bad:
+        raise RuntimeError("kernels that wait on streaming slots leave no room for the "
+                           "runtime's copy kernel:\n  " + "\n  ".join(bad))
     link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs]
     tl = _torch_lib()
     if tl:

@@ -21,6 +21,8 @@
 // measured 1.6-1.8x slower than these launches and is not kept.)
 #include <math.h>
 
+#include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "common.h"
@@ -909,6 +911,38 @@ long split_grid_for(int P, int P2, int I, int n_groups) {
   return g <= kSplitGridMax ? g : 0;
 }
 
+// Workgroups of a grid-stride launch over a map whose slots may stream, all
+// of which may wait for slots at the same time.  The runtime copies small
+// host rows (fp8 scale rows, a few KB) with a kernel of its own (one
+// 512-thread workgroup, 16 VGPRs per lane), not the copy engine; if waiting
+// workgroups held every CU, such a copy could not start and the waits it
+// feeds would run to their bound.  The grid therefore leaves one of the
+// kernel's workgroup places per CU free: (workgroups per CU at its occupancy
+// - 1) x CUs, looked up once per device and kernel.  The split launch keeps
+// one item per workgroup (a loop over tickets costs it a wave of occupancy);
+// build.py checks instead that at full occupancy its waves leave that
+// copy kernel's 32 VGPRs per SIMD free.
+constexpr int kWaitDevices = 64;
+enum WaitKernel { kWaitG1Bf16, kWaitG1Fp8, kWaitG2Bf16, kWaitG2Fp8, kWaitKinds };
+std::atomic<int> g_wait_grid[kWaitDevices][kWaitKinds];
+
+template <typename K>
+int wait_grid(K kernel, WaitKernel kind, int* out) {
+  int dev = 0;
+  SLUICE_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kWaitDevices) return SLUICE_E_INVAL;
+  int n = g_wait_grid[dev][kind].load(std::memory_order_relaxed);
+  if (n == 0) {
+    int per_cu = 0, cus = 0;
+    SLUICE_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0));
+    SLUICE_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    n = std::max(per_cu - 1, 1) * std::max(cus, 1);
+    g_wait_grid[dev][kind].store(n, std::memory_order_relaxed);
+  }
+  *out = n;
+  return SLUICE_OK;
+}
+
 // The align kernel stages the map of all E experts in LDS.
 int check_common(int T, int H, int I, int k, int E, int S, int n_sh, const void* x,
                  const void* w13, const void* w2, const float* tw, const int32_t* ti,
@@ -973,11 +1007,24 @@ int run_experts(const void* x, const ExpertW& W, const float* tw, const int32_t*
                        0, st, (const uint16_t*)x, w.act, Ww, plan, tw, cs, w.partial, w.handoff);
     SLUICE_HIP_CHECK(hipGetLastError());
   } else {
-    hipLaunchKernelGGL((moe_gemm1_kernel<FP8>), dim3(grid_for(P2, I / 16)), dim3(kThreads), 0,
-                       st, (const uint16_t*)x, Ww, plan, cs, w.act, (int32_t*)nullptr);
+    // Grid-stride launches (any grid gives the same product): where slots
+    // may stream, every workgroup may wait, so the grid stays within
+    // wait_grid's bound.
+    int g1 = grid_for(P2, I / 16), g2 = grid_for(P2, g2_groups(H, FP8));
+    if (Ww.wait.pending != nullptr) {
+      int c1 = 0, c2 = 0;
+      int rc = wait_grid(moe_gemm1_kernel<FP8>, FP8 ? kWaitG1Fp8 : kWaitG1Bf16, &c1);
+      if (rc == SLUICE_OK)
+        rc = wait_grid(moe_gemm2_kernel<FP8>, FP8 ? kWaitG2Fp8 : kWaitG2Bf16, &c2);
+      if (rc != SLUICE_OK) return rc;
+      g1 = std::min(g1, c1);
+      g2 = std::min(g2, c2);
+    }
+    hipLaunchKernelGGL((moe_gemm1_kernel<FP8>), dim3(g1), dim3(kThreads), 0, st,
+                       (const uint16_t*)x, Ww, plan, cs, w.act, (int32_t*)nullptr);
     SLUICE_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL((moe_gemm2_kernel<FP8>), dim3(grid_for(P2, g2_groups(H, FP8))),
-                       dim3(kThreads), 0, st, w.act, Ww, plan, tw, cs, w.partial);
+    hipLaunchKernelGGL((moe_gemm2_kernel<FP8>), dim3(g2), dim3(kThreads), 0, st, w.act, Ww, plan,
+                       tw, cs, w.partial);
     SLUICE_HIP_CHECK(hipGetLastError());
   }
   return launch_combine(w.partial, plan + kPlanHeader + (size_t)kBlockInts * P, T, k, n_sh, H,
