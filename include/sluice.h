@@ -253,9 +253,17 @@ int sluice_layer_create(int E, int local_n, int num_slots, int protected_cap,
 int sluice_layer_destroy(sluice_layer* layer);
 
 /* Register one per-expert parameter: slot buffer base (device, [S, row])
- * and pinned host store base ([local_n, row]), row_bytes per expert. */
+ * and pinned host store base ([local_n, row]), row_bytes per expert.
+ * On a layer with a device map, rows of at most 32 KB (multiples of 16
+ * bytes, 16-byte aligned) in device-visible pinned memory are copied by the
+ * gap kernel itself when it answers a gap before the rows land (up to 4
+ * such params); other rows go through hipMemcpyAsync on the copy lanes. */
 int sluice_layer_add_param(sluice_layer* layer, void* slot_base_dev,
                            const void* host_base, size_t row_bytes);
+
+/* No counterpart in the reference.  How many of the layer's params the gap
+ * kernel copies itself (see sluice_layer_add_param). */
+int sluice_layer_pulled_params(sluice_layer* layer);
 
 /* Mark a slot as pre-filled with `local` outside the SLRU segments (full
  * residency pre-fill and static pins, offloader.py:1000-1010, 1046-1083);

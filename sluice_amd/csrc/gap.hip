@@ -178,6 +178,7 @@ struct GapMailbox {
   int32_t host_pad[10];
   int32_t slot_global[SLUICE_MAX_SLOTS];  // slot -> global id, -1 = empty
   int32_t fill[SLUICE_MAX_SLOTS];         // the filled slots
+  int32_t fill_src[SLUICE_MAX_SLOTS];     // the host row (local expert) each fill takes
   int32_t slot_ready[SLUICE_MAX_SLOTS];   // stamp of the last gap whose rows into the slot landed
 };
 
@@ -258,13 +259,62 @@ constexpr int kGapMaxPerThread = SLUICE_MAX_EXPERTS / kLookupThreads;
 // still stream (0 = none); prev: [0] = count, [1..] = the slots the last
 // waiting gap filled, cleared by the next gap (the expert product of that
 // gap's step waited for each of them).
+// Per-expert params whose rows are small (fp8 block-scale rows, a few KB)
+// and live in device-visible pinned host memory: a gap that answers before
+// its rows land copies them into the filled slots itself, right after it
+// installs the map.  A hipMemcpyAsync of so few bytes runs as a runtime
+// copy kernel on the CUs, not on the copy engine, and the expert product's
+// pending workgroups, which wait for these slots, could hold every CU it
+// needs.  (The big rows stay on the copy engine, which needs no CU.)
+constexpr int kMaxPull = 4;
+constexpr size_t kPullMaxRowBytes = 32 << 10;
+struct PullRows {
+  int n;                         // params copied by the gap kernel
+  int rows;                      // host rows of each (the layer's local experts)
+  int vecs[kMaxPull];            // 16-byte vectors per row
+  const u32x4_t* src[kMaxPull];  // host rows, device view
+  u32x4_t* dst[kMaxPull];        // slot rows
+};
+constexpr int kPullU = 8;  // vectors per thread in flight
+
+// Copy the pulled params' rows of the nf fills (slot fslot[f] takes host row
+// fsrc[f]) from host memory into the slots: every (param, fill, vector)
+// index in one flat range, kPullU loads in flight per thread.
+__device__ void pull_rows(const PullRows& pull, const int* fslot, const int* fsrc, int nf, int S,
+                          int tid) {
+  int per_fill = 0;
+  for (int p = 0; p < pull.n; ++p) per_fill += pull.vecs[p];
+  const int total = nf * per_fill;
+  for (int j0 = 0; j0 < total; j0 += kPullU * kLookupThreads) {
+    u32x4_t v[kPullU];
+    u32x4_t* dst[kPullU];
+#pragma unroll
+    for (int u = 0; u < kPullU; ++u) {
+      const int j = j0 + u * kLookupThreads + tid;
+      dst[u] = nullptr;
+      if (j >= total) continue;
+      const int f = j / per_fill;
+      int w = j - f * per_fill, p = 0;
+      while (p + 1 < pull.n && w >= pull.vecs[p]) w -= pull.vecs[p++];
+      const int sl = fslot[f], src = fsrc[f];
+      if ((unsigned)sl >= (unsigned)S || (unsigned)src >= (unsigned)pull.rows) continue;
+      v[u] = pull.src[p][(size_t)src * pull.vecs[p] + w];
+      dst[u] = pull.dst[p] + (size_t)sl * pull.vecs[p] + w;
+    }
+#pragma unroll
+    for (int u = 0; u < kPullU; ++u)
+      if (dst[u] != nullptr) *dst[u] = v[u];
+  }
+}
+
 __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     const int32_t* __restrict__ ids, int n, int32_t* __restrict__ map,
     const int32_t* __restrict__ local_of, int E, GapMailbox* mb, int32_t* dev_state,
     int32_t* __restrict__ pending, int32_t* __restrict__ prev, int S, const int32_t* abort_flag,
     const long long* bound, const u32x4_t* __restrict__ copy_src, u32x4_t* __restrict__ copy_dst,
-    int copy_vecs, int32_t* __restrict__ plan) {
+    int copy_vecs, int32_t* __restrict__ plan, PullRows pull) {
   __shared__ int present[SLUICE_MAX_EXPERTS];
+  __shared__ int s_fslot[SLUICE_MAX_SLOTS], s_fsrc[SLUICE_MAX_SLOTS];
   __shared__ sluice_plan::Scratch psc;
   __shared__ int s_uniq[SLUICE_MAX_EXPERTS];
   __shared__ int wcount[kWaves];
@@ -413,13 +463,14 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
       // their counts.
       constexpr int kPer = SLUICE_MAX_SLOTS / kLookupThreads;
       static_assert(SLUICE_MAX_SLOTS % kLookupThreads == 0, "answer words per thread");
-      int sg[kPer], fl[kPer];
+      int sg[kPer], fl[kPer], fs[kPer];
       const int ns_word = ld_host(&mb->n_slots), nf_word = ld_host(&mb->n_fill);
 #pragma unroll
       for (int u = 0; u < kPer; ++u) {
         const int i = u * kLookupThreads + tid;
         sg[u] = i < S ? ld_host(&mb->slot_global[i]) : -1;
         fl[u] = i < S ? ld_host(&mb->fill[i]) : -1;
+        fs[u] = i < S && pull.n > 0 ? ld_host(&mb->fill_src[i]) : -1;
       }
       const int nS = min(ns_word, S);
       for (int e = tid; e < E; e += kLookupThreads) present[e] = -1;
@@ -452,8 +503,14 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
           if (plan != nullptr) psc.pend[sl] = 1;
         }
         prev[1 + i] = ok ? sl : 0;
+        s_fslot[i] = ok ? sl : -1;
+        s_fsrc[i] = fs[u];
       }
       if (tid == 0) prev[0] = nf;
+      if (pull.n > 0 && nf > 0) {
+        __syncthreads();
+        pull_rows(pull, s_fslot, s_fsrc, nf, S, tid);
+      }
     }
   }
   // The expert product's plan of these ids over the map (and pending marks)
@@ -592,7 +649,8 @@ struct ParamRows {
   char* slot_base;
   const char* host_base;
   size_t row_bytes;
-  int lane;  // copy lane of this param's rows
+  int lane;                         // copy lane of this param's rows
+  const char* host_dev = nullptr;   // device view of host_base when the gap kernel pulls the rows
 };
 
 struct sluice_gap_server;
@@ -676,7 +734,10 @@ void respond(sluice_layer* L, int32_t stamp, int code, int n_fill) {
     L->c.slot_globals(mb->slot_global);
     mb->n_slots = L->c.S;
     mb->standing = 1;
-    for (int i = 0; i < n_fill; ++i) mb->fill[i] = L->streams[2 * i + 1];
+    for (int i = 0; i < n_fill; ++i) {
+      mb->fill[i] = L->streams[2 * i + 1];
+      mb->fill_src[i] = L->streams[2 * i];
+    }
     mb->n_fill = n_fill;
   } else {
     mb->n_fill = 0;
@@ -815,6 +876,10 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     for (int i = 0; rc == SLUICE_OK && i < n_streams; ++i) {
       const int local = L->streams[2 * i], slot = L->streams[2 * i + 1];
       for (const ParamRows& p : L->params) {
+        if (early && p.host_dev != nullptr) {  // the gap kernel copies these rows itself
+          L->bytes += (int64_t)p.row_bytes;
+          continue;
+        }
         int left = g_fail_after.load(std::memory_order_relaxed);
         while (left >= 0 && !g_fail_after.compare_exchange_weak(left, left - 1)) {
         }
@@ -896,10 +961,19 @@ int launch_gap(sluice_layer* L, const int32_t* ids, int n, const void* hs_src, v
   if (hs_bytes > 0 && (hs_src == nullptr || hs_dst == nullptr)) return SLUICE_E_INVAL;
   const int E = L->c.E, S = L->c.S;
   int32_t* pending = L->dev_block + E + 3;
+  PullRows pull{};
+  pull.rows = L->c.local_n;
+  for (const ParamRows& p : L->params) {
+    if (p.host_dev == nullptr) continue;
+    pull.vecs[pull.n] = (int)(p.row_bytes / 16);
+    pull.src[pull.n] = (const u32x4_t*)p.host_dev;
+    pull.dst[pull.n] = (u32x4_t*)p.slot_base;
+    ++pull.n;
+  }
   hipLaunchKernelGGL(gap_kernel, dim3(1), dim3(kLookupThreads), 0, st, ids, n, L->map_dev,
                      L->dev_block, E, L->mb_dev, L->dev_block + E, pending, pending + S, S,
                      g_abort_dev, g_dev[L->device].bound_dev, (const u32x4_t*)hs_src, (u32x4_t*)hs_dst,
-                     (int)(hs_bytes / 16), plan);
+                     (int)(hs_bytes / 16), plan, pull);
   return (int)hipGetLastError();
 }
 
@@ -990,6 +1064,21 @@ extern "C" int sluice_layer_add_param(sluice_layer* L, void* slot_base_dev, cons
     return SLUICE_E_INVAL;
   std::lock_guard<std::mutex> lk(L->mu);
   L->params.push_back({(char*)slot_base_dev, (const char*)host_base, row_bytes, 0});
+  // Small rows in device-visible pinned memory are pulled by the gap kernel
+  // (PullRows); a layer without a device, or pageable host memory, keeps
+  // host copies.
+  ParamRows& np = L->params.back();
+  int n_pulled = 0;
+  for (const ParamRows& q : L->params) n_pulled += q.host_dev != nullptr;
+  if (L->mb != nullptr && row_bytes <= kPullMaxRowBytes && row_bytes % 16 == 0 &&
+      (((uintptr_t)host_base | (uintptr_t)slot_base_dev) & 15) == 0 && n_pulled < kMaxPull) {
+    void* dp = nullptr;
+    if (hipHostGetDevicePointer(&dp, const_cast<void*>(host_base), 0) == hipSuccess &&
+        dp != nullptr)
+      np.host_dev = (const char*)dp;
+    else
+      (void)hipGetLastError();  // pageable memory: not an error of this call
+  }
   // Lanes: largest rows first, each to the lane with the fewest bytes so
   // far (bf16: w13 | w2; fp8: w13 | w2 + both scale rows).
   std::vector<int> order(L->params.size());
@@ -1008,6 +1097,14 @@ extern "C" int sluice_layer_add_param(sluice_layer* L, void* slot_base_dev, cons
     L->lane_mask |= 1u << best;
   }
   return SLUICE_OK;
+}
+
+extern "C" int sluice_layer_pulled_params(sluice_layer* L) {
+  if (L == nullptr) return SLUICE_E_INVAL;
+  std::lock_guard<std::mutex> lk(L->mu);
+  int n = 0;
+  for (const ParamRows& p : L->params) n += p.host_dev != nullptr;
+  return n;
 }
 
 extern "C" int sluice_layer_pin(sluice_layer* L, int local, int debit_protected, int* slot_out) {

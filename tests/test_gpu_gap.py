@@ -220,17 +220,23 @@ def _slot_bytes_match_host(cache):
 
 
 @pytest.mark.parametrize("fast_hit", [False, True])
-def test_device_gap_v3_fp8_streams_four_rows_per_miss(monkeypatch, slru_golden, fast_hit):
+@pytest.mark.parametrize("H,I,pulled", [(256, 128, 2), (512, 256, 2)])
+def test_device_gap_v3_fp8_streams_four_rows_per_miss(monkeypatch, slru_golden, fast_hit, H, I,
+                                                      pulled):
     """The DeepSeek-V3-shaped golden trace (E = 256, 64 slots, top-8, 8
     tokens per step), replayed on an fp8 layer: per step the stream-ins
     (local -> slot) and the slot state, segment order and device map of the
     reference; the bytes of all four per-expert params of every slot equal
-    their host rows; bytes streamed = misses x the four rows' size."""
+    their host rows; bytes streamed = misses x the four rows' size.  The
+    rows of at most 32 KB in whole 16-byte vectors are copied by the gap
+    kernel itself, the others go over the copy lanes (H=512: both scale rows
+    pulled; H=256: the 32 KB w2 row and the 16-byte w13 scale row pulled,
+    the 64 KB w13 row and the 8-byte w2 scale row on the lanes)."""
     case = [c for c in slru_golden["cases"]
             if c["name"] == "v3_s64_zipf" and c["fast_hit"] == fast_hit][0]
-    print(f"v3 fp8 gap fast_hit={fast_hit}", flush=True)
+    print(f"v3 fp8 gap fast_hit={fast_hit} H={H} I={I}", flush=True)
     E, k = case["E"], case["k"]
-    layer = _Fp8Layer(E)
+    layer = _Fp8Layer(E, H, I)
     off = _offloader(monkeypatch, case["slots"], case["protect_frac"], fast_hit)
     off.wrap_modules(iter([layer]))
     with torch.cuda.device(DEV):
@@ -238,9 +244,11 @@ def test_device_gap_v3_fp8_streams_four_rows_per_miss(monkeypatch, slru_golden, 
     cache = off._caches[id(layer)]
     assert sorted(cache.param_names) == ["w13_weight", "w13_weight_scale", "w2_weight",
                                          "w2_weight_scale"]
-    assert cache.bytes_per_expert == 2 * 128 * 256 + 256 * 128 + (2 * 2 + 2 * 1) * 4
+    nh, ni = H // 128, I // 128
+    assert cache.bytes_per_expert == 2 * I * H + H * I + (2 * ni * nh + nh * ni) * 4
     off._rs_caches.append(cache)
     from sluice_amd import _lib
+    assert _lib.load().sluice_layer_pulled_params(cache.handle) == pulled
     cache.plan = torch.zeros(_lib.load().sluice_moe_plan_ints(1, cache.num_slots),
                              dtype=torch.int32, device=DEV)
     hs = torch.zeros((8, 256), dtype=torch.bfloat16, device=DEV)
