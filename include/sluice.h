@@ -359,8 +359,11 @@ int sluice_gap_set_pipelined(int on);
  * stamps up with the device's, clears the pending-slot marks and writes the
  * host's standing map into the device map (which may lag the slot cache:
  * a device wait that ended after the host served its record, or fills
- * dropped after a failed copy).  No counterpart in the reference, whose gap
- * errors end the engine. */
+ * dropped after a failed copy).  It also copies again the rows the gap
+ * kernel copies itself (sluice_layer_pulled_params) into every slot the
+ * cache holds: a gap the host answered but the device never installed left
+ * them out.  No counterpart in the reference, whose gap errors end the
+ * engine. */
 int sluice_layer_gap_resync(sluice_layer* layer);
 
 /* Recovery from a fill whose rows did not land: the expert in `slot` leaves

@@ -523,6 +523,21 @@ __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
 #endif
 }
 
+// Resynchronisation after a failed gap: the pulled params' rows of every
+// slot the host's cache holds (mb->fill / fill_src, nf entries), so that a
+// gap the host answered but the device never installed (its wait ended
+// first) leaves no slot without its small rows.
+__global__ __launch_bounds__(kLookupThreads) void pull_slots_kernel(const GapMailbox* mb, int nf,
+                                                                    int S, PullRows pull) {
+  __shared__ int s_fslot[SLUICE_MAX_SLOTS], s_fsrc[SLUICE_MAX_SLOTS];
+  for (int i = threadIdx.x; i < nf; i += kLookupThreads) {
+    s_fslot[i] = ld_host(&mb->fill[i]);
+    s_fsrc[i] = ld_host(&mb->fill_src[i]);
+  }
+  __syncthreads();
+  pull_rows(pull, s_fslot, s_fsrc, nf, S, threadIdx.x);
+}
+
 // ---------------------------------------------------------------------------
 // Per-device resources: the copy lanes (default priority, non-blocking
 // streams) and the wall-clock rate; one process-wide abort flag in pinned
@@ -954,13 +969,8 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
   return rc;
 }
 
-int launch_gap(sluice_layer* L, const int32_t* ids, int n, const void* hs_src, void* hs_dst,
-               size_t hs_bytes, int32_t* plan, hipStream_t st) {
-  if ((hs_bytes & 15) != 0 || ((uintptr_t)hs_src & 15) != 0 || ((uintptr_t)hs_dst & 15) != 0)
-    return SLUICE_E_INVAL;
-  if (hs_bytes > 0 && (hs_src == nullptr || hs_dst == nullptr)) return SLUICE_E_INVAL;
-  const int E = L->c.E, S = L->c.S;
-  int32_t* pending = L->dev_block + E + 3;
+// The params the gap kernel copies itself (sluice_layer_add_param).
+PullRows pull_rows_of(const sluice_layer* L) {
   PullRows pull{};
   pull.rows = L->c.local_n;
   for (const ParamRows& p : L->params) {
@@ -970,6 +980,17 @@ int launch_gap(sluice_layer* L, const int32_t* ids, int n, const void* hs_src, v
     pull.dst[pull.n] = (u32x4_t*)p.slot_base;
     ++pull.n;
   }
+  return pull;
+}
+
+int launch_gap(sluice_layer* L, const int32_t* ids, int n, const void* hs_src, void* hs_dst,
+               size_t hs_bytes, int32_t* plan, hipStream_t st) {
+  if ((hs_bytes & 15) != 0 || ((uintptr_t)hs_src & 15) != 0 || ((uintptr_t)hs_dst & 15) != 0)
+    return SLUICE_E_INVAL;
+  if (hs_bytes > 0 && (hs_src == nullptr || hs_dst == nullptr)) return SLUICE_E_INVAL;
+  const int E = L->c.E, S = L->c.S;
+  int32_t* pending = L->dev_block + E + 3;
+  const PullRows pull = pull_rows_of(L);
   hipLaunchKernelGGL(gap_kernel, dim3(1), dim3(kLookupThreads), 0, st, ids, n, L->map_dev,
                      L->dev_block, E, L->mb_dev, L->dev_block + E, pending, pending + S, S,
                      g_abort_dev, g_dev[L->device].bound_dev, (const u32x4_t*)hs_src, (u32x4_t*)hs_dst,
@@ -1288,6 +1309,25 @@ extern "C" int sluice_layer_gap_resync(sluice_layer* L) {
                                hipMemcpyHostToDevice));
     L->c.map_is_standing = true;
     __atomic_store_n(&L->mb->standing, 1, __ATOMIC_RELEASE);
+    // A gap the host answered early skipped the rows the device pulls; if
+    // the device's wait ended before it read that answer, they never came.
+    // Pull them again for every slot the cache holds.
+    const PullRows pull = pull_rows_of(L);
+    int nf = 0;
+    for (int sl = 0; pull.n > 0 && sl < L->c.S; ++sl) {
+      const int loc = L->c.expert_in_slot[sl];
+      if (loc < 0) continue;
+      L->mb->fill[nf] = sl;
+      L->mb->fill_src[nf] = loc;
+      ++nf;
+    }
+    L->mb->n_fill = 0;
+    if (nf > 0) {
+      hipLaunchKernelGGL(pull_slots_kernel, dim3(1), dim3(kLookupThreads), 0, nullptr, L->mb_dev,
+                         nf, L->c.S, pull);
+      SLUICE_HIP_CHECK(hipGetLastError());
+      SLUICE_HIP_CHECK(hipStreamSynchronize(nullptr));
+    }
   }
   L->host_stamp = dev_stamp;
   L->done_stamp.store(dev_stamp);

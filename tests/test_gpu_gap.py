@@ -277,6 +277,43 @@ def test_device_gap_v3_fp8_streams_four_rows_per_miss(monkeypatch, slru_golden, 
     off.close()
 
 
+def test_resync_restores_the_pulled_rows_of_every_cached_slot(monkeypatch):
+    """The gap kernel copies an fp8 layer's scale rows into the slots it
+    fills; a gap the host answered but the device never installed (its wait
+    ended first) would leave them out, and the resync after such a failure
+    copies them again for every slot the cache holds.  Forced from the host:
+    after a few served gaps the slots' scale rows are zeroed, and
+    sluice_layer_gap_resync brings back every cached slot's host rows."""
+    from sluice_amd import _lib
+
+    E, S, k = 64, 16, 4
+    print("resync re-pulls scale rows", flush=True)
+    layer = _Fp8Layer(E, 512, 256)
+    off = _offloader(monkeypatch, S, 0.5, False)
+    off.wrap_modules(iter([layer]))
+    with torch.cuda.device(DEV):
+        off.post_init()
+    cache = off._caches[id(layer)]
+    off._rs_caches.append(cache)
+    lib = _lib.load()
+    assert lib.sluice_layer_pulled_params(cache.handle) == 2
+    hs = torch.zeros((2, 512), dtype=torch.bfloat16, device=DEV)
+    rng = np.random.default_rng(5)
+    for _ in range(4):
+        ids = torch.from_numpy(rng.choice(E, 2 * k, replace=False).astype(np.int32)).to(DEV)
+        torch.ops.vllm.sluice_stream_gap(hs, ids.view(-1, k), 0)
+    torch.cuda.synchronize()
+    _slot_bytes_match_host(cache)
+    cached = [s for s, loc in enumerate(cache.expert_in_slot) if loc is not None]
+    assert len(cached) >= 8
+    for name in ("w13_weight_scale", "w2_weight_scale"):
+        cache.gpu_cache[name].zero_()
+    torch.cuda.synchronize()
+    assert lib.sluice_layer_gap_resync(cache.handle) == 0
+    _slot_bytes_match_host(cache)
+    off.close()
+
+
 @pytest.mark.parametrize("mode", ["abort", "timeout"])
 def test_unserved_gap_wait_ends_and_resync_resumes(monkeypatch, mode):
     """Failure handling forced from the host: a gap whose ids miss is
