@@ -79,11 +79,14 @@ def _run(cmd: list[str]) -> str:
 
 # Room the split launch of the expert product must leave per SIMD.  Its
 # pending workgroups wait for slots while the copies that fill them run, and
-# the runtime copies small host rows (fp8 scale rows) with a kernel of its
-# own: one 512-thread workgroup (two waves per SIMD) allocating 16 VGPRs per
-# lane (the rocprofv3 kernel trace of __amd_rocclr_copyBuffer on MI355X).  If
-# the split launch's waves filled the 512-VGPR file of every SIMD, such a copy
-# could not start while they wait and the waits would run to their bound.
+# the runtime copies small host rows with a kernel of its own: one
+# 512-thread workgroup (two waves per SIMD) allocating 16 VGPRs per lane (the
+# rocprofv3 kernel trace of __amd_rocclr_copyBuffer on MI355X).  If the split
+# launch's waves filled the 512-VGPR file of every SIMD, such a copy could not
+# start while they wait and the waits would run to their bound.  The gap
+# kernel copies the small rows it can reach itself (fp8 scale rows in pinned
+# memory); this keeps room for the rest (pageable host memory, rows not in
+# whole 16-byte vectors).
 VGPR_FILE = 512
 COPY_KERNEL_VGPRS_PER_SIMD = 2 * 16
 WAITING_KERNELS = ("moe_gemm2_split_kernel",)
