@@ -254,10 +254,11 @@ int sluice_layer_destroy(sluice_layer* layer);
 
 /* Register one per-expert parameter: slot buffer base (device, [S, row])
  * and pinned host store base ([local_n, row]), row_bytes per expert.
- * On a layer with a device map, rows of at most 32 KB (multiples of 16
- * bytes, 16-byte aligned) in device-visible pinned memory are copied by the
- * gap kernel itself when it answers a gap before the rows land (up to 4
- * such params); other rows go through hipMemcpyAsync on the copy lanes. */
+ * On a layer with a device map, params with rows of at most 32 KB (whole
+ * 16-byte vectors; up to 4 such params) are copied into HBM whole here
+ * (local_n rows), and a gap answered before its rows land copies their rows
+ * into the filled slots from there in the gap kernel; other rows go through
+ * hipMemcpyAsync on the copy lanes. */
 int sluice_layer_add_param(sluice_layer* layer, void* slot_base_dev,
                            const void* host_base, size_t row_bytes);
 

@@ -84,9 +84,8 @@ def _run(cmd: list[str]) -> str:
 # rocprofv3 kernel trace of __amd_rocclr_copyBuffer on MI355X).  If the split
 # launch's waves filled the 512-VGPR file of every SIMD, such a copy could not
 # start while they wait and the waits would run to their bound.  The gap
-# kernel copies the small rows it can reach itself (fp8 scale rows in pinned
-# memory); this keeps room for the rest (pageable host memory, rows not in
-# whole 16-byte vectors).
+# kernel copies small rows itself (fp8 scale rows); this keeps room for the
+# rest (rows not in whole 16-byte vectors, more than 4 such params).
 VGPR_FILE = 512
 COPY_KERNEL_VGPRS_PER_SIMD = 2 * 16
 WAITING_KERNELS = ("moe_gemm2_split_kernel",)

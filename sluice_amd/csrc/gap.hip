@@ -259,20 +259,22 @@ constexpr int kGapMaxPerThread = SLUICE_MAX_EXPERTS / kLookupThreads;
 // still stream (0 = none); prev: [0] = count, [1..] = the slots the last
 // waiting gap filled, cleared by the next gap (the expert product of that
 // gap's step waited for each of them).
-// Per-expert params whose rows are small (fp8 block-scale rows, a few KB)
-// and live in device-visible pinned host memory: a gap that answers before
-// its rows land copies them into the filled slots itself, right after it
-// installs the map.  A hipMemcpyAsync of so few bytes runs as a runtime
-// copy kernel on the CUs, not on the copy engine, and the expert product's
-// pending workgroups, which wait for these slots, could hold every CU it
-// needs.  (The big rows stay on the copy engine, which needs no CU.)
+// Per-expert params whose rows are small (fp8 block-scale rows, a few KB):
+// the layer keeps a copy of all their rows in HBM, and a gap that answers
+// before its rows land copies them into the filled slots itself, right
+// after it installs the map.  A hipMemcpyAsync of so few bytes runs as a
+// runtime copy kernel on the CUs, not on the copy engine, and the expert
+// product's pending workgroups, which wait for these slots, could hold every
+// CU it needs; and a read of host memory issued while the copy engine fills
+// the link waits tens of microseconds behind it.  (The big rows stay on the
+// copy engine, which needs no CU.)
 constexpr int kMaxPull = 4;
 constexpr size_t kPullMaxRowBytes = 32 << 10;
 struct PullRows {
   int n;                         // params copied by the gap kernel
   int rows;                      // host rows of each (the layer's local experts)
   int vecs[kMaxPull];            // 16-byte vectors per row
-  const u32x4_t* src[kMaxPull];  // host rows, device view
+  const u32x4_t* src[kMaxPull];  // all rows of the param, in HBM
   u32x4_t* dst[kMaxPull];        // slot rows
 };
 constexpr int kPullU = 8;  // vectors per thread in flight
@@ -664,8 +666,8 @@ struct ParamRows {
   char* slot_base;
   const char* host_base;
   size_t row_bytes;
-  int lane;                         // copy lane of this param's rows
-  const char* host_dev = nullptr;   // device view of host_base when the gap kernel pulls the rows
+  int lane;                 // copy lane of this param's rows
+  char* rows_dev = nullptr;  // HBM copy of all host rows when the gap kernel pulls them
 };
 
 struct sluice_gap_server;
@@ -891,7 +893,7 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     for (int i = 0; rc == SLUICE_OK && i < n_streams; ++i) {
       const int local = L->streams[2 * i], slot = L->streams[2 * i + 1];
       for (const ParamRows& p : L->params) {
-        if (early && p.host_dev != nullptr) {  // the gap kernel copies these rows itself
+        if (early && p.rows_dev != nullptr) {  // the gap kernel copies these rows itself
           L->bytes += (int64_t)p.row_bytes;
           continue;
         }
@@ -974,9 +976,9 @@ PullRows pull_rows_of(const sluice_layer* L) {
   PullRows pull{};
   pull.rows = L->c.local_n;
   for (const ParamRows& p : L->params) {
-    if (p.host_dev == nullptr) continue;
+    if (p.rows_dev == nullptr) continue;
     pull.vecs[pull.n] = (int)(p.row_bytes / 16);
-    pull.src[pull.n] = (const u32x4_t*)p.host_dev;
+    pull.src[pull.n] = (const u32x4_t*)p.rows_dev;
     pull.dst[pull.n] = (u32x4_t*)p.slot_base;
     ++pull.n;
   }
@@ -1060,6 +1062,12 @@ extern "C" int sluice_layer_destroy(sluice_layer* L) {
   int rc = SLUICE_OK;
   if (L->map_dev != nullptr && L->mb != nullptr) slotwait_unregister(L->map_dev);
   for (hipEvent_t ev : L->fill_ev) (void)hipEventDestroy(ev);
+  for (ParamRows& p : L->params)
+    if (p.rows_dev != nullptr) {
+      const hipError_t e = hipFree(p.rows_dev);
+      if (e != hipSuccess) rc = (int)e;
+      p.rows_dev = nullptr;
+    }
   if (L->mb != nullptr) {
     hipError_t e = hipHostFree(L->mb);
     if (e != hipSuccess) rc = (int)e;
@@ -1085,20 +1093,24 @@ extern "C" int sluice_layer_add_param(sluice_layer* L, void* slot_base_dev, cons
     return SLUICE_E_INVAL;
   std::lock_guard<std::mutex> lk(L->mu);
   L->params.push_back({(char*)slot_base_dev, (const char*)host_base, row_bytes, 0});
-  // Small rows in device-visible pinned memory are pulled by the gap kernel
-  // (PullRows); a layer without a device, or pageable host memory, keeps
-  // host copies.
+  // Small rows are pulled by the gap kernel from a copy of all of them in
+  // HBM (PullRows); a layer without a device keeps host copies.
   ParamRows& np = L->params.back();
   int n_pulled = 0;
-  for (const ParamRows& q : L->params) n_pulled += q.host_dev != nullptr;
+  for (const ParamRows& q : L->params) n_pulled += q.rows_dev != nullptr;
   if (L->mb != nullptr && row_bytes <= kPullMaxRowBytes && row_bytes % 16 == 0 &&
-      (((uintptr_t)host_base | (uintptr_t)slot_base_dev) & 15) == 0 && n_pulled < kMaxPull) {
-    void* dp = nullptr;
-    if (hipHostGetDevicePointer(&dp, const_cast<void*>(host_base), 0) == hipSuccess &&
-        dp != nullptr)
-      np.host_dev = (const char*)dp;
-    else
-      (void)hipGetLastError();  // pageable memory: not an error of this call
+      ((uintptr_t)slot_base_dev & 15) == 0 && n_pulled < kMaxPull) {
+    const size_t all = row_bytes * (size_t)L->c.local_n;
+    void* d = nullptr;
+    hipError_t e = hipMalloc(&d, all);
+    if (e == hipSuccess) e = hipMemcpy(d, host_base, all, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      if (d != nullptr) (void)hipFree(d);
+      (void)hipGetLastError();  // reported here, not by the caller's next call
+      L->params.pop_back();
+      return (int)e;
+    }
+    np.rows_dev = (char*)d;
   }
   // Lanes: largest rows first, each to the lane with the fewest bytes so
   // far (bf16: w13 | w2; fp8: w13 | w2 + both scale rows).
@@ -1124,7 +1136,7 @@ extern "C" int sluice_layer_pulled_params(sluice_layer* L) {
   if (L == nullptr) return SLUICE_E_INVAL;
   std::lock_guard<std::mutex> lk(L->mu);
   int n = 0;
-  for (const ParamRows& p : L->params) n += p.host_dev != nullptr;
+  for (const ParamRows& p : L->params) n += p.rows_dev != nullptr;
   return n;
 }
 

@@ -916,9 +916,9 @@ long split_grid_for(int P, int P2, int I, int n_groups) {
 // host rows (a few KB) with a kernel of its own (one 512-thread workgroup,
 // 16 VGPRs per lane), not the copy engine; if waiting workgroups held every
 // CU, such a copy could not start and the waits it feeds would run to their
-// bound.  The gap kernel copies the small rows it can reach itself (fp8
-// scale rows in pinned memory), so this guards the rest (pageable host
-// memory, rows not in whole 16-byte vectors).  The grid leaves one of the
+// bound.  The gap kernel copies small rows itself (fp8 scale rows), so this
+// guards the rest (rows not in whole 16-byte vectors, more than 4 such
+// params).  The grid leaves one of the
 // kernel's workgroup places per CU free: (workgroups per CU at its occupancy
 // - 1) x CUs, looked up once per device and kernel.  The split launch keeps
 // one item per workgroup (a loop over tickets costs it a wave of occupancy);
