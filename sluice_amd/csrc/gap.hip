@@ -255,10 +255,6 @@ __device__ int wait_eq(const int32_t* p, int32_t want, const int32_t* abort_flag
 // 0, so later gaps skip that bus read), [2] the last host ack read.
 constexpr int kGapMaxPerThread = SLUICE_MAX_EXPERTS / kLookupThreads;
 
-// pending [S]: the stamp of the gap that filled each slot, while its rows may
-// still stream (0 = none); prev: [0] = count, [1..] = the slots the last
-// waiting gap filled, cleared by the next gap (the expert product of that
-// gap's step waited for each of them).
 // Per-expert params whose rows are small (fp8 block-scale rows, a few KB):
 // the layer keeps a copy of all their rows in HBM, and a gap that answers
 // before its rows land copies them into the filled slots itself, right
@@ -279,8 +275,8 @@ struct PullRows {
 };
 constexpr int kPullU = 8;  // vectors per thread in flight
 
-// Copy the pulled params' rows of the nf fills (slot fslot[f] takes host row
-// fsrc[f]) from host memory into the slots: every (param, fill, vector)
+// Copy the pulled params' rows of the nf fills (slot fslot[f] takes row
+// fsrc[f]) from their HBM copy into the slots: every (param, fill, vector)
 // index in one flat range, kPullU loads in flight per thread.
 __device__ void pull_rows(const PullRows& pull, const int* fslot, const int* fsrc, int nf, int S,
                           int tid) {
@@ -309,6 +305,10 @@ __device__ void pull_rows(const PullRows& pull, const int* fslot, const int* fsr
   }
 }
 
+// pending [S]: the stamp of the gap that filled each slot, while its rows may
+// still stream (0 = none); prev: [0] = count, [1..] = the slots the last
+// waiting gap filled, cleared by the next gap (the expert product of that
+// gap's step waited for each of them).
 __global__ __launch_bounds__(kLookupThreads) void gap_kernel(
     const int32_t* __restrict__ ids, int n, int32_t* __restrict__ map,
     const int32_t* __restrict__ local_of, int E, GapMailbox* mb, int32_t* dev_state,
