@@ -38,6 +38,7 @@ typedef struct ihipStream_t* sluice_stream_t; /* == hipStream_t */
 #define SLUICE_E_STATE (-5)    /* object used in a state it does not allow */
 #define SLUICE_E_ABORTED (-6)  /* a device gap wait ended by the abort flag */
 #define SLUICE_E_SCRATCH (-7)  /* call too large for the no-alloc entry's scratch */
+#define SLUICE_E_COPY (-8)     /* a host-to-device row copy failed to issue or complete */
 
 /* Kernel limits (checked on the host before every launch). */
 #define SLUICE_MAX_EXPERTS 1024  /* global experts E per layer */

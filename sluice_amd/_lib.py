@@ -26,6 +26,7 @@ SLUICE_E_NOMEM = -4
 SLUICE_E_STATE = -5
 SLUICE_E_ABORTED = -6
 SLUICE_E_SCRATCH = -7
+SLUICE_E_COPY = -8
 NOALLOC_SCRATCH_BYTES = 8 << 20  # SLUICE_NOALLOC_SCRATCH_BYTES
 
 MAX_EXPERTS = 1024

@@ -146,12 +146,14 @@ def build(verbose: bool = False, trace: bool = False) -> str:
     if bad:
         raise RuntimeError("kernels that wait on streaming slots leave no room for the "
                            "runtime's copy kernel:\n  " + "\n  ".join(bad))
+    # libhsa-runtime64: the gap's row copies go to the SDMA engines directly
+    # (csrc/gap.hip), through the same HSA runtime HIP runs on
     link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs]
     tl = _torch_lib()
     if tl:
         link += [f"-L{tl}", f"-Wl,-rpath,{tl}"]
     tmp = out + ".tmp"
-    link += ["-o", tmp]
+    link += ["-lhsa-runtime64", "-o", tmp]
     _run(link)
     os.replace(tmp, out)
     if verbose:

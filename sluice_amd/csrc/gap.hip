@@ -54,6 +54,9 @@
 #include <thread>
 #include <vector>
 
+#include <hsa/hsa.h>
+#include <hsa/hsa_ext_amd.h>
+
 #include "common.h"
 #include "plan.h"
 #include "slotwait.h"
@@ -584,6 +587,17 @@ long long bound_ticks(long long clock_khz) {
 
 struct DeviceRes {
   hipStream_t copy[kLanes] = {};
+  // The streamed gap's row copies go to the SDMA engines through the HSA
+  // runtime (the one HIP itself runs on), not through HIP streams: a HIP
+  // stream shares an in-order hardware queue with other streams once a
+  // process has more streams than hardware queues (GPU_MAX_HW_QUEUES), and
+  // a copy, or the marker of its completion event, queued behind the expert
+  // product that waits for it would never run.  An SDMA copy's completion
+  // signal needs no compute queue.  Lane l's rows go to engine[l] (0: the
+  // runtime's choice).
+  bool hsa = false;
+  hsa_agent_t gpu_agent{}, cpu_agent{};
+  uint32_t engine[kLanes] = {};
   long long clock_khz = 0;
   // device word: the bound of every device wait, in wall-clock ticks; the
   // kernels read it when they start to wait (sluice_gap_set_timeout
@@ -595,6 +609,43 @@ DeviceRes g_dev[kMaxDevices];
 std::mutex g_dev_mu;
 int32_t* g_abort_host = nullptr;
 int32_t* g_abort_dev = nullptr;
+
+hsa_status_t first_cpu_agent(hsa_agent_t agent, void* data) {
+  hsa_device_type_t t;
+  if (hsa_agent_get_info(agent, HSA_AGENT_INFO_DEVICE, &t) != HSA_STATUS_SUCCESS)
+    return HSA_STATUS_SUCCESS;
+  if (t != HSA_DEVICE_TYPE_CPU) return HSA_STATUS_SUCCESS;
+  *static_cast<hsa_agent_t*>(data) = agent;
+  return HSA_STATUS_INFO_BREAK;
+}
+
+// The HSA agents of this device (the owner of its device memory) and of the
+// host, and one SDMA engine per copy lane among those the runtime reports
+// available for host-to-device copies.
+int hsa_setup(DeviceRes& r) {
+  if (hsa_init() != HSA_STATUS_SUCCESS) return SLUICE_E_COPY;  // counted: HIP holds one too
+  hsa_amd_pointer_info_t info;
+  memset(&info, 0, sizeof(info));
+  info.size = sizeof(info);
+  if (hsa_amd_pointer_info(r.bound_dev, &info, nullptr, nullptr, nullptr) != HSA_STATUS_SUCCESS ||
+      info.type == HSA_EXT_POINTER_TYPE_UNKNOWN)
+    return SLUICE_E_COPY;
+  r.gpu_agent = info.agentOwner;
+  hsa_agent_t cpu{};
+  const hsa_status_t st = hsa_iterate_agents(first_cpu_agent, &cpu);
+  if ((st != HSA_STATUS_SUCCESS && st != HSA_STATUS_INFO_BREAK) || cpu.handle == 0)
+    return SLUICE_E_COPY;
+  r.cpu_agent = cpu;
+  uint32_t mask = 0;
+  if (hsa_amd_memory_copy_engine_status(r.gpu_agent, r.cpu_agent, &mask) != HSA_STATUS_SUCCESS)
+    mask = 0;
+  int l = 0;
+  for (uint32_t bit = 1; bit != 0 && l < kLanes; bit <<= 1)
+    if (mask & bit) r.engine[l++] = bit;
+  for (; l < kLanes; ++l) r.engine[l] = l > 0 ? r.engine[l - 1] : 0;
+  r.hsa = true;
+  return SLUICE_OK;
+}
 
 int device_res(int dev, DeviceRes** out) {
   if (dev < 0 || dev >= kMaxDevices) return SLUICE_E_INVAL;
@@ -613,6 +664,10 @@ int device_res(int dev, DeviceRes** out) {
     const long long ticks = bound_ticks(r.clock_khz);
     SLUICE_HIP_CHECK(hipMemcpy(b, &ticks, sizeof(ticks), hipMemcpyHostToDevice));
     r.bound_dev = b;
+  }
+  if (!r.hsa) {
+    const int rc = hsa_setup(r);
+    if (rc != SLUICE_OK) return rc;
   }
   if (g_abort_host == nullptr) {
     void* p = nullptr;
@@ -697,8 +752,11 @@ struct sluice_layer {
   int32_t* ids_host = nullptr;  // pinned staging of the step's ids
   size_t ids_cap = 0;
   int64_t classic_steps = 0, classic_waves = 0;
-  // per group of experts a gap streams, one per lane: [kLanes * g + lane]
-  std::vector<hipEvent_t> fill_ev;
+  // per group of experts a gap streams: an HSA signal armed with the group's
+  // copy count, decremented by each copy as it completes; armed_groups of
+  // them may still have copies in flight after a failed stream-in
+  std::vector<hsa_signal_t> fill_sig;
+  int armed_groups = 0;
   unsigned lane_mask = 0;  // lanes that carry some param's rows
 };
 
@@ -781,17 +839,27 @@ int experts_per_event(const sluice_layer* L, int n_streams) {
   return std::max(1, std::min(k, n_streams));
 }
 
-// Spin until `ev` completed (bounded).  0 or an error code.
-int wait_event(hipEvent_t ev) {
+// Spin until signal `sig` counted down to zero (bounded).  0, or
+// SLUICE_E_COPY (a copy reported an error: the runtime sets the signal
+// negative) or SLUICE_E_TIMEOUT.
+int wait_signal(hsa_signal_t sig) {
   const double t0 = now_s();
   unsigned spins = 0;
   for (;;) {
-    const hipError_t q = hipEventQuery(ev);
-    if (q == hipSuccess) return SLUICE_OK;
-    if (q != hipErrorNotReady) return (int)q;
+    const hsa_signal_value_t v = hsa_signal_load_scacquire(sig);
+    if (v == 0) return SLUICE_OK;
+    if (v < 0) return SLUICE_E_COPY;
     _mm_pause();
     if ((++spins & 1023u) == 0 && now_s() - t0 > gap_timeout_s()) return SLUICE_E_TIMEOUT;
   }
+}
+
+// Wait (bounded) until no copy of the layer's last stream-in is in flight
+// (a copy that failed is not in flight either).  0 or SLUICE_E_TIMEOUT.
+int drain_copies(sluice_layer* L) {
+  for (int g = 0; g < L->armed_groups && g < (int)L->fill_sig.size(); ++g)
+    if (wait_signal(L->fill_sig[g]) == SLUICE_E_TIMEOUT) return SLUICE_E_TIMEOUT;
+  return SLUICE_OK;
 }
 
 // A record after the last one served has been posted (records are posted
@@ -879,46 +947,60 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
                        g_pipelined.load(std::memory_order_relaxed) != 0;
     const int per_event = experts_per_event(L, n_streams);
     const int n_events = (n_streams + per_event - 1) / per_event;
-    while (rc == SLUICE_OK && (int)L->fill_ev.size() < kLanes * n_events) {
-      hipEvent_t ev = nullptr;
-      const hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
-      if (e != hipSuccess) rc = (int)e;
-      else L->fill_ev.push_back(ev);
+    while (rc == SLUICE_OK && (int)L->fill_sig.size() < n_events) {
+      hsa_signal_t sig{};
+      if (hsa_signal_create(0, 0, nullptr, &sig) != HSA_STATUS_SUCCESS) rc = SLUICE_E_COPY;
+      else L->fill_sig.push_back(sig);
     }
+    // rows copied per expert (the gap kernel copies the pulled ones itself)
+    int n_copy = 0;
+    for (const ParamRows& p : L->params) n_copy += !(early && p.rows_dev != nullptr);
     // The link is the bottleneck of a missing step: the first expert's rows
     // are queued before the device is answered (its resident experts then
     // compute while the rows stream), the other experts' after.
     bool answered = !early;
-    int issued = 0;  // events recorded
+    int whole = 0;  // groups whose copies were all issued
     for (int i = 0; rc == SLUICE_OK && i < n_streams; ++i) {
+      const int g = i / per_event;
+      const int g_experts = std::min(per_event, n_streams - g * per_event);
+      if (i % per_event == 0) {
+        // armed with the group's copy count before its first copy
+        hsa_signal_store_relaxed(L->fill_sig[g], (hsa_signal_value_t)g_experts * n_copy);
+        L->armed_groups = g + 1;
+      }
       const int local = L->streams[2 * i], slot = L->streams[2 * i + 1];
+      int in_expert = 0;  // this expert's copies issued
       for (const ParamRows& p : L->params) {
-        if (early && p.rows_dev != nullptr) {  // the gap kernel copies these rows itself
-          L->bytes += (int64_t)p.row_bytes;
-          continue;
-        }
+        L->bytes += (int64_t)p.row_bytes;
+        if (early && p.rows_dev != nullptr) continue;  // the gap kernel copies these rows itself
         int left = g_fail_after.load(std::memory_order_relaxed);
         while (left >= 0 && !g_fail_after.compare_exchange_weak(left, left - 1)) {
         }
-        hipError_t e = left == 0 ? hipErrorInvalidValue
-                                 : hipMemcpyAsync(p.slot_base + (size_t)slot * p.row_bytes,
-                                                  p.host_base + (size_t)local * p.row_bytes,
-                                                  p.row_bytes, hipMemcpyHostToDevice,
-                                                  R->copy[p.lane]);
-        if (e != hipSuccess) {
-          rc = (int)e;
+        void* dst = p.slot_base + (size_t)slot * p.row_bytes;
+        const void* src = p.host_base + (size_t)local * p.row_bytes;
+        const uint32_t eng = R->engine[p.lane];
+        const hsa_status_t st =
+            left == 0 ? HSA_STATUS_ERROR
+            : eng != 0
+                ? hsa_amd_memory_async_copy_on_engine(dst, R->gpu_agent, src, R->cpu_agent,
+                                                      p.row_bytes, 0, nullptr, L->fill_sig[g],
+                                                      (hsa_amd_sdma_engine_id_t)eng, true)
+                : hsa_amd_memory_async_copy(dst, R->gpu_agent, src, R->cpu_agent, p.row_bytes, 0,
+                                            nullptr, L->fill_sig[g]);
+        if (st != HSA_STATUS_SUCCESS) {
+          L->bytes -= (int64_t)p.row_bytes;
+          rc = SLUICE_E_COPY;
           break;
         }
-        L->bytes += (int64_t)p.row_bytes;
+        ++in_expert;
         if (i == 0 && &p == &L->params[0]) SLUICE_HTRACE(23, L, want, p.lane);
       }
-      if (rc == SLUICE_OK && ((i + 1) % per_event == 0 || i + 1 == n_streams)) {
-        for (int l = 0; l < kLanes && rc == SLUICE_OK; ++l) {
-          if ((L->lane_mask >> l & 1u) == 0) continue;
-          const hipError_t e = hipEventRecord(L->fill_ev[kLanes * issued + l], R->copy[l]);
-          if (e != hipSuccess) rc = (int)e;
-        }
-        if (rc == SLUICE_OK) ++issued;
+      if (rc != SLUICE_OK) {
+        // the group's copies that were never issued will not count down
+        const int left_out = (g_experts - (i - g * per_event)) * n_copy - in_expert;
+        hsa_signal_subtract_relaxed(L->fill_sig[g], (hsa_signal_value_t)left_out);
+      } else if ((i + 1) % per_event == 0 || i + 1 == n_streams) {
+        whole = g + 1;
       }
       if (!answered && rc == SLUICE_OK) {
         respond(L, want, SLUICE_OK, n_streams);
@@ -929,14 +1011,12 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     // (a failure before the answer still answers the device: the map and
     // the fill list are the bookkeeping's; the slots are marked below)
     if (!answered) respond(L, want, SLUICE_OK, n_streams);
-    SLUICE_HTRACE(25, L, want, issued);
+    SLUICE_HTRACE(25, L, want, whole);
     // Each group of experts landed: mark its slots ready for this gap.
     int marked = 0;  // streams whose slots are marked
     int landed = 0;  // streams whose group's copies completed
-    for (int g = 0; g < issued; ++g) {
-      int w = SLUICE_OK;
-      for (int l = 0; l < kLanes && w == SLUICE_OK; ++l)
-        if (L->lane_mask >> l & 1u) w = wait_event(L->fill_ev[kLanes * g + l]);
+    for (int g = 0; g < whole; ++g) {
+      const int w = wait_signal(L->fill_sig[g]);
       if (w != SLUICE_OK) {
         if (rc == SLUICE_OK) rc = w;
         break;
@@ -948,6 +1028,9 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
         __atomic_store_n(&mb->slot_ready[L->streams[2 * marked + 1]], want, __ATOMIC_RELEASE);
       SLUICE_HTRACE(27, L, want, g);
     }
+    // every issued copy has completed (or the layer needs a resync, which
+    // waits for them again)
+    if (rc == SLUICE_OK || drain_copies(L) == SLUICE_OK) L->armed_groups = 0;
     if (rc != SLUICE_OK) {
       // A failed stream-in is reported to the caller (and, under the server,
       // raises the abort flag).  The device must not wait for rows that are
@@ -1061,7 +1144,8 @@ extern "C" int sluice_layer_destroy(sluice_layer* L) {
   if (L->server != nullptr) return SLUICE_E_STATE;
   int rc = SLUICE_OK;
   if (L->map_dev != nullptr && L->mb != nullptr) slotwait_unregister(L->map_dev);
-  for (hipEvent_t ev : L->fill_ev) (void)hipEventDestroy(ev);
+  if (drain_copies(L) != SLUICE_OK) return SLUICE_E_STATE;  // copies still write its slots
+  for (hsa_signal_t sig : L->fill_sig) (void)hsa_signal_destroy(sig);
   for (ParamRows& p : L->params)
     if (p.rows_dev != nullptr) {
       const hipError_t e = hipFree(p.rows_dev);
@@ -1307,6 +1391,12 @@ extern "C" int sluice_layer_gap_resync(sluice_layer* L) {
   const int rrc = device_res(L->device, &R);
   if (rrc != SLUICE_OK) return rrc;
   for (hipStream_t s : R->copy) SLUICE_HIP_CHECK(hipStreamSynchronize(s));
+  {
+    std::lock_guard<std::mutex> lk(L->mu);
+    const int d = drain_copies(L);
+    if (d != SLUICE_OK) return d;
+    L->armed_groups = 0;
+  }
   int32_t dev_stamp = 0;
   SLUICE_HIP_CHECK(hipMemcpy(&dev_stamp, L->dev_block + L->c.E, sizeof(int32_t),
                              hipMemcpyDeviceToHost));
@@ -1817,6 +1907,7 @@ extern "C" const char* sluice_strerror(int code) {
     case SLUICE_E_SCRATCH:
       return "the call needs more scratch than sluice_fused_experts_bf16_noalloc holds "
              "(SLUICE_NOALLOC_SCRATCH_BYTES); use sluice_fused_experts_bf16 with a workspace";
+    case SLUICE_E_COPY: return "a host-to-device row copy failed to issue or complete";
     default:
       if (code > 0) return hipGetErrorString((hipError_t)code);
       return "unknown sluice error";
