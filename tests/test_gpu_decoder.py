@@ -364,3 +364,43 @@ def test_offloaded_decode_equals_fully_resident_decode(monkeypatch, spec, layers
     full, full_misses = decode(E)
     assert misses > slots and full_misses == 0, (misses, full_misses)
     assert np.array_equal(off, full)
+
+
+def test_decode_on_streams_that_share_hardware_queues():
+    """With more streams than the process has hardware queues (HIP shares an
+    in-order queue between streams beyond GPU_MAX_HW_QUEUES), a miss-heavy
+    pipelined decode runs on every stream: streams made before the decoder's
+    copy machinery and after it, 6 each, the one-graph step with the gap
+    server on each in turn.  The gap's row copies go to the SDMA engines with
+    HSA completion signals, so no copy waits behind the expert product that
+    waits for it; every gap wait is bounded at 5 s here, so a copy stuck
+    behind a kernel ends as an error, not a hang."""
+    from sluice_amd import _lib
+    from sluice_amd.decoder import SyntheticDecoder
+
+    lib = _lib.load()
+    before = [torch.cuda.Stream(device=DEV) for _ in range(6)]
+    for s in before:
+        with torch.cuda.stream(s):
+            torch.zeros(1, device=DEV).add_(1)
+    torch.cuda.synchronize()
+    assert lib.sluice_gap_set_timeout(5.0) == 0
+    dec = SyntheticDecoder("qwen3", max_batch=4, slots=32, gen_len=96, layers=4, device=DEV,
+                           seed=3, uniform_routing=True)
+    try:
+        after = [torch.cuda.Stream(device=DEV) for _ in range(6)]
+        misses = 0
+        for n, s in enumerate(before + after):
+            print(f"decode on extra stream {n}", flush=True)
+            with torch.cuda.stream(s):
+                dec.graphs = {}
+                dec.capture(4)
+                for _ in range(4):
+                    dec.step_graphs(4)
+                dec.sync()  # raises on a gap wait that reached its bound
+            now = dec.gap_counters()["misses"]
+            assert now > misses, n  # every stream's steps streamed experts
+            misses = now
+    finally:
+        dec.close()
+        lib.sluice_gap_set_timeout(0.0)
