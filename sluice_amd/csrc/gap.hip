@@ -48,7 +48,6 @@
 
 #include <algorithm>
 #include <atomic>
-#include <cmath>
 #include <mutex>
 #include <new>
 #include <thread>
@@ -821,23 +820,12 @@ void respond(sluice_layer* L, int32_t stamp, int code, int n_fill) {
   __atomic_store_n(&mb->resp_stamp, stamp, __ATOMIC_RELEASE);
 }
 
-// Experts whose rows share one completion event.  Each event recorded
-// between copies idles the copy engine a few microseconds (~6 us measured
-// between 9.4 MB copies), while a group's rows only become usable once the
-// whole group landed, which exposes the last group's expert product (its
-// weights read at HBM rate, ~5 TB/s) after the stream ends.  With T bytes
-// streamed, groups of g bytes cost about (T / g) * 6 us + g / 5 TB/s, least
-// at g = sqrt(3e7 B * T): one expert per event for a few misses, several for
-// a miss-dominated gap.
-int experts_per_event(const sluice_layer* L, int n_streams) {
-  size_t per_expert = 0;
-  for (const ParamRows& p : L->params) per_expert += p.row_bytes;
-  if (per_expert == 0 || n_streams <= 1) return 1;
-  const double total = (double)per_expert * (double)n_streams;
-  const double group = std::sqrt(3.0e7 * total);
-  const int k = (int)(group / (double)per_expert + 0.5);
-  return std::max(1, std::min(k, n_streams));
-}
+// Experts whose rows share one completion signal: one.  Every SDMA copy
+// decrements its group's signal as it completes anyway, so a finer grouping
+// costs the copy engine nothing (HIP completion events, recorded between
+// copies, each idled it ~6 us, which made groups of several experts pay),
+// and each expert's product starts as soon as its own rows landed.
+constexpr int kExpertsPerSignal = 1;
 
 // Spin until signal `sig` counted down to zero (bounded).  0, or
 // SLUICE_E_COPY (a copy reported an error: the runtime sets the signal
@@ -945,7 +933,7 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     // before the raise; the device map is left as it was, answered after.)
     const bool early = waits && grc == 0 && rc == SLUICE_OK &&
                        g_pipelined.load(std::memory_order_relaxed) != 0;
-    const int per_event = experts_per_event(L, n_streams);
+    const int per_event = kExpertsPerSignal;
     const int n_events = (n_streams + per_event - 1) / per_event;
     while (rc == SLUICE_OK && (int)L->fill_sig.size() < n_events) {
       hsa_signal_t sig{};

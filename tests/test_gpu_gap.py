@@ -491,13 +491,12 @@ def test_device_gap_with_no_tokens(monkeypatch, fast_hit):
 
 def test_failed_stream_in_drops_unlanded_fills_and_resync_installs_host_map(monkeypatch):
     """Failure handling forced from the host: in a gap whose 8 ids all miss
-    (Qwen3-sized experts, 9.4 MB each, so the fills stream in two groups of
-    5 and 3 experts with a completion event each), the 13th row copy is
-    made to fail (sluice_gap_inject_copy_failure).  The inline gap reports
-    the error; the device waited for nothing (its slots were marked ready);
-    the experts of the first group, seen to land, stay cached and hold their
-    host rows, those of the second leave the host's slot cache (their slots
-    free, taken next).  sluice_layer_gap_resync then writes the host's
+    (Qwen3-sized experts, two row copies each, one completion signal per
+    expert), the 13th row copy -- the first of the seventh expert -- is made
+    to fail (sluice_gap_inject_copy_failure).  The inline gap reports the
+    error; the device waited for nothing (its slots were marked ready); the
+    six experts seen to land stay cached and hold their host rows, the last
+    two leave the host's slot cache (their slots free, taken next).  sluice_layer_gap_resync then writes the host's
     standing map into the device map, and later gaps -- selecting the
     dropped experts again -- follow the oracle after the same drops."""
     from oracle.slru import LayerCache
@@ -545,7 +544,7 @@ def test_failed_stream_in_drops_unlanded_fills_and_resync_installs_host_map(monk
         lib.sluice_gap_inject_copy_failure(-1)
     streams = oracle.gap(missing.tolist())
     assert len(streams) == 8
-    for _, slot in streams[5:]:  # the second group's fills did not land
+    for _, slot in streams[6:]:  # the fills whose rows did not land
         assert oracle.unfill(slot)
     check_state()
     assert lib.sluice_layer_gap_resync(cache.handle) == 0
@@ -553,7 +552,7 @@ def test_failed_stream_in_drops_unlanded_fills_and_resync_installs_host_map(monk
     oracle.map, oracle.map_is_standing = oracle.standing_map(), True
     assert cache.expert_map_buf.cpu().tolist() == oracle.map
     _check_slots(cache, layer)
-    dropped = [oracle.global_of_local[loc] for loc, _ in streams[5:]]
+    dropped = [oracle.global_of_local[loc] for loc, _ in streams[6:]]
     for n in range(5):
         if n == 0:  # the dropped experts are selected again: they miss and stream
             others = rng.permutation([g for g in range(E) if g not in dropped])
