@@ -23,9 +23,9 @@
 //     reference's bookkeeping exactly (slru::Cache::gap: fast-hit, touches,
 //     claimed set, victims, overflow).  For a waiting device it answers with
 //     the standing slot table and the slots being filled, issues the misses'
-//     row copies as hipMemcpyAsync on the dedicated copy streams, and marks
-//     each filled slot ready once its rows landed (the expert product waits
-//     per slot).  It runs inline
+//     row copies as SDMA copies through the HSA runtime (two engines), and
+//     marks each filled slot ready once its rows landed (the expert product
+//     waits per slot).  It runs inline
 //     (sluice_layer_gap: launch + serve, the reference's eager op) or on a
 //     native server thread (sluice_gap_server_*), which makes the gap op
 //     capturable, so a whole decode step replays as one hipGraph.

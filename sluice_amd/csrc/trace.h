@@ -23,8 +23,8 @@
 //   host, gap service (layer id = the device map address >> 8):
 //     21 record copied out (v = misses the device counted)
 //     22 bookkeeping done (v = stream-ins)   23 first row copy issued
-//     24 device answered (v = experts per completion event)
-//     25 every row copy issued (v = events)  26 group g landed (v = g)
+//     24 device answered (v = experts per completion signal)
+//     25 every row copy issued (v = signals)  26 group g landed (v = g)
 //     27 group g's slots marked ready (v = g)
 #pragma once
 
