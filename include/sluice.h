@@ -254,7 +254,10 @@ int sluice_layer_create(int E, int local_n, int num_slots, int protected_cap,
 int sluice_layer_destroy(sluice_layer* layer);
 
 /* Register one per-expert parameter: slot buffer base (device, [S, row])
- * and pinned host store base ([local_n, row]), row_bytes per expert.
+ * and pinned host store base ([local_n, row]), row_bytes per expert.  On a
+ * layer with a device map both ranges must lie whole inside allocations the
+ * HIP/HSA runtime made or locked (SLUICE_E_INVAL otherwise): the gap copies
+ * rows with the SDMA engines directly.
  * On a layer with a device map, params with rows of at most 32 KB (whole
  * 16-byte vectors; up to 4 such params) are copied into HBM whole here
  * (local_n rows), and a gap answered before its rows land copies their rows

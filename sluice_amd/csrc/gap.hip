@@ -1159,9 +1159,35 @@ extern "C" int sluice_layer_destroy(sluice_layer* L) {
   return rc;
 }
 
+namespace {
+// [p, p + bytes) lies inside one allocation the HSA runtime knows (device
+// memory, or host memory it allocated or locked): the SDMA engines copy
+// from and to it directly, with no staging for pageable memory and no
+// bounds check of their own.
+bool known_range(const void* p, size_t bytes) {
+  hsa_amd_pointer_info_t info;
+  memset(&info, 0, sizeof(info));
+  info.size = sizeof(info);
+  if (hsa_amd_pointer_info(p, &info, nullptr, nullptr, nullptr) != HSA_STATUS_SUCCESS) return false;
+  if (info.type == HSA_EXT_POINTER_TYPE_UNKNOWN || bytes > info.sizeInBytes) return false;
+  const uintptr_t a = (uintptr_t)p;
+  for (const void* b : {info.hostBaseAddress, info.agentBaseAddress}) {
+    const uintptr_t base = (uintptr_t)b;
+    if (b != nullptr && a >= base && a - base <= info.sizeInBytes - bytes) return true;
+  }
+  return false;
+}
+}  // namespace
+
 extern "C" int sluice_layer_add_param(sluice_layer* L, void* slot_base_dev, const void* host_base,
                                       size_t row_bytes) {
   if (L == nullptr || slot_base_dev == nullptr || host_base == nullptr || row_bytes == 0)
+    return SLUICE_E_INVAL;
+  // A layer with a device copies these rows with the SDMA engines: both
+  // ranges must be allocations the runtime knows, whole.
+  if (L->mb != nullptr &&
+      (!known_range(host_base, row_bytes * (size_t)L->c.local_n) ||
+       !known_range(slot_base_dev, row_bytes * (size_t)L->c.S)))
     return SLUICE_E_INVAL;
   std::lock_guard<std::mutex> lk(L->mu);
   L->params.push_back({(char*)slot_base_dev, (const char*)host_base, row_bytes, 0});

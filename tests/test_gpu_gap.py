@@ -277,6 +277,34 @@ def test_device_gap_v3_fp8_streams_four_rows_per_miss(monkeypatch, slru_golden, 
     off.close()
 
 
+def test_add_param_takes_only_whole_runtime_allocations():
+    """A device layer copies its rows with the SDMA engines, which neither
+    stage pageable memory nor check bounds: sluice_layer_add_param refuses a
+    host store that is not a runtime allocation or is smaller than local_n
+    rows (the check is against allocations: a tensor inside a larger cached
+    device block passes), and takes exact-size pinned and device buffers."""
+    import ctypes
+    from sluice_amd import _lib, ops
+
+    lib = _lib.load()
+    E, S, row = 16, 8, 1 << 20
+    emap = torch.full((E,), -1, dtype=torch.int32, device=DEV)
+    h = ctypes.c_void_p()
+    assert lib.sluice_layer_create(E, E, S, S // 2, _lib.int32_array(range(E)), emap.data_ptr(),
+                                   ctypes.byref(h)) == 0
+    try:
+        slots = torch.empty((S, row), dtype=torch.uint8, device=DEV)
+        pinned = ops.HostStore((E, row), torch.uint8)
+        half = ops.HostStore((E // 2, row), torch.uint8)
+        pageable = np.zeros((E, row), dtype=np.uint8)
+        bad = _lib.SLUICE_E_INVAL
+        assert lib.sluice_layer_add_param(h, slots.data_ptr(), pageable.ctypes.data, row) == bad
+        assert lib.sluice_layer_add_param(h, slots.data_ptr(), half.data_ptr(), row) == bad
+        assert lib.sluice_layer_add_param(h, slots.data_ptr(), pinned.data_ptr(), row) == 0
+    finally:
+        assert lib.sluice_layer_destroy(h) == 0
+
+
 def test_resync_restores_the_pulled_rows_of_every_cached_slot(monkeypatch):
     """The gap kernel copies an fp8 layer's scale rows into the slots it
     fills; a gap the host answered but the device never installed (its wait
