@@ -751,11 +751,11 @@ struct sluice_layer {
   int32_t* ids_host = nullptr;  // pinned staging of the step's ids
   size_t ids_cap = 0;
   int64_t classic_steps = 0, classic_waves = 0;
-  // per group of experts a gap streams: an HSA signal armed with the group's
-  // copy count, decremented by each copy as it completes; armed_groups of
-  // them may still have copies in flight after a failed stream-in
+  // one HSA completion signal per row copy of a gap (armed at 1; the copy
+  // completes it); the first armed_copies of them may still be in flight
+  // after a failed stream-in
   std::vector<hsa_signal_t> fill_sig;
-  int armed_groups = 0;
+  int armed_copies = 0;
   unsigned lane_mask = 0;  // lanes that carry some param's rows
 };
 
@@ -820,16 +820,17 @@ void respond(sluice_layer* L, int32_t stamp, int code, int n_fill) {
   __atomic_store_n(&mb->resp_stamp, stamp, __ATOMIC_RELEASE);
 }
 
-// Experts whose rows share one completion signal: one.  Every SDMA copy
-// decrements its group's signal as it completes anyway, so a finer grouping
-// costs the copy engine nothing (HIP completion events, recorded between
-// copies, each idled it ~6 us, which made groups of several experts pay),
-// and each expert's product starts as soon as its own rows landed.
-constexpr int kExpertsPerSignal = 1;
-
-// Spin until signal `sig` counted down to zero (bounded).  0, or
-// SLUICE_E_COPY (a copy reported an error: the runtime sets the signal
-// negative) or SLUICE_E_TIMEOUT.
+// Every row copy of a gap has a completion signal of its own, armed at 1,
+// and an expert's slot is marked ready once all of its copies completed:
+// the product of each expert starts as soon as its own rows landed (a
+// completion costs the copy engine nothing, unlike a HIP event recorded
+// between copies, which idled it ~6 us).  The runtime completes a signal by
+// decrementing it, a tool that wraps the copy may store zero instead: one
+// signal per copy is right under either.
+//
+// Spin until signal `sig` reached zero (bounded).  0, or SLUICE_E_COPY (a
+// copy reported an error: the runtime sets the signal negative) or
+// SLUICE_E_TIMEOUT.
 int wait_signal(hsa_signal_t sig) {
   const double t0 = now_s();
   unsigned spins = 0;
@@ -845,8 +846,8 @@ int wait_signal(hsa_signal_t sig) {
 // Wait (bounded) until no copy of the layer's last stream-in is in flight
 // (a copy that failed is not in flight either).  0 or SLUICE_E_TIMEOUT.
 int drain_copies(sluice_layer* L) {
-  for (int g = 0; g < L->armed_groups && g < (int)L->fill_sig.size(); ++g)
-    if (wait_signal(L->fill_sig[g]) == SLUICE_E_TIMEOUT) return SLUICE_E_TIMEOUT;
+  for (int c = 0; c < L->armed_copies && c < (int)L->fill_sig.size(); ++c)
+    if (wait_signal(L->fill_sig[c]) == SLUICE_E_TIMEOUT) return SLUICE_E_TIMEOUT;
   return SLUICE_OK;
 }
 
@@ -933,37 +934,31 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     // before the raise; the device map is left as it was, answered after.)
     const bool early = waits && grc == 0 && rc == SLUICE_OK &&
                        g_pipelined.load(std::memory_order_relaxed) != 0;
-    const int per_event = kExpertsPerSignal;
-    const int n_events = (n_streams + per_event - 1) / per_event;
-    while (rc == SLUICE_OK && (int)L->fill_sig.size() < n_events) {
+    // rows copied per expert (the gap kernel copies the pulled ones itself)
+    int n_copy = 0;
+    for (const ParamRows& p : L->params) n_copy += !(early && p.rows_dev != nullptr);
+    const size_t n_sig = (size_t)n_streams * (size_t)n_copy;
+    while (rc == SLUICE_OK && L->fill_sig.size() < n_sig) {
       hsa_signal_t sig{};
       if (hsa_signal_create(0, 0, nullptr, &sig) != HSA_STATUS_SUCCESS) rc = SLUICE_E_COPY;
       else L->fill_sig.push_back(sig);
     }
-    // rows copied per expert (the gap kernel copies the pulled ones itself)
-    int n_copy = 0;
-    for (const ParamRows& p : L->params) n_copy += !(early && p.rows_dev != nullptr);
     // The link is the bottleneck of a missing step: the first expert's rows
     // are queued before the device is answered (its resident experts then
     // compute while the rows stream), the other experts' after.
     bool answered = !early;
-    int whole = 0;  // groups whose copies were all issued
+    int whole = 0;  // experts whose copies were all issued
+    int armed = 0;  // copies issued, each with its own signal
     for (int i = 0; rc == SLUICE_OK && i < n_streams; ++i) {
-      const int g = i / per_event;
-      const int g_experts = std::min(per_event, n_streams - g * per_event);
-      if (i % per_event == 0) {
-        // armed with the group's copy count before its first copy
-        hsa_signal_store_relaxed(L->fill_sig[g], (hsa_signal_value_t)g_experts * n_copy);
-        L->armed_groups = g + 1;
-      }
       const int local = L->streams[2 * i], slot = L->streams[2 * i + 1];
-      int in_expert = 0;  // this expert's copies issued
       for (const ParamRows& p : L->params) {
         L->bytes += (int64_t)p.row_bytes;
         if (early && p.rows_dev != nullptr) continue;  // the gap kernel copies these rows itself
         int left = g_fail_after.load(std::memory_order_relaxed);
         while (left >= 0 && !g_fail_after.compare_exchange_weak(left, left - 1)) {
         }
+        const hsa_signal_t sig = L->fill_sig[armed];
+        hsa_signal_store_relaxed(sig, 1);
         void* dst = p.slot_base + (size_t)slot * p.row_bytes;
         const void* src = p.host_base + (size_t)local * p.row_bytes;
         const uint32_t eng = R->engine[p.lane];
@@ -971,54 +966,51 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
             left == 0 ? HSA_STATUS_ERROR
             : eng != 0
                 ? hsa_amd_memory_async_copy_on_engine(dst, R->gpu_agent, src, R->cpu_agent,
-                                                      p.row_bytes, 0, nullptr, L->fill_sig[g],
+                                                      p.row_bytes, 0, nullptr, sig,
                                                       (hsa_amd_sdma_engine_id_t)eng, true)
                 : hsa_amd_memory_async_copy(dst, R->gpu_agent, src, R->cpu_agent, p.row_bytes, 0,
-                                            nullptr, L->fill_sig[g]);
+                                            nullptr, sig);
         if (st != HSA_STATUS_SUCCESS) {
+          hsa_signal_store_relaxed(sig, 0);
           L->bytes -= (int64_t)p.row_bytes;
           rc = SLUICE_E_COPY;
           break;
         }
-        ++in_expert;
+        L->armed_copies = ++armed;
         if (i == 0 && &p == &L->params[0]) SLUICE_HTRACE(23, L, want, p.lane);
       }
-      if (rc != SLUICE_OK) {
-        // the group's copies that were never issued will not count down
-        const int left_out = (g_experts - (i - g * per_event)) * n_copy - in_expert;
-        hsa_signal_subtract_relaxed(L->fill_sig[g], (hsa_signal_value_t)left_out);
-      } else if ((i + 1) % per_event == 0 || i + 1 == n_streams) {
-        whole = g + 1;
-      }
+      if (rc == SLUICE_OK) whole = i + 1;
       if (!answered && rc == SLUICE_OK) {
         respond(L, want, SLUICE_OK, n_streams);
         answered = true;
-        SLUICE_HTRACE(24, L, want, per_event);
+        SLUICE_HTRACE(24, L, want, n_copy);
       }
     }
     // (a failure before the answer still answers the device: the map and
     // the fill list are the bookkeeping's; the slots are marked below)
     if (!answered) respond(L, want, SLUICE_OK, n_streams);
-    SLUICE_HTRACE(25, L, want, whole);
-    // Each group of experts landed: mark its slots ready for this gap.
-    int marked = 0;  // streams whose slots are marked
-    int landed = 0;  // streams whose group's copies completed
-    for (int g = 0; g < whole; ++g) {
-      const int w = wait_signal(L->fill_sig[g]);
+    SLUICE_HTRACE(25, L, want, armed);
+    // Each expert landed (every one of its copies completed): mark its slot
+    // ready for this gap.
+    int landed = 0;  // streams whose copies completed, their slots marked
+    for (int i = 0; i < whole; ++i) {
+      int w = SLUICE_OK;
+      for (int c = 0; c < n_copy && w == SLUICE_OK; ++c)
+        w = wait_signal(L->fill_sig[(size_t)i * n_copy + c]);
       if (w != SLUICE_OK) {
         if (rc == SLUICE_OK) rc = w;
         break;
       }
-      landed = std::min(n_streams, (g + 1) * per_event);
-      SLUICE_HTRACE(26, L, want, g);
+      landed = i + 1;
+      SLUICE_HTRACE(26, L, want, i);
       if (!early) continue;
-      for (; marked < landed; ++marked)
-        __atomic_store_n(&mb->slot_ready[L->streams[2 * marked + 1]], want, __ATOMIC_RELEASE);
-      SLUICE_HTRACE(27, L, want, g);
+      __atomic_store_n(&mb->slot_ready[L->streams[2 * i + 1]], want, __ATOMIC_RELEASE);
+      SLUICE_HTRACE(27, L, want, i);
     }
+    int marked = landed;  // streams whose slots are marked
     // every issued copy has completed (or the layer needs a resync, which
     // waits for them again)
-    if (rc == SLUICE_OK || drain_copies(L) == SLUICE_OK) L->armed_groups = 0;
+    if (rc == SLUICE_OK || drain_copies(L) == SLUICE_OK) L->armed_copies = 0;
     if (rc != SLUICE_OK) {
       // A failed stream-in is reported to the caller (and, under the server,
       // raises the abort flag).  The device must not wait for rows that are
@@ -1409,7 +1401,7 @@ extern "C" int sluice_layer_gap_resync(sluice_layer* L) {
     std::lock_guard<std::mutex> lk(L->mu);
     const int d = drain_copies(L);
     if (d != SLUICE_OK) return d;
-    L->armed_groups = 0;
+    L->armed_copies = 0;
   }
   int32_t dev_stamp = 0;
   SLUICE_HIP_CHECK(hipMemcpy(&dev_stamp, L->dev_block + L->c.E, sizeof(int32_t),
