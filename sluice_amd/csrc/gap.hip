@@ -722,6 +722,7 @@ struct ParamRows {
   size_t row_bytes;
   int lane;                 // copy lane of this param's rows
   char* rows_dev = nullptr;  // HBM copy of all host rows when the gap kernel pulls them
+  hsa_agent_t host_agent{};  // the agent owning the host rows (0: the first CPU agent)
 };
 
 struct sluice_gap_server;
@@ -962,14 +963,15 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
         void* dst = p.slot_base + (size_t)slot * p.row_bytes;
         const void* src = p.host_base + (size_t)local * p.row_bytes;
         const uint32_t eng = R->engine[p.lane];
+        const hsa_agent_t from = p.host_agent.handle != 0 ? p.host_agent : R->cpu_agent;
         const hsa_status_t st =
             left == 0 ? HSA_STATUS_ERROR
             : eng != 0
-                ? hsa_amd_memory_async_copy_on_engine(dst, R->gpu_agent, src, R->cpu_agent,
-                                                      p.row_bytes, 0, nullptr, sig,
-                                                      (hsa_amd_sdma_engine_id_t)eng, true)
-                : hsa_amd_memory_async_copy(dst, R->gpu_agent, src, R->cpu_agent, p.row_bytes, 0,
-                                            nullptr, sig);
+                ? hsa_amd_memory_async_copy_on_engine(dst, R->gpu_agent, src, from, p.row_bytes, 0,
+                                                      nullptr, sig, (hsa_amd_sdma_engine_id_t)eng,
+                                                      true)
+                : hsa_amd_memory_async_copy(dst, R->gpu_agent, src, from, p.row_bytes, 0, nullptr,
+                                            sig);
         if (st != HSA_STATUS_SUCCESS) {
           hsa_signal_store_relaxed(sig, 0);
           L->bytes -= (int64_t)p.row_bytes;
@@ -1156,11 +1158,12 @@ namespace {
 // memory, or host memory it allocated or locked): the SDMA engines copy
 // from and to it directly, with no staging for pageable memory and no
 // bounds check of their own.
-bool known_range(const void* p, size_t bytes) {
+bool known_range(const void* p, size_t bytes, hsa_agent_t* owner = nullptr) {
   hsa_amd_pointer_info_t info;
   memset(&info, 0, sizeof(info));
   info.size = sizeof(info);
   if (hsa_amd_pointer_info(p, &info, nullptr, nullptr, nullptr) != HSA_STATUS_SUCCESS) return false;
+  if (owner != nullptr) *owner = info.agentOwner;
   if (info.type == HSA_EXT_POINTER_TYPE_UNKNOWN || bytes > info.sizeInBytes) return false;
   const uintptr_t a = (uintptr_t)p;
   for (const void* b : {info.hostBaseAddress, info.agentBaseAddress}) {
@@ -1177,12 +1180,18 @@ extern "C" int sluice_layer_add_param(sluice_layer* L, void* slot_base_dev, cons
     return SLUICE_E_INVAL;
   // A layer with a device copies these rows with the SDMA engines: both
   // ranges must be allocations the runtime knows, whole.
+  hsa_agent_t host_agent{};
   if (L->mb != nullptr &&
-      (!known_range(host_base, row_bytes * (size_t)L->c.local_n) ||
+      (!known_range(host_base, row_bytes * (size_t)L->c.local_n, &host_agent) ||
        !known_range(slot_base_dev, row_bytes * (size_t)L->c.S)))
     return SLUICE_E_INVAL;
   std::lock_guard<std::mutex> lk(L->mu);
   L->params.push_back({(char*)slot_base_dev, (const char*)host_base, row_bytes, 0});
+  hsa_device_type_t host_type{};
+  if (host_agent.handle != 0 &&
+      hsa_agent_get_info(host_agent, HSA_AGENT_INFO_DEVICE, &host_type) == HSA_STATUS_SUCCESS &&
+      host_type == HSA_DEVICE_TYPE_CPU)
+    L->params.back().host_agent = host_agent;
   // Small rows are pulled by the gap kernel from a copy of all of them in
   // HBM (PullRows); a layer without a device keeps host copies.
   ParamRows& np = L->params.back();
