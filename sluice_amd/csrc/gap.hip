@@ -48,6 +48,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <mutex>
 #include <new>
 #include <thread>
@@ -1080,8 +1081,17 @@ struct sluice_gap_server {
   std::atomic<int64_t> served{0};
 };
 
+// The server spins while gaps arrive (a decode step posts one per MoE layer,
+// every ~0.1 ms); after kServerIdleS without a record it naps kServerNapUs
+// between sweeps, so an idle engine does not hold a core.  The first gap
+// after such a pause is served up to one nap (plus the wake-up) late.
+constexpr double kServerIdleS = 5e-3;
+constexpr int kServerNapUs = 50;
+
 static void server_loop(sluice_gap_server* S) {
   (void)hipSetDevice(S->device);
+  double last = now_s();
+  unsigned idle = 0;
   while (!S->stop.load(std::memory_order_acquire)) {
     bool any = false;
     for (sluice_layer* L : S->layers) {
@@ -1095,7 +1105,17 @@ static void server_loop(sluice_gap_server* S) {
         __atomic_store_n(g_abort_host, 1, __ATOMIC_RELEASE);
       }
     }
-    if (!any) _mm_pause();
+    if (any) {
+      idle = 0;
+      last = -1.0;  // read the clock again on the next idle sweep
+      continue;
+    }
+    _mm_pause();
+    if ((++idle & 255u) != 0) continue;
+    const double t = now_s();
+    if (last < 0) last = t;
+    if (t - last > kServerIdleS)
+      std::this_thread::sleep_for(std::chrono::microseconds(kServerNapUs));
   }
 }
 
