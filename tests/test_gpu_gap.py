@@ -96,15 +96,22 @@ def _case_ids():
     return [f"{g['cases'][i]['name']}-fh{int(g['cases'][i]['fast_hit'])}" for i in _cases(g)]
 
 
+@pytest.mark.parametrize("rows", ["pulled", "sdma"])
 @pytest.mark.parametrize("idx", range(len(_case_ids())), ids=_case_ids())
-def test_device_gap_replays_reference(monkeypatch, slru_golden, idx):
+def test_device_gap_replays_reference(monkeypatch, slru_golden, idx, rows):
+    """A golden trace replayed through the device gap: per step the slot
+    state, the device map and the plan of the reference; every cached
+    slot's rows equal its host rows.  rows="pulled": 8 KB and 4 KB rows,
+    which the gap kernel copies itself; rows="sdma": 256 KB and 128 KB rows
+    on the copy engines."""
     case = slru_golden["cases"][_cases(slru_golden)[idx]]
-    print(f"gap case {case['name']} fast_hit={case['fast_hit']}", flush=True)
+    print(f"gap case {case['name']} fast_hit={case['fast_hit']} rows={rows}", flush=True)
     E, local_n, k = case["E"], case["local_n"], case["k"]
     emap = None
     if case["local_of"] is not None:
         emap = torch.tensor(case["local_of"], dtype=torch.int32)
-    layer = _Layer(E, local_n, expert_map=emap)
+    H, I = (64, 32) if rows == "pulled" else (1024, 64)
+    layer = _Layer(E, local_n, H=H, I=I, expert_map=emap)
     off = _offloader(monkeypatch, case["slots"], case["protect_frac"], case["fast_hit"])
     if case["pins"]:
         off._pin_layers = {0: list(case["pins"])}  # what SLUICE_PIN_FILE would hold
@@ -118,11 +125,12 @@ def test_device_gap_replays_reference(monkeypatch, slru_golden, idx):
     from sluice_amd import _lib
     cache.plan = torch.zeros(_lib.load().sluice_moe_plan_ints(1, cache.num_slots),
                              dtype=torch.int32, device=DEV)
+    assert _lib.load().sluice_layer_pulled_params(cache.handle) == (2 if rows == "pulled" else 0)
     assert cache.free_slots == case["init"]["free_slots"]
     assert cache.expert_in_slot == [None if v < 0 else v
                                     for v in case["init"]["expert_in_slot"]]
     _check_slots(cache, layer)  # pinned rows were copied in at install
-    hs = torch.zeros((1, 64), dtype=torch.bfloat16, device=DEV)
+    hs = torch.zeros((1, H), dtype=torch.bfloat16, device=DEV)
     for n, step in enumerate(case["steps"]):
         ids = torch.tensor(step["ids"], dtype=torch.int32, device=DEV).view(-1, k)
         overflow = False
