@@ -4,9 +4,10 @@
     python -m sluice_amd.build --trace    # sluice_amd/libsluice_hip_trace.so
 
 Each HIP source compiles to an object in parallel, then one link step makes
-``sluice_amd/libsluice_hip.so``.  The library links against the HIP runtime
-that torch ships (same soname as /opt/rocm's), with an rpath to it, so torch
-and the library always share one runtime.
+``sluice_amd/libsluice_hip.so``.  The library links against the HIP and HSA
+runtimes that torch ships (same sonames as /opt/rocm's), with an rpath to
+them, so torch and the library always share one runtime of each (load torch
+first).
 """
 
 from __future__ import annotations
