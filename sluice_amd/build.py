@@ -79,14 +79,14 @@ def _run(cmd: list[str]) -> str:
 
 
 # Room the split launch of the expert product must leave per SIMD.  Its
-# pending workgroups wait for slots while the copies that fill them run, and
-# the runtime copies small host rows with a kernel of its own: one
-# 512-thread workgroup (two waves per SIMD) allocating 16 VGPRs per lane (the
-# rocprofv3 kernel trace of __amd_rocclr_copyBuffer on MI355X).  If the split
-# launch's waves filled the 512-VGPR file of every SIMD, such a copy could not
-# start while they wait and the waits would run to their bound.  The gap
-# kernel copies small rows itself (fp8 scale rows); this keeps room for the
-# rest (rows not in whole 16-byte vectors, more than 4 such params).
+# pending workgroups wait for slots while the copies that fill them run.  The
+# gap's copies go to the SDMA engines, but a host-to-device copy that runs as
+# a kernel (a HIP-stream copy of small host rows, or any copy with SDMA
+# switched off in the runtime) is one 512-thread workgroup (two waves per
+# SIMD) allocating 16 VGPRs per lane (the rocprofv3 kernel trace of
+# __amd_rocclr_copyBuffer on MI355X).  If the split launch's waves filled the
+# 512-VGPR file of every SIMD, such a copy could not start while they wait
+# and the waits would run to their bound.
 VGPR_FILE = 512
 COPY_KERNEL_VGPRS_PER_SIMD = 2 * 16
 WAITING_KERNELS = ("moe_gemm2_split_kernel",)

@@ -261,12 +261,13 @@ constexpr int kGapMaxPerThread = SLUICE_MAX_EXPERTS / kLookupThreads;
 // Per-expert params whose rows are small (fp8 block-scale rows, a few KB):
 // the layer keeps a copy of all their rows in HBM, and a gap that answers
 // before its rows land copies them into the filled slots itself, right
-// after it installs the map.  A hipMemcpyAsync of so few bytes runs as a
-// runtime copy kernel on the CUs, not on the copy engine, and the expert
-// product's pending workgroups, which wait for these slots, could hold every
-// CU it needs; and a read of host memory issued while the copy engine fills
-// the link waits tens of microseconds behind it.  (The big rows stay on the
-// copy engine, which needs no CU.)
+// after it installs the map.  On a copy engine such a row would queue
+// behind the big rows of its lane and cost a completion of its own; as a
+// HIP-stream copy it ran as a runtime copy kernel on the CUs, which the
+// expert product's pending workgroups, waiting for these slots, could hold;
+// and a read of host memory issued while the copy engine fills the link
+// waits tens of microseconds behind it.  (The big rows stay on the copy
+// engines, which need no CU.)
 constexpr int kMaxPull = 4;
 constexpr size_t kPullMaxRowBytes = 32 << 10;
 struct PullRows {

@@ -912,13 +912,12 @@ long split_grid_for(int P, int P2, int I, int n_groups) {
 }
 
 // Workgroups of a grid-stride launch over a map whose slots may stream, all
-// of which may wait for slots at the same time.  The runtime copies small
-// host rows (a few KB) with a kernel of its own (one 512-thread workgroup,
-// 16 VGPRs per lane), not the copy engine; if waiting workgroups held every
-// CU, such a copy could not start and the waits it feeds would run to their
-// bound.  The gap kernel copies small rows itself (fp8 scale rows), so this
-// guards the rest (rows not in whole 16-byte vectors, more than 4 such
-// params).  The grid leaves one of the
+// of which may wait for slots at the same time.  The gap's row copies go to
+// the SDMA engines; a host-to-device copy that runs as a kernel instead (a
+// HIP-stream copy of small host rows, or any copy with SDMA switched off in
+// the runtime) is one 512-thread workgroup at 16 VGPRs per lane, and if
+// waiting workgroups held every CU, such a copy could not start and the
+// waits it feeds would run to their bound.  So the grid leaves one of the
 // kernel's workgroup places per CU free: (workgroups per CU at its occupancy
 // - 1) x CUs, looked up once per device and kernel.  The split launch keeps
 // one item per workgroup (a loop over tickets costs it a wave of occupancy);
