@@ -261,8 +261,10 @@ int sluice_layer_destroy(sluice_layer* layer);
  * On a layer with a device map, params with rows of at most 32 KB (whole
  * 16-byte vectors; up to 4 such params) are copied into HBM whole here
  * (local_n rows), and a gap answered before its rows land copies their rows
- * into the filled slots from there in the gap kernel; other rows go through
- * hipMemcpyAsync on the copy lanes. */
+ * into the filled slots from there in the gap kernel, so such host rows must
+ * hold their final contents when the param is registered.  A gap's other
+ * rows go to the SDMA engines through the HSA runtime (two copy lanes); the
+ * classic wave path copies with hipMemcpyAsync on HIP copy streams. */
 int sluice_layer_add_param(sluice_layer* layer, void* slot_base_dev,
                            const void* host_base, size_t row_bytes);
 
@@ -296,11 +298,11 @@ int sluice_layer_pin(sluice_layer* layer, int local, int debit_protected,
  * record, runs the reference's bookkeeping exactly (fast-hit, hit touches in
  * ascending id order, claimed set, victims), answers the device with the
  * standing slot table and the slots being filled, then streams the misses
- * as hipMemcpyAsync on the library's per-device copy lanes (two streams;
- * each per-expert param on the lane its layer assigned it, row bytes
- * balanced) and marks each filled slot ready once its rows landed on every
- * lane: the expert product computes resident
- * experts meanwhile and waits per filled slot.  `compute` (may be NULL) is
+ * as SDMA copies through the HSA runtime on two copy lanes (an SDMA engine
+ * each; each per-expert param on the lane its layer assigned it, row bytes
+ * balanced; the small pulled rows are copied by the gap kernel) and marks
+ * each filled slot ready once every copy of its rows completed: the expert
+ * product computes resident experts meanwhile and waits per filled slot.  `compute` (may be NULL) is
  * polled for errors while waiting.  SLUICE_E_OVERFLOW when the working set
  * does not fit (rows acquired before it still stream and land before the
  * answer, the map is left as it was, as in the reference).
