@@ -473,10 +473,12 @@ def measured_traffic(cfg, c, slots, uniform, algorithmic_bytes, kernel="moe_gemm
 
 def h2d_rates(dec):
     """Pinned host->device rates: one 64 MiB copy (the link's peak), and
-    expert stream-ins issued as the gap issues them -- one copy per
+    expert stream-ins laid out as the gap lays them out -- one copy per
     per-expert param per missing expert, slot rows <- host rows, each param
-    on its copy lane (two streams; the largest rows first, each to the lane
-    with fewer bytes so far: w13 | w2 for bf16)."""
+    on its copy lane (the largest rows first, each to the lane with fewer
+    bytes so far: w13 | w2 for bf16).  The lanes here are two HIP streams,
+    as on the classic wave path; the gap's own lanes are SDMA engines driven
+    through HSA, whose copy windows the gap timeline measures."""
     import torch
 
     from sluice_amd import _lib, ops

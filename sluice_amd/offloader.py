@@ -7,9 +7,9 @@ slot-buffer and expert-map layout, ``vllm::sluice_stream_gap`` op and
 patched ``runner._forward_entry``.  Underneath, the per-layer slot cache and
 the gap are native (libsluice_hip.so): a device kernel publishes the step's
 selected experts into pinned host memory, the native SLRU assigns slots as
-the reference's OrderedDict state machine does, missing experts stream with
-hipMemcpyAsync on two dedicated copy streams, and the device installs the
-standing expert map that the captured expert product reads by pointer.
+the reference's OrderedDict state machine does, missing experts stream as
+SDMA copies on two copy engines, and the device installs the standing
+expert map that the captured expert product reads by pointer.
 
 Execution model per MoE layer per decode step (T <= thr tokens):
 

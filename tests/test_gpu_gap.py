@@ -1,5 +1,5 @@
 """a3-a8 on the GPU: the device gap (slot-lookup kernel -> host record ->
-native SLRU -> hipMemcpyAsync of missing rows -> map kernel) replays the
+native SLRU -> SDMA copies of missing rows -> map kernel) replays the
 reference's golden traces bit for bit: stream-in order, slot assignment,
 segment order and the device expert map after every step, and every
 occupied slot's bytes equal the pinned host row of the expert it holds."""
