@@ -157,6 +157,7 @@ def run_batch(dec, c, steps, warmup, prefill=True, label=None):
         dec.step_graphs(c)
     dec.sync()
     before = dec.gap_counters()
+    stage0 = dec.off.stage_counters()
     cl0 = dec.off.classic_counters()
     pos0 = int(dec.state[c].pos[0]) if dec.has_attn else None
     # per-step times from events between the steps (the value is the
@@ -176,9 +177,14 @@ def run_batch(dec, c, steps, warmup, prefill=True, label=None):
     dec.sync()
     after = dec.gap_counters()
     delta = {k: after[k] - before[k] for k in after}
+    stage1 = dec.off.stage_counters()
+    sdelta = {k: stage1[k] - stage0[k] for k in ("filled", "h2d_bytes", "hits", "hit_bytes")}
     cl1 = dec.off.classic_counters()
     n_moe = len(dec.moe_layers)
-    h2d = delta["bytes"] / steps
+    # bytes over the host link: slot fills from the host store, plus the
+    # staging copies (a fill from a staged row moves HBM to HBM)
+    fill = delta["bytes"] / steps
+    h2d = (delta["bytes"] - sdelta["hit_bytes"] + sdelta["h2d_bytes"]) / steps
     return {
         "c": c, "steps": steps, "path": "classic" if dec.classic(c) else "gap",
         "routing": label or "zipf",
@@ -190,6 +196,12 @@ def run_batch(dec, c, steps, warmup, prefill=True, label=None):
         "gap_calls": delta["gaps"], "misses": delta["misses"],
         "fast_hits": delta["fast_hits"], "map_writes": delta["map_writes"],
         "h2d_bytes_per_step": h2d, "h2d_GBs_in_step": h2d / (dt / steps) / 1e9,
+        "fill_bytes_per_step": fill, "fill_GBs_in_step": fill / (dt / steps) / 1e9,
+        "staged": {"rows_per_layer": stage1["rows"] // max(n_moe, 1),
+                   "hits": sdelta["hits"],
+                   "hit_share_of_misses": sdelta["hits"] / max(delta["misses"], 1),
+                   "rows_filled": sdelta["filled"],
+                   "staging_h2d_bytes_per_step": sdelta["h2d_bytes"] / steps},
         "misses_per_layer_step": delta["misses"] / max(steps * n_moe, 1),
         "fast_hit_share": delta["fast_hits"] / max(delta["gaps"], 1),
         "prefill": {"tokens_per_sequence": dec.prompt_len if prefill else 0,
@@ -617,6 +629,7 @@ def measure(cfg, slots, batches, a, dev, gen_len, uniform=False, stores=None, lo
         log(f"{cfg} s{slots} c={c} ({r['path']}, {r['routing']}): {r['ms_per_step']:.3f} ms/step "
             f"{r['tok_per_s']:.1f} tok/s misses/layer-step={r['misses_per_layer_step']:.3f} "
             f"fast-hit={r['fast_hit_share']:.2%} H2D {r['h2d_GBs_in_step']:.1f} GB/s "
+            f"staged={r['staged']['hit_share_of_misses']:.1%} of misses "
             f"steps min/med/max {'/'.join(f'{v:.2f}' for v in r['step_ms_min_median_max'])} ms")
         rows.append(r)
     c_main = max(batches)

@@ -272,6 +272,28 @@ int sluice_layer_add_param(sluice_layer* layer, void* slot_base_dev,
  * kernel copies itself (see sluice_layer_add_param). */
 int sluice_layer_pulled_params(sluice_layer* layer);
 
+/* No counterpart in the reference.  Staging rows: `rows` (0..8) experts per
+ * layer kept in HBM outside the slots, each a copy of one expert the layer
+ * selects often but does not hold (the most selected ones, by counts of
+ * the gaps' selections halved every 4096 gaps).  A gap server fills them
+ * from the host store while the host link idles, in 1 MiB chunks on two
+ * SDMA engines the gap's own copies do not use, at most two chunks in
+ * flight per server.  A gap answered before its rows land copies a miss
+ * whose expert is staged into its slot from HBM, split over up to 12 more
+ * SDMA engines (device to device: ~45 us for a 17.3 MB expert instead of
+ * ~310 us over the link), ahead of the misses that cross the link.  Slot
+ * assignment, maps and slot bytes are what they are without staging.
+ * Costs rows x (bytes of the non-pulled params' rows) of HBM.  Call after
+ * every sluice_layer_add_param (which then returns SLUICE_E_STATE) with no
+ * gap server attached to the layer, not under graph capture (it allocates);
+ * a call with the count already set changes nothing.  SLUICE_E_INVAL when
+ * the device has no SDMA engines free for it. */
+int sluice_layer_set_staging(sluice_layer* layer, int rows);
+/* counters[6]: rows, rows holding an expert whole, rows filled so far,
+ * host-to-device bytes of staging copies, misses copied into their slots
+ * from a staged row, and those misses' bytes. */
+int sluice_layer_stage_counters(const sluice_layer* layer, int64_t* counters);
+
 /* Mark a slot as pre-filled with `local` outside the SLRU segments (full
  * residency pre-fill and static pins, offloader.py:1000-1010, 1046-1083);
  * debits protected_cap by one when `debit_protected` is set (pins). */

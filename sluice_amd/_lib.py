@@ -79,6 +79,8 @@ SIGNATURES = {
     "sluice_layer_destroy": (c_int, [_P]),
     "sluice_layer_add_param": (c_int, [_P, _P, _P, c_size_t]),
     "sluice_layer_pulled_params": (c_int, [_P]),
+    "sluice_layer_set_staging": (c_int, [_P, c_int]),
+    "sluice_layer_stage_counters": (c_int, [_P, _P]),
     "sluice_layer_pin": (c_int, [_P, c_int, c_int, POINTER(c_int)]),
     "sluice_layer_gap": (c_int, [_P, _P, c_int, c_int, _P]),
     "sluice_layer_gap_launch": (c_int, [_P, _P, c_int, _P, _P, c_size_t, _P, _P]),

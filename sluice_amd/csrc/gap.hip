@@ -560,6 +560,22 @@ __global__ __launch_bounds__(kLookupThreads) void pull_slots_kernel(const GapMai
 // ---------------------------------------------------------------------------
 constexpr int kLanes = 2;
 
+// Staging (sluice_layer_set_staging): rows in HBM outside the slots, each a
+// copy of one expert the layer selects often but does not hold, filled from
+// the host store while the link idles, in chunks on kStageLanes engines of
+// their own (at most kStageLanes chunks in flight per gap server, so a gap
+// whose copies start meanwhile shares the link with at most that).  A miss
+// whose expert is staged is copied into its slot from there, split over up
+// to kMaxD2d engines: device-to-device SDMA copies do not use the host link
+// and run ~59 GB/s per engine on MI355X, so a 17.3 MB expert lands in ~45 us
+// over 12 engines instead of ~310 us over the link, and a host copy on
+// another engine keeps its rate meanwhile.
+constexpr int kStageLanes = 2;
+constexpr int kMaxD2d = 12;
+constexpr size_t kStageChunk = 1 << 20;
+constexpr int kMaxStageRows = 8;
+constexpr int kStageHalfLife = 4096;  // gaps between halvings of the selection counts
+
 double now_s();
 
 #ifdef SLUICE_TRACE
@@ -599,10 +615,16 @@ struct DeviceRes {
   bool hsa = false;
   hsa_agent_t gpu_agent{}, cpu_agent{};
   uint32_t engine[kLanes] = {};
+  // staging: the engines that fill staging rows from the host (0: none
+  // free, no staging) and those that copy staged rows into slots
+  uint32_t stage_engine[kStageLanes] = {};
+  uint32_t d2d_engine[kMaxD2d] = {};
+  int n_d2d = 0;
   long long clock_khz = 0;
   // device word: the bound of every device wait, in wall-clock ticks; the
   // kernels read it when they start to wait (sluice_gap_set_timeout
-  // rewrites it, so graphs captured earlier follow the new bound)
+  // rewrites it, so graphs captured earlier follow the new bound).  Its
+  // 256-byte allocation's bytes 64..191 take the set-up's trial copies.
   long long* bound_dev = nullptr;
 };
 constexpr int kMaxDevices = 64;
@@ -618,6 +640,27 @@ hsa_status_t first_cpu_agent(hsa_agent_t agent, void* data) {
   if (t != HSA_DEVICE_TYPE_CPU) return HSA_STATUS_SUCCESS;
   *static_cast<hsa_agent_t*>(data) = agent;
   return HSA_STATUS_INFO_BREAK;
+}
+
+// A 64-byte device-to-device copy inside `scratch` (bytes 64..191 of a
+// 256-byte device allocation) completes on SDMA engine `eng`.  The runtime
+// in a torch process may report no engines for device-to-device copies
+// while they work, so each engine is tried.
+bool d2d_engine_works(const DeviceRes& r, char* scratch, uint32_t eng) {
+  hsa_signal_t sig{};
+  if (hsa_signal_create(1, 0, nullptr, &sig) != HSA_STATUS_SUCCESS) return false;
+  if (hsa_amd_memory_async_copy_on_engine(scratch + 128, r.gpu_agent, scratch + 64, r.gpu_agent, 64,
+                                          0, nullptr, sig, (hsa_amd_sdma_engine_id_t)eng,
+                                          true) != HSA_STATUS_SUCCESS) {
+    (void)hsa_signal_destroy(sig);
+    return false;
+  }
+  const double t0 = now_s();
+  hsa_signal_value_t v;
+  while ((v = hsa_signal_load_scacquire(sig)) > 0 && now_s() - t0 < 1.0) _mm_pause();
+  if (v > 0) return false;  // still in flight: the signal is left to it
+  (void)hsa_signal_destroy(sig);
+  return v == 0;
 }
 
 // The HSA agents of this device (the owner of its device memory) and of the
@@ -641,9 +684,34 @@ int hsa_setup(DeviceRes& r) {
   if (hsa_amd_memory_copy_engine_status(r.gpu_agent, r.cpu_agent, &mask) != HSA_STATUS_SUCCESS)
     mask = 0;
   int l = 0;
+  uint32_t used = 0;
   for (uint32_t bit = 1; bit != 0 && l < kLanes; bit <<= 1)
-    if (mask & bit) r.engine[l++] = bit;
+    if (mask & bit) {
+      r.engine[l++] = bit;
+      used |= bit;
+    }
   for (; l < kLanes; ++l) r.engine[l] = l > 0 ? r.engine[l - 1] : 0;
+  // staging engines: host-to-device engines neither lane uses, then
+  // device-to-device engines none of those uses
+  int ls = 0;
+  for (uint32_t bit = 1; bit != 0 && ls < kStageLanes; bit <<= 1)
+    if ((mask & bit) && !(used & bit)) {
+      r.stage_engine[ls++] = bit;
+      used |= bit;
+    }
+  uint32_t mask_d2d = 0;
+  if (hsa_amd_memory_copy_engine_status(r.gpu_agent, r.gpu_agent, &mask_d2d) != HSA_STATUS_SUCCESS ||
+      mask_d2d == 0)
+    mask_d2d = mask;
+  if (ls == kStageLanes)
+    for (uint32_t bit = 1; bit != 0 && r.n_d2d < kMaxD2d; bit <<= 1)
+      if ((mask_d2d & bit) && !(used & bit) &&
+          d2d_engine_works(r, reinterpret_cast<char*>(r.bound_dev), bit))
+        r.d2d_engine[r.n_d2d++] = bit;
+  if (ls < kStageLanes || r.n_d2d == 0) {
+    for (uint32_t& e : r.stage_engine) e = 0;
+    r.n_d2d = 0;
+  }
   r.hsa = true;
   return SLUICE_OK;
 }
@@ -760,6 +828,28 @@ struct sluice_layer {
   std::vector<hsa_signal_t> fill_sig;
   int armed_copies = 0;
   unsigned lane_mask = 0;  // lanes that carry some param's rows
+  std::vector<int> order, sig_end;  // a gap's streams in copy order; each one's last signal + 1
+  // Staging rows (sluice_layer_set_staging).  Row r holds (or is being
+  // filled with) expert `local`; its bytes are the non-pulled params' rows
+  // one after the other (stage_dev[p] + r * row_bytes for param p).
+  struct StageRow {
+    int local = -1;
+    int state = 0;      // kStageEmpty / kStageCopying / kStageReady
+    size_t issued = 0;  // bytes whose copies were issued
+    int in_flight = 0;  // of its chunks
+  };
+  std::vector<StageRow> stage;
+  std::vector<char*> stage_dev;  // per param (nullptr: pulled, or no staging)
+  std::vector<int> stage_parts;  // per param: copies that move a staged row into a slot
+  size_t stage_bytes = 0;        // one staged expert
+  hsa_signal_t stage_sig[kStageLanes] = {};
+  int stage_sig_row[kStageLanes] = {-1, -1};  // row of the chunk a signal tracks
+  size_t stage_sig_bytes[kStageLanes] = {};
+  std::vector<uint32_t> sel_count;  // [local_n] how often each expert was selected
+  int stage_gaps = 0;
+  bool stage_dirty = false;   // a gap was served since the rows were chosen
+  bool stage_broken = false;  // a staging copy failed: none until resync
+  int64_t stage_filled = 0, stage_h2d = 0, stage_hits = 0, stage_hit_bytes = 0;
 };
 
 namespace {
@@ -854,6 +944,182 @@ int drain_copies(sluice_layer* L) {
   return SLUICE_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Staging rows (L->mu held by the callers that other threads may race; the
+// gap server's own thread is the only one that issues staging copies).
+// ---------------------------------------------------------------------------
+constexpr int kStageEmpty = 0, kStageCopying = 1, kStageReady = 2;
+
+// The row holding expert `local` whole, or -1.
+int stage_ready_row(const sluice_layer* L, int local) {
+  for (size_t r = 0; r < L->stage.size(); ++r)
+    if (L->stage[r].state == kStageReady && L->stage[r].local == local) return (int)r;
+  return -1;
+}
+
+// A row still has bytes to copy.
+bool stage_has_copy(const sluice_layer* L) {
+  for (const sluice_layer::StageRow& row : L->stage)
+    if (row.state == kStageCopying && row.issued < L->stage_bytes) return true;
+  return false;
+}
+
+// Count the gap's selections: the staging candidates are the experts the
+// layer selects most often among those it does not hold (counts halved
+// every kStageHalfLife gaps, so they follow a drifting routing).
+void stage_count(sluice_layer* L) {
+  if (L->stage.empty()) return;
+  for (int32_t g : L->uniq) {
+    const int loc = (g >= 0 && g < L->c.E) ? L->c.local_of[g] : -1;
+    if (loc >= 0 && loc < L->c.local_n) ++L->sel_count[loc];
+  }
+  if (++L->stage_gaps >= kStageHalfLife) {
+    L->stage_gaps = 0;
+    for (uint32_t& v : L->sel_count) v >>= 1;
+  }
+  L->stage_dirty = true;
+}
+
+// Completed staging chunks; a row whose chunks all landed becomes ready.
+// A failed chunk empties its row and stops the layer's staging until
+// sluice_layer_gap_resync.
+void stage_poll(sluice_layer* L) {
+  for (int l = 0; l < kStageLanes; ++l) {
+    const int r = L->stage_sig_row[l];
+    if (r < 0) continue;
+    const hsa_signal_value_t v = hsa_signal_load_scacquire(L->stage_sig[l]);
+    if (v > 0) continue;
+    L->stage_sig_row[l] = -1;
+    sluice_layer::StageRow& row = L->stage[r];
+    --row.in_flight;
+    if (v < 0) {
+      L->stage_broken = true;
+      row.state = kStageEmpty;
+      row.local = -1;
+      continue;
+    }
+    L->stage_h2d += (int64_t)L->stage_sig_bytes[l];
+    if (row.state == kStageEmpty && row.in_flight == 0) L->stage_dirty = true;  // free again
+  }
+  for (sluice_layer::StageRow& row : L->stage)
+    if (row.state == kStageCopying && row.in_flight == 0 && row.issued == L->stage_bytes) {
+      row.state = kStageReady;
+      ++L->stage_filled;
+    }
+}
+
+// Give the rows to the most selected experts the layer does not hold
+// (count, then lower local id first).  A row keeps its expert while that
+// one is still wanted; a row being filled for an expert no longer wanted
+// stops, and is given out again once its chunks in flight landed.
+void stage_choose(sluice_layer* L) {
+  if (!L->stage_dirty) return;
+  L->stage_dirty = false;
+  const int n = (int)L->stage.size();
+  int want[kMaxStageRows];
+  int nw = 0;
+  for (int loc = 0; loc < L->c.local_n; ++loc) {
+    const uint32_t c = L->sel_count[loc];
+    if (c == 0 || L->c.slot_of[loc] >= 0) continue;
+    int pos = nw;
+    while (pos > 0 && L->sel_count[want[pos - 1]] < c) --pos;
+    if (pos >= n) continue;
+    if (nw < n) ++nw;
+    for (int j = nw - 1; j > pos; --j) want[j] = want[j - 1];
+    want[pos] = loc;
+  }
+  bool covered[kMaxStageRows] = {}, keep[kMaxStageRows] = {};
+  for (int r = 0; r < n; ++r) {
+    const sluice_layer::StageRow& row = L->stage[r];
+    for (int w = 0; w < nw && row.state != kStageEmpty; ++w)
+      if (!covered[w] && row.local == want[w]) {
+        covered[w] = keep[r] = true;
+        break;
+      }
+  }
+  int w = 0;
+  for (int r = 0; r < n; ++r) {
+    if (keep[r]) continue;
+    while (w < nw && covered[w]) ++w;
+    if (w >= nw) break;
+    sluice_layer::StageRow& row = L->stage[r];
+    if (row.state == kStageCopying) {
+      row.state = kStageEmpty;
+      row.local = -1;
+    }
+    if (row.in_flight > 0) continue;  // its chunks still write the row
+    row.local = want[w];
+    row.state = kStageCopying;
+    row.issued = 0;
+    covered[w] = true;
+  }
+}
+
+// Issue the next chunk of a row being filled, on staging lane l (free).
+// false if there is none to issue, or the copy could not be issued.
+bool stage_issue(sluice_layer* L, const DeviceRes* R, int l) {
+  for (size_t r = 0; r < L->stage.size(); ++r) {
+    sluice_layer::StageRow& row = L->stage[r];
+    if (row.state != kStageCopying || row.issued >= L->stage_bytes) continue;
+    size_t base = 0;  // the row's bytes: the staged params' rows one after the other
+    for (size_t pi = 0; pi < L->params.size(); ++pi) {
+      if (L->stage_dev[pi] == nullptr) continue;
+      const ParamRows& p = L->params[pi];
+      if (row.issued >= base + p.row_bytes) {
+        base += p.row_bytes;
+        continue;
+      }
+      const size_t in = row.issued - base;
+      const size_t len = std::min(kStageChunk, p.row_bytes - in);
+      char* dst = L->stage_dev[pi] + r * p.row_bytes + in;
+      const char* src = p.host_base + (size_t)row.local * p.row_bytes + in;
+      const hsa_agent_t from = p.host_agent.handle != 0 ? p.host_agent : R->cpu_agent;
+      hsa_signal_store_relaxed(L->stage_sig[l], 1);
+      if (hsa_amd_memory_async_copy_on_engine(dst, R->gpu_agent, src, from, len, 0, nullptr,
+                                              L->stage_sig[l],
+                                              (hsa_amd_sdma_engine_id_t)R->stage_engine[l],
+                                              true) != HSA_STATUS_SUCCESS) {
+        hsa_signal_store_relaxed(L->stage_sig[l], 0);
+        L->stage_broken = true;
+        row.state = kStageEmpty;
+        row.local = -1;
+        return false;
+      }
+      row.issued += len;
+      ++row.in_flight;
+      L->stage_sig_row[l] = (int)r;
+      L->stage_sig_bytes[l] = len;
+      return true;
+    }
+  }
+  return false;
+}
+
+// Wait (bounded) until no staging chunk of the layer is in flight.
+int stage_drain(sluice_layer* L) {
+  for (int l = 0; l < kStageLanes; ++l)
+    if (L->stage_sig_row[l] >= 0 && wait_signal(L->stage_sig[l]) == SLUICE_E_TIMEOUT)
+      return SLUICE_E_TIMEOUT;
+  stage_poll(L);
+  return SLUICE_OK;
+}
+
+// Free the layer's staging rows (no chunk in flight: L->mu held, drained).
+int stage_free(sluice_layer* L) {
+  int rc = SLUICE_OK;
+  for (char*& d : L->stage_dev)
+    if (d != nullptr) {
+      const hipError_t e = hipFree(d);
+      if (e != hipSuccess) rc = (int)e;
+      d = nullptr;
+    }
+  L->stage_dev.clear();
+  L->stage_parts.clear();
+  L->stage.clear();
+  L->stage_bytes = 0;
+  return rc;
+}
+
 // A record after the last one served has been posted (records are posted
 // in stamp order, so looking at the next stamp's slot is enough).
 bool record_pending(sluice_layer* L) {
@@ -919,6 +1185,7 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
   const bool was_standing = L->c.map_is_standing;
   const int grc = L->c.gap(L->uniq.data(), n_uniq, fast_hit, L->streams, map_write);
   const int n_streams = (int)L->streams.size() / 2;
+  stage_count(L);
   SLUICE_HTRACE(22, L, want, n_streams);
   int rc = SLUICE_OK;
   if (!waits) {
@@ -938,52 +1205,95 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     const bool early = waits && grc == 0 && rc == SLUICE_OK &&
                        g_pipelined.load(std::memory_order_relaxed) != 0;
     // rows copied per expert (the gap kernel copies the pulled ones itself)
-    int n_copy = 0;
-    for (const ParamRows& p : L->params) n_copy += !(early && p.rows_dev != nullptr);
-    const size_t n_sig = (size_t)n_streams * (size_t)n_copy;
+    int n_copy = 0, n_parts = 0;
+    for (size_t pi = 0; pi < L->params.size(); ++pi) {
+      n_copy += !(early && L->params[pi].rows_dev != nullptr);
+      if (!L->stage.empty() && L->stage_dev[pi] != nullptr) n_parts += L->stage_parts[pi];
+    }
+    // Copy order: the misses whose expert is staged first (their copies move
+    // HBM to HBM on engines of their own and land in tens of microseconds),
+    // then the others over the link.  A staged row serves only a gap
+    // answered before its rows land.
+    L->order.clear();
+    const bool from_stage = early && rc == SLUICE_OK && n_parts > 0 && R->n_d2d > 0;
+    int n_staged = 0;
+    if (from_stage)
+      for (int i = 0; i < n_streams; ++i)
+        if (stage_ready_row(L, L->streams[2 * i]) >= 0) L->order.push_back(i);
+    n_staged = (int)L->order.size();
+    for (int i = 0; i < n_streams; ++i)
+      if (n_staged == 0 || stage_ready_row(L, L->streams[2 * i]) < 0) L->order.push_back(i);
+    const size_t n_sig = (size_t)n_staged * (size_t)n_parts +
+                         (size_t)(n_streams - n_staged) * (size_t)n_copy;
     while (rc == SLUICE_OK && L->fill_sig.size() < n_sig) {
       hsa_signal_t sig{};
       if (hsa_signal_create(0, 0, nullptr, &sig) != HSA_STATUS_SUCCESS) rc = SLUICE_E_COPY;
       else L->fill_sig.push_back(sig);
     }
+    L->sig_end.assign((size_t)n_streams, 0);
     // The link is the bottleneck of a missing step: the first expert's rows
     // are queued before the device is answered (its resident experts then
     // compute while the rows stream), the other experts' after.
     bool answered = !early;
-    int whole = 0;  // experts whose copies were all issued
+    int whole = 0;  // experts (in copy order) whose copies were all issued
     int armed = 0;  // copies issued, each with its own signal
-    for (int i = 0; rc == SLUICE_OK && i < n_streams; ++i) {
+    // One copy with its own completion signal; false (rc set) if it failed
+    // to issue.
+    auto copy = [&](void* dst, const void* src, hsa_agent_t from, size_t bytes, uint32_t eng) {
+      int left = g_fail_after.load(std::memory_order_relaxed);
+      while (left >= 0 && !g_fail_after.compare_exchange_weak(left, left - 1)) {
+      }
+      const hsa_signal_t sig = L->fill_sig[armed];
+      hsa_signal_store_relaxed(sig, 1);
+      const hsa_status_t st =
+          left == 0 ? HSA_STATUS_ERROR
+          : eng != 0
+              ? hsa_amd_memory_async_copy_on_engine(dst, R->gpu_agent, src, from, bytes, 0, nullptr,
+                                                    sig, (hsa_amd_sdma_engine_id_t)eng, true)
+              : hsa_amd_memory_async_copy(dst, R->gpu_agent, src, from, bytes, 0, nullptr, sig);
+      if (st != HSA_STATUS_SUCCESS) {
+        hsa_signal_store_relaxed(sig, 0);
+        rc = SLUICE_E_COPY;
+        return false;
+      }
+      L->armed_copies = ++armed;
+      return true;
+    };
+    for (int j = 0; rc == SLUICE_OK && j < n_streams; ++j) {
+      const int i = L->order[j];
       const int local = L->streams[2 * i], slot = L->streams[2 * i + 1];
-      for (const ParamRows& p : L->params) {
+      const int srow = j < n_staged ? stage_ready_row(L, local) : -1;
+      int e = 0;  // next device-to-device engine
+      for (size_t pi = 0; rc == SLUICE_OK && pi < L->params.size(); ++pi) {
+        const ParamRows& p = L->params[pi];
         L->bytes += (int64_t)p.row_bytes;
         if (early && p.rows_dev != nullptr) continue;  // the gap kernel copies these rows itself
-        int left = g_fail_after.load(std::memory_order_relaxed);
-        while (left >= 0 && !g_fail_after.compare_exchange_weak(left, left - 1)) {
+        char* dst = p.slot_base + (size_t)slot * p.row_bytes;
+        if (srow >= 0) {
+          // the staged row in parts, over the device-to-device engines
+          const int parts = L->stage_parts[pi];
+          size_t part = (p.row_bytes + (size_t)parts - 1) / (size_t)parts;
+          part = (part + 4095) & ~(size_t)4095;
+          const char* src = L->stage_dev[pi] + (size_t)srow * p.row_bytes;
+          for (size_t off = 0; off < p.row_bytes && rc == SLUICE_OK; off += part)
+            copy(dst + off, src + off, R->gpu_agent, std::min(part, p.row_bytes - off),
+                 R->d2d_engine[e++ % R->n_d2d]);
+        } else {
+          const hsa_agent_t from = p.host_agent.handle != 0 ? p.host_agent : R->cpu_agent;
+          copy(dst, p.host_base + (size_t)local * p.row_bytes, from, p.row_bytes,
+               R->engine[p.lane]);
         }
-        const hsa_signal_t sig = L->fill_sig[armed];
-        hsa_signal_store_relaxed(sig, 1);
-        void* dst = p.slot_base + (size_t)slot * p.row_bytes;
-        const void* src = p.host_base + (size_t)local * p.row_bytes;
-        const uint32_t eng = R->engine[p.lane];
-        const hsa_agent_t from = p.host_agent.handle != 0 ? p.host_agent : R->cpu_agent;
-        const hsa_status_t st =
-            left == 0 ? HSA_STATUS_ERROR
-            : eng != 0
-                ? hsa_amd_memory_async_copy_on_engine(dst, R->gpu_agent, src, from, p.row_bytes, 0,
-                                                      nullptr, sig, (hsa_amd_sdma_engine_id_t)eng,
-                                                      true)
-                : hsa_amd_memory_async_copy(dst, R->gpu_agent, src, from, p.row_bytes, 0, nullptr,
-                                            sig);
-        if (st != HSA_STATUS_SUCCESS) {
-          hsa_signal_store_relaxed(sig, 0);
-          L->bytes -= (int64_t)p.row_bytes;
-          rc = SLUICE_E_COPY;
-          break;
-        }
-        L->armed_copies = ++armed;
-        if (i == 0 && &p == &L->params[0]) SLUICE_HTRACE(23, L, want, p.lane);
+        if (rc != SLUICE_OK) L->bytes -= (int64_t)p.row_bytes;
+        if (j == 0 && pi == 0) SLUICE_HTRACE(23, L, want, p.lane);
       }
-      if (rc == SLUICE_OK) whole = i + 1;
+      L->sig_end[j] = armed;
+      if (rc == SLUICE_OK) {
+        whole = j + 1;
+        if (srow >= 0) {
+          ++L->stage_hits;
+          L->stage_hit_bytes += (int64_t)L->stage_bytes;
+        }
+      }
       if (!answered && rc == SLUICE_OK) {
         respond(L, want, SLUICE_OK, n_streams);
         answered = true;
@@ -996,20 +1306,19 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     SLUICE_HTRACE(25, L, want, armed);
     // Each expert landed (every one of its copies completed): mark its slot
     // ready for this gap.
-    int landed = 0;  // streams whose copies completed, their slots marked
-    for (int i = 0; i < whole; ++i) {
+    int landed = 0;  // experts in copy order whose copies completed, their slots marked
+    for (int j = 0, c = 0; j < whole; ++j) {
       int w = SLUICE_OK;
-      for (int c = 0; c < n_copy && w == SLUICE_OK; ++c)
-        w = wait_signal(L->fill_sig[(size_t)i * n_copy + c]);
+      for (; c < L->sig_end[j] && w == SLUICE_OK; ++c) w = wait_signal(L->fill_sig[c]);
       if (w != SLUICE_OK) {
         if (rc == SLUICE_OK) rc = w;
         break;
       }
-      landed = i + 1;
-      SLUICE_HTRACE(26, L, want, i);
+      landed = j + 1;
+      SLUICE_HTRACE(26, L, want, j);
       if (!early) continue;
-      __atomic_store_n(&mb->slot_ready[L->streams[2 * i + 1]], want, __ATOMIC_RELEASE);
-      SLUICE_HTRACE(27, L, want, i);
+      __atomic_store_n(&mb->slot_ready[L->streams[2 * L->order[j] + 1]], want, __ATOMIC_RELEASE);
+      SLUICE_HTRACE(27, L, want, j);
     }
     int marked = landed;  // streams whose slots are marked
     // every issued copy has completed (or the layer needs a resync, which
@@ -1024,8 +1333,9 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
       // them until sluice_layer_gap_resync writes the host's.
       if (early)
         for (; marked < n_streams; ++marked)
-          __atomic_store_n(&mb->slot_ready[L->streams[2 * marked + 1]], want, __ATOMIC_RELEASE);
-      for (int i = landed; i < n_streams; ++i) (void)L->c.unfill(L->streams[2 * i + 1]);
+          __atomic_store_n(&mb->slot_ready[L->streams[2 * L->order[marked] + 1]], want,
+                           __ATOMIC_RELEASE);
+      for (int j = landed; j < n_streams; ++j) (void)L->c.unfill(L->streams[2 * L->order[j] + 1]);
     }
     if (early) {
       L->done_stamp.store(want, std::memory_order_release);
@@ -1080,7 +1390,50 @@ struct sluice_gap_server {
   std::atomic<bool> stop{false};
   std::atomic<int> error{0};
   std::atomic<int64_t> served{0};
+  // staging: the layer whose chunk each staging lane carries (nullptr:
+  // free), the layer whose gap comes next, and whether the last look found
+  // nothing to copy (no look again until a gap is served or a chunk lands)
+  sluice_layer* stage_lane[kStageLanes] = {};
+  size_t cursor = 0;
+  bool stage_quiet = false;
 };
+
+// One staging step, on a sweep that found no record: take in the chunks
+// that landed, then put a chunk on each free staging lane, for the layers
+// whose gaps come next first.  A layer whose last stream-in failed to drain
+// stages nothing.
+static void stage_step(sluice_gap_server* S) {
+  for (int l = 0; l < kStageLanes; ++l) {
+    sluice_layer* L = S->stage_lane[l];
+    if (L == nullptr || hsa_signal_load_relaxed(L->stage_sig[l]) > 0) continue;
+    std::lock_guard<std::mutex> lk(L->mu);
+    stage_poll(L);
+    S->stage_lane[l] = nullptr;
+    S->stage_quiet = false;
+  }
+  if (S->stage_quiet) return;
+  const size_t n = S->layers.size();
+  bool busy = false;
+  for (int l = 0; l < kStageLanes; ++l) {
+    if (S->stage_lane[l] != nullptr) {
+      busy = true;
+      continue;
+    }
+    for (size_t k = 0; k < n; ++k) {
+      sluice_layer* L = S->layers[(S->cursor + k) % n];
+      if (L->stage.empty() || L->stage_broken || L->armed_copies != 0) continue;
+      if (!L->stage_dirty && !stage_has_copy(L)) continue;
+      std::lock_guard<std::mutex> lk(L->mu);
+      stage_choose(L);
+      if (L->stage_sig_row[l] < 0 && stage_issue(L, &g_dev[L->device], l)) {
+        S->stage_lane[l] = L;
+        busy = true;
+        break;
+      }
+    }
+  }
+  if (!busy) S->stage_quiet = true;
+}
 
 // The server spins while gaps arrive (a decode step posts one per MoE layer,
 // every ~0.1 ms); after kServerIdleS without a record it naps kServerNapUs
@@ -1095,10 +1448,13 @@ static void server_loop(sluice_gap_server* S) {
   unsigned idle = 0;
   while (!S->stop.load(std::memory_order_acquire)) {
     bool any = false;
-    for (sluice_layer* L : S->layers) {
+    for (size_t i = 0; i < S->layers.size(); ++i) {
+      sluice_layer* L = S->layers[i];
       const int rc = serve_one(L, S->fast_hit, false, nullptr);
       if (rc == kNothing) continue;
       any = true;
+      S->cursor = (i + 1) % S->layers.size();
+      S->stage_quiet = false;
       S->served.fetch_add(1, std::memory_order_relaxed);
       if (rc != SLUICE_OK) {
         int zero = 0;
@@ -1111,6 +1467,7 @@ static void server_loop(sluice_gap_server* S) {
       last = -1.0;  // read the clock again on the next idle sweep
       continue;
     }
+    stage_step(S);
     _mm_pause();
     if ((++idle & 255u) != 0) continue;
     const double t = now_s();
@@ -1148,7 +1505,11 @@ extern "C" int sluice_layer_destroy(sluice_layer* L) {
   int rc = SLUICE_OK;
   if (L->map_dev != nullptr && L->mb != nullptr) slotwait_unregister(L->map_dev);
   if (drain_copies(L) != SLUICE_OK) return SLUICE_E_STATE;  // copies still write its slots
+  if (stage_drain(L) != SLUICE_OK) return SLUICE_E_STATE;   // chunks still write its staging rows
   for (hsa_signal_t sig : L->fill_sig) (void)hsa_signal_destroy(sig);
+  for (hsa_signal_t sig : L->stage_sig)
+    if (sig.handle != 0) (void)hsa_signal_destroy(sig);
+  rc = stage_free(L);
   for (ParamRows& p : L->params)
     if (p.rows_dev != nullptr) {
       const hipError_t e = hipFree(p.rows_dev);
@@ -1201,6 +1562,7 @@ extern "C" int sluice_layer_add_param(sluice_layer* L, void* slot_base_dev, cons
     return SLUICE_E_INVAL;
   // A layer with a device copies these rows with the SDMA engines: both
   // ranges must be allocations the runtime knows, whole.
+  if (!L->stage.empty()) return SLUICE_E_STATE;  // staging rows are laid out over the params
   hsa_agent_t host_agent{};
   if (L->mb != nullptr &&
       (!known_range(host_base, row_bytes * (size_t)L->c.local_n, &host_agent) ||
@@ -1258,6 +1620,67 @@ extern "C" int sluice_layer_pulled_params(sluice_layer* L) {
   int n = 0;
   for (const ParamRows& p : L->params) n += p.rows_dev != nullptr;
   return n;
+}
+
+extern "C" int sluice_layer_set_staging(sluice_layer* L, int rows) {
+  if (L == nullptr || rows < 0 || rows > kMaxStageRows || L->mb == nullptr) return SLUICE_E_INVAL;
+  if (L->server != nullptr) return SLUICE_E_STATE;
+  DeviceRes* R = nullptr;
+  const int drc = device_res(L->device, &R);
+  if (drc != SLUICE_OK) return drc;
+  std::lock_guard<std::mutex> lk(L->mu);
+  if ((int)L->stage.size() == rows) return SLUICE_OK;  // as set (a restarted server keeps them)
+  if (stage_drain(L) != SLUICE_OK) return SLUICE_E_TIMEOUT;
+  int rc = stage_free(L);
+  if (rc != SLUICE_OK || rows == 0) return rc;
+  if (R->n_d2d == 0) return SLUICE_E_INVAL;  // no copy engines free for staging
+  for (hsa_signal_t& sig : L->stage_sig)
+    if (sig.handle == 0 && hsa_signal_create(0, 0, nullptr, &sig) != HSA_STATUS_SUCCESS)
+      return SLUICE_E_COPY;
+  // the params the gap copies (the pulled ones come from their HBM copy)
+  size_t bytes = 0;
+  for (const ParamRows& p : L->params) bytes += p.rows_dev == nullptr ? p.row_bytes : 0;
+  if (bytes == 0) return SLUICE_OK;  // nothing to stage
+  L->stage_dev.assign(L->params.size(), nullptr);
+  L->stage_parts.assign(L->params.size(), 0);
+  for (size_t pi = 0; pi < L->params.size(); ++pi) {
+    const ParamRows& p = L->params[pi];
+    if (p.rows_dev != nullptr) continue;
+    void* d = nullptr;
+    const hipError_t e = hipMalloc(&d, p.row_bytes * (size_t)rows);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();  // reported here, not by the caller's next call
+      (void)stage_free(L);
+      return (int)e;
+    }
+    L->stage_dev[pi] = (char*)d;
+    // the device-to-device engines shared by the params in proportion to
+    // their bytes
+    const double share = (double)p.row_bytes / (double)bytes * R->n_d2d;
+    L->stage_parts[pi] = std::max(1, (int)(share + 0.5));
+  }
+  L->stage_bytes = bytes;
+  L->stage.assign((size_t)rows, sluice_layer::StageRow{});
+  L->sel_count.assign((size_t)L->c.local_n, 0);
+  L->stage_gaps = 0;
+  L->stage_dirty = false;
+  L->stage_broken = false;
+  return SLUICE_OK;
+}
+
+extern "C" int sluice_layer_stage_counters(const sluice_layer* Lc, int64_t* counters) {
+  if (Lc == nullptr || counters == nullptr) return SLUICE_E_INVAL;
+  sluice_layer* L = const_cast<sluice_layer*>(Lc);
+  std::lock_guard<std::mutex> lk(L->mu);
+  int ready = 0;
+  for (const sluice_layer::StageRow& row : L->stage) ready += row.state == kStageReady;
+  counters[0] = (int64_t)L->stage.size();
+  counters[1] = ready;
+  counters[2] = L->stage_filled;
+  counters[3] = L->stage_h2d;
+  counters[4] = L->stage_hits;
+  counters[5] = L->stage_hit_bytes;
+  return SLUICE_OK;
 }
 
 extern "C" int sluice_layer_pin(sluice_layer* L, int local, int debit_protected, int* slot_out) {
@@ -1358,7 +1781,11 @@ extern "C" int sluice_gap_server_destroy(sluice_gap_server* S) {
   if (S == nullptr) return SLUICE_OK;
   S->stop.store(true, std::memory_order_release);
   if (S->th.joinable()) S->th.join();
-  for (sluice_layer* L : S->layers) L->server = nullptr;
+  for (sluice_layer* L : S->layers) {
+    std::lock_guard<std::mutex> lk(L->mu);
+    (void)stage_drain(L);  // no staging chunk outlives the server
+    L->server = nullptr;
+  }
   const int err = S->error.load();
   delete S;
   return err;
@@ -1432,6 +1859,10 @@ extern "C" int sluice_layer_gap_resync(sluice_layer* L) {
     const int d = drain_copies(L);
     if (d != SLUICE_OK) return d;
     L->armed_copies = 0;
+    const int ds = stage_drain(L);
+    if (ds != SLUICE_OK) return ds;
+    L->stage_broken = false;  // a failed chunk emptied its row; staging resumes
+    L->stage_dirty = true;
   }
   int32_t dev_stamp = 0;
   SLUICE_HIP_CHECK(hipMemcpy(&dev_stamp, L->dev_block + L->c.E, sizeof(int32_t),

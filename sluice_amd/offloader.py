@@ -66,6 +66,12 @@ PIN_FILE_ENV = "SLUICE_PIN_FILE"
 # Full residency with the streaming hook kept (src/sluice/offloader.py:289-293,
 # 948-1012): every expert pre-filled into its own slot and pinned there.
 NO_STATIC_FULL_ENV = "SLUICE_NO_STATIC_FULL"
+# No counterpart in the reference: per router-split layer, how many experts
+# the gap server keeps staged in HBM outside the slots (the layer's most
+# selected experts it does not hold, copied while the host link idles; a
+# miss on one is copied into its slot from HBM).  0 turns staging off.
+STAGE_ROWS_ENV = "SLUICE_STAGE_ROWS"
+STAGE_ROWS_DEFAULT = 1
 
 # Graph split points under piecewise capture: the MoE ops (whose apply runs
 # the classic hook, which syncs the host) and the gap op.
@@ -493,6 +499,7 @@ class ExpertStreamOffloader(_OffloaderBase):
         self.pin_memory = torch.cuda.is_available()
         self.lfu = _env_flag(LFU_ENV)
         self.no_static_full = _env_flag(NO_STATIC_FULL_ENV)
+        self.stage_rows = min(max(_env_number(STAGE_ROWS_ENV, STAGE_ROWS_DEFAULT, int), 0), 8)
         self._caches: dict[int, _ExpertLayerCache] = {}
         self._layers: list[nn.Module] = []
         self._prepared_stores: dict[int, list] = {}  # pinned stores made before load
@@ -941,6 +948,13 @@ class ExpertStreamOffloader(_OffloaderBase):
         if self._server is not None or not self._rs_caches:
             return
         lib = _lib.load()
+        for c in self._rs_caches:
+            rc = lib.sluice_layer_set_staging(c.handle, self.stage_rows)
+            if rc == _lib.SLUICE_E_INVAL:  # no copy engines free for it on this device
+                logger.warning("Sluice: no staging rows (%s=%d): the device has no copy engines "
+                               "free for them", STAGE_ROWS_ENV, self.stage_rows)
+                continue
+            _lib.check(rc, "sluice_layer_set_staging")
         handles = (ctypes.c_void_p * len(self._rs_caches))(*[c.handle for c in self._rs_caches])
         srv = ctypes.c_void_p()
         _lib.check(lib.sluice_gap_server_create(handles, len(self._rs_caches),
@@ -992,6 +1006,20 @@ class ExpertStreamOffloader(_OffloaderBase):
         for c in self._rs_caches:
             for k_, v in c.stats().items():
                 tot[k_] += v
+        return tot
+
+    def stage_counters(self) -> dict:
+        """Staging rows summed over the armed layers: rows, rows holding an
+        expert whole, rows filled, host-to-device bytes of staging copies,
+        misses copied into their slots from a staged row, and their bytes."""
+        lib = _lib.load()
+        keys = ("rows", "ready", "filled", "h2d_bytes", "hits", "hit_bytes")
+        tot = dict.fromkeys(keys, 0)
+        ctr = (ctypes.c_int64 * 6)()
+        for c in self._rs_caches:
+            _lib.check(lib.sluice_layer_stage_counters(c.handle, ctr), "sluice_layer_stage_counters")
+            for i, k_ in enumerate(keys):
+                tot[k_] += ctr[i]
         return tot
 
     def get_gap_stats(self) -> dict:

@@ -285,6 +285,79 @@ def test_device_gap_v3_fp8_streams_four_rows_per_miss(monkeypatch, slru_golden, 
     off.close()
 
 
+_STAGED_CASES = [("v2lite_zipf", True, "bf16"), ("qwen3_s64_zipf", True, "bf16"),
+                 ("ep_half_owned", False, "bf16"), ("pinned", True, "bf16"),
+                 ("v3_s64_zipf", True, "fp8")]
+
+
+@pytest.mark.parametrize("name,fast_hit,kind", _STAGED_CASES,
+                         ids=[f"{n}-fh{int(f)}-{k}" for n, f, k in _STAGED_CASES])
+def test_staged_rows_leave_the_golden_replay_unchanged(monkeypatch, slru_golden, name, fast_hit,
+                                                       kind):
+    """A golden trace replayed through the gap server with two staging rows
+    per layer: the server fills them while the link idles (a pause after
+    most steps; every third step follows at once, so gaps also meet chunks
+    in flight), misses on staged experts are copied into their slots from
+    HBM.  Slot state, segment order and device map follow the reference at
+    every step, every cached slot's bytes equal its host rows, the bytes
+    filled stay misses x expert bytes, and on the Zipf traces some misses
+    were served from staged rows.  bf16 rows of 2 MB and 1 MB (two and one
+    staging chunks); fp8: the w13 and w2 rows staged, the scale rows pulled
+    by the gap kernel."""
+    import time
+
+    from sluice_amd import _lib
+
+    case = [c for c in slru_golden["cases"] if c["name"] == name and c["fast_hit"] == fast_hit][0]
+    print(f"staged gap case {name} fast_hit={fast_hit} {kind}", flush=True)
+    monkeypatch.setenv("SLUICE_STAGE_ROWS", "2")
+    E, local_n, k = case["E"], case["local_n"], case["k"]
+    emap = None
+    if case["local_of"] is not None:
+        emap = torch.tensor(case["local_of"], dtype=torch.int32)
+    if kind == "fp8":
+        layer, H = _Fp8Layer(E, 512, 256), 512
+    else:
+        H = 2048
+        layer = _Layer(E, local_n, H=H, I=256, expert_map=emap)
+    off = _offloader(monkeypatch, case["slots"], case["protect_frac"], fast_hit)
+    if case["pins"]:
+        off._pin_layers = {0: list(case["pins"])}
+    off.wrap_modules(iter([layer]))
+    with torch.cuda.device(DEV):
+        off.post_init()
+    cache = off._caches[id(layer)]
+    off._rs_caches.append(cache)
+    lib = _lib.load()
+    assert lib.sluice_layer_pulled_params(cache.handle) == (2 if kind == "fp8" else 0)
+    off.start_gap_server()
+    assert off.stage_counters()["rows"] == 2
+    hs = torch.zeros((1, H), dtype=torch.bfloat16, device=DEV)
+    for n, step in enumerate(case["steps"]):
+        assert not step["overflow"]
+        ids = torch.tensor(step["ids"], dtype=torch.int32, device=DEV).view(-1, k)
+        torch.ops.vllm.sluice_stream_gap(hs, ids, 0)
+        off.drain()
+        st = cache._state()
+        want = step["state"]
+        for key in ("slot_of", "expert_in_slot", "probation", "protected", "free_slots"):
+            assert st[key] == want[key], (n, key)
+        assert cache.expert_map_buf.cpu().tolist() == want["map"], n
+        if n % 25 == 0 or n == len(case["steps"]) - 1:
+            _slot_bytes_match_host(cache)
+        if n % 3 != 2:
+            time.sleep(0.002)  # the link idles: the server fills staging rows
+    sc = off.stage_counters()
+    s = cache.stats()
+    print(f"staging: {sc}, misses {s['misses']}", flush=True)
+    assert s["bytes"] == s["misses"] * cache.bytes_per_expert
+    assert sc["filled"] > 0 and sc["h2d_bytes"] > 0
+    assert sc["hits"] <= s["misses"]
+    if "zipf" in name:
+        assert sc["hits"] > 0
+    off.close()
+
+
 def test_add_param_takes_only_whole_runtime_allocations():
     """A device layer copies its rows with the SDMA engines, which neither
     stage pageable memory nor check bounds: sluice_layer_add_param refuses a
