@@ -562,16 +562,13 @@ constexpr int kLanes = 2;
 
 // Staging (sluice_layer_set_staging): rows in HBM outside the slots, each a
 // copy of one expert the layer selects often but does not hold, filled from
-// the host store while the link idles, in chunks on kStageLanes engines of
-// their own (at most kStageLanes chunks in flight per gap server, so a gap
-// whose copies start meanwhile shares the link with at most that).  A miss
-// whose expert is staged is copied into its slot from there, split over up
-// to kMaxD2d engines: device-to-device SDMA copies do not use the host link
-// and run ~59 GB/s per engine on MI355X, so a 17.3 MB expert lands in ~45 us
-// over 12 engines instead of ~310 us over the link, and a host copy on
-// another engine keeps its rate meanwhile.
+// the host store while the link idles, in chunks on kStageLanes SDMA engines
+// of their own (at most kStageLanes chunks in flight per gap server, so a
+// gap whose copies start meanwhile shares the link with at most that).  A
+// miss whose expert is staged is copied into its slot from there by the
+// runtime's device-to-device copy (a copy kernel: 17.3 MB in ~29 us on
+// MI355X, against ~310 us over the link).
 constexpr int kStageLanes = 2;
-constexpr int kMaxD2d = 12;
 constexpr size_t kStageChunk = 1 << 20;
 constexpr int kMaxStageRows = 8;
 constexpr int kStageHalfLife = 4096;  // gaps between halvings of the selection counts
@@ -616,15 +613,12 @@ struct DeviceRes {
   hsa_agent_t gpu_agent{}, cpu_agent{};
   uint32_t engine[kLanes] = {};
   // staging: the engines that fill staging rows from the host (0: none
-  // free, no staging) and those that copy staged rows into slots
+  // free, no staging)
   uint32_t stage_engine[kStageLanes] = {};
-  uint32_t d2d_engine[kMaxD2d] = {};
-  int n_d2d = 0;
   long long clock_khz = 0;
   // device word: the bound of every device wait, in wall-clock ticks; the
   // kernels read it when they start to wait (sluice_gap_set_timeout
-  // rewrites it, so graphs captured earlier follow the new bound).  Its
-  // 256-byte allocation's bytes 64..191 take the set-up's trial copies.
+  // rewrites it, so graphs captured earlier follow the new bound)
   long long* bound_dev = nullptr;
 };
 constexpr int kMaxDevices = 64;
@@ -640,27 +634,6 @@ hsa_status_t first_cpu_agent(hsa_agent_t agent, void* data) {
   if (t != HSA_DEVICE_TYPE_CPU) return HSA_STATUS_SUCCESS;
   *static_cast<hsa_agent_t*>(data) = agent;
   return HSA_STATUS_INFO_BREAK;
-}
-
-// A 64-byte device-to-device copy inside `scratch` (bytes 64..191 of a
-// 256-byte device allocation) completes on SDMA engine `eng`.  The runtime
-// in a torch process may report no engines for device-to-device copies
-// while they work, so each engine is tried.
-bool d2d_engine_works(const DeviceRes& r, char* scratch, uint32_t eng) {
-  hsa_signal_t sig{};
-  if (hsa_signal_create(1, 0, nullptr, &sig) != HSA_STATUS_SUCCESS) return false;
-  if (hsa_amd_memory_async_copy_on_engine(scratch + 128, r.gpu_agent, scratch + 64, r.gpu_agent, 64,
-                                          0, nullptr, sig, (hsa_amd_sdma_engine_id_t)eng,
-                                          true) != HSA_STATUS_SUCCESS) {
-    (void)hsa_signal_destroy(sig);
-    return false;
-  }
-  const double t0 = now_s();
-  hsa_signal_value_t v;
-  while ((v = hsa_signal_load_scacquire(sig)) > 0 && now_s() - t0 < 1.0) _mm_pause();
-  if (v > 0) return false;  // still in flight: the signal is left to it
-  (void)hsa_signal_destroy(sig);
-  return v == 0;
 }
 
 // The HSA agents of this device (the owner of its device memory) and of the
@@ -691,27 +664,16 @@ int hsa_setup(DeviceRes& r) {
       used |= bit;
     }
   for (; l < kLanes; ++l) r.engine[l] = l > 0 ? r.engine[l - 1] : 0;
-  // staging engines: host-to-device engines neither lane uses, then
-  // device-to-device engines none of those uses
+  // staging engines: reported host-to-device engines neither lane uses
+  // (only engines the runtime reports for a direction are used for it)
   int ls = 0;
   for (uint32_t bit = 1; bit != 0 && ls < kStageLanes; bit <<= 1)
     if ((mask & bit) && !(used & bit)) {
       r.stage_engine[ls++] = bit;
       used |= bit;
     }
-  uint32_t mask_d2d = 0;
-  if (hsa_amd_memory_copy_engine_status(r.gpu_agent, r.gpu_agent, &mask_d2d) != HSA_STATUS_SUCCESS ||
-      mask_d2d == 0)
-    mask_d2d = mask;
-  if (ls == kStageLanes)
-    for (uint32_t bit = 1; bit != 0 && r.n_d2d < kMaxD2d; bit <<= 1)
-      if ((mask_d2d & bit) && !(used & bit) &&
-          d2d_engine_works(r, reinterpret_cast<char*>(r.bound_dev), bit))
-        r.d2d_engine[r.n_d2d++] = bit;
-  if (ls < kStageLanes || r.n_d2d == 0) {
+  if (ls < kStageLanes)
     for (uint32_t& e : r.stage_engine) e = 0;
-    r.n_d2d = 0;
-  }
   r.hsa = true;
   return SLUICE_OK;
 }
@@ -840,7 +802,6 @@ struct sluice_layer {
   };
   std::vector<StageRow> stage;
   std::vector<char*> stage_dev;  // per param (nullptr: pulled, or no staging)
-  std::vector<int> stage_parts;  // per param: copies that move a staged row into a slot
   size_t stage_bytes = 0;        // one staged expert
   hsa_signal_t stage_sig[kStageLanes] = {};
   int stage_sig_row[kStageLanes] = {-1, -1};  // row of the chunk a signal tracks
@@ -1055,42 +1016,50 @@ void stage_choose(sluice_layer* L) {
   }
 }
 
-// Issue the next chunk of a row being filled, on staging lane l (free).
-// false if there is none to issue, or the copy could not be issued.
-bool stage_issue(sluice_layer* L, const DeviceRes* R, int l) {
+// The layer's row being filled whose expert is selected most often, or -1.
+int stage_next_row(const sluice_layer* L) {
+  int pick = -1;
   for (size_t r = 0; r < L->stage.size(); ++r) {
-    sluice_layer::StageRow& row = L->stage[r];
+    const sluice_layer::StageRow& row = L->stage[r];
     if (row.state != kStageCopying || row.issued >= L->stage_bytes) continue;
-    size_t base = 0;  // the row's bytes: the staged params' rows one after the other
-    for (size_t pi = 0; pi < L->params.size(); ++pi) {
-      if (L->stage_dev[pi] == nullptr) continue;
-      const ParamRows& p = L->params[pi];
-      if (row.issued >= base + p.row_bytes) {
-        base += p.row_bytes;
-        continue;
-      }
-      const size_t in = row.issued - base;
-      const size_t len = std::min(kStageChunk, p.row_bytes - in);
-      char* dst = L->stage_dev[pi] + r * p.row_bytes + in;
-      const char* src = p.host_base + (size_t)row.local * p.row_bytes + in;
-      const hsa_agent_t from = p.host_agent.handle != 0 ? p.host_agent : R->cpu_agent;
-      hsa_signal_store_relaxed(L->stage_sig[l], 1);
-      if (hsa_amd_memory_async_copy_on_engine(dst, R->gpu_agent, src, from, len, 0, nullptr,
-                                              L->stage_sig[l],
-                                              (hsa_amd_sdma_engine_id_t)R->stage_engine[l],
-                                              true) != HSA_STATUS_SUCCESS) {
-        hsa_signal_store_relaxed(L->stage_sig[l], 0);
-        L->stage_broken = true;
-        row.state = kStageEmpty;
-        row.local = -1;
-        return false;
-      }
-      row.issued += len;
-      ++row.in_flight;
-      L->stage_sig_row[l] = (int)r;
-      L->stage_sig_bytes[l] = len;
-      return true;
+    if (pick < 0 || L->sel_count[row.local] > L->sel_count[L->stage[pick].local]) pick = (int)r;
+  }
+  return pick;
+}
+
+// Issue the next chunk of row r (being filled), on staging lane l (free).
+// false if the copy could not be issued.
+bool stage_issue(sluice_layer* L, const DeviceRes* R, int l, int r) {
+  sluice_layer::StageRow& row = L->stage[r];
+  size_t base = 0;  // the row's bytes: the staged params' rows one after the other
+  for (size_t pi = 0; pi < L->params.size(); ++pi) {
+    if (L->stage_dev[pi] == nullptr) continue;
+    const ParamRows& p = L->params[pi];
+    if (row.issued >= base + p.row_bytes) {
+      base += p.row_bytes;
+      continue;
     }
+    const size_t in = row.issued - base;
+    const size_t len = std::min(kStageChunk, p.row_bytes - in);
+    char* dst = L->stage_dev[pi] + (size_t)r * p.row_bytes + in;
+    const char* src = p.host_base + (size_t)row.local * p.row_bytes + in;
+    const hsa_agent_t from = p.host_agent.handle != 0 ? p.host_agent : R->cpu_agent;
+    hsa_signal_store_relaxed(L->stage_sig[l], 1);
+    if (hsa_amd_memory_async_copy_on_engine(dst, R->gpu_agent, src, from, len, 0, nullptr,
+                                            L->stage_sig[l],
+                                            (hsa_amd_sdma_engine_id_t)R->stage_engine[l],
+                                            true) != HSA_STATUS_SUCCESS) {
+      hsa_signal_store_relaxed(L->stage_sig[l], 0);
+      L->stage_broken = true;
+      row.state = kStageEmpty;
+      row.local = -1;
+      return false;
+    }
+    row.issued += len;
+    ++row.in_flight;
+    L->stage_sig_row[l] = r;
+    L->stage_sig_bytes[l] = len;
+    return true;
   }
   return false;
 }
@@ -1114,7 +1083,6 @@ int stage_free(sluice_layer* L) {
       d = nullptr;
     }
   L->stage_dev.clear();
-  L->stage_parts.clear();
   L->stage.clear();
   L->stage_bytes = 0;
   return rc;
@@ -1205,40 +1173,33 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     const bool early = waits && grc == 0 && rc == SLUICE_OK &&
                        g_pipelined.load(std::memory_order_relaxed) != 0;
     // rows copied per expert (the gap kernel copies the pulled ones itself)
-    int n_copy = 0, n_parts = 0;
-    for (size_t pi = 0; pi < L->params.size(); ++pi) {
-      n_copy += !(early && L->params[pi].rows_dev != nullptr);
-      if (!L->stage.empty() && L->stage_dev[pi] != nullptr) n_parts += L->stage_parts[pi];
-    }
-    // Copy order: the misses whose expert is staged first (their copies move
-    // HBM to HBM on engines of their own and land in tens of microseconds),
-    // then the others over the link.  A staged row serves only a gap
-    // answered before its rows land.
+    int n_copy = 0;
+    for (const ParamRows& p : L->params) n_copy += !(early && p.rows_dev != nullptr);
+    // Copy order: the misses whose expert is staged first, then the others
+    // over the link.  A staged row serves only a gap answered before its
+    // rows land, and its copy (HBM to HBM) runs as a kernel of the runtime:
+    // the host waits for those copies before it answers, so no kernel ever
+    // waits for a copy that itself needs CUs (the device runs only the
+    // waiting gap kernel meanwhile).
     L->order.clear();
-    const bool from_stage = early && rc == SLUICE_OK && n_parts > 0 && R->n_d2d > 0;
-    int n_staged = 0;
+    const bool from_stage = early && rc == SLUICE_OK && !L->stage.empty();
     if (from_stage)
       for (int i = 0; i < n_streams; ++i)
         if (stage_ready_row(L, L->streams[2 * i]) >= 0) L->order.push_back(i);
-    n_staged = (int)L->order.size();
+    const int n_staged = (int)L->order.size();
     for (int i = 0; i < n_streams; ++i)
       if (n_staged == 0 || stage_ready_row(L, L->streams[2 * i]) < 0) L->order.push_back(i);
-    const size_t n_sig = (size_t)n_staged * (size_t)n_parts +
-                         (size_t)(n_streams - n_staged) * (size_t)n_copy;
+    const size_t n_sig = (size_t)n_streams * (size_t)n_copy;
     while (rc == SLUICE_OK && L->fill_sig.size() < n_sig) {
       hsa_signal_t sig{};
       if (hsa_signal_create(0, 0, nullptr, &sig) != HSA_STATUS_SUCCESS) rc = SLUICE_E_COPY;
       else L->fill_sig.push_back(sig);
     }
     L->sig_end.assign((size_t)n_streams, 0);
-    // The link is the bottleneck of a missing step: the first expert's rows
-    // are queued before the device is answered (its resident experts then
-    // compute while the rows stream), the other experts' after.
-    bool answered = !early;
     int whole = 0;  // experts (in copy order) whose copies were all issued
     int armed = 0;  // copies issued, each with its own signal
-    // One copy with its own completion signal; false (rc set) if it failed
-    // to issue.
+    // One copy with its own completion signal (engine 0: the runtime's
+    // choice); false (rc set) if it failed to issue.
     auto copy = [&](void* dst, const void* src, hsa_agent_t from, size_t bytes, uint32_t eng) {
       int left = g_fail_after.load(std::memory_order_relaxed);
       while (left >= 0 && !g_fail_after.compare_exchange_weak(left, left - 1)) {
@@ -1259,67 +1220,74 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
       L->armed_copies = ++armed;
       return true;
     };
-    for (int j = 0; rc == SLUICE_OK && j < n_streams; ++j) {
+    // Issue the copies of the j-th expert in copy order.
+    auto issue = [&](int j) {
       const int i = L->order[j];
       const int local = L->streams[2 * i], slot = L->streams[2 * i + 1];
       const int srow = j < n_staged ? stage_ready_row(L, local) : -1;
-      int e = 0;  // next device-to-device engine
       for (size_t pi = 0; rc == SLUICE_OK && pi < L->params.size(); ++pi) {
         const ParamRows& p = L->params[pi];
         L->bytes += (int64_t)p.row_bytes;
         if (early && p.rows_dev != nullptr) continue;  // the gap kernel copies these rows itself
         char* dst = p.slot_base + (size_t)slot * p.row_bytes;
-        if (srow >= 0) {
-          // the staged row in parts, over the device-to-device engines
-          const int parts = L->stage_parts[pi];
-          size_t part = (p.row_bytes + (size_t)parts - 1) / (size_t)parts;
-          part = (part + 4095) & ~(size_t)4095;
-          const char* src = L->stage_dev[pi] + (size_t)srow * p.row_bytes;
-          for (size_t off = 0; off < p.row_bytes && rc == SLUICE_OK; off += part)
-            copy(dst + off, src + off, R->gpu_agent, std::min(part, p.row_bytes - off),
-                 R->d2d_engine[e++ % R->n_d2d]);
-        } else {
-          const hsa_agent_t from = p.host_agent.handle != 0 ? p.host_agent : R->cpu_agent;
-          copy(dst, p.host_base + (size_t)local * p.row_bytes, from, p.row_bytes,
+        if (srow >= 0)
+          copy(dst, L->stage_dev[pi] + (size_t)srow * p.row_bytes, R->gpu_agent, p.row_bytes, 0);
+        else
+          copy(dst, p.host_base + (size_t)local * p.row_bytes,
+               p.host_agent.handle != 0 ? p.host_agent : R->cpu_agent, p.row_bytes,
                R->engine[p.lane]);
-        }
         if (rc != SLUICE_OK) L->bytes -= (int64_t)p.row_bytes;
-        if (j == 0 && pi == 0) SLUICE_HTRACE(23, L, want, p.lane);
+        if (j == n_staged && pi == 0) SLUICE_HTRACE(23, L, want, p.lane);
       }
       L->sig_end[j] = armed;
-      if (rc == SLUICE_OK) {
-        whole = j + 1;
-        if (srow >= 0) {
-          ++L->stage_hits;
-          L->stage_hit_bytes += (int64_t)L->stage_bytes;
-        }
+      if (rc != SLUICE_OK) return;
+      whole = j + 1;
+      if (srow >= 0) {
+        ++L->stage_hits;
+        L->stage_hit_bytes += (int64_t)L->stage_bytes;
       }
-      if (!answered && rc == SLUICE_OK) {
-        respond(L, want, SLUICE_OK, n_streams);
-        answered = true;
-        SLUICE_HTRACE(24, L, want, n_copy);
-      }
-    }
-    // (a failure before the answer still answers the device: the map and
-    // the fill list are the bookkeeping's; the slots are marked below)
-    if (!answered) respond(L, want, SLUICE_OK, n_streams);
-    SLUICE_HTRACE(25, L, want, armed);
-    // Each expert landed (every one of its copies completed): mark its slot
-    // ready for this gap.
-    int landed = 0;  // experts in copy order whose copies completed, their slots marked
-    for (int j = 0, c = 0; j < whole; ++j) {
+    };
+    // Wait for the j-th expert's copies (from signal *c on) and mark its
+    // slot ready for this gap.
+    auto land = [&](int j, int* c) {
       int w = SLUICE_OK;
-      for (; c < L->sig_end[j] && w == SLUICE_OK; ++c) w = wait_signal(L->fill_sig[c]);
+      for (; *c < L->sig_end[j] && w == SLUICE_OK; ++*c) w = wait_signal(L->fill_sig[*c]);
       if (w != SLUICE_OK) {
         if (rc == SLUICE_OK) rc = w;
-        break;
+        return false;
       }
-      landed = j + 1;
       SLUICE_HTRACE(26, L, want, j);
-      if (!early) continue;
-      __atomic_store_n(&mb->slot_ready[L->streams[2 * L->order[j] + 1]], want, __ATOMIC_RELEASE);
-      SLUICE_HTRACE(27, L, want, j);
+      if (early) {
+        __atomic_store_n(&mb->slot_ready[L->streams[2 * L->order[j] + 1]], want, __ATOMIC_RELEASE);
+        SLUICE_HTRACE(27, L, want, j);
+      }
+      return true;
+    };
+    // The link is the bottleneck of a missing step: the staged experts and
+    // the first expert over the link are queued, the staged ones landed,
+    // then the device is answered (its resident experts then compute while
+    // the rows stream), then the other experts queued.
+    int j = 0;
+    for (; rc == SLUICE_OK && j < n_staged; ++j) issue(j);
+    if (rc == SLUICE_OK && j < n_streams) issue(j++);
+    int landed = 0, c = 0;  // experts in copy order whose copies completed, their slots marked
+    bool landing = true;    // no wait failed
+    auto land_upto = [&](int n) {
+      while (landing && landed < n) {
+        if (land(landed, &c)) ++landed;
+        else landing = false;
+      }
+    };
+    land_upto(std::min(whole, n_staged));
+    // (a failure before the answer still answers the device: the map and
+    // the fill list are the bookkeeping's; the slots are marked below)
+    if (early) {
+      respond(L, want, SLUICE_OK, n_streams);
+      SLUICE_HTRACE(24, L, want, n_copy);
     }
+    for (; rc == SLUICE_OK && j < n_streams; ++j) issue(j);
+    SLUICE_HTRACE(25, L, want, armed);
+    land_upto(whole);
     int marked = landed;  // streams whose slots are marked
     // every issued copy has completed (or the layer needs a resync, which
     // waits for them again)
@@ -1399,9 +1367,11 @@ struct sluice_gap_server {
 };
 
 // One staging step, on a sweep that found no record: take in the chunks
-// that landed, then put a chunk on each free staging lane, for the layers
-// whose gaps come next first.  A layer whose last stream-in failed to drain
-// stages nothing.
+// that landed, then put a chunk on each free staging lane, for the row
+// whose expert its layer selects most often (every layer counts one gap
+// per step, so the counts compare across layers; the link's idle time is
+// the budget, so the likeliest hits go first).  A layer whose last
+// stream-in failed to drain stages nothing.
 static void stage_step(sluice_gap_server* S) {
   for (int l = 0; l < kStageLanes; ++l) {
     sluice_layer* L = S->stage_lane[l];
@@ -1419,16 +1389,26 @@ static void stage_step(sluice_gap_server* S) {
       busy = true;
       continue;
     }
+    sluice_layer* best = nullptr;
+    int best_row = -1;
     for (size_t k = 0; k < n; ++k) {
       sluice_layer* L = S->layers[(S->cursor + k) % n];
       if (L->stage.empty() || L->stage_broken || L->armed_copies != 0) continue;
-      if (!L->stage_dirty && !stage_has_copy(L)) continue;
+      if (L->stage_sig_row[l] >= 0 || (!L->stage_dirty && !stage_has_copy(L))) continue;
       std::lock_guard<std::mutex> lk(L->mu);
       stage_choose(L);
-      if (L->stage_sig_row[l] < 0 && stage_issue(L, &g_dev[L->device], l)) {
-        S->stage_lane[l] = L;
+      const int r = stage_next_row(L);
+      if (r >= 0 && (best == nullptr || L->sel_count[L->stage[r].local] >
+                                            best->sel_count[best->stage[best_row].local])) {
+        best = L;
+        best_row = r;
+      }
+    }
+    if (best != nullptr) {
+      std::lock_guard<std::mutex> lk(best->mu);
+      if (stage_issue(best, &g_dev[best->device], l, best_row)) {
+        S->stage_lane[l] = best;
         busy = true;
-        break;
       }
     }
   }
@@ -1633,7 +1613,7 @@ extern "C" int sluice_layer_set_staging(sluice_layer* L, int rows) {
   if (stage_drain(L) != SLUICE_OK) return SLUICE_E_TIMEOUT;
   int rc = stage_free(L);
   if (rc != SLUICE_OK || rows == 0) return rc;
-  if (R->n_d2d == 0) return SLUICE_E_INVAL;  // no copy engines free for staging
+  if (R->stage_engine[0] == 0) return SLUICE_E_INVAL;  // no copy engines free for staging
   for (hsa_signal_t& sig : L->stage_sig)
     if (sig.handle == 0 && hsa_signal_create(0, 0, nullptr, &sig) != HSA_STATUS_SUCCESS)
       return SLUICE_E_COPY;
@@ -1642,7 +1622,6 @@ extern "C" int sluice_layer_set_staging(sluice_layer* L, int rows) {
   for (const ParamRows& p : L->params) bytes += p.rows_dev == nullptr ? p.row_bytes : 0;
   if (bytes == 0) return SLUICE_OK;  // nothing to stage
   L->stage_dev.assign(L->params.size(), nullptr);
-  L->stage_parts.assign(L->params.size(), 0);
   for (size_t pi = 0; pi < L->params.size(); ++pi) {
     const ParamRows& p = L->params[pi];
     if (p.rows_dev != nullptr) continue;
@@ -1654,10 +1633,6 @@ extern "C" int sluice_layer_set_staging(sluice_layer* L, int rows) {
       return (int)e;
     }
     L->stage_dev[pi] = (char*)d;
-    // the device-to-device engines shared by the params in proportion to
-    // their bytes
-    const double share = (double)p.row_bytes / (double)bytes * R->n_d2d;
-    L->stage_parts[pi] = std::max(1, (int)(share + 0.5));
   }
   L->stage_bytes = bytes;
   L->stage.assign((size_t)rows, sluice_layer::StageRow{});

@@ -71,7 +71,7 @@ NO_STATIC_FULL_ENV = "SLUICE_NO_STATIC_FULL"
 # selected experts it does not hold, copied while the host link idles; a
 # miss on one is copied into its slot from HBM).  0 turns staging off.
 STAGE_ROWS_ENV = "SLUICE_STAGE_ROWS"
-STAGE_ROWS_DEFAULT = 1
+STAGE_ROWS_DEFAULT = 4
 
 # Graph split points under piecewise capture: the MoE ops (whose apply runs
 # the classic hook, which syncs the host) and the gap op.
