@@ -676,6 +676,87 @@ def test_failed_stream_in_drops_unlanded_fills_and_resync_installs_host_map(monk
     off.close()
 
 
+def test_failed_stream_in_with_staged_misses_keeps_what_landed(monkeypatch):
+    """Failure handling with staged rows, forced from the host.  Under the
+    gap server with four staging rows and a plain LRU (no protected
+    segment), eight experts X are selected four times, then evicted by
+    sixteen others: X are then the layer's most selected experts it does
+    not hold, and the four lowest ids of X get staged.  A gap selecting X
+    copies those four from HBM first, then the other four over the link;
+    the 10th row copy (the second of the first expert over the link) is
+    made to fail.  The gap reports the error, the four staged experts were
+    served from their rows and stay cached with their host rows, the other
+    four leave the slot cache; after reset_gaps later gaps follow the
+    oracle with the same drops."""
+    import time
+
+    from oracle.slru import LayerCache
+    from sluice_amd import _lib
+
+    E, S, k, H, I = 32, 16, 4, 2048, 768
+    print("failed stream-in with staged misses", flush=True)
+    monkeypatch.setenv("SLUICE_STAGE_ROWS", "4")
+    layer = _Layer(E, E, H=H, I=I)
+    off = _offloader(monkeypatch, S, 0.0, False)
+    off.wrap_modules(iter([layer]))
+    with torch.cuda.device(DEV):
+        off.post_init()
+    cache = off._caches[id(layer)]
+    off._rs_caches.append(cache)
+    off.start_gap_server()
+    lib = _lib.load()
+    oracle = LayerCache(E, E, S, 0.0)
+    hs = torch.zeros((2, 64), dtype=torch.bfloat16, device=DEV)
+    rng = np.random.default_rng(5)
+
+    def gap(ids_np):
+        torch.ops.vllm.sluice_stream_gap(hs[: len(ids_np) // k],
+                                         torch.from_numpy(ids_np).to(DEV).view(-1, k), 0)
+        off.drain()
+
+    def check_state():
+        st = cache._state()
+        assert st["expert_in_slot"] == [-1 if v is None else v for v in oracle.expert_in_slot]
+        assert st["probation"] == list(oracle.probation)
+        assert st["free_slots"] == list(oracle.free_slots)
+
+    perm = rng.permutation(E).astype(np.int32)
+    x, others = perm[:8], perm[8:24]
+    for ids_np in [x] * 4 + [others[:8], others[8:]]:
+        gap(ids_np)
+        oracle.gap(ids_np.tolist())
+        check_state()
+    assert all(oracle.slot_of.get(int(g)) is None for g in x)
+    t0 = time.monotonic()
+    while off.stage_counters()["ready"] < 4 and time.monotonic() - t0 < 5.0:
+        time.sleep(0.001)
+    assert off.stage_counters()["ready"] == 4
+    assert lib.sluice_gap_inject_copy_failure(9) == 0
+    try:
+        with pytest.raises(RuntimeError):
+            gap(np.sort(x))
+    finally:
+        lib.sluice_gap_inject_copy_failure(-1)
+    streams = oracle.gap(np.sort(x).tolist())
+    assert len(streams) == 8
+    for _, slot in streams[4:]:  # over the link: the first of them failed, none landed
+        assert oracle.unfill(slot)
+    check_state()
+    assert off.stage_counters()["hits"] == 4
+    off.reset_gaps()
+    oracle.map, oracle.map_is_standing = oracle.standing_map(), True
+    assert cache.expert_map_buf.cpu().tolist() == oracle.map
+    _slot_bytes_match_host(cache)
+    for n in range(6):
+        ids_np = rng.choice(E, 2 * k, replace=False).astype(np.int32)
+        gap(ids_np)
+        oracle.gap(ids_np.tolist())
+        check_state()
+        assert cache.expert_map_buf.cpu().tolist() == oracle.map, n
+    _slot_bytes_match_host(cache)
+    off.close()
+
+
 def test_wait_bound_set_after_capture_applies_to_replays(monkeypatch):
     """The bound of the gap's device waits is read when a wait begins, so a
     hipGraph captured under the default bound (20 s) follows a bound set
