@@ -889,7 +889,8 @@ def full_record(a, cfg, sp, slots, batches, gen_len, head, extras, cpu):
 
 # columns of the compact line's batch rows
 ROW_COLS = ["shape", "slots", "c", "path", "routing", "steps", "ms_per_step", "tok_per_s",
-            "misses_per_layer_step", "fast_hit_share", "h2d_GBs_in_step", "ref_tok_per_s"]
+            "misses_per_layer_step", "fast_hit_share", "staged_share_of_misses",
+            "h2d_GBs_in_step", "ref_tok_per_s"]
 LINE_LIMIT = 6000  # bytes; the last stdout line must stay whole in a short tail
 
 
@@ -924,7 +925,9 @@ def compact_line(rec):
             rows.append([shape, slots, r["c"], path, routing, r.get("steps", rec["steps"]),
                          _r(r["ms_per_step"], 3),
                          _r(r["tok_per_s"], 1), _r(r["misses_per_layer_step"], 3),
-                         _r(r["fast_hit_share"], 3), _r(r["h2d_GBs_in_step"], 1), ref])
+                         _r(r["fast_hit_share"], 3),
+                         _r((r.get("staged") or {}).get("hit_share_of_misses"), 3),
+                         _r(r["h2d_GBs_in_step"], 1), ref])
         if k1:
             key = f"{shape}/s{slots}/c{k1['c']}"
             g1[key] = _r(k1.get("frac", k1["achieved_GBs"] / HBM_PEAK_GBS), 3)
@@ -937,6 +940,7 @@ def compact_line(rec):
                  and r["orchestration"] == ORCH_GRAPH and r["routing"] not in ("locality",
                                                                               "matched")]
     in_step = head_rows[0]["h2d_GBs_in_step"] if head_rows else None
+    staging = (head_rows[0].get("staged") or {}).get("rows_per_layer") if head_rows else None
     line = {
         "metric": rec["metric"], "value": _r(rec["value"], 2), "unit": rec["unit"],
         "n_gpus": rec["n_gpus"], "steps": rec["steps"], "warmup": rec["warmup"],
@@ -949,7 +953,8 @@ def compact_line(rec):
                    "prompt_len": c["prompt_len"], "decode_len": c["decode_len"],
                    "routing": {k: c["routing"][k] for k in ("zipf_s", "rho", "sigma", "gate_std")
                                if k in c["routing"]},
-                   "baseline_ref": c.get("baseline_ref")},
+                   "baseline_ref": c.get("baseline_ref"),
+                   "staging_rows_per_layer": staging},
         "roofline": {"bound": roof["bound"], "achieved": _r(roof["achieved"], 1),
                      "peak": roof["peak"], "unit": roof["unit"], "frac": _r(roof["frac"], 4),
                      "traffic": roof["traffic"], "kernel": roof["kernel"],
