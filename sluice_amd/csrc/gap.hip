@@ -960,6 +960,7 @@ void stage_poll(sluice_layer* L) {
       continue;
     }
     L->stage_h2d += (int64_t)L->stage_sig_bytes[l];
+    SLUICE_HTRACE(29, L, 0, (int32_t)((L->stage_sig_bytes[l] >> 10) << 1 | (size_t)l));
     if (row.state == kStageEmpty && row.in_flight == 0) L->stage_dirty = true;  // free again
   }
   for (sluice_layer::StageRow& row : L->stage)
@@ -1059,6 +1060,7 @@ bool stage_issue(sluice_layer* L, const DeviceRes* R, int l, int r) {
     ++row.in_flight;
     L->stage_sig_row[l] = r;
     L->stage_sig_bytes[l] = len;
+    SLUICE_HTRACE(28, L, 0, (int32_t)((len >> 10) << 1 | (size_t)l));
     return true;
   }
   return false;
@@ -1237,7 +1239,7 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
                p.host_agent.handle != 0 ? p.host_agent : R->cpu_agent, p.row_bytes,
                R->engine[p.lane]);
         if (rc != SLUICE_OK) L->bytes -= (int64_t)p.row_bytes;
-        if (j == n_staged && pi == 0) SLUICE_HTRACE(23, L, want, p.lane);
+        if (j == n_staged && pi == 0) SLUICE_HTRACE(23, L, want, n_staged);
       }
       L->sig_end[j] = armed;
       if (rc != SLUICE_OK) return;

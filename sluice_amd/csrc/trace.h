@@ -22,10 +22,15 @@
 //     16 a pending gemm2 item done (ticket)
 //   host, gap service (layer id = the device map address >> 8):
 //     21 record copied out (v = misses the device counted)
-//     22 bookkeeping done (v = stream-ins)   23 first row copy issued
-//     24 device answered (v = experts per completion signal)
-//     25 every row copy issued (v = signals)  26 group g landed (v = g)
-//     27 group g's slots marked ready (v = g)
+//     22 bookkeeping done (v = stream-ins)
+//     23 first row copy over the link issued (v = experts before it in copy
+//        order: those served from staged rows)
+//     24 device answered (v = row copies per expert)
+//     25 every row copy issued (v = signals)
+//     26 expert j (copy order) landed (v = j)
+//     27 expert j's slot marked ready (v = j)
+//     28 staging chunk issued, 29 staging chunk seen landed (stamp 0,
+//        v = KiB << 1 | staging lane)
 #pragma once
 
 #include "common.h"

@@ -128,11 +128,19 @@ def analyse(rings, clock, layer_ids, steps, bytes_per_expert):
     for a, l, s, t in zip(tag, lid, stp, tg):
         G.setdefault((lay.get(int(l), -1), int(s)), {})[int(a)] = t
     H = {}
+    stage_open, stage_iv = {}, []  # staging chunks: issue time per (layer, lane), intervals
     for a, l, s, v, t in rings["host"]:
+        if a in (28, 29):
+            q = stage_open.setdefault((int(l), int(v) & 1), [])
+            if a == 28:
+                q.append(t)
+            elif q:
+                stage_iv.append((q.pop(0), t, (int(v) >> 1) * 1024))
+            continue
         k = (lay.get(int(l), -1), int(s) & 0xffffff)
         d = H.setdefault(k, {"groups": [], "marks": []})
         if a == 26:
-            d["groups"].append(t)
+            d["groups"].append((int(v), t))
         elif a == 27:
             d["marks"].append(t)
         else:
@@ -174,7 +182,10 @@ def analyse(rings, clock, layer_ids, steps, bytes_per_expert):
         for key, tg_ in (("seen", 21), ("booked", 22), ("first_copy", 23), ("answered", 24),
                          ("issued", 25)):
             r[key] = h.get(tg_, np.nan) - t0
-        r["landed"] = max(h["groups"]) - t0 if h["groups"] else np.nan
+        r["staged"] = h.get(("v", 23), len(h["groups"]))
+        r["landed"] = max(t for _, t in h["groups"]) - t0 if h["groups"] else np.nan
+        host = [t for j, t in h["groups"] if j >= r["staged"]]
+        r["landed_host"] = max(host) - t0 if host else np.nan
         r["marked"] = max(h["marks"]) - t0 if h["marks"] else np.nan
         def first(x):
             sel = seg_t[seg_tag == x]
@@ -197,6 +208,7 @@ def analyse(rings, clock, layer_ids, steps, bytes_per_expert):
             "n": int(len(v))}
 
     miss = [r for r in rows if r["streams"] > 0 and np.isfinite(r["landed"])]
+    link = [r for r in miss if np.isfinite(r["first_copy"]) and np.isfinite(r["landed_host"])]
     hit = [r for r in rows if r["streams"] == 0]
     out = {"layer_steps": len(rows), "with_stream_ins": len(miss), "without": len(hit),
            "head": {k: stat(r[k] for r in miss) for k in (
@@ -208,7 +220,7 @@ def analyse(rings, clock, layer_ids, steps, bytes_per_expert):
                                                                          "next")},
            "pending_item": {"gemm1_wait_end_to_done": stat(item_g1),
                             "gemm2_count_to_done": stat(item_g2)}}
-    win = [(r["landed"] - r["first_copy"], r["streams"]) for r in miss]
+    win = [(r["landed_host"] - r["first_copy"], r["streams"] - r["staged"]) for r in link]
     out["copy_window"] = {
         "rate_GBs_median": round(float(np.median([n * bytes_per_expert / w / 1e9
                                                   for w, n in win])), 2),
@@ -216,23 +228,47 @@ def analyse(rings, clock, layer_ids, steps, bytes_per_expert):
                                 "window_us_median": round(float(np.median(
                                     [w for w, m in win if m == n])) * 1e6, 1)}
                        for n in sorted({n for _, n in win})}}
-    # link idle between consecutive copy windows, in stream order
+    # link idle between consecutive copy windows over the link, in stream order
     seq = sorted(rows, key=lambda r: r["t0"])
     idle_tr, idle_skip, last_end, skipped = 0.0, 0.0, None, 0
     for r in seq:
-        if r["streams"] > 0 and np.isfinite(r["landed"]):
+        if r in link:
             if last_end is not None:
                 gap_s = r["t0"] + r["first_copy"] - last_end
                 if skipped:
                     idle_skip += gap_s
                 else:
                     idle_tr += gap_s
-            last_end, skipped = r["t0"] + r["landed"], 0
+            last_end, skipped = r["t0"] + r["landed_host"], 0
         else:
             skipped += 1
-    out["link_idle_ms_per_step"] = {
-        "between_consecutive_layers_with_stream_ins": round(idle_tr / steps * 1e3, 3),
-        "across_layers_without_stream_ins": round(idle_skip / steps * 1e3, 3)}
+    out["gap_copies_idle_ms_per_step"] = {
+        "between_consecutive_layers_with_copies_over_the_link": round(idle_tr / steps * 1e3, 3),
+        "across_layers_without_them": round(idle_skip / steps * 1e3, 3)}
+    # the link's busy time: the gaps' copy windows and the staging chunks
+    if seq:
+        iv = [(r["t0"] + r["first_copy"], r["t0"] + r["landed_host"]) for r in link]
+        iv += [(a, b) for a, b, _ in stage_iv]
+        lo = seq[0]["t0"]
+        hi = max([r["t0"] + (r["next"] if np.isfinite(r["next"]) else 0.0) for r in seq]
+                 + [b for _, b in iv])
+        busy, end = 0.0, lo
+        for a, b in sorted(iv):
+            a, b = max(a, end), min(b, hi)
+            if b > a:
+                busy += b - a
+                end = b
+        span = hi - lo
+        in_win = [x for x in stage_iv if lo <= x[0] < hi]
+        out["link"] = {
+            "busy_share": round(busy / span, 4) if span > 0 else None,
+            "idle_ms_per_step": round((span - busy) / steps * 1e3, 3),
+            "staging_chunks_per_step": round(len(in_win) / steps, 2),
+            "staging_MB_per_step": round(sum(x[2] for x in in_win) / steps / 1e6, 2),
+            "staging_chunk_us_median": round(float(np.median([b - a for a, b, _ in in_win]))
+                                             * 1e6, 1) if in_win else None,
+            "gaps_with_staged_misses": sum(1 for r in miss if r["staged"] > 0),
+            "gaps_all_staged": sum(1 for r in miss if r["staged"] >= r["streams"])}
     return out, rows
 
 

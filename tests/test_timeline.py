@@ -1,8 +1,10 @@
 """The gap-timeline analysis (sluice_amd/timeline.py) on synthetic trace
 rings whose answers are known: the clock mapping, the head and tail of a
-layer-step that streams, a layer-step that streams nothing, the pending
-items' own durations and the link-idle split.  No GPU: the rings are built
-here the way the trace build writes them (trace.h)."""
+layer-step that streams, a layer-step that streams nothing, a gap with one
+miss served from a staged row and one over the link, a staging chunk, the
+pending items' own durations, the link-idle split and the link's busy
+time.  No GPU: the rings are built here the way the trace build writes
+them (trace.h)."""
 
 import numpy as np
 
@@ -42,11 +44,20 @@ def _rings():
            _dev(11, 64, base + 540 * US),
            _dev(13, 8, base + 850 * US)]
     host = []
-    for lid, t0, landed in ((L0, 0.0, 316.0), (L2, 500.0, 800.0)):
-        for tag, v, us in ((21, 1, 2.5), (22, 1, 2.8), (23, 0, 6.0), (24, 1, 8.0), (25, 1, 9.0)):
+    # layer 0: one miss over the link; layer 2: one miss from a staged row
+    # (copy order 0, landed at 540 us) and one over the link (order 1)
+    for lid, t0, landed, staged in ((L0, 0.0, 316.0, 0), (L2, 500.0, 800.0, 1)):
+        for tag, v, us in ((21, 1 + staged, 2.5), (22, 1 + staged, 2.8), (23, staged, 6.0),
+                           (24, 1, 8.0), (25, 1, 9.0)):
             host.append((tag, lid, 5, v, h(t0 + us)))
-        host.append((26, lid, 5, 0, h(landed)))
-        host.append((27, lid, 5, 0, h(landed + 0.05)))
+        if staged:
+            host.append((26, lid, 5, 0, h(540.0)))
+            host.append((27, lid, 5, 0, h(540.05)))
+        host.append((26, lid, 5, staged, h(landed)))
+        host.append((27, lid, 5, staged, h(landed + 0.05)))
+    # a staging chunk of 1 MiB on staging lane 0, 330 -> 350 us
+    host.append((28, L0, 0, (1024 << 1) | 0, h(330.0)))
+    host.append((29, L0, 0, (1024 << 1) | 0, h(350.0)))
     host.append((21, L1, 5, 0, h(382.0)))
     host.append((22, L1, 5, 0, h(382.3)))
     rings = {"gap": np.array(gap, dtype=np.uint64), "moe": np.array(moe, dtype=np.uint64),
@@ -79,8 +90,17 @@ def test_analysis_recovers_the_known_timeline():
     # one streamed expert per window: 17.3 MB over (316 - 6) us and (800 - 506) us
     rates = [17_301_504 / 310e-6 / 1e9, 17_301_504 / 294e-6 / 1e9]
     assert abs(out["copy_window"]["rate_GBs_median"] - np.median(rates)) < 0.05
-    # the only link-idle stretch crosses the layer that streams nothing:
-    # landed at 316 us -> next first copy at 506 us
-    idle = out["link_idle_ms_per_step"]
-    assert idle["between_consecutive_layers_with_stream_ins"] == 0.0
-    assert abs(idle["across_layers_without_stream_ins"] - 0.190) < 1e-3
+    # the only idle stretch between the gaps' copies over the link crosses the
+    # layer that streams nothing: landed at 316 us -> next first copy at 506 us
+    idle = out["gap_copies_idle_ms_per_step"]
+    assert idle["between_consecutive_layers_with_copies_over_the_link"] == 0.0
+    assert abs(idle["across_layers_without_them"] - 0.190) < 1e-3
+    # the link over 0..800 us: copies 6-316 and 506-800, the staging chunk
+    # 330-350: busy 624 us, idle 176 us
+    link = out["link"]
+    assert abs(link["busy_share"] - 624 / 800) < 1e-3
+    assert abs(link["idle_ms_per_step"] - 0.176) < 1e-3
+    assert link["staging_chunks_per_step"] == 1.0
+    assert abs(link["staging_chunk_us_median"] - 20.0) < 0.05
+    assert abs(link["staging_MB_per_step"] - 1.05) < 1e-2
+    assert link["gaps_with_staged_misses"] == 1 and link["gaps_all_staged"] == 0
