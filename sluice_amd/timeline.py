@@ -37,6 +37,7 @@ import json
 import os
 import sys
 import time
+from collections import Counter
 
 import numpy as np
 
@@ -268,7 +269,11 @@ def analyse(rings, clock, layer_ids, steps, bytes_per_expert):
             "staging_chunk_us_median": round(float(np.median([b - a for a, b, _ in in_win]))
                                              * 1e6, 1) if in_win else None,
             "gaps_with_staged_misses": sum(1 for r in miss if r["staged"] > 0),
-            "gaps_all_staged": sum(1 for r in miss if r["staged"] >= r["streams"])}
+            "gaps_all_staged": sum(1 for r in miss if r["staged"] >= r["streams"]),
+            "gaps_by_misses_staged_and_over_the_link": {
+                f"{a}+{b}": n for (a, b), n in sorted(Counter(
+                    (min(r["staged"], r["streams"]), max(r["streams"] - r["staged"], 0))
+                    for r in miss).items())}}
     return out, rows
 
 
