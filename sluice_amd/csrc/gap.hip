@@ -30,6 +30,11 @@
 //     native server thread (sluice_gap_server_*), which makes the gap op
 //     capturable, so a whole decode step replays as one hipGraph.
 //
+//   staging rows (sluice_layer_set_staging): copies in HBM of the experts a
+//     layer selects most often but does not hold, which the server thread
+//     fills while the host link idles; a miss on one is copied into its slot
+//     from HBM before the device is answered.
+//
 // Ordering: a gap kernel runs only after all earlier work on its stream has
 // completed, so when the host sees its record no kernel of that stream can
 // still read a slot about to be overwritten (what the reference fences with
