@@ -65,6 +65,9 @@ def test_compact_line_fits_and_parses():
     assert first["shape"] == rec["config"]["model_shape"]
     head = dict(zip(cols, next(r for r in line["rows"] if r[2] == line["config"]["batch"])))
     assert head["ref_tok_per_s"] == 1062.6  # README.md:51, V2-Lite c=8
+    # the staging rows the headline ran with, and the share of its misses they served
+    assert line["config"]["staging_rows_per_layer"] == 4
+    assert 0.0 < head["staged_share_of_misses"] < 1.0
 
 
 def test_compact_line_stays_under_the_limit_with_every_row_doubled():
