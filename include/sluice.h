@@ -276,7 +276,7 @@ int sluice_layer_pulled_params(sluice_layer* layer);
  * layer kept in HBM outside the slots, each a copy of one expert the layer
  * selects often but does not hold (the most selected ones, by counts of
  * the gaps' selections halved every 4096 gaps).  A gap server fills them
- * from the host store while the host link idles, in 1 MiB chunks on two
+ * from the host store while the host link idles, in 2 MiB chunks on two
  * SDMA engines the gap's own copies do not use, at most two chunks in
  * flight per server.  A gap answered before its rows land copies a miss
  * whose expert is staged into its slot from HBM with the runtime's

@@ -574,7 +574,7 @@ constexpr int kLanes = 2;
 // runtime's device-to-device copy (a copy kernel: 17.3 MB in ~29 us on
 // MI355X, against ~310 us over the link).
 constexpr int kStageLanes = 2;
-constexpr size_t kStageChunk = 1 << 20;
+constexpr size_t kStageChunk = 2 << 20;
 constexpr int kMaxStageRows = 8;
 constexpr int kStageHalfLife = 4096;  // gaps between halvings of the selection counts
 
