@@ -158,6 +158,7 @@ def run_batch(dec, c, steps, warmup, prefill=True, label=None):
     dec.sync()
     before = dec.gap_counters()
     stage0 = dec.off.stage_counters()
+    codec0 = dec.off.codec_counters()
     cl0 = dec.off.classic_counters()
     pos0 = int(dec.state[c].pos[0]) if dec.has_attn else None
     # per-step times from events between the steps (the value is the
@@ -179,12 +180,15 @@ def run_batch(dec, c, steps, warmup, prefill=True, label=None):
     delta = {k: after[k] - before[k] for k in after}
     stage1 = dec.off.stage_counters()
     sdelta = {k: stage1[k] - stage0[k] for k in ("filled", "h2d_bytes", "hits", "hit_bytes")}
+    codec1 = dec.off.codec_counters()
     cl1 = dec.off.classic_counters()
     n_moe = len(dec.moe_layers)
-    # bytes over the host link: slot fills from the host store, plus the
-    # staging copies (a fill from a staged row moves HBM to HBM)
+    # bytes over the host link: the slot fills' copies from the host store
+    # (coded rows where the store is coded), plus the staging copies (a fill
+    # from a staged row moves HBM to HBM)
     fill = delta["bytes"] / steps
-    h2d = (delta["bytes"] - sdelta["hit_bytes"] + sdelta["h2d_bytes"]) / steps
+    link = codec1["link_bytes"] - codec0["link_bytes"]
+    h2d = (link + sdelta["h2d_bytes"]) / steps
     return {
         "c": c, "steps": steps, "path": "classic" if dec.classic(c) else "gap",
         "routing": label or "zipf",
@@ -202,6 +206,10 @@ def run_batch(dec, c, steps, warmup, prefill=True, label=None):
                    "hit_share_of_misses": sdelta["hits"] / max(delta["misses"], 1),
                    "rows_filled": sdelta["filled"],
                    "staging_h2d_bytes_per_step": sdelta["h2d_bytes"] / steps},
+        "coded": {"params_per_layer": codec1["params"] // max(n_moe, 1),
+                  "store_ratio": codec1["coded_bytes"] / max(codec1["store_bytes"], 1),
+                  "decodes": codec1["decodes"] - codec0["decodes"],
+                  "fill_link_bytes_per_step": link / steps},
         "misses_per_layer_step": delta["misses"] / max(steps * n_moe, 1),
         "fast_hit_share": delta["fast_hits"] / max(delta["gaps"], 1),
         "prefill": {"tokens_per_sequence": dec.prompt_len if prefill else 0,

@@ -296,6 +296,44 @@ int sluice_layer_set_staging(sluice_layer* layer, int rows);
  * from a staged row, and those misses' bytes. */
 int sluice_layer_stage_counters(const sluice_layer* layer, int64_t* counters);
 
+/* Coded host stores: no counterpart in the reference, which streams the
+ * rows as they are.  For every param whose bit is set in `bf16_params` (bit
+ * i = the i-th sluice_layer_add_param, its rows bf16 values, a multiple of
+ * 2048 per row; at most 4 params, the pulled ones excepted) the layer codes
+ * each expert's row losslessly into a pinned host store of its own
+ * (sluice_codec_encode, on up to 16 host threads): sign and mantissa whole,
+ * the exponent as a 4-bit offset from a base per 2048 values, exponents
+ * outside that window in a per-chunk escape list.  A param whose rows code
+ * to more than 7/8 of their bytes stays uncoded.  Under a gap server whose
+ * gaps are answered before their rows land (sluice_gap_set_pipelined(1)),
+ * a miss then copies the coded rows over the link into a ring in HBM that
+ * the server owns (at least 128 MiB, and twice the largest coded expert),
+ * and a decode kernel on the server's own stream writes the rows into the
+ * slot and marks it ready; staging rows hold coded rows too and are decoded
+ * from where they lie.  Slot bytes, maps and products are those of the
+ * uncoded store; every other path (inline gaps, classic waves, resync)
+ * copies the rows as they are, from the store given to add_param, which
+ * must stay valid.  Call before sluice_layer_set_staging and with no gap
+ * server serving the layer; 0 frees the coded stores; a call with the mask
+ * already set changes nothing.  SLUICE_E_STATE after staging is set. */
+int sluice_layer_set_codec(sluice_layer* layer, uint32_t bf16_params);
+/* counters[6]: params coded, bytes of one expert's coded params as rows,
+ * bytes of every local expert's coded rows, bytes of the slot fills' row
+ * copies over the link (served gaps and classic waves; coded or not),
+ * decode jobs launched, and those that decoded a staging row. */
+int sluice_layer_codec_counters(const sluice_layer* layer, int64_t* counters);
+
+/* The host store codec by itself.  sluice_codec_encode codes n bf16 values
+ * (n a multiple of 2048; rows 2-byte, out 4-byte aligned) into out (cap
+ * bytes; NULL to ask) and sets *coded_bytes; sluice_codec_decode decodes
+ * `coded_bytes` of a coded row in device memory into n bf16 values at
+ * out_dev (both 16-byte aligned) on `stream` and waits for it (it
+ * allocates a word of device memory per call). */
+int sluice_codec_encode(const void* rows, size_t n, void* out, size_t cap,
+                        size_t* coded_bytes);
+int sluice_codec_decode(const void* coded_dev, size_t n, size_t coded_bytes,
+                        void* out_dev, sluice_stream_t stream);
+
 /* Mark a slot as pre-filled with `local` outside the SLRU segments (full
  * residency pre-fill and static pins, offloader.py:1000-1010, 1046-1083);
  * debits protected_cap by one when `debit_protected` is set (pins). */

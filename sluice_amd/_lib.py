@@ -81,6 +81,10 @@ SIGNATURES = {
     "sluice_layer_pulled_params": (c_int, [_P]),
     "sluice_layer_set_staging": (c_int, [_P, c_int]),
     "sluice_layer_stage_counters": (c_int, [_P, _P]),
+    "sluice_layer_set_codec": (c_int, [_P, ctypes.c_uint32]),
+    "sluice_layer_codec_counters": (c_int, [_P, _P]),
+    "sluice_codec_encode": (c_int, [_P, ctypes.c_size_t, _P, ctypes.c_size_t, _P]),
+    "sluice_codec_decode": (c_int, [_P, ctypes.c_size_t, ctypes.c_size_t, _P, _P]),
     "sluice_layer_pin": (c_int, [_P, c_int, c_int, POINTER(c_int)]),
     "sluice_layer_gap": (c_int, [_P, _P, c_int, c_int, _P]),
     "sluice_layer_gap_launch": (c_int, [_P, _P, c_int, _P, _P, c_size_t, _P, _P]),

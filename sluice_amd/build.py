@@ -27,9 +27,13 @@ OUT = os.path.join(HERE, "libsluice_hip.so")
 # The gap-timeline build (-DSLUICE_TRACE: csrc/trace.h), loaded instead of the
 # default library when SLUICE_TRACE=1 (sluice_amd/timeline.py sets it).
 OUT_TRACE = os.path.join(HERE, "libsluice_hip_trace.so")
+# The decode kernel of coded host stores: a code object of its own, beside
+# the libraries, which load it with the HSA loader (csrc/codec.hip).
+DECODE_SOURCE = "codec_kernel.hip"
+OUT_DECODE = os.path.join(HERE, "codec_decode.hsaco")
 BUILD_DIR = os.path.join(ROOT, "_build")
 
-SOURCES = ["routing.hip", "gap.hip", "moe.hip", "decoder.hip", "probe.hip"]
+SOURCES = ["routing.hip", "gap.hip", "moe.hip", "decoder.hip", "probe.hip", "codec.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -90,6 +94,14 @@ def _run(cmd: list[str]) -> str:
 VGPR_FILE = 512
 COPY_KERNEL_VGPRS_PER_SIMD = 2 * 16
 WAITING_KERNELS = ("moe_gemm2_split_kernel",)
+# The gap server's decode of a coded expert (csrc/codec_kernel.hip) runs while the
+# split launch's pending workgroups wait for it: one 256-thread workgroup
+# (one wave per SIMD) must fit beside their waves.  Coded stores hold bf16
+# rows, and a layer's product waits for every expert its gap decodes, so the
+# decodes only ever need room beside the bf16 split launch.
+DECODE_KERNEL = "sluice_codec_decode_kernel"
+DECODE_WAVES_PER_SIMD = 1
+DECODE_BESIDE = ("moe_gemm2_split_kernelILb0E",)
 
 
 def kernel_resources(remarks: str) -> dict[str, dict[str, int]]:
@@ -128,6 +140,23 @@ def check_wait_room(remarks: str) -> list[str]:
     return bad
 
 
+def check_decode_room(moe_remarks: str, codec_remarks: str) -> list[str]:
+    """Waiting bf16 kernels whose waves, at their occupancy, leave less than
+    the decode kernel's VGPRs per SIMD free (empty: it fits beside all)."""
+    dec = [r for n, r in kernel_resources(codec_remarks).items() if DECODE_KERNEL in n]
+    if not dec:
+        return [f"{DECODE_KERNEL}: no resource remarks"]
+    need = DECODE_WAVES_PER_SIMD * max(vgpr_alloc(r["VGPRs"], r["AGPRs"]) for r in dec)
+    bad = []
+    for name, r in kernel_resources(moe_remarks).items():
+        if not any(k in name for k in DECODE_BESIDE):
+            continue
+        free = VGPR_FILE - r["Occupancy"] * vgpr_alloc(r["VGPRs"], r["AGPRs"])
+        if free < need:
+            bad.append(f"{name}: leaves {free} VGPRs per SIMD, the decode needs {need}")
+    return bad
+
+
 def build(verbose: bool = False, trace: bool = False) -> str:
     hipcc = _hipcc()
     bdir = os.path.join(BUILD_DIR, "trace") if trace else BUILD_DIR
@@ -141,12 +170,19 @@ def build(verbose: bool = False, trace: bool = False) -> str:
         cmds.append([hipcc, *HIPCC_FLAGS, *(["-DSLUICE_TRACE"] if trace else []),
                      *([RESOURCE_REMARKS] if src == "moe.hip" else []), "-c",
                      os.path.join(CSRC, src), "-o", obj])
+    dec_tmp = os.path.join(bdir, "codec_decode.hsaco")
+    cmds.append([hipcc, *HIPCC_FLAGS, "--cuda-device-only", "--no-gpu-bundle-output",
+                 RESOURCE_REMARKS, "-c", os.path.join(CSRC, DECODE_SOURCE), "-o", dec_tmp])
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
         logs = [fut.result() for fut in [ex.submit(_run, c) for c in cmds]]
     bad = check_wait_room(logs[SOURCES.index("moe.hip")])
     if bad:
         raise RuntimeError("kernels that wait on streaming slots leave no room for the "
                            "runtime's copy kernel:\n  " + "\n  ".join(bad))
+    bad = check_decode_room(logs[SOURCES.index("moe.hip")], logs[-1])
+    if bad:
+        raise RuntimeError("kernels that wait on streaming slots leave no room for the "
+                           "decode of coded experts:\n  " + "\n  ".join(bad))
     # libhsa-runtime64: the gap's row copies go to the SDMA engines directly
     # (csrc/gap.hip), through the same HSA runtime HIP runs on
     link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs]
@@ -157,6 +193,8 @@ def build(verbose: bool = False, trace: bool = False) -> str:
     link += ["-lhsa-runtime64", "-o", tmp]
     _run(link)
     os.replace(tmp, out)
+    shutil.copyfile(dec_tmp, OUT_DECODE + ".tmp")
+    os.replace(OUT_DECODE + ".tmp", OUT_DECODE)
     if verbose:
         print(f"built {out}")
     return out

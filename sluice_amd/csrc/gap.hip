@@ -54,6 +54,7 @@
 #include <algorithm>
 #include <atomic>
 #include <chrono>
+#include <deque>
 #include <mutex>
 #include <new>
 #include <thread>
@@ -62,6 +63,7 @@
 #include <hsa/hsa.h>
 #include <hsa/hsa_ext_amd.h>
 
+#include "codec.h"
 #include "common.h"
 #include "plan.h"
 #include "slotwait.h"
@@ -760,6 +762,39 @@ struct ParamRows {
   int lane;                 // copy lane of this param's rows
   char* rows_dev = nullptr;  // HBM copy of all host rows when the gap kernel pulls them
   hsa_agent_t host_agent{};  // the agent owning the host rows (0: the first CPU agent)
+  // Coded host store (sluice_layer_set_codec; nullptr: the rows stream as
+  // they are): expert `local`'s coded row at coded_base + local *
+  // coded_stride, coded_len[local] bytes.
+  char* coded_base = nullptr;
+  size_t coded_stride = 0;
+  std::vector<uint32_t> coded_len;
+  hsa_agent_t coded_agent{};
+};
+
+// Decode resources of a gap server whose layers hold coded host stores: the
+// device's decode queue, the word the jobs' last workgroups release their
+// sequence numbers into (jobs on the queue complete in order), and the ring
+// in HBM that coded rows land in before they are decoded into slots.
+struct CodecRes {
+  int device = 0;
+  CodecQueue* queue = nullptr;
+  uint32_t* wg_count = nullptr;             // device word, 0 between jobs
+  unsigned long long* done_host = nullptr;  // host-mapped: the last job completed
+  unsigned long long* done_dev = nullptr;
+  char* ring = nullptr;
+  size_t ring_bytes = 0, head = 0;
+  // ring regions in allocation order; a region is free again once the job
+  // that decodes it completed (or its copies failed)
+  struct Use {
+    int64_t id;
+    size_t off, len;
+    unsigned long long seq;
+    int state;
+  };
+  std::deque<Use> uses;
+  int64_t next_use = 0;
+  unsigned long long seq = 0;  // the last job launched (server thread)
+  std::atomic<unsigned long long> launched{0};  // the same, for other threads
 };
 
 struct sluice_gap_server;
@@ -804,6 +839,7 @@ struct sluice_layer {
     int state = 0;      // kStageEmpty / kStageCopying / kStageReady
     size_t issued = 0;  // bytes whose copies were issued
     int in_flight = 0;  // of its chunks
+    unsigned long long busy_seq = 0;  // decode job that reads the row (coded stores)
   };
   std::vector<StageRow> stage;
   std::vector<char*> stage_dev;  // per param (nullptr: pulled, or no staging)
@@ -816,6 +852,16 @@ struct sluice_layer {
   bool stage_dirty = false;   // a gap was served since the rows were chosen
   bool stage_broken = false;  // a staging copy failed: none until resync
   int64_t stage_filled = 0, stage_h2d = 0, stage_hits = 0, stage_hit_bytes = 0;
+  std::vector<size_t> stage_row_bytes;  // per param: bytes of one row in its staging buffer
+  // coded host stores (sluice_layer_set_codec): the params coded, and the
+  // decode resources of the gap server serving the layer (nullptr: none)
+  uint32_t codec_mask = 0;
+  struct CodecRes* codec = nullptr;
+  std::vector<size_t> ring_off;  // a gap's streams: offset of each one's coded rows in the ring
+  std::vector<int64_t> use_id;   // and the ring use holding them (0: none)
+  std::vector<int> srow_of;      // and the staging row each one is served from (-1: none)
+  int64_t link_bytes = 0;        // bytes of served gaps' row copies over the link
+  int64_t decodes = 0, decodes_staged = 0;
 };
 
 namespace {
@@ -911,6 +957,122 @@ int drain_copies(sluice_layer* L) {
 }
 
 // ---------------------------------------------------------------------------
+// Decode of coded experts (sluice_layer_set_codec), under a gap server.
+// ---------------------------------------------------------------------------
+constexpr int kUsePending = 0, kUseLaunched = 1, kUseDead = 2;
+constexpr size_t kRingAlign = 256;
+size_t ring_round(size_t v) { return (v + kRingAlign - 1) & ~(kRingAlign - 1); }
+
+bool coded(const ParamRows& p) { return p.coded_base != nullptr; }
+
+bool has_coded(const sluice_layer* L) {
+  for (const ParamRows& p : L->params)
+    if (coded(p)) return true;
+  return false;
+}
+
+unsigned long long codec_done(const CodecRes* C) {
+  return __atomic_load_n(C->done_host, __ATOMIC_ACQUIRE);
+}
+
+// Wait (bounded) until job `seq` has completed.
+int codec_wait(const CodecRes* C, unsigned long long seq) {
+  const double t0 = now_s();
+  unsigned spins = 0;
+  while (codec_done(C) < seq) {
+    _mm_pause();
+    if ((++spins & 1023u) == 0 && now_s() - t0 > gap_timeout_s()) return SLUICE_E_TIMEOUT;
+  }
+  return SLUICE_OK;
+}
+
+void ring_reap(CodecRes* C) {
+  const unsigned long long done = codec_done(C);
+  while (!C->uses.empty()) {
+    const CodecRes::Use& u = C->uses.front();
+    if (u.state == kUseDead || (u.state == kUseLaunched && u.seq <= done)) C->uses.pop_front();
+    else break;
+  }
+  if (C->uses.empty()) C->head = 0;
+}
+
+// A ring region of len bytes after the live ones (their order is the
+// allocation order): its use id, or 0 while the live regions leave no room.
+int64_t ring_take(CodecRes* C, size_t len, size_t* off) {
+  ring_reap(C);
+  size_t at = 0;
+  if (C->uses.empty()) {
+    if (len > C->ring_bytes) return 0;
+  } else {
+    const size_t tail = C->uses.front().off;
+    if (C->head > tail) {  // live: [tail, head)
+      if (C->head + len <= C->ring_bytes) at = C->head;
+      else if (len <= tail) at = 0;
+      else return 0;
+    } else {  // live: [tail, end) and [0, head)
+      if (C->head + len <= tail) at = C->head;
+      else return 0;
+    }
+  }
+  C->uses.push_back({++C->next_use, at, len, 0, kUsePending});
+  C->head = at + len;
+  *off = at;
+  return C->next_use;
+}
+
+void ring_set(CodecRes* C, int64_t id, int state, unsigned long long seq) {
+  for (auto it = C->uses.rbegin(); it != C->uses.rend(); ++it)
+    if (it->id == id) {
+      it->state = state;
+      it->seq = seq;
+      return;
+    }
+}
+
+// Launch the decode of expert `local`'s coded rows into `slot`: from the
+// ring at `ring_at`, or from staging row `srow` (>= 0).  The job's last
+// workgroup marks the slot ready for gap `stamp`.  *seq: the job's number.
+int launch_decode(sluice_layer* L, CodecRes* C, int local, int slot, int srow, size_t ring_at,
+                  int32_t stamp, unsigned long long* seq) {
+  CodecJob job{};
+  size_t at = ring_at;
+  for (size_t pi = 0; pi < L->params.size(); ++pi) {
+    const ParamRows& p = L->params[pi];
+    if (!coded(p)) continue;
+    if (job.n_part == kCodecMaxParts) return SLUICE_E_STATE;
+    const size_t n = p.row_bytes / 2;
+    const char* src = srow >= 0 ? L->stage_dev[pi] + (size_t)srow * L->stage_row_bytes[pi]
+                                : C->ring + at;
+    job.part[job.n_part++] = {(const uint8_t*)src,
+                              (uint16_t*)(p.slot_base + (size_t)slot * p.row_bytes),
+                              (uint32_t)(n / kCodecGroup), codec_escapes(n, p.coded_len[local])};
+    at += ring_round(p.coded_len[local]);
+  }
+  job.wg_count = C->wg_count;
+  job.ready = &L->mb_dev->slot_ready[slot];
+  job.stamp = stamp;
+  job.done = C->done_dev;
+  job.seq = C->seq + 1;
+  const int rc = codec_dispatch(C->queue, job);
+  if (rc != SLUICE_OK) return rc == SLUICE_E_INVAL ? SLUICE_E_STATE : rc;
+  *seq = ++C->seq;
+  C->launched.store(C->seq, std::memory_order_release);
+  ++L->decodes;
+  if (srow >= 0) ++L->decodes_staged;
+  return SLUICE_OK;
+}
+
+// The bytes of expert `local`'s rows that cross the link: its coded rows
+// where the store is coded (under a server's decode), else the rows.
+size_t link_bytes_of(const sluice_layer* L, int local, bool use_codec) {
+  size_t b = 0;
+  for (const ParamRows& p : L->params)
+    if (p.rows_dev == nullptr)
+      b += use_codec && coded(p) ? (size_t)p.coded_len[local] : p.row_bytes;
+  return b;
+}
+
+// ---------------------------------------------------------------------------
 // Staging rows (L->mu held by the callers that other threads may race; the
 // gap server's own thread is the only one that issues staging copies).
 // ---------------------------------------------------------------------------
@@ -923,11 +1085,28 @@ int stage_ready_row(const sluice_layer* L, int local) {
   return -1;
 }
 
+// Bytes of expert `local` a staging row holds: its coded rows where the
+// store is coded, else its rows (the params the gap kernel pulls aside).
+size_t stage_total(const sluice_layer* L, int local) {
+  size_t b = 0;
+  for (size_t pi = 0; pi < L->params.size(); ++pi) {
+    if (L->stage_dev[pi] == nullptr) continue;
+    const ParamRows& p = L->params[pi];
+    b += coded(p) ? (size_t)p.coded_len[local] : p.row_bytes;
+  }
+  return b;
+}
+
 // A row still has bytes to copy.
 bool stage_has_copy(const sluice_layer* L) {
   for (const sluice_layer::StageRow& row : L->stage)
-    if (row.state == kStageCopying && row.issued < L->stage_bytes) return true;
+    if (row.state == kStageCopying && row.issued < stage_total(L, row.local)) return true;
   return false;
+}
+
+// A decode job still reads the row.
+bool stage_busy(const sluice_layer* L, const sluice_layer::StageRow& row) {
+  return L->codec != nullptr && row.busy_seq > codec_done(L->codec);
 }
 
 // Count the gap's selections: the staging candidates are the experts the
@@ -969,7 +1148,8 @@ void stage_poll(sluice_layer* L) {
     if (row.state == kStageEmpty && row.in_flight == 0) L->stage_dirty = true;  // free again
   }
   for (sluice_layer::StageRow& row : L->stage)
-    if (row.state == kStageCopying && row.in_flight == 0 && row.issued == L->stage_bytes) {
+    if (row.state == kStageCopying && row.in_flight == 0 &&
+        row.issued == stage_total(L, row.local)) {
       row.state = kStageReady;
       ++L->stage_filled;
     }
@@ -1014,7 +1194,7 @@ void stage_choose(sluice_layer* L) {
       row.state = kStageEmpty;
       row.local = -1;
     }
-    if (row.in_flight > 0) continue;  // its chunks still write the row
+    if (row.in_flight > 0 || stage_busy(L, row)) continue;  // still written, or read
     row.local = want[w];
     row.state = kStageCopying;
     row.issued = 0;
@@ -1027,7 +1207,7 @@ int stage_next_row(const sluice_layer* L) {
   int pick = -1;
   for (size_t r = 0; r < L->stage.size(); ++r) {
     const sluice_layer::StageRow& row = L->stage[r];
-    if (row.state != kStageCopying || row.issued >= L->stage_bytes) continue;
+    if (row.state != kStageCopying || row.issued >= stage_total(L, row.local)) continue;
     if (pick < 0 || L->sel_count[row.local] > L->sel_count[L->stage[pick].local]) pick = (int)r;
   }
   return pick;
@@ -1041,15 +1221,19 @@ bool stage_issue(sluice_layer* L, const DeviceRes* R, int l, int r) {
   for (size_t pi = 0; pi < L->params.size(); ++pi) {
     if (L->stage_dev[pi] == nullptr) continue;
     const ParamRows& p = L->params[pi];
-    if (row.issued >= base + p.row_bytes) {
-      base += p.row_bytes;
+    const bool cd = coded(p);
+    const size_t bytes = cd ? (size_t)p.coded_len[row.local] : p.row_bytes;
+    if (row.issued >= base + bytes) {
+      base += bytes;
       continue;
     }
     const size_t in = row.issued - base;
-    const size_t len = std::min(kStageChunk, p.row_bytes - in);
-    char* dst = L->stage_dev[pi] + (size_t)r * p.row_bytes + in;
-    const char* src = p.host_base + (size_t)row.local * p.row_bytes + in;
-    const hsa_agent_t from = p.host_agent.handle != 0 ? p.host_agent : R->cpu_agent;
+    const size_t len = std::min(kStageChunk, bytes - in);
+    char* dst = L->stage_dev[pi] + (size_t)r * L->stage_row_bytes[pi] + in;
+    const char* src = (cd ? p.coded_base + (size_t)row.local * p.coded_stride
+                          : p.host_base + (size_t)row.local * p.row_bytes) + in;
+    const hsa_agent_t agent = cd ? p.coded_agent : p.host_agent;
+    const hsa_agent_t from = agent.handle != 0 ? agent : R->cpu_agent;
     hsa_signal_store_relaxed(L->stage_sig[l], 1);
     if (hsa_amd_memory_async_copy_on_engine(dst, R->gpu_agent, src, from, len, 0, nullptr,
                                             L->stage_sig[l],
@@ -1090,8 +1274,26 @@ int stage_free(sluice_layer* L) {
       d = nullptr;
     }
   L->stage_dev.clear();
+  L->stage_row_bytes.clear();
   L->stage.clear();
   L->stage_bytes = 0;
+  return rc;
+}
+
+// Free the layer's coded host stores (L->mu held; no server serves it).
+int codec_free(sluice_layer* L) {
+  int rc = SLUICE_OK;
+  for (ParamRows& p : L->params) {
+    if (p.coded_base != nullptr) {
+      const hipError_t e = hipHostFree(p.coded_base);
+      if (e != hipSuccess) rc = (int)e;
+    }
+    p.coded_base = nullptr;
+    p.coded_stride = 0;
+    p.coded_len.clear();
+    p.coded_agent = {};
+  }
+  L->codec_mask = 0;
   return rc;
 }
 
@@ -1179,6 +1381,12 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     // before the raise; the device map is left as it was, answered after.)
     const bool early = waits && grc == 0 && rc == SLUICE_OK &&
                        g_pipelined.load(std::memory_order_relaxed) != 0;
+    // Coded stores are decoded only under a gap server that answers before
+    // the rows land (the server's decode resources): the coded rows cross
+    // the link into the server's ring in HBM and a decode job writes each
+    // expert's rows into its slot, its last workgroup marking the slot
+    // ready; otherwise every row streams as it is.
+    CodecRes* C = early && rc == SLUICE_OK ? L->codec : nullptr;
     // rows copied per expert (the gap kernel copies the pulled ones itself)
     int n_copy = 0;
     for (const ParamRows& p : L->params) n_copy += !(early && p.rows_dev != nullptr);
@@ -1187,9 +1395,11 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
     // rows land, and its copy (HBM to HBM) runs as a kernel of the runtime:
     // the host waits for those copies before it answers, so no kernel ever
     // waits for a copy that itself needs CUs (the device runs only the
-    // waiting gap kernel meanwhile).
+    // waiting gap kernel meanwhile).  Coded staged rows are decoded from the
+    // row itself.
     L->order.clear();
-    const bool from_stage = early && rc == SLUICE_OK && !L->stage.empty();
+    const bool from_stage = early && rc == SLUICE_OK && !L->stage.empty() &&
+                            (C != nullptr || !has_coded(L));
     if (from_stage)
       for (int i = 0; i < n_streams; ++i)
         if (stage_ready_row(L, L->streams[2 * i]) >= 0) L->order.push_back(i);
@@ -1203,6 +1413,9 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
       else L->fill_sig.push_back(sig);
     }
     L->sig_end.assign((size_t)n_streams, 0);
+    L->srow_of.assign((size_t)n_streams, -1);
+    L->ring_off.assign((size_t)n_streams, 0);
+    L->use_id.assign((size_t)n_streams, 0);
     int whole = 0;  // experts (in copy order) whose copies were all issued
     int armed = 0;  // copies issued, each with its own signal
     // One copy with its own completion signal (engine 0: the runtime's
@@ -1227,35 +1440,8 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
       L->armed_copies = ++armed;
       return true;
     };
-    // Issue the copies of the j-th expert in copy order.
-    auto issue = [&](int j) {
-      const int i = L->order[j];
-      const int local = L->streams[2 * i], slot = L->streams[2 * i + 1];
-      const int srow = j < n_staged ? stage_ready_row(L, local) : -1;
-      for (size_t pi = 0; rc == SLUICE_OK && pi < L->params.size(); ++pi) {
-        const ParamRows& p = L->params[pi];
-        L->bytes += (int64_t)p.row_bytes;
-        if (early && p.rows_dev != nullptr) continue;  // the gap kernel copies these rows itself
-        char* dst = p.slot_base + (size_t)slot * p.row_bytes;
-        if (srow >= 0)
-          copy(dst, L->stage_dev[pi] + (size_t)srow * p.row_bytes, R->gpu_agent, p.row_bytes, 0);
-        else
-          copy(dst, p.host_base + (size_t)local * p.row_bytes,
-               p.host_agent.handle != 0 ? p.host_agent : R->cpu_agent, p.row_bytes,
-               R->engine[p.lane]);
-        if (rc != SLUICE_OK) L->bytes -= (int64_t)p.row_bytes;
-        if (j == n_staged && pi == 0) SLUICE_HTRACE(23, L, want, n_staged);
-      }
-      L->sig_end[j] = armed;
-      if (rc != SLUICE_OK) return;
-      whole = j + 1;
-      if (srow >= 0) {
-        ++L->stage_hits;
-        L->stage_hit_bytes += (int64_t)L->stage_bytes;
-      }
-    };
-    // Wait for the j-th expert's copies (from signal *c on) and mark its
-    // slot ready for this gap.
+    // Wait for the j-th expert's copies (from signal *c on), then mark its
+    // slot ready for this gap, or launch the decode that marks it.
     auto land = [&](int j, int* c) {
       int w = SLUICE_OK;
       for (; *c < L->sig_end[j] && w == SLUICE_OK; ++*c) w = wait_signal(L->fill_sig[*c]);
@@ -1265,18 +1451,25 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
       }
       SLUICE_HTRACE(26, L, want, j);
       if (early) {
-        __atomic_store_n(&mb->slot_ready[L->streams[2 * L->order[j] + 1]], want, __ATOMIC_RELEASE);
+        const int i = L->order[j];
+        const int slot = L->streams[2 * i + 1];
+        if (C != nullptr) {
+          unsigned long long seq = 0;
+          const int srow = L->srow_of[j];
+          w = launch_decode(L, C, L->streams[2 * i], slot, srow, L->ring_off[j], want, &seq);
+          if (w != SLUICE_OK) {
+            if (rc == SLUICE_OK) rc = w;
+            return false;
+          }
+          if (L->use_id[j] != 0) ring_set(C, L->use_id[j], kUseLaunched, seq);
+          if (srow >= 0) L->stage[srow].busy_seq = seq;
+        } else {
+          __atomic_store_n(&mb->slot_ready[slot], want, __ATOMIC_RELEASE);
+        }
         SLUICE_HTRACE(27, L, want, j);
       }
       return true;
     };
-    // The link is the bottleneck of a missing step: the staged experts and
-    // the first expert over the link are queued, the staged ones landed,
-    // then the device is answered (its resident experts then compute while
-    // the rows stream), then the other experts queued.
-    int j = 0;
-    for (; rc == SLUICE_OK && j < n_staged; ++j) issue(j);
-    if (rc == SLUICE_OK && j < n_streams) issue(j++);
     int landed = 0, c = 0;  // experts in copy order whose copies completed, their slots marked
     bool landing = true;    // no wait failed
     auto land_upto = [&](int n) {
@@ -1285,6 +1478,83 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
         else landing = false;
       }
     };
+    // Room in the ring for the j-th expert's coded rows: while the live
+    // regions leave none, land the oldest expert still landing (which
+    // launches its decode), else wait for the oldest decode.
+    auto ring_room = [&](int j, size_t need) {
+      for (;;) {
+        const int64_t id = ring_take(C, need, &L->ring_off[j]);
+        if (id != 0) {
+          L->use_id[j] = id;
+          return true;
+        }
+        if (landed < whole) {
+          land_upto(landed + 1);
+          if (!landing) return false;
+          continue;
+        }
+        const CodecRes::Use& u = C->uses.front();
+        const int w = u.state == kUseLaunched ? codec_wait(C, u.seq) : SLUICE_E_STATE;
+        if (w != SLUICE_OK) {
+          if (rc == SLUICE_OK) rc = w;
+          return false;
+        }
+      }
+    };
+    // Issue the copies of the j-th expert in copy order.
+    auto issue = [&](int j) {
+      const int i = L->order[j];
+      const int local = L->streams[2 * i], slot = L->streams[2 * i + 1];
+      const int srow = j < n_staged ? stage_ready_row(L, local) : -1;
+      L->srow_of[j] = srow;
+      if (C != nullptr && srow < 0) {
+        size_t need = 0;
+        for (const ParamRows& p : L->params) need += coded(p) ? ring_round(p.coded_len[local]) : 0;
+        if (!ring_room(j, need)) return;
+      }
+      size_t at = L->ring_off[j];
+      for (size_t pi = 0; rc == SLUICE_OK && pi < L->params.size(); ++pi) {
+        const ParamRows& p = L->params[pi];
+        L->bytes += (int64_t)p.row_bytes;
+        if (early && p.rows_dev != nullptr) continue;  // the gap kernel copies these rows itself
+        if (C != nullptr && coded(p)) {
+          if (srow < 0) {
+            const size_t len = p.coded_len[local];
+            if (copy(C->ring + at, p.coded_base + (size_t)local * p.coded_stride,
+                     p.coded_agent.handle != 0 ? p.coded_agent : R->cpu_agent, len,
+                     R->engine[p.lane]))
+              L->link_bytes += (int64_t)len;
+            at += ring_round(len);
+          }
+        } else {
+          char* dst = p.slot_base + (size_t)slot * p.row_bytes;
+          if (srow >= 0) {
+            copy(dst, L->stage_dev[pi] + (size_t)srow * L->stage_row_bytes[pi], R->gpu_agent,
+                 p.row_bytes, 0);
+          } else if (copy(dst, p.host_base + (size_t)local * p.row_bytes,
+                          p.host_agent.handle != 0 ? p.host_agent : R->cpu_agent, p.row_bytes,
+                          R->engine[p.lane])) {
+            L->link_bytes += (int64_t)p.row_bytes;
+          }
+        }
+        if (rc != SLUICE_OK) L->bytes -= (int64_t)p.row_bytes;
+        if (j == n_staged && pi == 0) SLUICE_HTRACE(23, L, want, n_staged);
+      }
+      L->sig_end[j] = armed;
+      if (rc != SLUICE_OK) return;
+      whole = j + 1;
+      if (srow >= 0) {
+        ++L->stage_hits;
+        L->stage_hit_bytes += (int64_t)link_bytes_of(L, local, C != nullptr);
+      }
+    };
+    // The link is the bottleneck of a missing step: the staged experts and
+    // the first expert over the link are queued, the staged ones landed,
+    // then the device is answered (its resident experts then compute while
+    // the rows stream), then the other experts queued.
+    int j = 0;
+    for (; rc == SLUICE_OK && j < n_staged; ++j) issue(j);
+    if (rc == SLUICE_OK && j < n_streams) issue(j++);
     land_upto(std::min(whole, n_staged));
     // (a failure before the answer still answers the device: the map and
     // the fill list are the bookkeeping's; the slots are marked below)
@@ -1311,6 +1581,10 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
           __atomic_store_n(&mb->slot_ready[L->streams[2 * L->order[marked] + 1]], want,
                            __ATOMIC_RELEASE);
       for (int j = landed; j < n_streams; ++j) (void)L->c.unfill(L->streams[2 * L->order[j] + 1]);
+      // their ring regions are free once no copy writes them
+      if (C != nullptr && L->armed_copies == 0)
+        for (int j = landed; j < n_streams; ++j)
+          if (L->use_id[j] != 0) ring_set(C, L->use_id[j], kUseDead, 0);
     }
     if (early) {
       L->done_stamp.store(want, std::memory_order_release);
@@ -1371,7 +1645,77 @@ struct sluice_gap_server {
   sluice_layer* stage_lane[kStageLanes] = {};
   size_t cursor = 0;
   bool stage_quiet = false;
+  CodecRes* codec = nullptr;  // decode resources (layers with coded stores)
 };
+
+namespace {
+// Smallest ring for coded rows; it holds at least two of the largest coded
+// experts of the server's layers.
+constexpr size_t kRingMin = 128u << 20;
+
+int codec_res_destroy(CodecRes* C) {
+  if (C == nullptr) return SLUICE_OK;
+  int rc = SLUICE_OK;
+  auto keep = [&](hipError_t e) {
+    if (e != hipSuccess && rc == SLUICE_OK) rc = (int)e;
+  };
+  if (C->queue != nullptr) {
+    // no decode job outlives its ring
+    const int q = codec_sync(C->queue, gap_timeout_s());
+    if (q != SLUICE_OK && rc == SLUICE_OK) rc = q;
+  }
+  if (C->ring != nullptr) keep(hipFree(C->ring));
+  if (C->wg_count != nullptr) keep(hipFree(C->wg_count));
+  if (C->done_host != nullptr) keep(hipHostFree(C->done_host));
+  delete C;
+  return rc;
+}
+
+// Decode resources on `device` with a ring of at least 2 * `largest` bytes.
+int codec_res_create(int device, size_t largest, CodecRes** out) {
+  *out = nullptr;
+  int cur = 0;
+  SLUICE_HIP_CHECK(hipGetDevice(&cur));
+  if (cur != device) SLUICE_HIP_CHECK(hipSetDevice(device));
+  CodecRes* C = new (std::nothrow) CodecRes();
+  if (C == nullptr) {
+    if (cur != device) (void)hipSetDevice(cur);
+    return SLUICE_E_NOMEM;
+  }
+  C->device = device;
+  C->ring_bytes = std::max(kRingMin, 2 * largest);
+  DeviceRes* R = nullptr;
+  int qrc = device_res(device, &R);
+  if (qrc == SLUICE_OK) qrc = codec_queue(device, R->gpu_agent, R->cpu_agent, &C->queue);
+  if (qrc != SLUICE_OK) {
+    if (cur != device) (void)hipSetDevice(cur);
+    delete C;
+    return qrc;
+  }
+  hipError_t e = hipMalloc((void**)&C->wg_count, 256);
+  if (e == hipSuccess) e = hipMemset(C->wg_count, 0, 256);
+  void* h = nullptr;
+  if (e == hipSuccess)
+    e = hipHostMalloc(&h, 256, hipHostMallocCoherent | hipHostMallocMapped | hipHostMallocPortable);
+  if (e == hipSuccess) {
+    C->done_host = static_cast<unsigned long long*>(h);
+    *C->done_host = 0;
+    void* d = nullptr;
+    e = hipHostGetDevicePointer(&d, h, 0);
+    C->done_dev = static_cast<unsigned long long*>(d);
+  }
+  if (e == hipSuccess) e = hipMalloc((void**)&C->ring, C->ring_bytes);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (cur != device) (void)hipSetDevice(cur);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();  // reported here, not by the caller's next call
+    (void)codec_res_destroy(C);
+    return (int)e;
+  }
+  *out = C;
+  return SLUICE_OK;
+}
+}  // namespace
 
 // One staging step, on a sweep that found no record: take in the chunks
 // that landed, then put a chunk on each free staging lane, for the row
@@ -1497,6 +1841,10 @@ extern "C" int sluice_layer_destroy(sluice_layer* L) {
   for (hsa_signal_t sig : L->stage_sig)
     if (sig.handle != 0) (void)hsa_signal_destroy(sig);
   rc = stage_free(L);
+  {
+    const int crc = codec_free(L);
+    if (rc == SLUICE_OK) rc = crc;
+  }
   for (ParamRows& p : L->params)
     if (p.rows_dev != nullptr) {
       const hipError_t e = hipFree(p.rows_dev);
@@ -1550,6 +1898,7 @@ extern "C" int sluice_layer_add_param(sluice_layer* L, void* slot_base_dev, cons
   // A layer with a device copies these rows with the SDMA engines: both
   // ranges must be allocations the runtime knows, whole.
   if (!L->stage.empty()) return SLUICE_E_STATE;  // staging rows are laid out over the params
+  if (L->codec_mask != 0) return SLUICE_E_STATE;  // and the coded stores
   hsa_agent_t host_agent{};
   if (L->mb != nullptr &&
       (!known_range(host_base, row_bytes * (size_t)L->c.local_n, &host_agent) ||
@@ -1624,16 +1973,23 @@ extern "C" int sluice_layer_set_staging(sluice_layer* L, int rows) {
   for (hsa_signal_t& sig : L->stage_sig)
     if (sig.handle == 0 && hsa_signal_create(0, 0, nullptr, &sig) != HSA_STATUS_SUCCESS)
       return SLUICE_E_COPY;
-  // the params the gap copies (the pulled ones come from their HBM copy)
+  // the params the gap copies (the pulled ones come from their HBM copy),
+  // coded where the store is coded
   size_t bytes = 0;
-  for (const ParamRows& p : L->params) bytes += p.rows_dev == nullptr ? p.row_bytes : 0;
+  L->stage_row_bytes.assign(L->params.size(), 0);
+  for (size_t pi = 0; pi < L->params.size(); ++pi) {
+    const ParamRows& p = L->params[pi];
+    if (p.rows_dev != nullptr) continue;
+    L->stage_row_bytes[pi] = coded(p) ? p.coded_stride : p.row_bytes;
+    bytes += L->stage_row_bytes[pi];
+  }
   if (bytes == 0) return SLUICE_OK;  // nothing to stage
   L->stage_dev.assign(L->params.size(), nullptr);
   for (size_t pi = 0; pi < L->params.size(); ++pi) {
     const ParamRows& p = L->params[pi];
     if (p.rows_dev != nullptr) continue;
     void* d = nullptr;
-    const hipError_t e = hipMalloc(&d, p.row_bytes * (size_t)rows);
+    const hipError_t e = hipMalloc(&d, L->stage_row_bytes[pi] * (size_t)rows);
     if (e != hipSuccess) {
       (void)hipGetLastError();  // reported here, not by the caller's next call
       (void)stage_free(L);
@@ -1662,6 +2018,92 @@ extern "C" int sluice_layer_stage_counters(const sluice_layer* Lc, int64_t* coun
   counters[3] = L->stage_h2d;
   counters[4] = L->stage_hits;
   counters[5] = L->stage_hit_bytes;
+  return SLUICE_OK;
+}
+
+namespace {
+// f(i) for every i in [0, n), on up to 16 host threads.
+template <typename F>
+void parallel_for(int n, F f) {
+  const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+  const int nt = (int)std::min<unsigned>(std::min(hw, 16u), (unsigned)std::max(n, 1));
+  std::atomic<int> next{0};
+  auto work = [&] {
+    for (int i; (i = next.fetch_add(1, std::memory_order_relaxed)) < n;) f(i);
+  };
+  std::vector<std::thread> th;
+  for (int t = 1; t < nt; ++t) th.emplace_back(work);
+  work();
+  for (std::thread& t : th) t.join();
+}
+}  // namespace
+
+extern "C" int sluice_layer_set_codec(sluice_layer* L, uint32_t bf16_params) {
+  if (L == nullptr || L->mb == nullptr) return SLUICE_E_INVAL;
+  if (L->server != nullptr) return SLUICE_E_STATE;
+  std::lock_guard<std::mutex> lk(L->mu);
+  if (bf16_params == L->codec_mask) return SLUICE_OK;  // as set (a restarted server keeps them)
+  if (!L->stage.empty()) return SLUICE_E_STATE;        // staging rows are laid out over them
+  int rc = codec_free(L);
+  if (rc != SLUICE_OK || bf16_params == 0) return rc;
+  const int local_n = L->c.local_n;
+  int n_coded = 0;
+  for (size_t pi = 0; pi < L->params.size() && pi < 32; ++pi) {
+    ParamRows& p = L->params[pi];
+    const size_t n = p.row_bytes / 2;
+    if (!((bf16_params >> pi) & 1u) || p.rows_dev != nullptr || n_coded == kCodecMaxParts ||
+        p.row_bytes % (2 * kCodecChunk) != 0 || n / kCodecGroup > 0xffffffffu ||
+        ((uintptr_t)p.host_base & 1) != 0)
+      continue;
+    const uint16_t* rows = reinterpret_cast<const uint16_t*>(p.host_base);
+    std::vector<size_t> len((size_t)local_n);
+    parallel_for(local_n, [&](int e) { len[e] = codec_coded_bytes(rows + (size_t)e * n, n); });
+    const size_t mx = *std::max_element(len.begin(), len.end());
+    // rows that code poorly (more than ~1 exponent in 8 escaped) stream as they are
+    if (mx > p.row_bytes / 8 * 7 || mx > 0xffffffffu) continue;
+    const size_t stride = ring_round(mx);
+    void* buf = nullptr;
+    const hipError_t e = hipHostMalloc(&buf, stride * (size_t)local_n, hipHostMallocPortable);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();  // reported here, not by the caller's next call
+      (void)codec_free(L);
+      return (int)e;
+    }
+    parallel_for(local_n, [&](int x) {
+      codec_encode(rows + (size_t)x * n, n, static_cast<uint8_t*>(buf) + (size_t)x * stride);
+    });
+    p.coded_base = static_cast<char*>(buf);
+    p.coded_stride = stride;
+    p.coded_len.assign(len.begin(), len.end());
+    hsa_agent_t owner{};
+    hsa_device_type_t t{};
+    if (known_range(buf, stride * (size_t)local_n, &owner) &&
+        hsa_agent_get_info(owner, HSA_AGENT_INFO_DEVICE, &t) == HSA_STATUS_SUCCESS &&
+        t == HSA_DEVICE_TYPE_CPU)
+      p.coded_agent = owner;
+    ++n_coded;
+  }
+  L->codec_mask = bf16_params;
+  return SLUICE_OK;
+}
+
+extern "C" int sluice_layer_codec_counters(const sluice_layer* Lc, int64_t* counters) {
+  if (Lc == nullptr || counters == nullptr) return SLUICE_E_INVAL;
+  sluice_layer* L = const_cast<sluice_layer*>(Lc);
+  std::lock_guard<std::mutex> lk(L->mu);
+  int64_t n = 0, rows = 0, coded_all = 0;
+  for (const ParamRows& p : L->params) {
+    if (!coded(p)) continue;
+    ++n;
+    rows += (int64_t)p.row_bytes;
+    for (uint32_t b : p.coded_len) coded_all += b;
+  }
+  counters[0] = n;
+  counters[1] = rows;
+  counters[2] = coded_all;
+  counters[3] = L->link_bytes;
+  counters[4] = L->decodes;
+  counters[5] = L->decodes_staged;
   return SLUICE_OK;
 }
 
@@ -1720,11 +2162,37 @@ extern "C" int sluice_gap_server_create(sluice_layer* const* layers, int n_layer
   }
   S->fast_hit = fast_hit != 0;
   S->device = S->layers[0]->device;
-  for (sluice_layer* L : S->layers) L->server = S;
+  size_t largest = 0;  // coded rows of one expert, as they lie in the ring
+  bool any_coded = false;
+  for (sluice_layer* L : S->layers) {
+    std::lock_guard<std::mutex> lk(L->mu);
+    if (!has_coded(L)) continue;
+    any_coded = true;
+    for (int loc = 0; loc < L->c.local_n; ++loc) {
+      size_t b = 0;
+      for (const ParamRows& p : L->params) b += coded(p) ? ring_round(p.coded_len[loc]) : 0;
+      largest = std::max(largest, b);
+    }
+  }
+  if (any_coded) {
+    const int crc = codec_res_create(S->device, largest, &S->codec);
+    if (crc != SLUICE_OK) {
+      delete S;
+      return crc;
+    }
+  }
+  for (sluice_layer* L : S->layers) {
+    L->server = S;
+    L->codec = has_coded(L) ? S->codec : nullptr;
+  }
   try {
     S->th = std::thread(server_loop, S);
   } catch (...) {
-    for (sluice_layer* L : S->layers) L->server = nullptr;
+    for (sluice_layer* L : S->layers) {
+      L->server = nullptr;
+      L->codec = nullptr;
+    }
+    (void)codec_res_destroy(S->codec);
     delete S;
     return SLUICE_E_NOMEM;
   }
@@ -1752,6 +2220,14 @@ extern "C" int sluice_gap_server_drain(sluice_gap_server* S, double timeout_s) {
       _mm_pause();
     }
   }
+  // and the decodes those records launched
+  if (S->codec != nullptr) {
+    const unsigned long long seq = S->codec->launched.load(std::memory_order_acquire);
+    while (codec_done(S->codec) < seq) {
+      if (now_s() - t0 > timeout_s) return SLUICE_E_TIMEOUT;
+      _mm_pause();
+    }
+  }
   return S->error.load();
 }
 
@@ -1767,10 +2243,12 @@ extern "C" int sluice_gap_server_destroy(sluice_gap_server* S) {
     std::lock_guard<std::mutex> lk(L->mu);
     (void)stage_drain(L);  // no staging chunk outlives the server
     L->server = nullptr;
+    L->codec = nullptr;
   }
   const int err = S->error.load();
+  const int crc = codec_res_destroy(S->codec);  // waits for the decode jobs
   delete S;
-  return err;
+  return err != SLUICE_OK ? err : crc;
 }
 
 extern "C" int sluice_gap_set_timeout(double seconds) {
@@ -1979,6 +2457,7 @@ int issue_wave_copies(sluice_layer* L, int w, DeviceRes* R) {
                                       p.host_base + (size_t)local * p.row_bytes, p.row_bytes,
                                       hipMemcpyHostToDevice, R->copy[p.lane]));
       L->bytes += (int64_t)p.row_bytes;
+      L->link_bytes += (int64_t)p.row_bytes;
     }
   }
   return SLUICE_OK;

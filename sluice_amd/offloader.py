@@ -72,6 +72,12 @@ NO_STATIC_FULL_ENV = "SLUICE_NO_STATIC_FULL"
 # miss on one is copied into its slot from HBM).  0 turns staging off.
 STAGE_ROWS_ENV = "SLUICE_STAGE_ROWS"
 STAGE_ROWS_DEFAULT = 4
+# No counterpart in the reference: under the gap server, each router-split
+# layer's bf16 expert rows also get a losslessly coded host store (12 bits
+# per value plus rare escapes); misses copy the coded rows over the link and
+# a decode kernel writes the exact rows into the slot.  0 turns it off.
+CODEC_ENV = "SLUICE_CODEC"
+CODEC_DEFAULT = 0
 
 # Graph split points under piecewise capture: the MoE ops (whose apply runs
 # the classic hook, which syncs the host) and the gap op.
@@ -500,6 +506,7 @@ class ExpertStreamOffloader(_OffloaderBase):
         self.lfu = _env_flag(LFU_ENV)
         self.no_static_full = _env_flag(NO_STATIC_FULL_ENV)
         self.stage_rows = min(max(_env_number(STAGE_ROWS_ENV, STAGE_ROWS_DEFAULT, int), 0), 8)
+        self.codec = _env_number(CODEC_ENV, CODEC_DEFAULT, int) != 0
         self._caches: dict[int, _ExpertLayerCache] = {}
         self._layers: list[nn.Module] = []
         self._prepared_stores: dict[int, list] = {}  # pinned stores made before load
@@ -949,8 +956,16 @@ class ExpertStreamOffloader(_OffloaderBase):
             return
         lib = _lib.load()
         for c in self._rs_caches:
-            # staging only speeds the path up: without its rows (no copy
-            # engines free, no HBM left for them) the layer streams as before
+            # the coded store and staging only speed the path up: without
+            # them (no pinned memory, no copy engines free, no HBM left) the
+            # layer streams as before
+            if self.codec:
+                mask = sum(1 << i for i, n in enumerate(c.param_names)
+                           if c.gpu_cache[n].dtype == torch.bfloat16)
+                rc = lib.sluice_layer_set_codec(c.handle, mask)
+                if rc != 0:
+                    logger.warning("Sluice: layer %s streams uncoded rows (%s=1): %s",
+                                   c.layer_name or c.ordinal, CODEC_ENV, _lib.strerror(rc))
             rc = lib.sluice_layer_set_staging(c.handle, self.stage_rows)
             if rc != 0:
                 logger.warning("Sluice: layer %s runs without staging rows (%s=%d): %s",
@@ -1021,6 +1036,24 @@ class ExpertStreamOffloader(_OffloaderBase):
             _lib.check(lib.sluice_layer_stage_counters(c.handle, ctr), "sluice_layer_stage_counters")
             for i, k_ in enumerate(keys):
                 tot[k_] += ctr[i]
+        return tot
+
+    def codec_counters(self) -> dict:
+        """Coded host stores summed over the armed layers: params coded,
+        bytes of one expert's coded params as rows (summed over layers),
+        bytes of every local expert's coded rows and (store_bytes) of the
+        same rows uncoded, bytes of the slot fills' copies over the link
+        (coded or not), decode jobs, and those that decoded a staging row."""
+        lib = _lib.load()
+        keys = ("params", "row_bytes", "coded_bytes", "link_bytes", "decodes", "decodes_staged")
+        tot = dict.fromkeys(keys, 0)
+        tot["store_bytes"] = 0  # the coded params' rows of every local expert, uncoded
+        ctr = (ctypes.c_int64 * 6)()
+        for c in self._rs_caches:
+            _lib.check(lib.sluice_layer_codec_counters(c.handle, ctr), "sluice_layer_codec_counters")
+            for i, k_ in enumerate(keys):
+                tot[k_] += ctr[i]
+            tot["store_bytes"] += ctr[1] * c.local_num_experts
         return tot
 
     def get_gap_stats(self) -> dict:

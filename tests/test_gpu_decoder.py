@@ -324,11 +324,11 @@ def test_full_size_mixed_classic_and_gap_steps_follow_the_oracle():
         dec.close()
 
 
-@pytest.mark.parametrize("spec,layers,slots,c,steps", [("v2lite", None, 48, 8, 24),
-                                                     ("qwen3", None, 64, 8, 16),
-                                                     ("v3", 2, 64, 8, 8)])
+@pytest.mark.parametrize("spec,layers,slots,c,steps,coded", [
+    ("v2lite", None, 48, 8, 24, False), ("qwen3", None, 64, 8, 16, False),
+    ("v3", 2, 64, 8, 8, False), ("v2lite", 8, 48, 8, 24, True), ("qwen3", 8, 64, 8, 16, True)])
 def test_offloaded_decode_equals_fully_resident_decode(monkeypatch, spec, layers, slots, c,
-                                                       steps):
+                                                       steps, coded):
     """Streaming experts must not change the output (the reference's own
     correctness demo, examples/bitcompare_v2lite.py: greedy ids of an
     offloaded run diffed against an all-resident one).  The same seeded
@@ -339,7 +339,8 @@ def test_offloaded_decode_equals_fully_resident_decode(monkeypatch, spec, layers
     nothing streams); the next tokens of every step (the output rows' bits
     for the MoE stack without attention) are identical.  The streaming runs
     keep the default staging rows, and on V2-Lite and Qwen3 some of their
-    misses are copied from staged rows."""
+    misses are copied from staged rows.  Coded: the host stores coded
+    (SLUICE_CODEC=1), every miss decoded into its slot."""
     from sluice_amd.decoder import SyntheticDecoder
 
     def decode(n_slots):
@@ -356,12 +357,18 @@ def test_offloaded_decode_equals_fully_resident_decode(monkeypatch, spec, layers
             dec.sync()
             streamed = dec.gap_counters()["misses"]
             staged = dec.off.stage_counters()["hits"]
+            if coded and n_slots < E:
+                cc = dec.off.codec_counters()
+                print(f"  codec {cc}", flush=True)
+                assert cc["params"] > 0 and cc["decodes"] == streamed
             return torch.stack(out).cpu().numpy(), streamed, staged
         finally:
             dec.close()
 
     E = __import__("sluice_amd.decoder", fromlist=["SPECS"]).SPECS[spec]["E"]
-    print(f"bitcompare {spec} slots {slots} vs {E}, c={c}, {steps} steps", flush=True)
+    print(f"bitcompare {spec} slots {slots} vs {E}, c={c}, {steps} steps, coded={coded}",
+          flush=True)
+    monkeypatch.setenv("SLUICE_CODEC", "1" if coded else "0")
     off, misses, staged = decode(slots)
     print(f"  misses {misses}, from staged rows {staged}", flush=True)
     monkeypatch.setenv("SLUICE_NO_STATIC_FULL", "1")

@@ -287,7 +287,9 @@ def test_device_gap_v3_fp8_streams_four_rows_per_miss(monkeypatch, slru_golden, 
 
 _STAGED_CASES = [("v2lite_zipf", True, "bf16"), ("qwen3_s64_zipf", True, "bf16"),
                  ("ep_half_owned", False, "bf16"), ("pinned", True, "bf16"),
-                 ("v3_s64_zipf", True, "fp8")]
+                 ("v3_s64_zipf", True, "fp8"), ("v2lite_zipf", True, "bf16-coded"),
+                 ("qwen3_s64_zipf", True, "bf16-coded"), ("ep_half_owned", False, "bf16-coded"),
+                 ("pinned", True, "bf16-coded")]
 
 
 @pytest.mark.parametrize("name,fast_hit,kind", _STAGED_CASES,
@@ -303,7 +305,9 @@ def test_staged_rows_leave_the_golden_replay_unchanged(monkeypatch, slru_golden,
     filled stay misses x expert bytes, and on the Zipf traces some misses
     were served from staged rows.  bf16 rows of 2 MB and 1 MB (two and one
     staging chunks); fp8: the w13 and w2 rows staged, the scale rows pulled
-    by the gap kernel."""
+    by the gap kernel.  bf16-coded: the host stores coded, every miss
+    decoded into its slot (from the ring or from its staging row), fewer
+    bytes over the link."""
     import time
 
     from sluice_amd import _lib
@@ -311,6 +315,7 @@ def test_staged_rows_leave_the_golden_replay_unchanged(monkeypatch, slru_golden,
     case = [c for c in slru_golden["cases"] if c["name"] == name and c["fast_hit"] == fast_hit][0]
     print(f"staged gap case {name} fast_hit={fast_hit} {kind}", flush=True)
     monkeypatch.setenv("SLUICE_STAGE_ROWS", "2")
+    monkeypatch.setenv("SLUICE_CODEC", "1" if kind == "bf16-coded" else "0")
     E, local_n, k = case["E"], case["local_n"], case["k"]
     emap = None
     if case["local_of"] is not None:
@@ -355,6 +360,18 @@ def test_staged_rows_leave_the_golden_replay_unchanged(monkeypatch, slru_golden,
     assert sc["hits"] <= s["misses"]
     if "zipf" in name:
         assert sc["hits"] > 0
+    cc = off.codec_counters()
+    print(f"codec: {cc}", flush=True)
+    # the rows that cross the link (fp8: the scale rows are pulled by the gap kernel)
+    row_bytes = sum(cache.gpu_cache[n][0].nbytes for n in cache.param_names if "scale" not in n)
+    over_link = (s["misses"] - sc["hits"]) * row_bytes
+    if kind == "bf16-coded":
+        assert cc["params"] == 2 and cc["decodes"] == s["misses"]
+        assert cc["decodes_staged"] == sc["hits"]
+        assert 0.7 * over_link < cc["link_bytes"] < 0.8 * over_link
+    else:
+        assert cc["params"] == 0 and cc["decodes"] == 0
+        assert cc["link_bytes"] == over_link
     off.close()
 
 
@@ -676,7 +693,8 @@ def test_failed_stream_in_drops_unlanded_fills_and_resync_installs_host_map(monk
     off.close()
 
 
-def test_failed_stream_in_with_staged_misses_keeps_what_landed(monkeypatch):
+@pytest.mark.parametrize("coded", [False, True], ids=["rows", "coded"])
+def test_failed_stream_in_with_staged_misses_keeps_what_landed(monkeypatch, coded):
     """Failure handling with staged rows, forced from the host.  Under the
     gap server with four staging rows and a plain LRU (no protected
     segment), eight experts X are selected four times, then evicted by
@@ -684,7 +702,8 @@ def test_failed_stream_in_with_staged_misses_keeps_what_landed(monkeypatch):
     not hold, and the four lowest ids of X get staged.  A gap selecting X
     copies those four from HBM first, then the other four over the link;
     the 10th row copy (the second of the first expert over the link) is
-    made to fail.  The gap reports the error, the four staged experts were
+    made to fail.  Coded: the staged experts are decoded from their rows
+    (no copies), so the 2nd row copy is the one that fails.  The gap reports the error, the four staged experts were
     served from their rows and stay cached with their host rows, the other
     four leave the slot cache; after reset_gaps later gaps follow the
     oracle with the same drops."""
@@ -694,8 +713,9 @@ def test_failed_stream_in_with_staged_misses_keeps_what_landed(monkeypatch):
     from sluice_amd import _lib
 
     E, S, k, H, I = 32, 16, 4, 2048, 768
-    print("failed stream-in with staged misses", flush=True)
+    print(f"failed stream-in with staged misses coded={coded}", flush=True)
     monkeypatch.setenv("SLUICE_STAGE_ROWS", "4")
+    monkeypatch.setenv("SLUICE_CODEC", "1" if coded else "0")
     layer = _Layer(E, E, H=H, I=I)
     off = _offloader(monkeypatch, S, 0.0, False)
     off.wrap_modules(iter([layer]))
@@ -731,7 +751,7 @@ def test_failed_stream_in_with_staged_misses_keeps_what_landed(monkeypatch):
     while off.stage_counters()["ready"] < 4 and time.monotonic() - t0 < 5.0:
         time.sleep(0.001)
     assert off.stage_counters()["ready"] == 4
-    assert lib.sluice_gap_inject_copy_failure(9) == 0
+    assert lib.sluice_gap_inject_copy_failure(1 if coded else 9) == 0
     try:
         with pytest.raises(RuntimeError):
             gap(np.sort(x))
@@ -743,6 +763,8 @@ def test_failed_stream_in_with_staged_misses_keeps_what_landed(monkeypatch):
         assert oracle.unfill(slot)
     check_state()
     assert off.stage_counters()["hits"] == 4
+    if coded:
+        assert off.codec_counters()["decodes_staged"] == 4
     off.reset_gaps()
     oracle.map, oracle.map_is_standing = oracle.standing_map(), True
     assert cache.expert_map_buf.cpu().tolist() == oracle.map
