@@ -26,7 +26,6 @@
 #include <stdint.h>
 
 constexpr size_t kCodecChunk = 2048;   // values per base exponent
-constexpr int kCodecGroup = 16;        // values a decoding lane handles at once
 constexpr int kCodecMaxParts = 4;      // coded rows one decode job writes
 constexpr uint32_t kCodecEscape = 15;  // nibble of an exponent outside the window
 constexpr int kCodecThreads = 256;     // threads of a decode workgroup
@@ -41,13 +40,13 @@ __host__ __device__ inline size_t codec_esc_off(size_t n) {
   return codec_esc_off_off(n) + 4 * (n / kCodecChunk + 1);
 }
 
-// One row to decode: n16 groups of kCodecGroup values from src (a coded row
-// in device memory holding n_esc escapes) to dst (n16 * kCodecGroup bf16
-// values).
+// One row to decode: n_chunk chunks of kCodecChunk values from src (a coded
+// row in device memory holding n_esc escapes) to dst (n_chunk *
+// kCodecChunk bf16 values).
 struct CodecPart {
   const uint8_t* src;
   uint16_t* dst;
-  uint32_t n16;
+  uint32_t n_chunk;
   uint32_t n_esc;
 };
 

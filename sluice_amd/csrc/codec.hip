@@ -246,12 +246,12 @@ int codec_queue(int device, hsa_agent_t gpu, hsa_agent_t cpu, CodecQueue** out) 
 
 int codec_dispatch(CodecQueue* Q, CodecJob& job) {
   size_t total = 0;
-  for (int p = 0; p < job.n_part; ++p) total += job.part[p].n16;
+  for (int p = 0; p < job.n_part; ++p) total += job.part[p].n_chunk;
   if (Q == nullptr || job.n_part <= 0 || job.n_part > kCodecMaxParts || total == 0 ||
       total > 0xffffffffu || job.wg_count == nullptr)
     return SLUICE_E_INVAL;
-  const size_t per_wg = (size_t)kCodecThreads * 4;
-  job.n_wg = (uint32_t)std::min<size_t>((total + per_wg - 1) / per_wg, kCodecMaxGrid);
+  // a workgroup decodes 4 chunks per round
+  job.n_wg = (uint32_t)std::min<size_t>((total + 3) / 4, kCodecMaxGrid);
   std::lock_guard<std::mutex> lk(Q->mu);
   if (Q->error.load() != 0) return Q->error.load();
   const int slot = (int)(Q->n % kArgSlots);
@@ -339,7 +339,7 @@ extern "C" int sluice_codec_encode(const void* rows, size_t n, void* out, size_t
 extern "C" int sluice_codec_decode(const void* coded_dev, size_t n, size_t coded_bytes,
                                    void* out_dev, sluice_stream_t stream) {
   if (coded_dev == nullptr || out_dev == nullptr || n == 0 || n % kCodecChunk != 0 ||
-      n / kCodecGroup > 0xffffffffu || coded_bytes < codec_esc_off(n) ||
+      n / kCodecChunk > 0xffffffffu || coded_bytes < codec_esc_off(n) ||
       (coded_bytes - codec_esc_off(n)) % 4 != 0 || ((uintptr_t)coded_dev & 15) != 0 ||
       ((uintptr_t)out_dev & 15) != 0)
     return SLUICE_E_INVAL;
@@ -367,7 +367,7 @@ extern "C" int sluice_codec_decode(const void* coded_dev, size_t n, size_t coded
   if (rc == SLUICE_OK) {
     CodecJob job{};
     job.part[0] = {static_cast<const uint8_t*>(coded_dev), static_cast<uint16_t*>(out_dev),
-                   (uint32_t)(n / kCodecGroup), codec_escapes(n, coded_bytes)};
+                   (uint32_t)(n / kCodecChunk), codec_escapes(n, coded_bytes)};
     job.n_part = 1;
     job.wg_count = count;
     rc = codec_dispatch(Q, job);

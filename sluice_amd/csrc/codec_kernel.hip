@@ -4,9 +4,10 @@
 // product that waits for a decoded slot may hold an in-order hardware queue
 // that HIP streams share, and a decode queued behind it would never run.
 //
-// The decode is byte work bound by HBM: each lane reads 16 sign/mantissa
-// bytes and 8 nibble bytes (coalesced across the wave) and writes 32 bytes
-// of bf16; a chunk's base exponent is one byte per 2048 values.  The kernel
+// The decode is byte work bound by HBM: per chunk of 2048 values each lane
+// reads 8 sign/mantissa bytes and 4 nibble bytes (coalesced across the
+// wave) and writes 16 bytes of bf16; the chunk's base exponent and escape
+// offsets are one scalar load each.  The kernel
 // allocates few registers and no LDS, so that it fits beside the expert
 // product's waiting workgroups (sluice_amd/build.py checks its registers),
 // and reads no implicit kernel arguments (the grid size is in the job), so
@@ -16,111 +17,119 @@
 
 namespace {
 
-constexpr uint32_t kGroupsPerChunk = kCodecChunk / kCodecGroup;
+constexpr int kCodecUnroll = 4;  // chunks a workgroup decodes per round
+static_assert(kCodecChunk == 8 * kCodecThreads, "a lane decodes 8 values of a chunk");
 
-// The exponent of value `pos` of chunk `chunk` from the escape list (0 if it
-// is not listed: a damaged row decodes wrongly but reads nothing outside it).
-__device__ __forceinline__ uint32_t escaped_exponent(const uint8_t* src, size_t n, uint32_t n_esc,
-                                                     uint32_t chunk, uint32_t pos) {
-  const uint32_t* off = reinterpret_cast<const uint32_t*>(src + codec_esc_off_off(n));
-  const uint32_t* esc = reinterpret_cast<const uint32_t*>(src + codec_esc_off(n));
-  uint32_t lo = min(off[chunk], n_esc), hi = min(off[chunk + 1], n_esc);
-  while (lo < hi) {
-    const uint32_t mid = (lo + hi) >> 1;
-    const uint32_t e = esc[mid], p = e >> 8;
-    if (p == pos) return e & 0xffu;
-    if (p < pos) lo = mid + 1;
-    else hi = mid;
-  }
-  return 0;
-}
-
-// Nibbles equal to kCodecEscape: bit 4i set for nibble i.
-__device__ __forceinline__ uint32_t escape_bits(uint32_t v) {
-  return v & (v >> 1) & (v >> 2) & (v >> 3) & 0x11111111u;
+// Device-coherent stores (written through the L2 of this XCD to memory):
+// the decoded rows are read by workgroups on every XCD, and with coherent
+// stores no wave has to write back a whole L2 before the slot is marked.
+__device__ __forceinline__ void st16_coh(void* p, const u32x4_t& v) {
+  uint64_t* q = static_cast<uint64_t*>(p);
+  __hip_atomic_store(q, (uint64_t)v[0] | (uint64_t)v[1] << 32, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(q + 1, (uint64_t)v[2] | (uint64_t)v[3] << 32, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(kCodecThreads) void sluice_codec_decode_kernel(CodecJob job) {
+  // A workgroup decodes kCodecUnroll chunks of 2048 values per round, each
+  // lane 8 values of each; the chunk, its part and its base exponent are the
+  // same for the whole workgroup (scalar loads).  After the round's stores,
+  // the escapes of its chunks are patched in parallel, one lane per entry.
   uint32_t total = 0;
 #pragma unroll
-  for (int q = 0; q < kCodecMaxParts; ++q) total += q < job.n_part ? job.part[q].n16 : 0u;
+  for (int q = 0; q < kCodecMaxParts; ++q) total += q < job.n_part ? job.part[q].n_chunk : 0u;
   const uint32_t tid = __builtin_amdgcn_workitem_id_x();
-  const uint32_t stride = job.n_wg * kCodecThreads;
-  for (uint32_t g = __builtin_amdgcn_workgroup_id_x() * kCodecThreads + tid; g < total;
-       g += stride) {
-    // The part holding group g.  A wave's 64 groups are consecutive from a
-    // multiple of 64 and every part is a multiple of 128 groups, so the
-    // wave's first group decides for all of its lanes (the part stays in
-    // scalar registers; static indices keep the job out of memory).
-    const uint32_t g0 = __builtin_amdgcn_readfirstlane(g);
-    uint32_t first = 0;
-    CodecPart pt = job.part[0];
+  const uint32_t wg = __builtin_amdgcn_workgroup_id_x();
+  for (uint32_t c0 = wg * kCodecUnroll; c0 < total; c0 += job.n_wg * kCodecUnroll) {
+    const uint8_t* src[kCodecUnroll];
+    uint16_t* dst[kCodecUnroll];
+    uint32_t loc[kCodecUnroll], nchk[kCodecUnroll], n_esc[kCodecUnroll];
+    u32x2_t sm[kCodecUnroll];
+    uint32_t nb[kCodecUnroll], base[kCodecUnroll];
 #pragma unroll
-    for (int q = 1; q < kCodecMaxParts; ++q)
-      if (q < job.n_part && g0 - first >= pt.n16) {
-        first += pt.n16;
-        pt = job.part[q];
-      }
-    const uint32_t loc = g - first;
-    const size_t n = (size_t)pt.n16 * kCodecGroup;
-    const u32x4_t sm = __builtin_nontemporal_load(
-        reinterpret_cast<const u32x4_t*>(pt.src + (size_t)loc * kCodecGroup));
-    const u32x2_t nb = __builtin_nontemporal_load(
-        reinterpret_cast<const u32x2_t*>(pt.src + n + (size_t)loc * (kCodecGroup / 2)));
-    const uint32_t chunk = loc / kGroupsPerChunk;
-    const uint32_t base = pt.src[codec_base_off(n) + chunk];
-    uint16_t* dst = pt.dst + (size_t)loc * kCodecGroup;
-    // Two values per 32-bit word, lane-parallel within the word: value 2p
-    // in the low half, 2p + 1 in the high half.  The sign/mantissa bytes
-    // and the byte of nibbles of pair p are placed at bytes 0 and 2 by byte
-    // permutes (selector 0x0c gives a zero byte).
-    const uint32_t base2 = base | base << 16;
+    for (int u = 0; u < kCodecUnroll; ++u) {
+      // the part holding chunk c (static indices: the job stays in registers)
+      const uint32_t c = min(c0 + u, total - 1);
+      uint32_t first = 0;
+      CodecPart pt = job.part[0];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+      for (int q = 1; q < kCodecMaxParts; ++q)
+        if (q < job.n_part && c - first >= pt.n_chunk) {
+          first += pt.n_chunk;
+          pt = job.part[q];
+        }
+      loc[u] = c - first;
+      nchk[u] = pt.n_chunk;
+      n_esc[u] = pt.n_esc;
+      src[u] = pt.src;
+      dst[u] = pt.dst + (size_t)loc[u] * kCodecChunk + 8 * tid;
+      const size_t n = (size_t)pt.n_chunk * kCodecChunk;
+      sm[u] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x2_t*>(pt.src + (size_t)loc[u] * kCodecChunk + 8 * tid));
+      nb[u] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(
+          pt.src + n + (size_t)loc[u] * (kCodecChunk / 2) + 4 * tid));
+      base[u] = pt.src[codec_base_off(n) + loc[u]];
+    }
+#pragma unroll
+    for (int u = 0; u < kCodecUnroll; ++u) {
+      if (c0 + u >= total) break;
+      // Two values per 32-bit word, lane-parallel within the word: value 2p
+      // in the low half, 2p + 1 in the high half.  The sign/mantissa bytes
+      // and the byte of nibbles of pair p are placed at bytes 0 and 2 by
+      // byte permutes (selector 0x0c gives a zero byte).
+      const uint32_t base2 = base[u] | base[u] << 16;
       uint32_t out[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int pr = 4 * h + k;  // pair: values 2 pr, 2 pr + 1
-        const uint32_t b0 = (uint32_t)(2 * pr) & 3u, nbyte = (uint32_t)pr & 3u;
-        const uint32_t t = __builtin_amdgcn_perm(0u, sm[pr >> 1],
+        const uint32_t b0 = (uint32_t)(2 * k) & 3u;
+        const uint32_t t = __builtin_amdgcn_perm(0u, sm[u][k >> 1],
                                                  b0 | 0x0c00u | (b0 + 1) << 16 | 0x0c000000u);
-        const uint32_t x = __builtin_amdgcn_perm(0u, nb[pr >> 2],
-                                                 nbyte | 0x0c00u | nbyte << 16 | 0x0c000000u);
+        const uint32_t x = __builtin_amdgcn_perm(0u, nb[u],
+                                                 (uint32_t)k | 0x0c00u | (uint32_t)k << 16 |
+                                                     0x0c000000u);
         const uint32_t ex = ((((x & 0x00f00000u) >> 4) | (x & 0xfu)) + base2) & 0x00ff00ffu;
         out[k] = ((t & 0x00800080u) << 8) | (t & 0x007f007fu) | (ex << 7);
       }
-      reinterpret_cast<u32x4_t*>(dst)[h] = u32x4_t{out[0], out[1], out[2], out[3]};
+      st16_coh(dst[u], u32x4_t{out[0], out[1], out[2], out[3]});
     }
-    // Escaped exponents (about 1 value in 6000 of a N(0, 0.02) row): the
-    // value is stored again, after the group's stores, by the same lane.
-    const uint32_t m0 = escape_bits(nb[0]), m1 = escape_bits(nb[1]);
-    if ((m0 | m1) != 0) {
-#pragma nounroll
-      for (int i = 0; i < kCodecGroup; ++i) {
-        if ((((i < 8 ? m0 : m1) >> (4 * (i & 7))) & 1u) == 0) continue;
-        const uint32_t s = pt.src[(size_t)loc * kCodecGroup + i];
-        const uint32_t e = escaped_exponent(pt.src, n, pt.n_esc, chunk,
-                                            (loc % kGroupsPerChunk) * kCodecGroup + (uint32_t)i);
-        dst[i] = (uint16_t)(((s & 0x80u) << 8) | (e << 7) | (s & 0x7fu));
+    // Escapes (about 1 value in 6000 of a N(0, 0.02) row, a few per round):
+    // stored again over the values above once every lane's stores completed.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kCodecUnroll; ++u) {
+      if (c0 + u >= total) break;
+      const size_t n = (size_t)nchk[u] * kCodecChunk;
+      const uint32_t* off = reinterpret_cast<const uint32_t*>(src[u] + codec_esc_off_off(n));
+      const uint32_t* esc = reinterpret_cast<const uint32_t*>(src[u] + codec_esc_off(n));
+      const uint32_t e0 = min(off[loc[u]], n_esc[u]), e1 = min(off[loc[u] + 1], n_esc[u]);
+      for (uint32_t e = e0 + tid; e < e1; e += kCodecThreads) {
+        const uint32_t ent = esc[e], pos = (ent >> 8) & (uint32_t)(kCodecChunk - 1);
+        const uint32_t sb = src[u][(size_t)loc[u] * kCodecChunk + pos];
+        uint16_t* d = dst[u] - 8 * tid + pos;
+        __hip_atomic_store(d, (uint16_t)(((sb & 0x80u) << 8) | ((ent & 0xffu) << 7) | (sb & 0x7fu)),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
-  // Every lane's stores are released at device scope before its workgroup
-  // counts itself; the last workgroup to count publishes the job.
-  __threadfence();
+  // Every lane's coherent stores have completed (reached memory) before its
+  // workgroup counts itself; the last workgroup to count publishes the job.
+  // The readers take a system-scope acquire (an L2 invalidate) after they
+  // see the mark, so no write-back is needed here.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(job.wg_count, 1u, __ATOMIC_ACQ_REL,
+    const uint32_t prev = __hip_atomic_fetch_add(job.wg_count, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
     if (prev == job.n_wg - 1) {
       __hip_atomic_store(job.wg_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (job.ready != nullptr)
-        __hip_atomic_store(job.ready, job.stamp, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(job.ready, job.stamp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       if (job.done != nullptr)
-        __hip_atomic_store(job.done, job.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(job.done, job.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
   }
 }
-

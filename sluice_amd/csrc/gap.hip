@@ -1045,7 +1045,7 @@ int launch_decode(sluice_layer* L, CodecRes* C, int local, int slot, int srow, s
                                 : C->ring + at;
     job.part[job.n_part++] = {(const uint8_t*)src,
                               (uint16_t*)(p.slot_base + (size_t)slot * p.row_bytes),
-                              (uint32_t)(n / kCodecGroup), codec_escapes(n, p.coded_len[local])};
+                              (uint32_t)(n / kCodecChunk), codec_escapes(n, p.coded_len[local])};
     at += ring_round(p.coded_len[local]);
   }
   job.wg_count = C->wg_count;
@@ -2052,7 +2052,7 @@ extern "C" int sluice_layer_set_codec(sluice_layer* L, uint32_t bf16_params) {
     ParamRows& p = L->params[pi];
     const size_t n = p.row_bytes / 2;
     if (!((bf16_params >> pi) & 1u) || p.rows_dev != nullptr || n_coded == kCodecMaxParts ||
-        p.row_bytes % (2 * kCodecChunk) != 0 || n / kCodecGroup > 0xffffffffu ||
+        p.row_bytes % (2 * kCodecChunk) != 0 || n / kCodecChunk > 0xffffffffu ||
         ((uintptr_t)p.host_base & 1) != 0)
       continue;
     const uint16_t* rows = reinterpret_cast<const uint16_t*>(p.host_base);
