@@ -206,7 +206,7 @@ def run_batch(dec, c, steps, warmup, prefill=True, label=None):
                    "hit_share_of_misses": sdelta["hits"] / max(delta["misses"], 1),
                    "rows_filled": sdelta["filled"],
                    "staging_h2d_bytes_per_step": sdelta["h2d_bytes"] / steps},
-        "coded": {"params_per_layer": codec1["params"] // max(n_moe, 1),
+        "coded": {"layers": codec1["layers"], "of_layers": n_moe,
                   "store_ratio": codec1["coded_bytes"] / max(codec1["store_bytes"], 1),
                   "decodes": codec1["decodes"] - codec0["decodes"],
                   "fill_link_bytes_per_step": link / steps},
@@ -898,7 +898,7 @@ def full_record(a, cfg, sp, slots, batches, gen_len, head, extras, cpu):
 # columns of the compact line's batch rows
 ROW_COLS = ["shape", "slots", "c", "path", "routing", "steps", "ms_per_step", "tok_per_s",
             "misses_per_layer_step", "fast_hit_share", "staged_share_of_misses",
-            "h2d_GBs_in_step", "ref_tok_per_s"]
+            "coded_layers", "h2d_GBs_in_step", "ref_tok_per_s"]
 LINE_LIMIT = 6000  # bytes; the last stdout line must stay whole in a short tail
 
 
@@ -935,6 +935,7 @@ def compact_line(rec):
                          _r(r["tok_per_s"], 1), _r(r["misses_per_layer_step"], 3),
                          _r(r["fast_hit_share"], 3),
                          _r((r.get("staged") or {}).get("hit_share_of_misses"), 3),
+                         (r.get("coded") or {}).get("layers"),
                          _r(r["h2d_GBs_in_step"], 1), ref])
         if k1:
             key = f"{shape}/s{slots}/c{k1['c']}"
@@ -949,6 +950,7 @@ def compact_line(rec):
                                                                               "matched")]
     in_step = head_rows[0]["h2d_GBs_in_step"] if head_rows else None
     staging = (head_rows[0].get("staged") or {}).get("rows_per_layer") if head_rows else None
+    coded = (head_rows[0].get("coded") or {}) if head_rows else {}
     line = {
         "metric": rec["metric"], "value": _r(rec["value"], 2), "unit": rec["unit"],
         "n_gpus": rec["n_gpus"], "steps": rec["steps"], "warmup": rec["warmup"],
@@ -962,7 +964,10 @@ def compact_line(rec):
                    "routing": {k: c["routing"][k] for k in ("zipf_s", "rho", "sigma", "gate_std")
                                if k in c["routing"]},
                    "baseline_ref": c.get("baseline_ref"),
-                   "staging_rows_per_layer": staging},
+                   "staging_rows_per_layer": staging,
+                   "coded_store": {"layers": coded.get("layers"), "of_layers": coded.get("of_layers"),
+                                   "bytes_frac": _r(coded.get("store_ratio"), 4)}
+                   if coded else None},
         "roofline": {"bound": roof["bound"], "achieved": _r(roof["achieved"], 1),
                      "peak": roof["peak"], "unit": roof["unit"], "frac": _r(roof["frac"], 4),
                      "traffic": roof["traffic"], "kernel": roof["kernel"],

@@ -1280,13 +1280,37 @@ int stage_free(sluice_layer* L) {
   return rc;
 }
 
+// Coded stores by the host rows they code: layers that stream from the
+// same host rows (one host pool shared by several layers) share one coded
+// store, freed with its last user.
+struct CodedStore {
+  const char* host_base;
+  size_t row_bytes;
+  int local_n;
+  char* base;
+  size_t stride;
+  std::vector<uint32_t> len;
+  hsa_agent_t agent;
+  int users;
+};
+std::mutex g_coded_mu;
+std::vector<CodedStore*> g_coded;
+
 // Free the layer's coded host stores (L->mu held; no server serves it).
 int codec_free(sluice_layer* L) {
   int rc = SLUICE_OK;
+  std::lock_guard<std::mutex> lk(g_coded_mu);
   for (ParamRows& p : L->params) {
     if (p.coded_base != nullptr) {
-      const hipError_t e = hipHostFree(p.coded_base);
-      if (e != hipSuccess) rc = (int)e;
+      for (size_t i = 0; i < g_coded.size(); ++i) {
+        CodedStore* cs = g_coded[i];
+        if (cs->base != p.coded_base || --cs->users > 0) continue;
+        const hipError_t e = hipHostFree(cs->base);
+        if (e != hipSuccess) rc = (int)e;
+        delete cs;
+        g_coded.erase(g_coded.begin() + (long)i);
+        break;
+      }
     }
     p.coded_base = nullptr;
     p.coded_stride = 0;
@@ -2055,6 +2079,23 @@ extern "C" int sluice_layer_set_codec(sluice_layer* L, uint32_t bf16_params) {
         p.row_bytes % (2 * kCodecChunk) != 0 || n / kCodecChunk > 0xffffffffu ||
         ((uintptr_t)p.host_base & 1) != 0)
       continue;
+    {  // the same host rows coded for another layer already
+      std::lock_guard<std::mutex> lk2(g_coded_mu);
+      CodedStore* hit = nullptr;
+      for (CodedStore* cs : g_coded)
+        if (cs->host_base == p.host_base && cs->row_bytes == p.row_bytes &&
+            cs->local_n == local_n)
+          hit = cs;
+      if (hit != nullptr) {
+        ++hit->users;
+        p.coded_base = hit->base;
+        p.coded_stride = hit->stride;
+        p.coded_len = hit->len;
+        p.coded_agent = hit->agent;
+        ++n_coded;
+        continue;
+      }
+    }
     const uint16_t* rows = reinterpret_cast<const uint16_t*>(p.host_base);
     std::vector<size_t> len((size_t)local_n);
     parallel_for(local_n, [&](int e) { len[e] = codec_coded_bytes(rows + (size_t)e * n, n); });
@@ -2081,6 +2122,11 @@ extern "C" int sluice_layer_set_codec(sluice_layer* L, uint32_t bf16_params) {
         hsa_agent_get_info(owner, HSA_AGENT_INFO_DEVICE, &t) == HSA_STATUS_SUCCESS &&
         t == HSA_DEVICE_TYPE_CPU)
       p.coded_agent = owner;
+    {
+      std::lock_guard<std::mutex> lk2(g_coded_mu);
+      g_coded.push_back(new CodedStore{p.host_base, p.row_bytes, local_n, p.coded_base,
+                                       p.coded_stride, p.coded_len, p.coded_agent, 1});
+    }
     ++n_coded;
   }
   L->codec_mask = bf16_params;

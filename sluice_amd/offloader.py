@@ -77,7 +77,26 @@ STAGE_ROWS_DEFAULT = 4
 # per value plus rare escapes); misses copy the coded rows over the link and
 # a decode kernel writes the exact rows into the slot.  0 turns it off.
 CODEC_ENV = "SLUICE_CODEC"
-CODEC_DEFAULT = 0
+CODEC_DEFAULT = 1
+# Pinned host memory (GiB) the process may hold in host stores, uncoded and
+# coded together: layers are coded in order while their coded stores fit.
+# Default: a fifth of the host's memory (on MI355X boxes with 288 GiB,
+# pinned allocations failed from 64-69 GiB, near a quarter of it).
+CODEC_PIN_GB_ENV = "SLUICE_CODEC_PIN_GB"
+CODEC_PIN_FRAC_DEFAULT = 0.2
+
+
+def _codec_pin_gib() -> float:
+    total = None
+    try:
+        with open("/proc/meminfo") as f:
+            for line in f:
+                if line.startswith("MemTotal:"):
+                    total = int(line.split()[1]) * 1024
+    except OSError:
+        pass
+    default = CODEC_PIN_FRAC_DEFAULT * total / 2**30 if total else 16.0
+    return _env_number(CODEC_PIN_GB_ENV, default, float)
 
 # Graph split points under piecewise capture: the MoE ops (whose apply runs
 # the classic hook, which syncs the host) and the gap op.
@@ -955,17 +974,30 @@ class ExpertStreamOffloader(_OffloaderBase):
         if self._server is not None or not self._rs_caches:
             return
         lib = _lib.load()
+        coding = self.codec
+        if coding:
+            # what coded stores may still take of the pinned budget
+            room = (_codec_pin_gib() * 2**30 - ops.pinned_store_bytes()
+                    - sum(self._layer_codec(c)["coded_bytes"] for c in self._rs_caches))
         for c in self._rs_caches:
             # the coded store and staging only speed the path up: without
-            # them (no pinned memory, no copy engines free, no HBM left) the
-            # layer streams as before
-            if self.codec:
-                mask = sum(1 << i for i, n in enumerate(c.param_names)
-                           if c.gpu_cache[n].dtype == torch.bfloat16)
-                rc = lib.sluice_layer_set_codec(c.handle, mask)
+            # them (no pinned memory left, no copy engines free, no HBM left)
+            # the layer streams as before
+            if coding and self._layer_codec(c)["params"] == 0:
+                bf16 = [i for i, n in enumerate(c.param_names)
+                        if c.gpu_cache[n].dtype == torch.bfloat16]
+                # coded rows take ~0.75 of the rows (12 bits per value)
+                need = 0.76 * c.local_num_experts * sum(
+                    c.gpu_cache[c.param_names[i]][0].nbytes for i in bf16)
+                rc = (lib.sluice_layer_set_codec(c.handle, sum(1 << i for i in bf16))
+                      if need <= room else _lib.SLUICE_E_NOMEM)
                 if rc != 0:
-                    logger.warning("Sluice: layer %s streams uncoded rows (%s=1): %s",
-                                   c.layer_name or c.ordinal, CODEC_ENV, _lib.strerror(rc))
+                    coding = False  # this layer and the ones after it stream uncoded rows
+                    logger.warning("Sluice: layer %s and later ones stream uncoded rows (%s=1, "
+                                   "%s=%.1f): %s", c.layer_name or c.ordinal, CODEC_ENV,
+                                   CODEC_PIN_GB_ENV, _codec_pin_gib(), _lib.strerror(rc))
+                else:
+                    room -= self._layer_codec(c)["coded_bytes"]
             rc = lib.sluice_layer_set_staging(c.handle, self.stage_rows)
             if rc != 0:
                 logger.warning("Sluice: layer %s runs without staging rows (%s=%d): %s",
@@ -1038,6 +1070,14 @@ class ExpertStreamOffloader(_OffloaderBase):
                 tot[k_] += ctr[i]
         return tot
 
+    @staticmethod
+    def _layer_codec(c) -> dict:
+        """One layer's coded store: params coded and bytes of its coded rows."""
+        ctr = (ctypes.c_int64 * 6)()
+        _lib.check(_lib.load().sluice_layer_codec_counters(c.handle, ctr),
+                   "sluice_layer_codec_counters")
+        return {"params": ctr[0], "coded_bytes": ctr[2]}
+
     def codec_counters(self) -> dict:
         """Coded host stores summed over the armed layers: params coded,
         bytes of one expert's coded params as rows (summed over layers),
@@ -1048,12 +1088,14 @@ class ExpertStreamOffloader(_OffloaderBase):
         keys = ("params", "row_bytes", "coded_bytes", "link_bytes", "decodes", "decodes_staged")
         tot = dict.fromkeys(keys, 0)
         tot["store_bytes"] = 0  # the coded params' rows of every local expert, uncoded
+        tot["layers"] = 0  # layers with a coded store
         ctr = (ctypes.c_int64 * 6)()
         for c in self._rs_caches:
             _lib.check(lib.sluice_layer_codec_counters(c.handle, ctr), "sluice_layer_codec_counters")
             for i, k_ in enumerate(keys):
                 tot[k_] += ctr[i]
             tot["store_bytes"] += ctr[1] * c.local_num_experts
+            tot["layers"] += ctr[0] > 0
         return tot
 
     def get_gap_stats(self) -> dict:

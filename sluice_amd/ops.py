@@ -318,6 +318,11 @@ if not _vllm_present() and not hasattr(torch.ops.vllm, "fused_experts"):
 _HOST_STORES: "weakref.WeakValueDictionary" = weakref.WeakValueDictionary()
 
 
+def pinned_store_bytes() -> int:
+    """Bytes of every live HostStore of the process."""
+    return sum(st.nbytes for st in list(_HOST_STORES.values()))
+
+
 def host_store_of(t: torch.Tensor):
     """The HostStore whose allocation holds all of tensor ``t`` (a CPU
     tensor), or None."""
