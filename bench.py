@@ -935,7 +935,8 @@ def compact_line(rec):
                          _r(r["tok_per_s"], 1), _r(r["misses_per_layer_step"], 3),
                          _r(r["fast_hit_share"], 3),
                          _r((r.get("staged") or {}).get("hit_share_of_misses"), 3),
-                         (r.get("coded") or {}).get("layers"),
+                         ((r.get("coded") or {}).get("layers")
+                          if (r.get("coded") or {}).get("decodes") else 0),
                          _r(r["h2d_GBs_in_step"], 1), ref])
         if k1:
             key = f"{shape}/s{slots}/c{k1['c']}"
