@@ -35,6 +35,12 @@
 //     fills while the host link idles; a miss on one is copied into its slot
 //     from HBM before the device is answered.
 //
+//   coded host stores (sluice_layer_set_codec): a miss copies its expert's
+//     losslessly coded rows (12 bits per bf16 value) over the link into a
+//     ring in HBM, and a decode job on the library's own HSA queue writes
+//     the rows into the slot and marks it ready; staging rows then hold
+//     coded rows, decoded from where they lie.
+//
 // Ordering: a gap kernel runs only after all earlier work on its stream has
 // completed, so when the host sees its record no kernel of that stream can
 // still read a slot about to be overwritten (what the reference fences with

@@ -117,7 +117,8 @@ class Clock:
 
 
 def analyse(rings, clock, layer_ids, steps, bytes_per_expert):
-    """Per-gap rows and the summary the module prints."""
+    """Per-gap rows and the summary the module prints (bytes_per_expert: the
+    bytes one streamed expert moves over the link)."""
     lay = {int(v): i for i, v in enumerate(layer_ids)}
     gap = rings["gap"]
     tag = (gap[:, 0] >> TAG_SHIFT).astype(int)
@@ -317,12 +318,20 @@ def main():
         rings = read_rings(lib)
         ids = [(m._expert_map.data_ptr() >> 8) & 0xffffffff for m in dec.moe_layers]
         per_expert = sum(t.nbytes // t.shape[0] for t in dec.caches[0].cpu_store.values())
-        summary, _ = analyse(rings, Clock(cal0, cal1), ids, a.steps, per_expert)
+        # bytes of an expert over the link: its coded rows in layers whose
+        # host store is coded (the mean over the layers, as a mix of both)
+        cc = dec.off.codec_counters()
+        ratio = cc["coded_bytes"] / cc["store_bytes"] if cc["store_bytes"] else 1.0
+        share = cc["layers"] / max(len(dec.moe_layers), 1)
+        link_per_expert = per_expert * (1.0 - share + share * ratio)
+        summary, _ = analyse(rings, Clock(cal0, cal1), ids, a.steps, link_per_expert)
         summary = {"workload": f"{a.config}-shaped decode, slots={a.slots}, c={c}, "
                                f"{a.steps} steps centred in a 256-token decode after "
                                f"128-token prompts (traced build)",
                    "ms_per_step": round(dt / a.steps * 1e3, 3),
-                   "bytes_per_expert": int(per_expert), **summary}
+                   "bytes_per_expert": int(per_expert),
+                   "coded_layers": int(cc["layers"]), "moe_layers": len(dec.moe_layers),
+                   "link_bytes_per_expert": int(link_per_expert), **summary}
     finally:
         dec.close()
     text = json.dumps(summary)

@@ -68,6 +68,13 @@ def test_compact_line_fits_and_parses():
     # the staging rows the headline ran with, and the share of its misses they served
     assert line["config"]["staging_rows_per_layer"] == 4
     assert 0.0 < head["staged_share_of_misses"] < 1.0
+    # coded host stores: every V2-Lite layer, at ~0.75 of the rows; the rows in
+    # the reference's orchestration decode nothing
+    coded = line["config"]["coded_store"]
+    assert coded["layers"] == coded["of_layers"] == 26 and 0.74 < coded["bytes_frac"] < 0.76
+    assert head["coded_layers"] == 26
+    assert all(dict(zip(cols, r))["coded_layers"] == 0 for r in line["rows"]
+               if r[cols.index("path")].endswith("/ref-orch"))
 
 
 def test_compact_line_stays_under_the_limit_with_every_row_doubled():
