@@ -311,9 +311,11 @@ int sluice_layer_stage_counters(const sluice_layer* layer, int64_t* counters);
  * and a decode kernel on the server's own stream writes the rows into the
  * slot and marks it ready; staging rows hold coded rows too and are decoded
  * from where they lie.  Slot bytes, maps and products are those of the
- * uncoded store; every other path (inline gaps, classic waves, resync)
- * copies the rows as they are, from the store given to add_param, which
- * must stay valid.  Call before sluice_layer_set_staging and with no gap
+ * uncoded store; every other path (inline gaps, classic waves, resync),
+ * and a gap server that could not set up its decode resources (no
+ * sluice_amd/codec_decode.hsaco beside the library, no HSA queue), copies
+ * the rows as they are, from the store given to add_param, which must stay
+ * valid.  Call before sluice_layer_set_staging and with no gap
  * server serving the layer; 0 frees the coded stores; a call with the mask
  * already set changes nothing.  SLUICE_E_STATE after staging is set. */
 int sluice_layer_set_codec(sluice_layer* layer, uint32_t bf16_params);

@@ -1775,6 +1775,7 @@ static void stage_step(sluice_gap_server* S) {
     for (size_t k = 0; k < n; ++k) {
       sluice_layer* L = S->layers[(S->cursor + k) % n];
       if (L->stage.empty() || L->stage_broken || L->armed_copies != 0) continue;
+      if (L->codec == nullptr && has_coded(L)) continue;  // coded rows it could not decode
       if (L->stage_sig_row[l] >= 0 || (!L->stage_dirty && !stage_has_copy(L))) continue;
       std::lock_guard<std::mutex> lk(L->mu);
       stage_choose(L);
@@ -2226,13 +2227,10 @@ extern "C" int sluice_gap_server_create(sluice_layer* const* layers, int n_layer
       largest = std::max(largest, b);
     }
   }
-  if (any_coded) {
-    const int crc = codec_res_create(S->device, largest, &S->codec);
-    if (crc != SLUICE_OK) {
-      delete S;
-      return crc;
-    }
-  }
+  // Without decode resources (no code object beside the library, no HSA
+  // queue) the layers stream their uncoded rows, which stay registered.
+  if (any_coded && codec_res_create(S->device, largest, &S->codec) != SLUICE_OK)
+    S->codec = nullptr;
   for (sluice_layer* L : S->layers) {
     L->server = S;
     L->codec = has_coded(L) ? S->codec : nullptr;
