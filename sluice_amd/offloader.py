@@ -71,7 +71,7 @@ NO_STATIC_FULL_ENV = "SLUICE_NO_STATIC_FULL"
 # selected experts it does not hold, copied while the host link idles; a
 # miss on one is copied into its slot from HBM).  0 turns staging off.
 STAGE_ROWS_ENV = "SLUICE_STAGE_ROWS"
-STAGE_ROWS_DEFAULT = 4
+STAGE_ROWS_DEFAULT = 6
 # No counterpart in the reference: under the gap server, each router-split
 # layer's bf16 expert rows also get a losslessly coded host store (12 bits
 # per value plus rare escapes); misses copy the coded rows over the link and

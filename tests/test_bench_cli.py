@@ -66,7 +66,7 @@ def test_compact_line_fits_and_parses():
     head = dict(zip(cols, next(r for r in line["rows"] if r[2] == line["config"]["batch"])))
     assert head["ref_tok_per_s"] == 1062.6  # README.md:51, V2-Lite c=8
     # the staging rows the headline ran with, and the share of its misses they served
-    assert line["config"]["staging_rows_per_layer"] == 4
+    assert line["config"]["staging_rows_per_layer"] == 6
     assert 0.0 < head["staged_share_of_misses"] < 1.0
     # coded host stores: every V2-Lite layer, at ~0.75 of the rows; the rows in
     # the reference's orchestration decode nothing
