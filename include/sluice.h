@@ -308,7 +308,8 @@ int sluice_layer_stage_counters(const sluice_layer* layer, int64_t* counters);
  * gaps are answered before their rows land (sluice_gap_set_pipelined(1)),
  * a miss then copies the coded rows over the link into a ring in HBM that
  * the server owns (at least 128 MiB, and twice the largest coded expert),
- * and a decode kernel on the server's own stream writes the rows into the
+ * and a decode kernel, dispatched on an HSA queue of the library's own
+ * (sluice_amd/codec_decode.hsaco, beside the library), writes the rows into the
  * slot and marks it ready; staging rows hold coded rows too and are decoded
  * from where they lie.  Slot bytes, maps and products are those of the
  * uncoded store; every other path (inline gaps, classic waves, resync),

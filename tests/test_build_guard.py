@@ -1,7 +1,8 @@
-"""The build's register-room guard (sluice_amd/build.py): the expert
+"""The build's register-room guards (sluice_amd/build.py): the expert
 product's split launch holds workgroups that wait for streaming slots while
 the runtime's copy kernel (two 16-VGPR waves per SIMD) must still find room
-to copy small host rows.  The guard reads hipcc's kernel-resource-usage
+to copy small host rows, and the decode of coded experts (one wave per SIMD)
+room to write the rows they wait for.  The guard reads hipcc's kernel-resource-usage
 remarks; here on remark text shaped like hipcc's, no compiler run."""
 
 from sluice_amd import build as b
@@ -56,3 +57,27 @@ def test_guard_ignores_kernels_that_do_not_hold_waiting_workgroups():
     # the grid-stride gemm2 launch fills the file, but its grid over a
     # streaming map leaves a workgroup place per CU free instead
     assert b.check_wait_room(_remarks(GEMM2, 116, 12, 4)) == []
+
+
+SPLIT_BF16 = "_ZN12_GLOBAL__N_122moe_gemm2_split_kernelILb0EEEvPKtPtNS_7ExpertW"
+DECODE = "sluice_codec_decode_kernel"
+
+
+def test_decode_room_beside_the_bf16_split_launch():
+    # the bf16 split launch at 4 waves x 112 leaves 64 VGPRs per SIMD: a
+    # 256-thread decode workgroup (one wave per SIMD) of up to 64 fits
+    split = _remarks(SPLIT_BF16, 98, 12, 4)
+    assert b.check_decode_room(split, _remarks(DECODE, 34, 0, 8)) == []
+    assert b.check_decode_room(split, _remarks(DECODE, 60, 0, 8)) == []  # 64 after rounding
+    bad = b.check_decode_room(split, _remarks(DECODE, 65, 0, 7))  # 72
+    assert len(bad) == 1 and "leaves 64 VGPRs per SIMD, the decode needs 72" in bad[0]
+
+
+def test_decode_room_needs_the_decode_kernels_remarks():
+    assert b.check_decode_room(_remarks(SPLIT_BF16, 98, 12, 4), "") == [
+        f"{DECODE}: no resource remarks"]
+
+
+def test_decode_room_ignores_the_fp8_split_launch():
+    # coded stores hold bf16 rows: decodes never wait beside the fp8 launch
+    assert b.check_decode_room(_remarks(SPLIT, 112, 8, 4), _remarks(DECODE, 60, 0, 8)) == []
