@@ -1523,8 +1523,12 @@ int serve_one(sluice_layer* L, bool fast_hit, bool block, hipStream_t compute) {
           if (!landing) return false;
           continue;
         }
-        const CodecRes::Use& u = C->uses.front();
-        const int w = u.state == kUseLaunched ? codec_wait(C, u.seq) : SLUICE_E_STATE;
+        // (no live region: the expert is larger than the ring, which the
+        // server sized for the largest coded expert of its layers)
+        const int w = C->uses.empty() ? SLUICE_E_STATE
+                      : C->uses.front().state == kUseLaunched
+                          ? codec_wait(C, C->uses.front().seq)
+                          : SLUICE_E_STATE;
         if (w != SLUICE_OK) {
           if (rc == SLUICE_OK) rc = w;
           return false;
