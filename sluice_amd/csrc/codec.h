@@ -4,12 +4,13 @@
 // so bytes that do not cross it are time saved.  A bf16 weight is sign (1),
 // exponent (8) and mantissa (7) bits; the mantissa and sign carry close to
 // 8 bits of information, the exponent of a weight matrix far fewer (2.5 bits
-// for N(0, 0.02) values: nearly all lie within 15 consecutive binades).  A
+// for N(0, 0.02) values: nearly all lie within 14 consecutive binades).  A
 // coded row keeps sign and mantissa whole and each exponent as a 4-bit
-// offset from a base chosen per chunk of kCodecChunk values; an exponent
-// outside [base, base + 14] is coded 15 and kept in the chunk's escape list.
-// 12 bits per value (0.75 of the row) plus the escapes; decoding gives the
-// row's bytes back exactly.
+// code: its offset from a base chosen per chunk of kCodecChunk values (0 to
+// 13), 14 for exponent 0 (zeros and subnormals), or 15 for an exponent
+// outside [base, base + 13], kept in the chunk's escape list.  12 bits per
+// value (0.75 of the row) plus the escapes; decoding gives the row's bytes
+// back exactly.
 //
 // Layout of a coded row of n values (n a multiple of kCodecChunk, nc =
 // n / kCodecChunk chunks):
@@ -27,6 +28,8 @@
 
 constexpr size_t kCodecChunk = 2048;   // values per base exponent
 constexpr int kCodecMaxParts = 4;      // coded rows one decode job writes
+constexpr uint32_t kCodecWindow = 14;  // binades a chunk's base starts
+constexpr uint32_t kCodecZero = 14;    // nibble of exponent 0 (zeros, subnormals)
 constexpr uint32_t kCodecEscape = 15;  // nibble of an exponent outside the window
 constexpr int kCodecThreads = 256;     // threads of a decode workgroup
 constexpr uint32_t kCodecMaxGrid = 512;

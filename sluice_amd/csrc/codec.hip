@@ -28,17 +28,19 @@
 
 namespace {
 
-// The first exponent of the window of 15 binades that holds most of the
-// chunk's values (the lowest such start on ties).
+// The first exponent of the window of kCodecWindow binades that holds most
+// of the chunk's values other than zeros and subnormals (exponent 0, coded
+// kCodecZero; the lowest such start on ties).
 int chunk_base(const uint16_t* v) {
   uint32_t h[256] = {};
   for (size_t i = 0; i < kCodecChunk; ++i) ++h[(v[i] >> 7) & 0xff];
+  h[0] = 0;
   uint32_t win = 0;
-  for (int e = 0; e < 15; ++e) win += h[e];
+  for (int e = 0; e < (int)kCodecWindow; ++e) win += h[e];
   uint32_t best = win;
   int base = 0;
-  for (int b = 1; b + 15 <= 256; ++b) {
-    win += h[b + 14] - h[b - 1];
+  for (int b = 1; b + (int)kCodecWindow <= 256; ++b) {
+    win += h[b + kCodecWindow - 1] - h[b - 1];
     if (win > best) {
       best = win;
       base = b;
@@ -60,7 +62,10 @@ size_t codec_coded_bytes(const uint16_t* v, size_t n) {
   for (size_t c = 0; c < n / kCodecChunk; ++c) {
     const uint16_t* x = v + c * kCodecChunk;
     const int b = chunk_base(x);
-    for (size_t i = 0; i < kCodecChunk; ++i) esc += (unsigned)(((x[i] >> 7) & 0xff) - b) > 14u;
+    for (size_t i = 0; i < kCodecChunk; ++i) {
+      const uint32_t e = (x[i] >> 7) & 0xffu;
+      esc += e != 0 && e - (uint32_t)b >= kCodecWindow;
+    }
   }
   return codec_esc_off(n) + 4 * esc;
 }
@@ -85,7 +90,7 @@ size_t codec_encode(const uint16_t* v, size_t n, uint8_t* out) {
         const uint32_t w = x[i + h], e = (w >> 7) & 0xffu;
         sm[c * kCodecChunk + i + h] = (uint8_t)(((w >> 8) & 0x80u) | (w & 0x7fu));
         const uint32_t d = e - (uint32_t)b;
-        code[h] = d <= 14u ? d : kCodecEscape;
+        code[h] = e == 0 ? kCodecZero : d < kCodecWindow ? d : kCodecEscape;
         if (code[h] == kCodecEscape) esc[ne++] = (uint32_t)(i + h) << 8 | e;
       }
       nib[(c * kCodecChunk + i) / 2] = (uint8_t)(code[0] | code[1] << 4);

@@ -90,7 +90,11 @@ extern "C" __global__ __launch_bounds__(kCodecThreads) void sluice_codec_decode_
         const uint32_t x = __builtin_amdgcn_perm(0u, nb[u],
                                                  (uint32_t)k | 0x0c00u | (uint32_t)k << 16 |
                                                      0x0c000000u);
-        const uint32_t ex = ((((x & 0x00f00000u) >> 4) | (x & 0xfu)) + base2) & 0x00ff00ffu;
+        const uint32_t code = ((x & 0x00f00000u) >> 4) | (x & 0xfu);
+        // a half whose code is kCodecZero takes exponent 0
+        const uint32_t y = code ^ (kCodecZero | kCodecZero << 16);
+        const uint32_t zero = ((y | (y >> 1) | (y >> 2) | (y >> 3)) & 0x00010001u) ^ 0x00010001u;
+        const uint32_t ex = ((code + base2) & 0x00ff00ffu) & ~(zero * 0xffu);
         out[k] = ((t & 0x00800080u) << 8) | (t & 0x007f007fu) | (ex << 7);
       }
       st16_coh(dst[u], u32x4_t{out[0], out[1], out[2], out[3]});
