@@ -302,8 +302,9 @@ int sluice_layer_stage_counters(const sluice_layer* layer, int64_t* counters);
  * 2048 per row; at most 4 params, the pulled ones excepted) the layer codes
  * each expert's row losslessly into a pinned host store of its own
  * (sluice_codec_encode, on up to 16 host threads): sign and mantissa whole,
- * the exponent as a 4-bit offset from a base per 2048 values, exponents
- * outside that window in a per-chunk escape list.  A param whose rows code
+ * the exponent as a 4-bit code (its offset in a 14-binade window based per
+ * 2048 values; 14 for exponent 0), exponents outside the window in a
+ * per-chunk escape list.  A param whose rows code
  * to more than 7/8 of their bytes stays uncoded.  Under a gap server whose
  * gaps are answered before their rows land (sluice_gap_set_pipelined(1)),
  * a miss then copies the coded rows over the link into a ring in HBM that
