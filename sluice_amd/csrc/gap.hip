@@ -1940,7 +1940,11 @@ extern "C" int sluice_layer_add_param(sluice_layer* L, void* slot_base_dev, cons
        !known_range(slot_base_dev, row_bytes * (size_t)L->c.S)))
     return SLUICE_E_INVAL;
   std::lock_guard<std::mutex> lk(L->mu);
-  L->params.push_back({(char*)slot_base_dev, (const char*)host_base, row_bytes, 0});
+  ParamRows row{};
+  row.slot_base = (char*)slot_base_dev;
+  row.host_base = (const char*)host_base;
+  row.row_bytes = row_bytes;
+  L->params.push_back(row);
   hsa_device_type_t host_type{};
   if (host_agent.handle != 0 &&
       hsa_agent_get_info(host_agent, HSA_AGENT_INFO_DEVICE, &host_type) == HSA_STATUS_SUCCESS &&
