@@ -394,9 +394,10 @@ def test_decode_on_streams_that_share_hardware_queues():
     pipelined decode runs on every stream: streams made before the decoder's
     copy machinery and after it, 6 each, the one-graph step with the gap
     server on each in turn.  The gap's row copies go to the SDMA engines with
-    HSA completion signals, so no copy waits behind the expert product that
-    waits for it; every gap wait is bounded at 5 s here, so a copy stuck
-    behind a kernel ends as an error, not a hang."""
+    HSA completion signals, and the coded rows' decodes run on an HSA queue
+    of the library's own, so neither waits behind the expert product that
+    waits for it; every gap wait is bounded at 5 s here, so a copy or decode
+    stuck behind a kernel ends as an error, not a hang."""
     from sluice_amd import _lib
     from sluice_amd.decoder import SyntheticDecoder
 
@@ -423,6 +424,8 @@ def test_decode_on_streams_that_share_hardware_queues():
             now = dec.gap_counters()["misses"]
             assert now > misses, n  # every stream's steps streamed experts
             misses = now
+        # the misses were decoded from the coded stores (the default)
+        assert dec.off.codec_counters()["decodes"] == misses
     finally:
         dec.close()
         lib.sluice_gap_set_timeout(0.0)
